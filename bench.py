@@ -1,0 +1,358 @@
+#!/usr/bin/env python3
+"""Decode-attention benchmark on one MI355X: µs/token and HBM GB/s (% of roofline).
+
+    python bench.py [--steps K] [--warmup W] [--workload stack8k|stack32k|long128k|ragged64|layer512]
+
+A step is one token's attention over the workload on synthetic, seeded,
+inputs resident in HBM:
+  stack8k   35-layer Gemma-4-E2B-shaped stack, batch 1, position 8192
+            (7 global layers full causal, RoPE theta 1e6; 28 local layers
+            with a 512-row window, theta 1e4), 35 separate f16 KV caches,
+            8 query heads / 1 KV head, head_dim 256.            [default]
+  stack32k  the same stack at position 32768.
+  long128k  one global layer attending 131072 rows.
+  ragged64  64 independent sequences, lengths uniform in [1024, 32768].
+  layer512  one local layer at position 512 (launch-bound).
+
+Per step the stack runs the producer-side prep of every layer (q/k RMSNorm +
+RoPE, weightless v-norm, f16 store of the new row) and the fused split-K
+decode attention of every layer. Several distinct cache sets are rotated so
+the bytes read each cycle exceed twice MI355X's 256 MB Infinity Cache and
+come from HBM. `value` is algorithmic bytes per step (K/V rows attended,
+f16, read once for all query heads; q read; attnOut written) over wall time
+per step. `roofline` is the dominant kernel (the decode split pass), timed
+with HIP events on its stream. `cpu_baseline` runs the oracle (the
+WGSL-semantics C restatement of the reference's six kernels, f32 caches,
+full-length score/softmax/output on every layer as the WGSL does) on the host.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "gemma4-webgpu_amd"))
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+MALL_BYTES = 256 << 20
+NQH, NKH, HD = 8, 1, 256
+EPS = 1e-6
+BASE_SEED = 20261201
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+# ---- workload description -----------------------------------------------------
+
+def workload_spec(name: str) -> dict:
+    from g4attn import e2b
+
+    if name in ("stack8k", "stack32k"):
+        pos = 8192 if name == "stack8k" else 32768
+        cfg = e2b.AttnConfig(num_layers=35)
+        layers = [dict(window=e2b.sliding_window(il, cfg), theta=e2b.rope_theta(il, cfg),
+                       divisor=e2b.apply_divisor(il, cfg), seq=pos + 1, pos=pos) for il in range(35)]
+        return dict(name=name, layers=layers, seed=BASE_SEED + (1 if name == "stack8k" else 5),
+                    desc=f"35-layer Gemma-4-E2B attention stack, bs1, position {pos} (7 global + 28 local W=512)")
+    if name == "long128k":
+        pos = 131071
+        return dict(name=name, layers=[dict(window=0, theta=1e6, divisor=1, seq=pos + 1, pos=pos)],
+                    seed=BASE_SEED + 4, desc="1 global layer, 131072 attended rows, bs1")
+    if name == "layer512":
+        return dict(name=name, layers=[dict(window=512, theta=1e4, divisor=0, seq=513, pos=512)],
+                    seed=BASE_SEED + 0, desc="1 local layer (W=512), position 512, bs1")
+    if name == "ragged64":
+        from g4attn import synth
+
+        lens = synth.ragged_lengths(BASE_SEED + 2, 64, 1024, 32768)
+        layers = [dict(window=0, theta=1e6, divisor=1, seq=int(L), pos=int(L) - 1) for L in lens]
+        return dict(name=name, layers=layers, seed=BASE_SEED + 2, prep=False,
+                    desc="64 sequences, ragged lengths U[1024, 32768], global attention (decode only)")
+    raise SystemExit(f"unknown workload {name}")
+
+
+def attended(seq: int, window: int) -> int:
+    return min(seq, window) if window else seq
+
+
+def step_bytes(spec: dict) -> int:
+    """Algorithmic HBM bytes of one step: attended K and V rows (f16) once for all query
+    heads, q read (f32) and attnOut written (f32) per layer."""
+    b = 0
+    for L in spec["layers"]:
+        b += 2 * attended(L["seq"], L["window"]) * NKH * HD * 2 + NQH * HD * 4 * 2
+    return b
+
+
+# ---- GPU side -----------------------------------------------------------------
+
+class CacheSet:
+    """One complete set of per-layer buffers (caches, q/k/v, outputs, tables)."""
+
+    def __init__(self, spec, set_idx, dev, torch, ops, synth, e2b):
+        self.layers = []
+        seed0 = spec["seed"] + 7919 * set_idx
+        rf = torch.tensor(e2b.rope_freqs_f16_bits(256), dtype=torch.int32).to(torch.int16).to(dev)
+        ones = torch.full((HD,), 0x3C00, dtype=torch.int16, device=dev)  # weight 1.0 (f16)
+        prep_rows = []
+        for il, L in enumerate(spec["layers"]):
+            rows = L["seq"]
+            kc = torch.empty(rows * NKH * HD, dtype=torch.float16, device=dev)
+            vc = torch.empty_like(kc)
+            n_att = attended(L["seq"], L["window"])
+            lo = L["seq"] - n_att
+            for cache, off in ((kc, 0), (vc, 1)):
+                x = synth.normal_torch(seed0 + 1000 * il + off, n_att * NKH * HD, dev).view(-1, HD)
+                ms = (x.double() ** 2).mean(dim=1, keepdim=True)
+                y = (x.double() / torch.sqrt(ms + EPS)).to(torch.float16)
+                cache.view(rows, -1)[lo:lo + n_att].copy_(y.view(n_att, -1))
+            q = synth.normal_torch(seed0 + 1000 * il + 2, NQH * HD, dev)
+            if not spec.get("prep", True):  # decode-only workloads take unit-RMS queries as given
+                qh = q.view(NQH, HD).double()
+                q = (qh / torch.sqrt((qh ** 2).mean(dim=1, keepdim=True) + EPS)).float().reshape(-1).contiguous()
+            k = synth.normal_torch(seed0 + 1000 * il + 3, NKH * HD, dev)
+            v = synth.normal_torch(seed0 + 1000 * il + 4, NKH * HD, dev)
+            out = torch.zeros(NQH * HD, dtype=torch.float32, device=dev)
+            self.layers.append(dict(q=q, k=k, v=v, kc=kc.view(torch.int16), vc=vc.view(torch.int16), out=out,
+                                    seq=L["seq"], window=L["window"], pos=L["pos"]))
+            prep_rows.append(dict(q=q, k=k, v=v, q_weight=ones, k_weight=ones, rope_freqs=rf,
+                                  k_cache=kc.view(torch.int16), v_cache=vc.view(torch.int16), head_dim=HD,
+                                  theta=L["theta"], apply_divisor=L["divisor"], store_kv=True,
+                                  max_seq_len=rows))
+        self.rf, self.ones = rf, ones
+        self.with_prep = spec.get("prep", True)
+        self.uniform_pos = len({L["pos"] for L in spec["layers"]}) == 1
+        self.prep_table = ops.make_prep_table(prep_rows, NQH, NKH, dev) if self.uniform_pos else None
+        self.prep_rows = prep_rows
+        entries = ops.make_entries([(l["q"], l["kc"], l["vc"], l["out"], l["seq"], l["window"], 1.0)
+                                    for l in self.layers], NQH, NKH, HD)
+        total = sum(attended(l["seq"], l["window"]) for l in self.layers)
+        self.ws = torch.empty(ops.decode_many_workspace_bytes(len(entries), NQH, NKH, HD, total),
+                              dtype=torch.uint8, device=dev)
+        self.plan = ops.attn_decode_many_prepare(entries, NQH, NKH, HD, self.ws)
+        self.ws1 = torch.empty(ops.decode_workspace_bytes(NQH, NKH, HD, max(l["seq"] for l in self.layers)),
+                               dtype=torch.uint8, device=dev)
+
+    def prep(self, ops):
+        if not self.with_prep:
+            return
+        if self.uniform_pos:
+            pos = self.layers[0]["pos"]
+            ops.attn_prep_many(self.prep_table, len(self.layers), NQH, NKH, EPS, pos, pos)
+        else:
+            for l, r in zip(self.layers, self.prep_rows):
+                ops.attn_prep(r["q"], r["k"], r["v"], r["q_weight"], r["k_weight"], r["rope_freqs"], r["k_cache"],
+                              r["v_cache"], NQH, NKH, HD, EPS, l["pos"], r["theta"], r["apply_divisor"], l["pos"],
+                              r["max_seq_len"])
+
+    def step_sequential(self, ops):
+        """The in-model order: per layer, prep then fused decode (split + merge)."""
+        for l, r in zip(self.layers, self.prep_rows):
+            ops.attn_prep(r["q"], r["k"], r["v"], r["q_weight"], r["k_weight"], r["rope_freqs"], r["k_cache"],
+                          r["v_cache"], NQH, NKH, HD, EPS, l["pos"], r["theta"], r["apply_divisor"], l["pos"],
+                          r["max_seq_len"])
+            ops.attn_decode(l["q"], l["kc"], l["vc"], l["out"], self.ws1, NQH, NKH, HD, l["seq"], 1.0, l["window"])
+
+
+def run_gpu(spec, args):
+    import torch
+
+    from g4attn import abi, e2b, ops, synth
+
+    abi.load()
+    abi.call("g4_set_device", 0)
+    dev = torch.device("cuda:0")
+    per_step = step_bytes(spec)
+    sets = args.sets or max(1, math.ceil(2 * MALL_BYTES / max(per_step, 1)) + 1)
+    if per_step < 4 << 20:
+        sets = 1  # tiny workloads are launch-bound; rotating sets changes nothing
+    log(f"workload {spec['name']}: {len(spec['layers'])} entries, {per_step / 1e6:.1f} MB/step, {sets} cache sets")
+    t0 = time.time()
+    csets = [CacheSet(spec, s, dev, torch, ops, synth, e2b) for s in range(sets)]
+    torch.cuda.synchronize()
+    log(f"inputs ready in {time.time() - t0:.1f}s")
+
+    stream = torch.cuda.current_stream()
+
+    def step(i, ev=None):
+        cs = csets[i % sets]
+        cs.prep(ops)
+        if ev is not None:
+            ev[0].record(stream)
+        ops.attn_decode_many_run_split(cs.plan)
+        if ev is not None:
+            ev[1].record(stream)
+        ops.attn_decode_many_run_merge(cs.plan)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    log(f"warmup {args.warmup} steps done")
+
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    for i in range(args.steps):
+        step(args.warmup + i, evs[i])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_start
+    split_ms = [a.elapsed_time(b) for a, b in evs]
+    split_ms.sort()
+    split_avg = sum(split_ms) / len(split_ms)
+    log(f"timed {args.steps} steps: {wall / args.steps * 1e6:.1f} us/step; split kernel avg {split_avg * 1e3:.1f} us"
+        f" median {split_ms[len(split_ms) // 2] * 1e3:.1f} us")
+
+    # Event-free timing of the same steps (events add small gaps between launches).
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    for i in range(args.steps):
+        step(i)
+    torch.cuda.synchronize()
+    wall_noev = time.perf_counter() - t1
+
+    result = dict(wall_s=min(wall, wall_noev), steps=args.steps, split_avg_ms=split_avg,
+                  split_median_ms=split_ms[len(split_ms) // 2], sets=sets, bytes=per_step)
+
+    # In-model order: layer after layer, each its own prep + decode launches, in a HIP graph.
+    if args.sequential and len(spec["layers"]) > 1:
+        g = torch.cuda.CUDAGraph()
+        cs = csets[0]
+        cs.step_sequential(ops)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g):
+            cs.step_sequential(ops)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            g.replay()
+        torch.cuda.synchronize()
+        n = max(10, args.steps // 2)
+        t2 = time.perf_counter()
+        for _ in range(n):
+            g.replay()
+        torch.cuda.synchronize()
+        result["sequential_us"] = (time.perf_counter() - t2) / n * 1e6
+        log(f"layer-sequential (graph replay, one cache set): {result['sequential_us']:.1f} us/step")
+    return result
+
+
+# ---- CPU baseline (oracle on the host) --------------------------------------------
+
+def run_cpu_baseline(spec, seconds: float):
+    import numpy as np
+
+    from g4attn import e2b, synth
+    from oracle import oracle as orc
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
+    orc.set_threads(threads)
+    rf = np.array(e2b.rope_freqs_f16_bits(256), dtype=np.uint16)
+    ones = np.full(HD, 0x3C00, dtype=np.uint16)
+    layers = spec["layers"]
+    # The reference's per-layer buffers: f32 caches of seq rows each (the WGSL scores and masks the rows
+    # outside a local window, so they are read too). Timing only: filled from numpy's generator.
+    rng = np.random.default_rng(spec["seed"])
+    caches = []
+    for L in layers:
+        rows = L["seq"]
+        kc = rng.standard_normal((rows, HD), dtype=np.float32)
+        vc = rng.standard_normal((rows, HD), dtype=np.float32)
+        caches.append((kc, vc))
+    log(f"cpu baseline: {threads} threads, {len(layers)} f32 cache pairs built")
+    q0 = [synth.normal(spec["seed"] + 97 * il, NQH * HD) for il in range(len(layers))]
+    kv0 = [(synth.normal(spec["seed"] + 97 * il + 1, HD), synth.normal(spec["seed"] + 97 * il + 2, HD))
+           for il in range(len(layers))]
+
+    with_prep = spec.get("prep", True)
+
+    def one_token():
+        for il, L in enumerate(layers):
+            kc, vc = caches[il]
+            if not with_prep:
+                orc.attention_chain(q0[il], kc, vc, NQH, NKH, HD, L["seq"], 1.0, L["window"])
+                continue
+            v = orc.per_head_rms_norm_no_weight(kv0[il][1], NKH, HD, EPS)
+            q = orc.fused_per_head_norm_rope(q0[il], ones, rf, NQH, HD, EPS, L["pos"], L["theta"], L["divisor"])
+            k = orc.fused_per_head_norm_rope(kv0[il][0], ones, rf, NKH, HD, EPS, L["pos"], L["theta"], L["divisor"])
+            kc[L["pos"]] = k  # kvCacheStore (f32 caches)
+            vc[L["pos"]] = v
+            orc.attention_chain(q, kc, vc, NQH, NKH, HD, L["seq"], 1.0, L["window"])
+
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        one_token()
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or n >= 1000:
+            break
+    per_token = el / n
+    return dict(per_token_s=per_token, tokens=n, threads=threads)
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="stack8k",
+                    choices=["stack8k", "stack32k", "long128k", "ragged64", "layer512"])
+    ap.add_argument("--sets", type=int, default=0, help="cache sets to rotate (0 = enough to exceed 2x MALL)")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--sequential", action=argparse.BooleanOptionalAction, default=True,
+                    help="also time the layer-after-layer issue order (HIP graph)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported (the attention path "
+              "would shard by sequence or by KV range across GPUs, which is not built here)", file=sys.stderr)
+        sys.exit(2)
+
+    spec = workload_spec(args.workload)
+    r = run_gpu(spec, args)
+    ms_per_step = r["wall_s"] / r["steps"] * 1e3
+    value = r["bytes"] / (ms_per_step * 1e-3) / 1e9
+    achieved = r["bytes"] / (r["split_avg_ms"] * 1e-3) / 1e9
+    line = {
+        "metric": "decode-attention us/token & HBM GB/s (% roofline), E2B-shaped, bs1",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "us_per_token": round(ms_per_step * 1e3, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16 KV, f32 accumulate",
+        "data": "synthetic (seeded splitmix64 N(0,1), unit-RMS rows), resident in HBM",
+        "config": {"workload": spec["desc"], "batch": 1, "num_q_heads": NQH, "num_kv_heads": NKH,
+                   "head_dim": HD, "bytes_per_step": r["bytes"], "cache_sets_rotated": r["sets"],
+                   "issue": "all layers of the step in one prep launch and one split-K decode launch pair"},
+        "roofline": {"bound": "hbm", "kernel": "k_decode_split", "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": None, "avg_us": round(r["split_avg_ms"] * 1e3, 2)},
+    }
+    if "sequential_us" in r:
+        line["layer_sequential_us_per_token"] = round(r["sequential_us"], 2)
+    if not args.no_cpu_baseline:
+        cpu = run_cpu_baseline(spec, args.cpu_seconds)
+        cpu_gbs = r["bytes"] / cpu["per_token_s"] / 1e9
+        line["cpu_baseline"] = {"value": round(cpu_gbs, 3), "unit": "GB/s", "cores": cpu["threads"], "kind": "port",
+                                "us_per_token": round(cpu["per_token_s"] * 1e6, 1),
+                                "sample": f"{cpu['tokens']} tokens of the same workload through the oracle's "
+                                          "restatement of the six reference WGSL kernels (f32 caches, full-length "
+                                          "scores on every layer); no WebGPU CPU adapter on the host"}
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,52 @@
+// Shared helpers for the gfx950 attention library: status handling, f16
+// vector types, lane helpers. Every kernel in this library is written for
+// CDNA4 wave64; nothing here is portable to other targets by design.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "../../include/g4attn.h"
+
+namespace g4 {
+
+// ---- status ----------------------------------------------------------------
+
+// Records `msg` as this thread's last error and returns `code`.
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int hip_fail(hipError_t e, const char* what);
+
+#define G4_CHECK_HIP(expr)                                 \
+    do {                                                   \
+        hipError_t e_ = (expr);                            \
+        if (e_ != hipSuccess) return ::g4::hip_fail(e_, #expr); \
+    } while (0)
+
+// After a kernel launch: reports launch-configuration errors synchronously.
+#define G4_CHECK_LAUNCH(name)                              \
+    do {                                                   \
+        hipError_t e_ = hipGetLastError();                 \
+        if (e_ != hipSuccess) return ::g4::hip_fail(e_, name); \
+    } while (0)
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// ---- types -----------------------------------------------------------------
+
+typedef _Float16 f16;
+typedef f16 f16x8 __attribute__((ext_vector_type(8)));
+typedef f16 f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+__device__ __forceinline__ float h2f(uint16_t h) {
+    return static_cast<float>(__builtin_bit_cast(f16, h));
+}
+__device__ __forceinline__ uint16_t f2h(float f) {  // round to nearest even
+    return __builtin_bit_cast(uint16_t, static_cast<f16>(f));
+}
+
+}  // namespace g4

@@ -1,0 +1,106 @@
+// Fused producer-side prep for one layer and one token, in one launch:
+// vNorm -> fusedNormRope(Q) -> fusedNormRope(K) -> kvCacheStore, the
+// sequence gemma4-webgpu dispatches as four passes (src/engine.ts:2056-2091;
+// shaders/per_head_rms_norm_no_weight.wgsl, fused_per_head_norm_rope.wgsl,
+// kv_cache_store.wgsl). Workgroup b handles one head: b < NQH a query head,
+// then NKH key heads, then NKH value heads. The per-head arithmetic is the
+// shared head_norm_rope, so q/k/v and the stored f16 rows are bit-identical
+// to the four reference kernels run in order. Launch-bound by nature
+// (NQH + 2*NKH workgroups of 256 threads), so fusing the four passes into
+// one removes three launches per producer layer.
+#include "ref_math.h"
+
+namespace g4 {
+
+__global__ __launch_bounds__(kWG) void k_attn_prep(float* __restrict__ q, float* __restrict__ k, float* __restrict__ v,
+                                                   const uint16_t* __restrict__ q_weight,
+                                                   const uint16_t* __restrict__ k_weight,
+                                                   const uint16_t* __restrict__ rope_freqs,
+                                                   uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache,
+                                                   g4_prep_params p) {
+    __shared__ float shared_sum[kWG];
+    const unsigned b = blockIdx.x;
+    const unsigned hd = p.head_dim;
+    if (b < p.num_q_heads) {
+        head_norm_rope(q + b * hd, q_weight, true, rope_freqs, hd, p.eps, p.position, p.theta, p.apply_divisor,
+                       shared_sum);
+        return;
+    }
+    const unsigned r = b - p.num_q_heads;
+    const bool is_k = r < p.num_kv_heads;
+    const unsigned h = is_k ? r : r - p.num_kv_heads;
+    float* x = (is_k ? k : v) + h * hd;
+    if (is_k) {
+        head_norm_rope(x, k_weight, true, rope_freqs, hd, p.eps, p.position, p.theta, p.apply_divisor, shared_sum);
+    } else {
+        head_norm_rope(x, nullptr, false, nullptr, hd, p.eps, 0, 0.0f, 0, shared_sum);
+    }
+    __syncthreads();  // the row written above is read back by other threads
+    uint16_t* dst = (is_k ? k_cache : v_cache) + ((uint64_t)p.slot * p.num_kv_heads + h) * hd;
+    for (unsigned i = threadIdx.x; i < hd; i += kWG) dst[i] = f2h(x[i]);
+}
+
+// Many layers: blockIdx.y selects the layer's table entry.
+__global__ __launch_bounds__(kWG) void k_attn_prep_many(const g4_prep_layer* __restrict__ layers,
+                                                        uint32_t num_q_heads, uint32_t num_kv_heads, float eps,
+                                                        uint32_t position, uint32_t slot) {
+    __shared__ float shared_sum[kWG];
+    const g4_prep_layer L = layers[blockIdx.y];
+    const unsigned b = blockIdx.x;
+    const unsigned hd = L.head_dim;
+    if (b < num_q_heads) {
+        head_norm_rope(L.q + b * hd, L.q_weight, true, L.rope_freqs, hd, eps, position, L.theta, L.apply_divisor,
+                       shared_sum);
+        return;
+    }
+    if (!L.store_kv || slot >= L.max_seq_len) return;
+    const unsigned r = b - num_q_heads;
+    const bool is_k = r < num_kv_heads;
+    const unsigned h = is_k ? r : r - num_kv_heads;
+    float* x = (is_k ? L.k : L.v) + h * hd;
+    if (is_k) {
+        head_norm_rope(x, L.k_weight, true, L.rope_freqs, hd, eps, position, L.theta, L.apply_divisor, shared_sum);
+    } else {
+        head_norm_rope(x, nullptr, false, nullptr, hd, eps, 0, 0.0f, 0, shared_sum);
+    }
+    __syncthreads();
+    uint16_t* dst = (is_k ? L.k_cache : L.v_cache) + ((uint64_t)slot * num_kv_heads + h) * hd;
+    for (unsigned i = threadIdx.x; i < hd; i += kWG) dst[i] = f2h(x[i]);
+}
+
+}  // namespace g4
+
+using namespace g4;
+
+extern "C" int g4_attn_prep_many(const g4_prep_layer* layers, uint32_t n_layers, uint32_t num_q_heads,
+                                 uint32_t num_kv_heads, float eps, uint32_t position, uint32_t slot,
+                                 void* stream) {
+    if (!layers) return fail(G4_EINVAL, "attnPrepMany: NULL layer table");
+    if (n_layers == 0) return G4_OK;
+    if (n_layers > 65535) return fail(G4_EINVAL, "attnPrepMany: %u layers (max 65535)", n_layers);
+    const unsigned blocks = num_q_heads + 2 * num_kv_heads;
+    if (blocks == 0) return G4_OK;
+    hipLaunchKernelGGL(k_attn_prep_many, dim3(blocks, n_layers), dim3(kWG), 0, as_stream(stream), layers,
+                       num_q_heads, num_kv_heads, eps, position, slot);
+    G4_CHECK_LAUNCH("attnPrepMany");
+    return G4_OK;
+}
+
+extern "C" int g4_attn_prep(float* q, float* k, float* v, const uint16_t* q_weight, const uint16_t* k_weight,
+                            const uint16_t* rope_freqs, uint16_t* k_cache, uint16_t* v_cache, g4_prep_params p,
+                            void* stream) {
+    if (!q || !q_weight) return fail(G4_EINVAL, "attnPrep: NULL q/q_weight");
+    if (p.head_dim == 0 || p.head_dim % 2) return fail(G4_EINVAL, "attnPrep: head_dim %u", p.head_dim);
+    if (p.apply_divisor && !rope_freqs) return fail(G4_EINVAL, "attnPrep: apply_divisor needs rope_freqs");
+    unsigned blocks = p.num_q_heads;
+    if (p.store_kv) {
+        if (!k || !v || !k_weight || !k_cache || !v_cache) return fail(G4_EINVAL, "attnPrep: store_kv with NULL k/v");
+        if (p.slot >= p.max_seq_len) return fail(G4_EINVAL, "attnPrep: slot %u >= max_seq_len %u", p.slot, p.max_seq_len);
+        blocks += 2 * p.num_kv_heads;
+    }
+    if (blocks == 0) return G4_OK;
+    hipLaunchKernelGGL(k_attn_prep, dim3(blocks), dim3(kWG), 0, as_stream(stream), q, k, v, q_weight, k_weight,
+                       rope_freqs, k_cache, v_cache, p);
+    G4_CHECK_LAUNCH("attnPrep");
+    return G4_OK;
+}

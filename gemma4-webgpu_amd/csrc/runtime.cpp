@@ -1,0 +1,107 @@
+// Device, stream and buffer entry points of the C ABI, and the per-thread
+// error slot behind g4_last_error(). These replace the WebGPU device, queue
+// and buffer calls the reference engine makes (src/engine.ts:350-353,
+// 402-437, 1347-1426); buffers stay owned by the caller.
+#include <stdarg.h>
+#include <string.h>
+
+#include "common.h"
+
+namespace g4 {
+
+static thread_local char t_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(t_err, sizeof t_err, fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(G4_EHIP, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
+}
+
+}  // namespace g4
+
+using namespace g4;
+
+extern "C" {
+
+const char* g4_last_error(void) { return t_err; }
+
+const char* g4_version(void) { return "g4attn 0.1 gfx950"; }
+
+int g4_device_count(int* count) {
+    if (!count) return fail(G4_EINVAL, "g4_device_count: count is NULL");
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess) n = 0;
+    *count = n;
+    return G4_OK;
+}
+
+int g4_set_device(int device) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n == 0) return fail(G4_ENODEV, "g4_set_device: no HIP device");
+    if (device < 0 || device >= n) return fail(G4_EINVAL, "g4_set_device: device %d out of range [0,%d)", device, n);
+    hipDeviceProp_t prop;
+    G4_CHECK_HIP(hipGetDeviceProperties(&prop, device));
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(G4_ENODEV, "g4_set_device: device %d is %s, this library is built for gfx950", device,
+                    prop.gcnArchName);
+    G4_CHECK_HIP(hipSetDevice(device));
+    return G4_OK;
+}
+
+int g4_stream_create(void** stream) {
+    if (!stream) return fail(G4_EINVAL, "g4_stream_create: stream is NULL");
+    hipStream_t s;
+    G4_CHECK_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    *stream = s;
+    return G4_OK;
+}
+
+int g4_stream_destroy(void* stream) {
+    if (!stream) return G4_OK;
+    G4_CHECK_HIP(hipStreamDestroy(as_stream(stream)));
+    return G4_OK;
+}
+
+int g4_stream_synchronize(void* stream) {
+    G4_CHECK_HIP(hipStreamSynchronize(as_stream(stream)));
+    return G4_OK;
+}
+
+int g4_malloc(void** dev_ptr, size_t bytes) {
+    if (!dev_ptr) return fail(G4_EINVAL, "g4_malloc: dev_ptr is NULL");
+    if (bytes == 0) return fail(G4_EINVAL, "g4_malloc: zero bytes");
+    G4_CHECK_HIP(hipMalloc(dev_ptr, bytes));
+    return G4_OK;
+}
+
+int g4_free(void* dev_ptr) {
+    if (!dev_ptr) return G4_OK;
+    G4_CHECK_HIP(hipFree(dev_ptr));
+    return G4_OK;
+}
+
+int g4_upload(void* dev_dst, size_t offset, const void* host_src, size_t bytes, void* stream) {
+    if (!dev_dst || (!host_src && bytes)) return fail(G4_EINVAL, "g4_upload: NULL pointer");
+    if (bytes == 0) return G4_OK;
+    G4_CHECK_HIP(hipMemcpyAsync(static_cast<char*>(dev_dst) + offset, host_src, bytes, hipMemcpyHostToDevice,
+                                as_stream(stream)));
+    return G4_OK;
+}
+
+int g4_download(void* host_dst, const void* dev_src, size_t offset, size_t bytes, void* stream) {
+    if (!host_dst || (!dev_src && bytes)) return fail(G4_EINVAL, "g4_download: NULL pointer");
+    if (bytes == 0) return G4_OK;
+    G4_CHECK_HIP(hipMemcpyAsync(host_dst, static_cast<const char*>(dev_src) + offset, bytes, hipMemcpyDeviceToHost,
+                                as_stream(stream)));
+    G4_CHECK_HIP(hipStreamSynchronize(as_stream(stream)));
+    return G4_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,151 @@
+"""ctypes declarations of the C ABI in include/g4attn.h.
+
+Loads gemma4-webgpu_amd/lib/libg4attn.so (built by gemma4-webgpu_amd/build.py).
+There is no fallback: if the library is missing, loading raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent.parent / "lib" / "libg4attn.so"
+
+G4_OK = 0
+G4_EINVAL = -1
+G4_EHIP = -2
+G4_ENOSPC = -3
+G4_ENODEV = -4
+
+
+class G4Error(RuntimeError):
+    def __init__(self, status: int, message: str):
+        super().__init__(f"g4attn status {status}: {message}")
+        self.status = status
+        self.message = message
+
+
+# ---- Params (reference uniform layouts, src/engine.ts:526-595) -------------
+
+class NormRopeParams(C.Structure):  # fused_per_head_norm_rope.wgsl:13
+    _fields_ = [("num_heads", C.c_uint32), ("head_dim", C.c_uint32), ("eps", C.c_float),
+                ("position", C.c_uint32), ("theta", C.c_float), ("apply_divisor", C.c_uint32)]
+
+
+class NormParams(C.Structure):  # per_head_rms_norm_no_weight.wgsl:8
+    _fields_ = [("num_heads", C.c_uint32), ("head_dim", C.c_uint32), ("eps", C.c_float), ("pad", C.c_uint32)]
+
+
+class KvStoreParams(C.Structure):  # kv_cache_store.wgsl:1
+    _fields_ = [("num_kv_heads", C.c_uint32), ("head_dim", C.c_uint32), ("position", C.c_uint32),
+                ("max_seq_len", C.c_uint32)]
+
+
+class AttnScoreParams(C.Structure):  # attn_score.wgsl:9
+    _fields_ = [("num_q_heads", C.c_uint32), ("num_kv_heads", C.c_uint32), ("head_dim", C.c_uint32),
+                ("seq_len", C.c_uint32), ("scale", C.c_float), ("sliding_window", C.c_uint32)]
+
+
+class SoftmaxParams(C.Structure):  # softmax.wgsl:1
+    _fields_ = [("num_heads", C.c_uint32), ("seq_len", C.c_uint32)]
+
+
+class AttnOutputParams(C.Structure):  # attn_output.wgsl:1
+    _fields_ = [("num_q_heads", C.c_uint32), ("num_kv_heads", C.c_uint32), ("head_dim", C.c_uint32),
+                ("seq_len", C.c_uint32)]
+
+
+class PrepParams(C.Structure):
+    _fields_ = [("num_q_heads", C.c_uint32), ("num_kv_heads", C.c_uint32), ("head_dim", C.c_uint32),
+                ("eps", C.c_float), ("position", C.c_uint32), ("theta", C.c_float),
+                ("apply_divisor", C.c_uint32), ("slot", C.c_uint32), ("max_seq_len", C.c_uint32),
+                ("store_kv", C.c_uint32)]
+
+
+class PrepLayer(C.Structure):
+    _fields_ = [("q", C.c_void_p), ("k", C.c_void_p), ("v", C.c_void_p), ("q_weight", C.c_void_p),
+                ("k_weight", C.c_void_p), ("rope_freqs", C.c_void_p), ("k_cache", C.c_void_p),
+                ("v_cache", C.c_void_p), ("head_dim", C.c_uint32), ("theta", C.c_float),
+                ("apply_divisor", C.c_uint32), ("store_kv", C.c_uint32), ("max_seq_len", C.c_uint32),
+                ("reserved", C.c_uint32 * 3)]
+
+
+class DecodeEntry(C.Structure):
+    _fields_ = [("q", C.c_void_p), ("k_cache", C.c_void_p), ("v_cache", C.c_void_p), ("out", C.c_void_p),
+                ("seq_len", C.c_uint32), ("sliding_window", C.c_uint32), ("scale", C.c_float),
+                ("reserved", C.c_uint32)]
+
+
+class DecodePlan(C.Structure):
+    _fields_ = [("opaque", C.c_uint64 * 8)]
+
+
+_P = C.c_void_p
+_U32 = C.c_uint32
+_SZ = C.c_size_t
+_INT = C.c_int
+
+# name -> argtypes (restype is int status for all but the two string getters)
+SIGNATURES: dict[str, list] = {
+    "g4_device_count": [C.POINTER(C.c_int)],
+    "g4_set_device": [_INT],
+    "g4_stream_create": [C.POINTER(C.c_void_p)],
+    "g4_stream_destroy": [_P],
+    "g4_stream_synchronize": [_P],
+    "g4_malloc": [C.POINTER(C.c_void_p), _SZ],
+    "g4_free": [_P],
+    "g4_upload": [_P, _SZ, _P, _SZ, _P],
+    "g4_download": [_P, _P, _SZ, _SZ, _P],
+    "g4_zero": [_P, _SZ, _P],
+    "g4_fused_per_head_norm_rope": [_P, _P, _P, NormRopeParams, _P],
+    "g4_per_head_rms_norm_no_weight": [_P, NormParams, _P],
+    "g4_kv_cache_store": [_P, _P, _P, _P, KvStoreParams, _P],
+    "g4_attn_score": [_P, _P, _P, AttnScoreParams, _P],
+    "g4_softmax": [_P, SoftmaxParams, _P],
+    "g4_attn_output": [_P, _P, _P, AttnOutputParams, _P],
+    "g4_attn_prep": [_P, _P, _P, _P, _P, _P, _P, _P, PrepParams, _P],
+    "g4_attn_prep_many": [_P, _U32, _U32, _U32, C.c_float, _U32, _U32, _P],
+    "g4_attn_decode_workspace_size": [_U32, _U32, _U32, _U32, C.POINTER(C.c_size_t)],
+    "g4_attn_decode": [_P, _P, _P, _P, AttnScoreParams, _P, _SZ, _P],
+    "g4_attn_decode_many_workspace_size": [_U32, _U32, _U32, _U32, C.c_uint64, C.POINTER(C.c_size_t)],
+    "g4_attn_decode_many_prepare": [C.POINTER(DecodeEntry), _U32, _U32, _U32, _U32, _P, _SZ,
+                                    C.POINTER(DecodePlan), _P],
+    "g4_attn_decode_many_run": [C.POINTER(DecodePlan), _P],
+    "g4_attn_decode_many_run_split": [C.POINTER(DecodePlan), _P],
+    "g4_attn_decode_many_run_merge": [C.POINTER(DecodePlan), _P],
+    "g4_attn_decode_many": [C.POINTER(DecodeEntry), _U32, _U32, _U32, _U32, _P, _SZ, _P],
+}
+STRING_FUNCS = ("g4_last_error", "g4_version")
+
+_lib: C.CDLL | None = None
+
+
+def load() -> C.CDLL:
+    """Load libg4attn.so once; raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    path = Path(os.environ.get("G4ATTN_LIB", LIB_PATH))
+    if not path.exists():
+        raise FileNotFoundError(f"{path} not built: run `python gemma4-webgpu_amd/build.py`")
+    lib = C.CDLL(str(path))
+    for name in STRING_FUNCS:
+        f = getattr(lib, name)
+        f.restype = C.c_char_p
+        f.argtypes = []
+    for name, args in SIGNATURES.items():
+        f = getattr(lib, name)
+        f.restype = C.c_int
+        f.argtypes = args
+    _lib = lib
+    return lib
+
+
+def check(status: int) -> None:
+    if status != G4_OK:
+        msg = load().g4_last_error().decode(errors="replace")
+        raise G4Error(status, msg)
+
+
+def call(name: str, *args) -> None:
+    check(getattr(load(), name)(*args))

@@ -1,0 +1,211 @@
+"""Tensor-level entry points over the C ABI (torch tensors on the HIP device).
+
+Names follow the reference's kernel registry (src/shaders.ts:43-74):
+fusedPerHeadNormRope, perHeadRmsNormNoWeight, kvCacheStore, attnScore,
+softmax, attnOutput; plus the fused attn_prep / attn_decode /
+attn_decode_many. Every wrapper checks device, dtype, contiguity and buffer
+sizes on the host before anything is enqueued, so a shape mismatch raises
+instead of reaching a kernel. torch is used for device memory and the
+current stream only; all arithmetic runs in libg4attn.so.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import torch
+
+from . import abi
+from .abi import (AttnOutputParams, AttnScoreParams, DecodeEntry, DecodePlan, KvStoreParams, NormParams,
+                  NormRopeParams, PrepLayer, PrepParams, SoftmaxParams)
+
+F16_TYPES = (torch.float16, torch.int16, torch.uint16)
+
+
+def _stream(stream=None) -> int:
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return int(stream.cuda_stream) if hasattr(stream, "cuda_stream") else int(stream)
+
+
+def _dev(t: torch.Tensor, name: str, dtypes, min_numel: int) -> int:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name}: expected a tensor")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name}: must be on the GPU, got {t.device}")
+    if t.dtype not in (dtypes if isinstance(dtypes, tuple) else (dtypes,)):
+        raise TypeError(f"{name}: dtype {t.dtype} not in {dtypes}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name}: must be contiguous")
+    if t.numel() < min_numel:
+        raise ValueError(f"{name}: {t.numel()} elements < {min_numel} required")
+    return t.data_ptr()
+
+
+def _f16(t, name, n):
+    return _dev(t, name, F16_TYPES, n)
+
+
+def _f32(t, name, n):
+    return _dev(t, name, torch.float32, n)
+
+
+# ---- the six reference kernels ---------------------------------------------
+
+def fused_per_head_norm_rope(data, weight, rope_freqs, num_heads, head_dim, eps, position, theta,
+                             apply_divisor, stream=None):
+    p = NormRopeParams(num_heads, head_dim, eps, position, theta, apply_divisor)
+    rf = _f16(rope_freqs, "rope_freqs", head_dim // 2) if apply_divisor else (
+        rope_freqs.data_ptr() if rope_freqs is not None else None)
+    abi.call("g4_fused_per_head_norm_rope", _f32(data, "data", num_heads * head_dim),
+             _f16(weight, "weight", head_dim), rf, p, _stream(stream))
+
+
+def per_head_rms_norm_no_weight(data, num_heads, head_dim, eps, stream=None):
+    p = NormParams(num_heads, head_dim, eps, 0)
+    abi.call("g4_per_head_rms_norm_no_weight", _f32(data, "data", num_heads * head_dim), p, _stream(stream))
+
+
+def kv_cache_store(k_in, v_in, k_cache, v_cache, num_kv_heads, head_dim, position, max_seq_len, stream=None):
+    n = num_kv_heads * head_dim
+    p = KvStoreParams(num_kv_heads, head_dim, position, max_seq_len)
+    need = (position + 1) * n
+    abi.call("g4_kv_cache_store", _f32(k_in, "k_in", n), _f32(v_in, "v_in", n), _f16(k_cache, "k_cache", need),
+             _f16(v_cache, "v_cache", need), p, _stream(stream))
+
+
+def attn_score(q, k_cache, scores, num_q_heads, num_kv_heads, head_dim, seq_len, scale, sliding_window,
+               stream=None):
+    p = AttnScoreParams(num_q_heads, num_kv_heads, head_dim, seq_len, scale, sliding_window)
+    abi.call("g4_attn_score", _f32(q, "q", num_q_heads * head_dim),
+             _f16(k_cache, "k_cache", seq_len * num_kv_heads * head_dim),
+             _f32(scores, "scores", num_q_heads * seq_len), p, _stream(stream))
+
+
+def softmax(scores, num_heads, seq_len, stream=None):
+    abi.call("g4_softmax", _f32(scores, "scores", num_heads * seq_len), SoftmaxParams(num_heads, seq_len),
+             _stream(stream))
+
+
+def attn_output(probs, v_cache, out, num_q_heads, num_kv_heads, head_dim, seq_len, stream=None):
+    p = AttnOutputParams(num_q_heads, num_kv_heads, head_dim, seq_len)
+    abi.call("g4_attn_output", _f32(probs, "probs", num_q_heads * seq_len),
+             _f16(v_cache, "v_cache", seq_len * num_kv_heads * head_dim),
+             _f32(out, "out", num_q_heads * head_dim), p, _stream(stream))
+
+
+# ---- fused paths ------------------------------------------------------------
+
+def attn_prep(q, k, v, q_weight, k_weight, rope_freqs, k_cache, v_cache, num_q_heads, num_kv_heads, head_dim,
+              eps, position, theta, apply_divisor, slot, max_seq_len, store_kv=True, stream=None):
+    p = PrepParams(num_q_heads, num_kv_heads, head_dim, eps, position, theta, apply_divisor, slot, max_seq_len,
+                   1 if store_kv else 0)
+    rf = _f16(rope_freqs, "rope_freqs", head_dim // 2) if apply_divisor else None
+    nkv = num_kv_heads * head_dim
+    if store_kv:
+        args = (_f32(k, "k", nkv), _f32(v, "v", nkv), _f16(k_weight, "k_weight", head_dim), rf,
+                _f16(k_cache, "k_cache", (slot + 1) * nkv), _f16(v_cache, "v_cache", (slot + 1) * nkv))
+        if k_cache.numel() < max_seq_len * nkv or v_cache.numel() < max_seq_len * nkv:
+            raise ValueError("attn_prep: caches smaller than max_seq_len rows")
+    else:
+        args = (None, None, None, rf, None, None)
+    k_ptr, v_ptr, kw_ptr, rf_ptr, kc_ptr, vc_ptr = args
+    abi.call("g4_attn_prep", _f32(q, "q", num_q_heads * head_dim), k_ptr, v_ptr,
+             _f16(q_weight, "q_weight", head_dim), kw_ptr, rf_ptr, kc_ptr, vc_ptr, p, _stream(stream))
+
+
+def make_prep_table(layers, num_q_heads, num_kv_heads, device):
+    """Validate per-layer prep bindings on the host and upload them as a device table.
+
+    layers: iterable of dicts with q, k, v, q_weight, k_weight, rope_freqs (or None), k_cache, v_cache
+    (tensors; k/v/k_weight/caches may be None when store_kv is False), head_dim, theta, apply_divisor,
+    store_kv, max_seq_len. Returns a uint8 device tensor holding the g4_prep_layer array.
+    """
+    layers = list(layers)
+    arr = (PrepLayer * len(layers))()
+    for i, L in enumerate(layers):
+        hd = int(L["head_dim"])
+        if hd <= 0 or hd % 2:
+            raise ValueError(f"layer {i}: head_dim {hd}")
+        store = bool(L["store_kv"])
+        nkv = num_kv_heads * hd
+        rf = L.get("rope_freqs")
+        if L["apply_divisor"] and rf is None:
+            raise ValueError(f"layer {i}: apply_divisor needs rope_freqs")
+        arr[i] = PrepLayer(
+            _f32(L["q"], f"layer {i} q", num_q_heads * hd),
+            _f32(L["k"], f"layer {i} k", nkv) if store else None,
+            _f32(L["v"], f"layer {i} v", nkv) if store else None,
+            _f16(L["q_weight"], f"layer {i} q_weight", hd),
+            _f16(L["k_weight"], f"layer {i} k_weight", hd) if store else None,
+            _f16(rf, f"layer {i} rope_freqs", hd // 2) if rf is not None else None,
+            _f16(L["k_cache"], f"layer {i} k_cache", L["max_seq_len"] * nkv) if store else None,
+            _f16(L["v_cache"], f"layer {i} v_cache", L["max_seq_len"] * nkv) if store else None,
+            hd, float(L["theta"]), int(L["apply_divisor"]), 1 if store else 0, int(L["max_seq_len"]),
+        )
+    host = torch.frombuffer(bytearray(bytes(arr)), dtype=torch.uint8)
+    return host.to(device)
+
+
+def attn_prep_many(table, n_layers, num_q_heads, num_kv_heads, eps, position, slot, stream=None):
+    abi.call("g4_attn_prep_many", _dev(table, "table", torch.uint8, n_layers * C.sizeof(PrepLayer)), n_layers,
+             num_q_heads, num_kv_heads, eps, position, slot, _stream(stream))
+
+
+def decode_workspace_bytes(num_q_heads, num_kv_heads, head_dim, max_seq_len) -> int:
+    n = C.c_size_t(0)
+    abi.call("g4_attn_decode_workspace_size", num_q_heads, num_kv_heads, head_dim, max_seq_len, C.byref(n))
+    return n.value
+
+
+def attn_decode(q, k_cache, v_cache, out, workspace, num_q_heads, num_kv_heads, head_dim, seq_len, scale=1.0,
+                sliding_window=0, stream=None):
+    p = AttnScoreParams(num_q_heads, num_kv_heads, head_dim, seq_len, scale, sliding_window)
+    rows = seq_len * num_kv_heads * head_dim
+    ws_ptr, ws_bytes = (None, 0) if workspace is None else (_dev(workspace, "workspace", torch.uint8, 0),
+                                                             workspace.numel())
+    abi.call("g4_attn_decode", _f32(q, "q", num_q_heads * head_dim), _f16(k_cache, "k_cache", rows),
+             _f16(v_cache, "v_cache", rows), _f32(out, "out", num_q_heads * head_dim), p, ws_ptr, ws_bytes,
+             _stream(stream))
+
+
+def decode_many_workspace_bytes(n_entries, num_q_heads, num_kv_heads, head_dim, total_rows) -> int:
+    n = C.c_size_t(0)
+    abi.call("g4_attn_decode_many_workspace_size", n_entries, num_q_heads, num_kv_heads, head_dim, total_rows,
+             C.byref(n))
+    return n.value
+
+
+def make_entries(items, num_q_heads, num_kv_heads, head_dim):
+    """items: iterable of (q, k_cache, v_cache, out, seq_len, sliding_window, scale)."""
+    items = list(items)
+    arr = (DecodeEntry * len(items))()
+    for i, (q, kc, vc, out, seq_len, window, scale) in enumerate(items):
+        rows = seq_len * num_kv_heads * head_dim
+        arr[i] = DecodeEntry(_f32(q, f"entry {i} q", num_q_heads * head_dim), _f16(kc, f"entry {i} k", rows),
+                             _f16(vc, f"entry {i} v", rows), _f32(out, f"entry {i} out", num_q_heads * head_dim),
+                             seq_len, window, scale, 0)
+    return arr
+
+
+def attn_decode_many_prepare(entries, num_q_heads, num_kv_heads, head_dim, workspace, stream=None) -> DecodePlan:
+    plan = DecodePlan()
+    abi.call("g4_attn_decode_many_prepare", entries, len(entries), num_q_heads, num_kv_heads, head_dim,
+             _dev(workspace, "workspace", torch.uint8, 0), workspace.numel(), C.byref(plan), _stream(stream))
+    return plan
+
+
+def attn_decode_many_run(plan: DecodePlan, stream=None):
+    abi.call("g4_attn_decode_many_run", C.byref(plan), _stream(stream))
+
+
+def attn_decode_many_run_split(plan: DecodePlan, stream=None):
+    abi.call("g4_attn_decode_many_run_split", C.byref(plan), _stream(stream))
+
+
+def attn_decode_many_run_merge(plan: DecodePlan, stream=None):
+    abi.call("g4_attn_decode_many_run_merge", C.byref(plan), _stream(stream))
+
+
+def attn_decode_many(entries, num_q_heads, num_kv_heads, head_dim, workspace, stream=None):
+    abi.call("g4_attn_decode_many", entries, len(entries), num_q_heads, num_kv_heads, head_dim,
+             _dev(workspace, "workspace", torch.uint8, 0), workspace.numel(), _stream(stream))

@@ -1,0 +1,259 @@
+/*
+ * g4attn.h — C ABI of the MI355X (gfx950) Gemma-4 attention library.
+ *
+ * Drop-in replacement for gemma4-webgpu's attention kernels: the six WGSL
+ * shaders registered in src/shaders.ts:43-74 and dispatched from
+ * src/engine.ts:2056-2095, plus the fused decode and prefill paths that the
+ * WGSL engine does not have. All signatures use plain pointers, sizes and POD
+ * structs; device buffers are opaque `void*` device addresses owned by the
+ * caller (the engine), as GPUBuffers are owned by GemmaEngineImpl
+ * (src/engine.ts:1347-1426) and only borrowed by the kernels.
+ *
+ * Conventions
+ *   - Every entry point returns 0 (G4_OK) or a negative status. The message of
+ *     the last failure on the calling thread is returned by g4_last_error().
+ *     WebGPU validation errors are asynchronous and silent; here a bad argument
+ *     is rejected before anything is enqueued.
+ *   - `stream` is a hipStream_t (NULL = the null stream). Kernel entry points
+ *     only enqueue; they never synchronise the host.
+ *   - Per-token fields (position, slot, seq_len) are passed by value and
+ *     captured at enqueue time. This gives the ordering WebGPU provides with
+ *     queue.writeBuffer before a later submit (src/engine.ts:1967-1987) without
+ *     mutable device uniforms, so two forwards may be in flight at once.
+ *   - Work vectors q/k/v/out are f32 [heads][head_dim] (src/engine.ts:1369-1371).
+ *     KV caches are f16 (IEEE binary16, round-to-nearest-even on store),
+ *     slot-major [max_seq][num_kv_heads][head_dim] (kv_cache_store.wgsl:15);
+ *     the WGSL caches hold the same layout in f32.
+ *   - Weights (q_norm / k_norm) and the rope_freqs table are f16, as the
+ *     reference binds them (fused_per_head_norm_rope.wgsl:15,17).
+ */
+#ifndef G4ATTN_H
+#define G4ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status ----------------------------------------------------------- */
+#define G4_OK 0
+#define G4_EINVAL (-1)  /* bad argument, rejected before enqueue */
+#define G4_EHIP (-2)    /* HIP runtime error */
+#define G4_ENOSPC (-3)  /* caller-provided workspace too small */
+#define G4_ENODEV (-4)  /* no usable gfx950 device */
+
+/* Message for the last non-zero status returned on this thread. */
+const char* g4_last_error(void);
+/* Library version string. */
+const char* g4_version(void);
+
+/* ---- device, streams, buffers ----------------------------------------- *
+ * Replace initWebGPU / device.createBuffer / queue.writeBuffer / mapAsync
+ * (src/engine.ts:350-353, 402-437, 1347-1426, 2309).                       */
+int g4_device_count(int* count);
+int g4_set_device(int device);
+int g4_stream_create(void** stream);
+int g4_stream_destroy(void* stream);
+int g4_stream_synchronize(void* stream);
+int g4_malloc(void** dev_ptr, size_t bytes);
+int g4_free(void* dev_ptr);
+/* queue.writeBuffer(buffer, offset, data): host -> device, ordered on stream. */
+int g4_upload(void* dev_dst, size_t offset, const void* host_src, size_t bytes, void* stream);
+/* copyBufferToBuffer + mapAsync: device -> host; returns after the copy is done. */
+int g4_download(void* host_dst, const void* dev_src, size_t offset, size_t bytes, void* stream);
+/* Zero `bytes` at dev_dst with a fill kernel (safe inside HIP graph capture). */
+int g4_zero(void* dev_dst, size_t bytes, void* stream);
+
+/* ---- Params: the reference's uniform structs, field for field -------- */
+
+/* fused_per_head_norm_rope.wgsl:13; built at src/engine.ts:583-588 */
+typedef struct g4_norm_rope_params {
+    uint32_t num_heads;
+    uint32_t head_dim;
+    float eps;
+    uint32_t position;
+    float theta;
+    uint32_t apply_divisor;
+} g4_norm_rope_params;
+
+/* per_head_rms_norm_no_weight.wgsl:8; built at src/engine.ts:539-541 */
+typedef struct g4_norm_params {
+    uint32_t num_heads;
+    uint32_t head_dim;
+    float eps;
+    uint32_t pad;
+} g4_norm_params;
+
+/* kv_cache_store.wgsl:1; built at src/engine.ts:548-550 */
+typedef struct g4_kv_store_params {
+    uint32_t num_kv_heads;
+    uint32_t head_dim;
+    uint32_t position; /* cache slot */
+    uint32_t max_seq_len;
+} g4_kv_store_params;
+
+/* attn_score.wgsl:9; built at src/engine.ts:562-567 */
+typedef struct g4_attn_score_params {
+    uint32_t num_q_heads;
+    uint32_t num_kv_heads;
+    uint32_t head_dim;
+    uint32_t seq_len;
+    float scale;
+    uint32_t sliding_window; /* 0 = full attention */
+} g4_attn_score_params;
+
+/* softmax.wgsl:1; built at src/engine.ts:493 */
+typedef struct g4_softmax_params {
+    uint32_t num_heads;
+    uint32_t seq_len;
+} g4_softmax_params;
+
+/* attn_output.wgsl:1; built at src/engine.ts:568-570 */
+typedef struct g4_attn_output_params {
+    uint32_t num_q_heads;
+    uint32_t num_kv_heads;
+    uint32_t head_dim;
+    uint32_t seq_len;
+} g4_attn_output_params;
+
+/* ---- the six reference kernels (registry names in src/shaders.ts:43-74) - *
+ * Same semantics, grids and reduction order as the WGSL; f16 caches.      */
+
+/* SHADERS.fusedPerHeadNormRope — fused_per_head_norm_rope.wgsl:20-64,
+ * dispatched at src/engine.ts:2078-2085. In place on data[num_heads*head_dim]. */
+int g4_fused_per_head_norm_rope(float* data, const uint16_t* weight, const uint16_t* rope_freqs,
+                                g4_norm_rope_params p, void* stream);
+
+/* SHADERS.perHeadRmsNormNoWeight — per_head_rms_norm_no_weight.wgsl:13-38,
+ * dispatched at src/engine.ts:2060-2066. In place. */
+int g4_per_head_rms_norm_no_weight(float* data, g4_norm_params p, void* stream);
+
+/* SHADERS.kvCacheStore — kv_cache_store.wgsl:8-18, dispatched at
+ * src/engine.ts:2089-2091. Writes row p.position of the f16 caches. */
+int g4_kv_cache_store(const float* k_in, const float* v_in, uint16_t* k_cache, uint16_t* v_cache,
+                      g4_kv_store_params p, void* stream);
+
+/* SHADERS.attnScore — attn_score.wgsl:15-40, dispatched at src/engine.ts:2092.
+ * scores[num_q_heads][seq_len] (head stride = seq_len). */
+int g4_attn_score(const float* q, const uint16_t* k_cache, float* scores, g4_attn_score_params p,
+                  void* stream);
+
+/* SHADERS.softmax — softmax.wgsl:7-46, dispatched at src/engine.ts:2093. In place. */
+int g4_softmax(float* scores, g4_softmax_params p, void* stream);
+
+/* SHADERS.attnOutput — attn_output.wgsl:7-23, dispatched at src/engine.ts:2094. */
+int g4_attn_output(const float* probs, const uint16_t* v_cache, float* out, g4_attn_output_params p,
+                   void* stream);
+
+/* ---- fused producer-side prep ----------------------------------------- *
+ * One launch for the vNorm -> fusedNormRope(Q, K) -> kvCacheStore sequence
+ * of src/engine.ts:2056-2091. Results are bit-identical to running the four
+ * reference kernels in that order. On KV-consumer layers (store_kv = 0, the
+ * layers that read a producer's cache, src/engine.ts:1518-1522) only Q is
+ * normalised and rotated and k/v/caches may be NULL.                        */
+typedef struct g4_prep_params {
+    uint32_t num_q_heads;
+    uint32_t num_kv_heads;
+    uint32_t head_dim;
+    float eps;
+    uint32_t position;      /* RoPE position */
+    float theta;
+    uint32_t apply_divisor; /* 1 on global layers: divide by rope_freqs[i] */
+    uint32_t slot;          /* cache row written (== position without a ring) */
+    uint32_t max_seq_len;
+    uint32_t store_kv;      /* 1 on producer layers */
+} g4_prep_params;
+
+int g4_attn_prep(float* q, float* k, float* v, const uint16_t* q_weight, const uint16_t* k_weight,
+                 const uint16_t* rope_freqs, uint16_t* k_cache, uint16_t* v_cache, g4_prep_params p,
+                 void* stream);
+
+/* Many layers' prep in one launch. `layers` is a DEVICE array of n_layers
+ * entries, built once by the engine (as bind groups are built once at init,
+ * src/engine.ts:1428-1923); position and slot are the per-token values.
+ * Grid: (num_q_heads + 2*num_kv_heads) x n_layers workgroups. The table is
+ * trusted: head_dim must be even and every pointer valid for its layer. A
+ * layer whose max_seq_len <= slot skips the store.                         */
+typedef struct g4_prep_layer {
+    float* q;
+    float* k;
+    float* v;
+    const uint16_t* q_weight;
+    const uint16_t* k_weight;
+    const uint16_t* rope_freqs;
+    uint16_t* k_cache;
+    uint16_t* v_cache;
+    uint32_t head_dim;
+    float theta;
+    uint32_t apply_divisor;
+    uint32_t store_kv;
+    uint32_t max_seq_len;
+    uint32_t reserved[3];
+} g4_prep_layer;
+
+int g4_attn_prep_many(const g4_prep_layer* layers, uint32_t n_layers, uint32_t num_q_heads,
+                      uint32_t num_kv_heads, float eps, uint32_t position, uint32_t slot, void* stream);
+
+/* ---- fused decode attention (attnScore -> softmax -> attnOutput) ------- *
+ * Flash-decoding on MFMA: one pass over the K/V rows of the attended range
+ * (the whole cache on global layers, the last sliding_window rows on local
+ * layers), split across workgroups, merged with a fixed-order log-sum-exp.
+ * out[num_q_heads][head_dim] equals the reference chain's attnOut within
+ * floating-point rounding. Requires head_dim == 256 and
+ * num_q_heads / num_kv_heads <= 8. The workspace holds the split partials;
+ * g4_attn_decode_workspace_size gives the bytes needed for seq_len up to
+ * max_seq_len (allocate once, like attnScores at src/engine.ts:1375).      */
+int g4_attn_decode_workspace_size(uint32_t num_q_heads, uint32_t num_kv_heads, uint32_t head_dim,
+                                  uint32_t max_seq_len, size_t* bytes);
+int g4_attn_decode(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, float* out,
+                   g4_attn_score_params p, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- many independent decode problems in one launch ------------------- *
+ * Each entry is one (query block, KV cache, length) problem: the layers of
+ * one token's attention stack when their queries are available together, or
+ * the sequences of a ragged batch (each with its own cache and length; the
+ * engine has one sequence, src/engine.ts:116, so batching is new here).
+ * Splits are sized so the whole set fills the GPU; ragged lengths get
+ * proportional numbers of workgroups.                                       */
+typedef struct g4_decode_entry {
+    const float* q;          /* [num_q_heads][head_dim] f32 */
+    const uint16_t* k_cache; /* f16 [rows][num_kv_heads][head_dim] */
+    const uint16_t* v_cache;
+    float* out;              /* [num_q_heads][head_dim] f32 */
+    uint32_t seq_len;        /* valid rows */
+    uint32_t sliding_window; /* 0 = full */
+    float scale;
+    uint32_t reserved;
+} g4_decode_entry;
+
+/* Workspace for up to n_entries problems attending total_rows rows in all. */
+int g4_attn_decode_many_workspace_size(uint32_t n_entries, uint32_t num_q_heads, uint32_t num_kv_heads,
+                                       uint32_t head_dim, uint64_t total_rows, size_t* bytes);
+
+/* A prepared launch: the split table lives in the workspace. Prepare when the
+ * entries change (each token, as the engine rewrites seq_len uniforms each
+ * token, src/engine.ts:1980-1987); run as often as wanted. Running a plan
+ * while another prepare on the same workspace is pending is a race. */
+typedef struct g4_decode_plan {
+    uint64_t opaque[8];
+} g4_decode_plan;
+
+int g4_attn_decode_many_prepare(const g4_decode_entry* entries, uint32_t n_entries, uint32_t num_q_heads,
+                                uint32_t num_kv_heads, uint32_t head_dim, void* workspace, size_t workspace_bytes,
+                                g4_decode_plan* plan, void* stream);
+int g4_attn_decode_many_run(const g4_decode_plan* plan, void* stream);
+/* The two launches of g4_attn_decode_many_run, separately: the split pass,
+ * then the log-sum-exp merge of entries with more than one split. */
+int g4_attn_decode_many_run_split(const g4_decode_plan* plan, void* stream);
+int g4_attn_decode_many_run_merge(const g4_decode_plan* plan, void* stream);
+/* prepare + run. */
+int g4_attn_decode_many(const g4_decode_entry* entries, uint32_t n_entries, uint32_t num_q_heads,
+                        uint32_t num_kv_heads, uint32_t head_dim, void* workspace, size_t workspace_bytes,
+                        void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* G4ATTN_H */
