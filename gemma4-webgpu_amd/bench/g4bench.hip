@@ -1,0 +1,264 @@
+// g4bench: command-line driver of the decode path over the C ABI, with no
+// Python or torch in the process (so it runs cleanly under rocprofv3
+// counter collection). Inputs are synthetic: f16 cache rows from a
+// counter-based hash (values in [-2, 2), unit-RMS scale), queries likewise.
+//
+//   g4bench [--workload stack8k|stack32k|long128k|ragged64|layer512|copy] [--iters N] [--sets S]
+//
+// `copy` runs a plain 512 MiB device copy kernel instead: the reference for
+// scaling FETCH_SIZE / WRITE_SIZE counter readings to bytes.
+//
+// Each iteration runs, on one stream: the multi-layer prep (when the workload
+// has one position for all entries), the split pass and the merge pass of a
+// prepared multi-entry decode plan, rotating over S cache sets.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <string>
+#include <vector>
+
+#include "../../include/g4attn.h"
+
+#define CK(x)                                                                       \
+    do {                                                                            \
+        int rc_ = (x);                                                              \
+        if (rc_) {                                                                  \
+            fprintf(stderr, "%s failed: %d %s\n", #x, rc_, g4_last_error());        \
+            exit(1);                                                                \
+        }                                                                           \
+    } while (0)
+#define HK(x)                                                                       \
+    do {                                                                            \
+        hipError_t e_ = (x);                                                        \
+        if (e_ != hipSuccess) {                                                     \
+            fprintf(stderr, "%s failed: %s\n", #x, hipGetErrorString(e_));          \
+            exit(1);                                                                \
+        }                                                                           \
+    } while (0)
+
+static const unsigned NQH = 8, NKH = 1, HD = 256;
+
+__device__ __forceinline__ float hash_unit(uint64_t x) {  // splitmix64 finaliser -> [-2, 2)
+    x += 0x9E3779B97F4A7C15ull;
+    x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+    x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+    x ^= x >> 31;
+    return (float)((x >> 40) * (1.0 / 16777216.0)) * 4.0f - 2.0f;
+}
+
+__global__ void k_fill_f16(_Float16* p, uint64_t n, uint64_t seed) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
+        p[i] = (_Float16)(hash_unit(seed * 0x100000001B3ull + i) * 0.866f);  // uniform[-2,2) has RMS 1.155
+}
+__global__ void k_fill_f32(float* p, uint64_t n, uint64_t seed) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
+        p[i] = hash_unit(seed * 0x100000001B3ull + i) * 0.866f;
+}
+
+// Plain copy of n 16-byte words: the counter calibration reference (reads and
+// writes exactly n * 16 bytes each).
+__global__ void k_copy(uint4* __restrict__ dst, const uint4* __restrict__ src, uint64_t n) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
+        dst[i] = src[i];
+}
+
+static int run_copy(int iters) {
+    const uint64_t bytes = 512ull << 20;
+    void *src, *dst;
+    CK(g4_malloc(&src, bytes));
+    CK(g4_malloc(&dst, bytes));
+    hipEvent_t a, b;
+    HK(hipEventCreate(&a));
+    HK(hipEventCreate(&b));
+    hipLaunchKernelGGL(k_copy, dim3(4096), dim3(256), 0, 0, (uint4*)dst, (const uint4*)src, bytes / 16);
+    HK(hipDeviceSynchronize());
+    HK(hipEventRecord(a, 0));
+    for (int i = 0; i < iters; i++)
+        hipLaunchKernelGGL(k_copy, dim3(4096), dim3(256), 0, 0, (uint4*)dst, (const uint4*)src, bytes / 16);
+    HK(hipEventRecord(b, 0));
+    HK(hipEventSynchronize(b));
+    float ms = 0;
+    HK(hipEventElapsedTime(&ms, a, b));
+    printf("copy: %llu bytes read + written per launch, %.1f GB/s (read+write)\n", (unsigned long long)bytes,
+           2.0 * bytes * iters / (ms * 1e-3) / 1e9);
+    return 0;
+}
+
+struct Layer {
+    unsigned seq, window, pos;
+    float theta;
+    unsigned divisor;
+};
+
+static std::vector<Layer> workload(const std::string& w) {
+    std::vector<Layer> L;
+    if (w == "stack8k" || w == "stack32k") {
+        unsigned pos = w == "stack8k" ? 8192 : 32768;
+        for (int i = 0; i < 35; i++) {
+            bool global = (i % 5) == 4;
+            L.push_back({pos + 1, global ? 0u : 512u, pos, global ? 1e6f : 1e4f, global ? 1u : 0u});
+        }
+    } else if (w == "long128k") {
+        L.push_back({131072, 0, 131071, 1e6f, 1});
+    } else if (w == "layer512") {
+        L.push_back({513, 512, 512, 1e4f, 0});
+    } else if (w == "ragged64") {
+        uint64_t s = 20261203;
+        for (int i = 0; i < 64; i++) {  // lengths in [1024, 32768]
+            s = s * 6364136223846793005ull + 1442695040888963407ull;
+            unsigned len = 1024 + (unsigned)((s >> 33) % (32768 - 1024 + 1));
+            L.push_back({len, 0, len - 1, 1e6f, 1});
+        }
+    } else {
+        fprintf(stderr, "unknown workload %s\n", w.c_str());
+        exit(2);
+    }
+    return L;
+}
+
+int main(int argc, char** argv) {
+    std::string wl = "stack8k", mode = "step";
+    int iters = 50, sets = 0;
+    for (int i = 1; i < argc; i++) {
+        if (!strcmp(argv[i], "--workload") && i + 1 < argc) wl = argv[++i];
+        else if (!strcmp(argv[i], "--iters") && i + 1 < argc) iters = atoi(argv[++i]);
+        else if (!strcmp(argv[i], "--sets") && i + 1 < argc) sets = atoi(argv[++i]);
+        else if (!strcmp(argv[i], "--mode") && i + 1 < argc) mode = argv[++i];
+        else {
+            fprintf(stderr, "usage: g4bench [--workload W] [--mode step|unfused] [--iters N] [--sets S]\n");
+            return 2;
+        }
+    }
+    CK(g4_set_device(0));
+    if (wl == "copy") return run_copy(iters);
+    std::vector<Layer> L = workload(wl);
+    const bool uniform_pos = wl.rfind("stack", 0) == 0 || L.size() == 1;
+    uint64_t step_bytes = 0, total_rows = 0;
+    for (auto& l : L) {
+        unsigned att = l.window && l.seq > l.window ? l.window : l.seq;
+        total_rows += att;
+        step_bytes += 2ull * att * NKH * HD * 2 + NQH * HD * 4 * 2;
+    }
+    if (sets <= 0) sets = step_bytes >= (64ull << 20) ? (int)((512ull << 20) / step_bytes) + 1 : 1;
+    printf("workload %s: %zu entries, %.1f MB/step, %d sets\n", wl.c_str(), L.size(), step_bytes / 1e6, sets);
+
+    hipStream_t st;
+    HK(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
+    std::vector<uint16_t> rf(256), ones(HD, 0x3C00);
+    for (int i = 0; i < 256; i++) rf[i] = i < 64 ? 0x3C00 : 0x7C00;
+    void *d_rf, *d_ones;
+    CK(g4_malloc(&d_rf, 512));
+    CK(g4_malloc(&d_ones, HD * 2));
+    CK(g4_upload(d_rf, 0, rf.data(), 512, st));
+    CK(g4_upload(d_ones, 0, ones.data(), HD * 2, st));
+
+    struct Set {
+        std::vector<void*> bufs;
+        g4_decode_plan plan;       // unfused: prep + split + merge
+        g4_decode_plan step_plan;  // one-launch step
+        void* ws;
+        void* step_ws;
+        void* prep_table;
+    };
+    std::vector<Set> S(sets);
+    size_t ws_bytes = 0, step_ws_bytes = 0;
+    CK(g4_attn_decode_many_workspace_size((uint32_t)L.size(), NQH, NKH, HD, total_rows, &ws_bytes));
+    CK(g4_attn_step_workspace_size((uint32_t)L.size(), NQH, NKH, HD, &step_ws_bytes));
+    uint64_t seed = 1;
+    for (int s = 0; s < sets; s++) {
+        std::vector<g4_decode_entry> ents;
+        std::vector<g4_prep_layer> preps;
+        std::vector<g4_step_entry> steps;
+        for (auto& l : L) {
+            void *kc, *vc, *q, *k, *v, *out;
+            const size_t cache_bytes = (size_t)l.seq * NKH * HD * 2;
+            CK(g4_malloc(&kc, cache_bytes));
+            CK(g4_malloc(&vc, cache_bytes));
+            CK(g4_malloc(&q, NQH * HD * 4));
+            CK(g4_malloc(&k, NKH * HD * 4));
+            CK(g4_malloc(&v, NKH * HD * 4));
+            CK(g4_malloc(&out, NQH * HD * 4));
+            hipLaunchKernelGGL(k_fill_f16, dim3(1024), dim3(256), 0, st, (_Float16*)kc, (uint64_t)cache_bytes / 2, seed++);
+            hipLaunchKernelGGL(k_fill_f16, dim3(1024), dim3(256), 0, st, (_Float16*)vc, (uint64_t)cache_bytes / 2, seed++);
+            hipLaunchKernelGGL(k_fill_f32, dim3(8), dim3(256), 0, st, (float*)q, (uint64_t)NQH * HD, seed++);
+            hipLaunchKernelGGL(k_fill_f32, dim3(1), dim3(256), 0, st, (float*)k, (uint64_t)NKH * HD, seed++);
+            hipLaunchKernelGGL(k_fill_f32, dim3(1), dim3(256), 0, st, (float*)v, (uint64_t)NKH * HD, seed++);
+            S[s].bufs.insert(S[s].bufs.end(), {kc, vc, q, k, v, out});
+            ents.push_back({(const float*)q, (const uint16_t*)kc, (const uint16_t*)vc, (float*)out, l.seq, l.window,
+                            1.0f, 0});
+            g4_prep_layer p = {};
+            p.q = (float*)q;
+            p.k = (float*)k;
+            p.v = (float*)v;
+            p.q_weight = p.k_weight = (const uint16_t*)d_ones;
+            p.rope_freqs = (const uint16_t*)d_rf;
+            p.k_cache = (uint16_t*)kc;
+            p.v_cache = (uint16_t*)vc;
+            p.head_dim = HD;
+            p.theta = l.theta;
+            p.apply_divisor = l.divisor;
+            p.store_kv = 1;
+            p.max_seq_len = l.seq;
+            preps.push_back(p);
+            g4_step_entry se = {};
+            se.q = (const float*)q;
+            se.k = (const float*)k;
+            se.v = (const float*)v;
+            se.q_weight = se.k_weight = (const uint16_t*)d_ones;
+            se.rope_freqs = (const uint16_t*)d_rf;
+            se.k_cache = (uint16_t*)kc;
+            se.v_cache = (uint16_t*)vc;
+            se.out = (float*)out;
+            se.seq_len = l.seq;
+            se.position = l.pos;
+            se.sliding_window = l.window;
+            se.store_kv = 1;
+            se.theta = l.theta;
+            se.apply_divisor = l.divisor;
+            se.scale = 1.0f;
+            se.eps = 1e-6f;
+            steps.push_back(se);
+        }
+        HK(hipGetLastError());
+        CK(g4_malloc(&S[s].ws, ws_bytes));
+        CK(g4_malloc(&S[s].prep_table, preps.size() * sizeof(g4_prep_layer)));
+        CK(g4_upload(S[s].prep_table, 0, preps.data(), preps.size() * sizeof(g4_prep_layer), st));
+        CK(g4_attn_decode_many_prepare(ents.data(), (uint32_t)ents.size(), NQH, NKH, HD, S[s].ws, ws_bytes,
+                                       &S[s].plan, st));
+        CK(g4_malloc(&S[s].step_ws, step_ws_bytes));
+        CK(g4_attn_step_prepare(steps.data(), (uint32_t)steps.size(), NQH, NKH, HD, S[s].step_ws, step_ws_bytes,
+                                &S[s].step_plan, st));
+    }
+    CK(g4_stream_synchronize(st));
+
+    const bool fused = mode == "step";
+    auto step = [&](int i) {
+        Set& s = S[i % sets];
+        if (fused) {
+            CK(g4_attn_step_run(&s.step_plan, st));
+            return;
+        }
+        if (uniform_pos) CK(g4_attn_prep_many((const g4_prep_layer*)s.prep_table, (uint32_t)L.size(), NQH, NKH, 1e-6f,
+                                              L[0].pos, L[0].pos, st));
+        CK(g4_attn_decode_many_run_split(&s.plan, st));
+        CK(g4_attn_decode_many_run_merge(&s.plan, st));
+    };
+    for (int i = 0; i < 5; i++) step(i);
+    CK(g4_stream_synchronize(st));
+    hipEvent_t a, b;
+    HK(hipEventCreate(&a));
+    HK(hipEventCreate(&b));
+    HK(hipEventRecord(a, st));
+    for (int i = 0; i < iters; i++) step(i);
+    HK(hipEventRecord(b, st));
+    HK(hipEventSynchronize(b));
+    float ms = 0;
+    HK(hipEventElapsedTime(&ms, a, b));
+    const double us = ms * 1e3 / iters;
+    printf("%s [%s]: %.2f us/step, %.1f GB/s algorithmic (%d iterations)\n", wl.c_str(), mode.c_str(), us,
+           step_bytes / (us * 1e3), iters);
+    return 0;
+}

@@ -5,6 +5,7 @@
 Outputs (in-tree, so they travel with the source tree to a GPU host):
     gemma4-webgpu_amd/lib/libg4attn.so   C ABI declared in include/g4attn.h
     gemma4-webgpu_amd/lib/g4attn.node    Node N-API addon over the same ABI
+    gemma4-webgpu_amd/lib/g4bench        C++ decode benchmark driver over the same ABI
 
 Every HIP source is compiled for gfx950 only, with packed-FP32 instruction
 selection disabled (-packed-fp32-ops).
@@ -70,6 +71,16 @@ def build_library(jobs: int | None = None) -> Path:
     return out
 
 
+def build_bench() -> Path:
+    """g4bench: C++ driver of the decode path over the C ABI (no Python in the process)."""
+    src = PKG / "bench" / "g4bench.hip"
+    out = LIB / "g4bench"
+    tmp = LIB / "g4bench.tmp"
+    _run([HIPCC, *HIP_FLAGS, str(src), "-o", str(tmp), f"-L{LIB}", "-lg4attn", "-Wl,-rpath,$ORIGIN"])
+    os.replace(tmp, out)
+    return out
+
+
 def build_addon() -> Path | None:
     """Node N-API addon: a thin C++ shim that links libg4attn.so (no HIP code)."""
     src = PKG / "addon" / "g4attn_napi.cc"
@@ -87,6 +98,7 @@ def build_addon() -> Path | None:
 def main() -> None:
     lib = build_library()
     print(f"built {lib}")
+    print(f"built {build_bench()}")
     addon = build_addon()
     if addon:
         print(f"built {addon}")

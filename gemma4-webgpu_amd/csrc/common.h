@@ -38,9 +38,23 @@ typedef _Float16 f16;
 typedef f16 f16x8 __attribute__((ext_vector_type(8)));
 typedef f16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr float kLog2e = 1.4426950408889634f;
+
+// Loads and stores through the global address space (global_load/store with
+// an SGPR base), for pointers the compiler cannot prove global by itself.
+template <typename T>
+__device__ __forceinline__ T ldg(const void* p) {
+    typedef const __attribute__((address_space(1))) T* gp;
+    return *(gp)(p);
+}
+template <typename T>
+__device__ __forceinline__ void stg(void* p, T v) {
+    typedef __attribute__((address_space(1))) T* gp;
+    *(gp)(p) = v;
+}
 
 __device__ __forceinline__ float h2f(uint16_t h) {
     return static_cast<float>(__builtin_bit_cast(f16, h));

@@ -1,82 +1,24 @@
 // Fused decode attention for gfx950: attnScore -> softmax -> attnOutput of
 // gemma4-webgpu (shaders/attn_score.wgsl:15-40, softmax.wgsl:7-46,
 // attn_output.wgsl:7-23, dispatched at src/engine.ts:2092-2094) as one
-// flash-decoding pass over the attended K/V rows.
+// flash-decoding pass over the attended K/V rows, reading rows already in
+// the cache (the prep or kvCacheStore has stored the current row).
 //
-// Work decomposition
-//   One workgroup (4 waves) per (split, kv head). A split is a contiguous run
-//   of `chunk` cache rows of one problem ("entry": a layer of a token's stack,
-//   or a sequence of a ragged batch). Each wave walks 32-row tiles of the
-//   split, keeps an online softmax state, and the 4 waves are combined through
-//   LDS. A problem with one split writes its output directly; otherwise the
-//   split writes (m, l, o) partials and k_decode_merge combines them with a
-//   fixed-order log-sum-exp. All G <= 8 query heads of a kv head are served
-//   by one read of each K/V row (GQA: the reference re-reads K and V once per
-//   query head).
-//
-// MFMA mapping (v_mfma_f32_16x16x32_f16; lane = 16*g + n)
-//   Scores  S^T[16 keys x 16 cols] = K[16 keys x 32 d] * Qc^T[32 d x 16 cols].
-//           Columns 0..7 hold the f16 "hi" part of q*scale*log2(e) for query
-//           heads 0..7, columns 8..15 the f16 "lo" residual, so hi+lo carries
-//           ~22 mantissa bits and scores keep f32-level accuracy. Lane (n, g)
-//           supplies K[key n][d in 32c + 8g .. +8]: one 16-byte load.
-//   Output  O^T[16 d x 16 cols] += V^T[16 d x 32 keys] * P^T[32 keys x 16 cols],
-//           P split into hi/lo columns the same way. Lane (n, g) loads 8 full
-//           16-byte pieces of V rows (lanes n = 0..15 of a row read 256
-//           contiguous bytes) and transposes the 8x8 f16 block in registers
-//           with v_perm_b32, so no LDS staging is needed for K or V.
-//   The hi and lo columns are added with one DPP row rotation by 8.
-//
-// Masking: rows outside [key_begin, key_end) get score -inf (probability 0,
-// as exp(-1e30 - max) == 0 in the reference) and their loads are clamped to
-// the last valid row, so nothing outside the attended rows is read.
+// Work decomposition: one workgroup (4 waves) per (split, kv head). A split is
+// a contiguous run of `chunk` cache rows of one problem ("entry": a layer of a
+// token's stack, or a sequence of a ragged batch). Each wave walks 32-row
+// tiles of the split with an online softmax (decode_core.h), the 4 waves are
+// combined through LDS, and a problem with one split writes its output
+// directly; otherwise the split writes (m, l, o) partials and k_decode_merge
+// combines them with a fixed-order log-sum-exp. All G <= 8 query heads of a kv
+// head are served by one read of each K/V row (the reference re-reads K and V
+// once per query head).
 #include <stdlib.h>
 #include <string.h>
 
-#include "common.h"
+#include "decode_core.h"
 
 namespace g4 {
-
-constexpr int kDecodeWaves = 4;
-constexpr int kDecodeThreads = 64 * kDecodeWaves;
-constexpr int kTileKeys = 32;
-constexpr int kMaxGroup = 8;  // query heads per kv head served by one MFMA column block
-
-struct DecodeEntryDev {
-    const float* q;       // [num_kv_heads][group][HD]
-    const uint16_t* k;    // [rows][num_kv_heads][HD]
-    const uint16_t* v;
-    float* out;           // [num_kv_heads][group][HD]
-    uint32_t key_begin;   // first attended row
-    uint32_t key_end;     // one past the last attended row
-    uint32_t split_base;  // first split index of this entry
-    uint32_t n_splits;
-    float qscale;         // attention scale * log2(e)
-    uint32_t pad;
-};
-
-struct DecodeArgs {
-    const DecodeEntryDev* table;  // device table, or nullptr to use `one`
-    DecodeEntryDev one;
-    uint32_t n_entries;
-    uint32_t num_kv_heads;
-    uint32_t group;
-    uint32_t chunk;       // rows per split, multiple of kTileKeys
-    float* part_o;        // [split][kv_head][group][HD]
-    float* part_ml;       // [split][kv_head][group][2]
-};
-
-__device__ __forceinline__ float dpp_ror8_add(float x) {
-    int y = __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x128, 0xf, 0xf, false);  // row_ror:8
-    return x + __builtin_bit_cast(float, y);
-}
-
-__device__ __forceinline__ uint32_t perm_lo(uint32_t a, uint32_t b) {  // (a.lo16, b.lo16)
-    return __builtin_amdgcn_perm(b, a, 0x05040100u);
-}
-__device__ __forceinline__ uint32_t perm_hi(uint32_t a, uint32_t b) {  // (a.hi16, b.hi16)
-    return __builtin_amdgcn_perm(b, a, 0x07060302u);
-}
 
 __device__ __forceinline__ DecodeEntryDev find_entry(const DecodeArgs& a, unsigned split) {
     if (!a.table) return a.one;
@@ -90,28 +32,16 @@ __device__ __forceinline__ DecodeEntryDev find_entry(const DecodeArgs& a, unsign
 }
 
 template <int HD>
-__global__ __launch_bounds__(kDecodeThreads) void k_decode_split(DecodeArgs a) {
-    constexpr int NC = HD / 32;   // K chunks of 32 d per score MFMA chain
-    constexpr int NB = HD / 128;  // V blocks of 16 lanes x 8 d
-    constexpr int NO = NB * 8;    // output MFMA tiles of 16 d
-
-    __shared__ float lds_o[kDecodeWaves][NO * 4][32];
-    __shared__ float lds_m[kDecodeWaves][kMaxGroup];
-    __shared__ float lds_l[kDecodeWaves][kMaxGroup];
+__global__ __launch_bounds__(kDecodeThreads, 2) void k_decode_split(DecodeArgs a) {
+    using D = DecodeDims<HD>;
+    __shared__ DecodeSmem<HD> sm;
 
     const unsigned split = blockIdx.x;
     const unsigned kvh = blockIdx.y;
     const DecodeEntryDev ent = find_entry(a, split);
-    const float* __restrict__ qp = ent.q;
-    const uint16_t* __restrict__ kp = ent.k;
-    const uint16_t* __restrict__ vp = ent.v;
-    float* __restrict__ outp = ent.out;
-    const unsigned key_end = ent.key_end;
-    const unsigned n_splits = ent.n_splits;
-    const float qscale = ent.qscale;
     const unsigned s_local = split - ent.split_base;
     const unsigned k0 = ent.key_begin + s_local * a.chunk;
-    const unsigned k1 = min(key_end, k0 + a.chunk);
+    const unsigned k1 = min(ent.key_end, k0 + a.chunk);
     const unsigned G = a.group;
 
     const int lane = threadIdx.x & 63;
@@ -121,198 +51,153 @@ __global__ __launch_bounds__(kDecodeThreads) void k_decode_split(DecodeArgs a) {
     const int head = n & 7;
     const bool lo_col = n >= 8;
     const uint64_t row_stride = (uint64_t)a.num_kv_heads * HD;  // f16 elements per cache row
-    const uint16_t* K = kp + (uint64_t)kvh * HD;
-    const uint16_t* V = vp + (uint64_t)kvh * HD;
-
-    // Query operand: q * scale * log2(e), split into f16 hi + lo columns.
-    f16x8 qop[NC];
-    {
-        const float* qh = qp + ((uint64_t)kvh * G + head) * HD;
-        const bool live = (unsigned)head < G;
-#pragma unroll
-        for (int c = 0; c < NC; c++) {
-            f16x8 v;
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                float x = live ? qh[c * 32 + g * 8 + i] * qscale : 0.0f;
-                f16 hi = (f16)x;
-                v[i] = lo_col ? (f16)(x - (float)hi) : hi;
-            }
-            qop[c] = v;
-        }
-    }
-
-    float m_run = -INFINITY;
-    float l_run = 0.0f;
-    f32x4 acc[NO];
-#pragma unroll
-    for (int i = 0; i < NO; i++) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    const unsigned nkeys = k1 - k0;
+    // Byte offsets from the wave-uniform cache base stay 32-bit (caches are
+    // limited to 4 GiB on the host), so loads use an SGPR base + VGPR offset.
+    const char* Kb = reinterpret_cast<const char*>(ent.k + (uint64_t)kvh * HD);
+    const char* Vb = reinterpret_cast<const char*>(ent.v + (uint64_t)kvh * HD);
+    const uint32_t row_bytes = (uint32_t)row_stride * 2u;
     const unsigned last = k1 - 1;
-    for (unsigned t0 = (unsigned)wave * kTileKeys; t0 < nkeys; t0 += kDecodeWaves * kTileKeys) {
-        const unsigned kt0 = k0 + t0;
-        // ---- loads: K in score-operand layout, V as 16-byte row pieces ----
-        f16x8 kreg[2][NC];
-#pragma unroll
-        for (int h2 = 0; h2 < 2; h2++) {
-            const unsigned key = min(kt0 + h2 * 16 + n, last);
-            const uint16_t* row = K + key * row_stride + g * 8;
-#pragma unroll
-            for (int c = 0; c < NC; c++) kreg[h2][c] = *reinterpret_cast<const f16x8*>(row + c * 32);
-        }
-        u32x4 vreg[NB][8];
-#pragma unroll
-        for (int t = 0; t < 8; t++) {
-            const unsigned key = min(kt0 + (t < 4 ? g * 4 + t : 16 + g * 4 + (t - 4)), last);
-            const uint16_t* row = V + key * row_stride;
-#pragma unroll
-            for (int b = 0; b < NB; b++) vreg[b][t] = *reinterpret_cast<const u32x4*>(row + (n + 16 * b) * 8);
-        }
+    const unsigned nkeys = k1 - k0;
+    constexpr unsigned kStride = kDecodeWaves * kTileKeys;
 
-        // ---- scores (log2 units) ----
-        f32x4 s[2];
-#pragma unroll
-        for (int h2 = 0; h2 < 2; h2++) {
-            s[h2] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int c = 0; c < NC; c++) s[h2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kreg[h2][c], qop[c], s[h2], 0, 0, 0);
-        }
-        float sv[8];
-        float tmax = -INFINITY;
-#pragma unroll
-        for (int h2 = 0; h2 < 2; h2++)
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                float x = dpp_ror8_add(s[h2][j]);
-                const unsigned key = kt0 + h2 * 16 + g * 4 + j;
-                x = key < k1 ? x : -INFINITY;
-                sv[h2 * 4 + j] = x;
-                tmax = fmaxf(tmax, x);
-            }
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-        const float m_new = fmaxf(m_run, tmax);
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-        m_run = m_new;
-        f16x8 pop;
-        float psum = 0.0f;
-#pragma unroll
-        for (int t = 0; t < 8; t++) {
-            float p = __builtin_amdgcn_exp2f(sv[t] - m_new);
-            psum += p;
-            f16 hi = (f16)p;
-            pop[t] = lo_col ? (f16)(p - (float)hi) : hi;
-        }
-        l_run = l_run * alpha + psum;
-#pragma unroll
-        for (int i = 0; i < NO; i++) acc[i] *= alpha;
-
-        // ---- output: transpose each 8x8 f16 block of V, then MFMA ----
-#pragma unroll
-        for (int b = 0; b < NB; b++) {
-#pragma unroll
-            for (int e2 = 0; e2 < 4; e2++) {  // d pair (2*e2, 2*e2+1) lives in word e2 of every row piece
-                u32x4 lo, hi;
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    lo[q] = perm_lo(vreg[b][2 * q][e2], vreg[b][2 * q + 1][e2]);
-                    hi[q] = perm_hi(vreg[b][2 * q][e2], vreg[b][2 * q + 1][e2]);
-                }
-                acc[b * 8 + 2 * e2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, lo), pop,
-                                                                             acc[b * 8 + 2 * e2], 0, 0, 0);
-                acc[b * 8 + 2 * e2 + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, hi), pop,
-                                                                                 acc[b * 8 + 2 * e2 + 1], 0, 0, 0);
-            }
-        }
+    // Issue the first tile before the query is read, so both latencies overlap.
+    unsigned t0 = (unsigned)wave * kTileKeys;
+    f16x8 kreg[2][D::NC];
+    u32x4 vreg[D::NB][8];
+    if (t0 < nkeys) {
+        load_k_tile<HD>(Kb, row_bytes, last, n, g, k0 + t0, kreg);
+        load_v_tile<HD>(Vb, row_bytes, last, n, g, k0 + t0, vreg);
     }
 
-    // ---- per-wave totals: l over the 4 lane groups, hi+lo columns of o ----
-    l_run += __shfl_xor(l_run, 16);
-    l_run += __shfl_xor(l_run, 32);
+    // Query operand: q * scale * log2(e) as hi/lo f16 columns, built once per
+    // workgroup into LDS (all waves share it).
+    {
+        const bool live = (unsigned)head < G;
+        const float* qh = ent.q + ((uint64_t)kvh * G + (live ? head : 0)) * HD + g * 8;
+        const float qs = live ? ent.qscale : 0.0f;
 #pragma unroll
-    for (int i = 0; i < NO; i++)
+        for (int cc = 0; cc < D::NC / kDecodeWaves; cc++) {
+            const int c = wave * (D::NC / kDecodeWaves) + cc;
+            const f32x4 a4 = ldg<f32x4>(qh + c * 32);
+            const f32x4 b4 = ldg<f32x4>(qh + c * 32 + 4);
+            float x[8];
 #pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = dpp_ror8_add(acc[i][j]);
-    if (n < 8) {
-#pragma unroll
-        for (int i = 0; i < NO; i++)
-#pragma unroll
-            for (int j = 0; j < 4; j++) lds_o[wave][i * 4 + j][g * 8 + n] = acc[i][j];
-        if (g == 0) {
-            lds_m[wave][n] = m_run;
-            lds_l[wave][n] = l_run;
+            for (int i = 0; i < 8; i++) x[i] = (i < 4 ? a4[i] : b4[i - 4]) * qs;
+            store_q_chunk<HD>(sm, c, lane, x, lo_col);
         }
     }
     __syncthreads();
 
-    // ---- combine the 4 waves; write final output or the split partial ----
-    const int t = threadIdx.x;
-    const int lane32 = t & 31;
-    const int h = lane32 & 7;
-    const int gg = lane32 >> 3;
-    if ((unsigned)h >= G) return;
-    float mw[kDecodeWaves], M = -INFINITY;
+    float m_run = -INFINITY, l_run = 0.0f;
+    f32x4 acc[D::NO];
 #pragma unroll
-    for (int w = 0; w < kDecodeWaves; w++) {
-        mw[w] = lds_m[w][h];
-        M = fmaxf(M, mw[w]);
-    }
-    float L = 0.0f, sc[kDecodeWaves];
-#pragma unroll
-    for (int w = 0; w < kDecodeWaves; w++) {
-        sc[w] = __builtin_amdgcn_exp2f(mw[w] - M);
-        L += lds_l[w][h] * sc[w];
-    }
-    const bool final_out = n_splits == 1;
-    const float inv_l = 1.0f / L;
-    float* dst;
-    if (final_out) {
-        dst = outp + ((uint64_t)kvh * G + h) * HD;
-    } else {
-        const uint64_t pidx = ((uint64_t)split * a.num_kv_heads + kvh) * G + h;
-        dst = a.part_o + pidx * HD;
-        if (t < 32 && gg == 0) {
-            a.part_ml[pidx * 2 + 0] = M;
-            a.part_ml[pidx * 2 + 1] = L;
+    for (int i = 0; i < D::NO; i++) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (t0 < nkeys) {  // the first tile was requested above; the loop requests its own
+        tile_step<HD>(sm, lane, g, lo_col, k0 + t0, k1, kreg, vreg, m_run, l_run, acc);
+        for (t0 += kStride; t0 < nkeys; t0 += kStride) {
+            load_k_tile<HD>(Kb, row_bytes, last, n, g, k0 + t0, kreg);
+            load_v_tile<HD>(Vb, row_bytes, last, n, g, k0 + t0, vreg);
+            tile_step<HD>(sm, lane, g, lo_col, k0 + t0, k1, kreg, vreg, m_run, l_run, acc);
         }
     }
-    constexpr int kSlots = NO * 4;
-#pragma unroll
-    for (int sl = t >> 5; sl < kSlots; sl += kDecodeThreads / 32) {
-        float o = 0.0f;
-#pragma unroll
-        for (int w = 0; w < kDecodeWaves; w++) o += lds_o[w][sl][lane32] * sc[w];
-        const int i = sl >> 2, j = sl & 3;       // MFMA tile i = b*8 + e, row j
-        const int b = i >> 3, e = i & 7;
-        const int d = ((gg * 4 + j) + 16 * b) * 8 + e;
-        dst[d] = final_out ? o * inv_l : o;
-    }
+    wave_publish<HD>(sm, wave, n, g, m_run, l_run, acc);
+    __syncthreads();
+    const uint64_t pidx = ((uint64_t)split * a.num_kv_heads + kvh) * G;
+    wg_combine_write<HD>(sm, G, ent.n_splits == 1, ent.out + (uint64_t)kvh * G * HD, a.part_o + pidx * HD,
+                         a.part_ml + pidx * 2);
 }
 
-// Fixed-order log-sum-exp merge of the split partials of one entry.
+// Fixed-order log-sum-exp merge of the split partials: one workgroup per
+// (entry, kv head, query head). Each thread owns one output column d of one
+// of kGroups split groups (split s belongs to group s % kGroups). The first
+// batch of o partials is requested together with the per-split (m, l), so a
+// merge of up to kBatch * kGroups splits waits on memory once. Group sums are
+// added in group order, so the result does not depend on scheduling.
+constexpr int kMergeThreads = 1024;
+constexpr int kMaxMergeSplits = 8192;
+
 template <int HD>
-__global__ __launch_bounds__(256) void k_decode_merge(DecodeArgs a) {
+__global__ __launch_bounds__(kMergeThreads) void k_decode_merge(DecodeArgs a) {
+    constexpr int kGroups = kMergeThreads / HD;
+    constexpr int kBatch = 16;
+    constexpr int kWaves = kMergeThreads / 64;
+    __shared__ float sc[kMaxMergeSplits];
+    __shared__ float red[2][kWaves];
+    __shared__ float part[kGroups][HD];
     const DecodeEntryDev ent = a.table ? a.table[blockIdx.x] : a.one;
     const unsigned ns = ent.n_splits;
     if (ns <= 1) return;
-    const unsigned kvh = blockIdx.y;
-    const unsigned idx = blockIdx.z * 256 + threadIdx.x;
     const unsigned G = a.group;
-    if (idx >= G * HD) return;
-    const unsigned h = idx / HD, d = idx % HD;
-    const uint64_t stride = (uint64_t)a.num_kv_heads * G;  // partial records per split
-    const uint64_t base = ((uint64_t)ent.split_base * a.num_kv_heads + kvh) * G + h;
-    float M = -INFINITY;
-    for (unsigned s = 0; s < ns; s++) M = fmaxf(M, a.part_ml[(base + s * stride) * 2]);
-    float L = 0.0f, O = 0.0f;
-    for (unsigned s = 0; s < ns; s++) {
-        const uint64_t r = base + s * stride;
-        const float sc = __builtin_amdgcn_exp2f(a.part_ml[r * 2] - M);
-        L += a.part_ml[r * 2 + 1] * sc;
-        O += a.part_o[r * HD + d] * sc;
+    const unsigned kvh = blockIdx.y / G, h = blockIdx.y % G;
+    const unsigned t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const uint64_t rec_stride = (uint64_t)a.num_kv_heads * G;  // partial records per split
+    const uint64_t rec0 = ((uint64_t)ent.split_base * a.num_kv_heads + kvh) * G + h;
+    const unsigned grp = t / HD, d = t % HD;
+    const float* o = a.part_o + rec0 * HD + d;
+    const uint64_t o_stride = rec_stride * HD;
+
+    float v[kBatch];  // first batch of this thread's o partials, in flight during the (m, l) pass
+#pragma unroll
+    for (int u = 0; u < kBatch; u++) {
+        const unsigned s = grp + u * kGroups;
+        v[u] = s < ns ? ldg<float>(o + s * o_stride) : 0.0f;
     }
-    ent.out[((uint64_t)kvh * G + h) * HD + d] = O / L;
+    float mx = -INFINITY;
+    for (unsigned s = t; s < ns; s += kMergeThreads) {
+        const f32x2 ml = ldg<f32x2>(a.part_ml + (rec0 + s * rec_stride) * 2);
+        sc[s] = ml[0];
+        mx = fmaxf(mx, ml[0]);
+    }
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    if (lane == 0) red[0][wave] = mx;
+    __syncthreads();
+    float M = red[0][0];
+    for (int w = 1; w < kWaves; w++) M = fmaxf(M, red[0][w]);
+    float ls = 0.0f;
+    for (unsigned s = t; s < ns; s += kMergeThreads) {
+        const float f = __builtin_amdgcn_exp2f(sc[s] - M);
+        ls += ldg<float>(a.part_ml + (rec0 + s * rec_stride) * 2 + 1) * f;
+        sc[s] = f;
+    }
+    for (int off = 32; off > 0; off >>= 1) ls += __shfl_xor(ls, off);
+    if (lane == 0) red[1][wave] = ls;
+    __syncthreads();
+    float L = 0.0f;
+    for (int w = 0; w < kWaves; w++) L += red[1][w];
+
+    float acc = 0.0f;
+#pragma unroll
+    for (int u = 0; u < kBatch; u++) {
+        const unsigned s = grp + u * kGroups;
+        if (s < ns) acc += v[u] * sc[s];
+    }
+    for (unsigned s0 = grp + kBatch * kGroups; s0 < ns; s0 += kBatch * kGroups) {
+#pragma unroll
+        for (int u = 0; u < kBatch; u++) {
+            const unsigned s = s0 + u * kGroups;
+            v[u] = s < ns ? ldg<float>(o + s * o_stride) : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < kBatch; u++) {
+            const unsigned s = s0 + u * kGroups;
+            if (s < ns) acc += v[u] * sc[s];
+        }
+    }
+    part[grp][d] = acc;
+    __syncthreads();
+    if (grp == 0) {
+        float sum = part[0][d];
+#pragma unroll
+        for (int g2 = 1; g2 < kGroups; g2++) sum += part[g2][d];
+        stg<float>(ent.out + ((uint64_t)kvh * G + h) * HD + d, sum / L);
+    }
+}
+
+int launch_decode_merge(const DecodeArgs& a, unsigned n_entries, hipStream_t st) {
+    if (!n_entries) return G4_OK;
+    hipLaunchKernelGGL(k_decode_merge<256>, dim3(n_entries, a.num_kv_heads * a.group), dim3(kMergeThreads), 0, st, a);
+    G4_CHECK_LAUNCH("attnDecode merge");
+    return G4_OK;
 }
 
 }  // namespace g4
@@ -321,23 +206,34 @@ using namespace g4;
 
 namespace {
 
+int env_int(const char* name, int dflt) {
+    const char* s = getenv(name);
+    return s && *s ? atoi(s) : dflt;
+}
+
 constexpr unsigned kMinChunk = 128;
 constexpr unsigned kCUs = 256;
 
 inline unsigned round_up(unsigned x, unsigned m) { return (x + m - 1) / m * m; }
 
-// Rows per split: enough splits to put about two workgroups on every CU, but
-// never fewer than kMinChunk rows, so partial traffic stays small.
-unsigned pick_chunk(uint64_t total_rows, unsigned num_kv_heads) {
-    static int env = -1;
-    if (env < 0) {
-        const char* s = getenv("G4_DECODE_CHUNK");
-        env = s ? atoi(s) : 0;
+
+// Rows per split: about `wgs_per_cu` workgroups per CU over the whole launch
+// (G4_DECODE_WGS_PER_CU, default 2), never fewer than kMinChunk rows (so the
+// partials stay small next to the rows read), and never more than
+// kMaxMergeSplits splits for the longest entry. G4_DECODE_CHUNK overrides.
+unsigned pick_chunk(uint64_t total_rows, uint64_t max_entry_rows, unsigned num_kv_heads) {
+    static const int env_chunk = env_int("G4_DECODE_CHUNK", 0);
+    static const int wgs_per_cu = env_int("G4_DECODE_WGS_PER_CU", 2);
+    unsigned chunk;
+    if (env_chunk > 0) {
+        chunk = round_up((unsigned)env_chunk, kTileKeys);
+    } else {
+        const uint64_t target = (uint64_t)(wgs_per_cu > 0 ? wgs_per_cu : 2) * kCUs / (num_kv_heads ? num_kv_heads : 1);
+        const uint64_t c = (total_rows + target - 1) / (target ? target : 1);
+        chunk = round_up((unsigned)(c < kMinChunk ? kMinChunk : c), kTileKeys);
     }
-    if (env > 0) return round_up((unsigned)env, kTileKeys);
-    const uint64_t target = (uint64_t)2 * kCUs / (num_kv_heads ? num_kv_heads : 1);
-    uint64_t c = (total_rows + target - 1) / (target ? target : 1);
-    unsigned chunk = round_up((unsigned)(c < kMinChunk ? kMinChunk : c), kTileKeys);
+    const uint64_t floor_rows = (max_entry_rows + kMaxMergeSplits - 1) / kMaxMergeSplits;
+    if (chunk < floor_rows) chunk = round_up((unsigned)floor_rows, kTileKeys);
     return chunk;
 }
 
@@ -369,11 +265,7 @@ int launch_split(const DecodeArgs& a, unsigned total_splits, hipStream_t st) {
 }
 
 int launch_merge(const DecodeArgs& a, unsigned merge_entries, hipStream_t st) {
-    if (!merge_entries) return G4_OK;
-    const unsigned zb = (a.group * 256 + 255) / 256;
-    hipLaunchKernelGGL(k_decode_merge<256>, dim3(merge_entries, a.num_kv_heads, zb), dim3(256), 0, st, a);
-    G4_CHECK_LAUNCH("attnDecode merge");
-    return G4_OK;
+    return launch_decode_merge(a, merge_entries, st);
 }
 
 int launch(const DecodeArgs& a, unsigned total_splits, unsigned merge_entries, hipStream_t st) {
@@ -404,7 +296,7 @@ int g4_attn_decode(const float* q, const uint16_t* k_cache, const uint16_t* v_ca
     if (p.seq_len == 0) return fail(G4_EINVAL, "attnDecode: seq_len 0");
     uint32_t kb, ke;
     attended_range(p.seq_len, p.sliding_window, &kb, &ke);
-    const unsigned chunk = pick_chunk(ke - kb, p.num_kv_heads);
+    const unsigned chunk = pick_chunk(ke - kb, ke - kb, p.num_kv_heads);
     const unsigned ns = (ke - kb + chunk - 1) / chunk;
     const uint32_t group = p.num_q_heads / p.num_kv_heads;
     DecodeArgs a = {};
@@ -459,7 +351,7 @@ int g4_attn_decode_many_prepare(const g4_decode_entry* entries, uint32_t n_entri
     if (!plan) return fail(G4_EINVAL, "attnDecodeMany: plan is NULL");
     if (!entries || n_entries == 0) return fail(G4_EINVAL, "attnDecodeMany: no entries");
     if (n_entries > 65535) return fail(G4_EINVAL, "attnDecodeMany: %u entries (max 65535)", n_entries);
-    uint64_t total_rows = 0;
+    uint64_t total_rows = 0, max_rows = 0;
     for (uint32_t i = 0; i < n_entries; i++) {
         const g4_decode_entry& e = entries[i];
         if (!e.q || !e.k_cache || !e.v_cache || !e.out) return fail(G4_EINVAL, "attnDecodeMany: entry %u has NULL", i);
@@ -467,8 +359,9 @@ int g4_attn_decode_many_prepare(const g4_decode_entry* entries, uint32_t n_entri
         uint32_t kb, ke;
         attended_range(e.seq_len, e.sliding_window, &kb, &ke);
         total_rows += ke - kb;
+        if (ke - kb > max_rows) max_rows = ke - kb;
     }
-    const unsigned chunk = pick_chunk(total_rows, num_kv_heads);
+    const unsigned chunk = pick_chunk(total_rows, max_rows, num_kv_heads);
     const uint32_t group = num_q_heads / num_kv_heads;
     // Pinned staging for the table, reused once the previous upload has completed.
     static thread_local DecodeEntryDev* staging = nullptr;

@@ -1,0 +1,300 @@
+// Building blocks of the gfx950 flash-decoding kernels (decode.hip, step.hip):
+// the per-wave tile loop on MFMA and the per-workgroup combine of the four
+// waves' online-softmax states. Shared so that the unfused decode and the
+// fused one-launch step compute bit-identical attention.
+//
+// MFMA mapping (v_mfma_f32_16x16x32_f16; lane = 16*g + n)
+//   Scores  S^T[16 rows x 16 cols] = K[16 rows x 32 d] * Qc^T[32 d x 16 cols].
+//           Columns 0..7 hold the f16 "hi" part of q*scale*log2(e) for query
+//           heads 0..7, columns 8..15 the f16 "lo" residual, so hi+lo carries
+//           ~22 mantissa bits and scores keep f32-level accuracy. Lane (n, g)
+//           supplies K[row n][d in 32c + 8g .. +8]: one 16-byte load.
+//   Output  O^T[16 d x 16 cols] += V^T[16 d x 32 rows] * P^T[32 rows x 16 cols],
+//           P split into hi/lo columns the same way. Lane (n, g) loads 8
+//           16-byte pieces of V rows (lanes n = 0..15 of a row read 256
+//           contiguous bytes) and transposes the 8x8 f16 block in registers
+//           with v_perm_b32, so K and V go from HBM straight to registers.
+//   The hi and lo columns are added with one DPP row rotation by 8.
+// K and V rows are read once per token and never reused, so they are loaded
+// non-temporally (streaming loads measured ~10% faster than cached ones).
+#pragma once
+
+#include "common.h"
+
+namespace g4 {
+
+constexpr int kDecodeWaves = 4;
+constexpr int kDecodeThreads = 64 * kDecodeWaves;
+constexpr int kTileKeys = 32;
+constexpr int kMaxGroup = 8;  // query heads per kv head served by one MFMA column block
+
+template <typename T>
+__device__ __forceinline__ T ldg_stream(const void* p) {
+    typedef const __attribute__((address_space(1))) T* gp;
+    return __builtin_nontemporal_load((gp)(p));
+}
+
+__device__ __forceinline__ float dpp_ror8_add(float x) {
+    int y = __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x128, 0xf, 0xf, false);  // row_ror:8
+    return x + __builtin_bit_cast(float, y);
+}
+
+__device__ __forceinline__ uint32_t perm_lo(uint32_t a, uint32_t b) {  // (a.lo16, b.lo16)
+    return __builtin_amdgcn_perm(b, a, 0x05040100u);
+}
+__device__ __forceinline__ uint32_t perm_hi(uint32_t a, uint32_t b) {  // (a.hi16, b.hi16)
+    return __builtin_amdgcn_perm(b, a, 0x07060302u);
+}
+
+struct DecodeEntryDev {
+    const float* q;       // [num_kv_heads][group][HD]
+    const uint16_t* k;    // [rows][num_kv_heads][HD]
+    const uint16_t* v;
+    float* out;           // [num_kv_heads][group][HD]
+    uint32_t key_begin;   // first attended row
+    uint32_t key_end;     // one past the last attended row
+    uint32_t split_base;  // first split index of this entry
+    uint32_t n_splits;
+    float qscale;         // attention scale * log2(e)
+    uint32_t pad;
+};
+
+struct DecodeArgs {
+    const DecodeEntryDev* table;  // device table, or nullptr to use `one`
+    DecodeEntryDev one;
+    uint32_t n_entries;
+    uint32_t num_kv_heads;
+    uint32_t group;
+    uint32_t chunk;       // rows per split, multiple of kTileKeys
+    float* part_o;        // [split][kv_head][group][HD]
+    float* part_ml;       // [split][kv_head][group][2]
+};
+
+// Launches the fixed-order log-sum-exp merge of split partials (decode.hip)
+// for entries 0..n_entries-1 of a.table; entries with one split are skipped.
+int launch_decode_merge(const DecodeArgs& a, unsigned n_entries, hipStream_t st);
+
+template <int HD>
+struct DecodeDims {
+    static constexpr int NC = HD / 32;   // K chunks of 32 d per score MFMA chain
+    static constexpr int NB = HD / 128;  // V blocks of 16 lanes x 8 d
+    static constexpr int NO = NB * 8;    // output MFMA tiles of 16 d
+};
+
+// Workgroup memory of one decode workgroup.
+template <int HD>
+struct DecodeSmem {
+    f16x8 q[DecodeDims<HD>::NC][64];                       // score B operand, lane-major
+    float o[kDecodeWaves][DecodeDims<HD>::NO * 4][32];     // per-wave outputs for the combine
+    float m[kDecodeWaves][kMaxGroup];
+    float l[kDecodeWaves][kMaxGroup];
+};
+
+// Writes 8 consecutive q values (already times scale*log2(e)) of one column as
+// the lane's chunk c of the score operand: hi part in columns 0..7, lo in 8..15.
+template <int HD>
+__device__ __forceinline__ void store_q_chunk(DecodeSmem<HD>& sm, int c, int lane, const float (&x)[8], bool lo_col) {
+    f16x8 v;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const f16 hi = (f16)x[i];
+        v[i] = lo_col ? (f16)(x[i] - (float)hi) : hi;
+    }
+    sm.q[c][lane] = v;
+}
+
+// Tile loads. K in score-operand layout: lane (n, g) holds K[row n][32c + 8g .. +8].
+// Offsets are 32-bit bytes from the wave-uniform cache base of the kv head
+// (caches are limited to 4 GiB on the host), so loads use an SGPR base and a
+// VGPR offset. Rows beyond `last` are clamped to it.
+template <int HD>
+__device__ __forceinline__ void load_k_tile(const char* Kb, uint32_t row_bytes, unsigned last, int n, int g, unsigned kt0,
+                                            f16x8 (&kr)[2][DecodeDims<HD>::NC]) {
+#pragma unroll
+    for (int h2 = 0; h2 < 2; h2++) {
+        const uint32_t off = min(kt0 + h2 * 16 + n, last) * row_bytes + (uint32_t)g * 16u;
+#pragma unroll
+        for (int c = 0; c < DecodeDims<HD>::NC; c++) kr[h2][c] = ldg_stream<f16x8>(Kb + (off + c * 64u));
+    }
+}
+
+// V as 16-byte row pieces: lane (n, g) holds V[row(g, t)][8(n + 16b) .. +8],
+// row(g, t) = 4g + t for t < 4, 16 + 4g + (t - 4) otherwise.
+__device__ __forceinline__ unsigned v_row(int g, int t) { return t < 4 ? g * 4 + t : 16 + g * 4 + (t - 4); }
+
+template <int HD>
+__device__ __forceinline__ void load_v_tile(const char* Vb, uint32_t row_bytes, unsigned last, int n, int g, unsigned kt0,
+                                            u32x4 (&vr)[DecodeDims<HD>::NB][8]) {
+#pragma unroll
+    for (int t = 0; t < 8; t++) {
+        const uint32_t off = min(kt0 + v_row(g, t), last) * row_bytes + (uint32_t)n * 16u;
+#pragma unroll
+        for (int b = 0; b < DecodeDims<HD>::NB; b++) vr[b][t] = ldg_stream<u32x4>(Vb + (off + b * 256u));
+    }
+}
+
+// Replaces the pieces of row `row` (where loaded, including clamped loads) with
+// the given f16 row held in LDS: the current token's row, not yet in the cache.
+template <int HD>
+__device__ __forceinline__ void override_row(unsigned last, int n, int g, unsigned kt0, unsigned row,
+                                             const f16x8* knew, const f16x8* vnew,
+                                             f16x8 (&kr)[2][DecodeDims<HD>::NC], u32x4 (&vr)[DecodeDims<HD>::NB][8]) {
+#pragma unroll
+    for (int h2 = 0; h2 < 2; h2++)
+        if (min(kt0 + h2 * 16 + n, last) == row) {
+#pragma unroll
+            for (int c = 0; c < DecodeDims<HD>::NC; c++) kr[h2][c] = knew[c * 4 + g];
+        }
+#pragma unroll
+    for (int t = 0; t < 8; t++)
+        if (min(kt0 + v_row(g, t), last) == row) {
+#pragma unroll
+            for (int b = 0; b < DecodeDims<HD>::NB; b++) vr[b][t] = __builtin_bit_cast(u32x4, vnew[n + 16 * b]);
+        }
+}
+
+// Consumes one 32-row tile (already in registers) into a wave's online-softmax
+// state: running max m (log2 units) and sum l of its column, and the O^T
+// accumulators. Rows at or beyond `k1` are masked (probability 0, as
+// exp(-1e30 - max) == 0 in the reference); their loads were clamped in range.
+// (The state is passed as separate references: wrapped in a struct it is not
+// kept in registers and spills.)
+template <int HD>
+__device__ __forceinline__ void tile_step(const DecodeSmem<HD>& sm, int lane, int g, bool lo_col, unsigned kt0,
+                                          unsigned k1, const f16x8 (&kreg)[2][DecodeDims<HD>::NC],
+                                          const u32x4 (&vreg)[DecodeDims<HD>::NB][8], float& m_run, float& l_run,
+                                          f32x4 (&acc)[DecodeDims<HD>::NO]) {
+    constexpr int NC = DecodeDims<HD>::NC, NB = DecodeDims<HD>::NB, NO = DecodeDims<HD>::NO;
+    f32x4 s[2];
+#pragma unroll
+    for (int h2 = 0; h2 < 2; h2++) {
+        s[h2] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < NC; c++) s[h2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kreg[h2][c], sm.q[c][lane], s[h2], 0, 0, 0);
+    }
+    float sv[8];
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int h2 = 0; h2 < 2; h2++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            float x = dpp_ror8_add(s[h2][j]);
+            const unsigned row = kt0 + h2 * 16 + g * 4 + j;
+            x = row < k1 ? x : -INFINITY;
+            sv[h2 * 4 + j] = x;
+            tmax = fmaxf(tmax, x);
+        }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+    const float m_new = fmaxf(m_run, tmax);
+    if (__any(m_new > m_run)) {  // rescale only when some column's running max moved
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+        l_run *= alpha;
+#pragma unroll
+        for (int i = 0; i < NO; i++) acc[i] *= alpha;
+    }
+    m_run = m_new;
+    f16x8 pop;
+    float psum = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 8; t++) {
+        const float p = __builtin_amdgcn_exp2f(sv[t] - m_new);
+        psum += p;
+        const f16 hi = (f16)p;
+        pop[t] = lo_col ? (f16)(p - (float)hi) : hi;
+    }
+    l_run += psum;
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+#pragma unroll
+        for (int e2 = 0; e2 < 4; e2++) {  // d pair (2*e2, 2*e2+1) lives in word e2 of every row piece
+            u32x4 lo, hi;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                lo[q] = perm_lo(vreg[b][2 * q][e2], vreg[b][2 * q + 1][e2]);
+                hi[q] = perm_hi(vreg[b][2 * q][e2], vreg[b][2 * q + 1][e2]);
+            }
+            acc[b * 8 + 2 * e2] =
+                __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, lo), pop, acc[b * 8 + 2 * e2], 0, 0, 0);
+            acc[b * 8 + 2 * e2 + 1] =
+                __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, hi), pop, acc[b * 8 + 2 * e2 + 1], 0, 0, 0);
+        }
+    }
+}
+
+// Publishes a wave's final state to workgroup memory (sums over the 4 lane
+// groups, hi + lo columns added).
+template <int HD>
+__device__ __forceinline__ void wave_publish(DecodeSmem<HD>& sm, int wave, int n, int g, float m_run, float l_run,
+                                             f32x4 (&acc)[DecodeDims<HD>::NO]) {
+    constexpr int NO = DecodeDims<HD>::NO;
+    float l = l_run;
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+#pragma unroll
+    for (int i = 0; i < NO; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = dpp_ror8_add(acc[i][j]);
+    if (n < 8) {
+#pragma unroll
+        for (int i = 0; i < NO; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) sm.o[wave][i * 4 + j][g * 8 + n] = acc[i][j];
+        if (g == 0) {
+            sm.m[wave][n] = m_run;
+            sm.l[wave][n] = l;
+        }
+    }
+}
+
+// Combines the 4 waves (after a barrier) and writes either the normalised
+// output out[h][d] (final) or the unnormalised partial o[h][d] with (m, l)
+// per head, for the G heads of one kv head. Thread t covers lane32 = t & 31
+// (head t & 7, lane group (t >> 3) & 3) of 8 output slots.
+// `extra_m` (optional, per head, log2 units) with `extra_v` (one f16 row shared
+// by the heads) adds a fifth state holding a single row of weight 1: the
+// current token's row when it was not part of the tile loop.
+template <int HD>
+__device__ __forceinline__ void wg_combine_write(const DecodeSmem<HD>& sm, unsigned G, bool final_out, float* out,
+                                                 float* part_o, float* part_ml, const float* extra_m = nullptr,
+                                                 const f16* extra_v = nullptr) {
+    constexpr int NO = DecodeDims<HD>::NO;
+    const int t = threadIdx.x;
+    const int lane32 = t & 31;
+    const int h = lane32 & 7;
+    const int gg = lane32 >> 3;
+    if ((unsigned)h >= G) return;
+    float mw[kDecodeWaves], M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kDecodeWaves; w++) {
+        mw[w] = sm.m[w][h];
+        M = fmaxf(M, mw[w]);
+    }
+    const float me = extra_m ? extra_m[h] : -INFINITY;
+    M = fmaxf(M, me);
+    float L = 0.0f, sc[kDecodeWaves];
+#pragma unroll
+    for (int w = 0; w < kDecodeWaves; w++) {
+        sc[w] = __builtin_amdgcn_exp2f(mw[w] - M);
+        L += sm.l[w][h] * sc[w];
+    }
+    const float se = extra_m ? __builtin_amdgcn_exp2f(me - M) : 0.0f;
+    L += se;
+    const float inv_l = 1.0f / L;  // L includes the extra state
+    float* dst = final_out ? out + (uint64_t)h * HD : part_o + (uint64_t)h * HD;
+    if (!final_out && t < 32 && gg == 0) stg<f32x2>(part_ml + h * 2, f32x2{M, L});
+    constexpr int kSlots = NO * 4;
+#pragma unroll
+    for (int sl = t >> 5; sl < kSlots; sl += kDecodeThreads / 32) {
+        float o = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kDecodeWaves; w++) o += sm.o[w][sl][lane32] * sc[w];
+        const int i = sl >> 2, j = sl & 3;  // MFMA tile i = b*8 + e, row j
+        const int b = i >> 3, e = i & 7;
+        const int d = ((gg * 4 + j) + 16 * b) * 8 + e;
+        if (extra_m) o += (float)extra_v[d] * se;
+        stg<float>(dst + d, final_out ? o * inv_l : o);
+    }
+}
+
+}  // namespace g4

@@ -18,39 +18,37 @@ __global__ __launch_bounds__(kWG) void k_attn_prep(float* __restrict__ q, float*
                                                    const uint16_t* __restrict__ rope_freqs,
                                                    uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache,
                                                    g4_prep_params p) {
-    __shared__ float shared_sum[kWG];
+    __shared__ float scratch[kNormScratch];
     const unsigned b = blockIdx.x;
     const unsigned hd = p.head_dim;
     if (b < p.num_q_heads) {
         head_norm_rope(q + b * hd, q_weight, true, rope_freqs, hd, p.eps, p.position, p.theta, p.apply_divisor,
-                       shared_sum);
+                       scratch);
         return;
     }
     const unsigned r = b - p.num_q_heads;
     const bool is_k = r < p.num_kv_heads;
     const unsigned h = is_k ? r : r - p.num_kv_heads;
     float* x = (is_k ? k : v) + h * hd;
-    if (is_k) {
-        head_norm_rope(x, k_weight, true, rope_freqs, hd, p.eps, p.position, p.theta, p.apply_divisor, shared_sum);
-    } else {
-        head_norm_rope(x, nullptr, false, nullptr, hd, p.eps, 0, 0.0f, 0, shared_sum);
-    }
-    __syncthreads();  // the row written above is read back by other threads
     uint16_t* dst = (is_k ? k_cache : v_cache) + ((uint64_t)p.slot * p.num_kv_heads + h) * hd;
-    for (unsigned i = threadIdx.x; i < hd; i += kWG) dst[i] = f2h(x[i]);
+    if (is_k) {
+        head_norm_rope(x, k_weight, true, rope_freqs, hd, p.eps, p.position, p.theta, p.apply_divisor, scratch, dst);
+    } else {
+        head_norm_rope(x, nullptr, false, nullptr, hd, p.eps, 0, 0.0f, 0, scratch, dst);
+    }
 }
 
 // Many layers: blockIdx.y selects the layer's table entry.
 __global__ __launch_bounds__(kWG) void k_attn_prep_many(const g4_prep_layer* __restrict__ layers,
                                                         uint32_t num_q_heads, uint32_t num_kv_heads, float eps,
                                                         uint32_t position, uint32_t slot) {
-    __shared__ float shared_sum[kWG];
+    __shared__ float scratch[kNormScratch];
     const g4_prep_layer L = layers[blockIdx.y];
     const unsigned b = blockIdx.x;
     const unsigned hd = L.head_dim;
     if (b < num_q_heads) {
         head_norm_rope(L.q + b * hd, L.q_weight, true, L.rope_freqs, hd, eps, position, L.theta, L.apply_divisor,
-                       shared_sum);
+                       scratch);
         return;
     }
     if (!L.store_kv || slot >= L.max_seq_len) return;
@@ -58,14 +56,12 @@ __global__ __launch_bounds__(kWG) void k_attn_prep_many(const g4_prep_layer* __r
     const bool is_k = r < num_kv_heads;
     const unsigned h = is_k ? r : r - num_kv_heads;
     float* x = (is_k ? L.k : L.v) + h * hd;
-    if (is_k) {
-        head_norm_rope(x, L.k_weight, true, L.rope_freqs, hd, eps, position, L.theta, L.apply_divisor, shared_sum);
-    } else {
-        head_norm_rope(x, nullptr, false, nullptr, hd, eps, 0, 0.0f, 0, shared_sum);
-    }
-    __syncthreads();
     uint16_t* dst = (is_k ? L.k_cache : L.v_cache) + ((uint64_t)slot * num_kv_heads + h) * hd;
-    for (unsigned i = threadIdx.x; i < hd; i += kWG) dst[i] = f2h(x[i]);
+    if (is_k) {
+        head_norm_rope(x, L.k_weight, true, L.rope_freqs, hd, eps, position, L.theta, L.apply_divisor, scratch, dst);
+    } else {
+        head_norm_rope(x, nullptr, false, nullptr, hd, eps, 0, 0.0f, 0, scratch, dst);
+    }
 }
 
 }  // namespace g4

@@ -23,18 +23,18 @@ __global__ __launch_bounds__(kWG) void k_fused_per_head_norm_rope(float* __restr
                                                                   const uint16_t* __restrict__ weight,
                                                                   const uint16_t* __restrict__ rope_freqs,
                                                                   g4_norm_rope_params p) {
-    __shared__ float shared_sum[kWG];
+    __shared__ float scratch[kNormScratch];
     const unsigned head = blockIdx.x;
     if (head >= p.num_heads) return;
     head_norm_rope(data + head * p.head_dim, weight, true, rope_freqs, p.head_dim, p.eps, p.position, p.theta,
-                   p.apply_divisor, shared_sum);
+                   p.apply_divisor, scratch);
 }
 
 __global__ __launch_bounds__(kWG) void k_per_head_rms_norm_no_weight(float* __restrict__ data, g4_norm_params p) {
-    __shared__ float shared_sum[kWG];
+    __shared__ float scratch[kNormScratch];
     const unsigned head = blockIdx.x;
     if (head >= p.num_heads) return;
-    head_norm_rope(data + head * p.head_dim, nullptr, false, nullptr, p.head_dim, p.eps, 0, 0.0f, 0, shared_sum);
+    head_norm_rope(data + head * p.head_dim, nullptr, false, nullptr, p.head_dim, p.eps, 0, 0.0f, 0, scratch);
 }
 
 __global__ __launch_bounds__(kWG) void k_kv_cache_store(const float* __restrict__ k_in, const float* __restrict__ v_in,

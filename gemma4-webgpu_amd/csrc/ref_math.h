@@ -42,41 +42,122 @@ __device__ __forceinline__ float rope_angle(unsigned i, unsigned head_dim, float
     return (float)position * freq;
 }
 
+// The reference's 128 -> 1 tree over 256 partials with two LDS steps
+// (strides 128, 64) and wave shuffles for strides 32..1: the same operand
+// pairs are added, so the total is bit-identical to wg_tree_sum. The total is
+// returned to every thread. `s` holds at least 256 floats.
+__device__ __forceinline__ float wg_tree_sum_fast(float partial, float* s, unsigned tid) {
+    s[tid] = partial;
+    __syncthreads();
+    if (tid < 128) s[tid] = s[tid] + s[tid + 128];
+    __syncthreads();
+    if (tid < 64) {
+        float x = s[tid] + s[tid + 64];
+        for (int stride = 32; stride > 0; stride >>= 1) x = x + __shfl_down(x, stride);
+        if (tid == 0) s[256] = x;
+    }
+    __syncthreads();
+    return s[256];
+}
+
 // Per-head RMSNorm (optionally weighted) + RoPE of one head held in global
-// memory, by one 256-thread workgroup; fused_per_head_norm_rope.wgsl:23-63
+// memory, by one 256-thread workgroup: fused_per_head_norm_rope.wgsl:23-63
 // when `weight` is non-null and rope is on, per_head_rms_norm_no_weight.wgsl:
-// 15-37 when weight is null and rope is off. `shared_sum` is a 256-float
-// workgroup buffer.
+// 15-37 when weight is null and rope is off. When `f16_out` is non-null the
+// final values are also stored there as f16 (the KV-cache row). `scratch`
+// is a workgroup buffer of at least 257 + head_dim floats.
+//
+// head_dim <= 512: RoPE factors are computed first (they do not depend on the
+// data, so the f64 transcendental latency overlaps the load and reduction),
+// and the rotate-half pairs are exchanged through LDS. Larger heads take the
+// literal loop form. Both evaluate the same expressions as the WGSL.
 __device__ __forceinline__ void head_norm_rope(float* __restrict__ data, const uint16_t* __restrict__ weight,
                                                bool rope, const uint16_t* __restrict__ rope_freqs,
                                                unsigned head_dim, float eps, unsigned position, float theta,
-                                               unsigned apply_divisor, float* shared_sum) {
+                                               unsigned apply_divisor, float* scratch,
+                                               uint16_t* __restrict__ f16_out = nullptr) {
     const unsigned tid = threadIdx.x;
+    const unsigned half_dim = head_dim / 2u;
+    if (head_dim <= 2 * kWG) {
+        float cos_a = 1.0f, sin_a = 0.0f;
+        if (rope && tid < half_dim) {
+            const float angle = rope_angle(tid, head_dim, theta, position, apply_divisor, rope_freqs);
+            cos_a = (float)cos((double)angle);
+            sin_a = (float)sin((double)angle);
+        }
+        float xv[2] = {0.0f, 0.0f};
+        float partial = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+            const unsigned i = tid + r * kWG;
+            if (i < head_dim) {
+                xv[r] = data[i];
+                partial = partial + xv[r] * xv[r];
+            }
+        }
+        const float rms = sqrtf(wg_tree_sum_fast(partial, scratch, tid) / (float)head_dim + eps);
+        float* buf = scratch + 257;
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+            const unsigned i = tid + r * kWG;
+            if (i < head_dim) {
+                xv[r] = weight ? xv[r] * h2f(weight[i]) / rms : xv[r] / rms;
+                if (rope) {
+                    buf[i] = xv[r];
+                } else {
+                    data[i] = xv[r];
+                    if (f16_out) f16_out[i] = f2h(xv[r]);
+                }
+            }
+        }
+        if (!rope) return;
+        __syncthreads();
+        if (tid < half_dim) {
+            const float x0 = buf[tid];
+            const float x1 = buf[tid + half_dim];
+            const float y0 = x0 * cos_a - x1 * sin_a;
+            const float y1 = x0 * sin_a + x1 * cos_a;
+            data[tid] = y0;
+            data[tid + half_dim] = y1;
+            if (f16_out) {
+                f16_out[tid] = f2h(y0);
+                f16_out[tid + half_dim] = f2h(y1);
+            }
+        }
+        return;
+    }
     float partial = 0.0f;
     for (unsigned i = tid; i < head_dim; i += kWG) {
         float val = data[i];
         partial = partial + val * val;
     }
-    shared_sum[tid] = partial;
+    scratch[tid] = partial;
     __syncthreads();
-    const float rms = sqrtf(wg_tree_sum(shared_sum, tid) / (float)head_dim + eps);
+    const float rms = sqrtf(wg_tree_sum(scratch, tid) / (float)head_dim + eps);
     if (weight) {
         for (unsigned i = tid; i < head_dim; i += kWG) data[i] = data[i] * h2f(weight[i]) / rms;
     } else {
         for (unsigned i = tid; i < head_dim; i += kWG) data[i] = data[i] / rms;
     }
     __syncthreads();
-    if (!rope) return;
-    const unsigned half_dim = head_dim / 2u;
-    for (unsigned i = tid; i < half_dim; i += kWG) {
-        float angle = rope_angle(i, head_dim, theta, position, apply_divisor, rope_freqs);
-        float cos_a = (float)cos((double)angle);
-        float sin_a = (float)sin((double)angle);
-        float x0 = data[i];
-        float x1 = data[i + half_dim];
-        data[i] = x0 * cos_a - x1 * sin_a;
-        data[i + half_dim] = x0 * sin_a + x1 * cos_a;
+    if (rope) {
+        for (unsigned i = tid; i < half_dim; i += kWG) {
+            float angle = rope_angle(i, head_dim, theta, position, apply_divisor, rope_freqs);
+            float cos_a = (float)cos((double)angle);
+            float sin_a = (float)sin((double)angle);
+            float x0 = data[i];
+            float x1 = data[i + half_dim];
+            data[i] = x0 * cos_a - x1 * sin_a;
+            data[i + half_dim] = x0 * sin_a + x1 * cos_a;
+        }
+    }
+    if (f16_out) {
+        __syncthreads();
+        for (unsigned i = tid; i < head_dim; i += kWG) f16_out[i] = f2h(data[i]);
     }
 }
+
+// Workgroup scratch for head_norm_rope with head_dim <= 512.
+constexpr unsigned kNormScratch = 257 + 2 * kWG;
 
 }  // namespace g4

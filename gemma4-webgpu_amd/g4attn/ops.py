@@ -16,7 +16,7 @@ import torch
 
 from . import abi
 from .abi import (AttnOutputParams, AttnScoreParams, DecodeEntry, DecodePlan, KvStoreParams, NormParams,
-                  NormRopeParams, PrepLayer, PrepParams, SoftmaxParams)
+                  NormRopeParams, PrepLayer, PrepParams, SoftmaxParams, StepEntry)
 
 F16_TYPES = (torch.float16, torch.int16, torch.uint16)
 
@@ -208,4 +208,52 @@ def attn_decode_many_run_merge(plan: DecodePlan, stream=None):
 
 def attn_decode_many(entries, num_q_heads, num_kv_heads, head_dim, workspace, stream=None):
     abi.call("g4_attn_decode_many", entries, len(entries), num_q_heads, num_kv_heads, head_dim,
+             _dev(workspace, "workspace", torch.uint8, 0), workspace.numel(), _stream(stream))
+
+
+# ---- one-launch decode step --------------------------------------------------
+
+def step_workspace_bytes(n_entries, num_q_heads, num_kv_heads, head_dim) -> int:
+    n = C.c_size_t(0)
+    abi.call("g4_attn_step_workspace_size", n_entries, num_q_heads, num_kv_heads, head_dim, C.byref(n))
+    return n.value
+
+
+def make_step_entries(items, num_q_heads, num_kv_heads, head_dim):
+    """items: iterable of dicts with q, k, v (raw f32 projections), q_weight, k_weight (f16), rope_freqs (f16 or
+    None), k_cache, v_cache (f16, at least seq_len rows), out (f32), seq_len, position, sliding_window, store_kv,
+    theta, apply_divisor, scale, eps."""
+    items = list(items)
+    arr = (StepEntry * len(items))()
+    for i, it in enumerate(items):
+        L = int(it["seq_len"])
+        nkv = num_kv_heads * head_dim
+        rf = it.get("rope_freqs")
+        if it["apply_divisor"] and rf is None:
+            raise ValueError(f"entry {i}: apply_divisor needs rope_freqs")
+        arr[i] = StepEntry(
+            _f32(it["q"], f"entry {i} q", num_q_heads * head_dim), _f32(it["k"], f"entry {i} k", nkv),
+            _f32(it["v"], f"entry {i} v", nkv), _f16(it["q_weight"], f"entry {i} q_weight", head_dim),
+            _f16(it["k_weight"], f"entry {i} k_weight", head_dim),
+            _f16(rf, f"entry {i} rope_freqs", head_dim // 2) if rf is not None else None,
+            _f16(it["k_cache"], f"entry {i} k_cache", L * nkv), _f16(it["v_cache"], f"entry {i} v_cache", L * nkv),
+            _f32(it["out"], f"entry {i} out", num_q_heads * head_dim), L, int(it["position"]),
+            int(it.get("sliding_window", 0)), 1 if it.get("store_kv", True) else 0, float(it["theta"]),
+            int(it["apply_divisor"]), float(it.get("scale", 1.0)), float(it.get("eps", 1e-6)))
+    return arr
+
+
+def attn_step_prepare(entries, num_q_heads, num_kv_heads, head_dim, workspace, stream=None) -> DecodePlan:
+    plan = DecodePlan()
+    abi.call("g4_attn_step_prepare", entries, len(entries), num_q_heads, num_kv_heads, head_dim,
+             _dev(workspace, "workspace", torch.uint8, 0), workspace.numel(), C.byref(plan), _stream(stream))
+    return plan
+
+
+def attn_step_run(plan: DecodePlan, stream=None):
+    abi.call("g4_attn_step_run", C.byref(plan), _stream(stream))
+
+
+def attn_step(entries, num_q_heads, num_kv_heads, head_dim, workspace, stream=None):
+    abi.call("g4_attn_step", entries, len(entries), num_q_heads, num_kv_heads, head_dim,
              _dev(workspace, "workspace", torch.uint8, 0), workspace.numel(), _stream(stream))

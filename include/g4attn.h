@@ -253,6 +253,49 @@ int g4_attn_decode_many(const g4_decode_entry* entries, uint32_t n_entries, uint
                         uint32_t num_kv_heads, uint32_t head_dim, void* workspace, size_t workspace_bytes,
                         void* stream);
 
+/* ---- one-launch decode step ---------------------------------------------
+ * The whole attention block of one token for many layers or sequences in one
+ * launch: per entry, q RMSNorm + RoPE, the current row's k (norm + RoPE) and v
+ * (weightless norm), the f16 store of that row (store_kv = 1, KV-producer
+ * layers; consumers pass their producer's cache and raw k/v with
+ * store_kv = 0), and split-K attention over the attended rows with the
+ * current row taken from registers. It replaces the dispatch sequence
+ * vNorm, fusedNormRopeQK, kvCacheStore, attnScore, softmax, attnOutput of
+ * src/engine.ts:2056-2094. Unlike the reference kernels, q/k/v are read
+ * only (the raw projections stay in their buffers); attnOut is written.
+ * Work is split evenly over the GPU across all entries. head_dim 256,
+ * up to 8 query heads per kv head. Prepare when the entries change (each
+ * token); run as often as wanted. */
+typedef struct g4_step_entry {
+    const float* q;            /* raw projection [num_q_heads][head_dim] f32 */
+    const float* k;            /* raw projection [num_kv_heads][head_dim] f32 */
+    const float* v;
+    const uint16_t* q_weight;  /* attn_q_norm, f16 [head_dim] */
+    const uint16_t* k_weight;  /* attn_k_norm, f16 [head_dim] */
+    const uint16_t* rope_freqs; /* f16 divisor table, read when apply_divisor */
+    uint16_t* k_cache;         /* f16 [rows][num_kv_heads][head_dim]; rows < seq_len - 1 hold earlier tokens */
+    uint16_t* v_cache;
+    float* out;                /* attnOut [num_q_heads][head_dim] f32 */
+    uint32_t seq_len;          /* rows including the current token's (its row is seq_len - 1) */
+    uint32_t position;         /* RoPE position of the current token */
+    uint32_t sliding_window;   /* 0 = full */
+    uint32_t store_kv;         /* 1: write the current row to the caches */
+    float theta;
+    uint32_t apply_divisor;
+    float scale;               /* attention scale (1.0 for Gemma 4) */
+    float eps;
+} g4_step_entry;
+
+int g4_attn_step_workspace_size(uint32_t n_entries, uint32_t num_q_heads, uint32_t num_kv_heads, uint32_t head_dim,
+                                size_t* bytes);
+int g4_attn_step_prepare(const g4_step_entry* entries, uint32_t n_entries, uint32_t num_q_heads,
+                         uint32_t num_kv_heads, uint32_t head_dim, void* workspace, size_t workspace_bytes,
+                         g4_decode_plan* plan, void* stream);
+int g4_attn_step_run(const g4_decode_plan* plan, void* stream);
+/* prepare + run. */
+int g4_attn_step(const g4_step_entry* entries, uint32_t n_entries, uint32_t num_q_heads, uint32_t num_kv_heads,
+                 uint32_t head_dim, void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

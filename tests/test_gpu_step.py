@@ -1,0 +1,182 @@
+"""GPU parity of the one-launch decode step (prep + split-K attention + merge in
+one kernel) against the oracle's reference sequence:
+vNorm -> fusedNormRope(Q) -> fusedNormRope(K) -> kvCacheStore -> attnScore ->
+softmax -> attnOutput (src/engine.ts:2056-2094).
+
+Bars: the stored f16 cache row is bit-identical to RNE of the oracle's k/v;
+attnOut within max-abs 2e-3 (f16 KV, f32 accumulate). Rows the step must not
+read (the current row before it is stored, rows outside a local window) are
+poisoned with NaN, so reading one shows up as a non-finite output.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import announce
+from g4attn import e2b, ops, synth
+from helpers import EPS, cache_f16_torch, f16_weight_bits, max_abs
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+NQH, NKH, HD = 8, 1, 256
+ROPE = np.array(e2b.rope_freqs_f16_bits(256), dtype=np.uint16)
+NAN16 = 0x7E00
+
+
+def t16(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).to(dev)
+
+
+class Layer:
+    """One entry: raw projections, weights, a cache holding rows 0..seq-2, and the oracle's expectation."""
+
+    def __init__(self, dev, seed, seq, window=0, theta=1e4, divisor=0, nqh=NQH, nkh=NKH, cache=None):
+        self.seq, self.window, self.theta, self.divisor = seq, window, theta, divisor
+        self.pos = seq - 1
+        rng_scale = 2.0
+        self.q = synth.normal(seed, nqh * HD) * rng_scale
+        self.k = synth.normal(seed + 1, nkh * HD) * rng_scale
+        self.v = synth.normal(seed + 2, nkh * HD) * rng_scale
+        self.qw, self.kw = f16_weight_bits(seed + 3, HD), f16_weight_bits(seed + 4, HD)
+        if cache is None:
+            kc = cache_f16_torch(seed + 5, seq, nkh, HD, dev).view(torch.int16).reshape(seq, nkh * HD)
+            vc = cache_f16_torch(seed + 6, seq, nkh, HD, dev).view(torch.int16).reshape(seq, nkh * HD)
+            kc[self.pos] = NAN16
+            vc[self.pos] = NAN16
+            if window and seq > window:  # rows outside the window are never read
+                kc[: seq - window] = NAN16
+                vc[: seq - window] = NAN16
+            self.kc, self.vc = kc.contiguous(), vc.contiguous()
+        else:
+            self.kc, self.vc = cache
+        self.out = torch.full((nqh * HD,), float("nan"), device=dev)
+        self.d = {n: torch.from_numpy(x.copy()).to(dev) for n, x in (("q", self.q), ("k", self.k), ("v", self.v))}
+        self.dqw, self.dkw, self.drf = t16(self.qw, dev), t16(self.kw, dev), t16(ROPE, dev)
+        self.nqh, self.nkh = nqh, nkh
+
+    def entry(self, store=True, raw_kv=None):
+        k, v = (self.d["k"], self.d["v"]) if raw_kv is None else raw_kv
+        return dict(q=self.d["q"], k=k, v=v, q_weight=self.dqw, k_weight=self.dkw, rope_freqs=self.drf,
+                    k_cache=self.kc, v_cache=self.vc, out=self.out, seq_len=self.seq, position=self.pos,
+                    sliding_window=self.window, store_kv=store, theta=self.theta, apply_divisor=self.divisor)
+
+    def expected(self, kv_from=None):
+        """Oracle: prep then the reference chain over f32-widened caches (current row = RNE(k'), RNE(v'))."""
+        src = kv_from or self
+        v_ = orc.per_head_rms_norm_no_weight(src.v, self.nkh, HD, EPS)
+        k_ = orc.fused_per_head_norm_rope(src.k, src.kw, ROPE, self.nkh, HD, EPS, src.pos, src.theta, src.divisor)
+        q_ = orc.fused_per_head_norm_rope(self.q, self.qw, ROPE, self.nqh, HD, EPS, self.pos, self.theta, self.divisor)
+        kb = self.kc.cpu().numpy().view(np.uint16).copy()
+        vb = self.vc.cpu().numpy().view(np.uint16).copy()
+        kb[self.pos] = orc.f32_to_f16_bits(k_)
+        vb[self.pos] = orc.f32_to_f16_bits(v_)
+        lo = self.seq - self.window if self.window and self.seq > self.window else 0
+        kf = orc.f16_bits_to_f32(kb[lo:]).reshape(-1)
+        vf = orc.f16_bits_to_f32(vb[lo:]).reshape(-1)
+        out = orc.attention_chain(q_, kf, vf, self.nqh, self.nkh, HD, self.seq - lo, 1.0, 0)
+        return out, kb[self.pos], vb[self.pos]
+
+
+def run_step(dev, entries, nqh=NQH, nkh=NKH, plan_runs=1):
+    arr = ops.make_step_entries(entries, nqh, nkh, HD)
+    ws = torch.empty(ops.step_workspace_bytes(len(entries), nqh, nkh, HD), dtype=torch.uint8, device=dev)
+    plan = ops.attn_step_prepare(arr, nqh, nkh, HD, ws)
+    for _ in range(plan_runs):
+        ops.attn_step_run(plan)
+    torch.cuda.synchronize()
+    return plan, ws
+
+
+def check(layer, want, kbits, vbits, label):
+    got = layer.out.cpu().numpy()
+    assert np.isfinite(got).all(), f"{label}: non-finite output (a poisoned row was read)"
+    err = max_abs(got, want)
+    assert err <= TOL, f"{label}: max-abs {err}"
+    np.testing.assert_array_equal(layer.kc[layer.pos].cpu().numpy().view(np.uint16), kbits, err_msg=label)
+    np.testing.assert_array_equal(layer.vc[layer.pos].cpu().numpy().view(np.uint16), vbits, err_msg=label)
+    return err
+
+
+SINGLE = [  # (seq, window, theta, divisor)
+    (513, 512, 1e4, 0), (1, 0, 1e4, 0), (2, 0, 1e6, 1), (33, 0, 1e6, 1), (64, 512, 1e4, 0), (1000, 512, 1e4, 0),
+    (8193, 0, 1e6, 1), (8193, 512, 1e4, 0), (32769, 0, 1e6, 1),
+]
+
+
+@pytest.mark.parametrize("seq,win,theta,div", SINGLE)
+def test_step_single_entry(dev, seq, win, theta, div):
+    announce(f"attnStep single seq={seq} win={win}")
+    L = Layer(dev, 100 + seq, seq, win, theta, div)
+    run_step(dev, [L.entry()])
+    want, kb, vb = L.expected()
+    err = check(L, want, kb, vb, f"seq={seq}")
+    print(f"seq={seq} win={win} err={err:.2e}")
+
+
+@pytest.mark.parametrize("seq", [2049, 8193])
+def test_step_e2b_stack(dev, seq):
+    """35 layers (7 global theta 1e6 with the rope_freqs divisor, 28 local W=512 theta 1e4) in one launch."""
+    announce(f"attnStep 35-layer stack seq={seq}")
+    cfg = e2b.AttnConfig(num_layers=35)
+    layers = [Layer(dev, 1000 * il + seq, seq, e2b.sliding_window(il, cfg), e2b.rope_theta(il, cfg),
+                    e2b.apply_divisor(il, cfg)) for il in range(35)]
+    run_step(dev, [L.entry() for L in layers])
+    worst = 0.0
+    for il, L in enumerate(layers):
+        want, kb, vb = L.expected()
+        worst = max(worst, check(L, want, kb, vb, f"layer {il}"))
+    print(f"stack seq={seq} worst err={worst:.2e}")
+
+
+def test_step_ragged_batch(dev):
+    lens = [1, 2, 31, 32, 33, 100, 511, 512, 513] + [int(x) for x in synth.ragged_lengths(77, 7, 1000, 9000)]
+    announce(f"attnStep ragged batch {lens}")
+    layers = [Layer(dev, 50 + i, L, 0, 1e6, 1) for i, L in enumerate(lens)]
+    run_step(dev, [L.entry() for L in layers])
+    for i, L in enumerate(layers):
+        want, kb, vb = L.expected()
+        check(L, want, kb, vb, f"seq {i} len {lens[i]}")
+
+
+def test_step_kv_consumer_layer(dev):
+    """A KV-consumer layer reads its producer's cache and current row in the same launch, without storing."""
+    announce("attnStep producer + consumer sharing a cache")
+    prod = Layer(dev, 7, 3000, 0, 1e6, 1)
+    cons = Layer(dev, 8, 3000, 0, 1e6, 1, cache=(prod.kc, prod.vc))
+    run_step(dev, [prod.entry(), cons.entry(store=False, raw_kv=(prod.d["k"], prod.d["v"]))])
+    want_p, kb, vb = prod.expected()
+    check(prod, want_p, kb, vb, "producer")
+    want_c, _, _ = cons.expected(kv_from=prod)
+    got = cons.out.cpu().numpy()
+    assert np.isfinite(got).all() and max_abs(got, want_c) <= TOL
+
+
+def test_step_replay_is_deterministic(dev):
+    """A prepared plan replays (merge counters reset themselves) and gives identical bits each time."""
+    announce("attnStep replay")
+    layers = [Layer(dev, 300 + i, s, w, 1e4, 0) for i, (s, w) in enumerate([(20000, 0), (700, 512), (5, 0)])]
+    arr = ops.make_step_entries([L.entry() for L in layers], NQH, NKH, HD)
+    ws = torch.empty(ops.step_workspace_bytes(3, NQH, NKH, HD), dtype=torch.uint8, device=dev)
+    plan = ops.attn_step_prepare(arr, NQH, NKH, HD, ws)
+    outs = []
+    for _ in range(3):
+        for L in layers:
+            L.out.fill_(float("nan"))
+        ops.attn_step_run(plan)
+        torch.cuda.synchronize()
+        outs.append(np.concatenate([L.out.cpu().numpy() for L in layers]).view(np.uint32))
+    np.testing.assert_array_equal(outs[0], outs[1])
+    np.testing.assert_array_equal(outs[0], outs[2])
+    for L in layers:
+        want, kb, vb = L.expected()
+        check(L, want, kb, vb, "replay")
+
+
+def test_step_gqa_two_kv_heads(dev):
+    announce("attnStep nqh=16 nkh=2")
+    L = Layer(dev, 9, 1500, 0, 1e6, 1, nqh=16, nkh=2)
+    run_step(dev, [L.entry()], nqh=16, nkh=2)
+    want, kb, vb = L.expected()
+    check(L, want, kb, vb, "gqa")
