@@ -108,39 +108,44 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void k_decode_split(DecodeArgs a
 }
 
 // Fixed-order log-sum-exp merge of the split partials: one workgroup per
-// (entry, kv head, query head). Each thread owns one output column d of one
-// of kGroups split groups (split s belongs to group s % kGroups). The first
-// batch of o partials is requested together with the per-split (m, l), so a
-// merge of up to kBatch * kGroups splits waits on memory once. Group sums are
-// added in group order, so the result does not depend on scheduling.
-constexpr int kMergeThreads = 1024;
+// (entry, kv head x query head, column chunk). The dc = HD / n_chunks columns
+// of a chunk are read as float4 by R = dc / 4 threads per record; the
+// P = 256 / R thread groups take records s = grp, grp + P, ... (a fixed
+// assignment) and their sums are added in group order, so the result does not
+// depend on scheduling. Long merges use more chunks, spreading their records
+// over more CUs. The first batch of partials is requested together with the
+// per-split (m, l), so a merge of up to kMergeBatch * P splits waits on memory
+// once.
+constexpr int kMergeThreads = 256;
+constexpr int kMergeBatch = 8;
 constexpr int kMaxMergeSplits = 8192;
+constexpr unsigned kMaxMergeChunks = 16;
 
 template <int HD>
-__global__ __launch_bounds__(kMergeThreads) void k_decode_merge(DecodeArgs a) {
-    constexpr int kGroups = kMergeThreads / HD;
-    constexpr int kBatch = 16;
+__global__ __launch_bounds__(kMergeThreads) void k_decode_merge(DecodeArgs a, unsigned n_chunks) {
     constexpr int kWaves = kMergeThreads / 64;
     __shared__ float sc[kMaxMergeSplits];
     __shared__ float red[2][kWaves];
-    __shared__ float part[kGroups][HD];
+    __shared__ f32x4 part[kMergeThreads];
     const DecodeEntryDev ent = a.table ? a.table[blockIdx.x] : a.one;
     const unsigned ns = ent.n_splits;
     if (ns <= 1) return;
     const unsigned G = a.group;
     const unsigned kvh = blockIdx.y / G, h = blockIdx.y % G;
     const unsigned t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const unsigned dc = HD / n_chunks, R = dc / 4, P = kMergeThreads / R;
+    const unsigned grp = t / R, q = t % R;
+    const unsigned d = blockIdx.z * dc + q * 4;
     const uint64_t rec_stride = (uint64_t)a.num_kv_heads * G;  // partial records per split
     const uint64_t rec0 = ((uint64_t)ent.split_base * a.num_kv_heads + kvh) * G + h;
-    const unsigned grp = t / HD, d = t % HD;
     const float* o = a.part_o + rec0 * HD + d;
     const uint64_t o_stride = rec_stride * HD;
 
-    float v[kBatch];  // first batch of this thread's o partials, in flight during the (m, l) pass
+    f32x4 v[kMergeBatch];  // first batch of this thread's partials, in flight during the (m, l) pass
 #pragma unroll
-    for (int u = 0; u < kBatch; u++) {
-        const unsigned s = grp + u * kGroups;
-        v[u] = s < ns ? ldg<float>(o + s * o_stride) : 0.0f;
+    for (int u = 0; u < kMergeBatch; u++) {
+        const unsigned s = grp + u * P;
+        v[u] = s < ns ? ldg<f32x4>(o + s * o_stride) : f32x4{0.f, 0.f, 0.f, 0.f};
     }
     float mx = -INFINITY;
     for (unsigned s = t; s < ns; s += kMergeThreads) {
@@ -165,37 +170,41 @@ __global__ __launch_bounds__(kMergeThreads) void k_decode_merge(DecodeArgs a) {
     float L = 0.0f;
     for (int w = 0; w < kWaves; w++) L += red[1][w];
 
-    float acc = 0.0f;
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int u = 0; u < kBatch; u++) {
-        const unsigned s = grp + u * kGroups;
+    for (int u = 0; u < kMergeBatch; u++) {
+        const unsigned s = grp + u * P;
         if (s < ns) acc += v[u] * sc[s];
     }
-    for (unsigned s0 = grp + kBatch * kGroups; s0 < ns; s0 += kBatch * kGroups) {
+    for (unsigned s0 = grp + kMergeBatch * P; s0 < ns; s0 += kMergeBatch * P) {
 #pragma unroll
-        for (int u = 0; u < kBatch; u++) {
-            const unsigned s = s0 + u * kGroups;
-            v[u] = s < ns ? ldg<float>(o + s * o_stride) : 0.0f;
+        for (int u = 0; u < kMergeBatch; u++) {
+            const unsigned s = s0 + u * P;
+            v[u] = s < ns ? ldg<f32x4>(o + s * o_stride) : f32x4{0.f, 0.f, 0.f, 0.f};
         }
 #pragma unroll
-        for (int u = 0; u < kBatch; u++) {
-            const unsigned s = s0 + u * kGroups;
+        for (int u = 0; u < kMergeBatch; u++) {
+            const unsigned s = s0 + u * P;
             if (s < ns) acc += v[u] * sc[s];
         }
     }
-    part[grp][d] = acc;
+    part[t] = acc;
     __syncthreads();
     if (grp == 0) {
-        float sum = part[0][d];
-#pragma unroll
-        for (int g2 = 1; g2 < kGroups; g2++) sum += part[g2][d];
-        stg<float>(ent.out + ((uint64_t)kvh * G + h) * HD + d, sum / L);
+        f32x4 sum = part[q];
+        for (unsigned g2 = 1; g2 < P; g2++) sum += part[g2 * R + q];
+        stg<f32x4>(ent.out + ((uint64_t)kvh * G + h) * HD + d, sum / L);
     }
 }
 
-int launch_decode_merge(const DecodeArgs& a, unsigned n_entries, hipStream_t st) {
-    if (!n_entries) return G4_OK;
-    hipLaunchKernelGGL(k_decode_merge<256>, dim3(n_entries, a.num_kv_heads * a.group), dim3(kMergeThreads), 0, st, a);
+int launch_decode_merge(const DecodeArgs& a, unsigned n_entries, unsigned max_splits, hipStream_t st) {
+    if (!n_entries || max_splits <= 1) return G4_OK;
+    if (max_splits > (unsigned)kMaxMergeSplits)
+        return fail(G4_EINVAL, "attnDecode merge: %u splits (max %d)", max_splits, kMaxMergeSplits);
+    unsigned chunks = 1;
+    while (chunks < kMaxMergeChunks && max_splits > 32 * chunks) chunks *= 2;
+    hipLaunchKernelGGL(k_decode_merge<256>, dim3(n_entries, a.num_kv_heads * a.group, chunks), dim3(kMergeThreads), 0,
+                       st, a, chunks);
     G4_CHECK_LAUNCH("attnDecode merge");
     return G4_OK;
 }
@@ -264,14 +273,10 @@ int launch_split(const DecodeArgs& a, unsigned total_splits, hipStream_t st) {
     return G4_OK;
 }
 
-int launch_merge(const DecodeArgs& a, unsigned merge_entries, hipStream_t st) {
-    return launch_decode_merge(a, merge_entries, st);
-}
-
-int launch(const DecodeArgs& a, unsigned total_splits, unsigned merge_entries, hipStream_t st) {
+int launch(const DecodeArgs& a, unsigned total_splits, unsigned merge_entries, unsigned max_splits, hipStream_t st) {
     int rc = launch_split(a, total_splits, st);
     if (rc) return rc;
-    return launch_merge(a, merge_entries, st);
+    return launch_decode_merge(a, merge_entries, max_splits, st);
 }
 
 }  // namespace
@@ -314,7 +319,7 @@ int g4_attn_decode(const float* q, const uint16_t* k_cache, const uint16_t* v_ca
         a.part_o = reinterpret_cast<float*>(static_cast<char*>(workspace) +
                                             align256((size_t)ns * p.num_kv_heads * group * 2 * sizeof(float)));
     }
-    return launch(a, ns, ns > 1 ? 1 : 0, as_stream(stream));
+    return launch(a, ns, 1, ns, as_stream(stream));
 }
 
 int g4_attn_decode_many_workspace_size(uint32_t n_entries, uint32_t num_q_heads, uint32_t num_kv_heads,
@@ -338,6 +343,7 @@ struct PlanRep {
     uint32_t chunk;
     uint32_t total_splits;
     uint32_t head_dim;
+    uint32_t max_splits;
     uint32_t magic;
 };
 static_assert(sizeof(PlanRep) <= sizeof(g4_decode_plan), "plan size");
@@ -377,6 +383,7 @@ int g4_attn_decode_many_prepare(const g4_decode_entry* entries, uint32_t n_entri
         staging_cap = n_entries;
     }
     uint64_t total_splits = 0;
+    uint32_t max_splits = 0;
     for (uint32_t i = 0; i < n_entries; i++) {
         const g4_decode_entry& e = entries[i];
         uint32_t kb, ke;
@@ -385,6 +392,7 @@ int g4_attn_decode_many_prepare(const g4_decode_entry* entries, uint32_t n_entri
         staging[i] = DecodeEntryDev{e.q, e.k_cache, e.v_cache, e.out, kb, ke, (uint32_t)total_splits, ns,
                                     e.scale * kLog2e, 0};
         total_splits += ns;
+        if (ns > max_splits) max_splits = ns;
     }
     if (total_splits > 0x7fffffffu) return fail(G4_EINVAL, "attnDecodeMany: too many splits");
     const size_t table_bytes = align256((size_t)n_entries * sizeof(DecodeEntryDev));
@@ -405,6 +413,7 @@ int g4_attn_decode_many_prepare(const g4_decode_entry* entries, uint32_t n_entri
     r.chunk = chunk;
     r.total_splits = (uint32_t)total_splits;
     r.head_dim = head_dim;
+    r.max_splits = max_splits;
     r.magic = kPlanMagic;
     memset(plan, 0, sizeof *plan);
     memcpy(plan, &r, sizeof r);
@@ -431,7 +440,7 @@ int g4_attn_decode_many_run(const g4_decode_plan* plan, void* stream) {
     DecodeArgs a;
     int rc = plan_args(plan, &r, &a);
     if (rc) return rc;
-    return launch(a, r.total_splits, r.n_entries, as_stream(stream));
+    return launch(a, r.total_splits, r.n_entries, r.max_splits, as_stream(stream));
 }
 
 int g4_attn_decode_many_run_split(const g4_decode_plan* plan, void* stream) {
@@ -447,7 +456,7 @@ int g4_attn_decode_many_run_merge(const g4_decode_plan* plan, void* stream) {
     DecodeArgs a;
     int rc = plan_args(plan, &r, &a);
     if (rc) return rc;
-    return launch_merge(a, r.n_entries, as_stream(stream));
+    return launch_decode_merge(a, r.n_entries, r.max_splits, as_stream(stream));
 }
 
 int g4_attn_decode_many(const g4_decode_entry* entries, uint32_t n_entries, uint32_t num_q_heads,

@@ -71,8 +71,9 @@ struct DecodeArgs {
 };
 
 // Launches the fixed-order log-sum-exp merge of split partials (decode.hip)
-// for entries 0..n_entries-1 of a.table; entries with one split are skipped.
-int launch_decode_merge(const DecodeArgs& a, unsigned n_entries, hipStream_t st);
+// for entries 0..n_entries-1 of a.table (or a.one); entries with one split are
+// skipped. max_splits: the largest n_splits among them.
+int launch_decode_merge(const DecodeArgs& a, unsigned n_entries, unsigned max_splits, hipStream_t st);
 
 template <int HD>
 struct DecodeDims {
@@ -249,17 +250,17 @@ __device__ __forceinline__ void wave_publish(DecodeSmem<HD>& sm, int wave, int n
 
 // Combines the 4 waves (after a barrier) and writes either the normalised
 // output out[h][d] (final) or the unnormalised partial o[h][d] with (m, l)
-// per head, for the G heads of one kv head. Thread t covers lane32 = t & 31
-// (head t & 7, lane group (t >> 3) & 3) of 8 output slots.
+// per head, for the G heads of one kv head. Thread t (0..255 within the four
+// waves that published) covers lane32 = t & 31 (head t & 7, lane group
+// (t >> 3) & 3) of 8 output slots.
 // `extra_m` (optional, per head, log2 units) with `extra_v` (one f16 row shared
 // by the heads) adds a fifth state holding a single row of weight 1: the
 // current token's row when it was not part of the tile loop.
 template <int HD>
 __device__ __forceinline__ void wg_combine_write(const DecodeSmem<HD>& sm, unsigned G, bool final_out, float* out,
                                                  float* part_o, float* part_ml, const float* extra_m = nullptr,
-                                                 const f16* extra_v = nullptr) {
+                                                 const f16* extra_v = nullptr, int t = threadIdx.x) {
     constexpr int NO = DecodeDims<HD>::NO;
-    const int t = threadIdx.x;
     const int lane32 = t & 31;
     const int h = lane32 & 7;
     const int gg = lane32 >> 3;

@@ -32,14 +32,19 @@ __device__ __forceinline__ float wg_tree_max(float* s, unsigned tid) {
 }
 
 // RoPE angle terms of pair i: freq = 1/pow(theta, 2i/HD) (optionally divided
-// by rope_freqs[i]), angle = f32(position) * freq.
-__device__ __forceinline__ float rope_angle(unsigned i, unsigned head_dim, float theta, unsigned position,
-                                            unsigned apply_divisor, const uint16_t* rope_freqs) {
+// by rope_freqs[i], given here as its value), angle = f32(position) * freq.
+__device__ __forceinline__ float rope_angle_val(unsigned i, unsigned head_dim, float theta, unsigned position,
+                                                 unsigned apply_divisor, float divisor) {
     float e = (float)(i * 2u) / (float)head_dim;
     float base_freq = 1.0f / (float)pow((double)theta, (double)e);
     float freq = base_freq;
-    if (apply_divisor != 0u) freq = base_freq / h2f(rope_freqs[i]);
+    if (apply_divisor != 0u) freq = base_freq / divisor;
     return (float)position * freq;
+}
+
+__device__ __forceinline__ float rope_angle(unsigned i, unsigned head_dim, float theta, unsigned position,
+                                            unsigned apply_divisor, const uint16_t* rope_freqs) {
+    return rope_angle_val(i, head_dim, theta, position, apply_divisor, apply_divisor ? h2f(rope_freqs[i]) : 1.0f);
 }
 
 // The reference's 128 -> 1 tree over 256 partials with two LDS steps

@@ -9,21 +9,25 @@
 // kv_cache_store.wgsl, attn_score.wgsl, softmax.wgsl, attn_output.wgsl),
 // with flash-decoding split-K and the split merge inside the same launch.
 //
-// Work split: all entries' attended rows form one sequence of 32-row tiles;
-// workgroup w takes tiles [w*T/W, (w+1)*T/W), so every workgroup streams the
-// same number of rows whatever the mix of long and short entries. A range that
-// crosses entries is processed entry by entry ("segments").
+// Work split: the host cuts every entry's attended rows into 32-row tiles and
+// gives each entry a number of workgroups proportional to its tiles (at least
+// one), choosing the tiles per workgroup so that all workgroups fit the GPU at
+// once; workgroup w then reads its entry and row range from a per-workgroup
+// table. No workgroup spans two entries.
 //
-// Per segment a workgroup computes the entry's post-norm, post-RoPE query
-// itself (from the raw projection; one wave per head, evaluating exactly the
-// reference's expressions and reduction tree, so the values are bit-identical
-// to the prep kernel's), overlapped with the first tile's loads. The
-// workgroup whose range holds the entry's last row (the current token's row)
+// Every workgroup computes its entry's post-norm, post-RoPE query itself (from
+// the raw projection; one wave per head, evaluating exactly the reference's
+// expressions and reduction tree, so the values are bit-identical to the prep
+// kernel's) while its first tile is in flight: the small operands are
+// requested before the tile (vector-memory results return in issue order, so
+// anything requested after the tile would wait for it), then the RoPE factors
+// (f64 transcendentals, one pair per lane, shared through LDS) and the norms
+// run under the tile's latency. The workgroup whose range holds the entry's last row (the current token's row)
 // also computes that row's k (norm + RoPE) and v (weightless norm), uses them
 // for that row instead of the cache, and stores them as f16 when the entry
 // owns the cache (KV-producer layers).
 //
-// Merge: a segment covering a whole entry writes attnOut directly; otherwise
+// Merge: a workgroup covering a whole entry writes attnOut directly; otherwise
 // it writes a partial record (m, l, unnormalised o per head) and the fixed-order
 // log-sum-exp merge kernel of decode.hip combines an entry's records in a
 // second launch. (Merging inside this launch needs a device-scope release per
@@ -50,11 +54,7 @@ struct StepEntryDev {
     uint16_t* k_cache;  // [rows][num_kv_heads][HD]
     uint16_t* v_cache;
     float* out;         // attnOut [num_kv_heads][group][HD]
-    uint32_t key_begin; // attended rows [key_begin, key_end); the current row is key_end - 1
-    uint32_t key_end;
-    uint32_t tile_base; // first global tile
-    uint32_t n_tiles;
-    uint32_t w_first;   // first workgroup on this entry
+    uint32_t key_end;   // one past the last attended row; the current row is key_end - 1
     uint32_t n_parts;   // workgroups on this entry
     uint32_t position;  // RoPE position
     uint32_t store_kv;
@@ -64,47 +64,38 @@ struct StepEntryDev {
     float eps;
 };
 
+// One workgroup's share: attended rows [row_begin, row_end) of entry `entry`.
+struct StepWorkDev {
+    uint32_t entry;
+    uint32_t row_begin;
+    uint32_t row_end;
+    uint32_t part;  // partial record slot, when the entry has more than one workgroup
+};
+
 struct StepArgs {
     const StepEntryDev* table;
-    uint32_t n_entries;
-    uint32_t total_tiles;
-    uint32_t n_wgs;
+    const StepWorkDev* work;
     uint32_t num_kv_heads;
     uint32_t group;
-    uint32_t pad;
-    float* part_ml;  // partial records [(w + e) * NKH + kvh][group][2]
-    float* part_o;   //                  [(w + e) * NKH + kvh][group][HD]
+    float* part_ml;  // partial records [part * NKH + kvh][group][2]
+    float* part_o;   //                  [part * NKH + kvh][group][HD]
 };
 
 constexpr int kStepHD = 256;
 
-// RoPE factors of pairs (l, l + 128) and (l + 64, l + 192) for lane l (head_dim
-// 256), exactly the reference expressions (rope_angle in ref_math.h).
+// RoPE factors of pairs (l, l + 128) and (l + 64, l + 192) for lane l (head_dim 256).
 struct RopeLane {
     float c0, s0, c1, s1;
 };
 
-// Not inlined: inlined into the segment loop, the f64 library code's constants
-// are hoisted out of the loop and spill.
-__device__ __attribute__((noinline)) RopeLane rope_lane(int lane, float theta, unsigned position,
-                                                        unsigned apply_divisor, const uint16_t* rope_freqs) {
-    RopeLane r;
-    const float a0 = rope_angle((unsigned)lane, kStepHD, theta, position, apply_divisor, rope_freqs);
-    const float a1 = rope_angle((unsigned)lane + 64u, kStepHD, theta, position, apply_divisor, rope_freqs);
-    r.c0 = (float)cos((double)a0);
-    r.s0 = (float)sin((double)a0);
-    r.c1 = (float)cos((double)a1);
-    r.s1 = (float)sin((double)a1);
-    return r;
-}
-
 // Per-head RMSNorm (+ RoPE) of one 256-wide head by one wave; lane l holds
-// x[l + 64j], j = 0..3, and receives the results in place. The sum of squares
-// adds the same pairs in the same order as the reference's workgroup tree
-// (strides 128, 64, then 32..1), so every value is bit-identical to
-// fused_per_head_norm_rope.wgsl / per_head_rms_norm_no_weight.wgsl.
-__device__ __forceinline__ void wave_norm_rope(float (&x)[4], const uint16_t* weight, bool rope, const RopeLane& r,
-                                               float eps, int lane) {
+// x[l + 64j], j = 0..3 (and the weight's f16 bits at the same places), and
+// receives the results in place. The sum of squares adds the same pairs in
+// the same order as the reference's workgroup tree (strides 128, 64, then
+// 32..1), so every value is bit-identical to fused_per_head_norm_rope.wgsl /
+// per_head_rms_norm_no_weight.wgsl.
+__device__ __forceinline__ void wave_norm_rope(float (&x)[4], const uint32_t (&wbits)[4], bool weighted, bool rope,
+                                               const RopeLane& r, float eps) {
 #pragma clang fp contract(off)
     float p[4];
 #pragma unroll
@@ -116,7 +107,7 @@ __device__ __forceinline__ void wave_norm_rope(float (&x)[4], const uint16_t* we
     const float total = __shfl(c, 0);
     const float rms = sqrtf(total / (float)kStepHD + eps);
 #pragma unroll
-    for (int j = 0; j < 4; j++) x[j] = weight ? x[j] * h2f(weight[lane + 64 * j]) / rms : x[j] / rms;
+    for (int j = 0; j < 4; j++) x[j] = weighted ? x[j] * h2f((uint16_t)wbits[j]) / rms : x[j] / rms;
     if (!rope) return;
     const float x0 = x[0], x1 = x[1], x2 = x[2], x3 = x[3];
     x[0] = x0 * r.c0 - x2 * r.s0;
@@ -130,84 +121,119 @@ struct StepSmem {
     float qf[kMaxGroup][kStepHD];  // post-prep q * qscale
     f16x8 knew[kStepHD / 8];       // current row's k and v, f16 (as stored)
     f16x8 vnew[kStepHD / 8];
+    float rope_c[kStepHD / 2];     // RoPE factors of the 128 pairs
+    float rope_s[kStepHD / 2];
     float mnew[kMaxGroup];         // current row's scores (log2 units)
 };
 
-__host__ __device__ __forceinline__ unsigned wg_of_tile(uint64_t x, uint64_t T, uint64_t W) {  // max w: floor(wT/W) <= x
-    return (unsigned)(((x + 1) * W - 1) / T);
-}
-
-// One segment: entry e, this workgroup's tiles [t_begin, t_end) of it (global
-// tile indices).
-__device__ __forceinline__ void attn_segment(const StepArgs a, StepSmem& sm, unsigned w, unsigned kvh,
-                                                       unsigned e, unsigned t_begin, unsigned t_end) {
+// Two workgroups per CU (launch bounds): enough rows in flight to cover the
+// HBM latency with one tile per wave.
+__global__ __launch_bounds__(kDecodeThreads, 2) void k_attn_step(StepArgs a) {
     using D = DecodeDims<kStepHD>;
     constexpr unsigned HD = kStepHD;
+    __shared__ StepSmem sm;
+    const unsigned kvh = blockIdx.y;
     const unsigned NKH = a.num_kv_heads;
     const unsigned G = a.group;
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: branches on it stay scalar
     const int n = lane & 15;
     const int g = lane >> 4;
     const int head = n & 7;
     const bool lo_col = n >= 8;
 
-    const StepEntryDev& ent = a.table[e];  // fields read where used (scalar loads)
-    const unsigned tile_base = ent.tile_base;
-    const unsigned key_begin = ent.key_begin, key_end = ent.key_end;
-    const unsigned k0 = key_begin + (t_begin - tile_base) * kTileKeys;
-    const unsigned k1 = min(key_end, key_begin + (t_end - tile_base) * kTileKeys);
-    const bool has_new = k1 == key_end;  // this segment holds the current token's row
+    const StepWorkDev wk = a.work[blockIdx.x];
+    const StepEntryDev& ent = a.table[wk.entry];  // fields read where used (scalar loads)
+    const unsigned key_end = ent.key_end;
+    const unsigned k0 = wk.row_begin;
+    const bool has_new = wk.row_end == key_end;  // this workgroup holds the current token's row
     const unsigned new_row = key_end - 1;
-    const unsigned k1t = has_new ? new_row : k1;  // rows read from the cache: [k0, k1t)
+    const unsigned k1t = has_new ? new_row : wk.row_end;  // rows read from the cache: [k0, k1t)
+    const unsigned nkeys = k1t - k0;
+    const unsigned last = nkeys ? k1t - 1 : k0;  // loads are clamped to it (k0 < key_end: in the cache)
 
-    const RopeLane rl = rope_lane(lane, ent.theta, ent.position, ent.apply_divisor, ent.rope_freqs);
-
+    // ---- small operands first, then the first tile ----
+    // Every load is unconditional (clamped to valid addresses where the value
+    // is not needed): with loads under branches the compiler cannot count the
+    // younger loads on every path, and its wait for a small operand would also
+    // wait for the tile. f16 values stay unconverted until used.
+    const unsigned pair = (unsigned)wave * 32u + (unsigned)(lane & 31);  // RoPE pair computed by this lane
+    const unsigned apply_divisor = ent.apply_divisor;
+    // Without the divisor the table may be absent: read a valid dummy instead.
+    const uint32_t fbits = ldg<uint16_t>((apply_divisor ? ent.rope_freqs : ent.q_weight) + pair);
+    float xq[2][4];
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+        const unsigned hq = min((unsigned)wave + kDecodeWaves * r, G - 1);
+        const float* src = ent.q + ((uint64_t)kvh * G + hq) * HD;
+#pragma unroll
+        for (int j = 0; j < 4; j++) xq[r][j] = ldg<float>(src + lane + 64 * j);
+    }
+    uint32_t wq[4], wn[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) wq[j] = ldg<uint16_t>(ent.q_weight + lane + 64 * j);
+    const bool do_new = has_new && wave < 2;  // wave 0: k, wave 1: v
+    float xn[4];
+    {
+        const float* src = (wave == 1 ? ent.v : ent.k) + (uint64_t)kvh * HD;
+#pragma unroll
+        for (int j = 0; j < 4; j++) xn[j] = ldg<float>(src + lane + 64 * j);
+#pragma unroll
+        for (int j = 0; j < 4; j++) wn[j] = ldg<uint16_t>(ent.k_weight + lane + 64 * j);
+    }
     const uint32_t row_bytes = NKH * HD * 2u;
     const char* Kb = reinterpret_cast<const char*>(ent.k_cache + (uint64_t)kvh * HD);
     const char* Vb = reinterpret_cast<const char*>(ent.v_cache + (uint64_t)kvh * HD);
-    const unsigned nkeys = k1t - k0;
-    const unsigned last = k1t - 1;  // only used when nkeys > 0
     constexpr unsigned kStride = kDecodeWaves * kTileKeys;
-
-    // First tile in flight while the query is normalised and rotated.
-    unsigned t0 = (unsigned)wave * kTileKeys;
+    unsigned t0 = (unsigned)wave * kTileKeys;  // a wave without a tile reads row `last` and discards it
     f16x8 kreg[2][D::NC];
     u32x4 vreg[D::NB][8];
-    if (t0 < nkeys) {
-        load_k_tile<HD>(Kb, row_bytes, last, n, g, k0 + t0, kreg);
-        load_v_tile<HD>(Vb, row_bytes, last, n, g, k0 + t0, vreg);
-    }
+    load_k_tile<HD>(Kb, row_bytes, last, n, g, k0 + t0, kreg);
+    load_v_tile<HD>(Vb, row_bytes, last, n, g, k0 + t0, vreg);
+    __builtin_amdgcn_sched_barrier(0);  // keep every request above ahead of the arithmetic below
 
-    // ---- prep: q heads (2 per wave), and the current row's k and v ----
-    const float qscale = ent.qscale, eps = ent.eps;
-    for (unsigned hq = (unsigned)wave; hq < G; hq += kDecodeWaves) {
-        const float* src = ent.q + ((uint64_t)kvh * G + hq) * HD;
-        float x[4];
-#pragma unroll
-        for (int j = 0; j < 4; j++) x[j] = ldg<float>(src + lane + 64 * j);
-        wave_norm_rope(x, ent.q_weight, true, rl, eps, lane);
-#pragma unroll
-        for (int j = 0; j < 4; j++) sm.qf[hq][lane + 64 * j] = x[j] * qscale;
-    }
-    if (has_new && wave < 2) {
-        const bool is_k = wave == 0;
-        const float* src = (is_k ? ent.k : ent.v) + (uint64_t)kvh * HD;
-        float x[4];
-#pragma unroll
-        for (int j = 0; j < 4; j++) x[j] = ldg<float>(src + lane + 64 * j);
-        wave_norm_rope(x, is_k ? ent.k_weight : nullptr, is_k, rl, eps, lane);
-        uint16_t* row = reinterpret_cast<uint16_t*>(is_k ? sm.knew : sm.vnew);
-#pragma unroll
-        for (int j = 0; j < 4; j++) row[lane + 64 * j] = f2h(x[j]);
-        if (ent.store_kv) {
-            uint16_t* dst = (is_k ? ent.k_cache : ent.v_cache) + ((uint64_t)new_row * NKH + kvh) * HD;
-#pragma unroll
-            for (int j = 0; j < 4; j++) stg<uint16_t>(dst + lane + 64 * j, f2h(x[j]));
+    // ---- RoPE factors (the reference's expressions, f64 transcendentals) ----
+    {
+        // Division by 1 is exact, so dividing unconditionally equals the
+        // reference's conditional division (and keeps the load unconditional).
+        const float div = apply_divisor ? h2f((uint16_t)fbits) : 1.0f;
+        const float ang = rope_angle_val(pair, HD, ent.theta, ent.position, 1u, div);
+        const float c = (float)cos((double)ang);
+        const float s = (float)sin((double)ang);
+        if (lane < 32) {
+            sm.rope_c[pair] = c;
+            sm.rope_s[pair] = s;
         }
     }
     __syncthreads();
-    // Score operand from the prepared query, and the current row's scores.
+
+    // ---- q heads (two per wave), the current row's k and v ----
+    const RopeLane rl = {sm.rope_c[lane], sm.rope_s[lane], sm.rope_c[lane + 64], sm.rope_s[lane + 64]};
+    const float qscale = ent.qscale, eps = ent.eps;
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+        const unsigned hq = (unsigned)wave + kDecodeWaves * r;
+        if (hq < G) {
+            wave_norm_rope(xq[r], wq, true, true, rl, eps);
+#pragma unroll
+            for (int j = 0; j < 4; j++) sm.qf[hq][lane + 64 * j] = xq[r][j] * qscale;
+        }
+    }
+    if (do_new) {
+        const bool is_k = wave == 0;
+        wave_norm_rope(xn, wn, is_k, is_k, rl, eps);
+        uint16_t* row = reinterpret_cast<uint16_t*>(is_k ? sm.knew : sm.vnew);
+#pragma unroll
+        for (int j = 0; j < 4; j++) row[lane + 64 * j] = f2h(xn[j]);
+        if (ent.store_kv) {
+            uint16_t* dst = (is_k ? ent.k_cache : ent.v_cache) + ((uint64_t)new_row * NKH + kvh) * HD;
+#pragma unroll
+            for (int j = 0; j < 4; j++) stg<uint16_t>(dst + lane + 64 * j, f2h(xn[j]));
+        }
+    }
+    __syncthreads();
+
+    // ---- score operand from the prepared query, and the current row's scores ----
     {
         const bool live = (unsigned)head < G;
 #pragma unroll
@@ -231,6 +257,7 @@ __device__ __forceinline__ void attn_segment(const StepArgs a, StepSmem& sm, uns
     }
     __syncthreads();
 
+    // ---- tiles ----
     float m_run = -INFINITY, l_run = 0.0f;
     f32x4 acc[D::NO];
 #pragma unroll
@@ -248,42 +275,12 @@ __device__ __forceinline__ void attn_segment(const StepArgs a, StepSmem& sm, uns
 
     const float* em = has_new ? sm.mnew : nullptr;
     const f16* ev = reinterpret_cast<const f16*>(sm.vnew);
-    float* out = ent.out + (uint64_t)kvh * G * HD;
-    const unsigned n_parts = ent.n_parts;
-    if (n_parts == 1) {
-        wg_combine_write<HD>(sm.dec, G, true, out, nullptr, nullptr, em, ev);
-        __syncthreads();
+    if (ent.n_parts == 1) {
+        wg_combine_write<HD>(sm.dec, G, true, ent.out + (uint64_t)kvh * G * HD, nullptr, nullptr, em, ev);
         return;
     }
-    // Partial record at slot (w + e) * NKH + kvh: unique, and consecutive over the
-    // workgroups of an entry, so the merge reads split_base = w_first + e.
-    const uint64_t rec = ((uint64_t)(w + e) * NKH + kvh) * G;
+    const uint64_t rec = ((uint64_t)wk.part * NKH + kvh) * G;
     wg_combine_write<HD>(sm.dec, G, false, nullptr, a.part_o + rec * HD, a.part_ml + rec * 2, em, ev);
-    __syncthreads();
-}
-
-__global__ __launch_bounds__(kDecodeThreads, 2) void k_attn_step(StepArgs a) {
-    __shared__ StepSmem sm;
-    const unsigned w = blockIdx.x;
-    const unsigned kvh = blockIdx.y;
-    const uint64_t T = a.total_tiles, W = a.n_wgs;
-    unsigned tb = (unsigned)((uint64_t)w * T / W);
-    const unsigned te = (unsigned)((uint64_t)(w + 1) * T / W);
-    unsigned e;  // entry holding tile tb: last with tile_base <= tb
-    {
-        unsigned lo = 0, hi = a.n_entries;
-        while (hi - lo > 1) {
-            const unsigned mid = (lo + hi) >> 1;
-            if (a.table[mid].tile_base <= tb) lo = mid;
-            else hi = mid;
-        }
-        e = lo;
-    }
-    for (; tb < te; e++) {
-        const unsigned seg_end = min(te, a.table[e].tile_base + a.table[e].n_tiles);
-        attn_segment(a, sm, w, kvh, e, tb, seg_end);
-        tb = seg_end;
-    }
 }
 
 }  // namespace g4
@@ -292,7 +289,10 @@ using namespace g4;
 
 namespace {
 
-constexpr unsigned kStepMaxWgs = 1024;
+// Partial records: an entry gets more than one workgroup only while the
+// workgroups fit one wave of the GPU (at most kStepMaxWgs), so at most that
+// many records exist.
+constexpr unsigned kStepMaxWgs = 4096;
 constexpr uint32_t kStepMagic = 0x67345354u;
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -305,27 +305,30 @@ int step_env(const char* name, int dflt) {
 struct StepPlanRep {
     char* ws;
     uint32_t n_entries;
-    uint32_t total_tiles;
     uint32_t n_wgs;
     uint32_t num_kv_heads;
     uint32_t group;
     uint32_t any_split;  // some entry spans more than one workgroup: run the merge
+    uint32_t max_parts;
     uint32_t magic;
 };
 static_assert(sizeof(StepPlanRep) <= sizeof(g4_decode_plan), "plan size");
 
 struct StepLayout {
-    size_t table, merge_table, part_ml, part_o, total;
+    size_t table, work, merge_table, part_ml, part_o, total;
 };
 
-StepLayout step_layout(uint64_t n, uint64_t wgs, uint64_t nkh, uint64_t group, uint64_t hd) {
+StepLayout step_layout(uint64_t n, uint64_t nkh, uint64_t group, uint64_t hd) {
     StepLayout L;
+    const uint64_t max_items = n > kStepMaxWgs ? n : kStepMaxWgs;
+    const uint64_t recs = (uint64_t)kStepMaxWgs * nkh * group;
     size_t off = 0;
     L.table = off;
     off += align256(n * sizeof(StepEntryDev));
+    L.work = off;
+    off += align256(max_items * sizeof(StepWorkDev));
     L.merge_table = off;
     off += align256(n * sizeof(DecodeEntryDev));
-    const uint64_t recs = (wgs + n) * nkh * group;
     L.part_ml = off;
     off += align256(recs * 2 * 4);
     L.part_o = off;
@@ -357,6 +360,25 @@ int stage_upload(Staging& sg, void* dst, const void* src, size_t bytes, hipStrea
     return G4_OK;
 }
 
+// Smallest tiles-per-workgroup with sum_e ceil(tiles_e / tpw) <= cap (cap >= n,
+// so tpw = max tiles always fits).
+uint64_t pick_tiles_per_wg(const std::vector<uint32_t>& tiles, uint64_t total, uint64_t max_tiles, uint64_t cap) {
+    auto wgs = [&](uint64_t tpw) {
+        uint64_t s = 0;
+        for (uint32_t t : tiles) s += (t + tpw - 1) / tpw;
+        return s;
+    };
+    uint64_t lo = (total + cap - 1) / cap, hi = max_tiles;
+    if (lo < 1) lo = 1;
+    if (lo > hi) lo = hi;
+    while (lo < hi) {
+        const uint64_t mid = (lo + hi) / 2;
+        if (wgs(mid) <= cap) hi = mid;
+        else lo = mid + 1;
+    }
+    return lo;
+}
+
 }  // namespace
 
 extern "C" {
@@ -367,23 +389,27 @@ int g4_attn_step_workspace_size(uint32_t n_entries, uint32_t num_q_heads, uint32
     if (head_dim != kStepHD) return fail(G4_EINVAL, "attnStep: head_dim %u unsupported (256)", head_dim);
     if (num_kv_heads == 0 || num_q_heads % num_kv_heads || num_q_heads / num_kv_heads > (uint32_t)kMaxGroup)
         return fail(G4_EINVAL, "attnStep: %u query heads over %u kv heads unsupported", num_q_heads, num_kv_heads);
-    *bytes = step_layout(n_entries, kStepMaxWgs, num_kv_heads, num_q_heads / num_kv_heads, head_dim).total;
+    if (num_kv_heads > 65535) return fail(G4_EINVAL, "attnStep: %u kv heads (max 65535)", num_kv_heads);
+    *bytes = step_layout(n_entries, num_kv_heads, num_q_heads / num_kv_heads, head_dim).total;
     return G4_OK;
 }
 
 int g4_attn_step_prepare(const g4_step_entry* entries, uint32_t n_entries, uint32_t num_q_heads,
                          uint32_t num_kv_heads, uint32_t head_dim, void* workspace, size_t workspace_bytes,
                          g4_decode_plan* plan, void* stream) {
-    size_t need_max = 0;
-    int rc = g4_attn_step_workspace_size(n_entries, num_q_heads, num_kv_heads, head_dim, &need_max);
+    size_t need = 0;
+    int rc = g4_attn_step_workspace_size(n_entries, num_q_heads, num_kv_heads, head_dim, &need);
     if (rc) return rc;
     if (!plan) return fail(G4_EINVAL, "attnStep: plan is NULL");
     if (!entries || n_entries == 0) return fail(G4_EINVAL, "attnStep: no entries");
     if (n_entries > 65535) return fail(G4_EINVAL, "attnStep: %u entries (max 65535)", n_entries);
+    if (!workspace || workspace_bytes < need)
+        return fail(G4_ENOSPC, "attnStep: workspace %zu bytes < %zu needed", workspace_bytes, need);
     const uint32_t G = num_q_heads / num_kv_heads;
     const uint64_t row_bytes = (uint64_t)num_kv_heads * head_dim * 2;
     std::vector<StepEntryDev> tab(n_entries);
-    uint64_t T = 0;
+    std::vector<uint32_t> key_begin(n_entries), tiles(n_entries);
+    uint64_t T = 0, max_tiles = 0;
     for (uint32_t i = 0; i < n_entries; i++) {
         const g4_step_entry& s = entries[i];
         if (!s.q || !s.k || !s.v || !s.q_weight || !s.k_weight || !s.k_cache || !s.v_cache || !s.out)
@@ -404,45 +430,62 @@ int g4_attn_step_prepare(const g4_step_entry* entries, uint32_t n_entries, uint3
         d.v_cache = s.v_cache;
         d.out = s.out;
         d.key_end = s.seq_len;
-        d.key_begin = (s.sliding_window != 0 && s.seq_len > s.sliding_window) ? s.seq_len - s.sliding_window : 0;
-        d.n_tiles = (d.key_end - d.key_begin + kTileKeys - 1) / kTileKeys;
-        d.tile_base = (uint32_t)T;
-        T += d.n_tiles;
         d.position = s.position;
         d.store_kv = s.store_kv;
         d.theta = s.theta;
         d.apply_divisor = s.apply_divisor;
         d.qscale = s.scale * kLog2e;
         d.eps = s.eps;
+        key_begin[i] = (s.sliding_window != 0 && s.seq_len > s.sliding_window) ? s.seq_len - s.sliding_window : 0;
+        tiles[i] = (s.seq_len - key_begin[i] + kTileKeys - 1) / kTileKeys;
+        T += tiles[i];
+        if (tiles[i] > max_tiles) max_tiles = tiles[i];
     }
-    if (T > 0x7fffffffull) return fail(G4_EINVAL, "attnStep: too many rows");
+    // Workgroups that fit the GPU at once (two per CU).
     static const int wgs_per_cu = step_env("G4_STEP_WGS_PER_CU", 2);
-    uint64_t W = (uint64_t)(wgs_per_cu > 0 ? wgs_per_cu : 2) * 256 / num_kv_heads;
-    if (W > kStepMaxWgs) W = kStepMaxWgs;
-    if (W > T) W = T;
-    if (W == 0) W = 1;
+    uint64_t fit = (uint64_t)(wgs_per_cu > 0 ? wgs_per_cu : 2) * 256 / num_kv_heads;
+    if (fit > kStepMaxWgs) fit = kStepMaxWgs;
+    if (fit < 1) fit = 1;
+    const uint64_t cap = fit > n_entries ? fit : n_entries;
+    const uint64_t tpw = pick_tiles_per_wg(tiles, T, max_tiles, cap);
+
+    std::vector<StepWorkDev> work;
+    work.reserve(cap);
     std::vector<DecodeEntryDev> merge(n_entries);
-    uint32_t any_split = 0;
+    uint32_t any_split = 0, parts = 0, max_parts = 0;
     for (uint32_t i = 0; i < n_entries; i++) {
         StepEntryDev& d = tab[i];
-        const unsigned w0 = wg_of_tile(d.tile_base, T, W);
-        const unsigned w1 = wg_of_tile((uint64_t)d.tile_base + d.n_tiles - 1, T, W);
-        d.w_first = w0;
-        d.n_parts = w1 - w0 + 1;
-        any_split |= d.n_parts > 1;
-        merge[i] = DecodeEntryDev{nullptr, nullptr, nullptr, d.out, 0, 0, w0 + i, d.n_parts, 0.0f, 0};
+        const uint64_t ne = tiles[i], we = (ne + tpw - 1) / tpw;
+        d.n_parts = (uint32_t)we;
+        const uint32_t part_base = we > 1 ? parts : 0;
+        for (uint64_t j = 0; j < we; j++) {
+            const uint64_t tb = j * ne / we, te = (j + 1) * ne / we;
+            const uint64_t rb = key_begin[i] + tb * kTileKeys;
+            const uint64_t re = key_begin[i] + te * kTileKeys;
+            work.push_back(StepWorkDev{i, (uint32_t)rb, (uint32_t)(re < d.key_end ? re : d.key_end),
+                                       we > 1 ? part_base + (uint32_t)j : 0u});
+        }
+        if (we > max_parts) max_parts = (uint32_t)we;
+        if (we > 1) {
+            parts += (uint32_t)we;
+            any_split = 1;
+        }
+        merge[i] = DecodeEntryDev{nullptr, nullptr, nullptr, d.out, 0, 0, part_base, (uint32_t)we, 0.0f, 0};
     }
-    const StepLayout L = step_layout(n_entries, W, num_kv_heads, G, head_dim);
-    if (!workspace || workspace_bytes < L.total)
-        return fail(G4_ENOSPC, "attnStep: workspace %zu bytes < %zu needed", workspace_bytes, L.total);
+    if (parts > kStepMaxWgs) return fail(G4_EINVAL, "attnStep: internal: %u partial records", parts);
+    const StepLayout L = step_layout(n_entries, num_kv_heads, G, head_dim);
     hipStream_t st = as_stream(stream);
     char* ws = static_cast<char*>(workspace);
-    static thread_local Staging sg_table, sg_merge;
+    static thread_local Staging sg_table, sg_work, sg_merge;
     rc = stage_upload(sg_table, ws + L.table, tab.data(), (size_t)n_entries * sizeof(StepEntryDev), st);
     if (rc) return rc;
-    rc = stage_upload(sg_merge, ws + L.merge_table, merge.data(), (size_t)n_entries * sizeof(DecodeEntryDev), st);
+    rc = stage_upload(sg_work, ws + L.work, work.data(), work.size() * sizeof(StepWorkDev), st);
     if (rc) return rc;
-    StepPlanRep r = {ws, n_entries, (uint32_t)T, (uint32_t)W, num_kv_heads, G, any_split, kStepMagic};
+    if (any_split) {
+        rc = stage_upload(sg_merge, ws + L.merge_table, merge.data(), (size_t)n_entries * sizeof(DecodeEntryDev), st);
+        if (rc) return rc;
+    }
+    StepPlanRep r = {ws, n_entries, (uint32_t)work.size(), num_kv_heads, G, any_split, max_parts, kStepMagic};
     memset(plan, 0, sizeof *plan);
     memcpy(plan, &r, sizeof r);
     return G4_OK;
@@ -453,12 +496,10 @@ int g4_attn_step_run(const g4_decode_plan* plan, void* stream) {
     StepPlanRep r;
     memcpy(&r, plan, sizeof r);
     if (r.magic != kStepMagic) return fail(G4_EINVAL, "attnStep: plan was not prepared by g4_attn_step_prepare");
-    const StepLayout L = step_layout(r.n_entries, r.n_wgs, r.num_kv_heads, r.group, kStepHD);
+    const StepLayout L = step_layout(r.n_entries, r.num_kv_heads, r.group, kStepHD);
     StepArgs a = {};
     a.table = reinterpret_cast<const StepEntryDev*>(r.ws + L.table);
-    a.n_entries = r.n_entries;
-    a.total_tiles = r.total_tiles;
-    a.n_wgs = r.n_wgs;
+    a.work = reinterpret_cast<const StepWorkDev*>(r.ws + L.work);
     a.num_kv_heads = r.num_kv_heads;
     a.group = r.group;
     a.part_ml = reinterpret_cast<float*>(r.ws + L.part_ml);
@@ -474,7 +515,7 @@ int g4_attn_step_run(const g4_decode_plan* plan, void* stream) {
     m.group = r.group;
     m.part_o = a.part_o;
     m.part_ml = a.part_ml;
-    return launch_decode_merge(m, r.n_entries, st);
+    return launch_decode_merge(m, r.n_entries, r.max_parts, st);
 }
 
 int g4_attn_step(const g4_step_entry* entries, uint32_t n_entries, uint32_t num_q_heads, uint32_t num_kv_heads,
