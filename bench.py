@@ -14,16 +14,18 @@ inputs resident in HBM:
   ragged64  64 independent sequences, lengths uniform in [1024, 32768].
   layer512  one local layer at position 512 (launch-bound).
 
-Per step the stack runs the producer-side prep of every layer (q/k RMSNorm +
-RoPE, weightless v-norm, f16 store of the new row) and the fused split-K
-decode attention of every layer. Several distinct cache sets are rotated so
-the bytes read each cycle exceed twice MI355X's 256 MB Infinity Cache and
-come from HBM. `value` is algorithmic bytes per step (K/V rows attended,
-f16, read once for all query heads; q read; attnOut written) over wall time
-per step. `roofline` is the dominant kernel (the decode split pass), timed
-with HIP events on its stream. `cpu_baseline` runs the oracle (the
-WGSL-semantics C restatement of the reference's six kernels, f32 caches,
-full-length score/softmax/output on every layer as the WGSL does) on the host.
+A step is one launch of the fused attention step over every entry (per entry:
+q/k RMSNorm + RoPE, weightless v-norm, f16 store of the new K/V row, split-K
+flash-decoding attention over the attended rows) plus the log-sum-exp merge
+launch. Several distinct cache sets are rotated so the bytes read each cycle
+exceed twice MI355X's 256 MB Infinity Cache and come from HBM. `value` is
+algorithmic bytes per step (K/V rows attended, f16, read once for all query
+heads; q read; attnOut written) over wall time per step. `roofline` is the
+dominant kernel (k_attn_step), timed with HIP events on its stream; its
+`traffic` comes from the committed rocprofv3 counter summary of the same
+workload. `cpu_baseline` runs the oracle (the WGSL-semantics C restatement of
+the reference's six kernels, f32 caches, full-length score/softmax/output on
+every layer as the WGSL does) on the host.
 """
 from __future__ import annotations
 
@@ -74,8 +76,8 @@ def workload_spec(name: str) -> dict:
 
         lens = synth.ragged_lengths(BASE_SEED + 2, 64, 1024, 32768)
         layers = [dict(window=0, theta=1e6, divisor=1, seq=int(L), pos=int(L) - 1) for L in lens]
-        return dict(name=name, layers=layers, seed=BASE_SEED + 2, prep=False,
-                    desc="64 sequences, ragged lengths U[1024, 32768], global attention (decode only)")
+        return dict(name=name, layers=layers, seed=BASE_SEED + 2,
+                    desc="64 sequences, ragged lengths U[1024, 32768], global attention")
     raise SystemExit(f"unknown workload {name}")
 
 
@@ -95,71 +97,53 @@ def step_bytes(spec: dict) -> int:
 # ---- GPU side -----------------------------------------------------------------
 
 class CacheSet:
-    """One complete set of per-layer buffers (caches, q/k/v, outputs, tables)."""
+    """One complete set of per-entry buffers (caches, raw q/k/v projections, outputs) and
+    the prepared one-launch step over all entries."""
 
     def __init__(self, spec, set_idx, dev, torch, ops, synth, e2b):
-        self.layers = []
+        self.entries = []
         seed0 = spec["seed"] + 7919 * set_idx
         rf = torch.tensor(e2b.rope_freqs_f16_bits(256), dtype=torch.int32).to(torch.int16).to(dev)
-        ones = torch.full((HD,), 0x3C00, dtype=torch.int16, device=dev)  # weight 1.0 (f16)
-        prep_rows = []
+        ones = torch.full((HD,), 0x3C00, dtype=torch.int16, device=dev)  # norm weights 1.0 (f16)
+        inv_freq = {}  # one RoPE inverse-frequency table per (theta, divisor), as a model holds them
         for il, L in enumerate(spec["layers"]):
+            key = (L["theta"], L["divisor"])
+            if key not in inv_freq:
+                inv_freq[key] = ops.rope_inv_freq(L["theta"], HD, L["divisor"], rf)
             rows = L["seq"]
             kc = torch.empty(rows * NKH * HD, dtype=torch.float16, device=dev)
             vc = torch.empty_like(kc)
             n_att = attended(L["seq"], L["window"])
             lo = L["seq"] - n_att
-            for cache, off in ((kc, 0), (vc, 1)):
+            for cache, off in ((kc, 0), (vc, 1)):  # rows the step reads: N(0,1), then RMS-normalised per head
                 x = synth.normal_torch(seed0 + 1000 * il + off, n_att * NKH * HD, dev).view(-1, HD)
                 ms = (x.double() ** 2).mean(dim=1, keepdim=True)
                 y = (x.double() / torch.sqrt(ms + EPS)).to(torch.float16)
                 cache.view(rows, -1)[lo:lo + n_att].copy_(y.view(n_att, -1))
-            q = synth.normal_torch(seed0 + 1000 * il + 2, NQH * HD, dev)
-            if not spec.get("prep", True):  # decode-only workloads take unit-RMS queries as given
-                qh = q.view(NQH, HD).double()
-                q = (qh / torch.sqrt((qh ** 2).mean(dim=1, keepdim=True) + EPS)).float().reshape(-1).contiguous()
-            k = synth.normal_torch(seed0 + 1000 * il + 3, NKH * HD, dev)
-            v = synth.normal_torch(seed0 + 1000 * il + 4, NKH * HD, dev)
-            out = torch.zeros(NQH * HD, dtype=torch.float32, device=dev)
-            self.layers.append(dict(q=q, k=k, v=v, kc=kc.view(torch.int16), vc=vc.view(torch.int16), out=out,
-                                    seq=L["seq"], window=L["window"], pos=L["pos"]))
-            prep_rows.append(dict(q=q, k=k, v=v, q_weight=ones, k_weight=ones, rope_freqs=rf,
-                                  k_cache=kc.view(torch.int16), v_cache=vc.view(torch.int16), head_dim=HD,
-                                  theta=L["theta"], apply_divisor=L["divisor"], store_kv=True,
-                                  max_seq_len=rows))
-        self.rf, self.ones = rf, ones
-        self.with_prep = spec.get("prep", True)
-        self.uniform_pos = len({L["pos"] for L in spec["layers"]}) == 1
-        self.prep_table = ops.make_prep_table(prep_rows, NQH, NKH, dev) if self.uniform_pos else None
-        self.prep_rows = prep_rows
-        entries = ops.make_entries([(l["q"], l["kc"], l["vc"], l["out"], l["seq"], l["window"], 1.0)
-                                    for l in self.layers], NQH, NKH, HD)
-        total = sum(attended(l["seq"], l["window"]) for l in self.layers)
-        self.ws = torch.empty(ops.decode_many_workspace_bytes(len(entries), NQH, NKH, HD, total),
-                              dtype=torch.uint8, device=dev)
-        self.plan = ops.attn_decode_many_prepare(entries, NQH, NKH, HD, self.ws)
-        self.ws1 = torch.empty(ops.decode_workspace_bytes(NQH, NKH, HD, max(l["seq"] for l in self.layers)),
-                               dtype=torch.uint8, device=dev)
+            self.entries.append(dict(
+                q=synth.normal_torch(seed0 + 1000 * il + 2, NQH * HD, dev),
+                k=synth.normal_torch(seed0 + 1000 * il + 3, NKH * HD, dev),
+                v=synth.normal_torch(seed0 + 1000 * il + 4, NKH * HD, dev),
+                q_weight=ones, k_weight=ones, rope_freqs=rf, rope_inv_freq=inv_freq[key], k_cache=kc.view(torch.int16),
+                v_cache=vc.view(torch.int16), out=torch.zeros(NQH * HD, dtype=torch.float32, device=dev),
+                seq_len=L["seq"], position=L["pos"], sliding_window=L["window"], store_kv=True,
+                theta=L["theta"], apply_divisor=L["divisor"], scale=1.0, eps=EPS))
+        arr = ops.make_step_entries(self.entries, NQH, NKH, HD)
+        self.ws = torch.empty(ops.step_workspace_bytes(len(self.entries), NQH, NKH, HD), dtype=torch.uint8,
+                              device=dev)
+        self.plan = ops.attn_step_prepare(arr, NQH, NKH, HD, self.ws)
+        self.layer_plans = None
 
-    def prep(self, ops):
-        if not self.with_prep:
-            return
-        if self.uniform_pos:
-            pos = self.layers[0]["pos"]
-            ops.attn_prep_many(self.prep_table, len(self.layers), NQH, NKH, EPS, pos, pos)
-        else:
-            for l, r in zip(self.layers, self.prep_rows):
-                ops.attn_prep(r["q"], r["k"], r["v"], r["q_weight"], r["k_weight"], r["rope_freqs"], r["k_cache"],
-                              r["v_cache"], NQH, NKH, HD, EPS, l["pos"], r["theta"], r["apply_divisor"], l["pos"],
-                              r["max_seq_len"])
+    def prepare_per_entry(self, torch, ops, dev):
+        """One single-entry plan per entry: the engine's issue order (layer after layer)."""
+        self.layer_ws = [torch.empty(ops.step_workspace_bytes(1, NQH, NKH, HD), dtype=torch.uint8, device=dev)
+                         for _ in self.entries]
+        self.layer_plans = [ops.attn_step_prepare(ops.make_step_entries([e], NQH, NKH, HD), NQH, NKH, HD, w)
+                            for e, w in zip(self.entries, self.layer_ws)]
 
     def step_sequential(self, ops):
-        """The in-model order: per layer, prep then fused decode (split + merge)."""
-        for l, r in zip(self.layers, self.prep_rows):
-            ops.attn_prep(r["q"], r["k"], r["v"], r["q_weight"], r["k_weight"], r["rope_freqs"], r["k_cache"],
-                          r["v_cache"], NQH, NKH, HD, EPS, l["pos"], r["theta"], r["apply_divisor"], l["pos"],
-                          r["max_seq_len"])
-            ops.attn_decode(l["q"], l["kc"], l["vc"], l["out"], self.ws1, NQH, NKH, HD, l["seq"], 1.0, l["window"])
+        for p in self.layer_plans:
+            ops.attn_step_run(p)
 
 
 def run_gpu(spec, args):
@@ -184,49 +168,50 @@ def run_gpu(spec, args):
 
     def step(i, ev=None):
         cs = csets[i % sets]
-        cs.prep(ops)
-        if ev is not None:
-            ev[0].record(stream)
-        ops.attn_decode_many_run_split(cs.plan)
-        if ev is not None:
-            ev[1].record(stream)
-        ops.attn_decode_many_run_merge(cs.plan)
+        if ev is None:
+            ops.attn_step_run(cs.plan)
+            return
+        ops.attn_step_run_attention_timed(cs.plan, ev[0], ev[1])
+        ops.attn_step_run_merge(cs.plan)
 
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
     log(f"warmup {args.warmup} steps done")
 
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    # Timed region: exactly `steps` steps, synchronised on both sides.
     torch.cuda.synchronize()
     t_start = time.perf_counter()
     for i in range(args.steps):
-        step(args.warmup + i, evs[i])
+        step(args.warmup + i)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t_start
-    split_ms = [a.elapsed_time(b) for a, b in evs]
-    split_ms.sort()
-    split_avg = sum(split_ms) / len(split_ms)
-    log(f"timed {args.steps} steps: {wall / args.steps * 1e6:.1f} us/step; split kernel avg {split_avg * 1e3:.1f} us"
-        f" median {split_ms[len(split_ms) // 2] * 1e3:.1f} us")
+    log(f"timed {args.steps} steps: {wall / args.steps * 1e6:.2f} us/step")
 
-    # Event-free timing of the same steps (events add small gaps between launches).
+    # The attention kernel alone: HIP events on its stream that take the kernel's own start and
+    # end timestamps (hipExtLaunchKernelGGL), the figure rocprofv3 reports for the same kernel.
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    for a_, b_ in evs:  # create the HIP events
+        a_.record(stream)
+        b_.record(stream)
     torch.cuda.synchronize()
-    t1 = time.perf_counter()
     for i in range(args.steps):
-        step(i)
+        step(args.warmup + i, evs[i])
     torch.cuda.synchronize()
-    wall_noev = time.perf_counter() - t1
+    att_ms = sorted(a.elapsed_time(b) for a, b in evs)
+    att_avg = sum(att_ms) / len(att_ms)
+    log(f"k_attn_step: avg {att_avg * 1e3:.2f} us, median {att_ms[len(att_ms) // 2] * 1e3:.2f} us (events)")
+    result = dict(wall_s=wall, steps=args.steps, attn_avg_ms=att_avg, attn_median_ms=att_ms[len(att_ms) // 2],
+                  sets=sets, bytes=per_step)
 
-    result = dict(wall_s=min(wall, wall_noev), steps=args.steps, split_avg_ms=split_avg,
-                  split_median_ms=split_ms[len(split_ms) // 2], sets=sets, bytes=per_step)
-
-    # In-model order: layer after layer, each its own prep + decode launches, in a HIP graph.
+    # The engine's issue order: one single-entry step (attention + merge) per layer, replayed as a HIP graph.
     if args.sequential and len(spec["layers"]) > 1:
-        g = torch.cuda.CUDAGraph()
         cs = csets[0]
+        cs.prepare_per_entry(torch, ops, dev)
+        torch.cuda.synchronize()
         cs.step_sequential(ops)
         torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
             cs.step_sequential(ops)
         torch.cuda.synchronize()
@@ -241,6 +226,18 @@ def run_gpu(spec, args):
         result["sequential_us"] = (time.perf_counter() - t2) / n * 1e6
         log(f"layer-sequential (graph replay, one cache set): {result['sequential_us']:.1f} us/step")
     return result
+
+
+def read_traffic(workload: str):
+    """HBM bytes per k_attn_step launch from the committed counter summary of this workload
+    (FETCH_SIZE and WRITE_SIZE passes of rocprofv3 --pmc, scaled by a copy kernel's reading)."""
+    f = ROOT / "profiles" / f"k_attn_step_{workload}_traffic.txt"
+    if not f.exists():
+        return None
+    for line in f.read_text().splitlines():
+        if line.startswith("hbm_bytes_per_launch:"):
+            return int(float(line.split(":", 1)[1]))
+    return None
 
 
 # ---- CPU baseline (oracle on the host) --------------------------------------------
@@ -319,7 +316,8 @@ def main():
     r = run_gpu(spec, args)
     ms_per_step = r["wall_s"] / r["steps"] * 1e3
     value = r["bytes"] / (ms_per_step * 1e-3) / 1e9
-    achieved = r["bytes"] / (r["split_avg_ms"] * 1e-3) / 1e9
+    achieved = r["bytes"] / (r["attn_avg_ms"] * 1e-3) / 1e9
+    traffic = read_traffic(args.workload)
     line = {
         "metric": "decode-attention us/token & HBM GB/s (% roofline), E2B-shaped, bs1",
         "value": round(value, 1),
@@ -336,10 +334,12 @@ def main():
         "data": "synthetic (seeded splitmix64 N(0,1), unit-RMS rows), resident in HBM",
         "config": {"workload": spec["desc"], "batch": 1, "num_q_heads": NQH, "num_kv_heads": NKH,
                    "head_dim": HD, "bytes_per_step": r["bytes"], "cache_sets_rotated": r["sets"],
-                   "issue": "all layers of the step in one prep launch and one split-K decode launch pair"},
-        "roofline": {"bound": "hbm", "kernel": "k_decode_split", "achieved": round(achieved, 1),
+                   "issue": "all entries of the step in one attention launch (q/k RMSNorm+RoPE, v-norm, KV "
+                            "store, split-K attention) plus one log-sum-exp merge launch"},
+        "roofline": {"bound": "hbm", "kernel": "k_attn_step", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None, "avg_us": round(r["split_avg_ms"] * 1e3, 2)},
+                     "traffic": traffic, "avg_us": round(r["attn_avg_ms"] * 1e3, 2),
+                     "traffic_source": f"profiles/k_attn_step_{args.workload}_traffic.txt" if traffic else None},
     }
     if "sequential_us" in r:
         line["layer_sequential_us_per_token"] = round(r["sequential_us"], 2)

@@ -1,0 +1,109 @@
+#!/usr/bin/env python3
+"""Summarise rocprofv3 CSV output into the short text records kept under profiles/.
+
+    profile_summary.py trace  --dir D --command "..." [--kernel REGEX]
+        Kernel table of a `rocprofv3 --kernel-trace --stats -f csv -d D -- ...` run.
+
+    profile_summary.py traffic --fetch D1 --write D2 --copy-fetch D3 --copy-write D4
+                               --kernel REGEX --command "..." [--algorithmic-bytes N]
+        HBM bytes per launch of the kernel matching REGEX from one FETCH_SIZE and
+        one WRITE_SIZE pass (`rocprofv3 --pmc FETCH_SIZE -f csv -d D1 -- ...`),
+        each scaled by what the same counter reads for g4bench's plain copy kernel
+        (512 MiB read and 512 MiB written per launch).
+
+Counter values are KiB per dispatch. The summary prints `hbm_bytes_per_launch:`,
+which bench.py reads as the roofline's `traffic`.
+"""
+from __future__ import annotations
+
+import argparse
+import csv
+import re
+import statistics
+import sys
+from pathlib import Path
+
+COPY_BYTES = 512 << 20
+
+
+def _csvs(d: str, suffix: str) -> list[Path]:
+    files = sorted(Path(d).rglob(f"*{suffix}"))
+    if not files:
+        raise SystemExit(f"no *{suffix} under {d}")
+    return files
+
+
+def counter_per_dispatch(d: str, counter: str, kernel_re: str) -> tuple[float, int]:
+    """Mean counter value (summed over the rows of one dispatch) over matching dispatches."""
+    per_dispatch: dict[str, float] = {}
+    rx = re.compile(kernel_re)
+    for f in _csvs(d, "counter_collection.csv"):
+        for row in csv.DictReader(f.open()):
+            if row["Counter_Name"] != counter or not rx.search(row["Kernel_Name"]):
+                continue
+            key = f"{f}:{row['Dispatch_Id']}"
+            per_dispatch[key] = per_dispatch.get(key, 0.0) + float(row["Counter_Value"])
+    if not per_dispatch:
+        raise SystemExit(f"no {counter} rows for kernel /{kernel_re}/ under {d}")
+    return statistics.fmean(per_dispatch.values()), len(per_dispatch)
+
+
+def cmd_trace(a) -> None:
+    rows = []
+    for f in _csvs(a.dir, "kernel_stats.csv"):
+        rows += list(csv.DictReader(f.open()))
+    print(f"command: {a.command}")
+    print("kernel stats (rocprofv3 --kernel-trace --stats; durations in us)")
+    print(f"{'kernel':60s} {'calls':>6s} {'avg':>9s} {'min':>9s} {'max':>9s} {'pct':>6s}")
+    for r in sorted(rows, key=lambda r: -float(r["TotalDurationNs"])):
+        name = r["Name"]
+        if a.kernel and not re.search(a.kernel, name):
+            continue
+        print(f"{name[:60]:60s} {int(r['Calls']):6d} {float(r['AverageNs']) / 1e3:9.2f} "
+              f"{float(r['MinNs']) / 1e3:9.2f} {float(r['MaxNs']) / 1e3:9.2f} {float(r['Percentage']):6.2f}")
+
+
+def cmd_traffic(a) -> None:
+    copy_re = r"k_copy"
+    cf, _ = counter_per_dispatch(a.copy_fetch, "FETCH_SIZE", copy_re)
+    cw, _ = counter_per_dispatch(a.copy_write, "WRITE_SIZE", copy_re)
+    fetch_scale = COPY_BYTES / (cf * 1024.0)
+    write_scale = COPY_BYTES / (cw * 1024.0)
+    kf, nf = counter_per_dispatch(a.fetch, "FETCH_SIZE", a.kernel)
+    kw, nw = counter_per_dispatch(a.write, "WRITE_SIZE", a.kernel)
+    fetch_b = kf * 1024.0 * fetch_scale
+    write_b = kw * 1024.0 * write_scale
+    print(f"command: {a.command}")
+    print(f"kernel: /{a.kernel}/ ({nf} dispatches in the FETCH_SIZE pass, {nw} in the WRITE_SIZE pass)")
+    print(f"copy calibration: FETCH_SIZE {cf:.1f} KiB and WRITE_SIZE {cw:.1f} KiB per 512 MiB copy launch")
+    print(f"fetch_scale: {fetch_scale:.4f}")
+    print(f"write_scale: {write_scale:.4f}")
+    print(f"fetch_kib_per_launch: {kf:.1f}")
+    print(f"write_kib_per_launch: {kw:.1f}")
+    print(f"hbm_read_bytes_per_launch: {fetch_b:.0f}")
+    print(f"hbm_write_bytes_per_launch: {write_b:.0f}")
+    print(f"hbm_bytes_per_launch: {fetch_b + write_b:.0f}")
+    if a.algorithmic_bytes:
+        print(f"algorithmic_bytes_per_launch: {a.algorithmic_bytes}")
+        print(f"traffic_over_algorithmic: {(fetch_b + write_b) / a.algorithmic_bytes:.4f}")
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    sub = ap.add_subparsers(dest="mode", required=True)
+    t = sub.add_parser("trace")
+    t.add_argument("--dir", required=True)
+    t.add_argument("--command", required=True)
+    t.add_argument("--kernel", default="")
+    f = sub.add_parser("traffic")
+    for k in ("fetch", "write", "copy_fetch", "copy_write"):
+        f.add_argument("--" + k.replace("_", "-"), dest=k, required=True)
+    f.add_argument("--kernel", required=True)
+    f.add_argument("--command", required=True)
+    f.add_argument("--algorithmic-bytes", type=int, default=0)
+    a = ap.parse_args()
+    {"trace": cmd_trace, "traffic": cmd_traffic}[a.mode](a)
+
+
+if __name__ == "__main__":
+    sys.exit(main())

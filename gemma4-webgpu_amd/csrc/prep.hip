@@ -100,3 +100,30 @@ extern "C" int g4_attn_prep(float* q, float* k, float* v, const uint16_t* q_weig
     G4_CHECK_LAUNCH("attnPrep");
     return G4_OK;
 }
+
+namespace g4 {
+
+// RoPE inverse frequencies of one (theta, divisor) configuration: the
+// position-independent factor of every angle (fused_per_head_norm_rope.wgsl:
+// 50-54), evaluated exactly as the reference kernels do.
+__global__ __launch_bounds__(kWG) void k_rope_inv_freq(float theta, unsigned head_dim, unsigned apply_divisor,
+                                                       const uint16_t* __restrict__ rope_freqs,
+                                                       float* __restrict__ inv_freq) {
+    const unsigned i = blockIdx.x * kWG + threadIdx.x;
+    if (i >= head_dim / 2) return;
+    inv_freq[i] = rope_inv_freq(i, head_dim, theta, apply_divisor, apply_divisor ? h2f(rope_freqs[i]) : 1.0f);
+}
+
+}  // namespace g4
+
+extern "C" int g4_rope_inv_freq(float theta, uint32_t head_dim, uint32_t apply_divisor, const uint16_t* rope_freqs,
+                                float* inv_freq, void* stream) {
+    if (!inv_freq) return fail(G4_EINVAL, "ropeInvFreq: NULL output");
+    if (head_dim == 0 || head_dim % 2) return fail(G4_EINVAL, "ropeInvFreq: head_dim %u", head_dim);
+    if (apply_divisor && !rope_freqs) return fail(G4_EINVAL, "ropeInvFreq: apply_divisor needs rope_freqs");
+    const unsigned half = head_dim / 2;
+    hipLaunchKernelGGL(k_rope_inv_freq, dim3((half + kWG - 1) / kWG), dim3(kWG), 0, as_stream(stream), theta,
+                       head_dim, apply_divisor, rope_freqs, inv_freq);
+    G4_CHECK_LAUNCH("ropeInvFreq");
+    return G4_OK;
+}

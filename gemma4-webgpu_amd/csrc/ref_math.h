@@ -31,15 +31,22 @@ __device__ __forceinline__ float wg_tree_max(float* s, unsigned tid) {
     return s[0];
 }
 
-// RoPE angle terms of pair i: freq = 1/pow(theta, 2i/HD) (optionally divided
-// by rope_freqs[i], given here as its value), angle = f32(position) * freq.
-__device__ __forceinline__ float rope_angle_val(unsigned i, unsigned head_dim, float theta, unsigned position,
-                                                 unsigned apply_divisor, float divisor) {
+// RoPE inverse frequency of pair i (fused_per_head_norm_rope.wgsl:50-54):
+// 1/pow(theta, 2i/HD) (pow in f64, rounded to f32), optionally divided by
+// rope_freqs[i] (given here as its value). Independent of the position.
+__device__ __forceinline__ float rope_inv_freq(unsigned i, unsigned head_dim, float theta, unsigned apply_divisor,
+                                               float divisor) {
     float e = (float)(i * 2u) / (float)head_dim;
     float base_freq = 1.0f / (float)pow((double)theta, (double)e);
     float freq = base_freq;
     if (apply_divisor != 0u) freq = base_freq / divisor;
-    return (float)position * freq;
+    return freq;
+}
+
+// The angle of pair i at `position` (fused_per_head_norm_rope.wgsl:55).
+__device__ __forceinline__ float rope_angle_val(unsigned i, unsigned head_dim, float theta, unsigned position,
+                                                unsigned apply_divisor, float divisor) {
+    return (float)position * rope_inv_freq(i, head_dim, theta, apply_divisor, divisor);
 }
 
 __device__ __forceinline__ float rope_angle(unsigned i, unsigned head_dim, float theta, unsigned position,

@@ -37,6 +37,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <hip/hip_ext.h>
+
 #include <vector>
 
 #include "decode_core.h"
@@ -51,6 +53,7 @@ struct StepEntryDev {
     const uint16_t* q_weight;
     const uint16_t* k_weight;
     const uint16_t* rope_freqs;
+    const float* rope_inv_freq;  // optional precomputed inverse frequencies
     uint16_t* k_cache;  // [rows][num_kv_heads][HD]
     uint16_t* v_cache;
     float* out;         // attnOut [num_kv_heads][group][HD]
@@ -139,7 +142,6 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void k_attn_step(StepArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: branches on it stay scalar
     const int n = lane & 15;
     const int g = lane >> 4;
-    const int head = n & 7;
     const bool lo_col = n >= 8;
 
     const StepWorkDev wk = a.work[blockIdx.x];
@@ -159,8 +161,10 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void k_attn_step(StepArgs a) {
     // wait for the tile. f16 values stay unconverted until used.
     const unsigned pair = (unsigned)wave * 32u + (unsigned)(lane & 31);  // RoPE pair computed by this lane
     const unsigned apply_divisor = ent.apply_divisor;
-    // Without the divisor the table may be absent: read a valid dummy instead.
+    const float* inv_tab = ent.rope_inv_freq;
+    // Absent tables are replaced by a valid dummy address (the values are not used).
     const uint32_t fbits = ldg<uint16_t>((apply_divisor ? ent.rope_freqs : ent.q_weight) + pair);
+    const float tab_freq = ldg<float>((inv_tab ? inv_tab : ent.q) + pair);
     float xq[2][4];
 #pragma unroll
     for (int r = 0; r < 2; r++) {
@@ -192,12 +196,16 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void k_attn_step(StepArgs a) {
     load_v_tile<HD>(Vb, row_bytes, last, n, g, k0 + t0, vreg);
     __builtin_amdgcn_sched_barrier(0);  // keep every request above ahead of the arithmetic below
 
-    // ---- RoPE factors (the reference's expressions, f64 transcendentals) ----
+    // ---- RoPE factors: one pair per lane (lanes 32..63 repeat 0..31), the
+    // reference's expressions with f64 transcendentals ----
     {
-        // Division by 1 is exact, so dividing unconditionally equals the
-        // reference's conditional division (and keeps the load unconditional).
-        const float div = apply_divisor ? h2f((uint16_t)fbits) : 1.0f;
-        const float ang = rope_angle_val(pair, HD, ent.theta, ent.position, 1u, div);
+        float freq;
+        if (inv_tab) {
+            freq = tab_freq;
+        } else {  // division by 1 is exact: dividing unconditionally keeps the load unconditional
+            freq = rope_inv_freq(pair, HD, ent.theta, 1u, apply_divisor ? h2f((uint16_t)fbits) : 1.0f);
+        }
+        const float ang = (float)ent.position * freq;
         const float c = (float)cos((double)ang);
         const float s = (float)sin((double)ang);
         if (lane < 32) {
@@ -207,16 +215,25 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void k_attn_step(StepArgs a) {
     }
     __syncthreads();
 
-    // ---- q heads (two per wave), the current row's k and v ----
+    // ---- q heads (two per wave) straight into the score operand; the current
+    // row's k and v ----
     const RopeLane rl = {sm.rope_c[lane], sm.rope_s[lane], sm.rope_c[lane + 64], sm.rope_s[lane + 64]};
     const float qscale = ent.qscale, eps = ent.eps;
+    f16* qop = reinterpret_cast<f16*>(sm.dec.q);  // [chunk c][operand lane 16*g + column][8]
 #pragma unroll
     for (int r = 0; r < 2; r++) {
         const unsigned hq = (unsigned)wave + kDecodeWaves * r;
-        if (hq < G) {
-            wave_norm_rope(xq[r], wq, true, true, rl, eps);
+        const bool live = hq < G;  // columns of absent heads are zero
+        if (live) wave_norm_rope(xq[r], wq, true, true, rl, eps);
 #pragma unroll
-            for (int j = 0; j < 4; j++) sm.qf[hq][lane + 64 * j] = xq[r][j] * qscale;
+        for (int j = 0; j < 4; j++) {
+            const unsigned d = (unsigned)lane + 64u * j;
+            const float x = live ? xq[r][j] * qscale : 0.0f;
+            if (live) sm.qf[hq][d] = x;
+            const f16 hi = (f16)x;  // hi in column hq, the f16 residual in column hq + 8
+            const unsigned base = ((d >> 5) * 64u + 16u * ((d >> 3) & 3u) + hq) * 8u + (d & 7u);
+            qop[base] = hi;
+            qop[base + 64] = (f16)(x - (float)hi);
         }
     }
     if (do_new) {
@@ -233,29 +250,17 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void k_attn_step(StepArgs a) {
     }
     __syncthreads();
 
-    // ---- score operand from the prepared query, and the current row's scores ----
-    {
-        const bool live = (unsigned)head < G;
+    // The current row's scores (read by the combine, after later barriers).
+    if (has_new) {
+        const f16* kn = reinterpret_cast<const f16*>(sm.knew);
+        for (unsigned h = (unsigned)wave; h < G; h += kDecodeWaves) {
+            float p = 0.0f;
 #pragma unroll
-        for (int cc = 0; cc < D::NC / kDecodeWaves; cc++) {
-            const int c = wave * (D::NC / kDecodeWaves) + cc;
-            float x[8];
-#pragma unroll
-            for (int i = 0; i < 8; i++) x[i] = live ? sm.qf[head][c * 32 + g * 8 + i] : 0.0f;
-            store_q_chunk<HD>(sm.dec, c, lane, x, lo_col);
-        }
-        if (has_new) {
-            const f16* kn = reinterpret_cast<const f16*>(sm.knew);
-            for (unsigned h = (unsigned)wave; h < G; h += kDecodeWaves) {
-                float p = 0.0f;
-#pragma unroll
-                for (int j = 0; j < 4; j++) p += sm.qf[h][lane + 64 * j] * (float)kn[lane + 64 * j];
-                for (int off = 32; off > 0; off >>= 1) p += __shfl_xor(p, off);
-                if (lane == 0) sm.mnew[h] = p;
-            }
+            for (int j = 0; j < 4; j++) p += sm.qf[h][lane + 64 * j] * (float)kn[lane + 64 * j];
+            for (int off = 32; off > 0; off >>= 1) p += __shfl_xor(p, off);
+            if (lane == 0) sm.mnew[h] = p;
         }
     }
-    __syncthreads();
 
     // ---- tiles ----
     float m_run = -INFINITY, l_run = 0.0f;
@@ -292,7 +297,7 @@ namespace {
 // Partial records: an entry gets more than one workgroup only while the
 // workgroups fit one wave of the GPU (at most kStepMaxWgs), so at most that
 // many records exist.
-constexpr unsigned kStepMaxWgs = 4096;
+constexpr unsigned kStepMaxWgs = 1024;
 constexpr uint32_t kStepMagic = 0x67345354u;
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -426,6 +431,7 @@ int g4_attn_step_prepare(const g4_step_entry* entries, uint32_t n_entries, uint3
         d.q_weight = s.q_weight;
         d.k_weight = s.k_weight;
         d.rope_freqs = s.rope_freqs;
+        d.rope_inv_freq = s.rope_inv_freq;
         d.k_cache = s.k_cache;
         d.v_cache = s.v_cache;
         d.out = s.out;
@@ -491,11 +497,17 @@ int g4_attn_step_prepare(const g4_step_entry* entries, uint32_t n_entries, uint3
     return G4_OK;
 }
 
-int g4_attn_step_run(const g4_decode_plan* plan, void* stream) {
+static int step_plan(const g4_decode_plan* plan, StepPlanRep* r) {
     if (!plan) return fail(G4_EINVAL, "attnStep: plan is NULL");
+    memcpy(r, plan, sizeof *r);
+    if (r->magic != kStepMagic) return fail(G4_EINVAL, "attnStep: plan was not prepared by g4_attn_step_prepare");
+    return G4_OK;
+}
+
+static int launch_attention(const g4_decode_plan* plan, void* stream, hipEvent_t start, hipEvent_t stop) {
     StepPlanRep r;
-    memcpy(&r, plan, sizeof r);
-    if (r.magic != kStepMagic) return fail(G4_EINVAL, "attnStep: plan was not prepared by g4_attn_step_prepare");
+    int rc = step_plan(plan, &r);
+    if (rc) return rc;
     const StepLayout L = step_layout(r.n_entries, r.num_kv_heads, r.group, kStepHD);
     StepArgs a = {};
     a.table = reinterpret_cast<const StepEntryDev*>(r.ws + L.table);
@@ -504,18 +516,44 @@ int g4_attn_step_run(const g4_decode_plan* plan, void* stream) {
     a.group = r.group;
     a.part_ml = reinterpret_cast<float*>(r.ws + L.part_ml);
     a.part_o = reinterpret_cast<float*>(r.ws + L.part_o);
-    hipStream_t st = as_stream(stream);
-    hipLaunchKernelGGL(k_attn_step, dim3(r.n_wgs, r.num_kv_heads), dim3(kDecodeThreads), 0, st, a);
+    if (start || stop)
+        hipExtLaunchKernelGGL(k_attn_step, dim3(r.n_wgs, r.num_kv_heads), dim3(kDecodeThreads), 0, as_stream(stream),
+                              start, stop, 0, a);
+    else
+        hipLaunchKernelGGL(k_attn_step, dim3(r.n_wgs, r.num_kv_heads), dim3(kDecodeThreads), 0, as_stream(stream), a);
     G4_CHECK_LAUNCH("attnStep");
+    return G4_OK;
+}
+
+int g4_attn_step_run_attention(const g4_decode_plan* plan, void* stream) {
+    return launch_attention(plan, stream, nullptr, nullptr);
+}
+
+int g4_attn_step_run_attention_timed(const g4_decode_plan* plan, void* stream, void* start_event, void* stop_event) {
+    if (!start_event || !stop_event) return fail(G4_EINVAL, "attnStep: timing events are NULL");
+    return launch_attention(plan, stream, static_cast<hipEvent_t>(start_event), static_cast<hipEvent_t>(stop_event));
+}
+
+int g4_attn_step_run_merge(const g4_decode_plan* plan, void* stream) {
+    StepPlanRep r;
+    int rc = step_plan(plan, &r);
+    if (rc) return rc;
     if (!r.any_split) return G4_OK;
+    const StepLayout L = step_layout(r.n_entries, r.num_kv_heads, r.group, kStepHD);
     DecodeArgs m = {};
     m.table = reinterpret_cast<const DecodeEntryDev*>(r.ws + L.merge_table);
     m.n_entries = r.n_entries;
     m.num_kv_heads = r.num_kv_heads;
     m.group = r.group;
-    m.part_o = a.part_o;
-    m.part_ml = a.part_ml;
-    return launch_decode_merge(m, r.n_entries, r.max_parts, st);
+    m.part_ml = reinterpret_cast<float*>(r.ws + L.part_ml);
+    m.part_o = reinterpret_cast<float*>(r.ws + L.part_o);
+    return launch_decode_merge(m, r.n_entries, r.max_parts, as_stream(stream));
+}
+
+int g4_attn_step_run(const g4_decode_plan* plan, void* stream) {
+    int rc = g4_attn_step_run_attention(plan, stream);
+    if (rc) return rc;
+    return g4_attn_step_run_merge(plan, stream);
 }
 
 int g4_attn_step(const g4_step_entry* entries, uint32_t n_entries, uint32_t num_q_heads, uint32_t num_kv_heads,

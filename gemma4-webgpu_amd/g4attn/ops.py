@@ -219,10 +219,22 @@ def step_workspace_bytes(n_entries, num_q_heads, num_kv_heads, head_dim) -> int:
     return n.value
 
 
+def rope_inv_freq(theta, head_dim, apply_divisor, rope_freqs=None, stream=None) -> torch.Tensor:
+    """The [head_dim/2] f32 RoPE inverse-frequency table of one (theta, divisor) configuration."""
+    if apply_divisor and rope_freqs is None:
+        raise ValueError("apply_divisor needs rope_freqs")
+    dev = rope_freqs.device if rope_freqs is not None else torch.device("cuda", torch.cuda.current_device())
+    out = torch.empty(head_dim // 2, dtype=torch.float32, device=dev)
+    rf = _f16(rope_freqs, "rope_freqs", head_dim // 2) if rope_freqs is not None else None
+    abi.call("g4_rope_inv_freq", float(theta), head_dim, 1 if apply_divisor else 0, rf, _f32(out, "out", head_dim // 2),
+             _stream(stream))
+    return out
+
+
 def make_step_entries(items, num_q_heads, num_kv_heads, head_dim):
     """items: iterable of dicts with q, k, v (raw f32 projections), q_weight, k_weight (f16), rope_freqs (f16 or
-    None), k_cache, v_cache (f16, at least seq_len rows), out (f32), seq_len, position, sliding_window, store_kv,
-    theta, apply_divisor, scale, eps."""
+    None), rope_inv_freq (optional f32 table from rope_inv_freq()), k_cache, v_cache (f16, at least seq_len rows),
+    out (f32), seq_len, position, sliding_window, store_kv, theta, apply_divisor, scale, eps."""
     items = list(items)
     arr = (StepEntry * len(items))()
     for i, it in enumerate(items):
@@ -236,6 +248,8 @@ def make_step_entries(items, num_q_heads, num_kv_heads, head_dim):
             _f32(it["v"], f"entry {i} v", nkv), _f16(it["q_weight"], f"entry {i} q_weight", head_dim),
             _f16(it["k_weight"], f"entry {i} k_weight", head_dim),
             _f16(rf, f"entry {i} rope_freqs", head_dim // 2) if rf is not None else None,
+            _f32(it["rope_inv_freq"], f"entry {i} rope_inv_freq", head_dim // 2)
+            if it.get("rope_inv_freq") is not None else None,
             _f16(it["k_cache"], f"entry {i} k_cache", L * nkv), _f16(it["v_cache"], f"entry {i} v_cache", L * nkv),
             _f32(it["out"], f"entry {i} out", num_q_heads * head_dim), L, int(it["position"]),
             int(it.get("sliding_window", 0)), 1 if it.get("store_kv", True) else 0, float(it["theta"]),
@@ -252,6 +266,24 @@ def attn_step_prepare(entries, num_q_heads, num_kv_heads, head_dim, workspace, s
 
 def attn_step_run(plan: DecodePlan, stream=None):
     abi.call("g4_attn_step_run", C.byref(plan), _stream(stream))
+
+
+def attn_step_run_attention(plan: DecodePlan, stream=None):
+    abi.call("g4_attn_step_run_attention", C.byref(plan), _stream(stream))
+
+
+def attn_step_run_merge(plan: DecodePlan, stream=None):
+    abi.call("g4_attn_step_run_merge", C.byref(plan), _stream(stream))
+
+
+def attn_step_run_attention_timed(plan: DecodePlan, start, stop, stream=None):
+    """The attention launch with torch.cuda.Events (timing enabled) that take the kernel's own
+    start and end timestamps. The events must exist: record each once before the first use."""
+    for e, name in ((start, "start"), (stop, "stop")):
+        if not getattr(e, "cuda_event", 0):
+            raise ValueError(f"{name} event has no HIP event yet (record it once first)")
+    abi.call("g4_attn_step_run_attention_timed", C.byref(plan), _stream(stream), C.c_void_p(start.cuda_event),
+             C.c_void_p(stop.cuda_event))
 
 
 def attn_step(entries, num_q_heads, num_kv_heads, head_dim, workspace, stream=None):

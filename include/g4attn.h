@@ -253,6 +253,16 @@ int g4_attn_decode_many(const g4_decode_entry* entries, uint32_t n_entries, uint
                         uint32_t num_kv_heads, uint32_t head_dim, void* workspace, size_t workspace_bytes,
                         void* stream);
 
+/* ---- RoPE inverse frequencies ---------------------------------------------
+ * inv_freq[i] = f32(1 / pow(theta, 2i/head_dim)) (divided by rope_freqs[i]
+ * when apply_divisor), i < head_dim/2: the position-independent factor of
+ * the angle in fused_per_head_norm_rope.wgsl:50-54, bit-identical to what
+ * g4_fused_per_head_norm_rope evaluates. A model has one table per RoPE
+ * configuration (Gemma 4: local theta 1e4; global theta 1e6 with the
+ * proportional divisor); compute them once and pass them in g4_step_entry. */
+int g4_rope_inv_freq(float theta, uint32_t head_dim, uint32_t apply_divisor, const uint16_t* rope_freqs,
+                     float* inv_freq, void* stream);
+
 /* ---- one-launch decode step ---------------------------------------------
  * The whole attention block of one token for many layers or sequences in one
  * launch: per entry, q RMSNorm + RoPE, the current row's k (norm + RoPE) and v
@@ -273,6 +283,8 @@ typedef struct g4_step_entry {
     const uint16_t* q_weight;  /* attn_q_norm, f16 [head_dim] */
     const uint16_t* k_weight;  /* attn_k_norm, f16 [head_dim] */
     const uint16_t* rope_freqs; /* f16 divisor table, read when apply_divisor */
+    const float* rope_inv_freq; /* optional [head_dim/2] table from g4_rope_inv_freq for this entry's
+                                   theta/divisor (computed once, at load); NULL: computed per launch */
     uint16_t* k_cache;         /* f16 [rows][num_kv_heads][head_dim]; rows < seq_len - 1 hold earlier tokens */
     uint16_t* v_cache;
     float* out;                /* attnOut [num_q_heads][head_dim] f32 */
@@ -292,6 +304,16 @@ int g4_attn_step_prepare(const g4_step_entry* entries, uint32_t n_entries, uint3
                          uint32_t num_kv_heads, uint32_t head_dim, void* workspace, size_t workspace_bytes,
                          g4_decode_plan* plan, void* stream);
 int g4_attn_step_run(const g4_decode_plan* plan, void* stream);
+/* The two launches of g4_attn_step_run, separately: the attention pass (one
+ * kernel for all entries), then the log-sum-exp merge of entries spread over
+ * more than one workgroup (nothing when there are none). */
+int g4_attn_step_run_attention(const g4_decode_plan* plan, void* stream);
+int g4_attn_step_run_merge(const g4_decode_plan* plan, void* stream);
+/* Measurement hook (the reference times passes with WebGPU timestamp
+ * queries, src/engine.ts:131-135, 411-414): the attention launch of
+ * g4_attn_step_run_attention with two hipEvent_t (created with timing enabled)
+ * that record the kernel's own start and end. */
+int g4_attn_step_run_attention_timed(const g4_decode_plan* plan, void* stream, void* start_event, void* stop_event);
 /* prepare + run. */
 int g4_attn_step(const g4_step_entry* entries, uint32_t n_entries, uint32_t num_q_heads, uint32_t num_kv_heads,
                  uint32_t head_dim, void* workspace, size_t workspace_bytes, void* stream);

@@ -124,6 +124,14 @@ def f16_bits_to_f32(h) -> np.ndarray:
 
 # ---- the six WGSL kernels ----------------------------------------------------
 
+def rope_inv_freq(theta, head_dim, apply_divisor, rope_freqs_bits=None) -> np.ndarray:
+    """fused_per_head_norm_rope.wgsl:50-54 for i < head_dim/2: the angle's position-independent factor."""
+    rf = _u16(rope_freqs_bits if rope_freqs_bits is not None else np.zeros(max(head_dim // 2, 1), np.uint16))
+    out = np.empty(head_dim // 2, dtype=np.float32)
+    lib().wr_rope_inv_freq(C.c_float(theta), C.c_uint32(head_dim), C.c_uint32(apply_divisor), _p(rf), _p(out))
+    return out
+
+
 def fused_per_head_norm_rope(data, weight_bits, rope_freqs_bits, num_heads, head_dim, eps, position, theta,
                              apply_divisor, num_workgroups=None):
     d = _f32(data)

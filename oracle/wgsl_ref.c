@@ -131,6 +131,22 @@ typedef struct { uint32_t num_q_heads, num_kv_heads, head_dim, seq_len; } wr_att
 
 /* ---- shaders/fused_per_head_norm_rope.wgsl:20-64 ----------------------- *
  * Dispatched with num_workgroups = num_heads (engine.ts:2078-2085).        */
+/* fused_per_head_norm_rope.wgsl:50-54: the position-independent factor of
+ * the angle of pair i. */
+static float rope_freq(uint32_t i, uint32_t head_dim, float theta, uint32_t apply_divisor,
+                       const uint16_t* rope_freqs) {
+    float base_freq = 1.0f / wgsl_pow(theta, (float)(i * 2u) / (float)head_dim);
+    float freq = base_freq;
+    if (apply_divisor != 0u) freq = base_freq / wr_f16_to_f32(rope_freqs[i]);
+    return freq;
+}
+
+/* The table of rope_freq over i < head_dim/2 (what g4_rope_inv_freq computes). */
+void wr_rope_inv_freq(float theta, uint32_t head_dim, uint32_t apply_divisor, const uint16_t* rope_freqs,
+                      float* out) {
+    for (uint32_t i = 0; i < head_dim / 2u; i++) out[i] = rope_freq(i, head_dim, theta, apply_divisor, rope_freqs);
+}
+
 void wr_fused_per_head_norm_rope(float* data, const uint16_t* weight, const wr_norm_rope_params* p,
                                  const uint16_t* rope_freqs, uint32_t num_workgroups) {
 #pragma omp parallel for schedule(static)
@@ -154,9 +170,7 @@ void wr_fused_per_head_norm_rope(float* data, const uint16_t* weight, const wr_n
         uint32_t half_dim = p->head_dim / 2u;
         for (uint32_t tid = 0; tid < WG; tid++) {
             for (uint32_t i = tid; i < half_dim; i += WG) {
-                float base_freq = 1.0f / wgsl_pow(p->theta, (float)(i * 2u) / (float)p->head_dim);
-                float freq = base_freq;
-                if (p->apply_divisor != 0u) freq = base_freq / wr_f16_to_f32(rope_freqs[i]);
+                float freq = rope_freq(i, p->head_dim, p->theta, p->apply_divisor, rope_freqs);
                 float angle = (float)p->position * freq;
                 float cos_a = wgsl_cos(angle);
                 float sin_a = wgsl_sin(angle);

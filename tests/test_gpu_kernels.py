@@ -55,6 +55,16 @@ def test_fused_per_head_norm_rope_bits(dev, nh, hd, pos, theta, div):
     np.testing.assert_array_equal(bits(d), want.view(np.uint32))
 
 
+@pytest.mark.parametrize("theta,div,hd", [(1e4, 0, 256), (1e6, 1, 256), (1e6, 0, 512), (5e5, 1, 64)])
+def test_rope_inv_freq_bits(dev, theta, div, hd):
+    announce(f"ropeInvFreq theta={theta} div={div} hd={hd}")
+    rf = ROPE_FREQS if hd // 2 <= ROPE_FREQS.size else np.resize(ROPE_FREQS, hd // 2)
+    want = orc.rope_inv_freq(theta, hd, div, rf)
+    got = ops.rope_inv_freq(theta, hd, div, t_u16(rf, dev) if div else None)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(bits(got), want.view(np.uint32))
+
+
 @pytest.mark.parametrize("nh,hd", [(1, 256), (1, 512), (4, 256), (3, 100)])
 def test_v_norm_bits(dev, nh, hd):
     announce(f"perHeadRmsNormNoWeight nh={nh} hd={hd}")

@@ -56,11 +56,14 @@ class Layer:
         self.dqw, self.dkw, self.drf = t16(self.qw, dev), t16(self.kw, dev), t16(ROPE, dev)
         self.nqh, self.nkh = nqh, nkh
 
-    def entry(self, store=True, raw_kv=None):
+    def entry(self, store=True, raw_kv=None, inv_freq=False):
         k, v = (self.d["k"], self.d["v"]) if raw_kv is None else raw_kv
-        return dict(q=self.d["q"], k=k, v=v, q_weight=self.dqw, k_weight=self.dkw, rope_freqs=self.drf,
-                    k_cache=self.kc, v_cache=self.vc, out=self.out, seq_len=self.seq, position=self.pos,
-                    sliding_window=self.window, store_kv=store, theta=self.theta, apply_divisor=self.divisor)
+        e = dict(q=self.d["q"], k=k, v=v, q_weight=self.dqw, k_weight=self.dkw, rope_freqs=self.drf,
+                 k_cache=self.kc, v_cache=self.vc, out=self.out, seq_len=self.seq, position=self.pos,
+                 sliding_window=self.window, store_kv=store, theta=self.theta, apply_divisor=self.divisor)
+        if inv_freq:
+            e["rope_inv_freq"] = ops.rope_inv_freq(self.theta, HD, self.divisor, self.drf)
+        return e
 
     def expected(self, kv_from=None):
         """Oracle: prep then the reference chain over f32-widened caches (current row = RNE(k'), RNE(v'))."""
@@ -115,6 +118,20 @@ def test_step_single_entry(dev, seq, win, theta, div):
     print(f"seq={seq} win={win} err={err:.2e}")
 
 
+@pytest.mark.parametrize("seq,win,theta,div", [(513, 512, 1e4, 0), (8193, 0, 1e6, 1), (40000, 0, 1e6, 1)])
+def test_step_rope_table_same_bits(dev, seq, win, theta, div):
+    """Entries carrying the precomputed inverse-frequency table give the same bits as entries without."""
+    announce(f"attnStep with rope_inv_freq seq={seq} win={win}")
+    L = Layer(dev, 400 + seq, seq, win, theta, div)
+    want, kb, vb = L.expected()
+    run_step(dev, [L.entry(inv_freq=True)])
+    check(L, want, kb, vb, "table")
+    with_table = L.out.cpu().numpy().copy()
+    L.out.fill_(float("nan"))
+    run_step(dev, [L.entry()])
+    np.testing.assert_array_equal(L.out.cpu().numpy().view(np.uint32), with_table.view(np.uint32))
+
+
 @pytest.mark.parametrize("seq", [2049, 8193])
 def test_step_e2b_stack(dev, seq):
     """35 layers (7 global theta 1e6 with the rope_freqs divisor, 28 local W=512 theta 1e4) in one launch."""
@@ -122,7 +139,7 @@ def test_step_e2b_stack(dev, seq):
     cfg = e2b.AttnConfig(num_layers=35)
     layers = [Layer(dev, 1000 * il + seq, seq, e2b.sliding_window(il, cfg), e2b.rope_theta(il, cfg),
                     e2b.apply_divisor(il, cfg)) for il in range(35)]
-    run_step(dev, [L.entry() for L in layers])
+    run_step(dev, [L.entry(inv_freq=il % 2 == 0) for il, L in enumerate(layers)])
     worst = 0.0
     for il, L in enumerate(layers):
         want, kb, vb = L.expected()

@@ -167,6 +167,25 @@ def test_rope_invariants(oracle):
     assert np.max(np.abs(g[:, :64] - yr[:, :64])) > 0.1
 
 
+@pytest.mark.parametrize("theta,div,hd", [(1e4, 0, 256), (1e6, 1, 256), (1e6, 0, 512), (1e4, 1, 256)])
+def test_rope_inv_freq_table(oracle, theta, div, hd):
+    """The angle's position-independent factor, restated in numpy: the same f32 steps."""
+    got = oracle.rope_inv_freq(theta, hd, div, ROPE_FREQS if div else None)
+    pos = 1
+    want = _f32_angles(pos, theta, hd, div)  # f32(1) * freq == freq
+    np.testing.assert_array_equal(got.view(np.uint32), want.astype(np.float32).view(np.uint32))
+    assert got[0] == (1.0 / ROPE_FREQS[0:1].view(np.float16).astype(np.float32)[0] if div else 1.0)
+    # angle = f32(pos) * freq reproduces the norm-rope kernel's rotation exactly
+    x = synth.rms_normalize_rows(synth.normal(5, hd).reshape(1, hd)).ravel()
+    ang = (np.float32(777) * got).astype(np.float64)
+    c, s_ = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    y = cf.rms_norm(x, None, 0.0, hd).astype(np.float32)
+    h = hd // 2
+    rot = np.concatenate([y[:h] * c - y[h:] * s_, y[:h] * s_ + y[h:] * c])
+    np.testing.assert_allclose(oracle.fused_per_head_norm_rope(x, ONES(hd), ROPE_FREQS, 1, hd, 0.0, 777, theta, div),
+                               rot, atol=2e-6)
+
+
 # ---- kv cache store --------------------------------------------------------------
 
 def test_kv_cache_store_rows(oracle):
