@@ -106,10 +106,16 @@ static std::vector<Layer> workload(const std::string& w) {
     } else if (w == "layer512") {
         L.push_back({513, 512, 512, 1e4f, 0});
     } else if (w == "ragged64") {
-        uint64_t s = 20261203;
-        for (int i = 0; i < 64; i++) {  // lengths in [1024, 32768]
-            s = s * 6364136223846793005ull + 1442695040888963407ull;
-            unsigned len = 1024 + (unsigned)((s >> 33) % (32768 - 1024 + 1));
+        // lengths uniform in [1024, 32768]: lo + floor(u * (hi - lo + 1)), u the top 53 bits of
+        // splitmix64 element i of stream 20261203 (the sequence bench.py draws)
+        const uint64_t seed = 20261203;
+        for (uint64_t i = 1; i <= 64; i++) {
+            uint64_t z = seed + i * 0x9E3779B97F4A7C15ull;
+            z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+            z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+            z ^= z >> 31;
+            const double u = (double)(z >> 11) * (1.0 / 9007199254740992.0);
+            const unsigned len = 1024 + (unsigned)floor(u * (32768 - 1024 + 1));
             L.push_back({len, 0, len - 1, 1e6f, 1});
         }
     } else {
@@ -144,6 +150,7 @@ int main(int argc, char** argv) {
     }
     if (sets <= 0) sets = step_bytes >= (64ull << 20) ? (int)((512ull << 20) / step_bytes) + 1 : 1;
     printf("workload %s: %zu entries, %.1f MB/step, %d sets\n", wl.c_str(), L.size(), step_bytes / 1e6, sets);
+    printf("bytes_per_step: %llu\n", (unsigned long long)step_bytes);
 
     hipStream_t st;
     HK(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
