@@ -1,0 +1,566 @@
+// g4attn.node: Node N-API addon over the C ABI of libg4attn.so (include/g4attn.h).
+//
+// A thin shim: device pointers and streams travel as BigInt, Params structs as
+// the uniform bytes the engine already builds (makeUniformMixed,
+// src/engine.ts:460-478), copied by value into the C struct after a size
+// check. A non-zero status from the library becomes a thrown JS Error carrying
+// g4_last_error(). Every call enqueues on the given stream and returns; only
+// download() and streamSynchronize() wait.
+#include <node_api.h>
+#include <stdint.h>
+#include <string.h>
+
+#include <string>
+#include <vector>
+
+#include "g4attn.h"
+
+namespace {
+
+#define NAPI_OK(env, call)                                  \
+    do {                                                    \
+        if ((call) != napi_ok) {                            \
+            napi_throw_error((env), nullptr, "N-API call failed: " #call); \
+            return nullptr;                                 \
+        }                                                   \
+    } while (0)
+
+napi_value throw_status(napi_env env, int status) {
+    std::string msg = std::string("g4attn status ") + std::to_string(status) + ": " + g4_last_error();
+    napi_throw_error(env, nullptr, msg.c_str());
+    return nullptr;
+}
+
+struct Args {
+    napi_env env;
+    std::vector<napi_value> v;
+    bool ok = true;
+
+    Args(napi_env e, napi_callback_info info, size_t expect) : env(e), v(expect) {
+        size_t n = expect;
+        if (napi_get_cb_info(e, info, &n, v.data(), nullptr, nullptr) != napi_ok || n < expect) {
+            napi_throw_type_error(e, nullptr, ("expected " + std::to_string(expect) + " arguments").c_str());
+            ok = false;
+        }
+    }
+
+    // Device pointer or stream: BigInt (or 0 / null for the null stream).
+    void* ptr(size_t i) {
+        if (!ok) return nullptr;
+        napi_valuetype t;
+        napi_typeof(env, v[i], &t);
+        if (t == napi_null || t == napi_undefined) return nullptr;
+        if (t == napi_number) {
+            int64_t x = 0;
+            napi_get_value_int64(env, v[i], &x);
+            if (x != 0) fail("argument " + std::to_string(i) + ": pointers are BigInt");
+            return nullptr;
+        }
+        uint64_t x = 0;
+        bool lossless = false;
+        if (napi_get_value_bigint_uint64(env, v[i], &x, &lossless) != napi_ok || !lossless) {
+            fail("argument " + std::to_string(i) + ": expected a BigInt pointer");
+            return nullptr;
+        }
+        return reinterpret_cast<void*>(static_cast<uintptr_t>(x));
+    }
+    uint32_t u32(size_t i) {
+        uint32_t x = 0;
+        if (ok && napi_get_value_uint32(env, v[i], &x) != napi_ok) fail("argument " + std::to_string(i) + ": expected a number");
+        return x;
+    }
+    double f64(size_t i) {
+        double x = 0;
+        if (ok && napi_get_value_double(env, v[i], &x) != napi_ok) fail("argument " + std::to_string(i) + ": expected a number");
+        return x;
+    }
+    // Bytes of a TypedArray / DataView / Buffer argument.
+    bool bytes(size_t i, void** data, size_t* len) {
+        if (!ok) return false;
+        bool is_ta = false, is_dv = false;
+        napi_is_typedarray(env, v[i], &is_ta);
+        napi_is_dataview(env, v[i], &is_dv);
+        if (is_ta) {
+            napi_typedarray_type type;
+            size_t n;
+            napi_value ab;
+            size_t off;
+            napi_get_typedarray_info(env, v[i], &type, &n, data, &ab, &off);
+            size_t elem = 1;
+            switch (type) {
+                case napi_int16_array: case napi_uint16_array: elem = 2; break;
+                case napi_int32_array: case napi_uint32_array: case napi_float32_array: elem = 4; break;
+                case napi_float64_array: case napi_bigint64_array: case napi_biguint64_array: elem = 8; break;
+                default: elem = 1;
+            }
+            *len = n * elem;
+            return true;
+        }
+        if (is_dv) {
+            napi_value ab;
+            size_t off;
+            napi_get_dataview_info(env, v[i], len, data, &ab, &off);
+            return true;
+        }
+        fail("argument " + std::to_string(i) + ": expected a TypedArray or DataView");
+        return false;
+    }
+    // A Params struct from its uniform bytes (at least sizeof(T); the engine pads uniforms to 16).
+    template <typename T>
+    bool params(size_t i, T* out) {
+        void* d = nullptr;
+        size_t n = 0;
+        if (!bytes(i, &d, &n)) return false;
+        if (n < sizeof(T)) {
+            fail("argument " + std::to_string(i) + ": params are " + std::to_string(n) + " bytes, need " +
+                 std::to_string(sizeof(T)));
+            return false;
+        }
+        memcpy(out, d, sizeof(T));
+        return true;
+    }
+    void fail(const std::string& m) {
+        if (ok) napi_throw_type_error(env, nullptr, m.c_str());
+        ok = false;
+    }
+};
+
+napi_value undefined(napi_env env) {
+    napi_value u;
+    napi_get_undefined(env, &u);
+    return u;
+}
+
+napi_value bigint(napi_env env, void* p) {
+    napi_value r;
+    napi_create_bigint_uint64(env, static_cast<uint64_t>(reinterpret_cast<uintptr_t>(p)), &r);
+    return r;
+}
+
+napi_value number(napi_env env, double x) {
+    napi_value r;
+    napi_create_double(env, x, &r);
+    return r;
+}
+
+#define CALL(env, expr)                       \
+    do {                                      \
+        int st_ = (expr);                     \
+        if (st_ != G4_OK) return throw_status((env), st_); \
+    } while (0)
+
+// ---- device, streams, memory ------------------------------------------------
+
+napi_value Version(napi_env env, napi_callback_info) {
+    napi_value r;
+    napi_create_string_utf8(env, g4_version(), NAPI_AUTO_LENGTH, &r);
+    return r;
+}
+
+napi_value DeviceCount(napi_env env, napi_callback_info) {
+    int n = 0;
+    CALL(env, g4_device_count(&n));
+    return number(env, n);
+}
+
+napi_value SetDevice(napi_env env, napi_callback_info info) {
+    Args a(env, info, 1);
+    const uint32_t d = a.u32(0);
+    if (!a.ok) return nullptr;
+    CALL(env, g4_set_device((int)d));
+    return undefined(env);
+}
+
+napi_value StreamCreate(napi_env env, napi_callback_info) {
+    void* s = nullptr;
+    CALL(env, g4_stream_create(&s));
+    return bigint(env, s);
+}
+
+napi_value StreamDestroy(napi_env env, napi_callback_info info) {
+    Args a(env, info, 1);
+    void* s = a.ptr(0);
+    if (!a.ok) return nullptr;
+    CALL(env, g4_stream_destroy(s));
+    return undefined(env);
+}
+
+napi_value StreamSynchronize(napi_env env, napi_callback_info info) {
+    Args a(env, info, 1);
+    void* s = a.ptr(0);
+    if (!a.ok) return nullptr;
+    CALL(env, g4_stream_synchronize(s));
+    return undefined(env);
+}
+
+napi_value Malloc(napi_env env, napi_callback_info info) {
+    Args a(env, info, 1);
+    const double bytes = a.f64(0);
+    if (!a.ok) return nullptr;
+    if (bytes <= 0) {
+        napi_throw_range_error(env, nullptr, "malloc: size must be positive");
+        return nullptr;
+    }
+    void* p = nullptr;
+    CALL(env, g4_malloc(&p, (size_t)bytes));
+    return bigint(env, p);
+}
+
+napi_value Free(napi_env env, napi_callback_info info) {
+    Args a(env, info, 1);
+    void* p = a.ptr(0);
+    if (!a.ok) return nullptr;
+    CALL(env, g4_free(p));
+    return undefined(env);
+}
+
+// upload(dst, offset, data, stream): enqueues a copy of `data`'s bytes
+// (hipMemcpyAsync; the HIP runtime stages pageable source memory before it
+// returns, so `data` may be reused afterwards).
+napi_value Upload(napi_env env, napi_callback_info info) {
+    Args a(env, info, 4);
+    void* dst = a.ptr(0);
+    const double off = a.f64(1);
+    void* d = nullptr;
+    size_t n = 0;
+    a.bytes(2, &d, &n);
+    void* s = a.ptr(3);
+    if (!a.ok) return nullptr;
+    CALL(env, g4_upload(dst, (size_t)off, d, n, s));
+    return undefined(env);
+}
+
+// download(src, offset, out, stream): copies into `out` and waits for it.
+napi_value Download(napi_env env, napi_callback_info info) {
+    Args a(env, info, 4);
+    void* src = a.ptr(0);
+    const double off = a.f64(1);
+    void* d = nullptr;
+    size_t n = 0;
+    a.bytes(2, &d, &n);
+    void* s = a.ptr(3);
+    if (!a.ok) return nullptr;
+    CALL(env, g4_download(d, src, (size_t)off, n, s));
+    return undefined(env);
+}
+
+napi_value Zero(napi_env env, napi_callback_info info) {
+    Args a(env, info, 3);
+    void* p = a.ptr(0);
+    const double n = a.f64(1);
+    void* s = a.ptr(2);
+    if (!a.ok) return nullptr;
+    CALL(env, g4_zero(p, (size_t)n, s));
+    return undefined(env);
+}
+
+// ---- the six reference kernels (bindings in WGSL @binding order) -----------
+
+napi_value FusedPerHeadNormRope(napi_env env, napi_callback_info info) {
+    Args a(env, info, 5);  // data, weight, rope_freqs, params, stream
+    void* data = a.ptr(0);
+    void* w = a.ptr(1);
+    void* rf = a.ptr(2);
+    g4_norm_rope_params p;
+    a.params(3, &p);
+    void* s = a.ptr(4);
+    if (!a.ok) return nullptr;
+    CALL(env, g4_fused_per_head_norm_rope((float*)data, (const uint16_t*)w, (const uint16_t*)rf, p, s));
+    return undefined(env);
+}
+
+napi_value PerHeadRmsNormNoWeight(napi_env env, napi_callback_info info) {
+    Args a(env, info, 3);  // data, params, stream
+    void* data = a.ptr(0);
+    g4_norm_params p;
+    a.params(1, &p);
+    void* s = a.ptr(2);
+    if (!a.ok) return nullptr;
+    CALL(env, g4_per_head_rms_norm_no_weight((float*)data, p, s));
+    return undefined(env);
+}
+
+napi_value KvCacheStore(napi_env env, napi_callback_info info) {
+    Args a(env, info, 6);  // k_in, v_in, k_cache, v_cache, params, stream
+    void* k = a.ptr(0);
+    void* v = a.ptr(1);
+    void* kc = a.ptr(2);
+    void* vc = a.ptr(3);
+    g4_kv_store_params p;
+    a.params(4, &p);
+    void* s = a.ptr(5);
+    if (!a.ok) return nullptr;
+    CALL(env, g4_kv_cache_store((const float*)k, (const float*)v, (uint16_t*)kc, (uint16_t*)vc, p, s));
+    return undefined(env);
+}
+
+napi_value AttnScore(napi_env env, napi_callback_info info) {
+    Args a(env, info, 5);  // q, k_cache, scores, params, stream
+    void* q = a.ptr(0);
+    void* kc = a.ptr(1);
+    void* sc = a.ptr(2);
+    g4_attn_score_params p;
+    a.params(3, &p);
+    void* s = a.ptr(4);
+    if (!a.ok) return nullptr;
+    CALL(env, g4_attn_score((const float*)q, (const uint16_t*)kc, (float*)sc, p, s));
+    return undefined(env);
+}
+
+napi_value Softmax(napi_env env, napi_callback_info info) {
+    Args a(env, info, 3);  // scores, params, stream
+    void* sc = a.ptr(0);
+    g4_softmax_params p;
+    a.params(1, &p);
+    void* s = a.ptr(2);
+    if (!a.ok) return nullptr;
+    CALL(env, g4_softmax((float*)sc, p, s));
+    return undefined(env);
+}
+
+napi_value AttnOutput(napi_env env, napi_callback_info info) {
+    Args a(env, info, 5);  // probs, v_cache, output, params, stream
+    void* pr = a.ptr(0);
+    void* vc = a.ptr(1);
+    void* o = a.ptr(2);
+    g4_attn_output_params p;
+    a.params(3, &p);
+    void* s = a.ptr(4);
+    if (!a.ok) return nullptr;
+    CALL(env, g4_attn_output((const float*)pr, (const uint16_t*)vc, (float*)o, p, s));
+    return undefined(env);
+}
+
+// ---- RoPE tables and the one-launch step -----------------------------------
+
+napi_value RopeInvFreq(napi_env env, napi_callback_info info) {
+    Args a(env, info, 6);  // theta, head_dim, apply_divisor, rope_freqs, out, stream
+    const double theta = a.f64(0);
+    const uint32_t hd = a.u32(1), div = a.u32(2);
+    void* rf = a.ptr(3);
+    void* out = a.ptr(4);
+    void* s = a.ptr(5);
+    if (!a.ok) return nullptr;
+    CALL(env, g4_rope_inv_freq((float)theta, hd, div, (const uint16_t*)rf, (float*)out, s));
+    return undefined(env);
+}
+
+napi_value AttnStepWorkspaceSize(napi_env env, napi_callback_info info) {
+    Args a(env, info, 4);  // n_entries, num_q_heads, num_kv_heads, head_dim
+    const uint32_t n = a.u32(0), nqh = a.u32(1), nkh = a.u32(2), hd = a.u32(3);
+    if (!a.ok) return nullptr;
+    size_t bytes = 0;
+    CALL(env, g4_attn_step_workspace_size(n, nqh, nkh, hd, &bytes));
+    return number(env, (double)bytes);
+}
+
+bool get_prop(napi_env env, napi_value obj, const char* key, napi_value* out) {
+    bool has = false;
+    napi_has_named_property(env, obj, key, &has);
+    if (!has) return false;
+    napi_get_named_property(env, obj, key, out);
+    napi_valuetype t;
+    napi_typeof(env, *out, &t);
+    return t != napi_undefined && t != napi_null;
+}
+
+// One g4_step_entry from a JS object with the same field names in camelCase.
+bool step_entry(Args& a, napi_value obj, size_t idx, g4_step_entry* e) {
+    napi_env env = a.env;
+    memset(e, 0, sizeof *e);
+    struct {
+        const char* key;
+        const void** dst;
+        bool required;
+    } ptrs[] = {
+        {"q", (const void**)&e->q, true},
+        {"k", (const void**)&e->k, true},
+        {"v", (const void**)&e->v, true},
+        {"qWeight", (const void**)&e->q_weight, true},
+        {"kWeight", (const void**)&e->k_weight, true},
+        {"ropeFreqs", (const void**)&e->rope_freqs, false},
+        {"ropeInvFreq", (const void**)&e->rope_inv_freq, false},
+        {"kCache", (const void**)&e->k_cache, true},
+        {"vCache", (const void**)&e->v_cache, true},
+        {"out", (const void**)&e->out, true},
+    };
+    for (auto& p : ptrs) {
+        napi_value v;
+        if (!get_prop(env, obj, p.key, &v)) {
+            if (p.required) {
+                a.fail("entry " + std::to_string(idx) + ": missing " + p.key);
+                return false;
+            }
+            continue;
+        }
+        uint64_t x = 0;
+        bool lossless = false;
+        if (napi_get_value_bigint_uint64(env, v, &x, &lossless) != napi_ok || !lossless) {
+            a.fail("entry " + std::to_string(idx) + ": " + p.key + " must be a BigInt pointer");
+            return false;
+        }
+        *p.dst = reinterpret_cast<const void*>(static_cast<uintptr_t>(x));
+    }
+    struct {
+        const char* key;
+        uint32_t* dst;
+        uint32_t dflt;
+        bool required;
+    } u32s[] = {
+        {"seqLen", &e->seq_len, 0, true},
+        {"position", &e->position, 0, true},
+        {"slidingWindow", &e->sliding_window, 0, false},
+        {"storeKv", &e->store_kv, 1, false},
+        {"applyDivisor", &e->apply_divisor, 0, false},
+    };
+    for (auto& f : u32s) {
+        napi_value v;
+        *f.dst = f.dflt;
+        if (!get_prop(env, obj, f.key, &v)) {
+            if (f.required) {
+                a.fail("entry " + std::to_string(idx) + ": missing " + f.key);
+                return false;
+            }
+            continue;
+        }
+        napi_valuetype t;
+        napi_typeof(env, v, &t);
+        if (t == napi_boolean) {
+            bool b = false;
+            napi_get_value_bool(env, v, &b);
+            *f.dst = b ? 1u : 0u;
+        } else if (napi_get_value_uint32(env, v, f.dst) != napi_ok) {
+            a.fail("entry " + std::to_string(idx) + ": " + f.key + " must be a number");
+            return false;
+        }
+    }
+    struct {
+        const char* key;
+        float* dst;
+        float dflt;
+        bool required;
+    } f32s[] = {
+        {"theta", &e->theta, 0.0f, true},
+        {"scale", &e->scale, 1.0f, false},
+        {"eps", &e->eps, 1e-6f, false},
+    };
+    for (auto& f : f32s) {
+        napi_value v;
+        *f.dst = f.dflt;
+        if (!get_prop(env, obj, f.key, &v)) {
+            if (f.required) {
+                a.fail("entry " + std::to_string(idx) + ": missing " + f.key);
+                return false;
+            }
+            continue;
+        }
+        double x = 0;
+        if (napi_get_value_double(env, v, &x) != napi_ok) {
+            a.fail("entry " + std::to_string(idx) + ": " + f.key + " must be a number");
+            return false;
+        }
+        *f.dst = (float)x;
+    }
+    return true;
+}
+
+// attnStepPrepare(entries[], nqh, nkh, hd, workspace, workspaceBytes, stream) -> plan (Uint8Array)
+napi_value AttnStepPrepare(napi_env env, napi_callback_info info) {
+    Args a(env, info, 7);
+    if (!a.ok) return nullptr;
+    bool is_array = false;
+    napi_is_array(env, a.v[0], &is_array);
+    if (!is_array) {
+        napi_throw_type_error(env, nullptr, "attnStepPrepare: entries must be an array");
+        return nullptr;
+    }
+    uint32_t n = 0;
+    napi_get_array_length(env, a.v[0], &n);
+    std::vector<g4_step_entry> ents(n);
+    for (uint32_t i = 0; i < n; i++) {
+        napi_value obj;
+        napi_get_element(env, a.v[0], i, &obj);
+        if (!step_entry(a, obj, i, &ents[i])) return nullptr;
+    }
+    const uint32_t nqh = a.u32(1), nkh = a.u32(2), hd = a.u32(3);
+    void* ws = a.ptr(4);
+    const double ws_bytes = a.f64(5);
+    void* s = a.ptr(6);
+    if (!a.ok) return nullptr;
+    napi_value ab, plan;
+    void* pdata = nullptr;
+    NAPI_OK(env, napi_create_arraybuffer(env, sizeof(g4_decode_plan), &pdata, &ab));
+    CALL(env, g4_attn_step_prepare(ents.data(), n, nqh, nkh, hd, ws, (size_t)ws_bytes,
+                                   static_cast<g4_decode_plan*>(pdata), s));
+    NAPI_OK(env, napi_create_typedarray(env, napi_uint8_array, sizeof(g4_decode_plan), ab, 0, &plan));
+    return plan;
+}
+
+napi_value AttnStepRun(napi_env env, napi_callback_info info) {
+    Args a(env, info, 2);  // plan, stream
+    void* d = nullptr;
+    size_t n = 0;
+    a.bytes(0, &d, &n);
+    void* s = a.ptr(1);
+    if (!a.ok) return nullptr;
+    if (n != sizeof(g4_decode_plan)) {
+        napi_throw_type_error(env, nullptr, "attnStepRun: not a plan from attnStepPrepare");
+        return nullptr;
+    }
+    g4_decode_plan plan;
+    memcpy(&plan, d, sizeof plan);
+    CALL(env, g4_attn_step_run(&plan, s));
+    return undefined(env);
+}
+
+napi_value Init(napi_env env, napi_value exports) {
+    struct {
+        const char* name;
+        napi_callback cb;
+    } fns[] = {
+        {"version", Version},
+        {"deviceCount", DeviceCount},
+        {"setDevice", SetDevice},
+        {"streamCreate", StreamCreate},
+        {"streamDestroy", StreamDestroy},
+        {"streamSynchronize", StreamSynchronize},
+        {"malloc", Malloc},
+        {"free", Free},
+        {"upload", Upload},
+        {"download", Download},
+        {"zero", Zero},
+        {"fusedPerHeadNormRope", FusedPerHeadNormRope},
+        {"perHeadRmsNormNoWeight", PerHeadRmsNormNoWeight},
+        {"kvCacheStore", KvCacheStore},
+        {"attnScore", AttnScore},
+        {"softmax", Softmax},
+        {"attnOutput", AttnOutput},
+        {"ropeInvFreq", RopeInvFreq},
+        {"attnStepWorkspaceSize", AttnStepWorkspaceSize},
+        {"attnStepPrepare", AttnStepPrepare},
+        {"attnStepRun", AttnStepRun},
+    };
+    for (auto& f : fns) {
+        napi_value fn;
+        NAPI_OK(env, napi_create_function(env, f.name, NAPI_AUTO_LENGTH, f.cb, nullptr, &fn));
+        NAPI_OK(env, napi_set_named_property(env, exports, f.name, fn));
+    }
+    // Struct sizes, for callers that check them against their own layouts.
+    struct {
+        const char* name;
+        size_t size;
+    } sizes[] = {
+        {"sizeofNormRopeParams", sizeof(g4_norm_rope_params)},
+        {"sizeofNormParams", sizeof(g4_norm_params)},
+        {"sizeofKvStoreParams", sizeof(g4_kv_store_params)},
+        {"sizeofAttnScoreParams", sizeof(g4_attn_score_params)},
+        {"sizeofSoftmaxParams", sizeof(g4_softmax_params)},
+        {"sizeofAttnOutputParams", sizeof(g4_attn_output_params)},
+    };
+    for (auto& s : sizes) NAPI_OK(env, napi_set_named_property(env, exports, s.name, number(env, (double)s.size)));
+    return exports;
+}
+
+}  // namespace
+
+NAPI_MODULE(NODE_GYP_MODULE_NAME, Init)

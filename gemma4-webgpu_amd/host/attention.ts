@@ -1,0 +1,267 @@
+// Host side of the gfx950 attention path: the engine's attention dispatch
+// surface (src/shaders.ts:43-74 names, src/engine.ts:2056-2094 call order),
+// served by libg4attn.so through the g4attn.node N-API addon.
+//
+// - Kernel names are the engine's SHADERS keys; bindings are passed in the
+//   WGSL @binding order of each shader; Params are the same uniform bytes the
+//   engine builds with makeUniformMixed (src/engine.ts:460-478) and patches
+//   per token with wb() (src/engine.ts:1967-1987), passed by value at enqueue
+//   time, so a later patch never affects work already enqueued.
+// - The backend is chosen once, at construction; no call falls back to
+//   anything else. Every library error is thrown as an Error with the
+//   library's message.
+// - attnStep is the fused replacement of the six dispatches for any number of
+//   layers or sequences (one attention launch plus one merge launch).
+
+declare const require: any;
+declare const __dirname: string;
+
+export type AttnKernelName =
+  | 'fusedPerHeadNormRope'
+  | 'perHeadRmsNormNoWeight'
+  | 'kvCacheStore'
+  | 'attnScore'
+  | 'softmax'
+  | 'attnOutput';
+
+export type FusedKernelName = 'attnStep';
+
+export type UniformValue = { u: number } | { f: number };
+
+// Storage bindings of each kernel in @binding order (the uniform is separate).
+export const BINDINGS: Record<AttnKernelName, string[]> = {
+  fusedPerHeadNormRope: ['data', 'weight', 'rope_freqs'],  // fused_per_head_norm_rope.wgsl:14-17
+  perHeadRmsNormNoWeight: ['data'],                          // per_head_rms_norm_no_weight.wgsl:9
+  kvCacheStore: ['k_in', 'v_in', 'k_cache', 'v_cache'],     // kv_cache_store.wgsl:2-5
+  attnScore: ['q', 'k_cache', 'scores'],                     // attn_score.wgsl:10-12
+  softmax: ['scores'],                                       // softmax.wgsl:2
+  attnOutput: ['probs', 'v_cache', 'output'],                // attn_output.wgsl:2-4
+};
+
+// Params byte sizes (struct Params of each shader).
+export const PARAMS_BYTES: Record<AttnKernelName, number> = {
+  fusedPerHeadNormRope: 24,
+  perHeadRmsNormNoWeight: 16,
+  kvCacheStore: 16,
+  attnScore: 24,
+  softmax: 8,
+  attnOutput: 16,
+};
+
+// Profiler pass labels of the engine (src/engine.ts:2056-2094), plus the fused step.
+export const PASS_LABELS: Record<string, string> = {
+  perHeadRmsNormNoWeight: 'attn.vNorm',
+  fusedPerHeadNormRope: 'attn.fusedNormRopeQK',
+  kvCacheStore: 'attn.kvCacheStore',
+  attnScore: 'attn.attnScore',
+  softmax: 'attn.softmax',
+  attnOutput: 'attn.attnOutput',
+  attnStep: 'attn.decodeFused',
+};
+
+// The engine's makeUniformMixed: 4-byte fields, at least 16 bytes.
+export class Uniform {
+  readonly bytes: Uint8Array;
+  private readonly u32: Uint32Array;
+  private readonly f32: Float32Array;
+
+  constructor(values: UniformValue[]) {
+    const size = Math.max(values.length * 4, 16);
+    const ab = new ArrayBuffer(size);
+    this.u32 = new Uint32Array(ab);
+    this.f32 = new Float32Array(ab);
+    this.bytes = new Uint8Array(ab);
+    for (let i = 0; i < values.length; i++) {
+      const v = values[i];
+      if ('u' in v) this.u32[i] = v.u;
+      else this.f32[i] = v.f;
+    }
+  }
+
+  // The engine's wb(buffer, byteOffset, u32Value) per-token patch.
+  writeU32(byteOffset: number, value: number): void {
+    this.u32[byteOffset >> 2] = value >>> 0;
+  }
+
+  writeF32(byteOffset: number, value: number): void {
+    this.f32[byteOffset >> 2] = value;
+  }
+}
+
+export interface DeviceBuffer {
+  readonly ptr: bigint;
+  readonly size: number;
+}
+
+// One entry of the fused step: a layer of a token's stack or a sequence of a batch.
+export interface StepEntry {
+  q: DeviceBuffer;            // raw projection f32 [NQH][HD] (read only)
+  k: DeviceBuffer;            // raw projection f32 [NKH][HD]
+  v: DeviceBuffer;
+  qWeight: DeviceBuffer;      // attn_q_norm f16 [HD]
+  kWeight: DeviceBuffer;      // attn_k_norm f16 [HD]
+  ropeFreqs?: DeviceBuffer;   // f16 divisor table (global layers)
+  ropeInvFreq?: DeviceBuffer; // f32 [HD/2] table from ropeInvFreq()
+  kCache: DeviceBuffer;       // f16 [rows][NKH][HD]
+  vCache: DeviceBuffer;
+  out: DeviceBuffer;          // attnOut f32 [NQH][HD]
+  seqLen: number;             // rows including the current token's (row seqLen - 1)
+  position: number;           // RoPE position
+  slidingWindow?: number;     // 0 = full
+  storeKv?: boolean;          // false on KV-consumer layers
+  theta: number;
+  applyDivisor?: number;
+  scale?: number;
+  eps?: number;
+}
+
+export interface StepShape {
+  numQHeads: number;
+  numKvHeads: number;
+  headDim: number;
+}
+
+// What g4attn.node exports (gemma4-webgpu_amd/addon/g4attn_napi.cc).
+export interface Addon {
+  version(): string;
+  deviceCount(): number;
+  setDevice(d: number): void;
+  streamCreate(): bigint;
+  streamDestroy(s: bigint): void;
+  streamSynchronize(s: bigint): void;
+  malloc(bytes: number): bigint;
+  free(p: bigint): void;
+  upload(dst: bigint, offset: number, data: any, s: bigint): void;
+  download(src: bigint, offset: number, out: any, s: bigint): void;
+  zero(p: bigint, bytes: number, s: bigint): void;
+  fusedPerHeadNormRope(data: bigint, w: bigint, rf: bigint, p: Uint8Array, s: bigint): void;
+  perHeadRmsNormNoWeight(data: bigint, p: Uint8Array, s: bigint): void;
+  kvCacheStore(k: bigint, v: bigint, kc: bigint, vc: bigint, p: Uint8Array, s: bigint): void;
+  attnScore(q: bigint, kc: bigint, sc: bigint, p: Uint8Array, s: bigint): void;
+  softmax(sc: bigint, p: Uint8Array, s: bigint): void;
+  attnOutput(pr: bigint, vc: bigint, o: bigint, p: Uint8Array, s: bigint): void;
+  ropeInvFreq(theta: number, hd: number, div: number, rf: any, out: bigint, s: bigint): void;
+  attnStepWorkspaceSize(n: number, nqh: number, nkh: number, hd: number): number;
+  attnStepPrepare(entries: any[], nqh: number, nkh: number, hd: number, ws: bigint, wsBytes: number,
+    s: bigint): Uint8Array;
+  attnStepRun(plan: Uint8Array, s: bigint): void;
+  [key: string]: any;
+}
+
+export function loadAddon(path?: string): Addon {
+  const p = path || require('path').join(__dirname, '..', 'lib', 'g4attn.node');
+  return require(p) as Addon;
+}
+
+// The kernel table: SHADERS name -> launch with (bindings in @binding order, Params bytes).
+type Launch = (g4: Addon, b: bigint[], p: Uint8Array, s: bigint) => void;
+export const KERNELS: Record<AttnKernelName, Launch> = {
+  fusedPerHeadNormRope: function (g4, b, p, s) { g4.fusedPerHeadNormRope(b[0], b[1], b[2], p, s); },
+  perHeadRmsNormNoWeight: function (g4, b, p, s) { g4.perHeadRmsNormNoWeight(b[0], p, s); },
+  kvCacheStore: function (g4, b, p, s) { g4.kvCacheStore(b[0], b[1], b[2], b[3], p, s); },
+  attnScore: function (g4, b, p, s) { g4.attnScore(b[0], b[1], b[2], p, s); },
+  softmax: function (g4, b, p, s) { g4.softmax(b[0], p, s); },
+  attnOutput: function (g4, b, p, s) { g4.attnOutput(b[0], b[1], b[2], p, s); },
+};
+
+export class HipAttention {
+  readonly stream: bigint;
+  private readonly g4: Addon;
+  private alive: boolean;
+
+  constructor(addon: Addon, device: number) {
+    this.g4 = addon;
+    addon.setDevice(device);
+    this.stream = addon.streamCreate();
+    this.alive = true;
+  }
+
+  version(): string {
+    return this.g4.version();
+  }
+
+  createBuffer(size: number): DeviceBuffer {
+    return { ptr: this.g4.malloc(size), size: size };
+  }
+
+  destroyBuffer(b: DeviceBuffer): void {
+    this.g4.free(b.ptr);
+  }
+
+  writeBuffer(b: DeviceBuffer, offset: number, data: ArrayBufferView): void {
+    if (offset + data.byteLength > b.size) throw new RangeError(`writeBuffer: ${offset}+${data.byteLength} > ${b.size}`);
+    this.g4.upload(b.ptr, offset, data, this.stream);
+  }
+
+  // Blocking read (the engine's mapAsync readback, made synchronous).
+  readBuffer(b: DeviceBuffer, offset: number, out: ArrayBufferView): void {
+    if (offset + out.byteLength > b.size) throw new RangeError(`readBuffer: ${offset}+${out.byteLength} > ${b.size}`);
+    this.g4.download(b.ptr, offset, out, this.stream);
+  }
+
+  clearBuffer(b: DeviceBuffer): void {
+    this.g4.zero(b.ptr, b.size, this.stream);
+  }
+
+  // setPipeline(name) + setBindGroup(bindings, params) + dispatchWorkgroups, as one enqueue.
+  dispatch(name: AttnKernelName, bindings: DeviceBuffer[], params: Uniform): void {
+    const launch = KERNELS[name];
+    if (!launch) throw new Error(`unknown attention kernel ${name}`);
+    const want = BINDINGS[name];
+    if (bindings.length !== want.length) {
+      throw new Error(`${name}: ${bindings.length} bindings, expected ${want.length} (${want.join(', ')})`);
+    }
+    if (params.bytes.byteLength < PARAMS_BYTES[name]) throw new Error(`${name}: params too short`);
+    launch(this.g4, bindings.map(function (b) { return b.ptr; }), params.bytes, this.stream);
+  }
+
+  ropeInvFreq(theta: number, headDim: number, applyDivisor: number, ropeFreqs: DeviceBuffer | null,
+    out: DeviceBuffer): void {
+    this.g4.ropeInvFreq(theta, headDim, applyDivisor, ropeFreqs ? ropeFreqs.ptr : null, out.ptr, this.stream);
+  }
+
+  attnStepWorkspaceSize(nEntries: number, shape: StepShape): number {
+    return this.g4.attnStepWorkspaceSize(nEntries, shape.numQHeads, shape.numKvHeads, shape.headDim);
+  }
+
+  // Prepare once per token (the entries' seqLen/position change); run as often as wanted.
+  attnStepPrepare(entries: StepEntry[], shape: StepShape, workspace: DeviceBuffer): Uint8Array {
+    const flat = entries.map(function (e) {
+      return {
+        q: e.q.ptr, k: e.k.ptr, v: e.v.ptr, qWeight: e.qWeight.ptr, kWeight: e.kWeight.ptr,
+        ropeFreqs: e.ropeFreqs ? e.ropeFreqs.ptr : undefined,
+        ropeInvFreq: e.ropeInvFreq ? e.ropeInvFreq.ptr : undefined,
+        kCache: e.kCache.ptr, vCache: e.vCache.ptr, out: e.out.ptr,
+        seqLen: e.seqLen, position: e.position, slidingWindow: e.slidingWindow || 0,
+        storeKv: e.storeKv === undefined ? true : e.storeKv, theta: e.theta, applyDivisor: e.applyDivisor || 0,
+        scale: e.scale === undefined ? 1.0 : e.scale, eps: e.eps === undefined ? 1e-6 : e.eps,
+      };
+    });
+    return this.g4.attnStepPrepare(flat, shape.numQHeads, shape.numKvHeads, shape.headDim, workspace.ptr,
+      workspace.size, this.stream);
+  }
+
+  attnStepRun(plan: Uint8Array): void {
+    this.g4.attnStepRun(plan, this.stream);
+  }
+
+  attnStep(entries: StepEntry[], shape: StepShape, workspace: DeviceBuffer): void {
+    this.attnStepRun(this.attnStepPrepare(entries, shape, workspace));
+  }
+
+  synchronize(): void {
+    this.g4.streamSynchronize(this.stream);
+  }
+
+  dispose(): void {
+    if (!this.alive) return;
+    this.g4.streamSynchronize(this.stream);
+    this.g4.streamDestroy(this.stream);
+    this.alive = false;
+  }
+}
+
+// The backend, selected once at init.
+export function createAttention(device?: number, addonPath?: string): HipAttention {
+  return new HipAttention(loadAddon(addonPath), device || 0);
+}

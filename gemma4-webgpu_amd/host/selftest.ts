@@ -1,0 +1,136 @@
+// Checks of the TypeScript host over the N-API addon, driven by tests/test_host_node.py.
+//
+//   node host/run.js cpu            layout and table checks (no GPU work)
+//   node host/run.js layer <dir>    one attention layer from <dir>/case.json + case.bin, run twice on the
+//                                   GPU: the engine's six dispatches in order (src/engine.ts:2056-2094),
+//                                   and the fused attnStep; results go to <dir>/out.bin for the oracle check.
+
+import { BINDINGS, KERNELS, PARAMS_BYTES, PASS_LABELS, Uniform, HipAttention, loadAddon } from './attention';
+import type { AttnKernelName, DeviceBuffer } from './attention';
+
+declare const require: any;
+declare const process: any;
+
+const fs = require('fs');
+const path = require('path');
+
+function fail(msg: string): never {
+  throw new Error(msg);
+}
+
+export function cpuChecks(): string[] {
+  const done: string[] = [];
+  const g4 = loadAddon();
+  const names = Object.keys(BINDINGS).sort();
+  if (Object.keys(KERNELS).sort().join() !== names.join()) fail('KERNELS and BINDINGS name different kernels');
+  for (const n of names) if (!PASS_LABELS[n]) fail(`no pass label for ${n}`);
+  done.push('kernel table');
+  const sizes: Record<string, string> = {
+    fusedPerHeadNormRope: 'sizeofNormRopeParams', perHeadRmsNormNoWeight: 'sizeofNormParams',
+    kvCacheStore: 'sizeofKvStoreParams', attnScore: 'sizeofAttnScoreParams', softmax: 'sizeofSoftmaxParams',
+    attnOutput: 'sizeofAttnOutputParams',
+  };
+  for (const n of names) {
+    const want = g4[sizes[n]];
+    const have = PARAMS_BYTES[n as AttnKernelName];
+    if (have !== want) fail(`${n}: params ${have} B, C struct ${want} B`);
+  }
+  done.push('params sizes');
+  // Uniform layout: the engine's fusedNormRopeQ list, then the per-token position patch at byte 12.
+  const u = new Uniform([{ u: 8 }, { u: 256 }, { f: 1e-6 }, { u: 0 }, { f: 1e4 }, { u: 1 }]);
+  u.writeU32(12, 8192);
+  const dv = new DataView(u.bytes.buffer);
+  if (dv.getUint32(0, true) !== 8 || dv.getUint32(4, true) !== 256 || dv.getUint32(12, true) !== 8192 ||
+    dv.getUint32(20, true) !== 1 || Math.abs(dv.getFloat32(8, true) - 1e-6) > 1e-12 || dv.getFloat32(16, true) !== 1e4) {
+    fail('uniform layout');
+  }
+  if (new Uniform([{ u: 1 }]).bytes.byteLength !== 16) fail('uniforms are padded to 16 bytes');
+  done.push('uniform layout');
+  if (typeof g4.version() !== 'string') fail('version');
+  done.push('addon loaded: ' + g4.version());
+  return done;
+}
+
+interface CaseSpec {
+  nqh: number; nkh: number; hd: number; seq: number; pos: number; window: number; theta: number; div: number;
+  eps: number; arrays: Record<string, number[]>;
+}
+
+function layer(dir: string): string[] {
+  const spec = JSON.parse(fs.readFileSync(path.join(dir, 'case.json'), 'utf8')) as CaseSpec;
+  const bin: Uint8Array = fs.readFileSync(path.join(dir, 'case.bin'));
+  const att = new HipAttention(loadAddon(), 0);
+  const NQH = spec.nqh, NKH = spec.nkh, HD = spec.hd, SEQ = spec.seq;
+  const bufs: DeviceBuffer[] = [];
+  function upload(name: string): DeviceBuffer {
+    const r = spec.arrays[name];
+    const b = att.createBuffer(r[1]);
+    att.writeBuffer(b, 0, bin.subarray(r[0], r[0] + r[1]));
+    bufs.push(b);
+    return b;
+  }
+  function alloc(bytes: number): DeviceBuffer {
+    const b = att.createBuffer(bytes);
+    bufs.push(b);
+    return b;
+  }
+  const qw = upload('qw'), kw = upload('kw'), rf = upload('rf');
+
+  // (1) the engine's order over the six kernels, uniforms built as the engine builds them
+  const q1 = upload('q'), k1 = upload('k'), v1 = upload('v'), kc1 = upload('kc'), vc1 = upload('vc');
+  const scores = alloc(NQH * SEQ * 4), out1 = alloc(NQH * HD * 4);
+  const vNorm = new Uniform([{ u: NKH }, { u: HD }, { f: spec.eps }, { u: 0 }]);
+  const normRopeQ = new Uniform([{ u: NQH }, { u: HD }, { f: spec.eps }, { u: 0 }, { f: spec.theta }, { u: spec.div }]);
+  const normRopeK = new Uniform([{ u: NKH }, { u: HD }, { f: spec.eps }, { u: 0 }, { f: spec.theta }, { u: spec.div }]);
+  const kvStore = new Uniform([{ u: NKH }, { u: HD }, { u: 0 }, { u: SEQ }]);
+  const score = new Uniform([{ u: NQH }, { u: NKH }, { u: HD }, { u: 0 }, { f: 1.0 }, { u: spec.window }]);
+  const softmax = new Uniform([{ u: NQH }, { u: 0 }]);
+  const output = new Uniform([{ u: NQH }, { u: NKH }, { u: HD }, { u: 0 }]);
+  // per-token patches (src/engine.ts:1977-1987)
+  normRopeQ.writeU32(12, spec.pos);
+  normRopeK.writeU32(12, spec.pos);
+  kvStore.writeU32(8, spec.pos);
+  score.writeU32(12, SEQ);
+  softmax.writeU32(4, SEQ);
+  output.writeU32(12, SEQ);
+  att.dispatch('perHeadRmsNormNoWeight', [v1], vNorm);
+  att.dispatch('fusedPerHeadNormRope', [q1, qw, rf], normRopeQ);
+  att.dispatch('fusedPerHeadNormRope', [k1, kw, rf], normRopeK);
+  att.dispatch('kvCacheStore', [k1, v1, kc1, vc1], kvStore);
+  att.dispatch('attnScore', [q1, kc1, scores], score);
+  att.dispatch('softmax', [scores], softmax);
+  att.dispatch('attnOutput', [scores, vc1, out1], output);
+
+  // (2) the fused step on fresh copies of the same inputs, with the RoPE table
+  const q2 = upload('q'), k2 = upload('k'), v2 = upload('v'), kc2 = upload('kc'), vc2 = upload('vc');
+  const out2 = alloc(NQH * HD * 4), inv = alloc(HD / 2 * 4);
+  att.ropeInvFreq(spec.theta, HD, spec.div, rf, inv);
+  const shape = { numQHeads: NQH, numKvHeads: NKH, headDim: HD };
+  const ws = alloc(att.attnStepWorkspaceSize(1, shape));
+  att.attnStep([{
+    q: q2, k: k2, v: v2, qWeight: qw, kWeight: kw, ropeFreqs: rf, ropeInvFreq: inv, kCache: kc2, vCache: vc2,
+    out: out2, seqLen: SEQ, position: spec.pos, slidingWindow: spec.window, storeKv: true, theta: spec.theta,
+    applyDivisor: spec.div, scale: 1.0, eps: spec.eps,
+  }], shape, ws);
+
+  // results: out1, out2 (f32), then the stored row of kc1, vc1, kc2, vc2 (f16)
+  const row = NKH * HD * 2, o = NQH * HD * 4;
+  const res = new Uint8Array(2 * o + 4 * row);
+  att.readBuffer(out1, 0, res.subarray(0, o));
+  att.readBuffer(out2, 0, res.subarray(o, 2 * o));
+  const caches = [kc1, vc1, kc2, vc2];
+  for (let i = 0; i < 4; i++) att.readBuffer(caches[i], spec.pos * row, res.subarray(2 * o + i * row, 2 * o + (i + 1) * row));
+  fs.writeFileSync(path.join(dir, 'out.bin'), res);
+  for (const b of bufs) att.destroyBuffer(b);
+  att.dispose();
+  return ['engine order: 7 dispatches', 'attnStep: 1 entry', 'results written'];
+}
+
+export function main(argv: string[]): void {
+  const mode = argv[0];
+  let done: string[];
+  if (mode === 'cpu') done = cpuChecks();
+  else if (mode === 'layer') done = layer(argv[1]);
+  else fail(`usage: run.js cpu | layer <dir>`);
+  process.stdout.write(JSON.stringify({ ok: true, checks: done }) + '\n');
+}
