@@ -13,6 +13,11 @@ inputs resident in HBM:
   long128k  one global layer attending 131072 rows.
   ragged64  64 independent sequences, lengths uniform in [1024, 32768].
   layer512  one local layer at position 512 (launch-bound).
+  prefill4k causal prefill of a 4096-token prompt on MFMA: one global and one
+            512-window local layer, as 512-token chunks (16 entries in one
+            launch); f16 Q/K/V (unit-RMS rows). Reported in TFLOP/s
+            (algorithmic 4*HD*NQH per attended key per token) against the
+            2.5 PFLOP/s dense f16 MFMA peak.
 
 A step is one launch of the fused attention step over every entry (per entry:
 q/k RMSNorm + RoPE, weightless v-norm, f16 store of the new K/V row, split-K
@@ -294,13 +299,127 @@ def run_cpu_baseline(spec, seconds: float):
     return dict(per_token_s=per_token, tokens=n, threads=threads)
 
 
+# ---- prefill (MFMA) ------------------------------------------------------------------
+
+PREFILL_T, PREFILL_CHUNK, PREFILL_WINDOWS = 4096, 512, (0, 512)
+MFMA_F16_PEAK_TFLOPS = 2500.0
+
+
+def prefill_flops() -> float:
+    f = 0.0
+    for w in PREFILL_WINDOWS:
+        for i in range(PREFILL_T):
+            f += 4.0 * HD * NQH * (min(i + 1, w) if w else i + 1)
+    return f
+
+
+def run_prefill_gpu(args):
+    import torch
+
+    from g4attn import abi, ops, synth
+
+    abi.load()
+    abi.call("g4_set_device", 0)
+    dev = torch.device("cuda:0")
+
+    def unit_f16(seed, rows):
+        x = synth.normal_torch(seed, rows * HD, dev).view(rows, HD).double()
+        return (x / torch.sqrt((x ** 2).mean(dim=1, keepdim=True) + EPS)).to(torch.float16).view(-1)
+
+    layers, entries = [], []
+    for li, w in enumerate(PREFILL_WINDOWS):
+        q = unit_f16(BASE_SEED + 30 + li, PREFILL_T * NQH).view(torch.int16)
+        kc = unit_f16(BASE_SEED + 40 + li, PREFILL_T * NKH).view(torch.int16)
+        vc = unit_f16(BASE_SEED + 50 + li, PREFILL_T * NKH).view(torch.int16)
+        out = torch.empty(PREFILL_T * NQH * HD, dtype=torch.float32, device=dev)
+        layers.append((q, kc, vc, out))
+        for c0 in range(0, PREFILL_T, PREFILL_CHUNK):
+            entries.append(dict(q=q[c0 * NQH * HD:], k_cache=kc, v_cache=vc, out=out[c0 * NQH * HD:],
+                                n_tokens=PREFILL_CHUNK, start=c0, sliding_window=w, scale=1.0))
+    arr = ops.make_prefill_entries(entries, NQH, NKH, HD)
+    ws = torch.empty(ops.prefill_workspace_bytes(arr, NQH, NKH, HD), dtype=torch.uint8, device=dev)
+    plan = ops.attn_prefill_prepare(arr, NQH, NKH, HD, ws)
+    for _ in range(args.warmup):
+        ops.attn_prefill_run(plan)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        ops.attn_prefill_run(plan)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    stream = torch.cuda.current_stream()
+    for a_, b_ in evs:
+        a_.record(stream)
+        b_.record(stream)
+    torch.cuda.synchronize()
+    for a_, b_ in evs:
+        ops.attn_prefill_run_timed(plan, a_, b_)
+    torch.cuda.synchronize()
+    k_ms = sum(a_.elapsed_time(b_) for a_, b_ in evs) / len(evs)
+    log(f"prefill4k: {wall / args.steps * 1e6:.1f} us/step, k_prefill avg {k_ms * 1e3:.1f} us")
+    return dict(wall_s=wall, steps=args.steps, kernel_ms=k_ms, entries=len(entries))
+
+
+def run_prefill_cpu(seconds: float):
+    """The reference computes a prompt as one decode step per token: the oracle's chain at sampled
+    positions (every 256th token of each layer), timed and scaled by the attended keys."""
+    import numpy as np
+
+    from oracle import oracle as orc
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
+    orc.set_threads(threads)
+    rng = np.random.default_rng(BASE_SEED)
+    kc = rng.standard_normal((PREFILL_T, HD), dtype=np.float32)
+    vc = rng.standard_normal((PREFILL_T, HD), dtype=np.float32)
+    q = rng.standard_normal(NQH * HD, dtype=np.float32)
+    done_flops, el, n = 0.0, 0.0, 0
+    t0 = time.perf_counter()
+    while el < seconds and n < 100000:  # the sampled positions, repeated until the time budget is used
+        for w in PREFILL_WINDOWS:
+            for t in range(PREFILL_T - 1, -1, -256):
+                seq = t + 1
+                orc.attention_chain(q, kc[:seq].reshape(-1), vc[:seq].reshape(-1), NQH, NKH, HD, seq, 1.0, w)
+                done_flops += 4.0 * HD * NQH * (min(seq, w) if w else seq)
+                n += 1
+        el = time.perf_counter() - t0
+    return dict(tflops=done_flops / el / 1e12, tokens=n, threads=threads, seconds=el)
+
+
+def main_prefill(args):
+    r = run_prefill_gpu(args)
+    flops = prefill_flops()
+    ms_per_step = r["wall_s"] / r["steps"] * 1e3
+    value = flops / (ms_per_step * 1e-3) / 1e12
+    achieved = flops / (r["kernel_ms"] * 1e-3) / 1e12
+    line = {
+        "metric": "prefill-attention TFLOP/s (% MFMA roofline), E2B-shaped, 4096-token prompt",
+        "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f16 Q/K/V/P, f32 accumulate", "data": "synthetic (seeded splitmix64 N(0,1), unit-RMS rows)",
+        "config": {"workload": "causal prefill, 4096 tokens, 1 global + 1 local (W=512) layer, 512-token chunks "
+                               "(16 entries, one launch)", "num_q_heads": NQH, "num_kv_heads": NKH, "head_dim": HD,
+                   "flops_per_step": flops},
+        "roofline": {"bound": "mfma", "kernel": "k_prefill", "achieved": round(achieved, 2),
+                     "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4),
+                     "traffic": None, "avg_us": round(r["kernel_ms"] * 1e3, 2)},
+    }
+    if not args.no_cpu_baseline:
+        c = run_prefill_cpu(args.cpu_seconds)
+        line["cpu_baseline"] = {"value": round(c["tflops"], 5), "unit": "TFLOP/s", "cores": c["threads"],
+                                "kind": "port", "sample": f"{c['tokens']} per-token decode chains of the oracle at "
+                                f"every 256th position of both layers ({c['seconds']:.1f} s), scaled by attended keys"}
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="stack8k",
-                    choices=["stack8k", "stack32k", "long128k", "ragged64", "layer512"])
+                    choices=["stack8k", "stack32k", "long128k", "ragged64", "layer512", "prefill4k"])
     ap.add_argument("--sets", type=int, default=0, help="cache sets to rotate (0 = enough to exceed 2x MALL)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -312,6 +431,9 @@ def main():
               "would shard by sequence or by KV range across GPUs, which is not built here)", file=sys.stderr)
         sys.exit(2)
 
+    if args.workload == "prefill4k":
+        main_prefill(args)
+        return
     spec = workload_spec(args.workload)
     r = run_gpu(spec, args)
     ms_per_step = r["wall_s"] / r["steps"] * 1e3

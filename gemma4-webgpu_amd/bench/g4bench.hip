@@ -3,7 +3,11 @@
 // counter collection). Inputs are synthetic: f16 cache rows from a
 // counter-based hash (values in [-2, 2), unit-RMS scale), queries likewise.
 //
-//   g4bench [--workload stack8k|stack32k|long128k|ragged64|layer512|copy] [--iters N] [--sets S]
+//   g4bench [--workload stack8k|stack32k|long128k|ragged64|layer512|prefill4k|copy] [--iters N] [--sets S]
+//
+// `prefill4k` runs the causal MFMA prefill of a 4096-token prompt for one
+// global layer and one 512-window local layer, as 512-token chunks (16
+// entries in one launch; --mode whole: one entry per layer).
 //
 // `copy` runs a plain 512 MiB device copy kernel instead: the reference for
 // scaling FETCH_SIZE / WRITE_SIZE counter readings to bytes.
@@ -125,6 +129,55 @@ static std::vector<Layer> workload(const std::string& w) {
     return L;
 }
 
+// Causal prefill of a 4096-token prompt: one global and one W=512 local layer.
+static int run_prefill(const std::string& mode, int iters) {
+    const unsigned T = 4096, CH = mode == "whole" ? 4096 : 512, NQ = NQH, NK = NKH;
+    hipStream_t st;
+    HK(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
+    std::vector<g4_prefill_entry> ents;
+    double flops = 0;
+    for (int layer = 0; layer < 2; layer++) {
+        const unsigned window = layer ? 512u : 0u;
+        void *q, *kc, *vc, *out;
+        CK(g4_malloc(&q, (size_t)T * NQ * HD * 2));
+        CK(g4_malloc(&kc, (size_t)T * NK * HD * 2));
+        CK(g4_malloc(&vc, (size_t)T * NK * HD * 2));
+        CK(g4_malloc(&out, (size_t)T * NQ * HD * 4));
+        hipLaunchKernelGGL(k_fill_f16, dim3(1024), dim3(256), 0, st, (_Float16*)q, (uint64_t)T * NQ * HD, 11u + layer);
+        hipLaunchKernelGGL(k_fill_f16, dim3(1024), dim3(256), 0, st, (_Float16*)kc, (uint64_t)T * NK * HD, 21u + layer);
+        hipLaunchKernelGGL(k_fill_f16, dim3(1024), dim3(256), 0, st, (_Float16*)vc, (uint64_t)T * NK * HD, 31u + layer);
+        for (unsigned c0 = 0; c0 < T; c0 += CH) {
+            g4_prefill_entry e = {(const uint16_t*)q + (size_t)c0 * NQ * HD, (const uint16_t*)kc, (const uint16_t*)vc,
+                                  (float*)out + (size_t)c0 * NQ * HD, CH, c0, window, 1.0f};
+            ents.push_back(e);
+        }
+        for (unsigned i = 0; i < T; i++) flops += 4.0 * HD * NQ * (window && i + 1 > window ? window : i + 1);
+    }
+    HK(hipGetLastError());
+    size_t ws_bytes = 0;
+    CK(g4_attn_prefill_workspace_size(ents.data(), (uint32_t)ents.size(), NQ, NK, HD, &ws_bytes));
+    void* ws;
+    CK(g4_malloc(&ws, ws_bytes ? ws_bytes : 256));
+    g4_decode_plan plan;
+    CK(g4_attn_prefill_prepare(ents.data(), (uint32_t)ents.size(), NQ, NK, HD, ws, ws_bytes, &plan, st));
+    for (int i = 0; i < 3; i++) CK(g4_attn_prefill_run(&plan, st));
+    CK(g4_stream_synchronize(st));
+    hipEvent_t a, b;
+    HK(hipEventCreate(&a));
+    HK(hipEventCreate(&b));
+    HK(hipEventRecord(a, st));
+    for (int i = 0; i < iters; i++) CK(g4_attn_prefill_run(&plan, st));
+    HK(hipEventRecord(b, st));
+    HK(hipEventSynchronize(b));
+    float ms = 0;
+    HK(hipEventElapsedTime(&ms, a, b));
+    const double us = ms * 1e3 / iters;
+    printf("flops_per_step: %.0f\n", flops);
+    printf("prefill4k [%s]: %zu entries, %.2f us/step, %.1f TFLOP/s algorithmic (%d iterations)\n", mode.c_str(),
+           ents.size(), us, flops / (us * 1e-6) / 1e12, iters);
+    return 0;
+}
+
 int main(int argc, char** argv) {
     std::string wl = "stack8k", mode = "step";
     int iters = 50, sets = 0;
@@ -140,6 +193,7 @@ int main(int argc, char** argv) {
     }
     CK(g4_set_device(0));
     if (wl == "copy") return run_copy(iters);
+    if (wl == "prefill4k") return run_prefill(mode, iters);
     std::vector<Layer> L = workload(wl);
     const bool uniform_pos = wl.rfind("stack", 0) == 0 || L.size() == 1;
     uint64_t step_bytes = 0, total_rows = 0;

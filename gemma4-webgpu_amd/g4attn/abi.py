@@ -85,6 +85,12 @@ class StepEntry(C.Structure):
                 ("apply_divisor", C.c_uint32), ("scale", C.c_float), ("eps", C.c_float)]
 
 
+class PrefillEntry(C.Structure):
+    _fields_ = [("q", C.c_void_p), ("k_cache", C.c_void_p), ("v_cache", C.c_void_p), ("out", C.c_void_p),
+                ("n_tokens", C.c_uint32), ("start", C.c_uint32), ("sliding_window", C.c_uint32),
+                ("scale", C.c_float)]
+
+
 class DecodePlan(C.Structure):
     _fields_ = [("opaque", C.c_uint64 * 8)]
 
@@ -131,6 +137,12 @@ SIGNATURES: dict[str, list] = {
     "g4_attn_step_run_merge": [C.POINTER(DecodePlan), _P],
     "g4_attn_step_run_attention_timed": [C.POINTER(DecodePlan), _P, _P, _P],
     "g4_attn_step": [C.POINTER(StepEntry), _U32, _U32, _U32, _U32, _P, _SZ, _P],
+    "g4_attn_prefill_workspace_size": [C.POINTER(PrefillEntry), _U32, _U32, _U32, _U32, C.POINTER(C.c_size_t)],
+    "g4_attn_prefill_prepare": [C.POINTER(PrefillEntry), _U32, _U32, _U32, _U32, _P, _SZ, C.POINTER(DecodePlan),
+                                _P],
+    "g4_attn_prefill_run": [C.POINTER(DecodePlan), _P],
+    "g4_attn_prefill_run_timed": [C.POINTER(DecodePlan), _P, _P, _P],
+    "g4_attn_prefill": [C.POINTER(PrefillEntry), _U32, _U32, _U32, _U32, _P, _SZ, _P],
 }
 STRING_FUNCS = ("g4_last_error", "g4_version")
 

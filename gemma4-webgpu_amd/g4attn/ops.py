@@ -289,3 +289,53 @@ def attn_step_run_attention_timed(plan: DecodePlan, start, stop, stream=None):
 def attn_step(entries, num_q_heads, num_kv_heads, head_dim, workspace, stream=None):
     abi.call("g4_attn_step", entries, len(entries), num_q_heads, num_kv_heads, head_dim,
              _dev(workspace, "workspace", torch.uint8, 0), workspace.numel(), _stream(stream))
+
+
+# ---- causal prefill ------------------------------------------------------------
+
+def make_prefill_entries(items, num_q_heads, num_kv_heads, head_dim):
+    """items: dicts with q (f16 [n_tokens][NQH][HD]), k_cache, v_cache (f16, at least start + n_tokens rows),
+    out (f32 [n_tokens][NQH][HD]), n_tokens, start, sliding_window, scale."""
+    from .abi import PrefillEntry
+
+    items = list(items)
+    arr = (PrefillEntry * len(items))()
+    for i, it in enumerate(items):
+        T, s0 = int(it["n_tokens"]), int(it["start"])
+        kv = (s0 + T) * num_kv_heads * head_dim
+        arr[i] = PrefillEntry(_f16(it["q"], f"entry {i} q", T * num_q_heads * head_dim),
+                              _f16(it["k_cache"], f"entry {i} k_cache", kv), _f16(it["v_cache"], f"entry {i} v_cache", kv),
+                              _f32(it["out"], f"entry {i} out", T * num_q_heads * head_dim), T, s0,
+                              int(it.get("sliding_window", 0)), float(it.get("scale", 1.0)))
+    return arr
+
+
+def prefill_workspace_bytes(entries, num_q_heads, num_kv_heads, head_dim) -> int:
+    n = C.c_size_t()
+    abi.call("g4_attn_prefill_workspace_size", entries, len(entries), num_q_heads, num_kv_heads, head_dim,
+             C.byref(n))
+    return n.value
+
+
+def attn_prefill_prepare(entries, num_q_heads, num_kv_heads, head_dim, workspace, stream=None) -> DecodePlan:
+    plan = DecodePlan()
+    abi.call("g4_attn_prefill_prepare", entries, len(entries), num_q_heads, num_kv_heads, head_dim,
+             _dev(workspace, "workspace", torch.uint8, 0), workspace.numel(), C.byref(plan), _stream(stream))
+    return plan
+
+
+def attn_prefill_run(plan: DecodePlan, stream=None):
+    abi.call("g4_attn_prefill_run", C.byref(plan), _stream(stream))
+
+
+def attn_prefill_run_timed(plan: DecodePlan, start, stop, stream=None):
+    for e, name in ((start, "start"), (stop, "stop")):
+        if not getattr(e, "cuda_event", 0):
+            raise ValueError(f"{name} event has no HIP event yet (record it once first)")
+    abi.call("g4_attn_prefill_run_timed", C.byref(plan), _stream(stream), C.c_void_p(start.cuda_event),
+             C.c_void_p(stop.cuda_event))
+
+
+def attn_prefill(entries, num_q_heads, num_kv_heads, head_dim, workspace, stream=None):
+    abi.call("g4_attn_prefill", entries, len(entries), num_q_heads, num_kv_heads, head_dim,
+             _dev(workspace, "workspace", torch.uint8, 0), workspace.numel(), _stream(stream))

@@ -318,6 +318,42 @@ int g4_attn_step_run_attention_timed(const g4_decode_plan* plan, void* stream, v
 int g4_attn_step(const g4_step_entry* entries, uint32_t n_entries, uint32_t num_q_heads, uint32_t num_kv_heads,
                  uint32_t head_dim, void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---- causal prefill on MFMA ---------------------------------------------
+ * The reference runs a prompt as one decode step per token (src/engine.ts:
+ * 2469-2475); this computes the same attention for a chunk of tokens at once.
+ * Token t of an entry sits at position start + t and attends cache rows
+ * [lo, start + t], lo = start + t + 1 - sliding_window on local layers
+ * (0 when that is negative or the window is 0): out[t] equals the decode step
+ * at that position (attn_score.wgsl -> softmax.wgsl -> attn_output.wgsl)
+ * within f32/f16 rounding. q is the post norm + RoPE query in f16; the
+ * caches already hold the chunk's own K/V rows. Several entries (chunks,
+ * layers, sequences) go in one launch. head_dim 256, 32 % (num_q_heads /
+ * num_kv_heads) == 0. */
+typedef struct g4_prefill_entry {
+    const uint16_t* q;        /* f16 [n_tokens][num_q_heads][head_dim] */
+    const uint16_t* k_cache;  /* f16 [rows][num_kv_heads][head_dim], rows >= start + n_tokens */
+    const uint16_t* v_cache;
+    float* out;               /* f32 [n_tokens][num_q_heads][head_dim] */
+    uint32_t n_tokens;
+    uint32_t start;           /* position of token 0 */
+    uint32_t sliding_window;  /* 0 = full */
+    float scale;              /* attention scale (1.0 for Gemma 4) */
+} g4_prefill_entry;
+
+int g4_attn_prefill_workspace_size(const g4_prefill_entry* entries, uint32_t n_entries, uint32_t num_q_heads,
+                                   uint32_t num_kv_heads, uint32_t head_dim, size_t* bytes);
+int g4_attn_prefill_prepare(const g4_prefill_entry* entries, uint32_t n_entries, uint32_t num_q_heads,
+                            uint32_t num_kv_heads, uint32_t head_dim, void* workspace, size_t workspace_bytes,
+                            g4_decode_plan* plan, void* stream);
+int g4_attn_prefill_run(const g4_decode_plan* plan, void* stream);
+/* Measurement hook: g4_attn_prefill_run with two hipEvent_t (timing enabled)
+ * that record the attention kernel's own start and end (the merge, when the
+ * plan has one, follows untimed). */
+int g4_attn_prefill_run_timed(const g4_decode_plan* plan, void* stream, void* start_event, void* stop_event);
+/* prepare + run. */
+int g4_attn_prefill(const g4_prefill_entry* entries, uint32_t n_entries, uint32_t num_q_heads, uint32_t num_kv_heads,
+                    uint32_t head_dim, void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

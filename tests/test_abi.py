@@ -48,6 +48,8 @@ STRUCTS = {
     "g4_prep_layer": abi.PrepLayer,
     "g4_decode_entry": abi.DecodeEntry,
     "g4_decode_plan": abi.DecodePlan,
+    "g4_step_entry": abi.StepEntry,
+    "g4_prefill_entry": abi.PrefillEntry,
 }
 
 

@@ -1,0 +1,120 @@
+"""GPU parity of the MFMA causal prefill (g4_attn_prefill) against the oracle.
+
+The reference has no prefill kernel; it runs one decode step per prompt token
+(src/engine.ts:2469-2475). So token t of an entry (position start + t) is
+checked against the oracle's attnScore -> softmax -> attnOutput chain at
+seq_len = start + t + 1, with the local-layer window, on the same f16 cache
+rows and the f16 query widened to f32. Bar: max-abs 2e-3 (P is rounded to f16
+for the output MFMA). Parts of long key ranges go through the log-sum-exp
+merge (start 2900: three 1024-key parts).
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import announce
+from g4attn import ops, synth
+from helpers import cache_f16, max_abs
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+HD = 256
+TOL = 2e-3
+
+
+class Chunk:
+    def __init__(self, dev, seed, start, T, window, nqh=8, nkh=1):
+        self.start, self.T, self.window, self.nqh, self.nkh = start, T, window, nqh, nkh
+        rows = start + T
+        self.kc = cache_f16(seed, rows, nkh, HD)
+        self.vc = cache_f16(seed + 1, rows, nkh, HD)
+        q = synth.rms_normalize_rows(synth.normal(seed + 2, T * nqh * HD).reshape(T * nqh, HD))
+        self.qb = orc.f32_to_f16_bits(q).reshape(T, nqh * HD)
+        t16 = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16).reshape(-1)).to(dev)  # noqa: E731
+        self.dq, self.dk, self.dv = t16(self.qb), t16(self.kc), t16(self.vc)
+        self.out = torch.full((T * nqh * HD,), float("nan"), dtype=torch.float32, device=dev)
+
+    def entry(self):
+        return dict(q=self.dq, k_cache=self.dk, v_cache=self.dv, out=self.out, n_tokens=self.T, start=self.start,
+                    sliding_window=self.window, scale=1.0)
+
+    def expected(self):
+        rows = self.start + self.T
+        kf = orc.f16_bits_to_f32(self.kc).reshape(rows, -1)
+        vf = orc.f16_bits_to_f32(self.vc).reshape(rows, -1)
+        qf = orc.f16_bits_to_f32(self.qb).reshape(self.T, -1)
+        want = np.empty((self.T, self.nqh * HD), np.float32)
+        for t in range(self.T):
+            seq = self.start + t + 1
+            want[t] = orc.attention_chain(qf[t], kf[:seq].reshape(-1), vf[:seq].reshape(-1), self.nqh, self.nkh,
+                                          HD, seq, 1.0, self.window)
+        return want.reshape(-1)
+
+
+def run(dev, chunks, nqh=8, nkh=1):
+    arr = ops.make_prefill_entries([c.entry() for c in chunks], nqh, nkh, HD)
+    ws = torch.empty(max(ops.prefill_workspace_bytes(arr, nqh, nkh, HD), 1), dtype=torch.uint8, device=dev)
+    plan = ops.attn_prefill_prepare(arr, nqh, nkh, HD, ws)
+    ops.attn_prefill_run(plan)
+    torch.cuda.synchronize()
+    return plan, ws
+
+
+def check(c, label):
+    got = c.out.cpu().numpy()
+    assert np.isfinite(got).all(), f"{label}: non-finite output"
+    err = max_abs(got, c.expected())
+    assert err <= TOL, f"{label}: max-abs {err}"
+    return err
+
+
+CASES = [  # (start, T, window)
+    (0, 40, 0), (0, 100, 32), (600, 70, 512), (2900, 24, 0), (5, 1, 0), (0, 16, 512), (1000, 33, 512),
+]
+
+
+@pytest.mark.parametrize("start,T,window", CASES)
+def test_prefill_chunk(dev, start, T, window):
+    announce(f"attnPrefill start={start} T={T} window={window}")
+    c = Chunk(dev, 31 + start + T, start, T, window)
+    run(dev, [c])
+    print(f"start={start} T={T} W={window} err={check(c, 'chunk'):.2e}")
+
+
+def test_prefill_many_chunks_one_launch(dev):
+    """A global and a local layer, each as two consecutive chunks, in one launch."""
+    announce("attnPrefill 4 entries in one launch")
+    chunks = [Chunk(dev, 7, 0, 64, 0), Chunk(dev, 8, 64, 64, 0), Chunk(dev, 9, 0, 64, 48), Chunk(dev, 10, 64, 64, 48)]
+    run(dev, chunks)
+    for i, c in enumerate(chunks):
+        check(c, f"entry {i}")
+
+
+def test_prefill_gqa_two_kv_heads(dev):
+    announce("attnPrefill nqh=4 nkh=2")
+    c = Chunk(dev, 12, 10, 33, 0, nqh=4, nkh=2)
+    run(dev, [c], nqh=4, nkh=2)
+    check(c, "gqa")
+
+
+def test_prefill_replay_identical(dev):
+    announce("attnPrefill replay")
+    c = Chunk(dev, 13, 2000, 40, 0)
+    plan, ws = run(dev, [c])
+    first = c.out.cpu().numpy().copy()
+    c.out.fill_(float("nan"))
+    ops.attn_prefill_run(plan)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(c.out.cpu().numpy().view(np.uint32), first.view(np.uint32))
+    check(c, "replay")
+
+
+def test_prefill_rejects_bad_shapes(dev):
+    c = Chunk(dev, 14, 0, 4, 0)
+    arr = ops.make_prefill_entries([c.entry()], 8, 1, HD)
+    from g4attn.abi import G4Error
+    with pytest.raises(G4Error):
+        ops.prefill_workspace_bytes(arr, 8, 1, 128)
+    with pytest.raises(G4Error):
+        ops.prefill_workspace_bytes(arr, 24, 1, HD)
