@@ -191,6 +191,31 @@ def test_step_replay_is_deterministic(dev):
         check(L, want, kb, vb, "replay")
 
 
+def test_step_stack_replays_bitwise(dev):
+    """The 35-layer stack replayed many times: every replay gives the same bits (split records and
+    the fixed-order merge), within tolerance of the oracle."""
+    announce("attnStep stack replays")
+    cfg = e2b.AttnConfig(num_layers=35)
+    layers = [Layer(dev, 500 + il, 4097, e2b.sliding_window(il, cfg), e2b.rope_theta(il, cfg),
+                    e2b.apply_divisor(il, cfg)) for il in range(35)]
+    arr = ops.make_step_entries([L.entry() for L in layers], NQH, NKH, HD)
+    ws = torch.empty(ops.step_workspace_bytes(35, NQH, NKH, HD), dtype=torch.uint8, device=dev)
+    plan = ops.attn_step_prepare(arr, NQH, NKH, HD, ws)
+    first = None
+    for rep in range(12):
+        for L in layers:
+            L.out.fill_(float("nan"))
+        ops.attn_step_run(plan)
+        torch.cuda.synchronize()
+        got = np.concatenate([L.out.cpu().numpy() for L in layers]).view(np.uint32)
+        if first is None:
+            first = got.copy()
+        np.testing.assert_array_equal(got, first, err_msg=f"replay {rep}")
+    for L in layers[:6]:
+        want, kb, vb = L.expected()
+        check(L, want, kb, vb, "stack replay")
+
+
 def test_step_gqa_two_kv_heads(dev):
     announce("attnStep nqh=16 nkh=2")
     L = Layer(dev, 9, 1500, 0, 1e6, 1, nqh=16, nkh=2)
