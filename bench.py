@@ -107,14 +107,17 @@ class CacheSet:
 
     def __init__(self, spec, set_idx, dev, torch, ops, synth, e2b):
         self.entries = []
+        import numpy as np
+
         seed0 = spec["seed"] + 7919 * set_idx
-        rf = torch.tensor(e2b.rope_freqs_f16_bits(256), dtype=torch.int32).to(torch.int16).to(dev)
+        rf_bits = np.array(e2b.rope_freqs_f16_bits(256), dtype=np.uint16)
+        rf = torch.from_numpy(rf_bits.view(np.int16)).to(dev)
         ones = torch.full((HD,), 0x3C00, dtype=torch.int16, device=dev)  # norm weights 1.0 (f16)
         inv_freq = {}  # one RoPE inverse-frequency table per (theta, divisor), as a model holds them
         for il, L in enumerate(spec["layers"]):
             key = (L["theta"], L["divisor"])
             if key not in inv_freq:
-                inv_freq[key] = ops.rope_inv_freq(L["theta"], HD, L["divisor"], rf)
+                inv_freq[key] = ops.rope_inv_freq_host(L["theta"], HD, L["divisor"], rf_bits)
             rows = L["seq"]
             kc = torch.empty(rows * NKH * HD, dtype=torch.float16, device=dev)
             vc = torch.empty_like(kc)
@@ -129,7 +132,7 @@ class CacheSet:
                 q=synth.normal_torch(seed0 + 1000 * il + 2, NQH * HD, dev),
                 k=synth.normal_torch(seed0 + 1000 * il + 3, NKH * HD, dev),
                 v=synth.normal_torch(seed0 + 1000 * il + 4, NKH * HD, dev),
-                q_weight=ones, k_weight=ones, rope_freqs=rf, rope_inv_freq=inv_freq[key], k_cache=kc.view(torch.int16),
+                q_weight=ones, k_weight=ones, rope_freqs=rf, rope_inv_freq_host=inv_freq[key], k_cache=kc.view(torch.int16),
                 v_cache=vc.view(torch.int16), out=torch.zeros(NQH * HD, dtype=torch.float32, device=dev),
                 seq_len=L["seq"], position=L["pos"], sliding_window=L["window"], store_kv=True,
                 theta=L["theta"], apply_divisor=L["divisor"], scale=1.0, eps=EPS))

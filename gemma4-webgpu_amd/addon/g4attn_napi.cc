@@ -345,6 +345,27 @@ napi_value RopeInvFreq(napi_env env, napi_callback_info info) {
     return undefined(env);
 }
 
+napi_value RopeInvFreqHost(napi_env env, napi_callback_info info) {
+    Args a(env, info, 5);  // theta, head_dim, apply_divisor, rope_freqs bits (Uint16Array or null), out (Float32Array)
+    const double theta = a.f64(0);
+    const uint32_t hd = a.u32(1), div = a.u32(2);
+    if (!a.ok) return nullptr;
+    napi_valuetype t;
+    napi_typeof(env, a.v[3], &t);
+    void* rf = nullptr;
+    size_t rf_len = 0;
+    if (t != napi_null && t != napi_undefined && !a.bytes(3, &rf, &rf_len)) return nullptr;
+    void* out = nullptr;
+    size_t out_len = 0;
+    if (!a.bytes(4, &out, &out_len)) return nullptr;
+    if (out_len < (size_t)hd / 2 * 4 || (rf && rf_len < (size_t)hd / 2 * 2)) {
+        a.fail("ropeInvFreqHost: tables shorter than head_dim/2 values");
+        return nullptr;
+    }
+    CALL(env, g4_rope_inv_freq_host((float)theta, hd, div, (const uint16_t*)rf, (float*)out));
+    return undefined(env);
+}
+
 napi_value AttnStepWorkspaceSize(napi_env env, napi_callback_info info) {
     Args a(env, info, 4);  // n_entries, num_q_heads, num_kv_heads, head_dim
     const uint32_t n = a.u32(0), nqh = a.u32(1), nkh = a.u32(2), hd = a.u32(3);
@@ -365,7 +386,7 @@ bool get_prop(napi_env env, napi_value obj, const char* key, napi_value* out) {
 }
 
 // One g4_step_entry from a JS object with the same field names in camelCase.
-bool step_entry(Args& a, napi_value obj, size_t idx, g4_step_entry* e) {
+bool step_entry(Args& a, napi_value obj, size_t idx, uint32_t head_dim, g4_step_entry* e) {
     napi_env env = a.env;
     memset(e, 0, sizeof *e);
     struct {
@@ -379,7 +400,6 @@ bool step_entry(Args& a, napi_value obj, size_t idx, g4_step_entry* e) {
         {"qWeight", (const void**)&e->q_weight, true},
         {"kWeight", (const void**)&e->k_weight, true},
         {"ropeFreqs", (const void**)&e->rope_freqs, false},
-        {"ropeInvFreq", (const void**)&e->rope_inv_freq, false},
         {"kCache", (const void**)&e->k_cache, true},
         {"vCache", (const void**)&e->v_cache, true},
         {"out", (const void**)&e->out, true},
@@ -400,6 +420,23 @@ bool step_entry(Args& a, napi_value obj, size_t idx, g4_step_entry* e) {
             return false;
         }
         *p.dst = reinterpret_cast<const void*>(static_cast<uintptr_t>(x));
+    }
+    {  // the host RoPE inverse-frequency table: a Float32Array of head_dim/2 values, read during prepare
+        napi_value v;
+        if (get_prop(env, obj, "ropeInvFreq", &v)) {
+            bool is_ta = false;
+            napi_is_typedarray(env, v, &is_ta);
+            napi_typedarray_type type = napi_int8_array;
+            size_t n = 0, off = 0;
+            void* data = nullptr;
+            napi_value ab;
+            if (is_ta) napi_get_typedarray_info(env, v, &type, &n, &data, &ab, &off);
+            if (!is_ta || type != napi_float32_array || n < head_dim / 2) {
+                a.fail("entry " + std::to_string(idx) + ": ropeInvFreq must be a Float32Array of head_dim/2 values");
+                return false;
+            }
+            e->rope_inv_freq_host = static_cast<const float*>(data);
+        }
     }
     struct {
         const char* key;
@@ -476,13 +513,14 @@ napi_value AttnStepPrepare(napi_env env, napi_callback_info info) {
     }
     uint32_t n = 0;
     napi_get_array_length(env, a.v[0], &n);
+    const uint32_t nqh = a.u32(1), nkh = a.u32(2), hd = a.u32(3);
+    if (!a.ok) return nullptr;
     std::vector<g4_step_entry> ents(n);
     for (uint32_t i = 0; i < n; i++) {
         napi_value obj;
         napi_get_element(env, a.v[0], i, &obj);
-        if (!step_entry(a, obj, i, &ents[i])) return nullptr;
+        if (!step_entry(a, obj, i, hd, &ents[i])) return nullptr;
     }
-    const uint32_t nqh = a.u32(1), nkh = a.u32(2), hd = a.u32(3);
     void* ws = a.ptr(4);
     const double ws_bytes = a.f64(5);
     void* s = a.ptr(6);
@@ -536,6 +574,7 @@ napi_value Init(napi_env env, napi_value exports) {
         {"softmax", Softmax},
         {"attnOutput", AttnOutput},
         {"ropeInvFreq", RopeInvFreq},
+        {"ropeInvFreqHost", RopeInvFreqHost},
         {"attnStepWorkspaceSize", AttnStepWorkspaceSize},
         {"attnStepPrepare", AttnStepPrepare},
         {"attnStepRun", AttnStepRun},

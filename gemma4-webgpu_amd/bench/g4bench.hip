@@ -210,14 +210,15 @@ int main(int argc, char** argv) {
     HK(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
     std::vector<uint16_t> rf(256), ones(HD, 0x3C00);
     for (int i = 0; i < 256; i++) rf[i] = i < 64 ? 0x3C00 : 0x7C00;
-    void *d_rf, *d_ones, *d_inv[2];
+    void *d_rf, *d_ones;
+    std::vector<float> h_inv[2];
     CK(g4_malloc(&d_rf, 512));
     CK(g4_malloc(&d_ones, HD * 2));
     CK(g4_upload(d_rf, 0, rf.data(), 512, st));
     CK(g4_upload(d_ones, 0, ones.data(), HD * 2, st));
     for (int i = 0; i < 2; i++) {  // RoPE inverse frequencies: local (theta 1e4) and global (1e6, divisor)
-        CK(g4_malloc(&d_inv[i], HD / 2 * 4));
-        CK(g4_rope_inv_freq(i ? 1e6f : 1e4f, HD, i, (const uint16_t*)d_rf, (float*)d_inv[i], st));
+        h_inv[i].resize(HD / 2);
+        CK(g4_rope_inv_freq_host(i ? 1e6f : 1e4f, HD, i, rf.data(), h_inv[i].data()));
     }
 
     struct Set {
@@ -274,7 +275,7 @@ int main(int argc, char** argv) {
             se.v = (const float*)v;
             se.q_weight = se.k_weight = (const uint16_t*)d_ones;
             se.rope_freqs = (const uint16_t*)d_rf;
-            se.rope_inv_freq = (const float*)d_inv[l.divisor ? 1 : 0];
+            se.rope_inv_freq_host = h_inv[l.divisor ? 1 : 0].data();
             se.k_cache = (uint16_t*)kc;
             se.v_cache = (uint16_t*)vc;
             se.out = (float*)out;

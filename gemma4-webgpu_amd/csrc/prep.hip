@@ -127,3 +127,20 @@ extern "C" int g4_rope_inv_freq(float theta, uint32_t head_dim, uint32_t apply_d
     G4_CHECK_LAUNCH("ropeInvFreq");
     return G4_OK;
 }
+
+// The same table on the host (one configuration, computed once at load): the
+// same f32 expression with the host's pow, whose f64 result rounded to f32
+// equals the device's.
+extern "C" int g4_rope_inv_freq_host(float theta, uint32_t head_dim, uint32_t apply_divisor,
+                                     const uint16_t* rope_freqs_host, float* inv_freq_host) {
+    if (!inv_freq_host) return fail(G4_EINVAL, "ropeInvFreqHost: NULL output");
+    if (head_dim == 0 || head_dim % 2) return fail(G4_EINVAL, "ropeInvFreqHost: head_dim %u", head_dim);
+    if (apply_divisor && !rope_freqs_host) return fail(G4_EINVAL, "ropeInvFreqHost: apply_divisor needs rope_freqs");
+    for (uint32_t i = 0; i < head_dim / 2; i++) {
+        const float e = (float)(i * 2u) / (float)head_dim;
+        const float base_freq = 1.0f / (float)pow((double)theta, (double)e);
+        inv_freq_host[i] =
+            apply_divisor ? base_freq / (float)__builtin_bit_cast(_Float16, rope_freqs_host[i]) : base_freq;
+    }
+    return G4_OK;
+}

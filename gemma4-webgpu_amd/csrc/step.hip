@@ -39,6 +39,8 @@
 
 #include <hip/hip_ext.h>
 
+#include <map>
+#include <utility>
 #include <vector>
 
 #include "decode_core.h"
@@ -53,7 +55,7 @@ struct StepEntryDev {
     const uint16_t* q_weight;
     const uint16_t* k_weight;
     const uint16_t* rope_freqs;
-    const float* rope_inv_freq;  // optional precomputed inverse frequencies
+    const float* rope_cs;  // RoPE factors of this token [cos x 128][sin x 128] (host-computed), or nullptr
     uint16_t* k_cache;  // [rows][num_kv_heads][HD]
     uint16_t* v_cache;
     float* out;         // attnOut [num_kv_heads][group][HD]
@@ -124,7 +126,7 @@ struct StepSmem {
     float qf[kMaxGroup][kStepHD];  // post-prep q * qscale
     f16x8 knew[kStepHD / 8];       // current row's k and v, f16 (as stored)
     f16x8 vnew[kStepHD / 8];
-    float rope_c[kStepHD / 2];     // RoPE factors of the 128 pairs
+    float rope_c[kStepHD / 2];     // RoPE factors of the 128 pairs, when evaluated in the kernel
     float rope_s[kStepHD / 2];
     float mnew[kMaxGroup];         // current row's scores (log2 units)
 };
@@ -159,12 +161,15 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void k_attn_step(StepArgs a) {
     // is not needed): with loads under branches the compiler cannot count the
     // younger loads on every path, and its wait for a small operand would also
     // wait for the tile. f16 values stay unconverted until used.
-    const unsigned pair = (unsigned)wave * 32u + (unsigned)(lane & 31);  // RoPE pair computed by this lane
+    // RoPE factors of pairs (lane, lane + 64) from the host table; absent
+    // tables are replaced by valid dummy addresses (the values are not used).
+    const float* rcs = ent.rope_cs;
+    const float* rsrc = rcs ? rcs : ent.q;
+    const float rc0 = ldg<float>(rsrc + lane), rs0 = ldg<float>(rsrc + 128 + lane);
+    const float rc1 = ldg<float>(rsrc + 64 + lane), rs1 = ldg<float>(rsrc + 192 + lane);
+    const unsigned pair = (unsigned)wave * 32u + (unsigned)(lane & 31);  // pair evaluated by this lane otherwise
     const unsigned apply_divisor = ent.apply_divisor;
-    const float* inv_tab = ent.rope_inv_freq;
-    // Absent tables are replaced by a valid dummy address (the values are not used).
     const uint32_t fbits = ldg<uint16_t>((apply_divisor ? ent.rope_freqs : ent.q_weight) + pair);
-    const float tab_freq = ldg<float>((inv_tab ? inv_tab : ent.q) + pair);
     float xq[2][4];
 #pragma unroll
     for (int r = 0; r < 2; r++) {
@@ -196,28 +201,23 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void k_attn_step(StepArgs a) {
     load_v_tile<HD>(Vb, row_bytes, last, n, g, k0 + t0, vreg);
     __builtin_amdgcn_sched_barrier(0);  // keep every request above ahead of the arithmetic below
 
-    // ---- RoPE factors: one pair per lane (lanes 32..63 repeat 0..31), the
-    // reference's expressions with f64 transcendentals ----
-    {
-        float freq;
-        if (inv_tab) {
-            freq = tab_freq;
-        } else {  // division by 1 is exact: dividing unconditionally keeps the load unconditional
-            freq = rope_inv_freq(pair, HD, ent.theta, 1u, apply_divisor ? h2f((uint16_t)fbits) : 1.0f);
-        }
-        const float ang = (float)ent.position * freq;
-        const float c = (float)cos((double)ang);
-        const float s = (float)sin((double)ang);
-        if (lane < 32) {
-            sm.rope_c[pair] = c;
-            sm.rope_s[pair] = s;
-        }
-    }
-    __syncthreads();
-
     // ---- q heads (two per wave) straight into the score operand; the current
     // row's k and v ----
-    const RopeLane rl = {sm.rope_c[lane], sm.rope_s[lane], sm.rope_c[lane + 64], sm.rope_s[lane + 64]};
+    RopeLane rl = {rc0, rs0, rc1, rs1};
+    if (!rcs) {  // uniform: one pair per lane (lanes 32..63 repeat 0..31), the reference's expressions
+        // with f64 transcendentals; division by 1 is exact, so the load above stays unconditional
+        const float freq = rope_inv_freq(pair, HD, ent.theta, 1u, apply_divisor ? h2f((uint16_t)fbits) : 1.0f);
+        const float ang = (float)ent.position * freq;
+        const float c = (float)cos((double)ang);
+        const float sn = (float)sin((double)ang);
+        if (lane < 32) {
+            sm.rope_c[pair] = c;
+            sm.rope_s[pair] = sn;
+        }
+        __syncthreads();
+        rl = RopeLane{sm.rope_c[lane], sm.rope_s[lane], sm.rope_c[lane + 64], sm.rope_s[lane + 64]};
+    }
+
     const float qscale = ent.qscale, eps = ent.eps;
     f16* qop = reinterpret_cast<f16*>(sm.dec.q);  // [chunk c][operand lane 16*g + column][8]
 #pragma unroll
@@ -320,7 +320,7 @@ struct StepPlanRep {
 static_assert(sizeof(StepPlanRep) <= sizeof(g4_decode_plan), "plan size");
 
 struct StepLayout {
-    size_t table, work, merge_table, part_ml, part_o, total;
+    size_t table, rope, work, merge_table, part_ml, part_o, total;
 };
 
 StepLayout step_layout(uint64_t n, uint64_t nkh, uint64_t group, uint64_t hd) {
@@ -330,6 +330,8 @@ StepLayout step_layout(uint64_t n, uint64_t nkh, uint64_t group, uint64_t hd) {
     size_t off = 0;
     L.table = off;
     off += align256(n * sizeof(StepEntryDev));
+    L.rope = off;  // RoPE factors: at most one [cos x hd/2][sin x hd/2] set per entry
+    off += align256(n * hd * 4);
     L.work = off;
     off += align256(max_items * sizeof(StepWorkDev));
     L.merge_table = off;
@@ -350,6 +352,7 @@ struct Staging {
 };
 
 int stage_upload(Staging& sg, void* dst, const void* src, size_t bytes, hipStream_t st) {
+    if (bytes == 0) return G4_OK;
     if (!sg.done) G4_CHECK_HIP(hipEventCreateWithFlags(&sg.done, hipEventDisableTiming));
     G4_CHECK_HIP(hipEventSynchronize(sg.done));
     if (sg.cap < bytes) {
@@ -431,7 +434,6 @@ int g4_attn_step_prepare(const g4_step_entry* entries, uint32_t n_entries, uint3
         d.q_weight = s.q_weight;
         d.k_weight = s.k_weight;
         d.rope_freqs = s.rope_freqs;
-        d.rope_inv_freq = s.rope_inv_freq;
         d.k_cache = s.k_cache;
         d.v_cache = s.v_cache;
         d.out = s.out;
@@ -482,7 +484,37 @@ int g4_attn_step_prepare(const g4_step_entry* entries, uint32_t n_entries, uint3
     const StepLayout L = step_layout(n_entries, num_kv_heads, G, head_dim);
     hipStream_t st = as_stream(stream);
     char* ws = static_cast<char*>(workspace);
-    static thread_local Staging sg_table, sg_work, sg_merge;
+    // RoPE factors of each (inverse-frequency table, position) in use: the
+    // reference's cos/sin of the f32 angle, evaluated in f64 and rounded.
+    std::vector<float> rope;
+    {
+        std::map<std::pair<const float*, uint32_t>, uint32_t> seen;
+        const uint32_t half = head_dim / 2;
+        for (uint32_t i = 0; i < n_entries; i++) {
+            const g4_step_entry& s = entries[i];
+            if (!s.rope_inv_freq_host) continue;
+            const auto key = std::make_pair(s.rope_inv_freq_host, s.position);
+            auto it = seen.find(key);
+            uint32_t idx;
+            if (it != seen.end()) {
+                idx = it->second;
+            } else {
+                idx = (uint32_t)seen.size();
+                seen.emplace(key, idx);
+                rope.resize((size_t)(idx + 1) * head_dim);
+                float* c = rope.data() + (size_t)idx * head_dim;
+                for (uint32_t p = 0; p < half; p++) {
+                    const float ang = (float)s.position * s.rope_inv_freq_host[p];
+                    c[p] = (float)cos((double)ang);
+                    c[half + p] = (float)sin((double)ang);
+                }
+            }
+            tab[i].rope_cs = reinterpret_cast<const float*>(ws + L.rope) + (size_t)idx * head_dim;
+        }
+    }
+    static thread_local Staging sg_table, sg_work, sg_merge, sg_rope;
+    rc = stage_upload(sg_rope, ws + L.rope, rope.data(), rope.size() * sizeof(float), st);
+    if (rc) return rc;
     rc = stage_upload(sg_table, ws + L.table, tab.data(), (size_t)n_entries * sizeof(StepEntryDev), st);
     if (rc) return rc;
     rc = stage_upload(sg_work, ws + L.work, work.data(), work.size() * sizeof(StepWorkDev), st);

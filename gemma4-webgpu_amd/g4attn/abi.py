@@ -78,7 +78,7 @@ class DecodeEntry(C.Structure):
 
 class StepEntry(C.Structure):
     _fields_ = [("q", C.c_void_p), ("k", C.c_void_p), ("v", C.c_void_p), ("q_weight", C.c_void_p),
-                ("k_weight", C.c_void_p), ("rope_freqs", C.c_void_p), ("rope_inv_freq", C.c_void_p),
+                ("k_weight", C.c_void_p), ("rope_freqs", C.c_void_p), ("rope_inv_freq_host", C.c_void_p),
                 ("k_cache", C.c_void_p),
                 ("v_cache", C.c_void_p), ("out", C.c_void_p), ("seq_len", C.c_uint32), ("position", C.c_uint32),
                 ("sliding_window", C.c_uint32), ("store_kv", C.c_uint32), ("theta", C.c_float),
@@ -132,6 +132,7 @@ SIGNATURES: dict[str, list] = {
     "g4_attn_step_workspace_size": [_U32, _U32, _U32, _U32, C.POINTER(C.c_size_t)],
     "g4_attn_step_prepare": [C.POINTER(StepEntry), _U32, _U32, _U32, _U32, _P, _SZ, C.POINTER(DecodePlan), _P],
     "g4_rope_inv_freq": [C.c_float, _U32, _U32, _P, _P, _P],
+    "g4_rope_inv_freq_host": [C.c_float, _U32, _U32, _P, _P],
     "g4_attn_step_run": [C.POINTER(DecodePlan), _P],
     "g4_attn_step_run_attention": [C.POINTER(DecodePlan), _P],
     "g4_attn_step_run_merge": [C.POINTER(DecodePlan), _P],

@@ -231,9 +231,36 @@ def rope_inv_freq(theta, head_dim, apply_divisor, rope_freqs=None, stream=None) 
     return out
 
 
+def rope_inv_freq_host(theta, head_dim, apply_divisor, rope_freqs_bits=None):
+    """The [head_dim/2] RoPE inverse-frequency table computed on the host (numpy float32), for
+    step entries' rope_inv_freq_host; rope_freqs_bits: host f16 bits of the divisor table."""
+    import numpy as np
+
+    if apply_divisor and rope_freqs_bits is None:
+        raise ValueError("apply_divisor needs rope_freqs_bits")
+    out = np.empty(head_dim // 2, dtype=np.float32)
+    rf = None
+    if rope_freqs_bits is not None:
+        rf = np.ascontiguousarray(rope_freqs_bits, dtype=np.uint16)
+        if rf.size < head_dim // 2:
+            raise ValueError("rope_freqs_bits: too short")
+    abi.call("g4_rope_inv_freq_host", float(theta), head_dim, 1 if apply_divisor else 0,
+             rf.ctypes.data if rf is not None else None, out.ctypes.data)
+    return out
+
+
+def _host_f32(a, name, n):
+    import numpy as np
+
+    if not isinstance(a, np.ndarray) or a.dtype != np.float32 or not a.flags.c_contiguous or a.size < n:
+        raise TypeError(f"{name}: expected a contiguous host float32 array of at least {n} values")
+    return a.ctypes.data
+
+
 def make_step_entries(items, num_q_heads, num_kv_heads, head_dim):
     """items: iterable of dicts with q, k, v (raw f32 projections), q_weight, k_weight (f16), rope_freqs (f16 or
-    None), rope_inv_freq (optional f32 table from rope_inv_freq()), k_cache, v_cache (f16, at least seq_len rows),
+    None), rope_inv_freq_host (optional host f32 numpy table from rope_inv_freq_host(); kept alive by the caller
+    until prepare returns), k_cache, v_cache (f16, at least seq_len rows),
     out (f32), seq_len, position, sliding_window, store_kv, theta, apply_divisor, scale, eps."""
     items = list(items)
     arr = (StepEntry * len(items))()
@@ -248,8 +275,8 @@ def make_step_entries(items, num_q_heads, num_kv_heads, head_dim):
             _f32(it["v"], f"entry {i} v", nkv), _f16(it["q_weight"], f"entry {i} q_weight", head_dim),
             _f16(it["k_weight"], f"entry {i} k_weight", head_dim),
             _f16(rf, f"entry {i} rope_freqs", head_dim // 2) if rf is not None else None,
-            _f32(it["rope_inv_freq"], f"entry {i} rope_inv_freq", head_dim // 2)
-            if it.get("rope_inv_freq") is not None else None,
+            _host_f32(it["rope_inv_freq_host"], f"entry {i} rope_inv_freq_host", head_dim // 2)
+            if it.get("rope_inv_freq_host") is not None else None,
             _f16(it["k_cache"], f"entry {i} k_cache", L * nkv), _f16(it["v_cache"], f"entry {i} v_cache", L * nkv),
             _f32(it["out"], f"entry {i} out", num_q_heads * head_dim), L, int(it["position"]),
             int(it.get("sliding_window", 0)), 1 if it.get("store_kv", True) else 0, float(it["theta"]),

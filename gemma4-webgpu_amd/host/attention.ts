@@ -101,7 +101,7 @@ export interface StepEntry {
   qWeight: DeviceBuffer;      // attn_q_norm f16 [HD]
   kWeight: DeviceBuffer;      // attn_k_norm f16 [HD]
   ropeFreqs?: DeviceBuffer;   // f16 divisor table (global layers)
-  ropeInvFreq?: DeviceBuffer; // f32 [HD/2] table from ropeInvFreq()
+  ropeInvFreq?: Float32Array; // host f32 [HD/2] table from ropeInvFreqHost(); RoPE factors are then evaluated in prepare
   kCache: DeviceBuffer;       // f16 [rows][NKH][HD]
   vCache: DeviceBuffer;
   out: DeviceBuffer;          // attnOut f32 [NQH][HD]
@@ -141,6 +141,7 @@ export interface Addon {
   softmax(sc: bigint, p: Uint8Array, s: bigint): void;
   attnOutput(pr: bigint, vc: bigint, o: bigint, p: Uint8Array, s: bigint): void;
   ropeInvFreq(theta: number, hd: number, div: number, rf: any, out: bigint, s: bigint): void;
+  ropeInvFreqHost(theta: number, hd: number, div: number, rf: Uint16Array | null, out: Float32Array): void;
   attnStepWorkspaceSize(n: number, nqh: number, nkh: number, hd: number): number;
   attnStepPrepare(entries: any[], nqh: number, nkh: number, hd: number, ws: bigint, wsBytes: number,
     s: bigint): Uint8Array;
@@ -220,6 +221,13 @@ export class HipAttention {
     this.g4.ropeInvFreq(theta, headDim, applyDivisor, ropeFreqs ? ropeFreqs.ptr : null, out.ptr, this.stream);
   }
 
+  // The same table on the host, for StepEntry.ropeInvFreq; ropeFreqsBits: the f16 bits of the divisor table.
+  ropeInvFreqHost(theta: number, headDim: number, applyDivisor: number, ropeFreqsBits: Uint16Array | null): Float32Array {
+    const out = new Float32Array(headDim / 2);
+    this.g4.ropeInvFreqHost(theta, headDim, applyDivisor, ropeFreqsBits, out);
+    return out;
+  }
+
   attnStepWorkspaceSize(nEntries: number, shape: StepShape): number {
     return this.g4.attnStepWorkspaceSize(nEntries, shape.numQHeads, shape.numKvHeads, shape.headDim);
   }
@@ -230,7 +238,7 @@ export class HipAttention {
       return {
         q: e.q.ptr, k: e.k.ptr, v: e.v.ptr, qWeight: e.qWeight.ptr, kWeight: e.kWeight.ptr,
         ropeFreqs: e.ropeFreqs ? e.ropeFreqs.ptr : undefined,
-        ropeInvFreq: e.ropeInvFreq ? e.ropeInvFreq.ptr : undefined,
+        ropeInvFreq: e.ropeInvFreq,
         kCache: e.kCache.ptr, vCache: e.vCache.ptr, out: e.out.ptr,
         seqLen: e.seqLen, position: e.position, slidingWindow: e.slidingWindow || 0,
         storeKv: e.storeKv === undefined ? true : e.storeKv, theta: e.theta, applyDivisor: e.applyDivisor || 0,

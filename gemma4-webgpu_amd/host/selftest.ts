@@ -103,8 +103,11 @@ function layer(dir: string): string[] {
 
   // (2) the fused step on fresh copies of the same inputs, with the RoPE table
   const q2 = upload('q'), k2 = upload('k'), v2 = upload('v'), kc2 = upload('kc'), vc2 = upload('vc');
-  const out2 = alloc(NQH * HD * 4), inv = alloc(HD / 2 * 4);
-  att.ropeInvFreq(spec.theta, HD, spec.div, rf, inv);
+  const out2 = alloc(NQH * HD * 4);
+  const rfr = spec.arrays['rf'];
+  const rfBits = new Uint16Array(rfr[1] / 2);
+  new Uint8Array(rfBits.buffer).set(bin.subarray(rfr[0], rfr[0] + rfr[1]));
+  const inv = att.ropeInvFreqHost(spec.theta, HD, spec.div, rfBits);
   const shape = { numQHeads: NQH, numKvHeads: NKH, headDim: HD };
   const ws = alloc(att.attnStepWorkspaceSize(1, shape));
   att.attnStep([{

@@ -262,6 +262,11 @@ int g4_attn_decode_many(const g4_decode_entry* entries, uint32_t n_entries, uint
  * proportional divisor); compute them once and pass them in g4_step_entry. */
 int g4_rope_inv_freq(float theta, uint32_t head_dim, uint32_t apply_divisor, const uint16_t* rope_freqs,
                      float* inv_freq, void* stream);
+/* The same table computed on the host from host copies of the divisor table
+ * (what g4_step_entry.rope_inv_freq_host takes). Bit-identical to the device
+ * version. */
+int g4_rope_inv_freq_host(float theta, uint32_t head_dim, uint32_t apply_divisor, const uint16_t* rope_freqs_host,
+                          float* inv_freq_host);
 
 /* ---- one-launch decode step ---------------------------------------------
  * The whole attention block of one token for many layers or sequences in one
@@ -283,8 +288,9 @@ typedef struct g4_step_entry {
     const uint16_t* q_weight;  /* attn_q_norm, f16 [head_dim] */
     const uint16_t* k_weight;  /* attn_k_norm, f16 [head_dim] */
     const uint16_t* rope_freqs; /* f16 divisor table, read when apply_divisor */
-    const float* rope_inv_freq; /* optional [head_dim/2] table from g4_rope_inv_freq for this entry's
-                                   theta/divisor (computed once, at load); NULL: computed per launch */
+    const float* rope_inv_freq_host; /* optional HOST [head_dim/2] table from g4_rope_inv_freq_host for
+                                        this entry's theta/divisor (computed once, at load): prepare then
+                                        evaluates the RoPE factors on the host; NULL: in the kernel */
     uint16_t* k_cache;         /* f16 [rows][num_kv_heads][head_dim]; rows < seq_len - 1 hold earlier tokens */
     uint16_t* v_cache;
     float* out;                /* attnOut [num_q_heads][head_dim] f32 */

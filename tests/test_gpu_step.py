@@ -62,7 +62,7 @@ class Layer:
                  k_cache=self.kc, v_cache=self.vc, out=self.out, seq_len=self.seq, position=self.pos,
                  sliding_window=self.window, store_kv=store, theta=self.theta, apply_divisor=self.divisor)
         if inv_freq:
-            e["rope_inv_freq"] = ops.rope_inv_freq(self.theta, HD, self.divisor, self.drf)
+            e["rope_inv_freq_host"] = ops.rope_inv_freq_host(self.theta, HD, self.divisor, ROPE)
         return e
 
     def expected(self, kv_from=None):
@@ -120,8 +120,9 @@ def test_step_single_entry(dev, seq, win, theta, div):
 
 @pytest.mark.parametrize("seq,win,theta,div", [(513, 512, 1e4, 0), (8193, 0, 1e6, 1), (40000, 0, 1e6, 1)])
 def test_step_rope_table_same_bits(dev, seq, win, theta, div):
-    """Entries carrying the precomputed inverse-frequency table give the same bits as entries without."""
-    announce(f"attnStep with rope_inv_freq seq={seq} win={win}")
+    """Entries carrying the host inverse-frequency table (RoPE factors evaluated in prepare) give the same
+    bits as entries without (factors evaluated in the kernel)."""
+    announce(f"attnStep with a host RoPE table seq={seq} win={win}")
     L = Layer(dev, 400 + seq, seq, win, theta, div)
     want, kb, vb = L.expected()
     run_step(dev, [L.entry(inv_freq=True)])
