@@ -111,11 +111,12 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void k_decode_split(DecodeArgs a
 // (entry, kv head x query head, column chunk). The dc = HD / n_chunks columns
 // of a chunk are read as float4 by R = dc / 4 threads per record; the
 // P = 256 / R thread groups take records s = grp, grp + P, ... (a fixed
-// assignment) and their sums are added in group order, so the result does not
-// depend on scheduling. Long merges use more chunks, spreading their records
-// over more CUs. The first batch of partials is requested together with the
-// per-split (m, l), so a merge of up to kMergeBatch * P splits waits on memory
-// once.
+// assignment). Each thread requests a batch of its records' (m, l) and
+// columns at once and folds them into a running (m, l, o) in record order;
+// the groups' results are then rescaled to the common max and added in group
+// order, so the result does not depend on scheduling. A merge of up to
+// kMergeBatch * P records waits on memory once; long merges use more chunks
+// (P = 4 * chunks), spreading their records over more CUs.
 constexpr int kMergeThreads = 256;
 constexpr int kMergeBatch = 8;
 constexpr int kMaxMergeSplits = 8192;
@@ -123,76 +124,66 @@ constexpr unsigned kMaxMergeChunks = 16;
 
 template <int HD>
 __global__ __launch_bounds__(kMergeThreads) void k_decode_merge(DecodeArgs a, unsigned n_chunks) {
-    constexpr int kWaves = kMergeThreads / 64;
-    __shared__ float sc[kMaxMergeSplits];
-    __shared__ float red[2][kWaves];
     __shared__ f32x4 part[kMergeThreads];
+    __shared__ float gm[kMergeThreads], gl[kMergeThreads];  // per group: running max, rescaled l
     const DecodeEntryDev ent = a.table ? a.table[blockIdx.x] : a.one;
     const unsigned ns = ent.n_splits;
     if (ns <= 1) return;
     const unsigned G = a.group;
     const unsigned kvh = blockIdx.y / G, h = blockIdx.y % G;
-    const unsigned t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const unsigned t = threadIdx.x;
     const unsigned dc = HD / n_chunks, R = dc / 4, P = kMergeThreads / R;
     const unsigned grp = t / R, q = t % R;
     const unsigned d = blockIdx.z * dc + q * 4;
     const uint64_t rec_stride = (uint64_t)a.num_kv_heads * G;  // partial records per split
     const uint64_t rec0 = ((uint64_t)ent.split_base * a.num_kv_heads + kvh) * G + h;
     const float* o = a.part_o + rec0 * HD + d;
+    const float* ml = a.part_ml + rec0 * 2;
     const uint64_t o_stride = rec_stride * HD;
 
-    f32x4 v[kMergeBatch];  // first batch of this thread's partials, in flight during the (m, l) pass
-#pragma unroll
-    for (int u = 0; u < kMergeBatch; u++) {
-        const unsigned s = grp + u * P;
-        v[u] = s < ns ? ldg<f32x4>(o + s * o_stride) : f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-    float mx = -INFINITY;
-    for (unsigned s = t; s < ns; s += kMergeThreads) {
-        const f32x2 ml = ldg<f32x2>(a.part_ml + (rec0 + s * rec_stride) * 2);
-        sc[s] = ml[0];
-        mx = fmaxf(mx, ml[0]);
-    }
-    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-    if (lane == 0) red[0][wave] = mx;
-    __syncthreads();
-    float M = red[0][0];
-    for (int w = 1; w < kWaves; w++) M = fmaxf(M, red[0][w]);
-    float ls = 0.0f;
-    for (unsigned s = t; s < ns; s += kMergeThreads) {
-        const float f = __builtin_amdgcn_exp2f(sc[s] - M);
-        ls += ldg<float>(a.part_ml + (rec0 + s * rec_stride) * 2 + 1) * f;
-        sc[s] = f;
-    }
-    for (int off = 32; off > 0; off >>= 1) ls += __shfl_xor(ls, off);
-    if (lane == 0) red[1][wave] = ls;
-    __syncthreads();
-    float L = 0.0f;
-    for (int w = 0; w < kWaves; w++) L += red[1][w];
-
+    float m_run = -INFINITY, l_run = 0.0f;
     f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (unsigned s0 = grp; s0 < ns; s0 += kMergeBatch * P) {
+        f32x4 v[kMergeBatch];
+        f32x2 w[kMergeBatch];
 #pragma unroll
-    for (int u = 0; u < kMergeBatch; u++) {
-        const unsigned s = grp + u * P;
-        if (s < ns) acc += v[u] * sc[s];
-    }
-    for (unsigned s0 = grp + kMergeBatch * P; s0 < ns; s0 += kMergeBatch * P) {
+        for (int u = 0; u < kMergeBatch; u++) {  // every request of the batch before any use
+            const unsigned s = s0 + u * P;
+            const bool live = s < ns;
+            v[u] = live ? ldg<f32x4>(o + s * o_stride) : f32x4{0.f, 0.f, 0.f, 0.f};
+            w[u] = live ? ldg<f32x2>(ml + s * rec_stride * 2) : f32x2{-INFINITY, 0.f};
+        }
+        float mb = m_run;
+#pragma unroll
+        for (int u = 0; u < kMergeBatch; u++) mb = fmaxf(mb, w[u][0]);
+        const float c = mb == m_run ? 1.0f : __builtin_amdgcn_exp2f(m_run - mb);  // also 1 while both are -inf
+        acc *= c;
+        l_run *= c;
 #pragma unroll
         for (int u = 0; u < kMergeBatch; u++) {
-            const unsigned s = s0 + u * P;
-            v[u] = s < ns ? ldg<f32x4>(o + s * o_stride) : f32x4{0.f, 0.f, 0.f, 0.f};
+            if (s0 + u * P < ns) {
+                const float f = __builtin_amdgcn_exp2f(w[u][0] - mb);
+                acc += v[u] * f;
+                l_run += w[u][1] * f;
+            }
         }
-#pragma unroll
-        for (int u = 0; u < kMergeBatch; u++) {
-            const unsigned s = s0 + u * P;
-            if (s < ns) acc += v[u] * sc[s];
-        }
+        m_run = mb;
     }
-    part[t] = acc;
+    if (q == 0) gm[grp] = m_run;
+    __syncthreads();
+    float M = gm[0];
+    for (unsigned g2 = 1; g2 < P; g2++) M = fmaxf(M, gm[g2]);
+    const float sc = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - M);  // a group without records
+    part[t] = acc * sc;
+    if (q == 0) gl[grp] = l_run * sc;
     __syncthreads();
     if (grp == 0) {
         f32x4 sum = part[q];
-        for (unsigned g2 = 1; g2 < P; g2++) sum += part[g2 * R + q];
+        float L = gl[0];
+        for (unsigned g2 = 1; g2 < P; g2++) {
+            sum += part[g2 * R + q];
+            L += gl[g2];
+        }
         stg<f32x4>(ent.out + ((uint64_t)kvh * G + h) * HD + d, sum / L);
     }
 }
