@@ -91,6 +91,18 @@ class PrefillEntry(C.Structure):
                 ("scale", C.c_float)]
 
 
+class MatmulParams(C.Structure):  # matmul_quant.wgsl:12
+    _fields_ = [("M", C.c_uint32), ("N", C.c_uint32)]
+
+
+class SoftcapParams(C.Structure):  # logit_softcap.wgsl:5
+    _fields_ = [("size", C.c_uint32), ("cap", C.c_float)]
+
+
+class LmHeadParams(C.Structure):
+    _fields_ = [("vocab", C.c_uint32), ("hidden", C.c_uint32), ("cap", C.c_float)]
+
+
 class DecodePlan(C.Structure):
     _fields_ = [("opaque", C.c_uint64 * 8)]
 
@@ -144,6 +156,12 @@ SIGNATURES: dict[str, list] = {
     "g4_attn_prefill_run": [C.POINTER(DecodePlan), _P],
     "g4_attn_prefill_run_timed": [C.POINTER(DecodePlan), _P, _P, _P],
     "g4_attn_prefill": [C.POINTER(PrefillEntry), _U32, _U32, _U32, _U32, _P, _SZ, _P],
+    "g4_matmul_quant_f16": [_P, _P, _P, MatmulParams, _P],
+    "g4_logit_softcap": [_P, SoftcapParams, _P],
+    "g4_argmax": [_P, _P, _U32, _P],
+    "g4_lm_head_workspace_size": [LmHeadParams, C.POINTER(C.c_size_t)],
+    "g4_lm_head_argmax": [_P, _P, _P, _P, _P, _SZ, LmHeadParams, _P],
+    "g4_lm_head_argmax_timed": [_P, _P, _P, _P, _P, _SZ, LmHeadParams, _P, _P, _P],
 }
 STRING_FUNCS = ("g4_last_error", "g4_version")
 

@@ -15,8 +15,9 @@ import ctypes as C
 import torch
 
 from . import abi
-from .abi import (AttnOutputParams, AttnScoreParams, DecodeEntry, DecodePlan, KvStoreParams, NormParams,
-                  NormRopeParams, PrepLayer, PrepParams, SoftmaxParams, StepEntry)
+from .abi import (AttnOutputParams, AttnScoreParams, DecodeEntry, DecodePlan, KvStoreParams, LmHeadParams,
+                  MatmulParams, NormParams, NormRopeParams, PrepLayer, PrepParams, SoftcapParams, SoftmaxParams,
+                  StepEntry)
 
 F16_TYPES = (torch.float16, torch.int16, torch.uint16)
 
@@ -366,3 +367,53 @@ def attn_prefill_run_timed(plan: DecodePlan, start, stop, stream=None):
 def attn_prefill(entries, num_q_heads, num_kv_heads, head_dim, workspace, stream=None):
     abi.call("g4_attn_prefill", entries, len(entries), num_q_heads, num_kv_heads, head_dim,
              _dev(workspace, "workspace", torch.uint8, 0), workspace.numel(), _stream(stream))
+
+
+# ---- lm head -> logit softcap -> argmax ------------------------------------------
+
+def matmul_quant_f16(x, weight, out, M, N, stream=None):
+    """SHADERS.matmulQuant: out[m] = sum_k f16 weight[m][k] * x[k] (matmul_quant.wgsl order)."""
+    abi.call("g4_matmul_quant_f16", _f32(x, "input", N), _f16(weight, "weight", M * N), _f32(out, "output", M),
+             MatmulParams(M, N), _stream(stream))
+
+
+def logit_softcap(logits, size, cap, stream=None):
+    abi.call("g4_logit_softcap", _f32(logits, "logits", size), SoftcapParams(size, cap), _stream(stream))
+
+
+def argmax(logits, result, size, stream=None):
+    """SHADERS.argmax: result[0] = top-1 index under argmax.wgsl's rule."""
+    abi.call("g4_argmax", _f32(logits, "logits", size), _dev(result, "result", (torch.int32, torch.uint32), 1),
+             size, _stream(stream))
+
+
+def lm_head_workspace_bytes(vocab, hidden, cap) -> int:
+    n = C.c_size_t(0)
+    abi.call("g4_lm_head_workspace_size", LmHeadParams(vocab, hidden, cap), C.byref(n))
+    return int(n.value)
+
+
+def _lm_head_args(hidden, weight, logits, result, workspace, vocab, hidden_size, cap):
+    return (_f32(hidden, "hidden", hidden_size), _f16(weight, "weight", vocab * hidden_size),
+            _f32(logits, "logits", vocab) if logits is not None else None,
+            _dev(result, "result", (torch.int32, torch.uint32), 1), _dev(workspace, "workspace", torch.uint8, 0),
+            workspace.numel(), LmHeadParams(vocab, hidden_size, cap))
+
+
+def lm_head_argmax(hidden, weight, logits, result, workspace, vocab, hidden_size, cap, stream=None):
+    """lmHead -> logitSoftcap -> argmax in one streaming pass (+ a one-workgroup pick): result[0] = top-1
+    index; logits (optional) = the softcapped logits, bit-identical to the three-kernel chain."""
+    abi.call("g4_lm_head_argmax", *_lm_head_args(hidden, weight, logits, result, workspace, vocab, hidden_size, cap),
+             _stream(stream))
+
+
+def lm_head_argmax_timed(hidden, weight, logits, result, workspace, vocab, hidden_size, cap, start, stop,
+                         stream=None):
+    """lm_head_argmax with torch.cuda.Events (timing enabled) around the streaming kernel; the events
+    must exist (record each once before the first use)."""
+    for e, name in ((start, "start"), (stop, "stop")):
+        if not getattr(e, "cuda_event", 0):
+            raise ValueError(f"{name} event has no HIP event yet (record it once first)")
+    abi.call("g4_lm_head_argmax_timed", *_lm_head_args(hidden, weight, logits, result, workspace, vocab,
+                                                      hidden_size, cap),
+             _stream(stream), C.c_void_p(start.cuda_event), C.c_void_p(stop.cuda_event))

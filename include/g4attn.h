@@ -360,6 +360,60 @@ int g4_attn_prefill_run_timed(const g4_decode_plan* plan, void* stream, void* st
 int g4_attn_prefill(const g4_prefill_entry* entries, uint32_t n_entries, uint32_t num_q_heads, uint32_t num_kv_heads,
                     uint32_t head_dim, void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---- lm head -> logit softcap -> argmax (greedy top-1) ------------------
+ * src/engine.ts:2223-2255: lmHead (matmulQuant over the f16 tied embedding
+ * [vocab][hidden]), logitSoftcap (when final_logit_softcapping > 0), then
+ * sample.argmax (one workgroup). */
+
+/* matmul_quant.wgsl:12; built for lmHead as {M: vocab, N: hidden} */
+typedef struct g4_matmul_params {
+    uint32_t M;
+    uint32_t N;
+} g4_matmul_params;
+
+/* logit_softcap.wgsl:5 */
+typedef struct g4_softcap_params {
+    uint32_t size;
+    float cap;
+} g4_softcap_params;
+
+/* SHADERS.matmulQuant — matmul_quant.wgsl:20-52, dispatched by dispatchMatmul
+ * (src/engine.ts:363-377): output[m] = sum_k f16 weight[m][k] * input[k], in
+ * the shader's order (invocation tid sums k = tid mod 256 in order, then the
+ * 128 -> 1 tree): bit-identical to it. */
+int g4_matmul_quant_f16(const float* input, const uint16_t* weight, float* output, g4_matmul_params p, void* stream);
+
+/* SHADERS.logitSoftcap — logit_softcap.wgsl:9-16 (src/engine.ts:2230-2236). In place. */
+int g4_logit_softcap(float* logits, g4_softcap_params p, void* stream);
+
+/* SHADERS.argmax — argmax.wgsl:7-34 (src/engine.ts:2247-2250): result[0] =
+ * the index the shader's one workgroup picks, ties included. */
+int g4_argmax(const float* logits, uint32_t* result, uint32_t size, void* stream);
+
+/* The three passes above fused for the whole chip (new): one streaming pass
+ * over the weight computes each logit with matmul_quant.wgsl's summation
+ * order and logit_softcap.wgsl's expression (cap 0 = no softcap), so logits
+ * are bit-identical to the three-kernel chain; the top-1 is chosen by
+ * argmax.wgsl's rule (first maximum per index residue mod 256, residues
+ * compared through its 128 -> 1 tree), so result[0] equals the chain's
+ * argmax, ties included. logits may be NULL (not written). hidden % 256 == 0,
+ * 1024 <= hidden <= 2560; hidden and weight 16-byte aligned. The workspace (g4_lm_head_workspace_size bytes)
+ * holds per-workgroup candidates; nothing in it persists between calls. */
+typedef struct g4_lm_head_params {
+    uint32_t vocab;   /* rows of the weight */
+    uint32_t hidden;  /* columns; length of the input */
+    float cap;        /* final_logit_softcapping; 0 = none */
+} g4_lm_head_params;
+
+int g4_lm_head_workspace_size(g4_lm_head_params p, size_t* bytes);
+int g4_lm_head_argmax(const float* hidden, const uint16_t* weight, float* logits, uint32_t* result, void* workspace,
+                      size_t workspace_bytes, g4_lm_head_params p, void* stream);
+/* Measurement hook: g4_lm_head_argmax with two hipEvent_t (timing enabled)
+ * recorded around the streaming kernel (the small pick kernel follows). */
+int g4_lm_head_argmax_timed(const float* hidden, const uint16_t* weight, float* logits, uint32_t* result,
+                            void* workspace, size_t workspace_bytes, g4_lm_head_params p, void* stream,
+                            void* start_event, void* stop_event);
+
 #ifdef __cplusplus
 }
 #endif

@@ -67,3 +67,27 @@ def sdpa(q, k_cache, v_cache, num_q_heads, num_kv_heads, head_dim, seq_len, scal
 
 def softcap(x, cap):
     return np.tanh(np.clip(np.asarray(x, np.float64) / cap, -15.0, 15.0)) * cap
+
+
+def matvec(weight_f32, x):
+    """Textbook f64 matrix-vector product."""
+    return np.asarray(weight_f32, dtype=np.float64) @ np.asarray(x, dtype=np.float64)
+
+
+def bitrev8(r):
+    r = int(r)
+    return int(f"{r:08b}"[::-1], 2)
+
+
+def argmax_rule(x):
+    """Top-1 index under argmax.wgsl's rule, stated without its loops: the
+    maximum M over values above -1e30 (NaN excluded); among indices i with
+    x[i] == M the one with the smallest (bit-reversed 8-bit i mod 256, i); 0
+    when no value is above -1e30."""
+    x = np.asarray(x, dtype=np.float32)
+    ok = (x > np.float32(-1e30)) & ~np.isnan(x)
+    if not ok.any():
+        return 0
+    m = x[ok].max()
+    cand = np.nonzero(ok & (x == m))[0]
+    return int(min(cand, key=lambda i: (bitrev8(i % 256), i)))

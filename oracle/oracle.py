@@ -194,6 +194,16 @@ def attention_chain(q, k_cache, v_cache, num_q_heads, num_kv_heads, head_dim, se
     return attn_output(pr, v_cache, num_q_heads, num_kv_heads, head_dim, seq_len)
 
 
+def matmul_quant(x, weight_bits, M, N):
+    """matmul_quant.wgsl over f16 weight bits [M][N] and f32 input [N]; returns f32 [M]."""
+    x = _f32(x)
+    w = _u16(weight_bits)
+    assert x.size >= N and w.size >= M * N
+    out = np.empty(M, dtype=np.float32)
+    lib().wr_matmul_quant(_p(x), _p(w), _p(out), C.c_uint32(M), C.c_uint32(N))
+    return out
+
+
 def logit_softcap(logits, cap):
     x = _f32(logits)
     lib().wr_logit_softcap(_p(x), C.c_uint32(x.size), C.c_float(cap))

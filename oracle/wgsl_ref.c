@@ -31,7 +31,8 @@
  *   shaders/attn_score.wgsl:15-40
  *   shaders/softmax.wgsl:7-46
  *   shaders/attn_output.wgsl:7-23
- *   argmax semantics: shaders/argmax.wgsl:7-34, shaders/logit_softcap.wgsl:9-16
+ *   lm head and sampling: shaders/matmul_quant.wgsl:20-52 (f16 weights),
+ *     shaders/logit_softcap.wgsl:9-16, shaders/argmax.wgsl:7-34
  *   dispatch grids: src/engine.ts:2060-2094
  */
 #include <math.h>
@@ -319,6 +320,25 @@ void wr_attn_output(const float* probs, const float* v_cache, float* output, con
     }
 }
 
+/* ---- shaders/matmul_quant.wgsl:20-52 ------------------------------------ *
+ * One workgroup per output row m (dispatched by engine.ts dispatchMatmul,
+ * a 2D grid above 65535 rows; m = wg.y * ng.x + wg.x covers 0..M-1): the
+ * invocation tid sums weight[m, k] * input[k] over k = tid, tid + 256, ...
+ * in order (f16 weight widened exactly), then the 128 -> 1 tree.            */
+void wr_matmul_quant(const float* input, const uint16_t* weight, float* output, uint32_t M, uint32_t N) {
+#pragma omp parallel for schedule(static)
+    for (int64_t m = 0; m < (int64_t)M; m++) {
+        float partials[WG];
+        const uint16_t* row = weight + (uint64_t)m * N;
+        for (uint32_t tid = 0; tid < WG; tid++) {
+            float acc = 0.0f;
+            for (uint32_t k = tid; k < N; k += WG) acc = acc + wr_f16_to_f32(row[k]) * input[k];
+            partials[tid] = acc;
+        }
+        output[m] = tree_sum(partials);
+    }
+}
+
 /* ---- shaders/logit_softcap.wgsl:9-16 ------------------------------------ */
 void wr_logit_softcap(float* logits, uint32_t size, float cap) {
     for (uint32_t i = 0; i < size; i++) {
@@ -329,8 +349,13 @@ void wr_logit_softcap(float* logits, uint32_t size, float cap) {
 }
 
 /* ---- shaders/argmax.wgsl:7-34 (one workgroup) --------------------------- *
- * Per-invocation first strict maximum over i = tid (mod 256), then a tree
- * that keeps the lower tid on ties: ties resolve to the smallest i mod 256.  */
+ * Per-invocation first strict maximum over i = tid (mod 256) (values not
+ * above the -1e30 start and NaN never win; index 0 if nothing does), then the
+ * 128 -> 1 tree, in which a slot takes its partner's pair only when strictly
+ * greater. Among residues holding the maximum, the tree's last level prefers
+ * bit 0 of the residue clear, the level before bit 1, and so on: the winner is
+ * the residue with the smallest bit-reversed (8-bit) value, not the smallest
+ * residue (residues 1 and 4 tie: 4 wins).                                    */
 uint32_t wr_argmax(const float* logits, uint32_t size) {
     float smax[WG];
     uint32_t sidx[WG];

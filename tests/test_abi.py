@@ -50,6 +50,9 @@ STRUCTS = {
     "g4_decode_plan": abi.DecodePlan,
     "g4_step_entry": abi.StepEntry,
     "g4_prefill_entry": abi.PrefillEntry,
+    "g4_matmul_params": abi.MatmulParams,
+    "g4_softcap_params": abi.SoftcapParams,
+    "g4_lm_head_params": abi.LmHeadParams,
 }
 
 
@@ -57,7 +60,7 @@ def test_struct_layouts_match_c(tmp_path):
     """sizeof/offsetof from gcc on include/g4attn.h equal the ctypes mirrors."""
     lines = ["#include <stdio.h>", "#include <stddef.h>", f'#include "{HEADER}"', "int main(void) {"]
     for cname, py in STRUCTS.items():
-        lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
+        lines.append(f'printf("{cname} __sizeof__ %zu\\n", sizeof({cname}));')
         for fname, _ in py._fields_:
             lines.append(f'printf("{cname} {fname} %zu\\n", offsetof({cname}, {fname}));')
     lines.append("return 0; }")
@@ -71,7 +74,7 @@ def test_struct_layouts_match_c(tmp_path):
         cname, field, val = line.split()
         got[(cname, field)] = int(val)
     for cname, py in STRUCTS.items():
-        assert got[(cname, "size")] == C.sizeof(py), cname
+        assert got[(cname, "__sizeof__")] == C.sizeof(py), cname
         for fname, _ in py._fields_:
             assert got[(cname, fname)] == getattr(py, fname).offset, (cname, fname)
 
@@ -115,6 +118,26 @@ def test_argument_errors_rejected_on_host():
     assert st == abi.G4_EINVAL and "rope_freqs" in msg
     st, msg = _err(lambda L: L.g4_attn_decode_many_run(C.byref(abi.DecodePlan()), None))
     assert st == abi.G4_EINVAL and "not prepared" in msg
+
+
+def test_lm_head_argument_errors_rejected_on_host():
+    n = C.c_size_t(0)
+    lib = abi.load()
+    assert lib.g4_lm_head_workspace_size(abi.LmHeadParams(262144, 1536, 30.0), C.byref(n)) == abi.G4_OK
+    assert 0 < n.value <= 2048 * 8
+    st, msg = _err(lambda L: L.g4_lm_head_workspace_size(abi.LmHeadParams(1000, 300, 30.0), C.byref(n)))
+    assert st == abi.G4_EINVAL and "hidden 300" in msg
+    st, msg = _err(lambda L: L.g4_lm_head_workspace_size(abi.LmHeadParams(0, 1536, 30.0), C.byref(n)))
+    assert st == abi.G4_EINVAL and "vocab 0" in msg
+    p = abi.LmHeadParams(1000, 1536, 30.0)
+    st, msg = _err(lambda L: L.g4_lm_head_argmax(None, 16, None, 16, 16, 4096, p, None))
+    assert st == abi.G4_EINVAL and "NULL" in msg
+    st, msg = _err(lambda L: L.g4_lm_head_argmax(8, 16, None, 16, 16, 4096, p, None))
+    assert st == abi.G4_EINVAL and "aligned" in msg
+    st, msg = _err(lambda L: L.g4_lm_head_argmax(16, 16, None, 16, 16, 8, p, None))
+    assert st == abi.G4_ENOSPC and "workspace" in msg
+    st, msg = _err(lambda L: L.g4_lm_head_argmax(16, 16, None, 16, 16, 4096, abi.LmHeadParams(1000, 1536, -1.0), None))
+    assert st == abi.G4_EINVAL and "softcap" in msg
     n = C.c_size_t(0)
     st, _ = _err(lambda L: L.g4_attn_decode_workspace_size(8, 1, 256, 131072, C.byref(n)))
     assert st == abi.G4_OK and n.value > 131072 // 128 * 8 * 256 * 4

@@ -342,6 +342,75 @@ def test_argmax_tie_rule(oracle):
         assert oracle.argmax(y) == int(np.argmax(y))
 
 
+def test_argmax_tournament_known_answer(oracle):
+    """Hand-traced through argmax.wgsl's tree: residues 1 and 4 hold the same maximum. At stride 4
+    slot 0 takes residue 4's pair (strictly greater than its own 0); at stride 1 slot 0 (holding 4) meets
+    slot 1 (holding residue 1): equal, so slot 0 keeps index 4."""
+    x = np.zeros(256, np.float32)
+    x[[1, 4]] = 3.0
+    assert oracle.argmax(x) == 4
+    x[[1, 4]] = 0.0
+    x[[6, 9]] = 3.0  # bit-reversed: 6 -> 96, 9 -> 144: 6 wins
+    assert oracle.argmax(x) == 6
+
+
+def test_argmax_closed_form_rule(oracle):
+    """The oracle against the loop-free statement of the rule (closed_form.argmax_rule) on inputs with
+    many exact ties, NaN and values at or below the -1e30 start."""
+    rng = np.random.default_rng(7)
+    for trial in range(200):
+        n = int(rng.integers(1, 3000))
+        x = rng.integers(-3, 4, size=n).astype(np.float32)  # a handful of values: ties everywhere
+        if trial % 3 == 0:
+            x[rng.integers(0, n, size=max(1, n // 10))] = np.nan
+        if trial % 5 == 0:
+            x[rng.integers(0, n, size=max(1, n // 3))] = np.float32(-1e30)
+        assert oracle.argmax(x) == cf.argmax_rule(x), trial
+    assert oracle.argmax(np.array([np.nan, -1e30, -2e30], np.float32)) == 0
+    assert cf.argmax_rule(np.array([np.nan, -1e30], np.float32)) == 0
+
+
+def _f16_bits(a):
+    return np.asarray(a, dtype=np.float16).view(np.uint16)
+
+
+@pytest.mark.parametrize("M,N", [(37, 1536), (5, 300), (64, 2048), (3, 17)])
+def test_matmul_quant_closed_form(oracle, M, N):
+    rng = np.random.default_rng(M * 1000 + N)
+    w = rng.standard_normal((M, N)).astype(np.float16)
+    x = rng.standard_normal(N).astype(np.float32)
+    got = oracle.matmul_quant(x, _f16_bits(w), M, N)
+    want = cf.matvec(w.astype(np.float32), x)
+    np.testing.assert_allclose(got, want, rtol=0, atol=2e-4 * np.sqrt(N / 256))
+
+
+def test_matmul_quant_integers_exact(oracle):
+    """Small integers: every partial sum is exact, so any order gives the numpy integer product; a dropped
+    term, a wrong index or a transposed operand shows up as a difference."""
+    rng = np.random.default_rng(3)
+    M, N = 50, 1000
+    w = rng.integers(-8, 9, size=(M, N))
+    x = rng.integers(-8, 9, size=N)
+    got = oracle.matmul_quant(x.astype(np.float32), _f16_bits(w.astype(np.float16)), M, N)
+    assert np.array_equal(got, (w @ x).astype(np.float32))
+
+
+def test_matmul_quant_summation_order(oracle):
+    """matmul_quant.wgsl's order: invocation 0 adds k = 0 then k = 256 (2^27 - 2^27 = 0 exactly), and the
+    tree then adds invocation 128's 1.0: the result is 1. Summing k = 0, 1, 2, ... instead rounds
+    2^27 + 1 to 2^27 and gives 0."""
+    N = 512
+    w = np.zeros((1, N), np.float16)
+    w[0, [0, 128, 256]] = 1.0
+    x = np.zeros(N, np.float32)
+    x[0], x[128], x[256] = 2.0 ** 27, 1.0, -(2.0 ** 27)
+    assert oracle.matmul_quant(x, _f16_bits(w), 1, N)[0] == 1.0
+    seq = np.float32(0)
+    for k in range(N):
+        seq = np.float32(seq + np.float32(w[0, k]) * x[k])
+    assert seq == 0.0
+
+
 def test_softcap_closed_form(oracle):
     x = (synth.normal(4, 4096) * 40).astype(np.float32)
     np.testing.assert_allclose(oracle.logit_softcap(x, 30.0), cf.softcap(x, 30.0), atol=2e-5)
