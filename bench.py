@@ -18,6 +18,11 @@ inputs resident in HBM:
             launch); f16 Q/K/V (unit-RMS rows). Reported in TFLOP/s
             (algorithmic 4*HD*NQH per attended key per token) against the
             2.5 PFLOP/s dense f16 MFMA peak.
+  lmhead    the sampling head after the last layer (src/engine.ts:2223-2255)
+            at Gemma-4-E2B's shape: lm head over the f16 tied embedding
+            [262144][1536], logit softcap 30, greedy argmax, as one streaming
+            pass plus a one-workgroup pick. Reported in GB/s of algorithmic
+            bytes (weight + hidden + logits written).
 
 A step is one launch of the fused attention step over every entry (per entry:
 q/k RMSNorm + RoPE, weightless v-norm, f16 store of the new K/V row, split-K
@@ -239,7 +244,10 @@ def run_gpu(spec, args):
 def read_traffic(workload: str):
     """HBM bytes per k_attn_step launch from the committed counter summary of this workload
     (FETCH_SIZE and WRITE_SIZE passes of rocprofv3 --pmc, scaled by a copy kernel's reading)."""
-    f = ROOT / "profiles" / f"k_attn_step_{workload}_traffic.txt"
+    return read_traffic_file(ROOT / "profiles" / f"k_attn_step_{workload}_traffic.txt")
+
+
+def read_traffic_file(f: Path):
     if not f.exists():
         return None
     for line in f.read_text().splitlines():
@@ -416,13 +424,102 @@ def main_prefill(args):
     print(json.dumps(line), flush=True)
 
 
+# ---- sampling head (lm head GEMV + softcap + argmax) ------------------------------------
+
+LM_VOCAB, LM_HIDDEN, LM_CAP = 262144, 1536, 30.0
+
+
+def lm_bytes() -> int:
+    return LM_VOCAB * LM_HIDDEN * 2 + LM_HIDDEN * 4 + LM_VOCAB * 4
+
+
+def main_lmhead(args):
+    import numpy as np
+    import torch
+
+    from g4attn import abi, ops
+
+    abi.load()
+    abi.call("g4_set_device", 0)
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(BASE_SEED + 60)
+    w = (torch.randn(LM_VOCAB * LM_HIDDEN, generator=g, device=dev) * 0.05).to(torch.float16).view(torch.int16)
+    x = torch.randn(LM_HIDDEN, generator=g, device=dev)
+    logits = torch.empty(LM_VOCAB, device=dev)
+    res = torch.zeros(1, dtype=torch.int32, device=dev)
+    ws = torch.empty(ops.lm_head_workspace_bytes(LM_VOCAB, LM_HIDDEN, LM_CAP), dtype=torch.uint8, device=dev)
+
+    def step():
+        ops.lm_head_argmax(x, w, logits, res, ws, LM_VOCAB, LM_HIDDEN, LM_CAP)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    stream = torch.cuda.current_stream()
+    for a_, b_ in evs:
+        a_.record(stream)
+        b_.record(stream)
+    torch.cuda.synchronize()
+    for a_, b_ in evs:
+        ops.lm_head_argmax_timed(x, w, logits, res, ws, LM_VOCAB, LM_HIDDEN, LM_CAP, a_, b_)
+    torch.cuda.synchronize()
+    k_ms = sum(a_.elapsed_time(b_) for a_, b_ in evs) / len(evs)
+    nbytes = lm_bytes()
+    ms_per_step = wall / args.steps * 1e3
+    achieved = nbytes / (k_ms * 1e-3) / 1e9
+    traffic = read_traffic_file(ROOT / "profiles" / "k_lm_head_lmhead_traffic.txt")
+    log(f"lmhead: {ms_per_step * 1e3:.1f} us/step, k_lm_head avg {k_ms * 1e3:.1f} us, top-1 {int(res.item())}")
+    line = {
+        "metric": "sampling-head GB/s (% HBM roofline): lm head GEMV + softcap + argmax, E2B-shaped, bs1",
+        "value": round(nbytes / (ms_per_step * 1e-3) / 1e9, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5), "us_per_token": round(ms_per_step * 1e3, 2),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16 weight, f32 accumulate",
+        "data": "synthetic (torch seeded normal weights and hidden state), resident in HBM",
+        "config": {"workload": f"lm head {LM_VOCAB} x {LM_HIDDEN} (f16 tied embedding), softcap {LM_CAP}, argmax",
+                   "bytes_per_step": nbytes},
+        "roofline": {"bound": "hbm", "kernel": "k_lm_head", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "avg_us": round(k_ms * 1e3, 2),
+                     "traffic_source": "profiles/k_lm_head_lmhead_traffic.txt" if traffic else None},
+    }
+    if not args.no_cpu_baseline:
+        from oracle import oracle as orc
+
+        threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
+        orc.set_threads(threads)
+        rows = 32768
+        wb = w[: rows * LM_HIDDEN].cpu().numpy().view(np.uint16)
+        xh = x.cpu().numpy()
+        n, t0 = 0, time.perf_counter()
+        while True:  # matmulQuant + logitSoftcap + argmax over a sample of rows, scaled to the vocabulary
+            lg = orc.matmul_quant(xh, wb, rows, LM_HIDDEN)
+            orc.argmax(orc.logit_softcap(lg, LM_CAP))
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= args.cpu_seconds or n >= 10000:
+                break
+        per_token = el / n * (LM_VOCAB / rows)
+        line["cpu_baseline"] = {"value": round(nbytes / per_token / 1e9, 3), "unit": "GB/s", "cores": threads,
+                                "kind": "port", "us_per_token": round(per_token * 1e6, 1),
+                                "sample": f"{n} passes of the oracle's matmulQuant + logitSoftcap + argmax over "
+                                          f"{rows} of the {LM_VOCAB} rows ({el:.1f} s), scaled to the full vocabulary"}
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="stack8k",
-                    choices=["stack8k", "stack32k", "long128k", "ragged64", "layer512", "prefill4k"])
+                    choices=["stack8k", "stack32k", "long128k", "ragged64", "layer512", "prefill4k", "lmhead"])
     ap.add_argument("--sets", type=int, default=0, help="cache sets to rotate (0 = enough to exceed 2x MALL)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -436,6 +533,9 @@ def main():
 
     if args.workload == "prefill4k":
         main_prefill(args)
+        return
+    if args.workload == "lmhead":
+        main_lmhead(args)
         return
     spec = workload_spec(args.workload)
     r = run_gpu(spec, args)

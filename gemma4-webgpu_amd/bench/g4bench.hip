@@ -3,11 +3,15 @@
 // counter collection). Inputs are synthetic: f16 cache rows from a
 // counter-based hash (values in [-2, 2), unit-RMS scale), queries likewise.
 //
-//   g4bench [--workload stack8k|stack32k|long128k|ragged64|layer512|prefill4k|copy] [--iters N] [--sets S]
+//   g4bench [--workload stack8k|stack32k|long128k|ragged64|layer512|prefill4k|lmhead|copy] [--iters N]
+//           [--sets S] [--mode M]
 //
 // `prefill4k` runs the causal MFMA prefill of a 4096-token prompt for one
 // global layer and one 512-window local layer, as 512-token chunks (16
 // entries in one launch; --mode whole: one entry per layer).
+//
+// `lmhead` runs the sampling head (lm head GEMV, softcap, argmax) at Gemma 4
+// E2B's shape (--mode fused|chain).
 //
 // `copy` runs a plain 512 MiB device copy kernel instead: the reference for
 // scaling FETCH_SIZE / WRITE_SIZE counter readings to bytes.
@@ -88,6 +92,64 @@ static int run_copy(int iters) {
     HK(hipEventElapsedTime(&ms, a, b));
     printf("copy: %llu bytes read + written per launch, %.1f GB/s (read+write)\n", (unsigned long long)bytes,
            2.0 * bytes * iters / (ms * 1e-3) / 1e9);
+    return 0;
+}
+
+// Sampling head at Gemma 4 E2B's shape: the f16 tied embedding [262144][1536]
+// as the lm head, softcap 30, greedy argmax. mode `fused` (default): the
+// streaming lm head + pick; `chain`: matmulQuant, logitSoftcap, argmax as
+// the reference dispatches them. Two weight copies are rotated (1.6 GB).
+static int run_lmhead(const std::string& mode, int iters) {
+    const uint32_t V = 262144, H = 1536;
+    const float cap = 30.0f;
+    const uint64_t wbytes = (uint64_t)V * H * 2;
+    const uint64_t bytes = wbytes + (uint64_t)H * 4 + (uint64_t)V * 4;  // weight + hidden + logits
+    printf("workload lmhead: vocab %u hidden %u, %.1f MB/step\n", V, H, bytes / 1e6);
+    printf("bytes_per_step: %llu\n", (unsigned long long)bytes);
+    hipStream_t st;
+    HK(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
+    void *w[2], *x, *logits, *res, *ws;
+    size_t ws_bytes = 0;
+    g4_lm_head_params p = {V, H, cap};
+    CK(g4_lm_head_workspace_size(p, &ws_bytes));
+    for (int i = 0; i < 2; i++) {
+        CK(g4_malloc(&w[i], wbytes));
+        hipLaunchKernelGGL(k_fill_f16, dim3(4096), dim3(256), 0, st, (_Float16*)w[i], wbytes / 2, 77ull + i);
+    }
+    CK(g4_malloc(&x, H * 4));
+    CK(g4_malloc(&logits, V * 4));
+    CK(g4_malloc(&res, 4));
+    CK(g4_malloc(&ws, ws_bytes));
+    hipLaunchKernelGGL(k_fill_f32, dim3(8), dim3(256), 0, st, (float*)x, (uint64_t)H, 5ull);
+    HK(hipGetLastError());
+    const bool fused = mode != "chain";
+    auto step = [&](int i) {
+        const uint16_t* wi = (const uint16_t*)w[i & 1];
+        if (fused) {
+            CK(g4_lm_head_argmax((const float*)x, wi, (float*)logits, (uint32_t*)res, ws, ws_bytes, p, st));
+            return;
+        }
+        CK(g4_matmul_quant_f16((const float*)x, wi, (float*)logits, g4_matmul_params{V, H}, st));
+        CK(g4_logit_softcap((float*)logits, g4_softcap_params{V, cap}, st));
+        CK(g4_argmax((const float*)logits, (uint32_t*)res, V, st));
+    };
+    for (int i = 0; i < 3; i++) step(i);
+    CK(g4_stream_synchronize(st));
+    hipEvent_t a, b;
+    HK(hipEventCreate(&a));
+    HK(hipEventCreate(&b));
+    HK(hipEventRecord(a, st));
+    for (int i = 0; i < iters; i++) step(i);
+    HK(hipEventRecord(b, st));
+    HK(hipEventSynchronize(b));
+    float ms = 0;
+    HK(hipEventElapsedTime(&ms, a, b));
+    const double us = ms * 1e3 / iters;
+    step(0);  // the same weight copy in both modes: their top-1 must agree
+    uint32_t top = 0;
+    CK(g4_download(&top, res, 0, 4, st));
+    printf("lmhead [%s]: %.2f us/step, %.1f GB/s algorithmic (%d iterations), top-1 of weight copy 0: %u\n",
+           fused ? "fused" : "chain", us, bytes / (us * 1e3), iters, top);
     return 0;
 }
 
@@ -194,6 +256,7 @@ int main(int argc, char** argv) {
     CK(g4_set_device(0));
     if (wl == "copy") return run_copy(iters);
     if (wl == "prefill4k") return run_prefill(mode, iters);
+    if (wl == "lmhead") return run_lmhead(mode, iters);
     std::vector<Layer> L = workload(wl);
     const bool uniform_pos = wl.rfind("stack", 0) == 0 || L.size() == 1;
     uint64_t step_bytes = 0, total_rows = 0;
