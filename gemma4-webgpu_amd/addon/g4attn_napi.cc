@@ -331,6 +331,73 @@ napi_value AttnOutput(napi_env env, napi_callback_info info) {
     return undefined(env);
 }
 
+// ---- sampling head: lmHead, logitSoftcap, argmax ---------------------------
+
+napi_value MatmulQuant(napi_env env, napi_callback_info info) {
+    Args a(env, info, 5);  // input, weight, output, params {M, N}, stream
+    void* x = a.ptr(0);
+    void* w = a.ptr(1);
+    void* o = a.ptr(2);
+    g4_matmul_params p;
+    a.params(3, &p);
+    void* s = a.ptr(4);
+    if (!a.ok) return nullptr;
+    CALL(env, g4_matmul_quant_f16((const float*)x, (const uint16_t*)w, (float*)o, p, s));
+    return undefined(env);
+}
+
+napi_value LogitSoftcap(napi_env env, napi_callback_info info) {
+    Args a(env, info, 3);  // logits, params {size, cap}, stream
+    void* l = a.ptr(0);
+    g4_softcap_params p;
+    a.params(1, &p);
+    void* s = a.ptr(2);
+    if (!a.ok) return nullptr;
+    CALL(env, g4_logit_softcap((float*)l, p, s));
+    return undefined(env);
+}
+
+struct ArgmaxUniform {  // argmax.wgsl:3 (var<uniform> size: u32)
+    uint32_t size;
+};
+
+napi_value Argmax(napi_env env, napi_callback_info info) {
+    Args a(env, info, 4);  // logits, result, params {size}, stream
+    void* l = a.ptr(0);
+    void* r = a.ptr(1);
+    ArgmaxUniform p;
+    a.params(2, &p);
+    void* s = a.ptr(3);
+    if (!a.ok) return nullptr;
+    CALL(env, g4_argmax((const float*)l, (uint32_t*)r, p.size, s));
+    return undefined(env);
+}
+
+napi_value LmHeadWorkspaceSize(napi_env env, napi_callback_info info) {
+    Args a(env, info, 3);  // vocab, hidden, cap
+    g4_lm_head_params p = {a.u32(0), a.u32(1), (float)a.f64(2)};
+    if (!a.ok) return nullptr;
+    size_t bytes = 0;
+    CALL(env, g4_lm_head_workspace_size(p, &bytes));
+    return number(env, (double)bytes);
+}
+
+napi_value LmHeadArgmax(napi_env env, napi_callback_info info) {
+    Args a(env, info, 10);  // hidden, weight, logits (or null), result, workspace, workspaceBytes, vocab, hidden, cap, stream
+    void* h = a.ptr(0);
+    void* w = a.ptr(1);
+    void* l = a.ptr(2);
+    void* r = a.ptr(3);
+    void* ws = a.ptr(4);
+    const double ws_bytes = a.f64(5);
+    g4_lm_head_params p = {a.u32(6), a.u32(7), (float)a.f64(8)};
+    void* s = a.ptr(9);
+    if (!a.ok) return nullptr;
+    CALL(env, g4_lm_head_argmax((const float*)h, (const uint16_t*)w, (float*)l, (uint32_t*)r, ws, (size_t)ws_bytes, p,
+                                s));
+    return undefined(env);
+}
+
 // ---- RoPE tables and the one-launch step -----------------------------------
 
 napi_value RopeInvFreq(napi_env env, napi_callback_info info) {
@@ -573,6 +640,11 @@ napi_value Init(napi_env env, napi_value exports) {
         {"attnScore", AttnScore},
         {"softmax", Softmax},
         {"attnOutput", AttnOutput},
+        {"matmulQuant", MatmulQuant},
+        {"logitSoftcap", LogitSoftcap},
+        {"argmax", Argmax},
+        {"lmHeadWorkspaceSize", LmHeadWorkspaceSize},
+        {"lmHeadArgmax", LmHeadArgmax},
         {"ropeInvFreq", RopeInvFreq},
         {"ropeInvFreqHost", RopeInvFreqHost},
         {"attnStepWorkspaceSize", AttnStepWorkspaceSize},
@@ -595,6 +667,9 @@ napi_value Init(napi_env env, napi_value exports) {
         {"sizeofAttnScoreParams", sizeof(g4_attn_score_params)},
         {"sizeofSoftmaxParams", sizeof(g4_softmax_params)},
         {"sizeofAttnOutputParams", sizeof(g4_attn_output_params)},
+        {"sizeofMatmulParams", sizeof(g4_matmul_params)},
+        {"sizeofSoftcapParams", sizeof(g4_softcap_params)},
+        {"sizeofArgmaxParams", sizeof(ArgmaxUniform)},
     };
     for (auto& s : sizes) NAPI_OK(env, napi_set_named_property(env, exports, s.name, number(env, (double)s.size)));
     return exports;

@@ -24,28 +24,39 @@ export type AttnKernelName =
   | 'softmax'
   | 'attnOutput';
 
-export type FusedKernelName = 'attnStep';
+// The sampling head after the last layer (src/engine.ts:2223-2255).
+export type SampleKernelName = 'matmulQuant' | 'logitSoftcap' | 'argmax';
+
+export type KernelName = AttnKernelName | SampleKernelName;
+
+export type FusedKernelName = 'attnStep' | 'lmHeadArgmax';
 
 export type UniformValue = { u: number } | { f: number };
 
 // Storage bindings of each kernel in @binding order (the uniform is separate).
-export const BINDINGS: Record<AttnKernelName, string[]> = {
+export const BINDINGS: Record<KernelName, string[]> = {
   fusedPerHeadNormRope: ['data', 'weight', 'rope_freqs'],  // fused_per_head_norm_rope.wgsl:14-17
   perHeadRmsNormNoWeight: ['data'],                          // per_head_rms_norm_no_weight.wgsl:9
   kvCacheStore: ['k_in', 'v_in', 'k_cache', 'v_cache'],     // kv_cache_store.wgsl:2-5
   attnScore: ['q', 'k_cache', 'scores'],                     // attn_score.wgsl:10-12
   softmax: ['scores'],                                       // softmax.wgsl:2
   attnOutput: ['probs', 'v_cache', 'output'],                // attn_output.wgsl:2-4
+  matmulQuant: ['input', 'weight', 'output'],                // matmul_quant.wgsl:13-15 (f16 weight)
+  logitSoftcap: ['logits'],                                  // logit_softcap.wgsl:6
+  argmax: ['logits', 'result'],                              // argmax.wgsl:1-2
 };
 
 // Params byte sizes (struct Params of each shader).
-export const PARAMS_BYTES: Record<AttnKernelName, number> = {
+export const PARAMS_BYTES: Record<KernelName, number> = {
   fusedPerHeadNormRope: 24,
   perHeadRmsNormNoWeight: 16,
   kvCacheStore: 16,
   attnScore: 24,
   softmax: 8,
   attnOutput: 16,
+  matmulQuant: 8,
+  logitSoftcap: 8,
+  argmax: 4,
 };
 
 // Profiler pass labels of the engine (src/engine.ts:2056-2094), plus the fused step.
@@ -57,6 +68,10 @@ export const PASS_LABELS: Record<string, string> = {
   softmax: 'attn.softmax',
   attnOutput: 'attn.attnOutput',
   attnStep: 'attn.decodeFused',
+  matmulQuant: 'lmHead',
+  logitSoftcap: 'logitSoftcap',
+  argmax: 'sample.argmax',
+  lmHeadArgmax: 'sample.lmHeadArgmax',
 };
 
 // The engine's makeUniformMixed: 4-byte fields, at least 16 bytes.
@@ -115,6 +130,13 @@ export interface StepEntry {
   eps?: number;
 }
 
+// The fused sampling head: lm head over an f16 [vocab][hidden] weight, softcap (0 = none), argmax.
+export interface LmHeadShape {
+  vocab: number;
+  hidden: number;
+  cap: number;
+}
+
 export interface StepShape {
   numQHeads: number;
   numKvHeads: number;
@@ -140,6 +162,12 @@ export interface Addon {
   attnScore(q: bigint, kc: bigint, sc: bigint, p: Uint8Array, s: bigint): void;
   softmax(sc: bigint, p: Uint8Array, s: bigint): void;
   attnOutput(pr: bigint, vc: bigint, o: bigint, p: Uint8Array, s: bigint): void;
+  matmulQuant(x: bigint, w: bigint, o: bigint, p: Uint8Array, s: bigint): void;
+  logitSoftcap(l: bigint, p: Uint8Array, s: bigint): void;
+  argmax(l: bigint, r: bigint, p: Uint8Array, s: bigint): void;
+  lmHeadWorkspaceSize(vocab: number, hidden: number, cap: number): number;
+  lmHeadArgmax(h: bigint, w: bigint, l: bigint | null, r: bigint, ws: bigint, wsBytes: number, vocab: number,
+    hidden: number, cap: number, s: bigint): void;
   ropeInvFreq(theta: number, hd: number, div: number, rf: any, out: bigint, s: bigint): void;
   ropeInvFreqHost(theta: number, hd: number, div: number, rf: Uint16Array | null, out: Float32Array): void;
   attnStepWorkspaceSize(n: number, nqh: number, nkh: number, hd: number): number;
@@ -156,13 +184,16 @@ export function loadAddon(path?: string): Addon {
 
 // The kernel table: SHADERS name -> launch with (bindings in @binding order, Params bytes).
 type Launch = (g4: Addon, b: bigint[], p: Uint8Array, s: bigint) => void;
-export const KERNELS: Record<AttnKernelName, Launch> = {
+export const KERNELS: Record<KernelName, Launch> = {
   fusedPerHeadNormRope: function (g4, b, p, s) { g4.fusedPerHeadNormRope(b[0], b[1], b[2], p, s); },
   perHeadRmsNormNoWeight: function (g4, b, p, s) { g4.perHeadRmsNormNoWeight(b[0], p, s); },
   kvCacheStore: function (g4, b, p, s) { g4.kvCacheStore(b[0], b[1], b[2], b[3], p, s); },
   attnScore: function (g4, b, p, s) { g4.attnScore(b[0], b[1], b[2], p, s); },
   softmax: function (g4, b, p, s) { g4.softmax(b[0], p, s); },
   attnOutput: function (g4, b, p, s) { g4.attnOutput(b[0], b[1], b[2], p, s); },
+  matmulQuant: function (g4, b, p, s) { g4.matmulQuant(b[0], b[1], b[2], p, s); },
+  logitSoftcap: function (g4, b, p, s) { g4.logitSoftcap(b[0], p, s); },
+  argmax: function (g4, b, p, s) { g4.argmax(b[0], b[1], p, s); },
 };
 
 export class HipAttention {
@@ -205,9 +236,9 @@ export class HipAttention {
   }
 
   // setPipeline(name) + setBindGroup(bindings, params) + dispatchWorkgroups, as one enqueue.
-  dispatch(name: AttnKernelName, bindings: DeviceBuffer[], params: Uniform): void {
+  dispatch(name: KernelName, bindings: DeviceBuffer[], params: Uniform): void {
     const launch = KERNELS[name];
-    if (!launch) throw new Error(`unknown attention kernel ${name}`);
+    if (!launch) throw new Error(`unknown kernel ${name}`);
     const want = BINDINGS[name];
     if (bindings.length !== want.length) {
       throw new Error(`${name}: ${bindings.length} bindings, expected ${want.length} (${want.join(', ')})`);
@@ -255,6 +286,20 @@ export class HipAttention {
 
   attnStep(entries: StepEntry[], shape: StepShape, workspace: DeviceBuffer): void {
     this.attnStepRun(this.attnStepPrepare(entries, shape, workspace));
+  }
+
+  lmHeadWorkspaceSize(shape: LmHeadShape): number {
+    return this.g4.lmHeadWorkspaceSize(shape.vocab, shape.hidden, shape.cap);
+  }
+
+  // lmHead -> logitSoftcap -> sample.argmax in one streaming pass: result[0] (u32) = the top-1 index;
+  // logits (optional) = the softcapped logits, bit-identical to the three dispatches.
+  lmHeadArgmax(hidden: DeviceBuffer, weight: DeviceBuffer, logits: DeviceBuffer | null, result: DeviceBuffer,
+    workspace: DeviceBuffer, shape: LmHeadShape): void {
+    if (weight.size < shape.vocab * shape.hidden * 2) throw new RangeError('lmHeadArgmax: weight too small');
+    if (logits && logits.size < shape.vocab * 4) throw new RangeError('lmHeadArgmax: logits too small');
+    this.g4.lmHeadArgmax(hidden.ptr, weight.ptr, logits ? logits.ptr : null, result.ptr, workspace.ptr,
+      workspace.size, shape.vocab, shape.hidden, shape.cap, this.stream);
   }
 
   synchronize(): void {

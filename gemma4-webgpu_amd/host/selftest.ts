@@ -4,9 +4,12 @@
 //   node host/run.js layer <dir>    one attention layer from <dir>/case.json + case.bin, run twice on the
 //                                   GPU: the engine's six dispatches in order (src/engine.ts:2056-2094),
 //                                   and the fused attnStep; results go to <dir>/out.bin for the oracle check.
+//   node host/run.js head <dir>     the sampling head from <dir>/case.json + case.bin: the engine's lmHead,
+//                                   logitSoftcap and sample.argmax dispatches (src/engine.ts:2223-2255),
+//                                   then the fused lmHeadArgmax; results go to <dir>/out.bin.
 
 import { BINDINGS, KERNELS, PARAMS_BYTES, PASS_LABELS, Uniform, HipAttention, loadAddon } from './attention';
-import type { AttnKernelName, DeviceBuffer } from './attention';
+import type { DeviceBuffer, KernelName } from './attention';
 
 declare const require: any;
 declare const process: any;
@@ -28,11 +31,12 @@ export function cpuChecks(): string[] {
   const sizes: Record<string, string> = {
     fusedPerHeadNormRope: 'sizeofNormRopeParams', perHeadRmsNormNoWeight: 'sizeofNormParams',
     kvCacheStore: 'sizeofKvStoreParams', attnScore: 'sizeofAttnScoreParams', softmax: 'sizeofSoftmaxParams',
-    attnOutput: 'sizeofAttnOutputParams',
+    attnOutput: 'sizeofAttnOutputParams', matmulQuant: 'sizeofMatmulParams', logitSoftcap: 'sizeofSoftcapParams',
+    argmax: 'sizeofArgmaxParams',
   };
   for (const n of names) {
     const want = g4[sizes[n]];
-    const have = PARAMS_BYTES[n as AttnKernelName];
+    const have = PARAMS_BYTES[n as KernelName];
     if (have !== want) fail(`${n}: params ${have} B, C struct ${want} B`);
   }
   done.push('params sizes');
@@ -129,11 +133,57 @@ function layer(dir: string): string[] {
   return ['engine order: 7 dispatches', 'attnStep: 1 entry', 'results written'];
 }
 
+interface HeadSpec {
+  vocab: number; hidden: number; cap: number; arrays: Record<string, number[]>;
+}
+
+function head(dir: string): string[] {
+  const spec = JSON.parse(fs.readFileSync(path.join(dir, 'case.json'), 'utf8')) as HeadSpec;
+  const bin: Uint8Array = fs.readFileSync(path.join(dir, 'case.bin'));
+  const att = new HipAttention(loadAddon(), 0);
+  const V = spec.vocab, H = spec.hidden;
+  const bufs: DeviceBuffer[] = [];
+  function upload(name: string): DeviceBuffer {
+    const r = spec.arrays[name];
+    const b = att.createBuffer(r[1]);
+    att.writeBuffer(b, 0, bin.subarray(r[0], r[0] + r[1]));
+    bufs.push(b);
+    return b;
+  }
+  function alloc(bytes: number): DeviceBuffer {
+    const b = att.createBuffer(bytes);
+    bufs.push(b);
+    return b;
+  }
+  const x = upload('x'), w = upload('w');
+  // (1) the engine's three passes, uniforms as createUniformBuffers builds them
+  const logits1 = alloc(V * 4), res1 = alloc(16);
+  att.dispatch('matmulQuant', [x, w, logits1], new Uniform([{ u: V }, { u: H }]));
+  if (spec.cap > 0) att.dispatch('logitSoftcap', [logits1], new Uniform([{ u: V }, { f: spec.cap }]));
+  att.dispatch('argmax', [logits1, res1], new Uniform([{ u: V }]));
+  // (2) the fused pass
+  const logits2 = alloc(V * 4), res2 = alloc(16);
+  const shape = { vocab: V, hidden: H, cap: spec.cap };
+  const ws = alloc(att.lmHeadWorkspaceSize(shape));
+  att.lmHeadArgmax(x, w, logits2, res2, ws, shape);
+  // results: logits1, logits2 (f32), then result1, result2 (u32)
+  const res = new Uint8Array(2 * V * 4 + 8);
+  att.readBuffer(logits1, 0, res.subarray(0, V * 4));
+  att.readBuffer(logits2, 0, res.subarray(V * 4, 2 * V * 4));
+  att.readBuffer(res1, 0, res.subarray(2 * V * 4, 2 * V * 4 + 4));
+  att.readBuffer(res2, 0, res.subarray(2 * V * 4 + 4, 2 * V * 4 + 8));
+  fs.writeFileSync(path.join(dir, 'out.bin'), res);
+  for (const b of bufs) att.destroyBuffer(b);
+  att.dispose();
+  return ['engine order: 3 dispatches', 'lmHeadArgmax: 1 call', 'results written'];
+}
+
 export function main(argv: string[]): void {
   const mode = argv[0];
   let done: string[];
   if (mode === 'cpu') done = cpuChecks();
   else if (mode === 'layer') done = layer(argv[1]);
-  else fail(`usage: run.js cpu | layer <dir>`);
+  else if (mode === 'head') done = head(argv[1]);
+  else fail(`usage: run.js cpu | layer <dir> | head <dir>`);
   process.stdout.write(JSON.stringify({ ok: true, checks: done }) + '\n');
 }

@@ -2,7 +2,9 @@
 dispatches in order, with uniforms built and patched as src/engine.ts does, and the fused attnStep,
 both over the N-API addon. Checked against the oracle: the six-kernel path bit-identical (those
 kernels evaluate the reference's expressions), attnStep within max-abs 2e-3, and the stored f16
-K/V rows bit-identical on both paths.
+K/V rows bit-identical on both paths. The sampling head likewise (node host/run.js head): the
+engine's lmHead, logitSoftcap and sample.argmax dispatches and the fused lmHeadArgmax, logits
+bit-identical and top-1 equal to the oracle's.
 """
 import json
 import shutil
@@ -77,3 +79,31 @@ def test_layer_through_ts_host(tmp_path, seq, window, theta, div):
     assert np.isfinite(out_step).all() and max_abs(out_step, want) <= 2e-3
     for got, exp in zip(rows, (kbits, vbits, kbits, vbits)):
         np.testing.assert_array_equal(got, exp)
+
+
+@pytest.mark.skipif(NODE is None, reason="node is not installed")
+@pytest.mark.parametrize("vocab,hidden,cap", [(5000, 1536, 30.0), (777, 2048, 0.0)])
+def test_sampling_head_through_ts_host(tmp_path, vocab, hidden, cap):
+    announce(f"TS host sampling head vocab={vocab} hidden={hidden} cap={cap}")
+    rng = np.random.default_rng(vocab)
+    x = rng.standard_normal(hidden, dtype=np.float32)
+    w = (rng.standard_normal((vocab, hidden), dtype=np.float32) * 0.05).astype(np.float16).view(np.uint16)
+    w[[10, 266]] = (np.sign(x) * 0.2).astype(np.float16).view(np.uint16)  # a tie at the top
+    blob = x.tobytes() + w.tobytes()
+    (tmp_path / "case.bin").write_bytes(blob)
+    (tmp_path / "case.json").write_text(json.dumps(dict(vocab=vocab, hidden=hidden, cap=cap, arrays=dict(
+        x=[0, x.nbytes], w=[x.nbytes, w.nbytes]))))
+    r = subprocess.run([NODE, str(RUN), "head", str(tmp_path)], cwd=ROOT, capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 0, r.stderr
+    raw = (tmp_path / "out.bin").read_bytes()
+    n = vocab * 4
+    want = orc.matmul_quant(x, w, vocab, hidden)
+    if cap > 0:
+        want = orc.logit_softcap(want, cap)
+    top = orc.argmax(want)
+    assert top in (10, 266)
+    for i in range(2):
+        np.testing.assert_array_equal(np.frombuffer(raw[i * n:(i + 1) * n], np.uint32), want.view(np.uint32))
+    res = np.frombuffer(raw[2 * n:2 * n + 8], np.uint32)
+    assert res[0] == top and res[1] == top
