@@ -618,6 +618,127 @@ napi_value AttnStepRun(napi_env env, napi_callback_info info) {
     return undefined(env);
 }
 
+// ---- causal prefill ---------------------------------------------------------
+
+// One g4_prefill_entry from {q, kCache, vCache, out (BigInt pointers), nTokens, start, slidingWindow, scale}.
+bool prefill_entry(Args& a, napi_value obj, size_t idx, g4_prefill_entry* e) {
+    napi_env env = a.env;
+    memset(e, 0, sizeof *e);
+    const std::string at = "prefill entry " + std::to_string(idx) + ": ";
+    struct {
+        const char* key;
+        const void** dst;
+    } ptrs[] = {{"q", (const void**)&e->q}, {"kCache", (const void**)&e->k_cache},
+                {"vCache", (const void**)&e->v_cache}, {"out", (const void**)&e->out}};
+    for (auto& p : ptrs) {
+        napi_value v;
+        uint64_t x = 0;
+        bool lossless = false;
+        if (!get_prop(env, obj, p.key, &v) || napi_get_value_bigint_uint64(env, v, &x, &lossless) != napi_ok ||
+            !lossless) {
+            a.fail(at + p.key + " must be a BigInt pointer");
+            return false;
+        }
+        *p.dst = reinterpret_cast<const void*>(static_cast<uintptr_t>(x));
+    }
+    struct {
+        const char* key;
+        uint32_t* dst;
+        bool required;
+    } u32s[] = {{"nTokens", &e->n_tokens, true}, {"start", &e->start, true}, {"slidingWindow", &e->sliding_window, false}};
+    for (auto& f : u32s) {
+        napi_value v;
+        if (!get_prop(env, obj, f.key, &v)) {
+            if (f.required) {
+                a.fail(at + "missing " + f.key);
+                return false;
+            }
+            continue;
+        }
+        if (napi_get_value_uint32(env, v, f.dst) != napi_ok) {
+            a.fail(at + f.key + " must be a number");
+            return false;
+        }
+    }
+    e->scale = 1.0f;
+    napi_value v;
+    if (get_prop(env, obj, "scale", &v)) {
+        double x = 0;
+        if (napi_get_value_double(env, v, &x) != napi_ok) {
+            a.fail(at + "scale must be a number");
+            return false;
+        }
+        e->scale = (float)x;
+    }
+    return true;
+}
+
+bool prefill_entries(Args& a, size_t arg, std::vector<g4_prefill_entry>* ents) {
+    bool is_array = false;
+    napi_is_array(a.env, a.v[arg], &is_array);
+    if (!is_array) {
+        a.fail("prefill: entries must be an array");
+        return false;
+    }
+    uint32_t n = 0;
+    napi_get_array_length(a.env, a.v[arg], &n);
+    ents->resize(n);
+    for (uint32_t i = 0; i < n; i++) {
+        napi_value obj;
+        napi_get_element(a.env, a.v[arg], i, &obj);
+        if (!prefill_entry(a, obj, i, &(*ents)[i])) return false;
+    }
+    return true;
+}
+
+// attnPrefillWorkspaceSize(entries[], nqh, nkh, hd) -> bytes
+napi_value AttnPrefillWorkspaceSize(napi_env env, napi_callback_info info) {
+    Args a(env, info, 4);
+    std::vector<g4_prefill_entry> ents;
+    if (!a.ok || !prefill_entries(a, 0, &ents)) return nullptr;
+    const uint32_t nqh = a.u32(1), nkh = a.u32(2), hd = a.u32(3);
+    if (!a.ok) return nullptr;
+    size_t bytes = 0;
+    CALL(env, g4_attn_prefill_workspace_size(ents.data(), (uint32_t)ents.size(), nqh, nkh, hd, &bytes));
+    return number(env, (double)bytes);
+}
+
+// attnPrefillPrepare(entries[], nqh, nkh, hd, workspace, workspaceBytes, stream) -> plan (Uint8Array)
+napi_value AttnPrefillPrepare(napi_env env, napi_callback_info info) {
+    Args a(env, info, 7);
+    std::vector<g4_prefill_entry> ents;
+    if (!a.ok || !prefill_entries(a, 0, &ents)) return nullptr;
+    const uint32_t nqh = a.u32(1), nkh = a.u32(2), hd = a.u32(3);
+    void* ws = a.ptr(4);
+    const double ws_bytes = a.f64(5);
+    void* s = a.ptr(6);
+    if (!a.ok) return nullptr;
+    napi_value ab, plan;
+    void* pdata = nullptr;
+    NAPI_OK(env, napi_create_arraybuffer(env, sizeof(g4_decode_plan), &pdata, &ab));
+    CALL(env, g4_attn_prefill_prepare(ents.data(), (uint32_t)ents.size(), nqh, nkh, hd, ws, (size_t)ws_bytes,
+                                      static_cast<g4_decode_plan*>(pdata), s));
+    NAPI_OK(env, napi_create_typedarray(env, napi_uint8_array, sizeof(g4_decode_plan), ab, 0, &plan));
+    return plan;
+}
+
+napi_value AttnPrefillRun(napi_env env, napi_callback_info info) {
+    Args a(env, info, 2);  // plan, stream
+    void* d = nullptr;
+    size_t n = 0;
+    a.bytes(0, &d, &n);
+    void* s = a.ptr(1);
+    if (!a.ok) return nullptr;
+    if (n != sizeof(g4_decode_plan)) {
+        napi_throw_type_error(env, nullptr, "attnPrefillRun: not a plan from attnPrefillPrepare");
+        return nullptr;
+    }
+    g4_decode_plan plan;
+    memcpy(&plan, d, sizeof plan);
+    CALL(env, g4_attn_prefill_run(&plan, s));
+    return undefined(env);
+}
+
 napi_value Init(napi_env env, napi_value exports) {
     struct {
         const char* name;
@@ -650,6 +771,9 @@ napi_value Init(napi_env env, napi_value exports) {
         {"attnStepWorkspaceSize", AttnStepWorkspaceSize},
         {"attnStepPrepare", AttnStepPrepare},
         {"attnStepRun", AttnStepRun},
+        {"attnPrefillWorkspaceSize", AttnPrefillWorkspaceSize},
+        {"attnPrefillPrepare", AttnPrefillPrepare},
+        {"attnPrefillRun", AttnPrefillRun},
     };
     for (auto& f : fns) {
         napi_value fn;

@@ -29,7 +29,7 @@ export type SampleKernelName = 'matmulQuant' | 'logitSoftcap' | 'argmax';
 
 export type KernelName = AttnKernelName | SampleKernelName;
 
-export type FusedKernelName = 'attnStep' | 'lmHeadArgmax';
+export type FusedKernelName = 'attnStep' | 'attnPrefill' | 'lmHeadArgmax';
 
 export type UniformValue = { u: number } | { f: number };
 
@@ -68,6 +68,7 @@ export const PASS_LABELS: Record<string, string> = {
   softmax: 'attn.softmax',
   attnOutput: 'attn.attnOutput',
   attnStep: 'attn.decodeFused',
+  attnPrefill: 'attn.prefill',
   matmulQuant: 'lmHead',
   logitSoftcap: 'logitSoftcap',
   argmax: 'sample.argmax',
@@ -130,6 +131,20 @@ export interface StepEntry {
   eps?: number;
 }
 
+// One prefill entry: a chunk of tokens of one layer (or sequence). Token t sits at position start + t and
+// attends cache rows [lo, start + t] (lo = start + t + 1 - slidingWindow on local layers, else 0), the rows
+// the decode step at that position reads. The caches already hold the chunk's own K/V rows.
+export interface PrefillEntry {
+  q: DeviceBuffer;            // post norm + RoPE queries, f16 [nTokens][NQH][HD]
+  kCache: DeviceBuffer;       // f16 [rows >= start + nTokens][NKH][HD]
+  vCache: DeviceBuffer;
+  out: DeviceBuffer;          // f32 [nTokens][NQH][HD]
+  nTokens: number;
+  start: number;
+  slidingWindow?: number;     // 0 = full
+  scale?: number;
+}
+
 // The fused sampling head: lm head over an f16 [vocab][hidden] weight, softcap (0 = none), argmax.
 export interface LmHeadShape {
   vocab: number;
@@ -174,6 +189,10 @@ export interface Addon {
   attnStepPrepare(entries: any[], nqh: number, nkh: number, hd: number, ws: bigint, wsBytes: number,
     s: bigint): Uint8Array;
   attnStepRun(plan: Uint8Array, s: bigint): void;
+  attnPrefillWorkspaceSize(entries: any[], nqh: number, nkh: number, hd: number): number;
+  attnPrefillPrepare(entries: any[], nqh: number, nkh: number, hd: number, ws: bigint, wsBytes: number,
+    s: bigint): Uint8Array;
+  attnPrefillRun(plan: Uint8Array, s: bigint): void;
   [key: string]: any;
 }
 
@@ -286,6 +305,35 @@ export class HipAttention {
 
   attnStep(entries: StepEntry[], shape: StepShape, workspace: DeviceBuffer): void {
     this.attnStepRun(this.attnStepPrepare(entries, shape, workspace));
+  }
+
+  private static prefillFlat(entries: PrefillEntry[]): any[] {
+    return entries.map(function (e) {
+      return {
+        q: e.q.ptr, kCache: e.kCache.ptr, vCache: e.vCache.ptr, out: e.out.ptr, nTokens: e.nTokens,
+        start: e.start, slidingWindow: e.slidingWindow || 0, scale: e.scale === undefined ? 1.0 : e.scale,
+      };
+    });
+  }
+
+  attnPrefillWorkspaceSize(entries: PrefillEntry[], shape: StepShape): number {
+    return this.g4.attnPrefillWorkspaceSize(HipAttention.prefillFlat(entries), shape.numQHeads, shape.numKvHeads,
+      shape.headDim);
+  }
+
+  // Prepare once per set of chunks; run as often as wanted (one attention launch, plus a merge when a
+  // chunk's key range was split).
+  attnPrefillPrepare(entries: PrefillEntry[], shape: StepShape, workspace: DeviceBuffer): Uint8Array {
+    return this.g4.attnPrefillPrepare(HipAttention.prefillFlat(entries), shape.numQHeads, shape.numKvHeads,
+      shape.headDim, workspace.ptr, workspace.size, this.stream);
+  }
+
+  attnPrefillRun(plan: Uint8Array): void {
+    this.g4.attnPrefillRun(plan, this.stream);
+  }
+
+  attnPrefill(entries: PrefillEntry[], shape: StepShape, workspace: DeviceBuffer): void {
+    this.attnPrefillRun(this.attnPrefillPrepare(entries, shape, workspace));
   }
 
   lmHeadWorkspaceSize(shape: LmHeadShape): number {

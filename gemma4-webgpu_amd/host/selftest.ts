@@ -4,6 +4,8 @@
 //   node host/run.js layer <dir>    one attention layer from <dir>/case.json + case.bin, run twice on the
 //                                   GPU: the engine's six dispatches in order (src/engine.ts:2056-2094),
 //                                   and the fused attnStep; results go to <dir>/out.bin for the oracle check.
+//   node host/run.js prefill <dir>  two prefill chunks (entries) from <dir>/case.json + case.bin in one
+//                                   attnPrefill call; outputs go to <dir>/out.bin.
 //   node host/run.js head <dir>     the sampling head from <dir>/case.json + case.bin: the engine's lmHead,
 //                                   logitSoftcap and sample.argmax dispatches (src/engine.ts:2223-2255),
 //                                   then the fused lmHeadArgmax; results go to <dir>/out.bin.
@@ -133,6 +135,50 @@ function layer(dir: string): string[] {
   return ['engine order: 7 dispatches', 'attnStep: 1 entry', 'results written'];
 }
 
+interface PrefillSpec {
+  nqh: number; nkh: number; hd: number;
+  chunks: { start: number; nTokens: number; window: number; q: number[]; kc: number[]; vc: number[] }[];
+}
+
+function prefill(dir: string): string[] {
+  const spec = JSON.parse(fs.readFileSync(path.join(dir, 'case.json'), 'utf8')) as PrefillSpec;
+  const bin: Uint8Array = fs.readFileSync(path.join(dir, 'case.bin'));
+  const att = new HipAttention(loadAddon(), 0);
+  const bufs: DeviceBuffer[] = [];
+  function upload(r: number[]): DeviceBuffer {
+    const b = att.createBuffer(r[1]);
+    att.writeBuffer(b, 0, bin.subarray(r[0], r[0] + r[1]));
+    bufs.push(b);
+    return b;
+  }
+  const outs: DeviceBuffer[] = [];
+  const entries = spec.chunks.map(function (c) {
+    const out = att.createBuffer(c.nTokens * spec.nqh * spec.hd * 4);
+    bufs.push(out);
+    outs.push(out);
+    return {
+      q: upload(c.q), kCache: upload(c.kc), vCache: upload(c.vc), out: out, nTokens: c.nTokens, start: c.start,
+      slidingWindow: c.window, scale: 1.0,
+    };
+  });
+  const shape = { numQHeads: spec.nqh, numKvHeads: spec.nkh, headDim: spec.hd };
+  const ws = att.createBuffer(Math.max(att.attnPrefillWorkspaceSize(entries, shape), 1));
+  bufs.push(ws);
+  att.attnPrefill(entries, shape, ws);
+  let total = 0;
+  for (const o of outs) total += o.size;
+  const res = new Uint8Array(total);
+  let off = 0;
+  for (const o of outs) {
+    att.readBuffer(o, 0, res.subarray(off, off + o.size));
+    off += o.size;
+  }
+  fs.writeFileSync(path.join(dir, 'out.bin'), res);
+  for (const b of bufs) att.destroyBuffer(b);
+  att.dispose();
+  return ['attnPrefill: ' + entries.length + ' entries', 'results written'];
+}
+
 interface HeadSpec {
   vocab: number; hidden: number; cap: number; arrays: Record<string, number[]>;
 }
@@ -184,6 +230,7 @@ export function main(argv: string[]): void {
   if (mode === 'cpu') done = cpuChecks();
   else if (mode === 'layer') done = layer(argv[1]);
   else if (mode === 'head') done = head(argv[1]);
-  else fail(`usage: run.js cpu | layer <dir> | head <dir>`);
+  else if (mode === 'prefill') done = prefill(argv[1]);
+  else fail(`usage: run.js cpu | layer <dir> | prefill <dir> | head <dir>`);
   process.stdout.write(JSON.stringify({ ok: true, checks: done }) + '\n');
 }

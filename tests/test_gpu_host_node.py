@@ -4,7 +4,8 @@ both over the N-API addon. Checked against the oracle: the six-kernel path bit-i
 kernels evaluate the reference's expressions), attnStep within max-abs 2e-3, and the stored f16
 K/V rows bit-identical on both paths. The sampling head likewise (node host/run.js head): the
 engine's lmHead, logitSoftcap and sample.argmax dispatches and the fused lmHeadArgmax, logits
-bit-identical and top-1 equal to the oracle's.
+bit-identical and top-1 equal to the oracle's. And attnPrefill (node host/run.js prefill): two
+chunks in one call, each token within max-abs 2e-3 of the oracle's decode chain at its position.
 """
 import json
 import shutil
@@ -107,3 +108,40 @@ def test_sampling_head_through_ts_host(tmp_path, vocab, hidden, cap):
         np.testing.assert_array_equal(np.frombuffer(raw[i * n:(i + 1) * n], np.uint32), want.view(np.uint32))
     res = np.frombuffer(raw[2 * n:2 * n + 8], np.uint32)
     assert res[0] == top and res[1] == top
+
+
+@pytest.mark.skipif(NODE is None, reason="node is not installed")
+def test_prefill_through_ts_host(tmp_path):
+    announce("TS host attnPrefill: 2 chunks")
+    chunks, blob, spec = [], bytearray(), []
+    for i, (start, T, window) in enumerate(((0, 37, 0), (600, 20, 512))):
+        rows = start + T
+        kc, vc = cache_f16(70 + i, rows, NKH, HD), cache_f16(80 + i, rows, NKH, HD)
+        q = synth.rms_normalize_rows(synth.normal(90 + i, T * NQH * HD).reshape(T * NQH, HD))
+        qb = orc.f32_to_f16_bits(q).reshape(T, NQH * HD)
+        idx = {}
+        for name, a in (("q", qb), ("kc", kc), ("vc", vc)):
+            b = np.ascontiguousarray(a).tobytes()
+            idx[name] = [len(blob), len(b)]
+            blob += b
+        spec.append(dict(start=start, nTokens=T, window=window, **idx))
+        chunks.append((start, T, window, qb, kc, vc))
+    (tmp_path / "case.bin").write_bytes(bytes(blob))
+    (tmp_path / "case.json").write_text(json.dumps(dict(nqh=NQH, nkh=NKH, hd=HD, chunks=spec)))
+    r = subprocess.run([NODE, str(RUN), "prefill", str(tmp_path)], cwd=ROOT, capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 0, r.stderr
+    got = np.frombuffer((tmp_path / "out.bin").read_bytes(), np.float32)
+    off = 0
+    for start, T, window, qb, kc, vc in chunks:
+        rows = start + T
+        kf = orc.f16_bits_to_f32(kc).reshape(rows, -1)
+        vf = orc.f16_bits_to_f32(vc).reshape(rows, -1)
+        qf = orc.f16_bits_to_f32(qb).reshape(T, -1)
+        for t in range(T):
+            seq = start + t + 1
+            want = orc.attention_chain(qf[t], kf[:seq].reshape(-1), vf[:seq].reshape(-1), NQH, NKH, HD, seq, 1.0,
+                                       window)
+            g = got[off + t * NQH * HD: off + (t + 1) * NQH * HD]
+            assert np.isfinite(g).all() and max_abs(g, want) <= 2e-3, (start, t)
+        off += T * NQH * HD
