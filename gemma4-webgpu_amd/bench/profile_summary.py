@@ -11,6 +11,14 @@
         each scaled by what the same counter reads for g4bench's plain copy kernel
         (512 MiB read and 512 MiB written per launch).
 
+    profile_summary.py mfma --dir D --kernel REGEX --command "..." [--simds N] [--algorithmic-flops F]
+        MFMA utilisation of the kernel matching REGEX from one pass of
+        `rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE SQ_INSTS_VALU_MFMA_MOPS_F16 -f csv -d D`:
+        busy cycles summed over SIMDs / (active cycles of one XCD x SIMDs) (rocprofv3's
+        MfmaUtil expression; the CSV's GRBM_GUI_ACTIVE is the sum of the XCDs' equal
+        readings), next to rocprofv3's own MfmaUtil, and the f16 MFMA flops issued
+        (512 per MOP).
+
 Counter values are KiB per dispatch. The summary prints `hbm_bytes_per_launch:`,
 which bench.py reads as the roofline's `traffic`.
 """
@@ -33,8 +41,10 @@ def _csvs(d: str, suffix: str) -> list[Path]:
     return files
 
 
-def counter_per_dispatch(d: str, counter: str, kernel_re: str) -> tuple[float, int]:
-    """Mean counter value (summed over the rows of one dispatch) over matching dispatches."""
+def counter_per_dispatch(d: str, counter: str, kernel_re: str, reduce: str = "sum") -> tuple[float, int]:
+    """Mean counter value over matching dispatches; the rows of one dispatch (one per hardware
+    instance) are summed, or with reduce="max" the largest is taken (GRBM_GUI_ACTIVE reads one
+    row per XCD, each the whole dispatch's active cycles)."""
     per_dispatch: dict[str, float] = {}
     rx = re.compile(kernel_re)
     for f in _csvs(d, "counter_collection.csv"):
@@ -42,7 +52,11 @@ def counter_per_dispatch(d: str, counter: str, kernel_re: str) -> tuple[float, i
             if row["Counter_Name"] != counter or not rx.search(row["Kernel_Name"]):
                 continue
             key = f"{f}:{row['Dispatch_Id']}"
-            per_dispatch[key] = per_dispatch.get(key, 0.0) + float(row["Counter_Value"])
+            v = float(row["Counter_Value"])
+            if reduce == "max":
+                per_dispatch[key] = max(per_dispatch.get(key, 0.0), v)
+            else:
+                per_dispatch[key] = per_dispatch.get(key, 0.0) + v
     if not per_dispatch:
         raise SystemExit(f"no {counter} rows for kernel /{kernel_re}/ under {d}")
     return statistics.fmean(per_dispatch.values()), len(per_dispatch)
@@ -88,6 +102,30 @@ def cmd_traffic(a) -> None:
         print(f"traffic_over_algorithmic: {(fetch_b + write_b) / a.algorithmic_bytes:.4f}")
 
 
+def cmd_mfma(a) -> None:
+    busy, n = counter_per_dispatch(a.dir, "SQ_VALU_MFMA_BUSY_CYCLES", a.kernel)
+    active_sum, _ = counter_per_dispatch(a.dir, "GRBM_GUI_ACTIVE", a.kernel)
+    active = active_sum / a.xcds  # the CSV sums the XCDs' readings; each counts the dispatch's active cycles
+    mops, _ = counter_per_dispatch(a.dir, "SQ_INSTS_VALU_MFMA_MOPS_F16", a.kernel)
+    try:
+        derived, _ = counter_per_dispatch(a.dir, "MfmaUtil", a.kernel)
+    except SystemExit:
+        derived = None
+    print(f"command: {a.command}")
+    print(f"kernel: /{a.kernel}/ ({n} dispatches)")
+    print(f"sq_valu_mfma_busy_cycles_per_dispatch: {busy:.0f}")
+    print(f"grbm_gui_active_cycles_per_dispatch: {active_sum:.0f} (summed over {a.xcds} XCDs; {active:.0f} each)")
+    print(f"simds: {a.simds}")
+    print(f"mfma_util: {busy / (active * a.simds):.4f}")
+    if derived is not None:
+        print(f"rocprof_MfmaUtil_percent: {derived:.2f}")
+    flops = mops * 512.0
+    print(f"mfma_f16_flops_issued_per_dispatch: {flops:.4e}")
+    if a.algorithmic_flops:
+        print(f"algorithmic_flops_per_dispatch: {a.algorithmic_flops:.4e}")
+        print(f"issued_over_algorithmic: {flops / a.algorithmic_flops:.4f}")
+
+
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     sub = ap.add_subparsers(dest="mode", required=True)
@@ -101,8 +139,15 @@ def main() -> None:
     f.add_argument("--kernel", required=True)
     f.add_argument("--command", required=True)
     f.add_argument("--algorithmic-bytes", type=int, default=0)
+    m = sub.add_parser("mfma")
+    m.add_argument("--dir", required=True)
+    m.add_argument("--kernel", required=True)
+    m.add_argument("--command", required=True)
+    m.add_argument("--simds", type=int, default=1024)
+    m.add_argument("--xcds", type=int, default=8)
+    m.add_argument("--algorithmic-flops", type=float, default=0.0)
     a = ap.parse_args()
-    {"trace": cmd_trace, "traffic": cmd_traffic}[a.mode](a)
+    {"trace": cmd_trace, "traffic": cmd_traffic, "mfma": cmd_mfma}[a.mode](a)
 
 
 if __name__ == "__main__":
