@@ -188,8 +188,67 @@ __global__ __launch_bounds__(kMergeThreads) void k_decode_merge(DecodeArgs a, un
     }
 }
 
+// The same merge for entries of at most kSmallMergeSplits records: one
+// workgroup per (entry, kv head) covers all G query heads (256 / G threads per
+// head, COLS = G * HD / 256 columns per thread), so a merge of many entries
+// with few records (prefill tokens whose keys were cut into parts) needs G x
+// fewer workgroups. Every record's (m, l) and columns are requested at once
+// (indexes clamped to the last record; the extra ones weigh 0), then combined
+// in record order.
+constexpr unsigned kSmallMergeSplits = 8;
+
+template <int HD, int COLS>
+__global__ __launch_bounds__(kMergeThreads) void k_decode_merge_small(DecodeArgs a) {
+    constexpr unsigned TPH = HD / COLS;  // threads per query head
+    const DecodeEntryDev ent = a.table ? a.table[blockIdx.x] : a.one;
+    const unsigned ns = ent.n_splits;
+    if (ns <= 1) return;
+    const unsigned G = a.group, kvh = blockIdx.y;
+    const unsigned h = threadIdx.x / TPH, d = (threadIdx.x % TPH) * COLS;
+    if (h >= G) return;
+    const uint64_t rec_stride = (uint64_t)a.num_kv_heads * G;  // partial records per split
+    const uint64_t rec0 = ((uint64_t)ent.split_base * a.num_kv_heads + kvh) * G + h;
+    f32x4 v[kSmallMergeSplits][COLS / 4];
+    f32x2 w[kSmallMergeSplits];
+#pragma unroll
+    for (unsigned s = 0; s < kSmallMergeSplits; s++) {
+        const uint64_t rec = rec0 + (uint64_t)min(s, ns - 1) * rec_stride;
+        w[s] = ldg<f32x2>(a.part_ml + rec * 2);
+#pragma unroll
+        for (int c = 0; c < COLS / 4; c++) v[s][c] = ldg<f32x4>(a.part_o + rec * HD + d + 4 * c);
+    }
+    float M = w[0][0];
+#pragma unroll
+    for (unsigned s = 1; s < kSmallMergeSplits; s++)
+        if (s < ns) M = fmaxf(M, w[s][0]);
+    float L = 0.0f;
+    f32x4 acc[COLS / 4];
+#pragma unroll
+    for (int c = 0; c < COLS / 4; c++) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (unsigned s = 0; s < kSmallMergeSplits; s++) {
+        const float f = s < ns ? __builtin_amdgcn_exp2f(w[s][0] - M) : 0.0f;
+        L += w[s][1] * f;
+#pragma unroll
+        for (int c = 0; c < COLS / 4; c++) acc[c] += v[s][c] * f;
+    }
+    float* out = ent.out + ((uint64_t)kvh * G + h) * HD + d;
+#pragma unroll
+    for (int c = 0; c < COLS / 4; c++) stg<f32x4>(out + 4 * c, acc[c] / L);
+}
+
 int launch_decode_merge(const DecodeArgs& a, unsigned n_entries, unsigned max_splits, hipStream_t st) {
     if (!n_entries || max_splits <= 1) return G4_OK;
+    if (max_splits <= kSmallMergeSplits && (a.group == 8 || a.group == 4)) {
+        if (a.group == 8)
+            hipLaunchKernelGGL((k_decode_merge_small<256, 8>), dim3(n_entries, a.num_kv_heads), dim3(kMergeThreads), 0,
+                               st, a);
+        else
+            hipLaunchKernelGGL((k_decode_merge_small<256, 4>), dim3(n_entries, a.num_kv_heads), dim3(kMergeThreads), 0,
+                               st, a);
+        G4_CHECK_LAUNCH("attnDecode merge");
+        return G4_OK;
+    }
     if (max_splits > (unsigned)kMaxMergeSplits)
         return fail(G4_EINVAL, "attnDecode merge: %u splits (max %d)", max_splits, kMaxMergeSplits);
     unsigned chunks = 1;

@@ -298,6 +298,8 @@ namespace {
 // workgroups fit one wave of the GPU (at most kStepMaxWgs), so at most that
 // many records exist.
 constexpr unsigned kStepMaxWgs = 1024;
+constexpr unsigned kStepCUs = 256;         // MI355X compute units
+constexpr unsigned kStepOneWgTiles = 16;   // one workgroup per CU up to this many tiles each
 constexpr uint32_t kStepMagic = 0x67345354u;
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -313,7 +315,7 @@ struct StepPlanRep {
     uint32_t n_wgs;
     uint32_t num_kv_heads;
     uint32_t group;
-    uint32_t any_split;  // some entry spans more than one workgroup: run the merge
+    uint32_t n_merge;    // entries spanning more than one workgroup (listed in the merge table)
     uint32_t max_parts;
     uint32_t magic;
 };
@@ -449,9 +451,19 @@ int g4_attn_step_prepare(const g4_step_entry* entries, uint32_t n_entries, uint3
         T += tiles[i];
         if (tiles[i] > max_tiles) max_tiles = tiles[i];
     }
-    // Workgroups that fit the GPU at once (two per CU).
-    static const int wgs_per_cu = step_env("G4_STEP_WGS_PER_CU", 2);
-    uint64_t fit = (uint64_t)(wgs_per_cu > 0 ? wgs_per_cu : 2) * 256 / num_kv_heads;
+    // Workgroups in one wave of the GPU: one per CU while that leaves each
+    // workgroup at most kStepOneWgTiles tiles (four per wave), two per CU
+    // beyond. Measured: a second workgroup per CU adds a tail (it starts behind
+    // the first and is served after it) and more partial records, which only
+    // pays off when the per-wave rounds are many (stack32k: 48.9 µs at two per
+    // CU vs 56.0 at one; stack8k: 22.3 vs 24.0; long128k: 32.2 vs 34.4).
+    // Grids between one and two per CU are slower than both (CUs with two
+    // workgroups finish last). G4_STEP_WGS_PER_CU / G4_STEP_MAX_WGS override.
+    static const int wgs_per_cu = step_env("G4_STEP_WGS_PER_CU", 0);
+    static const int max_wgs = step_env("G4_STEP_MAX_WGS", 0);
+    const uint64_t per_cu = wgs_per_cu > 0 ? (uint64_t)wgs_per_cu
+                            : (T <= (uint64_t)kStepOneWgTiles * (kStepCUs / num_kv_heads) ? 1u : 2u);
+    uint64_t fit = max_wgs > 0 ? (uint64_t)max_wgs / num_kv_heads : per_cu * kStepCUs / num_kv_heads;
     if (fit > kStepMaxWgs) fit = kStepMaxWgs;
     if (fit < 1) fit = 1;
     const uint64_t cap = fit > n_entries ? fit : n_entries;
@@ -459,8 +471,9 @@ int g4_attn_step_prepare(const g4_step_entry* entries, uint32_t n_entries, uint3
 
     std::vector<StepWorkDev> work;
     work.reserve(cap);
-    std::vector<DecodeEntryDev> merge(n_entries);
-    uint32_t any_split = 0, parts = 0, max_parts = 0;
+    std::vector<DecodeEntryDev> merge;  // only the entries with partial records: the merge grid covers them alone
+    merge.reserve(n_entries);
+    uint32_t parts = 0, max_parts = 0;
     for (uint32_t i = 0; i < n_entries; i++) {
         StepEntryDev& d = tab[i];
         const uint64_t ne = tiles[i], we = (ne + tpw - 1) / tpw;
@@ -476,9 +489,8 @@ int g4_attn_step_prepare(const g4_step_entry* entries, uint32_t n_entries, uint3
         if (we > max_parts) max_parts = (uint32_t)we;
         if (we > 1) {
             parts += (uint32_t)we;
-            any_split = 1;
+            merge.push_back(DecodeEntryDev{nullptr, nullptr, nullptr, d.out, 0, 0, part_base, (uint32_t)we, 0.0f, 0});
         }
-        merge[i] = DecodeEntryDev{nullptr, nullptr, nullptr, d.out, 0, 0, part_base, (uint32_t)we, 0.0f, 0};
     }
     if (parts > kStepMaxWgs) return fail(G4_EINVAL, "attnStep: internal: %u partial records", parts);
     const StepLayout L = step_layout(n_entries, num_kv_heads, G, head_dim);
@@ -519,11 +531,12 @@ int g4_attn_step_prepare(const g4_step_entry* entries, uint32_t n_entries, uint3
     if (rc) return rc;
     rc = stage_upload(sg_work, ws + L.work, work.data(), work.size() * sizeof(StepWorkDev), st);
     if (rc) return rc;
-    if (any_split) {
-        rc = stage_upload(sg_merge, ws + L.merge_table, merge.data(), (size_t)n_entries * sizeof(DecodeEntryDev), st);
+    const uint32_t n_merge = (uint32_t)merge.size();
+    if (n_merge) {
+        rc = stage_upload(sg_merge, ws + L.merge_table, merge.data(), (size_t)n_merge * sizeof(DecodeEntryDev), st);
         if (rc) return rc;
     }
-    StepPlanRep r = {ws, n_entries, (uint32_t)work.size(), num_kv_heads, G, any_split, max_parts, kStepMagic};
+    StepPlanRep r = {ws, n_entries, (uint32_t)work.size(), num_kv_heads, G, n_merge, max_parts, kStepMagic};
     memset(plan, 0, sizeof *plan);
     memcpy(plan, &r, sizeof r);
     return G4_OK;
@@ -570,16 +583,16 @@ int g4_attn_step_run_merge(const g4_decode_plan* plan, void* stream) {
     StepPlanRep r;
     int rc = step_plan(plan, &r);
     if (rc) return rc;
-    if (!r.any_split) return G4_OK;
+    if (!r.n_merge) return G4_OK;
     const StepLayout L = step_layout(r.n_entries, r.num_kv_heads, r.group, kStepHD);
     DecodeArgs m = {};
     m.table = reinterpret_cast<const DecodeEntryDev*>(r.ws + L.merge_table);
-    m.n_entries = r.n_entries;
+    m.n_entries = r.n_merge;
     m.num_kv_heads = r.num_kv_heads;
     m.group = r.group;
     m.part_ml = reinterpret_cast<float*>(r.ws + L.part_ml);
     m.part_o = reinterpret_cast<float*>(r.ws + L.part_o);
-    return launch_decode_merge(m, r.n_entries, r.max_parts, as_stream(stream));
+    return launch_decode_merge(m, r.n_merge, r.max_parts, as_stream(stream));
 }
 
 int g4_attn_step_run(const g4_decode_plan* plan, void* stream) {

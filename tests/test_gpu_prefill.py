@@ -6,7 +6,7 @@ checked against the oracle's attnScore -> softmax -> attnOutput chain at
 seq_len = start + t + 1, with the local-layer window, on the same f16 cache
 rows and the f16 query widened to f32. Bar: max-abs 2e-3 (P is rounded to f16
 for the output MFMA). Parts of long key ranges go through the log-sum-exp
-merge (start 2900: three 1024-key parts).
+merge (start 2900: key ranges cut into parts of 1536 keys by default).
 """
 import numpy as np
 import pytest
@@ -71,6 +71,7 @@ def check(c, label):
 
 CASES = [  # (start, T, window)
     (0, 40, 0), (0, 100, 32), (600, 70, 512), (2900, 24, 0), (5, 1, 0), (0, 16, 512), (1000, 33, 512),
+    (20000, 8, 0),  # more than 8 parts: the merge takes its many-record form
 ]
 
 

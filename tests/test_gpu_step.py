@@ -223,3 +223,14 @@ def test_step_gqa_two_kv_heads(dev):
     run_step(dev, [L.entry()], nqh=16, nkh=2)
     want, kb, vb = L.expected()
     check(L, want, kb, vb, "gqa")
+
+
+@pytest.mark.parametrize("seq", [100, 250])
+def test_step_group4_few_parts(dev, seq):
+    """Four query heads per kv head and a few parts per entry: the merge takes its one-workgroup-per-entry
+    form (all heads of an entry, 4 columns per thread)."""
+    announce(f"attnStep nqh=8 nkh=2 seq={seq}")
+    L = Layer(dev, 31 + seq, seq, 0, 1e6, 1, nqh=8, nkh=2)
+    run_step(dev, [L.entry()], nqh=8, nkh=2)
+    want, kb, vb = L.expected()
+    check(L, want, kb, vb, f"group 4 seq={seq}")
