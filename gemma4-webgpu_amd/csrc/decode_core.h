@@ -83,18 +83,18 @@ struct DecodeDims {
 };
 
 // Workgroup memory of one decode workgroup.
-template <int HD>
+template <int HD, int W = kDecodeWaves>
 struct DecodeSmem {
-    f16x8 q[DecodeDims<HD>::NC][64];                       // score B operand, lane-major
-    float o[kDecodeWaves][DecodeDims<HD>::NO * 4][32];     // per-wave outputs for the combine
-    float m[kDecodeWaves][kMaxGroup];
-    float l[kDecodeWaves][kMaxGroup];
+    f16x8 q[DecodeDims<HD>::NC][64];          // score B operand, lane-major
+    float o[W][DecodeDims<HD>::NO * 4][32];   // per-wave outputs for the combine
+    float m[W][kMaxGroup];
+    float l[W][kMaxGroup];
 };
 
 // Writes 8 consecutive q values (already times scale*log2(e)) of one column as
 // the lane's chunk c of the score operand: hi part in columns 0..7, lo in 8..15.
-template <int HD>
-__device__ __forceinline__ void store_q_chunk(DecodeSmem<HD>& sm, int c, int lane, const float (&x)[8], bool lo_col) {
+template <int HD, int W>
+__device__ __forceinline__ void store_q_chunk(DecodeSmem<HD, W>& sm, int c, int lane, const float (&x)[8], bool lo_col) {
     f16x8 v;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
@@ -160,8 +160,8 @@ __device__ __forceinline__ void override_row(unsigned last, int n, int g, unsign
 // exp(-1e30 - max) == 0 in the reference); their loads were clamped in range.
 // (The state is passed as separate references: wrapped in a struct it is not
 // kept in registers and spills.)
-template <int HD>
-__device__ __forceinline__ void tile_step(const DecodeSmem<HD>& sm, int lane, int g, bool lo_col, unsigned kt0,
+template <int HD, int W>
+__device__ __forceinline__ void tile_step(const DecodeSmem<HD, W>& sm, int lane, int g, bool lo_col, unsigned kt0,
                                           unsigned k1, const f16x8 (&kreg)[2][DecodeDims<HD>::NC],
                                           const u32x4 (&vreg)[DecodeDims<HD>::NB][8], float& m_run, float& l_run,
                                           f32x4 (&acc)[DecodeDims<HD>::NO]) {
@@ -225,8 +225,8 @@ __device__ __forceinline__ void tile_step(const DecodeSmem<HD>& sm, int lane, in
 
 // Publishes a wave's final state to workgroup memory (sums over the 4 lane
 // groups, hi + lo columns added).
-template <int HD>
-__device__ __forceinline__ void wave_publish(DecodeSmem<HD>& sm, int wave, int n, int g, float m_run, float l_run,
+template <int HD, int W>
+__device__ __forceinline__ void wave_publish(DecodeSmem<HD, W>& sm, int wave, int n, int g, float m_run, float l_run,
                                              f32x4 (&acc)[DecodeDims<HD>::NO]) {
     constexpr int NO = DecodeDims<HD>::NO;
     float l = l_run;
@@ -248,16 +248,16 @@ __device__ __forceinline__ void wave_publish(DecodeSmem<HD>& sm, int wave, int n
     }
 }
 
-// Combines the 4 waves (after a barrier) and writes either the normalised
+// Combines the W waves (after a barrier) and writes either the normalised
 // output out[h][d] (final) or the unnormalised partial o[h][d] with (m, l)
-// per head, for the G heads of one kv head. Thread t (0..255 within the four
+// per head, for the G heads of one kv head. Thread t (0..64W-1 within the
 // waves that published) covers lane32 = t & 31 (head t & 7, lane group
-// (t >> 3) & 3) of 8 output slots.
+// (t >> 3) & 3) in every 2W-th output slot from slot t >> 5.
 // `extra_m` (optional, per head, log2 units) with `extra_v` (one f16 row shared
 // by the heads) adds a fifth state holding a single row of weight 1: the
 // current token's row when it was not part of the tile loop.
-template <int HD>
-__device__ __forceinline__ void wg_combine_write(const DecodeSmem<HD>& sm, unsigned G, bool final_out, float* out,
+template <int HD, int W>
+__device__ __forceinline__ void wg_combine_write(const DecodeSmem<HD, W>& sm, unsigned G, bool final_out, float* out,
                                                  float* part_o, float* part_ml, const float* extra_m = nullptr,
                                                  const f16* extra_v = nullptr, int t = threadIdx.x) {
     constexpr int NO = DecodeDims<HD>::NO;
@@ -265,17 +265,17 @@ __device__ __forceinline__ void wg_combine_write(const DecodeSmem<HD>& sm, unsig
     const int h = lane32 & 7;
     const int gg = lane32 >> 3;
     if ((unsigned)h >= G) return;
-    float mw[kDecodeWaves], M = -INFINITY;
+    float mw[W], M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kDecodeWaves; w++) {
+    for (int w = 0; w < W; w++) {
         mw[w] = sm.m[w][h];
         M = fmaxf(M, mw[w]);
     }
     const float me = extra_m ? extra_m[h] : -INFINITY;
     M = fmaxf(M, me);
-    float L = 0.0f, sc[kDecodeWaves];
+    float L = 0.0f, sc[W];
 #pragma unroll
-    for (int w = 0; w < kDecodeWaves; w++) {
+    for (int w = 0; w < W; w++) {
         sc[w] = __builtin_amdgcn_exp2f(mw[w] - M);
         L += sm.l[w][h] * sc[w];
     }
@@ -286,10 +286,10 @@ __device__ __forceinline__ void wg_combine_write(const DecodeSmem<HD>& sm, unsig
     if (!final_out && t < 32 && gg == 0) stg<f32x2>(part_ml + h * 2, f32x2{M, L});
     constexpr int kSlots = NO * 4;
 #pragma unroll
-    for (int sl = t >> 5; sl < kSlots; sl += kDecodeThreads / 32) {
+    for (int sl = t >> 5; sl < kSlots; sl += 2 * W) {
         float o = 0.0f;
 #pragma unroll
-        for (int w = 0; w < kDecodeWaves; w++) o += sm.o[w][sl][lane32] * sc[w];
+        for (int w = 0; w < W; w++) o += sm.o[w][sl][lane32] * sc[w];
         const int i = sl >> 2, j = sl & 3;  // MFMA tile i = b*8 + e, row j
         const int b = i >> 3, e = i & 7;
         const int d = ((gg * 4 + j) + 16 * b) * 8 + e;

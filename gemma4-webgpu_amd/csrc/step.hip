@@ -121,8 +121,9 @@ __device__ __forceinline__ void wave_norm_rope(float (&x)[4], const uint32_t (&w
     x[3] = x1 * r.s1 + x3 * r.c1;
 }
 
+template <int W>
 struct StepSmem {
-    DecodeSmem<kStepHD> dec;
+    DecodeSmem<kStepHD, W> dec;
     float qf[kMaxGroup][kStepHD];  // post-prep q * qscale
     f16x8 knew[kStepHD / 8];       // current row's k and v, f16 (as stored)
     f16x8 vnew[kStepHD / 8];
@@ -131,12 +132,15 @@ struct StepSmem {
     float mnew[kMaxGroup];         // current row's scores (log2 units)
 };
 
-// Two workgroups per CU (launch bounds): enough rows in flight to cover the
-// HBM latency with one tile per wave.
-__global__ __launch_bounds__(kDecodeThreads, 2) void k_attn_step(StepArgs a) {
+// W waves per workgroup, two waves per SIMD (launch bounds): two 4-wave
+// workgroups or one 8-wave workgroup per CU, enough rows in flight to cover
+// the HBM latency with one tile per wave.
+template <int W>
+__global__ __launch_bounds__(64 * W, 8 / W) void k_attn_step(StepArgs a) {
     using D = DecodeDims<kStepHD>;
     constexpr unsigned HD = kStepHD;
-    __shared__ StepSmem sm;
+    constexpr int kQPerWave = (kMaxGroup + W - 1) / W;  // query heads per wave
+    __shared__ StepSmem<W> sm;
     const unsigned kvh = blockIdx.y;
     const unsigned NKH = a.num_kv_heads;
     const unsigned G = a.group;
@@ -167,13 +171,13 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void k_attn_step(StepArgs a) {
     const float* rsrc = rcs ? rcs : ent.q;
     const float rc0 = ldg<float>(rsrc + lane), rs0 = ldg<float>(rsrc + 128 + lane);
     const float rc1 = ldg<float>(rsrc + 64 + lane), rs1 = ldg<float>(rsrc + 192 + lane);
-    const unsigned pair = (unsigned)wave * 32u + (unsigned)(lane & 31);  // pair evaluated by this lane otherwise
+    const unsigned pair = (unsigned)(wave & 3) * 32u + (unsigned)(lane & 31);  // pair evaluated by this lane otherwise
     const unsigned apply_divisor = ent.apply_divisor;
     const uint32_t fbits = ldg<uint16_t>((apply_divisor ? ent.rope_freqs : ent.q_weight) + pair);
-    float xq[2][4];
+    float xq[kQPerWave][4];
 #pragma unroll
-    for (int r = 0; r < 2; r++) {
-        const unsigned hq = min((unsigned)wave + kDecodeWaves * r, G - 1);
+    for (int r = 0; r < kQPerWave; r++) {
+        const unsigned hq = min((unsigned)wave + W * r, G - 1);
         const float* src = ent.q + ((uint64_t)kvh * G + hq) * HD;
 #pragma unroll
         for (int j = 0; j < 4; j++) xq[r][j] = ldg<float>(src + lane + 64 * j);
@@ -193,7 +197,7 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void k_attn_step(StepArgs a) {
     const uint32_t row_bytes = NKH * HD * 2u;
     const char* Kb = reinterpret_cast<const char*>(ent.k_cache + (uint64_t)kvh * HD);
     const char* Vb = reinterpret_cast<const char*>(ent.v_cache + (uint64_t)kvh * HD);
-    constexpr unsigned kStride = kDecodeWaves * kTileKeys;
+    constexpr unsigned kStride = W * kTileKeys;
     unsigned t0 = (unsigned)wave * kTileKeys;  // a wave without a tile reads row `last` and discards it
     f16x8 kreg[2][D::NC];
     u32x4 vreg[D::NB][8];
@@ -210,7 +214,7 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void k_attn_step(StepArgs a) {
         const float ang = (float)ent.position * freq;
         const float c = (float)cos((double)ang);
         const float sn = (float)sin((double)ang);
-        if (lane < 32) {
+        if (lane < 32 && wave < 4) {
             sm.rope_c[pair] = c;
             sm.rope_s[pair] = sn;
         }
@@ -221,8 +225,8 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void k_attn_step(StepArgs a) {
     const float qscale = ent.qscale, eps = ent.eps;
     f16* qop = reinterpret_cast<f16*>(sm.dec.q);  // [chunk c][operand lane 16*g + column][8]
 #pragma unroll
-    for (int r = 0; r < 2; r++) {
-        const unsigned hq = (unsigned)wave + kDecodeWaves * r;
+    for (int r = 0; r < kQPerWave; r++) {
+        const unsigned hq = (unsigned)wave + W * r;
         const bool live = hq < G;  // columns of absent heads are zero
         if (live) wave_norm_rope(xq[r], wq, true, true, rl, eps);
 #pragma unroll
@@ -253,7 +257,7 @@ __global__ __launch_bounds__(kDecodeThreads, 2) void k_attn_step(StepArgs a) {
     // The current row's scores (read by the combine, after later barriers).
     if (has_new) {
         const f16* kn = reinterpret_cast<const f16*>(sm.knew);
-        for (unsigned h = (unsigned)wave; h < G; h += kDecodeWaves) {
+        for (unsigned h = (unsigned)wave; h < G; h += W) {
             float p = 0.0f;
 #pragma unroll
             for (int j = 0; j < 4; j++) p += sm.qf[h][lane + 64 * j] * (float)kn[lane + 64 * j];
@@ -317,6 +321,7 @@ struct StepPlanRep {
     uint32_t group;
     uint32_t n_merge;    // entries spanning more than one workgroup (listed in the merge table)
     uint32_t max_parts;
+    uint32_t waves;      // waves per workgroup of the attention kernel (4 or 8)
     uint32_t magic;
 };
 static_assert(sizeof(StepPlanRep) <= sizeof(g4_decode_plan), "plan size");
@@ -451,18 +456,23 @@ int g4_attn_step_prepare(const g4_step_entry* entries, uint32_t n_entries, uint3
         T += tiles[i];
         if (tiles[i] > max_tiles) max_tiles = tiles[i];
     }
-    // Workgroups in one wave of the GPU: one per CU while that leaves each
-    // workgroup at most kStepOneWgTiles tiles (four per wave), two per CU
-    // beyond. Measured: a second workgroup per CU adds a tail (it starts behind
-    // the first and is served after it) and more partial records, which only
-    // pays off when the per-wave rounds are many (stack32k: 48.9 µs at two per
-    // CU vs 56.0 at one; stack8k: 22.3 vs 24.0; long128k: 32.2 vs 34.4).
-    // Grids between one and two per CU are slower than both (CUs with two
-    // workgroups finish last). G4_STEP_WGS_PER_CU / G4_STEP_MAX_WGS override.
+    // Workgroups in one wave of the GPU. Small steps (at most kStepOneWgTiles
+    // tiles per workgroup with one workgroup per CU) take one 8-wave
+    // workgroup per CU: two tile rounds per wave at most, one partial record
+    // per CU. Larger steps take two 4-wave workgroups per CU. Measured (µs,
+    // two 4-wave / one 4-wave / one 8-wave per CU): stack8k 24.0 / 22.3 / 21.9,
+    // long128k 34.4 / 32.0 / 31.5, stack32k 48.9 / 56.0 / 55.7, ragged64
+    // 190.9 / 199.6 / 197.8. A second workgroup per CU starts behind the first
+    // and is served after it, which only pays off when the per-wave rounds
+    // are many; grids between one and two per CU are slower than both (CUs
+    // with two workgroups finish last). G4_STEP_WAVES (4 or 8),
+    // G4_STEP_WGS_PER_CU and G4_STEP_MAX_WGS override.
+    static const int env_waves = step_env("G4_STEP_WAVES", 0);
     static const int wgs_per_cu = step_env("G4_STEP_WGS_PER_CU", 0);
     static const int max_wgs = step_env("G4_STEP_MAX_WGS", 0);
-    const uint64_t per_cu = wgs_per_cu > 0 ? (uint64_t)wgs_per_cu
-                            : (T <= (uint64_t)kStepOneWgTiles * (kStepCUs / num_kv_heads) ? 1u : 2u);
+    const bool small = T <= (uint64_t)kStepOneWgTiles * (kStepCUs / num_kv_heads);
+    const uint32_t waves = env_waves == 4 || env_waves == 8 ? (uint32_t)env_waves : (small ? 8u : 4u);
+    const uint64_t per_cu = wgs_per_cu > 0 ? (uint64_t)wgs_per_cu : (waves == 8 || small ? 1u : 2u);
     uint64_t fit = max_wgs > 0 ? (uint64_t)max_wgs / num_kv_heads : per_cu * kStepCUs / num_kv_heads;
     if (fit > kStepMaxWgs) fit = kStepMaxWgs;
     if (fit < 1) fit = 1;
@@ -536,7 +546,7 @@ int g4_attn_step_prepare(const g4_step_entry* entries, uint32_t n_entries, uint3
         rc = stage_upload(sg_merge, ws + L.merge_table, merge.data(), (size_t)n_merge * sizeof(DecodeEntryDev), st);
         if (rc) return rc;
     }
-    StepPlanRep r = {ws, n_entries, (uint32_t)work.size(), num_kv_heads, G, n_merge, max_parts, kStepMagic};
+    StepPlanRep r = {ws, n_entries, (uint32_t)work.size(), num_kv_heads, G, n_merge, max_parts, waves, kStepMagic};
     memset(plan, 0, sizeof *plan);
     memcpy(plan, &r, sizeof r);
     return G4_OK;
@@ -561,11 +571,15 @@ static int launch_attention(const g4_decode_plan* plan, void* stream, hipEvent_t
     a.group = r.group;
     a.part_ml = reinterpret_cast<float*>(r.ws + L.part_ml);
     a.part_o = reinterpret_cast<float*>(r.ws + L.part_o);
-    if (start || stop)
-        hipExtLaunchKernelGGL(k_attn_step, dim3(r.n_wgs, r.num_kv_heads), dim3(kDecodeThreads), 0, as_stream(stream),
-                              start, stop, 0, a);
-    else
-        hipLaunchKernelGGL(k_attn_step, dim3(r.n_wgs, r.num_kv_heads), dim3(kDecodeThreads), 0, as_stream(stream), a);
+    const dim3 grid(r.n_wgs, r.num_kv_heads);
+    hipStream_t st = as_stream(stream);
+    if (r.waves == 8) {
+        if (start || stop) hipExtLaunchKernelGGL(k_attn_step<8>, grid, dim3(512), 0, st, start, stop, 0, a);
+        else hipLaunchKernelGGL(k_attn_step<8>, grid, dim3(512), 0, st, a);
+    } else {
+        if (start || stop) hipExtLaunchKernelGGL(k_attn_step<4>, grid, dim3(256), 0, st, start, stop, 0, a);
+        else hipLaunchKernelGGL(k_attn_step<4>, grid, dim3(256), 0, st, a);
+    }
     G4_CHECK_LAUNCH("attnStep");
     return G4_OK;
 }

@@ -133,9 +133,11 @@ def test_step_rope_table_same_bits(dev, seq, win, theta, div):
     np.testing.assert_array_equal(L.out.cpu().numpy().view(np.uint32), with_table.view(np.uint32))
 
 
-@pytest.mark.parametrize("seq", [2049, 8193])
+@pytest.mark.parametrize("seq", [2049, 8193, 32769])
 def test_step_e2b_stack(dev, seq):
-    """35 layers (7 global theta 1e6 with the rope_freqs divisor, 28 local W=512 theta 1e4) in one launch."""
+    """35 layers (7 global theta 1e6 with the rope_freqs divisor, 28 local W=512 theta 1e4) in one launch.
+    Up to 8193 the step is small (one 8-wave workgroup per CU); at 32769 it takes two 4-wave workgroups
+    per CU."""
     announce(f"attnStep 35-layer stack seq={seq}")
     cfg = e2b.AttnConfig(num_layers=35)
     layers = [Layer(dev, 1000 * il + seq, seq, e2b.sliding_window(il, cfg), e2b.rope_theta(il, cfg),
@@ -146,6 +148,16 @@ def test_step_e2b_stack(dev, seq):
         want, kb, vb = L.expected()
         worst = max(worst, check(L, want, kb, vb, f"layer {il}"))
     print(f"stack seq={seq} worst err={worst:.2e}")
+
+
+def test_step_long_entry_two_workgroups_per_cu(dev):
+    """One entry of 140001 rows: more than 16 tiles per workgroup at one per CU, so the step takes two
+    4-wave workgroups per CU."""
+    announce("attnStep single seq=140001")
+    L = Layer(dev, 77, 140001, 0, 1e6, 1)
+    run_step(dev, [L.entry(inv_freq=True)])
+    want, kb, vb = L.expected()
+    check(L, want, kb, vb, "seq=140001")
 
 
 def test_step_ragged_batch(dev):
