@@ -479,6 +479,16 @@ int g4_attn_step_prepare(const g4_step_entry* entries, uint32_t n_entries, uint3
     const uint64_t cap = fit > n_entries ? fit : n_entries;
     const uint64_t tpw = pick_tiles_per_wg(tiles, T, max_tiles, cap);
 
+    // Tile ranges of the work items, entry by entry: tpw tiles per item,
+    // balanced within an entry.
+    std::vector<std::vector<uint64_t>> cuts(n_entries);  // per entry: tile boundaries 0 = c0 < c1 < ... = tiles
+    for (uint32_t i = 0; i < n_entries; i++) {
+        const uint64_t ne = tiles[i], we = (ne + tpw - 1) / tpw;
+        std::vector<uint64_t>& c = cuts[i];
+        c.resize(we + 1);
+        for (uint64_t j = 0; j <= we; j++) c[j] = j * ne / we;
+    }
+
     std::vector<StepWorkDev> work;
     work.reserve(cap);
     std::vector<DecodeEntryDev> merge;  // only the entries with partial records: the merge grid covers them alone
@@ -486,11 +496,11 @@ int g4_attn_step_prepare(const g4_step_entry* entries, uint32_t n_entries, uint3
     uint32_t parts = 0, max_parts = 0;
     for (uint32_t i = 0; i < n_entries; i++) {
         StepEntryDev& d = tab[i];
-        const uint64_t ne = tiles[i], we = (ne + tpw - 1) / tpw;
+        const uint64_t we = cuts[i].size() - 1;
         d.n_parts = (uint32_t)we;
         const uint32_t part_base = we > 1 ? parts : 0;
         for (uint64_t j = 0; j < we; j++) {
-            const uint64_t tb = j * ne / we, te = (j + 1) * ne / we;
+            const uint64_t tb = cuts[i][j], te = cuts[i][j + 1];
             const uint64_t rb = key_begin[i] + tb * kTileKeys;
             const uint64_t re = key_begin[i] + te * kTileKeys;
             work.push_back(StepWorkDev{i, (uint32_t)rb, (uint32_t)(re < d.key_end ? re : d.key_end),
@@ -502,7 +512,8 @@ int g4_attn_step_prepare(const g4_step_entry* entries, uint32_t n_entries, uint3
             merge.push_back(DecodeEntryDev{nullptr, nullptr, nullptr, d.out, 0, 0, part_base, (uint32_t)we, 0.0f, 0});
         }
     }
-    if (parts > kStepMaxWgs) return fail(G4_EINVAL, "attnStep: internal: %u partial records", parts);
+    if (parts > kStepMaxWgs || work.size() > cap)
+        return fail(G4_EINVAL, "attnStep: internal: %u partial records, %zu items", parts, work.size());
     const StepLayout L = step_layout(n_entries, num_kv_heads, G, head_dim);
     hipStream_t st = as_stream(stream);
     char* ws = static_cast<char*>(workspace);
