@@ -348,6 +348,7 @@ int g4_attn_decode(const float* q, const uint16_t* k_cache, const uint16_t* v_ca
     int rc = check_shape("attnDecode", p.num_q_heads, p.num_kv_heads, p.head_dim);
     if (rc) return rc;
     if (!q || !k_cache || !v_cache || !out) return fail(G4_EINVAL, "attnDecode: NULL pointer");
+    if (reinterpret_cast<uintptr_t>(out) & 15) return fail(G4_EINVAL, "attnDecode: out must be 16-byte aligned");
     if (p.seq_len == 0) return fail(G4_EINVAL, "attnDecode: seq_len 0");
     uint32_t kb, ke;
     attended_range(p.seq_len, p.sliding_window, &kb, &ke);
@@ -411,6 +412,8 @@ int g4_attn_decode_many_prepare(const g4_decode_entry* entries, uint32_t n_entri
     for (uint32_t i = 0; i < n_entries; i++) {
         const g4_decode_entry& e = entries[i];
         if (!e.q || !e.k_cache || !e.v_cache || !e.out) return fail(G4_EINVAL, "attnDecodeMany: entry %u has NULL", i);
+        if (reinterpret_cast<uintptr_t>(e.out) & 15)
+            return fail(G4_EINVAL, "attnDecodeMany: entry %u out must be 16-byte aligned", i);
         if (e.seq_len == 0) return fail(G4_EINVAL, "attnDecodeMany: entry %u seq_len 0", i);
         uint32_t kb, ke;
         attended_range(e.seq_len, e.sliding_window, &kb, &ke);

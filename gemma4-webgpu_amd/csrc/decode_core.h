@@ -251,16 +251,21 @@ __device__ __forceinline__ void wave_publish(DecodeSmem<HD, W>& sm, int wave, in
 // Combines the W waves (after a barrier) and writes either the normalised
 // output out[h][d] (final) or the unnormalised partial o[h][d] with (m, l)
 // per head, for the G heads of one kv head. Thread t (0..64W-1 within the
-// waves that published) covers lane32 = t & 31 (head t & 7, lane group
-// (t >> 3) & 3) in every 2W-th output slot from slot t >> 5.
+// waves that published) takes lane32 = t & 31 (head t & 7, lane group
+// (t >> 3) & 3) and E = 32 / W consecutive output columns of that head, read
+// from slots (b*8 + e)*4 + j of the published tiles (b, j, e-range chosen by
+// t >> 5), so its stores are 16-byte vectors.
 // `extra_m` (optional, per head, log2 units) with `extra_v` (one f16 row shared
-// by the heads) adds a fifth state holding a single row of weight 1: the
+// by the heads) adds a further state holding a single row of weight 1: the
 // current token's row when it was not part of the tile loop.
 template <int HD, int W>
 __device__ __forceinline__ void wg_combine_write(const DecodeSmem<HD, W>& sm, unsigned G, bool final_out, float* out,
                                                  float* part_o, float* part_ml, const float* extra_m = nullptr,
                                                  const f16* extra_v = nullptr, int t = threadIdx.x) {
     constexpr int NO = DecodeDims<HD>::NO;
+    static_assert(NO == 16, "slot mapping assumes two 8-tile column blocks");
+    constexpr int E = 32 / W;        // consecutive columns per thread
+    constexpr int EPB = 8 / E;       // e-ranges per (b, j)
     const int lane32 = t & 31;
     const int h = lane32 & 7;
     const int gg = lane32 >> 3;
@@ -284,18 +289,21 @@ __device__ __forceinline__ void wg_combine_write(const DecodeSmem<HD, W>& sm, un
     const float inv_l = 1.0f / L;  // L includes the extra state
     float* dst = final_out ? out + (uint64_t)h * HD : part_o + (uint64_t)h * HD;
     if (!final_out && t < 32 && gg == 0) stg<f32x2>(part_ml + h * 2, f32x2{M, L});
-    constexpr int kSlots = NO * 4;
+    const int k = t >> 5;  // 0 .. 2W-1
+    const int e0 = (k % EPB) * E, j = (k / EPB) & 3, b = k / (EPB * 4);
+    const int d0 = ((gg * 4 + j) + 16 * b) * 8 + e0;  // the E columns d0 .. d0 + E - 1
+    float o[E];
 #pragma unroll
-    for (int sl = t >> 5; sl < kSlots; sl += 2 * W) {
-        float o = 0.0f;
+    for (int e = 0; e < E; e++) {
+        const int sl = (b * 8 + e0 + e) * 4 + j;
+        float v = 0.0f;
 #pragma unroll
-        for (int w = 0; w < W; w++) o += sm.o[w][sl][lane32] * sc[w];
-        const int i = sl >> 2, j = sl & 3;  // MFMA tile i = b*8 + e, row j
-        const int b = i >> 3, e = i & 7;
-        const int d = ((gg * 4 + j) + 16 * b) * 8 + e;
-        if (extra_m) o += (float)extra_v[d] * se;
-        stg<float>(dst + d, final_out ? o * inv_l : o);
+        for (int w = 0; w < W; w++) v += sm.o[w][sl][lane32] * sc[w];
+        if (extra_m) v += (float)extra_v[d0 + e] * se;
+        o[e] = final_out ? v * inv_l : v;
     }
+#pragma unroll
+    for (int e = 0; e < E; e += 4) stg<f32x4>(dst + d0 + e, f32x4{o[e], o[e + 1], o[e + 2], o[e + 3]});
 }
 
 }  // namespace g4

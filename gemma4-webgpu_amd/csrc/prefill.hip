@@ -411,6 +411,8 @@ int check(const g4_prefill_entry* ents, uint32_t n, uint32_t nqh, uint32_t nkh, 
     for (uint32_t i = 0; i < n; i++) {
         const g4_prefill_entry& e = ents[i];
         if (!e.q || !e.k_cache || !e.v_cache || !e.out) return fail(G4_EINVAL, "attnPrefill: entry %u has NULL", i);
+        if (reinterpret_cast<uintptr_t>(e.out) & 15)
+            return fail(G4_EINVAL, "attnPrefill: entry %u out must be 16-byte aligned", i);
         if (e.n_tokens == 0) return fail(G4_EINVAL, "attnPrefill: entry %u has no tokens", i);
         if ((uint64_t)e.start + e.n_tokens > 0xffffffffull) return fail(G4_EINVAL, "attnPrefill: entry %u range", i);
     }

@@ -429,6 +429,8 @@ int g4_attn_step_prepare(const g4_step_entry* entries, uint32_t n_entries, uint3
         const g4_step_entry& s = entries[i];
         if (!s.q || !s.k || !s.v || !s.q_weight || !s.k_weight || !s.k_cache || !s.v_cache || !s.out)
             return fail(G4_EINVAL, "attnStep: entry %u has a NULL pointer", i);
+        if (reinterpret_cast<uintptr_t>(s.out) & 15)
+            return fail(G4_EINVAL, "attnStep: entry %u out must be 16-byte aligned", i);
         if (s.apply_divisor && !s.rope_freqs) return fail(G4_EINVAL, "attnStep: entry %u needs rope_freqs", i);
         if (s.seq_len == 0) return fail(G4_EINVAL, "attnStep: entry %u seq_len 0", i);
         if ((uint64_t)s.seq_len * row_bytes > 0xffffffffull)

@@ -202,7 +202,7 @@ int g4_attn_prep_many(const g4_prep_layer* layers, uint32_t n_layers, uint32_t n
  * layers), split across workgroups, merged with a fixed-order log-sum-exp.
  * out[num_q_heads][head_dim] equals the reference chain's attnOut within
  * floating-point rounding. Requires head_dim == 256 and
- * num_q_heads / num_kv_heads <= 8. The workspace holds the split partials;
+ * num_q_heads / num_kv_heads <= 8; out 16-byte aligned. The workspace holds the split partials;
  * g4_attn_decode_workspace_size gives the bytes needed for seq_len up to
  * max_seq_len (allocate once, like attnScores at src/engine.ts:1375).      */
 int g4_attn_decode_workspace_size(uint32_t num_q_heads, uint32_t num_kv_heads, uint32_t head_dim,
@@ -221,7 +221,7 @@ typedef struct g4_decode_entry {
     const float* q;          /* [num_q_heads][head_dim] f32 */
     const uint16_t* k_cache; /* f16 [rows][num_kv_heads][head_dim] */
     const uint16_t* v_cache;
-    float* out;              /* [num_q_heads][head_dim] f32 */
+    float* out;              /* [num_q_heads][head_dim] f32, 16-byte aligned */
     uint32_t seq_len;        /* valid rows */
     uint32_t sliding_window; /* 0 = full */
     float scale;
@@ -293,7 +293,7 @@ typedef struct g4_step_entry {
                                         evaluates the RoPE factors on the host; NULL: in the kernel */
     uint16_t* k_cache;         /* f16 [rows][num_kv_heads][head_dim]; rows < seq_len - 1 hold earlier tokens */
     uint16_t* v_cache;
-    float* out;                /* attnOut [num_q_heads][head_dim] f32 */
+    float* out;                /* attnOut [num_q_heads][head_dim] f32, 16-byte aligned */
     uint32_t seq_len;          /* rows including the current token's (its row is seq_len - 1) */
     uint32_t position;         /* RoPE position of the current token */
     uint32_t sliding_window;   /* 0 = full */
@@ -339,7 +339,7 @@ typedef struct g4_prefill_entry {
     const uint16_t* q;        /* f16 [n_tokens][num_q_heads][head_dim] */
     const uint16_t* k_cache;  /* f16 [rows][num_kv_heads][head_dim], rows >= start + n_tokens */
     const uint16_t* v_cache;
-    float* out;               /* f32 [n_tokens][num_q_heads][head_dim] */
+    float* out;               /* f32 [n_tokens][num_q_heads][head_dim], 16-byte aligned */
     uint32_t n_tokens;
     uint32_t start;           /* position of token 0 */
     uint32_t sliding_window;  /* 0 = full */

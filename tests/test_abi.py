@@ -159,3 +159,17 @@ def test_no_cpu_fallback_in_product_code():
     for f in list(pkg.rglob("*.py")) + list(pkg.rglob("*.js")) + list(pkg.rglob("*.cc")):
         text = f.read_text()
         assert "oracle" not in text.replace("oracle's", "").lower() or f.name == "build.py", f
+
+
+def test_misaligned_out_rejected_on_host():
+    """Outputs are written as 16-byte vectors: a misaligned out is refused before any launch."""
+    lib = abi.load()
+    n = C.c_size_t(0)
+    assert lib.g4_attn_step_workspace_size(1, 8, 1, 256, C.byref(n)) == abi.G4_OK
+    e = abi.StepEntry()
+    e.q = e.k = e.v = e.q_weight = e.k_weight = e.k_cache = e.v_cache = 256
+    e.out = 260
+    e.seq_len, e.position, e.theta, e.scale, e.eps = 10, 9, 1e4, 1.0, 1e-6
+    plan = abi.DecodePlan()
+    st, msg = _err(lambda L: L.g4_attn_step_prepare(C.byref(e), 1, 8, 1, 256, 256, n.value, C.byref(plan), None))
+    assert st == abi.G4_EINVAL and "16-byte aligned" in msg
