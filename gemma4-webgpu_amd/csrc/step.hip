@@ -69,16 +69,20 @@ struct StepEntryDev {
     float eps;
 };
 
-// One workgroup's share: attended rows [row_begin, row_end) of entry `entry`.
+// One workgroup's share: attended rows [row_begin, row_end) of entry `entry`,
+// with a copy of the entry, so that a workgroup's first loads depend on one
+// batch of scalar loads (a kernel starts with cold caches: each dependent
+// load in that chain costs a memory round trip).
 struct StepWorkDev {
-    uint32_t entry;
+    StepEntryDev ent;
     uint32_t row_begin;
     uint32_t row_end;
-    uint32_t part;  // partial record slot, when the entry has more than one workgroup
+    uint32_t part;   // partial record slot, when the entry has more than one workgroup
+    uint32_t entry;
 };
+static_assert(sizeof(StepWorkDev) == 128, "work item size");
 
 struct StepArgs {
-    const StepEntryDev* table;
     const StepWorkDev* work;
     uint32_t num_kv_heads;
     uint32_t group;
@@ -150,8 +154,8 @@ __global__ __launch_bounds__(64 * W, 8 / W) void k_attn_step(StepArgs a) {
     const int g = lane >> 4;
     const bool lo_col = n >= 8;
 
-    const StepWorkDev wk = a.work[blockIdx.x];
-    const StepEntryDev& ent = a.table[wk.entry];  // fields read where used (scalar loads)
+    const StepWorkDev& wk = a.work[blockIdx.x];  // fields read where used (scalar loads)
+    const StepEntryDev& ent = wk.ent;
     const unsigned key_end = ent.key_end;
     const unsigned k0 = wk.row_begin;
     const bool has_new = wk.row_end == key_end;  // this workgroup holds the current token's row
@@ -327,7 +331,7 @@ struct StepPlanRep {
 static_assert(sizeof(StepPlanRep) <= sizeof(g4_decode_plan), "plan size");
 
 struct StepLayout {
-    size_t table, rope, work, merge_table, part_ml, part_o, total;
+    size_t rope, work, merge_table, part_ml, part_o, total;
 };
 
 StepLayout step_layout(uint64_t n, uint64_t nkh, uint64_t group, uint64_t hd) {
@@ -335,8 +339,6 @@ StepLayout step_layout(uint64_t n, uint64_t nkh, uint64_t group, uint64_t hd) {
     const uint64_t max_items = n > kStepMaxWgs ? n : kStepMaxWgs;
     const uint64_t recs = (uint64_t)kStepMaxWgs * nkh * group;
     size_t off = 0;
-    L.table = off;
-    off += align256(n * sizeof(StepEntryDev));
     L.rope = off;  // RoPE factors: at most one [cos x hd/2][sin x hd/2] set per entry
     off += align256(n * hd * 4);
     L.work = off;
@@ -505,8 +507,12 @@ int g4_attn_step_prepare(const g4_step_entry* entries, uint32_t n_entries, uint3
             const uint64_t tb = cuts[i][j], te = cuts[i][j + 1];
             const uint64_t rb = key_begin[i] + tb * kTileKeys;
             const uint64_t re = key_begin[i] + te * kTileKeys;
-            work.push_back(StepWorkDev{i, (uint32_t)rb, (uint32_t)(re < d.key_end ? re : d.key_end),
-                                       we > 1 ? part_base + (uint32_t)j : 0u});
+            StepWorkDev w{};
+            w.row_begin = (uint32_t)rb;
+            w.row_end = (uint32_t)(re < d.key_end ? re : d.key_end);
+            w.part = we > 1 ? part_base + (uint32_t)j : 0u;
+            w.entry = i;
+            work.push_back(w);
         }
         if (we > max_parts) max_parts = (uint32_t)we;
         if (we > 1) {
@@ -547,10 +553,9 @@ int g4_attn_step_prepare(const g4_step_entry* entries, uint32_t n_entries, uint3
             tab[i].rope_cs = reinterpret_cast<const float*>(ws + L.rope) + (size_t)idx * head_dim;
         }
     }
-    static thread_local Staging sg_table, sg_work, sg_merge, sg_rope;
+    for (StepWorkDev& w : work) w.ent = tab[w.entry];  // entries complete (parts, RoPE factors)
+    static thread_local Staging sg_work, sg_merge, sg_rope;
     rc = stage_upload(sg_rope, ws + L.rope, rope.data(), rope.size() * sizeof(float), st);
-    if (rc) return rc;
-    rc = stage_upload(sg_table, ws + L.table, tab.data(), (size_t)n_entries * sizeof(StepEntryDev), st);
     if (rc) return rc;
     rc = stage_upload(sg_work, ws + L.work, work.data(), work.size() * sizeof(StepWorkDev), st);
     if (rc) return rc;
@@ -578,7 +583,6 @@ static int launch_attention(const g4_decode_plan* plan, void* stream, hipEvent_t
     if (rc) return rc;
     const StepLayout L = step_layout(r.n_entries, r.num_kv_heads, r.group, kStepHD);
     StepArgs a = {};
-    a.table = reinterpret_cast<const StepEntryDev*>(r.ws + L.table);
     a.work = reinterpret_cast<const StepWorkDev*>(r.ws + L.work);
     a.num_kv_heads = r.num_kv_heads;
     a.group = r.group;
