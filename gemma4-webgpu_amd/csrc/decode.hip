@@ -237,26 +237,34 @@ __global__ __launch_bounds__(kMergeThreads) void k_decode_merge_small(DecodeArgs
     for (int c = 0; c < COLS / 4; c++) stg<f32x4>(out + 4 * c, acc[c] / L);
 }
 
-int launch_decode_merge(const DecodeArgs& a, unsigned n_entries, unsigned max_splits, hipStream_t st) {
-    if (!n_entries || max_splits <= 1) return G4_OK;
+template <int HD>
+int launch_decode_merge_hd(const DecodeArgs& a, unsigned n_entries, unsigned max_splits, hipStream_t st) {
     if (max_splits <= kSmallMergeSplits && (a.group == 8 || a.group == 4)) {
+        const dim3 grid(n_entries, a.num_kv_heads);
         if (a.group == 8)
-            hipLaunchKernelGGL((k_decode_merge_small<256, 8>), dim3(n_entries, a.num_kv_heads), dim3(kMergeThreads), 0,
-                               st, a);
+            hipLaunchKernelGGL((k_decode_merge_small<HD, HD * 8 / 256>), grid, dim3(kMergeThreads), 0, st, a);
         else
-            hipLaunchKernelGGL((k_decode_merge_small<256, 4>), dim3(n_entries, a.num_kv_heads), dim3(kMergeThreads), 0,
-                               st, a);
+            hipLaunchKernelGGL((k_decode_merge_small<HD, HD * 4 / 256>), grid, dim3(kMergeThreads), 0, st, a);
         G4_CHECK_LAUNCH("attnDecode merge");
         return G4_OK;
     }
     if (max_splits > (unsigned)kMaxMergeSplits)
         return fail(G4_EINVAL, "attnDecode merge: %u splits (max %d)", max_splits, kMaxMergeSplits);
+    // one round trip covers kMergeBatch * P = kMergeBatch * 4 * kMergeThreads / HD records per chunk
+    constexpr unsigned kRecsPerChunk = kMergeBatch * 4 * kMergeThreads / HD;
     unsigned chunks = 1;
-    while (chunks < kMaxMergeChunks && max_splits > 32 * chunks) chunks *= 2;
-    hipLaunchKernelGGL(k_decode_merge<256>, dim3(n_entries, a.num_kv_heads * a.group, chunks), dim3(kMergeThreads), 0,
+    while (chunks < kMaxMergeChunks && max_splits > kRecsPerChunk * chunks) chunks *= 2;
+    hipLaunchKernelGGL(k_decode_merge<HD>, dim3(n_entries, a.num_kv_heads * a.group, chunks), dim3(kMergeThreads), 0,
                        st, a, chunks);
     G4_CHECK_LAUNCH("attnDecode merge");
     return G4_OK;
+}
+
+int launch_decode_merge(const DecodeArgs& a, unsigned n_entries, unsigned max_splits, hipStream_t st,
+                        unsigned head_dim) {
+    if (!n_entries || max_splits <= 1) return G4_OK;
+    if (head_dim == 512) return launch_decode_merge_hd<512>(a, n_entries, max_splits, st);
+    return launch_decode_merge_hd<256>(a, n_entries, max_splits, st);
 }
 
 }  // namespace g4

@@ -73,7 +73,9 @@ struct DecodeArgs {
 // Launches the fixed-order log-sum-exp merge of split partials (decode.hip)
 // for entries 0..n_entries-1 of a.table (or a.one); entries with one split are
 // skipped. max_splits: the largest n_splits among them.
-int launch_decode_merge(const DecodeArgs& a, unsigned n_entries, unsigned max_splits, hipStream_t st);
+// head_dim: 256 or 512.
+int launch_decode_merge(const DecodeArgs& a, unsigned n_entries, unsigned max_splits, hipStream_t st,
+                        unsigned head_dim = 256);
 
 template <int HD>
 struct DecodeDims {
@@ -252,9 +254,11 @@ __device__ __forceinline__ void wave_publish(DecodeSmem<HD, W>& sm, int wave, in
 // output out[h][d] (final) or the unnormalised partial o[h][d] with (m, l)
 // per head, for the G heads of one kv head. Thread t (0..64W-1 within the
 // waves that published) takes lane32 = t & 31 (head t & 7, lane group
-// (t >> 3) & 3) and E = 32 / W consecutive output columns of that head, read
-// from slots (b*8 + e)*4 + j of the published tiles (b, j, e-range chosen by
-// t >> 5), so its stores are 16-byte vectors.
+// (t >> 3) & 3). The output columns of a head come in ROWS = 4 * NB runs of 8
+// (d = ((gg*4 + j) + 16*b)*8 + e, run (b, j), e = 0..7, read from slot
+// (b*8 + e)*4 + j of the published tiles); k = t >> 5 takes runs k, k + 2W, ...
+// whole, or, with fewer runs than 2W, a part of run k / (2W / ROWS). Its
+// stores are 16-byte vectors.
 // `extra_m` (optional, per head, log2 units) with `extra_v` (one f16 row shared
 // by the heads) adds a further state holding a single row of weight 1: the
 // current token's row when it was not part of the tile loop.
@@ -262,10 +266,10 @@ template <int HD, int W>
 __device__ __forceinline__ void wg_combine_write(const DecodeSmem<HD, W>& sm, unsigned G, bool final_out, float* out,
                                                  float* part_o, float* part_ml, const float* extra_m = nullptr,
                                                  const f16* extra_v = nullptr, int t = threadIdx.x) {
-    constexpr int NO = DecodeDims<HD>::NO;
-    static_assert(NO == 16, "slot mapping assumes two 8-tile column blocks");
-    constexpr int E = 32 / W;        // consecutive columns per thread
-    constexpr int EPB = 8 / E;       // e-ranges per (b, j)
+    constexpr int NB = DecodeDims<HD>::NB;
+    constexpr int ROWS = 4 * NB;                        // runs of 8 columns per head and lane group
+    constexpr int EPB = ROWS >= 2 * W ? 1 : 2 * W / ROWS;  // threads per run
+    constexpr int E = 8 / EPB;                          // consecutive columns per thread and run
     const int lane32 = t & 31;
     const int h = lane32 & 7;
     const int gg = lane32 >> 3;
@@ -290,20 +294,24 @@ __device__ __forceinline__ void wg_combine_write(const DecodeSmem<HD, W>& sm, un
     float* dst = final_out ? out + (uint64_t)h * HD : part_o + (uint64_t)h * HD;
     if (!final_out && t < 32 && gg == 0) stg<f32x2>(part_ml + h * 2, f32x2{M, L});
     const int k = t >> 5;  // 0 .. 2W-1
-    const int e0 = (k % EPB) * E, j = (k / EPB) & 3, b = k / (EPB * 4);
-    const int d0 = ((gg * 4 + j) + 16 * b) * 8 + e0;  // the E columns d0 .. d0 + E - 1
-    float o[E];
 #pragma unroll
-    for (int e = 0; e < E; e++) {
-        const int sl = (b * 8 + e0 + e) * 4 + j;
-        float v = 0.0f;
+    for (int r0 = 0; r0 < (ROWS >= 2 * W ? ROWS : 2 * W); r0 += 2 * W) {
+        const int r = (r0 + k) / EPB;  // run (b, j)
+        const int e0 = ((r0 + k) % EPB) * E, j = r & 3, b = r >> 2;
+        const int d0 = ((gg * 4 + j) + 16 * b) * 8 + e0;  // the E columns d0 .. d0 + E - 1
+        float o[E];
 #pragma unroll
-        for (int w = 0; w < W; w++) v += sm.o[w][sl][lane32] * sc[w];
-        if (extra_m) v += (float)extra_v[d0 + e] * se;
-        o[e] = final_out ? v * inv_l : v;
+        for (int e = 0; e < E; e++) {
+            const int sl = (b * 8 + e0 + e) * 4 + j;
+            float v = 0.0f;
+#pragma unroll
+            for (int w = 0; w < W; w++) v += sm.o[w][sl][lane32] * sc[w];
+            if (extra_m) v += (float)extra_v[d0 + e] * se;
+            o[e] = final_out ? v * inv_l : v;
+        }
+#pragma unroll
+        for (int e = 0; e < E; e += 4) stg<f32x4>(dst + d0 + e, f32x4{o[e], o[e + 1], o[e + 2], o[e + 3]});
     }
-#pragma unroll
-    for (int e = 0; e < E; e += 4) stg<f32x4>(dst + d0 + e, f32x4{o[e], o[e + 1], o[e + 2], o[e + 3]});
 }
 
 }  // namespace g4

@@ -90,61 +90,72 @@ struct StepArgs {
     float* part_o;   //                  [part * NKH + kvh][group][HD]
 };
 
-constexpr int kStepHD = 256;
-
-// RoPE factors of pairs (l, l + 128) and (l + 64, l + 192) for lane l (head_dim 256).
+// RoPE factors of pairs (l + 64p, l + 64p + HD/2), p = 0 .. HD/128 - 1, for lane l.
+template <int PJ>
 struct RopeLane {
-    float c0, s0, c1, s1;
+    float c[PJ], s[PJ];
 };
 
-// Per-head RMSNorm (+ RoPE) of one 256-wide head by one wave; lane l holds
-// x[l + 64j], j = 0..3 (and the weight's f16 bits at the same places), and
-// receives the results in place. The sum of squares adds the same pairs in
-// the same order as the reference's workgroup tree (strides 128, 64, then
-// 32..1), so every value is bit-identical to fused_per_head_norm_rope.wgsl /
+// Per-head RMSNorm (+ RoPE) of one HD-wide head by one wave; lane l holds
+// x[l + 64j], j = 0 .. HD/64 - 1 (and the weight's f16 bits at the same
+// places), and receives the results in place. The sum of squares adds the
+// same terms in the same order as the reference's workgroup: partial t
+// (= l + 64q, q = 0..3) sums x[t]^2, x[t + 256]^2, ... in order, then the
+// tree with strides 128, 64 (in the lane) and 32..1 (across lanes), so every
+// value is bit-identical to fused_per_head_norm_rope.wgsl /
 // per_head_rms_norm_no_weight.wgsl.
-__device__ __forceinline__ void wave_norm_rope(float (&x)[4], const uint32_t (&wbits)[4], bool weighted, bool rope,
-                                               const RopeLane& r, float eps) {
+template <int J>
+__device__ __forceinline__ void wave_norm_rope(float (&x)[J], const uint32_t (&wbits)[J], bool weighted, bool rope,
+                                               const RopeLane<J / 2>& r, float eps) {
 #pragma clang fp contract(off)
-    float p[4];
+    constexpr int HD = 64 * J, PJ = J / 2;
+    float part[4];
 #pragma unroll
-    for (int j = 0; j < 4; j++) p[j] = x[j] * x[j];
-    const float a = p[0] + p[2];  // t = lane      : s[t] + s[t + 128]
-    const float b = p[1] + p[3];  // t = lane + 64 : s[t] + s[t + 128]
-    float c = a + b;              // stride 64
+    for (int q = 0; q < 4; q++) {
+        part[q] = x[q] * x[q];
+#pragma unroll
+        for (int m = 1; m < J / 4; m++) part[q] = part[q] + x[q + 4 * m] * x[q + 4 * m];
+    }
+    const float a = part[0] + part[2];  // t = lane      : s[t] + s[t + 128]
+    const float b = part[1] + part[3];  // t = lane + 64 : s[t] + s[t + 128]
+    float c = a + b;                    // stride 64
     for (int stride = 32; stride > 0; stride >>= 1) c = c + __shfl_down(c, stride);
     const float total = __shfl(c, 0);
-    const float rms = sqrtf(total / (float)kStepHD + eps);
+    const float rms = sqrtf(total / (float)HD + eps);
 #pragma unroll
-    for (int j = 0; j < 4; j++) x[j] = weighted ? x[j] * h2f((uint16_t)wbits[j]) / rms : x[j] / rms;
+    for (int j = 0; j < J; j++) x[j] = weighted ? x[j] * h2f((uint16_t)wbits[j]) / rms : x[j] / rms;
     if (!rope) return;
-    const float x0 = x[0], x1 = x[1], x2 = x[2], x3 = x[3];
-    x[0] = x0 * r.c0 - x2 * r.s0;
-    x[2] = x0 * r.s0 + x2 * r.c0;
-    x[1] = x1 * r.c1 - x3 * r.s1;
-    x[3] = x1 * r.s1 + x3 * r.c1;
+#pragma unroll
+    for (int p = 0; p < PJ; p++) {
+        const float x0 = x[p], x1 = x[p + PJ];
+        x[p] = x0 * r.c[p] - x1 * r.s[p];
+        x[p + PJ] = x0 * r.s[p] + x1 * r.c[p];
+    }
 }
 
-template <int W>
+template <int W, int HD>
 struct StepSmem {
-    DecodeSmem<kStepHD, W> dec;
-    float qf[kMaxGroup][kStepHD];  // post-prep q * qscale
-    f16x8 knew[kStepHD / 8];       // current row's k and v, f16 (as stored)
-    f16x8 vnew[kStepHD / 8];
-    float rope_c[kStepHD / 2];     // RoPE factors of the 128 pairs, when evaluated in the kernel
-    float rope_s[kStepHD / 2];
-    float mnew[kMaxGroup];         // current row's scores (log2 units)
+    DecodeSmem<HD, W> dec;
+    float qf[kMaxGroup][HD];  // post-prep q * qscale
+    f16x8 knew[HD / 8];       // current row's k and v, f16 (as stored)
+    f16x8 vnew[HD / 8];
+    float rope_c[HD / 2];     // RoPE factors of the HD/2 pairs, when evaluated in the kernel
+    float rope_s[HD / 2];
+    float mnew[kMaxGroup];    // current row's scores (log2 units)
 };
 
-// W waves per workgroup, two waves per SIMD (launch bounds): two 4-wave
-// workgroups or one 8-wave workgroup per CU, enough rows in flight to cover
-// the HBM latency with one tile per wave.
-template <int W>
-__global__ __launch_bounds__(64 * W, 8 / W) void k_attn_step(StepArgs a) {
-    using D = DecodeDims<kStepHD>;
-    constexpr unsigned HD = kStepHD;
+// W waves per workgroup. head_dim 256: two waves per SIMD (two 4-wave
+// workgroups or one 8-wave workgroup per CU), enough rows in flight to cover
+// the HBM latency with one 32-row tile per wave. head_dim 512: one 4-wave
+// workgroup per CU at one wave per SIMD (a 32-row tile is 64 KB of K and V,
+// the accumulators take 128 registers more).
+template <int W, int HD>
+__global__ __launch_bounds__(64 * W, HD == 256 ? 8 / W : 1) void k_attn_step(StepArgs a) {
+    using D = DecodeDims<HD>;
+    constexpr int J = HD / 64;                          // elements of a head per lane
+    constexpr int PJ = J / 2;                           // RoPE pairs per lane
     constexpr int kQPerWave = (kMaxGroup + W - 1) / W;  // query heads per wave
-    __shared__ StepSmem<W> sm;
+    __shared__ StepSmem<W, HD> sm;
     const unsigned kvh = blockIdx.y;
     const unsigned NKH = a.num_kv_heads;
     const unsigned G = a.group;
@@ -169,34 +180,38 @@ __global__ __launch_bounds__(64 * W, 8 / W) void k_attn_step(StepArgs a) {
     // is not needed): with loads under branches the compiler cannot count the
     // younger loads on every path, and its wait for a small operand would also
     // wait for the tile. f16 values stay unconverted until used.
-    // RoPE factors of pairs (lane, lane + 64) from the host table; absent
-    // tables are replaced by valid dummy addresses (the values are not used).
+    // RoPE factors of this lane's pairs from the host table; absent tables are
+    // replaced by valid dummy addresses (the values are not used).
     const float* rcs = ent.rope_cs;
     const float* rsrc = rcs ? rcs : ent.q;
-    const float rc0 = ldg<float>(rsrc + lane), rs0 = ldg<float>(rsrc + 128 + lane);
-    const float rc1 = ldg<float>(rsrc + 64 + lane), rs1 = ldg<float>(rsrc + 192 + lane);
-    const unsigned pair = (unsigned)(wave & 3) * 32u + (unsigned)(lane & 31);  // pair evaluated by this lane otherwise
+    RopeLane<PJ> rl;
+#pragma unroll
+    for (int p = 0; p < PJ; p++) {
+        rl.c[p] = ldg<float>(rsrc + lane + 64 * p);
+        rl.s[p] = ldg<float>(rsrc + HD / 2 + lane + 64 * p);
+    }
+    const unsigned pair = threadIdx.x % (HD / 2);  // pair evaluated by this thread otherwise
     const unsigned apply_divisor = ent.apply_divisor;
     const uint32_t fbits = ldg<uint16_t>((apply_divisor ? ent.rope_freqs : ent.q_weight) + pair);
-    float xq[kQPerWave][4];
+    float xq[kQPerWave][J];
 #pragma unroll
     for (int r = 0; r < kQPerWave; r++) {
         const unsigned hq = min((unsigned)wave + W * r, G - 1);
         const float* src = ent.q + ((uint64_t)kvh * G + hq) * HD;
 #pragma unroll
-        for (int j = 0; j < 4; j++) xq[r][j] = ldg<float>(src + lane + 64 * j);
+        for (int j = 0; j < J; j++) xq[r][j] = ldg<float>(src + lane + 64 * j);
     }
-    uint32_t wq[4], wn[4];
+    uint32_t wq[J], wn[J];
 #pragma unroll
-    for (int j = 0; j < 4; j++) wq[j] = ldg<uint16_t>(ent.q_weight + lane + 64 * j);
+    for (int j = 0; j < J; j++) wq[j] = ldg<uint16_t>(ent.q_weight + lane + 64 * j);
     const bool do_new = has_new && wave < 2;  // wave 0: k, wave 1: v
-    float xn[4];
+    float xn[J];
     {
         const float* src = (wave == 1 ? ent.v : ent.k) + (uint64_t)kvh * HD;
 #pragma unroll
-        for (int j = 0; j < 4; j++) xn[j] = ldg<float>(src + lane + 64 * j);
+        for (int j = 0; j < J; j++) xn[j] = ldg<float>(src + lane + 64 * j);
 #pragma unroll
-        for (int j = 0; j < 4; j++) wn[j] = ldg<uint16_t>(ent.k_weight + lane + 64 * j);
+        for (int j = 0; j < J; j++) wn[j] = ldg<uint16_t>(ent.k_weight + lane + 64 * j);
     }
     const uint32_t row_bytes = NKH * HD * 2u;
     const char* Kb = reinterpret_cast<const char*>(ent.k_cache + (uint64_t)kvh * HD);
@@ -209,21 +224,23 @@ __global__ __launch_bounds__(64 * W, 8 / W) void k_attn_step(StepArgs a) {
     load_v_tile<HD>(Vb, row_bytes, last, n, g, k0 + t0, vreg);
     __builtin_amdgcn_sched_barrier(0);  // keep every request above ahead of the arithmetic below
 
-    // ---- q heads (two per wave) straight into the score operand; the current
-    // row's k and v ----
-    RopeLane rl = {rc0, rs0, rc1, rs1};
-    if (!rcs) {  // uniform: one pair per lane (lanes 32..63 repeat 0..31), the reference's expressions
-        // with f64 transcendentals; division by 1 is exact, so the load above stays unconditional
+    // ---- q heads straight into the score operand; the current row's k and v ----
+    if (!rcs) {  // uniform: one pair per thread, the reference's expressions with f64
+        // transcendentals; division by 1 is exact, so the load above stays unconditional
         const float freq = rope_inv_freq(pair, HD, ent.theta, 1u, apply_divisor ? h2f((uint16_t)fbits) : 1.0f);
         const float ang = (float)ent.position * freq;
         const float c = (float)cos((double)ang);
         const float sn = (float)sin((double)ang);
-        if (lane < 32 && wave < 4) {
+        if (threadIdx.x < HD / 2) {
             sm.rope_c[pair] = c;
             sm.rope_s[pair] = sn;
         }
         __syncthreads();
-        rl = RopeLane{sm.rope_c[lane], sm.rope_s[lane], sm.rope_c[lane + 64], sm.rope_s[lane + 64]};
+#pragma unroll
+        for (int p = 0; p < PJ; p++) {
+            rl.c[p] = sm.rope_c[lane + 64 * p];
+            rl.s[p] = sm.rope_s[lane + 64 * p];
+        }
     }
 
     const float qscale = ent.qscale, eps = ent.eps;
@@ -232,9 +249,9 @@ __global__ __launch_bounds__(64 * W, 8 / W) void k_attn_step(StepArgs a) {
     for (int r = 0; r < kQPerWave; r++) {
         const unsigned hq = (unsigned)wave + W * r;
         const bool live = hq < G;  // columns of absent heads are zero
-        if (live) wave_norm_rope(xq[r], wq, true, true, rl, eps);
+        if (live) wave_norm_rope<J>(xq[r], wq, true, true, rl, eps);
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
+        for (int j = 0; j < J; j++) {
             const unsigned d = (unsigned)lane + 64u * j;
             const float x = live ? xq[r][j] * qscale : 0.0f;
             if (live) sm.qf[hq][d] = x;
@@ -246,14 +263,14 @@ __global__ __launch_bounds__(64 * W, 8 / W) void k_attn_step(StepArgs a) {
     }
     if (do_new) {
         const bool is_k = wave == 0;
-        wave_norm_rope(xn, wn, is_k, is_k, rl, eps);
+        wave_norm_rope<J>(xn, wn, is_k, is_k, rl, eps);
         uint16_t* row = reinterpret_cast<uint16_t*>(is_k ? sm.knew : sm.vnew);
 #pragma unroll
-        for (int j = 0; j < 4; j++) row[lane + 64 * j] = f2h(xn[j]);
+        for (int j = 0; j < J; j++) row[lane + 64 * j] = f2h(xn[j]);
         if (ent.store_kv) {
             uint16_t* dst = (is_k ? ent.k_cache : ent.v_cache) + ((uint64_t)new_row * NKH + kvh) * HD;
 #pragma unroll
-            for (int j = 0; j < 4; j++) stg<uint16_t>(dst + lane + 64 * j, f2h(xn[j]));
+            for (int j = 0; j < J; j++) stg<uint16_t>(dst + lane + 64 * j, f2h(xn[j]));
         }
     }
     __syncthreads();
@@ -264,7 +281,7 @@ __global__ __launch_bounds__(64 * W, 8 / W) void k_attn_step(StepArgs a) {
         for (unsigned h = (unsigned)wave; h < G; h += W) {
             float p = 0.0f;
 #pragma unroll
-            for (int j = 0; j < 4; j++) p += sm.qf[h][lane + 64 * j] * (float)kn[lane + 64 * j];
+            for (int j = 0; j < J; j++) p += sm.qf[h][lane + 64 * j] * (float)kn[lane + 64 * j];
             for (int off = 32; off > 0; off >>= 1) p += __shfl_xor(p, off);
             if (lane == 0) sm.mnew[h] = p;
         }
@@ -326,6 +343,7 @@ struct StepPlanRep {
     uint32_t n_merge;    // entries spanning more than one workgroup (listed in the merge table)
     uint32_t max_parts;
     uint32_t waves;      // waves per workgroup of the attention kernel (4 or 8)
+    uint32_t head_dim;   // 256 or 512
     uint32_t magic;
 };
 static_assert(sizeof(StepPlanRep) <= sizeof(g4_decode_plan), "plan size");
@@ -403,7 +421,8 @@ extern "C" {
 int g4_attn_step_workspace_size(uint32_t n_entries, uint32_t num_q_heads, uint32_t num_kv_heads, uint32_t head_dim,
                                 size_t* bytes) {
     if (!bytes) return fail(G4_EINVAL, "g4_attn_step_workspace_size: bytes is NULL");
-    if (head_dim != kStepHD) return fail(G4_EINVAL, "attnStep: head_dim %u unsupported (256)", head_dim);
+    if (head_dim != 256 && head_dim != 512)
+        return fail(G4_EINVAL, "attnStep: head_dim %u unsupported (256 or 512)", head_dim);
     if (num_kv_heads == 0 || num_q_heads % num_kv_heads || num_q_heads / num_kv_heads > (uint32_t)kMaxGroup)
         return fail(G4_EINVAL, "attnStep: %u query heads over %u kv heads unsupported", num_q_heads, num_kv_heads);
     if (num_kv_heads > 65535) return fail(G4_EINVAL, "attnStep: %u kv heads (max 65535)", num_kv_heads);
@@ -474,9 +493,13 @@ int g4_attn_step_prepare(const g4_step_entry* entries, uint32_t n_entries, uint3
     static const int env_waves = step_env("G4_STEP_WAVES", 0);
     static const int wgs_per_cu = step_env("G4_STEP_WGS_PER_CU", 0);
     static const int max_wgs = step_env("G4_STEP_MAX_WGS", 0);
+    // head_dim 512 has one form: one 4-wave workgroup per CU.
     const bool small = T <= (uint64_t)kStepOneWgTiles * (kStepCUs / num_kv_heads);
-    const uint32_t waves = env_waves == 4 || env_waves == 8 ? (uint32_t)env_waves : (small ? 8u : 4u);
-    const uint64_t per_cu = wgs_per_cu > 0 ? (uint64_t)wgs_per_cu : (waves == 8 || small ? 1u : 2u);
+    const uint32_t waves =
+        head_dim == 512 ? 4u : env_waves == 4 || env_waves == 8 ? (uint32_t)env_waves : (small ? 8u : 4u);
+    const uint64_t per_cu = head_dim == 512 ? 1u
+                            : wgs_per_cu > 0 ? (uint64_t)wgs_per_cu
+                                             : (waves == 8 || small ? 1u : 2u);
     uint64_t fit = max_wgs > 0 ? (uint64_t)max_wgs / num_kv_heads : per_cu * kStepCUs / num_kv_heads;
     if (fit > kStepMaxWgs) fit = kStepMaxWgs;
     if (fit < 1) fit = 1;
@@ -564,7 +587,8 @@ int g4_attn_step_prepare(const g4_step_entry* entries, uint32_t n_entries, uint3
         rc = stage_upload(sg_merge, ws + L.merge_table, merge.data(), (size_t)n_merge * sizeof(DecodeEntryDev), st);
         if (rc) return rc;
     }
-    StepPlanRep r = {ws, n_entries, (uint32_t)work.size(), num_kv_heads, G, n_merge, max_parts, waves, kStepMagic};
+    StepPlanRep r = {ws,       n_entries, (uint32_t)work.size(), num_kv_heads, G, n_merge, max_parts,
+                     waves,    head_dim,  kStepMagic};
     memset(plan, 0, sizeof *plan);
     memcpy(plan, &r, sizeof r);
     return G4_OK;
@@ -581,7 +605,7 @@ static int launch_attention(const g4_decode_plan* plan, void* stream, hipEvent_t
     StepPlanRep r;
     int rc = step_plan(plan, &r);
     if (rc) return rc;
-    const StepLayout L = step_layout(r.n_entries, r.num_kv_heads, r.group, kStepHD);
+    const StepLayout L = step_layout(r.n_entries, r.num_kv_heads, r.group, r.head_dim);
     StepArgs a = {};
     a.work = reinterpret_cast<const StepWorkDev*>(r.ws + L.work);
     a.num_kv_heads = r.num_kv_heads;
@@ -590,12 +614,15 @@ static int launch_attention(const g4_decode_plan* plan, void* stream, hipEvent_t
     a.part_o = reinterpret_cast<float*>(r.ws + L.part_o);
     const dim3 grid(r.n_wgs, r.num_kv_heads);
     hipStream_t st = as_stream(stream);
-    if (r.waves == 8) {
-        if (start || stop) hipExtLaunchKernelGGL(k_attn_step<8>, grid, dim3(512), 0, st, start, stop, 0, a);
-        else hipLaunchKernelGGL(k_attn_step<8>, grid, dim3(512), 0, st, a);
+    if (r.head_dim == 512) {
+        if (start || stop) hipExtLaunchKernelGGL((k_attn_step<4, 512>), grid, dim3(256), 0, st, start, stop, 0, a);
+        else hipLaunchKernelGGL((k_attn_step<4, 512>), grid, dim3(256), 0, st, a);
+    } else if (r.waves == 8) {
+        if (start || stop) hipExtLaunchKernelGGL((k_attn_step<8, 256>), grid, dim3(512), 0, st, start, stop, 0, a);
+        else hipLaunchKernelGGL((k_attn_step<8, 256>), grid, dim3(512), 0, st, a);
     } else {
-        if (start || stop) hipExtLaunchKernelGGL(k_attn_step<4>, grid, dim3(256), 0, st, start, stop, 0, a);
-        else hipLaunchKernelGGL(k_attn_step<4>, grid, dim3(256), 0, st, a);
+        if (start || stop) hipExtLaunchKernelGGL((k_attn_step<4, 256>), grid, dim3(256), 0, st, start, stop, 0, a);
+        else hipLaunchKernelGGL((k_attn_step<4, 256>), grid, dim3(256), 0, st, a);
     }
     G4_CHECK_LAUNCH("attnStep");
     return G4_OK;
@@ -615,7 +642,7 @@ int g4_attn_step_run_merge(const g4_decode_plan* plan, void* stream) {
     int rc = step_plan(plan, &r);
     if (rc) return rc;
     if (!r.n_merge) return G4_OK;
-    const StepLayout L = step_layout(r.n_entries, r.num_kv_heads, r.group, kStepHD);
+    const StepLayout L = step_layout(r.n_entries, r.num_kv_heads, r.group, r.head_dim);
     DecodeArgs m = {};
     m.table = reinterpret_cast<const DecodeEntryDev*>(r.ws + L.merge_table);
     m.n_entries = r.n_merge;
@@ -623,7 +650,7 @@ int g4_attn_step_run_merge(const g4_decode_plan* plan, void* stream) {
     m.group = r.group;
     m.part_ml = reinterpret_cast<float*>(r.ws + L.part_ml);
     m.part_o = reinterpret_cast<float*>(r.ws + L.part_o);
-    return launch_decode_merge(m, r.n_merge, r.max_parts, as_stream(stream));
+    return launch_decode_merge(m, r.n_merge, r.max_parts, as_stream(stream), r.head_dim);
 }
 
 int g4_attn_step_run(const g4_decode_plan* plan, void* stream) {

@@ -32,17 +32,17 @@ def t16(a, dev):
 class Layer:
     """One entry: raw projections, weights, a cache holding rows 0..seq-2, and the oracle's expectation."""
 
-    def __init__(self, dev, seed, seq, window=0, theta=1e4, divisor=0, nqh=NQH, nkh=NKH, cache=None):
-        self.seq, self.window, self.theta, self.divisor = seq, window, theta, divisor
+    def __init__(self, dev, seed, seq, window=0, theta=1e4, divisor=0, nqh=NQH, nkh=NKH, cache=None, hd=HD):
+        self.seq, self.window, self.theta, self.divisor, self.hd = seq, window, theta, divisor, hd
         self.pos = seq - 1
         rng_scale = 2.0
-        self.q = synth.normal(seed, nqh * HD) * rng_scale
-        self.k = synth.normal(seed + 1, nkh * HD) * rng_scale
-        self.v = synth.normal(seed + 2, nkh * HD) * rng_scale
-        self.qw, self.kw = f16_weight_bits(seed + 3, HD), f16_weight_bits(seed + 4, HD)
+        self.q = synth.normal(seed, nqh * hd) * rng_scale
+        self.k = synth.normal(seed + 1, nkh * hd) * rng_scale
+        self.v = synth.normal(seed + 2, nkh * hd) * rng_scale
+        self.qw, self.kw = f16_weight_bits(seed + 3, hd), f16_weight_bits(seed + 4, hd)
         if cache is None:
-            kc = cache_f16_torch(seed + 5, seq, nkh, HD, dev).view(torch.int16).reshape(seq, nkh * HD)
-            vc = cache_f16_torch(seed + 6, seq, nkh, HD, dev).view(torch.int16).reshape(seq, nkh * HD)
+            kc = cache_f16_torch(seed + 5, seq, nkh, hd, dev).view(torch.int16).reshape(seq, nkh * hd)
+            vc = cache_f16_torch(seed + 6, seq, nkh, hd, dev).view(torch.int16).reshape(seq, nkh * hd)
             kc[self.pos] = NAN16
             vc[self.pos] = NAN16
             if window and seq > window:  # rows outside the window are never read
@@ -51,7 +51,7 @@ class Layer:
             self.kc, self.vc = kc.contiguous(), vc.contiguous()
         else:
             self.kc, self.vc = cache
-        self.out = torch.full((nqh * HD,), float("nan"), device=dev)
+        self.out = torch.full((nqh * hd,), float("nan"), device=dev)
         self.d = {n: torch.from_numpy(x.copy()).to(dev) for n, x in (("q", self.q), ("k", self.k), ("v", self.v))}
         self.dqw, self.dkw, self.drf = t16(self.qw, dev), t16(self.kw, dev), t16(ROPE, dev)
         self.nqh, self.nkh = nqh, nkh
@@ -62,15 +62,16 @@ class Layer:
                  k_cache=self.kc, v_cache=self.vc, out=self.out, seq_len=self.seq, position=self.pos,
                  sliding_window=self.window, store_kv=store, theta=self.theta, apply_divisor=self.divisor)
         if inv_freq:
-            e["rope_inv_freq_host"] = ops.rope_inv_freq_host(self.theta, HD, self.divisor, ROPE)
+            e["rope_inv_freq_host"] = ops.rope_inv_freq_host(self.theta, self.hd, self.divisor, ROPE)
         return e
 
     def expected(self, kv_from=None):
         """Oracle: prep then the reference chain over f32-widened caches (current row = RNE(k'), RNE(v'))."""
         src = kv_from or self
-        v_ = orc.per_head_rms_norm_no_weight(src.v, self.nkh, HD, EPS)
-        k_ = orc.fused_per_head_norm_rope(src.k, src.kw, ROPE, self.nkh, HD, EPS, src.pos, src.theta, src.divisor)
-        q_ = orc.fused_per_head_norm_rope(self.q, self.qw, ROPE, self.nqh, HD, EPS, self.pos, self.theta, self.divisor)
+        hd = self.hd
+        v_ = orc.per_head_rms_norm_no_weight(src.v, self.nkh, hd, EPS)
+        k_ = orc.fused_per_head_norm_rope(src.k, src.kw, ROPE, self.nkh, hd, EPS, src.pos, src.theta, src.divisor)
+        q_ = orc.fused_per_head_norm_rope(self.q, self.qw, ROPE, self.nqh, hd, EPS, self.pos, self.theta, self.divisor)
         kb = self.kc.cpu().numpy().view(np.uint16).copy()
         vb = self.vc.cpu().numpy().view(np.uint16).copy()
         kb[self.pos] = orc.f32_to_f16_bits(k_)
@@ -78,14 +79,14 @@ class Layer:
         lo = self.seq - self.window if self.window and self.seq > self.window else 0
         kf = orc.f16_bits_to_f32(kb[lo:]).reshape(-1)
         vf = orc.f16_bits_to_f32(vb[lo:]).reshape(-1)
-        out = orc.attention_chain(q_, kf, vf, self.nqh, self.nkh, HD, self.seq - lo, 1.0, 0)
+        out = orc.attention_chain(q_, kf, vf, self.nqh, self.nkh, hd, self.seq - lo, 1.0, 0)
         return out, kb[self.pos], vb[self.pos]
 
 
-def run_step(dev, entries, nqh=NQH, nkh=NKH, plan_runs=1):
-    arr = ops.make_step_entries(entries, nqh, nkh, HD)
-    ws = torch.empty(ops.step_workspace_bytes(len(entries), nqh, nkh, HD), dtype=torch.uint8, device=dev)
-    plan = ops.attn_step_prepare(arr, nqh, nkh, HD, ws)
+def run_step(dev, entries, nqh=NQH, nkh=NKH, plan_runs=1, hd=HD):
+    arr = ops.make_step_entries(entries, nqh, nkh, hd)
+    ws = torch.empty(ops.step_workspace_bytes(len(entries), nqh, nkh, hd), dtype=torch.uint8, device=dev)
+    plan = ops.attn_step_prepare(arr, nqh, nkh, hd, ws)
     for _ in range(plan_runs):
         ops.attn_step_run(plan)
     torch.cuda.synchronize()
@@ -246,3 +247,38 @@ def test_step_group4_few_parts(dev, seq):
     run_step(dev, [L.entry()], nqh=8, nkh=2)
     want, kb, vb = L.expected()
     check(L, want, kb, vb, f"group 4 seq={seq}")
+
+
+HD512 = [  # (seq, window, theta, divisor): E2B global layers have head_dim 512
+    (1, 0, 1e6, 1), (33, 0, 1e6, 1), (513, 0, 1e6, 1), (8193, 0, 1e6, 1), (40000, 0, 1e6, 1), (1000, 512, 1e4, 0),
+]
+
+
+@pytest.mark.parametrize("seq,win,theta,div", HD512)
+def test_step_head_dim_512(dev, seq, win, theta, div):
+    """head_dim 512 (one 4-wave workgroup per CU): the stored rows bit-identical, attnOut within 2e-3, with and
+    without the host RoPE table (same bits)."""
+    announce(f"attnStep hd=512 seq={seq} win={win}")
+    L = Layer(dev, 600 + seq, seq, win, theta, div, hd=512)
+    want, kb, vb = L.expected()
+    run_step(dev, [L.entry(inv_freq=True)], hd=512)
+    err = check(L, want, kb, vb, f"hd512 seq={seq}")
+    with_table = L.out.cpu().numpy().copy()
+    L.out.fill_(float("nan"))
+    run_step(dev, [L.entry()], hd=512)
+    np.testing.assert_array_equal(L.out.cpu().numpy().view(np.uint32), with_table.view(np.uint32))
+    print(f"hd512 seq={seq} err={err:.2e}")
+
+
+def test_step_head_dim_512_layers_and_group4(dev):
+    """The seven E2B global layers at 8193 rows in one launch, and a 4:1 group at head_dim 512."""
+    announce("attnStep hd=512 7 global layers; nqh=8 nkh=2")
+    layers = [Layer(dev, 700 + i, 8193, 0, 1e6, 1, hd=512) for i in range(7)]
+    run_step(dev, [L.entry(inv_freq=True) for L in layers], hd=512)
+    for i, L in enumerate(layers):
+        want, kb, vb = L.expected()
+        check(L, want, kb, vb, f"global layer {i}")
+    L = Layer(dev, 800, 3000, 0, 1e6, 1, nqh=8, nkh=2, hd=512)
+    run_step(dev, [L.entry()], nqh=8, nkh=2, hd=512)
+    want, kb, vb = L.expected()
+    check(L, want, kb, vb, "hd512 group 4")
