@@ -157,6 +157,7 @@ struct Layer {
     unsigned seq, window, pos;
     float theta;
     unsigned divisor;
+    unsigned hd = HD;  // head_dim (E2B: 256 on local layers, 512 on global layers)
 };
 
 static std::vector<Layer> workload(const std::string& w) {
@@ -167,8 +168,16 @@ static std::vector<Layer> workload(const std::string& w) {
             bool global = (i % 5) == 4;
             L.push_back({pos + 1, global ? 0u : 512u, pos, global ? 1e6f : 1e4f, global ? 1u : 0u});
         }
+    } else if (w == "e2b8k" || w == "e2b32k") {  // the real E2B head dims: global layers at 512
+        unsigned pos = w == "e2b8k" ? 8192 : 32768;
+        for (int i = 0; i < 35; i++) {
+            bool global = (i % 5) == 4;
+            L.push_back({pos + 1, global ? 0u : 512u, pos, global ? 1e6f : 1e4f, global ? 1u : 0u, global ? 512u : 256u});
+        }
     } else if (w == "long128k") {
         L.push_back({131072, 0, 131071, 1e6f, 1});
+    } else if (w == "long128k_hd512") {
+        L.push_back({131072, 0, 131071, 1e6f, 1, 512});
     } else if (w == "layer512") {
         L.push_back({513, 512, 512, 1e4f, 0});
     } else if (w == "ragged64") {
@@ -263,7 +272,13 @@ int main(int argc, char** argv) {
     for (auto& l : L) {
         unsigned att = l.window && l.seq > l.window ? l.window : l.seq;
         total_rows += att;
-        step_bytes += 2ull * att * NKH * HD * 2 + NQH * HD * 4 * 2;
+        step_bytes += 2ull * att * NKH * l.hd * 2 + NQH * l.hd * 4 * 2;
+    }
+    bool all256 = true;
+    for (auto& l : L) all256 = all256 && l.hd == HD;
+    if (mode != "step" && !all256) {
+        fprintf(stderr, "workload %s: head_dim 512 layers run on the fused step only (--mode step)\n", wl.c_str());
+        return 2;
     }
     if (sets <= 0) sets = step_bytes >= (64ull << 20) ? (int)((512ull << 20) / step_bytes) + 1 : 1;
     printf("workload %s: %zu entries, %.1f MB/step, %d sets\n", wl.c_str(), L.size(), step_bytes / 1e6, sets);
@@ -271,50 +286,53 @@ int main(int argc, char** argv) {
 
     hipStream_t st;
     HK(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
-    std::vector<uint16_t> rf(256), ones(HD, 0x3C00);
+    std::vector<uint16_t> rf(256), ones(512, 0x3C00);
     for (int i = 0; i < 256; i++) rf[i] = i < 64 ? 0x3C00 : 0x7C00;
     void *d_rf, *d_ones;
-    std::vector<float> h_inv[2];
+    std::vector<float> h_inv[2][2];  // [head_dim 256 / 512][local theta 1e4 / global 1e6 with divisor]
     CK(g4_malloc(&d_rf, 512));
-    CK(g4_malloc(&d_ones, HD * 2));
+    CK(g4_malloc(&d_ones, 512 * 2));
     CK(g4_upload(d_rf, 0, rf.data(), 512, st));
-    CK(g4_upload(d_ones, 0, ones.data(), HD * 2, st));
-    for (int i = 0; i < 2; i++) {  // RoPE inverse frequencies: local (theta 1e4) and global (1e6, divisor)
-        h_inv[i].resize(HD / 2);
-        CK(g4_rope_inv_freq_host(i ? 1e6f : 1e4f, HD, i, rf.data(), h_inv[i].data()));
-    }
+    CK(g4_upload(d_ones, 0, ones.data(), 512 * 2, st));
+    for (int h = 0; h < 2; h++)
+        for (int i = 0; i < 2; i++) {
+            const unsigned hd = h ? 512 : 256;
+            h_inv[h][i].resize(hd / 2);
+            CK(g4_rope_inv_freq_host(i ? 1e6f : 1e4f, hd, i, rf.data(), h_inv[h][i].data()));
+        }
 
     struct Set {
         std::vector<void*> bufs;
-        g4_decode_plan plan;       // unfused: prep + split + merge
-        g4_decode_plan step_plan;  // one-launch step
-        void* ws;
-        void* step_ws;
-        void* prep_table;
+        g4_decode_plan plan;          // unfused: prep + split + merge
+        g4_decode_plan step_plan[2];  // one-launch step per head_dim group (256, 512)
+        bool has_step[2] = {false, false};
+        void* ws = nullptr;
+        void* step_ws[2] = {nullptr, nullptr};
+        void* prep_table = nullptr;
     };
     std::vector<Set> S(sets);
-    size_t ws_bytes = 0, step_ws_bytes = 0;
-    CK(g4_attn_decode_many_workspace_size((uint32_t)L.size(), NQH, NKH, HD, total_rows, &ws_bytes));
-    CK(g4_attn_step_workspace_size((uint32_t)L.size(), NQH, NKH, HD, &step_ws_bytes));
+    size_t ws_bytes = 0;
+    if (all256) CK(g4_attn_decode_many_workspace_size((uint32_t)L.size(), NQH, NKH, HD, total_rows, &ws_bytes));
     uint64_t seed = 1;
     for (int s = 0; s < sets; s++) {
         std::vector<g4_decode_entry> ents;
         std::vector<g4_prep_layer> preps;
-        std::vector<g4_step_entry> steps;
+        std::vector<g4_step_entry> steps[2];
         for (auto& l : L) {
             void *kc, *vc, *q, *k, *v, *out;
-            const size_t cache_bytes = (size_t)l.seq * NKH * HD * 2;
+            const unsigned hd = l.hd;
+            const size_t cache_bytes = (size_t)l.seq * NKH * hd * 2;
             CK(g4_malloc(&kc, cache_bytes));
             CK(g4_malloc(&vc, cache_bytes));
-            CK(g4_malloc(&q, NQH * HD * 4));
-            CK(g4_malloc(&k, NKH * HD * 4));
-            CK(g4_malloc(&v, NKH * HD * 4));
-            CK(g4_malloc(&out, NQH * HD * 4));
+            CK(g4_malloc(&q, NQH * hd * 4));
+            CK(g4_malloc(&k, NKH * hd * 4));
+            CK(g4_malloc(&v, NKH * hd * 4));
+            CK(g4_malloc(&out, NQH * hd * 4));
             hipLaunchKernelGGL(k_fill_f16, dim3(1024), dim3(256), 0, st, (_Float16*)kc, (uint64_t)cache_bytes / 2, seed++);
             hipLaunchKernelGGL(k_fill_f16, dim3(1024), dim3(256), 0, st, (_Float16*)vc, (uint64_t)cache_bytes / 2, seed++);
-            hipLaunchKernelGGL(k_fill_f32, dim3(8), dim3(256), 0, st, (float*)q, (uint64_t)NQH * HD, seed++);
-            hipLaunchKernelGGL(k_fill_f32, dim3(1), dim3(256), 0, st, (float*)k, (uint64_t)NKH * HD, seed++);
-            hipLaunchKernelGGL(k_fill_f32, dim3(1), dim3(256), 0, st, (float*)v, (uint64_t)NKH * HD, seed++);
+            hipLaunchKernelGGL(k_fill_f32, dim3(8), dim3(256), 0, st, (float*)q, (uint64_t)NQH * hd, seed++);
+            hipLaunchKernelGGL(k_fill_f32, dim3(2), dim3(256), 0, st, (float*)k, (uint64_t)NKH * hd, seed++);
+            hipLaunchKernelGGL(k_fill_f32, dim3(2), dim3(256), 0, st, (float*)v, (uint64_t)NKH * hd, seed++);
             S[s].bufs.insert(S[s].bufs.end(), {kc, vc, q, k, v, out});
             ents.push_back({(const float*)q, (const uint16_t*)kc, (const uint16_t*)vc, (float*)out, l.seq, l.window,
                             1.0f, 0});
@@ -338,7 +356,7 @@ int main(int argc, char** argv) {
             se.v = (const float*)v;
             se.q_weight = se.k_weight = (const uint16_t*)d_ones;
             se.rope_freqs = (const uint16_t*)d_rf;
-            se.rope_inv_freq_host = h_inv[l.divisor ? 1 : 0].data();
+            se.rope_inv_freq_host = h_inv[hd == 512 ? 1 : 0][l.divisor ? 1 : 0].data();
             se.k_cache = (uint16_t*)kc;
             se.v_cache = (uint16_t*)vc;
             se.out = (float*)out;
@@ -350,17 +368,26 @@ int main(int argc, char** argv) {
             se.apply_divisor = l.divisor;
             se.scale = 1.0f;
             se.eps = 1e-6f;
-            steps.push_back(se);
+            steps[hd == 512 ? 1 : 0].push_back(se);
         }
         HK(hipGetLastError());
-        CK(g4_malloc(&S[s].ws, ws_bytes));
-        CK(g4_malloc(&S[s].prep_table, preps.size() * sizeof(g4_prep_layer)));
-        CK(g4_upload(S[s].prep_table, 0, preps.data(), preps.size() * sizeof(g4_prep_layer), st));
-        CK(g4_attn_decode_many_prepare(ents.data(), (uint32_t)ents.size(), NQH, NKH, HD, S[s].ws, ws_bytes,
-                                       &S[s].plan, st));
-        CK(g4_malloc(&S[s].step_ws, step_ws_bytes));
-        CK(g4_attn_step_prepare(steps.data(), (uint32_t)steps.size(), NQH, NKH, HD, S[s].step_ws, step_ws_bytes,
-                                &S[s].step_plan, st));
+        if (all256) {
+            CK(g4_malloc(&S[s].ws, ws_bytes));
+            CK(g4_malloc(&S[s].prep_table, preps.size() * sizeof(g4_prep_layer)));
+            CK(g4_upload(S[s].prep_table, 0, preps.data(), preps.size() * sizeof(g4_prep_layer), st));
+            CK(g4_attn_decode_many_prepare(ents.data(), (uint32_t)ents.size(), NQH, NKH, HD, S[s].ws, ws_bytes,
+                                           &S[s].plan, st));
+        }
+        for (int h = 0; h < 2; h++) {  // one step per head_dim group (E2B: local layers, then global layers)
+            if (steps[h].empty()) continue;
+            const unsigned hd = h ? 512 : 256;
+            size_t b = 0;
+            CK(g4_attn_step_workspace_size((uint32_t)steps[h].size(), NQH, NKH, hd, &b));
+            CK(g4_malloc(&S[s].step_ws[h], b));
+            CK(g4_attn_step_prepare(steps[h].data(), (uint32_t)steps[h].size(), NQH, NKH, hd, S[s].step_ws[h], b,
+                                    &S[s].step_plan[h], st));
+            S[s].has_step[h] = true;
+        }
     }
     CK(g4_stream_synchronize(st));
 
@@ -368,7 +395,8 @@ int main(int argc, char** argv) {
     auto step = [&](int i) {
         Set& s = S[i % sets];
         if (fused) {
-            CK(g4_attn_step_run(&s.step_plan, st));
+            for (int h = 0; h < 2; h++)
+                if (s.has_step[h]) CK(g4_attn_step_run(&s.step_plan[h], st));
             return;
         }
         if (uniform_pos) CK(g4_attn_prep_many((const g4_prep_layer*)s.prep_table, (uint32_t)L.size(), NQH, NKH, 1e-6f,
