@@ -29,13 +29,13 @@ NQH, NKH, HD = 8, 1, 256
 ROPE = np.array(e2b.rope_freqs_f16_bits(256), dtype=np.uint16)
 
 
-def write_case(d: Path, seed, seq, window, theta, div):
+def write_case(d: Path, seed, seq, window, theta, div, hd=HD):
     pos = seq - 1
     arrs = {
-        "q": synth.normal(seed, NQH * HD) * 2.0, "k": synth.normal(seed + 1, NKH * HD) * 2.0,
-        "v": synth.normal(seed + 2, NKH * HD) * 2.0, "qw": f16_weight_bits(seed + 3, HD),
-        "kw": f16_weight_bits(seed + 4, HD), "rf": ROPE,
-        "kc": cache_f16(seed + 5, seq, NKH, HD).reshape(-1), "vc": cache_f16(seed + 6, seq, NKH, HD).reshape(-1),
+        "q": synth.normal(seed, NQH * hd) * 2.0, "k": synth.normal(seed + 1, NKH * hd) * 2.0,
+        "v": synth.normal(seed + 2, NKH * hd) * 2.0, "qw": f16_weight_bits(seed + 3, hd),
+        "kw": f16_weight_bits(seed + 4, hd), "rf": ROPE,
+        "kc": cache_f16(seed + 5, seq, NKH, hd).reshape(-1), "vc": cache_f16(seed + 6, seq, NKH, hd).reshape(-1),
     }
     blob, index = bytearray(), {}
     for name, a in arrs.items():
@@ -43,39 +43,40 @@ def write_case(d: Path, seed, seq, window, theta, div):
         index[name] = [len(blob), len(b)]
         blob += b
     (d / "case.bin").write_bytes(bytes(blob))
-    (d / "case.json").write_text(json.dumps(dict(nqh=NQH, nkh=NKH, hd=HD, seq=seq, pos=pos, window=window,
+    (d / "case.json").write_text(json.dumps(dict(nqh=NQH, nkh=NKH, hd=hd, seq=seq, pos=pos, window=window,
                                                  theta=theta, div=div, eps=EPS, arrays=index)))
     return arrs, pos
 
 
-def expected(arrs, seq, pos, window, theta, div):
-    v_ = orc.per_head_rms_norm_no_weight(arrs["v"], NKH, HD, EPS)
-    k_ = orc.fused_per_head_norm_rope(arrs["k"], arrs["kw"], ROPE, NKH, HD, EPS, pos, theta, div)
-    q_ = orc.fused_per_head_norm_rope(arrs["q"], arrs["qw"], ROPE, NQH, HD, EPS, pos, theta, div)
-    kb = arrs["kc"].reshape(seq, NKH * HD).copy()
-    vb = arrs["vc"].reshape(seq, NKH * HD).copy()
+def expected(arrs, seq, pos, window, theta, div, hd=HD):
+    v_ = orc.per_head_rms_norm_no_weight(arrs["v"], NKH, hd, EPS)
+    k_ = orc.fused_per_head_norm_rope(arrs["k"], arrs["kw"], ROPE, NKH, hd, EPS, pos, theta, div)
+    q_ = orc.fused_per_head_norm_rope(arrs["q"], arrs["qw"], ROPE, NQH, hd, EPS, pos, theta, div)
+    kb = arrs["kc"].reshape(seq, NKH * hd).copy()
+    vb = arrs["vc"].reshape(seq, NKH * hd).copy()
     kb[pos] = orc.f32_to_f16_bits(k_)
     vb[pos] = orc.f32_to_f16_bits(v_)
     out = orc.attention_chain(q_, orc.f16_bits_to_f32(kb).reshape(-1), orc.f16_bits_to_f32(vb).reshape(-1),
-                              NQH, NKH, HD, seq, 1.0, window)
+                              NQH, NKH, hd, seq, 1.0, window)
     return out, kb[pos], vb[pos]
 
 
 @pytest.mark.skipif(NODE is None, reason="node is not installed")
-@pytest.mark.parametrize("seq,window,theta,div", [(513, 512, 1e4, 0), (2049, 0, 1e6, 1), (7, 0, 1e4, 0)])
-def test_layer_through_ts_host(tmp_path, seq, window, theta, div):
-    announce(f"TS host layer seq={seq} window={window}")
-    arrs, pos = write_case(tmp_path, 77 + seq, seq, window, theta, div)
+@pytest.mark.parametrize("seq,window,theta,div,hd", [(513, 512, 1e4, 0, 256), (2049, 0, 1e6, 1, 256),
+                                                     (7, 0, 1e4, 0, 256), (2049, 0, 1e6, 1, 512)])
+def test_layer_through_ts_host(tmp_path, seq, window, theta, div, hd):
+    announce(f"TS host layer seq={seq} window={window} hd={hd}")
+    arrs, pos = write_case(tmp_path, 77 + seq, seq, window, theta, div, hd)
     r = subprocess.run([NODE, str(RUN), "layer", str(tmp_path)], cwd=ROOT, capture_output=True, text=True,
                        timeout=120)
     assert r.returncode == 0, r.stderr
     raw = (tmp_path / "out.bin").read_bytes()
-    o = NQH * HD * 4
-    row = NKH * HD * 2
+    o = NQH * hd * 4
+    row = NKH * hd * 2
     out_ref = np.frombuffer(raw[:o], np.float32)
     out_step = np.frombuffer(raw[o:2 * o], np.float32)
     rows = [np.frombuffer(raw[2 * o + i * row:2 * o + (i + 1) * row], np.uint16) for i in range(4)]
-    want, kbits, vbits = expected(arrs, seq, pos, window, theta, div)
+    want, kbits, vbits = expected(arrs, seq, pos, window, theta, div, hd)
     np.testing.assert_array_equal(out_ref.view(np.uint32), want.view(np.uint32))
     assert np.isfinite(out_step).all() and max_abs(out_step, want) <= 2e-3
     for got, exp in zip(rows, (kbits, vbits, kbits, vbits)):
