@@ -7,14 +7,8 @@
 //   argmax        shaders/argmax.wgsl:7-34          one workgroup
 //
 // The fused path (k_lm_head + k_lm_head_pick) streams the f16 weight once
-// over the whole chip. Each logit keeps matmul_quant.wgsl's summation order:
-// the 256 partial sums p[t] = sum_j w[t + 256 j] x[t + 256 j] (in j order)
-// followed by the 128 -> 1 tree. A half-wave (32 lanes) owns one row: lane l
-// loads 16 bytes (8 columns) of every 256-column block, so it holds partials
-// t = 8 l .. 8 l + 7 and accumulates them in j order; the tree's strides
-// 128..8 pair lanes l and l ^ 16 .. l ^ 1 (butterfly: both lanes form the
-// same commutative sum), strides 4, 2, 1 stay in the lane. Every lane of the
-// half ends with the row's logit, bit-identical to the shader's.
+// over the whole chip. Each logit keeps matmul_quant.wgsl's summation order
+// (gemv_core.h: one row per half-wave), bit-identical to the shader's.
 //
 // The top-1 follows argmax.wgsl: per index residue mod 256 the first strict
 // maximum, then the 128 -> 1 tree, which keeps its own pair on ties. Among
@@ -28,7 +22,7 @@
 // with none, the result is index 0, as in the shader.
 #include <hip/hip_ext.h>
 
-#include "ref_math.h"
+#include "gemv_core.h"
 
 namespace g4 {
 
@@ -114,12 +108,6 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
     return ((uint64_t)hi << 32) | lo;
 }
 
-template <typename T>
-__device__ __forceinline__ T ldg_nt(const void* p) {
-    typedef const __attribute__((address_space(1))) T* gp;
-    return __builtin_nontemporal_load((gp)(p));
-}
-
 template <int NJ>
 __global__ __launch_bounds__(kLmWaves * 64) void k_lm_head(const float* __restrict__ x,
                                                            const uint16_t* __restrict__ weight,
@@ -130,15 +118,7 @@ __global__ __launch_bounds__(kLmWaves * 64) void k_lm_head(const float* __restri
     const unsigned lq = lane & 31, half = lane >> 5;
 
     float xr[NJ][8];  // x[256 j + 8 lq + e]
-#pragma unroll
-    for (int j = 0; j < NJ; j++) {
-        const f32x4 a = ldg<f32x4>(x + 256 * j + 8 * lq), b = ldg<f32x4>(x + 256 * j + 8 * lq + 4);
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            xr[j][e] = a[e];
-            xr[j][e + 4] = b[e];
-        }
-    }
+    gemv_load_x<NJ>(x, lq, xr);
 
     uint64_t best = 0;
     const unsigned nblocks = (vocab + kLmBlockRows - 1) / kLmBlockRows;
@@ -147,27 +127,8 @@ __global__ __launch_bounds__(kLmWaves * 64) void k_lm_head(const float* __restri
         float val = 0.0f;
         for (unsigned pr = 0; pr < kLmBlockRows / 2; pr++) {
             const unsigned row = min(blk * kLmBlockRows + 2 * pr + half, vocab - 1);  // clamped: tail rows discarded
-            const uint16_t* w = weight + (uint64_t)row * N + 8 * lq;
-            f16x8 wv[NJ];
-#pragma unroll
-            for (int j = 0; j < NJ; j++) wv[j] = ldg_nt<f16x8>(w + 256 * j);
-            float acc[8];
-#pragma unroll
-            for (int e = 0; e < 8; e++) acc[e] = 0.0f;
-#pragma unroll
-            for (int j = 0; j < NJ; j++)
-#pragma unroll
-                for (int e = 0; e < 8; e++) acc[e] = acc[e] + (float)wv[j][e] * xr[j][e];
-#pragma unroll
-            for (int m = 16; m >= 1; m >>= 1)  // tree strides 128 .. 8
-#pragma unroll
-                for (int e = 0; e < 8; e++) acc[e] = acc[e] + __shfl_xor(acc[e], m);
-#pragma unroll
-            for (int e = 0; e < 4; e++) acc[e] = acc[e] + acc[e + 4];  // stride 4
-            acc[0] = acc[0] + acc[2];                                    // stride 2
-            acc[1] = acc[1] + acc[3];
-            acc[0] = acc[0] + acc[1];                                    // stride 1
-            if (lq == pr) val = acc[0];  // lane lq of half h keeps row 2 lq + h of the block
+            const float dot = gemv_row_dot<NJ>(weight + (uint64_t)row * N, xr, lq);
+            if (lq == pr) val = dot;  // lane lq of half h keeps row 2 lq + h of the block
         }
         const unsigned row = blk * kLmBlockRows + 2 * lq + half;
         const float v = cap > 0.0f ? softcap_val(val, cap) : val;

@@ -103,6 +103,10 @@ class LmHeadParams(C.Structure):
     _fields_ = [("vocab", C.c_uint32), ("hidden", C.c_uint32), ("cap", C.c_float)]
 
 
+class LinearSeg(C.Structure):
+    _fields_ = [("weight", C.c_void_p), ("out", C.c_void_p), ("rows", C.c_uint32)]
+
+
 class DecodePlan(C.Structure):
     _fields_ = [("opaque", C.c_uint64 * 8)]
 
@@ -157,6 +161,7 @@ SIGNATURES: dict[str, list] = {
     "g4_attn_prefill_run_timed": [C.POINTER(DecodePlan), _P, _P, _P],
     "g4_attn_prefill": [C.POINTER(PrefillEntry), _U32, _U32, _U32, _U32, _P, _SZ, _P],
     "g4_matmul_quant_f16": [_P, _P, _P, MatmulParams, _P],
+    "g4_linear_f16": [_P, _U32, C.POINTER(LinearSeg), _U32, _P],
     "g4_logit_softcap": [_P, SoftcapParams, _P],
     "g4_argmax": [_P, _P, _U32, _P],
     "g4_lm_head_workspace_size": [LmHeadParams, C.POINTER(C.c_size_t)],

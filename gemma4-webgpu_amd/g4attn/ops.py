@@ -15,7 +15,7 @@ import ctypes as C
 import torch
 
 from . import abi
-from .abi import (AttnOutputParams, AttnScoreParams, DecodeEntry, DecodePlan, KvStoreParams, LmHeadParams,
+from .abi import (AttnOutputParams, AttnScoreParams, DecodeEntry, DecodePlan, KvStoreParams, LinearSeg, LmHeadParams,
                   MatmulParams, NormParams, NormRopeParams, PrepLayer, PrepParams, SoftcapParams, SoftmaxParams,
                   StepEntry)
 
@@ -375,6 +375,15 @@ def matmul_quant_f16(x, weight, out, M, N, stream=None):
     """SHADERS.matmulQuant: out[m] = sum_k f16 weight[m][k] * x[k] (matmul_quant.wgsl order)."""
     abi.call("g4_matmul_quant_f16", _f32(x, "input", N), _f16(weight, "weight", M * N), _f32(out, "output", M),
              MatmulParams(M, N), _stream(stream))
+
+
+def linear_f16(x, n, segments, stream=None):
+    """attn.linearQKV / attn.linearOut: for each (weight f16 [rows][n], out f32 [rows], rows) segment,
+    out = weight @ x with matmul_quant.wgsl's summation order; up to four segments in one launch."""
+    segs = (LinearSeg * len(segments))()
+    for i, (w, out, rows) in enumerate(segments):
+        segs[i] = LinearSeg(_f16(w, f"segment {i} weight", rows * n), _f32(out, f"segment {i} out", rows), rows)
+    abi.call("g4_linear_f16", _f32(x, "input", n), n, segs, len(segments), _stream(stream))
 
 
 def logit_softcap(logits, size, cap, stream=None):

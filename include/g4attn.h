@@ -360,6 +360,21 @@ int g4_attn_prefill_run_timed(const g4_decode_plan* plan, void* stream, void* st
 int g4_attn_prefill(const g4_prefill_entry* entries, uint32_t n_entries, uint32_t num_q_heads, uint32_t num_kv_heads,
                     uint32_t head_dim, void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---- the f16 projections either side of the block ------------------------
+ * attn.linearQKV (src/engine.ts:2045-2051) and attn.linearOut (:2096):
+ * matmulQuant / matmulQuantMR4 over f16 weights. One call runs up to four
+ * weight matrices that read the same input (q, k and v in one launch);
+ * out[r] of each segment is bit-identical to matmul_quant.wgsl's row r.
+ * n (input length) a multiple of 256 in [1024, 4096]; input and weights
+ * 16-byte aligned. */
+typedef struct g4_linear_seg {
+    const uint16_t* weight;  /* f16 [rows][n] */
+    float* out;              /* f32 [rows] */
+    uint32_t rows;
+} g4_linear_seg;
+
+int g4_linear_f16(const float* input, uint32_t n, const g4_linear_seg* segs, uint32_t n_segs, void* stream);
+
 /* ---- lm head -> logit softcap -> argmax (greedy top-1) ------------------
  * src/engine.ts:2223-2255: lmHead (matmulQuant over the f16 tied embedding
  * [vocab][hidden]), logitSoftcap (when final_logit_softcapping > 0), then

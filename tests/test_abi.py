@@ -53,6 +53,7 @@ STRUCTS = {
     "g4_matmul_params": abi.MatmulParams,
     "g4_softcap_params": abi.SoftcapParams,
     "g4_lm_head_params": abi.LmHeadParams,
+    "g4_linear_seg": abi.LinearSeg,
 }
 
 
