@@ -452,6 +452,52 @@ bool get_prop(napi_env env, napi_value obj, const char* key, napi_value* out) {
     return t != napi_undefined && t != napi_null;
 }
 
+// ---- the projections either side of the block: attn.linearQKV / linearOut --
+
+// linear(input, n, segments[{weight, out, rows}], stream): up to four f16
+// weight matrices [rows][n] that read the same f32 input of length n.
+napi_value Linear(napi_env env, napi_callback_info info) {
+    Args a(env, info, 4);
+    void* x = a.ptr(0);
+    const uint32_t n = a.u32(1);
+    void* s = a.ptr(3);
+    if (!a.ok) return nullptr;
+    bool is_array = false;
+    napi_is_array(env, a.v[2], &is_array);
+    if (!is_array) {
+        a.fail("linear: segments must be an array");
+        return nullptr;
+    }
+    uint32_t count = 0;
+    napi_get_array_length(env, a.v[2], &count);
+    std::vector<g4_linear_seg> segs(count);
+    for (uint32_t i = 0; i < count; i++) {
+        napi_value obj, v;
+        napi_get_element(env, a.v[2], i, &obj);
+        const std::string at = "linear: segment " + std::to_string(i) + ": ";
+        const void* ptrs[2] = {};
+        const char* keys[2] = {"weight", "out"};
+        for (int k = 0; k < 2; k++) {
+            uint64_t p = 0;
+            bool lossless = false;
+            if (!get_prop(env, obj, keys[k], &v) || napi_get_value_bigint_uint64(env, v, &p, &lossless) != napi_ok ||
+                !lossless) {
+                a.fail(at + keys[k] + " must be a BigInt pointer");
+                return nullptr;
+            }
+            ptrs[k] = reinterpret_cast<const void*>(static_cast<uintptr_t>(p));
+        }
+        uint32_t rows = 0;
+        if (!get_prop(env, obj, "rows", &v) || napi_get_value_uint32(env, v, &rows) != napi_ok) {
+            a.fail(at + "rows must be a number");
+            return nullptr;
+        }
+        segs[i] = g4_linear_seg{static_cast<const uint16_t*>(ptrs[0]), (float*)const_cast<void*>(ptrs[1]), rows};
+    }
+    CALL(env, g4_linear_f16((const float*)x, n, segs.data(), count, s));
+    return undefined(env);
+}
+
 // One g4_step_entry from a JS object with the same field names in camelCase.
 bool step_entry(Args& a, napi_value obj, size_t idx, uint32_t head_dim, g4_step_entry* e) {
     napi_env env = a.env;
@@ -766,6 +812,7 @@ napi_value Init(napi_env env, napi_value exports) {
         {"argmax", Argmax},
         {"lmHeadWorkspaceSize", LmHeadWorkspaceSize},
         {"lmHeadArgmax", LmHeadArgmax},
+        {"linear", Linear},
         {"ropeInvFreq", RopeInvFreq},
         {"ropeInvFreqHost", RopeInvFreqHost},
         {"attnStepWorkspaceSize", AttnStepWorkspaceSize},

@@ -10,6 +10,9 @@
 // global layer and one 512-window local layer, as 512-token chunks (16
 // entries in one launch; --mode whole: one entry per layer).
 //
+// `proj256` / `proj512` run the block's projections (q, k, v and o_proj) of a
+// local / global E2B layer (--mode fused|chain).
+//
 // `lmhead` runs the sampling head (lm head GEMV, softcap, argmax) at Gemma 4
 // E2B's shape (--mode fused|chain).
 //
@@ -153,6 +156,76 @@ static int run_lmhead(const std::string& mode, int iters) {
     return 0;
 }
 
+// The attention block's projections at Gemma 4 E2B's shapes (hidden 1536):
+// attn.linearQKV (q, k, v: 8 + 1 + 1 heads of head_dim hd) and attn.linearOut
+// (hidden from 8 heads x hd), for a local (hd 256) or a global (hd 512)
+// layer. mode `fused`: g4_linear_f16 (q, k, v in one launch); `chain`: the
+// reference's one-workgroup-per-row matmulQuant per matrix. Weight sets are
+// rotated so the bytes read per cycle exceed twice the 256 MB MALL.
+static int run_proj(const std::string& wl, const std::string& mode, int iters) {
+    const uint32_t H = 1536, hd = wl == "proj512" ? 512 : 256, NQ = NQH * hd, NK = NKH * hd;
+    const uint64_t wbytes = ((uint64_t)(NQ + 2 * NK) * H + (uint64_t)H * NQ) * 2;
+    const uint64_t bytes = wbytes + (H + NQ) * 4 + (uint64_t)(NQ + 2 * NK + H) * 4;
+    const int sets = (int)((512ull << 20) / wbytes) + 1;
+    printf("workload %s: head_dim %u, %.2f MB of weights per layer, %d weight sets\n", wl.c_str(), hd, wbytes / 1e6,
+           sets);
+    printf("bytes_per_step: %llu\n", (unsigned long long)bytes);
+    hipStream_t st;
+    HK(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
+    void *x, *q, *k, *v, *attn, *y;
+    CK(g4_malloc(&x, H * 4));
+    CK(g4_malloc(&q, NQ * 4));
+    CK(g4_malloc(&k, NK * 4));
+    CK(g4_malloc(&v, NK * 4));
+    CK(g4_malloc(&attn, NQ * 4));
+    CK(g4_malloc(&y, H * 4));
+    hipLaunchKernelGGL(k_fill_f32, dim3(8), dim3(256), 0, st, (float*)x, (uint64_t)H, 3ull);
+    hipLaunchKernelGGL(k_fill_f32, dim3(8), dim3(256), 0, st, (float*)attn, (uint64_t)NQ, 4ull);
+    std::vector<void*> wq(sets), wk(sets), wv(sets), wo(sets);
+    for (int s = 0; s < sets; s++) {
+        CK(g4_malloc(&wq[s], (size_t)NQ * H * 2));
+        CK(g4_malloc(&wk[s], (size_t)NK * H * 2));
+        CK(g4_malloc(&wv[s], (size_t)NK * H * 2));
+        CK(g4_malloc(&wo[s], (size_t)H * NQ * 2));
+        hipLaunchKernelGGL(k_fill_f16, dim3(1024), dim3(256), 0, st, (_Float16*)wq[s], (uint64_t)NQ * H, 100ull + s);
+        hipLaunchKernelGGL(k_fill_f16, dim3(256), dim3(256), 0, st, (_Float16*)wk[s], (uint64_t)NK * H, 200ull + s);
+        hipLaunchKernelGGL(k_fill_f16, dim3(256), dim3(256), 0, st, (_Float16*)wv[s], (uint64_t)NK * H, 300ull + s);
+        hipLaunchKernelGGL(k_fill_f16, dim3(1024), dim3(256), 0, st, (_Float16*)wo[s], (uint64_t)H * NQ, 400ull + s);
+    }
+    HK(hipGetLastError());
+    const bool fused = mode != "chain";
+    auto step = [&](int i) {
+        const int s = i % sets;
+        if (fused) {
+            g4_linear_seg qkv[3] = {{(const uint16_t*)wq[s], (float*)q, NQ}, {(const uint16_t*)wk[s], (float*)k, NK},
+                                    {(const uint16_t*)wv[s], (float*)v, NK}};
+            CK(g4_linear_f16((const float*)x, H, qkv, 3, st));
+            g4_linear_seg o = {(const uint16_t*)wo[s], (float*)y, H};
+            CK(g4_linear_f16((const float*)attn, NQ, &o, 1, st));
+            return;
+        }
+        CK(g4_matmul_quant_f16((const float*)x, (const uint16_t*)wq[s], (float*)q, g4_matmul_params{NQ, H}, st));
+        CK(g4_matmul_quant_f16((const float*)x, (const uint16_t*)wk[s], (float*)k, g4_matmul_params{NK, H}, st));
+        CK(g4_matmul_quant_f16((const float*)x, (const uint16_t*)wv[s], (float*)v, g4_matmul_params{NK, H}, st));
+        CK(g4_matmul_quant_f16((const float*)attn, (const uint16_t*)wo[s], (float*)y, g4_matmul_params{H, NQ}, st));
+    };
+    for (int i = 0; i < 3; i++) step(i);
+    CK(g4_stream_synchronize(st));
+    hipEvent_t a, b;
+    HK(hipEventCreate(&a));
+    HK(hipEventCreate(&b));
+    HK(hipEventRecord(a, st));
+    for (int i = 0; i < iters; i++) step(i);
+    HK(hipEventRecord(b, st));
+    HK(hipEventSynchronize(b));
+    float ms = 0;
+    HK(hipEventElapsedTime(&ms, a, b));
+    const double us = ms * 1e3 / iters;
+    printf("%s [%s]: %.2f us/step (linearQKV + linearOut), %.1f GB/s algorithmic (%d iterations)\n", wl.c_str(),
+           fused ? "fused" : "chain", us, bytes / (us * 1e3), iters);
+    return 0;
+}
+
 struct Layer {
     unsigned seq, window, pos;
     float theta;
@@ -266,6 +339,7 @@ int main(int argc, char** argv) {
     if (wl == "copy") return run_copy(iters);
     if (wl == "prefill4k") return run_prefill(mode, iters);
     if (wl == "lmhead") return run_lmhead(mode, iters);
+    if (wl == "proj256" || wl == "proj512") return run_proj(wl, mode, iters);
     std::vector<Layer> L = workload(wl);
     const bool uniform_pos = wl.rfind("stack", 0) == 0 || L.size() == 1;
     uint64_t step_bytes = 0, total_rows = 0;

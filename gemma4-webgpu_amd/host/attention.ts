@@ -152,6 +152,13 @@ export interface LmHeadShape {
   cap: number;
 }
 
+// One f16 weight matrix of a projection: out[r] = sum_c weight[r][c] * input[c] (matmulQuant's rows).
+export interface LinearSegment {
+  weight: DeviceBuffer;       // f16 [rows][n]
+  out: DeviceBuffer;          // f32 [rows]
+  rows: number;
+}
+
 export interface StepShape {
   numQHeads: number;
   numKvHeads: number;
@@ -183,6 +190,7 @@ export interface Addon {
   lmHeadWorkspaceSize(vocab: number, hidden: number, cap: number): number;
   lmHeadArgmax(h: bigint, w: bigint, l: bigint | null, r: bigint, ws: bigint, wsBytes: number, vocab: number,
     hidden: number, cap: number, s: bigint): void;
+  linear(x: bigint, n: number, segs: { weight: bigint; out: bigint; rows: number }[], s: bigint): void;
   ropeInvFreq(theta: number, hd: number, div: number, rf: any, out: bigint, s: bigint): void;
   ropeInvFreqHost(theta: number, hd: number, div: number, rf: Uint16Array | null, out: Float32Array): void;
   attnStepWorkspaceSize(n: number, nqh: number, nkh: number, hd: number): number;
@@ -348,6 +356,18 @@ export class HipAttention {
     if (logits && logits.size < shape.vocab * 4) throw new RangeError('lmHeadArgmax: logits too small');
     this.g4.lmHeadArgmax(hidden.ptr, weight.ptr, logits ? logits.ptr : null, result.ptr, workspace.ptr,
       workspace.size, shape.vocab, shape.hidden, shape.cap, this.stream);
+  }
+
+  // attn.linearQKV (q, k, v in one launch: the three matrices read the same normed hidden state) and
+  // attn.linearOut (src/engine.ts:2045-2051, 2096): each row bit-identical to a matmulQuant dispatch.
+  linear(input: DeviceBuffer, n: number, segments: LinearSegment[]): void {
+    if (input.size < n * 4) throw new RangeError('linear: input too small');
+    const segs = segments.map(function (g, i) {
+      if (g.weight.size < g.rows * n * 2) throw new RangeError('linear: segment ' + i + ' weight too small');
+      if (g.out.size < g.rows * 4) throw new RangeError('linear: segment ' + i + ' out too small');
+      return { weight: g.weight.ptr, out: g.out.ptr, rows: g.rows };
+    });
+    this.g4.linear(input.ptr, n, segs, this.stream);
   }
 
   synchronize(): void {

@@ -9,6 +9,9 @@
 //   node host/run.js head <dir>     the sampling head from <dir>/case.json + case.bin: the engine's lmHead,
 //                                   logitSoftcap and sample.argmax dispatches (src/engine.ts:2223-2255),
 //                                   then the fused lmHeadArgmax; results go to <dir>/out.bin.
+//   node host/run.js linear <dir>   the projections from <dir>/case.json + case.bin: one matmulQuant
+//                                   dispatch per weight matrix (attn.linearQKV, src/engine.ts:2045-2051),
+//                                   then one linear call over all of them; results go to <dir>/out.bin.
 
 import { BINDINGS, KERNELS, PARAMS_BYTES, PASS_LABELS, Uniform, HipAttention, loadAddon } from './attention';
 import type { DeviceBuffer, KernelName } from './attention';
@@ -224,6 +227,51 @@ function head(dir: string): string[] {
   return ['engine order: 3 dispatches', 'lmHeadArgmax: 1 call', 'results written'];
 }
 
+interface LinearSpec {
+  n: number; rows: number[]; arrays: Record<string, number[]>;
+}
+
+function linear(dir: string): string[] {
+  const spec = JSON.parse(fs.readFileSync(path.join(dir, 'case.json'), 'utf8')) as LinearSpec;
+  const bin: Uint8Array = fs.readFileSync(path.join(dir, 'case.bin'));
+  const att = new HipAttention(loadAddon(), 0);
+  const bufs: DeviceBuffer[] = [];
+  function alloc(bytes: number): DeviceBuffer {
+    const b = att.createBuffer(bytes);
+    bufs.push(b);
+    return b;
+  }
+  function upload(name: string): DeviceBuffer {
+    const r = spec.arrays[name];
+    const b = alloc(r[1]);
+    att.writeBuffer(b, 0, bin.subarray(r[0], r[0] + r[1]));
+    return b;
+  }
+  const x = upload('x');
+  const ws = spec.rows.map(function (_r, i) { return upload('w' + i); });
+  const out1 = spec.rows.map(function (r) { return alloc(r * 4); });
+  const out2 = spec.rows.map(function (r) { return alloc(r * 4); });
+  // (1) the engine's dispatches: one matmulQuant per matrix, uniform {M: rows, N: n}
+  spec.rows.forEach(function (r, i) {
+    att.dispatch('matmulQuant', [x, ws[i], out1[i]], new Uniform([{ u: r }, { u: spec.n }]));
+  });
+  // (2) one launch over all of them
+  att.linear(x, spec.n, spec.rows.map(function (r, i) { return { weight: ws[i], out: out2[i], rows: r }; }));
+  const total = spec.rows.reduce(function (a, b) { return a + b; }, 0);
+  const res = new Uint8Array(2 * total * 4);
+  let off = 0;
+  for (const outs of [out1, out2]) {
+    spec.rows.forEach(function (r, i) {
+      att.readBuffer(outs[i], 0, res.subarray(off, off + r * 4));
+      off += r * 4;
+    });
+  }
+  fs.writeFileSync(path.join(dir, 'out.bin'), res);
+  for (const b of bufs) att.destroyBuffer(b);
+  att.dispose();
+  return [`engine order: ${spec.rows.length} dispatches`, 'linear: 1 call', 'results written'];
+}
+
 export function main(argv: string[]): void {
   const mode = argv[0];
   let done: string[];
@@ -231,6 +279,7 @@ export function main(argv: string[]): void {
   else if (mode === 'layer') done = layer(argv[1]);
   else if (mode === 'head') done = head(argv[1]);
   else if (mode === 'prefill') done = prefill(argv[1]);
-  else fail(`usage: run.js cpu | layer <dir> | prefill <dir> | head <dir>`);
+  else if (mode === 'linear') done = linear(argv[1]);
+  else fail(`usage: run.js cpu | layer <dir> | prefill <dir> | head <dir> | linear <dir>`);
   process.stdout.write(JSON.stringify({ ok: true, checks: done }) + '\n');
 }

@@ -6,6 +6,8 @@ K/V rows bit-identical on both paths. The sampling head likewise (node host/run.
 engine's lmHead, logitSoftcap and sample.argmax dispatches and the fused lmHeadArgmax, logits
 bit-identical and top-1 equal to the oracle's. And attnPrefill (node host/run.js prefill): two
 chunks in one call, each token within max-abs 2e-3 of the oracle's decode chain at its position.
+The projections (node host/run.js linear): one matmulQuant dispatch per matrix and one linear call,
+both bit-identical to the oracle's matmulQuant.
 """
 import json
 import shutil
@@ -146,3 +148,28 @@ def test_prefill_through_ts_host(tmp_path):
             g = got[off + t * NQH * HD: off + (t + 1) * NQH * HD]
             assert np.isfinite(g).all() and max_abs(g, want) <= 2e-3, (start, t)
         off += T * NQH * HD
+
+
+@pytest.mark.skipif(NODE is None, reason="node is not installed")
+@pytest.mark.parametrize("n,rows", [(1536, [2048, 256, 256]), (4096, [1536]), (2048, [7, 300, 1, 33])])
+def test_linear_through_ts_host(tmp_path, n, rows):
+    announce(f"TS host linear n={n} rows={rows}")
+    rng = np.random.default_rng(n + len(rows))
+    x = rng.standard_normal(n, dtype=np.float32)
+    ws = [(rng.standard_normal((r, n), dtype=np.float32) * 0.05).astype(np.float16).view(np.uint16) for r in rows]
+    arrays, blob = dict(x=[0, x.nbytes]), [x.tobytes()]
+    off = x.nbytes
+    for i, w in enumerate(ws):
+        arrays[f"w{i}"] = [off, w.nbytes]
+        blob.append(w.tobytes())
+        off += w.nbytes
+    (tmp_path / "case.bin").write_bytes(b"".join(blob))
+    (tmp_path / "case.json").write_text(json.dumps(dict(n=n, rows=rows, arrays=arrays)))
+    r = subprocess.run([NODE, str(RUN), "linear", str(tmp_path)], cwd=ROOT, capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 0, r.stderr
+    got = np.frombuffer((tmp_path / "out.bin").read_bytes(), np.uint32)
+    want = np.concatenate([orc.matmul_quant(x, w, rr, n) for w, rr in zip(ws, rows)]).view(np.uint32)
+    total = sum(rows)
+    np.testing.assert_array_equal(got[:total], want)
+    np.testing.assert_array_equal(got[total:], want)
