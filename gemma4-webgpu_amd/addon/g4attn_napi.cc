@@ -508,10 +508,10 @@ bool step_entry(Args& a, napi_value obj, size_t idx, uint32_t head_dim, g4_step_
         bool required;
     } ptrs[] = {
         {"q", (const void**)&e->q, true},
-        {"k", (const void**)&e->k, true},
-        {"v", (const void**)&e->v, true},
+        {"k", (const void**)&e->k, false},  // k, v, kWeight absent: the current row is already cached
+        {"v", (const void**)&e->v, false},
         {"qWeight", (const void**)&e->q_weight, true},
-        {"kWeight", (const void**)&e->k_weight, true},
+        {"kWeight", (const void**)&e->k_weight, false},
         {"ropeFreqs", (const void**)&e->rope_freqs, false},
         {"kCache", (const void**)&e->k_cache, true},
         {"vCache", (const void**)&e->v_cache, true},

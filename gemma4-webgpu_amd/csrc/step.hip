@@ -62,12 +62,15 @@ struct StepEntryDev {
     uint32_t key_end;   // one past the last attended row; the current row is key_end - 1
     uint32_t n_parts;   // workgroups on this entry
     uint32_t position;  // RoPE position
-    uint32_t store_kv;
+    uint32_t flags;     // kStoreKv | kRowCached
     float theta;
     uint32_t apply_divisor;
     float qscale;       // attention scale * log2(e)
     float eps;
 };
+
+constexpr uint32_t kStoreKv = 1;    // write the current row's k and v to the caches
+constexpr uint32_t kRowCached = 2;  // the current row is already in the cache: read it like the others
 
 // One workgroup's share: attended rows [row_begin, row_end) of entry `entry`,
 // with a copy of the entry, so that a workgroup's first loads depend on one
@@ -169,7 +172,8 @@ __global__ __launch_bounds__(64 * W, HD == 256 ? 8 / W : 1) void k_attn_step(Ste
     const StepEntryDev& ent = wk.ent;
     const unsigned key_end = ent.key_end;
     const unsigned k0 = wk.row_begin;
-    const bool has_new = wk.row_end == key_end;  // this workgroup holds the current token's row
+    // This workgroup holds the current token's row, and computes it (unless it is already cached).
+    const bool has_new = wk.row_end == key_end && !(ent.flags & kRowCached);
     const unsigned new_row = key_end - 1;
     const unsigned k1t = has_new ? new_row : wk.row_end;  // rows read from the cache: [k0, k1t)
     const unsigned nkeys = k1t - k0;
@@ -267,7 +271,7 @@ __global__ __launch_bounds__(64 * W, HD == 256 ? 8 / W : 1) void k_attn_step(Ste
         uint16_t* row = reinterpret_cast<uint16_t*>(is_k ? sm.knew : sm.vnew);
 #pragma unroll
         for (int j = 0; j < J; j++) row[lane + 64 * j] = f2h(xn[j]);
-        if (ent.store_kv) {
+        if (ent.flags & kStoreKv) {
             uint16_t* dst = (is_k ? ent.k_cache : ent.v_cache) + ((uint64_t)new_row * NKH + kvh) * HD;
 #pragma unroll
             for (int j = 0; j < J; j++) stg<uint16_t>(dst + lane + 64 * j, f2h(xn[j]));
@@ -448,8 +452,13 @@ int g4_attn_step_prepare(const g4_step_entry* entries, uint32_t n_entries, uint3
     uint64_t T = 0, max_tiles = 0;
     for (uint32_t i = 0; i < n_entries; i++) {
         const g4_step_entry& s = entries[i];
-        if (!s.q || !s.k || !s.v || !s.q_weight || !s.k_weight || !s.k_cache || !s.v_cache || !s.out)
+        if (!s.q || !s.q_weight || !s.k_cache || !s.v_cache || !s.out)
             return fail(G4_EINVAL, "attnStep: entry %u has a NULL pointer", i);
+        const bool cached = !s.k && !s.v && !s.k_weight;  // consumer whose producer stored the row already
+        if (!cached && (!s.k || !s.v || !s.k_weight))
+            return fail(G4_EINVAL, "attnStep: entry %u: k, v and k_weight are all set or all NULL", i);
+        if (cached && s.store_kv)
+            return fail(G4_EINVAL, "attnStep: entry %u: store_kv needs the raw k and v", i);
         if (reinterpret_cast<uintptr_t>(s.out) & 15)
             return fail(G4_EINVAL, "attnStep: entry %u out must be 16-byte aligned", i);
         if (s.apply_divisor && !s.rope_freqs) return fail(G4_EINVAL, "attnStep: entry %u needs rope_freqs", i);
@@ -459,17 +468,19 @@ int g4_attn_step_prepare(const g4_step_entry* entries, uint32_t n_entries, uint3
         StepEntryDev& d = tab[i];
         d = StepEntryDev{};
         d.q = s.q;
-        d.k = s.k;
-        d.v = s.v;
+        // Cached rows: the kernel's unconditional loads of k, v and k_weight read q and q_weight
+        // instead (valid addresses; the values are not used).
+        d.k = cached ? s.q : s.k;
+        d.v = cached ? s.q : s.v;
         d.q_weight = s.q_weight;
-        d.k_weight = s.k_weight;
+        d.k_weight = cached ? s.q_weight : s.k_weight;
         d.rope_freqs = s.rope_freqs;
         d.k_cache = s.k_cache;
         d.v_cache = s.v_cache;
         d.out = s.out;
         d.key_end = s.seq_len;
         d.position = s.position;
-        d.store_kv = s.store_kv;
+        d.flags = (s.store_kv ? kStoreKv : 0u) | (cached ? kRowCached : 0u);
         d.theta = s.theta;
         d.apply_divisor = s.apply_divisor;
         d.qscale = s.scale * kLog2e;

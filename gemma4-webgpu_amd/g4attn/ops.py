@@ -262,7 +262,9 @@ def make_step_entries(items, num_q_heads, num_kv_heads, head_dim):
     """items: iterable of dicts with q, k, v (raw f32 projections), q_weight, k_weight (f16), rope_freqs (f16 or
     None), rope_inv_freq_host (optional host f32 numpy table from rope_inv_freq_host(); kept alive by the caller
     until prepare returns), k_cache, v_cache (f16, at least seq_len rows),
-    out (f32), seq_len, position, sliding_window, store_kv, theta, apply_divisor, scale, eps."""
+    out (f32), seq_len, position, sliding_window, store_kv, theta, apply_divisor, scale, eps.
+    k, v and k_weight None (with store_kv False): the current row is already in the cache (a KV-consumer
+    layer stepped after its producer)."""
     items = list(items)
     arr = (StepEntry * len(items))()
     for i, it in enumerate(items):
@@ -271,10 +273,13 @@ def make_step_entries(items, num_q_heads, num_kv_heads, head_dim):
         rf = it.get("rope_freqs")
         if it["apply_divisor"] and rf is None:
             raise ValueError(f"entry {i}: apply_divisor needs rope_freqs")
+        def opt(t, conv, name, n):
+            return None if t is None else conv(t, name, n)
+
         arr[i] = StepEntry(
-            _f32(it["q"], f"entry {i} q", num_q_heads * head_dim), _f32(it["k"], f"entry {i} k", nkv),
-            _f32(it["v"], f"entry {i} v", nkv), _f16(it["q_weight"], f"entry {i} q_weight", head_dim),
-            _f16(it["k_weight"], f"entry {i} k_weight", head_dim),
+            _f32(it["q"], f"entry {i} q", num_q_heads * head_dim), opt(it.get("k"), _f32, f"entry {i} k", nkv),
+            opt(it.get("v"), _f32, f"entry {i} v", nkv), _f16(it["q_weight"], f"entry {i} q_weight", head_dim),
+            opt(it.get("k_weight"), _f16, f"entry {i} k_weight", head_dim),
             _f16(rf, f"entry {i} rope_freqs", head_dim // 2) if rf is not None else None,
             _host_f32(it["rope_inv_freq_host"], f"entry {i} rope_inv_freq_host", head_dim // 2)
             if it.get("rope_inv_freq_host") is not None else None,

@@ -112,10 +112,10 @@ export interface DeviceBuffer {
 // One entry of the fused step: a layer of a token's stack or a sequence of a batch.
 export interface StepEntry {
   q: DeviceBuffer;            // raw projection f32 [NQH][HD] (read only)
-  k: DeviceBuffer;            // raw projection f32 [NKH][HD]
-  v: DeviceBuffer;
+  k?: DeviceBuffer;           // raw projection f32 [NKH][HD]; k, v and kWeight absent (with storeKv false):
+  v?: DeviceBuffer;           // the current row is already in the cache (a consumer layer after its producer)
   qWeight: DeviceBuffer;      // attn_q_norm f16 [HD]
-  kWeight: DeviceBuffer;      // attn_k_norm f16 [HD]
+  kWeight?: DeviceBuffer;     // attn_k_norm f16 [HD]
   ropeFreqs?: DeviceBuffer;   // f16 divisor table (global layers)
   ropeInvFreq?: Float32Array; // host f32 [HD/2] table from ropeInvFreqHost(); RoPE factors are then evaluated in prepare
   kCache: DeviceBuffer;       // f16 [rows][NKH][HD]
@@ -294,7 +294,8 @@ export class HipAttention {
   attnStepPrepare(entries: StepEntry[], shape: StepShape, workspace: DeviceBuffer): Uint8Array {
     const flat = entries.map(function (e) {
       return {
-        q: e.q.ptr, k: e.k.ptr, v: e.v.ptr, qWeight: e.qWeight.ptr, kWeight: e.kWeight.ptr,
+        q: e.q.ptr, k: e.k ? e.k.ptr : undefined, v: e.v ? e.v.ptr : undefined, qWeight: e.qWeight.ptr,
+        kWeight: e.kWeight ? e.kWeight.ptr : undefined,
         ropeFreqs: e.ropeFreqs ? e.ropeFreqs.ptr : undefined,
         ropeInvFreq: e.ropeInvFreq,
         kCache: e.kCache.ptr, vCache: e.vCache.ptr, out: e.out.ptr,

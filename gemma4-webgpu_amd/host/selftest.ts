@@ -9,12 +9,18 @@
 //   node host/run.js head <dir>     the sampling head from <dir>/case.json + case.bin: the engine's lmHead,
 //                                   logitSoftcap and sample.argmax dispatches (src/engine.ts:2223-2255),
 //                                   then the fused lmHeadArgmax; results go to <dir>/out.bin.
+//   node host/run.js batch <dir>    continuous batching from <dir>/case.json + case.bin: sequences are
+//                                   submitted, admitted into cache slots and released over several token
+//                                   steps of a DecodeScheduler, one attnStep per layer over the active
+//                                   sequences; every attnOut goes to <dir>/out.bin, in step, layer and
+//                                   admission order.
 //   node host/run.js linear <dir>   the projections from <dir>/case.json + case.bin: one matmulQuant
 //                                   dispatch per weight matrix (attn.linearQKV, src/engine.ts:2045-2051),
 //                                   then one linear call over all of them; results go to <dir>/out.bin.
 
 import { BINDINGS, KERNELS, PARAMS_BYTES, PASS_LABELS, Uniform, HipAttention, loadAddon } from './attention';
 import type { DeviceBuffer, KernelName } from './attention';
+import { DecodeScheduler, SlotTable } from './scheduler';
 
 declare const require: any;
 declare const process: any;
@@ -24,6 +30,57 @@ const path = require('path');
 
 function fail(msg: string): never {
   throw new Error(msg);
+}
+
+function throws(f: () => void, what: string): void {
+  let threw = false;
+  try {
+    f();
+  } catch (e) {
+    threw = true;
+  }
+  if (!threw) fail(`expected an error: ${what}`);
+}
+
+function same(a: any, b: any, what: string): void {
+  if (JSON.stringify(a) !== JSON.stringify(b)) fail(`${what}: ${JSON.stringify(a)} != ${JSON.stringify(b)}`);
+}
+
+// The continuous-batching bookkeeping: FIFO admission into the lowest free slot, release and reuse,
+// the per-token advance, and the errors.
+function slotTableChecks(): void {
+  const t = new SlotTable(2, 10);
+  t.submit('a', 3);
+  t.submit('b', 0);
+  t.submit('c', 9);
+  same(t.admit(), ['a', 'b'], 'first admission');
+  same(t.activeIds(), ['a', 'b'], 'active');
+  same(t.waitingIds(), ['c'], 'waiting');
+  same([t.slotOf('a'), t.slotOf('b')], [0, 1], 'slots');
+  same(t.admit(), [], 'no free slot');
+  t.release('a');
+  same(t.admit(), ['c'], 'admission after release');
+  same(t.slotOf('c'), 0, 'freed slot reused');
+  same(t.activeIds(), ['b', 'c'], 'admission order');
+  throws(function () { t.submit('b', 1); }, 'duplicate id');
+  throws(function () { t.submit('d', 10); }, 'length beyond the cache');
+  throws(function () { t.submit('d', -1); }, 'negative length');
+  t.advance();
+  same([t.lengthOf('b'), t.lengthOf('c')], [1, 10], 'advance');
+  if (!t.isFull('c') || t.isFull('b')) fail('isFull');
+  throws(function () { t.advance(); }, 'advance past a full sequence');
+  same([t.lengthOf('b'), t.lengthOf('c')], [1, 10], 'a failed advance changes nothing');
+  throws(function () { t.release('zz'); }, 'unknown id');
+  t.submit('d', 2);
+  t.submit('e', 2);
+  t.release('d');
+  same(t.waitingIds(), ['e'], 'release of a waiting request');
+  t.release('b');
+  t.release('c');
+  same(t.admit(), ['e'], 'admission into an empty table');
+  same(t.slotOf('e'), 0, 'lowest free slot first');
+  throws(function () { t.lengthOf('b'); }, 'released sequence');
+  throws(function () { return new SlotTable(0, 4); }, 'zero capacity');
 }
 
 export function cpuChecks(): string[] {
@@ -55,6 +112,8 @@ export function cpuChecks(): string[] {
   }
   if (new Uniform([{ u: 1 }]).bytes.byteLength !== 16) fail('uniforms are padded to 16 bytes');
   done.push('uniform layout');
+  slotTableChecks();
+  done.push('slot table');
   if (typeof g4.version() !== 'string') fail('version');
   done.push('addon loaded: ' + g4.version());
   return done;
@@ -272,6 +331,94 @@ function linear(dir: string): string[] {
   return [`engine order: ${spec.rows.length} dispatches`, 'linear: 1 call', 'results written'];
 }
 
+interface BatchSpec {
+  nqh: number; nkh: number; hd: number; maxBatch: number; maxSeqLen: number; eps: number;
+  layers: { slidingWindow: number; theta: number; applyDivisor: number; kvSource: number; headDim: number }[];
+  steps: { release: string[]; submit: [string, number][]; admitted: string[] }[];
+  arrays: Record<string, number[]>;
+}
+
+function batch(dir: string): string[] {
+  const spec = JSON.parse(fs.readFileSync(path.join(dir, 'case.json'), 'utf8')) as BatchSpec;
+  const bin: Uint8Array = fs.readFileSync(path.join(dir, 'case.bin'));
+  const att = new HipAttention(loadAddon(), 0);
+  const bufs: DeviceBuffer[] = [];
+  function bytesOf(name: string): Uint8Array {
+    const r = spec.arrays[name];
+    if (!r) fail(`case.bin has no ${name}`);
+    return bin.subarray(r[0], r[0] + r[1]);
+  }
+  function upload(name: string): DeviceBuffer {
+    const data = bytesOf(name);
+    const b = att.createBuffer(data.byteLength);
+    att.writeBuffer(b, 0, data);
+    bufs.push(b);
+    return b;
+  }
+  const rfBytes = bytesOf('rf');
+  const rfBits = new Uint16Array(rfBytes.buffer.slice(rfBytes.byteOffset, rfBytes.byteOffset + rfBytes.byteLength));
+  const rf = upload('rf');
+  const layers = spec.layers.map(function (L, l) {
+    return {
+      slidingWindow: L.slidingWindow, theta: L.theta, applyDivisor: L.applyDivisor, kvSource: L.kvSource,
+      headDim: L.headDim, qWeight: upload('qw' + l), kWeight: upload('kw' + l), ropeFreqs: rf,
+      ropeInvFreq: att.ropeInvFreqHost(L.theta, L.headDim, L.applyDivisor, rfBits), eps: spec.eps,
+    };
+  });
+  const sched = new DecodeScheduler(att, {
+    shape: { numQHeads: spec.nqh, numKvHeads: spec.nkh, headDim: spec.hd }, layers: layers,
+    maxBatch: spec.maxBatch, maxSeqLen: spec.maxSeqLen,
+  });
+  const outs: Uint8Array[] = [];
+  let launches = 0;
+  spec.steps.forEach(function (st, si) {
+    st.release.forEach(function (id) { sched.release(id); });
+    st.submit.forEach(function (s) { sched.submit(s[0], s[1]); });
+    const admitted = sched.admit();
+    same(admitted, st.admitted, `step ${si}: admitted`);
+    admitted.forEach(function (id) {  // the prompt rows, as prefill would have left them
+      spec.layers.forEach(function (L, l) {
+        if (L.kvSource !== l) return;
+        const kc = bytesOf(`kc:${id}:${l}`), vc = bytesOf(`vc:${id}:${l}`);
+        if (kc.byteLength) att.writeBuffer(sched.kCache(id, l), 0, kc);
+        if (vc.byteLength) att.writeBuffer(sched.vCache(id, l), 0, vc);
+      });
+    });
+    spec.layers.forEach(function (_L, l) {
+      const ids = sched.activeIds();
+      const producer = spec.layers[l].kvSource === l;
+      ids.forEach(function (id) {  // attn.linearQKV's outputs (attn.linearQ's alone on consumer layers)
+        att.writeBuffer(sched.q(id, l), 0, bytesOf(`q:${si}:${id}:${l}`));
+        if (!producer) return;
+        att.writeBuffer(sched.k(id, l), 0, bytesOf(`k:${si}:${id}:${l}`));
+        att.writeBuffer(sched.v(id, l), 0, bytesOf(`v:${si}:${id}:${l}`));
+      });
+      if (sched.stepLayer(l) !== ids.length) fail('stepLayer count');
+      launches++;
+      ids.forEach(function (id) {
+        const o = sched.out(id, l);
+        const host = new Uint8Array(o.size);
+        att.readBuffer(o, 0, host);
+        outs.push(host);
+      });
+    });
+    sched.advance();
+  });
+  let total = 0;
+  for (const o of outs) total += o.byteLength;
+  const res = new Uint8Array(total);
+  let off = 0;
+  for (const o of outs) {
+    res.set(o, off);
+    off += o.byteLength;
+  }
+  fs.writeFileSync(path.join(dir, 'out.bin'), res);
+  sched.dispose();
+  for (const b of bufs) att.destroyBuffer(b);
+  att.dispose();
+  return [`${spec.steps.length} token steps`, `${launches} attnStep launches`, `${outs.length} outputs written`];
+}
+
 export function main(argv: string[]): void {
   const mode = argv[0];
   let done: string[];
@@ -280,6 +427,7 @@ export function main(argv: string[]): void {
   else if (mode === 'head') done = head(argv[1]);
   else if (mode === 'prefill') done = prefill(argv[1]);
   else if (mode === 'linear') done = linear(argv[1]);
-  else fail(`usage: run.js cpu | layer <dir> | prefill <dir> | head <dir> | linear <dir>`);
+  else if (mode === 'batch') done = batch(argv[1]);
+  else fail(`usage: run.js cpu | layer <dir> | prefill <dir> | head <dir> | linear <dir> | batch <dir>`);
   process.stdout.write(JSON.stringify({ ok: true, checks: done }) + '\n');
 }

@@ -272,19 +272,24 @@ int g4_rope_inv_freq_host(float theta, uint32_t head_dim, uint32_t apply_divisor
  * The whole attention block of one token for many layers or sequences in one
  * launch: per entry, q RMSNorm + RoPE, the current row's k (norm + RoPE) and v
  * (weightless norm), the f16 store of that row (store_kv = 1, KV-producer
- * layers; consumers pass their producer's cache and raw k/v with
- * store_kv = 0), and split-K attention over the attended rows with the
- * current row taken from registers. It replaces the dispatch sequence
+ * layers), and split-K attention over the attended rows with the current row
+ * taken from registers. KV-consumer layers (src/engine.ts:1518-1522) read
+ * their producer's cache with store_kv = 0, in one of two ways: with their
+ * producer's raw k/v and k_weight, when the producer's entry runs in the same
+ * launch (the current row is recomputed, bit-identical to the stored one); or
+ * with k, v and k_weight NULL, when the producer's step already stored the
+ * row (the engine's layer-by-layer order, where consumers project only q):
+ * the current row is then read from the cache like the others. It replaces the dispatch sequence
  * vNorm, fusedNormRopeQK, kvCacheStore, attnScore, softmax, attnOutput of
  * src/engine.ts:2056-2094. Unlike the reference kernels, q/k/v are read
  * only (the raw projections stay in their buffers); attnOut is written.
- * Work is split evenly over the GPU across all entries. head_dim 256,
- * up to 8 query heads per kv head. Prepare when the entries change (each
+ * Work is split evenly over the GPU across all entries. head_dim 256 or
+ * 512 (one per call), up to 8 query heads per kv head. Prepare when the entries change (each
  * token); run as often as wanted. */
 typedef struct g4_step_entry {
     const float* q;            /* raw projection [num_q_heads][head_dim] f32 */
-    const float* k;            /* raw projection [num_kv_heads][head_dim] f32 */
-    const float* v;
+    const float* k;            /* raw projection [num_kv_heads][head_dim] f32; NULL: the current row is */
+    const float* v;            /* already in the cache (k, v, k_weight all NULL, store_kv 0) */
     const uint16_t* q_weight;  /* attn_q_norm, f16 [head_dim] */
     const uint16_t* k_weight;  /* attn_k_norm, f16 [head_dim] */
     const uint16_t* rope_freqs; /* f16 divisor table, read when apply_divisor */

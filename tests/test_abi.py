@@ -174,3 +174,20 @@ def test_misaligned_out_rejected_on_host():
     plan = abi.DecodePlan()
     st, msg = _err(lambda L: L.g4_attn_step_prepare(C.byref(e), 1, 8, 1, 256, 256, n.value, C.byref(plan), None))
     assert st == abi.G4_EINVAL and "16-byte aligned" in msg
+
+
+def test_step_cached_row_entries_checked_on_host():
+    """A consumer entry whose producer already stored the current row passes k, v and k_weight all NULL
+    (and store_kv 0); a partial set, or store_kv without the raw k and v, is refused before any launch."""
+    lib = abi.load()
+    n = C.c_size_t(0)
+    assert lib.g4_attn_step_workspace_size(1, 8, 1, 256, C.byref(n)) == abi.G4_OK
+    plan = abi.DecodePlan()
+    for k, v, kw, store, want in [(256, None, 256, 0, "all set or all NULL"), (None, None, 256, 0, "all set or all NULL"),
+                                  (None, None, None, 1, "store_kv needs the raw k and v")]:
+        e = abi.StepEntry()
+        e.q = e.q_weight = e.k_cache = e.v_cache = e.out = 256
+        e.k, e.v, e.k_weight, e.store_kv = k, v, kw, store
+        e.seq_len, e.position, e.theta, e.scale, e.eps = 10, 9, 1e4, 1.0, 1e-6
+        st, msg = _err(lambda L: L.g4_attn_step_prepare(C.byref(e), 1, 8, 1, 256, 256, n.value, C.byref(plan), None))
+        assert st == abi.G4_EINVAL and want in msg, (k, v, kw, store, msg)

@@ -173,3 +173,102 @@ def test_linear_through_ts_host(tmp_path, n, rows):
     total = sum(rows)
     np.testing.assert_array_equal(got[:total], want)
     np.testing.assert_array_equal(got[total:], want)
+
+
+@pytest.mark.skipif(NODE is None, reason="node is not installed")
+def test_continuous_batching_through_ts_host(tmp_path):
+    """DecodeScheduler (host/scheduler.ts): sequences are submitted, admitted into three cache slots
+    (FIFO, lowest free slot), released and replaced over four token steps. Each step runs every layer
+    as one attnStep over the active sequences: a local head_dim-256 producer (window 40), a global
+    head_dim-512 producer, and a local consumer of layer 0 that projects only q and reads the row its
+    producer stored earlier in the same token. Every attnOut is checked against the oracle's decode
+    chain over the cache the oracle keeps for each sequence, within max-abs 2e-3."""
+    announce("TS host continuous batching")
+    layers = [dict(slidingWindow=40, theta=1e4, applyDivisor=0, kvSource=0, headDim=256),
+              dict(slidingWindow=0, theta=1e6, applyDivisor=1, kvSource=1, headDim=512),
+              dict(slidingWindow=40, theta=1e4, applyDivisor=0, kvSource=0, headDim=256)]
+    max_batch, max_seq = 3, 300
+    steps = [dict(release=[], submit=[["A", 100], ["B", 37], ["C", 250], ["D", 5]], admitted=["A", "B", "C"]),
+             dict(release=["B"], submit=[], admitted=["D"]),
+             dict(release=["A"], submit=[["E", 0]], admitted=["E"]),
+             dict(release=[], submit=[], admitted=[])]
+    arrays, blob = {}, bytearray()
+
+    def put(name, a):
+        b = np.ascontiguousarray(a).tobytes()
+        arrays[name] = [len(blob), len(b)]
+        blob.extend(b)
+
+    put("rf", ROPE)
+    qw = [f16_weight_bits(900 + l, L["headDim"]) for l, L in enumerate(layers)]
+    kw = [f16_weight_bits(950 + l, L["headDim"]) for l, L in enumerate(layers)]
+    for l in range(len(layers)):
+        put(f"qw{l}", qw[l])
+        put(f"kw{l}", kw[l])
+    producers = [l for l, L in enumerate(layers) if L["kvSource"] == l]
+    cache, length, active, waiting, expected = {}, {}, [], [], []
+    seed = 1000
+    for si, st in enumerate(steps):
+        for sid in st["release"]:
+            active.remove(sid)
+        waiting += st["submit"]
+        admitted = []
+        while waiting and len(active) < max_batch:
+            sid, n = waiting.pop(0)
+            active.append(sid)
+            admitted.append(sid)
+            length[sid] = n
+            for p in producers:
+                hd = layers[p]["headDim"]
+                kc = np.zeros((max_seq, NKH * hd), np.uint16)
+                vc = np.zeros((max_seq, NKH * hd), np.uint16)
+                if n:
+                    kc[:n] = cache_f16(seed, n, NKH, hd).reshape(n, -1)
+                    vc[:n] = cache_f16(seed + 1, n, NKH, hd).reshape(n, -1)
+                seed += 2
+                cache[(sid, p)] = [kc, vc]
+                put(f"kc:{sid}:{p}", kc[:n])
+                put(f"vc:{sid}:{p}", vc[:n])
+        assert admitted == st["admitted"]
+        for l, L in enumerate(layers):
+            hd, src = L["headDim"], L["kvSource"]
+            for sid in active:
+                pos = length[sid]
+                q = synth.normal(seed, NQH * hd) * 2.0
+                k = synth.normal(seed + 1, NKH * hd) * 2.0
+                v = synth.normal(seed + 2, NKH * hd) * 2.0
+                seed += 3
+                put(f"q:{si}:{sid}:{l}", q)
+                if src == l:
+                    put(f"k:{si}:{sid}:{l}", k)
+                    put(f"v:{si}:{sid}:{l}", v)
+                    k_ = orc.fused_per_head_norm_rope(k, kw[l], ROPE, NKH, hd, EPS, pos, L["theta"], L["applyDivisor"])
+                    v_ = orc.per_head_rms_norm_no_weight(v, NKH, hd, EPS)
+                    cache[(sid, l)][0][pos] = orc.f32_to_f16_bits(k_)
+                    cache[(sid, l)][1][pos] = orc.f32_to_f16_bits(v_)
+                q_ = orc.fused_per_head_norm_rope(q, qw[l], ROPE, NQH, hd, EPS, pos, L["theta"], L["applyDivisor"])
+                kc, vc = cache[(sid, src)]
+                seq = pos + 1
+                out = orc.attention_chain(q_, orc.f16_bits_to_f32(kc[:seq]).reshape(-1),
+                                          orc.f16_bits_to_f32(vc[:seq]).reshape(-1), NQH, NKH, hd, seq, 1.0,
+                                          L["slidingWindow"])
+                expected.append((si, l, sid, out))
+        for sid in active:
+            length[sid] += 1
+    (tmp_path / "case.bin").write_bytes(bytes(blob))
+    (tmp_path / "case.json").write_text(json.dumps(dict(nqh=NQH, nkh=NKH, hd=256, maxBatch=max_batch,
+                                                        maxSeqLen=max_seq, eps=EPS, layers=layers, steps=steps,
+                                                        arrays=arrays)))
+    r = subprocess.run([NODE, str(RUN), "batch", str(tmp_path)], cwd=ROOT, capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 0, r.stderr
+    got = np.frombuffer((tmp_path / "out.bin").read_bytes(), np.float32)
+    off, worst = 0, 0.0
+    for si, l, sid, want in expected:
+        g = got[off:off + want.size]
+        off += want.size
+        err = max_abs(g, want)
+        worst = max(worst, err)
+        assert np.isfinite(g).all() and err <= 2e-3, (si, l, sid, err)
+    assert off == got.size
+    print(f"continuous batching: {len(expected)} outputs, worst max-abs {worst:.2e}")

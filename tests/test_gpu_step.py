@@ -184,6 +184,28 @@ def test_step_kv_consumer_layer(dev):
     assert np.isfinite(got).all() and max_abs(got, want_c) <= TOL
 
 
+@pytest.mark.parametrize("seq,win,theta,div,hd", [(3000, 0, 1e6, 1, 256), (1, 0, 1e4, 0, 256), (700, 512, 1e4, 0, 256),
+                                                 (40000, 0, 1e6, 1, 256), (5000, 0, 1e6, 1, 512)])
+def test_step_kv_consumer_after_producer(dev, seq, win, theta, div, hd):
+    """The engine's layer-by-layer order: the producer's step stores the current row, then the consumer's
+    step (a launch of its own, k, v and k_weight NULL) reads that row from the cache like the others."""
+    announce(f"attnStep consumer after producer seq={seq} win={win} hd={hd}")
+    prod = Layer(dev, 17 + seq, seq, win, theta, div, hd=hd)
+    cons = Layer(dev, 18 + seq, seq, win, theta, div, cache=(prod.kc, prod.vc), hd=hd)
+    run_step(dev, [prod.entry()], hd=hd)
+    want_p, kb, vb = prod.expected()
+    check(prod, want_p, kb, vb, "producer")
+    e = cons.entry(store=False)
+    e["k"] = e["v"] = e["k_weight"] = None
+    run_step(dev, [e], hd=hd)
+    want_c, _, _ = cons.expected(kv_from=prod)
+    got = cons.out.cpu().numpy()
+    err = max_abs(got, want_c)
+    assert np.isfinite(got).all() and err <= TOL, err
+    np.testing.assert_array_equal(prod.kc[prod.pos].cpu().numpy().view(np.uint16), kb)  # not stored again
+    print(f"consumer after producer seq={seq} hd={hd}: err={err:.2e}")
+
+
 def test_step_replay_is_deterministic(dev):
     """A prepared plan replays (merge counters reset themselves) and gives identical bits each time."""
     announce("attnStep replay")
