@@ -244,6 +244,79 @@ napi_value Download(napi_env env, napi_callback_info info) {
     return undefined(env);
 }
 
+// readAsync(src, offset, out, stream) -> Promise<void>: mapAsync's shape. The
+// copy is enqueued now, on the stream (ordered after what is already there,
+// and before anything enqueued later); the wait and the copy into `out` run on
+// a worker thread, and the promise settles on the JS thread. `out` is held by
+// a reference until then.
+struct ReadWork {
+    napi_async_work work = nullptr;
+    napi_deferred deferred = nullptr;
+    napi_ref out_ref = nullptr;
+    g4_readback* handle = nullptr;
+    void* dst = nullptr;
+    int status = G4_OK;
+    std::string msg;
+};
+
+void read_execute(napi_env, void* data) {
+    ReadWork* w = static_cast<ReadWork*>(data);
+    w->status = g4_readback_finish(w->handle, w->dst);
+    if (w->status != G4_OK) w->msg = g4_last_error();
+}
+
+void read_complete(napi_env env, napi_status st, void* data) {
+    ReadWork* w = static_cast<ReadWork*>(data);
+    if (st == napi_ok && w->status == G4_OK) {
+        napi_value u;
+        napi_get_undefined(env, &u);
+        napi_resolve_deferred(env, w->deferred, u);
+    } else {
+        if (st != napi_ok && w->status == G4_OK) {  // cancelled before it ran: the handle is still open
+            g4_readback_finish(w->handle, nullptr);
+            w->msg = "readAsync: cancelled";
+        }
+        const std::string text = "g4attn status " + std::to_string(w->status) + ": " + w->msg;
+        napi_value m, err;
+        napi_create_string_utf8(env, text.c_str(), NAPI_AUTO_LENGTH, &m);
+        napi_create_error(env, nullptr, m, &err);
+        napi_reject_deferred(env, w->deferred, err);
+    }
+    napi_delete_reference(env, w->out_ref);
+    napi_delete_async_work(env, w->work);
+    delete w;
+}
+
+napi_value ReadAsync(napi_env env, napi_callback_info info) {
+    Args a(env, info, 4);
+    void* src = a.ptr(0);
+    const double off = a.f64(1);
+    void* d = nullptr;
+    size_t n = 0;
+    a.bytes(2, &d, &n);
+    void* s = a.ptr(3);
+    if (!a.ok) return nullptr;
+    g4_readback* h = nullptr;
+    CALL(env, g4_readback_begin(src, (size_t)off, n, s, &h));
+    ReadWork* w = new ReadWork;
+    w->handle = h;
+    w->dst = d;
+    napi_value promise, name;
+    if (napi_create_reference(env, a.v[2], 1, &w->out_ref) != napi_ok ||
+        napi_create_promise(env, &w->deferred, &promise) != napi_ok ||
+        napi_create_string_utf8(env, "g4attn.readAsync", NAPI_AUTO_LENGTH, &name) != napi_ok ||
+        napi_create_async_work(env, nullptr, name, read_execute, read_complete, w, &w->work) != napi_ok ||
+        napi_queue_async_work(env, w->work) != napi_ok) {
+        g4_readback_finish(h, nullptr);  // the copy finishes; nothing waits for it
+        if (w->out_ref) napi_delete_reference(env, w->out_ref);
+        if (w->work) napi_delete_async_work(env, w->work);
+        delete w;
+        napi_throw_error(env, nullptr, "readAsync: could not queue the wait");
+        return nullptr;
+    }
+    return promise;
+}
+
 napi_value Zero(napi_env env, napi_callback_info info) {
     Args a(env, info, 3);
     void* p = a.ptr(0);
@@ -800,6 +873,7 @@ napi_value Init(napi_env env, napi_value exports) {
         {"free", Free},
         {"upload", Upload},
         {"download", Download},
+        {"readAsync", ReadAsync},
         {"zero", Zero},
         {"fusedPerHeadNormRope", FusedPerHeadNormRope},
         {"perHeadRmsNormNoWeight", PerHeadRmsNormNoWeight},

@@ -104,4 +104,47 @@ int g4_download(void* host_dst, const void* dev_src, size_t offset, size_t bytes
     return G4_OK;
 }
 
+// Readback in two halves (the engine's copyBufferToBuffer into a staging
+// buffer, then mapAsync, src/engine.ts:2309): `begin` enqueues the copy into
+// pinned staging memory on the stream, so it is ordered with the work already
+// enqueued there, and records an event; `finish` (from any thread) waits for
+// the event, copies the bytes out and frees the staging memory.
+struct g4_readback {
+    void* staging;
+    size_t bytes;
+    hipEvent_t done;
+};
+
+int g4_readback_begin(const void* dev_src, size_t offset, size_t bytes, void* stream, g4_readback** handle) {
+    if (!handle) return fail(G4_EINVAL, "g4_readback_begin: handle is NULL");
+    *handle = nullptr;
+    if (!dev_src || bytes == 0) return fail(G4_EINVAL, "g4_readback_begin: NULL source or zero bytes");
+    g4_readback* r = new g4_readback{nullptr, bytes, nullptr};
+    hipError_t e = hipHostMalloc(&r->staging, bytes, hipHostMallocDefault);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&r->done, hipEventDisableTiming);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(r->staging, static_cast<const char*>(dev_src) + offset, bytes, hipMemcpyDeviceToHost,
+                           as_stream(stream));
+    if (e == hipSuccess) e = hipEventRecord(r->done, as_stream(stream));
+    if (e != hipSuccess) {
+        if (r->done) (void)hipEventDestroy(r->done);
+        if (r->staging) (void)hipHostFree(r->staging);
+        delete r;
+        return hip_fail(e, "g4_readback_begin");
+    }
+    *handle = r;
+    return G4_OK;
+}
+
+int g4_readback_finish(g4_readback* handle, void* host_dst) {
+    if (!handle) return fail(G4_EINVAL, "g4_readback_finish: handle is NULL");
+    hipError_t e = hipEventSynchronize(handle->done);
+    if (e == hipSuccess && host_dst) memcpy(host_dst, handle->staging, handle->bytes);
+    (void)hipEventDestroy(handle->done);
+    (void)hipHostFree(handle->staging);
+    delete handle;
+    if (e != hipSuccess) return hip_fail(e, "g4_readback_finish");
+    return G4_OK;
+}
+
 }  // extern "C"

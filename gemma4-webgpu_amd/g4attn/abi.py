@@ -127,6 +127,8 @@ SIGNATURES: dict[str, list] = {
     "g4_free": [_P],
     "g4_upload": [_P, _SZ, _P, _SZ, _P],
     "g4_download": [_P, _P, _SZ, _SZ, _P],
+    "g4_readback_begin": [_P, _SZ, _SZ, _P, C.POINTER(_P)],
+    "g4_readback_finish": [_P, _P],
     "g4_zero": [_P, _SZ, _P],
     "g4_fused_per_head_norm_rope": [_P, _P, _P, NormRopeParams, _P],
     "g4_per_head_rms_norm_no_weight": [_P, NormParams, _P],

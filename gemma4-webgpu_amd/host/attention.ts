@@ -177,6 +177,7 @@ export interface Addon {
   free(p: bigint): void;
   upload(dst: bigint, offset: number, data: any, s: bigint): void;
   download(src: bigint, offset: number, out: any, s: bigint): void;
+  readAsync(src: bigint, offset: number, out: any, s: bigint): Promise<void>;
   zero(p: bigint, bytes: number, s: bigint): void;
   fusedPerHeadNormRope(data: bigint, w: bigint, rf: bigint, p: Uint8Array, s: bigint): void;
   perHeadRmsNormNoWeight(data: bigint, p: Uint8Array, s: bigint): void;
@@ -256,6 +257,16 @@ export class HipAttention {
   readBuffer(b: DeviceBuffer, offset: number, out: ArrayBufferView): void {
     if (offset + out.byteLength > b.size) throw new RangeError(`readBuffer: ${offset}+${out.byteLength} > ${b.size}`);
     this.g4.download(b.ptr, offset, out, this.stream);
+  }
+
+  // mapAsync's shape: the copy is ordered on the stream now (after the work already enqueued, before
+  // anything enqueued later); the promise resolves once `out` holds the bytes. The wait runs off the
+  // JS thread.
+  readBufferAsync(b: DeviceBuffer, offset: number, out: ArrayBufferView): Promise<void> {
+    if (offset + out.byteLength > b.size) {
+      return Promise.reject(new RangeError(`readBufferAsync: ${offset}+${out.byteLength} > ${b.size}`));
+    }
+    return this.g4.readAsync(b.ptr, offset, out, this.stream);
   }
 
   clearBuffer(b: DeviceBuffer): void {

@@ -14,6 +14,9 @@
 //                                   steps of a DecodeScheduler, one attnStep per layer over the active
 //                                   sequences; every attnOut goes to <dir>/out.bin, in step, layer and
 //                                   admission order.
+//   node host/run.js readback <dir> f32 values from <dir>/case.bin: logitSoftcap in place, then two
+//                                   readBufferAsync calls around a clearBuffer; both results (the
+//                                   softcapped values, then zeros) go to <dir>/out.bin.
 //   node host/run.js linear <dir>   the projections from <dir>/case.json + case.bin: one matmulQuant
 //                                   dispatch per weight matrix (attn.linearQKV, src/engine.ts:2045-2051),
 //                                   then one linear call over all of them; results go to <dir>/out.bin.
@@ -419,8 +422,42 @@ function batch(dir: string): string[] {
   return [`${spec.steps.length} token steps`, `${launches} attnStep launches`, `${outs.length} outputs written`];
 }
 
+// Promise readback: each copy is ordered where it was issued on the stream, whatever enqueues follow it.
+function readback(dir: string): Promise<string[]> {
+  const bin: Uint8Array = fs.readFileSync(path.join(dir, 'case.bin'));
+  const n = bin.byteLength / 4;
+  const att = new HipAttention(loadAddon(), 0);
+  const b = att.createBuffer(bin.byteLength);
+  att.writeBuffer(b, 0, bin);
+  att.dispatch('logitSoftcap', [b], new Uniform([{ u: n }, { f: 30.0 }]));
+  const first = new Uint8Array(bin.byteLength), second = new Uint8Array(bin.byteLength);
+  const p1 = att.readBufferAsync(b, 0, first);  // after the softcap
+  att.clearBuffer(b);                           // enqueued after the first copy: not in `first`
+  const p2 = att.readBufferAsync(b, 0, second);
+  const tooLong = att.readBufferAsync(b, 8, new Uint8Array(bin.byteLength)).then(
+    function () { fail('readBufferAsync past the end resolved'); }, function () { return 'range error rejected'; });
+  return Promise.all([p1, p2, tooLong]).then(function (r) {
+    const res = new Uint8Array(2 * bin.byteLength);
+    res.set(first, 0);
+    res.set(second, bin.byteLength);
+    fs.writeFileSync(path.join(dir, 'out.bin'), res);
+    att.destroyBuffer(b);
+    att.dispose();
+    return ['2 promise readbacks around a clear', r[2] as string, 'results written'];
+  });
+}
+
 export function main(argv: string[]): void {
   const mode = argv[0];
+  if (mode === 'readback') {
+    readback(argv[1]).then(function (done) {
+      process.stdout.write(JSON.stringify({ ok: true, checks: done }) + '\n');
+    }, function (e) {
+      process.stderr.write(String(e && e.stack ? e.stack : e) + '\n');
+      process.exitCode = 1;
+    });
+    return;
+  }
   let done: string[];
   if (mode === 'cpu') done = cpuChecks();
   else if (mode === 'layer') done = layer(argv[1]);
@@ -428,6 +465,6 @@ export function main(argv: string[]): void {
   else if (mode === 'prefill') done = prefill(argv[1]);
   else if (mode === 'linear') done = linear(argv[1]);
   else if (mode === 'batch') done = batch(argv[1]);
-  else fail(`usage: run.js cpu | layer <dir> | prefill <dir> | head <dir> | linear <dir> | batch <dir>`);
+  else fail(`usage: run.js cpu | layer <dir> | prefill <dir> | head <dir> | linear <dir> | batch <dir> | readback <dir>`);
   process.stdout.write(JSON.stringify({ ok: true, checks: done }) + '\n');
 }

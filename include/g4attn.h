@@ -63,6 +63,15 @@ int g4_free(void* dev_ptr);
 int g4_upload(void* dev_dst, size_t offset, const void* host_src, size_t bytes, void* stream);
 /* copyBufferToBuffer + mapAsync: device -> host; returns after the copy is done. */
 int g4_download(void* host_dst, const void* dev_src, size_t offset, size_t bytes, void* stream);
+/* The same readback in two halves, for callers that wait off their issuing
+ * thread (mapAsync's promise): begin enqueues the copy into pinned staging
+ * memory on `stream`, ordered after the work already enqueued there, and
+ * returns a handle; finish, from any thread, waits for that copy, writes the
+ * bytes to host_dst (NULL: discard them) and releases the handle. Every
+ * begun readback must be finished exactly once. */
+typedef struct g4_readback g4_readback;
+int g4_readback_begin(const void* dev_src, size_t offset, size_t bytes, void* stream, g4_readback** handle);
+int g4_readback_finish(g4_readback* handle, void* host_dst);
 /* Zero `bytes` at dev_dst with a fill kernel (safe inside HIP graph capture). */
 int g4_zero(void* dev_dst, size_t bytes, void* stream);
 

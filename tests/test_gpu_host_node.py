@@ -272,3 +272,20 @@ def test_continuous_batching_through_ts_host(tmp_path):
         assert np.isfinite(g).all() and err <= 2e-3, (si, l, sid, err)
     assert off == got.size
     print(f"continuous batching: {len(expected)} outputs, worst max-abs {worst:.2e}")
+
+
+@pytest.mark.skipif(NODE is None, reason="node is not installed")
+def test_promise_readback_through_ts_host(tmp_path):
+    """readBufferAsync (mapAsync's shape): the copy is ordered where it was issued, so the values read
+    before a later clearBuffer are the soft-capped ones (bit-identical to the oracle), and those read
+    after it are zeros; a read past the end rejects."""
+    announce("TS host promise readback")
+    x = np.random.default_rng(4).standard_normal(300000, dtype=np.float32) * 400.0
+    (tmp_path / "case.bin").write_bytes(x.tobytes())
+    r = subprocess.run([NODE, str(RUN), "readback", str(tmp_path)], cwd=ROOT, capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 0, r.stderr
+    assert '"ok":true' in r.stdout
+    got = np.frombuffer((tmp_path / "out.bin").read_bytes(), np.uint32)
+    np.testing.assert_array_equal(got[:x.size], orc.logit_softcap(x, 30.0).view(np.uint32))
+    assert not got[x.size:].any()
