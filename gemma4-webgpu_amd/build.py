@@ -50,10 +50,15 @@ def _run(cmd: list[str]) -> None:
         print(out, file=sys.stderr)
 
 
+# Per-file code generation options. prefill.hip: MFMA accumulators in VGPRs (the
+# pipelined prefill rescales them with plain VALU; its q operand is kept in AGPRs).
+FILE_FLAGS = {"prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def _compile(src: Path) -> Path:
     obj = OBJ / (src.name + ".o")
     lang = [] if src.suffix == ".hip" else ["-x", "hip"]
-    _run([HIPCC, *HIP_FLAGS, *lang, "-c", str(src), "-o", str(obj)])
+    _run([HIPCC, *HIP_FLAGS, *FILE_FLAGS.get(src.name, []), *lang, "-c", str(src), "-o", str(obj)])
     return obj
 
 

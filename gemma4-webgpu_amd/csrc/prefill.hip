@@ -49,6 +49,7 @@ constexpr int kPfWaves = 4;
 constexpr int kPfThreads = 64 * kPfWaves;
 constexpr int kPfRows = 32 * kPfWaves;   // q-rows per tile
 constexpr int kPfKeys = 32;              // keys per tile
+constexpr float kPfLazy = 8.0f;          // lazy-rescale threshold (log2 units): probabilities <= 256
 constexpr int kKRowBytes = kPfHD * 2 + 16;       // padded K row in LDS
 constexpr int kVtRowBytes = kPfKeys * 2 + 16;    // padded V^T row (one d) in LDS
 
@@ -61,6 +62,9 @@ struct PrefillEntryDev {
     uint32_t start;       // position of token 0
     uint32_t window;      // 0 = full
     float qscale;         // scale * log2(e)
+    const uint16_t* vt;   // V^T in 32-key blocks [kv head][block][HD][32] (pipelined kernel)
+    uint32_t vt_blocks;   // blocks per kv head
+    uint32_t pad;
 };
 
 // One workgroup: tile `tile` of entry `entry`, keys [key_begin, key_end).
@@ -221,15 +225,21 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_prefill(PrefillArgs a) {
             tmax = fmaxf(tmax, x[r]);
         }
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-        const float m_new = fmaxf(m_run, tmax);
-        if (__any(m_new > m_run)) {
-            const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+        // Lazy rescale: the reference max moves only when the tile's max exceeds it by more than
+        // kPfLazy (log2 units), so probabilities stay below 2^kPfLazy and the accumulators (in AGPRs:
+        // a rescale is a read, multiply and write of all 128) are rescaled a few times per row
+        // instead of on nearly every tile. From -inf the first finite max always moves it.
+        const bool move = tmax > m_run + kPfLazy;
+        if (__any(move)) {
+            const float m_new = move ? tmax : m_run;
+            // 0 from -inf (acc and l are 0 there); 1 on lanes that keep their max
+            const float alpha = move ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
             l_run *= alpha;
 #pragma unroll
             for (int b = 0; b < 8; b++) acc[b] *= alpha;
+            m_run = m_new;
         }
-        m_run = m_new;
-        const float mu = m_new == -INFINITY ? 0.0f : m_new;
+        const float mu = m_run == -INFINITY ? 0.0f : m_run;
         f16x8 pop[2];
 #pragma unroll
         for (int r = 0; r < 16; r++) {
@@ -279,6 +289,273 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_prefill(PrefillArgs a) {
     if (half == 0) stg<f32x2>(a.part_ml + rec * 2, f32x2{m_run, L});
 }
 
+// ---- pipelined form: LDS-DMA tiles, pre-transposed V ----------------------
+//
+// The same per-tile arithmetic, fed differently: K rows and V^T blocks go from
+// global memory straight into LDS (global_load_lds_dwordx4, no register
+// staging), kPfStages tiles deep, one barrier per tile. V is transposed once
+// per prefill call into 32-key blocks [HD][32] (k_vt_blocks), so a V^T tile is
+// one contiguous 16 KiB read. The 16-byte chunks of both LDS tiles are
+// XOR-swizzled so that the MFMA operand reads (eight lanes per LDS cycle, each
+// a different row) hit distinct banks.
+
+constexpr int kPfStages = 4;
+constexpr unsigned kPfTileBytes = kPfKeys * kPfHD * 2;  // one K tile, or one V^T tile: 16 KiB
+
+struct PrefillDmaSmem {
+    unsigned char k[kPfStages][kPfTileBytes];   // key row r: chunk c (8 d) at r*512 + ((c ^ swz_k(r)) * 16)
+    unsigned char vt[kPfStages][kPfTileBytes];  // d row: chunk c (8 keys) at d*64 + ((c ^ swz_v(d)) * 16)
+};
+
+__device__ __forceinline__ unsigned swz_k(unsigned r) { return (r & 3u) | ((r >> 1) & 4u); }
+__device__ __forceinline__ unsigned swz_v(unsigned d) { return (d >> 1) & 3u; }
+
+// One LDS-DMA instruction: lane j copies 16 bytes from its global address to
+// LDS byte address lds + 16 j (lds wave-uniform). M0 carries the LDS base and
+// is restored afterwards. Completion is counted by vmcnt, which the compiler
+// does not track for this statement: the pipeline waits for it explicitly.
+__device__ __forceinline__ void lds_dma16(const void* gaddr, uint32_t lds) {
+    uint32_t saved;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+                 : "=&s"(saved)
+                 : "v"(gaddr), "s"(lds)
+                 : "memory");
+}
+
+// Waits until at most `younger` tiles' DMAs of this wave are still in flight
+// (8 instructions per tile), then joins the workgroup's barrier.
+__device__ __forceinline__ void dma_wait_barrier(int younger) {
+    if (younger >= 2)
+        asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
+    else if (younger == 1)
+        asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
+    else
+        asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// This wave's share of tile `kt0` (32-aligned): K rows 8w .. 8w+7 (2 per
+// instruction) and V^T rows 64w .. 64w+63 (16 per instruction).
+__device__ __forceinline__ void dma_tile(PrefillDmaSmem& sm, int st, int wave, int lane, const char* Kb,
+                                         uint32_t row_bytes, unsigned kt0, unsigned last, const char* vtb) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const unsigned inst = 4u * wave + i;
+        const unsigned r = 2u * inst + (unsigned)(lane >> 5);
+        const unsigned c = ((unsigned)lane & 31u) ^ swz_k(r);
+        const unsigned row = min(kt0 + r, last);
+        lds_dma16(Kb + ((uint64_t)row * row_bytes + c * 16u),
+                  __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sm.k[st][inst * 1024u]));
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const unsigned inst = 4u * wave + i;
+        const unsigned d = 16u * inst + (unsigned)(lane >> 2);
+        const unsigned c = ((unsigned)lane & 3u) ^ swz_v(d);
+        lds_dma16(vtb + (d * 64u + c * 16u),
+                  __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sm.vt[st][inst * 1024u]));
+    }
+}
+
+__global__ __launch_bounds__(kPfThreads, 1) void k_prefill_dma(PrefillArgs a) {
+    __shared__ PrefillDmaSmem sm;
+    const PrefillWorkDev wk = a.work[blockIdx.x];
+    const PrefillEntryDev& ent = a.table[wk.entry];
+    const unsigned kvh = blockIdx.y;
+    const unsigned G = a.group, NQH = a.num_q_heads, NKH = a.num_kv_heads;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int half = lane >> 5;
+    const int col = lane & 31;
+
+    const unsigned rho = (unsigned)wk.tile * kPfRows + (unsigned)wave * 32u + (unsigned)col;
+    const unsigned tok = rho / G, head = rho % G;
+    const bool row_live = tok < ent.n_tokens;
+    const unsigned tok_c = row_live ? tok : ent.n_tokens - 1;
+    const unsigned pos = ent.start + tok_c;
+    const unsigned lo = (ent.window != 0 && pos + 1 > ent.window) ? pos + 1 - ent.window : 0u;
+    const unsigned hi = row_live ? pos : 0u;
+    const bool dead = !row_live;
+    // Tiles inside [lo, hi] of every row of the wave need no mask (most tiles of a long prefix).
+    unsigned wave_lo = lo, wave_hi = dead ? 0u : hi;
+    for (int off = 32; off > 0; off >>= 1) {
+        wave_lo = max(wave_lo, (unsigned)__shfl_xor((int)wave_lo, off));
+        wave_hi = min(wave_hi, (unsigned)__shfl_xor((int)wave_hi, off));
+    }
+
+    f16x8 qop[16];
+    {
+        const uint16_t* qr = ent.q + ((uint64_t)tok_c * NQH + kvh * G + head) * kPfHD + 8 * half;
+#pragma unroll
+        for (int s = 0; s < 16; s++) qop[s] = ldg<f16x8>(qr + 16 * s);
+        // Wait for q here, before any DMA is issued (the compiler's own wait for these loads would
+        // otherwise also wait for every DMA in flight at the first MFMA), and keep it in AGPRs: the
+        // score MFMA reads its B operand from there, and the VGPRs hold the output accumulators
+        // (this file is compiled with MFMA accumulators in VGPRs, so that their rescale is plain VALU).
+#pragma unroll
+        for (int s = 0; s < 16; s++) asm volatile("" : "+a"(qop[s]));
+    }
+
+    const uint32_t row_bytes = NKH * kPfHD * 2u;
+    const char* Kb = reinterpret_cast<const char*>(ent.k + (uint64_t)kvh * kPfHD);
+    const char* VTb = reinterpret_cast<const char*>(ent.vt + (uint64_t)kvh * ent.vt_blocks * (kPfHD * 32));
+    const unsigned kb = wk.key_begin, ke = wk.key_end, last = ke - 1;  // kb is 32-aligned
+    const int n_tiles = (int)((ke - kb + kPfKeys - 1) / kPfKeys);
+    const float qs = ent.qscale;
+
+#pragma unroll
+    for (int p = 0; p < kPfStages - 1; p++)
+        if (p < n_tiles) {
+            const unsigned kt0 = kb + (unsigned)p * kPfKeys;
+            dma_tile(sm, p, wave, lane, Kb, row_bytes, kt0, last, VTb + (uint64_t)(kt0 >> 5) * kPfTileBytes);
+        }
+
+    float m_run = -INFINITY, l_run = 0.0f;
+    f32x16 acc[8];
+#pragma unroll
+    for (int b = 0; b < 8; b++) acc[b] = f32x16{};
+    // LDS operand addresses inside a stage: K chunk c = 2s + half of row krow; V^T chunk 2s + half of row 32b + col.
+    const unsigned krow = key_of_row((unsigned)col);
+    const unsigned kx = swz_k(krow), vx = swz_v((unsigned)col);
+    unsigned koff[4];
+#pragma unroll
+    for (int b = 0; b < 4; b++) koff[b] = krow * 512u + ((((unsigned)(2 * b + half)) ^ kx) << 4);
+    unsigned voff[2];
+#pragma unroll
+    for (int s = 0; s < 2; s++) voff[s] = (unsigned)col * 64u + ((((unsigned)(2 * s + half)) ^ vx) << 4);
+
+    for (int it = 0; it < n_tiles; it++) {
+        const int st = it % kPfStages;
+        const unsigned kt0 = kb + (unsigned)it * kPfKeys;
+        dma_wait_barrier(min(n_tiles - 1 - it, kPfStages - 2));
+        if (it + kPfStages - 1 < n_tiles) {  // into the stage every wave finished with (tile it - 1)
+            const unsigned kn = kt0 + (kPfStages - 1) * kPfKeys;
+            dma_tile(sm, (it + kPfStages - 1) % kPfStages, wave, lane, Kb, row_bytes, kn, last,
+                     VTb + (uint64_t)(kn >> 5) * kPfTileBytes);
+        }
+
+        const unsigned char* kbuf = sm.k[st];
+        f32x16 s0 = f32x16{};
+#pragma unroll
+        for (int s = 0; s < 16; s++) {
+            const f16x8 k0 = *reinterpret_cast<const f16x8*>(kbuf + koff[s & 3] + 128u * (s >> 2));
+            s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(k0, qop[s], s0, 0, 0, 0);
+        }
+        float x[16];
+        float tmax = -INFINITY;
+        if (kt0 >= wave_lo && kt0 + (kPfKeys - 1) <= wave_hi) {  // uniform: no key of the tile is masked
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                x[r] = s0[r] * qs;
+                tmax = fmaxf(tmax, x[r]);
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const unsigned key = kt0 + 16u * (r >> 3) + 8u * half + (r & 7);
+                const bool ok = !dead && key >= lo && key <= hi;
+                x[r] = ok ? s0[r] * qs : -INFINITY;
+                tmax = fmaxf(tmax, x[r]);
+            }
+        }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+        const bool move = tmax > m_run + kPfLazy;
+        const bool rescale = __any(move);
+        float alpha = 1.0f;
+        if (rescale) {
+            const float m_new = move ? tmax : m_run;
+            alpha = move ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
+            l_run *= alpha;
+            m_run = m_new;
+        }
+        const float mu = m_run == -INFINITY ? 0.0f : m_run;
+        f16x8 pop[2];
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const float p = __builtin_amdgcn_exp2f(x[r] - mu);
+            l_run += p;
+            pop[r >> 3][r & 7] = (f16)p;
+        }
+        if (rescale) {
+#pragma unroll
+            for (int b = 0; b < 8; b++) acc[b] *= alpha;
+        }
+        const unsigned char* vbuf = sm.vt[st];
+#pragma unroll
+        for (int b = 0; b < 8; b++) {
+#pragma unroll
+            for (int s = 0; s < 2; s++) {
+                const f16x8 vop = *reinterpret_cast<const f16x8*>(vbuf + voff[s] + 2048u * b);
+                acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vop, pop[s], acc[b], 0, 0, 0);
+            }
+        }
+    }
+
+    const float L = l_run + __shfl_xor(l_run, 32);
+    if (dead) return;
+    const uint64_t qrow = (uint64_t)tok * NQH + kvh * G + head;
+    if (wk.n_parts == 1) {
+        float* dst = ent.out + qrow * kPfHD + 4 * half;
+        const float inv = 1.0f / L;
+#pragma unroll
+        for (int b = 0; b < 8; b++)
+#pragma unroll
+            for (int g = 0; g < 4; g++)
+                stg<f32x4>(dst + 32 * b + 8 * g, f32x4{acc[b][4 * g] * inv, acc[b][4 * g + 1] * inv,
+                                                      acc[b][4 * g + 2] * inv, acc[b][4 * g + 3] * inv});
+        return;
+    }
+    const unsigned tile_tok0 = (unsigned)wk.tile * kPfRows / G;
+    const uint64_t slot = (uint64_t)wk.split_base + (uint64_t)(tok - tile_tok0) * wk.n_parts + wk.part;
+    const uint64_t rec = (slot * NKH + kvh) * G + head;
+    float* po = a.part_o + rec * kPfHD + 4 * half;
+#pragma unroll
+    for (int b = 0; b < 8; b++)
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+            stg<f32x4>(po + 32 * b + 8 * g, f32x4{acc[b][4 * g], acc[b][4 * g + 1], acc[b][4 * g + 2], acc[b][4 * g + 3]});
+    if (half == 0) stg<f32x2>(a.part_ml + rec * 2, f32x2{m_run, L});
+}
+
+// V of one cache in 32-key blocks [kv head][block][HD][32] (f16): block j holds
+// rows 32 j .. 32 j + 31 (rows past the cache's end repeat its last row).
+struct VtCacheDev {
+    const uint16_t* v;   // f16 [rows][num_kv_heads][HD]
+    uint16_t* vt;
+    uint32_t rows;
+    uint32_t blocks;
+    uint32_t block0;     // first global block index of this cache in the launch
+    uint32_t pad;
+};
+
+__global__ __launch_bounds__(256) void k_vt_blocks(const VtCacheDev* caches, uint32_t n_caches, uint32_t nkh) {
+    __shared__ __attribute__((aligned(16))) uint16_t tb[kPfKeys][kPfHD + 8];
+    unsigned c = 0;
+    while (c + 1 < n_caches && blockIdx.x >= caches[c + 1].block0) c++;
+    const VtCacheDev cd = caches[c];
+    const unsigned blk = blockIdx.x - cd.block0;
+    const unsigned kvh = blockIdx.y;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const unsigned piece = threadIdx.x + 256u * i;  // 32 keys x 32 chunks of 8 d
+        const unsigned key = piece >> 5, ch = piece & 31u;
+        const unsigned row = min(blk * 32u + key, cd.rows - 1);
+        const u32x4 x = ldg<u32x4>(cd.v + ((uint64_t)row * nkh + kvh) * kPfHD + ch * 8u);
+        *reinterpret_cast<u32x4*>(&tb[key][ch * 8u]) = x;
+    }
+    __syncthreads();
+    uint16_t* dst = cd.vt + ((uint64_t)kvh * cd.blocks + blk) * (kPfHD * 32);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const unsigned piece = threadIdx.x + 256u * i;  // 256 d x 4 chunks of 8 keys
+        const unsigned d = piece >> 2, kc = piece & 3u;
+        u32x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            o[e] = (uint32_t)tb[8 * kc + 2 * e][d] | ((uint32_t)tb[8 * kc + 2 * e + 1][d] << 16);
+        stg<u32x4>(dst + d * 32u + kc * 8u, o);
+    }
+}
+
 }  // namespace g4
 
 using namespace g4;
@@ -304,6 +581,9 @@ struct PrefillPlanRep {
     uint32_t num_kv_heads;
     uint32_t magic;
     uint32_t off_work, off_merge, off_ml, off_o;  // workspace byte offsets (workspaces stay under 4 GiB)
+    uint32_t off_vtc;      // V^T cache table (pipelined form)
+    uint32_t n_vtc;        // caches to transpose (0: the register-staged form)
+    uint32_t vt_blocks;    // their 32-key blocks, in total
 };
 static_assert(sizeof(PrefillPlanRep) <= sizeof(g4_decode_plan), "plan size");
 
@@ -340,14 +620,55 @@ void tile_keys(const g4_prefill_entry& e, uint32_t G, uint32_t tile, uint32_t* k
 }
 
 struct Layout {
-    size_t table, work, merge, ml, o, total;
+    size_t table, work, merge, ml, o, vtc, vt, total;
 };
 
+// The caches whose V the pipelined form transposes: one per distinct v_cache,
+// long enough for every entry on it.
+struct VtPlan {
+    std::vector<const uint16_t*> v;
+    std::vector<uint32_t> rows, blocks, block0;
+    std::vector<size_t> off;      // byte offset of each cache's blocks in the V^T region
+    std::vector<uint32_t> of;     // entry -> cache
+    uint32_t total_blocks = 0;
+};
+
+bool prefill_dma_enabled() {
+    static const int env = pf_env("G4_PREFILL_DMA", 1);
+    return env != 0;
+}
+
 // Work list, merge list and workspace layout for a set of entries.
-int build(const g4_prefill_entry* ents, uint32_t n, uint32_t nqh, uint32_t nkh, uint32_t part_keys,
+int build(const g4_prefill_entry* ents, uint32_t n, uint32_t nqh, uint32_t nkh, uint32_t part_keys, bool dma,
           std::vector<PrefillEntryDev>* tab, std::vector<PrefillWorkDev>* work, std::vector<DecodeEntryDev>* merge,
-          uint32_t* max_parts, Layout* L) {
+          uint32_t* max_parts, Layout* L, VtPlan* vp) {
     const uint32_t G = nqh / nkh;
+    *vp = VtPlan{};
+    if (dma) {
+        vp->of.resize(n);
+        for (uint32_t i = 0; i < n; i++) {
+            const g4_prefill_entry& e = ents[i];
+            const uint32_t end = e.start + e.n_tokens;
+            uint32_t c = 0;
+            while (c < vp->v.size() && vp->v[c] != e.v_cache) c++;
+            if (c == vp->v.size()) {
+                vp->v.push_back(e.v_cache);
+                vp->rows.push_back(end);
+            } else if (end > vp->rows[c]) {
+                vp->rows[c] = end;
+            }
+            vp->of[i] = c;
+        }
+        size_t off = 0;
+        for (size_t c = 0; c < vp->v.size(); c++) {
+            const uint32_t blocks = (vp->rows[c] + kPfKeys - 1) / kPfKeys;
+            vp->blocks.push_back(blocks);
+            vp->block0.push_back(vp->total_blocks);
+            vp->off.push_back(off);
+            vp->total_blocks += blocks;
+            off += align256((size_t)nkh * blocks * kPfTileBytes);
+        }
+    }
     uint64_t slots = 0;
     *max_parts = 1;
     tab->resize(n);
@@ -359,11 +680,12 @@ int build(const g4_prefill_entry* ents, uint32_t n, uint32_t nqh, uint32_t nkh, 
     for (uint32_t i = 0; i < n; i++) {
         const g4_prefill_entry& e = ents[i];
         (*tab)[i] = PrefillEntryDev{e.q, e.k_cache, e.v_cache, e.out, e.n_tokens, e.start, e.sliding_window,
-                                    e.scale * kLog2e};
+                                    e.scale * kLog2e, nullptr, dma ? vp->blocks[vp->of[i]] : 0u, 0u};
         const uint32_t tiles = (uint32_t)(((uint64_t)e.n_tokens * G + kPfRows - 1) / kPfRows);
         for (uint32_t t = 0; t < tiles; t++) {
             uint32_t kb, ke;
             tile_keys(e, G, t, &kb, &ke);
+            if (dma) kb &= ~(uint32_t)(kPfKeys - 1);  // the pipelined form reads 32-aligned tiles
             const uint32_t nk = ke - kb;
             const uint32_t parts = (nk + part_keys - 1) / part_keys;
             const uint32_t tok0 = t * (uint32_t)kPfRows / G;
@@ -399,6 +721,10 @@ int build(const g4_prefill_entry* ents, uint32_t n, uint32_t nqh, uint32_t nkh, 
     off += align256(slots * nkh * G * 2 * sizeof(float));
     L->o = off;
     off += align256(slots * nkh * G * kPfHD * sizeof(float));
+    L->vtc = off;
+    off += align256(vp->v.size() * sizeof(VtCacheDev));
+    L->vt = off;
+    for (size_t c = 0; c < vp->v.size(); c++) off += align256((size_t)nkh * vp->blocks[c] * kPfTileBytes);
     L->total = off;
     return G4_OK;
 }
@@ -438,7 +764,9 @@ int g4_attn_prefill_workspace_size(const g4_prefill_entry* entries, uint32_t n_e
     std::vector<DecodeEntryDev> merge;
     uint32_t mp;
     Layout L;
-    rc = build(entries, n_entries, num_q_heads, num_kv_heads, part_keys_default(), &tab, &work, &merge, &mp, &L);
+    VtPlan vp;
+    rc = build(entries, n_entries, num_q_heads, num_kv_heads, part_keys_default(), prefill_dma_enabled(), &tab, &work,
+               &merge, &mp, &L, &vp);
     if (rc) return rc;
     *bytes = L.total;
     return G4_OK;
@@ -455,21 +783,31 @@ int g4_attn_prefill_prepare(const g4_prefill_entry* entries, uint32_t n_entries,
     std::vector<DecodeEntryDev> merge;
     uint32_t max_parts;
     Layout L;
-    rc = build(entries, n_entries, num_q_heads, num_kv_heads, part_keys_default(), &tab, &work, &merge, &max_parts,
-               &L);
+    VtPlan vp;
+    const bool dma = prefill_dma_enabled();
+    rc = build(entries, n_entries, num_q_heads, num_kv_heads, part_keys_default(), dma, &tab, &work, &merge,
+               &max_parts, &L, &vp);
     if (rc) return rc;
     if (max_parts > 8192) return fail(G4_EINVAL, "attnPrefill: %u key parts per tile (max 8192)", max_parts);
     if (!workspace || workspace_bytes < L.total)
         return fail(G4_ENOSPC, "attnPrefill: workspace %zu bytes < %zu needed", workspace_bytes, L.total);
-    if (L.o >= (1ull << 32)) return fail(G4_EINVAL, "attnPrefill: workspace layout exceeds 4 GiB");
+    if (L.vt >= (1ull << 32)) return fail(G4_EINVAL, "attnPrefill: workspace layout exceeds 4 GiB");
     hipStream_t st = as_stream(stream);
     char* ws = static_cast<char*>(workspace);
-    static thread_local Staging s_tab, s_work, s_merge;
+    std::vector<VtCacheDev> vtc(vp.v.size());
+    for (size_t c = 0; c < vp.v.size(); c++)
+        vtc[c] = VtCacheDev{vp.v[c], reinterpret_cast<uint16_t*>(ws + L.vt + vp.off[c]), vp.rows[c], vp.blocks[c],
+                            vp.block0[c], 0u};
+    if (dma)
+        for (uint32_t i = 0; i < n_entries; i++) tab[i].vt = vtc[vp.of[i]].vt;
+    static thread_local Staging s_tab, s_work, s_merge, s_vtc;
     rc = stage_upload(s_tab, ws + L.table, tab.data(), tab.size() * sizeof(PrefillEntryDev), st);
     if (rc) return rc;
     rc = stage_upload(s_work, ws + L.work, work.data(), work.size() * sizeof(PrefillWorkDev), st);
     if (rc) return rc;
     rc = stage_upload(s_merge, ws + L.merge, merge.data(), merge.size() * sizeof(DecodeEntryDev), st);
+    if (rc) return rc;
+    rc = stage_upload(s_vtc, ws + L.vtc, vtc.data(), vtc.size() * sizeof(VtCacheDev), st);
     if (rc) return rc;
     PrefillPlanRep r = {};
     r.ws = ws;
@@ -484,6 +822,9 @@ int g4_attn_prefill_prepare(const g4_prefill_entry* entries, uint32_t n_entries,
     r.off_merge = (uint32_t)L.merge;
     r.off_ml = (uint32_t)L.ml;
     r.off_o = (uint32_t)L.o;
+    r.off_vtc = (uint32_t)L.vtc;
+    r.n_vtc = dma ? (uint32_t)vp.v.size() : 0u;
+    r.vt_blocks = vp.total_blocks;
     memset(plan, 0, sizeof *plan);
     memcpy(plan, &r, sizeof r);
     return G4_OK;
@@ -503,11 +844,22 @@ static int prefill_run(const g4_decode_plan* plan, void* stream, hipEvent_t star
     a.part_ml = reinterpret_cast<float*>(r.ws + r.off_ml);
     a.part_o = reinterpret_cast<float*>(r.ws + r.off_o);
     hipStream_t st = as_stream(stream);
-    if (start_ev || stop_ev)
-        hipExtLaunchKernelGGL(k_prefill, dim3(r.n_work, r.num_kv_heads), dim3(kPfThreads), 0, st, start_ev, stop_ev, 0,
-                              a);
-    else
-        hipLaunchKernelGGL(k_prefill, dim3(r.n_work, r.num_kv_heads), dim3(kPfThreads), 0, st, a);
+    if (r.n_vtc) {  // V^T blocks for the pipelined form
+        hipLaunchKernelGGL(k_vt_blocks, dim3(r.vt_blocks, r.num_kv_heads), dim3(256), 0, st,
+                           reinterpret_cast<const VtCacheDev*>(r.ws + r.off_vtc), r.n_vtc, r.num_kv_heads);
+        G4_CHECK_LAUNCH("attnPrefill (V^T blocks)");
+    }
+    const dim3 grid(r.n_work, r.num_kv_heads);
+    if (r.n_vtc) {
+        if (start_ev || stop_ev)
+            hipExtLaunchKernelGGL(k_prefill_dma, grid, dim3(kPfThreads), 0, st, start_ev, stop_ev, 0, a);
+        else
+            hipLaunchKernelGGL(k_prefill_dma, grid, dim3(kPfThreads), 0, st, a);
+    } else if (start_ev || stop_ev) {
+        hipExtLaunchKernelGGL(k_prefill, grid, dim3(kPfThreads), 0, st, start_ev, stop_ev, 0, a);
+    } else {
+        hipLaunchKernelGGL(k_prefill, grid, dim3(kPfThreads), 0, st, a);
+    }
     G4_CHECK_LAUNCH("attnPrefill");
     if (!r.n_merge) return G4_OK;
     DecodeArgs m = {};
