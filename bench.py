@@ -368,7 +368,7 @@ def run_prefill_gpu(args):
         ops.attn_prefill_run_timed(plan, a_, b_)
     torch.cuda.synchronize()
     k_ms = sum(a_.elapsed_time(b_) for a_, b_ in evs) / len(evs)
-    log(f"prefill4k: {wall / args.steps * 1e6:.1f} us/step, k_prefill avg {k_ms * 1e3:.1f} us")
+    log(f"prefill4k: {wall / args.steps * 1e6:.1f} us/step, k_prefill_dma avg {k_ms * 1e3:.1f} us")
     return dict(wall_s=wall, steps=args.steps, kernel_ms=k_ms, entries=len(entries))
 
 
@@ -412,7 +412,7 @@ def main_prefill(args):
         "config": {"workload": "causal prefill, 4096 tokens, 1 global + 1 local (W=512) layer, 512-token chunks "
                                "(16 entries, one launch)", "num_q_heads": NQH, "num_kv_heads": NKH, "head_dim": HD,
                    "flops_per_step": flops},
-        "roofline": {"bound": "mfma", "kernel": "k_prefill", "achieved": round(achieved, 2),
+        "roofline": {"bound": "mfma", "kernel": "k_prefill_dma", "achieved": round(achieved, 2),
                      "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4),
                      "traffic": None, "avg_us": round(r["kernel_ms"] * 1e3, 2)},
     }
