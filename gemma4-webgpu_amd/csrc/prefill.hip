@@ -323,6 +323,22 @@ __device__ __forceinline__ void lds_dma16(const void* gaddr, uint32_t lds) {
                  : "memory");
 }
 
+// The same with a wave-uniform 64-bit base in SGPRs and a per-lane 32-bit
+// offset (the instruction's saddr form: no per-lane address arithmetic).
+__device__ __forceinline__ void lds_dma16_s(uint32_t voff, const void* sbase, uint32_t lds) {
+    uint32_t saved;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\tglobal_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
+                 : "=&s"(saved)
+                 : "v"(voff), "s"(sbase), "s"(lds)
+                 : "memory");
+}
+
+__device__ __forceinline__ const char* uniform_ptr(const char* p) {
+    const uint64_t x = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)x), hi = __builtin_amdgcn_readfirstlane((uint32_t)(x >> 32));
+    return reinterpret_cast<const char*>(((uint64_t)hi << 32) | lo);
+}
+
 // Waits until at most `younger` tiles' DMAs of this wave are still in flight
 // (8 instructions per tile), then joins the workgroup's barrier.
 __device__ __forceinline__ void dma_wait_barrier(int younger) {
@@ -335,7 +351,39 @@ __device__ __forceinline__ void dma_wait_barrier(int younger) {
 }
 
 // This wave's share of tile `kt0` (32-aligned): K rows 8w .. 8w+7 (2 per
-// instruction) and V^T rows 64w .. 64w+63 (16 per instruction).
+// instruction) and V^T rows 64w .. 64w+63 (16 per instruction). `koff` and
+// `voff` are the lane's byte offsets inside a K tile and a V^T block; a tile
+// whose rows all exist uses them with a uniform base, the last tile of a range
+// clamps its rows per lane.
+struct DmaOffsets {
+    uint32_t k[4], v[4];
+};
+
+__device__ __forceinline__ DmaOffsets dma_offsets(int wave, int lane, uint32_t row_bytes) {
+    DmaOffsets o;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const unsigned inst = 4u * wave + i;
+        const unsigned r = 2u * inst + (unsigned)(lane >> 5);
+        o.k[i] = r * row_bytes + ((((unsigned)lane & 31u) ^ swz_k(r)) << 4);
+        const unsigned d = 16u * inst + (unsigned)(lane >> 2);
+        o.v[i] = d * 64u + ((((unsigned)lane & 3u) ^ swz_v(d)) << 4);
+    }
+    return o;
+}
+
+__device__ __forceinline__ void dma_tile_fast(PrefillDmaSmem& sm, int st, int wave, const DmaOffsets& o,
+                                              const char* kbase, const char* vtb) {
+    const char* kb = uniform_ptr(kbase);
+    const char* vb = uniform_ptr(vtb);
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        lds_dma16_s(o.k[i], kb, __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sm.k[st][(4u * wave + i) * 1024u]));
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        lds_dma16_s(o.v[i], vb, __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sm.vt[st][(4u * wave + i) * 1024u]));
+}
+
 __device__ __forceinline__ void dma_tile(PrefillDmaSmem& sm, int st, int wave, int lane, const char* Kb,
                                          uint32_t row_bytes, unsigned kt0, unsigned last, const char* vtb) {
 #pragma unroll
@@ -376,12 +424,6 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_prefill_dma(PrefillArgs a) {
     const unsigned lo = (ent.window != 0 && pos + 1 > ent.window) ? pos + 1 - ent.window : 0u;
     const unsigned hi = row_live ? pos : 0u;
     const bool dead = !row_live;
-    // Tiles inside [lo, hi] of every row of the wave need no mask (most tiles of a long prefix).
-    unsigned wave_lo = lo, wave_hi = dead ? 0u : hi;
-    for (int off = 32; off > 0; off >>= 1) {
-        wave_lo = max(wave_lo, (unsigned)__shfl_xor((int)wave_lo, off));
-        wave_hi = min(wave_hi, (unsigned)__shfl_xor((int)wave_hi, off));
-    }
 
     f16x8 qop[16];
     {
@@ -403,12 +445,17 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_prefill_dma(PrefillArgs a) {
     const int n_tiles = (int)((ke - kb + kPfKeys - 1) / kPfKeys);
     const float qs = ent.qscale;
 
+    const DmaOffsets dof = dma_offsets(wave, lane, row_bytes);
+    auto issue = [&](int stage, unsigned t0) {
+        const char* vtb = VTb + (uint64_t)(t0 >> 5) * kPfTileBytes;
+        if (t0 + (kPfKeys - 1) <= last)
+            dma_tile_fast(sm, stage, wave, dof, Kb + (uint64_t)t0 * row_bytes, vtb);
+        else
+            dma_tile(sm, stage, wave, lane, Kb, row_bytes, t0, last, vtb);
+    };
 #pragma unroll
     for (int p = 0; p < kPfStages - 1; p++)
-        if (p < n_tiles) {
-            const unsigned kt0 = kb + (unsigned)p * kPfKeys;
-            dma_tile(sm, p, wave, lane, Kb, row_bytes, kt0, last, VTb + (uint64_t)(kt0 >> 5) * kPfTileBytes);
-        }
+        if (p < n_tiles) issue(p, kb + (unsigned)p * kPfKeys);
 
     float m_run = -INFINITY, l_run = 0.0f;
     f32x16 acc[8];
@@ -424,63 +471,49 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_prefill_dma(PrefillArgs a) {
 #pragma unroll
     for (int s = 0; s < 2; s++) voff[s] = (unsigned)col * 64u + ((((unsigned)(2 * s + half)) ^ vx) << 4);
 
-    for (int it = 0; it < n_tiles; it++) {
-        const int st = it % kPfStages;
-        const unsigned kt0 = kb + (unsigned)it * kPfKeys;
-        dma_wait_barrier(min(n_tiles - 1 - it, kPfStages - 2));
-        if (it + kPfStages - 1 < n_tiles) {  // into the stage every wave finished with (tile it - 1)
-            const unsigned kn = kt0 + (kPfStages - 1) * kPfKeys;
-            dma_tile(sm, (it + kPfStages - 1) % kPfStages, wave, lane, Kb, row_bytes, kn, last,
-                     VTb + (uint64_t)(kn >> 5) * kPfTileBytes);
-        }
-
-        const unsigned char* kbuf = sm.k[st];
-        f32x16 s0 = f32x16{};
+    // Software pipeline over tiles: the score MFMAs of tile it + 1 are issued in the same basic
+    // block as the softmax of tile it (independent work: the VALU runs while the matrix core
+    // works), then tile it's output MFMAs. Masking is branch-free for that reason: key in [lo, hi]
+    // is (key - lo) < span (unsigned), with span 0 for rows past the chunk.
+    const unsigned span = dead ? 0u : hi - lo + 1u;
+    auto scores = [&](int stage) {
+        const unsigned char* kbuf = sm.k[stage];
+        f32x16 sc = f32x16{};
 #pragma unroll
         for (int s = 0; s < 16; s++) {
             const f16x8 k0 = *reinterpret_cast<const f16x8*>(kbuf + koff[s & 3] + 128u * (s >> 2));
-            s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(k0, qop[s], s0, 0, 0, 0);
+            sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(k0, qop[s], sc, 0, 0, 0);
         }
-        float x[16];
-        float tmax = -INFINITY;
-        if (kt0 >= wave_lo && kt0 + (kPfKeys - 1) <= wave_hi) {  // uniform: no key of the tile is masked
+        return sc;
+    };
+    // Probabilities of one tile's raw scores (register r: key kt0 + 16 (r / 8) + 8 half + r % 8),
+    // with the lazy update of the row's reference max; returns whether any row moved it.
+    auto softmax = [&](f32x16 sc, unsigned kt0, f16x8 (&pop)[2], float& alpha) {
+        const unsigned rel = kt0 + 8u * (unsigned)half - lo;
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                x[r] = s0[r] * qs;
-                tmax = fmaxf(tmax, x[r]);
-            }
-        } else {
+        for (int r = 0; r < 16; r++)
+            sc[r] = rel + (unsigned)(16 * (r >> 3) + (r & 7)) < span ? sc[r] : -INFINITY;
+        float smax = sc[0];
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const unsigned key = kt0 + 16u * (r >> 3) + 8u * half + (r & 7);
-                const bool ok = !dead && key >= lo && key <= hi;
-                x[r] = ok ? s0[r] * qs : -INFINITY;
-                tmax = fmaxf(tmax, x[r]);
-            }
-        }
+        for (int r = 1; r < 16; r++) smax = fmaxf(smax, sc[r]);
+        float tmax = smax * qs;  // the scale is positive
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
         const bool move = tmax > m_run + kPfLazy;
-        const bool rescale = __any(move);
-        float alpha = 1.0f;
-        if (rescale) {
-            const float m_new = move ? tmax : m_run;
-            alpha = move ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
-            l_run *= alpha;
-            m_run = m_new;
-        }
-        const float mu = m_run == -INFINITY ? 0.0f : m_run;
-        f16x8 pop[2];
+        const float m_new = move ? tmax : m_run;
+        alpha = move ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;  // 0 from -inf (acc, l are 0)
+        l_run *= alpha;
+        m_run = m_new;
+        const float nmu = m_run == -INFINITY ? 0.0f : -m_run;
 #pragma unroll
         for (int r = 0; r < 16; r++) {
-            const float p = __builtin_amdgcn_exp2f(x[r] - mu);
+            const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], qs, nmu));
             l_run += p;
             pop[r >> 3][r & 7] = (f16)p;
         }
-        if (rescale) {
-#pragma unroll
-            for (int b = 0; b < 8; b++) acc[b] *= alpha;
-        }
-        const unsigned char* vbuf = sm.vt[st];
+        return __any(move);
+    };
+    auto output = [&](int stage, const f16x8 (&pop)[2]) {
+        const unsigned char* vbuf = sm.vt[stage];
 #pragma unroll
         for (int b = 0; b < 8; b++) {
 #pragma unroll
@@ -489,6 +522,34 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_prefill_dma(PrefillArgs a) {
                 acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vop, pop[s], acc[b], 0, 0, 0);
             }
         }
+    };
+
+    dma_wait_barrier(min(n_tiles - 1, kPfStages - 2));  // tile 0 is in LDS
+    f32x16 cur = scores(0);
+    int it = 0;
+    for (; it + 1 < n_tiles; it++) {
+        const unsigned kt0 = kb + (unsigned)it * kPfKeys;
+        dma_wait_barrier(min(n_tiles - 2 - it, kPfStages - 3));  // tile it + 1 is in LDS
+        if (it + kPfStages - 1 < n_tiles)  // into the stage every wave finished with (tile it - 1)
+            issue((it + kPfStages - 1) % kPfStages, kt0 + (kPfStages - 1) * kPfKeys);
+        const f32x16 nxt = scores((it + 1) % kPfStages);
+        f16x8 pop[2];
+        float alpha;
+        if (softmax(cur, kt0, pop, alpha)) {
+#pragma unroll
+            for (int b = 0; b < 8; b++) acc[b] *= alpha;
+        }
+        output(it % kPfStages, pop);
+        cur = nxt;
+    }
+    {
+        f16x8 pop[2];
+        float alpha;
+        if (softmax(cur, kb + (unsigned)it * kPfKeys, pop, alpha)) {
+#pragma unroll
+            for (int b = 0; b < 8; b++) acc[b] *= alpha;
+        }
+        output(it % kPfStages, pop);
     }
 
     const float L = l_run + __shfl_xor(l_run, 32);
