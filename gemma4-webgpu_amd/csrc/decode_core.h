@@ -46,6 +46,34 @@ __device__ __forceinline__ uint32_t perm_hi(uint32_t a, uint32_t b) {  // (a.hi1
     return __builtin_amdgcn_perm(b, a, 0x07060302u);
 }
 
+// One LDS-DMA instruction: lane j copies 16 bytes from its global address to
+// LDS byte address lds + 16 j (lds wave-uniform). M0 carries the LDS base and
+// is restored afterwards. Completion is counted by vmcnt, which the compiler
+// does not track for this statement: the pipeline waits for it explicitly.
+__device__ __forceinline__ void lds_dma16(const void* gaddr, uint32_t lds) {
+    uint32_t saved;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+                 : "=&s"(saved)
+                 : "v"(gaddr), "s"(lds)
+                 : "memory");
+}
+
+// The same with a wave-uniform 64-bit base in SGPRs and a per-lane 32-bit
+// offset (the instruction's saddr form: no per-lane address arithmetic).
+__device__ __forceinline__ void lds_dma16_s(uint32_t voff, const void* sbase, uint32_t lds) {
+    uint32_t saved;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\tglobal_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
+                 : "=&s"(saved)
+                 : "v"(voff), "s"(sbase), "s"(lds)
+                 : "memory");
+}
+
+__device__ __forceinline__ const char* uniform_ptr(const char* p) {
+    const uint64_t x = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)x), hi = __builtin_amdgcn_readfirstlane((uint32_t)(x >> 32));
+    return reinterpret_cast<const char*>(((uint64_t)hi << 32) | lo);
+}
+
 struct DecodeEntryDev {
     const float* q;       // [num_kv_heads][group][HD]
     const uint16_t* k;    // [rows][num_kv_heads][HD]
