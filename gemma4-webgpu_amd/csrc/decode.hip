@@ -32,7 +32,7 @@ __device__ __forceinline__ DecodeEntryDev find_entry(const DecodeArgs& a, unsign
 }
 
 template <int HD>
-__global__ __launch_bounds__(kDecodeThreads, 2) void k_decode_split(DecodeArgs a) {
+__global__ __launch_bounds__(kDecodeThreads, HD == 256 ? 2 : 1) void k_decode_split(DecodeArgs a) {
     using D = DecodeDims<HD>;
     __shared__ DecodeSmem<HD> sm;
 
@@ -288,9 +288,11 @@ inline unsigned round_up(unsigned x, unsigned m) { return (x + m - 1) / m * m; }
 // (G4_DECODE_WGS_PER_CU, default 2), never fewer than kMinChunk rows (so the
 // partials stay small next to the rows read), and never more than
 // kMaxMergeSplits splits for the longest entry. G4_DECODE_CHUNK overrides.
-unsigned pick_chunk(uint64_t total_rows, uint64_t max_entry_rows, unsigned num_kv_heads) {
+// head_dim 512 runs one workgroup per CU (its accumulators take twice the registers).
+unsigned pick_chunk(uint64_t total_rows, uint64_t max_entry_rows, unsigned num_kv_heads, unsigned head_dim) {
     static const int env_chunk = env_int("G4_DECODE_CHUNK", 0);
-    static const int wgs_per_cu = env_int("G4_DECODE_WGS_PER_CU", 2);
+    static const int env_wgs = env_int("G4_DECODE_WGS_PER_CU", 0);
+    const int wgs_per_cu = env_wgs > 0 ? env_wgs : (head_dim == 512 ? 1 : 2);
     unsigned chunk;
     if (env_chunk > 0) {
         chunk = round_up((unsigned)env_chunk, kTileKeys);
@@ -311,7 +313,7 @@ int check_shape(const char* who, uint32_t nqh, uint32_t nkh, uint32_t hd) {
         return fail(G4_EINVAL, "%s: num_q_heads %u not a positive multiple of num_kv_heads %u", who, nqh, nkh);
     if (nqh / nkh > (uint32_t)kMaxGroup)
         return fail(G4_EINVAL, "%s: %u query heads per kv head (max %d)", who, nqh / nkh, kMaxGroup);
-    if (hd != 256) return fail(G4_EINVAL, "%s: head_dim %u unsupported (256)", who, hd);
+    if (hd != 256 && hd != 512) return fail(G4_EINVAL, "%s: head_dim %u unsupported (256 or 512)", who, hd);
     return G4_OK;
 }
 
@@ -325,16 +327,20 @@ void attended_range(uint32_t seq_len, uint32_t window, uint32_t* begin, uint32_t
     *begin = (window != 0 && seq_len > window) ? seq_len - window : 0;
 }
 
-int launch_split(const DecodeArgs& a, unsigned total_splits, hipStream_t st) {
-    hipLaunchKernelGGL(k_decode_split<256>, dim3(total_splits, a.num_kv_heads), dim3(kDecodeThreads), 0, st, a);
+int launch_split(const DecodeArgs& a, unsigned total_splits, unsigned head_dim, hipStream_t st) {
+    if (head_dim == 512)
+        hipLaunchKernelGGL(k_decode_split<512>, dim3(total_splits, a.num_kv_heads), dim3(kDecodeThreads), 0, st, a);
+    else
+        hipLaunchKernelGGL(k_decode_split<256>, dim3(total_splits, a.num_kv_heads), dim3(kDecodeThreads), 0, st, a);
     G4_CHECK_LAUNCH("attnDecode split");
     return G4_OK;
 }
 
-int launch(const DecodeArgs& a, unsigned total_splits, unsigned merge_entries, unsigned max_splits, hipStream_t st) {
-    int rc = launch_split(a, total_splits, st);
+int launch(const DecodeArgs& a, unsigned total_splits, unsigned merge_entries, unsigned max_splits, unsigned head_dim,
+           hipStream_t st) {
+    int rc = launch_split(a, total_splits, head_dim, st);
     if (rc) return rc;
-    return launch_decode_merge(a, merge_entries, max_splits, st);
+    return launch_decode_merge(a, merge_entries, max_splits, st, head_dim);
 }
 
 }  // namespace
@@ -360,7 +366,7 @@ int g4_attn_decode(const float* q, const uint16_t* k_cache, const uint16_t* v_ca
     if (p.seq_len == 0) return fail(G4_EINVAL, "attnDecode: seq_len 0");
     uint32_t kb, ke;
     attended_range(p.seq_len, p.sliding_window, &kb, &ke);
-    const unsigned chunk = pick_chunk(ke - kb, ke - kb, p.num_kv_heads);
+    const unsigned chunk = pick_chunk(ke - kb, ke - kb, p.num_kv_heads, p.head_dim);
     const unsigned ns = (ke - kb + chunk - 1) / chunk;
     const uint32_t group = p.num_q_heads / p.num_kv_heads;
     DecodeArgs a = {};
@@ -378,7 +384,7 @@ int g4_attn_decode(const float* q, const uint16_t* k_cache, const uint16_t* v_ca
         a.part_o = reinterpret_cast<float*>(static_cast<char*>(workspace) +
                                             align256((size_t)ns * p.num_kv_heads * group * 2 * sizeof(float)));
     }
-    return launch(a, ns, 1, ns, as_stream(stream));
+    return launch(a, ns, 1, ns, p.head_dim, as_stream(stream));
 }
 
 int g4_attn_decode_many_workspace_size(uint32_t n_entries, uint32_t num_q_heads, uint32_t num_kv_heads,
@@ -428,7 +434,7 @@ int g4_attn_decode_many_prepare(const g4_decode_entry* entries, uint32_t n_entri
         total_rows += ke - kb;
         if (ke - kb > max_rows) max_rows = ke - kb;
     }
-    const unsigned chunk = pick_chunk(total_rows, max_rows, num_kv_heads);
+    const unsigned chunk = pick_chunk(total_rows, max_rows, num_kv_heads, head_dim);
     const uint32_t group = num_q_heads / num_kv_heads;
     // Pinned staging for the table, reused once the previous upload has completed.
     static thread_local DecodeEntryDev* staging = nullptr;
@@ -501,7 +507,7 @@ int g4_attn_decode_many_run(const g4_decode_plan* plan, void* stream) {
     DecodeArgs a;
     int rc = plan_args(plan, &r, &a);
     if (rc) return rc;
-    return launch(a, r.total_splits, r.n_entries, r.max_splits, as_stream(stream));
+    return launch(a, r.total_splits, r.n_entries, r.max_splits, r.head_dim, as_stream(stream));
 }
 
 int g4_attn_decode_many_run_split(const g4_decode_plan* plan, void* stream) {
@@ -509,7 +515,7 @@ int g4_attn_decode_many_run_split(const g4_decode_plan* plan, void* stream) {
     DecodeArgs a;
     int rc = plan_args(plan, &r, &a);
     if (rc) return rc;
-    return launch_split(a, r.total_splits, as_stream(stream));
+    return launch_split(a, r.total_splits, r.head_dim, as_stream(stream));
 }
 
 int g4_attn_decode_many_run_merge(const g4_decode_plan* plan, void* stream) {
@@ -517,7 +523,7 @@ int g4_attn_decode_many_run_merge(const g4_decode_plan* plan, void* stream) {
     DecodeArgs a;
     int rc = plan_args(plan, &r, &a);
     if (rc) return rc;
-    return launch_decode_merge(a, r.n_entries, r.max_splits, as_stream(stream));
+    return launch_decode_merge(a, r.n_entries, r.max_splits, as_stream(stream), r.head_dim);
 }
 
 int g4_attn_decode_many(const g4_decode_entry* entries, uint32_t n_entries, uint32_t num_q_heads,

@@ -210,7 +210,7 @@ int g4_attn_prep_many(const g4_prep_layer* layers, uint32_t n_layers, uint32_t n
  * (the whole cache on global layers, the last sliding_window rows on local
  * layers), split across workgroups, merged with a fixed-order log-sum-exp.
  * out[num_q_heads][head_dim] equals the reference chain's attnOut within
- * floating-point rounding. Requires head_dim == 256 and
+ * floating-point rounding. Requires head_dim 256 or 512 and
  * num_q_heads / num_kv_heads <= 8; out 16-byte aligned. The workspace holds the split partials;
  * g4_attn_decode_workspace_size gives the bytes needed for seq_len up to
  * max_seq_len (allocate once, like attnScores at src/engine.ts:1375).      */

@@ -202,3 +202,44 @@ def test_decode_rejects_bad_shapes(dev):
         ops.attn_decode(q, kc, kc, out, None, 8, 1, 256, 4000)
     with pytest.raises(ValueError):
         ops.attn_decode(q, kc, kc, out, None, 8, 1, 256, 4001)  # cache smaller than seq_len rows
+
+
+@pytest.mark.parametrize("seq,win", [(1, 0), (33, 0), (513, 512), (4097, 0), (20000, 0), (1000, 512)])
+def test_decode_head_dim_512(dev, seq, win):
+    """E2B global layers have head_dim 512: attnDecode at 512 against the oracle's chain and fp64 SDPA."""
+    nqh, nkh, hd = 8, 1, 512
+    announce(f"attnDecode hd=512 seq={seq} win={win}")
+    kc, vc = cache_f16(4000 + seq, seq, nkh, hd), cache_f16(5000 + seq, seq, nkh, hd)
+    q = unit_q(6000 + seq, nqh, hd)
+    want, kf, vf = oracle_chain(q, kc, vc, nqh, nkh, hd, seq, win)
+    got = run_decode(dev, q, kc, vc, nqh, nkh, hd, seq, win)
+    err = max_abs(got, want)
+    err64 = max_abs(got, cf.sdpa(q, kf, vf, nqh, nkh, hd, seq, 1.0, win))
+    print(f"hd=512 seq={seq} win={win} max|gpu-oracle|={err:.2e} max|gpu-fp64|={err64:.2e}")
+    assert np.isfinite(got).all()
+    assert err <= TOL and err64 <= TOL
+
+
+def test_decode_many_head_dim_512_ragged(dev):
+    """attnDecodeMany at head_dim 512: a ragged batch of global-layer sequences, GQA 4:1 and 8:1 shapes."""
+    for nqh, nkh in [(8, 1), (8, 2)]:
+        hd = 512
+        lens = [1, 77, 3000, 9000, 512]
+        announce(f"attnDecodeMany hd=512 nqh={nqh} nkh={nkh} lens={lens}")
+        items = []
+        for b, L in enumerate(lens):
+            kd = cache_f16_torch(800 + b, L, nkh, hd, dev)
+            vd = cache_f16_torch(900 + b, L, nkh, hd, dev)
+            q = unit_q(1000 + b, nqh, hd)
+            items.append((t_f32(q, dev), kd.view(torch.int16), vd.view(torch.int16),
+                          torch.full((nqh * hd,), float("nan"), device=dev), L, 0, 1.0))
+        entries = ops.make_entries(items, nqh, nkh, hd)
+        ws = torch.empty(ops.decode_many_workspace_bytes(len(items), nqh, nkh, hd, sum(lens)), dtype=torch.uint8,
+                         device=dev)
+        ops.attn_decode_many(entries, nqh, nkh, hd, ws)
+        torch.cuda.synchronize()
+        for b, (q, kd, vd, out, L, win, sc) in enumerate(items):
+            kc, vc = kd.cpu().numpy().view(np.uint16), vd.cpu().numpy().view(np.uint16)
+            want, _, _ = oracle_chain(q.cpu().numpy(), kc, vc, nqh, nkh, hd, L, 0)
+            err = max_abs(out.cpu().numpy(), want)
+            assert err <= TOL, f"nkh={nkh} seq {b} (len {L}): {err}"
