@@ -295,77 +295,102 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_prefill(PrefillArgs a) {
 // global memory straight into LDS (global_load_lds_dwordx4, no register
 // staging), kPfStages tiles deep, one barrier per tile. V is transposed once
 // per prefill call into 32-key blocks [HD][32] (k_vt_blocks), so a V^T tile is
-// one contiguous 16 KiB read. The 16-byte chunks of both LDS tiles are
-// XOR-swizzled so that the MFMA operand reads (eight lanes per LDS cycle, each
-// a different row) hit distinct banks.
+// one contiguous read. The 16-byte chunks of both LDS tiles are XOR-swizzled
+// so that the MFMA operand reads (eight lanes per LDS cycle, each a different
+// row) hit distinct banks.
+//
+// head_dim 512 (E2B global layers): a workgroup's output covers one half of
+// the head dimension (blockIdx.z), so the accumulators stay at 128 registers;
+// both halves compute the full-width scores (the K tile is 32 KiB, three
+// stages) and read their own 256 rows of the V^T block.
 
-constexpr int kPfStages = 4;
 constexpr unsigned kPfCUs = 256;  // MI355X compute units: one prefill workgroup each
-constexpr unsigned kPfTileBytes = kPfKeys * kPfHD * 2;  // one K tile, or one V^T tile: 16 KiB
+template <int HD>
+constexpr int kPfStages = HD == 256 ? 4 : 3;
+template <int HD>
+constexpr unsigned kPfKTileBytes = kPfKeys * HD * 2;  // one K tile; also one V^T block in global memory
+constexpr unsigned kPfVtTileBytes = kPfKeys * 256 * 2;  // the V^T rows of one 256-wide output half
 
+template <int HD>
 struct PrefillDmaSmem {
-    unsigned char k[kPfStages][kPfTileBytes];   // key row r: chunk c (8 d) at r*512 + ((c ^ swz_k(r)) * 16)
-    unsigned char vt[kPfStages][kPfTileBytes];  // d row: chunk c (8 keys) at d*64 + ((c ^ swz_v(d)) * 16)
+    unsigned char k[kPfStages<HD>][kPfKTileBytes<HD>];  // key row r: chunk c (8 d) at r*2HD + ((c ^ swz_k(r)) * 16)
+    unsigned char vt[kPfStages<HD>][kPfVtTileBytes];    // d row: chunk c (8 keys) at d*64 + ((c ^ swz_v(d)) * 16)
 };
 
 __device__ __forceinline__ unsigned swz_k(unsigned r) { return (r & 3u) | ((r >> 1) & 4u); }
 __device__ __forceinline__ unsigned swz_v(unsigned d) { return (d >> 1) & 3u; }
 
 // Waits until at most `younger` tiles' DMAs of this wave are still in flight
-// (8 instructions per tile), then joins the workgroup's barrier.
+// (PER instructions per tile), then joins the workgroup's barrier.
+template <int PER>
 __device__ __forceinline__ void dma_wait_barrier(int younger) {
     if (younger >= 2)
-        asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
+        asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(2 * PER) : "memory");
     else if (younger == 1)
-        asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
+        asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(PER) : "memory");
     else
         asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// This wave's share of tile `kt0` (32-aligned): K rows 8w .. 8w+7 (2 per
-// instruction) and V^T rows 64w .. 64w+63 (16 per instruction). `koff` and
-// `voff` are the lane's byte offsets inside a K tile and a V^T block; a tile
-// whose rows all exist uses them with a uniform base, the last tile of a range
-// clamps its rows per lane.
+// This wave's share of tile `kt0` (32-aligned): KI = HD/64 instructions of
+// K (1 KiB each: 2 rows at head_dim 256, 1 at 512) and 4 of V^T (16 rows of
+// 64 B each). `k` and `v` are the lane's byte offsets inside a K tile and a
+// V^T half block; a tile whose rows all exist uses them with a uniform base,
+// the last tile of a range clamps its rows per lane.
+template <int HD>
 struct DmaOffsets {
-    uint32_t k[4], v[4];
+    uint32_t k[HD / 64], v[4];
 };
 
-__device__ __forceinline__ DmaOffsets dma_offsets(int wave, int lane, uint32_t row_bytes) {
-    DmaOffsets o;
+template <int HD>
+__device__ __forceinline__ void dma_k_lane(int wave, int lane, int i, unsigned* r, unsigned* c) {
+    constexpr unsigned CPR = HD / 8, RPI = 64 / CPR;  // 16-byte chunks per K row, rows per instruction
+    const unsigned inst = (HD / 64u) * wave + i;
+    *r = RPI * inst + (unsigned)lane / CPR;
+    *c = ((unsigned)lane % CPR) ^ swz_k(*r);
+}
+
+template <int HD>
+__device__ __forceinline__ DmaOffsets<HD> dma_offsets(int wave, int lane, uint32_t row_bytes) {
+    DmaOffsets<HD> o;
+#pragma unroll
+    for (int i = 0; i < HD / 64; i++) {
+        unsigned r, c;
+        dma_k_lane<HD>(wave, lane, i, &r, &c);
+        o.k[i] = r * row_bytes + (c << 4);
+    }
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const unsigned inst = 4u * wave + i;
-        const unsigned r = 2u * inst + (unsigned)(lane >> 5);
-        o.k[i] = r * row_bytes + ((((unsigned)lane & 31u) ^ swz_k(r)) << 4);
-        const unsigned d = 16u * inst + (unsigned)(lane >> 2);
+        const unsigned d = 16u * (4u * wave + i) + (unsigned)(lane >> 2);
         o.v[i] = d * 64u + ((((unsigned)lane & 3u) ^ swz_v(d)) << 4);
     }
     return o;
 }
 
-__device__ __forceinline__ void dma_tile_fast(PrefillDmaSmem& sm, int st, int wave, const DmaOffsets& o,
+template <int HD>
+__device__ __forceinline__ void dma_tile_fast(PrefillDmaSmem<HD>& sm, int st, int wave, const DmaOffsets<HD>& o,
                                               const char* kbase, const char* vtb) {
     const char* kb = uniform_ptr(kbase);
     const char* vb = uniform_ptr(vtb);
 #pragma unroll
-    for (int i = 0; i < 4; i++)
-        lds_dma16_s(o.k[i], kb, __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sm.k[st][(4u * wave + i) * 1024u]));
+    for (int i = 0; i < HD / 64; i++)
+        lds_dma16_s(o.k[i], kb,
+                    __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sm.k[st][((HD / 64u) * wave + i) * 1024u]));
 #pragma unroll
     for (int i = 0; i < 4; i++)
         lds_dma16_s(o.v[i], vb, __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sm.vt[st][(4u * wave + i) * 1024u]));
 }
 
-__device__ __forceinline__ void dma_tile(PrefillDmaSmem& sm, int st, int wave, int lane, const char* Kb,
+template <int HD>
+__device__ __forceinline__ void dma_tile(PrefillDmaSmem<HD>& sm, int st, int wave, int lane, const char* Kb,
                                          uint32_t row_bytes, unsigned kt0, unsigned last, const char* vtb) {
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const unsigned inst = 4u * wave + i;
-        const unsigned r = 2u * inst + (unsigned)(lane >> 5);
-        const unsigned c = ((unsigned)lane & 31u) ^ swz_k(r);
+    for (int i = 0; i < HD / 64; i++) {
+        unsigned r, c;
+        dma_k_lane<HD>(wave, lane, i, &r, &c);
         const unsigned row = min(kt0 + r, last);
         lds_dma16(Kb + ((uint64_t)row * row_bytes + c * 16u),
-                  __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sm.k[st][inst * 1024u]));
+                  __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sm.k[st][((HD / 64u) * wave + i) * 1024u]));
     }
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -377,8 +402,11 @@ __device__ __forceinline__ void dma_tile(PrefillDmaSmem& sm, int st, int wave, i
     }
 }
 
+template <int HD>
 __global__ __launch_bounds__(kPfThreads, 1) void k_prefill_dma(PrefillArgs a) {
-    __shared__ PrefillDmaSmem sm;
+    constexpr int NS = kPfStages<HD>, NQ = HD / 16, PER = HD / 64 + 4;  // stages, score steps, DMAs per tile
+    __shared__ PrefillDmaSmem<HD> sm;
+    const unsigned dh = blockIdx.z;  // output half of the head dimension (head_dim 512)
     const PrefillWorkDev wk = a.work[blockIdx.x];
     const PrefillEntryDev& ent = a.table[wk.entry];
     const unsigned kvh = blockIdx.y;
@@ -397,36 +425,37 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_prefill_dma(PrefillArgs a) {
     const unsigned hi = row_live ? pos : 0u;
     const bool dead = !row_live;
 
-    f16x8 qop[16];
+    f16x8 qop[NQ];
     {
-        const uint16_t* qr = ent.q + ((uint64_t)tok_c * NQH + kvh * G + head) * kPfHD + 8 * half;
+        const uint16_t* qr = ent.q + ((uint64_t)tok_c * NQH + kvh * G + head) * HD + 8 * half;
 #pragma unroll
-        for (int s = 0; s < 16; s++) qop[s] = ldg<f16x8>(qr + 16 * s);
+        for (int s = 0; s < NQ; s++) qop[s] = ldg<f16x8>(qr + 16 * s);
         // Wait for q here, before any DMA is issued (the compiler's own wait for these loads would
         // otherwise also wait for every DMA in flight at the first MFMA), and keep it in AGPRs: the
         // score MFMA reads its B operand from there, and the VGPRs hold the output accumulators
         // (this file is compiled with MFMA accumulators in VGPRs, so that their rescale is plain VALU).
 #pragma unroll
-        for (int s = 0; s < 16; s++) asm volatile("" : "+a"(qop[s]));
+        for (int s = 0; s < NQ; s++) asm volatile("" : "+a"(qop[s]));
     }
 
-    const uint32_t row_bytes = NKH * kPfHD * 2u;
-    const char* Kb = reinterpret_cast<const char*>(ent.k + (uint64_t)kvh * kPfHD);
-    const char* VTb = reinterpret_cast<const char*>(ent.vt + (uint64_t)kvh * ent.vt_blocks * (kPfHD * 32));
+    const uint32_t row_bytes = NKH * HD * 2u;
+    const char* Kb = reinterpret_cast<const char*>(ent.k + (uint64_t)kvh * HD);
+    const char* VTb = reinterpret_cast<const char*>(ent.vt + (uint64_t)kvh * ent.vt_blocks * (HD * 32)) +
+                      (uint64_t)dh * kPfVtTileBytes;
     const unsigned kb = wk.key_begin, ke = wk.key_end, last = ke - 1;  // kb is 32-aligned
     const int n_tiles = (int)((ke - kb + kPfKeys - 1) / kPfKeys);
     const float qs = ent.qscale;
 
-    const DmaOffsets dof = dma_offsets(wave, lane, row_bytes);
+    const DmaOffsets<HD> dof = dma_offsets<HD>(wave, lane, row_bytes);
     auto issue = [&](int stage, unsigned t0) {
-        const char* vtb = VTb + (uint64_t)(t0 >> 5) * kPfTileBytes;
+        const char* vtb = VTb + (uint64_t)(t0 >> 5) * kPfKTileBytes<HD>;
         if (t0 + (kPfKeys - 1) <= last)
-            dma_tile_fast(sm, stage, wave, dof, Kb + (uint64_t)t0 * row_bytes, vtb);
+            dma_tile_fast<HD>(sm, stage, wave, dof, Kb + (uint64_t)t0 * row_bytes, vtb);
         else
-            dma_tile(sm, stage, wave, lane, Kb, row_bytes, t0, last, vtb);
+            dma_tile<HD>(sm, stage, wave, lane, Kb, row_bytes, t0, last, vtb);
     };
 #pragma unroll
-    for (int p = 0; p < kPfStages - 1; p++)
+    for (int p = 0; p < NS - 1; p++)
         if (p < n_tiles) issue(p, kb + (unsigned)p * kPfKeys);
 
     float m_run = -INFINITY, l_run = 0.0f;
@@ -438,7 +467,7 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_prefill_dma(PrefillArgs a) {
     const unsigned kx = swz_k(krow), vx = swz_v((unsigned)col);
     unsigned koff[4];
 #pragma unroll
-    for (int b = 0; b < 4; b++) koff[b] = krow * 512u + ((((unsigned)(2 * b + half)) ^ kx) << 4);
+    for (int b = 0; b < 4; b++) koff[b] = krow * (2u * HD) + ((((unsigned)(2 * b + half)) ^ kx) << 4);
     unsigned voff[2];
 #pragma unroll
     for (int s = 0; s < 2; s++) voff[s] = (unsigned)col * 64u + ((((unsigned)(2 * s + half)) ^ vx) << 4);
@@ -452,7 +481,7 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_prefill_dma(PrefillArgs a) {
         const unsigned char* kbuf = sm.k[stage];
         f32x16 sc = f32x16{};
 #pragma unroll
-        for (int s = 0; s < 16; s++) {
+        for (int s = 0; s < NQ; s++) {
             const f16x8 k0 = *reinterpret_cast<const f16x8*>(kbuf + koff[s & 3] + 128u * (s >> 2));
             sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(k0, qop[s], sc, 0, 0, 0);
         }
@@ -496,22 +525,22 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_prefill_dma(PrefillArgs a) {
         }
     };
 
-    dma_wait_barrier(min(n_tiles - 1, kPfStages - 2));  // tile 0 is in LDS
+    dma_wait_barrier<PER>(min(n_tiles - 1, NS - 2));  // tile 0 is in LDS
     f32x16 cur = scores(0);
     int it = 0;
     for (; it + 1 < n_tiles; it++) {
         const unsigned kt0 = kb + (unsigned)it * kPfKeys;
-        dma_wait_barrier(min(n_tiles - 2 - it, kPfStages - 3));  // tile it + 1 is in LDS
-        if (it + kPfStages - 1 < n_tiles)  // into the stage every wave finished with (tile it - 1)
-            issue((it + kPfStages - 1) % kPfStages, kt0 + (kPfStages - 1) * kPfKeys);
-        const f32x16 nxt = scores((it + 1) % kPfStages);
+        dma_wait_barrier<PER>(min(n_tiles - 2 - it, NS - 3));  // tile it + 1 is in LDS
+        if (it + NS - 1 < n_tiles)  // into the stage every wave finished with (tile it - 1)
+            issue((it + NS - 1) % NS, kt0 + (NS - 1) * kPfKeys);
+        const f32x16 nxt = scores((it + 1) % NS);
         f16x8 pop[2];
         float alpha;
         if (softmax(cur, kt0, pop, alpha)) {
 #pragma unroll
             for (int b = 0; b < 8; b++) acc[b] *= alpha;
         }
-        output(it % kPfStages, pop);
+        output(it % NS, pop);
         cur = nxt;
     }
     {
@@ -521,14 +550,14 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_prefill_dma(PrefillArgs a) {
 #pragma unroll
             for (int b = 0; b < 8; b++) acc[b] *= alpha;
         }
-        output(it % kPfStages, pop);
+        output(it % NS, pop);
     }
 
     const float L = l_run + __shfl_xor(l_run, 32);
     if (dead) return;
     const uint64_t qrow = (uint64_t)tok * NQH + kvh * G + head;
     if (wk.n_parts == 1) {
-        float* dst = ent.out + qrow * kPfHD + 4 * half;
+        float* dst = ent.out + qrow * HD + 256u * dh + 4 * half;
         const float inv = 1.0f / L;
 #pragma unroll
         for (int b = 0; b < 8; b++)
@@ -541,13 +570,13 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_prefill_dma(PrefillArgs a) {
     const unsigned tile_tok0 = (unsigned)wk.tile * kPfRows / G;
     const uint64_t slot = (uint64_t)wk.split_base + (uint64_t)(tok - tile_tok0) * wk.n_parts + wk.part;
     const uint64_t rec = (slot * NKH + kvh) * G + head;
-    float* po = a.part_o + rec * kPfHD + 4 * half;
+    float* po = a.part_o + rec * HD + 256u * dh + 4 * half;
 #pragma unroll
     for (int b = 0; b < 8; b++)
 #pragma unroll
         for (int g = 0; g < 4; g++)
             stg<f32x4>(po + 32 * b + 8 * g, f32x4{acc[b][4 * g], acc[b][4 * g + 1], acc[b][4 * g + 2], acc[b][4 * g + 3]});
-    if (half == 0) stg<f32x2>(a.part_ml + rec * 2, f32x2{m_run, L});
+    if (half == 0 && dh == 0) stg<f32x2>(a.part_ml + rec * 2, f32x2{m_run, L});  // both halves hold the same
 }
 
 // V of one cache in 32-key blocks [kv head][block][HD][32] (f16): block j holds
@@ -561,26 +590,27 @@ struct VtCacheDev {
     uint32_t pad;
 };
 
+template <int HD>
 __global__ __launch_bounds__(256) void k_vt_blocks(const VtCacheDev* caches, uint32_t n_caches, uint32_t nkh) {
-    __shared__ __attribute__((aligned(16))) uint16_t tb[kPfKeys][kPfHD + 8];
+    __shared__ __attribute__((aligned(16))) uint16_t tb[kPfKeys][HD + 8];
     unsigned c = 0;
     while (c + 1 < n_caches && blockIdx.x >= caches[c + 1].block0) c++;
     const VtCacheDev cd = caches[c];
     const unsigned blk = blockIdx.x - cd.block0;
     const unsigned kvh = blockIdx.y;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const unsigned piece = threadIdx.x + 256u * i;  // 32 keys x 32 chunks of 8 d
-        const unsigned key = piece >> 5, ch = piece & 31u;
+    for (int i = 0; i < HD / 64; i++) {
+        const unsigned piece = threadIdx.x + 256u * i;  // 32 keys x HD/8 chunks of 8 d
+        const unsigned key = piece / (HD / 8), ch = piece % (HD / 8);
         const unsigned row = min(blk * 32u + key, cd.rows - 1);
-        const u32x4 x = ldg<u32x4>(cd.v + ((uint64_t)row * nkh + kvh) * kPfHD + ch * 8u);
+        const u32x4 x = ldg<u32x4>(cd.v + ((uint64_t)row * nkh + kvh) * HD + ch * 8u);
         *reinterpret_cast<u32x4*>(&tb[key][ch * 8u]) = x;
     }
     __syncthreads();
-    uint16_t* dst = cd.vt + ((uint64_t)kvh * cd.blocks + blk) * (kPfHD * 32);
+    uint16_t* dst = cd.vt + ((uint64_t)kvh * cd.blocks + blk) * (HD * 32);
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const unsigned piece = threadIdx.x + 256u * i;  // 256 d x 4 chunks of 8 keys
+    for (int i = 0; i < HD / 64; i++) {
+        const unsigned piece = threadIdx.x + 256u * i;  // HD d x 4 chunks of 8 keys
         const unsigned d = piece >> 2, kc = piece & 3u;
         u32x4 o;
 #pragma unroll
@@ -611,8 +641,9 @@ struct PrefillPlanRep {
     uint32_t n_work;
     uint32_t n_merge;      // merge entries (tokens of split tiles)
     uint32_t max_parts;
-    uint32_t num_q_heads;
-    uint32_t num_kv_heads;
+    uint16_t num_q_heads;
+    uint16_t num_kv_heads;
+    uint32_t head_dim;
     uint32_t magic;
     uint32_t off_work, off_merge, off_ml, off_o;  // workspace byte offsets (workspaces stay under 4 GiB)
     uint32_t off_vtc;      // V^T cache table (pipelined form)
@@ -673,7 +704,7 @@ bool prefill_dma_enabled() {
 }
 
 // Work list, merge list and workspace layout for a set of entries.
-int build(const g4_prefill_entry* ents, uint32_t n, uint32_t nqh, uint32_t nkh, uint32_t part_keys, bool dma,
+int build(const g4_prefill_entry* ents, uint32_t n, uint32_t nqh, uint32_t nkh, uint32_t hd, uint32_t part_keys, bool dma,
           std::vector<PrefillEntryDev>* tab, std::vector<PrefillWorkDev>* work, std::vector<DecodeEntryDev>* merge,
           uint32_t* max_parts, Layout* L, VtPlan* vp) {
     const uint32_t G = nqh / nkh;
@@ -700,7 +731,7 @@ int build(const g4_prefill_entry* ents, uint32_t n, uint32_t nqh, uint32_t nkh, 
             vp->block0.push_back(vp->total_blocks);
             vp->off.push_back(off);
             vp->total_blocks += blocks;
-            off += align256((size_t)nkh * blocks * kPfTileBytes);
+            off += align256((size_t)nkh * blocks * kPfKeys * hd * 2);
         }
     }
     uint64_t slots = 0;
@@ -726,7 +757,7 @@ int build(const g4_prefill_entry* ents, uint32_t n, uint32_t nqh, uint32_t nkh, 
                 w += ke - (dma ? kb & ~(uint32_t)(kPfKeys - 1) : kb);
             }
         }
-        const uint64_t share = w * nkh * 115 / (100 * kPfCUs);
+        const uint64_t share = w * nkh * (hd / 256) * 115 / (100 * kPfCUs);  // head_dim 512: two halves
         part_keys = (uint32_t)std::min<uint64_t>(std::max<uint64_t>(share, 256), 1u << 30);
         part_keys = (part_keys + kPfKeys - 1) / kPfKeys * kPfKeys;
     }
@@ -751,7 +782,7 @@ int build(const g4_prefill_entry* ents, uint32_t n, uint32_t nqh, uint32_t nkh, 
             if (parts > 1) {
                 for (uint32_t tk = 0; tk < ntok; tk++)
                     merge->push_back(DecodeEntryDev{nullptr, nullptr, nullptr,
-                                                    e.out + (uint64_t)(tok0 + tk) * nqh * kPfHD, 0, 0,
+                                                    e.out + (uint64_t)(tok0 + tk) * nqh * hd, 0, 0,
                                                     base + tk * parts, parts, 0.0f, 0});
                 slots += (uint64_t)ntok * parts;
                 *max_parts = std::max(*max_parts, parts);
@@ -773,18 +804,19 @@ int build(const g4_prefill_entry* ents, uint32_t n, uint32_t nqh, uint32_t nkh, 
     L->ml = off;
     off += align256(slots * nkh * G * 2 * sizeof(float));
     L->o = off;
-    off += align256(slots * nkh * G * kPfHD * sizeof(float));
+    off += align256(slots * nkh * G * hd * sizeof(float));
     L->vtc = off;
     off += align256(vp->v.size() * sizeof(VtCacheDev));
     L->vt = off;
-    for (size_t c = 0; c < vp->v.size(); c++) off += align256((size_t)nkh * vp->blocks[c] * kPfTileBytes);
+    for (size_t c = 0; c < vp->v.size(); c++) off += align256((size_t)nkh * vp->blocks[c] * kPfKeys * hd * 2);
     L->total = off;
     return G4_OK;
 }
 
 int check(const g4_prefill_entry* ents, uint32_t n, uint32_t nqh, uint32_t nkh, uint32_t hd) {
     if (!ents || n == 0) return fail(G4_EINVAL, "attnPrefill: no entries");
-    if (hd != (uint32_t)kPfHD) return fail(G4_EINVAL, "attnPrefill: head_dim %u unsupported (256)", hd);
+    if (hd != 256 && !(hd == 512 && prefill_dma_enabled()))
+        return fail(G4_EINVAL, "attnPrefill: head_dim %u unsupported (256, or 512 in the pipelined form)", hd);
     if (nkh == 0 || nqh % nkh || nqh / nkh > (uint32_t)kMaxGroup || 32 % (nqh / nkh))
         return fail(G4_EINVAL, "attnPrefill: %u query heads over %u kv heads unsupported", nqh, nkh);
     for (uint32_t i = 0; i < n; i++) {
@@ -819,7 +851,8 @@ int g4_attn_prefill_workspace_size(const g4_prefill_entry* entries, uint32_t n_e
     uint32_t mp;
     Layout L;
     VtPlan vp;
-    rc = build(entries, n_entries, num_q_heads, num_kv_heads, part_keys_default(), prefill_dma_enabled(), &tab, &work,
+    rc = build(entries, n_entries, num_q_heads, num_kv_heads, head_dim, part_keys_default(), prefill_dma_enabled(), &tab,
+               &work,
                &merge, &mp, &L, &vp);
     if (rc) return rc;
     *bytes = L.total;
@@ -839,7 +872,7 @@ int g4_attn_prefill_prepare(const g4_prefill_entry* entries, uint32_t n_entries,
     Layout L;
     VtPlan vp;
     const bool dma = prefill_dma_enabled();
-    rc = build(entries, n_entries, num_q_heads, num_kv_heads, part_keys_default(), dma, &tab, &work, &merge,
+    rc = build(entries, n_entries, num_q_heads, num_kv_heads, head_dim, part_keys_default(), dma, &tab, &work, &merge,
                &max_parts, &L, &vp);
     if (rc) return rc;
     if (max_parts > 8192) return fail(G4_EINVAL, "attnPrefill: %u key parts per tile (max 8192)", max_parts);
@@ -869,8 +902,9 @@ int g4_attn_prefill_prepare(const g4_prefill_entry* entries, uint32_t n_entries,
     r.n_work = (uint32_t)work.size();
     r.n_merge = (uint32_t)merge.size();
     r.max_parts = max_parts;
-    r.num_q_heads = num_q_heads;
-    r.num_kv_heads = num_kv_heads;
+    r.num_q_heads = (uint16_t)num_q_heads;  // at most 8 per kv head (checked); kv heads below 2^16
+    r.num_kv_heads = (uint16_t)num_kv_heads;
+    r.head_dim = head_dim;
     r.magic = kPrefillMagic;
     r.off_work = (uint32_t)L.work;
     r.off_merge = (uint32_t)L.merge;
@@ -898,17 +932,28 @@ static int prefill_run(const g4_decode_plan* plan, void* stream, hipEvent_t star
     a.part_ml = reinterpret_cast<float*>(r.ws + r.off_ml);
     a.part_o = reinterpret_cast<float*>(r.ws + r.off_o);
     hipStream_t st = as_stream(stream);
+    const bool hd512 = r.head_dim == 512;
     if (r.n_vtc) {  // V^T blocks for the pipelined form
-        hipLaunchKernelGGL(k_vt_blocks, dim3(r.vt_blocks, r.num_kv_heads), dim3(256), 0, st,
-                           reinterpret_cast<const VtCacheDev*>(r.ws + r.off_vtc), r.n_vtc, r.num_kv_heads);
+        const VtCacheDev* vtc = reinterpret_cast<const VtCacheDev*>(r.ws + r.off_vtc);
+        const dim3 vgrid(r.vt_blocks, r.num_kv_heads);
+        if (hd512)
+            hipLaunchKernelGGL(k_vt_blocks<512>, vgrid, dim3(256), 0, st, vtc, r.n_vtc, (uint32_t)r.num_kv_heads);
+        else
+            hipLaunchKernelGGL(k_vt_blocks<256>, vgrid, dim3(256), 0, st, vtc, r.n_vtc, (uint32_t)r.num_kv_heads);
         G4_CHECK_LAUNCH("attnPrefill (V^T blocks)");
     }
-    const dim3 grid(r.n_work, r.num_kv_heads);
+    const dim3 grid(r.n_work, r.num_kv_heads, r.head_dim / 256);
     if (r.n_vtc) {
-        if (start_ev || stop_ev)
-            hipExtLaunchKernelGGL(k_prefill_dma, grid, dim3(kPfThreads), 0, st, start_ev, stop_ev, 0, a);
-        else
-            hipLaunchKernelGGL(k_prefill_dma, grid, dim3(kPfThreads), 0, st, a);
+        if (hd512) {
+            if (start_ev || stop_ev)
+                hipExtLaunchKernelGGL(k_prefill_dma<512>, grid, dim3(kPfThreads), 0, st, start_ev, stop_ev, 0, a);
+            else
+                hipLaunchKernelGGL(k_prefill_dma<512>, grid, dim3(kPfThreads), 0, st, a);
+        } else if (start_ev || stop_ev) {
+            hipExtLaunchKernelGGL(k_prefill_dma<256>, grid, dim3(kPfThreads), 0, st, start_ev, stop_ev, 0, a);
+        } else {
+            hipLaunchKernelGGL(k_prefill_dma<256>, grid, dim3(kPfThreads), 0, st, a);
+        }
     } else if (start_ev || stop_ev) {
         hipExtLaunchKernelGGL(k_prefill, grid, dim3(kPfThreads), 0, st, start_ev, stop_ev, 0, a);
     } else {
@@ -923,7 +968,7 @@ static int prefill_run(const g4_decode_plan* plan, void* stream, hipEvent_t star
     m.group = a.group;
     m.part_ml = a.part_ml;
     m.part_o = a.part_o;
-    return launch_decode_merge(m, r.n_merge, r.max_parts, st);
+    return launch_decode_merge(m, r.n_merge, r.max_parts, st, r.head_dim);
 }
 
 int g4_attn_prefill_run(const g4_decode_plan* plan, void* stream) { return prefill_run(plan, stream, nullptr, nullptr); }

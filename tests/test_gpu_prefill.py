@@ -6,7 +6,9 @@ checked against the oracle's attnScore -> softmax -> attnOutput chain at
 seq_len = start + t + 1, with the local-layer window, on the same f16 cache
 rows and the f16 query widened to f32. Bar: max-abs 2e-3 (P is rounded to f16
 for the output MFMA). Parts of long key ranges go through the log-sum-exp
-merge (start 2900: key ranges cut into parts of 1536 keys by default).
+merge (a call's parts are sized from its total work: these small calls cut
+key ranges into parts of 256 keys). head_dim 512 (E2B global layers) runs the
+pipelined form with each half of the output in its own workgroup.
 """
 import numpy as np
 import pytest
@@ -24,16 +26,16 @@ TOL = 2e-3
 
 
 class Chunk:
-    def __init__(self, dev, seed, start, T, window, nqh=8, nkh=1):
-        self.start, self.T, self.window, self.nqh, self.nkh = start, T, window, nqh, nkh
+    def __init__(self, dev, seed, start, T, window, nqh=8, nkh=1, hd=HD):
+        self.start, self.T, self.window, self.nqh, self.nkh, self.hd = start, T, window, nqh, nkh, hd
         rows = start + T
-        self.kc = cache_f16(seed, rows, nkh, HD)
-        self.vc = cache_f16(seed + 1, rows, nkh, HD)
-        q = synth.rms_normalize_rows(synth.normal(seed + 2, T * nqh * HD).reshape(T * nqh, HD))
-        self.qb = orc.f32_to_f16_bits(q).reshape(T, nqh * HD)
+        self.kc = cache_f16(seed, rows, nkh, hd)
+        self.vc = cache_f16(seed + 1, rows, nkh, hd)
+        q = synth.rms_normalize_rows(synth.normal(seed + 2, T * nqh * hd).reshape(T * nqh, hd))
+        self.qb = orc.f32_to_f16_bits(q).reshape(T, nqh * hd)
         t16 = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16).reshape(-1)).to(dev)  # noqa: E731
         self.dq, self.dk, self.dv = t16(self.qb), t16(self.kc), t16(self.vc)
-        self.out = torch.full((T * nqh * HD,), float("nan"), dtype=torch.float32, device=dev)
+        self.out = torch.full((T * nqh * hd,), float("nan"), dtype=torch.float32, device=dev)
 
     def entry(self):
         return dict(q=self.dq, k_cache=self.dk, v_cache=self.dv, out=self.out, n_tokens=self.T, start=self.start,
@@ -44,18 +46,18 @@ class Chunk:
         kf = orc.f16_bits_to_f32(self.kc).reshape(rows, -1)
         vf = orc.f16_bits_to_f32(self.vc).reshape(rows, -1)
         qf = orc.f16_bits_to_f32(self.qb).reshape(self.T, -1)
-        want = np.empty((self.T, self.nqh * HD), np.float32)
+        want = np.empty((self.T, self.nqh * self.hd), np.float32)
         for t in range(self.T):
             seq = self.start + t + 1
             want[t] = orc.attention_chain(qf[t], kf[:seq].reshape(-1), vf[:seq].reshape(-1), self.nqh, self.nkh,
-                                          HD, seq, 1.0, self.window)
+                                          self.hd, seq, 1.0, self.window)
         return want.reshape(-1)
 
 
-def run(dev, chunks, nqh=8, nkh=1):
-    arr = ops.make_prefill_entries([c.entry() for c in chunks], nqh, nkh, HD)
-    ws = torch.empty(max(ops.prefill_workspace_bytes(arr, nqh, nkh, HD), 1), dtype=torch.uint8, device=dev)
-    plan = ops.attn_prefill_prepare(arr, nqh, nkh, HD, ws)
+def run(dev, chunks, nqh=8, nkh=1, hd=HD):
+    arr = ops.make_prefill_entries([c.entry() for c in chunks], nqh, nkh, hd)
+    ws = torch.empty(max(ops.prefill_workspace_bytes(arr, nqh, nkh, hd), 1), dtype=torch.uint8, device=dev)
+    plan = ops.attn_prefill_prepare(arr, nqh, nkh, hd, ws)
     ops.attn_prefill_run(plan)
     torch.cuda.synchronize()
     return plan, ws
@@ -119,3 +121,25 @@ def test_prefill_rejects_bad_shapes(dev):
         ops.prefill_workspace_bytes(arr, 8, 1, 128)
     with pytest.raises(G4Error):
         ops.prefill_workspace_bytes(arr, 24, 1, HD)
+
+
+@pytest.mark.parametrize("start,T,window,nkh", [(0, 40, 0, 1), (2900, 24, 0, 1), (600, 70, 512, 1), (20000, 8, 0, 1),
+                                                (100, 33, 0, 2)])
+def test_prefill_head_dim_512(dev, start, T, window, nkh):
+    """head_dim 512: full-width scores in both output halves; parts merged at 512."""
+    announce(f"attnPrefill hd=512 start={start} T={T} window={window} nkh={nkh}")
+    nqh = 8
+    c = Chunk(dev, 51 + start + T, start, T, window, nqh=nqh, nkh=nkh, hd=512)
+    run(dev, [c], nqh=nqh, nkh=nkh, hd=512)
+    print(f"hd=512 start={start} T={T} W={window} err={check(c, 'hd512'):.2e}")
+
+
+def test_prefill_head_dim_512_with_256_in_one_process(dev):
+    """A local (256) and a global (512) layer's chunks, as E2B's prefill issues them: two calls."""
+    announce("attnPrefill hd 256 + 512")
+    a = Chunk(dev, 61, 0, 48, 32)
+    b = Chunk(dev, 62, 0, 48, 0, hd=512)
+    run(dev, [a])
+    run(dev, [b], hd=512)
+    check(a, "hd256")
+    check(b, "hd512")
