@@ -466,8 +466,26 @@ int main(int argc, char** argv) {
     CK(g4_stream_synchronize(st));
 
     const bool fused = mode == "step";
+    // mode graph: each set's step (attention launch + merge launch) captured once as a HIP graph
+    // and replayed; the plans' work tables are the same device memory, so replays read them.
+    std::vector<hipGraphExec_t> gexec(sets, nullptr);
+    if (mode == "graph") {
+        for (int si = 0; si < sets; si++) {
+            hipGraph_t g;
+            HK(hipStreamBeginCapture(st, hipStreamCaptureModeGlobal));
+            for (int h = 0; h < 2; h++)
+                if (S[si].has_step[h]) CK(g4_attn_step_run(&S[si].step_plan[h], st));
+            HK(hipStreamEndCapture(st, &g));
+            HK(hipGraphInstantiate(&gexec[si], g, nullptr, nullptr, 0));
+            HK(hipGraphDestroy(g));
+        }
+    }
     auto step = [&](int i) {
         Set& s = S[i % sets];
+        if (mode == "graph") {
+            HK(hipGraphLaunch(gexec[i % sets], st));
+            return;
+        }
         if (fused) {
             for (int h = 0; h < 2; h++)
                 if (s.has_step[h]) CK(g4_attn_step_run(&s.step_plan[h], st));
