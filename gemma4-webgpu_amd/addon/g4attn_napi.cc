@@ -419,6 +419,34 @@ napi_value MatmulQuant(napi_env env, napi_callback_info info) {
     return undefined(env);
 }
 
+napi_value MatmulQ8(napi_env env, napi_callback_info info) {
+    Args a(env, info, 6);  // input, qweight, qscale, output, params {M, N}, stream
+    void* x = a.ptr(0);
+    void* q = a.ptr(1);
+    void* sc = a.ptr(2);
+    void* o = a.ptr(3);
+    g4_matmul_params p;
+    a.params(4, &p);
+    void* s = a.ptr(5);
+    if (!a.ok) return nullptr;
+    CALL(env, g4_matmul_q8((const float*)x, (const int8_t*)q, (const uint16_t*)sc, (float*)o, p, s));
+    return undefined(env);
+}
+
+napi_value MatmulQ4K(napi_env env, napi_callback_info info) {
+    Args a(env, info, 6);  // input, qweight, qmeta, output, params {M, N}, stream
+    void* x = a.ptr(0);
+    void* q = a.ptr(1);
+    void* m = a.ptr(2);
+    void* o = a.ptr(3);
+    g4_matmul_params p;
+    a.params(4, &p);
+    void* s = a.ptr(5);
+    if (!a.ok) return nullptr;
+    CALL(env, g4_matmul_q4k((const float*)x, (const uint32_t*)q, (const uint16_t*)m, (float*)o, p, s));
+    return undefined(env);
+}
+
 napi_value LogitSoftcap(napi_env env, napi_callback_info info) {
     Args a(env, info, 3);  // logits, params {size, cap}, stream
     void* l = a.ptr(0);
@@ -568,6 +596,50 @@ napi_value Linear(napi_env env, napi_callback_info info) {
         segs[i] = g4_linear_seg{static_cast<const uint16_t*>(ptrs[0]), (float*)const_cast<void*>(ptrs[1]), rows};
     }
     CALL(env, g4_linear_f16((const float*)x, n, segs.data(), count, s));
+    return undefined(env);
+}
+
+// linearQuant(input, n, format, segments[{weight, meta, out, rows}], stream): format 1 = q8, 2 = q4k.
+napi_value LinearQuant(napi_env env, napi_callback_info info) {
+    Args a(env, info, 5);
+    void* x = a.ptr(0);
+    const uint32_t n = a.u32(1), format = a.u32(2);
+    void* s = a.ptr(4);
+    if (!a.ok) return nullptr;
+    bool is_array = false;
+    napi_is_array(env, a.v[3], &is_array);
+    if (!is_array) {
+        a.fail("linearQuant: segments must be an array");
+        return nullptr;
+    }
+    uint32_t count = 0;
+    napi_get_array_length(env, a.v[3], &count);
+    std::vector<g4_linear_qseg> segs(count);
+    for (uint32_t i = 0; i < count; i++) {
+        napi_value obj, v;
+        napi_get_element(env, a.v[3], i, &obj);
+        const std::string at = "linearQuant: segment " + std::to_string(i) + ": ";
+        const void* ptrs[3] = {};
+        const char* keys[3] = {"weight", "meta", "out"};
+        for (int k = 0; k < 3; k++) {
+            uint64_t p = 0;
+            bool lossless = false;
+            if (!get_prop(env, obj, keys[k], &v) || napi_get_value_bigint_uint64(env, v, &p, &lossless) != napi_ok ||
+                !lossless) {
+                a.fail(at + keys[k] + " must be a BigInt pointer");
+                return nullptr;
+            }
+            ptrs[k] = reinterpret_cast<const void*>(static_cast<uintptr_t>(p));
+        }
+        uint32_t rows = 0;
+        if (!get_prop(env, obj, "rows", &v) || napi_get_value_uint32(env, v, &rows) != napi_ok) {
+            a.fail(at + "rows must be a number");
+            return nullptr;
+        }
+        segs[i] = g4_linear_qseg{ptrs[0], static_cast<const uint16_t*>(ptrs[1]), (float*)const_cast<void*>(ptrs[2]),
+                                 rows};
+    }
+    CALL(env, g4_linear_quant((const float*)x, n, format, segs.data(), count, s));
     return undefined(env);
 }
 
@@ -887,6 +959,9 @@ napi_value Init(napi_env env, napi_value exports) {
         {"lmHeadWorkspaceSize", LmHeadWorkspaceSize},
         {"lmHeadArgmax", LmHeadArgmax},
         {"linear", Linear},
+        {"linearQuant", LinearQuant},
+        {"matmulQ8", MatmulQ8},
+        {"matmulQ4K", MatmulQ4K},
         {"ropeInvFreq", RopeInvFreq},
         {"ropeInvFreqHost", RopeInvFreqHost},
         {"attnStepWorkspaceSize", AttnStepWorkspaceSize},

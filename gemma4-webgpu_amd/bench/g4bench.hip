@@ -162,9 +162,16 @@ static int run_lmhead(const std::string& mode, int iters) {
 // layer. mode `fused`: g4_linear_f16 (q, k, v in one launch); `chain`: the
 // reference's one-workgroup-per-row matmulQuant per matrix. Weight sets are
 // rotated so the bytes read per cycle exceed twice the 256 MB MALL.
+//   --mode q8 | q4k: the same with the engine's quantized weights (g4_linear_quant), and
+//   q8chain | q4kchain: one matmulQ8 / matmulQ4K dispatch per matrix.
 static int run_proj(const std::string& wl, const std::string& mode, int iters) {
     const uint32_t H = 1536, hd = wl == "proj512" ? 512 : 256, NQ = NQH * hd, NK = NKH * hd;
-    const uint64_t wbytes = ((uint64_t)(NQ + 2 * NK) * H + (uint64_t)H * NQ) * 2;
+    const int fmt = mode.rfind("q8", 0) == 0 ? 1 : mode.rfind("q4k", 0) == 0 ? 2 : 0;
+    const bool qchain = fmt && mode.find("chain") != std::string::npos;
+    // bytes per weight element: f16 2; q8 1 + scale 2/32; q4k 1/2 + meta 2*16/256
+    const double bpe = fmt == 0 ? 2.0 : fmt == 1 ? 1.0 + 2.0 / 32 : 0.5 + 32.0 / 256;
+    const uint64_t welems = (uint64_t)(NQ + 2 * NK) * H + (uint64_t)H * NQ;
+    const uint64_t wbytes = (uint64_t)(welems * bpe);
     const uint64_t bytes = wbytes + (H + NQ) * 4 + (uint64_t)(NQ + 2 * NK + H) * 4;
     const int sets = (int)((512ull << 20) / wbytes) + 1;
     printf("workload %s: head_dim %u, %.2f MB of weights per layer, %d weight sets\n", wl.c_str(), hd, wbytes / 1e6,
@@ -181,21 +188,56 @@ static int run_proj(const std::string& wl, const std::string& mode, int iters) {
     CK(g4_malloc(&y, H * 4));
     hipLaunchKernelGGL(k_fill_f32, dim3(8), dim3(256), 0, st, (float*)x, (uint64_t)H, 3ull);
     hipLaunchKernelGGL(k_fill_f32, dim3(8), dim3(256), 0, st, (float*)attn, (uint64_t)NQ, 4ull);
-    std::vector<void*> wq(sets), wk(sets), wv(sets), wo(sets);
+    std::vector<void*> wq(sets), wk(sets), wv(sets), wo(sets), mq(sets), mk(sets), mv(sets), mo(sets);
+    // Weights are filled as f16 noise over the bytes they occupy (the quantized forms read them as int8 /
+    // nibbles, and their scale tables likewise as f16 noise): the timing does not depend on the values.
+    auto alloc_fill = [&](void** p, uint64_t elems, unsigned long long seed) {
+        const uint64_t bytes = fmt == 0 ? elems * 2 : fmt == 1 ? elems : elems / 2;
+        CK(g4_malloc(p, bytes));
+        hipLaunchKernelGGL(k_fill_f16, dim3(1024), dim3(256), 0, st, (_Float16*)*p, bytes / 2, seed);
+    };
+    auto alloc_meta = [&](void** p, uint64_t rows, uint32_t n, unsigned long long seed) {
+        if (!fmt) return;
+        const uint64_t vals = fmt == 1 ? rows * (n / 32) : rows * (n / 256) * 16;
+        CK(g4_malloc(p, vals * 2));
+        hipLaunchKernelGGL(k_fill_f16, dim3(64), dim3(256), 0, st, (_Float16*)*p, vals, seed);
+    };
     for (int s = 0; s < sets; s++) {
-        CK(g4_malloc(&wq[s], (size_t)NQ * H * 2));
-        CK(g4_malloc(&wk[s], (size_t)NK * H * 2));
-        CK(g4_malloc(&wv[s], (size_t)NK * H * 2));
-        CK(g4_malloc(&wo[s], (size_t)H * NQ * 2));
-        hipLaunchKernelGGL(k_fill_f16, dim3(1024), dim3(256), 0, st, (_Float16*)wq[s], (uint64_t)NQ * H, 100ull + s);
-        hipLaunchKernelGGL(k_fill_f16, dim3(256), dim3(256), 0, st, (_Float16*)wk[s], (uint64_t)NK * H, 200ull + s);
-        hipLaunchKernelGGL(k_fill_f16, dim3(256), dim3(256), 0, st, (_Float16*)wv[s], (uint64_t)NK * H, 300ull + s);
-        hipLaunchKernelGGL(k_fill_f16, dim3(1024), dim3(256), 0, st, (_Float16*)wo[s], (uint64_t)H * NQ, 400ull + s);
+        alloc_fill(&wq[s], (uint64_t)NQ * H, 100ull + s);
+        alloc_fill(&wk[s], (uint64_t)NK * H, 200ull + s);
+        alloc_fill(&wv[s], (uint64_t)NK * H, 300ull + s);
+        alloc_fill(&wo[s], (uint64_t)H * NQ, 400ull + s);
+        alloc_meta(&mq[s], NQ, H, 500ull + s);
+        alloc_meta(&mk[s], NK, H, 600ull + s);
+        alloc_meta(&mv[s], NK, H, 700ull + s);
+        alloc_meta(&mo[s], H, NQ, 800ull + s);
     }
     HK(hipGetLastError());
     const bool fused = mode != "chain";
     auto step = [&](int i) {
         const int s = i % sets;
+        if (fmt && !qchain) {
+            g4_linear_qseg qkv[3] = {{wq[s], (const uint16_t*)mq[s], (float*)q, NQ},
+                                     {wk[s], (const uint16_t*)mk[s], (float*)k, NK},
+                                     {wv[s], (const uint16_t*)mv[s], (float*)v, NK}};
+            CK(g4_linear_quant((const float*)x, H, (uint32_t)fmt, qkv, 3, st));
+            g4_linear_qseg o = {wo[s], (const uint16_t*)mo[s], (float*)y, H};
+            CK(g4_linear_quant((const float*)attn, NQ, (uint32_t)fmt, &o, 1, st));
+            return;
+        }
+        if (qchain) {
+            auto mm = [&](const float* in, void* w, void* m, float* out, uint32_t M, uint32_t N) {
+                if (fmt == 1)
+                    CK(g4_matmul_q8(in, (const int8_t*)w, (const uint16_t*)m, out, g4_matmul_params{M, N}, st));
+                else
+                    CK(g4_matmul_q4k(in, (const uint32_t*)w, (const uint16_t*)m, out, g4_matmul_params{M, N}, st));
+            };
+            mm((const float*)x, wq[s], mq[s], (float*)q, NQ, H);
+            mm((const float*)x, wk[s], mk[s], (float*)k, NK, H);
+            mm((const float*)x, wv[s], mv[s], (float*)v, NK, H);
+            mm((const float*)attn, wo[s], mo[s], (float*)y, H, NQ);
+            return;
+        }
         if (fused) {
             g4_linear_seg qkv[3] = {{(const uint16_t*)wq[s], (float*)q, NQ}, {(const uint16_t*)wk[s], (float*)k, NK},
                                     {(const uint16_t*)wv[s], (float*)v, NK}};
@@ -222,7 +264,7 @@ static int run_proj(const std::string& wl, const std::string& mode, int iters) {
     HK(hipEventElapsedTime(&ms, a, b));
     const double us = ms * 1e3 / iters;
     printf("%s [%s]: %.2f us/step (linearQKV + linearOut), %.1f GB/s algorithmic (%d iterations)\n", wl.c_str(),
-           fused ? "fused" : "chain", us, bytes / (us * 1e3), iters);
+           mode.c_str(), us, bytes / (us * 1e3), iters);
     return 0;
 }
 

@@ -64,4 +64,81 @@ __device__ __forceinline__ float gemv_row_dot(const uint16_t* row, const float (
     return acc[0] + acc[1];                                      // stride 1
 }
 
+// The same row value for quantized weights, in matmul_q8.wgsl's and
+// matmul_q4k.wgsl's per-element order (each operation rounded, no fused
+// multiply-add), with the same partials, j order and tree:
+//   Q8:  w = f32(int8) * f32(scale[k / 32]);           acc = acc + w * x[k]
+//   Q4K: w = f32(scale[sub]) * f32(nibble) + f32(min[sub]); acc = acc + w * x[k]
+// Lane l of the half-wave covers k = 256 j + 8 l .. + 7, which lie in one
+// 32-element block (Q8 scale 8 j + l / 4; Q4K super-block j, sub-block l / 4).
+template <int NJ>
+__device__ __forceinline__ float gemv_tree(float (&acc)[8]) {
+#pragma clang fp contract(off)
+#pragma unroll
+    for (int m = 16; m >= 1; m >>= 1)  // tree strides 128 .. 8
+#pragma unroll
+        for (int e = 0; e < 8; e++) acc[e] = acc[e] + __shfl_xor(acc[e], m);
+#pragma unroll
+    for (int e = 0; e < 4; e++) acc[e] = acc[e] + acc[e + 4];  // stride 4
+    acc[0] = acc[0] + acc[2];                                    // stride 2
+    acc[1] = acc[1] + acc[3];
+    return acc[0] + acc[1];                                      // stride 1
+}
+
+// qrow: the row's int8 weights (N bytes, 8-byte aligned); srow: its N/32 f16 scales.
+template <int NJ>
+__device__ __forceinline__ float gemv_row_dot_q8(const int8_t* qrow, const uint16_t* srow, const float (&xr)[NJ][8],
+                                                 unsigned lq) {
+#pragma clang fp contract(off)
+    uint64_t qv[NJ];
+    uint32_t sv[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        qv[j] = ldg_nt<uint64_t>(qrow + 256 * j + 8 * lq);
+        sv[j] = ldg<uint16_t>(srow + 8 * j + (lq >> 2));
+    }
+    float acc[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) acc[e] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const float sc = h2f((uint16_t)sv[j]);
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const float w = (float)(int8_t)(qv[j] >> (8 * e)) * sc;
+            acc[e] = acc[e] + w * xr[j][e];
+        }
+    }
+    return gemv_tree<NJ>(acc);
+}
+
+// qrow: the row's nibbles (N / 8 words, 8 per word, low nibble first); mrow: its
+// (N / 256) x 16 f16 values (8 scales, then 8 mins, per super-block).
+template <int NJ>
+__device__ __forceinline__ float gemv_row_dot_q4k(const uint32_t* qrow, const uint16_t* mrow, const float (&xr)[NJ][8],
+                                                  unsigned lq) {
+#pragma clang fp contract(off)
+    uint32_t qv[NJ], sv[NJ], mv[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        qv[j] = ldg_nt<uint32_t>(qrow + 32 * j + lq);
+        sv[j] = ldg<uint16_t>(mrow + 16 * j + (lq >> 2));
+        mv[j] = ldg<uint16_t>(mrow + 16 * j + 8 + (lq >> 2));
+    }
+    float acc[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) acc[e] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const float sc = h2f((uint16_t)sv[j]), mn = h2f((uint16_t)mv[j]);
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const float t = sc * (float)((qv[j] >> (4 * e)) & 15u);
+            const float w = t + mn;
+            acc[e] = acc[e] + w * xr[j][e];
+        }
+    }
+    return gemv_tree<NJ>(acc);
+}
+
 }  // namespace g4

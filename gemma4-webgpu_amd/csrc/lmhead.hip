@@ -3,6 +3,8 @@
 //
 // Reference-shaped kernels (bit-identical to the WGSL, one per pass):
 //   matmulQuant   shaders/matmul_quant.wgsl:20-52   one workgroup per row
+//   matmulQ8      shaders/matmul_q8.wgsl:31-64      one workgroup per row (int8, f16 block scales)
+//   matmulQ4K     shaders/matmul_q4k.wgsl:30-72     one workgroup per row (4-bit, f16 scale/min)
 //   logitSoftcap  shaders/logit_softcap.wgsl:9-16
 //   argmax        shaders/argmax.wgsl:7-34          one workgroup
 //
@@ -44,6 +46,51 @@ __global__ __launch_bounds__(kWG) void k_matmul_quant_f16(const float* __restric
     const uint16_t* row = weight + (uint64_t)m * p.N;
     float acc = 0.0f;
     for (unsigned k = tid; k < p.N; k += kWG) acc = acc + h2f(row[k]) * input[k];
+    partials[tid] = acc;
+    __syncthreads();
+    const float r = wg_tree_sum(partials, tid);
+    if (tid == 0) output[m] = r;
+}
+
+__global__ __launch_bounds__(kWG) void k_matmul_q8(const float* __restrict__ input, const int8_t* __restrict__ qweight,
+                                                   const uint16_t* __restrict__ qscale, float* __restrict__ output,
+                                                   g4_matmul_params p) {
+    __shared__ float partials[kWG];
+    const unsigned m = blockIdx.y * gridDim.x + blockIdx.x;
+    if (m >= p.M) return;
+    const unsigned tid = threadIdx.x;
+    const int8_t* row = qweight + (uint64_t)m * p.N;
+    const uint16_t* sc = qscale + (uint64_t)m * (p.N / 32);
+    float acc = 0.0f;
+    for (unsigned k = tid; k < p.N; k += kWG) {
+        const float w = (float)row[k] * h2f(sc[k >> 5]);
+        acc = acc + w * input[k];
+    }
+    partials[tid] = acc;
+    __syncthreads();
+    const float r = wg_tree_sum(partials, tid);
+    if (tid == 0) output[m] = r;
+}
+
+__global__ __launch_bounds__(kWG) void k_matmul_q4k(const float* __restrict__ input, const uint32_t* __restrict__ qweight,
+                                                    const uint16_t* __restrict__ qmeta, float* __restrict__ output,
+                                                    g4_matmul_params p) {
+    __shared__ float partials[kWG];
+    const unsigned m = blockIdx.y * gridDim.x + blockIdx.x;
+    if (m >= p.M) return;
+    const unsigned tid = threadIdx.x;
+    const uint64_t qbase = (uint64_t)m * p.N;
+    const uint16_t* meta = qmeta + (uint64_t)m * (p.N / 256) * 16;
+    float acc = 0.0f;
+    for (unsigned k = tid; k < p.N; k += kWG) {
+        const uint64_t fi = qbase + k;
+        const unsigned nib = (qweight[fi >> 3] >> ((fi & 7) * 4)) & 15u;
+        const uint16_t* mb = meta + (k >> 8) * 16;
+        const unsigned sub = (k & 255u) >> 5;
+        const float t = h2f(mb[sub]) * (float)nib;
+        const float w = t + h2f(mb[8 + sub]);
+        acc = acc + w * input[k];
+    }
     partials[tid] = acc;
     __syncthreads();
     const float r = wg_tree_sum(partials, tid);
@@ -255,18 +302,44 @@ int lm_head_run(const float* hidden, const uint16_t* weight, float* logits, uint
 
 extern "C" {
 
+// dispatchMatmul (src/engine.ts:370-377): M workgroups, or a sqrt-shaped 2D grid above 65535.
+static dim3 matmul_grid(uint32_t M) {
+    unsigned gx = M, gy = 1;
+    if (M > 65535u) {
+        gx = (unsigned)ceil(sqrt((double)M));
+        if (gx > 65535u) gx = 65535u;
+        gy = (M + gx - 1) / gx;
+    }
+    return dim3(gx, gy);
+}
+
 int g4_matmul_quant_f16(const float* input, const uint16_t* weight, float* output, g4_matmul_params p, void* stream) {
     if (!input || !weight || !output) return fail(G4_EINVAL, "matmulQuant: NULL pointer");
     if (p.M == 0) return G4_OK;
-    // dispatchMatmul (src/engine.ts:370-377): M workgroups, or a sqrt-shaped 2D grid above 65535
-    unsigned gx = p.M, gy = 1;
-    if (p.M > 65535u) {
-        gx = (unsigned)ceil(sqrt((double)p.M));
-        if (gx > 65535u) gx = 65535u;
-        gy = (p.M + gx - 1) / gx;
-    }
-    hipLaunchKernelGGL(k_matmul_quant_f16, dim3(gx, gy), dim3(kWG), 0, as_stream(stream), input, weight, output, p);
+    hipLaunchKernelGGL(k_matmul_quant_f16, matmul_grid(p.M), dim3(kWG), 0, as_stream(stream), input, weight, output, p);
     G4_CHECK_LAUNCH("matmulQuant");
+    return G4_OK;
+}
+
+int g4_matmul_q8(const float* input, const int8_t* qweight, const uint16_t* qscale, float* output, g4_matmul_params p,
+                 void* stream) {
+    if (!input || !qweight || !qscale || !output) return fail(G4_EINVAL, "matmulQ8: NULL pointer");
+    if (p.N % 32) return fail(G4_EINVAL, "matmulQ8: N %u is not a multiple of 32", p.N);
+    if (p.M == 0) return G4_OK;
+    hipLaunchKernelGGL(k_matmul_q8, matmul_grid(p.M), dim3(kWG), 0, as_stream(stream), input, qweight, qscale, output,
+                       p);
+    G4_CHECK_LAUNCH("matmulQ8");
+    return G4_OK;
+}
+
+int g4_matmul_q4k(const float* input, const uint32_t* qweight, const uint16_t* qmeta, float* output,
+                  g4_matmul_params p, void* stream) {
+    if (!input || !qweight || !qmeta || !output) return fail(G4_EINVAL, "matmulQ4K: NULL pointer");
+    if (p.N % 256) return fail(G4_EINVAL, "matmulQ4K: N %u is not a multiple of 256", p.N);
+    if (p.M == 0) return G4_OK;
+    hipLaunchKernelGGL(k_matmul_q4k, matmul_grid(p.M), dim3(kWG), 0, as_stream(stream), input, qweight, qmeta, output,
+                       p);
+    G4_CHECK_LAUNCH("matmulQ4K");
     return G4_OK;
 }
 

@@ -107,6 +107,13 @@ class LinearSeg(C.Structure):
     _fields_ = [("weight", C.c_void_p), ("out", C.c_void_p), ("rows", C.c_uint32)]
 
 
+class LinearQSeg(C.Structure):
+    _fields_ = [("weight", C.c_void_p), ("meta", C.c_void_p), ("out", C.c_void_p), ("rows", C.c_uint32)]
+
+
+G4_WEIGHT_Q8, G4_WEIGHT_Q4K = 1, 2
+
+
 class DecodePlan(C.Structure):
     _fields_ = [("opaque", C.c_uint64 * 8)]
 
@@ -164,6 +171,9 @@ SIGNATURES: dict[str, list] = {
     "g4_attn_prefill": [C.POINTER(PrefillEntry), _U32, _U32, _U32, _U32, _P, _SZ, _P],
     "g4_matmul_quant_f16": [_P, _P, _P, MatmulParams, _P],
     "g4_linear_f16": [_P, _U32, C.POINTER(LinearSeg), _U32, _P],
+    "g4_matmul_q8": [_P, _P, _P, _P, MatmulParams, _P],
+    "g4_matmul_q4k": [_P, _P, _P, _P, MatmulParams, _P],
+    "g4_linear_quant": [_P, _U32, _U32, C.POINTER(LinearQSeg), _U32, _P],
     "g4_logit_softcap": [_P, SoftcapParams, _P],
     "g4_argmax": [_P, _P, _U32, _P],
     "g4_lm_head_workspace_size": [LmHeadParams, C.POINTER(C.c_size_t)],

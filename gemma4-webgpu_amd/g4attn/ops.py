@@ -15,7 +15,8 @@ import ctypes as C
 import torch
 
 from . import abi
-from .abi import (AttnOutputParams, AttnScoreParams, DecodeEntry, DecodePlan, KvStoreParams, LinearSeg, LmHeadParams,
+from .abi import (G4_WEIGHT_Q4K, G4_WEIGHT_Q8, AttnOutputParams, AttnScoreParams, DecodeEntry, DecodePlan, KvStoreParams,
+                  LinearQSeg, LinearSeg, LmHeadParams,
                   MatmulParams, NormParams, NormRopeParams, PrepLayer, PrepParams, SoftcapParams, SoftmaxParams,
                   StepEntry)
 
@@ -389,6 +390,36 @@ def linear_f16(x, n, segments, stream=None):
     for i, (w, out, rows) in enumerate(segments):
         segs[i] = LinearSeg(_f16(w, f"segment {i} weight", rows * n), _f32(out, f"segment {i} out", rows), rows)
     abi.call("g4_linear_f16", _f32(x, "input", n), n, segs, len(segments), _stream(stream))
+
+
+I8_TYPES = (torch.int8, torch.uint8)
+U32_TYPES = (torch.int32, torch.uint32)
+
+
+def matmul_q8(x, qweight, qscale, out, M, N, stream=None):
+    """SHADERS.matmulQ8: out[m] = sum_k (int8 qweight[m][k] * f16 qscale[m][k / 32]) * x[k]."""
+    abi.call("g4_matmul_q8", _f32(x, "input", N), _dev(qweight, "qweight", I8_TYPES, M * N),
+             _f16(qscale, "qscale", M * (N // 32)), _f32(out, "output", M), MatmulParams(M, N), _stream(stream))
+
+
+def matmul_q4k(x, qweight, qmeta, out, M, N, stream=None):
+    """SHADERS.matmulQ4K: 4-bit weights packed 8 per u32 (low nibble first), f16 meta [M][N/256][16]."""
+    abi.call("g4_matmul_q4k", _f32(x, "input", N), _dev(qweight, "qweight", U32_TYPES, M * N // 8),
+             _f16(qmeta, "qmeta", M * (N // 256) * 16), _f32(out, "output", M), MatmulParams(M, N), _stream(stream))
+
+
+def linear_quant(x, n, fmt, segments, stream=None):
+    """The projections with quantized weights: fmt "q8" (segments of (int8 weight [rows][n], f16 scales
+    [rows][n/32], out, rows)) or "q4k" (u32 weight [rows][n/8], f16 meta [rows][n/256][16], out, rows)."""
+    q8 = fmt == "q8"
+    segs = (LinearQSeg * len(segments))()
+    for i, (w, meta, out, rows) in enumerate(segments):
+        wp = _dev(w, f"segment {i} weight", I8_TYPES, rows * n) if q8 else \
+            _dev(w, f"segment {i} weight", U32_TYPES, rows * n // 8)
+        mp = _f16(meta, f"segment {i} meta", rows * (n // 32 if q8 else n // 16))
+        segs[i] = LinearQSeg(wp, mp, _f32(out, f"segment {i} out", rows), rows)
+    abi.call("g4_linear_quant", _f32(x, "input", n), n, G4_WEIGHT_Q8 if q8 else G4_WEIGHT_Q4K, segs, len(segments),
+             _stream(stream))
 
 
 def logit_softcap(logits, size, cap, stream=None):

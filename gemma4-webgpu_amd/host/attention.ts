@@ -27,7 +27,10 @@ export type AttnKernelName =
 // The sampling head after the last layer (src/engine.ts:2223-2255).
 export type SampleKernelName = 'matmulQuant' | 'logitSoftcap' | 'argmax';
 
-export type KernelName = AttnKernelName | SampleKernelName;
+// The in-shader quantized GEMVs of the block's projections (weightQuant 'q8' / 'q4k', src/engine.ts:2040-2043).
+export type QuantKernelName = 'matmulQ8' | 'matmulQ4K';
+
+export type KernelName = AttnKernelName | SampleKernelName | QuantKernelName;
 
 export type FusedKernelName = 'attnStep' | 'attnPrefill' | 'lmHeadArgmax';
 
@@ -44,6 +47,8 @@ export const BINDINGS: Record<KernelName, string[]> = {
   matmulQuant: ['input', 'weight', 'output'],                // matmul_quant.wgsl:13-15 (f16 weight)
   logitSoftcap: ['logits'],                                  // logit_softcap.wgsl:6
   argmax: ['logits', 'result'],                              // argmax.wgsl:1-2
+  matmulQ8: ['input', 'qweight', 'qscale', 'output'],        // matmul_q8.wgsl:16-19
+  matmulQ4K: ['input', 'qweight', 'qmeta', 'output'],        // matmul_q4k.wgsl:20-23
 };
 
 // Params byte sizes (struct Params of each shader).
@@ -57,6 +62,8 @@ export const PARAMS_BYTES: Record<KernelName, number> = {
   matmulQuant: 8,
   logitSoftcap: 8,
   argmax: 4,
+  matmulQ8: 8,
+  matmulQ4K: 8,
 };
 
 // Profiler pass labels of the engine (src/engine.ts:2056-2094), plus the fused step.
@@ -73,6 +80,9 @@ export const PASS_LABELS: Record<string, string> = {
   logitSoftcap: 'logitSoftcap',
   argmax: 'sample.argmax',
   lmHeadArgmax: 'sample.lmHeadArgmax',
+  matmulQ8: 'attn.linearQKV',
+  matmulQ4K: 'attn.linearQKV',
+  linear: 'attn.linearQKV',
 };
 
 // The engine's makeUniformMixed: 4-byte fields, at least 16 bytes.
@@ -159,6 +169,15 @@ export interface LinearSegment {
   rows: number;
 }
 
+// One quantized weight matrix: q8 (int8 [rows][n] + f16 scales [rows][n/32]) or q4k (u32 [rows][n/8] +
+// f16 meta [rows][n/256][16]: 8 scales then 8 mins per 256-element super-block).
+export interface QuantSegment {
+  weight: DeviceBuffer;
+  meta: DeviceBuffer;
+  out: DeviceBuffer;          // f32 [rows]
+  rows: number;
+}
+
 export interface StepShape {
   numQHeads: number;
   numKvHeads: number;
@@ -186,6 +205,10 @@ export interface Addon {
   softmax(sc: bigint, p: Uint8Array, s: bigint): void;
   attnOutput(pr: bigint, vc: bigint, o: bigint, p: Uint8Array, s: bigint): void;
   matmulQuant(x: bigint, w: bigint, o: bigint, p: Uint8Array, s: bigint): void;
+  matmulQ8(x: bigint, q: bigint, sc: bigint, o: bigint, p: Uint8Array, s: bigint): void;
+  matmulQ4K(x: bigint, q: bigint, m: bigint, o: bigint, p: Uint8Array, s: bigint): void;
+  linearQuant(x: bigint, n: number, format: number, segs: { weight: bigint; meta: bigint; out: bigint; rows: number }[],
+    s: bigint): void;
   logitSoftcap(l: bigint, p: Uint8Array, s: bigint): void;
   argmax(l: bigint, r: bigint, p: Uint8Array, s: bigint): void;
   lmHeadWorkspaceSize(vocab: number, hidden: number, cap: number): number;
@@ -222,6 +245,8 @@ export const KERNELS: Record<KernelName, Launch> = {
   matmulQuant: function (g4, b, p, s) { g4.matmulQuant(b[0], b[1], b[2], p, s); },
   logitSoftcap: function (g4, b, p, s) { g4.logitSoftcap(b[0], p, s); },
   argmax: function (g4, b, p, s) { g4.argmax(b[0], b[1], p, s); },
+  matmulQ8: function (g4, b, p, s) { g4.matmulQ8(b[0], b[1], b[2], b[3], p, s); },
+  matmulQ4K: function (g4, b, p, s) { g4.matmulQ4K(b[0], b[1], b[2], b[3], p, s); },
 };
 
 export class HipAttention {
@@ -380,6 +405,19 @@ export class HipAttention {
       return { weight: g.weight.ptr, out: g.out.ptr, rows: g.rows };
     });
     this.g4.linear(input.ptr, n, segs, this.stream);
+  }
+
+  // The same with the engine's quantized weights: each row bit-identical to a matmulQ8 / matmulQ4K dispatch.
+  linearQuant(input: DeviceBuffer, n: number, format: 'q8' | 'q4k', segments: QuantSegment[]): void {
+    if (input.size < n * 4) throw new RangeError('linearQuant: input too small');
+    const q8 = format === 'q8';
+    const segs = segments.map(function (g, i) {
+      if (g.weight.size < g.rows * (q8 ? n : n / 2)) throw new RangeError('linearQuant: segment ' + i + ' weight too small');
+      if (g.meta.size < g.rows * (q8 ? n / 16 : n / 8)) throw new RangeError('linearQuant: segment ' + i + ' meta too small');
+      if (g.out.size < g.rows * 4) throw new RangeError('linearQuant: segment ' + i + ' out too small');
+      return { weight: g.weight.ptr, meta: g.meta.ptr, out: g.out.ptr, rows: g.rows };
+    });
+    this.g4.linearQuant(input.ptr, n, q8 ? 1 : 2, segs, this.stream);
   }
 
   synchronize(): void {

@@ -97,6 +97,7 @@ export function cpuChecks(): string[] {
     fusedPerHeadNormRope: 'sizeofNormRopeParams', perHeadRmsNormNoWeight: 'sizeofNormParams',
     kvCacheStore: 'sizeofKvStoreParams', attnScore: 'sizeofAttnScoreParams', softmax: 'sizeofSoftmaxParams',
     attnOutput: 'sizeofAttnOutputParams', matmulQuant: 'sizeofMatmulParams', logitSoftcap: 'sizeofSoftcapParams',
+    matmulQ8: 'sizeofMatmulParams', matmulQ4K: 'sizeofMatmulParams',
     argmax: 'sizeofArgmaxParams',
   };
   for (const n of names) {
@@ -290,7 +291,7 @@ function head(dir: string): string[] {
 }
 
 interface LinearSpec {
-  n: number; rows: number[]; arrays: Record<string, number[]>;
+  n: number; rows: number[]; format?: string; arrays: Record<string, number[]>;
 }
 
 function linear(dir: string): string[] {
@@ -310,15 +311,25 @@ function linear(dir: string): string[] {
     return b;
   }
   const x = upload('x');
+  const fmt = spec.format || 'f16';
   const ws = spec.rows.map(function (_r, i) { return upload('w' + i); });
+  const metas = fmt === 'f16' ? [] : spec.rows.map(function (_r, i) { return upload('m' + i); });
   const out1 = spec.rows.map(function (r) { return alloc(r * 4); });
   const out2 = spec.rows.map(function (r) { return alloc(r * 4); });
-  // (1) the engine's dispatches: one matmulQuant per matrix, uniform {M: rows, N: n}
+  // (1) the engine's dispatches: one matmulQuant / matmulQ8 / matmulQ4K per matrix, uniform {M: rows, N: n}
   spec.rows.forEach(function (r, i) {
-    att.dispatch('matmulQuant', [x, ws[i], out1[i]], new Uniform([{ u: r }, { u: spec.n }]));
+    const u = new Uniform([{ u: r }, { u: spec.n }]);
+    if (fmt === 'f16') att.dispatch('matmulQuant', [x, ws[i], out1[i]], u);
+    else att.dispatch(fmt === 'q8' ? 'matmulQ8' : 'matmulQ4K', [x, ws[i], metas[i], out1[i]], u);
   });
   // (2) one launch over all of them
-  att.linear(x, spec.n, spec.rows.map(function (r, i) { return { weight: ws[i], out: out2[i], rows: r }; }));
+  if (fmt === 'f16') {
+    att.linear(x, spec.n, spec.rows.map(function (r, i) { return { weight: ws[i], out: out2[i], rows: r }; }));
+  } else {
+    att.linearQuant(x, spec.n, fmt as 'q8' | 'q4k', spec.rows.map(function (r, i) {
+      return { weight: ws[i], meta: metas[i], out: out2[i], rows: r };
+    }));
+  }
   const total = spec.rows.reduce(function (a, b) { return a + b; }, 0);
   const res = new Uint8Array(2 * total * 4);
   let off = 0;

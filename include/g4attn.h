@@ -390,6 +390,23 @@ typedef struct g4_linear_seg {
 
 int g4_linear_f16(const float* input, uint32_t n, const g4_linear_seg* segs, uint32_t n_segs, void* stream);
 
+/* The same for the engine's in-shader quantized weights (weightQuant 'q8' /
+ * 'q4k', src/engine.ts:2040-2043): each row bit-identical to matmulQ8 /
+ * matmulQ4K. weight: int8 [rows][n] (q8) or u32 [rows][n/8] (q4k); meta: the
+ * f16 scales [rows][n/32] (q8) or scale/min table [rows][n/256][16] (q4k).
+ * Same limits as g4_linear_f16; weight 16-byte aligned. */
+#define G4_WEIGHT_Q8 1
+#define G4_WEIGHT_Q4K 2
+typedef struct g4_linear_qseg {
+    const void* weight;
+    const uint16_t* meta;
+    float* out;               /* f32 [rows] */
+    uint32_t rows;
+} g4_linear_qseg;
+
+int g4_linear_quant(const float* input, uint32_t n, uint32_t format, const g4_linear_qseg* segs, uint32_t n_segs,
+                    void* stream);
+
 /* ---- lm head -> logit softcap -> argmax (greedy top-1) ------------------
  * src/engine.ts:2223-2255: lmHead (matmulQuant over the f16 tied embedding
  * [vocab][hidden]), logitSoftcap (when final_logit_softcapping > 0), then
@@ -412,6 +429,17 @@ typedef struct g4_softcap_params {
  * the shader's order (invocation tid sums k = tid mod 256 in order, then the
  * 128 -> 1 tree): bit-identical to it. */
 int g4_matmul_quant_f16(const float* input, const uint16_t* weight, float* output, g4_matmul_params p, void* stream);
+/* shaders/matmul_q8.wgsl (matmulQ8; matmulQ8Mr, src/engine.ts:2040, has the
+ * same per-row arithmetic): int8 weights [M][N], one f16 scale per
+ * 32-element block [M][N/32]. N a multiple of 32. */
+int g4_matmul_q8(const float* input, const int8_t* qweight, const uint16_t* qscale, float* output, g4_matmul_params p,
+                 void* stream);
+/* shaders/matmul_q4k.wgsl (matmulQ4K; matmulQ4KMr likewise): 4-bit weights
+ * packed 8 per u32, low nibble first, over the flat [M][N] array; per row and
+ * 256-element super-block 16 f16 values, the 8 sub-block scales then the 8
+ * mins. N a multiple of 256. */
+int g4_matmul_q4k(const float* input, const uint32_t* qweight, const uint16_t* qmeta, float* output,
+                  g4_matmul_params p, void* stream);
 
 /* SHADERS.logitSoftcap — logit_softcap.wgsl:9-16 (src/engine.ts:2230-2236). In place. */
 int g4_logit_softcap(float* logits, g4_softcap_params p, void* stream);

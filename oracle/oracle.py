@@ -204,6 +204,30 @@ def matmul_quant(x, weight_bits, M, N):
     return out
 
 
+def matmul_q8(x, qweight, qscale_bits, M, N):
+    """matmul_q8.wgsl: int8 weights [M][N] (numpy int8 or their bytes), f16 scale bits [M][N/32], f32 input [N]."""
+    assert N % 32 == 0
+    x = _f32(x)
+    q = np.ascontiguousarray(qweight).view(np.int8).ravel()
+    s = _u16(qscale_bits).ravel()
+    assert x.size >= N and q.size >= M * N and s.size >= M * (N // 32)
+    out = np.empty(M, dtype=np.float32)
+    lib().wr_matmul_q8(_p(x), _p(q), _p(s), _p(out), C.c_uint32(M), C.c_uint32(N))
+    return out
+
+
+def matmul_q4k(x, qweight_words, qmeta_bits, M, N):
+    """matmul_q4k.wgsl: 4-bit weights packed 8 per u32 [M*N/8], f16 meta [M][N/256][16] (8 scales, 8 mins)."""
+    assert N % 256 == 0
+    x = _f32(x)
+    q = np.ascontiguousarray(qweight_words, dtype=np.uint32).ravel()
+    s = _u16(qmeta_bits).ravel()
+    assert x.size >= N and q.size >= M * N // 8 and s.size >= M * (N // 256) * 16
+    out = np.empty(M, dtype=np.float32)
+    lib().wr_matmul_q4k(_p(x), _p(q), _p(s), _p(out), C.c_uint32(M), C.c_uint32(N))
+    return out
+
+
 def logit_softcap(logits, cap):
     x = _f32(logits)
     lib().wr_logit_softcap(_p(x), C.c_uint32(x.size), C.c_float(cap))

@@ -339,6 +339,64 @@ void wr_matmul_quant(const float* input, const uint16_t* weight, float* output, 
     }
 }
 
+/* ---- shaders/matmul_q8.wgsl:31-64 (and matmul_q8_mr.wgsl:50-79, the same
+ * per-row order) -------------------------------------------------------------
+ * int8 weights (row-major [M][N], two's complement bytes), one f16 scale per
+ * 32-element block of a row ([M][N/32]). Partial t: acc + (q * scale) * x over
+ * k = t, t + 256, ..., each operation rounded to f32; then the 128 -> 1 tree. */
+void wr_matmul_q8(const float* input, const int8_t* qweight, const uint16_t* qscale, float* output, uint32_t M,
+                  uint32_t N) {
+#pragma omp parallel for schedule(static)
+    for (int64_t m = 0; m < (int64_t)M; m++) {
+        float partials[WG];
+        const int8_t* row = qweight + (uint64_t)m * N;
+        const uint16_t* sc = qscale + (uint64_t)m * (N / 32);
+        for (uint32_t tid = 0; tid < WG; tid++) {
+            float acc = 0.0f;
+            for (uint32_t k = tid; k < N; k += WG) {
+                const float w = (float)row[k] * wr_f16_to_f32(sc[k >> 5]);
+                const float prod = w * input[k];
+                acc = acc + prod;
+            }
+            partials[tid] = acc;
+        }
+        output[m] = tree_sum(partials);
+    }
+}
+
+/* ---- shaders/matmul_q4k.wgsl:34-58 (and matmul_q4k_mr.wgsl) ---------------
+ * 4-bit unsigned weights, 8 per u32 little-endian nibble order over the flat
+ * [M][N] array; per row and 256-element super-block, 16 f16 values: the scales
+ * of its 8 sub-blocks of 32, then their mins. dequant = scale * nibble + min
+ * (two rounded operations), acc + dequant * x; then the tree.                */
+void wr_matmul_q4k(const float* input, const uint32_t* qweight, const uint16_t* qmeta, float* output, uint32_t M,
+                   uint32_t N) {
+    const uint32_t nsblk = N / 256;
+#pragma omp parallel for schedule(static)
+    for (int64_t m = 0; m < (int64_t)M; m++) {
+        float partials[WG];
+        const uint64_t qbase = (uint64_t)m * N;
+        const uint64_t mbase_row = (uint64_t)m * nsblk * 16;
+        for (uint32_t tid = 0; tid < WG; tid++) {
+            float acc = 0.0f;
+            for (uint32_t k = tid; k < N; k += WG) {
+                const uint64_t fi = qbase + k;
+                const uint32_t nib = (qweight[fi >> 3] >> ((fi & 7) * 4)) & 0xfu;
+                const uint64_t mb = mbase_row + (uint64_t)(k >> 8) * 16;
+                const uint32_t sub = (k & 255u) >> 5;
+                const float scale = wr_f16_to_f32(qmeta[mb + sub]);
+                const float mn = wr_f16_to_f32(qmeta[mb + 8 + sub]);
+                const float t = scale * (float)nib;
+                const float dq = t + mn;
+                const float prod = dq * input[k];
+                acc = acc + prod;
+            }
+            partials[tid] = acc;
+        }
+        output[m] = tree_sum(partials);
+    }
+}
+
 /* ---- shaders/logit_softcap.wgsl:9-16 ------------------------------------ */
 void wr_logit_softcap(float* logits, uint32_t size, float cap) {
     for (uint32_t i = 0; i < size; i++) {

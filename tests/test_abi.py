@@ -54,6 +54,7 @@ STRUCTS = {
     "g4_softcap_params": abi.SoftcapParams,
     "g4_lm_head_params": abi.LmHeadParams,
     "g4_linear_seg": abi.LinearSeg,
+    "g4_linear_qseg": abi.LinearQSeg,
 }
 
 

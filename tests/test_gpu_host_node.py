@@ -289,3 +289,42 @@ def test_promise_readback_through_ts_host(tmp_path):
     got = np.frombuffer((tmp_path / "out.bin").read_bytes(), np.uint32)
     np.testing.assert_array_equal(got[:x.size], orc.logit_softcap(x, 30.0).view(np.uint32))
     assert not got[x.size:].any()
+
+
+@pytest.mark.skipif(NODE is None, reason="node is not installed")
+@pytest.mark.parametrize("fmt", ["q8", "q4k"])
+def test_quantized_linear_through_ts_host(tmp_path, fmt):
+    """The engine's matmulQ8 / matmulQ4K dispatches (one per matrix) and one linearQuant call, both
+    bit-identical to the oracle."""
+    announce(f"TS host linear {fmt}")
+    n, rows = 1536, [2048, 256, 256]
+    rng = np.random.default_rng(41)
+    x = rng.standard_normal(n, dtype=np.float32)
+    arrays, blob, wants = dict(x=[0, x.nbytes]), [x.tobytes()], []
+    off = x.nbytes
+    for i, r in enumerate(rows):
+        if fmt == "q8":
+            w = rng.integers(-128, 128, size=(r, n)).astype(np.int8)
+            m = (rng.random((r, n // 32)) * 0.002 + 1e-4).astype(np.float16).view(np.uint16)
+            wants.append(orc.matmul_q8(x, w, m, r, n))
+        else:
+            nib = rng.integers(0, 16, size=(r * n // 8, 8)).astype(np.uint32)
+            w = (nib << (4 * np.arange(8, dtype=np.uint32))).sum(axis=1, dtype=np.uint64).astype(np.uint32)
+            m = np.concatenate([(rng.random((r, n // 256, 8)) * 0.01).astype(np.float16),
+                                (rng.standard_normal((r, n // 256, 8)) * 0.05).astype(np.float16)], axis=2).view(np.uint16)
+            wants.append(orc.matmul_q4k(x, w, m, r, n))
+        for name, a in ((f"w{i}", w), (f"m{i}", m)):
+            b = np.ascontiguousarray(a).tobytes()
+            arrays[name] = [off, len(b)]
+            blob.append(b)
+            off += len(b)
+    (tmp_path / "case.bin").write_bytes(b"".join(blob))
+    (tmp_path / "case.json").write_text(json.dumps(dict(n=n, rows=rows, format=fmt, arrays=arrays)))
+    r = subprocess.run([NODE, str(RUN), "linear", str(tmp_path)], cwd=ROOT, capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 0, r.stderr
+    got = np.frombuffer((tmp_path / "out.bin").read_bytes(), np.uint32)
+    want = np.concatenate(wants).view(np.uint32)
+    total = sum(rows)
+    np.testing.assert_array_equal(got[:total], want)
+    np.testing.assert_array_equal(got[total:], want)

@@ -1,6 +1,7 @@
-"""GPU parity of the f16 projections either side of the attention block (attn.linearQKV,
-src/engine.ts:2045-2051; attn.linearOut, :2096) against the oracle's matmul_quant.wgsl restatement:
-bit-identical rows, one or several weight matrices per launch. And one producer layer end to end:
+"""GPU parity of the projections either side of the attention block (attn.linearQKV,
+src/engine.ts:2045-2051; attn.linearOut, :2096) against the oracle's matmul_quant.wgsl,
+matmul_q8.wgsl and matmul_q4k.wgsl restatements: bit-identical rows, one or several weight matrices
+per launch, and the reference-shaped matmulQ8 / matmulQ4K kernels likewise. And one producer layer end to end:
 normed hidden state -> q/k/v projections -> the one-launch step (norms, RoPE, KV store, attention)
 -> o_proj, against the oracle's matmulQuant x3 -> six reference kernels -> matmulQuant.
 """
@@ -39,6 +40,74 @@ def test_linear_bits(dev, N, rows):
     torch.cuda.synchronize()
     for i, (w, o, r) in enumerate(zip(ws, outs, rows)):
         want = orc.matmul_quant(x, w, r, N)
+        np.testing.assert_array_equal(o.cpu().numpy().view(np.uint32), want.view(np.uint32), err_msg=f"segment {i}")
+
+
+def q8_weights(seed, M, N):
+    rng = np.random.default_rng(seed)
+    q = rng.integers(-128, 128, size=(M, N)).astype(np.int8)
+    sc = (rng.random((M, N // 32)) * 0.002 + 1e-4).astype(np.float16).view(np.uint16)
+    return q, sc
+
+
+def q4k_weights(seed, M, N):
+    rng = np.random.default_rng(seed)
+    nib = rng.integers(0, 16, size=(M * N // 8, 8)).astype(np.uint32)
+    words = (nib << (4 * np.arange(8, dtype=np.uint32))).sum(axis=1, dtype=np.uint64).astype(np.uint32)
+    sb = N // 256
+    meta = np.concatenate([(rng.random((M, sb, 8)) * 0.01).astype(np.float16),
+                           (rng.standard_normal((M, sb, 8)) * 0.05).astype(np.float16)], axis=2)
+    return words, meta.view(np.uint16)
+
+
+def t_i8(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.int8)).to(dev)
+
+
+def t_u32(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint32).view(np.int32)).to(dev)
+
+
+@pytest.mark.parametrize("fmt,M,N", [("q8", 1000, 1536), ("q8", 70000, 256), ("q8", 5, 96), ("q4k", 1000, 1536),
+                                     ("q4k", 70000, 256), ("q4k", 3, 4096)])
+def test_matmul_quantized_reference_kernels(dev, fmt, M, N):
+    """matmulQ8 / matmulQ4K as the engine dispatches them (one workgroup per row; a 2D grid above 65535 rows)."""
+    announce(f"matmul {fmt} M={M} N={N}")
+    x = np.random.default_rng(N + M).standard_normal(N, dtype=np.float32)
+    out = torch.full((M,), float("nan"), device=dev)
+    if fmt == "q8":
+        q, sc = q8_weights(M + N, M, N)
+        ops.matmul_q8(t_f32(x, dev), t_i8(q, dev), t_u16(sc, dev), out, M, N)
+        want = orc.matmul_q8(x, q, sc, M, N)
+    else:
+        w, meta = q4k_weights(M + N, M, N)
+        ops.matmul_q4k(t_f32(x, dev), t_u32(w, dev), t_u16(meta, dev), out, M, N)
+        want = orc.matmul_q4k(x, w, meta, M, N)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("fmt", ["q8", "q4k"])
+@pytest.mark.parametrize("N,rows", [(1536, [2048, 256, 256]), (2048, [1536]), (4096, [1536]), (1024, [1]),
+                                    (1536, [3, 1, 262, 5]), (3072, [777])])
+def test_linear_quant_bits(dev, fmt, N, rows):
+    """The fused projections with q8 / q4k weights: each row bit-identical to matmulQ8 / matmulQ4K."""
+    announce(f"linear {fmt} N={N} rows={rows}")
+    x = np.random.default_rng(N + 5).standard_normal(N, dtype=np.float32)
+    segs, wants = [], []
+    outs = [torch.full((r,), float("nan"), device=dev) for r in rows]
+    for i, (r, o) in enumerate(zip(rows, outs)):
+        if fmt == "q8":
+            q, sc = q8_weights(N + 17 * i + r, r, N)
+            segs.append((t_i8(q, dev), t_u16(sc, dev), o, r))
+            wants.append(orc.matmul_q8(x, q, sc, r, N))
+        else:
+            w, meta = q4k_weights(N + 17 * i + r, r, N)
+            segs.append((t_u32(w, dev), t_u16(meta, dev), o, r))
+            wants.append(orc.matmul_q4k(x, w, meta, r, N))
+    ops.linear_quant(t_f32(x, dev), N, fmt, segs)
+    torch.cuda.synchronize()
+    for i, (o, want) in enumerate(zip(outs, wants)):
         np.testing.assert_array_equal(o.cpu().numpy().view(np.uint32), want.view(np.uint32), err_msg=f"segment {i}")
 
 

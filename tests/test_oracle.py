@@ -411,6 +411,80 @@ def test_matmul_quant_summation_order(oracle):
     assert seq == 0.0
 
 
+def _pack_nibbles(nib):
+    """[rows][N] values 0..15 -> u32 words, 8 per word, low nibble first (matmul_q4k.wgsl:42-44)."""
+    n = np.asarray(nib, dtype=np.uint32).reshape(-1, 8)
+    return (n << (4 * np.arange(8, dtype=np.uint32))).sum(axis=1, dtype=np.uint64).astype(np.uint32)
+
+
+def test_matmul_q8_equals_f16_path_on_exact_weights(oracle):
+    """Scales that are powers of two make every dequantized weight int8 * 2^-e exact in f16, so matmul_q8.wgsl
+    must equal matmul_quant.wgsl on those f16 weights bit for bit (the per-row order is the same, and matmul_quant
+    is pinned by its own tests). Scales differ per 32-block, so a wrong block index breaks the equality."""
+    rng = np.random.default_rng(8)
+    M, N = 37, 1024
+    q = rng.integers(-128, 128, size=(M, N)).astype(np.int8)
+    e = rng.integers(0, 6, size=(M, N // 32))
+    sc = (2.0 ** -e).astype(np.float16)
+    x = rng.standard_normal(N).astype(np.float32)
+    got = oracle.matmul_q8(x, q, _f16_bits(sc), M, N)
+    w = (q.astype(np.float32) * np.repeat(sc.astype(np.float32), 32, axis=1)).astype(np.float16)
+    assert (w.astype(np.float32) == q * np.repeat(sc.astype(np.float32), 32, axis=1)).all()
+    want = oracle.matmul_quant(x, _f16_bits(w), M, N)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_matmul_q8_closed_form(oracle):
+    rng = np.random.default_rng(9)
+    M, N = 64, 2048
+    q = rng.integers(-128, 128, size=(M, N)).astype(np.int8)
+    sc = (rng.random((M, N // 32)) * 0.02 + 1e-3).astype(np.float16)
+    x = rng.standard_normal(N).astype(np.float32)
+    got = oracle.matmul_q8(x, q, _f16_bits(sc), M, N)
+    w = q.astype(np.float64) * np.repeat(sc.astype(np.float64), 32, axis=1)
+    np.testing.assert_allclose(got, w @ x.astype(np.float64), rtol=0, atol=2e-4 * np.sqrt(N / 256))
+
+
+def test_matmul_q4k_equals_f16_path_on_exact_weights(oracle):
+    """Power-of-two scales and small half-integer mins: scale * nibble + min is exact in f16, so matmul_q4k.wgsl
+    equals matmul_quant.wgsl on the dequantized weights bit for bit. Scales and mins differ per sub-block and
+    super-block, and the nibbles are packed low nibble first: a swapped nibble order, a scale/min mix-up or a
+    wrong block index breaks the equality."""
+    rng = np.random.default_rng(10)
+    M, N = 29, 1536
+    nib = rng.integers(0, 16, size=(M, N))
+    sb = N // 256
+    scales = (2.0 ** -rng.integers(0, 4, size=(M, sb, 8))).astype(np.float16)
+    mins = (rng.integers(-8, 9, size=(M, sb, 8)) * 0.5).astype(np.float16)
+    meta = np.concatenate([scales, mins], axis=2)  # [M][sb][16]: 8 scales then 8 mins
+    x = rng.standard_normal(N).astype(np.float32)
+    got = oracle.matmul_q4k(x, _pack_nibbles(nib), _f16_bits(meta), M, N)
+    k = np.arange(N)
+    s_full = scales.astype(np.float32)[:, k // 256, (k % 256) // 32]
+    m_full = mins.astype(np.float32)[:, k // 256, (k % 256) // 32]
+    w32 = s_full * nib + m_full
+    w = w32.astype(np.float16)
+    assert (w.astype(np.float32) == w32).all()
+    want = oracle.matmul_quant(x, _f16_bits(w), M, N)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_matmul_q4k_closed_form(oracle):
+    rng = np.random.default_rng(11)
+    M, N = 40, 2048
+    nib = rng.integers(0, 16, size=(M, N))
+    sb = N // 256
+    meta = np.concatenate([(rng.random((M, sb, 8)) * 0.01).astype(np.float16),
+                           (rng.standard_normal((M, sb, 8)) * 0.05).astype(np.float16)], axis=2)
+    x = rng.standard_normal(N).astype(np.float32)
+    got = oracle.matmul_q4k(x, _pack_nibbles(nib), _f16_bits(meta), M, N)
+    k = np.arange(N)
+    s_full = meta[:, :, :8].astype(np.float64)[:, k // 256, (k % 256) // 32]
+    m_full = meta[:, :, 8:].astype(np.float64)[:, k // 256, (k % 256) // 32]
+    np.testing.assert_allclose(got, (s_full * nib + m_full) @ x.astype(np.float64), rtol=0,
+                               atol=2e-4 * np.sqrt(N / 256))
+
+
 def test_softcap_closed_form(oracle):
     x = (synth.normal(4, 4096) * 40).astype(np.float32)
     np.testing.assert_allclose(oracle.logit_softcap(x, 30.0), cf.softcap(x, 30.0), atol=2e-5)
