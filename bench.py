@@ -241,6 +241,41 @@ def run_gpu(spec, args):
     return result
 
 
+def measure_read_ceiling(torch, ops, gib: int = 2, reps: int = 10) -> float:
+    """GB/s of a plain nontemporal streaming read over `gib` GiB (g4_read_ceiling), timed with events on
+    the kernel's own start and end, best of `reps`: the measured ceiling next to the spec-sheet peak."""
+    dev = torch.device("cuda:0")
+    buf = torch.randint(0, 256, (gib << 30,), dtype=torch.uint8, device=dev)
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    for _ in range(3):
+        ops.read_ceiling(buf, sink)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    stream = torch.cuda.current_stream()
+    for a_, b_ in evs:
+        a_.record(stream)
+        b_.record(stream)
+    torch.cuda.synchronize()
+    for a_, b_ in evs:
+        ops.read_ceiling(buf, sink, a_, b_)
+    torch.cuda.synchronize()
+    ms = min(a_.elapsed_time(b_) for a_, b_ in evs)  # a ceiling: the best of the runs
+    del buf
+    return (gib << 30) / (ms * 1e-3) / 1e9
+
+
+def ceiling_fields(achieved_gbs: float) -> dict:
+    """The measured read-stream ceiling of this GPU and the kernel's fraction of it (next to `frac`, which
+    is against the spec sheet's 8 TB/s)."""
+    import torch
+
+    from g4attn import ops
+
+    c = measure_read_ceiling(torch, ops)
+    log(f"read-stream ceiling {c:.1f} GB/s")
+    return {"measured_ceiling": round(c, 1), "frac_of_measured_ceiling": round(achieved_gbs / c, 4),
+            "ceiling_source": "g4_read_ceiling: 2 GiB nontemporal 16-byte streaming read, best of 10"}
+
+
 def read_traffic(workload: str):
     """HBM bytes per k_attn_step launch from the committed counter summary of this workload
     (FETCH_SIZE and WRITE_SIZE passes of rocprofv3 --pmc, scaled by a copy kernel's reading)."""
@@ -489,6 +524,7 @@ def main_lmhead(args):
                      "avg_us": round(k_ms * 1e3, 2),
                      "traffic_source": "profiles/k_lm_head_lmhead_traffic.txt" if traffic else None},
     }
+    line["roofline"].update(ceiling_fields(achieved))
     if not args.no_cpu_baseline:
         from oracle import oracle as orc
 
@@ -566,6 +602,8 @@ def main():
                      "traffic": traffic, "avg_us": round(r["attn_avg_ms"] * 1e3, 2),
                      "traffic_source": f"profiles/k_attn_step_{args.workload}_traffic.txt" if traffic else None},
     }
+    ceiling = ceiling_fields(achieved)
+    line["roofline"].update(ceiling)
     if "sequential_us" in r:
         line["layer_sequential_us_per_token"] = round(r["sequential_us"], 2)
     if not args.no_cpu_baseline:

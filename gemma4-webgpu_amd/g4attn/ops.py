@@ -320,6 +320,15 @@ def attn_step_run_attention_timed(plan: DecodePlan, start, stop, stream=None):
              C.c_void_p(stop.cuda_event))
 
 
+def read_ceiling(buf, sink, start=None, stop=None, stream=None):
+    """The device's read-stream ceiling: streams buf (a contiguous GPU tensor) with the decode kernels'
+    nontemporal 16-byte loads; with events (timing enabled, recorded once before), they take the kernel's
+    own start and end."""
+    ev = [C.c_void_p(e.cuda_event) if e is not None else None for e in (start, stop)]
+    abi.call("g4_read_ceiling", _dev(buf, "buf", buf.dtype, 1), buf.numel() * buf.element_size(),
+             _dev(sink, "sink", (torch.int32, torch.uint32), 1), _stream(stream), ev[0], ev[1])
+
+
 def attn_step(entries, num_q_heads, num_kv_heads, head_dim, workspace, stream=None):
     abi.call("g4_attn_step", entries, len(entries), num_q_heads, num_kv_heads, head_dim,
              _dev(workspace, "workspace", torch.uint8, 0), workspace.numel(), _stream(stream))

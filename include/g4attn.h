@@ -72,6 +72,13 @@ int g4_download(void* host_dst, const void* dev_src, size_t offset, size_t bytes
 typedef struct g4_readback g4_readback;
 int g4_readback_begin(const void* dev_src, size_t offset, size_t bytes, void* stream, g4_readback** handle);
 int g4_readback_finish(g4_readback* handle, void* host_dst);
+/* Measurement hook (no counterpart in the reference): the device's read-stream
+ * ceiling. Streams `bytes` of buf with nontemporal 16-byte loads (the decode
+ * kernels' load form) and writes nothing (sink is only a guard against the
+ * loads being dropped); the two events, when given (created with timing),
+ * record the kernel's own start and end. bytes / elapsed is the ceiling that
+ * a kernel's achieved bandwidth is compared with, next to the spec sheet. */
+int g4_read_ceiling(const void* buf, size_t bytes, uint32_t* sink, void* stream, void* start_event, void* stop_event);
 /* Zero `bytes` at dev_dst with a fill kernel (safe inside HIP graph capture). */
 int g4_zero(void* dev_dst, size_t bytes, void* stream);
 
