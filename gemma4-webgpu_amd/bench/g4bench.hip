@@ -6,6 +6,12 @@
 //   g4bench [--workload stack8k|stack32k|long128k|ragged64|layer512|prefill4k|lmhead|copy] [--iters N]
 //           [--sets S] [--mode M]
 //
+// Decode workloads: the configurations above; `e2b8k` / `e2b32k` (35 layers at E2B's head dims,
+// 512 on global layers: one step per head_dim group); `e2bshared8k` / `e2bshared32k` (the same
+// with E2B's cache sharing: layers 15..34 read layer 13's or 14's cache and store nothing);
+// `long128k_hd512`. --mode step (default: the one-launch step), graph (the step replayed as a
+// captured HIP graph), or, for head_dim 256 only, the unfused prep + split + merge.
+//
 // `prefill4k` runs the causal MFMA prefill of a 4096-token prompt for one
 // global layer and one 512-window local layer, as 512-token chunks (16
 // entries in one launch; --mode whole: one entry per layer).
@@ -273,6 +279,7 @@ struct Layer {
     float theta;
     unsigned divisor;
     unsigned hd = HD;  // head_dim (E2B: 256 on local layers, 512 on global layers)
+    int src = -1;      // KV producer layer (E2B's shared layers); -1: its own cache
 };
 
 static std::vector<Layer> workload(const std::string& w) {
@@ -288,6 +295,15 @@ static std::vector<Layer> workload(const std::string& w) {
         for (int i = 0; i < 35; i++) {
             bool global = (i % 5) == 4;
             L.push_back({pos + 1, global ? 0u : 512u, pos, global ? 1e6f : 1e4f, global ? 1u : 0u, global ? 512u : 256u});
+        }
+    } else if (w == "e2bshared8k" || w == "e2bshared32k") {
+        // E2B's cache sharing (src/config/gemma4-e2b.ts:159-178): layers 15..34 read the cache of the
+        // last unshared layer of their type (13 local, 14 global) and store nothing
+        unsigned pos = w == "e2bshared8k" ? 8192 : 32768;
+        for (int i = 0; i < 35; i++) {
+            bool global = (i % 5) == 4;
+            L.push_back({pos + 1, global ? 0u : 512u, pos, global ? 1e6f : 1e4f, global ? 1u : 0u,
+                         global ? 512u : 256u, i < 15 ? -1 : (global ? 14 : 13)});
         }
     } else if (w == "long128k") {
         L.push_back({131072, 0, 131071, 1e6f, 1});
@@ -434,22 +450,38 @@ int main(int argc, char** argv) {
         std::vector<g4_decode_entry> ents;
         std::vector<g4_prep_layer> preps;
         std::vector<g4_step_entry> steps[2];
-        for (auto& l : L) {
+        std::vector<void*> lkc(L.size()), lvc(L.size()), lk(L.size()), lv(L.size());
+        for (size_t li = 0; li < L.size(); li++) {
+            const Layer& l = L[li];
             void *kc, *vc, *q, *k, *v, *out;
             const unsigned hd = l.hd;
             const size_t cache_bytes = (size_t)l.seq * NKH * hd * 2;
-            CK(g4_malloc(&kc, cache_bytes));
-            CK(g4_malloc(&vc, cache_bytes));
             CK(g4_malloc(&q, NQH * hd * 4));
-            CK(g4_malloc(&k, NKH * hd * 4));
-            CK(g4_malloc(&v, NKH * hd * 4));
             CK(g4_malloc(&out, NQH * hd * 4));
-            hipLaunchKernelGGL(k_fill_f16, dim3(1024), dim3(256), 0, st, (_Float16*)kc, (uint64_t)cache_bytes / 2, seed++);
-            hipLaunchKernelGGL(k_fill_f16, dim3(1024), dim3(256), 0, st, (_Float16*)vc, (uint64_t)cache_bytes / 2, seed++);
             hipLaunchKernelGGL(k_fill_f32, dim3(8), dim3(256), 0, st, (float*)q, (uint64_t)NQH * hd, seed++);
-            hipLaunchKernelGGL(k_fill_f32, dim3(2), dim3(256), 0, st, (float*)k, (uint64_t)NKH * hd, seed++);
-            hipLaunchKernelGGL(k_fill_f32, dim3(2), dim3(256), 0, st, (float*)v, (uint64_t)NKH * hd, seed++);
-            S[s].bufs.insert(S[s].bufs.end(), {kc, vc, q, k, v, out});
+            if (l.src >= 0) {  // a consumer: the producer's cache and raw k/v (the row is recomputed)
+                kc = lkc[l.src];
+                vc = lvc[l.src];
+                k = lk[l.src];
+                v = lv[l.src];
+                S[s].bufs.insert(S[s].bufs.end(), {q, out});
+            } else {
+                CK(g4_malloc(&kc, cache_bytes));
+                CK(g4_malloc(&vc, cache_bytes));
+                CK(g4_malloc(&k, NKH * hd * 4));
+                CK(g4_malloc(&v, NKH * hd * 4));
+                hipLaunchKernelGGL(k_fill_f16, dim3(1024), dim3(256), 0, st, (_Float16*)kc, (uint64_t)cache_bytes / 2,
+                                   seed++);
+                hipLaunchKernelGGL(k_fill_f16, dim3(1024), dim3(256), 0, st, (_Float16*)vc, (uint64_t)cache_bytes / 2,
+                                   seed++);
+                hipLaunchKernelGGL(k_fill_f32, dim3(2), dim3(256), 0, st, (float*)k, (uint64_t)NKH * hd, seed++);
+                hipLaunchKernelGGL(k_fill_f32, dim3(2), dim3(256), 0, st, (float*)v, (uint64_t)NKH * hd, seed++);
+                S[s].bufs.insert(S[s].bufs.end(), {kc, vc, q, k, v, out});
+            }
+            lkc[li] = kc;
+            lvc[li] = vc;
+            lk[li] = k;
+            lv[li] = v;
             ents.push_back({(const float*)q, (const uint16_t*)kc, (const uint16_t*)vc, (float*)out, l.seq, l.window,
                             1.0f, 0});
             g4_prep_layer p = {};
@@ -479,7 +511,7 @@ int main(int argc, char** argv) {
             se.seq_len = l.seq;
             se.position = l.pos;
             se.sliding_window = l.window;
-            se.store_kv = 1;
+            se.store_kv = l.src >= 0 ? 0 : 1;
             se.theta = l.theta;
             se.apply_divisor = l.divisor;
             se.scale = 1.0f;
