@@ -293,11 +293,12 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_prefill(PrefillArgs a) {
 //
 // The same per-tile arithmetic, fed differently: K rows and V^T blocks go from
 // global memory straight into LDS (global_load_lds_dwordx4, no register
-// staging), kPfStages tiles deep, one barrier per tile. V is transposed once
+// staging), one barrier per tile. V is transposed once
 // per prefill call into 32-key blocks [HD][32] (k_vt_blocks), so a V^T tile is
 // one contiguous read. The 16-byte chunks of both LDS tiles are XOR-swizzled
-// so that the MFMA operand reads (eight lanes per LDS cycle, each a different
-// row) hit distinct banks.
+// so that the MFMA operand reads hit distinct banks in every group of sixteen
+// lanes (a 128-bit LDS read is served 256 bytes at a time on gfx950; sixteen
+// lanes, each a different row, per LDS cycle).
 //
 // head_dim 512 (E2B global layers): a workgroup's output covers one half of
 // the head dimension (blockIdx.z), so the accumulators stay at 128 registers;
@@ -305,31 +306,42 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_prefill(PrefillArgs a) {
 // stages) and read their own 256 rows of the V^T block.
 
 constexpr unsigned kPfCUs = 256;  // MI355X compute units: one prefill workgroup each
+// Tile t's K rows are read by the score MFMAs of iteration t - 1 and its V^T
+// block by the output MFMAs of iteration t + 1; both are issued together at
+// iteration t - 1 - kPfDist. The K ring holds kPfDist + 1 tiles, the V^T ring
+// kPfDist + 3 (128 KiB of LDS at either head_dim).
 template <int HD>
-constexpr int kPfStages = HD == 256 ? 4 : 3;
+constexpr int kPfDist = HD == 256 ? 2 : 1;
+template <int HD>
+constexpr int kPfKStages = kPfDist<HD> + 1;
+template <int HD>
+constexpr int kPfVStages = kPfDist<HD> + 3;
 template <int HD>
 constexpr unsigned kPfKTileBytes = kPfKeys * HD * 2;  // one K tile; also one V^T block in global memory
 constexpr unsigned kPfVtTileBytes = kPfKeys * 256 * 2;  // the V^T rows of one 256-wide output half
 
 template <int HD>
 struct PrefillDmaSmem {
-    unsigned char k[kPfStages<HD>][kPfKTileBytes<HD>];  // key row r: chunk c (8 d) at r*2HD + ((c ^ swz_k(r)) * 16)
-    unsigned char vt[kPfStages<HD>][kPfVtTileBytes];    // d row: chunk c (8 keys) at d*64 + ((c ^ swz_v(d)) * 16)
+    unsigned char k[kPfKStages<HD>][kPfKTileBytes<HD>];  // key row r: chunk c (8 d) at r*2HD + ((c ^ swz_k(r)) * 16)
+    unsigned char vt[kPfVStages<HD>][kPfVtTileBytes];    // d row: chunk c (8 keys) at d*64 + ((c ^ swz_v(d)) * 16)
 };
 
-__device__ __forceinline__ unsigned swz_k(unsigned r) { return (r & 3u) | ((r >> 1) & 4u); }
-__device__ __forceinline__ unsigned swz_v(unsigned d) { return (d >> 1) & 3u; }
+__device__ __forceinline__ unsigned swz_k(unsigned r) { return r & 15u; }
+__device__ __forceinline__ unsigned swz_v(unsigned d) { return (d >> 2) & 3u; }
 
 // Waits until at most `younger` tiles' DMAs of this wave are still in flight
-// (PER instructions per tile), then joins the workgroup's barrier.
+// (PER instructions per tile) and this wave's LDS reads have returned, then
+// joins the workgroup's barrier.
 template <int PER>
 __device__ __forceinline__ void dma_wait_barrier(int younger) {
-    if (younger >= 2)
-        asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(2 * PER) : "memory");
+    if (younger >= 3)
+        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(3 * PER) : "memory");
+    else if (younger == 2)
+        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(2 * PER) : "memory");
     else if (younger == 1)
-        asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(PER) : "memory");
+        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(PER) : "memory");
     else
-        asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
 // This wave's share of tile `kt0` (32-aligned): KI = HD/64 instructions of
@@ -368,21 +380,21 @@ __device__ __forceinline__ DmaOffsets<HD> dma_offsets(int wave, int lane, uint32
 }
 
 template <int HD>
-__device__ __forceinline__ void dma_tile_fast(PrefillDmaSmem<HD>& sm, int st, int wave, const DmaOffsets<HD>& o,
+__device__ __forceinline__ void dma_tile_fast(PrefillDmaSmem<HD>& sm, int ks, int vs, int wave, const DmaOffsets<HD>& o,
                                               const char* kbase, const char* vtb) {
     const char* kb = uniform_ptr(kbase);
     const char* vb = uniform_ptr(vtb);
 #pragma unroll
     for (int i = 0; i < HD / 64; i++)
         lds_dma16_s(o.k[i], kb,
-                    __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sm.k[st][((HD / 64u) * wave + i) * 1024u]));
+                    __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sm.k[ks][((HD / 64u) * wave + i) * 1024u]));
 #pragma unroll
     for (int i = 0; i < 4; i++)
-        lds_dma16_s(o.v[i], vb, __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sm.vt[st][(4u * wave + i) * 1024u]));
+        lds_dma16_s(o.v[i], vb, __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sm.vt[vs][(4u * wave + i) * 1024u]));
 }
 
 template <int HD>
-__device__ __forceinline__ void dma_tile(PrefillDmaSmem<HD>& sm, int st, int wave, int lane, const char* Kb,
+__device__ __forceinline__ void dma_tile(PrefillDmaSmem<HD>& sm, int ks, int vs, int wave, int lane, const char* Kb,
                                          uint32_t row_bytes, unsigned kt0, unsigned last, const char* vtb) {
 #pragma unroll
     for (int i = 0; i < HD / 64; i++) {
@@ -390,7 +402,7 @@ __device__ __forceinline__ void dma_tile(PrefillDmaSmem<HD>& sm, int st, int wav
         dma_k_lane<HD>(wave, lane, i, &r, &c);
         const unsigned row = min(kt0 + r, last);
         lds_dma16(Kb + ((uint64_t)row * row_bytes + c * 16u),
-                  __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sm.k[st][((HD / 64u) * wave + i) * 1024u]));
+                  __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sm.k[ks][((HD / 64u) * wave + i) * 1024u]));
     }
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -398,13 +410,14 @@ __device__ __forceinline__ void dma_tile(PrefillDmaSmem<HD>& sm, int st, int wav
         const unsigned d = 16u * inst + (unsigned)(lane >> 2);
         const unsigned c = ((unsigned)lane & 3u) ^ swz_v(d);
         lds_dma16(vtb + (d * 64u + c * 16u),
-                  __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sm.vt[st][inst * 1024u]));
+                  __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sm.vt[vs][inst * 1024u]));
     }
 }
 
 template <int HD>
 __global__ __launch_bounds__(kPfThreads, 1) void k_prefill_dma(PrefillArgs a) {
-    constexpr int NS = kPfStages<HD>, NQ = HD / 16, PER = HD / 64 + 4;  // stages, score steps, DMAs per tile
+    constexpr int D = kPfDist<HD>, NK = kPfKStages<HD>, NV = kPfVStages<HD>;
+    constexpr int NQ = HD / 16, PER = HD / 64 + 4;  // score steps, DMAs per tile
     __shared__ PrefillDmaSmem<HD> sm;
     const unsigned dh = blockIdx.z;  // output half of the head dimension (head_dim 512)
     const PrefillWorkDev wk = a.work[blockIdx.x];
@@ -447,16 +460,17 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_prefill_dma(PrefillArgs a) {
     const float qs = ent.qscale;
 
     const DmaOffsets<HD> dof = dma_offsets<HD>(wave, lane, row_bytes);
-    auto issue = [&](int stage, unsigned t0) {
+    auto issue = [&](int t) __attribute__((always_inline)) {  // tile t of the range into K stage t % NK and V^T stage t % NV
+        const unsigned t0 = kb + (unsigned)t * kPfKeys;
         const char* vtb = VTb + (uint64_t)(t0 >> 5) * kPfKTileBytes<HD>;
         if (t0 + (kPfKeys - 1) <= last)
-            dma_tile_fast<HD>(sm, stage, wave, dof, Kb + (uint64_t)t0 * row_bytes, vtb);
+            dma_tile_fast<HD>(sm, t % NK, t % NV, wave, dof, Kb + (uint64_t)t0 * row_bytes, vtb);
         else
-            dma_tile<HD>(sm, stage, wave, lane, Kb, row_bytes, t0, last, vtb);
+            dma_tile<HD>(sm, t % NK, t % NV, wave, lane, Kb, row_bytes, t0, last, vtb);
     };
 #pragma unroll
-    for (int p = 0; p < NS - 1; p++)
-        if (p < n_tiles) issue(p, kb + (unsigned)p * kPfKeys);
+    for (int p = 0; p <= D; p++)
+        if (p < n_tiles) issue(p);
 
     float m_run = -INFINITY, l_run = 0.0f;
     f32x16 acc[8];
@@ -465,9 +479,9 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_prefill_dma(PrefillArgs a) {
     // LDS operand addresses inside a stage: K chunk c = 2s + half of row krow; V^T chunk 2s + half of row 32b + col.
     const unsigned krow = key_of_row((unsigned)col);
     const unsigned kx = swz_k(krow), vx = swz_v((unsigned)col);
-    unsigned koff[4];
+    unsigned koff[8];  // chunk 2s + half of the key row lies at koff[s % 8] + 256 (s / 8)
 #pragma unroll
-    for (int b = 0; b < 4; b++) koff[b] = krow * (2u * HD) + ((((unsigned)(2 * b + half)) ^ kx) << 4);
+    for (int b = 0; b < 8; b++) koff[b] = krow * (2u * HD) + ((((unsigned)(2 * b + half)) ^ kx) << 4);
     unsigned voff[2];
 #pragma unroll
     for (int s = 0; s < 2; s++) voff[s] = (unsigned)col * 64u + ((((unsigned)(2 * s + half)) ^ vx) << 4);
@@ -477,19 +491,19 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_prefill_dma(PrefillArgs a) {
     // works), then tile it's output MFMAs. Masking is branch-free for that reason: key in [lo, hi]
     // is (key - lo) < span (unsigned), with span 0 for rows past the chunk.
     const unsigned span = dead ? 0u : hi - lo + 1u;
-    auto scores = [&](int stage) {
+    auto scores = [&](int stage) __attribute__((always_inline)) {
         const unsigned char* kbuf = sm.k[stage];
         f32x16 sc = f32x16{};
 #pragma unroll
         for (int s = 0; s < NQ; s++) {
-            const f16x8 k0 = *reinterpret_cast<const f16x8*>(kbuf + koff[s & 3] + 128u * (s >> 2));
+            const f16x8 k0 = *reinterpret_cast<const f16x8*>(kbuf + koff[s & 7] + 256u * (s >> 3));
             sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(k0, qop[s], sc, 0, 0, 0);
         }
         return sc;
     };
     // Probabilities of one tile's raw scores (register r: key kt0 + 16 (r / 8) + 8 half + r % 8),
     // with the lazy update of the row's reference max; returns whether any row moved it.
-    auto softmax = [&](f32x16 sc, unsigned kt0, f16x8 (&pop)[2], float& alpha) {
+    auto softmax = [&](f32x16 sc, unsigned kt0, f16x8 (&pop)[2], float& alpha) __attribute__((always_inline)) {
         const unsigned rel = kt0 + 8u * (unsigned)half - lo;
 #pragma unroll
         for (int r = 0; r < 16; r++)
@@ -498,7 +512,10 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_prefill_dma(PrefillArgs a) {
 #pragma unroll
         for (int r = 1; r < 16; r++) smax = fmaxf(smax, sc[r]);
         float tmax = smax * qs;  // the scale is positive
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+        {
+            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(tmax), __float_as_uint(tmax), false, false);
+            tmax = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));  // max over both halves of the row
+        }
         const bool move = tmax > m_run + kPfLazy;
         const float m_new = move ? tmax : m_run;
         alpha = move ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;  // 0 from -inf (acc, l are 0)
@@ -513,7 +530,7 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_prefill_dma(PrefillArgs a) {
         }
         return __any(move);
     };
-    auto output = [&](int stage, const f16x8 (&pop)[2]) {
+    auto output = [&](int stage, const f16x8 (&pop)[2]) __attribute__((always_inline)) {
         const unsigned char* vbuf = sm.vt[stage];
 #pragma unroll
         for (int b = 0; b < 8; b++) {
@@ -525,32 +542,139 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_prefill_dma(PrefillArgs a) {
         }
     };
 
-    dma_wait_barrier<PER>(min(n_tiles - 1, NS - 2));  // tile 0 is in LDS
-    f32x16 cur = scores(0);
-    int it = 0;
-    for (; it + 1 < n_tiles; it++) {
-        const unsigned kt0 = kb + (unsigned)it * kPfKeys;
-        dma_wait_barrier<PER>(min(n_tiles - 2 - it, NS - 3));  // tile it + 1 is in LDS
-        if (it + NS - 1 < n_tiles)  // into the stage every wave finished with (tile it - 1)
-            issue((it + NS - 1) % NS, kt0 + (NS - 1) * kPfKeys);
-        const f32x16 nxt = scores((it + 1) % NS);
-        f16x8 pop[2];
-        float alpha;
-        if (softmax(cur, kt0, pop, alpha)) {
+    // One steady iteration in issue order: NQ steps, each one score MFMA of the next tile, every
+    // NQ/16 steps one output MFMA of the previous tile, the LDS operand reads R steps ahead, and one
+    // chunk of this tile's softmax (masking and row max; reference max and alpha; two exponentials,
+    // their f16 pair and its share of the row sum). sched_barrier(0) between the steps keeps that
+    // order, so that the VALU and LDS work of the one wave a SIMD holds runs under its MFMAs.
+    // `mask` is false for tiles whose keys lie inside the window of every row of the wave. The row
+    // sum adds the f16-rounded probabilities the output MFMAs use (packed dot products).
+    auto steady = [&](bool mask, int ks, int vs, unsigned kt0, f32x16& sc, const f16x8 (&pin)[2], f16x8 (&pout)[2],
+                      f32x16& nxt, float& alpha) __attribute__((always_inline)) {
+        constexpr int R = 3, OSTEP = NQ / 16;
+        const unsigned char* kbuf = sm.k[ks];
+        const unsigned char* vbuf = sm.vt[vs];
+        f16x8 kr[NQ], vr[16];
+        auto kread = [&](int s) __attribute__((always_inline)) { kr[s] = *reinterpret_cast<const f16x8*>(kbuf + koff[s & 7] + 256u * (s >> 3)); };
+        auto vread = [&](int o) __attribute__((always_inline)) { vr[o] = *reinterpret_cast<const f16x8*>(vbuf + voff[o & 1] + 2048u * (o >> 1)); };
 #pragma unroll
-            for (int b = 0; b < 8; b++) acc[b] *= alpha;
+        for (int i = 0; i < R; i++) {
+            vread(i);
+            kread(i);
         }
-        output(it % NS, pop);
-        cur = nxt;
-    }
+        const unsigned rel = kt0 + 8u * (unsigned)half - lo;
+        float mx[4], nmu = 0.0f;
+        bool moved = false;
+#pragma unroll
+        for (int j = 0; j < NQ; j++) {
+            if (j % OSTEP == 0) {
+                const int o = j / OSTEP;
+                acc[o >> 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vr[o], pin[o & 1], acc[o >> 1], 0, 0, 0);
+                if (o + R < 16) vread(o + R);
+            }
+            nxt = __builtin_amdgcn_mfma_f32_32x32x16_f16(kr[j], qop[j], j ? nxt : f32x16{}, 0, 0, 0);
+            if (j + R < NQ) kread(j + R);
+            if (j % OSTEP == 0) {
+                const int c = j / OSTEP;
+                if (c < 4) {
+                    if (mask) {
+#pragma unroll
+                        for (int e = 0; e < 4; e++) {
+                            const int r = 4 * c + e;
+                            sc[r] = rel + (unsigned)(16 * (r >> 3) + (r & 7)) < span ? sc[r] : -INFINITY;
+                        }
+                    }
+                    mx[c] = fmaxf(fmaxf(sc[4 * c], sc[4 * c + 1]), fmaxf(sc[4 * c + 2], sc[4 * c + 3]));
+                } else if (c == 4) {
+                    float tmax = fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3])) * qs;  // the scale is positive
+                    const auto sw =
+                        __builtin_amdgcn_permlane32_swap(__float_as_uint(tmax), __float_as_uint(tmax), false, false);
+                    tmax = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));  // max over both halves of the row
+                    const bool move = tmax > m_run + kPfLazy;
+                    const float m_new = move ? tmax : m_run;
+                    alpha = move ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;  // 0 from -inf (acc, l are 0)
+                    l_run *= alpha;
+                    m_run = m_new;
+                    nmu = m_run == -INFINITY ? 0.0f : -m_run;
+                    moved = __any(move);
+                } else if (c < 13) {
+                    const int r = 2 * (c - 5);
+                    const f16x2 h = f16x2{(f16)__builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], qs, nmu)),
+                                          (f16)__builtin_amdgcn_exp2f(__builtin_fmaf(sc[r + 1], qs, nmu))};
+                    pout[r >> 3][r & 7] = h[0];
+                    pout[r >> 3][(r & 7) + 1] = h[1];
+                    l_run = __builtin_amdgcn_fdot2(h, f16x2{(f16)1.0f, (f16)1.0f}, l_run, false);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        asm volatile("" : "+v"(pout[0]), "+v"(pout[1]), "+v"(l_run));  // formed before the rescale branch
+        return moved;
+    };
+
+    // Iteration it issues tile it + 1 + D, computes the scores of tile it + 1, the output of
+    // tile it - 1 and the probabilities of tile it: one basic block of independent MFMA and VALU
+    // work, then the rare rescale of the accumulators (after tile it - 1's output).
+    auto rescale = [&](float alpha) __attribute__((always_inline)) {
+#pragma unroll
+        for (int b = 0; b < 8; b++) acc[b] *= alpha;
+    };
+    // Tiles [t_in0, t_in1) of the range lie inside every row's window of this wave (no masking).
+    int t_in0, t_in1;
     {
-        f16x8 pop[2];
-        float alpha;
-        if (softmax(cur, kb + (unsigned)it * kPfKeys, pop, alpha)) {
+        int a0 = dead ? 0x7fffffff : (lo > kb ? (int)((lo - kb + kPfKeys - 1) / kPfKeys) : 0);
+        int a1 = dead || hi + 1 < kb ? 0 : (int)((hi + 1 - kb) / kPfKeys);
 #pragma unroll
-            for (int b = 0; b < 8; b++) acc[b] *= alpha;
+        for (int m = 32; m >= 1; m >>= 1) {
+            a0 = max(a0, __shfl_xor(a0, m));
+            a1 = min(a1, __shfl_xor(a1, m));
         }
-        output(it % NS, pop);
+        t_in0 = __builtin_amdgcn_readfirstlane(a0);
+        t_in1 = __builtin_amdgcn_readfirstlane(a1);
+    }
+    auto step = [&](bool mask, int it, f32x16& sc, const f16x8 (&pin)[2], f16x8 (&pout)[2], f32x16& nxt) __attribute__((always_inline)) {
+        dma_wait_barrier<PER>(min(n_tiles - 2 - it, D - 1));  // tile it + 1 is in LDS
+        if (it + 1 + D < n_tiles) issue(it + 1 + D);           // K stage of tile it, V^T stage of tile it - 2
+        float alpha;
+        if (steady(mask, (it + 1) % NK, (it - 1) % NV, kb + (unsigned)it * kPfKeys, sc, pin, pout, nxt, alpha))
+            rescale(alpha);
+    };
+    f16x8 pa[2], pb[2];
+    f32x16 sa, sb;
+    // Steady iteration it with masking, tile it's scores in sb and tile it - 1's probabilities in pa
+    // before and after.
+    auto step_masked = [&](int it) __attribute__((always_inline)) {
+        step(true, it, sb, pa, pb, sa);
+        sb = sa;
+        pa[0] = pb[0];
+        pa[1] = pb[1];
+    };
+    float alpha;
+    dma_wait_barrier<PER>(min(n_tiles - 1, D));  // tile 0 is in LDS
+    sa = scores(0);
+    if (n_tiles == 1) {
+        softmax(sa, kb, pa, alpha);  // the accumulators are still zero: no rescale
+        output(0, pa);
+    } else {
+        dma_wait_barrier<PER>(min(n_tiles - 2, D - 1));  // tile 1 is in LDS; every wave is past scores(0)
+        if (D + 1 < n_tiles) issue(D + 1);
+        sb = scores(1 % NK);
+        softmax(sa, kb, pa, alpha);
+        // Masked iterations before the tiles that lie inside every row's window, those tiles
+        // unmasked, two per pass (the score and probability registers alternate in place), then the
+        // masked rest (head_dim 512: every iteration masked, one form for the register budget).
+        int it = 1;
+        if constexpr (HD == 256) {
+            for (; it + 1 < n_tiles && it < t_in0; it++) step_masked(it);
+            for (; it + 2 < n_tiles && it + 1 < t_in1; it += 2) {
+                step(false, it, sb, pa, pb, sa);      // scores of tile it + 1 into sa, probabilities of tile it into pb
+                step(false, it + 1, sa, pb, pa, sb);  // scores of tile it + 2 into sb, probabilities of tile it + 1 into pa
+            }
+        }
+        for (; it + 1 < n_tiles; it++) step_masked(it);
+        output((it - 1) % NV, pa);
+        if (softmax(sb, kb + (unsigned)it * kPfKeys, pb, alpha)) rescale(alpha);
+        output(it % NV, pb);
     }
 
     const float L = l_run + __shfl_xor(l_run, 32);
