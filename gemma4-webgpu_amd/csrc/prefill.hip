@@ -344,16 +344,10 @@ __device__ __forceinline__ void dma_wait_barrier(int younger) {
         asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// This wave's share of tile `kt0` (32-aligned): KI = HD/64 instructions of
-// K (1 KiB each: 2 rows at head_dim 256, 1 at 512) and 4 of V^T (16 rows of
-// 64 B each). `k` and `v` are the lane's byte offsets inside a K tile and a
-// V^T half block; a tile whose rows all exist uses them with a uniform base,
-// the last tile of a range clamps its rows per lane.
-template <int HD>
-struct DmaOffsets {
-    uint32_t k[HD / 64], v[4];
-};
-
+// This wave's share of a tile: HD/64 DMA instructions of K (1 KiB each: 2
+// rows at head_dim 256, 1 at 512; rows past the range's last clamp to it) and
+// 4 of V^T (16 rows of 64 B each). dma_k_lane gives the lane's K row and
+// source chunk, dma_v_offsets its byte offsets inside a V^T half block.
 template <int HD>
 __device__ __forceinline__ void dma_k_lane(int wave, int lane, int i, unsigned* r, unsigned* c) {
     constexpr unsigned CPR = HD / 8, RPI = 64 / CPR;  // 16-byte chunks per K row, rows per instruction
@@ -362,56 +356,18 @@ __device__ __forceinline__ void dma_k_lane(int wave, int lane, int i, unsigned* 
     *c = ((unsigned)lane % CPR) ^ swz_k(*r);
 }
 
-template <int HD>
-__device__ __forceinline__ DmaOffsets<HD> dma_offsets(int wave, int lane, uint32_t row_bytes) {
-    DmaOffsets<HD> o;
-#pragma unroll
-    for (int i = 0; i < HD / 64; i++) {
-        unsigned r, c;
-        dma_k_lane<HD>(wave, lane, i, &r, &c);
-        o.k[i] = r * row_bytes + (c << 4);
-    }
+struct DmaVOffsets {
+    uint32_t v[4];
+};
+
+__device__ __forceinline__ DmaVOffsets dma_v_offsets(int wave, int lane) {
+    DmaVOffsets o;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const unsigned d = 16u * (4u * wave + i) + (unsigned)(lane >> 2);
         o.v[i] = d * 64u + ((((unsigned)lane & 3u) ^ swz_v(d)) << 4);
     }
     return o;
-}
-
-template <int HD>
-__device__ __forceinline__ void dma_tile_fast(PrefillDmaSmem<HD>& sm, int ks, int vs, int wave, const DmaOffsets<HD>& o,
-                                              const char* kbase, const char* vtb) {
-    const char* kb = uniform_ptr(kbase);
-    const char* vb = uniform_ptr(vtb);
-#pragma unroll
-    for (int i = 0; i < HD / 64; i++)
-        lds_dma16_s(o.k[i], kb,
-                    __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sm.k[ks][((HD / 64u) * wave + i) * 1024u]));
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-        lds_dma16_s(o.v[i], vb, __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sm.vt[vs][(4u * wave + i) * 1024u]));
-}
-
-template <int HD>
-__device__ __forceinline__ void dma_tile(PrefillDmaSmem<HD>& sm, int ks, int vs, int wave, int lane, const char* Kb,
-                                         uint32_t row_bytes, unsigned kt0, unsigned last, const char* vtb) {
-#pragma unroll
-    for (int i = 0; i < HD / 64; i++) {
-        unsigned r, c;
-        dma_k_lane<HD>(wave, lane, i, &r, &c);
-        const unsigned row = min(kt0 + r, last);
-        lds_dma16(Kb + ((uint64_t)row * row_bytes + c * 16u),
-                  __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sm.k[ks][((HD / 64u) * wave + i) * 1024u]));
-    }
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const unsigned inst = 4u * wave + i;
-        const unsigned d = 16u * inst + (unsigned)(lane >> 2);
-        const unsigned c = ((unsigned)lane & 3u) ^ swz_v(d);
-        lds_dma16(vtb + (d * 64u + c * 16u),
-                  __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sm.vt[vs][inst * 1024u]));
-    }
 }
 
 template <int HD>
@@ -438,19 +394,6 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_prefill_dma(PrefillArgs a) {
     const unsigned hi = row_live ? pos : 0u;
     const bool dead = !row_live;
 
-    f16x8 qop[NQ];
-    {
-        const uint16_t* qr = ent.q + ((uint64_t)tok_c * NQH + kvh * G + head) * HD + 8 * half;
-#pragma unroll
-        for (int s = 0; s < NQ; s++) qop[s] = ldg<f16x8>(qr + 16 * s);
-        // Wait for q here, before any DMA is issued (the compiler's own wait for these loads would
-        // otherwise also wait for every DMA in flight at the first MFMA), and keep it in AGPRs: the
-        // score MFMA reads its B operand from there, and the VGPRs hold the output accumulators
-        // (this file is compiled with MFMA accumulators in VGPRs, so that their rescale is plain VALU).
-#pragma unroll
-        for (int s = 0; s < NQ; s++) asm volatile("" : "+a"(qop[s]));
-    }
-
     const uint32_t row_bytes = NKH * HD * 2u;
     const char* Kb = reinterpret_cast<const char*>(ent.k + (uint64_t)kvh * HD);
     const char* VTb = reinterpret_cast<const char*>(ent.vt + (uint64_t)kvh * ent.vt_blocks * (HD * 32)) +
@@ -459,18 +402,42 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_prefill_dma(PrefillArgs a) {
     const int n_tiles = (int)((ke - kb + kPfKeys - 1) / kPfKeys);
     const float qs = ent.qscale;
 
-    const DmaOffsets<HD> dof = dma_offsets<HD>(wave, lane, row_bytes);
-    auto issue = [&](int t) __attribute__((always_inline)) {  // tile t of the range into K stage t % NK and V^T stage t % NV
-        const unsigned t0 = kb + (unsigned)t * kPfKeys;
-        const char* vtb = VTb + (uint64_t)(t0 >> 5) * kPfKTileBytes<HD>;
-        if (t0 + (kPfKeys - 1) <= last)
-            dma_tile_fast<HD>(sm, t % NK, t % NV, wave, dof, Kb + (uint64_t)t0 * row_bytes, vtb);
-        else
-            dma_tile<HD>(sm, t % NK, t % NV, wave, lane, Kb, row_bytes, t0, last, vtb);
+    const DmaVOffsets dof = dma_v_offsets(wave, lane);
+    // DMA instruction k (0 .. PER - 1: the K rows, then the V^T rows) of tile t, into K stage
+    // t % NK and V^T stage t % NV. A tile past the range reloads the range's last tile into those
+    // stages, which nobody reads, so that every iteration issues the same count (uniform waits).
+    auto dma_part = [&](int k, int t) __attribute__((always_inline)) {
+        const unsigned t0 = kb + (unsigned)min(t, n_tiles - 1) * kPfKeys;
+        if (k < HD / 64) {
+            unsigned r, c;
+            dma_k_lane<HD>(wave, lane, k, &r, &c);
+            lds_dma16_s(min(r, last - t0) * row_bytes + c * 16u, uniform_ptr(Kb + (uint64_t)t0 * row_bytes),
+                        __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sm.k[t % NK][((HD / 64u) * wave + k) * 1024u]));
+        } else {
+            const int i = k - HD / 64;
+            lds_dma16_s(dof.v[i], uniform_ptr(VTb + (uint64_t)(t0 >> 5) * kPfKTileBytes<HD>),
+                        __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sm.vt[t % NV][(4u * wave + i) * 1024u]));
+        }
+    };
+    auto issue = [&](int t) __attribute__((always_inline)) {
+#pragma unroll
+        for (int k = 0; k < PER; k++) dma_part(k, t);
     };
 #pragma unroll
-    for (int p = 0; p <= D; p++)
-        if (p < n_tiles) issue(p);
+    for (int p = 0; p <= D; p++) issue(p);
+
+    // q after the first tiles' DMAs, so that the two latencies overlap (the wait for q, in issue
+    // order, also covers those tiles). q stays in AGPRs: the score MFMA reads its B operand from
+    // there, and the VGPRs hold the output accumulators (this file is compiled with MFMA
+    // accumulators in VGPRs, so that their rescale is plain VALU).
+    f16x8 qop[NQ];
+    {
+        const uint16_t* qr = ent.q + ((uint64_t)tok_c * NQH + kvh * G + head) * HD + 8 * half;
+#pragma unroll
+        for (int s = 0; s < NQ; s++) qop[s] = ldg<f16x8>(qr + 16 * s);
+#pragma unroll
+        for (int s = 0; s < NQ; s++) asm volatile("" : "+a"(qop[s]));
+    }
 
     float m_run = -INFINITY, l_run = 0.0f;
     f32x16 acc[8];
@@ -543,14 +510,14 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_prefill_dma(PrefillArgs a) {
     };
 
     // One steady iteration in issue order: NQ steps, each one score MFMA of the next tile, every
-    // NQ/16 steps one output MFMA of the previous tile, the LDS operand reads R steps ahead, and one
-    // chunk of this tile's softmax (masking and row max; reference max and alpha; two exponentials,
+    // NQ/16 steps one output MFMA of the previous tile, the LDS operand reads R steps ahead, every
+    // two steps one DMA instruction of tile it + 1 + D, and one chunk of this tile's softmax (masking and row max; reference max and alpha; two exponentials,
     // their f16 pair and its share of the row sum). sched_barrier(0) between the steps keeps that
     // order, so that the VALU and LDS work of the one wave a SIMD holds runs under its MFMAs.
     // `mask` is false for tiles whose keys lie inside the window of every row of the wave. The row
     // sum adds the f16-rounded probabilities the output MFMAs use (packed dot products).
-    auto steady = [&](bool mask, int ks, int vs, unsigned kt0, f32x16& sc, const f16x8 (&pin)[2], f16x8 (&pout)[2],
-                      f32x16& nxt, float& alpha) __attribute__((always_inline)) {
+    auto steady = [&](bool mask, int ks, int vs, int tdma, unsigned kt0, f32x16& sc, const f16x8 (&pin)[2],
+                      f16x8 (&pout)[2], f32x16& nxt, float& alpha) __attribute__((always_inline)) {
         constexpr int R = 3, OSTEP = NQ / 16;
         const unsigned char* kbuf = sm.k[ks];
         const unsigned char* vbuf = sm.vt[vs];
@@ -574,6 +541,7 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_prefill_dma(PrefillArgs a) {
             }
             nxt = __builtin_amdgcn_mfma_f32_32x32x16_f16(kr[j], qop[j], j ? nxt : f32x16{}, 0, 0, 0);
             if (j + R < NQ) kread(j + R);
+            if (j % 2 == 0 && j / 2 < PER) dma_part(j / 2, tdma);  // tile it + 1 + D, one instruction per two steps
             if (j % OSTEP == 0) {
                 const int c = j / OSTEP;
                 if (c < 4) {
@@ -633,10 +601,10 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_prefill_dma(PrefillArgs a) {
         t_in1 = __builtin_amdgcn_readfirstlane(a1);
     }
     auto step = [&](bool mask, int it, f32x16& sc, const f16x8 (&pin)[2], f16x8 (&pout)[2], f32x16& nxt) __attribute__((always_inline)) {
-        dma_wait_barrier<PER>(min(n_tiles - 2 - it, D - 1));  // tile it + 1 is in LDS
-        if (it + 1 + D < n_tiles) issue(it + 1 + D);           // K stage of tile it, V^T stage of tile it - 2
+        dma_wait_barrier<PER>(D - 1);  // tile it + 1 is in LDS; tile it + 1 + D goes to the stages of K(it), V^T(it - 2)
         float alpha;
-        if (steady(mask, (it + 1) % NK, (it - 1) % NV, kb + (unsigned)it * kPfKeys, sc, pin, pout, nxt, alpha))
+        if (steady(mask, (it + 1) % NK, (it - 1) % NV, it + 1 + D, kb + (unsigned)it * kPfKeys, sc, pin, pout, nxt,
+                   alpha))
             rescale(alpha);
     };
     f16x8 pa[2], pb[2];
@@ -650,14 +618,14 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_prefill_dma(PrefillArgs a) {
         pa[1] = pb[1];
     };
     float alpha;
-    dma_wait_barrier<PER>(min(n_tiles - 1, D));  // tile 0 is in LDS
+    dma_wait_barrier<PER>(D);  // tile 0 is in LDS
     sa = scores(0);
     if (n_tiles == 1) {
         softmax(sa, kb, pa, alpha);  // the accumulators are still zero: no rescale
         output(0, pa);
     } else {
-        dma_wait_barrier<PER>(min(n_tiles - 2, D - 1));  // tile 1 is in LDS; every wave is past scores(0)
-        if (D + 1 < n_tiles) issue(D + 1);
+        dma_wait_barrier<PER>(D - 1);  // tile 1 is in LDS; every wave is past scores(0)
+        issue(D + 1);
         sb = scores(1 % NK);
         softmax(sa, kb, pa, alpha);
         // Masked iterations before the tiles that lie inside every row's window, those tiles
@@ -676,6 +644,7 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_prefill_dma(PrefillArgs a) {
         if (softmax(sb, kb + (unsigned)it * kPfKeys, pb, alpha)) rescale(alpha);
         output(it % NV, pb);
     }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no LDS write of this workgroup outlives it
 
     const float L = l_run + __shfl_xor(l_run, 32);
     if (dead) return;
