@@ -51,8 +51,10 @@ def _run(cmd: list[str]) -> None:
 
 
 # Per-file code generation options. prefill.hip: MFMA accumulators in VGPRs (the
-# pipelined prefill rescales them with plain VALU; its q operand is kept in AGPRs).
-FILE_FLAGS = {"prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+# pipelined prefill rescales them with plain VALU; its q operand is kept in AGPRs),
+# and IEEE mode off with NaN-free math, so that max over scores is one v_max each
+# instead of canonicalize + max (scores are finite or -inf; no NaN is produced).
+FILE_FLAGS = {"prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mno-amdgpu-ieee", "-fno-honor-nans"]}
 
 
 def _compile(src: Path) -> Path:

@@ -49,7 +49,7 @@ constexpr int kPfWaves = 4;
 constexpr int kPfThreads = 64 * kPfWaves;
 constexpr int kPfRows = 32 * kPfWaves;   // q-rows per tile
 constexpr int kPfKeys = 32;              // keys per tile
-constexpr float kPfLazy = 8.0f;          // lazy-rescale threshold (log2 units): probabilities <= 256
+constexpr float kPfLazy = 15.0f;         // lazy-rescale threshold (log2 units): probabilities <= 2^15 (f16 max 65504)
 constexpr int kKRowBytes = kPfHD * 2 + 16;       // padded K row in LDS
 constexpr int kVtRowBytes = kPfKeys * 2 + 16;    // padded V^T row (one d) in LDS
 
@@ -406,22 +406,43 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_prefill_dma(PrefillArgs a) {
     // DMA instruction k (0 .. PER - 1: the K rows, then the V^T rows) of tile t, into K stage
     // t % NK and V^T stage t % NV. A tile past the range reloads the range's last tile into those
     // stages, which nobody reads, so that every iteration issues the same count (uniform waits).
-    auto dma_part = [&](int k, int t) __attribute__((always_inline)) {
-        const unsigned t0 = kb + (unsigned)min(t, n_tiles - 1) * kPfKeys;
-        if (k < HD / 64) {
-            unsigned r, c;
-            dma_k_lane<HD>(wave, lane, k, &r, &c);
-            lds_dma16_s(min(r, last - t0) * row_bytes + c * 16u, uniform_ptr(Kb + (uint64_t)t0 * row_bytes),
-                        __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sm.k[t % NK][((HD / 64u) * wave + k) * 1024u]));
-        } else {
-            const int i = k - HD / 64;
-            lds_dma16_s(dof.v[i], uniform_ptr(VTb + (uint64_t)(t0 >> 5) * kPfKTileBytes<HD>),
-                        __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sm.vt[t % NV][(4u * wave + i) * 1024u]));
-        }
+    // dma_tile gives the tile's wave-uniform operands, dma_part issues one instruction.
+    struct DmaTile {
+        const char* k;     // the tile's first K row
+        const char* v;     // its V^T block (this output half)
+        uint32_t kclamp;   // byte offset of the range's last row from the tile's first
+        uint32_t lds_k, lds_v;  // this wave's first destination in the stages
+    };
+    uint32_t krow_off[HD / 64], kchunk_off[HD / 64];
+#pragma unroll
+    for (int k = 0; k < HD / 64; k++) {
+        unsigned r, c;
+        dma_k_lane<HD>(wave, lane, k, &r, &c);
+        krow_off[k] = r * row_bytes;
+        kchunk_off[k] = c * 16u;
+    }
+    auto dma_tile = [&](int t) __attribute__((always_inline)) {
+        t = __builtin_amdgcn_readfirstlane(t);
+        const int tc = min(t, n_tiles - 1);
+        const unsigned t0 = kb + (unsigned)tc * kPfKeys;
+        DmaTile d;
+        d.k = uniform_ptr(Kb + (uint64_t)t0 * row_bytes);
+        d.v = uniform_ptr(VTb + (uint64_t)(t0 >> 5) * kPfKTileBytes<HD>);
+        d.kclamp = __builtin_amdgcn_readfirstlane((last - t0) * row_bytes);
+        d.lds_k = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sm.k[t % NK][(HD / 64u) * wave * 1024u]);
+        d.lds_v = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sm.vt[t % NV][4u * wave * 1024u]);
+        return d;
+    };
+    auto dma_part = [&](int k, const DmaTile& d) __attribute__((always_inline)) {
+        if (k < HD / 64)
+            lds_dma16_s(min(krow_off[k], d.kclamp) + kchunk_off[k], d.k, d.lds_k + 1024u * k);
+        else
+            lds_dma16_s(dof.v[k - HD / 64], d.v, d.lds_v + 1024u * (k - HD / 64));
     };
     auto issue = [&](int t) __attribute__((always_inline)) {
+        const DmaTile d = dma_tile(t);
 #pragma unroll
-        for (int k = 0; k < PER; k++) dma_part(k, t);
+        for (int k = 0; k < PER; k++) dma_part(k, d);
     };
 #pragma unroll
     for (int p = 0; p <= D; p++) issue(p);
@@ -509,71 +530,83 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_prefill_dma(PrefillArgs a) {
         }
     };
 
-    // One steady iteration in issue order: NQ steps, each one score MFMA of the next tile, every
-    // NQ/16 steps one output MFMA of the previous tile, the LDS operand reads R steps ahead, every
-    // two steps one DMA instruction of tile it + 1 + D, and one chunk of this tile's softmax (masking and row max; reference max and alpha; two exponentials,
-    // their f16 pair and its share of the row sum). sched_barrier(0) between the steps keeps that
-    // order, so that the VALU and LDS work of the one wave a SIMD holds runs under its MFMAs.
-    // `mask` is false for tiles whose keys lie inside the window of every row of the wave. The row
-    // sum adds the f16-rounded probabilities the output MFMAs use (packed dot products).
-    auto steady = [&](bool mask, int ks, int vs, int tdma, unsigned kt0, f32x16& sc, const f16x8 (&pin)[2],
+    // One steady iteration in issue order: NQ steps, each one score MFMA of the next tile and, every
+    // NQ/16 steps, one output MFMA of the previous tile; the LDS operand reads R steps ahead, one DMA
+    // instruction of tile it + 1 + D every two steps, and after every MFMA one slot of this tile's
+    // softmax (slots 0-7: masking and running max of two scores; 8-9: the row's reference max and
+    // alpha; 10-25: one exponential each, every second one packing the f16 pair and adding it to
+    // the row sum with a dot product). A wave issues in order and an MFMA waits for the previous
+    // one, so VALU work placed after each MFMA runs in that MFMA's shadow; sched_barrier(0) keeps
+    // the order. `mask` is false for tiles whose keys lie inside the window of every row of the
+    // wave. The row sum adds the f16-rounded probabilities the output MFMAs use.
+    auto steady = [&](bool mask, int ks, int vs, const DmaTile& tdma, unsigned kt0, f32x16& sc, const f16x8 (&pin)[2],
                       f16x8 (&pout)[2], f32x16& nxt, float& alpha) __attribute__((always_inline)) {
         constexpr int R = 3, OSTEP = NQ / 16;
         const unsigned char* kbuf = sm.k[ks];
         const unsigned char* vbuf = sm.vt[vs];
         f16x8 kr[NQ], vr[16];
-        auto kread = [&](int s) __attribute__((always_inline)) { kr[s] = *reinterpret_cast<const f16x8*>(kbuf + koff[s & 7] + 256u * (s >> 3)); };
-        auto vread = [&](int o) __attribute__((always_inline)) { vr[o] = *reinterpret_cast<const f16x8*>(vbuf + voff[o & 1] + 2048u * (o >> 1)); };
+        auto kread = [&](int s) __attribute__((always_inline)) {
+            kr[s] = *reinterpret_cast<const f16x8*>(kbuf + koff[s & 7] + 256u * (s >> 3));
+        };
+        auto vread = [&](int o) __attribute__((always_inline)) {
+            vr[o] = *reinterpret_cast<const f16x8*>(vbuf + voff[o & 1] + 2048u * (o >> 1));
+        };
 #pragma unroll
         for (int i = 0; i < R; i++) {
             vread(i);
             kread(i);
         }
         const unsigned rel = kt0 + 8u * (unsigned)half - lo;
-        float mx[4], nmu = 0.0f;
+        float mx = -INFINITY, tmax = 0.0f, nmu = 0.0f;
+        float p[16];
         bool moved = false;
+        auto slot = [&](int q) __attribute__((always_inline)) {
+            if (q < 8) {
+                const int r = 2 * q;
+                if (mask) {
+                    sc[r] = rel + (unsigned)(16 * (r >> 3) + (r & 7)) < span ? sc[r] : -INFINITY;
+                    sc[r + 1] = rel + (unsigned)(16 * ((r + 1) >> 3) + ((r + 1) & 7)) < span ? sc[r + 1] : -INFINITY;
+                }
+                mx = fmaxf(mx, fmaxf(sc[r], sc[r + 1]));
+            } else if (q == 8) {
+                tmax = mx * qs;  // the scale is positive
+                const auto sw =
+                    __builtin_amdgcn_permlane32_swap(__float_as_uint(tmax), __float_as_uint(tmax), false, false);
+                tmax = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));  // max over both halves of the row
+            } else if (q == 9) {
+                const bool move = tmax > m_run + kPfLazy;
+                const float m_new = move ? tmax : m_run;
+                alpha = move ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;  // 0 from -inf (acc, l are 0)
+                l_run *= alpha;
+                m_run = m_new;
+                nmu = m_run == -INFINITY ? 0.0f : -m_run;
+                moved = __any(move);
+            } else if (q < 26) {
+                const int r = q - 10;
+                p[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], qs, nmu));
+                if (r & 1) {
+                    const f16x2 h = f16x2{(f16)p[r - 1], (f16)p[r]};
+                    pout[r >> 3][(r - 1) & 7] = h[0];
+                    pout[r >> 3][r & 7] = h[1];
+                    l_run = __builtin_amdgcn_fdot2(h, f16x2{(f16)1.0f, (f16)1.0f}, l_run, false);
+                }
+            }
+        };
+        nxt = f32x16{};
+        int q = 0;  // MFMAs issued so far
 #pragma unroll
         for (int j = 0; j < NQ; j++) {
             if (j % OSTEP == 0) {
                 const int o = j / OSTEP;
                 acc[o >> 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vr[o], pin[o & 1], acc[o >> 1], 0, 0, 0);
                 if (o + R < 16) vread(o + R);
+                slot(q++);
+                __builtin_amdgcn_sched_barrier(0);
             }
-            nxt = __builtin_amdgcn_mfma_f32_32x32x16_f16(kr[j], qop[j], j ? nxt : f32x16{}, 0, 0, 0);
+            nxt = __builtin_amdgcn_mfma_f32_32x32x16_f16(kr[j], qop[j], nxt, 0, 0, 0);
             if (j + R < NQ) kread(j + R);
-            if (j % 2 == 0 && j / 2 < PER) dma_part(j / 2, tdma);  // tile it + 1 + D, one instruction per two steps
-            if (j % OSTEP == 0) {
-                const int c = j / OSTEP;
-                if (c < 4) {
-                    if (mask) {
-#pragma unroll
-                        for (int e = 0; e < 4; e++) {
-                            const int r = 4 * c + e;
-                            sc[r] = rel + (unsigned)(16 * (r >> 3) + (r & 7)) < span ? sc[r] : -INFINITY;
-                        }
-                    }
-                    mx[c] = fmaxf(fmaxf(sc[4 * c], sc[4 * c + 1]), fmaxf(sc[4 * c + 2], sc[4 * c + 3]));
-                } else if (c == 4) {
-                    float tmax = fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3])) * qs;  // the scale is positive
-                    const auto sw =
-                        __builtin_amdgcn_permlane32_swap(__float_as_uint(tmax), __float_as_uint(tmax), false, false);
-                    tmax = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));  // max over both halves of the row
-                    const bool move = tmax > m_run + kPfLazy;
-                    const float m_new = move ? tmax : m_run;
-                    alpha = move ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;  // 0 from -inf (acc, l are 0)
-                    l_run *= alpha;
-                    m_run = m_new;
-                    nmu = m_run == -INFINITY ? 0.0f : -m_run;
-                    moved = __any(move);
-                } else if (c < 13) {
-                    const int r = 2 * (c - 5);
-                    const f16x2 h = f16x2{(f16)__builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], qs, nmu)),
-                                          (f16)__builtin_amdgcn_exp2f(__builtin_fmaf(sc[r + 1], qs, nmu))};
-                    pout[r >> 3][r & 7] = h[0];
-                    pout[r >> 3][(r & 7) + 1] = h[1];
-                    l_run = __builtin_amdgcn_fdot2(h, f16x2{(f16)1.0f, (f16)1.0f}, l_run, false);
-                }
-            }
+            if (j % 2 == 0 && j / 2 < PER) dma_part(j / 2, tdma);  // one instruction per two steps
+            slot(q++);
             __builtin_amdgcn_sched_barrier(0);
         }
         asm volatile("" : "+v"(pout[0]), "+v"(pout[1]), "+v"(l_run));  // formed before the rescale branch
@@ -601,10 +634,11 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_prefill_dma(PrefillArgs a) {
         t_in1 = __builtin_amdgcn_readfirstlane(a1);
     }
     auto step = [&](bool mask, int it, f32x16& sc, const f16x8 (&pin)[2], f16x8 (&pout)[2], f32x16& nxt) __attribute__((always_inline)) {
+        it = __builtin_amdgcn_readfirstlane(it);  // tile and stage arithmetic on the scalar unit
         dma_wait_barrier<PER>(D - 1);  // tile it + 1 is in LDS; tile it + 1 + D goes to the stages of K(it), V^T(it - 2)
         float alpha;
-        if (steady(mask, (it + 1) % NK, (it - 1) % NV, it + 1 + D, kb + (unsigned)it * kPfKeys, sc, pin, pout, nxt,
-                   alpha))
+        const DmaTile d = dma_tile(it + 1 + D);
+        if (steady(mask, (it + 1) % NK, (it - 1) % NV, d, kb + (unsigned)it * kPfKeys, sc, pin, pout, nxt, alpha))
             rescale(alpha);
     };
     f16x8 pa[2], pb[2];
