@@ -197,7 +197,9 @@ __global__ __launch_bounds__(kMergeThreads) void k_decode_merge(DecodeArgs a, un
 // in record order.
 constexpr unsigned kSmallMergeSplits = 8;
 
-template <int HD, int COLS>
+// NS: the launch's largest split count rounded up to 2, 4 or 8 (records past an entry's own count
+// are not loaded).
+template <int HD, int COLS, int NS>
 __global__ __launch_bounds__(kMergeThreads) void k_decode_merge_small(DecodeArgs a) {
     constexpr unsigned TPH = HD / COLS;  // threads per query head
     const DecodeEntryDev ent = a.table ? a.table[blockIdx.x] : a.one;
@@ -208,10 +210,10 @@ __global__ __launch_bounds__(kMergeThreads) void k_decode_merge_small(DecodeArgs
     if (h >= G) return;
     const uint64_t rec_stride = (uint64_t)a.num_kv_heads * G;  // partial records per split
     const uint64_t rec0 = ((uint64_t)ent.split_base * a.num_kv_heads + kvh) * G + h;
-    f32x4 v[kSmallMergeSplits][COLS / 4];
-    f32x2 w[kSmallMergeSplits];
+    f32x4 v[NS][COLS / 4];
+    f32x2 w[NS];
 #pragma unroll
-    for (unsigned s = 0; s < kSmallMergeSplits; s++) {
+    for (unsigned s = 0; s < (unsigned)NS; s++) {
         const uint64_t rec = rec0 + (uint64_t)min(s, ns - 1) * rec_stride;
         w[s] = ldg<f32x2>(a.part_ml + rec * 2);
 #pragma unroll
@@ -219,14 +221,14 @@ __global__ __launch_bounds__(kMergeThreads) void k_decode_merge_small(DecodeArgs
     }
     float M = w[0][0];
 #pragma unroll
-    for (unsigned s = 1; s < kSmallMergeSplits; s++)
+    for (unsigned s = 1; s < (unsigned)NS; s++)
         if (s < ns) M = fmaxf(M, w[s][0]);
     float L = 0.0f;
     f32x4 acc[COLS / 4];
 #pragma unroll
     for (int c = 0; c < COLS / 4; c++) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (unsigned s = 0; s < kSmallMergeSplits; s++) {
+    for (unsigned s = 0; s < (unsigned)NS; s++) {
         const float f = s < ns ? __builtin_amdgcn_exp2f(w[s][0] - M) : 0.0f;
         L += w[s][1] * f;
 #pragma unroll
@@ -241,10 +243,24 @@ template <int HD>
 int launch_decode_merge_hd(const DecodeArgs& a, unsigned n_entries, unsigned max_splits, hipStream_t st) {
     if (max_splits <= kSmallMergeSplits && (a.group == 8 || a.group == 4)) {
         const dim3 grid(n_entries, a.num_kv_heads);
-        if (a.group == 8)
-            hipLaunchKernelGGL((k_decode_merge_small<HD, HD * 8 / 256>), grid, dim3(kMergeThreads), 0, st, a);
-        else
-            hipLaunchKernelGGL((k_decode_merge_small<HD, HD * 4 / 256>), grid, dim3(kMergeThreads), 0, st, a);
+        const dim3 block(kMergeThreads);
+        if (a.group == 8) {
+            constexpr int C = HD * 8 / 256;
+            if (max_splits <= 2)
+                hipLaunchKernelGGL((k_decode_merge_small<HD, C, 2>), grid, block, 0, st, a);
+            else if (max_splits <= 4)
+                hipLaunchKernelGGL((k_decode_merge_small<HD, C, 4>), grid, block, 0, st, a);
+            else
+                hipLaunchKernelGGL((k_decode_merge_small<HD, C, 8>), grid, block, 0, st, a);
+        } else {
+            constexpr int C = HD * 4 / 256;
+            if (max_splits <= 2)
+                hipLaunchKernelGGL((k_decode_merge_small<HD, C, 2>), grid, block, 0, st, a);
+            else if (max_splits <= 4)
+                hipLaunchKernelGGL((k_decode_merge_small<HD, C, 4>), grid, block, 0, st, a);
+            else
+                hipLaunchKernelGGL((k_decode_merge_small<HD, C, 8>), grid, block, 0, st, a);
+        }
         G4_CHECK_LAUNCH("attnDecode merge");
         return G4_OK;
     }
