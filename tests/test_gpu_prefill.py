@@ -74,6 +74,9 @@ def check(c, label):
 CASES = [  # (start, T, window)
     (0, 40, 0), (0, 100, 32), (600, 70, 512), (2900, 24, 0), (5, 1, 0), (0, 16, 512), (1000, 33, 512),
     (20000, 8, 0),  # more than 8 parts: the merge takes its many-record form
+    (0, 512, 0),  # a full chunk: masked, interior (two per pass) and diagonal tiles
+    (3000, 200, 0),  # long ranges split into parts, odd and even tile counts
+    (300, 64, 16), (50, 40, 7),  # windows narrower than a 32-key tile: both bounds inside one tile
 ]
 
 
