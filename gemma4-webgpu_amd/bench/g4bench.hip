@@ -3,7 +3,7 @@
 // counter collection). Inputs are synthetic: f16 cache rows from a
 // counter-based hash (values in [-2, 2), unit-RMS scale), queries likewise.
 //
-//   g4bench [--workload stack8k|stack32k|long128k|ragged64|layer512|prefill4k|lmhead|copy] [--iters N]
+//   g4bench [--workload stack8k|stack32k|long128k|ragged64|layer512|prefill4k|prefill4k512|lmhead|copy] [--iters N]
 //           [--sets S] [--mode M]
 //
 // Decode workloads: the configurations above; `e2b8k` / `e2b32k` (35 layers at E2B's head dims,
@@ -14,7 +14,10 @@
 //
 // `prefill4k` runs the causal MFMA prefill of a 4096-token prompt for one
 // global layer and one 512-window local layer, as 512-token chunks (16
-// entries in one launch; --mode whole: one entry per layer).
+// entries in one launch; --mode whole: one entry per layer). `prefill4k512`
+// runs the global layer alone at head_dim 512 (E2B's global layers; each
+// output half's workgroup computes the full-width scores, so the MFMAs issue
+// 1.5x the algorithmic flops it reports).
 //
 // `proj256` / `proj512` run the block's projections (q, k, v and o_proj) of a
 // local / global E2B layer (--mode fused|chain).
@@ -332,36 +335,39 @@ static std::vector<Layer> workload(const std::string& w) {
 }
 
 // Causal prefill of a 4096-token prompt: one global and one W=512 local layer.
-static int run_prefill(const std::string& mode, int iters) {
+static int run_prefill(const std::string& wl, const std::string& mode, int iters) {
     const unsigned T = 4096, CH = mode == "whole" ? 4096 : 512, NQ = NQH, NK = NKH;
+    // prefill4k512: the global layer alone at head_dim 512 (E2B's global layers)
+    const unsigned hd = wl == "prefill4k512" ? 512u : (unsigned)HD;
+    const int n_layers = wl == "prefill4k512" ? 1 : 2;
     hipStream_t st;
     HK(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
     std::vector<g4_prefill_entry> ents;
     double flops = 0;
-    for (int layer = 0; layer < 2; layer++) {
+    for (int layer = 0; layer < n_layers; layer++) {
         const unsigned window = layer ? 512u : 0u;
         void *q, *kc, *vc, *out;
-        CK(g4_malloc(&q, (size_t)T * NQ * HD * 2));
-        CK(g4_malloc(&kc, (size_t)T * NK * HD * 2));
-        CK(g4_malloc(&vc, (size_t)T * NK * HD * 2));
-        CK(g4_malloc(&out, (size_t)T * NQ * HD * 4));
-        hipLaunchKernelGGL(k_fill_f16, dim3(1024), dim3(256), 0, st, (_Float16*)q, (uint64_t)T * NQ * HD, 11u + layer);
-        hipLaunchKernelGGL(k_fill_f16, dim3(1024), dim3(256), 0, st, (_Float16*)kc, (uint64_t)T * NK * HD, 21u + layer);
-        hipLaunchKernelGGL(k_fill_f16, dim3(1024), dim3(256), 0, st, (_Float16*)vc, (uint64_t)T * NK * HD, 31u + layer);
+        CK(g4_malloc(&q, (size_t)T * NQ * hd * 2));
+        CK(g4_malloc(&kc, (size_t)T * NK * hd * 2));
+        CK(g4_malloc(&vc, (size_t)T * NK * hd * 2));
+        CK(g4_malloc(&out, (size_t)T * NQ * hd * 4));
+        hipLaunchKernelGGL(k_fill_f16, dim3(1024), dim3(256), 0, st, (_Float16*)q, (uint64_t)T * NQ * hd, 11u + layer);
+        hipLaunchKernelGGL(k_fill_f16, dim3(1024), dim3(256), 0, st, (_Float16*)kc, (uint64_t)T * NK * hd, 21u + layer);
+        hipLaunchKernelGGL(k_fill_f16, dim3(1024), dim3(256), 0, st, (_Float16*)vc, (uint64_t)T * NK * hd, 31u + layer);
         for (unsigned c0 = 0; c0 < T; c0 += CH) {
-            g4_prefill_entry e = {(const uint16_t*)q + (size_t)c0 * NQ * HD, (const uint16_t*)kc, (const uint16_t*)vc,
-                                  (float*)out + (size_t)c0 * NQ * HD, CH, c0, window, 1.0f};
+            g4_prefill_entry e = {(const uint16_t*)q + (size_t)c0 * NQ * hd, (const uint16_t*)kc, (const uint16_t*)vc,
+                                  (float*)out + (size_t)c0 * NQ * hd, CH, c0, window, 1.0f};
             ents.push_back(e);
         }
-        for (unsigned i = 0; i < T; i++) flops += 4.0 * HD * NQ * (window && i + 1 > window ? window : i + 1);
+        for (unsigned i = 0; i < T; i++) flops += 4.0 * hd * NQ * (window && i + 1 > window ? window : i + 1);
     }
     HK(hipGetLastError());
     size_t ws_bytes = 0;
-    CK(g4_attn_prefill_workspace_size(ents.data(), (uint32_t)ents.size(), NQ, NK, HD, &ws_bytes));
+    CK(g4_attn_prefill_workspace_size(ents.data(), (uint32_t)ents.size(), NQ, NK, hd, &ws_bytes));
     void* ws;
     CK(g4_malloc(&ws, ws_bytes ? ws_bytes : 256));
     g4_decode_plan plan;
-    CK(g4_attn_prefill_prepare(ents.data(), (uint32_t)ents.size(), NQ, NK, HD, ws, ws_bytes, &plan, st));
+    CK(g4_attn_prefill_prepare(ents.data(), (uint32_t)ents.size(), NQ, NK, hd, ws, ws_bytes, &plan, st));
     for (int i = 0; i < 3; i++) CK(g4_attn_prefill_run(&plan, st));
     CK(g4_stream_synchronize(st));
     hipEvent_t a, b;
@@ -375,7 +381,7 @@ static int run_prefill(const std::string& mode, int iters) {
     HK(hipEventElapsedTime(&ms, a, b));
     const double us = ms * 1e3 / iters;
     printf("flops_per_step: %.0f\n", flops);
-    printf("prefill4k [%s]: %zu entries, %.2f us/step, %.1f TFLOP/s algorithmic (%d iterations)\n", mode.c_str(),
+    printf("%s [%s]: %zu entries, %.2f us/step, %.1f TFLOP/s algorithmic (%d iterations)\n", wl.c_str(), mode.c_str(),
            ents.size(), us, flops / (us * 1e-6) / 1e12, iters);
     return 0;
 }
@@ -395,7 +401,7 @@ int main(int argc, char** argv) {
     }
     CK(g4_set_device(0));
     if (wl == "copy") return run_copy(iters);
-    if (wl == "prefill4k") return run_prefill(mode, iters);
+    if (wl == "prefill4k" || wl == "prefill4k512") return run_prefill(wl, mode, iters);
     if (wl == "lmhead") return run_lmhead(mode, iters);
     if (wl == "proj256" || wl == "proj512") return run_proj(wl, mode, iters);
     std::vector<Layer> L = workload(wl);
