@@ -1,15 +1,21 @@
 #!/usr/bin/env python3
 """Decode-attention benchmark on one MI355X: µs/token and HBM GB/s (% of roofline).
 
-    python bench.py [--steps K] [--warmup W] [--workload stack8k|stack32k|long128k|ragged64|layer512]
+    python bench.py [--steps K] [--warmup W] [--workload NAME]
 
 A step is one token's attention over the workload on synthetic, seeded,
 inputs resident in HBM:
-  stack8k   35-layer Gemma-4-E2B-shaped stack, batch 1, position 8192
-            (7 global layers full causal, RoPE theta 1e6; 28 local layers
-            with a 512-row window, theta 1e4), 35 separate f16 KV caches,
-            8 query heads / 1 KV head, head_dim 256.            [default]
-  stack32k  the same stack at position 32768.
+  stack32k  35-layer Gemma-4-E2B-shaped stack, batch 1, position 32768 (7 global
+            layers full causal, RoPE theta 1e6; 28 local layers with a 512-row
+            window, theta 1e4), 35 separate f16 KV caches, 8 query heads / 1 KV
+            head, head_dim 256: the shape the decode target is set on.  [default]
+            The default run also measures stack8k and reports it under
+            "stack8k" in the same line.
+  stack8k   the same stack at position 8192.
+  e2b8k     the real Gemma-4-E2B stack at position 8192: head_dim 512 on the
+  e2b32k    7 global layers, layers 15..34 reading layer 13's (local) or 14's
+            (global) cache (KV sharing, src/config/gemma4-e2b.ts:159-178); one
+            launch per head_dim; e2b32k at position 32768.
   long128k  one global layer attending 131072 rows.
   ragged64  64 independent sequences, lengths uniform in [1024, 32768].
   layer512  one local layer at position 512 (launch-bound).
@@ -24,18 +30,21 @@ inputs resident in HBM:
             pass plus a one-workgroup pick. Reported in GB/s of algorithmic
             bytes (weight + hidden + logits written).
 
-A step is one launch of the fused attention step over every entry (per entry:
-q/k RMSNorm + RoPE, weightless v-norm, f16 store of the new K/V row, split-K
-flash-decoding attention over the attended rows) plus the log-sum-exp merge
-launch. Several distinct cache sets are rotated so the bytes read each cycle
-exceed twice MI355X's 256 MB Infinity Cache and come from HBM. `value` is
-algorithmic bytes per step (K/V rows attended, f16, read once for all query
-heads; q read; attnOut written) over wall time per step. `roofline` is the
-dominant kernel (k_attn_step), timed with HIP events on its stream; its
-`traffic` comes from the committed rocprofv3 counter summary of the same
-workload. `cpu_baseline` runs the oracle (the WGSL-semantics C restatement of
-the reference's six kernels, f32 caches, full-length score/softmax/output on
-every layer as the WGSL does) on the host.
+A decode step is one launch of the fused attention step over every entry of a
+head_dim (per entry: q/k RMSNorm + RoPE, weightless v-norm, f16 store of the
+new K/V row, split-K flash-decoding attention over the attended rows), plus
+the log-sum-exp merge launch when the plan has split entries. Several
+distinct cache sets are rotated so the bytes read each cycle exceed twice
+MI355X's 256 MB Infinity Cache and come from HBM. `value` is algorithmic bytes
+per step (K/V rows attended, f16, read once for all query heads; q read;
+attnOut written) over wall time per step. `roofline` is the dominant kernel
+(k_attn_step), timed with HIP events on its stream; its `traffic` comes from
+the committed rocprofv3 counter summary of the same workload. `decode_loop`
+advances the position every step and re-prepares every entry (host partition,
+RoPE factors, table uploads) inside the timed region. `cpu_baseline` runs the
+oracle (the WGSL-semantics C restatement of the reference's six kernels, f32
+caches, full-length score/softmax/output on every layer as the WGSL does) on
+the host.
 """
 from __future__ import annotations
 
@@ -56,6 +65,7 @@ MALL_BYTES = 256 << 20
 NQH, NKH, HD = 8, 1, 256
 EPS = 1e-6
 BASE_SEED = 20261201
+DEFAULT_WORKLOAD = "stack32k"
 
 
 def log(msg: str) -> None:
@@ -65,27 +75,45 @@ def log(msg: str) -> None:
 # ---- workload description -----------------------------------------------------
 
 def workload_spec(name: str) -> dict:
+    """Layers (entries) of one step: window, theta, divisor, seq (rows incl. the current one), pos,
+    hd (head_dim) and producer (the entry whose cache it reads; itself for a KV producer)."""
     from g4attn import e2b
+
+    def layer(**kw):
+        d = dict(hd=HD, producer=None)
+        d.update(kw)
+        return d
 
     if name in ("stack8k", "stack32k"):
         pos = 8192 if name == "stack8k" else 32768
         cfg = e2b.AttnConfig(num_layers=35)
-        layers = [dict(window=e2b.sliding_window(il, cfg), theta=e2b.rope_theta(il, cfg),
-                       divisor=e2b.apply_divisor(il, cfg), seq=pos + 1, pos=pos) for il in range(35)]
+        layers = [layer(window=e2b.sliding_window(il, cfg), theta=e2b.rope_theta(il, cfg),
+                        divisor=e2b.apply_divisor(il, cfg), seq=pos + 1, pos=pos) for il in range(35)]
         return dict(name=name, layers=layers, seed=BASE_SEED + (1 if name == "stack8k" else 5),
-                    desc=f"35-layer Gemma-4-E2B attention stack, bs1, position {pos} (7 global + 28 local W=512)")
+                    desc=f"35-layer Gemma-4-E2B attention stack, bs1, position {pos} (7 global + 28 local W=512), "
+                         "head_dim 256, 35 separate caches")
+    if name in ("e2b8k", "e2b32k"):
+        pos = 8192 if name == "e2b8k" else 32768
+        cfg = e2b.AttnConfig(num_layers=35)
+        pmap = e2b.compute_kv_producer_map(cfg)
+        layers = [layer(window=e2b.sliding_window(il, cfg), theta=e2b.rope_theta(il, cfg),
+                        divisor=e2b.apply_divisor(il, cfg), seq=pos + 1, pos=pos, hd=e2b.head_dim(il, cfg),
+                        producer=None if pmap[il] == il else pmap[il]) for il in range(35)]
+        return dict(name=name, layers=layers, seed=BASE_SEED + (6 if name == "e2b8k" else 7),
+                    desc=f"Gemma-4-E2B attention stack, bs1, position {pos}: head_dim 512 on the 7 global layers, "
+                         "layers 15..34 reading layer 13's / 14's cache, one launch per head_dim")
     if name == "long128k":
         pos = 131071
-        return dict(name=name, layers=[dict(window=0, theta=1e6, divisor=1, seq=pos + 1, pos=pos)],
+        return dict(name=name, layers=[layer(window=0, theta=1e6, divisor=1, seq=pos + 1, pos=pos)],
                     seed=BASE_SEED + 4, desc="1 global layer, 131072 attended rows, bs1")
     if name == "layer512":
-        return dict(name=name, layers=[dict(window=512, theta=1e4, divisor=0, seq=513, pos=512)],
+        return dict(name=name, layers=[layer(window=512, theta=1e4, divisor=0, seq=513, pos=512)],
                     seed=BASE_SEED + 0, desc="1 local layer (W=512), position 512, bs1")
     if name == "ragged64":
-        from g4attn import synth
+        from g4attn import workloads
 
-        lens = synth.ragged_lengths(BASE_SEED + 2, 64, 1024, 32768)
-        layers = [dict(window=0, theta=1e6, divisor=1, seq=int(L), pos=int(L) - 1) for L in lens]
+        lens = workloads.ragged64_lengths()
+        layers = [layer(window=0, theta=1e6, divisor=1, seq=L, pos=L - 1) for L in lens]
         return dict(name=name, layers=layers, seed=BASE_SEED + 2,
                     desc="64 sequences, ragged lengths U[1024, 32768], global attention")
     raise SystemExit(f"unknown workload {name}")
@@ -95,71 +123,107 @@ def attended(seq: int, window: int) -> int:
     return min(seq, window) if window else seq
 
 
+def layer_bytes(L: dict) -> int:
+    """Algorithmic HBM bytes of one entry: attended K and V rows (f16) once for all query heads,
+    q read (f32) and attnOut written (f32). A KV-consumer layer reads its producer's rows again."""
+    return 2 * attended(L["seq"], L["window"]) * NKH * L["hd"] * 2 + NQH * L["hd"] * 4 * 2
+
+
 def step_bytes(spec: dict) -> int:
-    """Algorithmic HBM bytes of one step: attended K and V rows (f16) once for all query
-    heads, q read (f32) and attnOut written (f32) per layer."""
-    b = 0
-    for L in spec["layers"]:
-        b += 2 * attended(L["seq"], L["window"]) * NKH * HD * 2 + NQH * HD * 4 * 2
-    return b
+    return sum(layer_bytes(L) for L in spec["layers"])
 
 
 # ---- GPU side -----------------------------------------------------------------
 
 class CacheSet:
-    """One complete set of per-entry buffers (caches, raw q/k/v projections, outputs) and
-    the prepared one-launch step over all entries."""
+    """One complete set of per-entry buffers (caches, raw q/k/v projections, outputs) and the
+    prepared one-launch steps over the entries (one per head_dim)."""
 
-    def __init__(self, spec, set_idx, dev, torch, ops, synth, e2b):
-        self.entries = []
+    def __init__(self, spec, set_idx, dev, torch, ops, synth, e2b, extra_rows=0):
         import numpy as np
 
         seed0 = spec["seed"] + 7919 * set_idx
         rf_bits = np.array(e2b.rope_freqs_f16_bits(256), dtype=np.uint16)
         rf = torch.from_numpy(rf_bits.view(np.int16)).to(dev)
-        ones = torch.full((HD,), 0x3C00, dtype=torch.int16, device=dev)  # norm weights 1.0 (f16)
-        inv_freq = {}  # one RoPE inverse-frequency table per (theta, divisor), as a model holds them
+        ones = {hd: torch.full((hd,), 0x3C00, dtype=torch.int16, device=dev) for hd in (256, 512)}  # f16 1.0
+        self.inv_freq = {}  # one RoPE inverse-frequency table per (theta, divisor, head_dim), as a model holds them
+        self.items = []
         for il, L in enumerate(spec["layers"]):
-            key = (L["theta"], L["divisor"])
-            if key not in inv_freq:
-                inv_freq[key] = ops.rope_inv_freq_host(L["theta"], HD, L["divisor"], rf_bits)
-            rows = L["seq"]
-            kc = torch.empty(rows * NKH * HD, dtype=torch.float16, device=dev)
-            vc = torch.empty_like(kc)
-            n_att = attended(L["seq"], L["window"])
-            lo = L["seq"] - n_att
-            for cache, off in ((kc, 0), (vc, 1)):  # rows the step reads: N(0,1), then RMS-normalised per head
-                x = synth.normal_torch(seed0 + 1000 * il + off, n_att * NKH * HD, dev).view(-1, HD)
-                ms = (x.double() ** 2).mean(dim=1, keepdim=True)
-                y = (x.double() / torch.sqrt(ms + EPS)).to(torch.float16)
-                cache.view(rows, -1)[lo:lo + n_att].copy_(y.view(n_att, -1))
-            self.entries.append(dict(
-                q=synth.normal_torch(seed0 + 1000 * il + 2, NQH * HD, dev),
-                k=synth.normal_torch(seed0 + 1000 * il + 3, NKH * HD, dev),
-                v=synth.normal_torch(seed0 + 1000 * il + 4, NKH * HD, dev),
-                q_weight=ones, k_weight=ones, rope_freqs=rf, rope_inv_freq_host=inv_freq[key], k_cache=kc.view(torch.int16),
-                v_cache=vc.view(torch.int16), out=torch.zeros(NQH * HD, dtype=torch.float32, device=dev),
-                seq_len=L["seq"], position=L["pos"], sliding_window=L["window"], store_kv=True,
-                theta=L["theta"], apply_divisor=L["divisor"], scale=1.0, eps=EPS))
-        arr = ops.make_step_entries(self.entries, NQH, NKH, HD)
-        self.ws = torch.empty(ops.step_workspace_bytes(len(self.entries), NQH, NKH, HD), dtype=torch.uint8,
-                              device=dev)
-        self.plan = ops.attn_step_prepare(arr, NQH, NKH, HD, self.ws)
+            hd = L["hd"]
+            key = (L["theta"], L["divisor"], hd)
+            if key not in self.inv_freq:
+                self.inv_freq[key] = ops.rope_inv_freq_host(L["theta"], hd, L["divisor"], rf_bits)
+            it = dict(q=synth.normal_torch(seed0 + 1000 * il + 2, NQH * hd, dev), q_weight=ones[hd],
+                      rope_freqs=rf, rope_inv_freq_host=self.inv_freq[key],
+                      out=torch.zeros(NQH * hd, dtype=torch.float32, device=dev), seq_len=L["seq"],
+                      position=L["pos"], sliding_window=L["window"], theta=L["theta"], apply_divisor=L["divisor"],
+                      scale=1.0, eps=EPS)
+            if L["producer"] is None:
+                rows = L["seq"] + extra_rows
+                kc = torch.empty(rows * NKH * hd, dtype=torch.float16, device=dev)
+                vc = torch.empty_like(kc)
+                n_att = attended(L["seq"], L["window"])
+                lo = L["seq"] - n_att
+                for cache, off in ((kc, 0), (vc, 1)):  # rows the step reads: N(0,1), then RMS-normalised per head
+                    x = synth.normal_torch(seed0 + 1000 * il + off, n_att * NKH * hd, dev).view(-1, hd)
+                    ms = (x.double() ** 2).mean(dim=1, keepdim=True)
+                    y = (x.double() / torch.sqrt(ms + EPS)).to(torch.float16)
+                    cache.view(rows, -1)[lo:lo + n_att].copy_(y.view(n_att, -1))
+                it.update(k=synth.normal_torch(seed0 + 1000 * il + 3, NKH * hd, dev),
+                          v=synth.normal_torch(seed0 + 1000 * il + 4, NKH * hd, dev), k_weight=ones[hd],
+                          k_cache=kc.view(torch.int16), v_cache=vc.view(torch.int16), store_kv=True)
+            else:  # a consumer in its producer's launch: the producer's raw k/v and k_norm, no store
+                p = self.items[L["producer"]]
+                it.update(k=p["k"], v=p["v"], k_weight=p["k_weight"], k_cache=p["k_cache"], v_cache=p["v_cache"],
+                          store_kv=False)
+            it["hd"] = hd
+            self.items.append(it)
+        self.groups = []  # (head_dim, entry indexes, ctypes entries, workspace, plan)
+        for hd in sorted({it["hd"] for it in self.items}):
+            idx = [i for i, it in enumerate(self.items) if it["hd"] == hd]
+            arr = ops.make_step_entries([self.items[i] for i in idx], NQH, NKH, hd)
+            ws = torch.empty(ops.step_workspace_bytes(len(idx), NQH, NKH, hd), dtype=torch.uint8, device=dev)
+            self.groups.append([hd, idx, arr, ws, ops.attn_step_prepare(arr, NQH, NKH, hd, ws)])
         self.layer_plans = None
+
+    def run(self, ops, ev=None):
+        for gi, (hd, idx, arr, ws, plan) in enumerate(self.groups):
+            if ev is None:
+                ops.attn_step_run(plan)
+            else:
+                ops.attn_step_run_attention_timed(plan, ev[gi][0], ev[gi][1])
+                ops.attn_step_run_merge(plan)
+
+    def advance(self, ops):
+        """The next token: every entry one row longer, re-prepared (the engine rewrites the position,
+        slot and seq_len uniforms every token, src/engine.ts:1967-1987)."""
+        from g4attn import abi
+
+        for g in self.groups:
+            hd, idx, arr, ws, plan = g
+            for j in range(len(idx)):
+                arr[j].seq_len += 1
+                arr[j].position += 1
+            g[4] = ops.attn_step_prepare(arr, NQH, NKH, hd, ws)
 
     def prepare_per_entry(self, torch, ops, dev):
         """One single-entry plan per entry: the engine's issue order (layer after layer)."""
-        self.layer_ws = [torch.empty(ops.step_workspace_bytes(1, NQH, NKH, HD), dtype=torch.uint8, device=dev)
-                         for _ in self.entries]
-        self.layer_plans = [ops.attn_step_prepare(ops.make_step_entries([e], NQH, NKH, HD), NQH, NKH, HD, w)
-                            for e, w in zip(self.entries, self.layer_ws)]
+        self.layer_plans = []
+        for it in self.items:
+            hd = it["hd"]
+            w = torch.empty(ops.step_workspace_bytes(1, NQH, NKH, hd), dtype=torch.uint8, device=dev)
+            e = dict(it)
+            if not it["store_kv"]:  # engine order: the producer's step already stored the row
+                e["k"] = e["v"] = e["k_weight"] = None
+            self.layer_plans.append((w, ops.attn_step_prepare(ops.make_step_entries([e], NQH, NKH, hd), NQH, NKH,
+                                                              hd, w)))
 
     def step_sequential(self, ops):
-        for p in self.layer_plans:
+        for _, p in self.layer_plans:
             ops.attn_step_run(p)
 
 
-def run_gpu(spec, args):
+def run_gpu(spec, args, decode_loop=False):
     import torch
 
     from g4attn import abi, e2b, ops, synth
@@ -171,21 +235,18 @@ def run_gpu(spec, args):
     sets = args.sets or max(1, math.ceil(2 * MALL_BYTES / max(per_step, 1)) + 1)
     if per_step < 4 << 20:
         sets = 1  # tiny workloads are launch-bound; rotating sets changes nothing
+    loop_tokens = args.warmup + args.steps if decode_loop else 0
     log(f"workload {spec['name']}: {len(spec['layers'])} entries, {per_step / 1e6:.1f} MB/step, {sets} cache sets")
     t0 = time.time()
-    csets = [CacheSet(spec, s, dev, torch, ops, synth, e2b) for s in range(sets)]
+    csets = [CacheSet(spec, s, dev, torch, ops, synth, e2b, extra_rows=loop_tokens) for s in range(sets)]
     torch.cuda.synchronize()
     log(f"inputs ready in {time.time() - t0:.1f}s")
 
     stream = torch.cuda.current_stream()
+    n_groups = len(csets[0].groups)
 
     def step(i, ev=None):
-        cs = csets[i % sets]
-        if ev is None:
-            ops.attn_step_run(cs.plan)
-            return
-        ops.attn_step_run_attention_timed(cs.plan, ev[0], ev[1])
-        ops.attn_step_run_merge(cs.plan)
+        csets[i % sets].run(ops, ev)
 
     for i in range(args.warmup):
         step(i)
@@ -201,21 +262,46 @@ def run_gpu(spec, args):
     wall = time.perf_counter() - t_start
     log(f"timed {args.steps} steps: {wall / args.steps * 1e6:.2f} us/step")
 
-    # The attention kernel alone: HIP events on its stream that take the kernel's own start and
+    # The attention kernels alone: HIP events on their stream that take each kernel's own start and
     # end timestamps (hipExtLaunchKernelGGL), the figure rocprofv3 reports for the same kernel.
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
-    for a_, b_ in evs:  # create the HIP events
-        a_.record(stream)
-        b_.record(stream)
+    evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n_groups)]
+           for _ in range(args.steps)]
+    for per in evs:  # create the HIP events
+        for a_, b_ in per:
+            a_.record(stream)
+            b_.record(stream)
     torch.cuda.synchronize()
     for i in range(args.steps):
         step(args.warmup + i, evs[i])
     torch.cuda.synchronize()
-    att_ms = sorted(a.elapsed_time(b) for a, b in evs)
+    att_ms = sorted(sum(a.elapsed_time(b) for a, b in per) for per in evs)
     att_avg = sum(att_ms) / len(att_ms)
-    log(f"k_attn_step: avg {att_avg * 1e3:.2f} us, median {att_ms[len(att_ms) // 2] * 1e3:.2f} us (events)")
+    log(f"k_attn_step: avg {att_avg * 1e3:.2f} us, median {att_ms[len(att_ms) // 2] * 1e3:.2f} us (events, "
+        f"{n_groups} launch(es) per step)")
     result = dict(wall_s=wall, steps=args.steps, attn_avg_ms=att_avg, attn_median_ms=att_ms[len(att_ms) // 2],
-                  sets=sets, bytes=per_step)
+                  sets=sets, bytes=per_step, launches=n_groups)
+
+    if decode_loop:
+        # A position-advancing decode loop: every step re-prepares every entry one row further (host
+        # partition, RoPE factors, pinned-ring table uploads) and runs it, all inside the timed region.
+        for i in range(args.warmup):
+            cs = csets[i % sets]
+            cs.advance(ops)
+            cs.run(ops)
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+        host = 0.0
+        for i in range(args.steps):
+            cs = csets[(args.warmup + i) % sets]
+            h0 = time.perf_counter()
+            cs.advance(ops)
+            host += time.perf_counter() - h0
+            cs.run(ops)
+        torch.cuda.synchronize()
+        result["loop_us"] = (time.perf_counter() - t2) / args.steps * 1e6
+        result["loop_prepare_us"] = host / args.steps * 1e6
+        log(f"decode loop (prepare + run per token): {result['loop_us']:.2f} us/token, prepare "
+            f"{result['loop_prepare_us']:.2f} us/token on the host")
 
     # The engine's issue order: one single-entry step (attention + merge) per layer, replayed as a HIP graph.
     if args.sequential and len(spec["layers"]) > 1:
@@ -238,6 +324,8 @@ def run_gpu(spec, args):
         torch.cuda.synchronize()
         result["sequential_us"] = (time.perf_counter() - t2) / n * 1e6
         log(f"layer-sequential (graph replay, one cache set): {result['sequential_us']:.1f} us/step")
+    del csets
+    torch.cuda.empty_cache()
     return result
 
 
@@ -263,15 +351,21 @@ def measure_read_ceiling(torch, ops, gib: int = 2, reps: int = 10) -> float:
     return (gib << 30) / (ms * 1e-3) / 1e9
 
 
+_CEILING = None
+
+
 def ceiling_fields(achieved_gbs: float) -> dict:
     """The measured read-stream ceiling of this GPU and the kernel's fraction of it (next to `frac`, which
     is against the spec sheet's 8 TB/s)."""
+    global _CEILING
     import torch
 
     from g4attn import ops
 
-    c = measure_read_ceiling(torch, ops)
-    log(f"read-stream ceiling {c:.1f} GB/s")
+    if _CEILING is None:
+        _CEILING = measure_read_ceiling(torch, ops)
+        log(f"read-stream ceiling {_CEILING:.1f} GB/s")
+    c = _CEILING
     return {"measured_ceiling": round(c, 1), "frac_of_measured_ceiling": round(achieved_gbs / c, 4),
             "ceiling_source": "g4_read_ceiling: 2 GiB nontemporal 16-byte streaming read, best of 10"}
 
@@ -302,36 +396,36 @@ def run_cpu_baseline(spec, seconds: float):
     threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
     orc.set_threads(threads)
     rf = np.array(e2b.rope_freqs_f16_bits(256), dtype=np.uint16)
-    ones = np.full(HD, 0x3C00, dtype=np.uint16)
     layers = spec["layers"]
     # The reference's per-layer buffers: f32 caches of seq rows each (the WGSL scores and masks the rows
-    # outside a local window, so they are read too). Timing only: filled from numpy's generator.
+    # outside a local window, so they are read too); consumer layers read their producer's. Timing only:
+    # filled from numpy's generator.
     rng = np.random.default_rng(spec["seed"])
-    caches = []
-    for L in layers:
-        rows = L["seq"]
-        kc = rng.standard_normal((rows, HD), dtype=np.float32)
-        vc = rng.standard_normal((rows, HD), dtype=np.float32)
-        caches.append((kc, vc))
-    log(f"cpu baseline: {threads} threads, {len(layers)} f32 cache pairs built")
-    q0 = [synth.normal(spec["seed"] + 97 * il, NQH * HD) for il in range(len(layers))]
-    kv0 = [(synth.normal(spec["seed"] + 97 * il + 1, HD), synth.normal(spec["seed"] + 97 * il + 2, HD))
-           for il in range(len(layers))]
-
-    with_prep = spec.get("prep", True)
+    caches = {}
+    for il, L in enumerate(layers):
+        if L["producer"] is None:
+            rows = L["seq"]
+            caches[il] = (rng.standard_normal((rows, L["hd"]), dtype=np.float32),
+                          rng.standard_normal((rows, L["hd"]), dtype=np.float32))
+    log(f"cpu baseline: {threads} threads, {len(caches)} f32 cache pairs built")
+    q0 = [synth.normal(spec["seed"] + 97 * il, NQH * L["hd"]) for il, L in enumerate(layers)]
+    kv0 = [(synth.normal(spec["seed"] + 97 * il + 1, L["hd"]), synth.normal(spec["seed"] + 97 * il + 2, L["hd"]))
+           for il, L in enumerate(layers)]
 
     def one_token():
         for il, L in enumerate(layers):
-            kc, vc = caches[il]
-            if not with_prep:
-                orc.attention_chain(q0[il], kc, vc, NQH, NKH, HD, L["seq"], 1.0, L["window"])
-                continue
-            v = orc.per_head_rms_norm_no_weight(kv0[il][1], NKH, HD, EPS)
-            q = orc.fused_per_head_norm_rope(q0[il], ones, rf, NQH, HD, EPS, L["pos"], L["theta"], L["divisor"])
-            k = orc.fused_per_head_norm_rope(kv0[il][0], ones, rf, NKH, HD, EPS, L["pos"], L["theta"], L["divisor"])
-            kc[L["pos"]] = k  # kvCacheStore (f32 caches)
-            vc[L["pos"]] = v
-            orc.attention_chain(q, kc, vc, NQH, NKH, HD, L["seq"], 1.0, L["window"])
+            hd = L["hd"]
+            ones = np.full(hd, 0x3C00, dtype=np.uint16)
+            own = L["producer"] is None
+            kc, vc = caches[il if own else L["producer"]]
+            q = orc.fused_per_head_norm_rope(q0[il], ones, rf, NQH, hd, EPS, L["pos"], L["theta"], L["divisor"])
+            if own:
+                v = orc.per_head_rms_norm_no_weight(kv0[il][1], NKH, hd, EPS)
+                k = orc.fused_per_head_norm_rope(kv0[il][0], ones, rf, NKH, hd, EPS, L["pos"], L["theta"],
+                                                 L["divisor"])
+                kc[L["pos"]] = k  # kvCacheStore (f32 caches)
+                vc[L["pos"]] = v
+            orc.attention_chain(q, kc, vc, NQH, NKH, hd, L["seq"], 1.0, L["window"])
 
     n = 0
     t0 = time.perf_counter()
@@ -347,41 +441,18 @@ def run_cpu_baseline(spec, seconds: float):
 
 # ---- prefill (MFMA) ------------------------------------------------------------------
 
-PREFILL_T, PREFILL_CHUNK, PREFILL_WINDOWS = 4096, 512, (0, 512)
 MFMA_F16_PEAK_TFLOPS = 2500.0
-
-
-def prefill_flops() -> float:
-    f = 0.0
-    for w in PREFILL_WINDOWS:
-        for i in range(PREFILL_T):
-            f += 4.0 * HD * NQH * (min(i + 1, w) if w else i + 1)
-    return f
 
 
 def run_prefill_gpu(args):
     import torch
 
-    from g4attn import abi, ops, synth
+    from g4attn import abi, ops, workloads
 
     abi.load()
     abi.call("g4_set_device", 0)
     dev = torch.device("cuda:0")
-
-    def unit_f16(seed, rows):
-        x = synth.normal_torch(seed, rows * HD, dev).view(rows, HD).double()
-        return (x / torch.sqrt((x ** 2).mean(dim=1, keepdim=True) + EPS)).to(torch.float16).view(-1)
-
-    layers, entries = [], []
-    for li, w in enumerate(PREFILL_WINDOWS):
-        q = unit_f16(BASE_SEED + 30 + li, PREFILL_T * NQH).view(torch.int16)
-        kc = unit_f16(BASE_SEED + 40 + li, PREFILL_T * NKH).view(torch.int16)
-        vc = unit_f16(BASE_SEED + 50 + li, PREFILL_T * NKH).view(torch.int16)
-        out = torch.empty(PREFILL_T * NQH * HD, dtype=torch.float32, device=dev)
-        layers.append((q, kc, vc, out))
-        for c0 in range(0, PREFILL_T, PREFILL_CHUNK):
-            entries.append(dict(q=q[c0 * NQH * HD:], k_cache=kc, v_cache=vc, out=out[c0 * NQH * HD:],
-                                n_tokens=PREFILL_CHUNK, start=c0, sliding_window=w, scale=1.0))
+    _, entries = workloads.prefill4k(dev, NQH, NKH, HD)
     arr = ops.make_prefill_entries(entries, NQH, NKH, HD)
     ws = torch.empty(ops.prefill_workspace_bytes(arr, NQH, NKH, HD), dtype=torch.uint8, device=dev)
     plan = ops.attn_prefill_prepare(arr, NQH, NKH, HD, ws)
@@ -412,6 +483,7 @@ def run_prefill_cpu(seconds: float):
     positions (every 256th token of each layer), timed and scaled by the attended keys."""
     import numpy as np
 
+    from g4attn.workloads import PREFILL_T, PREFILL_WINDOWS
     from oracle import oracle as orc
 
     threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
@@ -434,8 +506,10 @@ def run_prefill_cpu(seconds: float):
 
 
 def main_prefill(args):
+    from g4attn import workloads
+
     r = run_prefill_gpu(args)
-    flops = prefill_flops()
+    flops = workloads.prefill_flops(NQH, HD)
     ms_per_step = r["wall_s"] / r["steps"] * 1e3
     value = flops / (ms_per_step * 1e-3) / 1e12
     achieved = flops / (r["kernel_ms"] * 1e-3) / 1e12
@@ -549,36 +623,13 @@ def main_lmhead(args):
     print(json.dumps(line), flush=True)
 
 
-def main():
-    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="stack8k",
-                    choices=["stack8k", "stack32k", "long128k", "ragged64", "layer512", "prefill4k", "lmhead"])
-    ap.add_argument("--sets", type=int, default=0, help="cache sets to rotate (0 = enough to exceed 2x MALL)")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--sequential", action=argparse.BooleanOptionalAction, default=True,
-                    help="also time the layer-after-layer issue order (HIP graph)")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported (the attention path "
-              "would shard by sequence or by KV range across GPUs, which is not built here)", file=sys.stderr)
-        sys.exit(2)
-
-    if args.workload == "prefill4k":
-        main_prefill(args)
-        return
-    if args.workload == "lmhead":
-        main_lmhead(args)
-        return
-    spec = workload_spec(args.workload)
-    r = run_gpu(spec, args)
+def decode_line(name, args, decode_loop):
+    spec = workload_spec(name)
+    r = run_gpu(spec, args, decode_loop=decode_loop)
     ms_per_step = r["wall_s"] / r["steps"] * 1e3
     value = r["bytes"] / (ms_per_step * 1e-3) / 1e9
     achieved = r["bytes"] / (r["attn_avg_ms"] * 1e-3) / 1e9
-    traffic = read_traffic(args.workload)
+    traffic = read_traffic(name)
     line = {
         "metric": "decode-attention us/token & HBM GB/s (% roofline), E2B-shaped, bs1",
         "value": round(value, 1),
@@ -593,17 +644,25 @@ def main():
         "vs_baseline": None,
         "dtype": "f16 KV, f32 accumulate",
         "data": "synthetic (seeded splitmix64 N(0,1), unit-RMS rows), resident in HBM",
-        "config": {"workload": spec["desc"], "batch": 1, "num_q_heads": NQH, "num_kv_heads": NKH,
-                   "head_dim": HD, "bytes_per_step": r["bytes"], "cache_sets_rotated": r["sets"],
-                   "issue": "all entries of the step in one attention launch (q/k RMSNorm+RoPE, v-norm, KV "
-                            "store, split-K attention) plus one log-sum-exp merge launch"},
-        "roofline": {"bound": "hbm", "kernel": "k_attn_step", "achieved": round(achieved, 1),
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic, "avg_us": round(r["attn_avg_ms"] * 1e3, 2),
-                     "traffic_source": f"profiles/k_attn_step_{args.workload}_traffic.txt" if traffic else None},
+        "config": {"workload": name, "description": spec["desc"], "batch": 1, "num_q_heads": NQH,
+                   "num_kv_heads": NKH, "head_dims": sorted({L["hd"] for L in spec["layers"]}),
+                   "bytes_per_step": r["bytes"], "cache_sets_rotated": r["sets"],
+                   "issue": "per head_dim, all entries of the step in one attention launch (q/k RMSNorm+RoPE, "
+                            "v-norm, KV store, split-K attention) plus the log-sum-exp merge launch when the plan "
+                            "has split entries"},
+        "roofline": {"bound": "hbm", "kernel": "k_attn_step", "launches_per_step": r["launches"],
+                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "avg_us": round(r["attn_avg_ms"] * 1e3, 2),
+                     "traffic_source": f"profiles/k_attn_step_{name}_traffic.txt" if traffic else None},
     }
-    ceiling = ceiling_fields(achieved)
-    line["roofline"].update(ceiling)
+    line["roofline"].update(ceiling_fields(achieved))
+    if "loop_us" in r:
+        line["decode_loop"] = {"us_per_token": round(r["loop_us"], 2),
+                               "prepare_us_per_token": round(r["loop_prepare_us"], 2),
+                               "GBps": round(r["bytes"] / (r["loop_us"] * 1e-6) / 1e9, 1),
+                               "what": "position advanced every token; every entry re-prepared (host partition, "
+                                       "RoPE factors, pinned-ring uploads) and run, inside the timed region"}
     if "sequential_us" in r:
         line["layer_sequential_us_per_token"] = round(r["sequential_us"], 2)
     if not args.no_cpu_baseline:
@@ -614,6 +673,46 @@ def main():
                                 "sample": f"{cpu['tokens']} tokens of the same workload through the oracle's "
                                           "restatement of the six reference WGSL kernels (f32 caches, full-length "
                                           "scores on every layer); no WebGPU CPU adapter on the host"}
+    return line
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default=DEFAULT_WORKLOAD,
+                    choices=["stack32k", "stack8k", "e2b8k", "e2b32k", "long128k", "ragged64", "layer512",
+                             "prefill4k", "lmhead"])
+    ap.add_argument("--sets", type=int, default=0, help="cache sets to rotate (0 = enough to exceed 2x MALL)")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--sequential", action=argparse.BooleanOptionalAction, default=True,
+                    help="also time the layer-after-layer issue order (HIP graph)")
+    ap.add_argument("--decode-loop", action=argparse.BooleanOptionalAction, default=True,
+                    help="also time a position-advancing decode loop (prepare + run per token)")
+    ap.add_argument("--also", default=None,
+                    help="a second decode workload reported nested in the same line (default: stack8k when the "
+                         "workload is the default)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported (the attention path "
+              "would shard by sequence or by KV range across GPUs, which is not built here)", file=sys.stderr)
+        sys.exit(2)
+
+    if args.workload == "prefill4k":
+        main_prefill(args)
+        return
+    if args.workload == "lmhead":
+        main_lmhead(args)
+        return
+    line = decode_line(args.workload, args, args.decode_loop)
+    also = args.also if args.also is not None else ("stack8k" if args.workload == DEFAULT_WORKLOAD else "")
+    if also:
+        sub = decode_line(also, args, args.decode_loop)
+        keep = ("value", "unit", "ms_per_step", "us_per_token", "config", "roofline", "decode_loop",
+                "layer_sequential_us_per_token", "cpu_baseline")
+        line[also] = {k: sub[k] for k in keep if k in sub}
     print(json.dumps(line), flush=True)
 
 

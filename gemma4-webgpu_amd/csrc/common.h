@@ -32,6 +32,19 @@ int hip_fail(hipError_t e, const char* what);
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
+// Host -> device upload of a prepared table, ordered on `st`, through pinned
+// staging memory from a per-thread ring of slots. A slot is reused only once
+// the copy that last read it has completed; when every slot is still in flight
+// the ring grows (up to kStageMaxSlots slots, past which the oldest slot is
+// waited for), so enqueueing never waits on the GPU in practice.
+constexpr int kStageMaxSlots = 4096;
+int stage_upload(void* dst, const void* src, size_t bytes, hipStream_t st);
+// Slots currently held by the calling thread's ring (for tests).
+int stage_slots();
+
+// Compute units of the current device (queried once per device).
+unsigned device_cus();
+
 // ---- types -----------------------------------------------------------------
 
 typedef _Float16 f16;

@@ -16,6 +16,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <vector>
+
 #include "decode_core.h"
 
 namespace g4 {
@@ -162,7 +164,10 @@ __global__ __launch_bounds__(kMergeThreads) void k_decode_merge(DecodeArgs a, un
 #pragma unroll
         for (int u = 0; u < kMergeBatch; u++) {
             if (s0 + u * P < ns) {
-                const float f = __builtin_amdgcn_exp2f(w[u][0] - mb);
+                // A record whose keys were all masked (a prefill part past a token's
+                // position: m = -inf, l = 0, o = 0) weighs 0; exp2(-inf - -inf) would be NaN
+                // while every record of this group so far is of that kind.
+                const float f = w[u][0] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(w[u][0] - mb);
                 acc += v[u] * f;
                 l_run += w[u][1] * f;
             }
@@ -228,8 +233,8 @@ __global__ __launch_bounds__(kMergeThreads) void k_decode_merge_small(DecodeArgs
 #pragma unroll
     for (int c = 0; c < COLS / 4; c++) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (unsigned s = 0; s < (unsigned)NS; s++) {
-        const float f = s < ns ? __builtin_amdgcn_exp2f(w[s][0] - M) : 0.0f;
+    for (unsigned s = 0; s < (unsigned)NS; s++) {  // M is finite: every token attends at least its own key
+        const float f = s < ns && w[s][0] != -INFINITY ? __builtin_amdgcn_exp2f(w[s][0] - M) : 0.0f;
         L += w[s][1] * f;
 #pragma unroll
         for (int c = 0; c < COLS / 4; c++) acc[c] += v[s][c] * f;
@@ -295,7 +300,6 @@ int env_int(const char* name, int dflt) {
 }
 
 constexpr unsigned kMinChunk = 128;
-constexpr unsigned kCUs = 256;
 
 inline unsigned round_up(unsigned x, unsigned m) { return (x + m - 1) / m * m; }
 
@@ -313,7 +317,7 @@ unsigned pick_chunk(uint64_t total_rows, uint64_t max_entry_rows, unsigned num_k
     if (env_chunk > 0) {
         chunk = round_up((unsigned)env_chunk, kTileKeys);
     } else {
-        const uint64_t target = (uint64_t)(wgs_per_cu > 0 ? wgs_per_cu : 2) * kCUs / (num_kv_heads ? num_kv_heads : 1);
+        const uint64_t target = (uint64_t)(wgs_per_cu > 0 ? wgs_per_cu : 2) * device_cus() / (num_kv_heads ? num_kv_heads : 1);
         const uint64_t c = (total_rows + target - 1) / (target ? target : 1);
         chunk = round_up((unsigned)(c < kMinChunk ? kMinChunk : c), kTileKeys);
     }
@@ -452,19 +456,7 @@ int g4_attn_decode_many_prepare(const g4_decode_entry* entries, uint32_t n_entri
     }
     const unsigned chunk = pick_chunk(total_rows, max_rows, num_kv_heads, head_dim);
     const uint32_t group = num_q_heads / num_kv_heads;
-    // Pinned staging for the table, reused once the previous upload has completed.
-    static thread_local DecodeEntryDev* staging = nullptr;
-    static thread_local uint32_t staging_cap = 0;
-    static thread_local hipEvent_t staged = nullptr;
-    if (!staged) G4_CHECK_HIP(hipEventCreateWithFlags(&staged, hipEventDisableTiming));
-    G4_CHECK_HIP(hipEventSynchronize(staged));
-    if (staging_cap < n_entries) {
-        if (staging) G4_CHECK_HIP(hipHostFree(staging));
-        staging = nullptr;
-        staging_cap = 0;
-        G4_CHECK_HIP(hipHostMalloc((void**)&staging, (size_t)n_entries * sizeof(DecodeEntryDev), hipHostMallocDefault));
-        staging_cap = n_entries;
-    }
+    std::vector<DecodeEntryDev> staging(n_entries);
     uint64_t total_splits = 0;
     uint32_t max_splits = 0;
     for (uint32_t i = 0; i < n_entries; i++) {
@@ -483,8 +475,8 @@ int g4_attn_decode_many_prepare(const g4_decode_entry* entries, uint32_t n_entri
     if (!workspace || workspace_bytes < need)
         return fail(G4_ENOSPC, "attnDecodeMany: workspace %zu bytes < %zu needed", workspace_bytes, need);
     hipStream_t st = as_stream(stream);
-    G4_CHECK_HIP(hipMemcpyAsync(workspace, staging, (size_t)n_entries * sizeof(DecodeEntryDev), hipMemcpyHostToDevice, st));
-    G4_CHECK_HIP(hipEventRecord(staged, st));
+    rc = stage_upload(workspace, staging.data(), (size_t)n_entries * sizeof(DecodeEntryDev), st);
+    if (rc) return rc;
     PlanRep r = {};
     r.table = static_cast<const DecodeEntryDev*>(workspace);
     char* ws = static_cast<char*>(workspace) + table_bytes;

@@ -305,7 +305,6 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_prefill(PrefillArgs a) {
 // both halves compute the full-width scores (the K tile is 32 KiB, three
 // stages) and read their own 256 rows of the V^T block.
 
-constexpr unsigned kPfCUs = 256;  // MI355X compute units: one prefill workgroup each
 // Tile t's K rows are read by the score MFMAs of iteration t - 1 and its V^T
 // block by the output MFMAs of iteration t + 1; both are issued together at
 // iteration t - 1 - kPfDist. The K ring holds kPfDist + 1 tiles, the V^T ring
@@ -779,29 +778,6 @@ struct PrefillPlanRep {
 };
 static_assert(sizeof(PrefillPlanRep) <= sizeof(g4_decode_plan), "plan size");
 
-struct Staging {
-    void* buf = nullptr;
-    size_t cap = 0;
-    hipEvent_t done = nullptr;
-};
-
-int stage_upload(Staging& sg, void* dst, const void* src, size_t bytes, hipStream_t st) {
-    if (!bytes) return G4_OK;
-    if (!sg.done) G4_CHECK_HIP(hipEventCreateWithFlags(&sg.done, hipEventDisableTiming));
-    G4_CHECK_HIP(hipEventSynchronize(sg.done));
-    if (sg.cap < bytes) {
-        if (sg.buf) G4_CHECK_HIP(hipHostFree(sg.buf));
-        sg.buf = nullptr;
-        sg.cap = 0;
-        G4_CHECK_HIP(hipHostMalloc(&sg.buf, bytes, hipHostMallocDefault));
-        sg.cap = bytes;
-    }
-    memcpy(sg.buf, src, bytes);
-    G4_CHECK_HIP(hipMemcpyAsync(dst, sg.buf, bytes, hipMemcpyHostToDevice, st));
-    G4_CHECK_HIP(hipEventRecord(sg.done, st));
-    return G4_OK;
-}
-
 // The key range of tile `tile`: [lo of its first token, position of its last token].
 void tile_keys(const g4_prefill_entry& e, uint32_t G, uint32_t tile, uint32_t* kb, uint32_t* ke) {
     const uint32_t t0 = tile * (uint32_t)kPfRows / G;
@@ -884,7 +860,7 @@ int build(const g4_prefill_entry* ents, uint32_t n, uint32_t nqh, uint32_t nkh, 
                 w += ke - (dma ? kb & ~(uint32_t)(kPfKeys - 1) : kb);
             }
         }
-        const uint64_t share = w * nkh * (hd / 256) * 115 / (100 * kPfCUs);  // head_dim 512: two halves
+        const uint64_t share = w * nkh * (hd / 256) * 115 / (100 * (uint64_t)device_cus());  // head_dim 512: two halves
         part_keys = (uint32_t)std::min<uint64_t>(std::max<uint64_t>(share, 256), 1u << 30);
         part_keys = (part_keys + kPfKeys - 1) / kPfKeys * kPfKeys;
     }
@@ -1014,14 +990,13 @@ int g4_attn_prefill_prepare(const g4_prefill_entry* entries, uint32_t n_entries,
                             vp.block0[c], 0u};
     if (dma)
         for (uint32_t i = 0; i < n_entries; i++) tab[i].vt = vtc[vp.of[i]].vt;
-    static thread_local Staging s_tab, s_work, s_merge, s_vtc;
-    rc = stage_upload(s_tab, ws + L.table, tab.data(), tab.size() * sizeof(PrefillEntryDev), st);
+    rc = stage_upload(ws + L.table, tab.data(), tab.size() * sizeof(PrefillEntryDev), st);
     if (rc) return rc;
-    rc = stage_upload(s_work, ws + L.work, work.data(), work.size() * sizeof(PrefillWorkDev), st);
+    rc = stage_upload(ws + L.work, work.data(), work.size() * sizeof(PrefillWorkDev), st);
     if (rc) return rc;
-    rc = stage_upload(s_merge, ws + L.merge, merge.data(), merge.size() * sizeof(DecodeEntryDev), st);
+    rc = stage_upload(ws + L.merge, merge.data(), merge.size() * sizeof(DecodeEntryDev), st);
     if (rc) return rc;
-    rc = stage_upload(s_vtc, ws + L.vtc, vtc.data(), vtc.size() * sizeof(VtCacheDev), st);
+    rc = stage_upload(ws + L.vtc, vtc.data(), vtc.size() * sizeof(VtCacheDev), st);
     if (rc) return rc;
     PrefillPlanRep r = {};
     r.ws = ws;

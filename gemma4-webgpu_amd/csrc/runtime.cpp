@@ -5,6 +5,10 @@
 #include <stdarg.h>
 #include <string.h>
 
+#include <map>
+#include <mutex>
+#include <vector>
+
 #include "common.h"
 
 namespace g4 {
@@ -21,6 +25,89 @@ int fail(int code, const char* fmt, ...) {
 
 int hip_fail(hipError_t e, const char* what) {
     return fail(G4_EHIP, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
+}
+
+namespace {
+
+struct StageSlot {
+    void* buf = nullptr;
+    size_t cap = 0;
+    hipEvent_t done = nullptr;  // recorded after the copy that last read buf
+};
+
+// The calling thread's ring. Slots and their pinned buffers live until the
+// thread ends (they are not returned to the runtime, which may already be torn
+// down when thread-local storage is destroyed at process exit).
+struct StageRing {
+    std::vector<StageSlot> slots;
+    size_t next = 0;
+};
+
+StageRing& ring() {
+    static thread_local StageRing* r = new StageRing();
+    return *r;
+}
+
+}  // namespace
+
+int stage_upload(void* dst, const void* src, size_t bytes, hipStream_t st) {
+    if (bytes == 0) return G4_OK;
+    StageRing& R = ring();
+    // A free slot: never used, or its last copy has completed (hipEventQuery
+    // does not wait). Slots are tried from the oldest use on.
+    StageSlot* s = nullptr;
+    const size_t n = R.slots.size();
+    for (size_t i = 0; i < n && !s; i++) {
+        StageSlot& c = R.slots[(R.next + i) % n];
+        const hipError_t q = hipEventQuery(c.done);
+        if (q == hipSuccess) {
+            s = &c;
+            R.next = (R.next + i + 1) % n;
+        } else if (q != hipErrorNotReady) {
+            return hip_fail(q, "stage_upload: hipEventQuery");
+        }
+    }
+    if (!s && n < (size_t)kStageMaxSlots) {
+        StageSlot fresh;
+        G4_CHECK_HIP(hipEventCreateWithFlags(&fresh.done, hipEventDisableTiming));
+        R.slots.insert(R.slots.begin() + R.next, fresh);  // the newest use sits just before `next`
+        s = &R.slots[R.next];
+        R.next = (R.next + 1) % R.slots.size();
+    }
+    if (!s) {  // kStageMaxSlots copies in flight: wait for the oldest
+        s = &R.slots[R.next];
+        R.next = (R.next + 1) % n;
+        G4_CHECK_HIP(hipEventSynchronize(s->done));
+    }
+    if (s->cap < bytes) {
+        if (s->buf) G4_CHECK_HIP(hipHostFree(s->buf));
+        s->buf = nullptr;
+        s->cap = 0;
+        const size_t cap = bytes < 4096 ? 4096 : bytes;
+        G4_CHECK_HIP(hipHostMalloc(&s->buf, cap, hipHostMallocDefault));
+        s->cap = cap;
+    }
+    memcpy(s->buf, src, bytes);
+    G4_CHECK_HIP(hipMemcpyAsync(dst, s->buf, bytes, hipMemcpyHostToDevice, st));
+    G4_CHECK_HIP(hipEventRecord(s->done, st));
+    return G4_OK;
+}
+
+int stage_slots() { return (int)ring().slots.size(); }
+
+unsigned device_cus() {
+    static std::mutex mu;
+    static std::map<int, unsigned> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) dev = -1;
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = cache.find(dev);
+    if (it != cache.end()) return it->second;
+    int cus = 0;
+    if (dev < 0 || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+        cus = 256;  // MI355X
+    cache.emplace(dev, (unsigned)cus);
+    return (unsigned)cus;
 }
 
 }  // namespace g4

@@ -327,7 +327,6 @@ namespace {
 // workgroups fit one wave of the GPU (at most kStepMaxWgs), so at most that
 // many records exist.
 constexpr unsigned kStepMaxWgs = 1024;
-constexpr unsigned kStepCUs = 256;         // MI355X compute units
 constexpr unsigned kStepOneWgTiles = 16;   // one workgroup per CU up to this many tiles each
 constexpr uint32_t kStepMagic = 0x67345354u;
 
@@ -373,30 +372,6 @@ StepLayout step_layout(uint64_t n, uint64_t nkh, uint64_t group, uint64_t hd) {
     off += align256(recs * hd * 4);
     L.total = off;
     return L;
-}
-
-// Pinned host staging for one table upload, reused once its previous copy completed.
-struct Staging {
-    void* buf = nullptr;
-    size_t cap = 0;
-    hipEvent_t done = nullptr;
-};
-
-int stage_upload(Staging& sg, void* dst, const void* src, size_t bytes, hipStream_t st) {
-    if (bytes == 0) return G4_OK;
-    if (!sg.done) G4_CHECK_HIP(hipEventCreateWithFlags(&sg.done, hipEventDisableTiming));
-    G4_CHECK_HIP(hipEventSynchronize(sg.done));
-    if (sg.cap < bytes) {
-        if (sg.buf) G4_CHECK_HIP(hipHostFree(sg.buf));
-        sg.buf = nullptr;
-        sg.cap = 0;
-        G4_CHECK_HIP(hipHostMalloc(&sg.buf, bytes, hipHostMallocDefault));
-        sg.cap = bytes;
-    }
-    memcpy(sg.buf, src, bytes);
-    G4_CHECK_HIP(hipMemcpyAsync(dst, sg.buf, bytes, hipMemcpyHostToDevice, st));
-    G4_CHECK_HIP(hipEventRecord(sg.done, st));
-    return G4_OK;
 }
 
 // Smallest tiles-per-workgroup with sum_e ceil(tiles_e / tpw) <= cap (cap >= n,
@@ -505,13 +480,14 @@ int g4_attn_step_prepare(const g4_step_entry* entries, uint32_t n_entries, uint3
     static const int wgs_per_cu = step_env("G4_STEP_WGS_PER_CU", 0);
     static const int max_wgs = step_env("G4_STEP_MAX_WGS", 0);
     // head_dim 512 has one form: one 4-wave workgroup per CU.
-    const bool small = T <= (uint64_t)kStepOneWgTiles * (kStepCUs / num_kv_heads);
+    const uint64_t cus = device_cus();
+    const bool small = T <= (uint64_t)kStepOneWgTiles * (cus / num_kv_heads);
     const uint32_t waves =
         head_dim == 512 ? 4u : env_waves == 4 || env_waves == 8 ? (uint32_t)env_waves : (small ? 8u : 4u);
     const uint64_t per_cu = head_dim == 512 ? 1u
                             : wgs_per_cu > 0 ? (uint64_t)wgs_per_cu
                                              : (waves == 8 || small ? 1u : 2u);
-    uint64_t fit = max_wgs > 0 ? (uint64_t)max_wgs / num_kv_heads : per_cu * kStepCUs / num_kv_heads;
+    uint64_t fit = max_wgs > 0 ? (uint64_t)max_wgs / num_kv_heads : per_cu * cus / num_kv_heads;
     if (fit > kStepMaxWgs) fit = kStepMaxWgs;
     if (fit < 1) fit = 1;
     const uint64_t cap = fit > n_entries ? fit : n_entries;
@@ -588,14 +564,13 @@ int g4_attn_step_prepare(const g4_step_entry* entries, uint32_t n_entries, uint3
         }
     }
     for (StepWorkDev& w : work) w.ent = tab[w.entry];  // entries complete (parts, RoPE factors)
-    static thread_local Staging sg_work, sg_merge, sg_rope;
-    rc = stage_upload(sg_rope, ws + L.rope, rope.data(), rope.size() * sizeof(float), st);
+    rc = stage_upload(ws + L.rope, rope.data(), rope.size() * sizeof(float), st);
     if (rc) return rc;
-    rc = stage_upload(sg_work, ws + L.work, work.data(), work.size() * sizeof(StepWorkDev), st);
+    rc = stage_upload(ws + L.work, work.data(), work.size() * sizeof(StepWorkDev), st);
     if (rc) return rc;
     const uint32_t n_merge = (uint32_t)merge.size();
     if (n_merge) {
-        rc = stage_upload(sg_merge, ws + L.merge_table, merge.data(), (size_t)n_merge * sizeof(DecodeEntryDev), st);
+        rc = stage_upload(ws + L.merge_table, merge.data(), (size_t)n_merge * sizeof(DecodeEntryDev), st);
         if (rc) return rc;
     }
     StepPlanRep r = {ws,       n_entries, (uint32_t)work.size(), num_kv_heads, G, n_merge, max_parts,

@@ -104,6 +104,17 @@ def test_prefill_gqa_two_kv_heads(dev):
     check(c, "gqa")
 
 
+@pytest.mark.parametrize("nqh,nkh", [(2, 2), (4, 2), (8, 8)])
+def test_prefill_fully_masked_part_small_groups(dev, nqh, nkh):
+    """Query groups of 1 and 2 heads take the general merge. start=200, T=60 cuts the keys into
+    [0, 256) and [256, 260): for positions 200..255 every key of the second part is masked, so
+    that part's record is (m=-inf, l=0, o=0) and must weigh nothing in the merge."""
+    announce(f"attnPrefill fully masked part nqh={nqh} nkh={nkh}")
+    c = Chunk(dev, 70 + nqh + nkh, 200, 60, 0, nqh=nqh, nkh=nkh)
+    plan, _ = run(dev, [c], nqh=nqh, nkh=nkh)
+    check(c, f"masked part G={nqh // nkh}")
+
+
 def test_prefill_replay_identical(dev):
     announce("attnPrefill replay")
     c = Chunk(dev, 13, 2000, 40, 0)
@@ -146,3 +157,40 @@ def test_prefill_head_dim_512_with_256_in_one_process(dev):
     run(dev, [b], hd=512)
     check(a, "hd256")
     check(b, "hd512")
+
+
+@pytest.mark.timeout(900)
+def test_prefill4k_bench_plan(dev):
+    """The exact launch bench.py times for the 4096-token prompt (workloads.prefill4k: a global and a
+    512-window local layer, eight 512-token chunks each, 16 entries in one launch; key parts sized from
+    the whole call's work, longest items first, the merge's few-record form). Checked against the
+    oracle's decode chain: every token of each layer's first and last chunk, every 8th token elsewhere.
+    Local layers are checked over their window's rows (the masked rows weigh exactly 0)."""
+    from g4attn import workloads
+
+    announce("attnPrefill prefill4k bench plan (16 entries, one launch)")
+    layers, entries = workloads.prefill4k(dev, 8, 1, HD)
+    arr = ops.make_prefill_entries(entries, 8, 1, HD)
+    ws = torch.empty(ops.prefill_workspace_bytes(arr, 8, 1, HD), dtype=torch.uint8, device=dev)
+    for _, _, _, out, _ in layers:
+        out.fill_(float("nan"))
+    plan = ops.attn_prefill_prepare(arr, 8, 1, HD, ws)
+    ops.attn_prefill_run(plan)
+    torch.cuda.synchronize()
+    T, C = workloads.PREFILL_T, workloads.PREFILL_CHUNK
+    tokens = sorted(set(range(C)) | set(range(T - C, T)) | set(range(C, T - C, 8)))
+    worst = 0.0
+    for q, kc, vc, out, w in layers:
+        got = out.cpu().numpy().reshape(T, 8 * HD)
+        assert np.isfinite(got).all(), f"window {w}: non-finite output"
+        qf = orc.f16_bits_to_f32(q.cpu().numpy().view(np.uint16)).reshape(T, 8 * HD)
+        kf = orc.f16_bits_to_f32(kc.cpu().numpy().view(np.uint16)).reshape(T, HD)
+        vf = orc.f16_bits_to_f32(vc.cpu().numpy().view(np.uint16)).reshape(T, HD)
+        for t in tokens:
+            lo = t + 1 - w if w and t + 1 > w else 0
+            want = orc.attention_chain(qf[t], kf[lo:t + 1].reshape(-1), vf[lo:t + 1].reshape(-1), 8, 1, HD,
+                                       t + 1 - lo, 1.0, 0)
+            err = max_abs(got[t], want)
+            assert err <= TOL, f"window {w} token {t}: max-abs {err}"
+            worst = max(worst, err)
+        print(f"prefill4k window={w}: {len(tokens)} tokens checked, worst err {worst:.2e}", flush=True)

@@ -304,3 +304,21 @@ def test_step_head_dim_512_layers_and_group4(dev):
     run_step(dev, [L.entry()], nqh=8, nkh=2, hd=512)
     want, kb, vb = L.expected()
     check(L, want, kb, vb, "hd512 group 4")
+
+
+@pytest.mark.timeout(900)
+def test_step_ragged64_bench_set(dev):
+    """The 64 ragged sequences bench.py times (lengths U[1024, 32768] from the same seed; global layers,
+    theta 1e6 with the divisor table, host RoPE tables), all in one plan; every sequence checked."""
+    from g4attn import workloads
+
+    lens = workloads.ragged64_lengths()
+    announce(f"attnStep ragged64 bench set: {len(lens)} sequences, {sum(lens)} rows")
+    layers = [Layer(dev, 9000 + i, L, 0, 1e6, 1) for i, L in enumerate(lens)]
+    run_step(dev, [L.entry(inv_freq=True) for L in layers])
+    worst = 0.0
+    for i, L in enumerate(layers):
+        want, kb, vb = L.expected()
+        worst = max(worst, check(L, want, kb, vb, f"seq {i} len {lens[i]}"))
+        if i % 16 == 15:
+            print(f"ragged64: {i + 1} sequences checked, worst err {worst:.2e}", flush=True)
