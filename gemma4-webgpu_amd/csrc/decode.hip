@@ -16,6 +16,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <map>
+#include <mutex>
 #include <vector>
 
 #include "decode_core.h"
@@ -292,6 +294,40 @@ int launch_decode_merge(const DecodeArgs& a, unsigned n_entries, unsigned max_sp
 
 using namespace g4;
 
+// ---- scratch of the allocation-free decode (g4_attn_decode_noalloc) ----------
+// Split partials of one decode call in a fixed device array instead of a
+// caller's workspace: records (m, l) and o for up to kNoAllocSplits splits of
+// up to kNoAllocHeads query heads at head_dim up to 512. Each GPU the library
+// runs on holds its own copy until the process ends.
+constexpr unsigned kNoAllocSplits = 512;
+constexpr unsigned kNoAllocHeads = 8;
+constexpr size_t kNoAllocMlBytes = (size_t)kNoAllocSplits * kNoAllocHeads * 2 * sizeof(float);  // 32 KiB
+constexpr size_t kNoAllocBytes = kNoAllocMlBytes + (size_t)kNoAllocSplits * kNoAllocHeads * 512 * sizeof(float);
+static __device__ __align__(256) unsigned char scratch[kNoAllocBytes];
+
+namespace {
+
+// The device address of `scratch` on the current device, looked up once per
+// device with that device current (the host-side name is not a device address).
+int noalloc_scratch(char** out) {
+    static std::mutex mu;
+    static std::map<int, char*> addr;
+    int dev = 0;
+    G4_CHECK_HIP(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = addr.find(dev);
+    if (it == addr.end()) {
+        void* p = nullptr;
+        G4_CHECK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (!p) return fail(G4_EHIP, "attnDecodeNoAlloc: no device address for the scratch array");
+        it = addr.emplace(dev, static_cast<char*>(p)).first;
+    }
+    *out = it->second;
+    return G4_OK;
+}
+
+}  // namespace
+
 namespace {
 
 int env_int(const char* name, int dflt) {
@@ -403,6 +439,43 @@ int g4_attn_decode(const float* q, const uint16_t* k_cache, const uint16_t* v_ca
         a.part_ml = static_cast<float*>(workspace);
         a.part_o = reinterpret_cast<float*>(static_cast<char*>(workspace) +
                                             align256((size_t)ns * p.num_kv_heads * group * 2 * sizeof(float)));
+    }
+    return launch(a, ns, 1, ns, p.head_dim, as_stream(stream));
+}
+
+int g4_attn_decode_noalloc(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, float* out,
+                           g4_attn_score_params p, void* stream) {
+    int rc = check_shape("attnDecodeNoAlloc", p.num_q_heads, p.num_kv_heads, p.head_dim);
+    if (rc) return rc;
+    if (p.num_q_heads > kNoAllocHeads)
+        return fail(G4_EINVAL, "attnDecodeNoAlloc: %u query heads (the scratch array holds at most %u)", p.num_q_heads,
+                    kNoAllocHeads);
+    if (!q || !k_cache || !v_cache || !out) return fail(G4_EINVAL, "attnDecodeNoAlloc: NULL pointer");
+    if (reinterpret_cast<uintptr_t>(out) & 15) return fail(G4_EINVAL, "attnDecodeNoAlloc: out must be 16-byte aligned");
+    if (p.seq_len == 0) return fail(G4_EINVAL, "attnDecodeNoAlloc: seq_len 0");
+    uint32_t kb, ke;
+    attended_range(p.seq_len, p.sliding_window, &kb, &ke);
+    // g4_attn_decode's split size, raised where needed so that the splits fit the scratch array.
+    unsigned chunk = pick_chunk(ke - kb, ke - kb, p.num_kv_heads, p.head_dim);
+    const unsigned min_chunk = round_up((ke - kb + kNoAllocSplits - 1) / kNoAllocSplits, kTileKeys);
+    if (chunk < min_chunk) chunk = min_chunk;
+    const unsigned ns = (ke - kb + chunk - 1) / chunk;
+    const uint32_t group = p.num_q_heads / p.num_kv_heads;
+    if ((size_t)ns * p.num_q_heads > (size_t)kNoAllocSplits * kNoAllocHeads)
+        return fail(G4_EINVAL, "attnDecodeNoAlloc: %u splits of %u heads exceed the scratch array", ns, p.num_q_heads);
+    DecodeArgs a = {};
+    a.table = nullptr;
+    a.one = DecodeEntryDev{q, k_cache, v_cache, out, kb, ke, 0, ns, p.scale * kLog2e, 0};
+    a.n_entries = 1;
+    a.num_kv_heads = p.num_kv_heads;
+    a.group = group;
+    a.chunk = chunk;
+    if (ns > 1) {
+        char* base = nullptr;
+        rc = noalloc_scratch(&base);
+        if (rc) return rc;
+        a.part_ml = reinterpret_cast<float*>(base);
+        a.part_o = reinterpret_cast<float*>(base + kNoAllocMlBytes);
     }
     return launch(a, ns, 1, ns, p.head_dim, as_stream(stream));
 }

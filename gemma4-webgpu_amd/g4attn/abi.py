@@ -147,6 +147,7 @@ SIGNATURES: dict[str, list] = {
     "g4_attn_prep_many": [_P, _U32, _U32, _U32, C.c_float, _U32, _U32, _P],
     "g4_attn_decode_workspace_size": [_U32, _U32, _U32, _U32, C.POINTER(C.c_size_t)],
     "g4_attn_decode": [_P, _P, _P, _P, AttnScoreParams, _P, _SZ, _P],
+    "g4_attn_decode_noalloc": [_P, _P, _P, _P, AttnScoreParams, _P],
     "g4_attn_decode_many_workspace_size": [_U32, _U32, _U32, _U32, C.c_uint64, C.POINTER(C.c_size_t)],
     "g4_attn_decode_many_prepare": [C.POINTER(DecodeEntry), _U32, _U32, _U32, _U32, _P, _SZ,
                                     C.POINTER(DecodePlan), _P],

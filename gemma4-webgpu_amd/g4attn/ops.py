@@ -170,6 +170,15 @@ def attn_decode(q, k_cache, v_cache, out, workspace, num_q_heads, num_kv_heads, 
              _stream(stream))
 
 
+def attn_decode_noalloc(q, k_cache, v_cache, out, num_q_heads, num_kv_heads, head_dim, seq_len, scale=1.0,
+                        sliding_window=0, stream=None):
+    """attn_decode without a workspace: the split partials use the library's fixed scratch array."""
+    p = AttnScoreParams(num_q_heads, num_kv_heads, head_dim, seq_len, scale, sliding_window)
+    rows = seq_len * num_kv_heads * head_dim
+    abi.call("g4_attn_decode_noalloc", _f32(q, "q", num_q_heads * head_dim), _f16(k_cache, "k_cache", rows),
+             _f16(v_cache, "v_cache", rows), _f32(out, "out", num_q_heads * head_dim), p, _stream(stream))
+
+
 def decode_many_workspace_bytes(n_entries, num_q_heads, num_kv_heads, head_dim, total_rows) -> int:
     n = C.c_size_t(0)
     abi.call("g4_attn_decode_many_workspace_size", n_entries, num_q_heads, num_kv_heads, head_dim, total_rows,

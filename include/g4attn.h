@@ -229,6 +229,19 @@ int g4_attn_decode_workspace_size(uint32_t num_q_heads, uint32_t num_kv_heads, u
 int g4_attn_decode(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, float* out,
                    g4_attn_score_params p, void* workspace, size_t workspace_bytes, void* stream);
 
+/* The same decode with no workspace argument and no allocation (no hipMalloc,
+ * hipFree or allocating library call), for callers that cannot allocate:
+ * code under HIP graph capture, tight serving loops. No counterpart in the
+ * reference. The split partials live in a fixed device array of the library
+ * (8.03 MiB per GPU, held until the process ends): num_q_heads <= 8, and at
+ * most 512 splits (the split size grows for longer ranges). Every call on a
+ * GPU uses that GPU's one array, so calls that overlap on one GPU (on
+ * different streams, or from different threads) race; calls ordered on one
+ * stream do not. Same results as g4_attn_decode where both pick the same
+ * split size. */
+int g4_attn_decode_noalloc(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, float* out,
+                           g4_attn_score_params p, void* stream);
+
 /* ---- many independent decode problems in one launch ------------------- *
  * Each entry is one (query block, KV cache, length) problem: the layers of
  * one token's attention stack when their queries are available together, or
