@@ -54,7 +54,11 @@ def _run(cmd: list[str]) -> None:
 # pipelined prefill rescales them with plain VALU; its q operand is kept in AGPRs),
 # and IEEE mode off with NaN-free math, so that max over scores is one v_max each
 # instead of canonicalize + max (scores are finite or -inf; no NaN is produced).
-FILE_FLAGS = {"prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mno-amdgpu-ieee", "-fno-honor-nans"]}
+# step.hip, decode.hip: kernel arguments (scalars and pointers) preloaded into
+# SGPRs at wave start, so a workgroup's first scalar load is its work item.
+FILE_FLAGS = {"prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mno-amdgpu-ieee", "-fno-honor-nans"],
+              "step.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"],
+              "decode.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"]}
 
 
 def _compile(src: Path) -> Path:

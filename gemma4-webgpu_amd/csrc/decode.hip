@@ -126,11 +126,34 @@ constexpr int kMergeBatch = 8;
 constexpr int kMaxMergeSplits = 8192;
 constexpr unsigned kMaxMergeChunks = 16;
 
+// The merge kernels take scalars and pointers (preloaded into SGPRs at wave
+// start; decode.hip is compiled with kernarg preloading): the entry is then
+// one batch of scalar loads from the table, or the single entry's fields
+// passed by value when there is no table.
+
+__device__ __forceinline__ DecodeEntryDev merge_entry(const DecodeEntryDev* table, float* one_out,
+                                                      uint32_t one_split_base, uint32_t one_splits) {
+    if (table) return table[blockIdx.x];
+    DecodeEntryDev e{};
+    e.out = one_out;
+    e.split_base = one_split_base;
+    e.n_splits = one_splits;
+    return e;
+}
+
 template <int HD>
-__global__ __launch_bounds__(kMergeThreads) void k_decode_merge(DecodeArgs a, unsigned n_chunks) {
+__global__ __launch_bounds__(kMergeThreads) void k_decode_merge(const DecodeEntryDev* __restrict__ table, float* one_out,
+                                                                uint32_t one_split_base, uint32_t one_splits,
+                                                                float* part_ml, float* part_o, uint32_t num_kv_heads,
+                                                                uint32_t group, uint32_t n_chunks) {
     __shared__ f32x4 part[kMergeThreads];
     __shared__ float gm[kMergeThreads], gl[kMergeThreads];  // per group: running max, rescaled l
-    const DecodeEntryDev ent = a.table ? a.table[blockIdx.x] : a.one;
+    const DecodeEntryDev ent = merge_entry(table, one_out, one_split_base, one_splits);
+    DecodeArgs a{};
+    a.num_kv_heads = num_kv_heads;
+    a.group = group;
+    a.part_ml = part_ml;
+    a.part_o = part_o;
     const unsigned ns = ent.n_splits;
     if (ns <= 1) return;
     const unsigned G = a.group;
@@ -207,9 +230,18 @@ constexpr unsigned kSmallMergeSplits = 8;
 // NS: the launch's largest split count rounded up to 2, 4 or 8 (records past an entry's own count
 // are not loaded).
 template <int HD, int COLS, int NS>
-__global__ __launch_bounds__(kMergeThreads) void k_decode_merge_small(DecodeArgs a) {
+__global__ __launch_bounds__(kMergeThreads) void k_decode_merge_small(const DecodeEntryDev* __restrict__ table,
+                                                                      float* one_out, uint32_t one_split_base,
+                                                                      uint32_t one_splits, float* part_ml,
+                                                                      float* part_o, uint32_t num_kv_heads,
+                                                                      uint32_t group) {
     constexpr unsigned TPH = HD / COLS;  // threads per query head
-    const DecodeEntryDev ent = a.table ? a.table[blockIdx.x] : a.one;
+    const DecodeEntryDev ent = merge_entry(table, one_out, one_split_base, one_splits);
+    DecodeArgs a{};
+    a.num_kv_heads = num_kv_heads;
+    a.group = group;
+    a.part_ml = part_ml;
+    a.part_o = part_o;
     const unsigned ns = ent.n_splits;
     if (ns <= 1) return;
     const unsigned G = a.group, kvh = blockIdx.y;
@@ -246,6 +278,9 @@ __global__ __launch_bounds__(kMergeThreads) void k_decode_merge_small(DecodeArgs
     for (int c = 0; c < COLS / 4; c++) stg<f32x4>(out + 4 * c, acc[c] / L);
 }
 
+#define MERGE_KARGS                                                                                               \
+    a.table, a.one.out, a.one.split_base, a.one.n_splits, a.part_ml, a.part_o, a.num_kv_heads, a.group
+
 template <int HD>
 int launch_decode_merge_hd(const DecodeArgs& a, unsigned n_entries, unsigned max_splits, hipStream_t st) {
     if (max_splits <= kSmallMergeSplits && (a.group == 8 || a.group == 4)) {
@@ -254,19 +289,19 @@ int launch_decode_merge_hd(const DecodeArgs& a, unsigned n_entries, unsigned max
         if (a.group == 8) {
             constexpr int C = HD * 8 / 256;
             if (max_splits <= 2)
-                hipLaunchKernelGGL((k_decode_merge_small<HD, C, 2>), grid, block, 0, st, a);
+                hipLaunchKernelGGL((k_decode_merge_small<HD, C, 2>), grid, block, 0, st, MERGE_KARGS);
             else if (max_splits <= 4)
-                hipLaunchKernelGGL((k_decode_merge_small<HD, C, 4>), grid, block, 0, st, a);
+                hipLaunchKernelGGL((k_decode_merge_small<HD, C, 4>), grid, block, 0, st, MERGE_KARGS);
             else
-                hipLaunchKernelGGL((k_decode_merge_small<HD, C, 8>), grid, block, 0, st, a);
+                hipLaunchKernelGGL((k_decode_merge_small<HD, C, 8>), grid, block, 0, st, MERGE_KARGS);
         } else {
             constexpr int C = HD * 4 / 256;
             if (max_splits <= 2)
-                hipLaunchKernelGGL((k_decode_merge_small<HD, C, 2>), grid, block, 0, st, a);
+                hipLaunchKernelGGL((k_decode_merge_small<HD, C, 2>), grid, block, 0, st, MERGE_KARGS);
             else if (max_splits <= 4)
-                hipLaunchKernelGGL((k_decode_merge_small<HD, C, 4>), grid, block, 0, st, a);
+                hipLaunchKernelGGL((k_decode_merge_small<HD, C, 4>), grid, block, 0, st, MERGE_KARGS);
             else
-                hipLaunchKernelGGL((k_decode_merge_small<HD, C, 8>), grid, block, 0, st, a);
+                hipLaunchKernelGGL((k_decode_merge_small<HD, C, 8>), grid, block, 0, st, MERGE_KARGS);
         }
         G4_CHECK_LAUNCH("attnDecode merge");
         return G4_OK;
@@ -278,10 +313,12 @@ int launch_decode_merge_hd(const DecodeArgs& a, unsigned n_entries, unsigned max
     unsigned chunks = 1;
     while (chunks < kMaxMergeChunks && max_splits > kRecsPerChunk * chunks) chunks *= 2;
     hipLaunchKernelGGL(k_decode_merge<HD>, dim3(n_entries, a.num_kv_heads * a.group, chunks), dim3(kMergeThreads), 0,
-                       st, a, chunks);
+                       st, MERGE_KARGS, chunks);
     G4_CHECK_LAUNCH("attnDecode merge");
     return G4_OK;
 }
+
+#undef MERGE_KARGS
 
 int launch_decode_merge(const DecodeArgs& a, unsigned n_entries, unsigned max_splits, hipStream_t st,
                         unsigned head_dim) {

@@ -184,25 +184,32 @@ __device__ __forceinline__ void override_row(unsigned last, int n, int g, unsign
         }
 }
 
-// Consumes one 32-row tile (already in registers) into a wave's online-softmax
-// state: running max m (log2 units) and sum l of its column, and the O^T
-// accumulators. Rows at or beyond `k1` are masked (probability 0, as
-// exp(-1e30 - max) == 0 in the reference); their loads were clamped in range.
-// (The state is passed as separate references: wrapped in a struct it is not
-// kept in registers and spills.)
+// The score half of a tile: S^T of the tile's 32 rows for the 16 operand
+// columns (two 16-row halves), from K in registers and q in LDS. After this
+// the K registers are free (the next tile's K can be requested into them).
 template <int HD, int W>
-__device__ __forceinline__ void tile_step(const DecodeSmem<HD, W>& sm, int lane, int g, bool lo_col, unsigned kt0,
-                                          unsigned k1, const f16x8 (&kreg)[2][DecodeDims<HD>::NC],
-                                          const u32x4 (&vreg)[DecodeDims<HD>::NB][8], float& m_run, float& l_run,
-                                          f32x4 (&acc)[DecodeDims<HD>::NO]) {
-    constexpr int NC = DecodeDims<HD>::NC, NB = DecodeDims<HD>::NB, NO = DecodeDims<HD>::NO;
-    f32x4 s[2];
+__device__ __forceinline__ void tile_scores(const DecodeSmem<HD, W>& sm, int lane,
+                                            const f16x8 (&kreg)[2][DecodeDims<HD>::NC], f32x4 (&s)[2]) {
+    constexpr int NC = DecodeDims<HD>::NC;
 #pragma unroll
     for (int h2 = 0; h2 < 2; h2++) {
         s[h2] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int c = 0; c < NC; c++) s[h2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kreg[h2][c], sm.q[c][lane], s[h2], 0, 0, 0);
     }
+}
+
+// The rest of a tile: online softmax of the scores into a wave's state
+// (running max m (log2 units) and sum l of its column) and the O^T
+// accumulators, from V in registers. Rows at or beyond `k1` are masked
+// (probability 0, as exp(-1e30 - max) == 0 in the reference); their loads
+// were clamped in range. (The state is passed as separate references: wrapped
+// in a struct it is not kept in registers and spills.)
+template <int HD>
+__device__ __forceinline__ void tile_update(const f32x4 (&s)[2], int g, bool lo_col, unsigned kt0, unsigned k1,
+                                            const u32x4 (&vreg)[DecodeDims<HD>::NB][8], float& m_run, float& l_run,
+                                            f32x4 (&acc)[DecodeDims<HD>::NO]) {
+    constexpr int NB = DecodeDims<HD>::NB, NO = DecodeDims<HD>::NO;
     float sv[8];
     float tmax = -INFINITY;
 #pragma unroll
@@ -251,6 +258,17 @@ __device__ __forceinline__ void tile_step(const DecodeSmem<HD, W>& sm, int lane,
                 __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, hi), pop, acc[b * 8 + 2 * e2 + 1], 0, 0, 0);
         }
     }
+}
+
+// Consumes one 32-row tile (already in registers) into a wave's online-softmax state.
+template <int HD, int W>
+__device__ __forceinline__ void tile_step(const DecodeSmem<HD, W>& sm, int lane, int g, bool lo_col, unsigned kt0,
+                                          unsigned k1, const f16x8 (&kreg)[2][DecodeDims<HD>::NC],
+                                          const u32x4 (&vreg)[DecodeDims<HD>::NB][8], float& m_run, float& l_run,
+                                          f32x4 (&acc)[DecodeDims<HD>::NO]) {
+    f32x4 s[2];
+    tile_scores<HD>(sm, lane, kreg, s);
+    tile_update<HD>(s, g, lo_col, kt0, k1, vreg, m_run, l_run, acc);
 }
 
 // Publishes a wave's final state to workgroup memory (sums over the 4 lane

@@ -152,8 +152,17 @@ struct StepSmem {
 // the HBM latency with one 32-row tile per wave. head_dim 512: one 4-wave
 // workgroup per CU at one wave per SIMD (a 32-row tile is 64 KB of K and V,
 // the accumulators take 128 registers more).
+//
+// The arguments are scalars and pointers (not one struct) so that they are
+// preloaded into SGPRs at wave start (the file is compiled with kernarg
+// preloading), and the work item is copied by value: its fields arrive in one
+// batch of scalar loads. Reading fields where used, or selecting a field's
+// address by a value loaded before, chains dependent scalar loads (measured:
+// six round trips, ~4.6 us before a workgroup's first vector load).
 template <int W, int HD>
-__global__ __launch_bounds__(64 * W, HD == 256 ? 8 / W : 1) void k_attn_step(StepArgs a) {
+__global__ __launch_bounds__(64 * W, HD == 256 ? 8 / W : 1) void k_attn_step(
+    const StepWorkDev* __restrict__ work, float* part_ml, float* part_o, uint32_t num_kv_heads, uint32_t group) {
+    const StepArgs a{work, num_kv_heads, group, part_ml, part_o};
     using D = DecodeDims<HD>;
     constexpr int J = HD / 64;                          // elements of a head per lane
     constexpr int PJ = J / 2;                           // RoPE pairs per lane
@@ -168,7 +177,7 @@ __global__ __launch_bounds__(64 * W, HD == 256 ? 8 / W : 1) void k_attn_step(Ste
     const int g = lane >> 4;
     const bool lo_col = n >= 8;
 
-    const StepWorkDev& wk = a.work[blockIdx.x];  // fields read where used (scalar loads)
+    const StepWorkDev wk = work[blockIdx.x];
     const StepEntryDev& ent = wk.ent;
     const unsigned key_end = ent.key_end;
     const unsigned k0 = wk.row_begin;
@@ -601,14 +610,20 @@ static int launch_attention(const g4_decode_plan* plan, void* stream, hipEvent_t
     const dim3 grid(r.n_wgs, r.num_kv_heads);
     hipStream_t st = as_stream(stream);
     if (r.head_dim == 512) {
-        if (start || stop) hipExtLaunchKernelGGL((k_attn_step<4, 512>), grid, dim3(256), 0, st, start, stop, 0, a);
-        else hipLaunchKernelGGL((k_attn_step<4, 512>), grid, dim3(256), 0, st, a);
+        if (start || stop) hipExtLaunchKernelGGL((k_attn_step<4, 512>), grid, dim3(256), 0, st, start, stop, 0, a.work, a.part_ml, a.part_o,
+                                  a.num_kv_heads, a.group);
+        else hipLaunchKernelGGL((k_attn_step<4, 512>), grid, dim3(256), 0, st, a.work, a.part_ml, a.part_o, a.num_kv_heads,
+                               a.group);
     } else if (r.waves == 8) {
-        if (start || stop) hipExtLaunchKernelGGL((k_attn_step<8, 256>), grid, dim3(512), 0, st, start, stop, 0, a);
-        else hipLaunchKernelGGL((k_attn_step<8, 256>), grid, dim3(512), 0, st, a);
+        if (start || stop) hipExtLaunchKernelGGL((k_attn_step<8, 256>), grid, dim3(512), 0, st, start, stop, 0, a.work, a.part_ml, a.part_o,
+                                  a.num_kv_heads, a.group);
+        else hipLaunchKernelGGL((k_attn_step<8, 256>), grid, dim3(512), 0, st, a.work, a.part_ml, a.part_o, a.num_kv_heads,
+                               a.group);
     } else {
-        if (start || stop) hipExtLaunchKernelGGL((k_attn_step<4, 256>), grid, dim3(256), 0, st, start, stop, 0, a);
-        else hipLaunchKernelGGL((k_attn_step<4, 256>), grid, dim3(256), 0, st, a);
+        if (start || stop) hipExtLaunchKernelGGL((k_attn_step<4, 256>), grid, dim3(256), 0, st, start, stop, 0, a.work, a.part_ml, a.part_o,
+                                  a.num_kv_heads, a.group);
+        else hipLaunchKernelGGL((k_attn_step<4, 256>), grid, dim3(256), 0, st, a.work, a.part_ml, a.part_o, a.num_kv_heads,
+                               a.group);
     }
     G4_CHECK_LAUNCH("attnStep");
     return G4_OK;

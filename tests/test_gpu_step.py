@@ -322,3 +322,32 @@ def test_step_ragged64_bench_set(dev):
         worst = max(worst, check(L, want, kb, vb, f"seq {i} len {lens[i]}"))
         if i % 16 == 15:
             print(f"ragged64: {i + 1} sequences checked, worst err {worst:.2e}", flush=True)
+
+
+@pytest.mark.parametrize("seq,win", [(33, 0), (300, 0), (513, 512), (1000, 512), (1500, 0), (2049, 0), (4000, 0)])
+def test_step_single_entry_replays(dev, seq, win):
+    """A small single-entry step (the engine's layer-by-layer order), cut into a few parts and merged.
+    Replayed three times: every replay gives the same bits."""
+    announce(f"attnStep few parts seq={seq} win={win}")
+    L = Layer(dev, 1300 + seq, seq, win, 1e4 if win else 1e6, 0 if win else 1)
+    want, kb, vb = L.expected()
+    plan, ws = run_step(dev, [L.entry(inv_freq=True)])
+    check(L, want, kb, vb, f"seq={seq}")
+    first = L.out.cpu().numpy().copy()
+    for rep in range(3):
+        L.out.fill_(float("nan"))
+        ops.attn_step_run(plan)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(L.out.cpu().numpy().view(np.uint32), first.view(np.uint32),
+                                      err_msg=f"replay {rep}")
+
+
+def test_step_mixed_part_counts(dev):
+    """Entries of few parts, of many parts and whole entries in one step, run twice on one plan."""
+    announce("attnStep mixed part counts")
+    specs = [(8193, 0), (513, 512), (40, 0), (2000, 0), (700, 512), (20000, 0), (3, 0), (1025, 0)]
+    layers = [Layer(dev, 1400 + i, s, w, 1e4 if w else 1e6, 0 if w else 1) for i, (s, w) in enumerate(specs)]
+    wants = [L.expected() for L in layers]
+    plan, ws = run_step(dev, [L.entry(inv_freq=i % 2 == 0) for i, L in enumerate(layers)], plan_runs=2)
+    for i, (L, (want, kb, vb)) in enumerate(zip(layers, wants)):
+        check(L, want, kb, vb, f"entry {i}")
