@@ -930,6 +930,31 @@ napi_value AttnPrefillRun(napi_env env, napi_callback_info info) {
     return undefined(env);
 }
 
+// ---- chunked prompt prep -------------------------------------------------------
+
+// attnPromptPrep(q, k, v, qWeight, kWeight, ropeFreqs, qOut, kCache, vCache, params (g4_prompt_prep_params
+// bytes), stream); k, v, kWeight, kCache, vCache null on KV-consumer layers.
+napi_value AttnPromptPrep(napi_env env, napi_callback_info info) {
+    Args a(env, info, 11);
+    void* q = a.ptr(0);
+    void* k = a.ptr(1);
+    void* v = a.ptr(2);
+    void* qw = a.ptr(3);
+    void* kw = a.ptr(4);
+    void* rf = a.ptr(5);
+    void* qo = a.ptr(6);
+    void* kc = a.ptr(7);
+    void* vc = a.ptr(8);
+    g4_prompt_prep_params p;
+    a.params(9, &p);
+    void* s = a.ptr(10);
+    if (!a.ok) return nullptr;
+    CALL(env, g4_attn_prompt_prep((const float*)q, (const float*)k, (const float*)v, (const uint16_t*)qw,
+                                  (const uint16_t*)kw, (const uint16_t*)rf, (uint16_t*)qo, (uint16_t*)kc,
+                                  (uint16_t*)vc, p, s));
+    return undefined(env);
+}
+
 napi_value Init(napi_env env, napi_value exports) {
     struct {
         const char* name;
@@ -970,6 +995,7 @@ napi_value Init(napi_env env, napi_value exports) {
         {"attnPrefillWorkspaceSize", AttnPrefillWorkspaceSize},
         {"attnPrefillPrepare", AttnPrefillPrepare},
         {"attnPrefillRun", AttnPrefillRun},
+        {"attnPromptPrep", AttnPromptPrep},
     };
     for (auto& f : fns) {
         napi_value fn;

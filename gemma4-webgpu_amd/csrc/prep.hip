@@ -64,6 +64,69 @@ __global__ __launch_bounds__(kWG) void k_attn_prep_many(const g4_prep_layer* __r
     }
 }
 
+// Chunked prompt prep: the producer-side prep of every token of a prompt
+// chunk in one launch. The engine runs vNorm -> fusedNormRope(Q, K) ->
+// kvCacheStore once per prompt token (src/engine.ts:2460-2479, each token
+// through 2056-2091). One workgroup per token: its threads first evaluate the
+// token's RoPE factors once (cos and sin of the f32 angle of every pair, in
+// f64 as the reference does) into LDS, then its four waves take the token's
+// head slots in turn: slots 0 .. NQH-1 are the query heads (norm + RoPE,
+// written as f16: the query operand g4_attn_prefill takes), then NKH key
+// heads (norm + RoPE, stored as cache row start + t), then NKH value heads
+// (weightless norm, stored). The per-head arithmetic is wave_norm_rope (the
+// reference's 256 partials and 128 -> 1 tree), so every stored value is the
+// f16 rounding of what the reference kernels compute token by token.
+template <int HD>
+__global__ __launch_bounds__(kWG) void k_prompt_prep(const float* __restrict__ q, const float* __restrict__ k,
+                                                     const float* __restrict__ v,
+                                                     const uint16_t* __restrict__ q_weight,
+                                                     const uint16_t* __restrict__ k_weight,
+                                                     const uint16_t* __restrict__ rope_freqs,
+                                                     uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_cache,
+                                                     uint16_t* __restrict__ v_cache, g4_prompt_prep_params p) {
+    constexpr int J = HD / 64, PJ = J / 2;
+    static_assert(HD / 2 <= kWG, "one thread per RoPE pair");
+    __shared__ float rc[HD / 2], rs[HD / 2];
+    const unsigned t = blockIdx.x;
+    const unsigned pos = p.start + t;
+    if (threadIdx.x < HD / 2) {
+        const float ang = rope_angle(threadIdx.x, HD, p.theta, pos, p.apply_divisor, rope_freqs);
+        rc[threadIdx.x] = (float)cos((double)ang);
+        rs[threadIdx.x] = (float)sin((double)ang);
+    }
+    __syncthreads();
+    const unsigned lane = threadIdx.x & 63;
+    const unsigned wave = threadIdx.x >> 6;
+    RopeLane<PJ> rl;
+#pragma unroll
+    for (int pp = 0; pp < PJ; pp++) {
+        rl.c[pp] = rc[lane + 64 * pp];
+        rl.s[pp] = rs[lane + 64 * pp];
+    }
+    const unsigned S = p.num_q_heads + (p.store_kv ? 2 * p.num_kv_heads : 0);
+    for (unsigned slot = wave; slot < S; slot += kWG / 64) {  // uniform per wave
+        const bool is_q = slot < p.num_q_heads;
+        const unsigned r = slot - p.num_q_heads;
+        const bool is_k = !is_q && r < p.num_kv_heads;
+        const bool rope = is_q || is_k;  // v: weightless norm only
+        const unsigned h = is_q ? slot : (is_k ? r : r - p.num_kv_heads);
+        const float* src = is_q ? q + ((uint64_t)t * p.num_q_heads + h) * HD
+                                : (is_k ? k : v) + ((uint64_t)t * p.num_kv_heads + h) * HD;
+        float x[J];
+        uint32_t wb[J];
+#pragma unroll
+        for (int j = 0; j < J; j++) {
+            x[j] = src[lane + 64 * j];
+            wb[j] = rope ? (is_q ? q_weight : k_weight)[lane + 64 * j] : 0u;
+        }
+        wave_norm_rope<J>(x, wb, rope, rope, rl, p.eps);
+        uint16_t* dst = is_q ? q_out + ((uint64_t)t * p.num_q_heads + h) * HD
+                             : (is_k ? k_cache : v_cache) + ((uint64_t)pos * p.num_kv_heads + h) * HD;
+#pragma unroll
+        for (int j = 0; j < J; j++) dst[lane + 64 * j] = f2h(x[j]);
+    }
+}
+
 }  // namespace g4
 
 using namespace g4;
@@ -98,6 +161,35 @@ extern "C" int g4_attn_prep(float* q, float* k, float* v, const uint16_t* q_weig
     hipLaunchKernelGGL(k_attn_prep, dim3(blocks), dim3(kWG), 0, as_stream(stream), q, k, v, q_weight, k_weight,
                        rope_freqs, k_cache, v_cache, p);
     G4_CHECK_LAUNCH("attnPrep");
+    return G4_OK;
+}
+
+extern "C" int g4_attn_prompt_prep(const float* q, const float* k, const float* v, const uint16_t* q_weight,
+                                   const uint16_t* k_weight, const uint16_t* rope_freqs, uint16_t* q_out,
+                                   uint16_t* k_cache, uint16_t* v_cache, g4_prompt_prep_params p, void* stream) {
+    if (p.head_dim != 256 && p.head_dim != 512)
+        return fail(G4_EINVAL, "attnPromptPrep: head_dim %u unsupported (256 or 512)", p.head_dim);
+    if (p.num_q_heads == 0 || p.num_kv_heads == 0) return fail(G4_EINVAL, "attnPromptPrep: no heads");
+    if (!q || !q_weight || !q_out) return fail(G4_EINVAL, "attnPromptPrep: NULL q/q_weight/q_out");
+    if (p.apply_divisor && !rope_freqs) return fail(G4_EINVAL, "attnPromptPrep: apply_divisor needs rope_freqs");
+    if (p.store_kv) {
+        if (!k || !v || !k_weight || !k_cache || !v_cache)
+            return fail(G4_EINVAL, "attnPromptPrep: store_kv with NULL k/v/k_weight/caches");
+        if ((uint64_t)p.start + p.n_tokens > p.max_seq_len)
+            return fail(G4_EINVAL, "attnPromptPrep: rows %u..%u past max_seq_len %u", p.start,
+                        p.start + p.n_tokens - 1, p.max_seq_len);
+    }
+    if ((uint64_t)p.start + p.n_tokens > 0xffffffffull) return fail(G4_EINVAL, "attnPromptPrep: position range");
+    if (p.n_tokens == 0) return G4_OK;
+    if (p.n_tokens > 0x7fffffffu) return fail(G4_EINVAL, "attnPromptPrep: too many tokens");
+    hipStream_t st = as_stream(stream);
+    if (p.head_dim == 512)
+        hipLaunchKernelGGL(k_prompt_prep<512>, dim3(p.n_tokens), dim3(kWG), 0, st, q, k, v, q_weight, k_weight,
+                           rope_freqs, q_out, k_cache, v_cache, p);
+    else
+        hipLaunchKernelGGL(k_prompt_prep<256>, dim3(p.n_tokens), dim3(kWG), 0, st, q, k, v, q_weight, k_weight,
+                           rope_freqs, q_out, k_cache, v_cache, p);
+    G4_CHECK_LAUNCH("attnPromptPrep");
     return G4_OK;
 }
 

@@ -172,4 +172,47 @@ __device__ __forceinline__ void head_norm_rope(float* __restrict__ data, const u
 // Workgroup scratch for head_norm_rope with head_dim <= 512.
 constexpr unsigned kNormScratch = 257 + 2 * kWG;
 
+// RoPE factors of pairs (l + 64p, l + 64p + HD/2), p = 0 .. HD/128 - 1, for lane l.
+template <int PJ>
+struct RopeLane {
+    float c[PJ], s[PJ];
+};
+
+// Per-head RMSNorm (+ RoPE) of one HD-wide head by one wave; lane l holds
+// x[l + 64j], j = 0 .. HD/64 - 1 (and the weight's f16 bits at the same
+// places), and receives the results in place. The sum of squares adds the
+// same terms in the same order as the reference's workgroup: partial t
+// (= l + 64q, q = 0..3) sums x[t]^2, x[t + 256]^2, ... in order, then the
+// tree with strides 128, 64 (in the lane) and 32..1 (across lanes), so every
+// value is bit-identical to fused_per_head_norm_rope.wgsl /
+// per_head_rms_norm_no_weight.wgsl.
+template <int J>
+__device__ __forceinline__ void wave_norm_rope(float (&x)[J], const uint32_t (&wbits)[J], bool weighted, bool rope,
+                                               const RopeLane<J / 2>& r, float eps) {
+#pragma clang fp contract(off)
+    constexpr int HD = 64 * J, PJ = J / 2;
+    float part[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        part[q] = x[q] * x[q];
+#pragma unroll
+        for (int m = 1; m < J / 4; m++) part[q] = part[q] + x[q + 4 * m] * x[q + 4 * m];
+    }
+    const float a = part[0] + part[2];  // t = lane      : s[t] + s[t + 128]
+    const float b = part[1] + part[3];  // t = lane + 64 : s[t] + s[t + 128]
+    float c = a + b;                    // stride 64
+    for (int stride = 32; stride > 0; stride >>= 1) c = c + __shfl_down(c, stride);
+    const float total = __shfl(c, 0);
+    const float rms = sqrtf(total / (float)HD + eps);
+#pragma unroll
+    for (int j = 0; j < J; j++) x[j] = weighted ? x[j] * h2f((uint16_t)wbits[j]) / rms : x[j] / rms;
+    if (!rope) return;
+#pragma unroll
+    for (int p = 0; p < PJ; p++) {
+        const float x0 = x[p], x1 = x[p + PJ];
+        x[p] = x0 * r.c[p] - x1 * r.s[p];
+        x[p + PJ] = x0 * r.s[p] + x1 * r.c[p];
+    }
+}
+
 }  // namespace g4

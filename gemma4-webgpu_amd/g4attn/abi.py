@@ -91,6 +91,12 @@ class PrefillEntry(C.Structure):
                 ("scale", C.c_float)]
 
 
+class PromptPrepParams(C.Structure):
+    _fields_ = [("num_q_heads", C.c_uint32), ("num_kv_heads", C.c_uint32), ("head_dim", C.c_uint32),
+                ("n_tokens", C.c_uint32), ("start", C.c_uint32), ("eps", C.c_float), ("theta", C.c_float),
+                ("apply_divisor", C.c_uint32), ("store_kv", C.c_uint32), ("max_seq_len", C.c_uint32)]
+
+
 class MatmulParams(C.Structure):  # matmul_quant.wgsl:12
     _fields_ = [("M", C.c_uint32), ("N", C.c_uint32)]
 
@@ -170,6 +176,7 @@ SIGNATURES: dict[str, list] = {
     "g4_attn_prefill_run": [C.POINTER(DecodePlan), _P],
     "g4_attn_prefill_run_timed": [C.POINTER(DecodePlan), _P, _P, _P],
     "g4_attn_prefill": [C.POINTER(PrefillEntry), _U32, _U32, _U32, _U32, _P, _SZ, _P],
+    "g4_attn_prompt_prep": [_P, _P, _P, _P, _P, _P, _P, _P, _P, PromptPrepParams, _P],
     "g4_matmul_quant_f16": [_P, _P, _P, MatmulParams, _P],
     "g4_linear_f16": [_P, _U32, C.POINTER(LinearSeg), _U32, _P],
     "g4_read_ceiling": [_P, _SZ, _P, _P, _P, _P],

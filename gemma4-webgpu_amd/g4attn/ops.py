@@ -18,7 +18,7 @@ from . import abi
 from .abi import (G4_WEIGHT_Q4K, G4_WEIGHT_Q8, AttnOutputParams, AttnScoreParams, DecodeEntry, DecodePlan, KvStoreParams,
                   LinearQSeg, LinearSeg, LmHeadParams,
                   MatmulParams, NormParams, NormRopeParams, PrepLayer, PrepParams, SoftcapParams, SoftmaxParams,
-                  StepEntry)
+                  StepEntry, PromptPrepParams)
 
 F16_TYPES = (torch.float16, torch.int16, torch.uint16)
 
@@ -341,6 +341,28 @@ def read_ceiling(buf, sink, start=None, stop=None, stream=None):
 def attn_step(entries, num_q_heads, num_kv_heads, head_dim, workspace, stream=None):
     abi.call("g4_attn_step", entries, len(entries), num_q_heads, num_kv_heads, head_dim,
              _dev(workspace, "workspace", torch.uint8, 0), workspace.numel(), _stream(stream))
+
+
+# ---- chunked prompt prep ----------------------------------------------------------
+
+def attn_prompt_prep(q, q_weight, q_out, n_tokens, start, num_q_heads, num_kv_heads, head_dim, theta, apply_divisor,
+                     rope_freqs=None, k=None, v=None, k_weight=None, k_cache=None, v_cache=None, max_seq_len=0,
+                     eps=1e-6, stream=None):
+    """q/k/v/norm+RoPE/store of n_tokens prompt tokens at positions start.. in one launch. q: f32
+    [n_tokens][NQH][HD]; q_out: f16 [n_tokens][NQH][HD]; with k (and v, k_weight, caches of max_seq_len rows)
+    the layer is a KV producer and rows start .. start + n_tokens - 1 are stored."""
+    store = k is not None
+    nq = n_tokens * num_q_heads * head_dim
+    nk = n_tokens * num_kv_heads * head_dim
+    p = PromptPrepParams(num_q_heads, num_kv_heads, head_dim, n_tokens, start, eps, theta, 1 if apply_divisor else 0,
+                         1 if store else 0, max_seq_len)
+    rows = max_seq_len * num_kv_heads * head_dim
+    abi.call("g4_attn_prompt_prep", _f32(q, "q", nq), _f32(k, "k", nk) if store else None,
+             _f32(v, "v", nk) if store else None, _f16(q_weight, "q_weight", head_dim),
+             _f16(k_weight, "k_weight", head_dim) if store else None,
+             _f16(rope_freqs, "rope_freqs", head_dim // 2) if rope_freqs is not None else None,
+             _f16(q_out, "q_out", nq), _f16(k_cache, "k_cache", rows) if store else None,
+             _f16(v_cache, "v_cache", rows) if store else None, p, _stream(stream))
 
 
 # ---- causal prefill ------------------------------------------------------------

@@ -2,9 +2,9 @@
 checks exactly the plan the benchmark times.
 
 prefill4k   causal prefill of a 4096-token prompt: one global layer and one 512-window
-            local layer, each as eight 512-token chunks, 16 entries in one launch; f16
-            Q/K/V drawn N(0,1) then RMS-normalised per row (q stands for the post norm +
-            RoPE query).
+            local layer, each as eight 512-token chunks, 16 entries in one launch; the
+            f16 query and K/V rows come from raw N(0,1) projections through the
+            chunked prompt prep (q/k RMSNorm + RoPE, v-norm, K/V store).
 ragged64    64 sequences, lengths uniform in [1024, 32768] (seeded).
 """
 from __future__ import annotations
@@ -21,30 +21,46 @@ def ragged64_lengths():
     return [int(x) for x in synth.ragged_lengths(BASE_SEED + 2, 64, 1024, 32768)]
 
 
-def unit_rows_f16(seed: int, rows: int, width: int, dev):
-    """rows x width N(0,1) from stream `seed`, each row RMS-normalised, as f16 on `dev` (flat)."""
-    import torch
-
-    x = synth.normal_torch(seed, rows * width, dev).view(rows, width).double()
-    return (x / torch.sqrt((x ** 2).mean(dim=1, keepdim=True) + EPS)).to(torch.float16).view(-1)
-
-
 def prefill4k(dev, nqh=8, nkh=1, hd=256, T=PREFILL_T, chunk=PREFILL_CHUNK, windows=PREFILL_WINDOWS):
-    """Per layer (q, k_cache, v_cache, out, window) device tensors, and the prefill entries: every
-    chunk of every layer, in layer order then chunk order."""
+    """A prompt's attention for one global and one local layer, from raw projections.
+
+    Per layer: raw f32 q/k/v projections N(0,1) (one row of each head per token), norm weights 1.0 and
+    the engine's rope_freqs table; the chunked prompt prep (q/k RMSNorm + RoPE at every position, v
+    weightless norm, f16 K/V rows stored) fills the f16 query and the caches. Returns the per-layer
+    device tensors (q f16, k_cache, v_cache, out, window), the prefill entries (every chunk of every
+    layer, layer order then chunk order) and `prep()`, which re-runs the two layers' prep launches."""
+    import numpy as np
     import torch
 
-    layers, entries = [], []
+    from . import e2b, ops
+
+    rf_bits = np.array(e2b.rope_freqs_f16_bits(256), dtype=np.uint16)
+    rf = torch.from_numpy(rf_bits.view(np.int16)).to(dev)
+    ones = torch.full((hd,), 0x3C00, dtype=torch.int16, device=dev)
+    layers, entries, preps = [], [], []
     for li, w in enumerate(windows):
-        q = unit_rows_f16(BASE_SEED + 30 + li, T * nqh, hd, dev).view(torch.int16)
-        kc = unit_rows_f16(BASE_SEED + 40 + li, T * nkh, hd, dev).view(torch.int16)
-        vc = unit_rows_f16(BASE_SEED + 50 + li, T * nkh, hd, dev).view(torch.int16)
+        qr = synth.normal_torch(BASE_SEED + 30 + li, T * nqh * hd, dev)
+        kr = synth.normal_torch(BASE_SEED + 40 + li, T * nkh * hd, dev)
+        vr = synth.normal_torch(BASE_SEED + 50 + li, T * nkh * hd, dev)
+        q = torch.empty(T * nqh * hd, dtype=torch.int16, device=dev)
+        kc = torch.empty(T * nkh * hd, dtype=torch.int16, device=dev)
+        vc = torch.empty_like(kc)
         out = torch.empty(T * nqh * hd, dtype=torch.float32, device=dev)
+        theta, div = (1e4, 0) if w else (1e6, 1)
+        preps.append(dict(q=qr, q_weight=ones, q_out=q, n_tokens=T, start=0, num_q_heads=nqh, num_kv_heads=nkh,
+                          head_dim=hd, theta=theta, apply_divisor=div, rope_freqs=rf, k=kr, v=vr, k_weight=ones,
+                          k_cache=kc, v_cache=vc, max_seq_len=T, eps=EPS))
         layers.append((q, kc, vc, out, w))
         for c0 in range(0, T, chunk):
             entries.append(dict(q=q[c0 * nqh * hd:], k_cache=kc, v_cache=vc, out=out[c0 * nqh * hd:],
                                 n_tokens=min(chunk, T - c0), start=c0, sliding_window=w, scale=1.0))
-    return layers, entries
+
+    def prep():
+        for kw in preps:
+            ops.attn_prompt_prep(**kw)
+
+    prep()
+    return layers, entries, prep
 
 
 def prefill_flops(nqh=8, hd=256, T=PREFILL_T, windows=PREFILL_WINDOWS) -> float:

@@ -32,7 +32,7 @@ export type QuantKernelName = 'matmulQ8' | 'matmulQ4K';
 
 export type KernelName = AttnKernelName | SampleKernelName | QuantKernelName;
 
-export type FusedKernelName = 'attnStep' | 'attnPrefill' | 'lmHeadArgmax';
+export type FusedKernelName = 'attnStep' | 'attnPrefill' | 'attnPromptPrep' | 'lmHeadArgmax';
 
 export type UniformValue = { u: number } | { f: number };
 
@@ -76,6 +76,7 @@ export const PASS_LABELS: Record<string, string> = {
   attnOutput: 'attn.attnOutput',
   attnStep: 'attn.decodeFused',
   attnPrefill: 'attn.prefill',
+  attnPromptPrep: 'attn.promptPrep',
   matmulQuant: 'lmHead',
   logitSoftcap: 'logitSoftcap',
   argmax: 'sample.argmax',
@@ -155,6 +156,26 @@ export interface PrefillEntry {
   scale?: number;
 }
 
+// The prep of a prompt chunk of one layer (the engine's per-token vNorm -> fusedNormRope(Q, K) ->
+// kvCacheStore, src/engine.ts:2460-2479, for every token at once). Token t sits at position start + t.
+export interface PromptPrep {
+  q: DeviceBuffer;            // raw projections f32 [nTokens][NQH][HD] (read only)
+  k?: DeviceBuffer;           // f32 [nTokens][NKH][HD]; k, v, kWeight and the caches absent on KV-consumer
+  v?: DeviceBuffer;           // layers (only q is prepared)
+  qWeight: DeviceBuffer;      // attn_q_norm f16 [HD]
+  kWeight?: DeviceBuffer;     // attn_k_norm f16 [HD]
+  ropeFreqs?: DeviceBuffer;   // f16 divisor table (global layers)
+  qOut: DeviceBuffer;         // f16 [nTokens][NQH][HD]: PrefillEntry.q
+  kCache?: DeviceBuffer;      // f16 [maxSeqLen][NKH][HD]: rows start .. start + nTokens - 1 are written
+  vCache?: DeviceBuffer;
+  nTokens: number;
+  start: number;
+  theta: number;
+  applyDivisor: number;
+  maxSeqLen?: number;
+  eps?: number;
+}
+
 // The fused sampling head: lm head over an f16 [vocab][hidden] weight, softcap (0 = none), argmax.
 export interface LmHeadShape {
   vocab: number;
@@ -225,6 +246,8 @@ export interface Addon {
   attnPrefillPrepare(entries: any[], nqh: number, nkh: number, hd: number, ws: bigint, wsBytes: number,
     s: bigint): Uint8Array;
   attnPrefillRun(plan: Uint8Array, s: bigint): void;
+  attnPromptPrep(q: bigint, k: bigint | null, v: bigint | null, qw: bigint, kw: bigint | null, rf: bigint | null,
+    qOut: bigint, kc: bigint | null, vc: bigint | null, p: Uint8Array, s: bigint): void;
   [key: string]: any;
 }
 
@@ -379,6 +402,23 @@ export class HipAttention {
 
   attnPrefill(entries: PrefillEntry[], shape: StepShape, workspace: DeviceBuffer): void {
     this.attnPrefillRun(this.attnPrefillPrepare(entries, shape, workspace));
+  }
+
+  // One launch for every token of a chunk; q goes out as the f16 query of attnPrefill, and producer
+  // layers store their K/V rows, bit-identical to the per-token reference kernels.
+  attnPromptPrep(p: PromptPrep, shape: StepShape): void {
+    const store = p.k !== undefined;
+    if (store && (!p.v || !p.kWeight || !p.kCache || !p.vCache || p.maxSeqLen === undefined)) {
+      throw new Error('attnPromptPrep: a producer layer needs k, v, kWeight, kCache, vCache and maxSeqLen');
+    }
+    const params = new Uniform([
+      { u: shape.numQHeads }, { u: shape.numKvHeads }, { u: shape.headDim }, { u: p.nTokens }, { u: p.start },
+      { f: p.eps === undefined ? 1e-6 : p.eps }, { f: p.theta }, { u: p.applyDivisor }, { u: store ? 1 : 0 },
+      { u: p.maxSeqLen || 0 },
+    ]);
+    function ptr(b: DeviceBuffer | undefined): bigint | null { return b ? b.ptr : null; }
+    this.g4.attnPromptPrep(p.q.ptr, ptr(p.k), ptr(p.v), p.qWeight.ptr, ptr(p.kWeight), ptr(p.ropeFreqs),
+      p.qOut.ptr, ptr(p.kCache), ptr(p.vCache), params.bytes, this.stream);
   }
 
   lmHeadWorkspaceSize(shape: LmHeadShape): number {

@@ -4,6 +4,8 @@
 //   node host/run.js layer <dir>    one attention layer from <dir>/case.json + case.bin, run twice on the
 //                                   GPU: the engine's six dispatches in order (src/engine.ts:2056-2094),
 //                                   and the fused attnStep; results go to <dir>/out.bin for the oracle check.
+//   node host/run.js promptprep <dir>  the chunked prompt prep of one producer layer from <dir>/case.json +
+//                                   case.bin; q_out and both caches go to <dir>/out.bin.
 //   node host/run.js prefill <dir>  two prefill chunks (entries) from <dir>/case.json + case.bin in one
 //                                   attnPrefill call; outputs go to <dir>/out.bin.
 //   node host/run.js head <dir>     the sampling head from <dir>/case.json + case.bin: the engine's lmHead,
@@ -245,6 +247,48 @@ function prefill(dir: string): string[] {
   return ['attnPrefill: ' + entries.length + ' entries', 'results written'];
 }
 
+interface PromptPrepSpec {
+  nqh: number; nkh: number; hd: number; start: number; nTokens: number; theta: number; div: number; rows: number;
+  arrays: Record<string, number[]>;
+}
+
+// The chunked prompt prep of one producer layer; out.bin = q_out, then the whole K and V caches.
+function promptPrep(dir: string): string[] {
+  const spec = JSON.parse(fs.readFileSync(path.join(dir, 'case.json'), 'utf8')) as PromptPrepSpec;
+  const bin: Uint8Array = fs.readFileSync(path.join(dir, 'case.bin'));
+  const att = new HipAttention(loadAddon(), 0);
+  const bufs: DeviceBuffer[] = [];
+  function upload(r: number[]): DeviceBuffer {
+    const b = att.createBuffer(r[1]);
+    att.writeBuffer(b, 0, bin.subarray(r[0], r[0] + r[1]));
+    bufs.push(b);
+    return b;
+  }
+  function alloc(bytes: number): DeviceBuffer {
+    const b = att.createBuffer(bytes);
+    att.clearBuffer(b);
+    bufs.push(b);
+    return b;
+  }
+  const A = spec.arrays;
+  const qOut = alloc(spec.nTokens * spec.nqh * spec.hd * 2);
+  const kc = alloc(spec.rows * spec.nkh * spec.hd * 2);
+  const vc = alloc(spec.rows * spec.nkh * spec.hd * 2);
+  att.attnPromptPrep({
+    q: upload(A.q), k: upload(A.k), v: upload(A.v), qWeight: upload(A.qw), kWeight: upload(A.kw),
+    ropeFreqs: upload(A.rf), qOut: qOut, kCache: kc, vCache: vc, nTokens: spec.nTokens, start: spec.start,
+    theta: spec.theta, applyDivisor: spec.div, maxSeqLen: spec.rows,
+  }, { numQHeads: spec.nqh, numKvHeads: spec.nkh, headDim: spec.hd });
+  const res = new Uint8Array(qOut.size + kc.size + vc.size);
+  att.readBuffer(qOut, 0, res.subarray(0, qOut.size));
+  att.readBuffer(kc, 0, res.subarray(qOut.size, qOut.size + kc.size));
+  att.readBuffer(vc, 0, res.subarray(qOut.size + kc.size));
+  fs.writeFileSync(path.join(dir, 'out.bin'), res);
+  for (const b of bufs) att.destroyBuffer(b);
+  att.dispose();
+  return ['attnPromptPrep: ' + spec.nTokens + ' tokens', 'results written'];
+}
+
 interface HeadSpec {
   vocab: number; hidden: number; cap: number; arrays: Record<string, number[]>;
 }
@@ -474,8 +518,9 @@ export function main(argv: string[]): void {
   else if (mode === 'layer') done = layer(argv[1]);
   else if (mode === 'head') done = head(argv[1]);
   else if (mode === 'prefill') done = prefill(argv[1]);
+  else if (mode === 'promptprep') done = promptPrep(argv[1]);
   else if (mode === 'linear') done = linear(argv[1]);
   else if (mode === 'batch') done = batch(argv[1]);
-  else fail(`usage: run.js cpu | layer <dir> | prefill <dir> | head <dir> | linear <dir> | batch <dir> | readback <dir>`);
+  else fail(`usage: run.js cpu | layer <dir> | prefill <dir> | promptprep <dir> | head <dir> | linear <dir> | batch <dir> | readback <dir>`);
   process.stdout.write(JSON.stringify({ ok: true, checks: done }) + '\n');
 }

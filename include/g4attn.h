@@ -398,6 +398,35 @@ int g4_attn_prefill_run_timed(const g4_decode_plan* plan, void* stream, void* st
 int g4_attn_prefill(const g4_prefill_entry* entries, uint32_t n_entries, uint32_t num_q_heads, uint32_t num_kv_heads,
                     uint32_t head_dim, void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---- chunked prompt prep ----------------------------------------------------
+ * The producer-side prep of every token of a prompt chunk in one launch: the
+ * engine runs vNorm -> fusedNormRope(Q, K) -> kvCacheStore once per prompt
+ * token (src/engine.ts:2460-2479, each through 2056-2091). Token t sits at
+ * position (and cache row) start + t. Per token: q (norm with q_weight +
+ * RoPE) written to q_out as f16 (the query g4_attn_prefill takes); on
+ * producer layers (store_kv) k (norm with k_weight + RoPE) and v (weightless
+ * norm) stored as f16 rows start + t of the caches. Every value is the f16
+ * rounding of what fused_per_head_norm_rope.wgsl / per_head_rms_norm_no_weight
+ * .wgsl compute for that token, bit for bit. q, k, v are read only.        */
+typedef struct g4_prompt_prep_params {
+    uint32_t num_q_heads;
+    uint32_t num_kv_heads;
+    uint32_t head_dim;       /* 256 or 512 */
+    uint32_t n_tokens;
+    uint32_t start;          /* position of token 0 */
+    float eps;
+    float theta;
+    uint32_t apply_divisor;  /* 1 on global layers: divide by rope_freqs[i] */
+    uint32_t store_kv;       /* 1 on producer layers */
+    uint32_t max_seq_len;    /* cache rows (start + n_tokens <= max_seq_len when store_kv) */
+} g4_prompt_prep_params;
+
+/* q: f32 [n_tokens][num_q_heads][head_dim]; k, v: f32 [n_tokens][num_kv_heads][head_dim]
+ * (NULL with store_kv 0); q_out: f16 [n_tokens][num_q_heads][head_dim]. */
+int g4_attn_prompt_prep(const float* q, const float* k, const float* v, const uint16_t* q_weight,
+                        const uint16_t* k_weight, const uint16_t* rope_freqs, uint16_t* q_out, uint16_t* k_cache,
+                        uint16_t* v_cache, g4_prompt_prep_params p, void* stream);
+
 /* ---- the f16 projections either side of the block ------------------------
  * attn.linearQKV (src/engine.ts:2045-2051) and attn.linearOut (:2096):
  * matmulQuant / matmulQuantMR4 over f16 weights. One call runs up to four

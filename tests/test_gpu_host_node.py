@@ -328,3 +328,43 @@ def test_quantized_linear_through_ts_host(tmp_path, fmt):
     total = sum(rows)
     np.testing.assert_array_equal(got[:total], want)
     np.testing.assert_array_equal(got[total:], want)
+
+
+@pytest.mark.skipif(NODE is None, reason="node is not installed")
+@pytest.mark.parametrize("start,T,hd,theta,div", [(0, 64, 256, 1e4, 0), (5000, 33, 512, 1e6, 1)])
+def test_prompt_prep_through_ts_host(tmp_path, start, T, hd, theta, div):
+    """HipAttention.attnPromptPrep over the addon: q_out and the stored K/V rows bit-identical to the oracle's
+    per-token fused_per_head_norm_rope / per_head_rms_norm_no_weight rounded to f16; other rows untouched."""
+    announce(f"TS host attnPromptPrep start={start} T={T} hd={hd}")
+    seed = 300 + start + T
+    rows = start + T + 2
+    arrs = {"q": synth.normal(seed, T * NQH * hd), "k": synth.normal(seed + 1, T * NKH * hd),
+            "v": synth.normal(seed + 2, T * NKH * hd), "qw": f16_weight_bits(seed + 3, hd),
+            "kw": f16_weight_bits(seed + 4, hd), "rf": ROPE}
+    blob, index = bytearray(), {}
+    for name, a in arrs.items():
+        b = np.ascontiguousarray(a).tobytes()
+        index[name] = [len(blob), len(b)]
+        blob += b
+    (tmp_path / "case.bin").write_bytes(bytes(blob))
+    (tmp_path / "case.json").write_text(json.dumps(dict(nqh=NQH, nkh=NKH, hd=hd, start=start, nTokens=T,
+                                                        theta=theta, div=div, rows=rows, arrays=index)))
+    r = subprocess.run([NODE, str(RUN), "promptprep", str(tmp_path)], cwd=ROOT, capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 0, r.stderr
+    raw = np.frombuffer((tmp_path / "out.bin").read_bytes(), np.uint16)
+    nq = T * NQH * hd
+    q_out = raw[:nq].reshape(T, NQH * hd)
+    kc = raw[nq:nq + rows * NKH * hd].reshape(rows, NKH * hd)
+    vc = raw[nq + rows * NKH * hd:].reshape(rows, NKH * hd)
+    for t in range(T):
+        pos = start + t
+        q_ = orc.fused_per_head_norm_rope(arrs["q"][t * NQH * hd:(t + 1) * NQH * hd], arrs["qw"], ROPE, NQH, hd, EPS,
+                                          pos, theta, div)
+        k_ = orc.fused_per_head_norm_rope(arrs["k"][t * NKH * hd:(t + 1) * NKH * hd], arrs["kw"], ROPE, NKH, hd, EPS,
+                                          pos, theta, div)
+        v_ = orc.per_head_rms_norm_no_weight(arrs["v"][t * NKH * hd:(t + 1) * NKH * hd], NKH, hd, EPS)
+        np.testing.assert_array_equal(q_out[t], orc.f32_to_f16_bits(q_), err_msg=f"q token {t}")
+        np.testing.assert_array_equal(kc[pos], orc.f32_to_f16_bits(k_), err_msg=f"k token {t}")
+        np.testing.assert_array_equal(vc[pos], orc.f32_to_f16_bits(v_), err_msg=f"v token {t}")
+    assert (kc[:start] == 0).all() and (kc[start + T:] == 0).all() and (vc[:start] == 0).all()

@@ -169,7 +169,7 @@ def test_prefill4k_bench_plan(dev):
     from g4attn import workloads
 
     announce("attnPrefill prefill4k bench plan (16 entries, one launch)")
-    layers, entries = workloads.prefill4k(dev, 8, 1, HD)
+    layers, entries, _ = workloads.prefill4k(dev, 8, 1, HD)
     arr = ops.make_prefill_entries(entries, 8, 1, HD)
     ws = torch.empty(ops.prefill_workspace_bytes(arr, 8, 1, HD), dtype=torch.uint8, device=dev)
     for _, _, _, out, _ in layers:

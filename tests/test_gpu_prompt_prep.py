@@ -1,0 +1,158 @@
+"""GPU parity of the chunked prompt prep (g4_attn_prompt_prep) against the oracle, bit for bit.
+
+The engine preps a prompt one token at a time: vNorm -> fusedNormRope(Q) -> fusedNormRope(K) ->
+kvCacheStore at each position (src/engine.ts:2460-2479 -> 2056-2091). The chunked prep does every
+token of a chunk in one launch. For each token t at position start + t: q_out[t] must equal the f16
+rounding of the oracle's fused_per_head_norm_rope(q_t) bit for bit, and on producer layers the cache
+rows start + t must equal the f16 rounding of the oracle's normed and rotated k_t and weightless-normed
+v_t; rows outside the chunk stay untouched. Then the prepped chunk through g4_attn_prefill is checked
+against the oracle's decode chain on the same f16 query (max-abs 2e-3).
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import announce
+from g4attn import e2b, ops, synth
+from helpers import EPS, f16_weight_bits, max_abs
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+ROPE = np.array(e2b.rope_freqs_f16_bits(256), dtype=np.uint16)
+POISON = 0x5A5A
+
+
+def t16(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16).reshape(-1)).to(dev)
+
+
+class Chunk:
+    def __init__(self, dev, seed, start, T, hd, theta, div, nqh=8, nkh=1, store=True):
+        self.start, self.T, self.hd, self.theta, self.div, self.nqh, self.nkh = start, T, hd, theta, div, nqh, nkh
+        self.q = synth.normal(seed, T * nqh * hd) * 2.0
+        self.k = synth.normal(seed + 1, T * nkh * hd) * 2.0
+        self.v = synth.normal(seed + 2, T * nkh * hd) * 2.0
+        self.qw, self.kw = f16_weight_bits(seed + 3, hd), f16_weight_bits(seed + 4, hd)
+        self.rows = start + T + 3
+        self.dq, self.dk, self.dv = (torch.from_numpy(x.copy()).to(dev) for x in (self.q, self.k, self.v))
+        self.q_out = torch.full((T * nqh * hd,), POISON, dtype=torch.int16, device=dev)
+        self.kc = torch.full((self.rows * nkh * hd,), POISON, dtype=torch.int16, device=dev)
+        self.vc = torch.full_like(self.kc, POISON)
+        self.store = store
+        self.dqw, self.dkw, self.drf = t16(self.qw, dev), t16(self.kw, dev), t16(ROPE, dev)
+
+    def run(self):
+        kw = dict(k=self.dk, v=self.dv, k_weight=self.dkw, k_cache=self.kc, v_cache=self.vc,
+                  max_seq_len=self.rows) if self.store else {}
+        ops.attn_prompt_prep(self.dq, self.dqw, self.q_out, self.T, self.start, self.nqh, self.nkh, self.hd,
+                             self.theta, self.div, rope_freqs=self.drf, eps=EPS, **kw)
+        torch.cuda.synchronize()
+
+    def expected(self):
+        hd, nqh, nkh = self.hd, self.nqh, self.nkh
+        qo = np.empty((self.T, nqh * hd), np.uint16)
+        ko = np.empty((self.T, nkh * hd), np.uint16)
+        vo = np.empty((self.T, nkh * hd), np.uint16)
+        for t in range(self.T):
+            pos = self.start + t
+            qt = self.q[t * nqh * hd:(t + 1) * nqh * hd]
+            qo[t] = orc.f32_to_f16_bits(orc.fused_per_head_norm_rope(qt, self.qw, ROPE, nqh, hd, EPS, pos,
+                                                                     self.theta, self.div))
+            kt = self.k[t * nkh * hd:(t + 1) * nkh * hd]
+            vt = self.v[t * nkh * hd:(t + 1) * nkh * hd]
+            ko[t] = orc.f32_to_f16_bits(orc.fused_per_head_norm_rope(kt, self.kw, ROPE, nkh, hd, EPS, pos,
+                                                                     self.theta, self.div))
+            vo[t] = orc.f32_to_f16_bits(orc.per_head_rms_norm_no_weight(vt, nkh, hd, EPS))
+        return qo, ko, vo
+
+    def check(self):
+        qo, ko, vo = self.expected()
+        got_q = self.q_out.cpu().numpy().view(np.uint16).reshape(self.T, -1)
+        np.testing.assert_array_equal(got_q, qo, err_msg="q_out")
+        kc = self.kc.cpu().numpy().view(np.uint16).reshape(self.rows, -1)
+        vc = self.vc.cpu().numpy().view(np.uint16).reshape(self.rows, -1)
+        s, e = self.start, self.start + self.T
+        if self.store:
+            np.testing.assert_array_equal(kc[s:e], ko, err_msg="k rows")
+            np.testing.assert_array_equal(vc[s:e], vo, err_msg="v rows")
+        else:
+            assert (kc[s:e] == POISON).all() and (vc[s:e] == POISON).all(), "consumer layer stored rows"
+        for c, name in ((kc, "k"), (vc, "v")):
+            assert (c[:s] == POISON).all() and (c[e:] == POISON).all(), f"{name} rows outside the chunk written"
+
+
+@pytest.mark.parametrize("start,T,hd,theta,div", [
+    (0, 512, 256, 1e4, 0),            # local layer, the first chunk
+    (131071 - 511, 512, 256, 1e6, 1),  # global layer, positions up to 131071
+    (4096, 512, 512, 1e6, 1),         # E2B global layer (head_dim 512)
+    (77, 5, 256, 1e4, 0),             # a short ragged chunk
+])
+def test_prompt_prep_bit_exact(dev, start, T, hd, theta, div):
+    announce(f"attnPromptPrep start={start} T={T} hd={hd} theta={theta}")
+    c = Chunk(dev, 500 + start + hd, start, T, hd, theta, div)
+    c.run()
+    c.check()
+
+
+def test_prompt_prep_consumer_and_gqa(dev):
+    """A KV-consumer layer (q only) and a 4:1 group with two kv heads."""
+    announce("attnPromptPrep consumer layer; nqh=8 nkh=2")
+    c = Chunk(dev, 71, 300, 64, 256, 1e4, 0, store=False)
+    c.run()
+    c.check()
+    g = Chunk(dev, 72, 0, 40, 256, 1e6, 1, nqh=8, nkh=2)
+    g.run()
+    g.check()
+
+
+def test_prompt_prep_rejects(dev):
+    from g4attn.abi import G4Error
+    c = Chunk(dev, 73, 10, 8, 256, 1e4, 0)
+    with pytest.raises(G4Error):  # rows past the cache
+        ops.attn_prompt_prep(c.dq, c.dqw, c.q_out, c.T, c.rows, 8, 1, 256, 1e4, 0, k=c.dk, v=c.dv, k_weight=c.dkw,
+                             k_cache=c.kc, v_cache=c.vc, max_seq_len=c.rows)
+    with pytest.raises(G4Error):  # head_dim 128
+        ops.attn_prompt_prep(c.dq, c.dqw, c.q_out, 1, 0, 8, 1, 128, 1e4, 0)
+
+
+def test_prompt_prep_then_prefill(dev):
+    """Two 256-token chunks of a global layer: each chunk prepped (q, k, v norm/RoPE, K/V stored) then run
+    through the prefill; tokens checked against the oracle's per-token decode chain on the stored rows."""
+    announce("attnPromptPrep + attnPrefill, two chunks")
+    T, hd, theta, div = 256, 256, 1e6, 1
+    rows = 2 * T
+    qw, kw = f16_weight_bits(81, hd), f16_weight_bits(82, hd)
+    kc = torch.zeros(rows * hd, dtype=torch.int16, device=dev)
+    vc = torch.zeros_like(kc)
+    out = torch.full((rows * 8 * hd,), float("nan"), dtype=torch.float32, device=dev)
+    qbits = torch.empty(rows * 8 * hd, dtype=torch.int16, device=dev)
+    dqw, dkw, drf = t16(qw, dev), t16(kw, dev), t16(ROPE, dev)
+    q = synth.normal(83, rows * 8 * hd)
+    k = synth.normal(84, rows * hd)
+    v = synth.normal(85, rows * hd)
+    for c in range(2):
+        s = c * T
+        dq = torch.from_numpy(q[s * 8 * hd:(s + T) * 8 * hd].copy()).to(dev)
+        dk = torch.from_numpy(k[s * hd:(s + T) * hd].copy()).to(dev)
+        dv = torch.from_numpy(v[s * hd:(s + T) * hd].copy()).to(dev)
+        ops.attn_prompt_prep(dq, dqw, qbits[s * 8 * hd:], T, s, 8, 1, hd, theta, div, rope_freqs=drf, k=dk, v=dv,
+                             k_weight=dkw, k_cache=kc, v_cache=vc, max_seq_len=rows, eps=EPS)
+        e = dict(q=qbits[s * 8 * hd:], k_cache=kc, v_cache=vc, out=out[s * 8 * hd:], n_tokens=T, start=s,
+                 sliding_window=0, scale=1.0)
+        arr = ops.make_prefill_entries([e], 8, 1, hd)
+        ws = torch.empty(max(ops.prefill_workspace_bytes(arr, 8, 1, hd), 1), dtype=torch.uint8, device=dev)
+        ops.attn_prefill(arr, 8, 1, hd, ws)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().reshape(rows, -1)
+    kf = orc.f16_bits_to_f32(kc.cpu().numpy().view(np.uint16)).reshape(rows, hd)
+    vf = orc.f16_bits_to_f32(vc.cpu().numpy().view(np.uint16)).reshape(rows, hd)
+    worst = 0.0
+    for t in list(range(0, rows, 7)) + [rows - 1]:
+        qt = orc.fused_per_head_norm_rope(q[t * 8 * hd:(t + 1) * 8 * hd], qw, ROPE, 8, hd, EPS, t, theta, div)
+        qt = orc.f16_bits_to_f32(orc.f32_to_f16_bits(qt))  # the prefill's query operand is f16
+        want = orc.attention_chain(qt, kf[:t + 1].reshape(-1), vf[:t + 1].reshape(-1), 8, 1, hd, t + 1, 1.0, 0)
+        err = max_abs(got[t], want)
+        assert err <= 2e-3, f"token {t}: max-abs {err}"
+        worst = max(worst, err)
+    print(f"prep + prefill: worst err {worst:.2e}")
