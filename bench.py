@@ -49,6 +49,7 @@ the host.
 from __future__ import annotations
 
 import argparse
+import ctypes as C
 import json
 import math
 import os
@@ -197,14 +198,22 @@ class CacheSet:
     def advance(self, ops):
         """The next token: every entry one row longer, re-prepared (the engine rewrites the position,
         slot and seq_len uniforms every token, src/engine.ts:1967-1987)."""
-        from g4attn import abi
-
         for g in self.groups:
             hd, idx, arr, ws, plan = g
-            for j in range(len(idx)):
-                arr[j].seq_len += 1
-                arr[j].position += 1
+            for f in self._fields(arr):  # seq_len and position of every entry, one vectorised bump each
+                f += 1
             g[4] = ops.attn_step_prepare(arr, NQH, NKH, hd, ws)
+
+    @staticmethod
+    def _fields(arr):
+        """numpy views of the seq_len and position fields of a ctypes StepEntry array (writes go to it)."""
+        import numpy as np
+
+        from g4attn.abi import StepEntry
+
+        u32 = np.frombuffer(arr, dtype=np.uint32)
+        stride = C.sizeof(StepEntry) // 4
+        return [u32[StepEntry.seq_len.offset // 4::stride], u32[StepEntry.position.offset // 4::stride]]
 
     def prepare_per_entry(self, torch, ops, dev):
         """One single-entry plan per entry: the engine's issue order (layer after layer)."""

@@ -8,6 +8,7 @@
 #include <stdio.h>
 
 #include "../../include/g4attn.h"
+#include "tables.h"
 
 namespace g4 {
 
@@ -54,8 +55,6 @@ typedef f16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-constexpr float kLog2e = 1.4426950408889634f;
 
 // Loads and stores through the global address space (global_load/store with
 // an SGPR base), for pointers the compiler cannot prove global by itself.

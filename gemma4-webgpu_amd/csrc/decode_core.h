@@ -25,8 +25,6 @@ namespace g4 {
 
 constexpr int kDecodeWaves = 4;
 constexpr int kDecodeThreads = 64 * kDecodeWaves;
-constexpr int kTileKeys = 32;
-constexpr int kMaxGroup = 8;  // query heads per kv head served by one MFMA column block
 
 template <typename T>
 __device__ __forceinline__ T ldg_stream(const void* p) {
@@ -74,18 +72,6 @@ __device__ __forceinline__ const char* uniform_ptr(const char* p) {
     return reinterpret_cast<const char*>(((uint64_t)hi << 32) | lo);
 }
 
-struct DecodeEntryDev {
-    const float* q;       // [num_kv_heads][group][HD]
-    const uint16_t* k;    // [rows][num_kv_heads][HD]
-    const uint16_t* v;
-    float* out;           // [num_kv_heads][group][HD]
-    uint32_t key_begin;   // first attended row
-    uint32_t key_end;     // one past the last attended row
-    uint32_t split_base;  // first split index of this entry
-    uint32_t n_splits;
-    float qscale;         // attention scale * log2(e)
-    uint32_t pad;
-};
 
 struct DecodeArgs {
     const DecodeEntryDev* table;  // device table, or nullptr to use `one`

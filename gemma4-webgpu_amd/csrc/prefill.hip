@@ -904,12 +904,12 @@ int build(const g4_prefill_entry* ents, uint32_t n, uint32_t nqh, uint32_t nkh, 
     off += align256(work->size() * sizeof(PrefillWorkDev));
     L->merge = off;
     off += align256(merge->size() * sizeof(DecodeEntryDev));
+    L->vtc = off;  // the four tables are contiguous: prepare uploads them in one copy
+    off += align256(vp->v.size() * sizeof(VtCacheDev));
     L->ml = off;
     off += align256(slots * nkh * G * 2 * sizeof(float));
     L->o = off;
     off += align256(slots * nkh * G * hd * sizeof(float));
-    L->vtc = off;
-    off += align256(vp->v.size() * sizeof(VtCacheDev));
     L->vt = off;
     for (size_t c = 0; c < vp->v.size(); c++) off += align256((size_t)nkh * vp->blocks[c] * kPfKeys * hd * 2);
     L->total = off;
@@ -990,13 +990,12 @@ int g4_attn_prefill_prepare(const g4_prefill_entry* entries, uint32_t n_entries,
                             vp.block0[c], 0u};
     if (dma)
         for (uint32_t i = 0; i < n_entries; i++) tab[i].vt = vtc[vp.of[i]].vt;
-    rc = stage_upload(ws + L.table, tab.data(), tab.size() * sizeof(PrefillEntryDev), st);
-    if (rc) return rc;
-    rc = stage_upload(ws + L.work, work.data(), work.size() * sizeof(PrefillWorkDev), st);
-    if (rc) return rc;
-    rc = stage_upload(ws + L.merge, merge.data(), merge.size() * sizeof(DecodeEntryDev), st);
-    if (rc) return rc;
-    rc = stage_upload(ws + L.vtc, vtc.data(), vtc.size() * sizeof(VtCacheDev), st);
+    std::vector<char> blob(L.vtc - L.table + vtc.size() * sizeof(VtCacheDev));
+    memcpy(blob.data(), tab.data(), tab.size() * sizeof(PrefillEntryDev));
+    memcpy(blob.data() + (L.work - L.table), work.data(), work.size() * sizeof(PrefillWorkDev));
+    if (!merge.empty()) memcpy(blob.data() + (L.merge - L.table), merge.data(), merge.size() * sizeof(DecodeEntryDev));
+    if (!vtc.empty()) memcpy(blob.data() + (L.vtc - L.table), vtc.data(), vtc.size() * sizeof(VtCacheDev));
+    rc = stage_upload(ws + L.table, blob.data(), blob.size(), st);  // the four tables in one copy
     if (rc) return rc;
     PrefillPlanRep r = {};
     r.ws = ws;

@@ -45,45 +45,9 @@
 
 #include "decode_core.h"
 #include "ref_math.h"
+#include "step_plan.h"
 
 namespace g4 {
-
-struct StepEntryDev {
-    const float* q;  // raw projections, [num_kv_heads][group][HD] and [num_kv_heads][HD]
-    const float* k;
-    const float* v;
-    const uint16_t* q_weight;
-    const uint16_t* k_weight;
-    const uint16_t* rope_freqs;
-    const float* rope_cs;  // RoPE factors of this token [cos x 128][sin x 128] (host-computed), or nullptr
-    uint16_t* k_cache;  // [rows][num_kv_heads][HD]
-    uint16_t* v_cache;
-    float* out;         // attnOut [num_kv_heads][group][HD]
-    uint32_t key_end;   // one past the last attended row; the current row is key_end - 1
-    uint32_t n_parts;   // workgroups on this entry
-    uint32_t position;  // RoPE position
-    uint32_t flags;     // kStoreKv | kRowCached
-    float theta;
-    uint32_t apply_divisor;
-    float qscale;       // attention scale * log2(e)
-    float eps;
-};
-
-constexpr uint32_t kStoreKv = 1;    // write the current row's k and v to the caches
-constexpr uint32_t kRowCached = 2;  // the current row is already in the cache: read it like the others
-
-// One workgroup's share: attended rows [row_begin, row_end) of entry `entry`,
-// with a copy of the entry, so that a workgroup's first loads depend on one
-// batch of scalar loads (a kernel starts with cold caches: each dependent
-// load in that chain costs a memory round trip).
-struct StepWorkDev {
-    StepEntryDev ent;
-    uint32_t row_begin;
-    uint32_t row_end;
-    uint32_t part;   // partial record slot, when the entry has more than one workgroup
-    uint32_t entry;
-};
-static_assert(sizeof(StepWorkDev) == 128, "work item size");
 
 struct StepArgs {
     const StepWorkDev* work;
@@ -289,14 +253,7 @@ using namespace g4;
 
 namespace {
 
-// Partial records: an entry gets more than one workgroup only while the
-// workgroups fit one wave of the GPU (at most kStepMaxWgs), so at most that
-// many records exist.
-constexpr unsigned kStepMaxWgs = 1024;
-constexpr unsigned kStepOneWgTiles = 16;   // one workgroup per CU up to this many tiles each
 constexpr uint32_t kStepMagic = 0x67345354u;
-
-inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 int step_env(const char* name, int dflt) {
     const char* s = getenv(name);
@@ -314,50 +271,10 @@ struct StepPlanRep {
     uint32_t waves;      // waves per workgroup of the attention kernel (4 or 8)
     uint32_t head_dim;   // 256 or 512
     uint32_t magic;
+    uint32_t off_merge;  // byte offsets of the merge table and the RoPE factors in the tables region
+    uint32_t off_rope;
 };
 static_assert(sizeof(StepPlanRep) <= sizeof(g4_decode_plan), "plan size");
-
-struct StepLayout {
-    size_t rope, work, merge_table, part_ml, part_o, total;
-};
-
-StepLayout step_layout(uint64_t n, uint64_t nkh, uint64_t group, uint64_t hd) {
-    StepLayout L;
-    const uint64_t max_items = n > kStepMaxWgs ? n : kStepMaxWgs;
-    const uint64_t recs = (uint64_t)kStepMaxWgs * nkh * group;
-    size_t off = 0;
-    L.rope = off;  // RoPE factors: at most one [cos x hd/2][sin x hd/2] set per entry
-    off += align256(n * hd * 4);
-    L.work = off;
-    off += align256(max_items * sizeof(StepWorkDev));
-    L.merge_table = off;
-    off += align256(n * sizeof(DecodeEntryDev));
-    L.part_ml = off;
-    off += align256(recs * 2 * 4);
-    L.part_o = off;
-    off += align256(recs * hd * 4);
-    L.total = off;
-    return L;
-}
-
-// Smallest tiles-per-workgroup with sum_e ceil(tiles_e / tpw) <= cap (cap >= n,
-// so tpw = max tiles always fits).
-uint64_t pick_tiles_per_wg(const std::vector<uint32_t>& tiles, uint64_t total, uint64_t max_tiles, uint64_t cap) {
-    auto wgs = [&](uint64_t tpw) {
-        uint64_t s = 0;
-        for (uint32_t t : tiles) s += (t + tpw - 1) / tpw;
-        return s;
-    };
-    uint64_t lo = (total + cap - 1) / cap, hi = max_tiles;
-    if (lo < 1) lo = 1;
-    if (lo > hi) lo = hi;
-    while (lo < hi) {
-        const uint64_t mid = (lo + hi) / 2;
-        if (wgs(mid) <= cap) hi = mid;
-        else lo = mid + 1;
-    }
-    return lo;
-}
 
 }  // namespace
 
@@ -382,165 +299,28 @@ int g4_attn_step_prepare(const g4_step_entry* entries, uint32_t n_entries, uint3
     int rc = g4_attn_step_workspace_size(n_entries, num_q_heads, num_kv_heads, head_dim, &need);
     if (rc) return rc;
     if (!plan) return fail(G4_EINVAL, "attnStep: plan is NULL");
-    if (!entries || n_entries == 0) return fail(G4_EINVAL, "attnStep: no entries");
-    if (n_entries > 65535) return fail(G4_EINVAL, "attnStep: %u entries (max 65535)", n_entries);
     if (!workspace || workspace_bytes < need)
         return fail(G4_ENOSPC, "attnStep: workspace %zu bytes < %zu needed", workspace_bytes, need);
+    // G4_STEP_WAVES (4 or 8), G4_STEP_WGS_PER_CU and G4_STEP_MAX_WGS override the grid choice.
+    static const StepTuning tune = [] {
+        StepTuning t;
+        t.waves = step_env("G4_STEP_WAVES", 0);
+        t.wgs_per_cu = step_env("G4_STEP_WGS_PER_CU", 0);
+        t.max_wgs = step_env("G4_STEP_MAX_WGS", 0);
+        return t;
+    }();
     const uint32_t G = num_q_heads / num_kv_heads;
-    const uint64_t row_bytes = (uint64_t)num_kv_heads * head_dim * 2;
-    std::vector<StepEntryDev> tab(n_entries);
-    std::vector<uint32_t> key_begin(n_entries), tiles(n_entries);
-    uint64_t T = 0, max_tiles = 0;
-    for (uint32_t i = 0; i < n_entries; i++) {
-        const g4_step_entry& s = entries[i];
-        if (!s.q || !s.q_weight || !s.k_cache || !s.v_cache || !s.out)
-            return fail(G4_EINVAL, "attnStep: entry %u has a NULL pointer", i);
-        const bool cached = !s.k && !s.v && !s.k_weight;  // consumer whose producer stored the row already
-        if (!cached && (!s.k || !s.v || !s.k_weight))
-            return fail(G4_EINVAL, "attnStep: entry %u: k, v and k_weight are all set or all NULL", i);
-        if (cached && s.store_kv)
-            return fail(G4_EINVAL, "attnStep: entry %u: store_kv needs the raw k and v", i);
-        if (reinterpret_cast<uintptr_t>(s.out) & 15)
-            return fail(G4_EINVAL, "attnStep: entry %u out must be 16-byte aligned", i);
-        if (s.apply_divisor && !s.rope_freqs) return fail(G4_EINVAL, "attnStep: entry %u needs rope_freqs", i);
-        if (s.seq_len == 0) return fail(G4_EINVAL, "attnStep: entry %u seq_len 0", i);
-        if ((uint64_t)s.seq_len * row_bytes > 0xffffffffull)
-            return fail(G4_EINVAL, "attnStep: entry %u cache exceeds 4 GiB", i);
-        StepEntryDev& d = tab[i];
-        d = StepEntryDev{};
-        d.q = s.q;
-        // Cached rows: the kernel's unconditional loads of k, v and k_weight read q and q_weight
-        // instead (valid addresses; the values are not used).
-        d.k = cached ? s.q : s.k;
-        d.v = cached ? s.q : s.v;
-        d.q_weight = s.q_weight;
-        d.k_weight = cached ? s.q_weight : s.k_weight;
-        d.rope_freqs = s.rope_freqs;
-        d.k_cache = s.k_cache;
-        d.v_cache = s.v_cache;
-        d.out = s.out;
-        d.key_end = s.seq_len;
-        d.position = s.position;
-        d.flags = (s.store_kv ? kStoreKv : 0u) | (cached ? kRowCached : 0u);
-        d.theta = s.theta;
-        d.apply_divisor = s.apply_divisor;
-        d.qscale = s.scale * kLog2e;
-        d.eps = s.eps;
-        key_begin[i] = (s.sliding_window != 0 && s.seq_len > s.sliding_window) ? s.seq_len - s.sliding_window : 0;
-        tiles[i] = (s.seq_len - key_begin[i] + kTileKeys - 1) / kTileKeys;
-        T += tiles[i];
-        if (tiles[i] > max_tiles) max_tiles = tiles[i];
-    }
-    // Workgroups in one wave of the GPU. Small steps (at most kStepOneWgTiles
-    // tiles per workgroup with one workgroup per CU) take one 8-wave
-    // workgroup per CU: two tile rounds per wave at most, one partial record
-    // per CU. Larger steps take two 4-wave workgroups per CU. Measured (µs,
-    // two 4-wave / one 4-wave / one 8-wave per CU): stack8k 24.0 / 22.3 / 21.9,
-    // long128k 34.4 / 32.0 / 31.5, stack32k 48.9 / 56.0 / 55.7, ragged64
-    // 190.9 / 199.6 / 197.8. A second workgroup per CU starts behind the first
-    // and is served after it, which only pays off when the per-wave rounds
-    // are many; grids between one and two per CU are slower than both (CUs
-    // with two workgroups finish last). G4_STEP_WAVES (4 or 8),
-    // G4_STEP_WGS_PER_CU and G4_STEP_MAX_WGS override.
-    static const int env_waves = step_env("G4_STEP_WAVES", 0);
-    static const int wgs_per_cu = step_env("G4_STEP_WGS_PER_CU", 0);
-    static const int max_wgs = step_env("G4_STEP_MAX_WGS", 0);
-    // head_dim 512 has one form: one 4-wave workgroup per CU.
-    const uint64_t cus = device_cus();
-    const bool small = T <= (uint64_t)kStepOneWgTiles * (cus / num_kv_heads);
-    const uint32_t waves =
-        head_dim == 512 ? 4u : env_waves == 4 || env_waves == 8 ? (uint32_t)env_waves : (small ? 8u : 4u);
-    const uint64_t per_cu = head_dim == 512 ? 1u
-                            : wgs_per_cu > 0 ? (uint64_t)wgs_per_cu
-                                             : (waves == 8 || small ? 1u : 2u);
-    uint64_t fit = max_wgs > 0 ? (uint64_t)max_wgs / num_kv_heads : per_cu * cus / num_kv_heads;
-    if (fit > kStepMaxWgs) fit = kStepMaxWgs;
-    if (fit < 1) fit = 1;
-    const uint64_t cap = fit > n_entries ? fit : n_entries;
-    const uint64_t tpw = pick_tiles_per_wg(tiles, T, max_tiles, cap);
-
-    // Tile ranges of the work items, entry by entry: tpw tiles per item,
-    // balanced within an entry.
-    std::vector<std::vector<uint64_t>> cuts(n_entries);  // per entry: tile boundaries 0 = c0 < c1 < ... = tiles
-    for (uint32_t i = 0; i < n_entries; i++) {
-        const uint64_t ne = tiles[i], we = (ne + tpw - 1) / tpw;
-        std::vector<uint64_t>& c = cuts[i];
-        c.resize(we + 1);
-        for (uint64_t j = 0; j <= we; j++) c[j] = j * ne / we;
-    }
-
-    std::vector<StepWorkDev> work;
-    work.reserve(cap);
-    std::vector<DecodeEntryDev> merge;  // only the entries with partial records: the merge grid covers them alone
-    merge.reserve(n_entries);
-    uint32_t parts = 0, max_parts = 0;
-    for (uint32_t i = 0; i < n_entries; i++) {
-        StepEntryDev& d = tab[i];
-        const uint64_t we = cuts[i].size() - 1;
-        d.n_parts = (uint32_t)we;
-        const uint32_t part_base = we > 1 ? parts : 0;
-        for (uint64_t j = 0; j < we; j++) {
-            const uint64_t tb = cuts[i][j], te = cuts[i][j + 1];
-            const uint64_t rb = key_begin[i] + tb * kTileKeys;
-            const uint64_t re = key_begin[i] + te * kTileKeys;
-            StepWorkDev w{};
-            w.row_begin = (uint32_t)rb;
-            w.row_end = (uint32_t)(re < d.key_end ? re : d.key_end);
-            w.part = we > 1 ? part_base + (uint32_t)j : 0u;
-            w.entry = i;
-            work.push_back(w);
-        }
-        if (we > max_parts) max_parts = (uint32_t)we;
-        if (we > 1) {
-            parts += (uint32_t)we;
-            merge.push_back(DecodeEntryDev{nullptr, nullptr, nullptr, d.out, 0, 0, part_base, (uint32_t)we, 0.0f, 0});
-        }
-    }
-    if (parts > kStepMaxWgs || work.size() > cap)
-        return fail(G4_EINVAL, "attnStep: internal: %u partial records, %zu items", parts, work.size());
     const StepLayout L = step_layout(n_entries, num_kv_heads, G, head_dim);
-    hipStream_t st = as_stream(stream);
     char* ws = static_cast<char*>(workspace);
-    // RoPE factors of each (inverse-frequency table, position) in use: the
-    // reference's cos/sin of the f32 angle, evaluated in f64 and rounded.
-    std::vector<float> rope;
-    {
-        std::map<std::pair<const float*, uint32_t>, uint32_t> seen;
-        const uint32_t half = head_dim / 2;
-        for (uint32_t i = 0; i < n_entries; i++) {
-            const g4_step_entry& s = entries[i];
-            if (!s.rope_inv_freq_host) continue;
-            const auto key = std::make_pair(s.rope_inv_freq_host, s.position);
-            auto it = seen.find(key);
-            uint32_t idx;
-            if (it != seen.end()) {
-                idx = it->second;
-            } else {
-                idx = (uint32_t)seen.size();
-                seen.emplace(key, idx);
-                rope.resize((size_t)(idx + 1) * head_dim);
-                float* c = rope.data() + (size_t)idx * head_dim;
-                for (uint32_t p = 0; p < half; p++) {
-                    const float ang = (float)s.position * s.rope_inv_freq_host[p];
-                    c[p] = (float)cos((double)ang);
-                    c[half + p] = (float)sin((double)ang);
-                }
-            }
-            tab[i].rope_cs = reinterpret_cast<const float*>(ws + L.rope) + (size_t)idx * head_dim;
-        }
-    }
-    for (StepWorkDev& w : work) w.ent = tab[w.entry];  // entries complete (parts, RoPE factors)
-    rc = stage_upload(ws + L.rope, rope.data(), rope.size() * sizeof(float), st);
+    StepPlanHost ph;
+    char err[256];
+    rc = plan_step(entries, n_entries, num_q_heads, num_kv_heads, head_dim, device_cus(), tune, ws + L.tables, &ph,
+                   err, sizeof err);
+    if (rc) return fail(rc, "%s", err);
+    rc = stage_upload(ws + L.tables, ph.blob.data(), ph.blob.size(), as_stream(stream));  // the tables in one copy
     if (rc) return rc;
-    rc = stage_upload(ws + L.work, work.data(), work.size() * sizeof(StepWorkDev), st);
-    if (rc) return rc;
-    const uint32_t n_merge = (uint32_t)merge.size();
-    if (n_merge) {
-        rc = stage_upload(ws + L.merge_table, merge.data(), (size_t)n_merge * sizeof(DecodeEntryDev), st);
-        if (rc) return rc;
-    }
-    StepPlanRep r = {ws,       n_entries, (uint32_t)work.size(), num_kv_heads, G, n_merge, max_parts,
-                     waves,    head_dim,  kStepMagic};
+    StepPlanRep r = {ws,       n_entries, ph.n_wgs, num_kv_heads, G, ph.n_merge, ph.max_parts,
+                     ph.waves, head_dim,  kStepMagic, (uint32_t)ph.off_merge, (uint32_t)ph.off_rope};
     memset(plan, 0, sizeof *plan);
     memcpy(plan, &r, sizeof r);
     return G4_OK;
@@ -559,7 +339,7 @@ static int launch_attention(const g4_decode_plan* plan, void* stream, hipEvent_t
     if (rc) return rc;
     const StepLayout L = step_layout(r.n_entries, r.num_kv_heads, r.group, r.head_dim);
     StepArgs a = {};
-    a.work = reinterpret_cast<const StepWorkDev*>(r.ws + L.work);
+    a.work = reinterpret_cast<const StepWorkDev*>(r.ws + L.tables);
     a.num_kv_heads = r.num_kv_heads;
     a.group = r.group;
     a.part_ml = reinterpret_cast<float*>(r.ws + L.part_ml);
@@ -602,7 +382,7 @@ int g4_attn_step_run_merge(const g4_decode_plan* plan, void* stream) {
     if (!r.n_merge) return G4_OK;
     const StepLayout L = step_layout(r.n_entries, r.num_kv_heads, r.group, r.head_dim);
     DecodeArgs m = {};
-    m.table = reinterpret_cast<const DecodeEntryDev*>(r.ws + L.merge_table);
+    m.table = reinterpret_cast<const DecodeEntryDev*>(r.ws + L.tables + r.off_merge);
     m.n_entries = r.n_merge;
     m.num_kv_heads = r.num_kv_heads;
     m.group = r.group;

@@ -1,0 +1,260 @@
+// Host-side planning of the one-launch decode step (step.hip): argument
+// checks, the partition of every entry's attended rows into workgroups, the
+// merge table, the token's RoPE factors and the workspace layout. Plain C++
+// (no HIP), so the same code runs in CPU-only test programs.
+//
+// Partition: each entry's attended rows become 32-row tiles; the planner
+// picks the smallest tiles-per-workgroup such that the entries' workgroups
+// (sum over entries of ceil(tiles / tpw)) fit one wave of the GPU, and cuts
+// each entry into that many balanced, contiguous row ranges. A workgroup never
+// spans two entries. An entry cut into more than one part writes partial
+// records, listed in the merge table for the log-sum-exp merge launch.
+#pragma once
+
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <map>
+#include <utility>
+#include <vector>
+
+#include "../../include/g4attn.h"
+#include "tables.h"
+
+namespace g4 {
+
+// Partial records: an entry gets more than one workgroup only while the
+// workgroups fit one wave of the GPU (at most kStepMaxWgs), so at most that
+// many records exist.
+constexpr unsigned kStepMaxWgs = 1024;
+constexpr unsigned kStepOneWgTiles = 16;  // one workgroup per CU up to this many tiles each
+
+inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// The tables region holds, packed by each prepare and uploaded in one copy,
+// the work table, the merge table and the RoPE factors (their offsets are in
+// the plan); the partial records follow at a fixed offset.
+struct StepLayout {
+    size_t tables, part_ml, part_o, total;
+};
+
+inline StepLayout step_layout(uint64_t n, uint64_t nkh, uint64_t group, uint64_t hd) {
+    StepLayout L;
+    const uint64_t max_items = n > kStepMaxWgs ? n : kStepMaxWgs;
+    const uint64_t recs = (uint64_t)kStepMaxWgs * nkh * group;
+    size_t off = 0;
+    L.tables = off;  // work items, merge entries, and at most one [cos x hd/2][sin x hd/2] set per entry
+    off += align256(max_items * sizeof(StepWorkDev)) + align256(n * sizeof(DecodeEntryDev)) + align256(n * hd * 4);
+    L.part_ml = off;
+    off += align256(recs * 2 * 4);
+    L.part_o = off;
+    off += align256(recs * hd * 4);
+    L.total = off;
+    return L;
+}
+
+// Smallest tiles-per-workgroup with sum_e ceil(tiles_e / tpw) <= cap (cap >= n,
+// so tpw = max tiles always fits).
+inline uint64_t pick_tiles_per_wg(const std::vector<uint32_t>& tiles, uint64_t total, uint64_t max_tiles,
+                                  uint64_t cap) {
+    auto wgs = [&](uint64_t tpw) {
+        uint64_t s = 0;
+        for (uint32_t t : tiles) s += (t + tpw - 1) / tpw;
+        return s;
+    };
+    uint64_t lo = (total + cap - 1) / cap, hi = max_tiles;
+    if (lo < 1) lo = 1;
+    if (lo > hi) lo = hi;
+    while (lo < hi) {
+        const uint64_t mid = (lo + hi) / 2;
+        if (wgs(mid) <= cap) hi = mid;
+        else lo = mid + 1;
+    }
+    return lo;
+}
+
+// Overrides of the grid choice (0 = the default rule).
+struct StepTuning {
+    int waves = 0;       // 4 or 8 waves per workgroup (head_dim 256)
+    int wgs_per_cu = 0;  // workgroups per CU
+    int max_wgs = 0;     // cap on the workgroups of the launch
+};
+
+struct StepPlanHost {
+    uint32_t waves = 0;      // waves per workgroup of the attention kernel
+    uint32_t n_wgs = 0;      // workgroups (work items)
+    uint32_t n_merge = 0;    // entries in the merge table
+    uint32_t max_parts = 0;  // largest part count of an entry
+    uint32_t parts = 0;      // partial-record slots in use
+    size_t off_merge = 0;    // byte offsets in the tables blob
+    size_t off_rope = 0;
+    std::vector<char> blob;  // work table | merge table | RoPE factors, ready to upload to the tables region
+};
+
+// Checks the step's arguments and plans it. `tables` is the device address of
+// the workspace's tables region (the entries' RoPE-factor pointers point into
+// it); `cus` the device's compute units. On failure returns a G4_ status and
+// writes a message to err.
+inline int plan_step(const g4_step_entry* entries, uint32_t n_entries, uint32_t num_q_heads, uint32_t num_kv_heads,
+                     uint32_t head_dim, uint64_t cus, const StepTuning& tune, const char* tables, StepPlanHost* out,
+                     char* err, size_t errlen) {
+#define PLAN_FAIL(code, ...)                   \
+    do {                                       \
+        snprintf(err, errlen, __VA_ARGS__);    \
+        return code;                           \
+    } while (0)
+    if (head_dim != 256 && head_dim != 512) PLAN_FAIL(G4_EINVAL, "attnStep: head_dim %u unsupported (256 or 512)", head_dim);
+    if (num_kv_heads == 0 || num_q_heads % num_kv_heads || num_q_heads / num_kv_heads > (uint32_t)kMaxGroup)
+        PLAN_FAIL(G4_EINVAL, "attnStep: %u query heads over %u kv heads unsupported", num_q_heads, num_kv_heads);
+    if (num_kv_heads > 65535) PLAN_FAIL(G4_EINVAL, "attnStep: %u kv heads (max 65535)", num_kv_heads);
+    if (!entries || n_entries == 0) PLAN_FAIL(G4_EINVAL, "attnStep: no entries");
+    if (n_entries > 65535) PLAN_FAIL(G4_EINVAL, "attnStep: %u entries (max 65535)", n_entries);
+    const uint64_t row_bytes = (uint64_t)num_kv_heads * head_dim * 2;
+    std::vector<StepEntryDev> tab(n_entries);
+    std::vector<uint32_t> key_begin(n_entries), tiles(n_entries);
+    uint64_t T = 0, max_tiles = 0;
+    for (uint32_t i = 0; i < n_entries; i++) {
+        const g4_step_entry& s = entries[i];
+        if (!s.q || !s.q_weight || !s.k_cache || !s.v_cache || !s.out)
+            PLAN_FAIL(G4_EINVAL, "attnStep: entry %u has a NULL pointer", i);
+        const bool cached = !s.k && !s.v && !s.k_weight;  // consumer whose producer stored the row already
+        if (!cached && (!s.k || !s.v || !s.k_weight))
+            PLAN_FAIL(G4_EINVAL, "attnStep: entry %u: k, v and k_weight are all set or all NULL", i);
+        if (cached && s.store_kv) PLAN_FAIL(G4_EINVAL, "attnStep: entry %u: store_kv needs the raw k and v", i);
+        if (reinterpret_cast<uintptr_t>(s.out) & 15)
+            PLAN_FAIL(G4_EINVAL, "attnStep: entry %u out must be 16-byte aligned", i);
+        if (s.apply_divisor && !s.rope_freqs) PLAN_FAIL(G4_EINVAL, "attnStep: entry %u needs rope_freqs", i);
+        if (s.seq_len == 0) PLAN_FAIL(G4_EINVAL, "attnStep: entry %u seq_len 0", i);
+        if ((uint64_t)s.seq_len * row_bytes > 0xffffffffull)
+            PLAN_FAIL(G4_EINVAL, "attnStep: entry %u cache exceeds 4 GiB", i);
+        StepEntryDev& d = tab[i];
+        d = StepEntryDev{};
+        d.q = s.q;
+        // Cached rows: the kernel's unconditional loads of k, v and k_weight read q and q_weight
+        // instead (valid addresses; the values are not used).
+        d.k = cached ? s.q : s.k;
+        d.v = cached ? s.q : s.v;
+        d.q_weight = s.q_weight;
+        d.k_weight = cached ? s.q_weight : s.k_weight;
+        d.rope_freqs = s.rope_freqs;
+        d.k_cache = s.k_cache;
+        d.v_cache = s.v_cache;
+        d.out = s.out;
+        d.key_end = s.seq_len;
+        d.position = s.position;
+        d.flags = (s.store_kv ? kStoreKv : 0u) | (cached ? kRowCached : 0u);
+        d.theta = s.theta;
+        d.apply_divisor = s.apply_divisor;
+        d.qscale = s.scale * kLog2e;
+        d.eps = s.eps;
+        key_begin[i] = (s.sliding_window != 0 && s.seq_len > s.sliding_window) ? s.seq_len - s.sliding_window : 0;
+        tiles[i] = (s.seq_len - key_begin[i] + kTileKeys - 1) / kTileKeys;
+        T += tiles[i];
+        if (tiles[i] > max_tiles) max_tiles = tiles[i];
+    }
+    // Workgroups in one wave of the GPU. Small steps (at most kStepOneWgTiles
+    // tiles per workgroup with one workgroup per CU) take one 8-wave
+    // workgroup per CU: two tile rounds per wave at most, one partial record
+    // per CU. Larger steps take two 4-wave workgroups per CU. Measured (us,
+    // two 4-wave / one 4-wave / one 8-wave per CU): stack8k 24.0 / 22.3 / 21.9,
+    // long128k 34.4 / 32.0 / 31.5, stack32k 48.9 / 56.0 / 55.7, ragged64
+    // 190.9 / 199.6 / 197.8. A second workgroup per CU starts behind the first
+    // and is served after it, which only pays off when the per-wave rounds
+    // are many; grids between one and two per CU are slower than both (CUs
+    // with two workgroups finish last). head_dim 512 has one form: one 4-wave
+    // workgroup per CU.
+    if (cus < 1) cus = 1;
+    const bool small = T <= (uint64_t)kStepOneWgTiles * (cus / num_kv_heads);
+    const uint32_t waves = head_dim == 512 ? 4u
+                           : tune.waves == 4 || tune.waves == 8 ? (uint32_t)tune.waves
+                                                                 : (small ? 8u : 4u);
+    const uint64_t per_cu = head_dim == 512 ? 1u
+                            : tune.wgs_per_cu > 0 ? (uint64_t)tune.wgs_per_cu
+                                                  : (waves == 8 || small ? 1u : 2u);
+    uint64_t fit = tune.max_wgs > 0 ? (uint64_t)tune.max_wgs / num_kv_heads : per_cu * cus / num_kv_heads;
+    if (fit > kStepMaxWgs) fit = kStepMaxWgs;
+    if (fit < 1) fit = 1;
+    const uint64_t cap = fit > n_entries ? fit : n_entries;
+    const uint64_t tpw = pick_tiles_per_wg(tiles, T, max_tiles, cap);
+
+    // Work items entry by entry: tpw tiles per item, balanced within an entry.
+    std::vector<StepWorkDev> work;
+    work.reserve(cap);
+    std::vector<DecodeEntryDev> merge;  // only the entries with partial records: the merge grid covers them alone
+    merge.reserve(n_entries);
+    uint32_t parts = 0, max_parts = 0;
+    for (uint32_t i = 0; i < n_entries; i++) {
+        StepEntryDev& d = tab[i];
+        const uint64_t ne = tiles[i], we = (ne + tpw - 1) / tpw;
+        d.n_parts = (uint32_t)we;
+        const uint32_t part_base = we > 1 ? parts : 0;
+        for (uint64_t j = 0; j < we; j++) {
+            const uint64_t tb = j * ne / we, te = (j + 1) * ne / we;
+            const uint64_t rb = key_begin[i] + tb * kTileKeys;
+            const uint64_t re = key_begin[i] + te * kTileKeys;
+            StepWorkDev w{};
+            w.row_begin = (uint32_t)rb;
+            w.row_end = (uint32_t)(re < d.key_end ? re : d.key_end);
+            w.part = we > 1 ? part_base + (uint32_t)j : 0u;
+            w.entry = i;
+            work.push_back(w);
+        }
+        if (we > max_parts) max_parts = (uint32_t)we;
+        if (we > 1) {
+            parts += (uint32_t)we;
+            merge.push_back(DecodeEntryDev{nullptr, nullptr, nullptr, d.out, 0, 0, part_base, (uint32_t)we, 0.0f, 0});
+        }
+    }
+    if (parts > kStepMaxWgs || work.size() > cap)
+        PLAN_FAIL(G4_EINVAL, "attnStep: internal: %u partial records, %zu items", parts, work.size());
+
+    // Tables blob: work items | merge table | RoPE factors.
+    const size_t off_merge = align256(work.size() * sizeof(StepWorkDev));
+    const size_t off_rope = off_merge + align256(merge.size() * sizeof(DecodeEntryDev));
+    // RoPE factors of each (inverse-frequency table, position) in use: the
+    // reference's cos/sin of the f32 angle, evaluated in f64 and rounded.
+    std::vector<float> rope;
+    {
+        std::map<std::pair<const float*, uint32_t>, uint32_t> seen;
+        const uint32_t half = head_dim / 2;
+        for (uint32_t i = 0; i < n_entries; i++) {
+            const g4_step_entry& s = entries[i];
+            if (!s.rope_inv_freq_host) continue;
+            const auto key = std::make_pair(s.rope_inv_freq_host, s.position);
+            auto it = seen.find(key);
+            uint32_t idx;
+            if (it != seen.end()) {
+                idx = it->second;
+            } else {
+                idx = (uint32_t)seen.size();
+                seen.emplace(key, idx);
+                rope.resize((size_t)(idx + 1) * head_dim);
+                float* c = rope.data() + (size_t)idx * head_dim;
+                for (uint32_t p = 0; p < half; p++) {
+                    const float ang = (float)s.position * s.rope_inv_freq_host[p];
+                    c[p] = (float)cos((double)ang);
+                    c[half + p] = (float)sin((double)ang);
+                }
+            }
+            tab[i].rope_cs = reinterpret_cast<const float*>(tables + off_rope) + (size_t)idx * head_dim;
+        }
+    }
+    for (StepWorkDev& w : work) w.ent = tab[w.entry];  // entries complete (parts, RoPE factors)
+    out->blob.assign(off_rope + rope.size() * sizeof(float), 0);
+    memcpy(out->blob.data(), work.data(), work.size() * sizeof(StepWorkDev));
+    if (!merge.empty()) memcpy(out->blob.data() + off_merge, merge.data(), merge.size() * sizeof(DecodeEntryDev));
+    if (!rope.empty()) memcpy(out->blob.data() + off_rope, rope.data(), rope.size() * sizeof(float));
+    out->waves = waves;
+    out->n_wgs = (uint32_t)work.size();
+    out->n_merge = (uint32_t)merge.size();
+    out->max_parts = max_parts;
+    out->parts = parts;
+    out->off_merge = off_merge;
+    out->off_rope = off_rope;
+    return G4_OK;
+#undef PLAN_FAIL
+}
+
+}  // namespace g4

@@ -1,0 +1,144 @@
+// CPU check of the one-launch step's host planner (gemma4-webgpu_amd/csrc/step_plan.h), built with g++
+// under AddressSanitizer and UndefinedBehaviorSanitizer by tests/test_step_plan.py. Reads scenarios from
+// stdin, one per line:
+//   nqh nkh hd cus seq:window[:c] ...      (c: a KV-consumer entry whose row is already cached)
+// plans each and checks the plan's invariants; prints "ok <n_wgs> <n_merge>" per scenario, or an error
+// and exits 1.
+#include <stdio.h>
+#include <string.h>
+
+#include <iostream>
+#include <sstream>
+#include <string>
+#include <vector>
+
+#include "../gemma4-webgpu_amd/csrc/step_plan.h"
+
+using namespace g4;
+
+static int bad(int line, const char* what) {
+    printf("FAIL line %d: %s\n", line, what);
+    return 1;
+}
+
+int main() {
+    std::string text;
+    int line = 0;
+    // Fake device addresses: the planner stores them and never dereferences them.
+    char* const dev = reinterpret_cast<char*>(uintptr_t(1) << 40);
+    while (std::getline(std::cin, text)) {
+        line++;
+        std::istringstream in(text);
+        uint32_t nqh, nkh, hd, cus;
+        if (!(in >> nqh >> nkh >> hd >> cus)) continue;
+        std::vector<g4_step_entry> ents;
+        std::vector<std::vector<float>> inv;  // host RoPE tables (read by the planner)
+        std::string tok;
+        while (in >> tok) {
+            uint32_t seq = 0, win = 0;
+            char c = 0;
+            sscanf(tok.c_str(), "%u:%u:%c", &seq, &win, &c);
+            g4_step_entry e{};
+            const uintptr_t base = uintptr_t(ents.size() + 1) << 32;
+            e.q = reinterpret_cast<const float*>(base + 0x1000);
+            e.q_weight = reinterpret_cast<const uint16_t*>(base + 0x2000);
+            if (c != 'c') {
+                e.k = reinterpret_cast<const float*>(base + 0x3000);
+                e.v = reinterpret_cast<const float*>(base + 0x4000);
+                e.k_weight = reinterpret_cast<const uint16_t*>(base + 0x5000);
+                e.store_kv = 1;
+            }
+            e.k_cache = reinterpret_cast<uint16_t*>(base + 0x10000000);
+            e.v_cache = reinterpret_cast<uint16_t*>(base + 0x20000000);
+            e.out = reinterpret_cast<float*>(base + 0x30000000);
+            e.seq_len = seq;
+            e.position = seq - 1;
+            e.sliding_window = win;
+            e.theta = win ? 1e4f : 1e6f;
+            e.apply_divisor = win ? 0 : 1;
+            e.rope_freqs = reinterpret_cast<const uint16_t*>(base + 0x6000);
+            e.scale = 1.0f;
+            e.eps = 1e-6f;
+            if (ents.size() % 2 == 0) {  // every other entry carries a host RoPE table
+                inv.emplace_back(hd / 2);
+                for (uint32_t i = 0; i < hd / 2; i++) inv.back()[i] = 1.0f / (float)(i + 1);
+            }
+            ents.push_back(e);
+        }
+        // attach the tables after the vector stopped growing (pointers stay valid)
+        for (size_t i = 0, t = 0; i < ents.size(); i += 2, t++) ents[i].rope_inv_freq_host = inv[t].data();
+        const uint32_t n = (uint32_t)ents.size();
+        const StepLayout L = step_layout(n, nkh, nqh / nkh, hd);
+        StepPlanHost ph;
+        char err[256] = "";
+        const int rc = plan_step(ents.data(), n, nqh, nkh, hd, cus, StepTuning{}, dev + L.tables, &ph, err,
+                                 sizeof err);
+        if (rc) {
+            printf("FAIL line %d: plan_step: %s\n", line, err);
+            return 1;
+        }
+        // the blob fits the tables region, and its parts do not overlap
+        if (ph.blob.size() > L.part_ml - L.tables) return bad(line, "tables blob exceeds the tables region");
+        if (ph.off_merge < ph.n_wgs * sizeof(StepWorkDev)) return bad(line, "merge table overlaps the work table");
+        if (ph.off_rope < ph.off_merge + ph.n_merge * sizeof(DecodeEntryDev)) return bad(line, "rope overlaps merge");
+        const size_t cap = n > kStepMaxWgs ? n : kStepMaxWgs;
+        if (ph.n_wgs > cap) return bad(line, "more work items than the workspace holds");
+        if (ph.parts > kStepMaxWgs) return bad(line, "more partial records than the workspace holds");
+        const StepWorkDev* work = reinterpret_cast<const StepWorkDev*>(ph.blob.data());
+        const DecodeEntryDev* merge = reinterpret_cast<const DecodeEntryDev*>(ph.blob.data() + ph.off_merge);
+        const size_t rope_bytes = ph.blob.size() - ph.off_rope;
+        std::vector<std::vector<const StepWorkDev*>> per(n);
+        for (uint32_t w = 0; w < ph.n_wgs; w++) {
+            if (work[w].entry >= n) return bad(line, "work item names no entry");
+            per[work[w].entry].push_back(&work[w]);
+        }
+        std::vector<char> slot_used(ph.parts, 0);
+        uint32_t n_split = 0;
+        for (uint32_t i = 0; i < n; i++) {
+            const g4_step_entry& e = ents[i];
+            const uint32_t kb = (e.sliding_window && e.seq_len > e.sliding_window) ? e.seq_len - e.sliding_window : 0;
+            const auto& items = per[i];
+            if (items.empty()) return bad(line, "entry without workgroups");
+            uint32_t next = kb;
+            for (size_t j = 0; j < items.size(); j++) {  // items of an entry are consecutive, in row order
+                const StepWorkDev& w = *items[j];
+                if (w.row_begin != next || w.row_end <= w.row_begin) return bad(line, "rows not covered once, in order");
+                if (w.row_end > e.seq_len) return bad(line, "rows past seq_len");
+                if (w.ent.n_parts != items.size()) return bad(line, "n_parts disagrees with the work items");
+                if (w.ent.key_end != e.seq_len || w.ent.position != e.position || w.ent.out != e.out ||
+                    w.ent.k_cache != e.k_cache)
+                    return bad(line, "entry copy differs from the entry");
+                const bool cached = !e.k;
+                if (cached != ((w.ent.flags & kRowCached) != 0) || (w.ent.flags & kStoreKv) != (e.store_kv ? kStoreKv : 0))
+                    return bad(line, "flags");
+                if (items.size() > 1) {
+                    if (w.part >= ph.parts || slot_used[w.part]) return bad(line, "partial-record slot reused or out of range");
+                    slot_used[w.part] = 1;
+                }
+                if (e.rope_inv_freq_host) {
+                    const char* rc_ptr = reinterpret_cast<const char*>(w.ent.rope_cs);
+                    const char* r0 = dev + L.tables + ph.off_rope;
+                    if (rc_ptr < r0 || rc_ptr + hd * 4 > r0 + rope_bytes || (rc_ptr - r0) % (hd * 4))
+                        return bad(line, "RoPE factor pointer outside the factors");
+                } else if (w.ent.rope_cs) {
+                    return bad(line, "RoPE factors without a host table");
+                }
+                next = w.row_end;
+            }
+            if (next != e.seq_len) return bad(line, "attended rows not fully covered");
+            if (items.size() > 1) {
+                bool found = false;
+                for (uint32_t m = 0; m < ph.n_merge; m++)
+                    if (merge[m].out == e.out) {
+                        found = merge[m].n_splits == items.size() && merge[m].split_base == items[0]->part;
+                        break;
+                    }
+                if (!found) return bad(line, "split entry missing from the merge table");
+                n_split++;
+            }
+        }
+        if (n_split != ph.n_merge) return bad(line, "merge table lists entries that are not split");
+        printf("ok %u %u\n", ph.n_wgs, ph.n_merge);
+    }
+    return 0;
+}
