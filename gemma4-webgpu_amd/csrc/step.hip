@@ -40,6 +40,7 @@
 #include <hip/hip_ext.h>
 
 #include <map>
+#include <type_traits>
 #include <utility>
 #include <vector>
 
@@ -109,131 +110,148 @@ __global__ __launch_bounds__(64 * W, HD == 256 ? 8 / W : 1) void k_attn_step(
     const unsigned nkeys = k1t - k0;
     const unsigned last = nkeys ? k1t - 1 : k0;  // loads are clamped to it (k0 < key_end: in the cache)
 
-    // ---- small operands first, then the first tile ----
-    // Every load is unconditional (clamped to valid addresses where the value
-    // is not needed): with loads under branches the compiler cannot count the
-    // younger loads on every path, and its wait for a small operand would also
-    // wait for the tile. f16 values stay unconverted until used.
-    // RoPE factors of this lane's pairs from the host table; absent tables are
-    // replaced by valid dummy addresses (the values are not used).
-    const float* rcs = ent.rope_cs;
-    const float* rsrc = rcs ? rcs : ent.q;
-    RopeLane<PJ> rl;
-#pragma unroll
-    for (int p = 0; p < PJ; p++) {
-        rl.c[p] = ldg<float>(rsrc + lane + 64 * p);
-        rl.s[p] = ldg<float>(rsrc + HD / 2 + lane + 64 * p);
-    }
-    const unsigned pair = threadIdx.x % (HD / 2);  // pair evaluated by this thread otherwise
-    const unsigned apply_divisor = ent.apply_divisor;
-    const uint32_t fbits = ldg<uint16_t>((apply_divisor ? ent.rope_freqs : ent.q_weight) + pair);
-    float xq[kQPerWave][J];
-#pragma unroll
-    for (int r = 0; r < kQPerWave; r++) {
-        const unsigned hq = min((unsigned)wave + W * r, G - 1);
-        const float* src = ent.q + ((uint64_t)kvh * G + hq) * HD;
-#pragma unroll
-        for (int j = 0; j < J; j++) xq[r][j] = ldg<float>(src + lane + 64 * j);
-    }
-    uint32_t wq[J], wn[J];
-#pragma unroll
-    for (int j = 0; j < J; j++) wq[j] = ldg<uint16_t>(ent.q_weight + lane + 64 * j);
-    const bool do_new = has_new && wave < 2;  // wave 0: k, wave 1: v
-    float xn[J];
-    {
-        const float* src = (wave == 1 ? ent.v : ent.k) + (uint64_t)kvh * HD;
-#pragma unroll
-        for (int j = 0; j < J; j++) xn[j] = ldg<float>(src + lane + 64 * j);
-#pragma unroll
-        for (int j = 0; j < J; j++) wn[j] = ldg<uint16_t>(ent.k_weight + lane + 64 * j);
-    }
-    const uint32_t row_bytes = NKH * HD * 2u;
-    const char* Kb = reinterpret_cast<const char*>(ent.k_cache + (uint64_t)kvh * HD);
-    const char* Vb = reinterpret_cast<const char*>(ent.v_cache + (uint64_t)kvh * HD);
     constexpr unsigned kStride = W * kTileKeys;
-    unsigned t0 = (unsigned)wave * kTileKeys;  // a wave without a tile reads row `last` and discards it
-    f16x8 kreg[2][D::NC];
-    u32x4 vreg[D::NB][8];
-    load_k_tile<HD>(Kb, row_bytes, last, n, g, k0 + t0, kreg);
-    load_v_tile<HD>(Vb, row_bytes, last, n, g, k0 + t0, vreg);
-    __builtin_amdgcn_sched_barrier(0);  // keep every request above ahead of the arithmetic below
-
-    // ---- q heads straight into the score operand; the current row's k and v ----
-    if (!rcs) {  // uniform: one pair per thread, the reference's expressions with f64
-        // transcendentals; division by 1 is exact, so the load above stays unconditional
-        const float freq = rope_inv_freq(pair, HD, ent.theta, 1u, apply_divisor ? h2f((uint16_t)fbits) : 1.0f);
-        const float ang = (float)ent.position * freq;
-        const float c = (float)cos((double)ang);
-        const float sn = (float)sin((double)ang);
-        if (threadIdx.x < HD / 2) {
-            sm.rope_c[pair] = c;
-            sm.rope_s[pair] = sn;
-        }
-        __syncthreads();
-#pragma unroll
-        for (int p = 0; p < PJ; p++) {
-            rl.c[p] = sm.rope_c[lane + 64 * p];
-            rl.s[p] = sm.rope_s[lane + 64 * p];
-        }
-    }
-
-    const float qscale = ent.qscale, eps = ent.eps;
-    f16* qop = reinterpret_cast<f16*>(sm.dec.q);  // [chunk c][operand lane 16*g + column][8]
-#pragma unroll
-    for (int r = 0; r < kQPerWave; r++) {
-        const unsigned hq = (unsigned)wave + W * r;
-        const bool live = hq < G;  // columns of absent heads are zero
-        if (live) wave_norm_rope<J>(xq[r], wq, true, true, rl, eps);
-#pragma unroll
-        for (int j = 0; j < J; j++) {
-            const unsigned d = (unsigned)lane + 64u * j;
-            const float x = live ? xq[r][j] * qscale : 0.0f;
-            if (live) sm.qf[hq][d] = x;
-            const f16 hi = (f16)x;  // hi in column hq, the f16 residual in column hq + 8
-            const unsigned base = ((d >> 5) * 64u + 16u * ((d >> 3) & 3u) + hq) * 8u + (d & 7u);
-            qop[base] = hi;
-            qop[base + 64] = (f16)(x - (float)hi);
-        }
-    }
-    if (do_new) {
-        const bool is_k = wave == 0;
-        wave_norm_rope<J>(xn, wn, is_k, is_k, rl, eps);
-        uint16_t* row = reinterpret_cast<uint16_t*>(is_k ? sm.knew : sm.vnew);
-#pragma unroll
-        for (int j = 0; j < J; j++) row[lane + 64 * j] = f2h(xn[j]);
-        if (ent.flags & kStoreKv) {
-            uint16_t* dst = (is_k ? ent.k_cache : ent.v_cache) + ((uint64_t)new_row * NKH + kvh) * HD;
-#pragma unroll
-            for (int j = 0; j < J; j++) stg<uint16_t>(dst + lane + 64 * j, f2h(xn[j]));
-        }
-    }
-    __syncthreads();
-
-    // The current row's scores (read by the combine, after later barriers).
-    if (has_new) {
-        const f16* kn = reinterpret_cast<const f16*>(sm.knew);
-        for (unsigned h = (unsigned)wave; h < G; h += W) {
-            float p = 0.0f;
-#pragma unroll
-            for (int j = 0; j < J; j++) p += sm.qf[h][lane + 64 * j] * (float)kn[lane + 64 * j];
-            for (int off = 32; off > 0; off >>= 1) p += __shfl_xor(p, off);
-            if (lane == 0) sm.mnew[h] = p;
-        }
-    }
-
-    // ---- tiles ----
+    unsigned t0 = (unsigned)wave * kTileKeys;
     float m_run = -INFINITY, l_run = 0.0f;
     f32x4 acc[D::NO];
 #pragma unroll
     for (int i = 0; i < D::NO; i++) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-    if (t0 < nkeys) {  // the first tile was requested above; the loop requests its own
-        tile_step<HD>(sm.dec, lane, g, lo_col, k0 + t0, k1t, kreg, vreg, m_run, l_run, acc);
-        for (t0 += kStride; t0 < nkeys; t0 += kStride) {
+
+    // The prologue and the tiles, as two straight-line copies: waves with a
+    // first tile and waves without one (short parts: a one-tile part leaves
+    // seven of eight waves without rows). Within one copy every load is
+    // unconditional (clamped to valid addresses where the value is not needed):
+    // with loads under branches the compiler cannot count the younger loads on
+    // every path, and its wait for a small operand would also wait for the
+    // tile. A wave without rows issues no tile loads at all: a CU's load path
+    // takes the same time for a clamped load as for a real one (~0.2 us per
+    // wave and tile at head_dim 256), which would delay the one real tile.
+    // Both copies meet the same barriers in the same order.
+    auto body = [&](auto tile_tag) {
+        constexpr bool kTile = decltype(tile_tag)::value;
+        // ---- small operands first, then the first tile ----
+        // f16 values stay unconverted until used. RoPE factors of this lane's
+        // pairs from the host table; absent tables are replaced by valid dummy
+        // addresses (the values are not used).
+        const float* rcs = ent.rope_cs;
+        const float* rsrc = rcs ? rcs : ent.q;
+        RopeLane<PJ> rl;
+#pragma unroll
+        for (int p = 0; p < PJ; p++) {
+            rl.c[p] = ldg<float>(rsrc + lane + 64 * p);
+            rl.s[p] = ldg<float>(rsrc + HD / 2 + lane + 64 * p);
+        }
+        const unsigned pair = threadIdx.x % (HD / 2);  // pair evaluated by this thread otherwise
+        const unsigned apply_divisor = ent.apply_divisor;
+        const uint32_t fbits = ldg<uint16_t>((apply_divisor ? ent.rope_freqs : ent.q_weight) + pair);
+        float xq[kQPerWave][J];
+#pragma unroll
+        for (int r = 0; r < kQPerWave; r++) {
+            const unsigned hq = min((unsigned)wave + W * r, G - 1);
+            const float* src = ent.q + ((uint64_t)kvh * G + hq) * HD;
+#pragma unroll
+            for (int j = 0; j < J; j++) xq[r][j] = ldg<float>(src + lane + 64 * j);
+        }
+        uint32_t wq[J], wn[J];
+#pragma unroll
+        for (int j = 0; j < J; j++) wq[j] = ldg<uint16_t>(ent.q_weight + lane + 64 * j);
+        const bool do_new = has_new && wave < 2;  // wave 0: k, wave 1: v
+        float xn[J];
+        {
+            const float* src = (wave == 1 ? ent.v : ent.k) + (uint64_t)kvh * HD;
+#pragma unroll
+            for (int j = 0; j < J; j++) xn[j] = ldg<float>(src + lane + 64 * j);
+#pragma unroll
+            for (int j = 0; j < J; j++) wn[j] = ldg<uint16_t>(ent.k_weight + lane + 64 * j);
+        }
+        const uint32_t row_bytes = NKH * HD * 2u;
+        const char* Kb = reinterpret_cast<const char*>(ent.k_cache + (uint64_t)kvh * HD);
+        const char* Vb = reinterpret_cast<const char*>(ent.v_cache + (uint64_t)kvh * HD);
+        f16x8 kreg[2][D::NC];
+        u32x4 vreg[D::NB][8];
+        if constexpr (kTile) {
             load_k_tile<HD>(Kb, row_bytes, last, n, g, k0 + t0, kreg);
             load_v_tile<HD>(Vb, row_bytes, last, n, g, k0 + t0, vreg);
-            tile_step<HD>(sm.dec, lane, g, lo_col, k0 + t0, k1t, kreg, vreg, m_run, l_run, acc);
         }
-    }
+        __builtin_amdgcn_sched_barrier(0);  // keep every request above ahead of the arithmetic below
+
+        // ---- q heads straight into the score operand; the current row's k and v ----
+        if (!rcs) {  // uniform: one pair per thread, the reference's expressions with f64
+            // transcendentals; division by 1 is exact, so the load above stays unconditional
+            const float freq = rope_inv_freq(pair, HD, ent.theta, 1u, apply_divisor ? h2f((uint16_t)fbits) : 1.0f);
+            const float ang = (float)ent.position * freq;
+            const float c = (float)cos((double)ang);
+            const float sn = (float)sin((double)ang);
+            if (threadIdx.x < HD / 2) {
+                sm.rope_c[pair] = c;
+                sm.rope_s[pair] = sn;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int p = 0; p < PJ; p++) {
+                rl.c[p] = sm.rope_c[lane + 64 * p];
+                rl.s[p] = sm.rope_s[lane + 64 * p];
+            }
+        }
+
+        const float qscale = ent.qscale, eps = ent.eps;
+        f16* qop = reinterpret_cast<f16*>(sm.dec.q);  // [chunk c][operand lane 16*g + column][8]
+#pragma unroll
+        for (int r = 0; r < kQPerWave; r++) {
+            const unsigned hq = (unsigned)wave + W * r;
+            const bool live = hq < G;  // columns of absent heads are zero
+            if (live) wave_norm_rope<J>(xq[r], wq, true, true, rl, eps);
+#pragma unroll
+            for (int j = 0; j < J; j++) {
+                const unsigned d = (unsigned)lane + 64u * j;
+                const float x = live ? xq[r][j] * qscale : 0.0f;
+                if (live) sm.qf[hq][d] = x;
+                const f16 hi = (f16)x;  // hi in column hq, the f16 residual in column hq + 8
+                const unsigned base = ((d >> 5) * 64u + 16u * ((d >> 3) & 3u) + hq) * 8u + (d & 7u);
+                qop[base] = hi;
+                qop[base + 64] = (f16)(x - (float)hi);
+            }
+        }
+        if (do_new) {
+            const bool is_k = wave == 0;
+            wave_norm_rope<J>(xn, wn, is_k, is_k, rl, eps);
+            uint16_t* row = reinterpret_cast<uint16_t*>(is_k ? sm.knew : sm.vnew);
+#pragma unroll
+            for (int j = 0; j < J; j++) row[lane + 64 * j] = f2h(xn[j]);
+            if (ent.flags & kStoreKv) {
+                uint16_t* dst = (is_k ? ent.k_cache : ent.v_cache) + ((uint64_t)new_row * NKH + kvh) * HD;
+#pragma unroll
+                for (int j = 0; j < J; j++) stg<uint16_t>(dst + lane + 64 * j, f2h(xn[j]));
+            }
+        }
+        __syncthreads();
+
+        // The current row's scores (read by the combine, after later barriers).
+        if (has_new) {
+            const f16* kn = reinterpret_cast<const f16*>(sm.knew);
+            for (unsigned h = (unsigned)wave; h < G; h += W) {
+                float p = 0.0f;
+#pragma unroll
+                for (int j = 0; j < J; j++) p += sm.qf[h][lane + 64 * j] * (float)kn[lane + 64 * j];
+                for (int off = 32; off > 0; off >>= 1) p += __shfl_xor(p, off);
+                if (lane == 0) sm.mnew[h] = p;
+            }
+        }
+
+        // ---- tiles ----
+        if constexpr (kTile) {  // the first tile was requested above; the loop requests its own
+            tile_step<HD>(sm.dec, lane, g, lo_col, k0 + t0, k1t, kreg, vreg, m_run, l_run, acc);
+            for (t0 += kStride; t0 < nkeys; t0 += kStride) {
+                load_k_tile<HD>(Kb, row_bytes, last, n, g, k0 + t0, kreg);
+                load_v_tile<HD>(Vb, row_bytes, last, n, g, k0 + t0, vreg);
+                tile_step<HD>(sm.dec, lane, g, lo_col, k0 + t0, k1t, kreg, vreg, m_run, l_run, acc);
+            }
+        }
+    };
+    if (t0 < nkeys)  // uniform: wave and nkeys are scalars
+        body(std::true_type{});
+    else
+        body(std::false_type{});
     wave_publish<HD>(sm.dec, wave, n, g, m_run, l_run, acc);
     __syncthreads();
 
