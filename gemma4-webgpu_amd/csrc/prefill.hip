@@ -44,6 +44,14 @@ namespace g4 {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
+// Work-item and workgroup ids straight from the builtins: this file is compiled
+// with IEEE mode off, and the device library's id functions behind threadIdx
+// and blockIdx (built with it on) are then called rather than inlined.
+__device__ __forceinline__ unsigned tid_x() { return __builtin_amdgcn_workitem_id_x(); }
+__device__ __forceinline__ unsigned wg_x() { return __builtin_amdgcn_workgroup_id_x(); }
+__device__ __forceinline__ unsigned wg_y() { return __builtin_amdgcn_workgroup_id_y(); }
+__device__ __forceinline__ unsigned wg_z() { return __builtin_amdgcn_workgroup_id_z(); }
+
 constexpr int kPfHD = 256;
 constexpr int kPfWaves = 4;
 constexpr int kPfThreads = 64 * kPfWaves;
@@ -108,7 +116,7 @@ struct TileRegs {
 
 __device__ __forceinline__ void tile_load(const char* Kb, const char* Vb, uint32_t row_bytes, unsigned kt0,
                                           unsigned last, TileRegs& r) {
-    const int t = threadIdx.x;
+    const int t = tid_x();
     if (t < 128) {
         const int kg = t >> 5, dg = t & 31;  // keys 8kg..8kg+8, d 8dg..8dg+8
 #pragma unroll
@@ -128,7 +136,7 @@ __device__ __forceinline__ void tile_load(const char* Kb, const char* Vb, uint32
 }
 
 __device__ __forceinline__ void tile_store(PrefillSmem& sm, int buf, const TileRegs& r) {
-    const int t = threadIdx.x;
+    const int t = tid_x();
     if (t < 128) {
         const int kg = t >> 5, dg = t & 31;
         // out[c] = the 8 keys at d = 8dg + c: word w holds keys (2w, 2w + 1), d-half c%2 of word c/2
@@ -154,12 +162,12 @@ __device__ __forceinline__ void tile_store(PrefillSmem& sm, int buf, const TileR
 
 __global__ __launch_bounds__(kPfThreads, 1) void k_prefill(PrefillArgs a) {
     __shared__ PrefillSmem sm;
-    const PrefillWorkDev wk = a.work[blockIdx.x];
+    const PrefillWorkDev wk = a.work[wg_x()];
     const PrefillEntryDev& ent = a.table[wk.entry];
-    const unsigned kvh = blockIdx.y;
+    const unsigned kvh = wg_y();
     const unsigned G = a.group, NQH = a.num_q_heads, NKH = a.num_kv_heads;
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = tid_x() & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid_x() >> 6);
     const int half = lane >> 5;    // which 8 of each 16 keys / d elements this lane supplies
     const int col = lane & 31;     // this lane's q-row within the wave
 
@@ -374,13 +382,13 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_prefill_dma(PrefillArgs a) {
     constexpr int D = kPfDist<HD>, NK = kPfKStages<HD>, NV = kPfVStages<HD>;
     constexpr int NQ = HD / 16, PER = HD / 64 + 4;  // score steps, DMAs per tile
     __shared__ PrefillDmaSmem<HD> sm;
-    const unsigned dh = blockIdx.z;  // output half of the head dimension (head_dim 512)
-    const PrefillWorkDev wk = a.work[blockIdx.x];
+    const unsigned dh = wg_z();  // output half of the head dimension (head_dim 512)
+    const PrefillWorkDev wk = a.work[wg_x()];
     const PrefillEntryDev& ent = a.table[wk.entry];
-    const unsigned kvh = blockIdx.y;
+    const unsigned kvh = wg_y();
     const unsigned G = a.group, NQH = a.num_q_heads, NKH = a.num_kv_heads;
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = tid_x() & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid_x() >> 6);
     const int half = lane >> 5;
     const int col = lane & 31;
 
@@ -705,6 +713,369 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_prefill_dma(PrefillArgs a) {
     if (half == 0 && dh == 0) stg<f32x2>(a.part_ml + rec * 2, f32x2{m_run, L});  // both halves hold the same
 }
 
+// ---- two waves per SIMD: score waves and output waves (head_dim 256) -------
+//
+// The same tiles, rings, DMA schedule and per-tile arithmetic as k_prefill_dma,
+// with the work of one 32-row wave split over two waves that share a SIMD:
+// waves 0..3 ("score waves") compute the scores and the online softmax of
+// their 32 q-rows, waves 4..7 ("output waves") accumulate O^T of the same rows
+// over the full head dimension and issue the tile DMAs. Wave w and w + 4 are
+// placed on one SIMD, so the softmax VALU of one wave runs while the other
+// wave's MFMAs hold the matrix core, and no MFMA is issued twice. The
+// probabilities (f16, already in the output MFMA's B-operand layout) and each
+// row's rescale factor pass through LDS lane to lane (lane l of both waves
+// holds q-row l % 32), two slots per pair.
+//
+// Phases, one barrier each. Phase it (1 <= it <= n - 2): the score wave
+// computes the scores of tile it + 1 and the probabilities of tile it (slot
+// it % 2); the output wave rescales by alpha(it - 1), adds tile it - 1's
+// output and issues tile it + 1 + D. Prologue: scores of tiles 0 and 1 and
+// the probabilities of tile 0. Epilogue: probabilities of tile n - 1 with the
+// output of tile n - 2, then the output of tile n - 1, then (m, l) to LDS for
+// the output waves' stores. Both roles pass the same number of barriers.
+struct PrefillPpSmem {
+    PrefillDmaSmem<256> t;
+    f16x8 p[4][2][2][64];  // [pair][slot][operand register][lane]
+    float alpha[4][2][64];
+    float ml[4][2][64];    // [pair][m, l][lane]
+};
+
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+__global__ __launch_bounds__(512, 1) void k_prefill_pp(PrefillArgs a) {
+    constexpr int HD = 256;
+    constexpr int D = kPfDist<HD>, NK = kPfKStages<HD>, NV = kPfVStages<HD>;
+    constexpr int NQ = HD / 16, PER = HD / 64 + 4;  // score steps, DMAs per tile and score wave
+    constexpr int R = 3;                             // LDS operand reads ahead of their MFMA
+    __shared__ PrefillPpSmem sm;
+    const PrefillWorkDev wk = a.work[wg_x()];
+    const PrefillEntryDev& ent = a.table[wk.entry];
+    const unsigned kvh = wg_y();
+    const unsigned G = a.group, NQH = a.num_q_heads, NKH = a.num_kv_heads;
+    const int lane = tid_x() & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid_x() >> 6);
+    const int pair = wave & 3;
+    const int half = lane >> 5;
+    const int col = lane & 31;
+
+    const unsigned rho = (unsigned)wk.tile * kPfRows + (unsigned)pair * 32u + (unsigned)col;
+    const unsigned tok = rho / G, head = rho % G;
+    const bool row_live = tok < ent.n_tokens;
+    const unsigned tok_c = row_live ? tok : ent.n_tokens - 1;
+    const unsigned kb = wk.key_begin, ke = wk.key_end, last = ke - 1;  // kb is 32-aligned
+    const int n_tiles = (int)((ke - kb + kPfKeys - 1) / kPfKeys);
+
+    const uint32_t row_bytes = NKH * HD * 2u;
+    const char* Kb = reinterpret_cast<const char*>(ent.k + (uint64_t)kvh * HD);
+    const char* VTb = reinterpret_cast<const char*>(ent.vt + (uint64_t)kvh * ent.vt_blocks * (HD * 32));
+    const DmaVOffsets dof = dma_v_offsets(pair, lane);
+    struct DmaTile {
+        const char* k;
+        const char* v;
+        uint32_t kclamp;
+        uint32_t lds_k, lds_v;
+    };
+    uint32_t krow_off[HD / 64], kchunk_off[HD / 64];
+#pragma unroll
+    for (int k = 0; k < HD / 64; k++) {
+        unsigned r, c;
+        dma_k_lane<HD>(pair, lane, k, &r, &c);
+        krow_off[k] = r * row_bytes;
+        kchunk_off[k] = c * 16u;
+    }
+    auto dma_tile = [&](int t) __attribute__((always_inline)) {
+        t = __builtin_amdgcn_readfirstlane(t);
+        const int tc = min(t, n_tiles - 1);
+        const unsigned t0 = kb + (unsigned)tc * kPfKeys;
+        DmaTile d;
+        d.k = uniform_ptr(Kb + (uint64_t)t0 * row_bytes);
+        d.v = uniform_ptr(VTb + (uint64_t)(t0 >> 5) * kPfKTileBytes<HD>);
+        d.kclamp = __builtin_amdgcn_readfirstlane((last - t0) * row_bytes);
+        d.lds_k = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sm.t.k[t % NK][(HD / 64u) * pair * 1024u]);
+        d.lds_v = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sm.t.vt[t % NV][4u * pair * 1024u]);
+        return d;
+    };
+    auto dma_part = [&](int k, const DmaTile& d) __attribute__((always_inline)) {
+        if (k < HD / 64)
+            lds_dma16_s(min(krow_off[k], d.kclamp) + kchunk_off[k], d.k, d.lds_k + 1024u * k);
+        else
+            lds_dma16_s(dof.v[k - HD / 64], d.v, d.lds_v + 1024u * (k - HD / 64));
+    };
+    auto issue = [&](int t) __attribute__((always_inline)) {
+        const DmaTile d = dma_tile(t);
+#pragma unroll
+        for (int k = 0; k < PER; k++) dma_part(k, d);
+    };
+
+    if (wave < 4) {
+        // ---------------- score wave ----------------
+        // Each score wave also issues its quarter of every tile's DMAs (the output waves carry the
+        // longer part of each phase): tiles 0..D first, so that their latency overlaps q's.
+#pragma unroll
+        for (int p = 0; p <= D; p++) issue(p);
+        const unsigned pos = ent.start + tok_c;
+        const unsigned lo = (ent.window != 0 && pos + 1 > ent.window) ? pos + 1 - ent.window : 0u;
+        const unsigned hi = row_live ? pos : 0u;
+        const bool dead = !row_live;
+        const float qs = ent.qscale;
+        // The score MFMA's B operand. The kernel uses no AGPRs: a kernel that does gets half of its
+        // 256 registers (two waves per SIMD) as AGPRs, and the output wave's 128 accumulators plus
+        // its operands need more than the other half.
+        f16x8 qop[NQ];
+        {
+            const uint16_t* qr = ent.q + ((uint64_t)tok_c * NQH + kvh * G + head) * HD + 8 * half;
+#pragma unroll
+            for (int s = 0; s < NQ; s++) qop[s] = ldg<f16x8>(qr + 16 * s);
+        }
+        float m_run = -INFINITY, l_run = 0.0f;
+        const unsigned krow = key_of_row((unsigned)col);
+        const unsigned kx = swz_k(krow);
+        unsigned koff[8];  // chunk 2s + half of the key row lies at koff[s % 8] + 256 (s / 8)
+#pragma unroll
+        for (int b = 0; b < 8; b++) koff[b] = krow * (2u * HD) + ((((unsigned)(2 * b + half)) ^ kx) << 4);
+        const unsigned span = dead ? 0u : hi - lo + 1u;
+
+        auto scores = [&](int stage) __attribute__((always_inline)) {
+            const unsigned char* kbuf = sm.t.k[stage];
+            f32x16 sc = f32x16{};
+#pragma unroll
+            for (int s = 0; s < NQ; s++) {
+                const f16x8 k0 = *reinterpret_cast<const f16x8*>(kbuf + koff[s & 7] + 256u * (s >> 3));
+                sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(k0, qop[s], sc, 0, 0, 0);
+            }
+            return sc;
+        };
+        // Probabilities of one tile's raw scores (register r: key kt0 + 16 (r / 8) + 8 half + r % 8),
+        // with the lazy update of the row's reference max (alpha: the accumulators' rescale factor, 1
+        // when the reference did not move).
+        auto softmax = [&](f32x16 sc, unsigned kt0, f16x8 (&pop)[2], float& alpha) __attribute__((always_inline)) {
+            const unsigned rel = kt0 + 8u * (unsigned)half - lo;
+#pragma unroll
+            for (int r = 0; r < 16; r++)
+                sc[r] = rel + (unsigned)(16 * (r >> 3) + (r & 7)) < span ? sc[r] : -INFINITY;
+            float smax = sc[0];
+#pragma unroll
+            for (int r = 1; r < 16; r++) smax = fmaxf(smax, sc[r]);
+            float tmax = smax * qs;  // the scale is positive
+            {
+                const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(tmax), __float_as_uint(tmax), false, false);
+                tmax = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));  // max over both halves of the row
+            }
+            const bool move = tmax > m_run + kPfLazy;
+            const float m_new = move ? tmax : m_run;
+            alpha = move ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;  // 0 from -inf (acc, l are 0)
+            l_run *= alpha;
+            m_run = m_new;
+            const float nmu = m_run == -INFINITY ? 0.0f : -m_run;
+#pragma unroll
+            for (int r = 0; r < 16; r += 2) {
+                const f16x2 h = f16x2{(f16)__builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], qs, nmu)),
+                                      (f16)__builtin_amdgcn_exp2f(__builtin_fmaf(sc[r + 1], qs, nmu))};
+                pop[r >> 3][r & 7] = h[0];
+                pop[r >> 3][(r + 1) & 7] = h[1];
+                l_run = __builtin_amdgcn_fdot2(h, f16x2{(f16)1.0f, (f16)1.0f}, l_run, false);
+            }
+        };
+        // One phase: the NQ score MFMAs of the next tile with this tile's softmax cut into 26 slots
+        // spread over them (0-7: masking and running max of two scores; 8-9: the row's reference max
+        // and alpha; 10-25: one exponential each, every second one packing the f16 pair and adding it
+        // to the row sum), sched_barrier(0) keeping that order. `mask` is false for tiles inside the
+        // window of every row of the wave.
+        auto steady = [&](bool mask, int ks, unsigned kt0, const DmaTile& tdma, f32x16& sc, f16x8 (&pout)[2],
+                          f32x16& nxt, float& alpha) __attribute__((always_inline)) {
+            const unsigned char* kbuf = sm.t.k[ks];
+            f16x8 kr[NQ];
+            auto kread = [&](int s) __attribute__((always_inline)) {
+                kr[s] = *reinterpret_cast<const f16x8*>(kbuf + koff[s & 7] + 256u * (s >> 3));
+            };
+#pragma unroll
+            for (int i = 0; i < R; i++) kread(i);
+            const unsigned rel = kt0 + 8u * (unsigned)half - lo;
+            float mx = -INFINITY, tmax = 0.0f, nmu = 0.0f;
+            float p[16];
+            auto slot = [&](int q) __attribute__((always_inline)) {
+                if (q < 8) {
+                    const int r = 2 * q;
+                    if (mask) {
+                        sc[r] = rel + (unsigned)(16 * (r >> 3) + (r & 7)) < span ? sc[r] : -INFINITY;
+                        sc[r + 1] = rel + (unsigned)(16 * ((r + 1) >> 3) + ((r + 1) & 7)) < span ? sc[r + 1] : -INFINITY;
+                    }
+                    mx = fmaxf(mx, fmaxf(sc[r], sc[r + 1]));
+                } else if (q == 8) {
+                    tmax = mx * qs;
+                    const auto sw =
+                        __builtin_amdgcn_permlane32_swap(__float_as_uint(tmax), __float_as_uint(tmax), false, false);
+                    tmax = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+                } else if (q == 9) {
+                    const bool move = tmax > m_run + kPfLazy;
+                    const float m_new = move ? tmax : m_run;
+                    alpha = move ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
+                    l_run *= alpha;
+                    m_run = m_new;
+                    nmu = m_run == -INFINITY ? 0.0f : -m_run;
+                } else if (q < 26) {
+                    const int r = q - 10;
+                    p[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], qs, nmu));
+                    if (r & 1) {
+                        const f16x2 h = f16x2{(f16)p[r - 1], (f16)p[r]};
+                        pout[r >> 3][(r - 1) & 7] = h[0];
+                        pout[r >> 3][r & 7] = h[1];
+                        l_run = __builtin_amdgcn_fdot2(h, f16x2{(f16)1.0f, (f16)1.0f}, l_run, false);
+                    }
+                }
+            };
+            nxt = f32x16{};
+            int q = 0;
+#pragma unroll
+            for (int j = 0; j < NQ; j++) {
+                nxt = __builtin_amdgcn_mfma_f32_32x32x16_f16(kr[j], qop[j], nxt, 0, 0, 0);
+                if (j + R < NQ) kread(j + R);
+                if (j % 2 == 0 && j / 2 < PER) dma_part(j / 2, tdma);  // one instruction per two steps
+#pragma unroll
+                for (; q < 26 * (j + 1) / NQ; q++) slot(q);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        };
+        auto put = [&](int it, const f16x8 (&pp)[2], float alpha) __attribute__((always_inline)) {
+            sm.p[pair][it & 1][0][lane] = pp[0];
+            sm.p[pair][it & 1][1][lane] = pp[1];
+            sm.alpha[pair][it & 1][lane] = alpha;
+        };
+        int t_in0, t_in1;  // tiles [t_in0, t_in1) lie inside every row's window of this wave
+        {
+            int a0 = dead ? 0x7fffffff : (lo > kb ? (int)((lo - kb + kPfKeys - 1) / kPfKeys) : 0);
+            int a1 = dead || hi + 1 < kb ? 0 : (int)((hi + 1 - kb) / kPfKeys);
+#pragma unroll
+            for (int m = 32; m >= 1; m >>= 1) {
+                a0 = max(a0, __shfl_xor(a0, m));
+                a1 = min(a1, __shfl_xor(a1, m));
+            }
+            t_in0 = __builtin_amdgcn_readfirstlane(a0);
+            t_in1 = __builtin_amdgcn_readfirstlane(a1);
+        }
+        f16x8 pa[2], pb[2];
+        f32x16 sa, sb;
+        float alpha;
+        auto step = [&](bool mask, int it, f32x16& sc, f16x8 (&pout)[2], f32x16& nxt) __attribute__((always_inline)) {
+            it = __builtin_amdgcn_readfirstlane(it);
+            dma_wait_barrier<PER>(D - 1);  // tile it + 1 is in LDS; tile it + 1 + D goes to the stages of K(it), V^T(it - 2)
+            float al;
+            const DmaTile d = dma_tile(it + 1 + D);
+            steady(mask, (it + 1) % NK, kb + (unsigned)it * kPfKeys, d, sc, pout, nxt, al);
+            put(it, pout, al);
+        };
+        dma_wait_barrier<PER>(D);  // tile 0 is in LDS
+        sa = scores(0);
+        if (n_tiles == 1) {
+            softmax(sa, kb, pa, alpha);
+            put(0, pa, alpha);
+        } else {
+            dma_wait_barrier<PER>(D - 1);  // tile 1 is in LDS; every wave is past scores(0)
+            issue(D + 1);
+            sb = scores(1 % NK);
+            softmax(sa, kb, pa, alpha);
+            put(0, pa, alpha);
+            int it = 1;
+            for (; it + 1 < n_tiles && it < t_in0; it++) {
+                step(true, it, sb, pb, sa);
+                sb = sa;
+            }
+            for (; it + 2 < n_tiles && it + 1 < t_in1; it += 2) {
+                step(false, it, sb, pb, sa);      // scores of tile it + 1 into sa
+                step(false, it + 1, sa, pa, sb);  // scores of tile it + 2 into sb
+            }
+            for (; it + 1 < n_tiles; it++) {
+                step(true, it, sb, pb, sa);
+                sb = sa;
+            }
+            lds_barrier();
+            softmax(sb, kb + (unsigned)it * kPfKeys, pb, alpha);
+            put(it, pb, alpha);
+        }
+        lds_barrier();  // the output waves add the last tile
+        sm.ml[pair][0][lane] = m_run;
+        sm.ml[pair][1][lane] = l_run + __shfl_xor(l_run, 32);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no LDS write of this workgroup outlives it
+        lds_barrier();
+        return;
+    }
+
+    // ---------------- output wave ----------------
+    f32x16 acc[8];
+#pragma unroll
+    for (int b = 0; b < 8; b++) acc[b] = f32x16{};
+    const unsigned vx = swz_v((unsigned)col);
+    unsigned voff[2];
+#pragma unroll
+    for (int s = 0; s < 2; s++) voff[s] = (unsigned)col * 64u + ((((unsigned)(2 * s + half)) ^ vx) << 4);
+    // Tile it's output: its probabilities and alpha from the score wave's slot, the rescale when a
+    // row's reference max moved, then the 16 MFMAs with the V^T operands read R ahead.
+    auto output = [&](int it) __attribute__((always_inline)) {
+        it = __builtin_amdgcn_readfirstlane(it);
+        const unsigned char* vbuf = sm.t.vt[it % NV];
+        f16x8 vr[16];
+        auto vread = [&](int o) __attribute__((always_inline)) {
+            vr[o] = *reinterpret_cast<const f16x8*>(vbuf + voff[o & 1] + 2048u * (o >> 1));
+        };
+#pragma unroll
+        for (int i = 0; i < R; i++) vread(i);
+        const f16x8 pin[2] = {sm.p[pair][it & 1][0][lane], sm.p[pair][it & 1][1][lane]};
+        const float al = sm.alpha[pair][it & 1][lane];
+        if (__any(al != 1.0f)) {
+#pragma unroll
+            for (int b = 0; b < 8; b++) acc[b] *= al;
+        }
+#pragma unroll
+        for (int o = 0; o < 16; o++) {
+            acc[o >> 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vr[o], pin[o & 1], acc[o >> 1], 0, 0, 0);
+            if (o + R < 16) vread(o + R);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    lds_barrier();  // tile 0 is in LDS
+    if (n_tiles == 1) {
+        lds_barrier();
+        output(0);
+    } else {
+        lds_barrier();  // tile 1 is in LDS
+        int it = 1;
+        for (; it + 1 < n_tiles; it++) {
+            lds_barrier();  // tile it + 1 is in LDS
+            output(it - 1);
+        }
+        lds_barrier();
+        output(it - 1);
+        lds_barrier();
+        output(it);
+    }
+    lds_barrier();  // (m, l) of every row are in LDS
+    const float m_fin = sm.ml[pair][0][lane];
+    const float L = sm.ml[pair][1][lane];
+    if (!row_live) return;
+    const uint64_t qrow = (uint64_t)tok * NQH + kvh * G + head;
+    if (wk.n_parts == 1) {
+        float* dst = ent.out + qrow * HD + 4 * half;
+        const float inv = 1.0f / L;
+#pragma unroll
+        for (int b = 0; b < 8; b++)
+#pragma unroll
+            for (int g = 0; g < 4; g++)
+                stg<f32x4>(dst + 32 * b + 8 * g, f32x4{acc[b][4 * g] * inv, acc[b][4 * g + 1] * inv,
+                                                      acc[b][4 * g + 2] * inv, acc[b][4 * g + 3] * inv});
+        return;
+    }
+    const unsigned tile_tok0 = (unsigned)wk.tile * kPfRows / G;
+    const uint64_t slot = (uint64_t)wk.split_base + (uint64_t)(tok - tile_tok0) * wk.n_parts + wk.part;
+    const uint64_t rec = (slot * NKH + kvh) * G + head;
+    float* po = a.part_o + rec * HD + 4 * half;
+#pragma unroll
+    for (int b = 0; b < 8; b++)
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+            stg<f32x4>(po + 32 * b + 8 * g, f32x4{acc[b][4 * g], acc[b][4 * g + 1], acc[b][4 * g + 2], acc[b][4 * g + 3]});
+    if (half == 0) stg<f32x2>(a.part_ml + rec * 2, f32x2{m_fin, L});
+}
+
 // V of one cache in 32-key blocks [kv head][block][HD][32] (f16): block j holds
 // rows 32 j .. 32 j + 31 (rows past the cache's end repeat its last row).
 struct VtCacheDev {
@@ -720,13 +1091,13 @@ template <int HD>
 __global__ __launch_bounds__(256) void k_vt_blocks(const VtCacheDev* caches, uint32_t n_caches, uint32_t nkh) {
     __shared__ __attribute__((aligned(16))) uint16_t tb[kPfKeys][HD + 8];
     unsigned c = 0;
-    while (c + 1 < n_caches && blockIdx.x >= caches[c + 1].block0) c++;
+    while (c + 1 < n_caches && wg_x() >= caches[c + 1].block0) c++;
     const VtCacheDev cd = caches[c];
-    const unsigned blk = blockIdx.x - cd.block0;
-    const unsigned kvh = blockIdx.y;
+    const unsigned blk = wg_x() - cd.block0;
+    const unsigned kvh = wg_y();
 #pragma unroll
     for (int i = 0; i < HD / 64; i++) {
-        const unsigned piece = threadIdx.x + 256u * i;  // 32 keys x HD/8 chunks of 8 d
+        const unsigned piece = tid_x() + 256u * i;  // 32 keys x HD/8 chunks of 8 d
         const unsigned key = piece / (HD / 8), ch = piece % (HD / 8);
         const unsigned row = min(blk * 32u + key, cd.rows - 1);
         const u32x4 x = ldg<u32x4>(cd.v + ((uint64_t)row * nkh + kvh) * HD + ch * 8u);
@@ -736,7 +1107,7 @@ __global__ __launch_bounds__(256) void k_vt_blocks(const VtCacheDev* caches, uin
     uint16_t* dst = cd.vt + ((uint64_t)kvh * cd.blocks + blk) * (HD * 32);
 #pragma unroll
     for (int i = 0; i < HD / 64; i++) {
-        const unsigned piece = threadIdx.x + 256u * i;  // HD d x 4 chunks of 8 keys
+        const unsigned piece = tid_x() + 256u * i;  // HD d x 4 chunks of 8 keys
         const unsigned d = piece >> 2, kc = piece & 3u;
         u32x4 o;
 #pragma unroll
@@ -803,6 +1174,13 @@ struct VtPlan {
 
 bool prefill_dma_enabled() {
     static const int env = pf_env("G4_PREFILL_DMA", 1);
+    return env != 0;
+}
+
+// head_dim 256 in the pipelined form: the two-waves-per-SIMD kernel (k_prefill_pp), or with
+// G4_PREFILL_PP=0 the one-wave-per-SIMD kernel (k_prefill_dma<256>).
+bool prefill_pp_enabled() {
+    static const int env = pf_env("G4_PREFILL_PP", 1);
     return env != 0;
 }
 
@@ -1050,6 +1428,11 @@ static int prefill_run(const g4_decode_plan* plan, void* stream, hipEvent_t star
                 hipExtLaunchKernelGGL(k_prefill_dma<512>, grid, dim3(kPfThreads), 0, st, start_ev, stop_ev, 0, a);
             else
                 hipLaunchKernelGGL(k_prefill_dma<512>, grid, dim3(kPfThreads), 0, st, a);
+        } else if (prefill_pp_enabled()) {
+            if (start_ev || stop_ev)
+                hipExtLaunchKernelGGL(k_prefill_pp, grid, dim3(2 * kPfThreads), 0, st, start_ev, stop_ev, 0, a);
+            else
+                hipLaunchKernelGGL(k_prefill_pp, grid, dim3(2 * kPfThreads), 0, st, a);
         } else if (start_ev || stop_ev) {
             hipExtLaunchKernelGGL(k_prefill_dma<256>, grid, dim3(kPfThreads), 0, st, start_ev, stop_ev, 0, a);
         } else {
