@@ -67,6 +67,8 @@ NQH, NKH, HD = 8, 1, 256
 EPS = 1e-6
 BASE_SEED = 20261201
 DEFAULT_WORKLOAD = "stack32k"
+# the prefill kernel at head_dim 256 (G4_PREFILL_PP=0 selects the one-wave-per-SIMD form)
+PREFILL_KERNEL = "k_prefill_dma" if os.environ.get("G4_PREFILL_PP", "1") == "0" else "k_prefill_pp"
 
 
 def log(msg: str) -> None:
@@ -386,12 +388,16 @@ def read_traffic(workload: str):
 
 
 def read_traffic_file(f: Path):
+    """HBM bytes of the kernel per step: the summary's per-step figure for steps of several launches
+    (one per head_dim group), else its per-launch figure."""
     if not f.exists():
         return None
+    vals = {}
     for line in f.read_text().splitlines():
-        if line.startswith("hbm_bytes_per_launch:"):
-            return int(float(line.split(":", 1)[1]))
-    return None
+        k, _, v = line.partition(":")
+        if k in ("hbm_bytes_per_launch", "hbm_bytes_per_step"):
+            vals[k] = int(float(v))
+    return vals.get("hbm_bytes_per_step", vals.get("hbm_bytes_per_launch"))
 
 
 # ---- CPU baseline (oracle on the host) --------------------------------------------
@@ -497,7 +503,7 @@ def run_prefill_gpu(args):
         ops.attn_prefill_run_timed(plan, a_, b_)
     torch.cuda.synchronize()
     k_ms = sum(a_.elapsed_time(b_) for a_, b_ in evs) / len(evs)
-    log(f"prefill4k: {wall / args.steps * 1e6:.1f} us/step (prep {prep_us:.1f} us), k_prefill_dma avg "
+    log(f"prefill4k: {wall / args.steps * 1e6:.1f} us/step (prep {prep_us:.1f} us), {PREFILL_KERNEL} avg "
         f"{k_ms * 1e3:.1f} us")
     return dict(wall_s=wall, steps=args.steps, kernel_ms=k_ms, entries=len(entries), prep_us=prep_us)
 
@@ -547,7 +553,7 @@ def main_prefill(args):
                    "f16 K/V store; one launch per layer) then one prefill launch over 512-token chunks (16 entries)",
                    "num_q_heads": NQH, "num_kv_heads": NKH, "head_dim": HD, "flops_per_step": flops,
                    "prep_us_per_step": round(r["prep_us"], 2)},
-        "roofline": {"bound": "mfma", "kernel": "k_prefill_dma", "achieved": round(achieved, 2),
+        "roofline": {"bound": "mfma", "kernel": PREFILL_KERNEL, "achieved": round(achieved, 2),
                      "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4),
                      "traffic": None, "avg_us": round(r["kernel_ms"] * 1e3, 2)},
     }

@@ -5,7 +5,7 @@
         Kernel table of a `rocprofv3 --kernel-trace --stats -f csv -d D -- ...` run.
 
     profile_summary.py traffic --fetch D1 --write D2 --copy-fetch D3 --copy-write D4
-                               --kernel REGEX --command "..." [--algorithmic-bytes N]
+                               --kernel REGEX --command "..." [--algorithmic-bytes N] [--launches K]
         HBM bytes per launch of the kernel matching REGEX from one FETCH_SIZE and
         one WRITE_SIZE pass (`rocprofv3 --pmc FETCH_SIZE -f csv -d D1 -- ...`),
         each scaled by what the same counter reads for g4bench's plain copy kernel
@@ -97,7 +97,16 @@ def cmd_traffic(a) -> None:
     print(f"hbm_read_bytes_per_launch: {fetch_b:.0f}")
     print(f"hbm_write_bytes_per_launch: {write_b:.0f}")
     print(f"hbm_bytes_per_launch: {fetch_b + write_b:.0f}")
-    if a.algorithmic_bytes:
+    if a.launches > 1:
+        # a step of several launches of the kernel (one per head_dim group), one of each per step:
+        # the per-dispatch mean times the launches is the step's bytes
+        per_step = (fetch_b + write_b) * a.launches
+        print(f"launches_per_step: {a.launches}")
+        print(f"hbm_bytes_per_step: {per_step:.0f}")
+        if a.algorithmic_bytes:
+            print(f"algorithmic_bytes_per_step: {a.algorithmic_bytes}")
+            print(f"traffic_over_algorithmic: {per_step / a.algorithmic_bytes:.4f}")
+    elif a.algorithmic_bytes:
         print(f"algorithmic_bytes_per_launch: {a.algorithmic_bytes}")
         print(f"traffic_over_algorithmic: {(fetch_b + write_b) / a.algorithmic_bytes:.4f}")
 
@@ -138,7 +147,8 @@ def main() -> None:
         f.add_argument("--" + k.replace("_", "-"), dest=k, required=True)
     f.add_argument("--kernel", required=True)
     f.add_argument("--command", required=True)
-    f.add_argument("--algorithmic-bytes", type=int, default=0)
+    f.add_argument("--algorithmic-bytes", type=int, default=0, help="per step when --launches > 1")
+    f.add_argument("--launches", type=int, default=1, help="launches of the kernel per step (one of each kind)")
     m = sub.add_parser("mfma")
     m.add_argument("--dir", required=True)
     m.add_argument("--kernel", required=True)
