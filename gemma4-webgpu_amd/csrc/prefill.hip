@@ -1076,6 +1076,355 @@ __global__ __launch_bounds__(512, 1) void k_prefill_pp(PrefillArgs a) {
     if (half == 0) stg<f32x2>(a.part_ml + rec * 2, f32x2{m_fin, L});
 }
 
+// ---- head_dim 512: shared scores, six waves -----------------------------------
+//
+// The head_dim 512 form of k_prefill_pp. A workgroup takes one 64-row half of a
+// work item's 128 q-rows (grid z). Waves 2 and 3 ("score waves") compute the
+// scores and softmax of 32 rows each at the full width (q in 128 registers,
+// 32 score MFMAs per tile); waves 0, 1, 4 and 5 ("output waves") accumulate
+// one 256-wide half of the output of one score wave's rows (wave w: rows of
+// score wave 2 + (w & 1), half w >> 2; 16 MFMAs per tile). Waves are placed on
+// the SIMDs round robin, so each score wave has a SIMD to itself and the two
+// SIMDs left hold two output waves each: 32 MFMAs per SIMD and tile, and no
+// MFMA is issued twice (the one-wave form computes the full scores in both
+// halves' workgroups, 1.5x the algorithmic MFMA work).
+//
+// LDS: two K stages and two V^T stages of 32 KiB (a full 512-wide block), the
+// probabilities and rescale factors of the two score waves. Each role DMAs
+// what it reads, one phase ahead: the score waves tile t + 1's K rows while
+// they score tile t (into the stage of tile t - 1), the output waves tile t's
+// V^T block while they add tile t - 1 (into the stage of tile t - 2). So every
+// barrier waits for all of the wave's DMAs (only the previous phase's are in
+// flight). Phases as in k_prefill_pp; both roles pass n + 3 barriers for n
+// tiles (3 for one tile).
+struct PrefillPp512Smem {
+    unsigned char k[2][kPfKeys * 512 * 2];  // key row r: chunk c (8 d) at r*1024 + ((c ^ swz_k(r)) * 16)
+    unsigned char vt[2][512 * kPfKeys * 2];  // d row: chunk c (8 keys) at d*64 + ((c ^ swz_v(d)) * 16)
+    f16x8 p[2][2][2][64];                    // [score wave][slot][operand register][lane]
+    float alpha[2][2][64];
+    float ml[2][2][64];                      // [score wave][m, l][lane]
+};
+
+__device__ __forceinline__ void vm_barrier() {
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+__global__ __launch_bounds__(384, 1) void k_prefill_pp512(PrefillArgs a) {
+    constexpr int HD = 512;
+    constexpr int NQ = HD / 16;  // score steps
+    constexpr int R = 3;         // LDS operand reads ahead of their MFMA
+    __shared__ PrefillPp512Smem sm;
+    const unsigned zh = wg_z();  // row half of the work item's query tile
+    const PrefillWorkDev wk = a.work[wg_x()];
+    const PrefillEntryDev& ent = a.table[wk.entry];
+    const unsigned kvh = wg_y();
+    const unsigned G = a.group, NQH = a.num_q_heads, NKH = a.num_kv_heads;
+    const int lane = tid_x() & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid_x() >> 6);
+    const bool scorer = wave == 2 || wave == 3;
+    const int sw = scorer ? wave - 2 : (wave & 1);  // the score wave whose rows this wave holds
+    const int half = lane >> 5;
+    const int col = lane & 31;
+
+    const unsigned rho = (unsigned)wk.tile * kPfRows + 64u * zh + (unsigned)sw * 32u + (unsigned)col;
+    const unsigned tok = rho / G, head = rho % G;
+    const bool row_live = tok < ent.n_tokens;
+    const unsigned tok_c = row_live ? tok : ent.n_tokens - 1;
+    const unsigned kb = wk.key_begin, ke = wk.key_end, last = ke - 1;  // kb is 32-aligned
+    const int n_tiles = (int)((ke - kb + kPfKeys - 1) / kPfKeys);
+    const uint32_t row_bytes = NKH * HD * 2u;
+
+    if (scorer) {
+        // ---------------- score wave ----------------
+        const char* Kb = reinterpret_cast<const char*>(ent.k + (uint64_t)kvh * HD);
+        // Rows 16 sw .. 16 sw + 15 of tile t's K into stage t & 1 (rows past the range clamp to its last).
+        auto kdma = [&](int t) __attribute__((always_inline)) {
+            t = __builtin_amdgcn_readfirstlane(t);
+            const unsigned t0 = kb + (unsigned)t * kPfKeys;
+            const char* src = uniform_ptr(Kb + (uint64_t)t0 * row_bytes);
+            const uint32_t kclamp = __builtin_amdgcn_readfirstlane((last - t0) * row_bytes);
+            const uint32_t lds = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sm.k[t & 1][0]);
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const unsigned r = 16u * sw + (unsigned)i;  // swz_k(r) = i
+                lds_dma16_s(min(r * row_bytes, kclamp) + ((((unsigned)lane) ^ (unsigned)i) << 4), src, lds + r * 1024u);
+            }
+        };
+        kdma(0);
+        const unsigned pos = ent.start + tok_c;
+        const unsigned lo = (ent.window != 0 && pos + 1 > ent.window) ? pos + 1 - ent.window : 0u;
+        const unsigned hi = row_live ? pos : 0u;
+        const bool dead = !row_live;
+        const float qs = ent.qscale;
+        f16x8 qop[NQ];  // the score MFMA's B operand (the kernel uses no AGPRs)
+        {
+            const uint16_t* qr = ent.q + ((uint64_t)tok_c * NQH + kvh * G + head) * HD + 8 * half;
+#pragma unroll
+            for (int s = 0; s < NQ; s++) qop[s] = ldg<f16x8>(qr + 16 * s);
+        }
+        float m_run = -INFINITY, l_run = 0.0f;
+        const unsigned krow = key_of_row((unsigned)col);
+        const unsigned kx = swz_k(krow);
+        unsigned koff[8];  // chunk 2s + half of the key row lies at koff[s % 8] + 256 (s / 8)
+#pragma unroll
+        for (int b = 0; b < 8; b++) koff[b] = krow * (2u * HD) + ((((unsigned)(2 * b + half)) ^ kx) << 4);
+        const unsigned span = dead ? 0u : hi - lo + 1u;
+
+        auto scores = [&](int stage) __attribute__((always_inline)) {
+            const unsigned char* kbuf = sm.k[stage];
+            f32x16 sc = f32x16{};
+#pragma unroll
+            for (int s = 0; s < NQ; s++) {
+                const f16x8 k0 = *reinterpret_cast<const f16x8*>(kbuf + koff[s & 7] + 256u * (s >> 3));
+                sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(k0, qop[s], sc, 0, 0, 0);
+            }
+            return sc;
+        };
+        auto softmax = [&](f32x16 sc, unsigned kt0, f16x8 (&pop)[2], float& alpha) __attribute__((always_inline)) {
+            const unsigned rel = kt0 + 8u * (unsigned)half - lo;
+#pragma unroll
+            for (int r = 0; r < 16; r++)
+                sc[r] = rel + (unsigned)(16 * (r >> 3) + (r & 7)) < span ? sc[r] : -INFINITY;
+            float smax = sc[0];
+#pragma unroll
+            for (int r = 1; r < 16; r++) smax = fmaxf(smax, sc[r]);
+            float tmax = smax * qs;  // the scale is positive
+            {
+                const auto swp = __builtin_amdgcn_permlane32_swap(__float_as_uint(tmax), __float_as_uint(tmax), false, false);
+                tmax = fmaxf(__uint_as_float(swp[0]), __uint_as_float(swp[1]));  // max over both halves of the row
+            }
+            const bool move = tmax > m_run + kPfLazy;
+            const float m_new = move ? tmax : m_run;
+            alpha = move ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;  // 0 from -inf (acc, l are 0)
+            l_run *= alpha;
+            m_run = m_new;
+            const float nmu = m_run == -INFINITY ? 0.0f : -m_run;
+#pragma unroll
+            for (int r = 0; r < 16; r += 2) {
+                const f16x2 h = f16x2{(f16)__builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], qs, nmu)),
+                                      (f16)__builtin_amdgcn_exp2f(__builtin_fmaf(sc[r + 1], qs, nmu))};
+                pop[r >> 3][r & 7] = h[0];
+                pop[r >> 3][(r + 1) & 7] = h[1];
+                l_run = __builtin_amdgcn_fdot2(h, f16x2{(f16)1.0f, (f16)1.0f}, l_run, false);
+            }
+        };
+        // One phase: the NQ score MFMAs of the next tile with this tile's softmax cut into 26 slots
+        // spread over them (as in k_prefill_pp).
+        auto steady = [&](bool mask, int ks, unsigned kt0, f32x16& sc, f16x8 (&pout)[2], f32x16& nxt,
+                          float& alpha) __attribute__((always_inline)) {
+            const unsigned char* kbuf = sm.k[ks];
+            f16x8 kr[NQ];
+            auto kread = [&](int s) __attribute__((always_inline)) {
+                kr[s] = *reinterpret_cast<const f16x8*>(kbuf + koff[s & 7] + 256u * (s >> 3));
+            };
+#pragma unroll
+            for (int i = 0; i < R; i++) kread(i);
+            const unsigned rel = kt0 + 8u * (unsigned)half - lo;
+            float mx = -INFINITY, tmax = 0.0f, nmu = 0.0f;
+            float p[16];
+            auto slot = [&](int q) __attribute__((always_inline)) {
+                if (q < 8) {
+                    const int r = 2 * q;
+                    if (mask) {
+                        sc[r] = rel + (unsigned)(16 * (r >> 3) + (r & 7)) < span ? sc[r] : -INFINITY;
+                        sc[r + 1] = rel + (unsigned)(16 * ((r + 1) >> 3) + ((r + 1) & 7)) < span ? sc[r + 1] : -INFINITY;
+                    }
+                    mx = fmaxf(mx, fmaxf(sc[r], sc[r + 1]));
+                } else if (q == 8) {
+                    tmax = mx * qs;
+                    const auto swp =
+                        __builtin_amdgcn_permlane32_swap(__float_as_uint(tmax), __float_as_uint(tmax), false, false);
+                    tmax = fmaxf(__uint_as_float(swp[0]), __uint_as_float(swp[1]));
+                } else if (q == 9) {
+                    const bool move = tmax > m_run + kPfLazy;
+                    const float m_new = move ? tmax : m_run;
+                    alpha = move ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
+                    l_run *= alpha;
+                    m_run = m_new;
+                    nmu = m_run == -INFINITY ? 0.0f : -m_run;
+                } else if (q < 26) {
+                    const int r = q - 10;
+                    p[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], qs, nmu));
+                    if (r & 1) {
+                        const f16x2 h = f16x2{(f16)p[r - 1], (f16)p[r]};
+                        pout[r >> 3][(r - 1) & 7] = h[0];
+                        pout[r >> 3][r & 7] = h[1];
+                        l_run = __builtin_amdgcn_fdot2(h, f16x2{(f16)1.0f, (f16)1.0f}, l_run, false);
+                    }
+                }
+            };
+            nxt = f32x16{};
+            int q = 0;
+#pragma unroll
+            for (int j = 0; j < NQ; j++) {
+                nxt = __builtin_amdgcn_mfma_f32_32x32x16_f16(kr[j], qop[j], nxt, 0, 0, 0);
+                if (j + R < NQ) kread(j + R);
+#pragma unroll
+                for (; q < 26 * (j + 1) / NQ; q++) slot(q);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        };
+        auto put = [&](int it, const f16x8 (&pp)[2], float alpha) __attribute__((always_inline)) {
+            sm.p[sw][it & 1][0][lane] = pp[0];
+            sm.p[sw][it & 1][1][lane] = pp[1];
+            sm.alpha[sw][it & 1][lane] = alpha;
+        };
+        int t_in0, t_in1;  // tiles [t_in0, t_in1) lie inside every row's window of this wave
+        {
+            int a0 = dead ? 0x7fffffff : (lo > kb ? (int)((lo - kb + kPfKeys - 1) / kPfKeys) : 0);
+            int a1 = dead || hi + 1 < kb ? 0 : (int)((hi + 1 - kb) / kPfKeys);
+#pragma unroll
+            for (int m = 32; m >= 1; m >>= 1) {
+                a0 = max(a0, __shfl_xor(a0, m));
+                a1 = min(a1, __shfl_xor(a1, m));
+            }
+            t_in0 = __builtin_amdgcn_readfirstlane(a0);
+            t_in1 = __builtin_amdgcn_readfirstlane(a1);
+        }
+        f16x8 pa[2], pb[2];
+        f32x16 sa, sb;
+        float alpha;
+        auto step = [&](bool mask, int it, f32x16& sc, f16x8 (&pout)[2], f32x16& nxt) __attribute__((always_inline)) {
+            it = __builtin_amdgcn_readfirstlane(it);
+            vm_barrier();  // tile it + 1's K is in LDS
+            if (it + 2 < n_tiles) kdma(it + 2);  // into the stage of tile it, scored in the previous phase
+            float al;
+            steady(mask, (it + 1) & 1, kb + (unsigned)it * kPfKeys, sc, pout, nxt, al);
+            put(it, pout, al);
+        };
+        vm_barrier();  // tile 0's K is in LDS
+        if (n_tiles > 1) kdma(1);
+        sa = scores(0);
+        if (n_tiles == 1) {
+            softmax(sa, kb, pa, alpha);
+            put(0, pa, alpha);
+        } else {
+            vm_barrier();  // tile 1's K is in LDS
+            if (n_tiles > 2) kdma(2);
+            sb = scores(1);
+            softmax(sa, kb, pa, alpha);
+            put(0, pa, alpha);
+            int it = 1;
+            for (; it + 1 < n_tiles && it < t_in0; it++) {
+                step(true, it, sb, pb, sa);
+                sb = sa;
+            }
+            for (; it + 2 < n_tiles && it + 1 < t_in1; it += 2) {
+                step(false, it, sb, pb, sa);
+                step(false, it + 1, sa, pa, sb);
+            }
+            for (; it + 1 < n_tiles; it++) {
+                step(true, it, sb, pb, sa);
+                sb = sa;
+            }
+            lds_barrier();
+            softmax(sb, kb + (unsigned)it * kPfKeys, pb, alpha);
+            put(it, pb, alpha);
+        }
+        lds_barrier();  // the output waves add the last tile
+        sm.ml[sw][0][lane] = m_run;
+        sm.ml[sw][1][lane] = l_run + __shfl_xor(l_run, 32);
+        lds_barrier();
+        return;
+    }
+
+    // ---------------- output wave ----------------
+    const int dh = wave >> 2;  // output half of the head dimension
+    const char* VTb = reinterpret_cast<const char*>(ent.vt + (uint64_t)kvh * ent.vt_blocks * (HD * 32));
+    // This wave's quarter of tile t's V^T block (d rows 256 dh + 128 (wave & 1) + 0..127) into stage t & 1.
+    const unsigned d0 = 256u * dh + 128u * (unsigned)(wave & 1);
+    uint32_t voffs[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const unsigned d = d0 + 16u * i + ((unsigned)lane >> 2);
+        voffs[i] = d * 64u + ((((unsigned)lane & 3u) ^ swz_v(d)) << 4);
+    }
+    auto vdma = [&](int t) __attribute__((always_inline)) {
+        t = __builtin_amdgcn_readfirstlane(t);
+        const unsigned t0 = kb + (unsigned)t * kPfKeys;
+        const char* src = uniform_ptr(VTb + (uint64_t)(t0 >> 5) * kPfKTileBytes<HD>);
+        const uint32_t lds = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sm.vt[t & 1][d0 * 64u]);
+#pragma unroll
+        for (int i = 0; i < 8; i++) lds_dma16_s(voffs[i], src, lds + 1024u * i);
+    };
+    f32x16 acc[8];
+#pragma unroll
+    for (int b = 0; b < 8; b++) acc[b] = f32x16{};
+    const unsigned vx = swz_v((unsigned)col);
+    unsigned voff[2];
+#pragma unroll
+    for (int s = 0; s < 2; s++) voff[s] = (unsigned)col * 64u + ((((unsigned)(2 * s + half)) ^ vx) << 4);
+    // Tile it's output for this half: probabilities and alpha from the score wave's slot, the
+    // rescale when a row's reference max moved, the 16 MFMAs with the V^T operands read R ahead.
+    auto output = [&](int it) __attribute__((always_inline)) {
+        it = __builtin_amdgcn_readfirstlane(it);
+        const unsigned char* vbuf = sm.vt[it & 1] + 256u * 64u * dh;
+        f16x8 vr[16];
+        auto vread = [&](int o) __attribute__((always_inline)) {
+            vr[o] = *reinterpret_cast<const f16x8*>(vbuf + voff[o & 1] + 2048u * (o >> 1));
+        };
+#pragma unroll
+        for (int i = 0; i < R; i++) vread(i);
+        const f16x8 pin[2] = {sm.p[sw][it & 1][0][lane], sm.p[sw][it & 1][1][lane]};
+        const float al = sm.alpha[sw][it & 1][lane];
+        if (__any(al != 1.0f)) {
+#pragma unroll
+            for (int b = 0; b < 8; b++) acc[b] *= al;
+        }
+#pragma unroll
+        for (int o = 0; o < 16; o++) {
+            acc[o >> 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vr[o], pin[o & 1], acc[o >> 1], 0, 0, 0);
+            if (o + R < 16) vread(o + R);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    vm_barrier();  // (tile 0's K)
+    vdma(0);
+    if (n_tiles == 1) {
+        vm_barrier();  // tile 0's V^T is in LDS
+        output(0);
+    } else {
+        vm_barrier();  // (tile 1's K)
+        int it = 1;
+        for (; it + 1 < n_tiles; it++) {
+            vm_barrier();  // tile it - 1's V^T is in LDS
+            vdma(it);      // into the stage of tile it - 2, added in the previous phase
+            output(it - 1);
+        }
+        vm_barrier();
+        vdma(it);  // the last tile's V^T (it = n - 1)
+        output(it - 1);
+        vm_barrier();
+        output(it);
+    }
+    lds_barrier();  // (m, l) of every row are in LDS
+    const float m_fin = sm.ml[sw][0][lane];
+    const float L = sm.ml[sw][1][lane];
+    if (!row_live) return;
+    const uint64_t qrow = (uint64_t)tok * NQH + kvh * G + head;
+    if (wk.n_parts == 1) {
+        float* dst = ent.out + qrow * HD + 256u * dh + 4 * half;
+        const float inv = 1.0f / L;
+#pragma unroll
+        for (int b = 0; b < 8; b++)
+#pragma unroll
+            for (int g = 0; g < 4; g++)
+                stg<f32x4>(dst + 32 * b + 8 * g, f32x4{acc[b][4 * g] * inv, acc[b][4 * g + 1] * inv,
+                                                      acc[b][4 * g + 2] * inv, acc[b][4 * g + 3] * inv});
+        return;
+    }
+    const unsigned tile_tok0 = (unsigned)wk.tile * kPfRows / G;
+    const uint64_t slot = (uint64_t)wk.split_base + (uint64_t)(tok - tile_tok0) * wk.n_parts + wk.part;
+    const uint64_t rec = (slot * NKH + kvh) * G + head;
+    float* po = a.part_o + rec * HD + 256u * dh + 4 * half;
+#pragma unroll
+    for (int b = 0; b < 8; b++)
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+            stg<f32x4>(po + 32 * b + 8 * g, f32x4{acc[b][4 * g], acc[b][4 * g + 1], acc[b][4 * g + 2], acc[b][4 * g + 3]});
+    if (half == 0 && dh == 0) stg<f32x2>(a.part_ml + rec * 2, f32x2{m_fin, L});
+}
+
 // V of one cache in 32-key blocks [kv head][block][HD][32] (f16): block j holds
 // rows 32 j .. 32 j + 31 (rows past the cache's end repeat its last row).
 struct VtCacheDev {
@@ -1177,8 +1526,8 @@ bool prefill_dma_enabled() {
     return env != 0;
 }
 
-// head_dim 256 in the pipelined form: the two-waves-per-SIMD kernel (k_prefill_pp), or with
-// G4_PREFILL_PP=0 the one-wave-per-SIMD kernel (k_prefill_dma<256>).
+// The pipelined form's kernels: score and output waves sharing the scores (k_prefill_pp at head_dim
+// 256, k_prefill_pp512 at 512), or with G4_PREFILL_PP=0 one wave per SIMD (k_prefill_dma).
 bool prefill_pp_enabled() {
     static const int env = pf_env("G4_PREFILL_PP", 1);
     return env != 0;
@@ -1423,7 +1772,12 @@ static int prefill_run(const g4_decode_plan* plan, void* stream, hipEvent_t star
     }
     const dim3 grid(r.n_work, r.num_kv_heads, r.head_dim / 256);
     if (r.n_vtc) {
-        if (hd512) {
+        if (hd512 && prefill_pp_enabled()) {  // grid z: the row half of each work item's query tile
+            if (start_ev || stop_ev)
+                hipExtLaunchKernelGGL(k_prefill_pp512, grid, dim3(6 * 64), 0, st, start_ev, stop_ev, 0, a);
+            else
+                hipLaunchKernelGGL(k_prefill_pp512, grid, dim3(6 * 64), 0, st, a);
+        } else if (hd512) {  // grid z: the output half of the head dimension
             if (start_ev || stop_ev)
                 hipExtLaunchKernelGGL(k_prefill_dma<512>, grid, dim3(kPfThreads), 0, st, start_ev, stop_ev, 0, a);
             else
