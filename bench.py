@@ -233,6 +233,36 @@ class CacheSet:
         for _, p in self.layer_plans:
             ops.attn_step_run(p)
 
+    def prepare_chain(self, torch, dev, hidden=1536):
+        """The projections either side of every layer's attention (random f16 weights of E2B's shapes):
+        attn.linearQKV into the entry's raw q/k/v (q alone for a consumer, whose k/v come from its
+        producer) and attn.linearOut from attnOut (src/engine.ts:2045-2052, 2096)."""
+        self.hidden = hidden
+        self.x = torch.randn(hidden, device=dev)
+        self.chain = []
+        for it, (_, plan) in zip(self.items, self.layer_plans):
+            hd = it["hd"]
+            n = NQH * hd
+            segs = [(NQH * hd, it["q"])]
+            if it["store_kv"]:
+                segs += [(NKH * hd, it["k"]), (NKH * hd, it["v"])]
+            qkv = [((torch.randn(rows, hidden, device=dev) * 0.02).half().view(torch.int16), out, rows)
+                   for rows, out in segs]
+            wo = (torch.randn(hidden, n, device=dev) * 0.02).half().view(torch.int16)
+            self.chain.append((plan, qkv, n, wo, it["out"], torch.empty(hidden, device=dev)))
+
+    def step_chain(self, ops, fused):
+        """One token in the engine's order: per layer, q/k/v projection, attention pass, then the merge
+        launch and o_proj (four launches) or o_proj with the merge folded in (three launches)."""
+        for plan, qkv, n, wo, attn_out, y in self.chain:
+            ops.linear_f16(self.x, self.hidden, qkv)
+            ops.attn_step_run_attention(plan)
+            if fused:
+                ops.attn_step_run_out(plan, n, [(wo, y, self.hidden)])
+            else:
+                ops.attn_step_run_merge(plan)
+                ops.linear_f16(attn_out, n, [(wo, y, self.hidden)])
+
 
 def run_gpu(spec, args, decode_loop=False):
     import torch
@@ -314,27 +344,45 @@ def run_gpu(spec, args, decode_loop=False):
         log(f"decode loop (prepare + run per token): {result['loop_us']:.2f} us/token, prepare "
             f"{result['loop_prepare_us']:.2f} us/token on the host")
 
-    # The engine's issue order: one single-entry step (attention + merge) per layer, replayed as a HIP graph.
-    if args.sequential and len(spec["layers"]) > 1:
-        cs = csets[0]
-        cs.prepare_per_entry(torch, ops, dev)
-        torch.cuda.synchronize()
-        cs.step_sequential(ops)
+    # The engine's issue order: one single-entry step (attention + merge) per layer, replayed as a HIP graph;
+    # then the same with each layer's projections around it. Each replay is queued behind a short spin kernel,
+    # so the host has submitted the whole graph before the GPU reaches it, and events on the stream time the
+    # GPU's execution alone (a graph's host-side submission grows with its nodes and, for one layer, takes
+    # longer than the GPU work it submits).
+    def graph_us(fn):
+        fn()
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            cs.step_sequential(ops)
+            fn()
         torch.cuda.synchronize()
         for _ in range(3):
             g.replay()
         torch.cuda.synchronize()
-        n = max(10, args.steps // 2)
-        t2 = time.perf_counter()
-        for _ in range(n):
+        times = []
+        for _ in range(max(10, args.steps // 2)):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda._sleep(2_000_000)
+            e0.record(stream)
             g.replay()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            times.append(e0.elapsed_time(e1) * 1e3)
+        times.sort()
+        return times[len(times) // 2]
+
+    if args.sequential:
+        cs = csets[0]
+        cs.prepare_per_entry(torch, ops, dev)
         torch.cuda.synchronize()
-        result["sequential_us"] = (time.perf_counter() - t2) / n * 1e6
-        log(f"layer-sequential (graph replay, one cache set): {result['sequential_us']:.1f} us/step")
+        if len(spec["layers"]) > 1:
+            result["sequential_us"] = graph_us(lambda: cs.step_sequential(ops))
+            log(f"layer-sequential (graph replay, GPU time, one cache set): {result['sequential_us']:.1f} us/step")
+        cs.prepare_chain(torch, dev)
+        result["chain_us"] = graph_us(lambda: cs.step_chain(ops, fused=False))
+        result["chain_fused_us"] = graph_us(lambda: cs.step_chain(ops, fused=True))
+        log(f"layer chain with projections (graph replay, GPU time): {result['chain_us']:.1f} us/token with the merge "
+            f"launch, {result['chain_fused_us']:.1f} us/token with the merge folded into o_proj")
     del csets
     torch.cuda.empty_cache()
     return result
@@ -697,6 +745,13 @@ def decode_line(name, args, decode_loop):
                                        "RoPE factors, pinned-ring uploads) and run, inside the timed region"}
     if "sequential_us" in r:
         line["layer_sequential_us_per_token"] = round(r["sequential_us"], 2)
+    if "chain_us" in r:
+        line["layer_chain"] = {
+            "merge_launch_us_per_token": round(r["chain_us"], 2),
+            "merge_in_o_proj_us_per_token": round(r["chain_fused_us"], 2),
+            "what": "per token, every layer in the engine's order: q/k/v projection, attention pass, then the merge "
+                    "launch and o_proj, or o_proj with the merge folded in (g4_attn_step_run_out); f16 weights of "
+                    "E2B's shapes (hidden 1536); a HIP graph queued ahead of the GPU, median GPU time of a replay"}
     if not args.no_cpu_baseline:
         cpu = run_cpu_baseline(spec, args.cpu_seconds)
         cpu_gbs = r["bytes"] / cpu["per_token_s"] / 1e9
@@ -743,7 +798,7 @@ def main():
     if also:
         sub = decode_line(also, args, args.decode_loop)
         keep = ("value", "unit", "ms_per_step", "us_per_token", "config", "roofline", "decode_loop",
-                "layer_sequential_us_per_token", "cpu_baseline")
+                "layer_sequential_us_per_token", "layer_chain", "cpu_baseline")
         line[also] = {k: sub[k] for k in keep if k in sub}
     print(json.dumps(line), flush=True)
 

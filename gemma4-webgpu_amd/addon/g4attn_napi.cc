@@ -555,27 +555,22 @@ bool get_prop(napi_env env, napi_value obj, const char* key, napi_value* out) {
 
 // ---- the projections either side of the block: attn.linearQKV / linearOut --
 
-// linear(input, n, segments[{weight, out, rows}], stream): up to four f16
-// weight matrices [rows][n] that read the same f32 input of length n.
-napi_value Linear(napi_env env, napi_callback_info info) {
-    Args a(env, info, 4);
-    void* x = a.ptr(0);
-    const uint32_t n = a.u32(1);
-    void* s = a.ptr(3);
-    if (!a.ok) return nullptr;
+// An array of {weight, out (BigInt pointers), rows} as g4_linear_seg.
+bool linear_segs(Args& a, napi_value arr, const char* who, std::vector<g4_linear_seg>* segs) {
+    napi_env env = a.env;
     bool is_array = false;
-    napi_is_array(env, a.v[2], &is_array);
+    napi_is_array(env, arr, &is_array);
     if (!is_array) {
-        a.fail("linear: segments must be an array");
-        return nullptr;
+        a.fail(std::string(who) + ": segments must be an array");
+        return false;
     }
     uint32_t count = 0;
-    napi_get_array_length(env, a.v[2], &count);
-    std::vector<g4_linear_seg> segs(count);
+    napi_get_array_length(env, arr, &count);
+    segs->assign(count, g4_linear_seg{});
     for (uint32_t i = 0; i < count; i++) {
         napi_value obj, v;
-        napi_get_element(env, a.v[2], i, &obj);
-        const std::string at = "linear: segment " + std::to_string(i) + ": ";
+        napi_get_element(env, arr, i, &obj);
+        const std::string at = std::string(who) + ": segment " + std::to_string(i) + ": ";
         const void* ptrs[2] = {};
         const char* keys[2] = {"weight", "out"};
         for (int k = 0; k < 2; k++) {
@@ -584,18 +579,31 @@ napi_value Linear(napi_env env, napi_callback_info info) {
             if (!get_prop(env, obj, keys[k], &v) || napi_get_value_bigint_uint64(env, v, &p, &lossless) != napi_ok ||
                 !lossless) {
                 a.fail(at + keys[k] + " must be a BigInt pointer");
-                return nullptr;
+                return false;
             }
             ptrs[k] = reinterpret_cast<const void*>(static_cast<uintptr_t>(p));
         }
         uint32_t rows = 0;
         if (!get_prop(env, obj, "rows", &v) || napi_get_value_uint32(env, v, &rows) != napi_ok) {
             a.fail(at + "rows must be a number");
-            return nullptr;
+            return false;
         }
-        segs[i] = g4_linear_seg{static_cast<const uint16_t*>(ptrs[0]), (float*)const_cast<void*>(ptrs[1]), rows};
+        (*segs)[i] = g4_linear_seg{static_cast<const uint16_t*>(ptrs[0]), (float*)const_cast<void*>(ptrs[1]), rows};
     }
-    CALL(env, g4_linear_f16((const float*)x, n, segs.data(), count, s));
+    return true;
+}
+
+// linear(input, n, segments[{weight, out, rows}], stream): up to four f16
+// weight matrices [rows][n] that read the same f32 input of length n.
+napi_value Linear(napi_env env, napi_callback_info info) {
+    Args a(env, info, 4);
+    void* x = a.ptr(0);
+    const uint32_t n = a.u32(1);
+    void* s = a.ptr(3);
+    if (!a.ok) return nullptr;
+    std::vector<g4_linear_seg> segs;
+    if (!linear_segs(a, a.v[2], "linear", &segs)) return nullptr;
+    CALL(env, g4_linear_f16((const float*)x, n, segs.data(), (uint32_t)segs.size(), s));
     return undefined(env);
 }
 
@@ -809,6 +817,44 @@ napi_value AttnStepRun(napi_env env, napi_callback_info info) {
     return undefined(env);
 }
 
+// The plan argument of the step's run calls (a 64-byte array from attnStepPrepare).
+bool step_plan_arg(Args& a, size_t i, const char* who, g4_decode_plan* plan) {
+    void* d = nullptr;
+    size_t n = 0;
+    a.bytes(i, &d, &n);
+    if (!a.ok) return false;
+    if (n != sizeof(g4_decode_plan)) {
+        a.fail(std::string(who) + ": not a plan from attnStepPrepare");
+        return false;
+    }
+    memcpy(plan, d, sizeof *plan);
+    return true;
+}
+
+napi_value AttnStepRunAttention(napi_env env, napi_callback_info info) {
+    Args a(env, info, 2);  // plan, stream
+    g4_decode_plan plan;
+    if (!step_plan_arg(a, 0, "attnStepRunAttention", &plan)) return nullptr;
+    void* s = a.ptr(1);
+    if (!a.ok) return nullptr;
+    CALL(env, g4_attn_step_run_attention(&plan, s));
+    return undefined(env);
+}
+
+// attnStepRunOut(plan, segments[{weight, out, rows}], stream): attn.linearOut of every entry with the
+// step's merge folded in.
+napi_value AttnStepRunOut(napi_env env, napi_callback_info info) {
+    Args a(env, info, 3);
+    g4_decode_plan plan;
+    if (!step_plan_arg(a, 0, "attnStepRunOut", &plan)) return nullptr;
+    void* s = a.ptr(2);
+    if (!a.ok) return nullptr;
+    std::vector<g4_linear_seg> segs;
+    if (!linear_segs(a, a.v[1], "attnStepRunOut", &segs)) return nullptr;
+    CALL(env, g4_attn_step_run_out(&plan, segs.data(), (uint32_t)segs.size(), s));
+    return undefined(env);
+}
+
 // ---- causal prefill ---------------------------------------------------------
 
 // One g4_prefill_entry from {q, kCache, vCache, out (BigInt pointers), nTokens, start, slidingWindow, scale}.
@@ -992,6 +1038,8 @@ napi_value Init(napi_env env, napi_value exports) {
         {"attnStepWorkspaceSize", AttnStepWorkspaceSize},
         {"attnStepPrepare", AttnStepPrepare},
         {"attnStepRun", AttnStepRun},
+        {"attnStepRunAttention", AttnStepRunAttention},
+        {"attnStepRunOut", AttnStepRunOut},
         {"attnPrefillWorkspaceSize", AttnPrefillWorkspaceSize},
         {"attnPrefillPrepare", AttnPrefillPrepare},
         {"attnPrefillRun", AttnPrefillRun},

@@ -21,6 +21,7 @@
 #include <vector>
 
 #include "decode_core.h"
+#include "gemv_core.h"
 
 namespace g4 {
 
@@ -227,37 +228,28 @@ __global__ __launch_bounds__(kMergeThreads) void k_decode_merge(const DecodeEntr
 // in record order.
 constexpr unsigned kSmallMergeSplits = 8;
 
-// NS: the launch's largest split count rounded up to 2, 4 or 8 (records past an entry's own count
-// are not loaded).
+// One query head's columns [d, d + COLS) of the first `ns` records from rec0
+// (record s at rec0 + s * rec_stride), for NS slots: every (m, l) and column is
+// requested at once, indexes clamped to the last record (the extra slots
+// weigh 0 in merge_small_fold).
 template <int HD, int COLS, int NS>
-__global__ __launch_bounds__(kMergeThreads) void k_decode_merge_small(const DecodeEntryDev* __restrict__ table,
-                                                                      float* one_out, uint32_t one_split_base,
-                                                                      uint32_t one_splits, float* part_ml,
-                                                                      float* part_o, uint32_t num_kv_heads,
-                                                                      uint32_t group) {
-    constexpr unsigned TPH = HD / COLS;  // threads per query head
-    const DecodeEntryDev ent = merge_entry(table, one_out, one_split_base, one_splits);
-    DecodeArgs a{};
-    a.num_kv_heads = num_kv_heads;
-    a.group = group;
-    a.part_ml = part_ml;
-    a.part_o = part_o;
-    const unsigned ns = ent.n_splits;
-    if (ns <= 1) return;
-    const unsigned G = a.group, kvh = blockIdx.y;
-    const unsigned h = threadIdx.x / TPH, d = (threadIdx.x % TPH) * COLS;
-    if (h >= G) return;
-    const uint64_t rec_stride = (uint64_t)a.num_kv_heads * G;  // partial records per split
-    const uint64_t rec0 = ((uint64_t)ent.split_base * a.num_kv_heads + kvh) * G + h;
-    f32x4 v[NS][COLS / 4];
-    f32x2 w[NS];
+__device__ __forceinline__ void merge_small_load(const float* part_ml, const float* part_o, uint64_t rec0,
+                                                 uint64_t rec_stride, unsigned ns, unsigned d,
+                                                 f32x4 (&v)[NS][COLS / 4], f32x2 (&w)[NS]) {
 #pragma unroll
     for (unsigned s = 0; s < (unsigned)NS; s++) {
         const uint64_t rec = rec0 + (uint64_t)min(s, ns - 1) * rec_stride;
-        w[s] = ldg<f32x2>(a.part_ml + rec * 2);
+        w[s] = ldg<f32x2>(part_ml + rec * 2);
 #pragma unroll
-        for (int c = 0; c < COLS / 4; c++) v[s][c] = ldg<f32x4>(a.part_o + rec * HD + d + 4 * c);
+        for (int c = 0; c < COLS / 4; c++) v[s][c] = ldg<f32x4>(part_o + rec * HD + d + 4 * c);
     }
+}
+
+// The merged columns: common max M, then the rescaled l and o summed in record
+// order, o / l.
+template <int COLS, int NS>
+__device__ __forceinline__ void merge_small_fold(const f32x4 (&v)[NS][COLS / 4], const f32x2 (&w)[NS], unsigned ns,
+                                                 f32x4 (&res)[COLS / 4]) {
     float M = w[0][0];
 #pragma unroll
     for (unsigned s = 1; s < (unsigned)NS; s++)
@@ -273,9 +265,35 @@ __global__ __launch_bounds__(kMergeThreads) void k_decode_merge_small(const Deco
 #pragma unroll
         for (int c = 0; c < COLS / 4; c++) acc[c] += v[s][c] * f;
     }
+#pragma unroll
+    for (int c = 0; c < COLS / 4; c++) res[c] = acc[c] / L;
+}
+
+// NS: the launch's largest split count rounded up to 2, 4 or 8 (records past an entry's own count
+// are not loaded).
+template <int HD, int COLS, int NS>
+__global__ __launch_bounds__(kMergeThreads) void k_decode_merge_small(const DecodeEntryDev* __restrict__ table,
+                                                                      float* one_out, uint32_t one_split_base,
+                                                                      uint32_t one_splits, float* part_ml,
+                                                                      float* part_o, uint32_t num_kv_heads,
+                                                                      uint32_t group) {
+    constexpr unsigned TPH = HD / COLS;  // threads per query head
+    const DecodeEntryDev ent = merge_entry(table, one_out, one_split_base, one_splits);
+    const unsigned ns = ent.n_splits;
+    if (ns <= 1) return;
+    const unsigned G = group, kvh = blockIdx.y;
+    const unsigned h = threadIdx.x / TPH, d = (threadIdx.x % TPH) * COLS;
+    if (h >= G) return;
+    const uint64_t rec_stride = (uint64_t)num_kv_heads * G;  // partial records per split
+    const uint64_t rec0 = ((uint64_t)ent.split_base * num_kv_heads + kvh) * G + h;
+    f32x4 v[NS][COLS / 4];
+    f32x2 w[NS];
+    merge_small_load<HD, COLS, NS>(part_ml, part_o, rec0, rec_stride, ns, d, v, w);
+    f32x4 res[COLS / 4];
+    merge_small_fold<COLS, NS>(v, w, ns, res);
     float* out = ent.out + ((uint64_t)kvh * G + h) * HD + d;
 #pragma unroll
-    for (int c = 0; c < COLS / 4; c++) stg<f32x4>(out + 4 * c, acc[c] / L);
+    for (int c = 0; c < COLS / 4; c++) stg<f32x4>(out + 4 * c, res[c]);
 }
 
 #define MERGE_KARGS                                                                                               \
@@ -325,6 +343,165 @@ int launch_decode_merge(const DecodeArgs& a, unsigned n_entries, unsigned max_sp
     if (!n_entries || max_splits <= 1) return G4_OK;
     if (head_dim == 512) return launch_decode_merge_hd<512>(a, n_entries, max_splits, st);
     return launch_decode_merge_hd<256>(a, n_entries, max_splits, st);
+}
+
+// attn.linearOut after a decode step (src/engine.ts:2096, the projection that
+// follows the attention block), with the step's log-sum-exp merge folded in, so
+// that a layer's attention output needs no launch of its own. Workgroup (x, e)
+// serves entry e: when the entry was cut into parts it merges their records
+// (merge_small_load / merge_small_fold: the arithmetic and record order of
+// k_decode_merge_small, so the values are bit-identical to the merge launch's),
+// keeps the merged attnOut in LDS, and workgroups with x == 0 also write it to
+// the entry's attnOut; otherwise it reads attnOut. Its four waves then take
+// rows_per_wave rows each of seg[e]'s weight, two at a time, with k_linear's
+// row arithmetic (gemv_core.h), so each row is bit-identical to g4_linear_f16
+// over the merged attnOut. The first row pair's weights are requested after
+// the records and before the merge arithmetic, so they arrive under it.
+// NS > 1: the merged form (one kv head; COLS = group * HD / 256 columns per
+// thread, NJ = COLS); NS = 1: every entry's attnOut is final.
+template <int HD, int COLS, int NS, int NJ>
+__global__ __launch_bounds__(256) void k_step_out(StepOutArgs a) {
+    constexpr unsigned N = NJ * 256;
+    __shared__ float xs[NS > 1 ? N : 4];
+    const unsigned e = blockIdx.y;
+    const DecodeEntryDev ent = a.ents[e];
+    const OutSegDev sg = a.seg[e];
+    const unsigned t = threadIdx.x, lane = t & 63, lq = lane & 31, half = lane >> 5;
+    const unsigned gw = blockIdx.x * 4 + (t >> 6);
+    const unsigned rows = sg.rows;
+    const unsigned r0 = gw * a.rows_per_wave;
+    const unsigned r1 = min(r0 + a.rows_per_wave, rows);
+    float xr[NJ][8];
+    f16x8 wv[NJ];
+    const uint16_t* w0 = sg.w + (uint64_t)min(r0 + half, rows - 1) * N;  // clamped: a valid address
+    bool merged = false;
+    if constexpr (NS > 1) {
+        if (a.merge && ent.n_splits > 1) {  // uniform: the entry's fields are scalars
+            merged = true;
+            constexpr unsigned TPH = HD / COLS;  // threads per query head (TPH * group = 256)
+            const unsigned h = t / TPH, d = (t % TPH) * COLS;
+            const unsigned ns = ent.n_splits;
+            f32x4 v[NS][COLS / 4];
+            f32x2 w[NS];
+            merge_small_load<HD, COLS, NS>(a.part_ml, a.part_o, (uint64_t)ent.split_base * a.group + h, a.group,
+                                           ns, d, v, w);
+            gemv_row_load<NJ>(w0, lq, wv);
+            f32x4 res[COLS / 4];
+            merge_small_fold<COLS, NS>(v, w, ns, res);
+            float* xo = xs + h * HD + d;
+#pragma unroll
+            for (int c = 0; c < COLS / 4; c++) *reinterpret_cast<f32x4*>(xo + 4 * c) = res[c];
+            if (blockIdx.x == 0) {
+#pragma unroll
+                for (int c = 0; c < COLS / 4; c++) stg<f32x4>(ent.out + h * HD + d + 4 * c, res[c]);
+            }
+            __syncthreads();
+#pragma unroll
+            for (int j = 0; j < NJ; j++) {
+                const f32x4 p = *reinterpret_cast<const f32x4*>(xs + 256 * j + 8 * lq);
+                const f32x4 q = *reinterpret_cast<const f32x4*>(xs + 256 * j + 8 * lq + 4);
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    xr[j][u] = p[u];
+                    xr[j][u + 4] = q[u];
+                }
+            }
+        }
+    }
+    if (!merged) {
+        gemv_load_x<NJ>(ent.out, lq, xr);
+        gemv_row_load<NJ>(w0, lq, wv);
+    }
+    for (unsigned r = r0; r < r1; r += 2) {
+        const unsigned row = r + half;
+        const bool valid = row < r1;
+        if (r != r0) gemv_row_load<NJ>(sg.w + (uint64_t)(valid ? row : r1 - 1) * N, lq, wv);
+        const float y = gemv_row_fold<NJ>(wv, xr);
+        if (valid && lq == 0) sg.y[row] = y;
+    }
+}
+
+bool step_out_merges(unsigned max_parts, unsigned group, unsigned num_kv_heads) {
+    return max_parts > 1 && max_parts <= kSmallMergeSplits && (group == 4 || group == 8) && num_kv_heads == 1;
+}
+
+namespace {
+
+// Waves of a 256-thread kernel resident on the device at once.
+unsigned resident_waves_of(const void* kernel) {
+    static std::mutex mu;
+    static std::map<std::pair<int, const void*>, unsigned> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = cache.find({dev, kernel});
+    if (it != cache.end()) return it->second;
+    int per_cu = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, 0) != hipSuccess || per_cu < 1) per_cu = 1;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 256;
+    const unsigned w = (unsigned)per_cu * (unsigned)cus * 4;
+    cache.emplace(std::make_pair(dev, kernel), w);
+    return w;
+}
+
+// Rows per wave spread every entry's rows over the resident waves (at least
+// one row pair per wave); grid x covers the longest entry.
+template <int HD, int COLS, int NS, int NJ>
+int run_step_out(StepOutArgs& a, unsigned n_entries, hipStream_t st) {
+    const auto kernel = k_step_out<HD, COLS, NS, NJ>;
+    uint64_t total = 0;
+    unsigned max_rows = 0;
+    for (unsigned i = 0; i < n_entries; i++) {
+        total += a.seg[i].rows;
+        max_rows = max(max_rows, a.seg[i].rows);
+    }
+    const uint64_t waves = resident_waves_of(reinterpret_cast<const void*>(kernel));
+    uint64_t rpw = 2 * ((total + 2 * waves - 1) / (2 * waves));
+    if (rpw < 2) rpw = 2;
+    a.rows_per_wave = (uint32_t)rpw;
+    const uint64_t wave_count = (max_rows + rpw - 1) / rpw;
+    hipLaunchKernelGGL(kernel, dim3((unsigned)((wave_count + 3) / 4), n_entries), dim3(256), 0, st, a);
+    G4_CHECK_LAUNCH("attnStepOut");
+    return G4_OK;
+}
+
+template <int HD, int COLS>
+int run_step_out_merged(StepOutArgs& a, unsigned n_entries, unsigned max_parts, hipStream_t st) {
+    if (max_parts <= 2) return run_step_out<HD, COLS, 2, COLS>(a, n_entries, st);
+    if (max_parts <= 4) return run_step_out<HD, COLS, 4, COLS>(a, n_entries, st);
+    return run_step_out<HD, COLS, 8, COLS>(a, n_entries, st);
+}
+
+}  // namespace
+
+int launch_step_out(StepOutArgs& a, unsigned n_entries, unsigned max_parts, unsigned head_dim, unsigned n,
+                    hipStream_t st) {
+    if (a.merge) {
+        if (!step_out_merges(max_parts, a.group, a.num_kv_heads) || n != a.group * head_dim)
+            return fail(G4_EINVAL, "attnStepOut: internal: merge of %u parts, group %u, %u kv heads", max_parts,
+                        a.group, a.num_kv_heads);
+        if (head_dim == 512)
+            return a.group == 8 ? run_step_out_merged<512, 16>(a, n_entries, max_parts, st)
+                                : run_step_out_merged<512, 8>(a, n_entries, max_parts, st);
+        return a.group == 8 ? run_step_out_merged<256, 8>(a, n_entries, max_parts, st)
+                            : run_step_out_merged<256, 4>(a, n_entries, max_parts, st);
+    }
+    switch (n / 256) {
+        case 4: return run_step_out<256, 4, 1, 4>(a, n_entries, st);
+        case 5: return run_step_out<256, 4, 1, 5>(a, n_entries, st);
+        case 6: return run_step_out<256, 4, 1, 6>(a, n_entries, st);
+        case 7: return run_step_out<256, 4, 1, 7>(a, n_entries, st);
+        case 8: return run_step_out<256, 4, 1, 8>(a, n_entries, st);
+        case 9: return run_step_out<256, 4, 1, 9>(a, n_entries, st);
+        case 10: return run_step_out<256, 4, 1, 10>(a, n_entries, st);
+        case 11: return run_step_out<256, 4, 1, 11>(a, n_entries, st);
+        case 12: return run_step_out<256, 4, 1, 12>(a, n_entries, st);
+        case 13: return run_step_out<256, 4, 1, 13>(a, n_entries, st);
+        case 14: return run_step_out<256, 4, 1, 14>(a, n_entries, st);
+        case 15: return run_step_out<256, 4, 1, 15>(a, n_entries, st);
+        case 16: return run_step_out<256, 4, 1, 16>(a, n_entries, st);
+        default: return fail(G4_EINVAL, "attnStepOut: input length %u unsupported", n);
+    }
 }
 
 }  // namespace g4

@@ -91,6 +91,37 @@ struct DecodeArgs {
 int launch_decode_merge(const DecodeArgs& a, unsigned n_entries, unsigned max_splits, hipStream_t st,
                         unsigned head_dim = 256);
 
+// attn.linearOut over the entries of a decode step, with the step's merge
+// folded in (decode.hip): workgroup (x, e) merges entry e's partial records
+// (or reads its attnOut when the entry had one part, or when `merge` is 0),
+// and workgroups x == 0 write the merged attnOut; then its waves take rows
+// of seg[e]'s f16 weight like k_linear (linear.hip), each row bit-identical to
+// g4_linear_f16 over the merged attnOut.
+constexpr int kOutMaxSegs = 64;
+struct OutSegDev {
+    const uint16_t* w;  // f16 [rows][n]
+    float* y;           // f32 [rows]
+    uint32_t rows;
+    uint32_t pad;
+};
+struct StepOutArgs {
+    const DecodeEntryDev* ents;  // per entry: out (attnOut), split_base, n_splits
+    const float* part_ml;
+    const float* part_o;
+    uint32_t num_kv_heads;
+    uint32_t group;
+    uint32_t rows_per_wave;  // even
+    uint32_t merge;          // 1: entries with more than one part are merged here; 0: attnOut is final
+    OutSegDev seg[kOutMaxSegs];
+};
+// n = num_kv_heads * group * head_dim (a multiple of 256 in [1024, 4096]);
+// max_parts: the largest part count of an entry. Merges here when max_parts
+// <= 8, group is 4 or 8 and num_kv_heads is 1 (otherwise the caller runs the
+// merge launch first and passes merge = 0).
+bool step_out_merges(unsigned max_parts, unsigned group, unsigned num_kv_heads);
+int launch_step_out(StepOutArgs& a, unsigned n_entries, unsigned max_parts, unsigned head_dim, unsigned n,
+                    hipStream_t st);
+
 template <int HD>
 struct DecodeDims {
     static constexpr int NC = HD / 32;   // K chunks of 32 d per score MFMA chain

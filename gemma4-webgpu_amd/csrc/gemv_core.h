@@ -37,15 +37,19 @@ __device__ __forceinline__ void gemv_load_x(const float* x, unsigned lq, float (
     }
 }
 
-// The row's value (in every lane of the half-wave); `row` points at the
-// row's first element, 16-byte aligned.
+// The lane's weights of a row (8 columns of every 256-column block); `row`
+// points at the row's first element, 16-byte aligned.
 template <int NJ>
-__device__ __forceinline__ float gemv_row_dot(const uint16_t* row, const float (&xr)[NJ][8], unsigned lq) {
-#pragma clang fp contract(off)
+__device__ __forceinline__ void gemv_row_load(const uint16_t* row, unsigned lq, f16x8 (&wv)[NJ]) {
     const uint16_t* w = row + 8 * lq;
-    f16x8 wv[NJ];
 #pragma unroll
     for (int j = 0; j < NJ; j++) wv[j] = ldg_nt<f16x8>(w + 256 * j);
+}
+
+// The row's value from weights loaded by gemv_row_load (in every lane of the half-wave).
+template <int NJ>
+__device__ __forceinline__ float gemv_row_fold(const f16x8 (&wv)[NJ], const float (&xr)[NJ][8]) {
+#pragma clang fp contract(off)
     float acc[8];
 #pragma unroll
     for (int e = 0; e < 8; e++) acc[e] = 0.0f;
@@ -62,6 +66,15 @@ __device__ __forceinline__ float gemv_row_dot(const uint16_t* row, const float (
     acc[0] = acc[0] + acc[2];                                    // stride 2
     acc[1] = acc[1] + acc[3];
     return acc[0] + acc[1];                                      // stride 1
+}
+
+// The row's value (in every lane of the half-wave); `row` points at the
+// row's first element, 16-byte aligned.
+template <int NJ>
+__device__ __forceinline__ float gemv_row_dot(const uint16_t* row, const float (&xr)[NJ][8], unsigned lq) {
+    f16x8 wv[NJ];
+    gemv_row_load<NJ>(row, lq, wv);
+    return gemv_row_fold<NJ>(wv, xr);
 }
 
 // The same row value for quantized weights, in matmul_q8.wgsl's and

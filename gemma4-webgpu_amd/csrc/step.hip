@@ -289,8 +289,9 @@ struct StepPlanRep {
     uint32_t waves;      // waves per workgroup of the attention kernel (4 or 8)
     uint32_t head_dim;   // 256 or 512
     uint32_t magic;
-    uint32_t off_merge;  // byte offsets of the merge table and the RoPE factors in the tables region
+    uint32_t off_merge;  // byte offsets of the merge table, the entry table and the RoPE factors in the tables region
     uint32_t off_rope;
+    uint32_t off_ents;
 };
 static_assert(sizeof(StepPlanRep) <= sizeof(g4_decode_plan), "plan size");
 
@@ -337,8 +338,9 @@ int g4_attn_step_prepare(const g4_step_entry* entries, uint32_t n_entries, uint3
     if (rc) return fail(rc, "%s", err);
     rc = stage_upload(ws + L.tables, ph.blob.data(), ph.blob.size(), as_stream(stream));  // the tables in one copy
     if (rc) return rc;
-    StepPlanRep r = {ws,       n_entries, ph.n_wgs, num_kv_heads, G, ph.n_merge, ph.max_parts,
-                     ph.waves, head_dim,  kStepMagic, (uint32_t)ph.off_merge, (uint32_t)ph.off_rope};
+    StepPlanRep r = {ws,       n_entries,  ph.n_wgs,   num_kv_heads,           G,
+                     ph.n_merge, ph.max_parts, ph.waves, head_dim, kStepMagic, (uint32_t)ph.off_merge,
+                     (uint32_t)ph.off_rope, (uint32_t)ph.off_ents};
     memset(plan, 0, sizeof *plan);
     memcpy(plan, &r, sizeof r);
     return G4_OK;
@@ -407,6 +409,40 @@ int g4_attn_step_run_merge(const g4_decode_plan* plan, void* stream) {
     m.part_ml = reinterpret_cast<float*>(r.ws + L.part_ml);
     m.part_o = reinterpret_cast<float*>(r.ws + L.part_o);
     return launch_decode_merge(m, r.n_merge, r.max_parts, as_stream(stream), r.head_dim);
+}
+
+int g4_attn_step_run_out(const g4_decode_plan* plan, const g4_linear_seg* o_proj, uint32_t n_segs, void* stream) {
+    StepPlanRep r;
+    int rc = step_plan(plan, &r);
+    if (rc) return rc;
+    if (!o_proj) return fail(G4_EINVAL, "attnStepOut: o_proj is NULL");
+    if (n_segs != r.n_entries)
+        return fail(G4_EINVAL, "attnStepOut: %u weight segments for a step of %u entries", n_segs, r.n_entries);
+    if (n_segs > (uint32_t)kOutMaxSegs)
+        return fail(G4_EINVAL, "attnStepOut: %u entries (max %d)", n_segs, kOutMaxSegs);
+    const uint32_t n = r.num_kv_heads * r.group * r.head_dim;
+    if (n % 256 || n / 256 < 4 || n / 256 > 16)
+        return fail(G4_EINVAL, "attnStepOut: input length %u unsupported (a multiple of 256 in [1024, 4096])", n);
+    const StepLayout L = step_layout(r.n_entries, r.num_kv_heads, r.group, r.head_dim);
+    StepOutArgs a = {};
+    for (uint32_t i = 0; i < n_segs; i++) {
+        const g4_linear_seg& sg = o_proj[i];
+        if (!sg.weight || !sg.out) return fail(G4_EINVAL, "attnStepOut: segment %u has a NULL pointer", i);
+        if (reinterpret_cast<uintptr_t>(sg.weight) & 15)
+            return fail(G4_EINVAL, "attnStepOut: segment %u weight must be 16-byte aligned", i);
+        if (sg.rows == 0 || sg.rows > 0x7fffffffu) return fail(G4_EINVAL, "attnStepOut: segment %u has %u rows", i, sg.rows);
+        a.seg[i] = OutSegDev{sg.weight, sg.out, sg.rows, 0};
+    }
+    hipStream_t st = as_stream(stream);
+    const bool fused = step_out_merges(r.max_parts, r.group, r.num_kv_heads);
+    if (!fused && (rc = g4_attn_step_run_merge(plan, stream))) return rc;
+    a.ents = reinterpret_cast<const DecodeEntryDev*>(r.ws + L.tables + r.off_ents);
+    a.part_ml = reinterpret_cast<const float*>(r.ws + L.part_ml);
+    a.part_o = reinterpret_cast<const float*>(r.ws + L.part_o);
+    a.num_kv_heads = r.num_kv_heads;
+    a.group = r.group;
+    a.merge = fused ? 1u : 0u;
+    return launch_step_out(a, r.n_entries, r.max_parts, r.head_dim, n, st);
 }
 
 int g4_attn_step_run(const g4_decode_plan* plan, void* stream) {

@@ -168,6 +168,7 @@ SIGNATURES: dict[str, list] = {
     "g4_attn_step_run": [C.POINTER(DecodePlan), _P],
     "g4_attn_step_run_attention": [C.POINTER(DecodePlan), _P],
     "g4_attn_step_run_merge": [C.POINTER(DecodePlan), _P],
+    "g4_attn_step_run_out": [C.POINTER(DecodePlan), C.POINTER(LinearSeg), _U32, _P],
     "g4_attn_step_run_attention_timed": [C.POINTER(DecodePlan), _P, _P, _P],
     "g4_attn_step": [C.POINTER(StepEntry), _U32, _U32, _U32, _U32, _P, _SZ, _P],
     "g4_attn_prefill_workspace_size": [C.POINTER(PrefillEntry), _U32, _U32, _U32, _U32, C.POINTER(C.c_size_t)],

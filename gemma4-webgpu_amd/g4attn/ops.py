@@ -319,6 +319,16 @@ def attn_step_run_merge(plan: DecodePlan, stream=None):
     abi.call("g4_attn_step_run_merge", C.byref(plan), _stream(stream))
 
 
+def attn_step_run_out(plan: DecodePlan, n, segments, stream=None):
+    """attn.linearOut after g4_attn_step_run_attention, with the step's merge folded in: one
+    (weight f16 [rows][n], out f32 [rows], rows) segment per entry of the plan, n = num_q_heads * head_dim.
+    Writes every entry's attnOut as g4_attn_step_run_merge does and out = weight @ attnOut."""
+    segs = (LinearSeg * len(segments))()
+    for i, (w, out, rows) in enumerate(segments):
+        segs[i] = LinearSeg(_f16(w, f"segment {i} weight", rows * n), _f32(out, f"segment {i} out", rows), rows)
+    abi.call("g4_attn_step_run_out", C.byref(plan), segs, len(segments), _stream(stream))
+
+
 def attn_step_run_attention_timed(plan: DecodePlan, start, stop, stream=None):
     """The attention launch with torch.cuda.Events (timing enabled) that take the kernel's own
     start and end timestamps. The events must exist: record each once before the first use."""

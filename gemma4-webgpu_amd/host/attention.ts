@@ -242,6 +242,8 @@ export interface Addon {
   attnStepPrepare(entries: any[], nqh: number, nkh: number, hd: number, ws: bigint, wsBytes: number,
     s: bigint): Uint8Array;
   attnStepRun(plan: Uint8Array, s: bigint): void;
+  attnStepRunAttention(plan: Uint8Array, s: bigint): void;
+  attnStepRunOut(plan: Uint8Array, segs: { weight: bigint; out: bigint; rows: number }[], s: bigint): void;
   attnPrefillWorkspaceSize(entries: any[], nqh: number, nkh: number, hd: number): number;
   attnPrefillPrepare(entries: any[], nqh: number, nkh: number, hd: number, ws: bigint, wsBytes: number,
     s: bigint): Uint8Array;
@@ -373,6 +375,25 @@ export class HipAttention {
 
   attnStep(entries: StepEntry[], shape: StepShape, workspace: DeviceBuffer): void {
     this.attnStepRun(this.attnStepPrepare(entries, shape, workspace));
+  }
+
+  // The attention pass of a prepared step alone; attnStepOut then finishes it.
+  attnStepRunAttention(plan: Uint8Array): void {
+    this.g4.attnStepRunAttention(plan, this.stream);
+  }
+
+  // attn.linearOut of every entry of a step after attnStepRunAttention (src/engine.ts:2096), with the step's
+  // merge folded into the projection's launch: each entry's attnOut is written as attnStepRun writes it, and
+  // segments[i].out = segments[i].weight (f16 [rows][numQHeads * headDim]) x attnOut, each row bit-identical
+  // to linear() over that attnOut. One segment per entry, in entry order.
+  attnStepOut(plan: Uint8Array, shape: StepShape, segments: LinearSegment[]): void {
+    const n = shape.numQHeads * shape.headDim;
+    const segs = segments.map(function (g, i) {
+      if (g.weight.size < g.rows * n * 2) throw new RangeError('attnStepOut: segment ' + i + ' weight too small');
+      if (g.out.size < g.rows * 4) throw new RangeError('attnStepOut: segment ' + i + ' out too small');
+      return { weight: g.weight.ptr, out: g.out.ptr, rows: g.rows };
+    });
+    this.g4.attnStepRunOut(plan, segs, this.stream);
   }
 
   private static prefillFlat(entries: PrefillEntry[]): any[] {

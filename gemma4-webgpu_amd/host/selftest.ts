@@ -127,7 +127,7 @@ export function cpuChecks(): string[] {
 
 interface CaseSpec {
   nqh: number; nkh: number; hd: number; seq: number; pos: number; window: number; theta: number; div: number;
-  eps: number; arrays: Record<string, number[]>;
+  eps: number; oRows: number; arrays: Record<string, number[]>;
 }
 
 function layer(dir: string): string[] {
@@ -190,17 +190,36 @@ function layer(dir: string): string[] {
     applyDivisor: spec.div, scale: 1.0, eps: spec.eps,
   }], shape, ws);
 
-  // results: out1, out2 (f32), then the stored row of kc1, vc1, kc2, vc2 (f16)
-  const row = NKH * HD * 2, o = NQH * HD * 4;
-  const res = new Uint8Array(2 * o + 4 * row);
+  // (3) the same step as attention pass + attn.linearOut with the merge folded in, and linear() over (2)'s attnOut
+  const q3 = upload('q'), k3 = upload('k'), v3 = upload('v'), kc3 = upload('kc'), vc3 = upload('vc');
+  const out3 = alloc(NQH * HD * 4), wo = upload('wo');
+  const R = spec.oRows;
+  const y3 = alloc(R * 4), y2 = alloc(R * 4);
+  const ws3 = alloc(att.attnStepWorkspaceSize(1, shape));
+  const plan3 = att.attnStepPrepare([{
+    q: q3, k: k3, v: v3, qWeight: qw, kWeight: kw, ropeFreqs: rf, ropeInvFreq: inv, kCache: kc3, vCache: vc3,
+    out: out3, seqLen: SEQ, position: spec.pos, slidingWindow: spec.window, storeKv: true, theta: spec.theta,
+    applyDivisor: spec.div, scale: 1.0, eps: spec.eps,
+  }], shape, ws3);
+  att.attnStepRunAttention(plan3);
+  att.attnStepOut(plan3, shape, [{ weight: wo, out: y3, rows: R }]);
+  att.linear(out2, NQH * HD, [{ weight: wo, out: y2, rows: R }]);
+
+  // results: out1, out2, out3 (f32), y2, y3 (f32), then the stored row of kc1, vc1, kc2, vc2 (f16)
+  const row = NKH * HD * 2, o = NQH * HD * 4, yb = R * 4;
+  const res = new Uint8Array(3 * o + 2 * yb + 4 * row);
   att.readBuffer(out1, 0, res.subarray(0, o));
   att.readBuffer(out2, 0, res.subarray(o, 2 * o));
+  att.readBuffer(out3, 0, res.subarray(2 * o, 3 * o));
+  att.readBuffer(y2, 0, res.subarray(3 * o, 3 * o + yb));
+  att.readBuffer(y3, 0, res.subarray(3 * o + yb, 3 * o + 2 * yb));
+  const base = 3 * o + 2 * yb;
   const caches = [kc1, vc1, kc2, vc2];
-  for (let i = 0; i < 4; i++) att.readBuffer(caches[i], spec.pos * row, res.subarray(2 * o + i * row, 2 * o + (i + 1) * row));
+  for (let i = 0; i < 4; i++) att.readBuffer(caches[i], spec.pos * row, res.subarray(base + i * row, base + (i + 1) * row));
   fs.writeFileSync(path.join(dir, 'out.bin'), res);
   for (const b of bufs) att.destroyBuffer(b);
   att.dispose();
-  return ['engine order: 7 dispatches', 'attnStep: 1 entry', 'results written'];
+  return ['engine order: 7 dispatches', 'attnStep: 1 entry', 'attnStepOut: 1 entry', 'results written'];
 }
 
 interface PrefillSpec {

@@ -442,6 +442,20 @@ typedef struct g4_linear_seg {
 
 int g4_linear_f16(const float* input, uint32_t n, const g4_linear_seg* segs, uint32_t n_segs, void* stream);
 
+/* attn.linearOut after a prepared decode step (src/engine.ts:2096, after the
+ * attention block of :2056-2094), with the step's log-sum-exp merge folded
+ * into the projection's launch. Call after g4_attn_step_run_attention, in
+ * place of g4_attn_step_run_merge: for every entry i of the plan, attnOut
+ * (the entry's `out`) is merged and written exactly as g4_attn_step_run_merge
+ * writes it, and o_proj[i].out receives o_proj[i].weight (f16
+ * [rows][num_q_heads * head_dim]) times attnOut, each row bit-identical to
+ * g4_linear_f16 over that attnOut. One launch when no entry spans more than 8
+ * workgroups of the attention pass and the step has one kv head of 4 or 8
+ * query heads; otherwise the merge launch, then the projection launch.
+ * n_segs: the plan's entry count (at most 64); num_q_heads * head_dim a
+ * multiple of 256 in [1024, 4096]; weights 16-byte aligned. */
+int g4_attn_step_run_out(const g4_decode_plan* plan, const g4_linear_seg* o_proj, uint32_t n_segs, void* stream);
+
 /* The same for the engine's in-shader quantized weights (weightQuant 'q8' /
  * 'q4k', src/engine.ts:2040-2043): each row bit-identical to matmulQ8 /
  * matmulQ4K. weight: int8 [rows][n] (q8) or u32 [rows][n/8] (q4k); meta: the

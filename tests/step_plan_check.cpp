@@ -80,12 +80,14 @@ int main() {
         // the blob fits the tables region, and its parts do not overlap
         if (ph.blob.size() > L.part_ml - L.tables) return bad(line, "tables blob exceeds the tables region");
         if (ph.off_merge < ph.n_wgs * sizeof(StepWorkDev)) return bad(line, "merge table overlaps the work table");
-        if (ph.off_rope < ph.off_merge + ph.n_merge * sizeof(DecodeEntryDev)) return bad(line, "rope overlaps merge");
+        if (ph.off_ents < ph.off_merge + ph.n_merge * sizeof(DecodeEntryDev)) return bad(line, "entries overlap merge");
+        if (ph.off_rope < ph.off_ents + n * sizeof(DecodeEntryDev)) return bad(line, "rope overlaps the entry table");
         const size_t cap = n > kStepMaxWgs ? n : kStepMaxWgs;
         if (ph.n_wgs > cap) return bad(line, "more work items than the workspace holds");
         if (ph.parts > kStepMaxWgs) return bad(line, "more partial records than the workspace holds");
         const StepWorkDev* work = reinterpret_cast<const StepWorkDev*>(ph.blob.data());
         const DecodeEntryDev* merge = reinterpret_cast<const DecodeEntryDev*>(ph.blob.data() + ph.off_merge);
+        const DecodeEntryDev* etab = reinterpret_cast<const DecodeEntryDev*>(ph.blob.data() + ph.off_ents);
         const size_t rope_bytes = ph.blob.size() - ph.off_rope;
         std::vector<std::vector<const StepWorkDev*>> per(n);
         for (uint32_t w = 0; w < ph.n_wgs; w++) {
@@ -126,6 +128,10 @@ int main() {
                 next = w.row_end;
             }
             if (next != e.seq_len) return bad(line, "attended rows not fully covered");
+            // the entry table: attnOut, parts, and the first record of a split entry
+            if (etab[i].out != e.out || etab[i].n_splits != items.size() ||
+                (items.size() > 1 && etab[i].split_base != items[0]->part))
+                return bad(line, "entry table disagrees with the work items");
             if (items.size() > 1) {
                 bool found = false;
                 for (uint32_t m = 0; m < ph.n_merge; m++)

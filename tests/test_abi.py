@@ -120,6 +120,8 @@ def test_argument_errors_rejected_on_host():
     assert st == abi.G4_EINVAL and "rope_freqs" in msg
     st, msg = _err(lambda L: L.g4_attn_decode_many_run(C.byref(abi.DecodePlan()), None))
     assert st == abi.G4_EINVAL and "not prepared" in msg
+    st, msg = _err(lambda L: L.g4_attn_step_run_out(C.byref(abi.DecodePlan()), None, 1, None))
+    assert st == abi.G4_EINVAL and "not prepared" in msg
 
 
 def test_lm_head_argument_errors_rejected_on_host():

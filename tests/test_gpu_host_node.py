@@ -7,7 +7,9 @@ engine's lmHead, logitSoftcap and sample.argmax dispatches and the fused lmHeadA
 bit-identical and top-1 equal to the oracle's. And attnPrefill (node host/run.js prefill): two
 chunks in one call, each token within max-abs 2e-3 of the oracle's decode chain at its position.
 The projections (node host/run.js linear): one matmulQuant dispatch per matrix and one linear call,
-both bit-identical to the oracle's matmulQuant.
+both bit-identical to the oracle's matmulQuant. The layer case also runs the step as its attention
+pass plus attnStepOut (attn.linearOut with the merge folded in): attnOut bit-identical to attnStep's,
+and the projected rows bit-identical to linear() over it and to the oracle's matmulQuant.
 """
 import json
 import shutil
@@ -29,6 +31,7 @@ RUN = ROOT / "gemma4-webgpu_amd" / "host" / "run.js"
 NODE = shutil.which("node")
 NQH, NKH, HD = 8, 1, 256
 ROPE = np.array(e2b.rope_freqs_f16_bits(256), dtype=np.uint16)
+O_ROWS = 96  # o_proj rows of the layer case
 
 
 def write_case(d: Path, seed, seq, window, theta, div, hd=HD):
@@ -38,6 +41,8 @@ def write_case(d: Path, seed, seq, window, theta, div, hd=HD):
         "v": synth.normal(seed + 2, NKH * hd) * 2.0, "qw": f16_weight_bits(seed + 3, hd),
         "kw": f16_weight_bits(seed + 4, hd), "rf": ROPE,
         "kc": cache_f16(seed + 5, seq, NKH, hd).reshape(-1), "vc": cache_f16(seed + 6, seq, NKH, hd).reshape(-1),
+        "wo": (np.random.default_rng(seed + 7).standard_normal((O_ROWS, NQH * hd), dtype=np.float32) * 0.02)
+        .astype(np.float16).view(np.uint16).reshape(-1),
     }
     blob, index = bytearray(), {}
     for name, a in arrs.items():
@@ -46,7 +51,7 @@ def write_case(d: Path, seed, seq, window, theta, div, hd=HD):
         blob += b
     (d / "case.bin").write_bytes(bytes(blob))
     (d / "case.json").write_text(json.dumps(dict(nqh=NQH, nkh=NKH, hd=hd, seq=seq, pos=pos, window=window,
-                                                 theta=theta, div=div, eps=EPS, arrays=index)))
+                                                 theta=theta, div=div, eps=EPS, oRows=O_ROWS, arrays=index)))
     return arrs, pos
 
 
@@ -75,14 +80,24 @@ def test_layer_through_ts_host(tmp_path, seq, window, theta, div, hd):
     raw = (tmp_path / "out.bin").read_bytes()
     o = NQH * hd * 4
     row = NKH * hd * 2
+    yb = O_ROWS * 4
     out_ref = np.frombuffer(raw[:o], np.float32)
     out_step = np.frombuffer(raw[o:2 * o], np.float32)
-    rows = [np.frombuffer(raw[2 * o + i * row:2 * o + (i + 1) * row], np.uint16) for i in range(4)]
+    out_split = np.frombuffer(raw[2 * o:3 * o], np.float32)
+    y_linear = np.frombuffer(raw[3 * o:3 * o + yb], np.float32)
+    y_out = np.frombuffer(raw[3 * o + yb:3 * o + 2 * yb], np.float32)
+    base = 3 * o + 2 * yb
+    rows = [np.frombuffer(raw[base + i * row:base + (i + 1) * row], np.uint16) for i in range(4)]
     want, kbits, vbits = expected(arrs, seq, pos, window, theta, div, hd)
     np.testing.assert_array_equal(out_ref.view(np.uint32), want.view(np.uint32))
     assert np.isfinite(out_step).all() and max_abs(out_step, want) <= 2e-3
     for got, exp in zip(rows, (kbits, vbits, kbits, vbits)):
         np.testing.assert_array_equal(got, exp)
+    # attention pass + attnStepOut: attnOut as attnStep writes it, rows as linear() and matmulQuant give them
+    np.testing.assert_array_equal(out_split.view(np.uint32), out_step.view(np.uint32))
+    np.testing.assert_array_equal(y_out.view(np.uint32), y_linear.view(np.uint32))
+    np.testing.assert_array_equal(y_out.view(np.uint32),
+                                  orc.matmul_quant(out_step, arrs["wo"], O_ROWS, NQH * hd).view(np.uint32))
 
 
 @pytest.mark.skipif(NODE is None, reason="node is not installed")
