@@ -11,6 +11,12 @@
         each scaled by what the same counter reads for g4bench's plain copy kernel
         (512 MiB read and 512 MiB written per launch).
 
+    profile_summary.py gaps --dir D --command "..." [--kernel REGEX] [--max-gap US]
+        From the per-dispatch kernel trace: median duration per kernel, and the median idle
+        time between one kernel's end and the next kernel's start for each pair of kernels that
+        follow each other on the stream (gaps above --max-gap, default 20 us, are left out: host
+        waits between timed sections).
+
     profile_summary.py mfma --dir D --kernel REGEX --command "..." [--simds N] [--algorithmic-flops F]
         MFMA utilisation of the kernel matching REGEX from one pass of
         `rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE SQ_INSTS_VALU_MFMA_MOPS_F16 -f csv -d D`:
@@ -67,7 +73,8 @@ def cmd_trace(a) -> None:
     for f in _csvs(a.dir, "kernel_stats.csv"):
         rows += list(csv.DictReader(f.open()))
     print(f"command: {a.command}")
-    print("kernel stats (rocprofv3 --kernel-trace --stats; durations in us)")
+    print("kernel stats (rocprofv3 --kernel-trace --stats; durations in us)" +
+          (f"; kernels matching /{a.kernel}/" if a.kernel else ""))
     print(f"{'kernel':60s} {'calls':>6s} {'avg':>9s} {'min':>9s} {'max':>9s} {'pct':>6s}")
     for r in sorted(rows, key=lambda r: -float(r["TotalDurationNs"])):
         name = r["Name"]
@@ -75,6 +82,42 @@ def cmd_trace(a) -> None:
             continue
         print(f"{name[:60]:60s} {int(r['Calls']):6d} {float(r['AverageNs']) / 1e3:9.2f} "
               f"{float(r['MinNs']) / 1e3:9.2f} {float(r['MaxNs']) / 1e3:9.2f} {float(r['Percentage']):6.2f}")
+
+
+def _short(name: str) -> str:
+    m = re.search(r"(k_\w+(?:<[^>]*>)?)", name)
+    return m.group(1) if m else name[:40]
+
+
+def cmd_gaps(a) -> None:
+    disp = []
+    for f in _csvs(a.dir, "kernel_trace.csv"):
+        for r in csv.DictReader(f.open()):
+            disp.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), _short(r["Kernel_Name"])))
+    disp.sort()
+    dur: dict[str, list[float]] = {}
+    gap: dict[tuple[str, str], list[float]] = {}
+    for i, (s0, e0, k) in enumerate(disp):
+        dur.setdefault(k, []).append((e0 - s0) / 1e3)
+        if i + 1 < len(disp):
+            s1, _, k1 = disp[i + 1]
+            g = (s1 - e0) / 1e3
+            if 0 <= g <= a.max_gap:
+                gap.setdefault((k, k1), []).append(g)
+    rx = re.compile(a.kernel) if a.kernel else None
+    print(f"command: {a.command}")
+    print("per-dispatch kernel trace (rocprofv3 --kernel-trace); durations and gaps in us, medians" +
+          (f"; kernels matching /{a.kernel}/" if a.kernel else ""))
+    print(f"{'kernel':44s} {'dispatches':>10s} {'median':>8s}")
+    for k, v in sorted(dur.items(), key=lambda kv: -sum(kv[1])):
+        if rx and not rx.search(k):
+            continue
+        print(f"{k:44s} {len(v):10d} {statistics.median(v):8.2f}")
+    print(f"{'gap: end of -> start of':60s} {'count':>6s} {'median':>8s}")
+    for (k0, k1), v in sorted(gap.items(), key=lambda kv: -len(kv[1])):
+        if rx and not (rx.search(k0) and rx.search(k1)):
+            continue
+        print(f"{k0 + ' -> ' + k1:60s} {len(v):6d} {statistics.median(v):8.2f}")
 
 
 def cmd_traffic(a) -> None:
@@ -142,6 +185,11 @@ def main() -> None:
     t.add_argument("--dir", required=True)
     t.add_argument("--command", required=True)
     t.add_argument("--kernel", default="")
+    g = sub.add_parser("gaps")
+    g.add_argument("--dir", required=True)
+    g.add_argument("--command", required=True)
+    g.add_argument("--kernel", default="")
+    g.add_argument("--max-gap", type=float, default=20.0)
     f = sub.add_parser("traffic")
     for k in ("fetch", "write", "copy_fetch", "copy_write"):
         f.add_argument("--" + k.replace("_", "-"), dest=k, required=True)
@@ -157,7 +205,7 @@ def main() -> None:
     m.add_argument("--xcds", type=int, default=8)
     m.add_argument("--algorithmic-flops", type=float, default=0.0)
     a = ap.parse_args()
-    {"trace": cmd_trace, "traffic": cmd_traffic, "mfma": cmd_mfma}[a.mode](a)
+    {"trace": cmd_trace, "gaps": cmd_gaps, "traffic": cmd_traffic, "mfma": cmd_mfma}[a.mode](a)
 
 
 if __name__ == "__main__":
