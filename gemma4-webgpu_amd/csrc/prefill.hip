@@ -733,8 +733,10 @@ __global__ __launch_bounds__(kPfThreads, 1) void k_prefill_dma(PrefillArgs a) {
 // the probabilities of tile 0. Epilogue: probabilities of tile n - 1 with the
 // output of tile n - 2, then the output of tile n - 1, then (m, l) to LDS for
 // the output waves' stores. Both roles pass the same number of barriers.
+constexpr int kPpStages = 4;  // K and V^T stages (a power of two: a tile's stage is t & 3)
 struct PrefillPpSmem {
-    PrefillDmaSmem<256> t;
+    unsigned char k[kPpStages][kPfKTileBytes<256>];  // key row r: chunk c (8 d) at r*512 + ((c ^ swz_k(r)) * 16)
+    unsigned char vt[kPpStages][kPfVtTileBytes];     // d row: chunk c (8 keys) at d*64 + ((c ^ swz_v(d)) * 16)
     f16x8 p[4][2][2][64];  // [pair][slot][operand register][lane]
     float alpha[4][2][64];
     float ml[4][2][64];    // [pair][m, l][lane]
@@ -742,11 +744,28 @@ struct PrefillPpSmem {
 
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// Waits until at most N DMA instructions of this wave are in flight and its
+// LDS reads have returned, then joins the workgroup's barrier.
+template <int N>
+__device__ __forceinline__ void vm_wait_barrier() {
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+// lds_dma16_s for a kernel in which the compiler itself never uses M0 (checked
+// in the assembly of k_prefill_pp: its only M0 writes are these): M0 is set
+// and left, two scalar instructions fewer per DMA than saving and restoring it.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"  // M0 is a reserved register: clobbering it is what is meant
+__device__ __forceinline__ void lds_dma16_m0(uint32_t voff, const void* sbase, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
 __global__ __launch_bounds__(512, 1) void k_prefill_pp(PrefillArgs a) {
     constexpr int HD = 256;
-    constexpr int D = kPfDist<HD>, NK = kPfKStages<HD>, NV = kPfVStages<HD>;
-    constexpr int NQ = HD / 16, PER = HD / 64 + 4;  // score steps, DMAs per tile and score wave
-    constexpr int R = 3;                             // LDS operand reads ahead of their MFMA
+    constexpr unsigned SM = kPpStages - 1;                       // stage of tile t: t & SM
+    constexpr int NQ = HD / 16, KPER = HD / 64, PER = KPER + 4;  // score steps; K and all DMAs per tile and score wave
+    constexpr int R = 3;                                         // LDS operand reads ahead of their MFMA
     __shared__ PrefillPpSmem sm;
     const PrefillWorkDev wk = a.work[wg_x()];
     const PrefillEntryDev& ent = a.table[wk.entry];
@@ -769,50 +788,49 @@ __global__ __launch_bounds__(512, 1) void k_prefill_pp(PrefillArgs a) {
     const char* Kb = reinterpret_cast<const char*>(ent.k + (uint64_t)kvh * HD);
     const char* VTb = reinterpret_cast<const char*>(ent.vt + (uint64_t)kvh * ent.vt_blocks * (HD * 32));
     const DmaVOffsets dof = dma_v_offsets(pair, lane);
-    struct DmaTile {
+    // One DMA request: the K rows of tile tk and the V^T block of tile tv (tiles past the range
+    // reload its last tile into stages nobody reads).
+    struct DmaTiles {
         const char* k;
         const char* v;
         uint32_t kclamp;
         uint32_t lds_k, lds_v;
     };
-    uint32_t krow_off[HD / 64], kchunk_off[HD / 64];
+    uint32_t krow_off[KPER], kchunk_off[KPER];
 #pragma unroll
-    for (int k = 0; k < HD / 64; k++) {
+    for (int k = 0; k < KPER; k++) {
         unsigned r, c;
         dma_k_lane<HD>(pair, lane, k, &r, &c);
         krow_off[k] = r * row_bytes;
         kchunk_off[k] = c * 16u;
     }
-    auto dma_tile = [&](int t) __attribute__((always_inline)) {
-        t = __builtin_amdgcn_readfirstlane(t);
-        const int tc = min(t, n_tiles - 1);
-        const unsigned t0 = kb + (unsigned)tc * kPfKeys;
-        DmaTile d;
-        d.k = uniform_ptr(Kb + (uint64_t)t0 * row_bytes);
-        d.v = uniform_ptr(VTb + (uint64_t)(t0 >> 5) * kPfKTileBytes<HD>);
-        d.kclamp = __builtin_amdgcn_readfirstlane((last - t0) * row_bytes);
-        d.lds_k = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sm.t.k[t % NK][(HD / 64u) * pair * 1024u]);
-        d.lds_v = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sm.t.vt[t % NV][4u * pair * 1024u]);
+    auto dma_tiles = [&](unsigned tk, unsigned tv) __attribute__((always_inline)) {
+        tk = __builtin_amdgcn_readfirstlane(tk);
+        tv = __builtin_amdgcn_readfirstlane(tv);
+        const unsigned nl = (unsigned)n_tiles - 1;
+        const unsigned k0 = kb + min(tk, nl) * kPfKeys, v0 = kb + min(tv, nl) * kPfKeys;
+        DmaTiles d;
+        d.k = uniform_ptr(Kb + (uint64_t)k0 * row_bytes);
+        d.v = uniform_ptr(VTb + (uint64_t)(v0 >> 5) * kPfKTileBytes<HD>);
+        d.kclamp = __builtin_amdgcn_readfirstlane((last - k0) * row_bytes);
+        d.lds_k = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sm.k[tk & SM][KPER * pair * 1024u]);
+        d.lds_v = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sm.vt[tv & SM][4u * pair * 1024u]);
         return d;
     };
-    auto dma_part = [&](int k, const DmaTile& d) __attribute__((always_inline)) {
-        if (k < HD / 64)
-            lds_dma16_s(min(krow_off[k], d.kclamp) + kchunk_off[k], d.k, d.lds_k + 1024u * k);
+    auto dma_part = [&](int k, const DmaTiles& d) __attribute__((always_inline)) {
+        if (k < KPER)
+            lds_dma16_m0(min(krow_off[k], d.kclamp) + kchunk_off[k], d.k, d.lds_k + 1024u * k);
         else
-            lds_dma16_s(dof.v[k - HD / 64], d.v, d.lds_v + 1024u * (k - HD / 64));
-    };
-    auto issue = [&](int t) __attribute__((always_inline)) {
-        const DmaTile d = dma_tile(t);
-#pragma unroll
-        for (int k = 0; k < PER; k++) dma_part(k, d);
+            lds_dma16_m0(dof.v[k - KPER], d.v, d.lds_v + 1024u * (k - KPER));
     };
 
     if (wave < 4) {
         // ---------------- score wave ----------------
         // Each score wave also issues its quarter of every tile's DMAs (the output waves carry the
-        // longer part of each phase): tiles 0..D first, so that their latency overlaps q's.
-#pragma unroll
-        for (int p = 0; p <= D; p++) issue(p);
+        // longer part of each phase). Phase j >= 2 requests K(j + 1) and V^T(j - 1), each two phases
+        // ahead of its first reader (the score MFMAs of phase j + 2, the output MFMAs of phase
+        // j + 2); the prologue requests K(0..2) and V^T(0) after q, so that the first barrier waits
+        // for q and K(0) only.
         const unsigned pos = ent.start + tok_c;
         const unsigned lo = (ent.window != 0 && pos + 1 > ent.window) ? pos + 1 - ent.window : 0u;
         const unsigned hi = row_live ? pos : 0u;
@@ -827,6 +845,17 @@ __global__ __launch_bounds__(512, 1) void k_prefill_pp(PrefillArgs a) {
 #pragma unroll
             for (int s = 0; s < NQ; s++) qop[s] = ldg<f16x8>(qr + 16 * s);
         }
+        {
+            const DmaTiles d0 = dma_tiles(0, 0), d1 = dma_tiles(1, 0), d2 = dma_tiles(2, 0);
+#pragma unroll
+            for (int k = 0; k < KPER; k++) dma_part(k, d0);
+#pragma unroll
+            for (int k = 0; k < KPER; k++) dma_part(k, d1);
+#pragma unroll
+            for (int k = 0; k < KPER; k++) dma_part(k, d2);
+#pragma unroll
+            for (int k = KPER; k < PER; k++) dma_part(k, d0);  // V^T(0)
+        }
         float m_run = -INFINITY, l_run = 0.0f;
         const unsigned krow = key_of_row((unsigned)col);
         const unsigned kx = swz_k(krow);
@@ -836,7 +865,7 @@ __global__ __launch_bounds__(512, 1) void k_prefill_pp(PrefillArgs a) {
         const unsigned span = dead ? 0u : hi - lo + 1u;
 
         auto scores = [&](int stage) __attribute__((always_inline)) {
-            const unsigned char* kbuf = sm.t.k[stage];
+            const unsigned char* kbuf = sm.k[stage];
             f32x16 sc = f32x16{};
 #pragma unroll
             for (int s = 0; s < NQ; s++) {
@@ -881,9 +910,9 @@ __global__ __launch_bounds__(512, 1) void k_prefill_pp(PrefillArgs a) {
         // and alpha; 10-25: one exponential each, every second one packing the f16 pair and adding it
         // to the row sum), sched_barrier(0) keeping that order. `mask` is false for tiles inside the
         // window of every row of the wave.
-        auto steady = [&](bool mask, int ks, unsigned kt0, const DmaTile& tdma, f32x16& sc, f16x8 (&pout)[2],
+        auto steady = [&](bool mask, unsigned ks, unsigned kt0, const DmaTiles& tdma, f32x16& sc, f16x8 (&pout)[2],
                           f32x16& nxt, float& alpha) __attribute__((always_inline)) {
-            const unsigned char* kbuf = sm.t.k[ks];
+            const unsigned char* kbuf = sm.k[ks];
             f16x8 kr[NQ];
             auto kread = [&](int s) __attribute__((always_inline)) {
                 kr[s] = *reinterpret_cast<const f16x8*>(kbuf + koff[s & 7] + 256u * (s >> 3));
@@ -956,23 +985,30 @@ __global__ __launch_bounds__(512, 1) void k_prefill_pp(PrefillArgs a) {
         f16x8 pa[2], pb[2];
         f32x16 sa, sb;
         float alpha;
+        // Phase it + 2: K(it + 1) and V^T(it - 1) are in LDS; the phase requests K(it + 3) (into the
+        // stage of K(it - 1)) and V^T(it + 1) (into the stage of V^T(it - 3)), scores tile it + 1 and
+        // turns tile it into probabilities.
         auto step = [&](bool mask, int it, f32x16& sc, f16x8 (&pout)[2], f32x16& nxt) __attribute__((always_inline)) {
-            it = __builtin_amdgcn_readfirstlane(it);
-            dma_wait_barrier<PER>(D - 1);  // tile it + 1 is in LDS; tile it + 1 + D goes to the stages of K(it), V^T(it - 2)
+            const unsigned ut = (unsigned)__builtin_amdgcn_readfirstlane(it);
+            vm_wait_barrier<PER>();
             float al;
-            const DmaTile d = dma_tile(it + 1 + D);
-            steady(mask, (it + 1) % NK, kb + (unsigned)it * kPfKeys, d, sc, pout, nxt, al);
+            const DmaTiles d = dma_tiles(ut + 3, ut + 1);
+            steady(mask, (ut + 1) & SM, kb + ut * kPfKeys, d, sc, pout, nxt, al);
             put(it, pout, al);
         };
-        dma_wait_barrier<PER>(D);  // tile 0 is in LDS
+        vm_wait_barrier<3 * KPER>();  // barrier 1: q and K(0) are in; K(1), K(2), V^T(0) may be in flight
         sa = scores(0);
         if (n_tiles == 1) {
             softmax(sa, kb, pa, alpha);
             put(0, pa, alpha);
         } else {
-            dma_wait_barrier<PER>(D - 1);  // tile 1 is in LDS; every wave is past scores(0)
-            issue(D + 1);
-            sb = scores(1 % NK);
+            vm_wait_barrier<PER>();  // barrier 2: K(1) is in LDS; every wave is past scores(0)
+            {
+                const DmaTiles d = dma_tiles(3, 1);
+#pragma unroll
+                for (int k = 0; k < PER; k++) dma_part(k, d);
+            }
+            sb = scores(1);
             softmax(sa, kb, pa, alpha);
             put(0, pa, alpha);
             int it = 1;
@@ -988,14 +1024,15 @@ __global__ __launch_bounds__(512, 1) void k_prefill_pp(PrefillArgs a) {
                 step(true, it, sb, pb, sa);
                 sb = sa;
             }
-            lds_barrier();
+            vm_wait_barrier<PER>();  // barrier n + 1: V^T(n - 2) is in LDS
             softmax(sb, kb + (unsigned)it * kPfKeys, pb, alpha);
             put(it, pb, alpha);
         }
-        lds_barrier();  // the output waves add the last tile
+        // barrier n + 2 (2 when n = 1): V^T(n - 1) is in LDS, and no DMA of this wave is in flight
+        // (none may outlive the workgroup); the output waves add the last tile
+        vm_wait_barrier<0>();
         sm.ml[pair][0][lane] = m_run;
         sm.ml[pair][1][lane] = l_run + __shfl_xor(l_run, 32);
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no LDS write of this workgroup outlives it
         lds_barrier();
         return;
     }
@@ -1012,7 +1049,7 @@ __global__ __launch_bounds__(512, 1) void k_prefill_pp(PrefillArgs a) {
     // row's reference max moved, then the 16 MFMAs with the V^T operands read R ahead.
     auto output = [&](int it) __attribute__((always_inline)) {
         it = __builtin_amdgcn_readfirstlane(it);
-        const unsigned char* vbuf = sm.t.vt[it % NV];
+        const unsigned char* vbuf = sm.vt[(unsigned)it & SM];
         f16x8 vr[16];
         auto vread = [&](int o) __attribute__((always_inline)) {
             vr[o] = *reinterpret_cast<const f16x8*>(vbuf + voff[o & 1] + 2048u * (o >> 1));
