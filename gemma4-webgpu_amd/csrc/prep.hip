@@ -67,15 +67,19 @@ __global__ __launch_bounds__(kWG) void k_attn_prep_many(const g4_prep_layer* __r
 // Chunked prompt prep: the producer-side prep of every token of a prompt
 // chunk in one launch. The engine runs vNorm -> fusedNormRope(Q, K) ->
 // kvCacheStore once per prompt token (src/engine.ts:2460-2479, each token
-// through 2056-2091). One workgroup per token: its threads first evaluate the
-// token's RoPE factors once (cos and sin of the f32 angle of every pair, in
-// f64 as the reference does) into LDS, then its four waves take the token's
-// head slots in turn: slots 0 .. NQH-1 are the query heads (norm + RoPE,
-// written as f16: the query operand g4_attn_prefill takes), then NKH key
-// heads (norm + RoPE, stored as cache row start + t), then NKH value heads
-// (weightless norm, stored). The per-head arithmetic is wave_norm_rope (the
-// reference's 256 partials and 128 -> 1 tree), so every stored value is the
-// f16 rounding of what the reference kernels compute token by token.
+// through 2056-2091). One workgroup per kPrepTokens consecutive tokens: its
+// threads first evaluate the RoPE inverse frequencies once (the reference's
+// f32 expression with its f64 pow; they do not depend on the position), then
+// the cos and sin of every pair's f32 angle at each of its tokens' positions
+// (in f64, as the reference does) into LDS; then its four waves take the
+// tokens' head slots in turn: per token, slots 0 .. NQH-1 are the query heads
+// (norm + RoPE, written as f16: the query operand g4_attn_prefill takes), then
+// NKH key heads (norm + RoPE, stored as cache row start + t), then NKH value
+// heads (weightless norm, stored). The per-head arithmetic is wave_norm_rope
+// (the reference's 256 partials and 128 -> 1 tree), so every stored value is
+// the f16 rounding of what the reference kernels compute token by token.
+constexpr unsigned kPrepTokens = 2;  // measured: 1, 2, 4, 8 tokens -> 43.0, 40.6, 43.3, 52.4 us (prefill4k, both layers)
+
 template <int HD>
 __global__ __launch_bounds__(kWG) void k_prompt_prep(const float* __restrict__ q, const float* __restrict__ k,
                                                      const float* __restrict__ v,
@@ -85,26 +89,29 @@ __global__ __launch_bounds__(kWG) void k_prompt_prep(const float* __restrict__ q
                                                      uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_cache,
                                                      uint16_t* __restrict__ v_cache, g4_prompt_prep_params p) {
     constexpr int J = HD / 64, PJ = J / 2;
-    static_assert(HD / 2 <= kWG, "one thread per RoPE pair");
-    __shared__ float rc[HD / 2], rs[HD / 2];
-    const unsigned t = blockIdx.x;
-    const unsigned pos = p.start + t;
-    if (threadIdx.x < HD / 2) {
-        const float ang = rope_angle(threadIdx.x, HD, p.theta, pos, p.apply_divisor, rope_freqs);
-        rc[threadIdx.x] = (float)cos((double)ang);
-        rs[threadIdx.x] = (float)sin((double)ang);
+    constexpr unsigned NP = HD / 2;  // RoPE pairs
+    static_assert(NP <= kWG, "one thread per RoPE pair");
+    __shared__ float inv[NP];
+    __shared__ float rc[kPrepTokens][NP], rs[kPrepTokens][NP];
+    const unsigned t0 = blockIdx.x * kPrepTokens;
+    const unsigned nt = min(kPrepTokens, p.n_tokens - t0);  // tokens of this workgroup (the last may have fewer)
+    if (threadIdx.x < NP)
+        inv[threadIdx.x] = rope_inv_freq(threadIdx.x, HD, p.theta, p.apply_divisor,
+                                         p.apply_divisor ? h2f(rope_freqs[threadIdx.x]) : 1.0f);
+    __syncthreads();
+    for (unsigned i = threadIdx.x; i < nt * NP; i += kWG) {
+        const unsigned tt = i / NP, pr = i % NP;
+        const float ang = (float)(p.start + t0 + tt) * inv[pr];  // rope_angle's expression
+        rc[tt][pr] = (float)cos((double)ang);
+        rs[tt][pr] = (float)sin((double)ang);
     }
     __syncthreads();
     const unsigned lane = threadIdx.x & 63;
     const unsigned wave = threadIdx.x >> 6;
-    RopeLane<PJ> rl;
-#pragma unroll
-    for (int pp = 0; pp < PJ; pp++) {
-        rl.c[pp] = rc[lane + 64 * pp];
-        rl.s[pp] = rs[lane + 64 * pp];
-    }
     const unsigned S = p.num_q_heads + (p.store_kv ? 2 * p.num_kv_heads : 0);
-    for (unsigned slot = wave; slot < S; slot += kWG / 64) {  // uniform per wave
+    for (unsigned w = wave; w < nt * S; w += kWG / 64) {  // uniform per wave
+        const unsigned tt = w / S, slot = w % S;
+        const unsigned t = t0 + tt, pos = p.start + t;
         const bool is_q = slot < p.num_q_heads;
         const unsigned r = slot - p.num_q_heads;
         const bool is_k = !is_q && r < p.num_kv_heads;
@@ -118,6 +125,12 @@ __global__ __launch_bounds__(kWG) void k_prompt_prep(const float* __restrict__ q
         for (int j = 0; j < J; j++) {
             x[j] = src[lane + 64 * j];
             wb[j] = rope ? (is_q ? q_weight : k_weight)[lane + 64 * j] : 0u;
+        }
+        RopeLane<PJ> rl;
+#pragma unroll
+        for (int pp = 0; pp < PJ; pp++) {
+            rl.c[pp] = rc[tt][lane + 64 * pp];
+            rl.s[pp] = rs[tt][lane + 64 * pp];
         }
         wave_norm_rope<J>(x, wb, rope, rope, rl, p.eps);
         uint16_t* dst = is_q ? q_out + ((uint64_t)t * p.num_q_heads + h) * HD
@@ -183,12 +196,13 @@ extern "C" int g4_attn_prompt_prep(const float* q, const float* k, const float* 
     if (p.n_tokens == 0) return G4_OK;
     if (p.n_tokens > 0x7fffffffu) return fail(G4_EINVAL, "attnPromptPrep: too many tokens");
     hipStream_t st = as_stream(stream);
+    const dim3 grid((p.n_tokens + kPrepTokens - 1) / kPrepTokens);
     if (p.head_dim == 512)
-        hipLaunchKernelGGL(k_prompt_prep<512>, dim3(p.n_tokens), dim3(kWG), 0, st, q, k, v, q_weight, k_weight,
-                           rope_freqs, q_out, k_cache, v_cache, p);
+        hipLaunchKernelGGL(k_prompt_prep<512>, grid, dim3(kWG), 0, st, q, k, v, q_weight, k_weight, rope_freqs, q_out,
+                           k_cache, v_cache, p);
     else
-        hipLaunchKernelGGL(k_prompt_prep<256>, dim3(p.n_tokens), dim3(kWG), 0, st, q, k, v, q_weight, k_weight,
-                           rope_freqs, q_out, k_cache, v_cache, p);
+        hipLaunchKernelGGL(k_prompt_prep<256>, grid, dim3(kWG), 0, st, q, k, v, q_weight, k_weight, rope_freqs, q_out,
+                           k_cache, v_cache, p);
     G4_CHECK_LAUNCH("attnPromptPrep");
     return G4_OK;
 }

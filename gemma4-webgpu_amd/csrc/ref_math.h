@@ -178,6 +178,28 @@ struct RopeLane {
     float c[PJ], s[PJ];
 };
 
+// The reference's tree over one value per lane, strides 32, 16, 8, 4, 2, 1:
+// lane 0 ends with ((v0 + v32) + (v16 + v48)) + ... , the operand pairs of a
+// shuffle-down tree, and the total is returned to every lane. Strides 32 and
+// 16 swap lane halves and row pairs (v_permlane32_swap / v_permlane16_swap,
+// every lane then holds its butterfly sum), strides 8..1 shift within 16-lane
+// rows (DPP row_shl: lane l takes lane l + s), so no step goes through LDS.
+__device__ __forceinline__ float wave_tree_sum(float c) {
+    {
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(c), __float_as_uint(c), false, false);
+        c = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+    }
+    {
+        const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(c), __float_as_uint(c), false, false);
+        c = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+    }
+    c = c + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(c), 0x108, 0xf, 0xf, false));  // row_shl:8
+    c = c + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(c), 0x104, 0xf, 0xf, false));  // row_shl:4
+    c = c + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(c), 0x102, 0xf, 0xf, false));  // row_shl:2
+    c = c + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(c), 0x101, 0xf, 0xf, false));  // row_shl:1
+    return __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(c)));
+}
+
 // Per-head RMSNorm (+ RoPE) of one HD-wide head by one wave; lane l holds
 // x[l + 64j], j = 0 .. HD/64 - 1 (and the weight's f16 bits at the same
 // places), and receives the results in place. The sum of squares adds the
@@ -200,9 +222,7 @@ __device__ __forceinline__ void wave_norm_rope(float (&x)[J], const uint32_t (&w
     }
     const float a = part[0] + part[2];  // t = lane      : s[t] + s[t + 128]
     const float b = part[1] + part[3];  // t = lane + 64 : s[t] + s[t + 128]
-    float c = a + b;                    // stride 64
-    for (int stride = 32; stride > 0; stride >>= 1) c = c + __shfl_down(c, stride);
-    const float total = __shfl(c, 0);
+    const float total = wave_tree_sum(a + b);  // stride 64, then 32 .. 1
     const float rms = sqrtf(total / (float)HD + eps);
 #pragma unroll
     for (int j = 0; j < J; j++) x[j] = weighted ? x[j] * h2f((uint16_t)wbits[j]) / rms : x[j] / rms;
