@@ -416,7 +416,7 @@ __global__ __launch_bounds__(256) void k_step_out(StepOutArgs a) {
         const unsigned row = r + half;
         const bool valid = row < r1;
         if (r != r0) gemv_row_load<NJ>(sg.w + (uint64_t)(valid ? row : r1 - 1) * N, lq, wv);
-        const float y = gemv_row_fold<NJ>(wv, xr);
+        const float y = gemv_row_fold<NJ, false>(wv, xr);  // the row's value in lane 0 of the half
         if (valid && lq == 0) sg.y[row] = y;
     }
 }

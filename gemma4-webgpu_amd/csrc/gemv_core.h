@@ -7,10 +7,9 @@
 // A half-wave (32 lanes) owns one row: lane l (0..31 within the half) loads
 // 16 bytes (8 columns) of every 256-column block with nontemporal loads, so
 // it holds partials t = 8 l .. 8 l + 7 and accumulates them in j order. The
-// tree's strides 128..8 pair lanes l and l ^ 16 .. l ^ 1 (butterfly: both
-// lanes form the same commutative sum), strides 4, 2, 1 stay in the lane.
-// Every lane of the half ends with the row's value, bit-identical to the
-// shader's.
+// tree's strides 128..8 pair lanes l and l + 16 .. l + 1 (gemv_tree_sum),
+// strides 4, 2, 1 stay in the lane. The row's value, bit-identical to the
+// shader's, ends in every lane of the half or in its lane 0 (kAll).
 #pragma once
 
 #include "ref_math.h"
@@ -46,8 +45,50 @@ __device__ __forceinline__ void gemv_row_load(const uint16_t* row, unsigned lq, 
     for (int j = 0; j < NJ; j++) wv[j] = ldg_nt<f16x8>(w + 256 * j);
 }
 
-// The row's value from weights loaded by gemv_row_load (in every lane of the half-wave).
-template <int NJ>
+// The tree over the half-wave's 256 partials (8 per lane). kAll: every lane of
+// the half ends with the value (strides 128 .. 8 as butterflies between lanes
+// l and l ^ 16 .. l ^ 1, through LDS shuffles); otherwise only lane 0 of each
+// half does, with the same operand pairs: stride 128 swaps 16-lane rows
+// (v_permlane16_swap, both lanes of a pair then hold their sum) and strides
+// 64 .. 8 shift within rows (DPP row_shl: lane l takes lane l + s), all in
+// VALU. Strides 4, 2, 1 stay in the lane.
+template <bool kAll>
+__device__ __forceinline__ float gemv_tree_sum(float (&acc)[8]) {
+#pragma clang fp contract(off)
+    if constexpr (kAll) {
+#pragma unroll
+        for (int m = 16; m >= 1; m >>= 1)  // tree strides 128 .. 8
+#pragma unroll
+            for (int e = 0; e < 8; e++) acc[e] = acc[e] + __shfl_xor(acc[e], m);
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(acc[e]), __float_as_uint(acc[e]), false, false);
+            acc[e] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);  // stride 128
+        }
+#pragma unroll
+        for (int e = 0; e < 8; e++)  // stride 64
+            acc[e] = acc[e] + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(acc[e]), 0x108, 0xf, 0xf, false));
+#pragma unroll
+        for (int e = 0; e < 8; e++)  // stride 32
+            acc[e] = acc[e] + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(acc[e]), 0x104, 0xf, 0xf, false));
+#pragma unroll
+        for (int e = 0; e < 8; e++)  // stride 16
+            acc[e] = acc[e] + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(acc[e]), 0x102, 0xf, 0xf, false));
+#pragma unroll
+        for (int e = 0; e < 8; e++)  // stride 8
+            acc[e] = acc[e] + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(acc[e]), 0x101, 0xf, 0xf, false));
+    }
+#pragma unroll
+    for (int e = 0; e < 4; e++) acc[e] = acc[e] + acc[e + 4];  // stride 4
+    acc[0] = acc[0] + acc[2];                                    // stride 2
+    acc[1] = acc[1] + acc[3];
+    return acc[0] + acc[1];                                      // stride 1
+}
+
+// The row's value from weights loaded by gemv_row_load (in every lane of the
+// half-wave, or in its lane 0 when kAll is false).
+template <int NJ, bool kAll = true>
 __device__ __forceinline__ float gemv_row_fold(const f16x8 (&wv)[NJ], const float (&xr)[NJ][8]) {
 #pragma clang fp contract(off)
     float acc[8];
@@ -57,24 +98,20 @@ __device__ __forceinline__ float gemv_row_fold(const f16x8 (&wv)[NJ], const floa
     for (int j = 0; j < NJ; j++)
 #pragma unroll
         for (int e = 0; e < 8; e++) acc[e] = acc[e] + (float)wv[j][e] * xr[j][e];
-#pragma unroll
-    for (int m = 16; m >= 1; m >>= 1)  // tree strides 128 .. 8
-#pragma unroll
-        for (int e = 0; e < 8; e++) acc[e] = acc[e] + __shfl_xor(acc[e], m);
-#pragma unroll
-    for (int e = 0; e < 4; e++) acc[e] = acc[e] + acc[e + 4];  // stride 4
-    acc[0] = acc[0] + acc[2];                                    // stride 2
-    acc[1] = acc[1] + acc[3];
-    return acc[0] + acc[1];                                      // stride 1
+    return gemv_tree_sum<kAll>(acc);
 }
 
-// The row's value (in every lane of the half-wave); `row` points at the
-// row's first element, 16-byte aligned.
-template <int NJ>
+// The row's value (in every lane of the half-wave, or in its lane 0 when kAll
+// is false); `row` points at the row's first element, 16-byte aligned.
+template <int NJ, bool kAll = true>
 __device__ __forceinline__ float gemv_row_dot(const uint16_t* row, const float (&xr)[NJ][8], unsigned lq) {
     f16x8 wv[NJ];
     gemv_row_load<NJ>(row, lq, wv);
-    return gemv_row_fold<NJ>(wv, xr);
+    // Every weight load is issued before the arithmetic: left to itself the compiler spreads the
+    // loads of the lane-0 form (which needs fewer registers) over the products, and each then
+    // waits a memory round trip (k_linear at input 4096: 11.0 us instead of 6.1).
+    if constexpr (!kAll) __builtin_amdgcn_sched_barrier(0);
+    return gemv_row_fold<NJ, kAll>(wv, xr);
 }
 
 // The same row value for quantized weights, in matmul_q8.wgsl's and
@@ -84,22 +121,8 @@ __device__ __forceinline__ float gemv_row_dot(const uint16_t* row, const float (
 //   Q4K: w = f32(scale[sub]) * f32(nibble) + f32(min[sub]); acc = acc + w * x[k]
 // Lane l of the half-wave covers k = 256 j + 8 l .. + 7, which lie in one
 // 32-element block (Q8 scale 8 j + l / 4; Q4K super-block j, sub-block l / 4).
-template <int NJ>
-__device__ __forceinline__ float gemv_tree(float (&acc)[8]) {
-#pragma clang fp contract(off)
-#pragma unroll
-    for (int m = 16; m >= 1; m >>= 1)  // tree strides 128 .. 8
-#pragma unroll
-        for (int e = 0; e < 8; e++) acc[e] = acc[e] + __shfl_xor(acc[e], m);
-#pragma unroll
-    for (int e = 0; e < 4; e++) acc[e] = acc[e] + acc[e + 4];  // stride 4
-    acc[0] = acc[0] + acc[2];                                    // stride 2
-    acc[1] = acc[1] + acc[3];
-    return acc[0] + acc[1];                                      // stride 1
-}
-
 // qrow: the row's int8 weights (N bytes, 8-byte aligned); srow: its N/32 f16 scales.
-template <int NJ>
+template <int NJ, bool kAll = true>
 __device__ __forceinline__ float gemv_row_dot_q8(const int8_t* qrow, const uint16_t* srow, const float (&xr)[NJ][8],
                                                  unsigned lq) {
 #pragma clang fp contract(off)
@@ -110,6 +133,7 @@ __device__ __forceinline__ float gemv_row_dot_q8(const int8_t* qrow, const uint1
         qv[j] = ldg_nt<uint64_t>(qrow + 256 * j + 8 * lq);
         sv[j] = ldg<uint16_t>(srow + 8 * j + (lq >> 2));
     }
+    if constexpr (!kAll) __builtin_amdgcn_sched_barrier(0);  // every load before the arithmetic (gemv_row_dot)
     float acc[8];
 #pragma unroll
     for (int e = 0; e < 8; e++) acc[e] = 0.0f;
@@ -122,12 +146,12 @@ __device__ __forceinline__ float gemv_row_dot_q8(const int8_t* qrow, const uint1
             acc[e] = acc[e] + w * xr[j][e];
         }
     }
-    return gemv_tree<NJ>(acc);
+    return gemv_tree_sum<kAll>(acc);
 }
 
 // qrow: the row's nibbles (N / 8 words, 8 per word, low nibble first); mrow: its
 // (N / 256) x 16 f16 values (8 scales, then 8 mins, per super-block).
-template <int NJ>
+template <int NJ, bool kAll = true>
 __device__ __forceinline__ float gemv_row_dot_q4k(const uint32_t* qrow, const uint16_t* mrow, const float (&xr)[NJ][8],
                                                   unsigned lq) {
 #pragma clang fp contract(off)
@@ -138,6 +162,7 @@ __device__ __forceinline__ float gemv_row_dot_q4k(const uint32_t* qrow, const ui
         sv[j] = ldg<uint16_t>(mrow + 16 * j + (lq >> 2));
         mv[j] = ldg<uint16_t>(mrow + 16 * j + 8 + (lq >> 2));
     }
+    if constexpr (!kAll) __builtin_amdgcn_sched_barrier(0);  // every load before the arithmetic (gemv_row_dot)
     float acc[8];
 #pragma unroll
     for (int e = 0; e < 8; e++) acc[e] = 0.0f;
@@ -151,7 +176,7 @@ __device__ __forceinline__ float gemv_row_dot_q4k(const uint32_t* qrow, const ui
             acc[e] = acc[e] + w * xr[j][e];
         }
     }
-    return gemv_tree<NJ>(acc);
+    return gemv_tree_sum<kAll>(acc);
 }
 
 }  // namespace g4

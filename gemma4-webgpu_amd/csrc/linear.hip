@@ -41,13 +41,13 @@ template <int FMT, int NJ>
 __device__ __forceinline__ float linear_row(const LinearSegDev& sg, unsigned lr, const float (&xr)[NJ][8], unsigned lq) {
     constexpr unsigned N = NJ * 256;
     if constexpr (FMT == kQ8)
-        return gemv_row_dot_q8<NJ>(static_cast<const int8_t*>(sg.w) + (uint64_t)lr * N, sg.meta + (uint64_t)lr * (N / 32),
-                                   xr, lq);
+        return gemv_row_dot_q8<NJ, false>(static_cast<const int8_t*>(sg.w) + (uint64_t)lr * N,
+                                          sg.meta + (uint64_t)lr * (N / 32), xr, lq);
     else if constexpr (FMT == kQ4K)
-        return gemv_row_dot_q4k<NJ>(static_cast<const uint32_t*>(sg.w) + (uint64_t)lr * (N / 8),
-                                    sg.meta + (uint64_t)lr * (N / 16), xr, lq);
+        return gemv_row_dot_q4k<NJ, false>(static_cast<const uint32_t*>(sg.w) + (uint64_t)lr * (N / 8),
+                                           sg.meta + (uint64_t)lr * (N / 16), xr, lq);
     else
-        return gemv_row_dot<NJ>(static_cast<const uint16_t*>(sg.w) + (uint64_t)lr * N, xr, lq);
+        return gemv_row_dot<NJ, false>(static_cast<const uint16_t*>(sg.w) + (uint64_t)lr * N, xr, lq);
 }
 
 template <int FMT, int NJ>
@@ -69,7 +69,7 @@ __global__ __launch_bounds__(256) void k_linear(LinearArgs a) {
             if (i < (int)a.n_segs && gr >= a.seg[i].first) s = i;
         const LinearSegDev& sg = a.seg[s];
         const unsigned lr = gr - sg.first;
-        const float v = linear_row<FMT, NJ>(sg, lr, xr, lq);
+        const float v = linear_row<FMT, NJ>(sg, lr, xr, lq);  // the row's value in lane 0 of the half
         if (valid && lq == 0) sg.y[lr] = v;
     }
 }
