@@ -73,6 +73,27 @@ __device__ __forceinline__ const char* uniform_ptr(const char* p) {
 }
 
 
+// Butterfly steps between lanes l and l ^ 16 / l ^ 32 without an LDS round trip:
+// v_permlane16_swap / v_permlane32_swap exchange 16-lane rows / 32-lane halves,
+// so the two results hold a lane's own value and its partner's (in either
+// order: max and + commute, so every lane gets the same bits as x op partner).
+__device__ __forceinline__ float max_xor16(float x) {
+    const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+}
+__device__ __forceinline__ float max_xor32(float x) {
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+}
+__device__ __forceinline__ float add_xor16(float x) {
+    const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+}
+__device__ __forceinline__ float add_xor32(float x) {
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+}
+
 struct DecodeArgs {
     const DecodeEntryDev* table;  // device table, or nullptr to use `one`
     DecodeEntryDev one;
@@ -239,8 +260,8 @@ __device__ __forceinline__ void tile_update(const f32x4 (&s)[2], int g, bool lo_
             sv[h2 * 4 + j] = x;
             tmax = fmaxf(tmax, x);
         }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+    tmax = max_xor16(tmax);  // max over the four lane groups of a column
+    tmax = max_xor32(tmax);
     const float m_new = fmaxf(m_run, tmax);
     if (__any(m_new > m_run)) {  // rescale only when some column's running max moved
         const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
@@ -295,8 +316,8 @@ __device__ __forceinline__ void wave_publish(DecodeSmem<HD, W>& sm, int wave, in
                                              f32x4 (&acc)[DecodeDims<HD>::NO]) {
     constexpr int NO = DecodeDims<HD>::NO;
     float l = l_run;
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
+    l = add_xor16(l);
+    l = add_xor32(l);
 #pragma unroll
     for (int i = 0; i < NO; i++)
 #pragma unroll

@@ -233,7 +233,7 @@ __global__ __launch_bounds__(64 * W, HD == 256 ? 8 / W : 1) void k_attn_step(
                 float p = 0.0f;
 #pragma unroll
                 for (int j = 0; j < J; j++) p += sm.qf[h][lane + 64 * j] * (float)kn[lane + 64 * j];
-                for (int off = 32; off > 0; off >>= 1) p += __shfl_xor(p, off);
+                p = wave_tree_sum(p);  // the same operand pairs at lane 0 as a 32 .. 1 butterfly
                 if (lane == 0) sm.mnew[h] = p;
             }
         }
