@@ -34,7 +34,8 @@ int hip_fail(hipError_t e, const char* what);
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 // Host -> device upload of a prepared table, ordered on `st`, through pinned
-// staging memory from a per-thread ring of slots. A slot is reused only once
+// staging memory from a per-thread ring of slots, copied by a kernel on `st`
+// (16-byte aligned dst; otherwise by the copy engine). A slot is reused only once
 // the copy that last read it has completed; when every slot is still in flight
 // the ring grows (up to kStageMaxSlots slots, past which the oldest slot is
 // waited for), so enqueueing never waits on the GPU in practice.

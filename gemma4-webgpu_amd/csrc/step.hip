@@ -39,7 +39,6 @@
 
 #include <hip/hip_ext.h>
 
-#include <map>
 #include <type_traits>
 #include <utility>
 #include <vector>
@@ -331,7 +330,7 @@ int g4_attn_step_prepare(const g4_step_entry* entries, uint32_t n_entries, uint3
     const uint32_t G = num_q_heads / num_kv_heads;
     const StepLayout L = step_layout(n_entries, num_kv_heads, G, head_dim);
     char* ws = static_cast<char*>(workspace);
-    StepPlanHost ph;
+    static thread_local StepPlanHost ph;  // the planner's storage, kept between the thread's prepares
     char err[256];
     rc = plan_step(entries, n_entries, num_q_heads, num_kv_heads, head_dim, device_cus(), tune, ws + L.tables, &ph,
                    err, sizeof err);

@@ -16,7 +16,6 @@
 #include <stdlib.h>
 #include <string.h>
 
-#include <map>
 #include <utility>
 #include <vector>
 
@@ -94,12 +93,101 @@ struct StepPlanHost {
     size_t off_ents = 0;
     size_t off_rope = 0;
     std::vector<char> blob;  // work table | merge table | entry table | RoPE factors, ready to upload to the tables region
+    // Working storage of plan_step, kept with the blob between calls: a decode
+    // loop that plans every token allocates nothing once its step stops growing.
+    std::vector<StepEntryDev> tab;
+    std::vector<uint32_t> key_begin, tiles, rope_idx, rope_slot;
+    std::vector<std::pair<const float*, uint32_t>> rope_keys;
 };
+
+// The token's RoPE factors c[p] = f32(cos(a_p)), c[half + p] = f32(sin(a_p))
+// with a_p = f32(pos * inv[p]), cos and sin evaluated in f64: bit-identical to
+// (float)cos((double)a) and (float)sin((double)a) of the C library.
+//
+// Each pair comes from one Cody-Waite reduction a = k pi/2 + r (pi/2 in
+// three parts of 33, 33 and 53 bits: k P1 and k P2 are exact for |k| < 2^20)
+// and Taylor polynomials on |r| <= pi/4 (next terms below 2^-62 relative), a
+// few f64 ulps from the exact value. The C library is within one ulp of it,
+// so wherever the interval d +- 2^-46 |d| around this value rounds to one f32,
+// both round to that f32; the rare value near an f32 rounding boundary, and
+// any angle beyond 2^20 or not finite, is taken from the C library instead.
+inline void rope_factors(const float* inv, uint32_t pos, uint32_t half, float* c) {
+    constexpr double kTwoOverPi = 0x1.45f306dc9c883p-1;
+    constexpr double kP1 = 0x1.921fb544p+0, kP2 = 0x1.0b4611a6p-34, kP3 = 0x1.3198a2e037073p-69;
+    constexpr double kRound = 0x1.8p52;  // adding and subtracting it rounds to an integer (|x| < 2^51)
+    float* s = c + half;
+    uint8_t sure[256];  // half <= 256; a branch-free first pass, then the C library where unsure
+    uint32_t unsure = 0;
+    for (uint32_t p = 0; p < half; p++) {
+        const double x = (double)((float)pos * inv[p]);
+        const double kr = x * kTwoOverPi + kRound;
+        const double k = kr - kRound;
+        uint64_t kb;
+        memcpy(&kb, &kr, 8);
+        const double r = ((x - k * kP1) - k * kP2) - k * kP3;
+        const double z = r * r;
+        const double sr =
+            r + r * z *
+                    (-1.0 / 6 +
+                     z * (1.0 / 120 +
+                          z * (-1.0 / 5040 +
+                               z * (1.0 / 362880 +
+                                    z * (-1.0 / 39916800 +
+                                         z * (1.0 / 6227020800 +
+                                              z * (-1.0 / 1307674368000 + z * (1.0 / 355687428096000))))))));
+        const double cr =
+            1.0 + z * (-0.5 +
+                       z * (1.0 / 24 +
+                            z * (-1.0 / 720 +
+                                 z * (1.0 / 40320 +
+                                      z * (-1.0 / 3628800 +
+                                           z * (1.0 / 479001600 +
+                                                z * (-1.0 / 87178291200 +
+                                                     z * (1.0 / 20922789888000 + z * (-1.0 / 6402373705728000)))))))));
+        const uint64_t q = kb & 3u;  // quadrant: a = k pi/2 + r
+        const double sv = q & 1 ? cr : sr, cv = q & 1 ? sr : cr;
+        const double sin_a = q & 2 ? -sv : sv;
+        const double cos_a = (q + 1) & 2 ? -cv : cv;
+        const double es = 0x1p-46 * fabs(sin_a), ec = 0x1p-46 * fabs(cos_a);
+        const bool ok = fabs(x) <= 0x1p20 && (float)(sin_a - es) == (float)(sin_a + es) &&
+                        (float)(cos_a - ec) == (float)(cos_a + ec);
+        c[p] = (float)cos_a;
+        s[p] = (float)sin_a;
+        sure[p] = ok;
+        unsure += !ok;
+    }
+    if (unsure)
+        for (uint32_t p = 0; p < half; p++)
+            if (!sure[p]) {
+                const double x = (double)((float)pos * inv[p]);
+                c[p] = (float)cos(x);
+                s[p] = (float)sin(x);
+            }
+}
+
+// Index of the (inverse-frequency table, position) pair among the distinct
+// pairs seen so far, in order of first appearance (a new pair is appended).
+// Open addressing over `slot` (a power of two, at least twice the pairs; 0 =
+// empty, else index + 1).
+inline uint32_t rope_pair_index(StepPlanHost& ph, const float* table, uint32_t position) {
+    const uint64_t h = (reinterpret_cast<uintptr_t>(table) >> 4) * 0x9E3779B97F4A7C15ull ^ position * 0xC2B2AE3D27D4EB4Full;
+    const size_t mask = ph.rope_slot.size() - 1;
+    for (size_t i = (size_t)(h >> 32) & mask;; i = (i + 1) & mask) {
+        const uint32_t v = ph.rope_slot[i];
+        if (!v) {
+            ph.rope_keys.emplace_back(table, position);
+            ph.rope_slot[i] = (uint32_t)ph.rope_keys.size();
+            return (uint32_t)ph.rope_keys.size() - 1;
+        }
+        if (ph.rope_keys[v - 1].first == table && ph.rope_keys[v - 1].second == position) return v - 1;
+    }
+}
 
 // Checks the step's arguments and plans it. `tables` is the device address of
 // the workspace's tables region (the entries' RoPE-factor pointers point into
 // it); `cus` the device's compute units. On failure returns a G4_ status and
-// writes a message to err.
+// writes a message to err. The blob is written in place, every byte of it
+// (the alignment gaps between its tables are zero).
 inline int plan_step(const g4_step_entry* entries, uint32_t n_entries, uint32_t num_q_heads, uint32_t num_kv_heads,
                      uint32_t head_dim, uint64_t cus, const StepTuning& tune, const char* tables, StepPlanHost* out,
                      char* err, size_t errlen) {
@@ -115,8 +203,19 @@ inline int plan_step(const g4_step_entry* entries, uint32_t n_entries, uint32_t 
     if (!entries || n_entries == 0) PLAN_FAIL(G4_EINVAL, "attnStep: no entries");
     if (n_entries > 65535) PLAN_FAIL(G4_EINVAL, "attnStep: %u entries (max 65535)", n_entries);
     const uint64_t row_bytes = (uint64_t)num_kv_heads * head_dim * 2;
-    std::vector<StepEntryDev> tab(n_entries);
-    std::vector<uint32_t> key_begin(n_entries), tiles(n_entries);
+    StepPlanHost& ph = *out;
+    ph.tab.resize(n_entries);
+    ph.key_begin.resize(n_entries);
+    ph.tiles.resize(n_entries);
+    ph.rope_idx.resize(n_entries);
+    ph.rope_keys.clear();
+    {
+        size_t slots = 16;
+        while (slots < 2 * (size_t)n_entries) slots *= 2;
+        ph.rope_slot.assign(slots, 0u);
+    }
+    std::vector<uint32_t>& key_begin = ph.key_begin;
+    std::vector<uint32_t>& tiles = ph.tiles;
     uint64_t T = 0, max_tiles = 0;
     for (uint32_t i = 0; i < n_entries; i++) {
         const g4_step_entry& s = entries[i];
@@ -132,8 +231,7 @@ inline int plan_step(const g4_step_entry* entries, uint32_t n_entries, uint32_t 
         if (s.seq_len == 0) PLAN_FAIL(G4_EINVAL, "attnStep: entry %u seq_len 0", i);
         if ((uint64_t)s.seq_len * row_bytes > 0xffffffffull)
             PLAN_FAIL(G4_EINVAL, "attnStep: entry %u cache exceeds 4 GiB", i);
-        StepEntryDev& d = tab[i];
-        d = StepEntryDev{};
+        StepEntryDev& d = ph.tab[i];
         d.q = s.q;
         // Cached rows: the kernel's unconditional loads of k, v and k_weight read q and q_weight
         // instead (valid addresses; the values are not used).
@@ -142,10 +240,12 @@ inline int plan_step(const g4_step_entry* entries, uint32_t n_entries, uint32_t 
         d.q_weight = s.q_weight;
         d.k_weight = cached ? s.q_weight : s.k_weight;
         d.rope_freqs = s.rope_freqs;
+        d.rope_cs = nullptr;  // set below for entries with a host RoPE table
         d.k_cache = s.k_cache;
         d.v_cache = s.v_cache;
         d.out = s.out;
         d.key_end = s.seq_len;
+        d.n_parts = 0;  // set by the partition
         d.position = s.position;
         d.flags = (s.store_kv ? kStoreKv : 0u) | (cached ? kRowCached : 0u);
         d.theta = s.theta;
@@ -156,6 +256,8 @@ inline int plan_step(const g4_step_entry* entries, uint32_t n_entries, uint32_t 
         tiles[i] = (s.seq_len - key_begin[i] + kTileKeys - 1) / kTileKeys;
         T += tiles[i];
         if (tiles[i] > max_tiles) max_tiles = tiles[i];
+        // RoPE factors: one [cos x hd/2][sin x hd/2] set per distinct (table, position) pair
+        ph.rope_idx[i] = s.rope_inv_freq_host ? rope_pair_index(ph, s.rope_inv_freq_host, s.position) : ~0u;
     }
     // Workgroups in one wave of the GPU. Small steps (at most kStepOneWgTiles
     // tiles per workgroup with one workgroup per CU) take one 8-wave
@@ -187,92 +289,88 @@ inline int plan_step(const g4_step_entry* entries, uint32_t n_entries, uint32_t 
     // with the merge): 16 workgroups 10.82, 8 workgroups 10.20, 4 workgroups 10.47.
     if (waves == 8 && tune.max_wgs <= 0 && tpw < 2 && max_tiles >= 2) tpw = 2;
 
-    // Work items entry by entry: tpw tiles per item, balanced within an entry.
-    std::vector<StepWorkDev> work;
-    work.reserve(cap);
-    std::vector<DecodeEntryDev> merge;  // only the entries with partial records: the merge grid covers them alone
-    merge.reserve(n_entries);
-    uint32_t parts = 0, max_parts = 0;
+    // Sizes: work items (tpw tiles each, balanced within an entry), merge
+    // entries (entries with partial records: the merge grid covers them alone).
+    uint64_t n_work = 0;
+    uint32_t n_merge = 0, parts = 0, max_parts = 0;
     for (uint32_t i = 0; i < n_entries; i++) {
-        StepEntryDev& d = tab[i];
-        const uint64_t ne = tiles[i], we = (ne + tpw - 1) / tpw;
-        d.n_parts = (uint32_t)we;
-        const uint32_t part_base = we > 1 ? parts : 0;
+        const uint64_t we = (tiles[i] + tpw - 1) / tpw;
+        ph.tab[i].n_parts = (uint32_t)we;
+        n_work += we;
+        if (we > max_parts) max_parts = (uint32_t)we;
+        if (we > 1) {
+            n_merge++;
+            parts += (uint32_t)we;
+        }
+    }
+    if (parts > kStepMaxWgs || n_work > cap)
+        PLAN_FAIL(G4_EINVAL, "attnStep: internal: %u partial records, %llu items", parts, (unsigned long long)n_work);
+
+    // Tables blob: work items | merge table | entry table | RoPE factors.
+    const size_t off_merge = align256(n_work * sizeof(StepWorkDev));
+    const size_t off_ents = off_merge + align256(n_merge * sizeof(DecodeEntryDev));
+    const size_t off_rope = off_ents + align256(n_entries * sizeof(DecodeEntryDev));
+    const size_t rope_floats = ph.rope_keys.size() * head_dim;
+    ph.blob.resize(off_rope + rope_floats * sizeof(float));
+    char* blob = ph.blob.data();
+    memset(blob + n_work * sizeof(StepWorkDev), 0, off_merge - n_work * sizeof(StepWorkDev));
+    memset(blob + off_merge + n_merge * sizeof(DecodeEntryDev), 0, off_ents - off_merge - n_merge * sizeof(DecodeEntryDev));
+    memset(blob + off_ents + n_entries * sizeof(DecodeEntryDev), 0, off_rope - off_ents - n_entries * sizeof(DecodeEntryDev));
+
+    // RoPE factors of each distinct pair: the reference's cos/sin of the f32
+    // angle, evaluated in f64 and rounded.
+    {
+        float* rope = reinterpret_cast<float*>(blob + off_rope);
+        for (size_t k = 0; k < ph.rope_keys.size(); k++)
+            rope_factors(ph.rope_keys[k].first, ph.rope_keys[k].second, head_dim / 2, rope + k * head_dim);
+    }
+    // Work items entry by entry (each with a copy of its entry), the merge
+    // table and the entry table (every entry: attnOut, first record, parts).
+    StepWorkDev* work = reinterpret_cast<StepWorkDev*>(blob);
+    DecodeEntryDev* merge = reinterpret_cast<DecodeEntryDev*>(blob + off_merge);
+    DecodeEntryDev* ents = reinterpret_cast<DecodeEntryDev*>(blob + off_ents);
+    const float* rope_dev = reinterpret_cast<const float*>(tables + off_rope);
+    uint32_t part_next = 0;
+    for (uint32_t i = 0; i < n_entries; i++) {
+        StepEntryDev& d = ph.tab[i];
+        if (ph.rope_idx[i] != ~0u) d.rope_cs = rope_dev + (size_t)ph.rope_idx[i] * head_dim;
+        const uint64_t ne = tiles[i], we = d.n_parts;
+        const uint32_t part_base = we > 1 ? part_next : 0;
+        // Part j covers tiles [j ne / we, (j + 1) ne / we): the bounds advance by
+        // ne / we and carry the remainder, with no division per part.
+        const uint64_t step = ne / we, rem = ne % we;
+        uint64_t te = 0, acc = 0;
         for (uint64_t j = 0; j < we; j++) {
-            const uint64_t tb = j * ne / we, te = (j + 1) * ne / we;
+            const uint64_t tb = te;
+            te += step;
+            acc += rem;
+            if (acc >= we) {
+                acc -= we;
+                te++;
+            }
             const uint64_t rb = key_begin[i] + tb * kTileKeys;
             const uint64_t re = key_begin[i] + te * kTileKeys;
-            StepWorkDev w{};
+            StepWorkDev& w = *work++;
+            w.ent = d;
             w.row_begin = (uint32_t)rb;
             w.row_end = (uint32_t)(re < d.key_end ? re : d.key_end);
             w.part = we > 1 ? part_base + (uint32_t)j : 0u;
             w.entry = i;
-            work.push_back(w);
         }
-        if (we > max_parts) max_parts = (uint32_t)we;
         if (we > 1) {
-            parts += (uint32_t)we;
-            merge.push_back(DecodeEntryDev{nullptr, nullptr, nullptr, d.out, 0, 0, part_base, (uint32_t)we, 0.0f, 0});
+            part_next += (uint32_t)we;
+            *merge++ = DecodeEntryDev{nullptr, nullptr, nullptr, d.out, 0, 0, part_base, (uint32_t)we, 0.0f, 0};
         }
+        ents[i] = DecodeEntryDev{nullptr, nullptr, nullptr, d.out, 0, 0, part_base, (uint32_t)we, 0.0f, 0};
     }
-    if (parts > kStepMaxWgs || work.size() > cap)
-        PLAN_FAIL(G4_EINVAL, "attnStep: internal: %u partial records, %zu items", parts, work.size());
-
-    // Tables blob: work items | merge table | entry table | RoPE factors.
-    const size_t off_merge = align256(work.size() * sizeof(StepWorkDev));
-    const size_t off_ents = off_merge + align256(merge.size() * sizeof(DecodeEntryDev));
-    const size_t off_rope = off_ents + align256(n_entries * sizeof(DecodeEntryDev));
-    std::vector<DecodeEntryDev> ents(n_entries);  // every entry: attnOut, first record, parts
-    {
-        uint32_t m = 0;
-        for (uint32_t i = 0; i < n_entries; i++) {
-            const uint32_t np = tab[i].n_parts;
-            const uint32_t base = np > 1 ? merge[m++].split_base : 0u;
-            ents[i] = DecodeEntryDev{nullptr, nullptr, nullptr, tab[i].out, 0, 0, base, np, 0.0f, 0};
-        }
-    }
-    // RoPE factors of each (inverse-frequency table, position) in use: the
-    // reference's cos/sin of the f32 angle, evaluated in f64 and rounded.
-    std::vector<float> rope;
-    {
-        std::map<std::pair<const float*, uint32_t>, uint32_t> seen;
-        const uint32_t half = head_dim / 2;
-        for (uint32_t i = 0; i < n_entries; i++) {
-            const g4_step_entry& s = entries[i];
-            if (!s.rope_inv_freq_host) continue;
-            const auto key = std::make_pair(s.rope_inv_freq_host, s.position);
-            auto it = seen.find(key);
-            uint32_t idx;
-            if (it != seen.end()) {
-                idx = it->second;
-            } else {
-                idx = (uint32_t)seen.size();
-                seen.emplace(key, idx);
-                rope.resize((size_t)(idx + 1) * head_dim);
-                float* c = rope.data() + (size_t)idx * head_dim;
-                for (uint32_t p = 0; p < half; p++) {
-                    const float ang = (float)s.position * s.rope_inv_freq_host[p];
-                    c[p] = (float)cos((double)ang);
-                    c[half + p] = (float)sin((double)ang);
-                }
-            }
-            tab[i].rope_cs = reinterpret_cast<const float*>(tables + off_rope) + (size_t)idx * head_dim;
-        }
-    }
-    for (StepWorkDev& w : work) w.ent = tab[w.entry];  // entries complete (parts, RoPE factors)
-    out->blob.assign(off_rope + rope.size() * sizeof(float), 0);
-    memcpy(out->blob.data(), work.data(), work.size() * sizeof(StepWorkDev));
-    if (!merge.empty()) memcpy(out->blob.data() + off_merge, merge.data(), merge.size() * sizeof(DecodeEntryDev));
-    memcpy(out->blob.data() + off_ents, ents.data(), ents.size() * sizeof(DecodeEntryDev));
-    if (!rope.empty()) memcpy(out->blob.data() + off_rope, rope.data(), rope.size() * sizeof(float));
-    out->waves = waves;
-    out->n_wgs = (uint32_t)work.size();
-    out->n_merge = (uint32_t)merge.size();
-    out->max_parts = max_parts;
-    out->parts = parts;
-    out->off_merge = off_merge;
-    out->off_ents = off_ents;
-    out->off_rope = off_rope;
+    ph.waves = waves;
+    ph.n_wgs = (uint32_t)n_work;
+    ph.n_merge = n_merge;
+    ph.max_parts = max_parts;
+    ph.parts = parts;
+    ph.off_merge = off_merge;
+    ph.off_ents = off_ents;
+    ph.off_rope = off_rope;
     return G4_OK;
 #undef PLAN_FAIL
 }

@@ -2,8 +2,10 @@
 // under AddressSanitizer and UndefinedBehaviorSanitizer by tests/test_step_plan.py. Reads scenarios from
 // stdin, one per line:
 //   nqh nkh hd cus seq:window[:c] ...      (c: a KV-consumer entry whose row is already cached)
-// plans each and checks the plan's invariants; prints "ok <n_wgs> <n_merge>" per scenario, or an error
-// and exits 1.
+// plans each (one planner state for all, as a library thread keeps it) and checks the plan's
+// invariants; prints "ok <n_wgs> <n_merge>" per scenario, or an error and exits 1.
+// With the argument "rope <stride>", instead compares the planner's RoPE factors with the C library's
+// f64 cos and sin over positions 0, stride, 2 stride, ... up to 131071 and a set of large angles.
 #include <stdio.h>
 #include <string.h>
 
@@ -21,8 +23,41 @@ static int bad(int line, const char* what) {
     return 1;
 }
 
-int main() {
+// Every factor equals (float)cos/sin((double)angle) of the C library; returns the values compared.
+static long rope_sweep(uint32_t stride) {
+    long n = 0;
+    std::vector<float> inv(256), c(512);
+    const double thetas[] = {1e4, 1e6};
+    for (uint32_t hd : {256u, 512u})
+        for (double theta : thetas) {
+            for (uint32_t i = 0; i < hd / 2; i++) inv[i] = (float)(1.0 / pow(theta, 2.0 * i / hd));
+            std::vector<uint32_t> pos;
+            for (uint32_t p = 0; p < 131072; p += stride) pos.push_back(p);
+            for (uint32_t p : {131071u, 131072u, 1048575u, 1048576u, 16777216u, 4000000000u}) pos.push_back(p);
+            for (uint32_t p : pos) {
+                rope_factors(inv.data(), p, hd / 2, c.data());
+                for (uint32_t i = 0; i < hd / 2; i++, n++) {
+                    const double a = (double)((float)p * inv[i]);
+                    if (c[i] != (float)cos(a) || c[hd / 2 + i] != (float)sin(a)) {
+                        printf("FAIL rope: hd %u theta %g pos %u pair %u: %a %a, C library %a %a\n", hd, theta, p, i,
+                               c[i], c[hd / 2 + i], (float)cos(a), (float)sin(a));
+                        return -1;
+                    }
+                }
+            }
+        }
+    return n;
+}
+
+int main(int argc, char** argv) {
+    if (argc == 3 && !strcmp(argv[1], "rope")) {
+        const long n = rope_sweep((uint32_t)atoi(argv[2]));
+        if (n < 0) return 1;
+        printf("ok rope %ld\n", n);
+        return 0;
+    }
     std::string text;
+    StepPlanHost ph;  // reused by every scenario: the storage grows and shrinks between plans
     int line = 0;
     // Fake device addresses: the planner stores them and never dereferences them.
     char* const dev = reinterpret_cast<char*>(uintptr_t(1) << 40);
@@ -69,7 +104,6 @@ int main() {
         for (size_t i = 0, t = 0; i < ents.size(); i += 2, t++) ents[i].rope_inv_freq_host = inv[t].data();
         const uint32_t n = (uint32_t)ents.size();
         const StepLayout L = step_layout(n, nkh, nqh / nkh, hd);
-        StepPlanHost ph;
         char err[256] = "";
         const int rc = plan_step(ents.data(), n, nqh, nkh, hd, cus, StepTuning{}, dev + L.tables, &ph, err,
                                  sizeof err);
@@ -122,6 +156,12 @@ int main() {
                     const char* r0 = dev + L.tables + ph.off_rope;
                     if (rc_ptr < r0 || rc_ptr + hd * 4 > r0 + rope_bytes || (rc_ptr - r0) % (hd * 4))
                         return bad(line, "RoPE factor pointer outside the factors");
+                    const float* f = reinterpret_cast<const float*>(ph.blob.data() + (rc_ptr - (dev + L.tables)));
+                    for (uint32_t p = 0; p < hd / 2; p++) {
+                        const double a = (double)((float)e.position * e.rope_inv_freq_host[p]);
+                        if (f[p] != (float)cos(a) || f[hd / 2 + p] != (float)sin(a))
+                            return bad(line, "RoPE factors differ from the C library's cos and sin");
+                    }
                 } else if (w.ent.rope_cs) {
                     return bad(line, "RoPE factors without a host table");
                 }

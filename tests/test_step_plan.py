@@ -80,3 +80,13 @@ def test_step_plan_rejects_bad_entries(checker):
     # a zero-length entry fails the plan with a message, not a crash
     r = subprocess.run([str(checker)], input="8 1 256 256 0:0\n", capture_output=True, text=True, timeout=60)
     assert r.returncode == 1 and "seq_len 0" in r.stdout
+
+
+def test_rope_factors_match_the_c_library(checker):
+    """The planner's RoPE factors (Cody-Waite reduction and Taylor polynomials in f64, with the C library
+    taken near f32 rounding boundaries) equal (float)cos/sin((double)angle) of the C library at every
+    position 0..131071, at head_dim 256 and 512 and theta 1e4 and 1e6, and at angles past 2^20."""
+    r = subprocess.run([str(checker), "rope", "1"], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-4000:]
+    assert r.stdout.startswith("ok rope "), r.stdout
+    assert int(r.stdout.split()[2]) > 100_000_000
