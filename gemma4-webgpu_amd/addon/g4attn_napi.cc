@@ -543,6 +543,15 @@ napi_value AttnStepWorkspaceSize(napi_env env, napi_callback_info info) {
     return number(env, (double)bytes);
 }
 
+napi_value AttnStepLayersWorkspaceSize(napi_env env, napi_callback_info info) {
+    Args a(env, info, 4);  // n_layers, num_q_heads, num_kv_heads, head_dim
+    const uint32_t n = a.u32(0), nqh = a.u32(1), nkh = a.u32(2), hd = a.u32(3);
+    if (!a.ok) return nullptr;
+    size_t bytes = 0;
+    CALL(env, g4_attn_step_layers_workspace_size(n, nqh, nkh, hd, &bytes));
+    return number(env, (double)bytes);
+}
+
 bool get_prop(napi_env env, napi_value obj, const char* key, napi_value* out) {
     bool has = false;
     napi_has_named_property(env, obj, key, &has);
@@ -800,6 +809,46 @@ napi_value AttnStepPrepare(napi_env env, napi_callback_info info) {
     return plan;
 }
 
+// attnStepPrepareLayers(layers[], nqh, nkh, hd, workspace, workspaceBytes, stream) -> plan per layer
+// (an array of Uint8Arrays over one ArrayBuffer)
+napi_value AttnStepPrepareLayers(napi_env env, napi_callback_info info) {
+    Args a(env, info, 7);
+    if (!a.ok) return nullptr;
+    bool is_array = false;
+    napi_is_array(env, a.v[0], &is_array);
+    if (!is_array) {
+        napi_throw_type_error(env, nullptr, "attnStepPrepareLayers: layers must be an array");
+        return nullptr;
+    }
+    uint32_t n = 0;
+    napi_get_array_length(env, a.v[0], &n);
+    const uint32_t nqh = a.u32(1), nkh = a.u32(2), hd = a.u32(3);
+    if (!a.ok) return nullptr;
+    std::vector<g4_step_entry> ents(n);
+    for (uint32_t i = 0; i < n; i++) {
+        napi_value obj;
+        napi_get_element(env, a.v[0], i, &obj);
+        if (!step_entry(a, obj, i, hd, &ents[i])) return nullptr;
+    }
+    void* ws = a.ptr(4);
+    const double ws_bytes = a.f64(5);
+    void* s = a.ptr(6);
+    if (!a.ok) return nullptr;
+    napi_value ab, list;
+    void* pdata = nullptr;
+    NAPI_OK(env, napi_create_arraybuffer(env, (size_t)n * sizeof(g4_decode_plan), &pdata, &ab));
+    CALL(env, g4_attn_step_prepare_layers(ents.data(), n, nqh, nkh, hd, ws, (size_t)ws_bytes,
+                                          static_cast<g4_decode_plan*>(pdata), s));
+    NAPI_OK(env, napi_create_array_with_length(env, n, &list));
+    for (uint32_t i = 0; i < n; i++) {
+        napi_value plan;
+        NAPI_OK(env, napi_create_typedarray(env, napi_uint8_array, sizeof(g4_decode_plan), ab,
+                                            (size_t)i * sizeof(g4_decode_plan), &plan));
+        NAPI_OK(env, napi_set_element(env, list, i, plan));
+    }
+    return list;
+}
+
 napi_value AttnStepRun(napi_env env, napi_callback_info info) {
     Args a(env, info, 2);  // plan, stream
     void* d = nullptr;
@@ -1037,6 +1086,8 @@ napi_value Init(napi_env env, napi_value exports) {
         {"ropeInvFreqHost", RopeInvFreqHost},
         {"attnStepWorkspaceSize", AttnStepWorkspaceSize},
         {"attnStepPrepare", AttnStepPrepare},
+        {"attnStepLayersWorkspaceSize", AttnStepLayersWorkspaceSize},
+        {"attnStepPrepareLayers", AttnStepPrepareLayers},
         {"attnStepRun", AttnStepRun},
         {"attnStepRunAttention", AttnStepRunAttention},
         {"attnStepRunOut", AttnStepRunOut},

@@ -10,7 +10,11 @@
 // 512 on global layers: one step per head_dim group); `e2bshared8k` / `e2bshared32k` (the same
 // with E2B's cache sharing: layers 15..34 read layer 13's or 14's cache and store nothing);
 // `long128k_hd512`. --mode step (default: the one-launch step), graph (the step replayed as a
-// captured HIP graph), or, for head_dim 256 only, the unfused prep + split + merge.
+// captured HIP graph), or, for head_dim 256 only, the unfused prep + split + merge. Token loops,
+// where the position advances every iteration and every plan is prepared again inside the timed
+// region: --mode loop (one step per head_dim group per token), layers (the engine's layer order:
+// one g4_attn_step_prepare_layers per head_dim group per token, then each layer's attention and
+// merge launches in turn), layers_each (the same order with one g4_attn_step_prepare per layer).
 //
 // `prefill4k` runs the causal MFMA prefill of a 4096-token prompt for one
 // global layer and one 512-window local layer, as 512-token chunks (16
@@ -414,7 +418,12 @@ int main(int argc, char** argv) {
     }
     bool all256 = true;
     for (auto& l : L) all256 = all256 && l.hd == HD;
-    if (mode != "step" && !all256) {
+    // Token loops (the position advances every token; every plan is re-prepared inside the timed region):
+    // loop: one step per head_dim group per token; layers: the engine's order, every layer's plan from one
+    // g4_attn_step_prepare_layers per head_dim group, then layer by layer attention + merge; layers_each:
+    // the same order with one g4_attn_step_prepare per layer.
+    const bool token_loop = mode == "loop" || mode == "layers" || mode == "layers_each";
+    if (mode != "step" && !token_loop && !all256) {
         fprintf(stderr, "workload %s: head_dim 512 layers run on the fused step only (--mode step)\n", wl.c_str());
         return 2;
     }
@@ -441,6 +450,11 @@ int main(int argc, char** argv) {
 
     struct Set {
         std::vector<void*> bufs;
+        std::vector<g4_step_entry> steps[2];     // the step's entries per head_dim group (token loops bump them)
+        std::vector<std::pair<int, int>> order;  // layer -> (head_dim group, index in the group)
+        void* layers_ws[2] = {nullptr, nullptr};
+        size_t layers_ws_bytes[2] = {0, 0};
+        std::vector<g4_decode_plan> layer_plans[2];
         g4_decode_plan plan;          // unfused: prep + split + merge
         g4_decode_plan step_plan[2];  // one-launch step per head_dim group (256, 512)
         bool has_step[2] = {false, false};
@@ -452,16 +466,17 @@ int main(int argc, char** argv) {
     size_t ws_bytes = 0;
     if (all256) CK(g4_attn_decode_many_workspace_size((uint32_t)L.size(), NQH, NKH, HD, total_rows, &ws_bytes));
     uint64_t seed = 1;
+    const unsigned extra_rows = token_loop ? (unsigned)(iters / sets + 8) : 0;  // rows the loop's tokens append
     for (int s = 0; s < sets; s++) {
         std::vector<g4_decode_entry> ents;
         std::vector<g4_prep_layer> preps;
-        std::vector<g4_step_entry> steps[2];
+        std::vector<g4_step_entry>* steps = S[s].steps;
         std::vector<void*> lkc(L.size()), lvc(L.size()), lk(L.size()), lv(L.size());
         for (size_t li = 0; li < L.size(); li++) {
             const Layer& l = L[li];
             void *kc, *vc, *q, *k, *v, *out;
             const unsigned hd = l.hd;
-            const size_t cache_bytes = (size_t)l.seq * NKH * hd * 2;
+            const size_t cache_bytes = (size_t)(l.seq + extra_rows) * NKH * hd * 2;
             CK(g4_malloc(&q, NQH * hd * 4));
             CK(g4_malloc(&out, NQH * hd * 4));
             hipLaunchKernelGGL(k_fill_f32, dim3(8), dim3(256), 0, st, (float*)q, (uint64_t)NQH * hd, seed++);
@@ -522,6 +537,7 @@ int main(int argc, char** argv) {
             se.apply_divisor = l.divisor;
             se.scale = 1.0f;
             se.eps = 1e-6f;
+            S[s].order.emplace_back(hd == 512 ? 1 : 0, (int)steps[hd == 512 ? 1 : 0].size());
             steps[hd == 512 ? 1 : 0].push_back(se);
         }
         HK(hipGetLastError());
@@ -541,6 +557,12 @@ int main(int argc, char** argv) {
             CK(g4_attn_step_prepare(steps[h].data(), (uint32_t)steps[h].size(), NQH, NKH, hd, S[s].step_ws[h], b,
                                     &S[s].step_plan[h], st));
             S[s].has_step[h] = true;
+            if (token_loop) {
+                CK(g4_attn_step_layers_workspace_size((uint32_t)steps[h].size(), NQH, NKH, hd,
+                                                      &S[s].layers_ws_bytes[h]));
+                CK(g4_malloc(&S[s].layers_ws[h], S[s].layers_ws_bytes[h]));
+                S[s].layer_plans[h].resize(steps[h].size());
+            }
         }
     }
     CK(g4_stream_synchronize(st));
@@ -562,6 +584,40 @@ int main(int argc, char** argv) {
     }
     auto step = [&](int i) {
         Set& s = S[i % sets];
+        if (token_loop) {
+            for (int h = 0; h < 2; h++)
+                for (g4_step_entry& e : s.steps[h]) {
+                    e.seq_len++;
+                    e.position++;
+                }
+            for (int h = 0; h < 2; h++) {
+                if (!s.has_step[h]) continue;
+                const unsigned hd = h ? 512 : 256;
+                const uint32_t n = (uint32_t)s.steps[h].size();
+                if (mode == "loop") {
+                    size_t b = 0;
+                    CK(g4_attn_step_workspace_size(n, NQH, NKH, hd, &b));
+                    CK(g4_attn_step_prepare(s.steps[h].data(), n, NQH, NKH, hd, s.step_ws[h], b, &s.step_plan[h], st));
+                    CK(g4_attn_step_run(&s.step_plan[h], st));
+                } else if (mode == "layers") {
+                    CK(g4_attn_step_prepare_layers(s.steps[h].data(), n, NQH, NKH, hd, s.layers_ws[h],
+                                                   s.layers_ws_bytes[h], s.layer_plans[h].data(), st));
+                }
+            }
+            if (mode == "loop") return;
+            for (const auto& o : s.order) {  // the engine's layer order
+                const unsigned hd = o.first ? 512 : 256;
+                g4_decode_plan& plan = s.layer_plans[o.first][o.second];
+                if (mode == "layers_each") {
+                    const size_t one = s.layers_ws_bytes[o.first] / s.steps[o.first].size();
+                    CK(g4_attn_step_prepare(&s.steps[o.first][o.second], 1, NQH, NKH, hd,
+                                            (char*)s.layers_ws[o.first] + (size_t)o.second * one, one, &plan, st));
+                }
+                CK(g4_attn_step_run_attention(&plan, st));
+                CK(g4_attn_step_run_merge(&plan, st));
+            }
+            return;
+        }
         if (mode == "graph") {
             HK(hipGraphLaunch(gexec[i % sets], st));
             return;
@@ -576,13 +632,14 @@ int main(int argc, char** argv) {
         CK(g4_attn_decode_many_run_split(&s.plan, st));
         CK(g4_attn_decode_many_run_merge(&s.plan, st));
     };
-    for (int i = 0; i < 5; i++) step(i);
+    const int warm = token_loop ? sets : 5;  // token loops: every set once (its positions advance per use)
+    for (int i = 0; i < warm; i++) step(i);
     CK(g4_stream_synchronize(st));
     hipEvent_t a, b;
     HK(hipEventCreate(&a));
     HK(hipEventCreate(&b));
     HK(hipEventRecord(a, st));
-    for (int i = 0; i < iters; i++) step(i);
+    for (int i = 0; i < iters; i++) step(warm + i);
     HK(hipEventRecord(b, st));
     HK(hipEventSynchronize(b));
     float ms = 0;

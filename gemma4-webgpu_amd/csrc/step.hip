@@ -278,7 +278,8 @@ int step_env(const char* name, int dflt) {
 }
 
 struct StepPlanRep {
-    char* ws;
+    char* tables;   // the plan's tables region (work items | merge table | entry table | RoPE factors)
+    char* part_ml;  // its partial records: (m, l) pairs, then the o rows at step_part_o_offset()
     uint32_t n_entries;
     uint32_t n_wgs;
     uint32_t num_kv_heads;
@@ -310,6 +311,27 @@ int g4_attn_step_workspace_size(uint32_t n_entries, uint32_t num_q_heads, uint32
     return G4_OK;
 }
 
+// G4_STEP_WAVES (4 or 8), G4_STEP_WGS_PER_CU and G4_STEP_MAX_WGS override the grid choice.
+static const StepTuning& step_tuning() {
+    static const StepTuning tune = [] {
+        StepTuning t;
+        t.waves = step_env("G4_STEP_WAVES", 0);
+        t.wgs_per_cu = step_env("G4_STEP_WGS_PER_CU", 0);
+        t.max_wgs = step_env("G4_STEP_MAX_WGS", 0);
+        return t;
+    }();
+    return tune;
+}
+
+static void write_plan(g4_decode_plan* plan, char* tables, char* part_ml, uint32_t n_entries, uint32_t num_kv_heads,
+                       uint32_t G, uint32_t head_dim, const StepPlanHost& ph) {
+    StepPlanRep r = {tables,   part_ml,      n_entries, ph.n_wgs,  num_kv_heads,           G,
+                     ph.n_merge, ph.max_parts, ph.waves, head_dim, kStepMagic, (uint32_t)ph.off_merge,
+                     (uint32_t)ph.off_rope, (uint32_t)ph.off_ents};
+    memset(plan, 0, sizeof *plan);
+    memcpy(plan, &r, sizeof r);
+}
+
 int g4_attn_step_prepare(const g4_step_entry* entries, uint32_t n_entries, uint32_t num_q_heads,
                          uint32_t num_kv_heads, uint32_t head_dim, void* workspace, size_t workspace_bytes,
                          g4_decode_plan* plan, void* stream) {
@@ -319,36 +341,78 @@ int g4_attn_step_prepare(const g4_step_entry* entries, uint32_t n_entries, uint3
     if (!plan) return fail(G4_EINVAL, "attnStep: plan is NULL");
     if (!workspace || workspace_bytes < need)
         return fail(G4_ENOSPC, "attnStep: workspace %zu bytes < %zu needed", workspace_bytes, need);
-    // G4_STEP_WAVES (4 or 8), G4_STEP_WGS_PER_CU and G4_STEP_MAX_WGS override the grid choice.
-    static const StepTuning tune = [] {
-        StepTuning t;
-        t.waves = step_env("G4_STEP_WAVES", 0);
-        t.wgs_per_cu = step_env("G4_STEP_WGS_PER_CU", 0);
-        t.max_wgs = step_env("G4_STEP_MAX_WGS", 0);
-        return t;
-    }();
     const uint32_t G = num_q_heads / num_kv_heads;
     const StepLayout L = step_layout(n_entries, num_kv_heads, G, head_dim);
     char* ws = static_cast<char*>(workspace);
     static thread_local StepPlanHost ph;  // the planner's storage, kept between the thread's prepares
     char err[256];
-    rc = plan_step(entries, n_entries, num_q_heads, num_kv_heads, head_dim, device_cus(), tune, ws + L.tables, &ph,
-                   err, sizeof err);
+    rc = plan_step(entries, n_entries, num_q_heads, num_kv_heads, head_dim, device_cus(), step_tuning(),
+                   ws + L.tables, &ph, err, sizeof err);
     if (rc) return fail(rc, "%s", err);
     rc = stage_upload(ws + L.tables, ph.blob.data(), ph.blob.size(), as_stream(stream));  // the tables in one copy
     if (rc) return rc;
-    StepPlanRep r = {ws,       n_entries,  ph.n_wgs,   num_kv_heads,           G,
-                     ph.n_merge, ph.max_parts, ph.waves, head_dim, kStepMagic, (uint32_t)ph.off_merge,
-                     (uint32_t)ph.off_rope, (uint32_t)ph.off_ents};
-    memset(plan, 0, sizeof *plan);
-    memcpy(plan, &r, sizeof r);
+    write_plan(plan, ws + L.tables, ws + L.part_ml, n_entries, num_kv_heads, G, head_dim, ph);
+    return G4_OK;
+}
+
+// Layers workspace: every layer's tables region (as a one-entry step's), packed
+// from the start, then every layer's partial records (as a one-entry step's).
+int g4_attn_step_layers_workspace_size(uint32_t n_layers, uint32_t num_q_heads, uint32_t num_kv_heads,
+                                       uint32_t head_dim, size_t* bytes) {
+    size_t one = 0;
+    int rc = g4_attn_step_workspace_size(1, num_q_heads, num_kv_heads, head_dim, &one);
+    if (rc) return rc;
+    if (n_layers == 0 || n_layers > 65535) return fail(G4_EINVAL, "attnStepLayers: %u layers (1..65535)", n_layers);
+    *bytes = (size_t)n_layers * one;
+    return G4_OK;
+}
+
+int g4_attn_step_prepare_layers(const g4_step_entry* layers, uint32_t n_layers, uint32_t num_q_heads,
+                                uint32_t num_kv_heads, uint32_t head_dim, void* workspace, size_t workspace_bytes,
+                                g4_decode_plan* plans, void* stream) {
+    size_t need = 0;
+    int rc = g4_attn_step_layers_workspace_size(n_layers, num_q_heads, num_kv_heads, head_dim, &need);
+    if (rc) return rc;
+    if (!layers || !plans) return fail(G4_EINVAL, "attnStepLayers: NULL pointer");
+    if (!workspace || workspace_bytes < need)
+        return fail(G4_ENOSPC, "attnStepLayers: workspace %zu bytes < %zu needed", workspace_bytes, need);
+    for (uint32_t i = 0; i < n_layers; i++) memset(&plans[i], 0, sizeof plans[i]);
+    const uint32_t G = num_q_heads / num_kv_heads;
+    const StepLayout L1 = step_layout(1, num_kv_heads, G, head_dim);
+    const size_t tables_one = L1.part_ml, records_one = L1.total - L1.part_ml;
+    char* ws = static_cast<char*>(workspace);
+    char* const records = ws + (size_t)n_layers * tables_one;
+    static thread_local StepPlanHost ph;
+    static thread_local StepRopeShare share;  // RoPE factor sets placed by earlier layers of this upload
+    static thread_local std::vector<char> blob;
+    share.clear();
+    blob.clear();
+    char err[256];
+    for (uint32_t i = 0; i < n_layers; i++) {
+        char* const tables = ws + blob.size();
+        rc = plan_step(layers + i, 1, num_q_heads, num_kv_heads, head_dim, device_cus(), step_tuning(), tables, &ph,
+                       err, sizeof err, &share);
+        if (rc) return fail(rc, "attnStepLayers: layer %u: %s", i, err);
+        // packed tables never outgrow one layer's share of the region (each fits a one-entry step's)
+        const size_t at = blob.size(), bytes = align256(ph.blob.size());
+        blob.resize(at + bytes);
+        memcpy(blob.data() + at, ph.blob.data(), ph.blob.size());
+        memset(blob.data() + at + ph.blob.size(), 0, bytes - ph.blob.size());
+        write_plan(&plans[i], tables, records + (size_t)i * records_one, 1, num_kv_heads, G, head_dim, ph);
+    }
+    rc = stage_upload(ws, blob.data(), blob.size(), as_stream(stream));  // every layer's tables in one copy
+    if (rc) {
+        for (uint32_t i = 0; i < n_layers; i++) memset(&plans[i], 0, sizeof plans[i]);
+        return rc;
+    }
     return G4_OK;
 }
 
 static int step_plan(const g4_decode_plan* plan, StepPlanRep* r) {
     if (!plan) return fail(G4_EINVAL, "attnStep: plan is NULL");
     memcpy(r, plan, sizeof *r);
-    if (r->magic != kStepMagic) return fail(G4_EINVAL, "attnStep: plan was not prepared by g4_attn_step_prepare");
+    if (r->magic != kStepMagic)
+        return fail(G4_EINVAL, "attnStep: plan was not prepared by g4_attn_step_prepare or g4_attn_step_prepare_layers");
     return G4_OK;
 }
 
@@ -356,13 +420,12 @@ static int launch_attention(const g4_decode_plan* plan, void* stream, hipEvent_t
     StepPlanRep r;
     int rc = step_plan(plan, &r);
     if (rc) return rc;
-    const StepLayout L = step_layout(r.n_entries, r.num_kv_heads, r.group, r.head_dim);
     StepArgs a = {};
-    a.work = reinterpret_cast<const StepWorkDev*>(r.ws + L.tables);
+    a.work = reinterpret_cast<const StepWorkDev*>(r.tables);
     a.num_kv_heads = r.num_kv_heads;
     a.group = r.group;
-    a.part_ml = reinterpret_cast<float*>(r.ws + L.part_ml);
-    a.part_o = reinterpret_cast<float*>(r.ws + L.part_o);
+    a.part_ml = reinterpret_cast<float*>(r.part_ml);
+    a.part_o = reinterpret_cast<float*>(r.part_ml + step_part_o_offset(r.num_kv_heads, r.group));
     const dim3 grid(r.n_wgs, r.num_kv_heads);
     hipStream_t st = as_stream(stream);
     if (r.head_dim == 512) {
@@ -399,14 +462,13 @@ int g4_attn_step_run_merge(const g4_decode_plan* plan, void* stream) {
     int rc = step_plan(plan, &r);
     if (rc) return rc;
     if (!r.n_merge) return G4_OK;
-    const StepLayout L = step_layout(r.n_entries, r.num_kv_heads, r.group, r.head_dim);
     DecodeArgs m = {};
-    m.table = reinterpret_cast<const DecodeEntryDev*>(r.ws + L.tables + r.off_merge);
+    m.table = reinterpret_cast<const DecodeEntryDev*>(r.tables + r.off_merge);
     m.n_entries = r.n_merge;
     m.num_kv_heads = r.num_kv_heads;
     m.group = r.group;
-    m.part_ml = reinterpret_cast<float*>(r.ws + L.part_ml);
-    m.part_o = reinterpret_cast<float*>(r.ws + L.part_o);
+    m.part_ml = reinterpret_cast<float*>(r.part_ml);
+    m.part_o = reinterpret_cast<float*>(r.part_ml + step_part_o_offset(r.num_kv_heads, r.group));
     return launch_decode_merge(m, r.n_merge, r.max_parts, as_stream(stream), r.head_dim);
 }
 
@@ -422,7 +484,6 @@ int g4_attn_step_run_out(const g4_decode_plan* plan, const g4_linear_seg* o_proj
     const uint32_t n = r.num_kv_heads * r.group * r.head_dim;
     if (n % 256 || n / 256 < 4 || n / 256 > 16)
         return fail(G4_EINVAL, "attnStepOut: input length %u unsupported (a multiple of 256 in [1024, 4096])", n);
-    const StepLayout L = step_layout(r.n_entries, r.num_kv_heads, r.group, r.head_dim);
     StepOutArgs a = {};
     for (uint32_t i = 0; i < n_segs; i++) {
         const g4_linear_seg& sg = o_proj[i];
@@ -435,9 +496,9 @@ int g4_attn_step_run_out(const g4_decode_plan* plan, const g4_linear_seg* o_proj
     hipStream_t st = as_stream(stream);
     const bool fused = step_out_merges(r.max_parts, r.group, r.num_kv_heads);
     if (!fused && (rc = g4_attn_step_run_merge(plan, stream))) return rc;
-    a.ents = reinterpret_cast<const DecodeEntryDev*>(r.ws + L.tables + r.off_ents);
-    a.part_ml = reinterpret_cast<const float*>(r.ws + L.part_ml);
-    a.part_o = reinterpret_cast<const float*>(r.ws + L.part_o);
+    a.ents = reinterpret_cast<const DecodeEntryDev*>(r.tables + r.off_ents);
+    a.part_ml = reinterpret_cast<const float*>(r.part_ml);
+    a.part_o = reinterpret_cast<const float*>(r.part_ml + step_part_o_offset(r.num_kv_heads, r.group));
     a.num_kv_heads = r.num_kv_heads;
     a.group = r.group;
     a.merge = fused ? 1u : 0u;

@@ -41,6 +41,11 @@ struct StepLayout {
     size_t tables, part_ml, part_o, total;
 };
 
+// Bytes from a plan's (m, l) records to its o rows.
+inline size_t step_part_o_offset(uint64_t nkh, uint64_t group) {
+    return align256((uint64_t)kStepMaxWgs * nkh * group * 2 * 4);
+}
+
 inline StepLayout step_layout(uint64_t n, uint64_t nkh, uint64_t group, uint64_t hd) {
     StepLayout L;
     const uint64_t max_items = n > kStepMaxWgs ? n : kStepMaxWgs;
@@ -49,7 +54,7 @@ inline StepLayout step_layout(uint64_t n, uint64_t nkh, uint64_t group, uint64_t
     L.tables = off;  // work items, merge entries, all entries, and at most one [cos x hd/2][sin x hd/2] set per entry
     off += align256(max_items * sizeof(StepWorkDev)) + 2 * align256(n * sizeof(DecodeEntryDev)) + align256(n * hd * 4);
     L.part_ml = off;
-    off += align256(recs * 2 * 4);
+    off += step_part_o_offset(nkh, group);
     L.part_o = off;
     off += align256(recs * hd * 4);
     L.total = off;
@@ -98,6 +103,26 @@ struct StepPlanHost {
     std::vector<StepEntryDev> tab;
     std::vector<uint32_t> key_begin, tiles, rope_idx, rope_slot;
     std::vector<std::pair<const float*, uint32_t>> rope_keys;
+    std::vector<const float*> rope_dev;  // device address of each distinct pair's factors
+    std::vector<uint32_t> rope_set;      // its set in this blob, or ~0 when an earlier plan placed it
+};
+
+// RoPE factor sets already placed by the earlier plans of one upload (the
+// layers of a token planned one by one): a later plan that needs the same
+// (inverse-frequency table, position) pair points at that set instead of
+// carrying its own.
+struct StepRopeShare {
+    std::vector<std::pair<const float*, uint32_t>> keys;
+    std::vector<const float*> dev;
+    void clear() {
+        keys.clear();
+        dev.clear();
+    }
+    const float* find(const std::pair<const float*, uint32_t>& k) const {
+        for (size_t i = 0; i < keys.size(); i++)
+            if (keys[i] == k) return dev[i];
+        return nullptr;
+    }
 };
 
 // The token's RoPE factors c[p] = f32(cos(a_p)), c[half + p] = f32(sin(a_p))
@@ -190,7 +215,7 @@ inline uint32_t rope_pair_index(StepPlanHost& ph, const float* table, uint32_t p
 // (the alignment gaps between its tables are zero).
 inline int plan_step(const g4_step_entry* entries, uint32_t n_entries, uint32_t num_q_heads, uint32_t num_kv_heads,
                      uint32_t head_dim, uint64_t cus, const StepTuning& tune, const char* tables, StepPlanHost* out,
-                     char* err, size_t errlen) {
+                     char* err, size_t errlen, StepRopeShare* share = nullptr) {
 #define PLAN_FAIL(code, ...)                   \
     do {                                       \
         snprintf(err, errlen, __VA_ARGS__);    \
@@ -310,8 +335,17 @@ inline int plan_step(const g4_step_entry* entries, uint32_t n_entries, uint32_t 
     const size_t off_merge = align256(n_work * sizeof(StepWorkDev));
     const size_t off_ents = off_merge + align256(n_merge * sizeof(DecodeEntryDev));
     const size_t off_rope = off_ents + align256(n_entries * sizeof(DecodeEntryDev));
-    const size_t rope_floats = ph.rope_keys.size() * head_dim;
-    ph.blob.resize(off_rope + rope_floats * sizeof(float));
+    // Each distinct pair's factors: a set placed by an earlier plan of the share, or one of this blob's.
+    const float* rope_base = reinterpret_cast<const float*>(tables + off_rope);
+    size_t rope_sets = 0;
+    ph.rope_dev.resize(ph.rope_keys.size());
+    ph.rope_set.resize(ph.rope_keys.size());
+    for (size_t k = 0; k < ph.rope_keys.size(); k++) {
+        const float* shared = share ? share->find(ph.rope_keys[k]) : nullptr;
+        ph.rope_set[k] = shared ? ~0u : (uint32_t)rope_sets++;
+        ph.rope_dev[k] = shared ? shared : rope_base + (size_t)ph.rope_set[k] * head_dim;
+    }
+    ph.blob.resize(off_rope + rope_sets * head_dim * sizeof(float));
     char* blob = ph.blob.data();
     memset(blob + n_work * sizeof(StepWorkDev), 0, off_merge - n_work * sizeof(StepWorkDev));
     memset(blob + off_merge + n_merge * sizeof(DecodeEntryDev), 0, off_ents - off_merge - n_merge * sizeof(DecodeEntryDev));
@@ -321,19 +355,25 @@ inline int plan_step(const g4_step_entry* entries, uint32_t n_entries, uint32_t 
     // angle, evaluated in f64 and rounded.
     {
         float* rope = reinterpret_cast<float*>(blob + off_rope);
-        for (size_t k = 0; k < ph.rope_keys.size(); k++)
-            rope_factors(ph.rope_keys[k].first, ph.rope_keys[k].second, head_dim / 2, rope + k * head_dim);
+        for (size_t k = 0; k < ph.rope_keys.size(); k++) {
+            if (ph.rope_set[k] == ~0u) continue;  // placed by an earlier plan
+            rope_factors(ph.rope_keys[k].first, ph.rope_keys[k].second, head_dim / 2,
+                         rope + (size_t)ph.rope_set[k] * head_dim);
+            if (share) {
+                share->keys.push_back(ph.rope_keys[k]);
+                share->dev.push_back(ph.rope_dev[k]);
+            }
+        }
     }
     // Work items entry by entry (each with a copy of its entry), the merge
     // table and the entry table (every entry: attnOut, first record, parts).
     StepWorkDev* work = reinterpret_cast<StepWorkDev*>(blob);
     DecodeEntryDev* merge = reinterpret_cast<DecodeEntryDev*>(blob + off_merge);
     DecodeEntryDev* ents = reinterpret_cast<DecodeEntryDev*>(blob + off_ents);
-    const float* rope_dev = reinterpret_cast<const float*>(tables + off_rope);
     uint32_t part_next = 0;
     for (uint32_t i = 0; i < n_entries; i++) {
         StepEntryDev& d = ph.tab[i];
-        if (ph.rope_idx[i] != ~0u) d.rope_cs = rope_dev + (size_t)ph.rope_idx[i] * head_dim;
+        if (ph.rope_idx[i] != ~0u) d.rope_cs = ph.rope_dev[ph.rope_idx[i]];
         const uint64_t ne = tiles[i], we = d.n_parts;
         const uint32_t part_base = we > 1 ? part_next : 0;
         // Part j covers tiles [j ne / we, (j + 1) ne / we): the bounds advance by

@@ -307,6 +307,21 @@ def attn_step_prepare(entries, num_q_heads, num_kv_heads, head_dim, workspace, s
     return plan
 
 
+def step_layers_workspace_bytes(n_layers, num_q_heads, num_kv_heads, head_dim) -> int:
+    n = C.c_size_t(0)
+    abi.call("g4_attn_step_layers_workspace_size", n_layers, num_q_heads, num_kv_heads, head_dim, C.byref(n))
+    return n.value
+
+
+def attn_step_prepare_layers(layers, num_q_heads, num_kv_heads, head_dim, workspace, stream=None) -> list:
+    """One token's layers prepared together (one upload): a plan per layer, each run on its own in layer
+    order with attn_step_run_attention then attn_step_run_merge or attn_step_run_out."""
+    plans = (DecodePlan * len(layers))()
+    abi.call("g4_attn_step_prepare_layers", layers, len(layers), num_q_heads, num_kv_heads, head_dim,
+             _dev(workspace, "workspace", torch.uint8, 0), workspace.numel(), plans, _stream(stream))
+    return list(plans)
+
+
 def attn_step_run(plan: DecodePlan, stream=None):
     abi.call("g4_attn_step_run", C.byref(plan), _stream(stream))
 

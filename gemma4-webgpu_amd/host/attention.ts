@@ -241,6 +241,9 @@ export interface Addon {
   attnStepWorkspaceSize(n: number, nqh: number, nkh: number, hd: number): number;
   attnStepPrepare(entries: any[], nqh: number, nkh: number, hd: number, ws: bigint, wsBytes: number,
     s: bigint): Uint8Array;
+  attnStepLayersWorkspaceSize(n: number, nqh: number, nkh: number, hd: number): number;
+  attnStepPrepareLayers(layers: any[], nqh: number, nkh: number, hd: number, ws: bigint, wsBytes: number,
+    s: bigint): Uint8Array[];
   attnStepRun(plan: Uint8Array, s: bigint): void;
   attnStepRunAttention(plan: Uint8Array, s: bigint): void;
   attnStepRunOut(plan: Uint8Array, segs: { weight: bigint; out: bigint; rows: number }[], s: bigint): void;
@@ -353,7 +356,24 @@ export class HipAttention {
 
   // Prepare once per token (the entries' seqLen/position change); run as often as wanted.
   attnStepPrepare(entries: StepEntry[], shape: StepShape, workspace: DeviceBuffer): Uint8Array {
-    const flat = entries.map(function (e) {
+    return this.g4.attnStepPrepare(HipAttention.stepFlat(entries), shape.numQHeads, shape.numKvHeads,
+      shape.headDim, workspace.ptr, workspace.size, this.stream);
+  }
+
+  attnStepLayersWorkspaceSize(nLayers: number, shape: StepShape): number {
+    return this.g4.attnStepLayersWorkspaceSize(nLayers, shape.numQHeads, shape.numKvHeads, shape.headDim);
+  }
+
+  // One token's layers in the engine's order (src/engine.ts:2029-2156), prepared together once per token
+  // (where the engine patches every layer's uniforms, :1967-1987) with one table upload: a plan per layer,
+  // each run on its own, in layer order (attnStepRun, or attnStepRunAttention then attnStepOut).
+  attnStepPrepareLayers(layers: StepEntry[], shape: StepShape, workspace: DeviceBuffer): Uint8Array[] {
+    return this.g4.attnStepPrepareLayers(HipAttention.stepFlat(layers), shape.numQHeads, shape.numKvHeads,
+      shape.headDim, workspace.ptr, workspace.size, this.stream);
+  }
+
+  private static stepFlat(entries: StepEntry[]): any[] {
+    return entries.map(function (e) {
       return {
         q: e.q.ptr, k: e.k ? e.k.ptr : undefined, v: e.v ? e.v.ptr : undefined, qWeight: e.qWeight.ptr,
         kWeight: e.kWeight ? e.kWeight.ptr : undefined,
@@ -365,8 +385,6 @@ export class HipAttention {
         scale: e.scale === undefined ? 1.0 : e.scale, eps: e.eps === undefined ? 1e-6 : e.eps,
       };
     });
-    return this.g4.attnStepPrepare(flat, shape.numQHeads, shape.numKvHeads, shape.headDim, workspace.ptr,
-      workspace.size, this.stream);
   }
 
   attnStepRun(plan: Uint8Array): void {

@@ -205,9 +205,26 @@ function layer(dir: string): string[] {
   att.attnStepOut(plan3, shape, [{ weight: wo, out: y3, rows: R }]);
   att.linear(out2, NQH * HD, [{ weight: wo, out: y2, rows: R }]);
 
-  // results: out1, out2, out3 (f32), y2, y3 (f32), then the stored row of kc1, vc1, kc2, vc2 (f16)
+  // (4) two layers of one token prepared together (one upload, one RoPE set for both), each on fresh copies of
+  // the inputs: the first run as attention + merge, the second as attention + attn.linearOut
+  const step4 = [0, 1].map(function () {
+    return {
+      q: upload('q'), k: upload('k'), v: upload('v'), qWeight: qw, kWeight: kw, ropeFreqs: rf, ropeInvFreq: inv,
+      kCache: upload('kc'), vCache: upload('vc'), out: alloc(NQH * HD * 4), seqLen: SEQ, position: spec.pos,
+      slidingWindow: spec.window, storeKv: true, theta: spec.theta, applyDivisor: spec.div, scale: 1.0,
+      eps: spec.eps,
+    };
+  });
+  const y4 = alloc(R * 4);
+  const plans4 = att.attnStepPrepareLayers(step4, shape, alloc(att.attnStepLayersWorkspaceSize(2, shape)));
+  att.attnStepRun(plans4[0]);
+  att.attnStepRunAttention(plans4[1]);
+  att.attnStepOut(plans4[1], shape, [{ weight: wo, out: y4, rows: R }]);
+
+  // results: out1, out2, out3 (f32), y2, y3 (f32), the stored row of kc1, vc1, kc2, vc2 (f16), then (4)'s two
+  // attnOut (f32), its y (f32) and its layers' stored rows (k, v of each, f16)
   const row = NKH * HD * 2, o = NQH * HD * 4, yb = R * 4;
-  const res = new Uint8Array(3 * o + 2 * yb + 4 * row);
+  const res = new Uint8Array(3 * o + 2 * yb + 4 * row + 2 * o + yb + 4 * row);
   att.readBuffer(out1, 0, res.subarray(0, o));
   att.readBuffer(out2, 0, res.subarray(o, 2 * o));
   att.readBuffer(out3, 0, res.subarray(2 * o, 3 * o));
@@ -216,10 +233,20 @@ function layer(dir: string): string[] {
   const base = 3 * o + 2 * yb;
   const caches = [kc1, vc1, kc2, vc2];
   for (let i = 0; i < 4; i++) att.readBuffer(caches[i], spec.pos * row, res.subarray(base + i * row, base + (i + 1) * row));
+  const b4 = base + 4 * row;
+  att.readBuffer(step4[0].out, 0, res.subarray(b4, b4 + o));
+  att.readBuffer(step4[1].out, 0, res.subarray(b4 + o, b4 + 2 * o));
+  att.readBuffer(y4, 0, res.subarray(b4 + 2 * o, b4 + 2 * o + yb));
+  const c4 = [step4[0].kCache, step4[0].vCache, step4[1].kCache, step4[1].vCache];
+  for (let i = 0; i < 4; i++) {
+    const at = b4 + 2 * o + yb + i * row;
+    att.readBuffer(c4[i], spec.pos * row, res.subarray(at, at + row));
+  }
   fs.writeFileSync(path.join(dir, 'out.bin'), res);
   for (const b of bufs) att.destroyBuffer(b);
   att.dispose();
-  return ['engine order: 7 dispatches', 'attnStep: 1 entry', 'attnStepOut: 1 entry', 'results written'];
+  return ['engine order: 7 dispatches', 'attnStep: 1 entry', 'attnStepOut: 1 entry', 'attnStepPrepareLayers: 2 layers',
+    'results written'];
 }
 
 interface PrefillSpec {

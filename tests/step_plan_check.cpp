@@ -49,6 +49,64 @@ static long rope_sweep(uint32_t stride) {
     return n;
 }
 
+// A token's layers planned one by one into one packed upload (g4_attn_step_prepare_layers): each
+// layer's plan equals the one-entry plan of that layer except for its RoPE factors, which are its
+// own set at the first (table, position) pair of the upload and the first layer's set after that,
+// with the C library's values; the packed tables fit the layers' tables regions.
+static int check_layers(int line, const std::vector<g4_step_entry>& ents, uint32_t nqh, uint32_t nkh, uint32_t hd,
+                        uint32_t cus, char* dev) {
+    const uint32_t n = (uint32_t)ents.size();
+    const StepLayout L1 = step_layout(1, nkh, nqh / nkh, hd);
+    StepPlanHost ph, one;
+    StepRopeShare share;
+    std::vector<char> packed;
+    char err[256] = "";
+    for (uint32_t i = 0; i < n; i++) {
+        char* tables = dev + packed.size();
+        if (plan_step(&ents[i], 1, nqh, nkh, hd, cus, StepTuning{}, tables, &ph, err, sizeof err, &share) ||
+            plan_step(&ents[i], 1, nqh, nkh, hd, cus, StepTuning{}, tables, &one, err, sizeof err))
+            return bad(line, "layer plan failed");
+        if (ph.n_wgs != one.n_wgs || ph.off_rope != one.off_rope || ph.waves != one.waves ||
+            ph.max_parts != one.max_parts || ph.blob.size() > one.blob.size())
+            return bad(line, "layer plan differs from the one-entry plan");
+        const StepWorkDev* w = reinterpret_cast<const StepWorkDev*>(ph.blob.data());
+        const StepWorkDev* w1 = reinterpret_cast<const StepWorkDev*>(one.blob.data());
+        for (uint32_t k = 0; k < ph.n_wgs; k++) {
+            StepWorkDev a = w[k], b = w1[k];
+            a.ent.rope_cs = b.ent.rope_cs = nullptr;
+            if (memcmp(&a, &b, sizeof a)) return bad(line, "layer work item differs from the one-entry plan");
+        }
+        if (memcmp(ph.blob.data() + ph.n_wgs * sizeof(StepWorkDev), one.blob.data() + ph.n_wgs * sizeof(StepWorkDev),
+                   ph.off_rope - ph.n_wgs * sizeof(StepWorkDev)))
+            return bad(line, "layer merge or entry table differs from the one-entry plan");
+        const size_t at = packed.size();
+        packed.resize(at + align256(ph.blob.size()), 0);
+        memcpy(packed.data() + at, ph.blob.data(), ph.blob.size());
+        if (packed.size() > (size_t)(i + 1) * L1.part_ml) return bad(line, "packed tables exceed the layers' regions");
+        const g4_step_entry& e = ents[i];
+        const float* rc = w[0].ent.rope_cs;
+        if (!e.rope_inv_freq_host) {
+            if (rc) return bad(line, "layer RoPE factors without a host table");
+            continue;
+        }
+        const char* rp = reinterpret_cast<const char*>(rc);
+        if (rp < dev || rp + hd * 4 > dev + packed.size() || (size_t)(rp - dev) % 4)
+            return bad(line, "layer RoPE pointer outside the packed tables");
+        for (uint32_t j = 0; j < i; j++)  // the first earlier layer at the same pair owns the set
+            if (ents[j].rope_inv_freq_host == e.rope_inv_freq_host && ents[j].position == e.position) {
+                if (rp >= tables) return bad(line, "layer carries a RoPE set an earlier layer placed");
+                break;
+            }
+        const float* f = reinterpret_cast<const float*>(packed.data() + (rp - dev));
+        for (uint32_t p = 0; p < hd / 2; p++) {
+            const double a = (double)((float)e.position * e.rope_inv_freq_host[p]);
+            if (f[p] != (float)cos(a) || f[hd / 2 + p] != (float)sin(a))
+                return bad(line, "layer RoPE factors differ from the C library's cos and sin");
+        }
+    }
+    return 0;
+}
+
 int main(int argc, char** argv) {
     if (argc == 3 && !strcmp(argv[1], "rope")) {
         const long n = rope_sweep((uint32_t)atoi(argv[2]));
@@ -94,14 +152,16 @@ int main(int argc, char** argv) {
             e.rope_freqs = reinterpret_cast<const uint16_t*>(base + 0x6000);
             e.scale = 1.0f;
             e.eps = 1e-6f;
-            if (ents.size() % 2 == 0) {  // every other entry carries a host RoPE table
-                inv.emplace_back(hd / 2);
-                for (uint32_t i = 0; i < hd / 2; i++) inv.back()[i] = 1.0f / (float)(i + 1);
-            }
             ents.push_back(e);
         }
-        // attach the tables after the vector stopped growing (pointers stay valid)
-        for (size_t i = 0, t = 0; i < ents.size(); i += 2, t++) ents[i].rope_inv_freq_host = inv[t].data();
+        // Host RoPE tables: entries 0, 2, 4, ... carry one; entries 0 mod 4 their own, entries 2 mod 4 one of
+        // two tables shared by window kind (entries at one position then share factors).
+        inv.assign(ents.size() + 2, std::vector<float>(hd / 2));
+        for (size_t t = 0; t < inv.size(); t++)
+            for (uint32_t i = 0; i < hd / 2; i++) inv[t][i] = 1.0f / (float)(i + 1 + t % 3);
+        for (size_t i = 0; i < ents.size(); i += 2)
+            ents[i].rope_inv_freq_host =
+                i % 4 == 0 ? inv[i].data() : inv[ents.size() + (ents[i].sliding_window ? 1 : 0)].data();
         const uint32_t n = (uint32_t)ents.size();
         const StepLayout L = step_layout(n, nkh, nqh / nkh, hd);
         char err[256] = "";
@@ -184,6 +244,7 @@ int main(int argc, char** argv) {
             }
         }
         if (n_split != ph.n_merge) return bad(line, "merge table lists entries that are not split");
+        if (check_layers(line, ents, nqh, nkh, hd, cus, dev)) return 1;
         printf("ok %u %u\n", ph.n_wgs, ph.n_merge);
     }
     return 0;

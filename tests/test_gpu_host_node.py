@@ -98,6 +98,18 @@ def test_layer_through_ts_host(tmp_path, seq, window, theta, div, hd):
     np.testing.assert_array_equal(y_out.view(np.uint32), y_linear.view(np.uint32))
     np.testing.assert_array_equal(y_out.view(np.uint32),
                                   orc.matmul_quant(out_step, arrs["wo"], O_ROWS, NQH * hd).view(np.uint32))
+    # two layers prepared together (attnStepPrepareLayers): each layer's attnOut, rows and projection as the
+    # one-layer step gives them
+    b4 = base + 4 * row
+    for i in range(2):
+        got = np.frombuffer(raw[b4 + i * o:b4 + (i + 1) * o], np.float32)
+        np.testing.assert_array_equal(got.view(np.uint32), out_step.view(np.uint32), err_msg=f"layer {i}")
+    y4 = np.frombuffer(raw[b4 + 2 * o:b4 + 2 * o + yb], np.float32)
+    np.testing.assert_array_equal(y4.view(np.uint32), y_linear.view(np.uint32))
+    rows4 = [np.frombuffer(raw[b4 + 2 * o + yb + i * row:b4 + 2 * o + yb + (i + 1) * row], np.uint16)
+             for i in range(4)]
+    for got, exp in zip(rows4, (kbits, vbits, kbits, vbits)):
+        np.testing.assert_array_equal(got, exp)
 
 
 @pytest.mark.skipif(NODE is None, reason="node is not installed")

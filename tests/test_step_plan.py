@@ -3,8 +3,10 @@ AddressSanitizer and UndefinedBehaviorSanitizer: tests/step_plan_check.cpp plans
 (the 35-layer stacks at 8K and 32K, the E2B head_dim-512 group, the 64 ragged sequences, one 128K layer,
 one local layer) and random ragged sets, and checks every plan: each entry's attended rows covered once
 and in order by its workgroups, partial-record slots unique and inside the workspace, the merge table
-listing exactly the split entries, RoPE-factor pointers inside the uploaded factors, and the packed
-tables inside the workspace's tables region.
+listing exactly the split entries, RoPE-factor pointers inside the uploaded factors with the C library's
+values, and the packed tables inside the workspace's tables region. Every scenario is also planned layer by
+layer as g4_attn_step_prepare_layers does (one packed upload, RoPE sets shared between layers at one
+position): each layer's plan must equal its one-entry plan apart from the RoPE pointer.
 """
 import shutil
 import subprocess
