@@ -86,7 +86,9 @@ int stage_upload(void* dst, const void* src, size_t bytes, hipStream_t st) {
     }
     if (!s && n < (size_t)kStageMaxSlots) {
         StageSlot fresh;
-        G4_CHECK_HIP(hipEventCreateWithFlags(&fresh.done, hipEventDisableTiming));
+        // The host only learns from the event that the copy has read the slot: no timing, and no
+        // system-scope release (an L2 write-back) behind the copy.
+        G4_CHECK_HIP(hipEventCreateWithFlags(&fresh.done, hipEventDisableTiming | hipEventDisableSystemFence));
         R.slots.insert(R.slots.begin() + R.next, fresh);  // the newest use sits just before `next`
         s = &R.slots[R.next];
         R.next = (R.next + 1) % R.slots.size();
