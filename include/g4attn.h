@@ -16,9 +16,10 @@
  *     is rejected before anything is enqueued.
  *   - `stream` is a hipStream_t (NULL = the null stream). Kernel entry points
  *     only enqueue; they never synchronise the host. Prepare calls upload
- *     their tables through pinned staging slots that are reused only once
- *     the copy reading them has completed; a thread's ring grows instead of
- *     waiting, up to 4096 uploads in flight.
+ *     their tables through pinned staging slots, copied to the workspace by
+ *     a kernel on `stream`; a slot is reused only once the copy reading it has
+ *     completed, and a thread's ring grows instead of waiting, up to 4096
+ *     uploads in flight.
  *   - Per-token fields (position, slot, seq_len) are passed by value and
  *     captured at enqueue time. This gives the ordering WebGPU provides with
  *     queue.writeBuffer before a later submit (src/engine.ts:1967-1987) without
