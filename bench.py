@@ -11,7 +11,8 @@ inputs resident in HBM:
             head, head_dim 256: the shape the decode target is set on.  [default]
             The default run also measures stack8k and reports it under
             "stack8k" in the same line.
-  stack8k   the same stack at position 8192.
+  stack8k   the same stack at position 8192 (stack4k: 4096, stack128k: 131071; the
+            ends of the metric's 4K-128K context range).
   e2b8k     the real Gemma-4-E2B stack at position 8192: head_dim 512 on the
   e2b32k    7 global layers, layers 15..34 reading layer 13's (local) or 14's
             (global) cache (KV sharing, src/config/gemma4-e2b.ts:159-178); one
@@ -87,12 +88,13 @@ def workload_spec(name: str) -> dict:
         d.update(kw)
         return d
 
-    if name in ("stack8k", "stack32k"):
-        pos = 8192 if name == "stack8k" else 32768
+    stacks = {"stack4k": (4096, 8), "stack8k": (8192, 1), "stack32k": (32768, 5), "stack128k": (131071, 9)}
+    if name in stacks:
+        pos, seed_off = stacks[name]
         cfg = e2b.AttnConfig(num_layers=35)
         layers = [layer(window=e2b.sliding_window(il, cfg), theta=e2b.rope_theta(il, cfg),
                         divisor=e2b.apply_divisor(il, cfg), seq=pos + 1, pos=pos) for il in range(35)]
-        return dict(name=name, layers=layers, seed=BASE_SEED + (1 if name == "stack8k" else 5),
+        return dict(name=name, layers=layers, seed=BASE_SEED + seed_off,
                     desc=f"35-layer Gemma-4-E2B attention stack, bs1, position {pos} (7 global + 28 local W=512), "
                          "head_dim 256, 35 separate caches")
     if name in ("e2b8k", "e2b32k"):
@@ -769,8 +771,8 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default=DEFAULT_WORKLOAD,
-                    choices=["stack32k", "stack8k", "e2b8k", "e2b32k", "long128k", "ragged64", "layer512",
-                             "prefill4k", "lmhead"])
+                    choices=["stack32k", "stack8k", "stack4k", "stack128k", "e2b8k", "e2b32k", "long128k", "ragged64",
+                             "layer512", "prefill4k", "lmhead"])
     ap.add_argument("--sets", type=int, default=0, help="cache sets to rotate (0 = enough to exceed 2x MALL)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")

@@ -3,7 +3,8 @@
 // counter collection). Inputs are synthetic: f16 cache rows from a
 // counter-based hash (values in [-2, 2), unit-RMS scale), queries likewise.
 //
-//   g4bench [--workload stack8k|stack32k|long128k|ragged64|layer512|prefill4k|prefill4k512|lmhead|copy] [--iters N]
+//   g4bench [--workload stack4k|stack8k|stack32k|stack128k|long128k|ragged64|layer512|prefill4k|prefill4k512|
+//            lmhead|copy] [--iters N]
 //           [--sets S] [--mode M]
 //
 // Decode workloads: the configurations above; `e2b8k` / `e2b32k` (35 layers at E2B's head dims,
@@ -291,8 +292,8 @@ struct Layer {
 
 static std::vector<Layer> workload(const std::string& w) {
     std::vector<Layer> L;
-    if (w == "stack8k" || w == "stack32k") {
-        unsigned pos = w == "stack8k" ? 8192 : 32768;
+    if (w == "stack4k" || w == "stack8k" || w == "stack32k" || w == "stack128k") {
+        const unsigned pos = w == "stack4k" ? 4096 : w == "stack8k" ? 8192 : w == "stack32k" ? 32768 : 131071;
         for (int i = 0; i < 35; i++) {
             bool global = (i % 5) == 4;
             L.push_back({pos + 1, global ? 0u : 512u, pos, global ? 1e6f : 1e4f, global ? 1u : 0u});
