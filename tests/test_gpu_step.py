@@ -134,11 +134,11 @@ def test_step_rope_table_same_bits(dev, seq, win, theta, div):
     np.testing.assert_array_equal(L.out.cpu().numpy().view(np.uint32), with_table.view(np.uint32))
 
 
-@pytest.mark.parametrize("seq", [2049, 8193, 32769])
+@pytest.mark.parametrize("seq", [2049, 8193, 32769, 131072])
 def test_step_e2b_stack(dev, seq):
     """35 layers (7 global theta 1e6 with the rope_freqs divisor, 28 local W=512 theta 1e4) in one launch.
     Up to 8193 the step is small (one 8-wave workgroup per CU); at 32769 it takes two 4-wave workgroups
-    per CU."""
+    per CU; at 131072 (bench.py's stack128k shape) each workgroup takes ~57 tiles."""
     announce(f"attnStep 35-layer stack seq={seq}")
     cfg = e2b.AttnConfig(num_layers=35)
     layers = [Layer(dev, 1000 * il + seq, seq, e2b.sliding_window(il, cfg), e2b.rope_theta(il, cfg),
