@@ -1027,26 +1027,28 @@ napi_value AttnPrefillRun(napi_env env, napi_callback_info info) {
 
 // ---- chunked prompt prep -------------------------------------------------------
 
-// attnPromptPrep(q, k, v, qWeight, kWeight, ropeFreqs, qOut, kCache, vCache, params (g4_prompt_prep_params
-// bytes), stream); k, v, kWeight, kCache, vCache null on KV-consumer layers.
+// attnPromptPrep(q, k, v, qWeight, kWeight, ropeFreqs, ropeInvFreq, qOut, kCache, vCache, params
+// (g4_prompt_prep_params bytes), stream); k, v, kWeight, kCache, vCache null on KV-consumer layers,
+// ropeInvFreq null or the layer's device table from ropeInvFreq.
 napi_value AttnPromptPrep(napi_env env, napi_callback_info info) {
-    Args a(env, info, 11);
+    Args a(env, info, 12);
     void* q = a.ptr(0);
     void* k = a.ptr(1);
     void* v = a.ptr(2);
     void* qw = a.ptr(3);
     void* kw = a.ptr(4);
     void* rf = a.ptr(5);
-    void* qo = a.ptr(6);
-    void* kc = a.ptr(7);
-    void* vc = a.ptr(8);
+    void* inv = a.ptr(6);
+    void* qo = a.ptr(7);
+    void* kc = a.ptr(8);
+    void* vc = a.ptr(9);
     g4_prompt_prep_params p;
-    a.params(9, &p);
-    void* s = a.ptr(10);
+    a.params(10, &p);
+    void* s = a.ptr(11);
     if (!a.ok) return nullptr;
     CALL(env, g4_attn_prompt_prep((const float*)q, (const float*)k, (const float*)v, (const uint16_t*)qw,
-                                  (const uint16_t*)kw, (const uint16_t*)rf, (uint16_t*)qo, (uint16_t*)kc,
-                                  (uint16_t*)vc, p, s));
+                                  (const uint16_t*)kw, (const uint16_t*)rf, (const float*)inv, (uint16_t*)qo,
+                                  (uint16_t*)kc, (uint16_t*)vc, p, s));
     return undefined(env);
 }
 

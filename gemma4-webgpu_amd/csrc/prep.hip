@@ -68,8 +68,10 @@ __global__ __launch_bounds__(kWG) void k_attn_prep_many(const g4_prep_layer* __r
 // chunk in one launch. The engine runs vNorm -> fusedNormRope(Q, K) ->
 // kvCacheStore once per prompt token (src/engine.ts:2460-2479, each token
 // through 2056-2091). One workgroup per kPrepTokens consecutive tokens: its
-// threads first evaluate the RoPE inverse frequencies once (the reference's
-// f32 expression with its f64 pow; they do not depend on the position), then
+// threads first take the RoPE inverse frequencies (from the caller's table
+// when given, else the reference's f32 expression with its f64 pow; they do
+// not depend on the position: measured on prefill4k's two layers, the table
+// takes the prep from 41 to 37 us), then
 // the cos and sin of every pair's f32 angle at each of its tokens' positions
 // (in f64, as the reference does) into LDS; then its four waves take the
 // tokens' head slots in turn: per token, slots 0 .. NQH-1 are the query heads
@@ -86,6 +88,7 @@ __global__ __launch_bounds__(kWG) void k_prompt_prep(const float* __restrict__ q
                                                      const uint16_t* __restrict__ q_weight,
                                                      const uint16_t* __restrict__ k_weight,
                                                      const uint16_t* __restrict__ rope_freqs,
+                                                     const float* __restrict__ inv_table,
                                                      uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_cache,
                                                      uint16_t* __restrict__ v_cache, g4_prompt_prep_params p) {
     constexpr int J = HD / 64, PJ = J / 2;
@@ -96,14 +99,14 @@ __global__ __launch_bounds__(kWG) void k_prompt_prep(const float* __restrict__ q
     const unsigned t0 = blockIdx.x * kPrepTokens;
     const unsigned nt = min(kPrepTokens, p.n_tokens - t0);  // tokens of this workgroup (the last may have fewer)
     if (threadIdx.x < NP)
-        inv[threadIdx.x] = rope_inv_freq(threadIdx.x, HD, p.theta, p.apply_divisor,
-                                         p.apply_divisor ? h2f(rope_freqs[threadIdx.x]) : 1.0f);
+        inv[threadIdx.x] = inv_table ? inv_table[threadIdx.x]
+                                     : rope_inv_freq(threadIdx.x, HD, p.theta, p.apply_divisor,
+                                                     p.apply_divisor ? h2f(rope_freqs[threadIdx.x]) : 1.0f);
     __syncthreads();
     for (unsigned i = threadIdx.x; i < nt * NP; i += kWG) {
         const unsigned tt = i / NP, pr = i % NP;
         const float ang = (float)(p.start + t0 + tt) * inv[pr];  // rope_angle's expression
-        rc[tt][pr] = (float)cos((double)ang);
-        rs[tt][pr] = (float)sin((double)ang);
+        f64_cos_sin(ang, rc[tt][pr], rs[tt][pr]);
     }
     __syncthreads();
     const unsigned lane = threadIdx.x & 63;
@@ -178,13 +181,15 @@ extern "C" int g4_attn_prep(float* q, float* k, float* v, const uint16_t* q_weig
 }
 
 extern "C" int g4_attn_prompt_prep(const float* q, const float* k, const float* v, const uint16_t* q_weight,
-                                   const uint16_t* k_weight, const uint16_t* rope_freqs, uint16_t* q_out,
-                                   uint16_t* k_cache, uint16_t* v_cache, g4_prompt_prep_params p, void* stream) {
+                                   const uint16_t* k_weight, const uint16_t* rope_freqs, const float* rope_inv_freq,
+                                   uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache, g4_prompt_prep_params p,
+                                   void* stream) {
     if (p.head_dim != 256 && p.head_dim != 512)
         return fail(G4_EINVAL, "attnPromptPrep: head_dim %u unsupported (256 or 512)", p.head_dim);
     if (p.num_q_heads == 0 || p.num_kv_heads == 0) return fail(G4_EINVAL, "attnPromptPrep: no heads");
     if (!q || !q_weight || !q_out) return fail(G4_EINVAL, "attnPromptPrep: NULL q/q_weight/q_out");
-    if (p.apply_divisor && !rope_freqs) return fail(G4_EINVAL, "attnPromptPrep: apply_divisor needs rope_freqs");
+    if (p.apply_divisor && !rope_freqs && !rope_inv_freq)
+        return fail(G4_EINVAL, "attnPromptPrep: apply_divisor needs rope_freqs");
     if (p.store_kv) {
         if (!k || !v || !k_weight || !k_cache || !v_cache)
             return fail(G4_EINVAL, "attnPromptPrep: store_kv with NULL k/v/k_weight/caches");
@@ -198,11 +203,11 @@ extern "C" int g4_attn_prompt_prep(const float* q, const float* k, const float* 
     hipStream_t st = as_stream(stream);
     const dim3 grid((p.n_tokens + kPrepTokens - 1) / kPrepTokens);
     if (p.head_dim == 512)
-        hipLaunchKernelGGL(k_prompt_prep<512>, grid, dim3(kWG), 0, st, q, k, v, q_weight, k_weight, rope_freqs, q_out,
-                           k_cache, v_cache, p);
+        hipLaunchKernelGGL(k_prompt_prep<512>, grid, dim3(kWG), 0, st, q, k, v, q_weight, k_weight, rope_freqs,
+                           rope_inv_freq, q_out, k_cache, v_cache, p);
     else
-        hipLaunchKernelGGL(k_prompt_prep<256>, grid, dim3(kWG), 0, st, q, k, v, q_weight, k_weight, rope_freqs, q_out,
-                           k_cache, v_cache, p);
+        hipLaunchKernelGGL(k_prompt_prep<256>, grid, dim3(kWG), 0, st, q, k, v, q_weight, k_weight, rope_freqs,
+                           rope_inv_freq, q_out, k_cache, v_cache, p);
     G4_CHECK_LAUNCH("attnPromptPrep");
     return G4_OK;
 }

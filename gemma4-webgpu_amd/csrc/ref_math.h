@@ -43,6 +43,60 @@ __device__ __forceinline__ float rope_inv_freq(unsigned i, unsigned head_dim, fl
     return freq;
 }
 
+// f32(cos a) and f32(sin a) of an f32 angle evaluated in f64, as the reference
+// expressions are restated (fused_per_head_norm_rope.wgsl:56-57): equal to
+// (float)cos((double)a) and (float)sin((double)a). One Cody-Waite reduction
+// a = k pi/2 + r (pi/2 in parts of 33, 33 and 53 bits: k P1 and k P2 are exact
+// for |k| < 2^20) and Taylor polynomials on |r| <= pi/4 (next terms below
+// 2^-62 relative) leave the value d a few f64 ulps from the exact one; the
+// device library's cos and sin are within one ulp of it. Where d +- 2^-46 |d|
+// rounds to one f32, both round to that f32; a value near an f32 rounding
+// boundary, or an angle beyond 2^20 or not finite, takes the device library's
+// cos and sin.
+__device__ __forceinline__ void f64_cos_sin(float a, float& c, float& s) {
+    constexpr double kTwoOverPi = 0x1.45f306dc9c883p-1;
+    constexpr double kP1 = 0x1.921fb544p+0, kP2 = 0x1.0b4611a6p-34, kP3 = 0x1.3198a2e037073p-69;
+    constexpr double kRound = 0x1.8p52;  // adding and subtracting it rounds to an integer (|x| < 2^51)
+    const double x = (double)a;
+    const double kr = fma(x, kTwoOverPi, kRound);
+    const double k = kr - kRound;
+    const unsigned q = (unsigned)__double2loint(kr) & 3u;  // quadrant: a = k pi/2 + r
+    const double r = fma(-k, kP3, fma(-k, kP2, fma(-k, kP1, x)));
+    const double z = r * r;
+    double ps = 1.0 / 355687428096000;  // sin r = r + r z (-1/3! + z (1/5! - ...)), terms to r^17
+    ps = fma(z, ps, -1.0 / 1307674368000);
+    ps = fma(z, ps, 1.0 / 6227020800);
+    ps = fma(z, ps, -1.0 / 39916800);
+    ps = fma(z, ps, 1.0 / 362880);
+    ps = fma(z, ps, -1.0 / 5040);
+    ps = fma(z, ps, 1.0 / 120);
+    ps = fma(z, ps, -1.0 / 6);
+    const double sr = fma(r * z, ps, r);
+    double pc = -1.0 / 6402373705728000;  // cos r = 1 + z (-1/2! + z (1/4! - ...)), terms to r^18
+    pc = fma(z, pc, 1.0 / 20922789888000);
+    pc = fma(z, pc, -1.0 / 87178291200);
+    pc = fma(z, pc, 1.0 / 479001600);
+    pc = fma(z, pc, -1.0 / 3628800);
+    pc = fma(z, pc, 1.0 / 40320);
+    pc = fma(z, pc, -1.0 / 720);
+    pc = fma(z, pc, 1.0 / 24);
+    pc = fma(z, pc, -0.5);
+    const double cr = fma(z, pc, 1.0);
+    const double sv = q & 1u ? cr : sr, cv = q & 1u ? sr : cr;
+    const double sin_a = q & 2u ? -sv : sv;
+    const double cos_a = (q + 1u) & 2u ? -cv : cv;
+    const double es = 0x1p-46 * fabs(sin_a), ec = 0x1p-46 * fabs(cos_a);
+    const bool ok = fabs(x) <= 0x1p20 && (float)(sin_a - es) == (float)(sin_a + es) &&
+                    (float)(cos_a - ec) == (float)(cos_a + ec);
+    if (ok) {
+        c = (float)cos_a;
+        s = (float)sin_a;
+    } else {
+        c = (float)cos(x);
+        s = (float)sin(x);
+    }
+}
+
 // The angle of pair i at `position` (fused_per_head_norm_rope.wgsl:55).
 __device__ __forceinline__ float rope_angle_val(unsigned i, unsigned head_dim, float theta, unsigned position,
                                                 unsigned apply_divisor, float divisor) {

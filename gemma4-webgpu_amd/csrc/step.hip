@@ -179,8 +179,8 @@ __global__ __launch_bounds__(64 * W, HD == 256 ? 8 / W : 1) void k_attn_step(
             // transcendentals; division by 1 is exact, so the load above stays unconditional
             const float freq = rope_inv_freq(pair, HD, ent.theta, 1u, apply_divisor ? h2f((uint16_t)fbits) : 1.0f);
             const float ang = (float)ent.position * freq;
-            const float c = (float)cos((double)ang);
-            const float sn = (float)sin((double)ang);
+            float c, sn;
+            f64_cos_sin(ang, c, sn);
             if (threadIdx.x < HD / 2) {
                 sm.rope_c[pair] = c;
                 sm.rope_s[pair] = sn;

@@ -180,7 +180,7 @@ SIGNATURES: dict[str, list] = {
     "g4_attn_prefill_run": [C.POINTER(DecodePlan), _P],
     "g4_attn_prefill_run_timed": [C.POINTER(DecodePlan), _P, _P, _P],
     "g4_attn_prefill": [C.POINTER(PrefillEntry), _U32, _U32, _U32, _U32, _P, _SZ, _P],
-    "g4_attn_prompt_prep": [_P, _P, _P, _P, _P, _P, _P, _P, _P, PromptPrepParams, _P],
+    "g4_attn_prompt_prep": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, PromptPrepParams, _P],
     "g4_matmul_quant_f16": [_P, _P, _P, MatmulParams, _P],
     "g4_linear_f16": [_P, _U32, C.POINTER(LinearSeg), _U32, _P],
     "g4_read_ceiling": [_P, _SZ, _P, _P, _P, _P],

@@ -372,10 +372,11 @@ def attn_step(entries, num_q_heads, num_kv_heads, head_dim, workspace, stream=No
 
 def attn_prompt_prep(q, q_weight, q_out, n_tokens, start, num_q_heads, num_kv_heads, head_dim, theta, apply_divisor,
                      rope_freqs=None, k=None, v=None, k_weight=None, k_cache=None, v_cache=None, max_seq_len=0,
-                     eps=1e-6, stream=None):
+                     eps=1e-6, rope_inv_freq=None, stream=None):
     """q/k/v/norm+RoPE/store of n_tokens prompt tokens at positions start.. in one launch. q: f32
     [n_tokens][NQH][HD]; q_out: f16 [n_tokens][NQH][HD]; with k (and v, k_weight, caches of max_seq_len rows)
-    the layer is a KV producer and rows start .. start + n_tokens - 1 are stored."""
+    the layer is a KV producer and rows start .. start + n_tokens - 1 are stored. rope_inv_freq: optional
+    device table from rope_inv_freq() for this layer's theta/divisor (else each workgroup evaluates it)."""
     store = k is not None
     nq = n_tokens * num_q_heads * head_dim
     nk = n_tokens * num_kv_heads * head_dim
@@ -386,6 +387,7 @@ def attn_prompt_prep(q, q_weight, q_out, n_tokens, start, num_q_heads, num_kv_he
              _f32(v, "v", nk) if store else None, _f16(q_weight, "q_weight", head_dim),
              _f16(k_weight, "k_weight", head_dim) if store else None,
              _f16(rope_freqs, "rope_freqs", head_dim // 2) if rope_freqs is not None else None,
+             _f32(rope_inv_freq, "rope_inv_freq", head_dim // 2) if rope_inv_freq is not None else None,
              _f16(q_out, "q_out", nq), _f16(k_cache, "k_cache", rows) if store else None,
              _f16(v_cache, "v_cache", rows) if store else None, p, _stream(stream))
 

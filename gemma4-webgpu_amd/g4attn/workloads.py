@@ -47,9 +47,10 @@ def prefill4k(dev, nqh=8, nkh=1, hd=256, T=PREFILL_T, chunk=PREFILL_CHUNK, windo
         vc = torch.empty_like(kc)
         out = torch.empty(T * nqh * hd, dtype=torch.float32, device=dev)
         theta, div = (1e4, 0) if w else (1e6, 1)
+        inv = ops.rope_inv_freq(theta, hd, div, rf)  # the layer's inverse frequencies, once (as at load)
         preps.append(dict(q=qr, q_weight=ones, q_out=q, n_tokens=T, start=0, num_q_heads=nqh, num_kv_heads=nkh,
                           head_dim=hd, theta=theta, apply_divisor=div, rope_freqs=rf, k=kr, v=vr, k_weight=ones,
-                          k_cache=kc, v_cache=vc, max_seq_len=T, eps=EPS))
+                          k_cache=kc, v_cache=vc, max_seq_len=T, eps=EPS, rope_inv_freq=inv))
         layers.append((q, kc, vc, out, w))
         for c0 in range(0, T, chunk):
             entries.append(dict(q=q[c0 * nqh * hd:], k_cache=kc, v_cache=vc, out=out[c0 * nqh * hd:],

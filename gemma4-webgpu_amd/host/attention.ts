@@ -165,6 +165,7 @@ export interface PromptPrep {
   qWeight: DeviceBuffer;      // attn_q_norm f16 [HD]
   kWeight?: DeviceBuffer;     // attn_k_norm f16 [HD]
   ropeFreqs?: DeviceBuffer;   // f16 divisor table (global layers)
+  ropeInvFreq?: DeviceBuffer; // f32 [HD/2] from ropeInvFreq for this layer's theta/divisor (computed once, at load)
   qOut: DeviceBuffer;         // f16 [nTokens][NQH][HD]: PrefillEntry.q
   kCache?: DeviceBuffer;      // f16 [maxSeqLen][NKH][HD]: rows start .. start + nTokens - 1 are written
   vCache?: DeviceBuffer;
@@ -252,7 +253,7 @@ export interface Addon {
     s: bigint): Uint8Array;
   attnPrefillRun(plan: Uint8Array, s: bigint): void;
   attnPromptPrep(q: bigint, k: bigint | null, v: bigint | null, qw: bigint, kw: bigint | null, rf: bigint | null,
-    qOut: bigint, kc: bigint | null, vc: bigint | null, p: Uint8Array, s: bigint): void;
+    inv: bigint | null, qOut: bigint, kc: bigint | null, vc: bigint | null, p: Uint8Array, s: bigint): void;
   [key: string]: any;
 }
 
@@ -457,7 +458,7 @@ export class HipAttention {
     ]);
     function ptr(b: DeviceBuffer | undefined): bigint | null { return b ? b.ptr : null; }
     this.g4.attnPromptPrep(p.q.ptr, ptr(p.k), ptr(p.v), p.qWeight.ptr, ptr(p.kWeight), ptr(p.ropeFreqs),
-      p.qOut.ptr, ptr(p.kCache), ptr(p.vCache), params.bytes, this.stream);
+      ptr(p.ropeInvFreq), p.qOut.ptr, ptr(p.kCache), ptr(p.vCache), params.bytes, this.stream);
   }
 
   lmHeadWorkspaceSize(shape: LmHeadShape): number {

@@ -320,9 +320,12 @@ function promptPrep(dir: string): string[] {
   const qOut = alloc(spec.nTokens * spec.nqh * spec.hd * 2);
   const kc = alloc(spec.rows * spec.nkh * spec.hd * 2);
   const vc = alloc(spec.rows * spec.nkh * spec.hd * 2);
+  const rf = upload(A.rf);
+  const inv = alloc(spec.hd / 2 * 4);  // the layer's inverse frequencies, computed once (as at load)
+  att.ropeInvFreq(spec.theta, spec.hd, spec.div, rf, inv);
   att.attnPromptPrep({
     q: upload(A.q), k: upload(A.k), v: upload(A.v), qWeight: upload(A.qw), kWeight: upload(A.kw),
-    ropeFreqs: upload(A.rf), qOut: qOut, kCache: kc, vCache: vc, nTokens: spec.nTokens, start: spec.start,
+    ropeFreqs: rf, ropeInvFreq: inv, qOut: qOut, kCache: kc, vCache: vc, nTokens: spec.nTokens, start: spec.start,
     theta: spec.theta, applyDivisor: spec.div, maxSeqLen: spec.rows,
   }, { numQHeads: spec.nqh, numKvHeads: spec.nkh, headDim: spec.hd });
   const res = new Uint8Array(qOut.size + kc.size + vc.size);

@@ -442,10 +442,15 @@ typedef struct g4_prompt_prep_params {
 } g4_prompt_prep_params;
 
 /* q: f32 [n_tokens][num_q_heads][head_dim]; k, v: f32 [n_tokens][num_kv_heads][head_dim]
- * (NULL with store_kv 0); q_out: f16 [n_tokens][num_q_heads][head_dim]. */
+ * (NULL with store_kv 0); q_out: f16 [n_tokens][num_q_heads][head_dim].
+ * rope_inv_freq: optional device [head_dim/2] table from g4_rope_inv_freq for
+ * this layer's theta / divisor (computed once, at load; the same bits as the
+ * kernel's own evaluation); NULL: every workgroup evaluates the reference's
+ * f64 pow itself. */
 int g4_attn_prompt_prep(const float* q, const float* k, const float* v, const uint16_t* q_weight,
-                        const uint16_t* k_weight, const uint16_t* rope_freqs, uint16_t* q_out, uint16_t* k_cache,
-                        uint16_t* v_cache, g4_prompt_prep_params p, void* stream);
+                        const uint16_t* k_weight, const uint16_t* rope_freqs, const float* rope_inv_freq,
+                        uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache, g4_prompt_prep_params p,
+                        void* stream);
 
 /* ---- the f16 projections either side of the block ------------------------
  * attn.linearQKV (src/engine.ts:2045-2051) and attn.linearOut (:2096):

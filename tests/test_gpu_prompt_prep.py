@@ -42,11 +42,14 @@ class Chunk:
         self.store = store
         self.dqw, self.dkw, self.drf = t16(self.qw, dev), t16(self.kw, dev), t16(ROPE, dev)
 
-    def run(self):
+    def run(self, inv_table=False):
+        """inv_table: pass the layer's inverse-frequency table from g4_rope_inv_freq instead of letting each
+        workgroup evaluate it."""
         kw = dict(k=self.dk, v=self.dv, k_weight=self.dkw, k_cache=self.kc, v_cache=self.vc,
                   max_seq_len=self.rows) if self.store else {}
+        inv = ops.rope_inv_freq(self.theta, self.hd, self.div, self.drf) if inv_table else None
         ops.attn_prompt_prep(self.dq, self.dqw, self.q_out, self.T, self.start, self.nqh, self.nkh, self.hd,
-                             self.theta, self.div, rope_freqs=self.drf, eps=EPS, **kw)
+                             self.theta, self.div, rope_freqs=self.drf, eps=EPS, rope_inv_freq=inv, **kw)
         torch.cuda.synchronize()
 
     def expected(self):
@@ -82,16 +85,19 @@ class Chunk:
             assert (c[:s] == POISON).all() and (c[e:] == POISON).all(), f"{name} rows outside the chunk written"
 
 
-@pytest.mark.parametrize("start,T,hd,theta,div", [
-    (0, 512, 256, 1e4, 0),            # local layer, the first chunk
-    (131071 - 511, 512, 256, 1e6, 1),  # global layer, positions up to 131071
-    (4096, 512, 512, 1e6, 1),         # E2B global layer (head_dim 512)
-    (77, 5, 256, 1e4, 0),             # a short ragged chunk
+@pytest.mark.parametrize("start,T,hd,theta,div,inv_table", [
+    (0, 512, 256, 1e4, 0, False),            # local layer, the first chunk
+    (131071 - 511, 512, 256, 1e6, 1, False),  # global layer, positions up to 131071
+    (4096, 512, 512, 1e6, 1, False),         # E2B global layer (head_dim 512)
+    (77, 5, 256, 1e4, 0, False),             # a short ragged chunk
+    (60000, 512, 256, 1e4, 0, True),         # the inverse frequencies from the caller's table
+    (131071 - 511, 512, 256, 1e6, 1, True),
+    (4096, 512, 512, 1e6, 1, True),
 ])
-def test_prompt_prep_bit_exact(dev, start, T, hd, theta, div):
-    announce(f"attnPromptPrep start={start} T={T} hd={hd} theta={theta}")
+def test_prompt_prep_bit_exact(dev, start, T, hd, theta, div, inv_table):
+    announce(f"attnPromptPrep start={start} T={T} hd={hd} theta={theta} table={inv_table}")
     c = Chunk(dev, 500 + start + hd, start, T, hd, theta, div)
-    c.run()
+    c.run(inv_table)
     c.check()
 
 
