@@ -15,7 +15,8 @@
 // where the position advances every iteration and every plan is prepared again inside the timed
 // region: --mode loop (one step per head_dim group per token), layers (the engine's layer order:
 // one g4_attn_step_prepare_layers per head_dim group per token, then each layer's attention and
-// merge launches in turn), layers_each (the same order with one g4_attn_step_prepare per layer).
+// merge launches in turn), layers_each (the same order with one g4_attn_step_prepare per layer), chain
+// and chain_each (those two orders with each layer's q/k/v projection and o_proj around its attention).
 //
 // `prefill4k` runs the causal MFMA prefill of a 4096-token prompt for one
 // global layer and one 512-window local layer, as 512-token chunks (16
@@ -65,6 +66,7 @@
     } while (0)
 
 static const unsigned NQH = 8, NKH = 1, HD = 256;
+static const unsigned kHidden = 1536;  // E2B's hidden size: the projections' input length and o_proj rows
 
 __device__ __forceinline__ float hash_unit(uint64_t x) {  // splitmix64 finaliser -> [-2, 2)
     x += 0x9E3779B97F4A7C15ull;
@@ -423,7 +425,11 @@ int main(int argc, char** argv) {
     // loop: one step per head_dim group per token; layers: the engine's order, every layer's plan from one
     // g4_attn_step_prepare_layers per head_dim group, then layer by layer attention + merge; layers_each:
     // the same order with one g4_attn_step_prepare per layer.
-    const bool token_loop = mode == "loop" || mode == "layers" || mode == "layers_each";
+    // chain / chain_each: the same two orders with the layer's projections around its attention (q/k/v in
+    // one g4_linear_f16 launch, then o_proj with the merge folded in, g4_attn_step_run_out; f16 weights of
+    // E2B's shapes, hidden 1536, distinct per layer), as the engine runs a token.
+    const bool chain = mode == "chain" || mode == "chain_each";
+    const bool token_loop = mode == "loop" || mode == "layers" || mode == "layers_each" || chain;
     if (mode != "step" && !token_loop && !all256) {
         fprintf(stderr, "workload %s: head_dim 512 layers run on the fused step only (--mode step)\n", wl.c_str());
         return 2;
@@ -456,6 +462,8 @@ int main(int argc, char** argv) {
         void* layers_ws[2] = {nullptr, nullptr};
         size_t layers_ws_bytes[2] = {0, 0};
         std::vector<g4_decode_plan> layer_plans[2];
+        std::vector<void*> wqkv, wo, y;  // chain modes: per layer q/k/v weight rows, o_proj weight, o_proj output
+        void* x = nullptr;               // the layers' input (hidden 1536)
         g4_decode_plan plan;          // unfused: prep + split + merge
         g4_decode_plan step_plan[2];  // one-launch step per head_dim group (256, 512)
         bool has_step[2] = {false, false};
@@ -538,10 +546,29 @@ int main(int argc, char** argv) {
             se.apply_divisor = l.divisor;
             se.scale = 1.0f;
             se.eps = 1e-6f;
+            if (chain) {  // q, k, v weight rows [(NQH + 2 NKH) hd][1536] and o_proj [1536][NQH hd], f16
+                void *wq, *wov, *yv;
+                const size_t qkv_bytes = (size_t)(NQH + 2 * NKH) * hd * kHidden * 2;
+                const size_t o_bytes = (size_t)kHidden * NQH * hd * 2;
+                CK(g4_malloc(&wq, qkv_bytes));
+                CK(g4_malloc(&wov, o_bytes));
+                CK(g4_malloc(&yv, kHidden * 4));
+                hipLaunchKernelGGL(k_fill_f16, dim3(1024), dim3(256), 0, st, (_Float16*)wq, (uint64_t)qkv_bytes / 2, seed++);
+                hipLaunchKernelGGL(k_fill_f16, dim3(1024), dim3(256), 0, st, (_Float16*)wov, (uint64_t)o_bytes / 2, seed++);
+                S[s].wqkv.push_back(wq);
+                S[s].wo.push_back(wov);
+                S[s].y.push_back(yv);
+                S[s].bufs.insert(S[s].bufs.end(), {wq, wov, yv});
+            }
             S[s].order.emplace_back(hd == 512 ? 1 : 0, (int)steps[hd == 512 ? 1 : 0].size());
             steps[hd == 512 ? 1 : 0].push_back(se);
         }
         HK(hipGetLastError());
+        if (chain) {
+            CK(g4_malloc(&S[s].x, kHidden * 4));
+            hipLaunchKernelGGL(k_fill_f32, dim3(2), dim3(256), 0, st, (float*)S[s].x, (uint64_t)kHidden, seed++);
+            S[s].bufs.push_back(S[s].x);
+        }
         if (all256) {
             CK(g4_malloc(&S[s].ws, ws_bytes));
             CK(g4_malloc(&S[s].prep_table, preps.size() * sizeof(g4_prep_layer)));
@@ -600,22 +627,37 @@ int main(int argc, char** argv) {
                     CK(g4_attn_step_workspace_size(n, NQH, NKH, hd, &b));
                     CK(g4_attn_step_prepare(s.steps[h].data(), n, NQH, NKH, hd, s.step_ws[h], b, &s.step_plan[h], st));
                     CK(g4_attn_step_run(&s.step_plan[h], st));
-                } else if (mode == "layers") {
+                } else if (mode == "layers" || mode == "chain") {
                     CK(g4_attn_step_prepare_layers(s.steps[h].data(), n, NQH, NKH, hd, s.layers_ws[h],
                                                    s.layers_ws_bytes[h], s.layer_plans[h].data(), st));
                 }
             }
             if (mode == "loop") return;
-            for (const auto& o : s.order) {  // the engine's layer order
+            for (size_t li = 0; li < s.order.size(); li++) {  // the engine's layer order
+                const auto& o = s.order[li];
                 const unsigned hd = o.first ? 512 : 256;
                 g4_decode_plan& plan = s.layer_plans[o.first][o.second];
-                if (mode == "layers_each") {
+                const g4_step_entry& se = s.steps[o.first][o.second];
+                if (mode == "layers_each" || mode == "chain_each") {
                     const size_t one = s.layers_ws_bytes[o.first] / s.steps[o.first].size();
-                    CK(g4_attn_step_prepare(&s.steps[o.first][o.second], 1, NQH, NKH, hd,
-                                            (char*)s.layers_ws[o.first] + (size_t)o.second * one, one, &plan, st));
+                    CK(g4_attn_step_prepare(&se, 1, NQH, NKH, hd, (char*)s.layers_ws[o.first] + (size_t)o.second * one,
+                                            one, &plan, st));
+                }
+                if (chain) {  // attn.linearQKV (a consumer that recomputes its producer's row projects q/k/v too)
+                    const uint16_t* w = (const uint16_t*)s.wqkv[li];
+                    const g4_linear_seg segs[3] = {
+                        {w, (float*)se.q, NQH * hd},
+                        {w + (size_t)NQH * hd * kHidden, (float*)se.k, NKH * hd},
+                        {w + (size_t)(NQH + NKH) * hd * kHidden, (float*)se.v, NKH * hd}};
+                    CK(g4_linear_f16((const float*)s.x, kHidden, segs, se.store_kv ? 3u : 1u, st));
                 }
                 CK(g4_attn_step_run_attention(&plan, st));
-                CK(g4_attn_step_run_merge(&plan, st));
+                if (chain) {
+                    const g4_linear_seg out = {(const uint16_t*)s.wo[li], (float*)s.y[li], kHidden};
+                    CK(g4_attn_step_run_out(&plan, &out, 1, st));  // attn.linearOut with the merge folded in
+                } else {
+                    CK(g4_attn_step_run_merge(&plan, st));
+                }
             }
             return;
         }
