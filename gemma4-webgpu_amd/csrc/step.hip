@@ -392,7 +392,10 @@ int g4_attn_step_prepare_layers(const g4_step_entry* layers, uint32_t n_layers, 
         char* const tables = ws + blob.size();
         rc = plan_step(layers + i, 1, num_q_heads, num_kv_heads, head_dim, device_cus(), step_tuning(), tables, &ph,
                        err, sizeof err, &share);
-        if (rc) return fail(rc, "attnStepLayers: layer %u: %s", i, err);
+        if (rc) {  // no plan of this call is usable: their tables were never uploaded
+            for (uint32_t j = 0; j < i; j++) memset(&plans[j], 0, sizeof plans[j]);
+            return fail(rc, "attnStepLayers: layer %u: %s", i, err);
+        }
         // packed tables never outgrow one layer's share of the region (each fits a one-entry step's)
         const size_t at = blob.size(), bytes = align256(ph.blob.size());
         blob.resize(at + bytes);

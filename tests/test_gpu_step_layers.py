@@ -15,7 +15,7 @@ import pytest
 import torch
 
 from conftest import announce
-from g4attn import ops
+from g4attn import abi, ops
 from test_gpu_linear import t_u16, weights
 from test_gpu_step import ROPE, TOL, Layer
 
@@ -136,7 +136,11 @@ def test_layers_workspace_and_errors(dev):
     bad = ops.make_step_entries(entries, 8, 1, 256)
     bad[1].seq_len = 0
     ws = torch.empty(need, dtype=torch.uint8, device=dev)
+    plans = (abi.DecodePlan * 2)()
     with pytest.raises(RuntimeError, match="layer 1: attnStep: entry 0 seq_len 0"):
-        ops.attn_step_prepare_layers(bad, 8, 1, 256, ws)
+        abi.call("g4_attn_step_prepare_layers", bad, 2, 8, 1, 256, ws.data_ptr(), ws.numel(), plans, None)
+    for i in range(2):  # no plan of a failed call runs: layer 0's tables were never uploaded
+        with pytest.raises(RuntimeError, match="not prepared"):
+            ops.attn_step_run_attention(plans[i])
     torch.cuda.synchronize()
     del tabs
