@@ -544,11 +544,11 @@ napi_value AttnStepWorkspaceSize(napi_env env, napi_callback_info info) {
 }
 
 napi_value AttnStepLayersWorkspaceSize(napi_env env, napi_callback_info info) {
-    Args a(env, info, 4);  // n_layers, num_q_heads, num_kv_heads, head_dim
-    const uint32_t n = a.u32(0), nqh = a.u32(1), nkh = a.u32(2), hd = a.u32(3);
+    Args a(env, info, 5);  // n_layers, entries_per_layer, num_q_heads, num_kv_heads, head_dim
+    const uint32_t n = a.u32(0), e = a.u32(1), nqh = a.u32(2), nkh = a.u32(3), hd = a.u32(4);
     if (!a.ok) return nullptr;
     size_t bytes = 0;
-    CALL(env, g4_attn_step_layers_workspace_size(n, nqh, nkh, hd, &bytes));
+    CALL(env, g4_attn_step_layers_workspace_size(n, e, nqh, nkh, hd, &bytes));
     return number(env, (double)bytes);
 }
 
@@ -809,38 +809,43 @@ napi_value AttnStepPrepare(napi_env env, napi_callback_info info) {
     return plan;
 }
 
-// attnStepPrepareLayers(layers[], nqh, nkh, hd, workspace, workspaceBytes, stream) -> plan per layer
-// (an array of Uint8Arrays over one ArrayBuffer)
+// attnStepPrepareLayers(entries[], entriesPerLayer, nqh, nkh, hd, workspace, workspaceBytes, stream) -> plan
+// per layer (an array of Uint8Arrays over one ArrayBuffer); layer i is entries[i * entriesPerLayer ..).
 napi_value AttnStepPrepareLayers(napi_env env, napi_callback_info info) {
-    Args a(env, info, 7);
+    Args a(env, info, 8);
     if (!a.ok) return nullptr;
     bool is_array = false;
     napi_is_array(env, a.v[0], &is_array);
     if (!is_array) {
-        napi_throw_type_error(env, nullptr, "attnStepPrepareLayers: layers must be an array");
+        napi_throw_type_error(env, nullptr, "attnStepPrepareLayers: entries must be an array");
         return nullptr;
     }
     uint32_t n = 0;
     napi_get_array_length(env, a.v[0], &n);
-    const uint32_t nqh = a.u32(1), nkh = a.u32(2), hd = a.u32(3);
+    const uint32_t per = a.u32(1), nqh = a.u32(2), nkh = a.u32(3), hd = a.u32(4);
     if (!a.ok) return nullptr;
+    if (per == 0 || n % per) {
+        napi_throw_range_error(env, nullptr, "attnStepPrepareLayers: entries are not whole layers");
+        return nullptr;
+    }
     std::vector<g4_step_entry> ents(n);
     for (uint32_t i = 0; i < n; i++) {
         napi_value obj;
         napi_get_element(env, a.v[0], i, &obj);
         if (!step_entry(a, obj, i, hd, &ents[i])) return nullptr;
     }
-    void* ws = a.ptr(4);
-    const double ws_bytes = a.f64(5);
-    void* s = a.ptr(6);
+    void* ws = a.ptr(5);
+    const double ws_bytes = a.f64(6);
+    void* s = a.ptr(7);
     if (!a.ok) return nullptr;
+    const uint32_t nl = n / per;
     napi_value ab, list;
     void* pdata = nullptr;
-    NAPI_OK(env, napi_create_arraybuffer(env, (size_t)n * sizeof(g4_decode_plan), &pdata, &ab));
-    CALL(env, g4_attn_step_prepare_layers(ents.data(), n, nqh, nkh, hd, ws, (size_t)ws_bytes,
+    NAPI_OK(env, napi_create_arraybuffer(env, (size_t)nl * sizeof(g4_decode_plan), &pdata, &ab));
+    CALL(env, g4_attn_step_prepare_layers(ents.data(), nl, per, nqh, nkh, hd, ws, (size_t)ws_bytes,
                                           static_cast<g4_decode_plan*>(pdata), s));
-    NAPI_OK(env, napi_create_array_with_length(env, n, &list));
-    for (uint32_t i = 0; i < n; i++) {
+    NAPI_OK(env, napi_create_array_with_length(env, nl, &list));
+    for (uint32_t i = 0; i < nl; i++) {
         napi_value plan;
         NAPI_OK(env, napi_create_typedarray(env, napi_uint8_array, sizeof(g4_decode_plan), ab,
                                             (size_t)i * sizeof(g4_decode_plan), &plan));

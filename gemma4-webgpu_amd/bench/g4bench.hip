@@ -586,7 +586,7 @@ int main(int argc, char** argv) {
                                     &S[s].step_plan[h], st));
             S[s].has_step[h] = true;
             if (token_loop) {
-                CK(g4_attn_step_layers_workspace_size((uint32_t)steps[h].size(), NQH, NKH, hd,
+                CK(g4_attn_step_layers_workspace_size((uint32_t)steps[h].size(), 1, NQH, NKH, hd,
                                                       &S[s].layers_ws_bytes[h]));
                 CK(g4_malloc(&S[s].layers_ws[h], S[s].layers_ws_bytes[h]));
                 S[s].layer_plans[h].resize(steps[h].size());
@@ -628,7 +628,7 @@ int main(int argc, char** argv) {
                     CK(g4_attn_step_prepare(s.steps[h].data(), n, NQH, NKH, hd, s.step_ws[h], b, &s.step_plan[h], st));
                     CK(g4_attn_step_run(&s.step_plan[h], st));
                 } else if (mode == "layers" || mode == "chain") {
-                    CK(g4_attn_step_prepare_layers(s.steps[h].data(), n, NQH, NKH, hd, s.layers_ws[h],
+                    CK(g4_attn_step_prepare_layers(s.steps[h].data(), n, 1, NQH, NKH, hd, s.layers_ws[h],
                                                    s.layers_ws_bytes[h], s.layer_plans[h].data(), st));
                 }
             }

@@ -355,30 +355,33 @@ int g4_attn_step_prepare(const g4_step_entry* entries, uint32_t n_entries, uint3
     return G4_OK;
 }
 
-// Layers workspace: every layer's tables region (as a one-entry step's), packed
-// from the start, then every layer's partial records (as a one-entry step's).
-int g4_attn_step_layers_workspace_size(uint32_t n_layers, uint32_t num_q_heads, uint32_t num_kv_heads,
-                                       uint32_t head_dim, size_t* bytes) {
+// Layers workspace: every layer's tables region (as a step of entries_per_layer
+// entries), packed from the start, then every layer's partial records.
+int g4_attn_step_layers_workspace_size(uint32_t n_layers, uint32_t entries_per_layer, uint32_t num_q_heads,
+                                       uint32_t num_kv_heads, uint32_t head_dim, size_t* bytes) {
     size_t one = 0;
-    int rc = g4_attn_step_workspace_size(1, num_q_heads, num_kv_heads, head_dim, &one);
+    int rc = g4_attn_step_workspace_size(entries_per_layer, num_q_heads, num_kv_heads, head_dim, &one);
     if (rc) return rc;
     if (n_layers == 0 || n_layers > 65535) return fail(G4_EINVAL, "attnStepLayers: %u layers (1..65535)", n_layers);
+    if (entries_per_layer == 0 || entries_per_layer > 65535)
+        return fail(G4_EINVAL, "attnStepLayers: %u entries per layer (1..65535)", entries_per_layer);
     *bytes = (size_t)n_layers * one;
     return G4_OK;
 }
 
-int g4_attn_step_prepare_layers(const g4_step_entry* layers, uint32_t n_layers, uint32_t num_q_heads,
-                                uint32_t num_kv_heads, uint32_t head_dim, void* workspace, size_t workspace_bytes,
-                                g4_decode_plan* plans, void* stream) {
+int g4_attn_step_prepare_layers(const g4_step_entry* entries, uint32_t n_layers, uint32_t entries_per_layer,
+                                uint32_t num_q_heads, uint32_t num_kv_heads, uint32_t head_dim, void* workspace,
+                                size_t workspace_bytes, g4_decode_plan* plans, void* stream) {
     size_t need = 0;
-    int rc = g4_attn_step_layers_workspace_size(n_layers, num_q_heads, num_kv_heads, head_dim, &need);
+    int rc = g4_attn_step_layers_workspace_size(n_layers, entries_per_layer, num_q_heads, num_kv_heads, head_dim,
+                                                &need);
     if (rc) return rc;
-    if (!layers || !plans) return fail(G4_EINVAL, "attnStepLayers: NULL pointer");
+    if (!entries || !plans) return fail(G4_EINVAL, "attnStepLayers: NULL pointer");
     if (!workspace || workspace_bytes < need)
         return fail(G4_ENOSPC, "attnStepLayers: workspace %zu bytes < %zu needed", workspace_bytes, need);
     for (uint32_t i = 0; i < n_layers; i++) memset(&plans[i], 0, sizeof plans[i]);
-    const uint32_t G = num_q_heads / num_kv_heads;
-    const StepLayout L1 = step_layout(1, num_kv_heads, G, head_dim);
+    const uint32_t G = num_q_heads / num_kv_heads, E = entries_per_layer;
+    const StepLayout L1 = step_layout(E, num_kv_heads, G, head_dim);
     const size_t tables_one = L1.part_ml, records_one = L1.total - L1.part_ml;
     char* ws = static_cast<char*>(workspace);
     char* const records = ws + (size_t)n_layers * tables_one;
@@ -390,18 +393,18 @@ int g4_attn_step_prepare_layers(const g4_step_entry* layers, uint32_t n_layers, 
     char err[256];
     for (uint32_t i = 0; i < n_layers; i++) {
         char* const tables = ws + blob.size();
-        rc = plan_step(layers + i, 1, num_q_heads, num_kv_heads, head_dim, device_cus(), step_tuning(), tables, &ph,
-                       err, sizeof err, &share);
+        rc = plan_step(entries + (size_t)i * E, E, num_q_heads, num_kv_heads, head_dim, device_cus(), step_tuning(),
+                       tables, &ph, err, sizeof err, &share);
         if (rc) {  // no plan of this call is usable: their tables were never uploaded
             for (uint32_t j = 0; j < i; j++) memset(&plans[j], 0, sizeof plans[j]);
             return fail(rc, "attnStepLayers: layer %u: %s", i, err);
         }
-        // packed tables never outgrow one layer's share of the region (each fits a one-entry step's)
+        // packed tables never outgrow one layer's share of the region (each fits a step of E entries)
         const size_t at = blob.size(), bytes = align256(ph.blob.size());
         blob.resize(at + bytes);
         memcpy(blob.data() + at, ph.blob.data(), ph.blob.size());
         memset(blob.data() + at + ph.blob.size(), 0, bytes - ph.blob.size());
-        write_plan(&plans[i], tables, records + (size_t)i * records_one, 1, num_kv_heads, G, head_dim, ph);
+        write_plan(&plans[i], tables, records + (size_t)i * records_one, E, num_kv_heads, G, head_dim, ph);
     }
     rc = stage_upload(ws, blob.data(), blob.size(), as_stream(stream));  // every layer's tables in one copy
     if (rc) {

@@ -163,9 +163,9 @@ SIGNATURES: dict[str, list] = {
     "g4_attn_decode_many": [C.POINTER(DecodeEntry), _U32, _U32, _U32, _U32, _P, _SZ, _P],
     "g4_attn_step_workspace_size": [_U32, _U32, _U32, _U32, C.POINTER(C.c_size_t)],
     "g4_attn_step_prepare": [C.POINTER(StepEntry), _U32, _U32, _U32, _U32, _P, _SZ, C.POINTER(DecodePlan), _P],
-    "g4_attn_step_layers_workspace_size": [_U32, _U32, _U32, _U32, C.POINTER(C.c_size_t)],
-    "g4_attn_step_prepare_layers": [C.POINTER(StepEntry), _U32, _U32, _U32, _U32, _P, _SZ, C.POINTER(DecodePlan),
-                                    _P],
+    "g4_attn_step_layers_workspace_size": [_U32, _U32, _U32, _U32, _U32, C.POINTER(C.c_size_t)],
+    "g4_attn_step_prepare_layers": [C.POINTER(StepEntry), _U32, _U32, _U32, _U32, _U32, _P, _SZ,
+                                    C.POINTER(DecodePlan), _P],
     "g4_rope_inv_freq": [C.c_float, _U32, _U32, _P, _P, _P],
     "g4_rope_inv_freq_host": [C.c_float, _U32, _U32, _P, _P],
     "g4_attn_step_run": [C.POINTER(DecodePlan), _P],

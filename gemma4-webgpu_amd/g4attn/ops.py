@@ -307,17 +307,23 @@ def attn_step_prepare(entries, num_q_heads, num_kv_heads, head_dim, workspace, s
     return plan
 
 
-def step_layers_workspace_bytes(n_layers, num_q_heads, num_kv_heads, head_dim) -> int:
+def step_layers_workspace_bytes(n_layers, num_q_heads, num_kv_heads, head_dim, entries_per_layer=1) -> int:
     n = C.c_size_t(0)
-    abi.call("g4_attn_step_layers_workspace_size", n_layers, num_q_heads, num_kv_heads, head_dim, C.byref(n))
+    abi.call("g4_attn_step_layers_workspace_size", n_layers, entries_per_layer, num_q_heads, num_kv_heads, head_dim,
+             C.byref(n))
     return n.value
 
 
-def attn_step_prepare_layers(layers, num_q_heads, num_kv_heads, head_dim, workspace, stream=None) -> list:
-    """One token's layers prepared together (one upload): a plan per layer, each run on its own in layer
-    order with attn_step_run_attention then attn_step_run_merge or attn_step_run_out."""
-    plans = (DecodePlan * len(layers))()
-    abi.call("g4_attn_step_prepare_layers", layers, len(layers), num_q_heads, num_kv_heads, head_dim,
+def attn_step_prepare_layers(entries, num_q_heads, num_kv_heads, head_dim, workspace, entries_per_layer=1,
+                             stream=None) -> list:
+    """One token's layers prepared together (one upload): layer i is entries[i * entries_per_layer ..
+    (i + 1) * entries_per_layer); a plan per layer, each run on its own in layer order with
+    attn_step_run_attention then attn_step_run_merge or attn_step_run_out."""
+    if entries_per_layer < 1 or len(entries) % entries_per_layer:
+        raise ValueError(f"{len(entries)} entries are not whole layers of {entries_per_layer}")
+    n_layers = len(entries) // entries_per_layer
+    plans = (DecodePlan * n_layers)()
+    abi.call("g4_attn_step_prepare_layers", entries, n_layers, entries_per_layer, num_q_heads, num_kv_heads, head_dim,
              _dev(workspace, "workspace", torch.uint8, 0), workspace.numel(), plans, _stream(stream))
     return list(plans)
 

@@ -242,9 +242,9 @@ export interface Addon {
   attnStepWorkspaceSize(n: number, nqh: number, nkh: number, hd: number): number;
   attnStepPrepare(entries: any[], nqh: number, nkh: number, hd: number, ws: bigint, wsBytes: number,
     s: bigint): Uint8Array;
-  attnStepLayersWorkspaceSize(n: number, nqh: number, nkh: number, hd: number): number;
-  attnStepPrepareLayers(layers: any[], nqh: number, nkh: number, hd: number, ws: bigint, wsBytes: number,
-    s: bigint): Uint8Array[];
+  attnStepLayersWorkspaceSize(n: number, perLayer: number, nqh: number, nkh: number, hd: number): number;
+  attnStepPrepareLayers(entries: any[], perLayer: number, nqh: number, nkh: number, hd: number, ws: bigint,
+    wsBytes: number, s: bigint): Uint8Array[];
   attnStepRun(plan: Uint8Array, s: bigint): void;
   attnStepRunAttention(plan: Uint8Array, s: bigint): void;
   attnStepRunOut(plan: Uint8Array, segs: { weight: bigint; out: bigint; rows: number }[], s: bigint): void;
@@ -361,16 +361,20 @@ export class HipAttention {
       shape.headDim, workspace.ptr, workspace.size, this.stream);
   }
 
-  attnStepLayersWorkspaceSize(nLayers: number, shape: StepShape): number {
-    return this.g4.attnStepLayersWorkspaceSize(nLayers, shape.numQHeads, shape.numKvHeads, shape.headDim);
+  attnStepLayersWorkspaceSize(nLayers: number, shape: StepShape, entriesPerLayer?: number): number {
+    return this.g4.attnStepLayersWorkspaceSize(nLayers, entriesPerLayer || 1, shape.numQHeads, shape.numKvHeads,
+      shape.headDim);
   }
 
   // One token's layers in the engine's order (src/engine.ts:2029-2156), prepared together once per token
-  // (where the engine patches every layer's uniforms, :1967-1987) with one table upload: a plan per layer,
-  // each run on its own, in layer order (attnStepRun, or attnStepRunAttention then attnStepOut).
-  attnStepPrepareLayers(layers: StepEntry[], shape: StepShape, workspace: DeviceBuffer): Uint8Array[] {
-    return this.g4.attnStepPrepareLayers(HipAttention.stepFlat(layers), shape.numQHeads, shape.numKvHeads,
-      shape.headDim, workspace.ptr, workspace.size, this.stream);
+  // (where the engine patches every layer's uniforms, :1967-1987) with one table upload: layer i is
+  // entries[i * entriesPerLayer ..) (one per layer for a single sequence, the active batch for a batched
+  // decode); a plan per layer, each run on its own, in layer order (attnStepRun, or attnStepRunAttention
+  // then attnStepOut).
+  attnStepPrepareLayers(entries: StepEntry[], shape: StepShape, workspace: DeviceBuffer,
+    entriesPerLayer?: number): Uint8Array[] {
+    return this.g4.attnStepPrepareLayers(HipAttention.stepFlat(entries), entriesPerLayer || 1, shape.numQHeads,
+      shape.numKvHeads, shape.headDim, workspace.ptr, workspace.size, this.stream);
   }
 
   private static stepFlat(entries: StepEntry[]): any[] {

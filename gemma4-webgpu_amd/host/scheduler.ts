@@ -5,7 +5,9 @@
 // fixed number of cache slots, and leave when they finish, freeing their slot for the next request.
 // Each layer of a token step is one attnStep launch over every active sequence: a ragged batch, one
 // entry per sequence with its own length (the batched-decode workload of 64 sequences of 1K..32K
-// rows is one such launch).
+// rows is one such launch). beginToken() prepares every layer of the token step at once (one table
+// upload per head_dim group, attnStepPrepareLayers); stepLayer() then runs the layer's plan, or, without
+// it, prepares that layer alone.
 //
 // Memory is taken once, at construction: one pool holds every slot's K and V cache rows of every
 // KV-producer layer (consumer layers read their producer's rows, src/engine.ts:1518-1522), one holds
@@ -163,6 +165,9 @@ export class DecodeScheduler {
   private pool: DeviceBuffer;
   private work: DeviceBuffer;
   private workspace: DeviceBuffer;
+  private readonly groups: { layers: number[]; workspace: DeviceBuffer }[];  // layers per head_dim, in order
+  private tokenPlans: Uint8Array[] | null;     // beginToken's plans, one per layer
+  private tokenIds: string;                    // the active sequences they were prepared for
   private alive: boolean;
 
   constructor(att: HipAttention, cfg: SchedulerConfig) {
@@ -200,12 +205,33 @@ export class DecodeScheduler {
     let ws = 0;
     for (let l = 0; l < nl; l++) ws = Math.max(ws, att.attnStepWorkspaceSize(cfg.maxBatch, this.shapeOf(l)));
     this.workspace = att.createBuffer(ws);
+    // beginToken: a layers workspace per head_dim group, for a full batch
+    const byHd: number[][] = [];
+    for (let l = 0; l < nl; l++) {
+      let list: number[] | null = null;
+      for (const x of byHd) if (this.hdOf(x[0]) === this.hdOf(l)) list = x;
+      if (list) list.push(l);
+      else byHd.push([l]);
+    }
+    this.groups = [];
+    for (const layers of byHd) {
+      const bytes = att.attnStepLayersWorkspaceSize(layers.length, this.shapeOf(layers[0]), cfg.maxBatch);
+      this.groups.push({ layers: layers, workspace: att.createBuffer(bytes) });
+    }
+    this.tokenPlans = null;
+    this.tokenIds = '';
     this.alive = true;
   }
 
   submit(id: string, length: number): void { this.table.submit(id, length); }
-  admit(): string[] { return this.table.admit(); }
-  release(id: string): void { this.table.release(id); }
+  admit(): string[] {
+    this.tokenPlans = null;
+    return this.table.admit();
+  }
+  release(id: string): void {
+    this.tokenPlans = null;
+    this.table.release(id);
+  }
   activeIds(): string[] { return this.table.activeIds(); }
 
   // The sequence's K / V cache of `layer` (its producer's rows on consumer layers): f16 [maxSeqLen][NKH][HD].
@@ -245,16 +271,45 @@ export class DecodeScheduler {
     });
   }
 
+  // Every layer of the token step prepared at once, for the active sequences (the engine patches every
+  // layer's uniforms once per token, src/engine.ts:1967-1987): one attnStepPrepareLayers per head_dim
+  // group, one table upload each. Call after admit/release, before the token's first layer; stepLayer
+  // then runs the prepared plans. Returns the number of sequences prepared.
+  beginToken(): number {
+    this.tokenPlans = null;
+    const ids = this.table.activeIds();
+    if (!ids.length) return 0;
+    const plans: Uint8Array[] = new Array(this.cfg.layers.length);
+    for (const g of this.groups) {
+      const ents: StepEntry[] = [];
+      for (const l of g.layers) for (const e of this.entries(l)) ents.push(e);
+      const ps = this.att.attnStepPrepareLayers(ents, this.shapeOf(g.layers[0]), g.workspace, ids.length);
+      g.layers.forEach(function (l, i) { plans[l] = ps[i]; });
+    }
+    this.tokenPlans = plans;
+    this.tokenIds = ids.join('\n');
+    return ids.length;
+  }
+
   // One layer of the token step for every active sequence: one attention launch (plus the split
-  // merge). Returns the number of sequences stepped.
+  // merge), from beginToken's plan when it was prepared for these sequences, else prepared here.
+  // Returns the number of sequences stepped.
   stepLayer(layer: number): number {
+    const ids = this.table.activeIds();
+    if (this.tokenPlans && this.tokenIds === ids.join('\n')) {
+      this.att.attnStepRun(this.tokenPlans[layer]);
+      return ids.length;
+    }
     const ents = this.entries(layer);
     if (ents.length) this.att.attnStep(ents, this.shapeOf(layer), this.workspace);
     return ents.length;
   }
 
   // After the last layer of a token: every active sequence holds one more row.
-  advance(): void { this.table.advance(); }
+  advance(): void {
+    this.tokenPlans = null;
+    this.table.advance();
+  }
 
   dispose(): void {
     if (!this.alive) return;
@@ -262,6 +317,7 @@ export class DecodeScheduler {
     this.att.destroyBuffer(this.pool);
     this.att.destroyBuffer(this.work);
     this.att.destroyBuffer(this.workspace);
+    for (const g of this.groups) this.att.destroyBuffer(g.workspace);
     this.alive = false;
   }
 

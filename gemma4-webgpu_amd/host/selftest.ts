@@ -491,6 +491,8 @@ function batch(dir: string): string[] {
         if (vc.byteLength) att.writeBuffer(sched.vCache(id, l), 0, vc);
       });
     });
+    // odd steps prepare every layer at once (one upload per head_dim group), even steps layer by layer
+    if (si % 2 === 1 && sched.beginToken() !== sched.activeIds().length) fail('beginToken count');
     spec.layers.forEach(function (_L, l) {
       const ids = sched.activeIds();
       const producer = spec.layers[l].kvSource === l;

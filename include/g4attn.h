@@ -365,21 +365,25 @@ int g4_attn_step(const g4_step_entry* entries, uint32_t n_entries, uint32_t num_
  * layer q/k/v projection, attention block, output projection, each layer's
  * input the previous layer's output), prepared together: the engine patches
  * every layer's position, slot and seq_len uniforms once per token
- * (src/engine.ts:1967-1987) and then runs the layers one by one. layers[i]
- * becomes plans[i], a plan of that layer alone (partitioned as
- * g4_attn_step_prepare would partition a one-entry step, so that each layer
- * fills the GPU when it runs), and every layer's tables go up in one upload;
- * layers at one (inverse-frequency table, position) pair share one set of RoPE
- * factors. Each plan is run with g4_attn_step_run_attention followed by
- * g4_attn_step_run_merge or g4_attn_step_run_out, in layer order, as often as
- * wanted until the next prepare into the same workspace; the layers'
- * partial records are separate. One head_dim per call (E2B: one call per
- * head_dim group). Workspace: g4_attn_step_layers_workspace_size. */
-int g4_attn_step_layers_workspace_size(uint32_t n_layers, uint32_t num_q_heads, uint32_t num_kv_heads,
-                                       uint32_t head_dim, size_t* bytes);
-int g4_attn_step_prepare_layers(const g4_step_entry* layers, uint32_t n_layers, uint32_t num_q_heads,
-                                uint32_t num_kv_heads, uint32_t head_dim, void* workspace, size_t workspace_bytes,
-                                g4_decode_plan* plans, void* stream);
+ * (src/engine.ts:1967-1987) and then runs the layers one by one. Layer i is
+ * entries[i * entries_per_layer .. (i + 1) * entries_per_layer) (one entry
+ * per layer for the engine's single sequence; a batch of sequences per layer
+ * for a batched decode) and becomes plans[i], a plan of that layer alone
+ * (partitioned as g4_attn_step_prepare would partition it, so that each layer
+ * fills the GPU when it runs); every layer's tables go up in one upload, and
+ * layers at one (inverse-frequency table, position) pair share one set of
+ * RoPE factors. Each plan is run with g4_attn_step_run_attention followed by
+ * g4_attn_step_run_merge or g4_attn_step_run_out (or g4_attn_step_run), in
+ * layer order, as often as wanted until the next prepare into the same
+ * workspace; the layers' partial records are separate. One head_dim per call
+ * (E2B: one call per head_dim group). A failed call leaves every plan
+ * unprepared. Workspace: g4_attn_step_layers_workspace_size (enough for any
+ * smaller entries_per_layer too). */
+int g4_attn_step_layers_workspace_size(uint32_t n_layers, uint32_t entries_per_layer, uint32_t num_q_heads,
+                                       uint32_t num_kv_heads, uint32_t head_dim, size_t* bytes);
+int g4_attn_step_prepare_layers(const g4_step_entry* entries, uint32_t n_layers, uint32_t entries_per_layer,
+                                uint32_t num_q_heads, uint32_t num_kv_heads, uint32_t head_dim, void* workspace,
+                                size_t workspace_bytes, g4_decode_plan* plans, void* stream);
 
 /* ---- causal prefill on MFMA ---------------------------------------------
  * The reference runs a prompt as one decode step per token (src/engine.ts:

@@ -138,9 +138,50 @@ def test_layers_workspace_and_errors(dev):
     ws = torch.empty(need, dtype=torch.uint8, device=dev)
     plans = (abi.DecodePlan * 2)()
     with pytest.raises(RuntimeError, match="layer 1: attnStep: entry 0 seq_len 0"):
-        abi.call("g4_attn_step_prepare_layers", bad, 2, 8, 1, 256, ws.data_ptr(), ws.numel(), plans, None)
+        abi.call("g4_attn_step_prepare_layers", bad, 2, 1, 8, 1, 256, ws.data_ptr(), ws.numel(), plans, None)
     for i in range(2):  # no plan of a failed call runs: layer 0's tables were never uploaded
         with pytest.raises(RuntimeError, match="not prepared"):
             ops.attn_step_run_attention(plans[i])
     torch.cuda.synchronize()
+    del tabs
+
+
+def test_batched_layers_match_batches_prepared_alone(dev):
+    """Three layers of a batched decode (three sequences of different lengths per layer, as the TS host's
+    scheduler steps them), prepared together with entries_per_layer 3: every layer's attnOut and stored rows
+    bit-identical to that layer's three entries prepared alone, and within max-abs 2e-3 of the oracle."""
+    announce("attnStepLayers 3 layers x 3 sequences")
+    lens = [(700, 300, 2500), (700, 300, 2500), (700, 300, 2500)]
+    kinds = [(512, 1e4, 0), (0, 1e6, 1), (512, 1e4, 0)]
+    tabs = host_tables(256)
+    layers, entries = [], []
+    for li, ((win, theta, div), seqs) in enumerate(zip(kinds, lens)):
+        for si, seq in enumerate(seqs):
+            L = Layer(dev, 8300 + 37 * li + si, seq, win, theta, div)
+            e = L.entry()
+            e["rope_inv_freq_host"] = tabs[(theta, div)]
+            layers.append(L)
+            entries.append(e)
+    ref = []
+    for li in range(3):  # each layer's batch prepared alone
+        arr = ops.make_step_entries(entries[3 * li:3 * li + 3], 8, 1, 256)
+        ws1 = torch.empty(ops.step_workspace_bytes(3, 8, 1, 256), dtype=torch.uint8, device=dev)
+        ops.attn_step_run(ops.attn_step_prepare(arr, 8, 1, 256, ws1))
+        torch.cuda.synchronize()
+        ref += [bits(L.out) for L in layers[3 * li:3 * li + 3]]
+    arr = ops.make_step_entries(entries, 8, 1, 256)
+    ws = torch.empty(ops.step_layers_workspace_bytes(3, 8, 1, 256, entries_per_layer=3), dtype=torch.uint8,
+                     device=dev)
+    plans = ops.attn_step_prepare_layers(arr, 8, 1, 256, ws, entries_per_layer=3)
+    assert len(plans) == 3
+    for L in layers:
+        L.out.fill_(float("nan"))
+    for plan in plans:
+        ops.attn_step_run(plan)
+    torch.cuda.synchronize()
+    for i, L in enumerate(layers):
+        np.testing.assert_array_equal(bits(L.out), ref[i], err_msg=f"entry {i}")
+        want, kb, vb = L.expected()
+        assert float(np.abs(L.out.cpu().numpy() - want).max()) <= TOL, f"entry {i} vs the oracle"
+        np.testing.assert_array_equal(L.kc[L.pos].cpu().numpy().view(np.uint16), kb, err_msg=f"entry {i} K")
     del tabs
