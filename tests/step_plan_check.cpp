@@ -49,59 +49,63 @@ static long rope_sweep(uint32_t stride) {
     return n;
 }
 
-// A token's layers planned one by one into one packed upload (g4_attn_step_prepare_layers): each
-// layer's plan equals the one-entry plan of that layer except for its RoPE factors, which are its
-// own set at the first (table, position) pair of the upload and the first layer's set after that,
+// A token's layers planned one by one into one packed upload (g4_attn_step_prepare_layers with E entries
+// per layer): each layer's plan equals the plan of its E entries alone except for the RoPE factors, which
+// are its own set at the first (table, position) pair of the upload and the earlier layer's set after that,
 // with the C library's values; the packed tables fit the layers' tables regions.
-static int check_layers(int line, const std::vector<g4_step_entry>& ents, uint32_t nqh, uint32_t nkh, uint32_t hd,
-                        uint32_t cus, char* dev) {
-    const uint32_t n = (uint32_t)ents.size();
-    const StepLayout L1 = step_layout(1, nkh, nqh / nkh, hd);
+static int check_layers(int line, const std::vector<g4_step_entry>& ents, uint32_t E, uint32_t nqh, uint32_t nkh,
+                        uint32_t hd, uint32_t cus, char* dev) {
+    const uint32_t n = (uint32_t)ents.size() / E;
+    const StepLayout L1 = step_layout(E, nkh, nqh / nkh, hd);
     StepPlanHost ph, one;
     StepRopeShare share;
     std::vector<char> packed;
     char err[256] = "";
     for (uint32_t i = 0; i < n; i++) {
         char* tables = dev + packed.size();
-        if (plan_step(&ents[i], 1, nqh, nkh, hd, cus, StepTuning{}, tables, &ph, err, sizeof err, &share) ||
-            plan_step(&ents[i], 1, nqh, nkh, hd, cus, StepTuning{}, tables, &one, err, sizeof err))
+        const g4_step_entry* le = &ents[(size_t)i * E];
+        if (plan_step(le, E, nqh, nkh, hd, cus, StepTuning{}, tables, &ph, err, sizeof err, &share) ||
+            plan_step(le, E, nqh, nkh, hd, cus, StepTuning{}, tables, &one, err, sizeof err))
             return bad(line, "layer plan failed");
         if (ph.n_wgs != one.n_wgs || ph.off_rope != one.off_rope || ph.waves != one.waves ||
             ph.max_parts != one.max_parts || ph.blob.size() > one.blob.size())
-            return bad(line, "layer plan differs from the one-entry plan");
+            return bad(line, "layer plan differs from the plan of its entries alone");
         const StepWorkDev* w = reinterpret_cast<const StepWorkDev*>(ph.blob.data());
         const StepWorkDev* w1 = reinterpret_cast<const StepWorkDev*>(one.blob.data());
         for (uint32_t k = 0; k < ph.n_wgs; k++) {
             StepWorkDev a = w[k], b = w1[k];
             a.ent.rope_cs = b.ent.rope_cs = nullptr;
-            if (memcmp(&a, &b, sizeof a)) return bad(line, "layer work item differs from the one-entry plan");
+            if (memcmp(&a, &b, sizeof a)) return bad(line, "layer work item differs from the plan of its entries");
         }
         if (memcmp(ph.blob.data() + ph.n_wgs * sizeof(StepWorkDev), one.blob.data() + ph.n_wgs * sizeof(StepWorkDev),
                    ph.off_rope - ph.n_wgs * sizeof(StepWorkDev)))
-            return bad(line, "layer merge or entry table differs from the one-entry plan");
+            return bad(line, "layer merge or entry table differs from the plan of its entries");
         const size_t at = packed.size();
         packed.resize(at + align256(ph.blob.size()), 0);
         memcpy(packed.data() + at, ph.blob.data(), ph.blob.size());
         if (packed.size() > (size_t)(i + 1) * L1.part_ml) return bad(line, "packed tables exceed the layers' regions");
-        const g4_step_entry& e = ents[i];
-        const float* rc = w[0].ent.rope_cs;
-        if (!e.rope_inv_freq_host) {
-            if (rc) return bad(line, "layer RoPE factors without a host table");
-            continue;
-        }
-        const char* rp = reinterpret_cast<const char*>(rc);
-        if (rp < dev || rp + hd * 4 > dev + packed.size() || (size_t)(rp - dev) % 4)
-            return bad(line, "layer RoPE pointer outside the packed tables");
-        for (uint32_t j = 0; j < i; j++)  // the first earlier layer at the same pair owns the set
-            if (ents[j].rope_inv_freq_host == e.rope_inv_freq_host && ents[j].position == e.position) {
-                if (rp >= tables) return bad(line, "layer carries a RoPE set an earlier layer placed");
-                break;
+        for (uint32_t k = 0; k < ph.n_wgs; k++) {
+            const uint32_t ei = (uint32_t)i * E + w[k].entry;  // the entry in the whole list
+            const g4_step_entry& e = ents[ei];
+            const float* rc = w[k].ent.rope_cs;
+            if (!e.rope_inv_freq_host) {
+                if (rc) return bad(line, "layer RoPE factors without a host table");
+                continue;
             }
-        const float* f = reinterpret_cast<const float*>(packed.data() + (rp - dev));
-        for (uint32_t p = 0; p < hd / 2; p++) {
-            const double a = (double)((float)e.position * e.rope_inv_freq_host[p]);
-            if (f[p] != (float)cos(a) || f[hd / 2 + p] != (float)sin(a))
-                return bad(line, "layer RoPE factors differ from the C library's cos and sin");
+            const char* rp = reinterpret_cast<const char*>(rc);
+            if (rp < dev || rp + hd * 4 > dev + packed.size() || (size_t)(rp - dev) % 4)
+                return bad(line, "layer RoPE pointer outside the packed tables");
+            for (uint32_t j = 0; j < (uint32_t)i * E; j++)  // an earlier layer at the same pair owns the set
+                if (ents[j].rope_inv_freq_host == e.rope_inv_freq_host && ents[j].position == e.position) {
+                    if (rp >= tables) return bad(line, "layer carries a RoPE set an earlier layer placed");
+                    break;
+                }
+            const float* f = reinterpret_cast<const float*>(packed.data() + (rp - dev));
+            for (uint32_t p = 0; p < hd / 2; p++) {
+                const double a = (double)((float)e.position * e.rope_inv_freq_host[p]);
+                if (f[p] != (float)cos(a) || f[hd / 2 + p] != (float)sin(a))
+                    return bad(line, "layer RoPE factors differ from the C library's cos and sin");
+            }
         }
     }
     return 0;
@@ -244,7 +248,8 @@ int main(int argc, char** argv) {
             }
         }
         if (n_split != ph.n_merge) return bad(line, "merge table lists entries that are not split");
-        if (check_layers(line, ents, nqh, nkh, hd, cus, dev)) return 1;
+        if (check_layers(line, ents, 1, nqh, nkh, hd, cus, dev)) return 1;
+        if (n % 2 == 0 && check_layers(line, ents, 2, nqh, nkh, hd, cus, dev)) return 1;
         printf("ok %u %u\n", ph.n_wgs, ph.n_merge);
     }
     return 0;

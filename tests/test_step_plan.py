@@ -6,7 +6,8 @@ and in order by its workgroups, partial-record slots unique and inside the works
 listing exactly the split entries, RoPE-factor pointers inside the uploaded factors with the C library's
 values, and the packed tables inside the workspace's tables region. Every scenario is also planned layer by
 layer as g4_attn_step_prepare_layers does (one packed upload, RoPE sets shared between layers at one
-position): each layer's plan must equal its one-entry plan apart from the RoPE pointer.
+position), with one entry per layer and, for an even count, two: each layer's plan must equal the plan
+of its entries alone apart from the RoPE pointers.
 """
 import shutil
 import subprocess
