@@ -194,3 +194,37 @@ def test_step_cached_row_entries_checked_on_host():
         e.seq_len, e.position, e.theta, e.scale, e.eps = 10, 9, 1e4, 1.0, 1e-6
         st, msg = _err(lambda L: L.g4_attn_step_prepare(C.byref(e), 1, 8, 1, 256, 256, n.value, C.byref(plan), None))
         assert st == abi.G4_EINVAL and want in msg, (k, v, kw, store, msg)
+
+
+def test_layers_prepare_and_prompt_prep_checked_on_host():
+    """g4_attn_step_prepare_layers and g4_attn_prompt_prep refuse bad arguments before any upload or launch:
+    layer and entry counts, a bad entry in a later layer (reported with the layer, and no plan of the call
+    left usable), a divisor with neither rope_freqs nor the inverse-frequency table."""
+    lib = abi.load()
+    n = C.c_size_t(0)
+    st, msg = _err(lambda L: L.g4_attn_step_layers_workspace_size(0, 1, 8, 1, 256, C.byref(n)))
+    assert st == abi.G4_EINVAL and "layers" in msg
+    st, msg = _err(lambda L: L.g4_attn_step_layers_workspace_size(3, 0, 8, 1, 256, C.byref(n)))
+    assert st == abi.G4_EINVAL and "entries per layer" in msg
+    assert lib.g4_attn_step_layers_workspace_size(2, 3, 8, 1, 256, C.byref(n)) == abi.G4_OK
+    one = C.c_size_t(0)
+    assert lib.g4_attn_step_workspace_size(3, 8, 1, 256, C.byref(one)) == abi.G4_OK
+    assert n.value == 2 * one.value
+    ents = (abi.StepEntry * 2)()
+    for i, e in enumerate(ents):
+        e.q = e.k = e.v = e.q_weight = e.k_weight = e.k_cache = e.v_cache = 256
+        e.out = 260 if i == 1 else 256  # layer 1's attnOut misaligned
+        e.store_kv, e.seq_len, e.position, e.theta, e.scale, e.eps = 1, 10, 9, 1e4, 1.0, 1e-6
+    plans = (abi.DecodePlan * 2)()
+    assert lib.g4_attn_step_layers_workspace_size(2, 1, 8, 1, 256, C.byref(n)) == abi.G4_OK
+    st, msg = _err(lambda L: L.g4_attn_step_prepare_layers(ents, 2, 1, 8, 1, 256, 256, n.value, plans, None))
+    assert st == abi.G4_EINVAL and "layer 1" in msg and "16-byte aligned" in msg
+    for p in plans:
+        st, msg = _err(lambda L: L.g4_attn_step_run_attention(C.byref(p), None))
+        assert st == abi.G4_EINVAL and "not prepared" in msg
+    pp = abi.PromptPrepParams(8, 1, 128, 4, 0, 1e-6, 1e4, 0, 0, 0)
+    st, msg = _err(lambda L: L.g4_attn_prompt_prep(1, None, None, 1, None, None, None, 1, None, None, pp, None))
+    assert st == abi.G4_EINVAL and "head_dim 128" in msg
+    pp = abi.PromptPrepParams(8, 1, 256, 4, 0, 1e-6, 1e6, 1, 0, 0)
+    st, msg = _err(lambda L: L.g4_attn_prompt_prep(1, None, None, 1, None, None, None, 1, None, None, pp, None))
+    assert st == abi.G4_EINVAL and "rope_freqs" in msg
