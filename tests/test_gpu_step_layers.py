@@ -185,3 +185,54 @@ def test_batched_layers_match_batches_prepared_alone(dev):
         assert float(np.abs(L.out.cpu().numpy() - want).max()) <= TOL, f"entry {i} vs the oracle"
         np.testing.assert_array_equal(L.kc[L.pos].cpu().numpy().view(np.uint16), kb, err_msg=f"entry {i} K")
     del tabs
+
+
+def test_e2b_order_two_head_dim_groups(dev):
+    """A token in E2B's layer order with both head_dim groups: the local layers (head_dim 256) prepared
+    together and the global layers (head_dim 512) prepared together, each group in its own workspace,
+    then every layer run in layer order; every attnOut and o_proj row bit-identical to the layer
+    prepared alone."""
+    announce("attnStepLayers E2B order, head_dim 256 and 512 groups")
+    specs = [(700, 512, 1e4, 0, 256), (700, 512, 1e4, 0, 256), (2100, 0, 1e6, 1, 512), (700, 512, 1e4, 0, 256),
+             (700, 512, 1e4, 0, 256), (2100, 0, 1e6, 1, 512), (700, 512, 1e4, 0, 256)]
+    tabs = {256: host_tables(256), 512: host_tables(512)}
+    layers, entries = [], []
+    for i, (seq, win, theta, div, hd) in enumerate(specs):
+        L = Layer(dev, 9700 + 29 * i, seq, win, theta, div, hd=hd)
+        e = L.entry()
+        e["rope_inv_freq_host"] = tabs[hd][(theta, div)]
+        layers.append(L)
+        entries.append(e)
+    rows = H
+    wo = [t_u16(weights(800 + i, rows, 8 * s[4], 0.02), dev) for i, s in enumerate(specs)]
+    ref_out, ref_y = [], []
+    for L, e, w, s in zip(layers, entries, wo, specs):  # each layer prepared alone, in layer order
+        hd = s[4]
+        ws1 = torch.empty(ops.step_workspace_bytes(1, 8, 1, hd), dtype=torch.uint8, device=dev)
+        plan = ops.attn_step_prepare(ops.make_step_entries([e], 8, 1, hd), 8, 1, hd, ws1)
+        ops.attn_step_run_attention(plan)
+        y = torch.empty(rows, device=dev)
+        ops.attn_step_run_out(plan, 8 * hd, [(w, y, rows)])
+        torch.cuda.synchronize()
+        ref_out.append(bits(L.out))
+        ref_y.append(bits(y))
+    plans = [None] * len(specs)
+    keep = []
+    for hd in (256, 512):  # one prepare per head_dim group
+        idx = [i for i, s in enumerate(specs) if s[4] == hd]
+        arr = ops.make_step_entries([entries[i] for i in idx], 8, 1, hd)
+        ws = torch.empty(ops.step_layers_workspace_bytes(len(idx), 8, 1, hd), dtype=torch.uint8, device=dev)
+        keep.append(ws)
+        for i, p in zip(idx, ops.attn_step_prepare_layers(arr, 8, 1, hd, ws)):
+            plans[i] = p
+    for L in layers:
+        L.out.fill_(float("nan"))
+    ys = [torch.full((rows,), float("nan"), device=dev) for _ in specs]
+    for i, s in enumerate(specs):  # layer order across the groups
+        ops.attn_step_run_attention(plans[i])
+        ops.attn_step_run_out(plans[i], 8 * s[4], [(wo[i], ys[i], rows)])
+    torch.cuda.synchronize()
+    for i, L in enumerate(layers):
+        np.testing.assert_array_equal(bits(L.out), ref_out[i], err_msg=f"attnOut layer {i}")
+        np.testing.assert_array_equal(bits(ys[i]), ref_y[i], err_msg=f"o_proj layer {i}")
+    del tabs, keep
