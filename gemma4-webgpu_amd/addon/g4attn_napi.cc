@@ -317,6 +317,134 @@ napi_value ReadAsync(napi_env env, napi_callback_info info) {
     return promise;
 }
 
+// ---- timestamp queries (the engine's GPUQuerySet, src/engine.ts:3089-3110, 3208-3227, 3253-3288) ----
+
+napi_value QuerySetCreate(napi_env env, napi_callback_info info) {
+    Args a(env, info, 1);
+    const uint32_t count = a.u32(0);
+    if (!a.ok) return nullptr;
+    g4_query_set* q = nullptr;
+    CALL(env, g4_query_set_create(count, &q));
+    return bigint(env, q);
+}
+
+// A pass's begin and end (beginPass .. pass.end()): the kernels launched from this thread in between
+// carry the pair (slot, slot + 1).
+napi_value QueryBeginPass(napi_env env, napi_callback_info info) {
+    Args a(env, info, 2);
+    void* q = a.ptr(0);
+    const uint32_t slot = a.u32(1);
+    if (!a.ok) return nullptr;
+    CALL(env, g4_query_begin_pass(static_cast<g4_query_set*>(q), slot));
+    return undefined(env);
+}
+
+napi_value QueryEndPass(napi_env env, napi_callback_info) {
+    CALL(env, g4_query_end_pass());
+    return undefined(env);
+}
+
+napi_value QueryWrite(napi_env env, napi_callback_info info) {
+    Args a(env, info, 3);
+    void* q = a.ptr(0);
+    const uint32_t slot = a.u32(1);
+    void* s = a.ptr(2);
+    if (!a.ok) return nullptr;
+    CALL(env, g4_query_write(static_cast<g4_query_set*>(q), slot, s));
+    return undefined(env);
+}
+
+napi_value float64_array(napi_env env, const std::vector<double>& x) {
+    void* data = nullptr;
+    napi_value ab, arr;
+    NAPI_OK(env, napi_create_arraybuffer(env, x.size() * sizeof(double), &data, &ab));
+    if (!x.empty()) memcpy(data, x.data(), x.size() * sizeof(double));
+    NAPI_OK(env, napi_create_typedarray(env, napi_float64_array, x.size(), ab, 0, &arr));
+    return arr;
+}
+
+// resolveQuerySet + mapAsync as one blocking call: Float64Array of each pair's ns (NaN: not written).
+napi_value QueryResolve(napi_env env, napi_callback_info info) {
+    Args a(env, info, 3);
+    void* q = a.ptr(0);
+    const uint32_t first = a.u32(1), n = a.u32(2);
+    if (!a.ok) return nullptr;
+    std::vector<double> ns(n ? n : 1);
+    CALL(env, g4_query_resolve(static_cast<g4_query_set*>(q), first, n, ns.data()));
+    ns.resize(n);
+    return float64_array(env, ns);
+}
+
+struct QueryWork {
+    napi_async_work work = nullptr;
+    napi_deferred deferred = nullptr;
+    g4_query_set* set = nullptr;
+    uint32_t first = 0, n = 0;
+    std::vector<double> ns;
+    int status = G4_OK;
+    std::string msg;
+};
+
+void query_execute(napi_env, void* data) {
+    QueryWork* w = static_cast<QueryWork*>(data);
+    w->status = g4_query_resolve(w->set, w->first, w->n, w->ns.data());
+    if (w->status != G4_OK) w->msg = g4_last_error();
+}
+
+void query_complete(napi_env env, napi_status st, void* data) {
+    QueryWork* w = static_cast<QueryWork*>(data);
+    if (st == napi_ok && w->status == G4_OK) {
+        napi_value arr = float64_array(env, w->ns);
+        if (arr) napi_resolve_deferred(env, w->deferred, arr);
+    } else {
+        if (st != napi_ok && w->status == G4_OK) w->msg = "queryResolveAsync: cancelled";
+        const std::string text = "g4attn status " + std::to_string(w->status) + ": " + w->msg;
+        napi_value m, err;
+        napi_create_string_utf8(env, text.c_str(), NAPI_AUTO_LENGTH, &m);
+        napi_create_error(env, nullptr, m, &err);
+        napi_reject_deferred(env, w->deferred, err);
+    }
+    napi_delete_async_work(env, w->work);
+    delete w;
+}
+
+// The same, waited for off the JS thread (mapAsync's promise). The set must stay alive, and its slots
+// unwritten, until the promise settles.
+napi_value QueryResolveAsync(napi_env env, napi_callback_info info) {
+    Args a(env, info, 3);
+    void* q = a.ptr(0);
+    const uint32_t first = a.u32(1), n = a.u32(2);
+    if (!a.ok) return nullptr;
+    if (!q || n == 0) {
+        napi_throw_range_error(env, nullptr, "queryResolveAsync: no set, or no slots");
+        return nullptr;
+    }
+    QueryWork* w = new QueryWork;
+    w->set = static_cast<g4_query_set*>(q);
+    w->first = first;
+    w->n = n;
+    w->ns.assign(n, 0.0);
+    napi_value promise, name;
+    if (napi_create_promise(env, &w->deferred, &promise) != napi_ok ||
+        napi_create_string_utf8(env, "g4attn.queryResolveAsync", NAPI_AUTO_LENGTH, &name) != napi_ok ||
+        napi_create_async_work(env, nullptr, name, query_execute, query_complete, w, &w->work) != napi_ok ||
+        napi_queue_async_work(env, w->work) != napi_ok) {
+        if (w->work) napi_delete_async_work(env, w->work);
+        delete w;
+        napi_throw_error(env, nullptr, "queryResolveAsync: could not queue the wait");
+        return nullptr;
+    }
+    return promise;
+}
+
+napi_value QuerySetDestroy(napi_env env, napi_callback_info info) {
+    Args a(env, info, 1);
+    void* q = a.ptr(0);
+    if (!a.ok) return nullptr;
+    CALL(env, g4_query_set_destroy(static_cast<g4_query_set*>(q)));
+    return undefined(env);
+}
+
 napi_value Zero(napi_env env, napi_callback_info info) {
     Args a(env, info, 3);
     void* p = a.ptr(0);
@@ -1073,6 +1201,13 @@ napi_value Init(napi_env env, napi_value exports) {
         {"upload", Upload},
         {"download", Download},
         {"readAsync", ReadAsync},
+        {"querySetCreate", QuerySetCreate},
+        {"queryBeginPass", QueryBeginPass},
+        {"queryEndPass", QueryEndPass},
+        {"queryWrite", QueryWrite},
+        {"queryResolve", QueryResolve},
+        {"queryResolveAsync", QueryResolveAsync},
+        {"querySetDestroy", QuerySetDestroy},
         {"zero", Zero},
         {"fusedPerHeadNormRope", FusedPerHeadNormRope},
         {"perHeadRmsNormNoWeight", PerHeadRmsNormNoWeight},

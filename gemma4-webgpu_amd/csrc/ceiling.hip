@@ -48,7 +48,7 @@ int g4_read_ceiling(const void* buf, size_t bytes, uint32_t* sink, void* stream,
         hipExtLaunchKernelGGL(k_read_ceiling, grid, block, 0, st, static_cast<hipEvent_t>(start_event),
                               static_cast<hipEvent_t>(stop_event), 0, src, (uint64_t)(bytes / 16), sink);
     else
-        hipLaunchKernelGGL(k_read_ceiling, grid, block, 0, st, src, (uint64_t)(bytes / 16), sink);
+        G4_LAUNCH(k_read_ceiling, grid, block, 0, st, src, (uint64_t)(bytes / 16), sink);
     G4_CHECK_LAUNCH("readCeiling");
     return G4_OK;
 }

@@ -3,6 +3,7 @@
 // CDNA4 wave64; nothing here is portable to other targets by design.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -32,6 +33,23 @@ int hip_fail(hipError_t e, const char* what);
     } while (0)
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Per-pass timing: while the calling thread has a pass open
+// (g4_query_begin_pass), every kernel the library launches takes the pass's
+// events on its own dispatch (the first kernel the begin event, at its start;
+// each kernel the end event, at its end, so the last one's end stands), so no
+// marker packet sits between kernels. pass_events returns false when no pass
+// is open.
+bool pass_events(hipEvent_t* start, hipEvent_t* stop);
+
+#define G4_LAUNCH(K, GRID, BLOCK, SHM, ST, ...)                                         \
+    do {                                                                                \
+        hipEvent_t g4_ps_ = nullptr, g4_pe_ = nullptr;                                  \
+        if (::g4::pass_events(&g4_ps_, &g4_pe_))                                        \
+            hipExtLaunchKernelGGL(K, GRID, BLOCK, SHM, ST, g4_ps_, g4_pe_, 0, __VA_ARGS__); \
+        else                                                                            \
+            hipLaunchKernelGGL(K, GRID, BLOCK, SHM, ST, __VA_ARGS__);                   \
+    } while (0)
 
 // Host -> device upload of a prepared table, ordered on `st`, through pinned
 // staging memory from a per-thread ring of slots, copied by a kernel on `st`

@@ -307,19 +307,19 @@ int launch_decode_merge_hd(const DecodeArgs& a, unsigned n_entries, unsigned max
         if (a.group == 8) {
             constexpr int C = HD * 8 / 256;
             if (max_splits <= 2)
-                hipLaunchKernelGGL((k_decode_merge_small<HD, C, 2>), grid, block, 0, st, MERGE_KARGS);
+                G4_LAUNCH((k_decode_merge_small<HD, C, 2>), grid, block, 0, st, MERGE_KARGS);
             else if (max_splits <= 4)
-                hipLaunchKernelGGL((k_decode_merge_small<HD, C, 4>), grid, block, 0, st, MERGE_KARGS);
+                G4_LAUNCH((k_decode_merge_small<HD, C, 4>), grid, block, 0, st, MERGE_KARGS);
             else
-                hipLaunchKernelGGL((k_decode_merge_small<HD, C, 8>), grid, block, 0, st, MERGE_KARGS);
+                G4_LAUNCH((k_decode_merge_small<HD, C, 8>), grid, block, 0, st, MERGE_KARGS);
         } else {
             constexpr int C = HD * 4 / 256;
             if (max_splits <= 2)
-                hipLaunchKernelGGL((k_decode_merge_small<HD, C, 2>), grid, block, 0, st, MERGE_KARGS);
+                G4_LAUNCH((k_decode_merge_small<HD, C, 2>), grid, block, 0, st, MERGE_KARGS);
             else if (max_splits <= 4)
-                hipLaunchKernelGGL((k_decode_merge_small<HD, C, 4>), grid, block, 0, st, MERGE_KARGS);
+                G4_LAUNCH((k_decode_merge_small<HD, C, 4>), grid, block, 0, st, MERGE_KARGS);
             else
-                hipLaunchKernelGGL((k_decode_merge_small<HD, C, 8>), grid, block, 0, st, MERGE_KARGS);
+                G4_LAUNCH((k_decode_merge_small<HD, C, 8>), grid, block, 0, st, MERGE_KARGS);
         }
         G4_CHECK_LAUNCH("attnDecode merge");
         return G4_OK;
@@ -330,7 +330,7 @@ int launch_decode_merge_hd(const DecodeArgs& a, unsigned n_entries, unsigned max
     constexpr unsigned kRecsPerChunk = kMergeBatch * 4 * kMergeThreads / HD;
     unsigned chunks = 1;
     while (chunks < kMaxMergeChunks && max_splits > kRecsPerChunk * chunks) chunks *= 2;
-    hipLaunchKernelGGL(k_decode_merge<HD>, dim3(n_entries, a.num_kv_heads * a.group, chunks), dim3(kMergeThreads), 0,
+    G4_LAUNCH(k_decode_merge<HD>, dim3(n_entries, a.num_kv_heads * a.group, chunks), dim3(kMergeThreads), 0,
                        st, MERGE_KARGS, chunks);
     G4_CHECK_LAUNCH("attnDecode merge");
     return G4_OK;
@@ -460,7 +460,7 @@ int run_step_out(StepOutArgs& a, unsigned n_entries, hipStream_t st) {
     if (rpw < 2) rpw = 2;
     a.rows_per_wave = (uint32_t)rpw;
     const uint64_t wave_count = (max_rows + rpw - 1) / rpw;
-    hipLaunchKernelGGL(kernel, dim3((unsigned)((wave_count + 3) / 4), n_entries), dim3(256), 0, st, a);
+    G4_LAUNCH(kernel, dim3((unsigned)((wave_count + 3) / 4), n_entries), dim3(256), 0, st, a);
     G4_CHECK_LAUNCH("attnStepOut");
     return G4_OK;
 }
@@ -599,9 +599,9 @@ void attended_range(uint32_t seq_len, uint32_t window, uint32_t* begin, uint32_t
 
 int launch_split(const DecodeArgs& a, unsigned total_splits, unsigned head_dim, hipStream_t st) {
     if (head_dim == 512)
-        hipLaunchKernelGGL(k_decode_split<512>, dim3(total_splits, a.num_kv_heads), dim3(kDecodeThreads), 0, st, a);
+        G4_LAUNCH(k_decode_split<512>, dim3(total_splits, a.num_kv_heads), dim3(kDecodeThreads), 0, st, a);
     else
-        hipLaunchKernelGGL(k_decode_split<256>, dim3(total_splits, a.num_kv_heads), dim3(kDecodeThreads), 0, st, a);
+        G4_LAUNCH(k_decode_split<256>, dim3(total_splits, a.num_kv_heads), dim3(kDecodeThreads), 0, st, a);
     G4_CHECK_LAUNCH("attnDecode split");
     return G4_OK;
 }

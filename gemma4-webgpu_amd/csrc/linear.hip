@@ -96,7 +96,7 @@ int launch_linear(LinearArgs& a, hipStream_t st) {
     if (rpw < 2) rpw = 2;
     a.rows_per_wave = rpw;
     const unsigned n_waves = (a.total_rows + rpw - 1) / rpw;
-    hipLaunchKernelGGL((k_linear<FMT, NJ>), dim3((n_waves + 3) / 4), dim3(256), 0, st, a);
+    G4_LAUNCH((k_linear<FMT, NJ>), dim3((n_waves + 3) / 4), dim3(256), 0, st, a);
     G4_CHECK_LAUNCH("linear");
     return G4_OK;
 }

@@ -244,7 +244,7 @@ void launch_lm_head(unsigned& wgs, hipStream_t st, hipEvent_t start, hipEvent_t 
         hipExtLaunchKernelGGL(k_lm_head<NJ>, dim3(wgs), dim3(kLmWaves * 64), 0, st, start, stop, 0, x, w, logits, best,
                               vocab, cap);
     else
-        hipLaunchKernelGGL(k_lm_head<NJ>, dim3(wgs), dim3(kLmWaves * 64), 0, st, x, w, logits, best, vocab, cap);
+        G4_LAUNCH(k_lm_head<NJ>, dim3(wgs), dim3(kLmWaves * 64), 0, st, x, w, logits, best, vocab, cap);
 }
 
 }  // namespace g4
@@ -293,7 +293,7 @@ int lm_head_run(const float* hidden, const uint16_t* weight, float* logits, uint
         default: launch_lm_head<10>(wgs, st, start, stop, hidden, weight, logits, best, p.vocab, p.cap); break;
     }
     G4_CHECK_LAUNCH("lmHead");
-    hipLaunchKernelGGL(k_lm_head_pick, dim3(1), dim3(256), 0, st, best, wgs, result);
+    G4_LAUNCH(k_lm_head_pick, dim3(1), dim3(256), 0, st, best, wgs, result);
     G4_CHECK_LAUNCH("lmHead pick");
     return G4_OK;
 }
@@ -316,7 +316,7 @@ static dim3 matmul_grid(uint32_t M) {
 int g4_matmul_quant_f16(const float* input, const uint16_t* weight, float* output, g4_matmul_params p, void* stream) {
     if (!input || !weight || !output) return fail(G4_EINVAL, "matmulQuant: NULL pointer");
     if (p.M == 0) return G4_OK;
-    hipLaunchKernelGGL(k_matmul_quant_f16, matmul_grid(p.M), dim3(kWG), 0, as_stream(stream), input, weight, output, p);
+    G4_LAUNCH(k_matmul_quant_f16, matmul_grid(p.M), dim3(kWG), 0, as_stream(stream), input, weight, output, p);
     G4_CHECK_LAUNCH("matmulQuant");
     return G4_OK;
 }
@@ -326,7 +326,7 @@ int g4_matmul_q8(const float* input, const int8_t* qweight, const uint16_t* qsca
     if (!input || !qweight || !qscale || !output) return fail(G4_EINVAL, "matmulQ8: NULL pointer");
     if (p.N % 32) return fail(G4_EINVAL, "matmulQ8: N %u is not a multiple of 32", p.N);
     if (p.M == 0) return G4_OK;
-    hipLaunchKernelGGL(k_matmul_q8, matmul_grid(p.M), dim3(kWG), 0, as_stream(stream), input, qweight, qscale, output,
+    G4_LAUNCH(k_matmul_q8, matmul_grid(p.M), dim3(kWG), 0, as_stream(stream), input, qweight, qscale, output,
                        p);
     G4_CHECK_LAUNCH("matmulQ8");
     return G4_OK;
@@ -337,7 +337,7 @@ int g4_matmul_q4k(const float* input, const uint32_t* qweight, const uint16_t* q
     if (!input || !qweight || !qmeta || !output) return fail(G4_EINVAL, "matmulQ4K: NULL pointer");
     if (p.N % 256) return fail(G4_EINVAL, "matmulQ4K: N %u is not a multiple of 256", p.N);
     if (p.M == 0) return G4_OK;
-    hipLaunchKernelGGL(k_matmul_q4k, matmul_grid(p.M), dim3(kWG), 0, as_stream(stream), input, qweight, qmeta, output,
+    G4_LAUNCH(k_matmul_q4k, matmul_grid(p.M), dim3(kWG), 0, as_stream(stream), input, qweight, qmeta, output,
                        p);
     G4_CHECK_LAUNCH("matmulQ4K");
     return G4_OK;
@@ -346,14 +346,14 @@ int g4_matmul_q4k(const float* input, const uint32_t* qweight, const uint16_t* q
 int g4_logit_softcap(float* logits, g4_softcap_params p, void* stream) {
     if (!logits) return fail(G4_EINVAL, "logitSoftcap: NULL logits");
     if (p.size == 0) return G4_OK;
-    hipLaunchKernelGGL(k_logit_softcap, dim3((p.size + kWG - 1) / kWG), dim3(kWG), 0, as_stream(stream), logits, p);
+    G4_LAUNCH(k_logit_softcap, dim3((p.size + kWG - 1) / kWG), dim3(kWG), 0, as_stream(stream), logits, p);
     G4_CHECK_LAUNCH("logitSoftcap");
     return G4_OK;
 }
 
 int g4_argmax(const float* logits, uint32_t* result, uint32_t size, void* stream) {
     if (!logits || !result) return fail(G4_EINVAL, "argmax: NULL pointer");
-    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(kWG), 0, as_stream(stream), logits, result, size);
+    G4_LAUNCH(k_argmax, dim3(1), dim3(kWG), 0, as_stream(stream), logits, result, size);
     G4_CHECK_LAUNCH("argmax");
     return G4_OK;
 }

@@ -1802,9 +1802,9 @@ static int prefill_run(const g4_decode_plan* plan, void* stream, hipEvent_t star
         const VtCacheDev* vtc = reinterpret_cast<const VtCacheDev*>(r.ws + r.off_vtc);
         const dim3 vgrid(r.vt_blocks, r.num_kv_heads);
         if (hd512)
-            hipLaunchKernelGGL(k_vt_blocks<512>, vgrid, dim3(256), 0, st, vtc, r.n_vtc, (uint32_t)r.num_kv_heads);
+            G4_LAUNCH(k_vt_blocks<512>, vgrid, dim3(256), 0, st, vtc, r.n_vtc, (uint32_t)r.num_kv_heads);
         else
-            hipLaunchKernelGGL(k_vt_blocks<256>, vgrid, dim3(256), 0, st, vtc, r.n_vtc, (uint32_t)r.num_kv_heads);
+            G4_LAUNCH(k_vt_blocks<256>, vgrid, dim3(256), 0, st, vtc, r.n_vtc, (uint32_t)r.num_kv_heads);
         G4_CHECK_LAUNCH("attnPrefill (V^T blocks)");
     }
     const dim3 grid(r.n_work, r.num_kv_heads, r.head_dim / 256);
@@ -1813,26 +1813,26 @@ static int prefill_run(const g4_decode_plan* plan, void* stream, hipEvent_t star
             if (start_ev || stop_ev)
                 hipExtLaunchKernelGGL(k_prefill_pp512, grid, dim3(6 * 64), 0, st, start_ev, stop_ev, 0, a);
             else
-                hipLaunchKernelGGL(k_prefill_pp512, grid, dim3(6 * 64), 0, st, a);
+                G4_LAUNCH(k_prefill_pp512, grid, dim3(6 * 64), 0, st, a);
         } else if (hd512) {  // grid z: the output half of the head dimension
             if (start_ev || stop_ev)
                 hipExtLaunchKernelGGL(k_prefill_dma<512>, grid, dim3(kPfThreads), 0, st, start_ev, stop_ev, 0, a);
             else
-                hipLaunchKernelGGL(k_prefill_dma<512>, grid, dim3(kPfThreads), 0, st, a);
+                G4_LAUNCH(k_prefill_dma<512>, grid, dim3(kPfThreads), 0, st, a);
         } else if (prefill_pp_enabled()) {
             if (start_ev || stop_ev)
                 hipExtLaunchKernelGGL(k_prefill_pp, grid, dim3(2 * kPfThreads), 0, st, start_ev, stop_ev, 0, a);
             else
-                hipLaunchKernelGGL(k_prefill_pp, grid, dim3(2 * kPfThreads), 0, st, a);
+                G4_LAUNCH(k_prefill_pp, grid, dim3(2 * kPfThreads), 0, st, a);
         } else if (start_ev || stop_ev) {
             hipExtLaunchKernelGGL(k_prefill_dma<256>, grid, dim3(kPfThreads), 0, st, start_ev, stop_ev, 0, a);
         } else {
-            hipLaunchKernelGGL(k_prefill_dma<256>, grid, dim3(kPfThreads), 0, st, a);
+            G4_LAUNCH(k_prefill_dma<256>, grid, dim3(kPfThreads), 0, st, a);
         }
     } else if (start_ev || stop_ev) {
         hipExtLaunchKernelGGL(k_prefill, grid, dim3(kPfThreads), 0, st, start_ev, stop_ev, 0, a);
     } else {
-        hipLaunchKernelGGL(k_prefill, grid, dim3(kPfThreads), 0, st, a);
+        G4_LAUNCH(k_prefill, grid, dim3(kPfThreads), 0, st, a);
     }
     G4_CHECK_LAUNCH("attnPrefill");
     if (!r.n_merge) return G4_OK;

@@ -155,7 +155,7 @@ extern "C" int g4_attn_prep_many(const g4_prep_layer* layers, uint32_t n_layers,
     if (n_layers > 65535) return fail(G4_EINVAL, "attnPrepMany: %u layers (max 65535)", n_layers);
     const unsigned blocks = num_q_heads + 2 * num_kv_heads;
     if (blocks == 0) return G4_OK;
-    hipLaunchKernelGGL(k_attn_prep_many, dim3(blocks, n_layers), dim3(kWG), 0, as_stream(stream), layers,
+    G4_LAUNCH(k_attn_prep_many, dim3(blocks, n_layers), dim3(kWG), 0, as_stream(stream), layers,
                        num_q_heads, num_kv_heads, eps, position, slot);
     G4_CHECK_LAUNCH("attnPrepMany");
     return G4_OK;
@@ -174,7 +174,7 @@ extern "C" int g4_attn_prep(float* q, float* k, float* v, const uint16_t* q_weig
         blocks += 2 * p.num_kv_heads;
     }
     if (blocks == 0) return G4_OK;
-    hipLaunchKernelGGL(k_attn_prep, dim3(blocks), dim3(kWG), 0, as_stream(stream), q, k, v, q_weight, k_weight,
+    G4_LAUNCH(k_attn_prep, dim3(blocks), dim3(kWG), 0, as_stream(stream), q, k, v, q_weight, k_weight,
                        rope_freqs, k_cache, v_cache, p);
     G4_CHECK_LAUNCH("attnPrep");
     return G4_OK;
@@ -203,10 +203,10 @@ extern "C" int g4_attn_prompt_prep(const float* q, const float* k, const float* 
     hipStream_t st = as_stream(stream);
     const dim3 grid((p.n_tokens + kPrepTokens - 1) / kPrepTokens);
     if (p.head_dim == 512)
-        hipLaunchKernelGGL(k_prompt_prep<512>, grid, dim3(kWG), 0, st, q, k, v, q_weight, k_weight, rope_freqs,
+        G4_LAUNCH(k_prompt_prep<512>, grid, dim3(kWG), 0, st, q, k, v, q_weight, k_weight, rope_freqs,
                            rope_inv_freq, q_out, k_cache, v_cache, p);
     else
-        hipLaunchKernelGGL(k_prompt_prep<256>, grid, dim3(kWG), 0, st, q, k, v, q_weight, k_weight, rope_freqs,
+        G4_LAUNCH(k_prompt_prep<256>, grid, dim3(kWG), 0, st, q, k, v, q_weight, k_weight, rope_freqs,
                            rope_inv_freq, q_out, k_cache, v_cache, p);
     G4_CHECK_LAUNCH("attnPromptPrep");
     return G4_OK;
@@ -233,7 +233,7 @@ extern "C" int g4_rope_inv_freq(float theta, uint32_t head_dim, uint32_t apply_d
     if (head_dim == 0 || head_dim % 2) return fail(G4_EINVAL, "ropeInvFreq: head_dim %u", head_dim);
     if (apply_divisor && !rope_freqs) return fail(G4_EINVAL, "ropeInvFreq: apply_divisor needs rope_freqs");
     const unsigned half = head_dim / 2;
-    hipLaunchKernelGGL(k_rope_inv_freq, dim3((half + kWG - 1) / kWG), dim3(kWG), 0, as_stream(stream), theta,
+    G4_LAUNCH(k_rope_inv_freq, dim3((half + kWG - 1) / kWG), dim3(kWG), 0, as_stream(stream), theta,
                        head_dim, apply_divisor, rope_freqs, inv_freq);
     G4_CHECK_LAUNCH("ropeInvFreq");
     return G4_OK;

@@ -140,7 +140,7 @@ int g4_fused_per_head_norm_rope(float* data, const uint16_t* weight, const uint1
     if (p.apply_divisor && !rope_freqs) return fail(G4_EINVAL, "fusedPerHeadNormRope: apply_divisor needs rope_freqs");
     if (p.head_dim == 0 || p.head_dim % 2) return fail(G4_EINVAL, "fusedPerHeadNormRope: head_dim %u", p.head_dim);
     if (p.num_heads == 0) return G4_OK;
-    hipLaunchKernelGGL(k_fused_per_head_norm_rope, dim3(p.num_heads), dim3(kWG), 0, as_stream(stream), data, weight,
+    G4_LAUNCH(k_fused_per_head_norm_rope, dim3(p.num_heads), dim3(kWG), 0, as_stream(stream), data, weight,
                        rope_freqs, p);
     G4_CHECK_LAUNCH("fusedPerHeadNormRope");
     return G4_OK;
@@ -150,7 +150,7 @@ int g4_per_head_rms_norm_no_weight(float* data, g4_norm_params p, void* stream) 
     if (!data) return fail(G4_EINVAL, "perHeadRmsNormNoWeight: NULL data");
     if (p.head_dim == 0) return fail(G4_EINVAL, "perHeadRmsNormNoWeight: head_dim 0");
     if (p.num_heads == 0) return G4_OK;
-    hipLaunchKernelGGL(k_per_head_rms_norm_no_weight, dim3(p.num_heads), dim3(kWG), 0, as_stream(stream), data, p);
+    G4_LAUNCH(k_per_head_rms_norm_no_weight, dim3(p.num_heads), dim3(kWG), 0, as_stream(stream), data, p);
     G4_CHECK_LAUNCH("perHeadRmsNormNoWeight");
     return G4_OK;
 }
@@ -162,7 +162,7 @@ int g4_kv_cache_store(const float* k_in, const float* v_in, uint16_t* k_cache, u
         return fail(G4_EINVAL, "kvCacheStore: slot %u >= max_seq_len %u", p.position, p.max_seq_len);
     const uint64_t total = (uint64_t)p.num_kv_heads * p.head_dim;
     if (total == 0) return G4_OK;
-    hipLaunchKernelGGL(k_kv_cache_store, dim3(ceil_div_u(total, kWG)), dim3(kWG), 0, as_stream(stream), k_in, v_in,
+    G4_LAUNCH(k_kv_cache_store, dim3(ceil_div_u(total, kWG)), dim3(kWG), 0, as_stream(stream), k_in, v_in,
                        k_cache, v_cache, p);
     G4_CHECK_LAUNCH("kvCacheStore");
     return G4_OK;
@@ -176,7 +176,7 @@ int g4_attn_score(const float* q, const uint16_t* k_cache, float* scores, g4_att
                     p.num_kv_heads);
     const uint64_t total = (uint64_t)p.num_q_heads * p.seq_len;
     if (total == 0) return G4_OK;
-    hipLaunchKernelGGL(k_attn_score, dim3(ceil_div_u(total, kWG)), dim3(kWG), 0, as_stream(stream), q, k_cache,
+    G4_LAUNCH(k_attn_score, dim3(ceil_div_u(total, kWG)), dim3(kWG), 0, as_stream(stream), q, k_cache,
                        scores, p);
     G4_CHECK_LAUNCH("attnScore");
     return G4_OK;
@@ -186,7 +186,7 @@ int g4_softmax(float* scores, g4_softmax_params p, void* stream) {
     if (!scores) return fail(G4_EINVAL, "softmax: NULL scores");
     if (p.seq_len == 0) return fail(G4_EINVAL, "softmax: seq_len 0");
     if (p.num_heads == 0) return G4_OK;
-    hipLaunchKernelGGL(k_softmax, dim3(p.num_heads), dim3(kWG), 0, as_stream(stream), scores, p);
+    G4_LAUNCH(k_softmax, dim3(p.num_heads), dim3(kWG), 0, as_stream(stream), scores, p);
     G4_CHECK_LAUNCH("softmax");
     return G4_OK;
 }
@@ -198,7 +198,7 @@ int g4_attn_output(const float* probs, const uint16_t* v_cache, float* out, g4_a
                     p.num_kv_heads);
     const uint64_t total = (uint64_t)p.num_q_heads * p.head_dim;
     if (total == 0) return G4_OK;
-    hipLaunchKernelGGL(k_attn_output, dim3(ceil_div_u(total, kWG)), dim3(kWG), 0, as_stream(stream), probs, v_cache,
+    G4_LAUNCH(k_attn_output, dim3(ceil_div_u(total, kWG)), dim3(kWG), 0, as_stream(stream), probs, v_cache,
                        out, p);
     G4_CHECK_LAUNCH("attnOutput");
     return G4_OK;
@@ -212,7 +212,7 @@ int g4_zero(void* dev_dst, size_t bytes, void* stream) {
     const unsigned tail = (unsigned)(bytes % 4);
     unsigned blocks = words ? ceil_div_u(words, kWG) : 1;
     if (blocks > 4096) blocks = 4096;
-    hipLaunchKernelGGL(k_zero, dim3(blocks), dim3(kWG), 0, as_stream(stream), static_cast<uint32_t*>(dev_dst), words,
+    G4_LAUNCH(k_zero, dim3(blocks), dim3(kWG), 0, as_stream(stream), static_cast<uint32_t*>(dev_dst), words,
                        static_cast<uint8_t*>(dev_dst) + words * 4, tail);
     G4_CHECK_LAUNCH("g4_zero");
     return G4_OK;

@@ -2,6 +2,7 @@
 // error slot behind g4_last_error(). These replace the WebGPU device, queue
 // and buffer calls the reference engine makes (src/engine.ts:350-353,
 // 402-437, 1347-1426); buffers stay owned by the caller.
+#include <math.h>
 #include <stdarg.h>
 #include <string.h>
 
@@ -261,6 +262,128 @@ int g4_readback_finish(g4_readback* handle, void* host_dst) {
     (void)hipHostFree(handle->staging);
     delete handle;
     if (e != hipSuccess) return hip_fail(e, "g4_readback_finish");
+    return G4_OK;
+}
+
+}  // extern "C"
+
+// Timestamp queries (the engine's GPUQuerySet, src/engine.ts:3089-3110,
+// 3208-3227, 3253-3288): one timing event per slot, and a flag per slot that
+// says it was written since the last resolve. A slot is written either by a
+// marker on the stream (g4_query_write: the GPU's timestamp once the work
+// before it has finished; the marker costs a few microseconds of GPU time) or
+// by the kernels of an open pass (g4_query_begin_pass: the timestamps are the
+// kernels' own start and end, with nothing launched between them). Markers
+// release to agent scope only (no system-scope cache write-back: a timestamp
+// orders nothing for the host). The events live as long as the set.
+struct g4_query_set {
+    std::vector<hipEvent_t> ev;
+    std::vector<uint8_t> written;
+};
+
+namespace {
+
+struct OpenPass {
+    g4_query_set* set = nullptr;  // null: no pass open on this thread
+    uint32_t slot = 0;
+    bool started = false;
+};
+
+thread_local OpenPass t_pass;
+
+}  // namespace
+
+bool g4::pass_events(hipEvent_t* start, hipEvent_t* stop) {
+    OpenPass& p = t_pass;
+    if (!p.set) return false;
+    *start = p.started ? nullptr : p.set->ev[p.slot];
+    *stop = p.set->ev[p.slot + 1];
+    p.set->written[p.slot] = p.set->written[p.slot + 1] = 1;
+    p.started = true;
+    return true;
+}
+
+extern "C" {
+
+static const uint32_t kMaxQuerySlots = 65536;
+
+int g4_query_set_create(uint32_t count, g4_query_set** out) {
+    if (!out) return fail(G4_EINVAL, "g4_query_set_create: out is NULL");
+    *out = nullptr;
+    if (count == 0 || count > kMaxQuerySlots)
+        return fail(G4_EINVAL, "g4_query_set_create: count %u outside 1 .. %u", count, kMaxQuerySlots);
+    g4_query_set* q = new g4_query_set;
+    q->ev.assign(count, nullptr);
+    q->written.assign(count, 0);
+    for (uint32_t i = 0; i < count; ++i) {
+        const hipError_t e = hipEventCreateWithFlags(&q->ev[i], hipEventDisableSystemFence);
+        if (e != hipSuccess) {
+            for (uint32_t j = 0; j < i; ++j) (void)hipEventDestroy(q->ev[j]);
+            delete q;
+            return hip_fail(e, "g4_query_set_create: hipEventCreate");
+        }
+    }
+    *out = q;
+    return G4_OK;
+}
+
+int g4_query_write(g4_query_set* set, uint32_t slot, void* stream) {
+    if (!set) return fail(G4_EINVAL, "g4_query_write: set is NULL");
+    if (slot >= set->ev.size())
+        return fail(G4_EINVAL, "g4_query_write: slot %u outside a set of %zu", slot, set->ev.size());
+    G4_CHECK_HIP(hipEventRecord(set->ev[slot], as_stream(stream)));
+    set->written[slot] = 1;
+    return G4_OK;
+}
+
+int g4_query_begin_pass(g4_query_set* set, uint32_t slot) {
+    if (!set) return fail(G4_EINVAL, "g4_query_begin_pass: set is NULL");
+    if ((uint64_t)slot + 2 > set->ev.size())
+        return fail(G4_EINVAL, "g4_query_begin_pass: slots %u, %u outside a set of %zu", slot, slot + 1,
+                    set->ev.size());
+    if (t_pass.set) return fail(G4_EINVAL, "g4_query_begin_pass: a pass is already open on this thread");
+    t_pass.set = set;
+    t_pass.slot = slot;
+    t_pass.started = false;
+    return G4_OK;
+}
+
+int g4_query_end_pass(void) {
+    if (!t_pass.set) return fail(G4_EINVAL, "g4_query_end_pass: no pass open on this thread");
+    t_pass = OpenPass();
+    return G4_OK;
+}
+
+int g4_query_resolve(g4_query_set* set, uint32_t first, uint32_t n_pairs, double* ns_out) {
+    if (!set) return fail(G4_EINVAL, "g4_query_resolve: set is NULL");
+    if (n_pairs == 0 || !ns_out) return fail(G4_EINVAL, "g4_query_resolve: n_pairs == 0 or ns_out is NULL");
+    if ((uint64_t)first + 2ull * n_pairs > set->ev.size())
+        return fail(G4_EINVAL, "g4_query_resolve: %u pairs from slot %u outside a set of %zu", n_pairs, first,
+                    set->ev.size());
+    if (t_pass.set == set) return fail(G4_EINVAL, "g4_query_resolve: a pass of this set is still open");
+    for (uint32_t i = 0; i < n_pairs; ++i) {
+        const uint32_t b = first + 2 * i, e = b + 1;
+        ns_out[i] = NAN;
+        if (!set->written[b] || !set->written[e]) continue;
+        G4_CHECK_HIP(hipEventSynchronize(set->ev[e]));
+        float ms = 0.f;
+        G4_CHECK_HIP(hipEventElapsedTime(&ms, set->ev[b], set->ev[e]));
+        ns_out[i] = (double)ms * 1e6;
+    }
+    for (uint32_t i = 0; i < 2 * n_pairs; ++i) set->written[first + i] = 0;
+    return G4_OK;
+}
+
+int g4_query_set_destroy(g4_query_set* set) {
+    if (!set) return fail(G4_EINVAL, "g4_query_set_destroy: set is NULL");
+    if (t_pass.set == set) t_pass = OpenPass();
+    hipError_t first_err = hipSuccess;
+    for (hipEvent_t e : set->ev) {
+        const hipError_t r = hipEventDestroy(e);
+        if (r != hipSuccess && first_err == hipSuccess) first_err = r;
+    }
+    delete set;
+    if (first_err != hipSuccess) return hip_fail(first_err, "g4_query_set_destroy");
     return G4_OK;
 }
 

@@ -437,17 +437,17 @@ static int launch_attention(const g4_decode_plan* plan, void* stream, hipEvent_t
     if (r.head_dim == 512) {
         if (start || stop) hipExtLaunchKernelGGL((k_attn_step<4, 512>), grid, dim3(256), 0, st, start, stop, 0, a.work, a.part_ml, a.part_o,
                                   a.num_kv_heads, a.group);
-        else hipLaunchKernelGGL((k_attn_step<4, 512>), grid, dim3(256), 0, st, a.work, a.part_ml, a.part_o, a.num_kv_heads,
+        else G4_LAUNCH((k_attn_step<4, 512>), grid, dim3(256), 0, st, a.work, a.part_ml, a.part_o, a.num_kv_heads,
                                a.group);
     } else if (r.waves == 8) {
         if (start || stop) hipExtLaunchKernelGGL((k_attn_step<8, 256>), grid, dim3(512), 0, st, start, stop, 0, a.work, a.part_ml, a.part_o,
                                   a.num_kv_heads, a.group);
-        else hipLaunchKernelGGL((k_attn_step<8, 256>), grid, dim3(512), 0, st, a.work, a.part_ml, a.part_o, a.num_kv_heads,
+        else G4_LAUNCH((k_attn_step<8, 256>), grid, dim3(512), 0, st, a.work, a.part_ml, a.part_o, a.num_kv_heads,
                                a.group);
     } else {
         if (start || stop) hipExtLaunchKernelGGL((k_attn_step<4, 256>), grid, dim3(256), 0, st, start, stop, 0, a.work, a.part_ml, a.part_o,
                                   a.num_kv_heads, a.group);
-        else hipLaunchKernelGGL((k_attn_step<4, 256>), grid, dim3(256), 0, st, a.work, a.part_ml, a.part_o, a.num_kv_heads,
+        else G4_LAUNCH((k_attn_step<4, 256>), grid, dim3(256), 0, st, a.work, a.part_ml, a.part_o, a.num_kv_heads,
                                a.group);
     }
     G4_CHECK_LAUNCH("attnStep");

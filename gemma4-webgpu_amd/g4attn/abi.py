@@ -142,6 +142,12 @@ SIGNATURES: dict[str, list] = {
     "g4_download": [_P, _P, _SZ, _SZ, _P],
     "g4_readback_begin": [_P, _SZ, _SZ, _P, C.POINTER(_P)],
     "g4_readback_finish": [_P, _P],
+    "g4_query_set_create": [_U32, C.POINTER(_P)],
+    "g4_query_begin_pass": [_P, _U32],
+    "g4_query_end_pass": [],
+    "g4_query_write": [_P, _U32, _P],
+    "g4_query_resolve": [_P, _U32, _U32, C.POINTER(C.c_double)],
+    "g4_query_set_destroy": [_P],
     "g4_zero": [_P, _SZ, _P],
     "g4_fused_per_head_norm_rope": [_P, _P, _P, NormRopeParams, _P],
     "g4_per_head_rms_norm_no_weight": [_P, NormParams, _P],

@@ -369,6 +369,40 @@ def read_ceiling(buf, sink, start=None, stop=None, stream=None):
              _dev(sink, "sink", (torch.int32, torch.uint32), 1), _stream(stream), ev[0], ev[1])
 
 
+class QuerySet:
+    """Timestamp queries for labelled passes (g4_query_set_*; the engine's GPUQuerySet, src/engine.ts:
+    3089-3110, 3208-3227, 3253-3288). begin_pass(slot) .. end_pass(): the library kernels launched from
+    this thread in between carry the pair (slot, slot+1) on their own dispatches; write(slot) records a
+    marker in stream order instead. resolve(first, n_pairs) waits and returns each pair's ns (float64,
+    NaN for a pair not written since its last resolve)."""
+
+    def __init__(self, count: int):
+        h = C.c_void_p(0)
+        abi.call("g4_query_set_create", count, C.byref(h))
+        self.handle, self.count = h, count
+
+    def begin_pass(self, slot: int):
+        abi.call("g4_query_begin_pass", self.handle, slot)
+
+    @staticmethod
+    def end_pass():
+        abi.call("g4_query_end_pass")
+
+    def write(self, slot: int, stream=None):
+        abi.call("g4_query_write", self.handle, slot, _stream(stream))
+
+    def resolve(self, first: int, n_pairs: int):
+        import numpy as np
+        out = np.zeros(max(n_pairs, 1), np.float64)
+        abi.call("g4_query_resolve", self.handle, first, n_pairs, out.ctypes.data_as(C.POINTER(C.c_double)))
+        return out[:n_pairs]
+
+    def close(self):
+        if self.handle:
+            abi.call("g4_query_set_destroy", self.handle)
+            self.handle = None
+
+
 def attn_step(entries, num_q_heads, num_kv_heads, head_dim, workspace, stream=None):
     abi.call("g4_attn_step", entries, len(entries), num_q_heads, num_kv_heads, head_dim,
              _dev(workspace, "workspace", torch.uint8, 0), workspace.numel(), _stream(stream))

@@ -84,7 +84,23 @@ export const PASS_LABELS: Record<string, string> = {
   matmulQ8: 'attn.linearQKV',
   matmulQ4K: 'attn.linearQKV',
   linear: 'attn.linearQKV',
+  linearOut: 'attn.linearOut',
+  attnStepOut: 'attn.linearOut',
 };
+
+// The profiler's report types (src/types.ts:490-515).
+export interface ProfileCapability {
+  timestampQuerySupported: boolean;
+  timestampQueryOnAdapterButUnrequested: boolean;
+  querySlots: number;
+}
+
+export interface ProfileReport {
+  perLabel: Array<{ label: string; samples_n: number; p50_ns: number; p95_ns: number; mean_ns: number; total_ns: number }>;
+  forwardMedian_ns: number;
+  forwardSamples_n: number;
+  overflow: boolean;
+}
 
 // The engine's makeUniformMixed: 4-byte fields, at least 16 bytes.
 export class Uniform {
@@ -219,6 +235,13 @@ export interface Addon {
   upload(dst: bigint, offset: number, data: any, s: bigint): void;
   download(src: bigint, offset: number, out: any, s: bigint): void;
   readAsync(src: bigint, offset: number, out: any, s: bigint): Promise<void>;
+  querySetCreate(count: number): bigint;
+  queryBeginPass(set: bigint, slot: number): void;
+  queryEndPass(): void;
+  queryWrite(set: bigint, slot: number, s: bigint): void;
+  queryResolve(set: bigint, first: number, nPairs: number): Float64Array;
+  queryResolveAsync(set: bigint, first: number, nPairs: number): Promise<Float64Array>;
+  querySetDestroy(set: bigint): void;
   zero(p: bigint, bytes: number, s: bigint): void;
   fusedPerHeadNormRope(data: bigint, w: bigint, rf: bigint, p: Uint8Array, s: bigint): void;
   perHeadRmsNormNoWeight(data: bigint, p: Uint8Array, s: bigint): void;
@@ -278,10 +301,25 @@ export const KERNELS: Record<KernelName, Launch> = {
   matmulQ4K: function (g4, b, p, s) { g4.matmulQ4K(b[0], b[1], b[2], b[3], p, s); },
 };
 
+// Query slots per forward (the engine's PROFILE_QUERY_SLOTS, src/engine.ts:148): two per timed pass.
+export const PROFILE_QUERY_SLOTS = 2048;
+
 export class HipAttention {
   readonly stream: bigint;
   private readonly g4: Addon;
   private alive: boolean;
+  // Per-pass GPU timing (src/engine.ts:136-148, 3085-3288): two query slots per labelled pass, resolved
+  // by collectProfileSamples() after a forward's passes are enqueued. A forward writes its own query set;
+  // collect hands it to the resolve and the next forward takes another from the free list (or a new one),
+  // so a forward enqueued while the last one resolves does not overwrite its timestamps.
+  private profileActive = false;
+  private profileQuerySet: bigint | null = null;
+  private readonly profileFreeSets: bigint[] = [];
+  private profileSlotCursor = 0;
+  private profilePassLabels: string[] = [];
+  private readonly profileSamples: Map<string, number[]> = new Map();
+  private readonly profileForwardTotals_ns: number[] = [];
+  private profileOverflow = false;
 
   constructor(addon: Addon, device: number) {
     this.g4 = addon;
@@ -336,7 +374,12 @@ export class HipAttention {
       throw new Error(`${name}: ${bindings.length} bindings, expected ${want.length} (${want.join(', ')})`);
     }
     if (params.bytes.byteLength < PARAMS_BYTES[name]) throw new Error(`${name}: params too short`);
-    launch(this.g4, bindings.map(function (b) { return b.ptr; }), params.bytes, this.stream);
+    const slot = this.beginPass(PASS_LABELS[name]);
+    try {
+      launch(this.g4, bindings.map(function (b) { return b.ptr; }), params.bytes, this.stream);
+    } finally {
+      this.endPass(slot);
+    }
   }
 
   ropeInvFreq(theta: number, headDim: number, applyDivisor: number, ropeFreqs: DeviceBuffer | null,
@@ -393,7 +436,12 @@ export class HipAttention {
   }
 
   attnStepRun(plan: Uint8Array): void {
-    this.g4.attnStepRun(plan, this.stream);
+    const slot = this.beginPass(PASS_LABELS.attnStep);
+    try {
+      this.g4.attnStepRun(plan, this.stream);
+    } finally {
+      this.endPass(slot);
+    }
   }
 
   attnStep(entries: StepEntry[], shape: StepShape, workspace: DeviceBuffer): void {
@@ -402,7 +450,12 @@ export class HipAttention {
 
   // The attention pass of a prepared step alone; attnStepOut then finishes it.
   attnStepRunAttention(plan: Uint8Array): void {
-    this.g4.attnStepRunAttention(plan, this.stream);
+    const slot = this.beginPass(PASS_LABELS.attnStep);
+    try {
+      this.g4.attnStepRunAttention(plan, this.stream);
+    } finally {
+      this.endPass(slot);
+    }
   }
 
   // attn.linearOut of every entry of a step after attnStepRunAttention (src/engine.ts:2096), with the step's
@@ -416,7 +469,12 @@ export class HipAttention {
       if (g.out.size < g.rows * 4) throw new RangeError('attnStepOut: segment ' + i + ' out too small');
       return { weight: g.weight.ptr, out: g.out.ptr, rows: g.rows };
     });
-    this.g4.attnStepRunOut(plan, segs, this.stream);
+    const slot = this.beginPass(PASS_LABELS.attnStepOut);
+    try {
+      this.g4.attnStepRunOut(plan, segs, this.stream);
+    } finally {
+      this.endPass(slot);
+    }
   }
 
   private static prefillFlat(entries: PrefillEntry[]): any[] {
@@ -441,7 +499,12 @@ export class HipAttention {
   }
 
   attnPrefillRun(plan: Uint8Array): void {
-    this.g4.attnPrefillRun(plan, this.stream);
+    const slot = this.beginPass(PASS_LABELS.attnPrefill);
+    try {
+      this.g4.attnPrefillRun(plan, this.stream);
+    } finally {
+      this.endPass(slot);
+    }
   }
 
   attnPrefill(entries: PrefillEntry[], shape: StepShape, workspace: DeviceBuffer): void {
@@ -461,8 +524,13 @@ export class HipAttention {
       { u: p.maxSeqLen || 0 },
     ]);
     function ptr(b: DeviceBuffer | undefined): bigint | null { return b ? b.ptr : null; }
-    this.g4.attnPromptPrep(p.q.ptr, ptr(p.k), ptr(p.v), p.qWeight.ptr, ptr(p.kWeight), ptr(p.ropeFreqs),
-      ptr(p.ropeInvFreq), p.qOut.ptr, ptr(p.kCache), ptr(p.vCache), params.bytes, this.stream);
+    const slot = this.beginPass(PASS_LABELS.attnPromptPrep);
+    try {
+      this.g4.attnPromptPrep(p.q.ptr, ptr(p.k), ptr(p.v), p.qWeight.ptr, ptr(p.kWeight), ptr(p.ropeFreqs),
+        ptr(p.ropeInvFreq), p.qOut.ptr, ptr(p.kCache), ptr(p.vCache), params.bytes, this.stream);
+    } finally {
+      this.endPass(slot);
+    }
   }
 
   lmHeadWorkspaceSize(shape: LmHeadShape): number {
@@ -475,24 +543,35 @@ export class HipAttention {
     workspace: DeviceBuffer, shape: LmHeadShape): void {
     if (weight.size < shape.vocab * shape.hidden * 2) throw new RangeError('lmHeadArgmax: weight too small');
     if (logits && logits.size < shape.vocab * 4) throw new RangeError('lmHeadArgmax: logits too small');
-    this.g4.lmHeadArgmax(hidden.ptr, weight.ptr, logits ? logits.ptr : null, result.ptr, workspace.ptr,
-      workspace.size, shape.vocab, shape.hidden, shape.cap, this.stream);
+    const slot = this.beginPass(PASS_LABELS.lmHeadArgmax);
+    try {
+      this.g4.lmHeadArgmax(hidden.ptr, weight.ptr, logits ? logits.ptr : null, result.ptr, workspace.ptr,
+        workspace.size, shape.vocab, shape.hidden, shape.cap, this.stream);
+    } finally {
+      this.endPass(slot);
+    }
   }
 
   // attn.linearQKV (q, k, v in one launch: the three matrices read the same normed hidden state) and
   // attn.linearOut (src/engine.ts:2045-2051, 2096): each row bit-identical to a matmulQuant dispatch.
-  linear(input: DeviceBuffer, n: number, segments: LinearSegment[]): void {
+  // `label` names the pass for the profiler (default attn.linearQKV).
+  linear(input: DeviceBuffer, n: number, segments: LinearSegment[], label?: string): void {
     if (input.size < n * 4) throw new RangeError('linear: input too small');
     const segs = segments.map(function (g, i) {
       if (g.weight.size < g.rows * n * 2) throw new RangeError('linear: segment ' + i + ' weight too small');
       if (g.out.size < g.rows * 4) throw new RangeError('linear: segment ' + i + ' out too small');
       return { weight: g.weight.ptr, out: g.out.ptr, rows: g.rows };
     });
-    this.g4.linear(input.ptr, n, segs, this.stream);
+    const slot = this.beginPass(label || PASS_LABELS.linear);
+    try {
+      this.g4.linear(input.ptr, n, segs, this.stream);
+    } finally {
+      this.endPass(slot);
+    }
   }
 
   // The same with the engine's quantized weights: each row bit-identical to a matmulQ8 / matmulQ4K dispatch.
-  linearQuant(input: DeviceBuffer, n: number, format: 'q8' | 'q4k', segments: QuantSegment[]): void {
+  linearQuant(input: DeviceBuffer, n: number, format: 'q8' | 'q4k', segments: QuantSegment[], label?: string): void {
     if (input.size < n * 4) throw new RangeError('linearQuant: input too small');
     const q8 = format === 'q8';
     const segs = segments.map(function (g, i) {
@@ -501,7 +580,118 @@ export class HipAttention {
       if (g.out.size < g.rows * 4) throw new RangeError('linearQuant: segment ' + i + ' out too small');
       return { weight: g.weight.ptr, meta: g.meta.ptr, out: g.out.ptr, rows: g.rows };
     });
-    this.g4.linearQuant(input.ptr, n, q8 ? 1 : 2, segs, this.stream);
+    const slot = this.beginPass(label || PASS_LABELS.linear);
+    try {
+      this.g4.linearQuant(input.ptr, n, q8 ? 1 : 2, segs, this.stream);
+    } finally {
+      this.endPass(slot);
+    }
+  }
+
+  // ---- profiling (src/engine.ts:3085-3288) ----
+
+  getProfileCapability(): ProfileCapability {
+    return { timestampQuerySupported: true, timestampQueryOnAdapterButUnrequested: false,
+      querySlots: PROFILE_QUERY_SLOTS };
+  }
+
+  // Every pass enqueued from now on is timed, until disableProfile().
+  enableProfile(): void {
+    this.profileActive = true;
+  }
+
+  disableProfile(): void {
+    this.profileActive = false;
+  }
+
+  resetProfileSamples(): void {
+    this.profileSamples.clear();
+    this.profileForwardTotals_ns.length = 0;
+    this.profileOverflow = false;
+  }
+
+  // Per label: percentiles over the samples of every forward collected so far, largest p50 first.
+  getProfileReport(): ProfileReport {
+    const perLabel: ProfileReport['perLabel'] = [];
+    this.profileSamples.forEach(function (samples, label) {
+      if (samples.length === 0) return;
+      const sorted = samples.slice().sort(function (a, b) { return a - b; });
+      let sum = 0;
+      for (const x of samples) sum += x;
+      perLabel.push({
+        label: label, samples_n: samples.length,
+        p50_ns: sorted[Math.floor(sorted.length * 0.5)],
+        p95_ns: sorted[Math.min(sorted.length - 1, Math.floor(sorted.length * 0.95))],
+        mean_ns: sum / samples.length, total_ns: sum,
+      });
+    });
+    perLabel.sort(function (a, b) { return b.p50_ns - a.p50_ns; });
+    const fwd = this.profileForwardTotals_ns.slice().sort(function (a, b) { return a - b; });
+    return {
+      perLabel: perLabel,
+      forwardMedian_ns: fwd.length > 0 ? fwd[Math.floor(fwd.length * 0.5)] : 0,
+      forwardSamples_n: fwd.length,
+      overflow: this.profileOverflow,
+    };
+  }
+
+  // Ends a forward: waits (off the JS thread) for the timestamps of the passes enqueued since the last
+  // collect, adds each pass's duration to its label's samples and their sum to the forward totals.
+  collectProfileSamples(): Promise<void> {
+    const labels = this.profilePassLabels;
+    const used = this.profileSlotCursor;
+    const qs = this.profileQuerySet;
+    this.profilePassLabels = [];
+    this.profileSlotCursor = 0;
+    this.profileQuerySet = null;
+    if (qs === null) return Promise.resolve();
+    const self = this;
+    const release = function () {
+      if (self.alive) self.profileFreeSets.push(qs);
+      else self.g4.querySetDestroy(qs);
+    };
+    return this.g4.queryResolveAsync(qs, 0, used / 2).then(function (ns: Float64Array) {
+      release();
+      let total = 0;
+      for (let i = 0; i < labels.length; i++) {
+        const d = ns[i];
+        if (!(d > 0)) continue;  // NaN: the pass launched nothing
+        total += d;
+        let arr = self.profileSamples.get(labels[i]);
+        if (!arr) {
+          arr = [];
+          self.profileSamples.set(labels[i], arr);
+        }
+        arr.push(d);
+      }
+      if (total > 0) self.profileForwardTotals_ns.push(total);
+    }, function (e: any) {
+      release();
+      throw e;
+    });
+  }
+
+  // Opens a pass: the library kernels launched until endPass carry its two slots on their own dispatches
+  // (the first one's start, the last one's end). Returns the first slot, or -1 when profiling is off or
+  // the set is full (then the pass runs untimed and the report says overflow).
+  private beginPass(label: string): number {
+    if (!this.profileActive) return -1;
+    const slot = this.profileSlotCursor;
+    if (slot + 2 > PROFILE_QUERY_SLOTS) {
+      this.profileOverflow = true;
+      return -1;
+    }
+    if (this.profileQuerySet === null) {
+      this.profileQuerySet = this.profileFreeSets.pop() || this.g4.querySetCreate(PROFILE_QUERY_SLOTS);
+    }
+    this.g4.queryBeginPass(this.profileQuerySet, slot);
+    this.profileSlotCursor = slot + 2;
+    this.profilePassLabels.push(label);
+    return slot;
+  }
+
+  private endPass(slot: number): void {
+    if (slot >= 0) this.g4.queryEndPass();
   }
 
   synchronize(): void {
@@ -511,6 +701,10 @@ export class HipAttention {
   dispose(): void {
     if (!this.alive) return;
     this.g4.streamSynchronize(this.stream);
+    if (this.profileQuerySet !== null) this.g4.querySetDestroy(this.profileQuerySet);
+    this.profileQuerySet = null;
+    for (const q of this.profileFreeSets) this.g4.querySetDestroy(q);
+    this.profileFreeSets.length = 0;
     this.g4.streamDestroy(this.stream);
     this.alive = false;
   }

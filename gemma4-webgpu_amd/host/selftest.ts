@@ -553,10 +553,74 @@ function readback(dir: string): Promise<string[]> {
   });
 }
 
+// Per-pass GPU timing (enableProfile / collectProfileSamples / getProfileReport, src/engine.ts:3085-3288):
+// labels and sample counts per forward, durations bounded below by the bytes each pass moves at the 8 TB/s
+// HBM peak, a forward enqueued while the previous one resolves, the overflow flag, and no timing when off.
+async function profile(dir: string): Promise<string[]> {
+  const done: string[] = [];
+  const att = new HipAttention(loadAddon(), 0);
+  const n = 16 << 20;  // 64 MiB of logits: the soft-cap reads and writes 128 MiB
+  const big = att.createBuffer(n * 4), small = att.createBuffer(1024);
+  att.clearBuffer(big);
+  att.clearBuffer(small);
+  const capBig = new Uniform([{ u: n }, { f: 30.0 }]), capSmall = new Uniform([{ u: 256 }, { f: 30.0 }]);
+  const forward = function () {
+    att.dispatch('logitSoftcap', [big], capBig);
+    att.dispatch('logitSoftcap', [small], capSmall);
+    att.dispatch('logitSoftcap', [big], capBig);
+  };
+  forward();
+  await att.collectProfileSamples();
+  same(att.getProfileReport().perLabel.length, 0, 'passes timed while profiling is off');
+  att.enableProfile();
+  for (let f = 0; f < 3; f++) {
+    forward();
+    await att.collectProfileSamples();
+  }
+  forward();
+  const p1 = att.collectProfileSamples();
+  forward();  // enqueued while the previous forward's timestamps resolve: a set of its own
+  const p2 = att.collectProfileSamples();
+  await Promise.all([p1, p2]);
+  let r = att.getProfileReport();
+  same(r.forwardSamples_n, 5, 'forward samples');
+  same(r.overflow, false, 'overflow');
+  same(r.perLabel.length, 1, 'labels');
+  const s = r.perLabel[0];
+  same(s.label, 'logitSoftcap', 'label');
+  same(s.samples_n, 15, 'samples per label');
+  const floor = 2 * n * 4 / 8e12 * 1e9;  // ns for 128 MiB at 8 TB/s
+  if (!(s.p50_ns >= floor)) fail(`soft-cap pass p50 ${s.p50_ns} ns under the HBM floor ${floor} ns`);
+  if (!(s.p95_ns >= s.p50_ns && s.p95_ns < 5e6)) fail(`soft-cap pass p95 ${s.p95_ns} ns`);
+  if (!(r.forwardMedian_ns >= 2 * floor && r.forwardMedian_ns < 2e7)) fail(`forward median ${r.forwardMedian_ns} ns`);
+  if (Math.abs(s.total_ns - s.mean_ns * s.samples_n) > 1) fail('total != mean * samples');
+  done.push(`5 forwards timed: soft-cap p50 ${(s.p50_ns / 1e3).toFixed(1)} us (HBM floor ${(floor / 1e3).toFixed(1)} us), ` +
+    `forward median ${(r.forwardMedian_ns / 1e3).toFixed(1)} us`);
+  // more passes than the set holds: the excess runs untimed and the report says so
+  att.resetProfileSamples();
+  const slots = att.getProfileCapability().querySlots;
+  for (let i = 0; i < slots / 2 + 5; i++) att.dispatch('logitSoftcap', [small], capSmall);
+  await att.collectProfileSamples();
+  r = att.getProfileReport();
+  same(r.overflow, true, 'overflow after too many passes');
+  same(r.perLabel[0].samples_n <= slots / 2, true, 'samples within the set');
+  done.push(`overflow flagged after ${slots / 2 + 5} passes (${r.perLabel[0].samples_n} timed)`);
+  att.resetProfileSamples();
+  att.disableProfile();
+  forward();
+  await att.collectProfileSamples();
+  same(att.getProfileReport().perLabel.length, 0, 'passes timed after disableProfile');
+  done.push('no timing when off');
+  att.destroyBuffer(big);
+  att.destroyBuffer(small);
+  att.dispose();
+  return done;
+}
+
 export function main(argv: string[]): void {
   const mode = argv[0];
-  if (mode === 'readback') {
-    readback(argv[1]).then(function (done) {
+  if (mode === 'readback' || mode === 'profile') {
+    (mode === 'readback' ? readback(argv[1]) : profile(argv[1])).then(function (done) {
       process.stdout.write(JSON.stringify({ ok: true, checks: done }) + '\n');
     }, function (e) {
       process.stderr.write(String(e && e.stack ? e.stack : e) + '\n');
@@ -572,6 +636,6 @@ export function main(argv: string[]): void {
   else if (mode === 'promptprep') done = promptPrep(argv[1]);
   else if (mode === 'linear') done = linear(argv[1]);
   else if (mode === 'batch') done = batch(argv[1]);
-  else fail(`usage: run.js cpu | layer <dir> | prefill <dir> | promptprep <dir> | head <dir> | linear <dir> | batch <dir> | readback <dir>`);
+  else fail(`usage: run.js cpu | layer <dir> | prefill <dir> | promptprep <dir> | head <dir> | linear <dir> | batch <dir> | readback <dir> | profile`);
   process.stdout.write(JSON.stringify({ ok: true, checks: done }) + '\n');
 }

@@ -76,6 +76,28 @@ int g4_download(void* host_dst, const void* dev_src, size_t offset, size_t bytes
 typedef struct g4_readback g4_readback;
 int g4_readback_begin(const void* dev_src, size_t offset, size_t bytes, void* stream, g4_readback** handle);
 int g4_readback_finish(g4_readback* handle, void* host_dst);
+/* Timestamp queries for labelled passes: the engine's GPUQuerySet of type
+ * 'timestamp' (created in enableProfile, src/engine.ts:3089-3110), written at
+ * each pass's beginning and end (timestampWrites, :3208-3227) and resolved
+ * after submit (resolveQuerySet + mapAsync, :3253-3288). A set holds `count`
+ * slots (1 .. 65536); a pass uses a pair (slot, slot+1).
+ * begin_pass opens a pass on the calling thread (one at a time): every kernel
+ * the library launches from this thread until end_pass carries the pair on its
+ * own dispatch, the first kernel's start in `slot` and the last one's end in
+ * slot+1 (no packet is added between kernels). write instead records a marker
+ * for one slot on `stream`, in stream order (a few microseconds of GPU time
+ * each). resolve waits, from any thread, for n_pairs pairs from slot `first`
+ * and writes ns_out[i] = the time from slot first+2i to slot first+2i+1 in
+ * nanoseconds, or NaN where either slot was not written since the last resolve
+ * of it (a pass that launched nothing); the resolved slots may then be written
+ * again. */
+typedef struct g4_query_set g4_query_set;
+int g4_query_set_create(uint32_t count, g4_query_set** out);
+int g4_query_begin_pass(g4_query_set* set, uint32_t slot);
+int g4_query_end_pass(void);
+int g4_query_write(g4_query_set* set, uint32_t slot, void* stream);
+int g4_query_resolve(g4_query_set* set, uint32_t first, uint32_t n_pairs, double* ns_out);
+int g4_query_set_destroy(g4_query_set* set);
 /* Measurement hook (no counterpart in the reference): the device's read-stream
  * ceiling. Streams `bytes` of buf with nontemporal 16-byte loads (the decode
  * kernels' load form) and writes nothing (sink is only a guard against the

@@ -228,3 +228,25 @@ def test_layers_prepare_and_prompt_prep_checked_on_host():
     pp = abi.PromptPrepParams(8, 1, 256, 4, 0, 1e-6, 1e6, 1, 0, 0)
     st, msg = _err(lambda L: L.g4_attn_prompt_prep(1, None, None, 1, None, None, None, 1, None, None, pp, None))
     assert st == abi.G4_EINVAL and "rope_freqs" in msg
+
+
+def test_query_set_arguments_checked_on_host():
+    """The timestamp query set refuses a slot count of 0 or above 65536, NULL handles and NULL outputs,
+    and an end_pass with no pass open, before any HIP call."""
+    q = C.c_void_p(0)
+    for count in (0, 65537):
+        st, msg = _err(lambda L: L.g4_query_set_create(count, C.byref(q)))
+        assert st == abi.G4_EINVAL and "count" in msg and q.value is None
+    st, msg = _err(lambda L: L.g4_query_set_create(4, None))
+    assert st == abi.G4_EINVAL and "NULL" in msg
+    st, msg = _err(lambda L: L.g4_query_write(None, 0, None))
+    assert st == abi.G4_EINVAL and "NULL" in msg
+    st, msg = _err(lambda L: L.g4_query_begin_pass(None, 0))
+    assert st == abi.G4_EINVAL and "NULL" in msg
+    st, msg = _err(lambda L: L.g4_query_end_pass())
+    assert st == abi.G4_EINVAL and "no pass open" in msg
+    ns = (C.c_double * 4)()
+    st, msg = _err(lambda L: L.g4_query_resolve(None, 0, 2, ns))
+    assert st == abi.G4_EINVAL and "NULL" in msg
+    st, msg = _err(lambda L: L.g4_query_set_destroy(None))
+    assert st == abi.G4_EINVAL and "NULL" in msg

@@ -395,3 +395,17 @@ def test_prompt_prep_through_ts_host(tmp_path, start, T, hd, theta, div):
         np.testing.assert_array_equal(kc[pos], orc.f32_to_f16_bits(k_), err_msg=f"k token {t}")
         np.testing.assert_array_equal(vc[pos], orc.f32_to_f16_bits(v_), err_msg=f"v token {t}")
     assert (kc[:start] == 0).all() and (kc[start + T:] == 0).all() and (vc[:start] == 0).all()
+
+
+@pytest.mark.skipif(NODE is None, reason="node is not installed")
+def test_profiler_through_ts_host(tmp_path):
+    """Per-pass GPU timing in the TS host (enableProfile / collectProfileSamples / getProfileReport,
+    src/engine.ts:3085-3288): labels and sample counts per forward, each pass's p50 at least its bytes at
+    the 8 TB/s HBM peak, a forward enqueued while the previous one resolves, the overflow flag, and no
+    timing while profiling is off (the checks run in host/selftest.ts)."""
+    announce("TS host per-pass profiler")
+    r = subprocess.run([NODE, str(RUN), "profile", str(tmp_path)], cwd=ROOT, capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 0, r.stderr
+    assert '"ok":true' in r.stdout
+    print(r.stdout.strip())

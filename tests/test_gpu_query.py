@@ -1,0 +1,77 @@
+"""GPU checks of the timestamp query set (g4_query_set_*; the engine's per-pass timestamp queries,
+src/engine.ts:3208-3227, 3253-3288) through the C ABI.
+
+A pass (begin_pass .. end_pass) around one 256 MiB streaming read takes the kernel's own start and end:
+within 10% of the same read timed with events on its dispatch, and at least the time 256 MiB takes at
+the 8 TB/s HBM peak. A pass around two reads spans both (first kernel's start to the last one's end). A
+pass that launched nothing resolves to NaN. A marker pair (write) spans the work between the markers.
+Slots are written again after a resolve, and misuse is refused (a second open pass, a resolve of an
+open pass's set, pairs outside the set)."""
+import ctypes as C
+import math
+
+import pytest
+import torch
+
+from conftest import announce
+from g4attn import abi, ops
+
+pytestmark = pytest.mark.gpu
+
+MIB = 1 << 20
+
+
+def test_pass_pairs_time_their_kernels(dev):
+    announce("timestamp queries: passes around 256 MiB reads")
+    buf = torch.randint(0, 256, (256 * MIB,), dtype=torch.uint8, device=dev)
+    busy = torch.empty(1024 * MIB, dtype=torch.uint8, device=dev)
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    a_, b_ = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a_.record()
+    b_.record()
+    for _ in range(3):
+        ops.read_ceiling(buf, sink)
+    torch.cuda.synchronize()
+    floor_ns = 256 * MIB / 8e12 * 1e9  # 256 MiB at 8 TB/s
+    q = ops.QuerySet(8)
+    lib = abi.load()
+    try:
+        for rep in range(2):  # the second round writes the resolved slots again
+            ops.read_ceiling(busy, sink)  # the GPU is busy while the rest is enqueued behind it
+            ops.read_ceiling(buf, sink, a_, b_)  # the kernel's own time, for comparison
+            q.begin_pass(0)
+            ops.read_ceiling(buf, sink)
+            q.end_pass()
+            q.begin_pass(2)
+            ops.read_ceiling(buf, sink)
+            ops.read_ceiling(buf, sink)
+            q.end_pass()
+            q.begin_pass(4)  # launches nothing
+            q.end_pass()
+            q.write(6)
+            ops.read_ceiling(buf, sink)
+            q.write(7)
+            ns = q.resolve(0, 4)
+            kernel_ns = a_.elapsed_time(b_) * 1e6
+            print(f"round {rep}: passes {[round(x) if not math.isnan(x) else x for x in ns]} ns, "
+                  f"kernel {kernel_ns:.0f} ns")
+            one, two, empty, marked = ns
+            assert 0.9 * kernel_ns <= one <= 1.1 * kernel_ns and one >= floor_ns, (one, kernel_ns)
+            assert 1.8 * kernel_ns <= two <= 2.3 * kernel_ns and two >= 2 * floor_ns, (two, kernel_ns)
+            assert math.isnan(empty), empty
+            assert marked >= 0.9 * kernel_ns and marked >= floor_ns, (marked, kernel_ns)
+        q.begin_pass(0)
+        st = lib.g4_query_begin_pass(q.handle, 2)
+        assert st == abi.G4_EINVAL and "already open" in lib.g4_last_error().decode()
+        out = (C.c_double * 4)()
+        st = lib.g4_query_resolve(q.handle, 0, 1, out)
+        assert st == abi.G4_EINVAL and "still open" in lib.g4_last_error().decode()
+        q.end_pass()
+        st = lib.g4_query_resolve(q.handle, 6, 2, out)
+        assert st == abi.G4_EINVAL and "outside" in lib.g4_last_error().decode()
+        st = lib.g4_query_begin_pass(q.handle, 7)
+        assert st == abi.G4_EINVAL and "outside" in lib.g4_last_error().decode()
+        st = lib.g4_query_write(q.handle, 8, None)
+        assert st == abi.G4_EINVAL and "outside" in lib.g4_last_error().decode()
+    finally:
+        q.close()
