@@ -445,7 +445,9 @@ interface BatchSpec {
   arrays: Record<string, number[]>;
 }
 
-function batch(dir: string): string[] {
+// Profiled throughout: every token is one forward of the per-pass profiler, whose samples must cover
+// every attnStep launch while the outputs stay those the unprofiled path gives (checked by the caller).
+async function batch(dir: string): Promise<string[]> {
   const spec = JSON.parse(fs.readFileSync(path.join(dir, 'case.json'), 'utf8')) as BatchSpec;
   const bin: Uint8Array = fs.readFileSync(path.join(dir, 'case.bin'));
   const att = new HipAttention(loadAddon(), 0);
@@ -478,7 +480,9 @@ function batch(dir: string): string[] {
   });
   const outs: Uint8Array[] = [];
   let launches = 0;
-  spec.steps.forEach(function (st, si) {
+  att.enableProfile();
+  for (let si = 0; si < spec.steps.length; si++) {
+    const st = spec.steps[si];
     st.release.forEach(function (id) { sched.release(id); });
     st.submit.forEach(function (s) { sched.submit(s[0], s[1]); });
     const admitted = sched.admit();
@@ -512,7 +516,14 @@ function batch(dir: string): string[] {
       });
     });
     sched.advance();
-  });
+    await att.collectProfileSamples();
+  }
+  const rep = att.getProfileReport();
+  same(rep.forwardSamples_n, spec.steps.length, 'profiled forwards');
+  same(rep.perLabel.length, 1, 'profiled labels');
+  same(rep.perLabel[0].label, 'attn.decodeFused', 'profiled label');
+  same(rep.perLabel[0].samples_n, launches, 'profiled attnStep passes');
+  if (!(rep.perLabel[0].p50_ns > 0) || rep.overflow) fail('profile report');
   let total = 0;
   for (const o of outs) total += o.byteLength;
   const res = new Uint8Array(total);
@@ -525,7 +536,8 @@ function batch(dir: string): string[] {
   sched.dispose();
   for (const b of bufs) att.destroyBuffer(b);
   att.dispose();
-  return [`${spec.steps.length} token steps`, `${launches} attnStep launches`, `${outs.length} outputs written`];
+  return [`${spec.steps.length} token steps`, `${launches} attnStep launches`, `${outs.length} outputs written`,
+    `profiled: attn.decodeFused p50 ${(rep.perLabel[0].p50_ns / 1e3).toFixed(1)} us over ${launches} passes`];
 }
 
 // Promise readback: each copy is ordered where it was issued on the stream, whatever enqueues follow it.
@@ -619,8 +631,8 @@ async function profile(dir: string): Promise<string[]> {
 
 export function main(argv: string[]): void {
   const mode = argv[0];
-  if (mode === 'readback' || mode === 'profile') {
-    (mode === 'readback' ? readback(argv[1]) : profile(argv[1])).then(function (done) {
+  if (mode === 'readback' || mode === 'profile' || mode === 'batch') {
+    (mode === 'readback' ? readback(argv[1]) : mode === 'profile' ? profile(argv[1]) : batch(argv[1])).then(function (done) {
       process.stdout.write(JSON.stringify({ ok: true, checks: done }) + '\n');
     }, function (e) {
       process.stderr.write(String(e && e.stack ? e.stack : e) + '\n');
@@ -635,7 +647,6 @@ export function main(argv: string[]): void {
   else if (mode === 'prefill') done = prefill(argv[1]);
   else if (mode === 'promptprep') done = promptPrep(argv[1]);
   else if (mode === 'linear') done = linear(argv[1]);
-  else if (mode === 'batch') done = batch(argv[1]);
   else fail(`usage: run.js cpu | layer <dir> | prefill <dir> | promptprep <dir> | head <dir> | linear <dir> | batch <dir> | readback <dir> | profile`);
   process.stdout.write(JSON.stringify({ ok: true, checks: done }) + '\n');
 }

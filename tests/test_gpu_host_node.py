@@ -209,7 +209,9 @@ def test_continuous_batching_through_ts_host(tmp_path):
     as one attnStep over the active sequences: a local head_dim-256 producer (window 40), a global
     head_dim-512 producer, and a local consumer of layer 0 that projects only q and reads the row its
     producer stored earlier in the same token. Every attnOut is checked against the oracle's decode
-    chain over the cache the oracle keeps for each sequence, within max-abs 2e-3."""
+    chain over the cache the oracle keeps for each sequence, within max-abs 2e-3. The loop runs with the
+    per-pass profiler on (a forward per token step): the report must hold one attn.decodeFused sample
+    per attnStep launch, so timing changes no result."""
     announce("TS host continuous batching")
     layers = [dict(slidingWindow=40, theta=1e4, applyDivisor=0, kvSource=0, headDim=256),
               dict(slidingWindow=0, theta=1e6, applyDivisor=1, kvSource=1, headDim=512),
