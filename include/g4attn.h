@@ -84,7 +84,8 @@ int g4_readback_finish(g4_readback* handle, void* host_dst);
  * begin_pass opens a pass on the calling thread (one at a time): every kernel
  * the library launches from this thread until end_pass carries the pair on its
  * own dispatch, the first kernel's start in `slot` and the last one's end in
- * slot+1 (no packet is added between kernels). write instead records a marker
+ * slot+1 (no packet is added between kernels); keep passes closed around code
+ * under HIP graph capture. write instead records a marker
  * for one slot on `stream`, in stream order (a few microseconds of GPU time
  * each). resolve waits, from any thread, for n_pairs pairs from slot `first`
  * and writes ns_out[i] = the time from slot first+2i to slot first+2i+1 in
