@@ -41,8 +41,11 @@ per step (K/V rows attended, f16, read once for all query heads; q read;
 attnOut written) over wall time per step. `roofline` is the dominant kernel
 (k_attn_step), timed with HIP events on its stream; its `traffic` comes from
 the committed rocprofv3 counter summary of the same workload. `decode_loop`
-advances the position every step and re-prepares every entry (host partition,
-RoPE factors, table uploads) inside the timed region. `cpu_baseline` runs the
+advances the position every step inside the timed region: the prepared plan
+moves on the host (g4_attn_step_advance; the kernel evaluates the new
+position's RoPE factors) and is prepared again every 32 tokens; its
+`prepare_every_token` figure re-prepares every entry every token instead (host
+partition, RoPE factors, table uploads). `cpu_baseline` runs the
 oracle (the WGSL-semantics C restatement of the reference's six kernels, f32
 caches, full-length score/softmax/output on every layer as the WGSL does) on
 the host.
@@ -68,6 +71,7 @@ NQH, NKH, HD = 8, 1, 256
 EPS = 1e-6
 BASE_SEED = 20261201
 DEFAULT_WORKLOAD = "stack32k"
+REPLAN_TOKENS = 32  # decode loop: a plan advances on the host and is prepared again every this many tokens
 # the prefill kernel at head_dim 256 (G4_PREFILL_PP=0 selects the one-wave-per-SIMD form)
 PREFILL_KERNEL = "k_prefill_dma" if os.environ.get("G4_PREFILL_PP", "1") == "0" else "k_prefill_pp"
 
@@ -188,25 +192,33 @@ class CacheSet:
             idx = [i for i, it in enumerate(self.items) if it["hd"] == hd]
             arr = ops.make_step_entries([self.items[i] for i in idx], NQH, NKH, hd)
             ws = torch.empty(ops.step_workspace_bytes(len(idx), NQH, NKH, hd), dtype=torch.uint8, device=dev)
-            self.groups.append([hd, idx, arr, ws, ops.attn_step_prepare(arr, NQH, NKH, hd, ws)])
+            # [head_dim, entry indexes, ctypes entries, workspace, plan, tokens advanced since its prepare]
+            self.groups.append([hd, idx, arr, ws, ops.attn_step_prepare(arr, NQH, NKH, hd, ws), 0])
         self.layer_plans = None
 
     def run(self, ops, ev=None):
-        for gi, (hd, idx, arr, ws, plan) in enumerate(self.groups):
+        for gi, (hd, idx, arr, ws, plan, _) in enumerate(self.groups):
             if ev is None:
                 ops.attn_step_run(plan)
             else:
                 ops.attn_step_run_attention_timed(plan, ev[gi][0], ev[gi][1])
                 ops.attn_step_run_merge(plan)
 
-    def advance(self, ops):
-        """The next token: every entry one row longer, re-prepared (the engine rewrites the position,
-        slot and seq_len uniforms every token, src/engine.ts:1967-1987)."""
+    def advance(self, ops, replan_every):
+        """The next token: every entry one row longer (the engine rewrites the position, slot and seq_len
+        uniforms every token, src/engine.ts:1967-1987). The prepared plan advances on the host alone
+        (g4_attn_step_advance: nothing is enqueued) and is prepared again every `replan_every` tokens
+        (1: a full prepare every token: partition, RoPE factors, table upload)."""
         for g in self.groups:
-            hd, idx, arr, ws, plan = g
+            hd, idx, arr, ws, plan, since = g
             for f in self._fields(arr):  # seq_len and position of every entry, one vectorised bump each
                 f += 1
-            g[4] = ops.attn_step_prepare(arr, NQH, NKH, hd, ws)
+            if since + 1 < replan_every:
+                ops.attn_step_advance(plan, 1)
+                g[5] = since + 1
+            else:
+                g[4] = ops.attn_step_prepare(arr, NQH, NKH, hd, ws)
+                g[5] = 0
 
     @staticmethod
     def _fields(arr):
@@ -278,7 +290,7 @@ def run_gpu(spec, args, decode_loop=False):
     sets = args.sets or max(1, math.ceil(2 * MALL_BYTES / max(per_step, 1)) + 1)
     if per_step < 4 << 20:
         sets = 1  # tiny workloads are launch-bound; rotating sets changes nothing
-    loop_tokens = args.warmup + args.steps if decode_loop else 0
+    loop_tokens = 2 * (args.warmup + args.steps) if decode_loop else 0  # two loops append rows
     log(f"workload {spec['name']}: {len(spec['layers'])} entries, {per_step / 1e6:.1f} MB/step, {sets} cache sets")
     t0 = time.time()
     csets = [CacheSet(spec, s, dev, torch, ops, synth, e2b, extra_rows=loop_tokens) for s in range(sets)]
@@ -325,26 +337,29 @@ def run_gpu(spec, args, decode_loop=False):
                   sets=sets, bytes=per_step, launches=n_groups)
 
     if decode_loop:
-        # A position-advancing decode loop: every step re-prepares every entry one row further (host
-        # partition, RoPE factors, pinned-ring table uploads) and runs it, all inside the timed region.
-        for i in range(args.warmup):
-            cs = csets[i % sets]
-            cs.advance(ops)
-            cs.run(ops)
-        torch.cuda.synchronize()
-        t2 = time.perf_counter()
-        host = 0.0
-        for i in range(args.steps):
-            cs = csets[(args.warmup + i) % sets]
-            h0 = time.perf_counter()
-            cs.advance(ops)
-            host += time.perf_counter() - h0
-            cs.run(ops)
-        torch.cuda.synchronize()
-        result["loop_us"] = (time.perf_counter() - t2) / args.steps * 1e6
-        result["loop_prepare_us"] = host / args.steps * 1e6
-        log(f"decode loop (prepare + run per token): {result['loop_us']:.2f} us/token, prepare "
-            f"{result['loop_prepare_us']:.2f} us/token on the host")
+        # Position-advancing decode loops, all inside the timed region: every token every entry is one
+        # row further. "advance": the plan advances on the host (g4_attn_step_advance) and is prepared
+        # again every REPLAN_TOKENS tokens; "prepare every token": host partition, RoPE factors and
+        # pinned-ring table upload per token.
+        for key, every in (("loop", REPLAN_TOKENS), ("loop_each", 1)):
+            for i in range(args.warmup):
+                cs = csets[i % sets]
+                cs.advance(ops, every)
+                cs.run(ops)
+            torch.cuda.synchronize()
+            t2 = time.perf_counter()
+            host = 0.0
+            for i in range(args.steps):
+                cs = csets[(args.warmup + i) % sets]
+                h0 = time.perf_counter()
+                cs.advance(ops, every)
+                host += time.perf_counter() - h0
+                cs.run(ops)
+            torch.cuda.synchronize()
+            result[f"{key}_us"] = (time.perf_counter() - t2) / args.steps * 1e6
+            result[f"{key}_prepare_us"] = host / args.steps * 1e6
+            log(f"decode loop ({'advance, prepare every %d tokens' % every if every > 1 else 'prepare every token'}):"
+                f" {result[f'{key}_us']:.2f} us/token, host {result[f'{key}_prepare_us']:.2f} us/token")
 
     # The engine's issue order: one single-entry step (attention + merge) per layer, replayed as a HIP graph;
     # then the same with each layer's projections around it. Each replay is queued behind a short spin kernel,
@@ -743,8 +758,16 @@ def decode_line(name, args, decode_loop):
         line["decode_loop"] = {"us_per_token": round(r["loop_us"], 2),
                                "prepare_us_per_token": round(r["loop_prepare_us"], 2),
                                "GBps": round(r["bytes"] / (r["loop_us"] * 1e-6) / 1e9, 1),
-                               "what": "position advanced every token; every entry re-prepared (host partition, "
-                                       "RoPE factors, pinned-ring uploads) and run, inside the timed region"}
+                               "vs_replay": round(r["loop_us"] / (ms_per_step * 1e3), 4),
+                               "what": f"position advanced every token inside the timed region: the prepared plan "
+                                       f"advanced on the host (g4_attn_step_advance, RoPE factors of the new position "
+                                       f"evaluated in the kernel) and prepared again every {REPLAN_TOKENS} tokens; "
+                                       "prepare_us_per_token is the host time per token (Python included)",
+                               "prepare_every_token": {
+                                   "us_per_token": round(r["loop_each_us"], 2),
+                                   "prepare_us_per_token": round(r["loop_each_prepare_us"], 2),
+                                   "what": "every entry prepared again every token (host partition, RoPE factors, "
+                                           "pinned-ring table upload) and run"}}
     if "sequential_us" in r:
         line["layer_sequential_us_per_token"] = round(r["sequential_us"], 2)
     if "chain_us" in r:

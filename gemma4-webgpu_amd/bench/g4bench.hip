@@ -17,6 +17,8 @@
 // one g4_attn_step_prepare_layers per head_dim group per token, then each layer's attention and
 // merge launches in turn), layers_each (the same order with one g4_attn_step_prepare per layer), chain
 // and chain_each (those two orders with each layer's q/k/v projection and o_proj around its attention).
+// advance, layers_adv, chain_adv: loop, layers and chain with each plan advanced on the host every token
+// (g4_attn_step_advance) and prepared again every 32 tokens.
 //
 // `prefill4k` runs the causal MFMA prefill of a 4096-token prompt for one
 // global layer and one 512-window local layer, as 512-token chunks (16
@@ -428,6 +430,12 @@ int main(int argc, char** argv) {
     // chain / chain_each: the same two orders with the layer's projections around its attention (q/k/v in
     // one g4_linear_f16 launch, then o_proj with the merge folded in, g4_attn_step_run_out; f16 weights of
     // E2B's shapes, hidden 1536, distinct per layer), as the engine runs a token.
+    // advance / layers_adv / chain_adv: loop / layers / chain with the plans advanced every token
+    // (g4_attn_step_advance, host only) and prepared again every kReplan tokens.
+    const std::string mode_name = mode;
+    const bool advancing = mode == "advance" || mode == "layers_adv" || mode == "chain_adv";
+    if (advancing) mode = mode == "advance" ? "loop" : mode == "layers_adv" ? "layers" : "chain";
+    constexpr int kReplan = 32;
     const bool chain = mode == "chain" || mode == "chain_each";
     const bool token_loop = mode == "loop" || mode == "layers" || mode == "layers_each" || chain;
     if (mode != "step" && !token_loop && !all256) {
@@ -470,6 +478,7 @@ int main(int argc, char** argv) {
         void* ws = nullptr;
         void* step_ws[2] = {nullptr, nullptr};
         void* prep_table = nullptr;
+        int since_prepare = -1;  // tokens since the last prepare (-1: never prepared)
     };
     std::vector<Set> S(sets);
     size_t ws_bytes = 0;
@@ -618,7 +627,18 @@ int main(int argc, char** argv) {
                     e.seq_len++;
                     e.position++;
                 }
-            for (int h = 0; h < 2; h++) {
+            const bool replan = !advancing || s.since_prepare < 0 || s.since_prepare + 1 >= kReplan;
+            s.since_prepare = replan ? 0 : s.since_prepare + 1;
+            for (int h = 0; h < 2 && !replan; h++) {  // the next token of the prepared plans, on the host
+                if (!s.has_step[h]) continue;
+                if (mode == "loop") {
+                    CK(g4_attn_step_advance(&s.step_plan[h], 1));
+                    CK(g4_attn_step_run(&s.step_plan[h], st));
+                } else {
+                    for (g4_decode_plan& p : s.layer_plans[h]) CK(g4_attn_step_advance(&p, 1));
+                }
+            }
+            for (int h = 0; h < 2 && replan; h++) {
                 if (!s.has_step[h]) continue;
                 const unsigned hd = h ? 512 : 256;
                 const uint32_t n = (uint32_t)s.steps[h].size();
@@ -688,7 +708,7 @@ int main(int argc, char** argv) {
     float ms = 0;
     HK(hipEventElapsedTime(&ms, a, b));
     const double us = ms * 1e3 / iters;
-    printf("%s [%s]: %.2f us/step, %.1f GB/s algorithmic (%d iterations)\n", wl.c_str(), mode.c_str(), us,
+    printf("%s [%s]: %.2f us/step, %.1f GB/s algorithmic (%d iterations)\n", wl.c_str(), mode_name.c_str(), us,
            step_bytes / (us * 1e3), iters);
     return 0;
 }

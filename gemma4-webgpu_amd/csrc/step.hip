@@ -39,6 +39,7 @@
 
 #include <hip/hip_ext.h>
 
+#include <algorithm>
 #include <type_traits>
 #include <utility>
 #include <vector>
@@ -80,9 +81,16 @@ struct StepSmem {
 // batch of scalar loads. Reading fields where used, or selecting a field's
 // address by a value loaded before, chains dependent scalar loads (measured:
 // six round trips, ~4.6 us before a workgroup's first vector load).
+//
+// `adv`: tokens the plan has been advanced since it was prepared (0 for a plan
+// as prepared). Every entry then ends adv rows later at position + adv, its
+// parts move with its first attended row (step_part_rows), and the RoPE
+// factors are evaluated here from the inverse frequencies of the entry's set,
+// in f64 rounded to f32 as the host evaluates the prepared position's.
 template <int W, int HD>
 __global__ __launch_bounds__(64 * W, HD == 256 ? 8 / W : 1) void k_attn_step(
-    const StepWorkDev* __restrict__ work, float* part_ml, float* part_o, uint32_t num_kv_heads, uint32_t group) {
+    const StepWorkDev* __restrict__ work, float* part_ml, float* part_o, uint32_t num_kv_heads, uint32_t group,
+    uint32_t adv) {
     const StepArgs a{work, num_kv_heads, group, part_ml, part_o};
     using D = DecodeDims<HD>;
     constexpr int J = HD / 64;                          // elements of a head per lane
@@ -100,12 +108,14 @@ __global__ __launch_bounds__(64 * W, HD == 256 ? 8 / W : 1) void k_attn_step(
 
     const StepWorkDev wk = work[blockIdx.x];
     const StepEntryDev& ent = wk.ent;
-    const unsigned key_end = ent.key_end;
-    const unsigned k0 = wk.row_begin;
+    const unsigned key_end = ent.key_end + adv;
+    const unsigned position = ent.position + adv;
+    const StepRows rows = step_part_rows(wk.row_begin, wk.row_end, ent.key_end, ent.window, adv);
+    const unsigned k0 = rows.begin;
     // This workgroup holds the current token's row, and computes it (unless it is already cached).
-    const bool has_new = wk.row_end == key_end && !(ent.flags & kRowCached);
+    const bool has_new = rows.end == key_end && !(ent.flags & kRowCached);
     const unsigned new_row = key_end - 1;
-    const unsigned k1t = has_new ? new_row : wk.row_end;  // rows read from the cache: [k0, k1t)
+    const unsigned k1t = has_new ? new_row : rows.end;  // rows read from the cache: [k0, k1t)
     const unsigned nkeys = k1t - k0;
     const unsigned last = nkeys ? k1t - 1 : k0;  // loads are clamped to it (k0 < key_end: in the cache)
 
@@ -130,10 +140,13 @@ __global__ __launch_bounds__(64 * W, HD == 256 ? 8 / W : 1) void k_attn_step(
         constexpr bool kTile = decltype(tile_tag)::value;
         // ---- small operands first, then the first tile ----
         // f16 values stay unconverted until used. RoPE factors of this lane's
-        // pairs from the host table; absent tables are replaced by valid dummy
-        // addresses (the values are not used).
+        // pairs from the host-evaluated set (a plan as prepared); otherwise the
+        // pair's inverse frequency from the set, or the divisor to evaluate it
+        // with. Absent tables are replaced by valid dummy addresses (the values
+        // are not used).
         const float* rcs = ent.rope_cs;
-        const float* rsrc = rcs ? rcs : ent.q;
+        const bool host_cs = rcs && adv == 0;  // uniform
+        const float* rsrc = host_cs ? rcs : ent.q;
         RopeLane<PJ> rl;
 #pragma unroll
         for (int p = 0; p < PJ; p++) {
@@ -141,8 +154,11 @@ __global__ __launch_bounds__(64 * W, HD == 256 ? 8 / W : 1) void k_attn_step(
             rl.s[p] = ldg<float>(rsrc + HD / 2 + lane + 64 * p);
         }
         const unsigned pair = threadIdx.x % (HD / 2);  // pair evaluated by this thread otherwise
-        const unsigned apply_divisor = ent.apply_divisor;
+        const bool apply_divisor = ent.flags & kApplyDivisor;
         const uint32_t fbits = ldg<uint16_t>((apply_divisor ? ent.rope_freqs : ent.q_weight) + pair);
+        float inv_l[PJ];  // this lane's pairs' inverse frequencies from the set (advanced plans)
+#pragma unroll
+        for (int p = 0; p < PJ; p++) inv_l[p] = ldg<float>((rcs ? rcs + HD : ent.q) + lane + 64 * p);
         float xq[kQPerWave][J];
 #pragma unroll
         for (int r = 0; r < kQPerWave; r++) {
@@ -175,10 +191,14 @@ __global__ __launch_bounds__(64 * W, HD == 256 ? 8 / W : 1) void k_attn_step(
         __builtin_amdgcn_sched_barrier(0);  // keep every request above ahead of the arithmetic below
 
         // ---- q heads straight into the score operand; the current row's k and v ----
-        if (!rcs) {  // uniform: one pair per thread, the reference's expressions with f64
+        if (rcs && !host_cs) {  // uniform: each lane evaluates its own pairs at the advanced position,
+            // cos and sin of the f32 angle in f64 rounded to f32, as the host evaluates a prepared one
+#pragma unroll
+            for (int p = 0; p < PJ; p++) f64_cos_sin((float)position * inv_l[p], rl.c[p], rl.s[p]);
+        } else if (!rcs) {  // uniform: one pair per thread, the reference's expressions with f64
             // transcendentals; division by 1 is exact, so the load above stays unconditional
             const float freq = rope_inv_freq(pair, HD, ent.theta, 1u, apply_divisor ? h2f((uint16_t)fbits) : 1.0f);
-            const float ang = (float)ent.position * freq;
+            const float ang = (float)position * freq;
             float c, sn;
             f64_cos_sin(ang, c, sn);
             if (threadIdx.x < HD / 2) {
@@ -280,20 +300,29 @@ int step_env(const char* name, int dflt) {
 struct StepPlanRep {
     char* tables;   // the plan's tables region (work items | merge table | entry table | RoPE factors)
     char* part_ml;  // its partial records: (m, l) pairs, then the o rows at step_part_o_offset()
-    uint32_t n_entries;
-    uint32_t n_wgs;
-    uint32_t num_kv_heads;
-    uint32_t group;
-    uint32_t n_merge;    // entries spanning more than one workgroup (listed in the merge table)
-    uint32_t max_parts;
-    uint32_t waves;      // waves per workgroup of the attention kernel (4 or 8)
-    uint32_t head_dim;   // 256 or 512
+    uint16_t n_entries;     // <= 65535 (checked by the planner)
+    uint16_t num_kv_heads;  // <= 65535
+    uint16_t n_wgs;         // <= max(n_entries, kStepMaxWgs)
+    uint16_t n_merge;       // entries spanning more than one workgroup (listed in the merge table)
+    uint16_t max_parts;     // <= kStepMaxWgs
+    uint8_t group;          // <= kMaxGroup
+    uint8_t waves;          // waves per workgroup of the attention kernel (4 or 8)
+    uint32_t head_dim;      // 256 or 512
     uint32_t magic;
     uint32_t off_merge;  // byte offsets of the merge table, the entry table and the RoPE factors in the tables region
     uint32_t off_rope;
     uint32_t off_ents;
+    uint32_t adv;        // tokens advanced since the prepare (g4_attn_step_advance)
+    uint32_t max_rows;   // the largest seq_len of the prepared entries
+    uint32_t max_pos;    // the largest position of the prepared entries
 };
 static_assert(sizeof(StepPlanRep) <= sizeof(g4_decode_plan), "plan size");
+static_assert(kStepMaxWgs <= 65535 && kMaxGroup <= 255, "plan field widths");
+
+// A plan advances at most this many tokens between prepares: beyond it, the
+// part holding the last row of a full-attention entry would carry a growing
+// share of the rows (32 tokens add one 32-row tile to it).
+constexpr uint32_t kStepMaxAdvance = 4096;
 
 }  // namespace
 
@@ -323,11 +352,28 @@ static const StepTuning& step_tuning() {
     return tune;
 }
 
-static void write_plan(g4_decode_plan* plan, char* tables, char* part_ml, uint32_t n_entries, uint32_t num_kv_heads,
-                       uint32_t G, uint32_t head_dim, const StepPlanHost& ph) {
-    StepPlanRep r = {tables,   part_ml,      n_entries, ph.n_wgs,  num_kv_heads,           G,
-                     ph.n_merge, ph.max_parts, ph.waves, head_dim, kStepMagic, (uint32_t)ph.off_merge,
-                     (uint32_t)ph.off_rope, (uint32_t)ph.off_ents};
+static void write_plan(g4_decode_plan* plan, char* tables, char* part_ml, const g4_step_entry* entries,
+                       uint32_t n_entries, uint32_t num_kv_heads, uint32_t G, uint32_t head_dim,
+                       const StepPlanHost& ph) {
+    StepPlanRep r = {};
+    r.tables = tables;
+    r.part_ml = part_ml;
+    r.n_entries = (uint16_t)n_entries;
+    r.num_kv_heads = (uint16_t)num_kv_heads;
+    r.n_wgs = (uint16_t)ph.n_wgs;
+    r.n_merge = (uint16_t)ph.n_merge;
+    r.max_parts = (uint16_t)ph.max_parts;
+    r.group = (uint8_t)G;
+    r.waves = (uint8_t)ph.waves;
+    r.head_dim = head_dim;
+    r.magic = kStepMagic;
+    r.off_merge = (uint32_t)ph.off_merge;
+    r.off_rope = (uint32_t)ph.off_rope;
+    r.off_ents = (uint32_t)ph.off_ents;
+    for (uint32_t i = 0; i < n_entries; i++) {
+        r.max_rows = std::max(r.max_rows, entries[i].seq_len);
+        r.max_pos = std::max(r.max_pos, entries[i].position);
+    }
     memset(plan, 0, sizeof *plan);
     memcpy(plan, &r, sizeof r);
 }
@@ -351,7 +397,7 @@ int g4_attn_step_prepare(const g4_step_entry* entries, uint32_t n_entries, uint3
     if (rc) return fail(rc, "%s", err);
     rc = stage_upload(ws + L.tables, ph.blob.data(), ph.blob.size(), as_stream(stream));  // the tables in one copy
     if (rc) return rc;
-    write_plan(plan, ws + L.tables, ws + L.part_ml, n_entries, num_kv_heads, G, head_dim, ph);
+    write_plan(plan, ws + L.tables, ws + L.part_ml, entries, n_entries, num_kv_heads, G, head_dim, ph);
     return G4_OK;
 }
 
@@ -404,7 +450,8 @@ int g4_attn_step_prepare_layers(const g4_step_entry* entries, uint32_t n_layers,
         blob.resize(at + bytes);
         memcpy(blob.data() + at, ph.blob.data(), ph.blob.size());
         memset(blob.data() + at + ph.blob.size(), 0, bytes - ph.blob.size());
-        write_plan(&plans[i], tables, records + (size_t)i * records_one, E, num_kv_heads, G, head_dim, ph);
+        write_plan(&plans[i], tables, records + (size_t)i * records_one, entries + (size_t)i * E, E, num_kv_heads, G,
+                   head_dim, ph);
     }
     rc = stage_upload(ws, blob.data(), blob.size(), as_stream(stream));  // every layer's tables in one copy
     if (rc) {
@@ -434,23 +481,49 @@ static int launch_attention(const g4_decode_plan* plan, void* stream, hipEvent_t
     a.part_o = reinterpret_cast<float*>(r.part_ml + step_part_o_offset(r.num_kv_heads, r.group));
     const dim3 grid(r.n_wgs, r.num_kv_heads);
     hipStream_t st = as_stream(stream);
+    const uint32_t adv = r.adv;
     if (r.head_dim == 512) {
-        if (start || stop) hipExtLaunchKernelGGL((k_attn_step<4, 512>), grid, dim3(256), 0, st, start, stop, 0, a.work, a.part_ml, a.part_o,
-                                  a.num_kv_heads, a.group);
-        else G4_LAUNCH((k_attn_step<4, 512>), grid, dim3(256), 0, st, a.work, a.part_ml, a.part_o, a.num_kv_heads,
-                               a.group);
+        if (start || stop)
+            hipExtLaunchKernelGGL((k_attn_step<4, 512>), grid, dim3(256), 0, st, start, stop, 0, a.work, a.part_ml,
+                                  a.part_o, a.num_kv_heads, a.group, adv);
+        else
+            G4_LAUNCH((k_attn_step<4, 512>), grid, dim3(256), 0, st, a.work, a.part_ml, a.part_o, a.num_kv_heads,
+                      a.group, adv);
     } else if (r.waves == 8) {
-        if (start || stop) hipExtLaunchKernelGGL((k_attn_step<8, 256>), grid, dim3(512), 0, st, start, stop, 0, a.work, a.part_ml, a.part_o,
-                                  a.num_kv_heads, a.group);
-        else G4_LAUNCH((k_attn_step<8, 256>), grid, dim3(512), 0, st, a.work, a.part_ml, a.part_o, a.num_kv_heads,
-                               a.group);
+        if (start || stop)
+            hipExtLaunchKernelGGL((k_attn_step<8, 256>), grid, dim3(512), 0, st, start, stop, 0, a.work, a.part_ml,
+                                  a.part_o, a.num_kv_heads, a.group, adv);
+        else
+            G4_LAUNCH((k_attn_step<8, 256>), grid, dim3(512), 0, st, a.work, a.part_ml, a.part_o, a.num_kv_heads,
+                      a.group, adv);
     } else {
-        if (start || stop) hipExtLaunchKernelGGL((k_attn_step<4, 256>), grid, dim3(256), 0, st, start, stop, 0, a.work, a.part_ml, a.part_o,
-                                  a.num_kv_heads, a.group);
-        else G4_LAUNCH((k_attn_step<4, 256>), grid, dim3(256), 0, st, a.work, a.part_ml, a.part_o, a.num_kv_heads,
-                               a.group);
+        if (start || stop)
+            hipExtLaunchKernelGGL((k_attn_step<4, 256>), grid, dim3(256), 0, st, start, stop, 0, a.work, a.part_ml,
+                                  a.part_o, a.num_kv_heads, a.group, adv);
+        else
+            G4_LAUNCH((k_attn_step<4, 256>), grid, dim3(256), 0, st, a.work, a.part_ml, a.part_o, a.num_kv_heads,
+                      a.group, adv);
     }
     G4_CHECK_LAUNCH("attnStep");
+    return G4_OK;
+}
+
+int g4_attn_step_advance(g4_decode_plan* plan, uint32_t tokens) {
+    StepPlanRep r;
+    int rc = step_plan(plan, &r);
+    if (rc) return rc;
+    const uint64_t adv = (uint64_t)r.adv + tokens;
+    if (adv > kStepMaxAdvance)
+        return fail(G4_ERANGE, "attnStepAdvance: %llu tokens since the prepare (max %u): prepare again",
+                    (unsigned long long)adv, kStepMaxAdvance);
+    const uint64_t row_bytes = (uint64_t)r.num_kv_heads * r.head_dim * 2;
+    if ((r.max_rows + adv) * row_bytes > 0xffffffffull)
+        return fail(G4_EINVAL, "attnStepAdvance: a cache would exceed 4 GiB at %llu rows",
+                    (unsigned long long)(r.max_rows + adv));
+    if (r.max_pos + adv > 0xffffffffull)
+        return fail(G4_EINVAL, "attnStepAdvance: position %llu out of range", (unsigned long long)(r.max_pos + adv));
+    r.adv = (uint32_t)adv;
+    memcpy(plan, &r, sizeof r);
     return G4_OK;
 }
 

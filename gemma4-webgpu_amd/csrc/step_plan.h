@@ -32,6 +32,11 @@ constexpr unsigned kStepOneWgTiles = 16;  // one workgroup per CU up to this man
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// Floats of one RoPE set in the tables region: the factors at the plan's
+// position [cos x hd/2][sin x hd/2], then the inverse frequencies [hd/2] that
+// the kernel evaluates later positions from (advanced plans).
+inline constexpr uint64_t rope_set_floats(uint64_t hd) { return hd + hd / 2; }
+
 // The tables region holds, packed by each prepare and uploaded in one copy,
 // the work table, the merge table, the entry table (every entry's attnOut and
 // records, read by the merge folded into the output projection) and the RoPE
@@ -51,8 +56,9 @@ inline StepLayout step_layout(uint64_t n, uint64_t nkh, uint64_t group, uint64_t
     const uint64_t max_items = n > kStepMaxWgs ? n : kStepMaxWgs;
     const uint64_t recs = (uint64_t)kStepMaxWgs * nkh * group;
     size_t off = 0;
-    L.tables = off;  // work items, merge entries, all entries, and at most one [cos x hd/2][sin x hd/2] set per entry
-    off += align256(max_items * sizeof(StepWorkDev)) + 2 * align256(n * sizeof(DecodeEntryDev)) + align256(n * hd * 4);
+    L.tables = off;  // work items, merge entries, all entries, and at most one RoPE set per entry
+    off += align256(max_items * sizeof(StepWorkDev)) + 2 * align256(n * sizeof(DecodeEntryDev)) +
+           align256(n * rope_set_floats(hd) * 4);
     L.part_ml = off;
     off += step_part_o_offset(nkh, group);
     L.part_o = off;
@@ -107,21 +113,51 @@ struct StepPlanHost {
     std::vector<uint32_t> rope_set;      // its set in this blob, or ~0 when an earlier plan placed it
 };
 
+// Hash of an (inverse-frequency table, position) pair.
+inline uint64_t rope_key_hash(const float* table, uint32_t position) {
+    return (reinterpret_cast<uintptr_t>(table) >> 4) * 0x9E3779B97F4A7C15ull ^ position * 0xC2B2AE3D27D4EB4Full;
+}
+
 // RoPE factor sets already placed by the earlier plans of one upload (the
 // layers of a token planned one by one): a later plan that needs the same
 // (inverse-frequency table, position) pair points at that set instead of
-// carrying its own.
+// carrying its own. Looked up through open addressing (slot: 0 = empty, else
+// index + 1; at least twice as many slots as keys), so a batched prepare of
+// many sequences and layers stays linear in its entries.
 struct StepRopeShare {
     std::vector<std::pair<const float*, uint32_t>> keys;
     std::vector<const float*> dev;
+    std::vector<uint32_t> slot;
     void clear() {
         keys.clear();
         dev.clear();
+        slot.assign(64, 0u);
     }
     const float* find(const std::pair<const float*, uint32_t>& k) const {
-        for (size_t i = 0; i < keys.size(); i++)
-            if (keys[i] == k) return dev[i];
-        return nullptr;
+        if (slot.empty()) return nullptr;
+        const size_t mask = slot.size() - 1;
+        for (size_t i = (size_t)(rope_key_hash(k.first, k.second) >> 32) & mask;; i = (i + 1) & mask) {
+            const uint32_t v = slot[i];
+            if (!v) return nullptr;
+            if (keys[v - 1] == k) return dev[v - 1];
+        }
+    }
+    void add(const std::pair<const float*, uint32_t>& k, const float* d) {
+        if (2 * (keys.size() + 1) > slot.size()) {  // grow, then re-insert every key
+            slot.assign(slot.empty() ? 64 : 2 * slot.size(), 0u);
+            for (size_t j = 0; j < keys.size(); j++) place(j);
+        }
+        keys.push_back(k);
+        dev.push_back(d);
+        place(keys.size() - 1);
+    }
+
+  private:
+    void place(size_t j) {
+        const size_t mask = slot.size() - 1;
+        size_t i = (size_t)(rope_key_hash(keys[j].first, keys[j].second) >> 32) & mask;
+        while (slot[i]) i = (i + 1) & mask;
+        slot[i] = (uint32_t)j + 1;
     }
 };
 
@@ -195,7 +231,7 @@ inline void rope_factors(const float* inv, uint32_t pos, uint32_t half, float* c
 // Open addressing over `slot` (a power of two, at least twice the pairs; 0 =
 // empty, else index + 1).
 inline uint32_t rope_pair_index(StepPlanHost& ph, const float* table, uint32_t position) {
-    const uint64_t h = (reinterpret_cast<uintptr_t>(table) >> 4) * 0x9E3779B97F4A7C15ull ^ position * 0xC2B2AE3D27D4EB4Full;
+    const uint64_t h = rope_key_hash(table, position);
     const size_t mask = ph.rope_slot.size() - 1;
     for (size_t i = (size_t)(h >> 32) & mask;; i = (i + 1) & mask) {
         const uint32_t v = ph.rope_slot[i];
@@ -272,12 +308,12 @@ inline int plan_step(const g4_step_entry* entries, uint32_t n_entries, uint32_t 
         d.key_end = s.seq_len;
         d.n_parts = 0;  // set by the partition
         d.position = s.position;
-        d.flags = (s.store_kv ? kStoreKv : 0u) | (cached ? kRowCached : 0u);
+        d.flags = (s.store_kv ? kStoreKv : 0u) | (cached ? kRowCached : 0u) | (s.apply_divisor ? kApplyDivisor : 0u);
         d.theta = s.theta;
-        d.apply_divisor = s.apply_divisor;
+        d.window = s.sliding_window;
         d.qscale = s.scale * kLog2e;
         d.eps = s.eps;
-        key_begin[i] = (s.sliding_window != 0 && s.seq_len > s.sliding_window) ? s.seq_len - s.sliding_window : 0;
+        key_begin[i] = step_key_begin(s.seq_len, s.sliding_window);
         tiles[i] = (s.seq_len - key_begin[i] + kTileKeys - 1) / kTileKeys;
         T += tiles[i];
         if (tiles[i] > max_tiles) max_tiles = tiles[i];
@@ -343,9 +379,9 @@ inline int plan_step(const g4_step_entry* entries, uint32_t n_entries, uint32_t 
     for (size_t k = 0; k < ph.rope_keys.size(); k++) {
         const float* shared = share ? share->find(ph.rope_keys[k]) : nullptr;
         ph.rope_set[k] = shared ? ~0u : (uint32_t)rope_sets++;
-        ph.rope_dev[k] = shared ? shared : rope_base + (size_t)ph.rope_set[k] * head_dim;
+        ph.rope_dev[k] = shared ? shared : rope_base + (size_t)ph.rope_set[k] * rope_set_floats(head_dim);
     }
-    ph.blob.resize(off_rope + rope_sets * head_dim * sizeof(float));
+    ph.blob.resize(off_rope + rope_sets * rope_set_floats(head_dim) * sizeof(float));
     char* blob = ph.blob.data();
     memset(blob + n_work * sizeof(StepWorkDev), 0, off_merge - n_work * sizeof(StepWorkDev));
     memset(blob + off_merge + n_merge * sizeof(DecodeEntryDev), 0, off_ents - off_merge - n_merge * sizeof(DecodeEntryDev));
@@ -357,12 +393,10 @@ inline int plan_step(const g4_step_entry* entries, uint32_t n_entries, uint32_t 
         float* rope = reinterpret_cast<float*>(blob + off_rope);
         for (size_t k = 0; k < ph.rope_keys.size(); k++) {
             if (ph.rope_set[k] == ~0u) continue;  // placed by an earlier plan
-            rope_factors(ph.rope_keys[k].first, ph.rope_keys[k].second, head_dim / 2,
-                         rope + (size_t)ph.rope_set[k] * head_dim);
-            if (share) {
-                share->keys.push_back(ph.rope_keys[k]);
-                share->dev.push_back(ph.rope_dev[k]);
-            }
+            float* set = rope + (size_t)ph.rope_set[k] * rope_set_floats(head_dim);
+            rope_factors(ph.rope_keys[k].first, ph.rope_keys[k].second, head_dim / 2, set);
+            memcpy(set + head_dim, ph.rope_keys[k].first, head_dim / 2 * sizeof(float));  // the inverse frequencies
+            if (share) share->add(ph.rope_keys[k], ph.rope_dev[k]);
         }
     }
     // Work items entry by entry (each with a copy of its entry), the merge

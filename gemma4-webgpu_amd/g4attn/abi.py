@@ -16,6 +16,7 @@ G4_EINVAL = -1
 G4_EHIP = -2
 G4_ENOSPC = -3
 G4_ENODEV = -4
+G4_ERANGE = -5
 
 
 class G4Error(RuntimeError):
@@ -175,6 +176,7 @@ SIGNATURES: dict[str, list] = {
     "g4_rope_inv_freq": [C.c_float, _U32, _U32, _P, _P, _P],
     "g4_rope_inv_freq_host": [C.c_float, _U32, _U32, _P, _P],
     "g4_attn_step_run": [C.POINTER(DecodePlan), _P],
+    "g4_attn_step_advance": [C.POINTER(DecodePlan), C.c_uint32],
     "g4_attn_step_run_attention": [C.POINTER(DecodePlan), _P],
     "g4_attn_step_run_merge": [C.POINTER(DecodePlan), _P],
     "g4_attn_step_run_out": [C.POINTER(DecodePlan), C.POINTER(LinearSeg), _U32, _P],

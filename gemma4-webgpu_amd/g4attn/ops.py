@@ -328,6 +328,13 @@ def attn_step_prepare_layers(entries, num_q_heads, num_kv_heads, head_dim, works
     return list(plans)
 
 
+def attn_step_advance(plan: DecodePlan, tokens: int = 1):
+    """The next token(s) of a prepared plan without a new prepare: host-only (nothing is enqueued);
+    every entry's seq_len and position grow by `tokens` (g4_attn_step_advance). Raises G4Error with
+    status G4_ERANGE past 4096 tokens since the prepare."""
+    abi.call("g4_attn_step_advance", C.byref(plan), tokens)
+
+
 def attn_step_run(plan: DecodePlan, stream=None):
     abi.call("g4_attn_step_run", C.byref(plan), _stream(stream))
 

@@ -47,6 +47,7 @@ extern "C" {
 #define G4_EHIP (-2)    /* HIP runtime error */
 #define G4_ENOSPC (-3)  /* caller-provided workspace too small */
 #define G4_ENODEV (-4)  /* no usable gfx950 device */
+#define G4_ERANGE (-5)  /* a prepared plan was advanced past its limit: prepare it again */
 
 /* Message for the last non-zero status returned on this thread. */
 const char* g4_last_error(void);
@@ -371,6 +372,25 @@ int g4_attn_step_prepare(const g4_step_entry* entries, uint32_t n_entries, uint3
                          uint32_t num_kv_heads, uint32_t head_dim, void* workspace, size_t workspace_bytes,
                          g4_decode_plan* plan, void* stream);
 int g4_attn_step_run(const g4_decode_plan* plan, void* stream);
+/* The next token without a new prepare: every entry of the plan (every
+ * layer of the stack, every sequence of the batch) moves `tokens` decode steps
+ * ahead, seq_len and position both growing by `tokens`, the current row being
+ * the new last one, as the engine rewrites the position, slot and seq_len
+ * uniforms every token (src/engine.ts:1967-1987). Host-only: it changes the
+ * plan and enqueues nothing, so a decode loop's per-token host work is this
+ * call and the launches. The plan keeps its partition: the part holding the
+ * last row takes the new rows of a full-attention entry, and a windowed
+ * entry's parts slide with its window. The RoPE factors of later positions
+ * are evaluated in the kernel from the inverse frequencies of the entry's
+ * rope_inv_freq_host table (uploaded by the prepare), in f64 rounded to f32,
+ * as the prepare evaluates the prepared position's; entries without a host
+ * table evaluate theirs in the kernel at every position anyway. The caches
+ * must hold the new rows, as for a prepare. At most 4096 tokens per prepare
+ * (G4_ERANGE beyond; prepare again to rebalance the parts: every 32 tokens
+ * add one 32-row tile to the part holding the last row of a full-attention
+ * entry). Works on plans of g4_attn_step_prepare and of
+ * g4_attn_step_prepare_layers (advance each layer's plan). */
+int g4_attn_step_advance(g4_decode_plan* plan, uint32_t tokens);
 /* The two launches of g4_attn_step_run, separately: the attention pass (one
  * kernel for all entries), then the log-sum-exp merge of entries spread over
  * more than one workgroup (nothing when there are none). */

@@ -93,7 +93,7 @@ static int check_layers(int line, const std::vector<g4_step_entry>& ents, uint32
                 continue;
             }
             const char* rp = reinterpret_cast<const char*>(rc);
-            if (rp < dev || rp + hd * 4 > dev + packed.size() || (size_t)(rp - dev) % 4)
+            if (rp < dev || rp + rope_set_floats(hd) * 4 > dev + packed.size() || (size_t)(rp - dev) % 4)
                 return bad(line, "layer RoPE pointer outside the packed tables");
             for (uint32_t j = 0; j < (uint32_t)i * E; j++)  // an earlier layer at the same pair owns the set
                 if (ents[j].rope_inv_freq_host == e.rope_inv_freq_host && ents[j].position == e.position) {
@@ -105,6 +105,7 @@ static int check_layers(int line, const std::vector<g4_step_entry>& ents, uint32
                 const double a = (double)((float)e.position * e.rope_inv_freq_host[p]);
                 if (f[p] != (float)cos(a) || f[hd / 2 + p] != (float)sin(a))
                     return bad(line, "layer RoPE factors differ from the C library's cos and sin");
+                if (f[hd + p] != e.rope_inv_freq_host[p]) return bad(line, "layer RoPE set's inverse frequencies");
             }
         }
     }
@@ -209,8 +210,10 @@ int main(int argc, char** argv) {
                     w.ent.k_cache != e.k_cache)
                     return bad(line, "entry copy differs from the entry");
                 const bool cached = !e.k;
-                if (cached != ((w.ent.flags & kRowCached) != 0) || (w.ent.flags & kStoreKv) != (e.store_kv ? kStoreKv : 0))
+                if (cached != ((w.ent.flags & kRowCached) != 0) || (w.ent.flags & kStoreKv) != (e.store_kv ? kStoreKv : 0) ||
+                    ((w.ent.flags & kApplyDivisor) != 0) != (e.apply_divisor != 0))
                     return bad(line, "flags");
+                if (w.ent.window != e.sliding_window) return bad(line, "window");
                 if (items.size() > 1) {
                     if (w.part >= ph.parts || slot_used[w.part]) return bad(line, "partial-record slot reused or out of range");
                     slot_used[w.part] = 1;
@@ -218,13 +221,15 @@ int main(int argc, char** argv) {
                 if (e.rope_inv_freq_host) {
                     const char* rc_ptr = reinterpret_cast<const char*>(w.ent.rope_cs);
                     const char* r0 = dev + L.tables + ph.off_rope;
-                    if (rc_ptr < r0 || rc_ptr + hd * 4 > r0 + rope_bytes || (rc_ptr - r0) % (hd * 4))
+                    const size_t set_bytes = rope_set_floats(hd) * 4;
+                    if (rc_ptr < r0 || rc_ptr + set_bytes > r0 + rope_bytes || (rc_ptr - r0) % set_bytes)
                         return bad(line, "RoPE factor pointer outside the factors");
                     const float* f = reinterpret_cast<const float*>(ph.blob.data() + (rc_ptr - (dev + L.tables)));
                     for (uint32_t p = 0; p < hd / 2; p++) {
                         const double a = (double)((float)e.position * e.rope_inv_freq_host[p]);
                         if (f[p] != (float)cos(a) || f[hd / 2 + p] != (float)sin(a))
                             return bad(line, "RoPE factors differ from the C library's cos and sin");
+                        if (f[hd + p] != e.rope_inv_freq_host[p]) return bad(line, "RoPE set's inverse frequencies");
                     }
                 } else if (w.ent.rope_cs) {
                     return bad(line, "RoPE factors without a host table");
@@ -232,6 +237,21 @@ int main(int argc, char** argv) {
                 next = w.row_end;
             }
             if (next != e.seq_len) return bad(line, "attended rows not fully covered");
+            // The plan advanced by a tokens (the kernel's step_part_rows): the parts still cover the
+            // entry's attended rows [key_begin(seq_len + a), seq_len + a) once, in order, and the part
+            // that ends there is the one that held the last row (the one that computes the new row).
+            for (uint32_t a : {1u, 2u, 31u, 32u, 33u, 100u, 511u, 512u, 513u, 1000u, 4096u}) {
+                const uint32_t ke = e.seq_len + a;
+                uint32_t at = step_key_begin(ke, e.sliding_window);
+                for (size_t j = 0; j < items.size(); j++) {
+                    const StepWorkDev& w = *items[j];
+                    const StepRows r = step_part_rows(w.row_begin, w.row_end, w.ent.key_end, w.ent.window, a);
+                    if (r.begin != at || r.end <= r.begin) return bad(line, "advanced rows not covered once, in order");
+                    if ((r.end == ke) != (j + 1 == items.size())) return bad(line, "advanced last row in another part");
+                    at = r.end;
+                }
+                if (at != ke) return bad(line, "advanced rows not fully covered");
+            }
             // the entry table: attnOut, parts, and the first record of a split entry
             if (etab[i].out != e.out || etab[i].n_splits != items.size() ||
                 (items.size() > 1 && etab[i].split_base != items[0]->part))
