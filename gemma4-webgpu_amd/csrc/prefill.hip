@@ -1526,11 +1526,12 @@ struct PrefillPlanRep {
     uint32_t max_parts;
     uint16_t num_q_heads;
     uint16_t num_kv_heads;
-    uint32_t head_dim;
+    uint16_t head_dim;     // 256 or 512
+    uint16_t dma;          // 1: the pipelined forms (V read as V^T blocks); 0: the register-staged form
     uint32_t magic;
     uint32_t off_work, off_merge, off_ml, off_o;  // workspace byte offsets (workspaces stay under 4 GiB)
     uint32_t off_vtc;      // V^T cache table (pipelined form)
-    uint32_t n_vtc;        // caches to transpose (0: the register-staged form)
+    uint32_t n_vtc;        // caches to transpose (none when every entry brings its V^T cache)
     uint32_t vt_blocks;    // their 32-key blocks, in total
 };
 static_assert(sizeof(PrefillPlanRep) <= sizeof(g4_decode_plan), "plan size");
@@ -1548,8 +1549,9 @@ struct Layout {
     size_t table, work, merge, ml, o, vtc, vt, total;
 };
 
-// The caches whose V the pipelined form transposes: one per distinct v_cache,
-// long enough for every entry on it.
+// The caches whose V the pipelined form transposes: one per distinct v_cache
+// of the entries without a V^T cache of their own, long enough for every
+// entry on it.
 struct VtPlan {
     std::vector<const uint16_t*> v;
     std::vector<uint32_t> rows, blocks, block0;
@@ -1577,9 +1579,10 @@ int build(const g4_prefill_entry* ents, uint32_t n, uint32_t nqh, uint32_t nkh, 
     const uint32_t G = nqh / nkh;
     *vp = VtPlan{};
     if (dma) {
-        vp->of.resize(n);
+        vp->of.assign(n, ~0u);
         for (uint32_t i = 0; i < n; i++) {
             const g4_prefill_entry& e = ents[i];
+            if (e.vt_cache) continue;  // read from the entry's own V^T cache
             const uint32_t end = e.start + e.n_tokens;
             uint32_t c = 0;
             while (c < vp->v.size() && vp->v[c] != e.v_cache) c++;
@@ -1630,8 +1633,9 @@ int build(const g4_prefill_entry* ents, uint32_t n, uint32_t nqh, uint32_t nkh, 
     }
     for (uint32_t i = 0; i < n; i++) {
         const g4_prefill_entry& e = ents[i];
+        const uint32_t vt_blocks = !dma ? 0u : e.vt_cache ? (e.vt_rows + kPfKeys - 1) / kPfKeys : vp->blocks[vp->of[i]];
         (*tab)[i] = PrefillEntryDev{e.q, e.k_cache, e.v_cache, e.out, e.n_tokens, e.start, e.sliding_window,
-                                    e.scale * kLog2e, nullptr, dma ? vp->blocks[vp->of[i]] : 0u, 0u};
+                                    e.scale * kLog2e, dma ? e.vt_cache : nullptr, vt_blocks, 0u};
         const uint32_t tiles = (uint32_t)(((uint64_t)e.n_tokens * G + kPfRows - 1) / kPfRows);
         for (uint32_t t = 0; t < tiles; t++) {
             uint32_t kb, ke;
@@ -1693,6 +1697,11 @@ int check(const g4_prefill_entry* ents, uint32_t n, uint32_t nqh, uint32_t nkh, 
             return fail(G4_EINVAL, "attnPrefill: entry %u out must be 16-byte aligned", i);
         if (e.n_tokens == 0) return fail(G4_EINVAL, "attnPrefill: entry %u has no tokens", i);
         if ((uint64_t)e.start + e.n_tokens > 0xffffffffull) return fail(G4_EINVAL, "attnPrefill: entry %u range", i);
+        if (e.vt_cache && (uint64_t)e.start + e.n_tokens > e.vt_rows)
+            return fail(G4_EINVAL, "attnPrefill: entry %u attends rows up to %u past its V^T cache's %u rows", i,
+                        e.start + e.n_tokens - 1, e.vt_rows);
+        if (e.vt_cache && !prefill_dma_enabled())
+            return fail(G4_EINVAL, "attnPrefill: entry %u: a V^T cache needs the pipelined form", i);
     }
     return G4_OK;
 }
@@ -1753,7 +1762,8 @@ int g4_attn_prefill_prepare(const g4_prefill_entry* entries, uint32_t n_entries,
         vtc[c] = VtCacheDev{vp.v[c], reinterpret_cast<uint16_t*>(ws + L.vt + vp.off[c]), vp.rows[c], vp.blocks[c],
                             vp.block0[c], 0u};
     if (dma)
-        for (uint32_t i = 0; i < n_entries; i++) tab[i].vt = vtc[vp.of[i]].vt;
+        for (uint32_t i = 0; i < n_entries; i++)
+            if (!entries[i].vt_cache) tab[i].vt = vtc[vp.of[i]].vt;
     std::vector<char> blob(L.vtc - L.table + vtc.size() * sizeof(VtCacheDev));
     memcpy(blob.data(), tab.data(), tab.size() * sizeof(PrefillEntryDev));
     memcpy(blob.data() + (L.work - L.table), work.data(), work.size() * sizeof(PrefillWorkDev));
@@ -1769,7 +1779,7 @@ int g4_attn_prefill_prepare(const g4_prefill_entry* entries, uint32_t n_entries,
     r.max_parts = max_parts;
     r.num_q_heads = (uint16_t)num_q_heads;  // at most 8 per kv head (checked); kv heads below 2^16
     r.num_kv_heads = (uint16_t)num_kv_heads;
-    r.head_dim = head_dim;
+    r.head_dim = (uint16_t)head_dim;
     r.magic = kPrefillMagic;
     r.off_work = (uint32_t)L.work;
     r.off_merge = (uint32_t)L.merge;
@@ -1778,6 +1788,7 @@ int g4_attn_prefill_prepare(const g4_prefill_entry* entries, uint32_t n_entries,
     r.off_vtc = (uint32_t)L.vtc;
     r.n_vtc = dma ? (uint32_t)vp.v.size() : 0u;
     r.vt_blocks = vp.total_blocks;
+    r.dma = dma ? 1u : 0u;
     memset(plan, 0, sizeof *plan);
     memcpy(plan, &r, sizeof r);
     return G4_OK;
@@ -1808,7 +1819,7 @@ static int prefill_run(const g4_decode_plan* plan, void* stream, hipEvent_t star
         G4_CHECK_LAUNCH("attnPrefill (V^T blocks)");
     }
     const dim3 grid(r.n_work, r.num_kv_heads, r.head_dim / 256);
-    if (r.n_vtc) {
+    if (r.dma) {
         if (hd512 && prefill_pp_enabled()) {  // grid z: the row half of each work item's query tile
             if (start_ev || stop_ev)
                 hipExtLaunchKernelGGL(k_prefill_pp512, grid, dim3(6 * 64), 0, st, start_ev, stop_ev, 0, a);

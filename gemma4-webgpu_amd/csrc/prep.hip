@@ -82,6 +82,32 @@ __global__ __launch_bounds__(kWG) void k_attn_prep_many(const g4_prep_layer* __r
 // the f16 rounding of what the reference kernels compute token by token.
 constexpr unsigned kPrepTokens = 2;  // measured: 1, 2, 4, 8 tokens -> 43.0, 40.6, 43.3, 52.4 us (prefill4k, both layers)
 
+// Workgroups per 32-row block (kPrepTokens tokens each), and the XCDs whose
+// workgroups a launch interleaves (workgroup b runs on XCD b % kXcds).
+constexpr unsigned kPrepPerBlock = 32 / kPrepTokens;
+constexpr unsigned kXcds = 8;
+
+// The chunk's positions [start, start + n) in whole 32-row blocks from
+// base = start rounded down to 32: workgroup b takes the kPrepTokens
+// positions at base + kPrepTokens * (block * kPrepPerBlock + m) (those inside
+// the chunk), where the workgroups of one block share an XCD: x = b % kXcds,
+// i = b / kXcds, block = (i / kPrepPerBlock) * kXcds + x, m = i % kPrepPerBlock.
+// So the V^T block a workgroup writes into is written by one XCD's workgroups
+// only (its lines are assembled in one L2). The grid has
+// kXcds * kPrepPerBlock * ceil(blocks / kXcds) workgroups; those past the
+// last block exit.
+__device__ __forceinline__ unsigned prep_first_pos(unsigned b, unsigned base) {
+    const unsigned x = b % kXcds, i = b / kXcds;
+    const unsigned block = (i / kPrepPerBlock) * kXcds + x, m = i % kPrepPerBlock;
+    return base + (block * kPrepPerBlock + m) * kPrepTokens;
+}
+
+// vt_cache (optional): V^T in 32-row blocks [kv head][blocks][HD][32] f16,
+// blocks = ceil(max_seq_len / 32): row r of kv head h, element d at
+// [h][r / 32][d][r % 32]. The stored V rows go there too, and the rows of the
+// chunk's last block past its end are written as 0, so that a prefill reading
+// whole blocks multiplies finite values by the zero probabilities of keys it
+// does not attend (the next chunk's prep overwrites them).
 template <int HD>
 __global__ __launch_bounds__(kWG) void k_prompt_prep(const float* __restrict__ q, const float* __restrict__ k,
                                                      const float* __restrict__ v,
@@ -90,14 +116,28 @@ __global__ __launch_bounds__(kWG) void k_prompt_prep(const float* __restrict__ q
                                                      const uint16_t* __restrict__ rope_freqs,
                                                      const float* __restrict__ inv_table,
                                                      uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_cache,
-                                                     uint16_t* __restrict__ v_cache, g4_prompt_prep_params p) {
+                                                     uint16_t* __restrict__ v_cache, uint16_t* __restrict__ vt_cache,
+                                                     g4_prompt_prep_params p) {
     constexpr int J = HD / 64, PJ = J / 2;
     constexpr unsigned NP = HD / 2;  // RoPE pairs
     static_assert(NP <= kWG, "one thread per RoPE pair");
     __shared__ float inv[NP];
     __shared__ float rc[kPrepTokens][NP], rs[kPrepTokens][NP];
-    const unsigned t0 = blockIdx.x * kPrepTokens;
-    const unsigned nt = min(kPrepTokens, p.n_tokens - t0);  // tokens of this workgroup (the last may have fewer)
+    const unsigned base = p.start & ~31u, end = p.start + p.n_tokens;
+    const unsigned pos0 = prep_first_pos(blockIdx.x, base);
+    if (pos0 >= end) return;  // uniform: past the chunk's last block (or a block's pair past its end)
+    const unsigned lo = max(pos0, p.start);  // this workgroup's positions [lo, hi)
+    const unsigned hi = min(pos0 + kPrepTokens, end);
+    const unsigned nt = hi > lo ? hi - lo : 0u;
+    const unsigned t0 = lo - p.start;  // token index of position lo
+    if (vt_cache && p.store_kv && hi == end && (end & 31u)) {  // zeros past the chunk's end in its last block
+        const unsigned blocks = (p.max_seq_len + 31) / 32, pad = 32 - (end & 31u);
+        for (unsigned i = threadIdx.x; i < p.num_kv_heads * HD * pad; i += kWG) {
+            const unsigned r = end + i % pad, hd = i / pad, h = hd / HD, d = hd % HD;
+            vt_cache[(((uint64_t)h * blocks + r / 32) * HD + d) * 32 + r % 32] = 0;
+        }
+    }
+    if (nt == 0) return;
     if (threadIdx.x < NP)
         inv[threadIdx.x] = inv_table ? inv_table[threadIdx.x]
                                      : rope_inv_freq(threadIdx.x, HD, p.theta, p.apply_divisor,
@@ -105,13 +145,14 @@ __global__ __launch_bounds__(kWG) void k_prompt_prep(const float* __restrict__ q
     __syncthreads();
     for (unsigned i = threadIdx.x; i < nt * NP; i += kWG) {
         const unsigned tt = i / NP, pr = i % NP;
-        const float ang = (float)(p.start + t0 + tt) * inv[pr];  // rope_angle's expression
+        const float ang = (float)(lo + tt) * inv[pr];  // rope_angle's expression
         f64_cos_sin(ang, rc[tt][pr], rs[tt][pr]);
     }
     __syncthreads();
     const unsigned lane = threadIdx.x & 63;
     const unsigned wave = threadIdx.x >> 6;
     const unsigned S = p.num_q_heads + (p.store_kv ? 2 * p.num_kv_heads : 0);
+    const unsigned vt_blocks = (p.max_seq_len + 31) / 32;
     for (unsigned w = wave; w < nt * S; w += kWG / 64) {  // uniform per wave
         const unsigned tt = w / S, slot = w % S;
         const unsigned t = t0 + tt, pos = p.start + t;
@@ -140,6 +181,11 @@ __global__ __launch_bounds__(kWG) void k_prompt_prep(const float* __restrict__ q
                              : (is_k ? k_cache : v_cache) + ((uint64_t)pos * p.num_kv_heads + h) * HD;
 #pragma unroll
         for (int j = 0; j < J; j++) dst[lane + 64 * j] = f2h(x[j]);
+        if (vt_cache && !rope) {  // uniform: the V row into its V^T block too
+            uint16_t* vt = vt_cache + ((uint64_t)h * vt_blocks + pos / 32) * (HD * 32) + pos % 32;
+#pragma unroll
+            for (int j = 0; j < J; j++) vt[(lane + 64 * j) * 32] = f2h(x[j]);
+        }
     }
 }
 
@@ -180,10 +226,9 @@ extern "C" int g4_attn_prep(float* q, float* k, float* v, const uint16_t* q_weig
     return G4_OK;
 }
 
-extern "C" int g4_attn_prompt_prep(const float* q, const float* k, const float* v, const uint16_t* q_weight,
-                                   const uint16_t* k_weight, const uint16_t* rope_freqs, const float* rope_inv_freq,
-                                   uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache, g4_prompt_prep_params p,
-                                   void* stream) {
+static int prompt_prep(const float* q, const float* k, const float* v, const uint16_t* q_weight, const uint16_t* k_weight,
+                       const uint16_t* rope_freqs, const float* rope_inv_freq, uint16_t* q_out, uint16_t* k_cache,
+                       uint16_t* v_cache, uint16_t* vt_cache, const g4_prompt_prep_params& p, void* stream) {
     if (p.head_dim != 256 && p.head_dim != 512)
         return fail(G4_EINVAL, "attnPromptPrep: head_dim %u unsupported (256 or 512)", p.head_dim);
     if (p.num_q_heads == 0 || p.num_kv_heads == 0) return fail(G4_EINVAL, "attnPromptPrep: no heads");
@@ -197,19 +242,39 @@ extern "C" int g4_attn_prompt_prep(const float* q, const float* k, const float* 
             return fail(G4_EINVAL, "attnPromptPrep: rows %u..%u past max_seq_len %u", p.start,
                         p.start + p.n_tokens - 1, p.max_seq_len);
     }
-    if ((uint64_t)p.start + p.n_tokens > 0xffffffffull) return fail(G4_EINVAL, "attnPromptPrep: position range");
+    if (vt_cache && !p.store_kv) return fail(G4_EINVAL, "attnPromptPrep: vt_cache needs store_kv (a KV producer)");
+    if ((uint64_t)p.start + p.n_tokens + 31 > 0xffffffffull) return fail(G4_EINVAL, "attnPromptPrep: position range");
     if (p.n_tokens == 0) return G4_OK;
-    if (p.n_tokens > 0x7fffffffu) return fail(G4_EINVAL, "attnPromptPrep: too many tokens");
     hipStream_t st = as_stream(stream);
-    const dim3 grid((p.n_tokens + kPrepTokens - 1) / kPrepTokens);
+    const uint64_t blocks = ((uint64_t)p.start + p.n_tokens - (p.start & ~31u) + 31) / 32;
+    const uint64_t wgs = (blocks + kXcds - 1) / kXcds * kXcds * kPrepPerBlock;
+    if (wgs > 0x7fffffffu) return fail(G4_EINVAL, "attnPromptPrep: too many tokens");
+    const dim3 grid((uint32_t)wgs);
     if (p.head_dim == 512)
         G4_LAUNCH(k_prompt_prep<512>, grid, dim3(kWG), 0, st, q, k, v, q_weight, k_weight, rope_freqs,
-                           rope_inv_freq, q_out, k_cache, v_cache, p);
+                           rope_inv_freq, q_out, k_cache, v_cache, vt_cache, p);
     else
         G4_LAUNCH(k_prompt_prep<256>, grid, dim3(kWG), 0, st, q, k, v, q_weight, k_weight, rope_freqs,
-                           rope_inv_freq, q_out, k_cache, v_cache, p);
+                           rope_inv_freq, q_out, k_cache, v_cache, vt_cache, p);
     G4_CHECK_LAUNCH("attnPromptPrep");
     return G4_OK;
+}
+
+extern "C" int g4_attn_prompt_prep(const float* q, const float* k, const float* v, const uint16_t* q_weight,
+                                   const uint16_t* k_weight, const uint16_t* rope_freqs, const float* rope_inv_freq,
+                                   uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache, g4_prompt_prep_params p,
+                                   void* stream) {
+    return prompt_prep(q, k, v, q_weight, k_weight, rope_freqs, rope_inv_freq, q_out, k_cache, v_cache, nullptr, p,
+                       stream);
+}
+
+extern "C" int g4_attn_prompt_prep_vt(const float* q, const float* k, const float* v, const uint16_t* q_weight,
+                                      const uint16_t* k_weight, const uint16_t* rope_freqs, const float* rope_inv_freq,
+                                      uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache, uint16_t* vt_cache,
+                                      g4_prompt_prep_params p, void* stream) {
+    if (!vt_cache) return fail(G4_EINVAL, "attnPromptPrepVt: vt_cache is NULL");
+    return prompt_prep(q, k, v, q_weight, k_weight, rope_freqs, rope_inv_freq, q_out, k_cache, v_cache, vt_cache, p,
+                       stream);
 }
 
 namespace g4 {

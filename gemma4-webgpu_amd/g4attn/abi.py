@@ -89,7 +89,7 @@ class StepEntry(C.Structure):
 class PrefillEntry(C.Structure):
     _fields_ = [("q", C.c_void_p), ("k_cache", C.c_void_p), ("v_cache", C.c_void_p), ("out", C.c_void_p),
                 ("n_tokens", C.c_uint32), ("start", C.c_uint32), ("sliding_window", C.c_uint32),
-                ("scale", C.c_float)]
+                ("scale", C.c_float), ("vt_cache", C.c_void_p), ("vt_rows", C.c_uint32)]
 
 
 class PromptPrepParams(C.Structure):
@@ -189,6 +189,7 @@ SIGNATURES: dict[str, list] = {
     "g4_attn_prefill_run_timed": [C.POINTER(DecodePlan), _P, _P, _P],
     "g4_attn_prefill": [C.POINTER(PrefillEntry), _U32, _U32, _U32, _U32, _P, _SZ, _P],
     "g4_attn_prompt_prep": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, PromptPrepParams, _P],
+    "g4_attn_prompt_prep_vt": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, PromptPrepParams, _P],
     "g4_matmul_quant_f16": [_P, _P, _P, MatmulParams, _P],
     "g4_linear_f16": [_P, _U32, C.POINTER(LinearSeg), _U32, _P],
     "g4_read_ceiling": [_P, _SZ, _P, _P, _P, _P],

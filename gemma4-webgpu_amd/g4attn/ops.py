@@ -417,33 +417,46 @@ def attn_step(entries, num_q_heads, num_kv_heads, head_dim, workspace, stream=No
 
 # ---- chunked prompt prep ----------------------------------------------------------
 
+def vt_cache_elems(max_seq_len, num_kv_heads, head_dim) -> int:
+    """f16 elements of a V^T block cache for max_seq_len rows ([kv head][ceil(rows / 32)][HD][32])."""
+    return (max_seq_len + 31) // 32 * 32 * num_kv_heads * head_dim
+
+
 def attn_prompt_prep(q, q_weight, q_out, n_tokens, start, num_q_heads, num_kv_heads, head_dim, theta, apply_divisor,
                      rope_freqs=None, k=None, v=None, k_weight=None, k_cache=None, v_cache=None, max_seq_len=0,
-                     eps=1e-6, rope_inv_freq=None, stream=None):
+                     eps=1e-6, rope_inv_freq=None, vt_cache=None, stream=None):
     """q/k/v/norm+RoPE/store of n_tokens prompt tokens at positions start.. in one launch. q: f32
     [n_tokens][NQH][HD]; q_out: f16 [n_tokens][NQH][HD]; with k (and v, k_weight, caches of max_seq_len rows)
     the layer is a KV producer and rows start .. start + n_tokens - 1 are stored. rope_inv_freq: optional
-    device table from rope_inv_freq() for this layer's theta/divisor (else each workgroup evaluates it)."""
+    device table from rope_inv_freq() for this layer's theta/divisor (else each workgroup evaluates it).
+    vt_cache (KV producers): the V rows also go there as V^T blocks (g4_attn_prompt_prep_vt), of
+    vt_cache_elems(max_seq_len, ...) f16 elements."""
     store = k is not None
     nq = n_tokens * num_q_heads * head_dim
     nk = n_tokens * num_kv_heads * head_dim
     p = PromptPrepParams(num_q_heads, num_kv_heads, head_dim, n_tokens, start, eps, theta, 1 if apply_divisor else 0,
                          1 if store else 0, max_seq_len)
     rows = max_seq_len * num_kv_heads * head_dim
-    abi.call("g4_attn_prompt_prep", _f32(q, "q", nq), _f32(k, "k", nk) if store else None,
-             _f32(v, "v", nk) if store else None, _f16(q_weight, "q_weight", head_dim),
-             _f16(k_weight, "k_weight", head_dim) if store else None,
-             _f16(rope_freqs, "rope_freqs", head_dim // 2) if rope_freqs is not None else None,
-             _f32(rope_inv_freq, "rope_inv_freq", head_dim // 2) if rope_inv_freq is not None else None,
-             _f16(q_out, "q_out", nq), _f16(k_cache, "k_cache", rows) if store else None,
-             _f16(v_cache, "v_cache", rows) if store else None, p, _stream(stream))
+    args = [_f32(q, "q", nq), _f32(k, "k", nk) if store else None,
+            _f32(v, "v", nk) if store else None, _f16(q_weight, "q_weight", head_dim),
+            _f16(k_weight, "k_weight", head_dim) if store else None,
+            _f16(rope_freqs, "rope_freqs", head_dim // 2) if rope_freqs is not None else None,
+            _f32(rope_inv_freq, "rope_inv_freq", head_dim // 2) if rope_inv_freq is not None else None,
+            _f16(q_out, "q_out", nq), _f16(k_cache, "k_cache", rows) if store else None,
+            _f16(v_cache, "v_cache", rows) if store else None]
+    if vt_cache is None:
+        abi.call("g4_attn_prompt_prep", *args, p, _stream(stream))
+    else:
+        vt = _f16(vt_cache, "vt_cache", vt_cache_elems(max_seq_len, num_kv_heads, head_dim))
+        abi.call("g4_attn_prompt_prep_vt", *args, vt, p, _stream(stream))
 
 
 # ---- causal prefill ------------------------------------------------------------
 
 def make_prefill_entries(items, num_q_heads, num_kv_heads, head_dim):
     """items: dicts with q (f16 [n_tokens][NQH][HD]), k_cache, v_cache (f16, at least start + n_tokens rows),
-    out (f32 [n_tokens][NQH][HD]), n_tokens, start, sliding_window, scale."""
+    out (f32 [n_tokens][NQH][HD]), n_tokens, start, sliding_window, scale; optionally vt_cache (the V^T
+    blocks the prompt prep wrote) with vt_rows (the max_seq_len it was sized for)."""
     from .abi import PrefillEntry
 
     items = list(items)
@@ -451,10 +464,13 @@ def make_prefill_entries(items, num_q_heads, num_kv_heads, head_dim):
     for i, it in enumerate(items):
         T, s0 = int(it["n_tokens"]), int(it["start"])
         kv = (s0 + T) * num_kv_heads * head_dim
+        vt, vt_rows = it.get("vt_cache"), int(it.get("vt_rows", 0))
         arr[i] = PrefillEntry(_f16(it["q"], f"entry {i} q", T * num_q_heads * head_dim),
                               _f16(it["k_cache"], f"entry {i} k_cache", kv), _f16(it["v_cache"], f"entry {i} v_cache", kv),
                               _f32(it["out"], f"entry {i} out", T * num_q_heads * head_dim), T, s0,
-                              int(it.get("sliding_window", 0)), float(it.get("scale", 1.0)))
+                              int(it.get("sliding_window", 0)), float(it.get("scale", 1.0)),
+                              _f16(vt, f"entry {i} vt_cache", vt_cache_elems(vt_rows, num_kv_heads, head_dim))
+                              if vt is not None else None, vt_rows)
     return arr
 
 

@@ -4,7 +4,8 @@ checks exactly the plan the benchmark times.
 prefill4k   causal prefill of a 4096-token prompt: one global layer and one 512-window
             local layer, each as eight 512-token chunks, 16 entries in one launch; the
             f16 query and K/V rows come from raw N(0,1) projections through the
-            chunked prompt prep (q/k RMSNorm + RoPE, v-norm, K/V store).
+            chunked prompt prep (q/k RMSNorm + RoPE, v-norm, K/V store, and the V rows
+            as V^T blocks beside the cache, which the prefill reads V from).
 ragged64    64 sequences, lengths uniform in [1024, 32768] (seeded).
 """
 from __future__ import annotations
@@ -21,14 +22,16 @@ def ragged64_lengths():
     return [int(x) for x in synth.ragged_lengths(BASE_SEED + 2, 64, 1024, 32768)]
 
 
-def prefill4k(dev, nqh=8, nkh=1, hd=256, T=PREFILL_T, chunk=PREFILL_CHUNK, windows=PREFILL_WINDOWS):
+def prefill4k(dev, nqh=8, nkh=1, hd=256, T=PREFILL_T, chunk=PREFILL_CHUNK, windows=PREFILL_WINDOWS, vt=True):
     """A prompt's attention for one global and one local layer, from raw projections.
 
     Per layer: raw f32 q/k/v projections N(0,1) (one row of each head per token), norm weights 1.0 and
     the engine's rope_freqs table; the chunked prompt prep (q/k RMSNorm + RoPE at every position, v
     weightless norm, f16 K/V rows stored) fills the f16 query and the caches. Returns the per-layer
     device tensors (q f16, k_cache, v_cache, out, window), the prefill entries (every chunk of every
-    layer, layer order then chunk order) and `prep()`, which re-runs the two layers' prep launches."""
+    layer, layer order then chunk order) and `prep()`, which re-runs the two layers' prep launches.
+    vt: the prep also writes V^T blocks beside each cache and the entries read V from them (False: the
+    prefill transposes the attended rows itself at every call)."""
     import numpy as np
     import torch
 
@@ -45,16 +48,18 @@ def prefill4k(dev, nqh=8, nkh=1, hd=256, T=PREFILL_T, chunk=PREFILL_CHUNK, windo
         q = torch.empty(T * nqh * hd, dtype=torch.int16, device=dev)
         kc = torch.empty(T * nkh * hd, dtype=torch.int16, device=dev)
         vc = torch.empty_like(kc)
+        vtc = torch.empty(ops.vt_cache_elems(T, nkh, hd), dtype=torch.int16, device=dev) if vt else None
         out = torch.empty(T * nqh * hd, dtype=torch.float32, device=dev)
         theta, div = (1e4, 0) if w else (1e6, 1)
         inv = ops.rope_inv_freq(theta, hd, div, rf)  # the layer's inverse frequencies, once (as at load)
         preps.append(dict(q=qr, q_weight=ones, q_out=q, n_tokens=T, start=0, num_q_heads=nqh, num_kv_heads=nkh,
                           head_dim=hd, theta=theta, apply_divisor=div, rope_freqs=rf, k=kr, v=vr, k_weight=ones,
-                          k_cache=kc, v_cache=vc, max_seq_len=T, eps=EPS, rope_inv_freq=inv))
+                          k_cache=kc, v_cache=vc, max_seq_len=T, eps=EPS, rope_inv_freq=inv, vt_cache=vtc))
         layers.append((q, kc, vc, out, w))
         for c0 in range(0, T, chunk):
             entries.append(dict(q=q[c0 * nqh * hd:], k_cache=kc, v_cache=vc, out=out[c0 * nqh * hd:],
-                                n_tokens=min(chunk, T - c0), start=c0, sliding_window=w, scale=1.0))
+                                n_tokens=min(chunk, T - c0), start=c0, sliding_window=w, scale=1.0,
+                                vt_cache=vtc, vt_rows=T))
 
     def prep():
         for kw in preps:

@@ -449,6 +449,11 @@ typedef struct g4_prefill_entry {
     uint32_t start;           /* position of token 0 */
     uint32_t sliding_window;  /* 0 = full */
     float scale;              /* attention scale (1.0 for Gemma 4) */
+    const uint16_t* vt_cache; /* optional: v_cache's rows as V^T blocks [num_kv_heads][ceil(vt_rows / 32)]
+                                 [head_dim][32] f16, written by g4_attn_prompt_prep_vt; every row the entry
+                                 attends must have been stored there (rows a decode step stores are not).
+                                 NULL: every prefill call transposes the attended rows into its workspace */
+    uint32_t vt_rows;         /* rows the V^T cache was sized for (the prompt prep's max_seq_len) */
 } g4_prefill_entry;
 
 int g4_attn_prefill_workspace_size(const g4_prefill_entry* entries, uint32_t n_entries, uint32_t num_q_heads,
@@ -498,6 +503,18 @@ int g4_attn_prompt_prep(const float* q, const float* k, const float* v, const ui
                         const uint16_t* k_weight, const uint16_t* rope_freqs, const float* rope_inv_freq,
                         uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache, g4_prompt_prep_params p,
                         void* stream);
+/* The same, also writing the stored V rows into vt_cache, V^T in 32-row blocks
+ * [num_kv_heads][ceil(max_seq_len / 32)][head_dim][32] f16 (row r, element d
+ * at [h][r / 32][d][r % 32]): the layout g4_attn_prefill reads V in
+ * (g4_prefill_entry.vt_cache), kept beside the cache so that a prompt run as
+ * chunks transposes each row once rather than at every chunk's prefill. The
+ * rows of the chunk's last block past its end are written as 0 (the next
+ * chunk's prep overwrites them). No counterpart in the reference, whose
+ * attn_output.wgsl reads V row by row (src/engine.ts:2094). store_kv 1. */
+int g4_attn_prompt_prep_vt(const float* q, const float* k, const float* v, const uint16_t* q_weight,
+                           const uint16_t* k_weight, const uint16_t* rope_freqs, const float* rope_inv_freq,
+                           uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache, uint16_t* vt_cache,
+                           g4_prompt_prep_params p, void* stream);
 
 /* ---- the f16 projections either side of the block ------------------------
  * attn.linearQKV (src/engine.ts:2045-2051) and attn.linearOut (:2096):

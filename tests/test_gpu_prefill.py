@@ -160,16 +160,18 @@ def test_prefill_head_dim_512_with_256_in_one_process(dev):
 
 
 @pytest.mark.timeout(900)
-def test_prefill4k_bench_plan(dev):
+@pytest.mark.parametrize("vt", [True, False])
+def test_prefill4k_bench_plan(dev, vt):
     """The exact launch bench.py times for the 4096-token prompt (workloads.prefill4k: a global and a
     512-window local layer, eight 512-token chunks each, 16 entries in one launch; key parts sized from
-    the whole call's work, longest items first, the merge's few-record form). Checked against the
-    oracle's decode chain: every token of each layer's first and last chunk, every 8th token elsewhere.
-    Local layers are checked over their window's rows (the masked rows weigh exactly 0)."""
+    the whole call's work, longest items first, the merge's few-record form), with V read from the V^T
+    caches the prompt prep wrote (the benchmark's form) and transposed by the prefill itself. Checked
+    against the oracle's decode chain: every token of each layer's first and last chunk, every 8th token
+    elsewhere. Local layers are checked over their window's rows (the masked rows weigh exactly 0)."""
     from g4attn import workloads
 
-    announce("attnPrefill prefill4k bench plan (16 entries, one launch)")
-    layers, entries, _ = workloads.prefill4k(dev, 8, 1, HD)
+    announce(f"attnPrefill prefill4k bench plan (16 entries, one launch), V^T caches {vt}")
+    layers, entries, _ = workloads.prefill4k(dev, 8, 1, HD, vt=vt)
     arr = ops.make_prefill_entries(entries, 8, 1, HD)
     ws = torch.empty(ops.prefill_workspace_bytes(arr, 8, 1, HD), dtype=torch.uint8, device=dev)
     for _, _, _, out, _ in layers:
