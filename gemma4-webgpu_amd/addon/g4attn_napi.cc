@@ -999,6 +999,23 @@ napi_value AttnStepRun(napi_env env, napi_callback_info info) {
     return undefined(env);
 }
 
+// attnStepAdvance(plan, tokens): the prepared plan moves `tokens` decode steps ahead, in place (the
+// 64-byte array from attnStepPrepare / attnStepPrepareLayers); host only, nothing is enqueued.
+napi_value AttnStepAdvance(napi_env env, napi_callback_info info) {
+    Args a(env, info, 2);  // plan, tokens
+    void* d = nullptr;
+    size_t n = 0;
+    a.bytes(0, &d, &n);
+    const uint32_t tokens = a.u32(1);
+    if (!a.ok) return nullptr;
+    if (n != sizeof(g4_decode_plan)) {
+        napi_throw_type_error(env, nullptr, "attnStepAdvance: not a plan from attnStepPrepare");
+        return nullptr;
+    }
+    CALL(env, g4_attn_step_advance(static_cast<g4_decode_plan*>(d), tokens));
+    return undefined(env);
+}
+
 // The plan argument of the step's run calls (a 64-byte array from attnStepPrepare).
 bool step_plan_arg(Args& a, size_t i, const char* who, g4_decode_plan* plan) {
     void* d = nullptr;
@@ -1039,7 +1056,8 @@ napi_value AttnStepRunOut(napi_env env, napi_callback_info info) {
 
 // ---- causal prefill ---------------------------------------------------------
 
-// One g4_prefill_entry from {q, kCache, vCache, out (BigInt pointers), nTokens, start, slidingWindow, scale}.
+// One g4_prefill_entry from {q, kCache, vCache, out (BigInt pointers), nTokens, start, slidingWindow, scale,
+// and optionally vtCache (BigInt) with vtRows}.
 bool prefill_entry(Args& a, napi_value obj, size_t idx, g4_prefill_entry* e) {
     napi_env env = a.env;
     memset(e, 0, sizeof *e);
@@ -1064,7 +1082,8 @@ bool prefill_entry(Args& a, napi_value obj, size_t idx, g4_prefill_entry* e) {
         const char* key;
         uint32_t* dst;
         bool required;
-    } u32s[] = {{"nTokens", &e->n_tokens, true}, {"start", &e->start, true}, {"slidingWindow", &e->sliding_window, false}};
+    } u32s[] = {{"nTokens", &e->n_tokens, true}, {"start", &e->start, true}, {"slidingWindow", &e->sliding_window, false},
+                {"vtRows", &e->vt_rows, false}};
     for (auto& f : u32s) {
         napi_value v;
         if (!get_prop(env, obj, f.key, &v)) {
@@ -1081,6 +1100,15 @@ bool prefill_entry(Args& a, napi_value obj, size_t idx, g4_prefill_entry* e) {
     }
     e->scale = 1.0f;
     napi_value v;
+    if (get_prop(env, obj, "vtCache", &v)) {  // optional: the V^T blocks the prompt prep wrote
+        uint64_t x = 0;
+        bool lossless = false;
+        if (napi_get_value_bigint_uint64(env, v, &x, &lossless) != napi_ok || !lossless) {
+            a.fail(at + "vtCache must be a BigInt pointer");
+            return false;
+        }
+        e->vt_cache = reinterpret_cast<const uint16_t*>(static_cast<uintptr_t>(x));
+    }
     if (get_prop(env, obj, "scale", &v)) {
         double x = 0;
         if (napi_get_value_double(env, v, &x) != napi_ok) {
@@ -1185,6 +1213,31 @@ napi_value AttnPromptPrep(napi_env env, napi_callback_info info) {
     return undefined(env);
 }
 
+// attnPromptPrepVt(q, k, v, qWeight, kWeight, ropeFreqs, ropeInvFreq, qOut, kCache, vCache, vtCache, params,
+// stream): attnPromptPrep that also writes the V rows as V^T blocks (g4_attn_prompt_prep_vt).
+napi_value AttnPromptPrepVt(napi_env env, napi_callback_info info) {
+    Args a(env, info, 13);
+    void* q = a.ptr(0);
+    void* k = a.ptr(1);
+    void* v = a.ptr(2);
+    void* qw = a.ptr(3);
+    void* kw = a.ptr(4);
+    void* rf = a.ptr(5);
+    void* inv = a.ptr(6);
+    void* qo = a.ptr(7);
+    void* kc = a.ptr(8);
+    void* vc = a.ptr(9);
+    void* vt = a.ptr(10);
+    g4_prompt_prep_params p;
+    a.params(11, &p);
+    void* s = a.ptr(12);
+    if (!a.ok) return nullptr;
+    CALL(env, g4_attn_prompt_prep_vt((const float*)q, (const float*)k, (const float*)v, (const uint16_t*)qw,
+                                     (const uint16_t*)kw, (const uint16_t*)rf, (const float*)inv, (uint16_t*)qo,
+                                     (uint16_t*)kc, (uint16_t*)vc, (uint16_t*)vt, p, s));
+    return undefined(env);
+}
+
 napi_value Init(napi_env env, napi_value exports) {
     struct {
         const char* name;
@@ -1231,12 +1284,14 @@ napi_value Init(napi_env env, napi_value exports) {
         {"attnStepLayersWorkspaceSize", AttnStepLayersWorkspaceSize},
         {"attnStepPrepareLayers", AttnStepPrepareLayers},
         {"attnStepRun", AttnStepRun},
+        {"attnStepAdvance", AttnStepAdvance},
         {"attnStepRunAttention", AttnStepRunAttention},
         {"attnStepRunOut", AttnStepRunOut},
         {"attnPrefillWorkspaceSize", AttnPrefillWorkspaceSize},
         {"attnPrefillPrepare", AttnPrefillPrepare},
         {"attnPrefillRun", AttnPrefillRun},
         {"attnPromptPrep", AttnPromptPrep},
+        {"attnPromptPrepVt", AttnPromptPrepVt},
     };
     for (auto& f : fns) {
         napi_value fn;

@@ -170,6 +170,8 @@ export interface PrefillEntry {
   start: number;
   slidingWindow?: number;     // 0 = full
   scale?: number;
+  vtCache?: DeviceBuffer;     // V^T blocks of vCache written by attnPromptPrep (PromptPrep.vtCache), holding
+  vtRows?: number;            // every attended row; vtRows: the maxSeqLen it was sized for
 }
 
 // The prep of a prompt chunk of one layer (the engine's per-token vNorm -> fusedNormRope(Q, K) ->
@@ -185,6 +187,8 @@ export interface PromptPrep {
   qOut: DeviceBuffer;         // f16 [nTokens][NQH][HD]: PrefillEntry.q
   kCache?: DeviceBuffer;      // f16 [maxSeqLen][NKH][HD]: rows start .. start + nTokens - 1 are written
   vCache?: DeviceBuffer;
+  vtCache?: DeviceBuffer;     // producer layers, optional: the V rows also as V^T blocks
+                              // f16 [NKH][ceil(maxSeqLen / 32)][HD][32], which attnPrefill reads V from
   nTokens: number;
   start: number;
   theta: number;
@@ -269,6 +273,7 @@ export interface Addon {
   attnStepPrepareLayers(entries: any[], perLayer: number, nqh: number, nkh: number, hd: number, ws: bigint,
     wsBytes: number, s: bigint): Uint8Array[];
   attnStepRun(plan: Uint8Array, s: bigint): void;
+  attnStepAdvance(plan: Uint8Array, tokens: number): void;
   attnStepRunAttention(plan: Uint8Array, s: bigint): void;
   attnStepRunOut(plan: Uint8Array, segs: { weight: bigint; out: bigint; rows: number }[], s: bigint): void;
   attnPrefillWorkspaceSize(entries: any[], nqh: number, nkh: number, hd: number): number;
@@ -277,6 +282,8 @@ export interface Addon {
   attnPrefillRun(plan: Uint8Array, s: bigint): void;
   attnPromptPrep(q: bigint, k: bigint | null, v: bigint | null, qw: bigint, kw: bigint | null, rf: bigint | null,
     inv: bigint | null, qOut: bigint, kc: bigint | null, vc: bigint | null, p: Uint8Array, s: bigint): void;
+  attnPromptPrepVt(q: bigint, k: bigint, v: bigint, qw: bigint, kw: bigint, rf: bigint | null,
+    inv: bigint | null, qOut: bigint, kc: bigint, vc: bigint, vt: bigint, p: Uint8Array, s: bigint): void;
   [key: string]: any;
 }
 
@@ -444,6 +451,15 @@ export class HipAttention {
     }
   }
 
+  // The next token(s) of a prepared plan without a new prepare: every entry's seqLen and position grow by
+  // `tokens` (the engine's per-token uniform patch, src/engine.ts:1967-1987), in place, on the host alone
+  // (nothing is enqueued); the kernel evaluates the new positions' RoPE factors. Prepare again every few
+  // dozen tokens (the part holding a full layer's last row takes the new rows) and whenever the entries
+  // change otherwise; throws past 4096 tokens since the prepare.
+  attnStepAdvance(plan: Uint8Array, tokens?: number): void {
+    this.g4.attnStepAdvance(plan, tokens === undefined ? 1 : tokens);
+  }
+
   attnStep(entries: StepEntry[], shape: StepShape, workspace: DeviceBuffer): void {
     this.attnStepRun(this.attnStepPrepare(entries, shape, workspace));
   }
@@ -482,6 +498,7 @@ export class HipAttention {
       return {
         q: e.q.ptr, kCache: e.kCache.ptr, vCache: e.vCache.ptr, out: e.out.ptr, nTokens: e.nTokens,
         start: e.start, slidingWindow: e.slidingWindow || 0, scale: e.scale === undefined ? 1.0 : e.scale,
+        vtCache: e.vtCache ? e.vtCache.ptr : undefined, vtRows: e.vtRows || 0,
       };
     });
   }
@@ -523,11 +540,18 @@ export class HipAttention {
       { f: p.eps === undefined ? 1e-6 : p.eps }, { f: p.theta }, { u: p.applyDivisor }, { u: store ? 1 : 0 },
       { u: p.maxSeqLen || 0 },
     ]);
+    if (p.vtCache && !store) throw new Error('attnPromptPrep: vtCache on a layer that stores no rows');
     function ptr(b: DeviceBuffer | undefined): bigint | null { return b ? b.ptr : null; }
     const slot = this.beginPass(PASS_LABELS.attnPromptPrep);
     try {
-      this.g4.attnPromptPrep(p.q.ptr, ptr(p.k), ptr(p.v), p.qWeight.ptr, ptr(p.kWeight), ptr(p.ropeFreqs),
-        ptr(p.ropeInvFreq), p.qOut.ptr, ptr(p.kCache), ptr(p.vCache), params.bytes, this.stream);
+      if (p.vtCache) {  // a producer layer: k, v, kWeight and the caches were checked above
+        this.g4.attnPromptPrepVt(p.q.ptr, ptr(p.k) as bigint, ptr(p.v) as bigint, p.qWeight.ptr,
+          ptr(p.kWeight) as bigint, ptr(p.ropeFreqs), ptr(p.ropeInvFreq), p.qOut.ptr, ptr(p.kCache) as bigint,
+          ptr(p.vCache) as bigint, p.vtCache.ptr, params.bytes, this.stream);
+      } else {
+        this.g4.attnPromptPrep(p.q.ptr, ptr(p.k), ptr(p.v), p.qWeight.ptr, ptr(p.kWeight), ptr(p.ropeFreqs),
+          ptr(p.ropeInvFreq), p.qOut.ptr, ptr(p.kCache), ptr(p.vCache), params.bytes, this.stream);
+      }
     } finally {
       this.endPass(slot);
     }

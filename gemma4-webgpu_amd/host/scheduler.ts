@@ -6,8 +6,10 @@
 // Each layer of a token step is one attnStep launch over every active sequence: a ragged batch, one
 // entry per sequence with its own length (the batched-decode workload of 64 sequences of 1K..32K
 // rows is one such launch). beginToken() prepares every layer of the token step at once (one table
-// upload per head_dim group, attnStepPrepareLayers); stepLayer() then runs the layer's plan, or, without
-// it, prepares that layer alone.
+// upload per head_dim group, attnStepPrepareLayers), or, while the active sequences are the ones its
+// plans were prepared for, advances those plans one token on the host (attnStepAdvance; prepared again
+// every REPLAN_TOKENS tokens); stepLayer() then runs the layer's plan, or, without it, prepares that
+// layer alone.
 //
 // Memory is taken once, at construction: one pool holds every slot's K and V cache rows of every
 // KV-producer layer (consumer layers read their producer's rows, src/engine.ts:1518-1522), one holds
@@ -38,6 +40,10 @@ export interface SchedulerConfig {
   maxBatch: number;           // cache slots: sequences decoded together
   maxSeqLen: number;          // cache rows per slot and producer layer
 }
+
+// beginToken prepares the plans again after this many tokens of advancing them (the part holding a full
+// layer's last row takes the new rows meanwhile).
+export const REPLAN_TOKENS = 32;
 
 interface Waiting {
   id: string;
@@ -168,6 +174,10 @@ export class DecodeScheduler {
   private readonly groups: { layers: number[]; workspace: DeviceBuffer }[];  // layers per head_dim, in order
   private tokenPlans: Uint8Array[] | null;     // beginToken's plans, one per layer
   private tokenIds: string;                    // the active sequences they were prepared for
+  private token: number;                       // tokens stepped (advance() calls)
+  private plansToken: number;                  // the token the plans are at
+  private sincePrepare: number;                // tokens the plans were advanced since their prepare
+  prepares: number;                            // beginToken calls that prepared (the rest advanced)
   private alive: boolean;
 
   constructor(att: HipAttention, cfg: SchedulerConfig) {
@@ -220,13 +230,18 @@ export class DecodeScheduler {
     }
     this.tokenPlans = null;
     this.tokenIds = '';
+    this.token = 0;
+    this.plansToken = -1;
+    this.sincePrepare = 0;
+    this.prepares = 0;
     this.alive = true;
   }
 
   submit(id: string, length: number): void { this.table.submit(id, length); }
   admit(): string[] {
-    this.tokenPlans = null;
-    return this.table.admit();
+    const admitted = this.table.admit();
+    if (admitted.length) this.tokenPlans = null;  // the active set changed: prepare at the next beginToken
+    return admitted;
   }
   release(id: string): void {
     this.tokenPlans = null;
@@ -271,13 +286,25 @@ export class DecodeScheduler {
     });
   }
 
-  // Every layer of the token step prepared at once, for the active sequences (the engine patches every
-  // layer's uniforms once per token, src/engine.ts:1967-1987): one attnStepPrepareLayers per head_dim
-  // group, one table upload each. Call after admit/release, before the token's first layer; stepLayer
-  // then runs the prepared plans. Returns the number of sequences prepared.
+  // Every layer of the token step made ready at once, for the active sequences (the engine patches every
+  // layer's uniforms once per token, src/engine.ts:1967-1987): when the previous token's plans were made
+  // for the same sequences, each advances one token on the host (attnStepAdvance, nothing enqueued);
+  // otherwise, and every REPLAN_TOKENS tokens, one attnStepPrepareLayers per head_dim group, one table
+  // upload each. Call after admit/release, before the token's first layer; stepLayer then runs the
+  // plans. Returns the number of sequences.
   beginToken(): number {
-    this.tokenPlans = null;
     const ids = this.table.activeIds();
+    const key = ids.join('\n');
+    if (this.tokenPlans && this.tokenIds === key) {
+      if (this.plansToken === this.token) return ids.length;
+      if (this.plansToken + 1 === this.token && this.sincePrepare + 1 < REPLAN_TOKENS) {
+        for (const p of this.tokenPlans) this.att.attnStepAdvance(p, 1);
+        this.sincePrepare++;
+        this.plansToken = this.token;
+        return ids.length;
+      }
+    }
+    this.tokenPlans = null;
     if (!ids.length) return 0;
     const plans: Uint8Array[] = new Array(this.cfg.layers.length);
     for (const g of this.groups) {
@@ -287,7 +314,10 @@ export class DecodeScheduler {
       g.layers.forEach(function (l, i) { plans[l] = ps[i]; });
     }
     this.tokenPlans = plans;
-    this.tokenIds = ids.join('\n');
+    this.tokenIds = key;
+    this.plansToken = this.token;
+    this.sincePrepare = 0;
+    this.prepares++;
     return ids.length;
   }
 
@@ -296,7 +326,7 @@ export class DecodeScheduler {
   // Returns the number of sequences stepped.
   stepLayer(layer: number): number {
     const ids = this.table.activeIds();
-    if (this.tokenPlans && this.tokenIds === ids.join('\n')) {
+    if (this.tokenPlans && this.plansToken === this.token && this.tokenIds === ids.join('\n')) {
       this.att.attnStepRun(this.tokenPlans[layer]);
       return ids.length;
     }
@@ -305,9 +335,10 @@ export class DecodeScheduler {
     return ents.length;
   }
 
-  // After the last layer of a token: every active sequence holds one more row.
+  // After the last layer of a token: every active sequence holds one more row (the plans are now one
+  // token behind; the next beginToken advances them).
   advance(): void {
-    this.tokenPlans = null;
+    this.token++;
     this.table.advance();
   }
 

@@ -295,7 +295,7 @@ function prefill(dir: string): string[] {
 
 interface PromptPrepSpec {
   nqh: number; nkh: number; hd: number; start: number; nTokens: number; theta: number; div: number; rows: number;
-  arrays: Record<string, number[]>;
+  vt?: boolean; arrays: Record<string, number[]>;
 }
 
 // The chunked prompt prep of one producer layer; out.bin = q_out, then the whole K and V caches.
@@ -323,19 +323,36 @@ function promptPrep(dir: string): string[] {
   const rf = upload(A.rf);
   const inv = alloc(spec.hd / 2 * 4);  // the layer's inverse frequencies, computed once (as at load)
   att.ropeInvFreq(spec.theta, spec.hd, spec.div, rf, inv);
+  const shape = { numQHeads: spec.nqh, numKvHeads: spec.nkh, headDim: spec.hd };
+  // with spec.vt: the V rows also as V^T blocks, then the chunk's prefill reading V from them
+  const vt = spec.vt ? alloc(Math.ceil(spec.rows / 32) * 32 * spec.nkh * spec.hd * 2) : undefined;
   att.attnPromptPrep({
     q: upload(A.q), k: upload(A.k), v: upload(A.v), qWeight: upload(A.qw), kWeight: upload(A.kw),
     ropeFreqs: rf, ropeInvFreq: inv, qOut: qOut, kCache: kc, vCache: vc, nTokens: spec.nTokens, start: spec.start,
-    theta: spec.theta, applyDivisor: spec.div, maxSeqLen: spec.rows,
-  }, { numQHeads: spec.nqh, numKvHeads: spec.nkh, headDim: spec.hd });
-  const res = new Uint8Array(qOut.size + kc.size + vc.size);
-  att.readBuffer(qOut, 0, res.subarray(0, qOut.size));
-  att.readBuffer(kc, 0, res.subarray(qOut.size, qOut.size + kc.size));
-  att.readBuffer(vc, 0, res.subarray(qOut.size + kc.size));
+    theta: spec.theta, applyDivisor: spec.div, maxSeqLen: spec.rows, vtCache: vt,
+  }, shape);
+  const parts: DeviceBuffer[] = [qOut, kc, vc];
+  if (vt) {
+    const out = alloc(spec.nTokens * spec.nqh * spec.hd * 4);
+    const entries = [{ q: qOut, kCache: kc, vCache: vc, out: out, nTokens: spec.nTokens, start: spec.start,
+      vtCache: vt, vtRows: spec.rows }];
+    const ws = alloc(Math.max(att.attnPrefillWorkspaceSize(entries, shape), 1));
+    att.attnPrefill(entries, shape, ws);
+    parts.push(vt, out);
+  }
+  let total = 0;
+  for (const b of parts) total += b.size;
+  const res = new Uint8Array(total);
+  let off = 0;
+  for (const b of parts) {
+    att.readBuffer(b, 0, res.subarray(off, off + b.size));
+    off += b.size;
+  }
   fs.writeFileSync(path.join(dir, 'out.bin'), res);
   for (const b of bufs) att.destroyBuffer(b);
   att.dispose();
-  return ['attnPromptPrep: ' + spec.nTokens + ' tokens', 'results written'];
+  return ['attnPromptPrep: ' + spec.nTokens + ' tokens' + (vt ? ', V^T blocks, attnPrefill through them' : ''),
+    'results written'];
 }
 
 interface HeadSpec {
@@ -479,7 +496,7 @@ async function batch(dir: string): Promise<string[]> {
     maxBatch: spec.maxBatch, maxSeqLen: spec.maxSeqLen,
   });
   const outs: Uint8Array[] = [];
-  let launches = 0;
+  let launches = 0, begins = 0;
   att.enableProfile();
   for (let si = 0; si < spec.steps.length; si++) {
     const st = spec.steps[si];
@@ -495,8 +512,12 @@ async function batch(dir: string): Promise<string[]> {
         if (vc.byteLength) att.writeBuffer(sched.vCache(id, l), 0, vc);
       });
     });
-    // odd steps prepare every layer at once (one upload per head_dim group), even steps layer by layer
-    if (si % 2 === 1 && sched.beginToken() !== sched.activeIds().length) fail('beginToken count');
+    // steps 0, 4, 8, ... run layer by layer; the others make every layer ready at once (beginToken: a
+    // prepare, one upload per head_dim group, or the previous token's plans advanced on the host)
+    if (si % 4 !== 0) {
+      if (sched.beginToken() !== sched.activeIds().length) fail('beginToken count');
+      begins++;
+    }
     spec.layers.forEach(function (_L, l) {
       const ids = sched.activeIds();
       const producer = spec.layers[l].kvSource === l;
@@ -537,6 +558,7 @@ async function batch(dir: string): Promise<string[]> {
   for (const b of bufs) att.destroyBuffer(b);
   att.dispose();
   return [`${spec.steps.length} token steps`, `${launches} attnStep launches`, `${outs.length} outputs written`,
+    `beginToken: ${sched.prepares} prepared, ${begins - sched.prepares} advanced`,
     `profiled: attn.decodeFused p50 ${(rep.perLabel[0].p50_ns / 1e3).toFixed(1)} us over ${launches} passes`];
 }
 

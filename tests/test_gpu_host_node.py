@@ -205,7 +205,9 @@ def test_linear_through_ts_host(tmp_path, n, rows):
 @pytest.mark.skipif(NODE is None, reason="node is not installed")
 def test_continuous_batching_through_ts_host(tmp_path):
     """DecodeScheduler (host/scheduler.ts): sequences are submitted, admitted into three cache slots
-    (FIFO, lowest free slot), released and replaced over four token steps. Each step runs every layer
+    (FIFO, lowest free slot), released and replaced over eight token steps; steps 0 and 4 run layer by
+    layer, the rest prepare at beginToken (steps 1, 2 and 5) or, where the batch is the previous token's
+    (steps 3, 6 and 7), advance its plans on the host (attnStepAdvance). Each step runs every layer
     as one attnStep over the active sequences: a local head_dim-256 producer (window 40), a global
     head_dim-512 producer, and a local consumer of layer 0 that projects only q and reads the row its
     producer stored earlier in the same token. Every attnOut is checked against the oracle's decode
@@ -220,6 +222,10 @@ def test_continuous_batching_through_ts_host(tmp_path):
     steps = [dict(release=[], submit=[["A", 100], ["B", 37], ["C", 250], ["D", 5]], admitted=["A", "B", "C"]),
              dict(release=["B"], submit=[], admitted=["D"]),
              dict(release=["A"], submit=[["E", 0]], admitted=["E"]),
+             dict(release=[], submit=[], admitted=[]),
+             dict(release=["D"], submit=[["F", 60]], admitted=["F"]),
+             dict(release=[], submit=[], admitted=[]),
+             dict(release=[], submit=[], admitted=[]),
              dict(release=[], submit=[], admitted=[])]
     arrays, blob = {}, bytearray()
 
@@ -300,6 +306,7 @@ def test_continuous_batching_through_ts_host(tmp_path):
         worst = max(worst, err)
         assert np.isfinite(g).all() and err <= 2e-3, (si, l, sid, err)
     assert off == got.size
+    assert "beginToken: 3 prepared, 3 advanced" in r.stdout, r.stdout
     print(f"continuous batching: {len(expected)} outputs, worst max-abs {worst:.2e}")
 
 
@@ -360,11 +367,14 @@ def test_quantized_linear_through_ts_host(tmp_path, fmt):
 
 
 @pytest.mark.skipif(NODE is None, reason="node is not installed")
-@pytest.mark.parametrize("start,T,hd,theta,div", [(0, 64, 256, 1e4, 0), (5000, 33, 512, 1e6, 1)])
-def test_prompt_prep_through_ts_host(tmp_path, start, T, hd, theta, div):
+@pytest.mark.parametrize("start,T,hd,theta,div,vt", [(0, 64, 256, 1e4, 0, False), (5000, 33, 512, 1e6, 1, False),
+                                                     (1000, 77, 256, 1e6, 1, True)])
+def test_prompt_prep_through_ts_host(tmp_path, start, T, hd, theta, div, vt):
     """HipAttention.attnPromptPrep over the addon: q_out and the stored K/V rows bit-identical to the oracle's
-    per-token fused_per_head_norm_rope / per_head_rms_norm_no_weight rounded to f16; other rows untouched."""
-    announce(f"TS host attnPromptPrep start={start} T={T} hd={hd}")
+    per-token fused_per_head_norm_rope / per_head_rms_norm_no_weight rounded to f16; other rows untouched.
+    With a vtCache: the V^T blocks hold the stored V rows (the rest of the last block 0), and attnPrefill
+    of the chunk reading V from them matches the oracle's decode chain within 2e-3."""
+    announce(f"TS host attnPromptPrep start={start} T={T} hd={hd} vt={vt}")
     seed = 300 + start + T
     rows = start + T + 2
     arrs = {"q": synth.normal(seed, T * NQH * hd), "k": synth.normal(seed + 1, T * NKH * hd),
@@ -377,15 +387,33 @@ def test_prompt_prep_through_ts_host(tmp_path, start, T, hd, theta, div):
         blob += b
     (tmp_path / "case.bin").write_bytes(bytes(blob))
     (tmp_path / "case.json").write_text(json.dumps(dict(nqh=NQH, nkh=NKH, hd=hd, start=start, nTokens=T,
-                                                        theta=theta, div=div, rows=rows, arrays=index)))
+                                                        theta=theta, div=div, rows=rows, vt=vt, arrays=index)))
     r = subprocess.run([NODE, str(RUN), "promptprep", str(tmp_path)], cwd=ROOT, capture_output=True, text=True,
                        timeout=120)
     assert r.returncode == 0, r.stderr
-    raw = np.frombuffer((tmp_path / "out.bin").read_bytes(), np.uint16)
+    raw_bytes = (tmp_path / "out.bin").read_bytes()
+    raw = np.frombuffer(raw_bytes, np.uint16)
     nq = T * NQH * hd
+    nc = rows * NKH * hd
     q_out = raw[:nq].reshape(T, NQH * hd)
-    kc = raw[nq:nq + rows * NKH * hd].reshape(rows, NKH * hd)
-    vc = raw[nq + rows * NKH * hd:].reshape(rows, NKH * hd)
+    kc = raw[nq:nq + nc].reshape(rows, NKH * hd)
+    vc = raw[nq + nc:nq + 2 * nc].reshape(rows, NKH * hd)
+    if vt:
+        nb = (rows + 31) // 32
+        vtb = raw[nq + 2 * nc:nq + 2 * nc + nb * 32 * hd].reshape(nb, hd, 32)
+        want_vt = np.zeros((nb, hd, 32), np.uint16)  # allocated zeroed; the prep writes the chunk's rows
+        for r_ in range(start, start + T):
+            want_vt[r_ // 32, :, r_ % 32] = vc[r_]
+        np.testing.assert_array_equal(vtb, want_vt, err_msg="V^T blocks")
+        out = np.frombuffer(raw_bytes[2 * (nq + 2 * nc + nb * 32 * hd):], np.float32).reshape(T, NQH * hd)
+        kf = orc.f16_bits_to_f32(kc).reshape(rows, hd)
+        vf = orc.f16_bits_to_f32(vc).reshape(rows, hd)
+        for t in range(0, T, 4):
+            pos = start + t
+            qf = orc.f16_bits_to_f32(q_out[t])
+            want = orc.attention_chain(qf, kf[:pos + 1].reshape(-1), vf[:pos + 1].reshape(-1), NQH, NKH, hd, pos + 1,
+                                       1.0, 0)
+            assert max_abs(out[t], want) <= 2e-3, t
     for t in range(T):
         pos = start + t
         q_ = orc.fused_per_head_norm_rope(arrs["q"][t * NQH * hd:(t + 1) * NQH * hd], arrs["qw"], ROPE, NQH, hd, EPS,
