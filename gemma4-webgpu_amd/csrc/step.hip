@@ -7,7 +7,9 @@
 // i.e. the dispatch sequence of src/engine.ts:2056-2094 (shaders
 // per_head_rms_norm_no_weight.wgsl, fused_per_head_norm_rope.wgsl,
 // kv_cache_store.wgsl, attn_score.wgsl, softmax.wgsl, attn_output.wgsl),
-// with flash-decoding split-K and the split merge inside the same launch.
+// with flash-decoding split-K; entries split over several workgroups are
+// merged by a second launch (the log-sum-exp merge of decode.hip), or inside
+// the output projection's launch (k_step_out).
 //
 // Work split: the host cuts every entry's attended rows into 32-row tiles and
 // gives each entry a number of workgroups proportional to its tiles (at least

@@ -311,28 +311,118 @@ export const KERNELS: Record<KernelName, Launch> = {
 // Query slots per forward (the engine's PROFILE_QUERY_SLOTS, src/engine.ts:148): two per timed pass.
 export const PROFILE_QUERY_SLOTS = 2048;
 
+// The timing behind the profiler API. A forward (the passes enqueued between two harvests) owns one
+// query set and takes two slots of it per pass, in pass order. harvest() closes the forward and resolves
+// its set off the JS thread; the next pass opens a new forward on a spare set (or a new one), so the
+// passes enqueued while a resolve runs never re-record the events it reads. Durations accumulate per
+// label, and each forward's sum of durations is kept for the forward median. A pass that finds its
+// forward's set full runs untimed and the report says so.
+class PassTimer {
+  on = false;
+  private readonly g4: Addon;
+  private current: { set: bigint; labels: string[] } | null = null;  // the open forward
+  private readonly spares: bigint[] = [];
+  private readonly durations: Map<string, number[]> = new Map();
+  private readonly forwardSums: number[] = [];
+  private full = false;
+  private gone = false;
+
+  constructor(g4: Addon) {
+    this.g4 = g4;
+  }
+
+  begin(label: string): number {
+    if (!this.on) return -1;
+    if (this.current === null) {
+      const set = this.spares.length ? this.spares.pop() as bigint : this.g4.querySetCreate(PROFILE_QUERY_SLOTS);
+      this.current = { set: set, labels: [] };
+    }
+    const first = 2 * this.current.labels.length;
+    if (first + 2 > PROFILE_QUERY_SLOTS) {
+      this.full = true;
+      return -1;
+    }
+    this.g4.queryBeginPass(this.current.set, first);
+    this.current.labels.push(label);
+    return first;
+  }
+
+  harvest(): Promise<void> {
+    const fwd = this.current;
+    this.current = null;
+    if (fwd === null) return Promise.resolve();
+    const timer = this;
+    const recycle = function () {
+      if (timer.gone) timer.g4.querySetDestroy(fwd.set);
+      else timer.spares.push(fwd.set);
+    };
+    return this.g4.queryResolveAsync(fwd.set, 0, fwd.labels.length).then(function (ns: Float64Array) {
+      recycle();
+      let sum = 0;
+      fwd.labels.forEach(function (label, i) {
+        const d = ns[i];
+        if (!(d > 0)) return;  // NaN: the pass launched no kernel
+        sum += d;
+        const list = timer.durations.get(label);
+        if (list) list.push(d);
+        else timer.durations.set(label, [d]);
+      });
+      if (sum > 0) timer.forwardSums.push(sum);
+    }, function (e: any) {
+      recycle();
+      throw e;
+    });
+  }
+
+  clear(): void {
+    this.durations.clear();
+    this.forwardSums.length = 0;
+    this.full = false;
+  }
+
+  report(): ProfileReport {
+    // the sample at rank floor(n f) of the sorted samples (the last one at most)
+    function rank(sorted: number[], f: number): number {
+      return sorted[Math.min(sorted.length - 1, Math.floor(sorted.length * f))];
+    }
+    function ascending(a: number, b: number): number { return a - b; }
+    const rows: ProfileReport['perLabel'] = [];
+    this.durations.forEach(function (list, label) {
+      if (!list.length) return;
+      const sorted = list.slice().sort(ascending);
+      const total = list.reduce(function (acc, x) { return acc + x; }, 0);
+      rows.push({ label: label, samples_n: list.length, p50_ns: rank(sorted, 0.5), p95_ns: rank(sorted, 0.95),
+        mean_ns: total / list.length, total_ns: total });
+    });
+    rows.sort(function (a, b) { return b.p50_ns - a.p50_ns; });
+    const sums = this.forwardSums.slice().sort(ascending);
+    return { perLabel: rows, forwardMedian_ns: sums.length ? rank(sums, 0.5) : 0, forwardSamples_n: sums.length,
+      overflow: this.full };
+  }
+
+  // After the stream is drained: every set this timer holds is destroyed (one still being resolved is
+  // destroyed when its resolve ends).
+  destroy(): void {
+    this.gone = true;
+    if (this.current !== null) this.g4.querySetDestroy(this.current.set);
+    this.current = null;
+    for (const set of this.spares) this.g4.querySetDestroy(set);
+    this.spares.length = 0;
+  }
+}
+
 export class HipAttention {
   readonly stream: bigint;
   private readonly g4: Addon;
   private alive: boolean;
-  // Per-pass GPU timing (src/engine.ts:136-148, 3085-3288): two query slots per labelled pass, resolved
-  // by collectProfileSamples() after a forward's passes are enqueued. A forward writes its own query set;
-  // collect hands it to the resolve and the next forward takes another from the free list (or a new one),
-  // so a forward enqueued while the last one resolves does not overwrite its timestamps.
-  private profileActive = false;
-  private profileQuerySet: bigint | null = null;
-  private readonly profileFreeSets: bigint[] = [];
-  private profileSlotCursor = 0;
-  private profilePassLabels: string[] = [];
-  private readonly profileSamples: Map<string, number[]> = new Map();
-  private readonly profileForwardTotals_ns: number[] = [];
-  private profileOverflow = false;
+  private readonly timer: PassTimer;  // per-pass GPU timing (the engine's profiler API, below)
 
   constructor(addon: Addon, device: number) {
     this.g4 = addon;
     addon.setDevice(device);
     this.stream = addon.streamCreate();
     this.alive = true;
+    this.timer = new PassTimer(addon);
   }
 
   version(): string {
@@ -612,7 +702,7 @@ export class HipAttention {
     }
   }
 
-  // ---- profiling (src/engine.ts:3085-3288) ----
+  // ---- profiling: the engine's API and report (src/engine.ts:3085-3288, src/types.ts:490-515) ----
 
   getProfileCapability(): ProfileCapability {
     return { timestampQuerySupported: true, timestampQueryOnAdapterButUnrequested: false,
@@ -621,97 +711,32 @@ export class HipAttention {
 
   // Every pass enqueued from now on is timed, until disableProfile().
   enableProfile(): void {
-    this.profileActive = true;
+    this.timer.on = true;
   }
 
   disableProfile(): void {
-    this.profileActive = false;
+    this.timer.on = false;
   }
 
   resetProfileSamples(): void {
-    this.profileSamples.clear();
-    this.profileForwardTotals_ns.length = 0;
-    this.profileOverflow = false;
+    this.timer.clear();
   }
 
   // Per label: percentiles over the samples of every forward collected so far, largest p50 first.
   getProfileReport(): ProfileReport {
-    const perLabel: ProfileReport['perLabel'] = [];
-    this.profileSamples.forEach(function (samples, label) {
-      if (samples.length === 0) return;
-      const sorted = samples.slice().sort(function (a, b) { return a - b; });
-      let sum = 0;
-      for (const x of samples) sum += x;
-      perLabel.push({
-        label: label, samples_n: samples.length,
-        p50_ns: sorted[Math.floor(sorted.length * 0.5)],
-        p95_ns: sorted[Math.min(sorted.length - 1, Math.floor(sorted.length * 0.95))],
-        mean_ns: sum / samples.length, total_ns: sum,
-      });
-    });
-    perLabel.sort(function (a, b) { return b.p50_ns - a.p50_ns; });
-    const fwd = this.profileForwardTotals_ns.slice().sort(function (a, b) { return a - b; });
-    return {
-      perLabel: perLabel,
-      forwardMedian_ns: fwd.length > 0 ? fwd[Math.floor(fwd.length * 0.5)] : 0,
-      forwardSamples_n: fwd.length,
-      overflow: this.profileOverflow,
-    };
+    return this.timer.report();
   }
 
   // Ends a forward: waits (off the JS thread) for the timestamps of the passes enqueued since the last
   // collect, adds each pass's duration to its label's samples and their sum to the forward totals.
   collectProfileSamples(): Promise<void> {
-    const labels = this.profilePassLabels;
-    const used = this.profileSlotCursor;
-    const qs = this.profileQuerySet;
-    this.profilePassLabels = [];
-    this.profileSlotCursor = 0;
-    this.profileQuerySet = null;
-    if (qs === null) return Promise.resolve();
-    const self = this;
-    const release = function () {
-      if (self.alive) self.profileFreeSets.push(qs);
-      else self.g4.querySetDestroy(qs);
-    };
-    return this.g4.queryResolveAsync(qs, 0, used / 2).then(function (ns: Float64Array) {
-      release();
-      let total = 0;
-      for (let i = 0; i < labels.length; i++) {
-        const d = ns[i];
-        if (!(d > 0)) continue;  // NaN: the pass launched nothing
-        total += d;
-        let arr = self.profileSamples.get(labels[i]);
-        if (!arr) {
-          arr = [];
-          self.profileSamples.set(labels[i], arr);
-        }
-        arr.push(d);
-      }
-      if (total > 0) self.profileForwardTotals_ns.push(total);
-    }, function (e: any) {
-      release();
-      throw e;
-    });
+    return this.timer.harvest();
   }
 
   // Opens a pass: the library kernels launched until endPass carry its two slots on their own dispatches
-  // (the first one's start, the last one's end). Returns the first slot, or -1 when profiling is off or
-  // the set is full (then the pass runs untimed and the report says overflow).
+  // (the first one's start, the last one's end). Returns the pass's first slot, or -1 when it is untimed.
   private beginPass(label: string): number {
-    if (!this.profileActive) return -1;
-    const slot = this.profileSlotCursor;
-    if (slot + 2 > PROFILE_QUERY_SLOTS) {
-      this.profileOverflow = true;
-      return -1;
-    }
-    if (this.profileQuerySet === null) {
-      this.profileQuerySet = this.profileFreeSets.pop() || this.g4.querySetCreate(PROFILE_QUERY_SLOTS);
-    }
-    this.g4.queryBeginPass(this.profileQuerySet, slot);
-    this.profileSlotCursor = slot + 2;
-    this.profilePassLabels.push(label);
-    return slot;
+    return this.timer.begin(label);
   }
 
   private endPass(slot: number): void {
@@ -725,10 +750,7 @@ export class HipAttention {
   dispose(): void {
     if (!this.alive) return;
     this.g4.streamSynchronize(this.stream);
-    if (this.profileQuerySet !== null) this.g4.querySetDestroy(this.profileQuerySet);
-    this.profileQuerySet = null;
-    for (const q of this.profileFreeSets) this.g4.querySetDestroy(q);
-    this.profileFreeSets.length = 0;
+    this.timer.destroy();
     this.g4.streamDestroy(this.stream);
     this.alive = false;
   }
