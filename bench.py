@@ -251,6 +251,9 @@ class CacheSet:
         """The projections either side of every layer's attention (random f16 weights of E2B's shapes):
         attn.linearQKV into the entry's raw q/k/v (q alone for a consumer, whose k/v come from its
         producer) and attn.linearOut from attnOut (src/engine.ts:2045-2052, 2096)."""
+        import numpy as np
+
+        from g4attn import e2b, ops
         self.hidden = hidden
         self.x = torch.randn(hidden, device=dev)
         self.chain = []
@@ -264,6 +267,36 @@ class CacheSet:
                    for rows, out in segs]
             wo = (torch.randn(hidden, n, device=dev) * 0.02).half().view(torch.int16)
             self.chain.append((plan, qkv, n, wo, it["out"], torch.empty(hidden, device=dev)))
+        # The fused variant: attn.linearQKV with the prep as its epilogue (g4_linear_qkv_prep: projection,
+        # norms, RoPE, K/V row stored), then steps whose q is ready and whose current row is in the cache.
+        rf = torch.from_numpy(np.array(e2b.rope_freqs_f16_bits(256), np.uint16).view(np.int16)).to(dev)
+        self.rf_dev, self.inv_dev, self.ready = rf, {}, []
+        self.prep_ws = torch.zeros(ops.qkv_prep_workspace_bytes(NQH, NKH), dtype=torch.uint8, device=dev)
+        for it in self.items:
+            hd = it["hd"]
+            key = (it["theta"], it["apply_divisor"], hd)
+            if key not in self.inv_dev:
+                self.inv_dev[key] = ops.rope_inv_freq(it["theta"], hd, it["apply_divisor"], rf)
+            w = torch.empty(ops.step_workspace_bytes(1, NQH, NKH, hd), dtype=torch.uint8, device=dev)
+            e = dict(it, k=None, v=None, k_weight=None, store_kv=False, q_ready=True)
+            self.ready.append((w, ops.attn_step_prepare(ops.make_step_entries([e], NQH, NKH, hd), NQH, NKH, hd, w)))
+
+    def step_chain_prep(self, ops):
+        """One token in the engine's order with the fused projection: per layer, g4_linear_qkv_prep (q/k/v
+        projection with norms, RoPE and the K/V store as its epilogue), the attention pass on the ready q,
+        and o_proj with the merge folded in (three launches)."""
+        for (plan, qkv, n, wo, attn_out, y), (_, ready), it in zip(self.chain, self.ready, self.items):
+            hd = it["hd"]
+            store = it["store_kv"]
+            rows = it["k_cache"].numel() // (NKH * hd)
+            ops.linear_qkv_prep(self.x, self.hidden, "f16", qkv, it["q_weight"], NQH, NKH, hd, it["position"],
+                                it["theta"], it["apply_divisor"], self.prep_ws, k_weight=it["k_weight"],
+                                rope_freqs=self.rf_dev, rope_inv_freq=self.inv_dev[(it["theta"], it["apply_divisor"],
+                                                                                     hd)],
+                                k_cache=it["k_cache"] if store else None, v_cache=it["v_cache"] if store else None,
+                                slot=it["seq_len"] - 1, max_seq_len=rows)
+            ops.attn_step_run_attention(ready)
+            ops.attn_step_run_out(ready, n, [(wo, y, self.hidden)])
 
     def step_chain(self, ops, fused):
         """One token in the engine's order: per layer, q/k/v projection, attention pass, then the merge
@@ -398,8 +431,10 @@ def run_gpu(spec, args, decode_loop=False):
         cs.prepare_chain(torch, dev)
         result["chain_us"] = graph_us(lambda: cs.step_chain(ops, fused=False))
         result["chain_fused_us"] = graph_us(lambda: cs.step_chain(ops, fused=True))
+        result["chain_prep_us"] = graph_us(lambda: cs.step_chain_prep(ops))
         log(f"layer chain with projections (graph replay, GPU time): {result['chain_us']:.1f} us/token with the merge "
-            f"launch, {result['chain_fused_us']:.1f} us/token with the merge folded into o_proj")
+            f"launch, {result['chain_fused_us']:.1f} us/token with the merge folded into o_proj, "
+            f"{result['chain_prep_us']:.1f} us/token with the prep folded into the q/k/v projection as well")
     del csets
     torch.cuda.empty_cache()
     return result
@@ -774,8 +809,11 @@ def decode_line(name, args, decode_loop):
         line["layer_chain"] = {
             "merge_launch_us_per_token": round(r["chain_us"], 2),
             "merge_in_o_proj_us_per_token": round(r["chain_fused_us"], 2),
+            "prep_in_qkv_us_per_token": round(r["chain_prep_us"], 2),
             "what": "per token, every layer in the engine's order: q/k/v projection, attention pass, then the merge "
-                    "launch and o_proj, or o_proj with the merge folded in (g4_attn_step_run_out); f16 weights of "
+                    "launch and o_proj, or o_proj with the merge folded in (g4_attn_step_run_out), or with the "
+                    "norms, RoPE and K/V store folded into the q/k/v projection (g4_linear_qkv_prep) and the merge "
+                    "into o_proj; f16 weights of "
                     "E2B's shapes (hidden 1536); a HIP graph queued ahead of the GPU, median GPU time of a replay"}
     if not args.no_cpu_baseline:
         cpu = run_cpu_baseline(spec, args.cpu_seconds)

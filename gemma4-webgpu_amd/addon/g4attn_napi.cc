@@ -788,6 +788,79 @@ napi_value LinearQuant(napi_env env, napi_callback_info info) {
     return undefined(env);
 }
 
+// linearQkvPrepWorkspaceSize(numQHeads, numKvHeads): bytes of the per-head arrival counters.
+napi_value LinearQkvPrepWorkspaceSize(napi_env env, napi_callback_info info) {
+    Args a(env, info, 2);
+    const uint32_t nqh = a.u32(0), nkh = a.u32(1);
+    if (!a.ok) return nullptr;
+    size_t bytes = 0;
+    CALL(env, g4_linear_qkv_prep_workspace_size(nqh, nkh, &bytes));
+    napi_value r;
+    NAPI_OK(env, napi_create_double(env, (double)bytes, &r));
+    return r;
+}
+
+// linearQkvPrep(x, n, format, segments [{weight, meta (q8 / q4k), out, rows}], qWeight, kWeight, ropeFreqs,
+// ropeInvFreq, kCache, vCache, params (g4_qkv_prep_params bytes), workspace, stream): g4_linear_qkv_prep;
+// kWeight and the caches null on KV-consumer layers (one segment).
+napi_value LinearQkvPrep(napi_env env, napi_callback_info info) {
+    Args a(env, info, 13);
+    void* x = a.ptr(0);
+    const uint32_t n = a.u32(1), format = a.u32(2);
+    void* qw = a.ptr(4);
+    void* kw = a.ptr(5);
+    void* rf = a.ptr(6);
+    void* inv = a.ptr(7);
+    void* kc = a.ptr(8);
+    void* vc = a.ptr(9);
+    g4_qkv_prep_params p;
+    a.params(10, &p);
+    void* ws = a.ptr(11);
+    void* s = a.ptr(12);
+    if (!a.ok) return nullptr;
+    bool is_array = false;
+    napi_is_array(env, a.v[3], &is_array);
+    if (!is_array) {
+        a.fail("linearQkvPrep: segments must be an array");
+        return nullptr;
+    }
+    uint32_t count = 0;
+    napi_get_array_length(env, a.v[3], &count);
+    std::vector<g4_linear_qseg> segs(count);
+    for (uint32_t i = 0; i < count; i++) {
+        napi_value obj, v;
+        napi_get_element(env, a.v[3], i, &obj);
+        const std::string at = "linearQkvPrep: segment " + std::to_string(i) + ": ";
+        const void* ptrs[3] = {};
+        const char* keys[3] = {"weight", "meta", "out"};
+        for (int k = 0; k < 3; k++) {
+            uint64_t q = 0;
+            bool lossless = false;
+            if (!get_prop(env, obj, keys[k], &v)) {
+                if (k == 1) continue;  // f16 weights have no meta
+                a.fail(at + keys[k] + " must be a BigInt pointer");
+                return nullptr;
+            }
+            if (napi_get_value_bigint_uint64(env, v, &q, &lossless) != napi_ok || !lossless) {
+                a.fail(at + keys[k] + " must be a BigInt pointer");
+                return nullptr;
+            }
+            ptrs[k] = reinterpret_cast<const void*>(static_cast<uintptr_t>(q));
+        }
+        uint32_t rows = 0;
+        if (!get_prop(env, obj, "rows", &v) || napi_get_value_uint32(env, v, &rows) != napi_ok) {
+            a.fail(at + "rows must be a number");
+            return nullptr;
+        }
+        segs[i] = g4_linear_qseg{ptrs[0], static_cast<const uint16_t*>(ptrs[1]), (float*)const_cast<void*>(ptrs[2]),
+                                 rows};
+    }
+    CALL(env, g4_linear_qkv_prep((const float*)x, n, format, segs.data(), count, (const uint16_t*)qw,
+                                 (const uint16_t*)kw, (const uint16_t*)rf, (const float*)inv, (uint16_t*)kc,
+                                 (uint16_t*)vc, p, ws, s));
+    return undefined(env);
+}
+
 // One g4_step_entry from a JS object with the same field names in camelCase.
 bool step_entry(Args& a, napi_value obj, size_t idx, uint32_t head_dim, g4_step_entry* e) {
     napi_env env = a.env;
@@ -852,6 +925,7 @@ bool step_entry(Args& a, napi_value obj, size_t idx, uint32_t head_dim, g4_step_
         {"slidingWindow", &e->sliding_window, 0, false},
         {"storeKv", &e->store_kv, 1, false},
         {"applyDivisor", &e->apply_divisor, 0, false},
+        {"qReady", &e->q_ready, 0, false},
     };
     for (auto& f : u32s) {
         napi_value v;
@@ -1275,6 +1349,8 @@ napi_value Init(napi_env env, napi_value exports) {
         {"lmHeadArgmax", LmHeadArgmax},
         {"linear", Linear},
         {"linearQuant", LinearQuant},
+        {"linearQkvPrepWorkspaceSize", LinearQkvPrepWorkspaceSize},
+        {"linearQkvPrep", LinearQkvPrep},
         {"matmulQ8", MatmulQ8},
         {"matmulQ4K", MatmulQ4K},
         {"ropeInvFreq", RopeInvFreq},
@@ -1312,6 +1388,7 @@ napi_value Init(napi_env env, napi_value exports) {
         {"sizeofMatmulParams", sizeof(g4_matmul_params)},
         {"sizeofSoftcapParams", sizeof(g4_softcap_params)},
         {"sizeofArgmaxParams", sizeof(ArgmaxUniform)},
+        {"sizeofQkvPrepParams", sizeof(g4_qkv_prep_params)},
     };
     for (auto& s : sizes) NAPI_OK(env, napi_set_named_property(env, exports, s.name, number(env, (double)s.size)));
     return exports;

@@ -216,12 +216,13 @@ __global__ __launch_bounds__(64 * W, HD == 256 ? 8 / W : 1) void k_attn_step(
         }
 
         const float qscale = ent.qscale, eps = ent.eps;
+        const bool q_ready = ent.flags & kQReady;  // uniform: q is the post-norm, post-RoPE query already
         f16* qop = reinterpret_cast<f16*>(sm.dec.q);  // [chunk c][operand lane 16*g + column][8]
 #pragma unroll
         for (int r = 0; r < kQPerWave; r++) {
             const unsigned hq = (unsigned)wave + W * r;
             const bool live = hq < G;  // columns of absent heads are zero
-            if (live) wave_norm_rope<J>(xq[r], wq, true, true, rl, eps);
+            if (live && !q_ready) wave_norm_rope<J>(xq[r], wq, true, true, rl, eps);
 #pragma unroll
             for (int j = 0; j < J; j++) {
                 const unsigned d = (unsigned)lane + 64u * j;

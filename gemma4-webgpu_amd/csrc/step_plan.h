@@ -308,7 +308,8 @@ inline int plan_step(const g4_step_entry* entries, uint32_t n_entries, uint32_t 
         d.key_end = s.seq_len;
         d.n_parts = 0;  // set by the partition
         d.position = s.position;
-        d.flags = (s.store_kv ? kStoreKv : 0u) | (cached ? kRowCached : 0u) | (s.apply_divisor ? kApplyDivisor : 0u);
+        d.flags = (s.store_kv ? kStoreKv : 0u) | (cached ? kRowCached : 0u) | (s.apply_divisor ? kApplyDivisor : 0u) |
+                  (s.q_ready ? kQReady : 0u);
         d.theta = s.theta;
         d.window = s.sliding_window;
         d.qscale = s.scale * kLog2e;

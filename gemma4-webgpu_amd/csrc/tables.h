@@ -51,6 +51,7 @@ struct StepEntryDev {
 constexpr uint32_t kStoreKv = 1;       // write the current row's k and v to the caches
 constexpr uint32_t kRowCached = 2;     // the current row is already in the cache: read it like the others
 constexpr uint32_t kApplyDivisor = 4;  // RoPE frequencies divided by rope_freqs (global layers)
+constexpr uint32_t kQReady = 8;        // q holds the post-norm, post-RoPE query: read as is
 
 // First attended row of an entry whose rows end at key_end. (constexpr: the
 // kernels and the host planner share these.)

@@ -83,13 +83,19 @@ class StepEntry(C.Structure):
                 ("k_cache", C.c_void_p),
                 ("v_cache", C.c_void_p), ("out", C.c_void_p), ("seq_len", C.c_uint32), ("position", C.c_uint32),
                 ("sliding_window", C.c_uint32), ("store_kv", C.c_uint32), ("theta", C.c_float),
-                ("apply_divisor", C.c_uint32), ("scale", C.c_float), ("eps", C.c_float)]
+                ("apply_divisor", C.c_uint32), ("scale", C.c_float), ("eps", C.c_float), ("q_ready", C.c_uint32)]
 
 
 class PrefillEntry(C.Structure):
     _fields_ = [("q", C.c_void_p), ("k_cache", C.c_void_p), ("v_cache", C.c_void_p), ("out", C.c_void_p),
                 ("n_tokens", C.c_uint32), ("start", C.c_uint32), ("sliding_window", C.c_uint32),
                 ("scale", C.c_float), ("vt_cache", C.c_void_p), ("vt_rows", C.c_uint32)]
+
+
+class QkvPrepParams(C.Structure):
+    _fields_ = [("num_q_heads", C.c_uint32), ("num_kv_heads", C.c_uint32), ("head_dim", C.c_uint32),
+                ("position", C.c_uint32), ("slot", C.c_uint32), ("max_seq_len", C.c_uint32), ("eps", C.c_float),
+                ("theta", C.c_float), ("apply_divisor", C.c_uint32), ("store_kv", C.c_uint32)]
 
 
 class PromptPrepParams(C.Structure):
@@ -118,7 +124,7 @@ class LinearQSeg(C.Structure):
     _fields_ = [("weight", C.c_void_p), ("meta", C.c_void_p), ("out", C.c_void_p), ("rows", C.c_uint32)]
 
 
-G4_WEIGHT_Q8, G4_WEIGHT_Q4K = 1, 2
+G4_WEIGHT_F16, G4_WEIGHT_Q8, G4_WEIGHT_Q4K = 0, 1, 2
 
 
 class DecodePlan(C.Structure):
@@ -196,6 +202,8 @@ SIGNATURES: dict[str, list] = {
     "g4_matmul_q8": [_P, _P, _P, _P, MatmulParams, _P],
     "g4_matmul_q4k": [_P, _P, _P, _P, MatmulParams, _P],
     "g4_linear_quant": [_P, _U32, _U32, C.POINTER(LinearQSeg), _U32, _P],
+    "g4_linear_qkv_prep_workspace_size": [_U32, _U32, C.POINTER(C.c_size_t)],
+    "g4_linear_qkv_prep": [_P, _U32, _U32, C.POINTER(LinearQSeg), _U32, _P, _P, _P, _P, _P, _P, QkvPrepParams, _P, _P],
     "g4_logit_softcap": [_P, SoftcapParams, _P],
     "g4_argmax": [_P, _P, _U32, _P],
     "g4_lm_head_workspace_size": [LmHeadParams, C.POINTER(C.c_size_t)],

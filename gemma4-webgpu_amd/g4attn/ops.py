@@ -272,7 +272,8 @@ def make_step_entries(items, num_q_heads, num_kv_heads, head_dim):
     """items: iterable of dicts with q, k, v (raw f32 projections), q_weight, k_weight (f16), rope_freqs (f16 or
     None), rope_inv_freq_host (optional host f32 numpy table from rope_inv_freq_host(); kept alive by the caller
     until prepare returns), k_cache, v_cache (f16, at least seq_len rows),
-    out (f32), seq_len, position, sliding_window, store_kv, theta, apply_divisor, scale, eps.
+    out (f32), seq_len, position, sliding_window, store_kv, theta, apply_divisor, scale, eps, and q_ready (q
+    already holds the post-norm, post-RoPE query, as linear_qkv_prep leaves it).
     k, v and k_weight None (with store_kv False): the current row is already in the cache (a KV-consumer
     layer stepped after its producer)."""
     items = list(items)
@@ -296,7 +297,8 @@ def make_step_entries(items, num_q_heads, num_kv_heads, head_dim):
             _f16(it["k_cache"], f"entry {i} k_cache", L * nkv), _f16(it["v_cache"], f"entry {i} v_cache", L * nkv),
             _f32(it["out"], f"entry {i} out", num_q_heads * head_dim), L, int(it["position"]),
             int(it.get("sliding_window", 0)), 1 if it.get("store_kv", True) else 0, float(it["theta"]),
-            int(it["apply_divisor"]), float(it.get("scale", 1.0)), float(it.get("eps", 1e-6)))
+            int(it["apply_divisor"]), float(it.get("scale", 1.0)), float(it.get("eps", 1e-6)),
+            1 if it.get("q_ready") else 0)
     return arr
 
 
@@ -550,6 +552,45 @@ def linear_quant(x, n, fmt, segments, stream=None):
         segs[i] = LinearQSeg(wp, mp, _f32(out, f"segment {i} out", rows), rows)
     abi.call("g4_linear_quant", _f32(x, "input", n), n, G4_WEIGHT_Q8 if q8 else G4_WEIGHT_Q4K, segs, len(segments),
              _stream(stream))
+
+
+def qkv_prep_workspace_bytes(num_q_heads, num_kv_heads) -> int:
+    n = C.c_size_t(0)
+    abi.call("g4_linear_qkv_prep_workspace_size", num_q_heads, num_kv_heads, C.byref(n))
+    return n.value
+
+
+def linear_qkv_prep(x, n, fmt, segments, q_weight, num_q_heads, num_kv_heads, head_dim, position, theta,
+                    apply_divisor, workspace, k_weight=None, rope_freqs=None, rope_inv_freq=None, k_cache=None,
+                    v_cache=None, slot=0, max_seq_len=0, eps=1e-6, stream=None):
+    """attn.linearQKV with the producer-side prep as its epilogue (g4_linear_qkv_prep). fmt "f16"
+    (segments of (weight f16 [rows][n], out, rows)), "q8" or "q4k" (as linear_quant); segments q, k, v
+    on a KV producer (k_weight, caches of max_seq_len rows and slot given), q alone otherwise. The
+    workspace (qkv_prep_workspace_bytes) must be zero before the first call."""
+    from .abi import QkvPrepParams
+
+    fmt_code = {"f16": abi.G4_WEIGHT_F16, "q8": G4_WEIGHT_Q8, "q4k": G4_WEIGHT_Q4K}[fmt]
+    segs = (LinearQSeg * len(segments))()
+    for i, sg in enumerate(segments):
+        if fmt == "f16":
+            w, out, rows = sg
+            wp, mp = _f16(w, f"segment {i} weight", rows * n), None
+        else:
+            w, meta, out, rows = sg
+            wp = _dev(w, f"segment {i} weight", I8_TYPES, rows * n) if fmt == "q8" else \
+                _dev(w, f"segment {i} weight", U32_TYPES, rows * n // 8)
+            mp = _f16(meta, f"segment {i} meta", rows * (n // 32 if fmt == "q8" else n // 16))
+        segs[i] = LinearQSeg(wp, mp, _f32(out, f"segment {i} out", rows), rows)
+    store = k_cache is not None
+    p = QkvPrepParams(num_q_heads, num_kv_heads, head_dim, position, slot, max_seq_len, eps, theta,
+                      1 if apply_divisor else 0, 1 if store else 0)
+    rows = max_seq_len * num_kv_heads * head_dim
+    abi.call("g4_linear_qkv_prep", _f32(x, "input", n), n, fmt_code, segs, len(segments),
+             _f16(q_weight, "q_weight", head_dim), _f16(k_weight, "k_weight", head_dim) if store else None,
+             _f16(rope_freqs, "rope_freqs", head_dim // 2) if rope_freqs is not None else None,
+             _f32(rope_inv_freq, "rope_inv_freq", head_dim // 2) if rope_inv_freq is not None else None,
+             _f16(k_cache, "k_cache", rows) if store else None, _f16(v_cache, "v_cache", rows) if store else None,
+             p, _dev(workspace, "workspace", torch.uint8, 0), _stream(stream))
 
 
 def logit_softcap(logits, size, cap, stream=None):

@@ -32,7 +32,7 @@ export type QuantKernelName = 'matmulQ8' | 'matmulQ4K';
 
 export type KernelName = AttnKernelName | SampleKernelName | QuantKernelName;
 
-export type FusedKernelName = 'attnStep' | 'attnPrefill' | 'attnPromptPrep' | 'lmHeadArgmax';
+export type FusedKernelName = 'attnStep' | 'attnPrefill' | 'attnPromptPrep' | 'lmHeadArgmax' | 'linearQkvPrep';
 
 export type UniformValue = { u: number } | { f: number };
 
@@ -86,6 +86,7 @@ export const PASS_LABELS: Record<string, string> = {
   linear: 'attn.linearQKV',
   linearOut: 'attn.linearOut',
   attnStepOut: 'attn.linearOut',
+  linearQkvPrep: 'attn.linearQKVPrep',
 };
 
 // The profiler's report types (src/types.ts:490-515).
@@ -156,6 +157,7 @@ export interface StepEntry {
   applyDivisor?: number;
   scale?: number;
   eps?: number;
+  qReady?: boolean;           // q already holds the post-norm, post-RoPE query (linearQkvPrep's output)
 }
 
 // One prefill entry: a chunk of tokens of one layer (or sequence). Token t sits at position start + t and
@@ -194,6 +196,30 @@ export interface PromptPrep {
   theta: number;
   applyDivisor: number;
   maxSeqLen?: number;
+  eps?: number;
+}
+
+// linearQkvPrep: one segment of the q/k/v projection (q, then k and v on producer layers).
+export interface QkvSegment {
+  weight: DeviceBuffer;       // f16 [rows][n], int8 [rows][n] (q8) or u32 [rows][n/8] (q4k)
+  meta?: DeviceBuffer;        // q8 / q4k scales (as linearQuant)
+  out: DeviceBuffer;          // f32 [rows]: the layer's q / k / v buffer
+  rows: number;
+}
+
+// linearQkvPrep's epilogue: the layer's norms, RoPE configuration and, on producer layers, the cache row.
+export interface QkvPrep {
+  qWeight: DeviceBuffer;      // attn_q_norm f16 [HD]
+  kWeight?: DeviceBuffer;     // attn_k_norm f16 [HD] (producer layers)
+  ropeFreqs?: DeviceBuffer;   // f16 divisor table (global layers)
+  ropeInvFreq?: DeviceBuffer; // f32 [HD/2] from ropeInvFreq (computed once, at load)
+  kCache?: DeviceBuffer;      // f16 [maxSeqLen][NKH][HD]: row `slot` is written (producer layers)
+  vCache?: DeviceBuffer;
+  position: number;
+  slot?: number;
+  maxSeqLen?: number;
+  theta: number;
+  applyDivisor?: number;
   eps?: number;
 }
 
@@ -258,6 +284,10 @@ export interface Addon {
   matmulQ4K(x: bigint, q: bigint, m: bigint, o: bigint, p: Uint8Array, s: bigint): void;
   linearQuant(x: bigint, n: number, format: number, segs: { weight: bigint; meta: bigint; out: bigint; rows: number }[],
     s: bigint): void;
+  linearQkvPrepWorkspaceSize(nqh: number, nkh: number): number;
+  linearQkvPrep(x: bigint, n: number, format: number, segs: { weight: bigint; meta?: bigint; out: bigint; rows: number }[],
+    qw: bigint, kw: bigint | null, rf: bigint | null, inv: bigint | null, kc: bigint | null, vc: bigint | null,
+    p: Uint8Array, ws: bigint, s: bigint): void;
   logitSoftcap(l: bigint, p: Uint8Array, s: bigint): void;
   argmax(l: bigint, r: bigint, p: Uint8Array, s: bigint): void;
   lmHeadWorkspaceSize(vocab: number, hidden: number, cap: number): number;
@@ -528,6 +558,7 @@ export class HipAttention {
         seqLen: e.seqLen, position: e.position, slidingWindow: e.slidingWindow || 0,
         storeKv: e.storeKv === undefined ? true : e.storeKv, theta: e.theta, applyDivisor: e.applyDivisor || 0,
         scale: e.scale === undefined ? 1.0 : e.scale, eps: e.eps === undefined ? 1e-6 : e.eps,
+        qReady: e.qReady ? 1 : 0,
       };
     });
   }
@@ -679,6 +710,42 @@ export class HipAttention {
     const slot = this.beginPass(label || PASS_LABELS.linear);
     try {
       this.g4.linear(input.ptr, n, segs, this.stream);
+    } finally {
+      this.endPass(slot);
+    }
+  }
+
+  linearQkvPrepWorkspaceSize(shape: StepShape): number {
+    return this.g4.linearQkvPrepWorkspaceSize(shape.numQHeads, shape.numKvHeads);
+  }
+
+  // attn.linearQKV with the producer-side prep as its epilogue (src/engine.ts:2045-2091 in one launch): q, k, v
+  // projected, then normalised per head in place (q and k with RoPE at `position`) and, on producer layers (k
+  // segments given), the k and v rows stored at row `slot` of the caches; every value bit-identical to the
+  // reference's dispatches. The result feeds attnStep entries with qReady (and the row read from the cache).
+  // format 'f16' (segments without meta), 'q8' or 'q4k'. workspace: linearQkvPrepWorkspaceSize bytes, cleared once.
+  linearQkvPrep(input: DeviceBuffer, n: number, format: 'f16' | 'q8' | 'q4k', segments: QkvSegment[], p: QkvPrep,
+    shape: StepShape, workspace: DeviceBuffer): void {
+    if (input.size < n * 4) throw new RangeError('linearQkvPrep: input too small');
+    const store = segments.length === 3;
+    if (store && (!p.kWeight || !p.kCache || !p.vCache || p.maxSeqLen === undefined)) {
+      throw new Error('linearQkvPrep: a producer layer needs kWeight, kCache, vCache and maxSeqLen');
+    }
+    const segs = segments.map(function (g) {
+      return g.meta ? { weight: g.weight.ptr, meta: g.meta.ptr, out: g.out.ptr, rows: g.rows }
+        : { weight: g.weight.ptr, out: g.out.ptr, rows: g.rows };
+    });
+    const params = new Uniform([
+      { u: shape.numQHeads }, { u: shape.numKvHeads }, { u: shape.headDim }, { u: p.position }, { u: p.slot || 0 },
+      { u: p.maxSeqLen || 0 }, { f: p.eps === undefined ? 1e-6 : p.eps }, { f: p.theta },
+      { u: p.applyDivisor || 0 }, { u: store ? 1 : 0 },
+    ]);
+    function ptr(b: DeviceBuffer | undefined): bigint | null { return b ? b.ptr : null; }
+    const slot = this.beginPass(PASS_LABELS.linearQkvPrep);
+    try {
+      this.g4.linearQkvPrep(input.ptr, n, format === 'q8' ? 1 : format === 'q4k' ? 2 : 0, segs, p.qWeight.ptr,
+        ptr(p.kWeight), ptr(p.ropeFreqs), ptr(p.ropeInvFreq), ptr(p.kCache), ptr(p.vCache), params.bytes,
+        workspace.ptr, this.stream);
     } finally {
       this.endPass(slot);
     }

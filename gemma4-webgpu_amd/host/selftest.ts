@@ -562,6 +562,60 @@ async function batch(dir: string): Promise<string[]> {
     `profiled: attn.decodeFused p50 ${(rep.perLabel[0].p50_ns / 1e3).toFixed(1)} us over ${launches} passes`];
 }
 
+interface QkvPrepSpec {
+  n: number; nqh: number; nkh: number; hd: number; position: number; slot: number; rows: number; theta: number;
+  div: number; seq: number; arrays: Record<string, number[]>;
+}
+
+// attn.linearQKV with the prep as its epilogue (linearQkvPrep), then the decode step reading the ready q and
+// the stored row: out.bin = q, k, v (f32), the cache rows, attnOut.
+function qkvPrep(dir: string): string[] {
+  const spec = JSON.parse(fs.readFileSync(path.join(dir, 'case.json'), 'utf8')) as QkvPrepSpec;
+  const bin: Uint8Array = fs.readFileSync(path.join(dir, 'case.bin'));
+  const att = new HipAttention(loadAddon(), 0);
+  const bufs: DeviceBuffer[] = [];
+  function alloc(bytes: number): DeviceBuffer {
+    const b = att.createBuffer(bytes);
+    att.clearBuffer(b);
+    bufs.push(b);
+    return b;
+  }
+  function upload(name: string): DeviceBuffer {
+    const r = spec.arrays[name];
+    const b = alloc(r[1]);
+    att.writeBuffer(b, 0, bin.subarray(r[0], r[0] + r[1]));
+    return b;
+  }
+  const shape = { numQHeads: spec.nqh, numKvHeads: spec.nkh, headDim: spec.hd };
+  const rows = [spec.nqh * spec.hd, spec.nkh * spec.hd, spec.nkh * spec.hd];
+  const outs = rows.map(function (r) { return alloc(r * 4); });
+  const kc = upload('kc'), vc = upload('vc');
+  const segs = rows.map(function (r, i) { return { weight: upload('w' + i), out: outs[i], rows: r }; });
+  const qw = upload('qw'), kw = upload('kw'), rf = upload('rf');
+  const ws = alloc(att.linearQkvPrepWorkspaceSize(shape));
+  att.linearQkvPrep(upload('x'), spec.n, 'f16', segs, {
+    qWeight: qw, kWeight: kw, ropeFreqs: rf, kCache: kc, vCache: vc, position: spec.position, slot: spec.slot,
+    maxSeqLen: spec.rows, theta: spec.theta, applyDivisor: spec.div,
+  }, shape, ws);
+  const attnOut = alloc(spec.nqh * spec.hd * 4);
+  const stepWs = alloc(att.attnStepWorkspaceSize(1, shape));
+  att.attnStep([{ q: outs[0], qWeight: qw, ropeFreqs: rf, kCache: kc, vCache: vc, out: attnOut, seqLen: spec.seq,
+    position: spec.position, storeKv: false, theta: spec.theta, applyDivisor: spec.div, qReady: true }], shape, stepWs);
+  const parts = [outs[0], outs[1], outs[2], kc, vc, attnOut];
+  let total = 0;
+  for (const b of parts) total += b.size;
+  const res = new Uint8Array(total);
+  let off = 0;
+  for (const b of parts) {
+    att.readBuffer(b, 0, res.subarray(off, off + b.size));
+    off += b.size;
+  }
+  fs.writeFileSync(path.join(dir, 'out.bin'), res);
+  for (const b of bufs) att.destroyBuffer(b);
+  att.dispose();
+  return ['linearQkvPrep: 1 call', 'attnStep (qReady): 1 call', 'results written'];
+}
+
 // Promise readback: each copy is ordered where it was issued on the stream, whatever enqueues follow it.
 function readback(dir: string): Promise<string[]> {
   const bin: Uint8Array = fs.readFileSync(path.join(dir, 'case.bin'));
@@ -669,6 +723,7 @@ export function main(argv: string[]): void {
   else if (mode === 'prefill') done = prefill(argv[1]);
   else if (mode === 'promptprep') done = promptPrep(argv[1]);
   else if (mode === 'linear') done = linear(argv[1]);
-  else fail(`usage: run.js cpu | layer <dir> | prefill <dir> | promptprep <dir> | head <dir> | linear <dir> | batch <dir> | readback <dir> | profile`);
+  else if (mode === 'qkvprep') done = qkvPrep(argv[1]);
+  else fail(`usage: run.js cpu | layer <dir> | prefill <dir> | promptprep <dir> | head <dir> | linear <dir> | qkvprep <dir> | batch <dir> | readback <dir> | profile`);
   process.stdout.write(JSON.stringify({ ok: true, checks: done }) + '\n');
 }

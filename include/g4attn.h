@@ -364,6 +364,9 @@ typedef struct g4_step_entry {
     uint32_t apply_divisor;
     float scale;               /* attention scale (1.0 for Gemma 4) */
     float eps;
+    uint32_t q_ready;          /* 1: q already holds the post-norm, post-RoPE query (what
+                                  fused_per_head_norm_rope.wgsl leaves in it; g4_linear_qkv_prep's output):
+                                  the step reads it as is; q_weight is then not read */
 } g4_step_entry;
 
 int g4_attn_step_workspace_size(uint32_t n_entries, uint32_t num_q_heads, uint32_t num_kv_heads, uint32_t head_dim,
@@ -550,6 +553,7 @@ int g4_attn_step_run_out(const g4_decode_plan* plan, const g4_linear_seg* o_proj
  * matmulQ4K. weight: int8 [rows][n] (q8) or u32 [rows][n/8] (q4k); meta: the
  * f16 scales [rows][n/32] (q8) or scale/min table [rows][n/256][16] (q4k).
  * Same limits as g4_linear_f16; weight 16-byte aligned. */
+#define G4_WEIGHT_F16 0
 #define G4_WEIGHT_Q8 1
 #define G4_WEIGHT_Q4K 2
 typedef struct g4_linear_qseg {
@@ -561,6 +565,42 @@ typedef struct g4_linear_qseg {
 
 int g4_linear_quant(const float* input, uint32_t n, uint32_t format, const g4_linear_qseg* segs, uint32_t n_segs,
                     void* stream);
+
+/* attn.linearQKV with the attention block's producer-side prep as its
+ * epilogue, in one launch: the dispatches linearQKV, vNorm, fusedNormRope(Q),
+ * fusedNormRope(K), kvCacheStore of src/engine.ts:2045-2091. segs: q
+ * (num_q_heads * head_dim rows), then k and v (num_kv_heads * head_dim rows
+ * each) on KV-producer layers (store_kv 1), q alone on consumer layers; weights
+ * in `format` (G4_WEIGHT_F16: meta NULL; G4_WEIGHT_Q8 / G4_WEIGHT_Q4K as for
+ * g4_linear_quant). Afterwards each segment's out holds what the reference
+ * leaves in its q / k / v buffers: the projection (rows bit-identical to
+ * matmulQuant / matmulQ8 / matmulQ4K) normalised per head in place, q and k
+ * with RoPE at `position` (bit-identical to fused_per_head_norm_rope.wgsl /
+ * per_head_rms_norm_no_weight.wgsl), and on producer layers row `slot` of the
+ * f16 caches [rows][num_kv_heads][head_dim] holds k and v (kv_cache_store.wgsl,
+ * f16 RNE). rope_inv_freq: optional device [head_dim / 2] table from
+ * g4_rope_inv_freq; NULL: evaluated from theta / rope_freqs. workspace:
+ * g4_linear_qkv_prep_workspace_size bytes of per-head arrival counters,
+ * zeroed once after allocation (every call leaves them zero); calls sharing a
+ * workspace must not overlap. head_dim 256 or 512; n as g4_linear_f16. */
+typedef struct g4_qkv_prep_params {
+    uint32_t num_q_heads;
+    uint32_t num_kv_heads;
+    uint32_t head_dim;       /* 256 or 512 */
+    uint32_t position;       /* RoPE position of the token */
+    uint32_t slot;           /* cache row the k and v rows go to */
+    uint32_t max_seq_len;    /* cache rows (slot < max_seq_len) */
+    float eps;
+    float theta;
+    uint32_t apply_divisor;  /* 1 on global layers: divide by rope_freqs[i] */
+    uint32_t store_kv;       /* 1 on KV-producer layers */
+} g4_qkv_prep_params;
+
+int g4_linear_qkv_prep_workspace_size(uint32_t num_q_heads, uint32_t num_kv_heads, size_t* bytes);
+int g4_linear_qkv_prep(const float* input, uint32_t n, uint32_t format, const g4_linear_qseg* segs, uint32_t n_segs,
+                       const uint16_t* q_weight, const uint16_t* k_weight, const uint16_t* rope_freqs,
+                       const float* rope_inv_freq, uint16_t* k_cache, uint16_t* v_cache, g4_qkv_prep_params p,
+                       void* workspace, void* stream);
 
 /* ---- lm head -> logit softcap -> argmax (greedy top-1) ------------------
  * src/engine.ts:2223-2255: lmHead (matmulQuant over the f16 tied embedding

@@ -439,3 +439,57 @@ def test_profiler_through_ts_host(tmp_path):
     assert r.returncode == 0, r.stderr
     assert '"ok":true' in r.stdout
     print(r.stdout.strip())
+
+
+@pytest.mark.skipif(NODE is None, reason="node is not installed")
+def test_linear_qkv_prep_through_ts_host(tmp_path):
+    """HipAttention.linearQkvPrep over the addon (the q/k/v projection with the norms, RoPE and K/V store as
+    its epilogue), then attnStep on the ready q with the row read from the cache: q, k, v and the stored row
+    bit-identical to the oracle's matmulQuant followed by the reference prep kernels; attnOut within 2e-3."""
+    announce("TS host linearQkvPrep -> attnStep(qReady)")
+    n, hd, theta, div, seq = 1536, 256, 1e6, 1, 300
+    pos = seq - 1
+    rng = np.random.default_rng(61)
+    x = rng.standard_normal(n, dtype=np.float32)
+    w = [(rng.standard_normal((r, n), dtype=np.float32) * 0.05).astype(np.float16).view(np.uint16)
+         for r in (NQH * hd, NKH * hd, NKH * hd)]
+    qw, kw = f16_weight_bits(62, hd), f16_weight_bits(63, hd)
+    kc = np.zeros((seq, NKH * hd), np.uint16)
+    vc = np.zeros((seq, NKH * hd), np.uint16)
+    kc[:pos] = cache_f16(64, pos, NKH, hd).reshape(pos, -1)
+    vc[:pos] = cache_f16(65, pos, NKH, hd).reshape(pos, -1)
+    arrs = {"x": x, "w0": w[0], "w1": w[1], "w2": w[2], "qw": qw, "kw": kw, "rf": ROPE, "kc": kc, "vc": vc}
+    blob, index = bytearray(), {}
+    for name, a in arrs.items():
+        b = np.ascontiguousarray(a).tobytes()
+        index[name] = [len(blob), len(b)]
+        blob += b
+    (tmp_path / "case.bin").write_bytes(bytes(blob))
+    (tmp_path / "case.json").write_text(json.dumps(dict(n=n, nqh=NQH, nkh=NKH, hd=hd, position=pos, slot=pos, rows=seq,
+                                                        theta=theta, div=div, seq=seq, arrays=index)))
+    r = subprocess.run([NODE, str(RUN), "qkvprep", str(tmp_path)], cwd=ROOT, capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 0, r.stderr
+    raw = (tmp_path / "out.bin").read_bytes()
+    sizes = [NQH * hd * 4, NKH * hd * 4, NKH * hd * 4, seq * NKH * hd * 2, seq * NKH * hd * 2, NQH * hd * 4]
+    parts, off = [], 0
+    for sz in sizes:
+        parts.append(raw[off:off + sz])
+        off += sz
+    q, k, v = (np.frombuffer(p_, np.float32) for p_ in parts[:3])
+    gkc, gvc = (np.frombuffer(p_, np.uint16).reshape(seq, -1) for p_ in parts[3:5])
+    out = np.frombuffer(parts[5], np.float32)
+    want_q = orc.fused_per_head_norm_rope(orc.matmul_quant(x, w[0], NQH * hd, n), qw, ROPE, NQH, hd, EPS, pos,
+                                          theta, div)
+    want_k = orc.fused_per_head_norm_rope(orc.matmul_quant(x, w[1], NKH * hd, n), kw, ROPE, NKH, hd, EPS, pos,
+                                          theta, div)
+    want_v = orc.per_head_rms_norm_no_weight(orc.matmul_quant(x, w[2], NKH * hd, n), NKH, hd, EPS)
+    np.testing.assert_array_equal(q.view(np.uint32), want_q.view(np.uint32))
+    np.testing.assert_array_equal(k.view(np.uint32), want_k.view(np.uint32))
+    np.testing.assert_array_equal(v.view(np.uint32), want_v.view(np.uint32))
+    np.testing.assert_array_equal(gkc[pos], orc.f32_to_f16_bits(want_k))
+    np.testing.assert_array_equal(gvc[pos], orc.f32_to_f16_bits(want_v))
+    np.testing.assert_array_equal(gkc[:pos], kc[:pos])
+    want = orc.attention_chain(want_q, orc.f16_bits_to_f32(gkc).reshape(-1), orc.f16_bits_to_f32(gvc).reshape(-1),
+                               NQH, NKH, hd, seq, 1.0, 0)
+    assert max_abs(out, want) <= 2e-3
