@@ -72,8 +72,7 @@ EPS = 1e-6
 BASE_SEED = 20261201
 DEFAULT_WORKLOAD = "stack32k"
 REPLAN_TOKENS = 32  # decode loop: a plan advances on the host and is prepared again every this many tokens
-# the prefill kernel at head_dim 256 (G4_PREFILL_PP=0 selects the one-wave-per-SIMD form)
-PREFILL_KERNEL = "k_prefill_dma" if os.environ.get("G4_PREFILL_PP", "1") == "0" else "k_prefill_pp"
+PREFILL_KERNEL = "k_prefill_pp"  # the prefill kernel at head_dim 256
 
 
 def log(msg: str) -> None:

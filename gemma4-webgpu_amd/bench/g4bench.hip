@@ -23,9 +23,7 @@
 // `prefill4k` runs the causal MFMA prefill of a 4096-token prompt for one
 // global layer and one 512-window local layer, as 512-token chunks (16
 // entries in one launch; --mode whole: one entry per layer). `prefill4k512`
-// runs the global layer alone at head_dim 512 (E2B's global layers; with
-// G4_PREFILL_PP=0, each output half's workgroup computes the full-width
-// scores, so the MFMAs issue 1.5x the algorithmic flops it reports).
+// runs the global layer alone at head_dim 512 (E2B's global layers).
 //
 // `proj256` / `proj512` run the block's projections (q, k, v and o_proj) of a
 // local / global E2B layer (--mode fused|chain).

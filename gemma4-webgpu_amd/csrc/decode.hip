@@ -544,33 +544,20 @@ int noalloc_scratch(char** out) {
 
 namespace {
 
-int env_int(const char* name, int dflt) {
-    const char* s = getenv(name);
-    return s && *s ? atoi(s) : dflt;
-}
-
 constexpr unsigned kMinChunk = 128;
 
 inline unsigned round_up(unsigned x, unsigned m) { return (x + m - 1) / m * m; }
 
 
-// Rows per split: about `wgs_per_cu` workgroups per CU over the whole launch
-// (G4_DECODE_WGS_PER_CU, default 2), never fewer than kMinChunk rows (so the
-// partials stay small next to the rows read), and never more than
-// kMaxMergeSplits splits for the longest entry. G4_DECODE_CHUNK overrides.
-// head_dim 512 runs one workgroup per CU (its accumulators take twice the registers).
+// Rows per split: about two workgroups per CU over the whole launch (one at
+// head_dim 512: its accumulators take twice the registers), never fewer than
+// kMinChunk rows (so the partials stay small next to the rows read), and never
+// more than kMaxMergeSplits splits for the longest entry.
 unsigned pick_chunk(uint64_t total_rows, uint64_t max_entry_rows, unsigned num_kv_heads, unsigned head_dim) {
-    static const int env_chunk = env_int("G4_DECODE_CHUNK", 0);
-    static const int env_wgs = env_int("G4_DECODE_WGS_PER_CU", 0);
-    const int wgs_per_cu = env_wgs > 0 ? env_wgs : (head_dim == 512 ? 1 : 2);
-    unsigned chunk;
-    if (env_chunk > 0) {
-        chunk = round_up((unsigned)env_chunk, kTileKeys);
-    } else {
-        const uint64_t target = (uint64_t)(wgs_per_cu > 0 ? wgs_per_cu : 2) * device_cus() / (num_kv_heads ? num_kv_heads : 1);
-        const uint64_t c = (total_rows + target - 1) / (target ? target : 1);
-        chunk = round_up((unsigned)(c < kMinChunk ? kMinChunk : c), kTileKeys);
-    }
+    const uint64_t wgs_per_cu = head_dim == 512 ? 1 : 2;
+    const uint64_t target = wgs_per_cu * device_cus() / (num_kv_heads ? num_kv_heads : 1);
+    const uint64_t c = (total_rows + target - 1) / (target ? target : 1);
+    unsigned chunk = round_up((unsigned)(c < kMinChunk ? kMinChunk : c), kTileKeys);
     const uint64_t floor_rows = (max_entry_rows + kMaxMergeSplits - 1) / kMaxMergeSplits;
     if (chunk < floor_rows) chunk = round_up((unsigned)floor_rows, kTileKeys);
     return chunk;

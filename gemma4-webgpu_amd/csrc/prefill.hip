@@ -10,10 +10,10 @@
 //
 // Query rows: one kv head's G query heads of every token ("q-rows"
 // rho = token * G + head). A workgroup takes a tile of 128 q-rows (128/G
-// tokens) and a contiguous part of its key range; each of its 4 waves owns 32
-// q-rows, held as the B operand of the score MFMA for the whole pass.
+// tokens) and a contiguous part of its key range, in groups of 32 q-rows whose
+// query is held as the B operand of the score MFMA for the whole pass.
 //
-// Per 32-key tile (shared by the 4 waves through LDS, double-buffered):
+// Per 32-key tile (K rows and V^T blocks shared through LDS rings):
 //   S^T[32 keys x 32 q-rows] = K[keys x 16 d] * Q^T[16 d x q-rows], 16 MFMAs over HD = 256.
 //     The MFMA's A row m holds key pi(m) = m with bits 2 and 3 swapped, so the
 //     result register r of lane l holds key 16*(r/8) + 8*(l/32) + r%8 of q-row
@@ -21,8 +21,8 @@
 //     .. +8) of the output MFMA for key step s.
 //   online softmax per q-row in log2 units (the two half-waves hold 16 keys each)
 //   O^T[32 d x 32 q-rows] += V^T[32 d x 16 keys] * P^T[16 keys x q-rows], 8 d blocks x 2 key steps.
-//     V is stored transposed in LDS ([d][key]); 8x8 f16 blocks are transposed
-//     in registers (v_perm_b32) between the global load and the LDS store.
+//     V is read as 32-key V^T blocks [HD][32]: kept beside the cache by the
+//     prompt prep, or transposed once per call (k_vt_blocks).
 // P is rounded to f16 for the output MFMA (relative error <= 2^-11 per
 // probability); scores and sums stay f32.
 //
@@ -52,25 +52,21 @@ __device__ __forceinline__ unsigned wg_x() { return __builtin_amdgcn_workgroup_i
 __device__ __forceinline__ unsigned wg_y() { return __builtin_amdgcn_workgroup_id_y(); }
 __device__ __forceinline__ unsigned wg_z() { return __builtin_amdgcn_workgroup_id_z(); }
 
-constexpr int kPfHD = 256;
 constexpr int kPfWaves = 4;
 constexpr int kPfThreads = 64 * kPfWaves;
 constexpr int kPfRows = 32 * kPfWaves;   // q-rows per tile
 constexpr int kPfKeys = 32;              // keys per tile
 constexpr float kPfLazy = 15.0f;         // lazy-rescale threshold (log2 units): probabilities <= 2^15 (f16 max 65504)
-constexpr int kKRowBytes = kPfHD * 2 + 16;       // padded K row in LDS
-constexpr int kVtRowBytes = kPfKeys * 2 + 16;    // padded V^T row (one d) in LDS
 
 struct PrefillEntryDev {
     const uint16_t* q;    // f16 [n_tokens][num_q_heads][HD]
     const uint16_t* k;    // f16 [rows][num_kv_heads][HD]
-    const uint16_t* v;
     float* out;           // f32 [n_tokens][num_q_heads][HD]
     uint32_t n_tokens;
     uint32_t start;       // position of token 0
     uint32_t window;      // 0 = full
     float qscale;         // scale * log2(e)
-    const uint16_t* vt;   // V^T in 32-key blocks [kv head][block][HD][32] (pipelined kernel)
+    const uint16_t* vt;   // V^T in 32-key blocks [kv head][block][HD][32]
     uint32_t vt_blocks;   // blocks per kv head
     uint32_t pad;
 };
@@ -98,258 +94,25 @@ struct PrefillArgs {
     float* part_o;   // [slot][num_kv_heads][group][HD]
 };
 
-struct PrefillSmem {
-    unsigned char k[2][kPfKeys * kKRowBytes];
-    unsigned char vt[2][kPfHD * kVtRowBytes];
-};
-
 __device__ __forceinline__ unsigned key_of_row(unsigned m) {  // swap bits 2 and 3
     return (m & ~12u) | ((m & 4u) << 1) | ((m & 8u) >> 1);
 }
 
-// Global -> LDS for one 32-key tile starting at row kt0 (rows past `last` clamp to it).
-// Threads 0..127 move V as 8x8 blocks (8 keys x 8 d), transposed on the way;
-// threads 128..255 copy K rows (8 pieces of 16 bytes each).
-struct TileRegs {
-    u32x4 x[8];
-};
-
-__device__ __forceinline__ void tile_load(const char* Kb, const char* Vb, uint32_t row_bytes, unsigned kt0,
-                                          unsigned last, TileRegs& r) {
-    const int t = tid_x();
-    if (t < 128) {
-        const int kg = t >> 5, dg = t & 31;  // keys 8kg..8kg+8, d 8dg..8dg+8
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const unsigned row = min(kt0 + 8u * kg + i, last);
-            r.x[i] = ldg<u32x4>(Vb + ((uint64_t)row * row_bytes + dg * 16u));
-        }
-    } else {
-        const int u = t - 128;
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int piece = u + 128 * i;  // 32 keys x 32 pieces of 16 bytes
-            const unsigned row = min(kt0 + (unsigned)(piece >> 5), last);
-            r.x[i] = ldg<u32x4>(Kb + ((uint64_t)row * row_bytes + (piece & 31) * 16u));
-        }
-    }
-}
-
-__device__ __forceinline__ void tile_store(PrefillSmem& sm, int buf, const TileRegs& r) {
-    const int t = tid_x();
-    if (t < 128) {
-        const int kg = t >> 5, dg = t & 31;
-        // out[c] = the 8 keys at d = 8dg + c: word w holds keys (2w, 2w + 1), d-half c%2 of word c/2
-#pragma unroll
-        for (int c = 0; c < 8; c++) {
-            u32x4 o;
-#pragma unroll
-            for (int w = 0; w < 4; w++) {
-                const uint32_t a = r.x[2 * w][c >> 1], b = r.x[2 * w + 1][c >> 1];
-                o[w] = (c & 1) ? perm_hi(a, b) : perm_lo(a, b);
-            }
-            *reinterpret_cast<u32x4*>(&sm.vt[buf][(8 * dg + c) * kVtRowBytes + kg * 16]) = o;
-        }
-    } else {
-        const int u = t - 128;
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int piece = u + 128 * i;
-            *reinterpret_cast<u32x4*>(&sm.k[buf][(piece >> 5) * kKRowBytes + (piece & 31) * 16]) = r.x[i];
-        }
-    }
-}
-
-__global__ __launch_bounds__(kPfThreads, 1) void k_prefill(PrefillArgs a) {
-    __shared__ PrefillSmem sm;
-    const PrefillWorkDev wk = a.work[wg_x()];
-    const PrefillEntryDev& ent = a.table[wk.entry];
-    const unsigned kvh = wg_y();
-    const unsigned G = a.group, NQH = a.num_q_heads, NKH = a.num_kv_heads;
-    const int lane = tid_x() & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid_x() >> 6);
-    const int half = lane >> 5;    // which 8 of each 16 keys / d elements this lane supplies
-    const int col = lane & 31;     // this lane's q-row within the wave
-
-    // This lane's q-row: token and head, its absolute position and key window.
-    const unsigned rho = (unsigned)wk.tile * kPfRows + (unsigned)wave * 32u + (unsigned)col;
-    const unsigned tok = rho / G, head = rho % G;
-    const bool row_live = tok < ent.n_tokens;
-    const unsigned tok_c = row_live ? tok : ent.n_tokens - 1;
-    const unsigned pos = ent.start + tok_c;
-    const unsigned lo = (ent.window != 0 && pos + 1 > ent.window) ? pos + 1 - ent.window : 0u;
-    const unsigned hi = row_live ? pos : 0u;  // rows outside [lo, hi] are masked; dead rows see none
-    const bool dead = !row_live;
-
-    // Q^T operand: 16 key-steps of 8 f16 (d = 16s + 8*half .. +8), loaded once.
-    f16x8 qop[16];
-    {
-        const uint16_t* qr = ent.q + ((uint64_t)tok_c * NQH + kvh * G + head) * kPfHD + 8 * half;
-#pragma unroll
-        for (int s = 0; s < 16; s++) qop[s] = ldg<f16x8>(qr + 16 * s);
-    }
-
-    const uint32_t row_bytes = NKH * kPfHD * 2u;
-    const char* Kb = reinterpret_cast<const char*>(ent.k + (uint64_t)kvh * kPfHD);
-    const char* Vb = reinterpret_cast<const char*>(ent.v + (uint64_t)kvh * kPfHD);
-    const unsigned kb = wk.key_begin, ke = wk.key_end, last = ke - 1;
-    const unsigned n_tiles = (ke - kb + kPfKeys - 1) / kPfKeys;
-    const float qs = ent.qscale;
-
-    TileRegs stage;
-    tile_load(Kb, Vb, row_bytes, kb, last, stage);
-    tile_store(sm, 0, stage);
-    __syncthreads();
-
-    float m_run = -INFINITY, l_run = 0.0f;
-    f32x16 acc[8];
-#pragma unroll
-    for (int b = 0; b < 8; b++) acc[b] = f32x16{};
-    const unsigned krow = key_of_row((unsigned)col);  // K row this lane supplies to the score MFMA
-
-    for (unsigned it = 0; it < n_tiles; it++) {
-        const int buf = it & 1;
-        const unsigned kt0 = kb + it * kPfKeys;
-        if (it + 1 < n_tiles) tile_load(Kb, Vb, row_bytes, kt0 + kPfKeys, last, stage);
-
-        // scores: two accumulators over alternating d steps for MFMA overlap
-        f32x16 s0 = f32x16{}, s1 = f32x16{};
-        const unsigned char* kr = &sm.k[buf][krow * kKRowBytes + 16 * half];
-#pragma unroll
-        for (int s = 0; s < 16; s += 2) {
-            const f16x8 k0 = *reinterpret_cast<const f16x8*>(kr + 32 * s);
-            const f16x8 k1 = *reinterpret_cast<const f16x8*>(kr + 32 * (s + 1));
-            s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(k0, qop[s], s0, 0, 0, 0);
-            s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(k1, qop[s + 1], s1, 0, 0, 0);
-        }
-        // mask, tile max (the two half-waves hold the row's other 16 keys)
-        float x[16];
-        float tmax = -INFINITY;
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const unsigned key = kt0 + 16u * (r >> 3) + 8u * half + (r & 7);
-            const bool ok = !dead && key < ke && key >= lo && key <= hi;
-            x[r] = ok ? (s0[r] + s1[r]) * qs : -INFINITY;
-            tmax = fmaxf(tmax, x[r]);
-        }
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-        // Lazy rescale: the reference max moves only when the tile's max exceeds it by more than
-        // kPfLazy (log2 units), so probabilities stay below 2^kPfLazy and the accumulators (in AGPRs:
-        // a rescale is a read, multiply and write of all 128) are rescaled a few times per row
-        // instead of on nearly every tile. From -inf the first finite max always moves it.
-        const bool move = tmax > m_run + kPfLazy;
-        if (__any(move)) {
-            const float m_new = move ? tmax : m_run;
-            // 0 from -inf (acc and l are 0 there); 1 on lanes that keep their max
-            const float alpha = move ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
-            l_run *= alpha;
-#pragma unroll
-            for (int b = 0; b < 8; b++) acc[b] *= alpha;
-            m_run = m_new;
-        }
-        const float mu = m_run == -INFINITY ? 0.0f : m_run;
-        f16x8 pop[2];
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const float p = __builtin_amdgcn_exp2f(x[r] - mu);
-            l_run += p;
-            pop[r >> 3][r & 7] = (f16)p;
-        }
-        // O^T += V^T P^T
-        const unsigned char* vr = &sm.vt[buf][col * kVtRowBytes + 16 * half];
-#pragma unroll
-        for (int b = 0; b < 8; b++) {
-#pragma unroll
-            for (int s = 0; s < 2; s++) {
-                const f16x8 vop = *reinterpret_cast<const f16x8*>(vr + (32 * b) * kVtRowBytes + 32 * s);
-                acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vop, pop[s], acc[b], 0, 0, 0);
-            }
-        }
-        if (it + 1 < n_tiles) tile_store(sm, buf ^ 1, stage);
-        __syncthreads();
-    }
-
-    // Row sums: this lane's 16 keys plus the other half-wave's.
-    const float L = l_run + __shfl_xor(l_run, 32);
-    if (dead) return;
-    // Lane holds O^T rows d = 32b + 8*(r/4) + 4*half + r%4 of its q-row: 4 consecutive d per group.
-    const uint64_t qrow = (uint64_t)tok * NQH + kvh * G + head;
-    if (wk.n_parts == 1) {
-        float* dst = ent.out + qrow * kPfHD + 4 * half;
-        const float inv = 1.0f / L;
-#pragma unroll
-        for (int b = 0; b < 8; b++)
-#pragma unroll
-            for (int g = 0; g < 4; g++)
-                stg<f32x4>(dst + 32 * b + 8 * g, f32x4{acc[b][4 * g] * inv, acc[b][4 * g + 1] * inv,
-                                                      acc[b][4 * g + 2] * inv, acc[b][4 * g + 3] * inv});
-        return;
-    }
-    const unsigned tile_tok0 = (unsigned)wk.tile * kPfRows / G;
-    const uint64_t slot = (uint64_t)wk.split_base + (uint64_t)(tok - tile_tok0) * wk.n_parts + wk.part;
-    const uint64_t rec = (slot * NKH + kvh) * G + head;
-    float* po = a.part_o + rec * kPfHD + 4 * half;
-#pragma unroll
-    for (int b = 0; b < 8; b++)
-#pragma unroll
-        for (int g = 0; g < 4; g++)
-            stg<f32x4>(po + 32 * b + 8 * g, f32x4{acc[b][4 * g], acc[b][4 * g + 1], acc[b][4 * g + 2], acc[b][4 * g + 3]});
-    if (half == 0) stg<f32x2>(a.part_ml + rec * 2, f32x2{m_run, L});
-}
-
-// ---- pipelined form: LDS-DMA tiles, pre-transposed V ----------------------
+// ---- tiles: LDS-DMA of K rows and V^T blocks -------------------------------
 //
-// The same per-tile arithmetic, fed differently: K rows and V^T blocks go from
-// global memory straight into LDS (global_load_lds_dwordx4, no register
-// staging), one barrier per tile. V is transposed once
-// per prefill call into 32-key blocks [HD][32] (k_vt_blocks), so a V^T tile is
-// one contiguous read. The 16-byte chunks of both LDS tiles are XOR-swizzled
-// so that the MFMA operand reads hit distinct banks in every group of sixteen
-// lanes (a 128-bit LDS read is served 256 bytes at a time on gfx950; sixteen
-// lanes, each a different row, per LDS cycle).
-//
-// head_dim 512 (E2B global layers): a workgroup's output covers one half of
-// the head dimension (blockIdx.z), so the accumulators stay at 128 registers;
-// both halves compute the full-width scores (the K tile is 32 KiB, three
-// stages) and read their own 256 rows of the V^T block.
+// K rows and V^T blocks go from global memory straight into LDS
+// (global_load_lds_dwordx4, no register staging), one barrier per tile; a V^T
+// tile is one contiguous read. The 16-byte chunks of both LDS tiles are
+// XOR-swizzled so that the MFMA operand reads hit distinct banks in every
+// group of sixteen lanes (a 128-bit LDS read is served 256 bytes at a time on
+// gfx950; sixteen lanes, each a different row, per LDS cycle).
 
-// Tile t's K rows are read by the score MFMAs of iteration t - 1 and its V^T
-// block by the output MFMAs of iteration t + 1; both are issued together at
-// iteration t - 1 - kPfDist. The K ring holds kPfDist + 1 tiles, the V^T ring
-// kPfDist + 3 (128 KiB of LDS at either head_dim).
-template <int HD>
-constexpr int kPfDist = HD == 256 ? 2 : 1;
-template <int HD>
-constexpr int kPfKStages = kPfDist<HD> + 1;
-template <int HD>
-constexpr int kPfVStages = kPfDist<HD> + 3;
 template <int HD>
 constexpr unsigned kPfKTileBytes = kPfKeys * HD * 2;  // one K tile; also one V^T block in global memory
 constexpr unsigned kPfVtTileBytes = kPfKeys * 256 * 2;  // the V^T rows of one 256-wide output half
 
-template <int HD>
-struct PrefillDmaSmem {
-    unsigned char k[kPfKStages<HD>][kPfKTileBytes<HD>];  // key row r: chunk c (8 d) at r*2HD + ((c ^ swz_k(r)) * 16)
-    unsigned char vt[kPfVStages<HD>][kPfVtTileBytes];    // d row: chunk c (8 keys) at d*64 + ((c ^ swz_v(d)) * 16)
-};
-
 __device__ __forceinline__ unsigned swz_k(unsigned r) { return r & 15u; }
 __device__ __forceinline__ unsigned swz_v(unsigned d) { return (d >> 2) & 3u; }
-
-// Waits until at most `younger` tiles' DMAs of this wave are still in flight
-// (PER instructions per tile) and this wave's LDS reads have returned, then
-// joins the workgroup's barrier.
-template <int PER>
-__device__ __forceinline__ void dma_wait_barrier(int younger) {
-    if (younger >= 3)
-        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(3 * PER) : "memory");
-    else if (younger == 2)
-        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(2 * PER) : "memory");
-    else if (younger == 1)
-        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(PER) : "memory");
-    else
-        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
 
 // This wave's share of a tile: HD/64 DMA instructions of K (1 KiB each: 2
 // rows at head_dim 256, 1 at 512; rows past the range's last clamp to it) and
@@ -377,346 +140,9 @@ __device__ __forceinline__ DmaVOffsets dma_v_offsets(int wave, int lane) {
     return o;
 }
 
-template <int HD>
-__global__ __launch_bounds__(kPfThreads, 1) void k_prefill_dma(PrefillArgs a) {
-    constexpr int D = kPfDist<HD>, NK = kPfKStages<HD>, NV = kPfVStages<HD>;
-    constexpr int NQ = HD / 16, PER = HD / 64 + 4;  // score steps, DMAs per tile
-    __shared__ PrefillDmaSmem<HD> sm;
-    const unsigned dh = wg_z();  // output half of the head dimension (head_dim 512)
-    const PrefillWorkDev wk = a.work[wg_x()];
-    const PrefillEntryDev& ent = a.table[wk.entry];
-    const unsigned kvh = wg_y();
-    const unsigned G = a.group, NQH = a.num_q_heads, NKH = a.num_kv_heads;
-    const int lane = tid_x() & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid_x() >> 6);
-    const int half = lane >> 5;
-    const int col = lane & 31;
-
-    const unsigned rho = (unsigned)wk.tile * kPfRows + (unsigned)wave * 32u + (unsigned)col;
-    const unsigned tok = rho / G, head = rho % G;
-    const bool row_live = tok < ent.n_tokens;
-    const unsigned tok_c = row_live ? tok : ent.n_tokens - 1;
-    const unsigned pos = ent.start + tok_c;
-    const unsigned lo = (ent.window != 0 && pos + 1 > ent.window) ? pos + 1 - ent.window : 0u;
-    const unsigned hi = row_live ? pos : 0u;
-    const bool dead = !row_live;
-
-    const uint32_t row_bytes = NKH * HD * 2u;
-    const char* Kb = reinterpret_cast<const char*>(ent.k + (uint64_t)kvh * HD);
-    const char* VTb = reinterpret_cast<const char*>(ent.vt + (uint64_t)kvh * ent.vt_blocks * (HD * 32)) +
-                      (uint64_t)dh * kPfVtTileBytes;
-    const unsigned kb = wk.key_begin, ke = wk.key_end, last = ke - 1;  // kb is 32-aligned
-    const int n_tiles = (int)((ke - kb + kPfKeys - 1) / kPfKeys);
-    const float qs = ent.qscale;
-
-    const DmaVOffsets dof = dma_v_offsets(wave, lane);
-    // DMA instruction k (0 .. PER - 1: the K rows, then the V^T rows) of tile t, into K stage
-    // t % NK and V^T stage t % NV. A tile past the range reloads the range's last tile into those
-    // stages, which nobody reads, so that every iteration issues the same count (uniform waits).
-    // dma_tile gives the tile's wave-uniform operands, dma_part issues one instruction.
-    struct DmaTile {
-        const char* k;     // the tile's first K row
-        const char* v;     // its V^T block (this output half)
-        uint32_t kclamp;   // byte offset of the range's last row from the tile's first
-        uint32_t lds_k, lds_v;  // this wave's first destination in the stages
-    };
-    uint32_t krow_off[HD / 64], kchunk_off[HD / 64];
-#pragma unroll
-    for (int k = 0; k < HD / 64; k++) {
-        unsigned r, c;
-        dma_k_lane<HD>(wave, lane, k, &r, &c);
-        krow_off[k] = r * row_bytes;
-        kchunk_off[k] = c * 16u;
-    }
-    auto dma_tile = [&](int t) __attribute__((always_inline)) {
-        t = __builtin_amdgcn_readfirstlane(t);
-        const int tc = min(t, n_tiles - 1);
-        const unsigned t0 = kb + (unsigned)tc * kPfKeys;
-        DmaTile d;
-        d.k = uniform_ptr(Kb + (uint64_t)t0 * row_bytes);
-        d.v = uniform_ptr(VTb + (uint64_t)(t0 >> 5) * kPfKTileBytes<HD>);
-        d.kclamp = __builtin_amdgcn_readfirstlane((last - t0) * row_bytes);
-        d.lds_k = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sm.k[t % NK][(HD / 64u) * wave * 1024u]);
-        d.lds_v = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&sm.vt[t % NV][4u * wave * 1024u]);
-        return d;
-    };
-    auto dma_part = [&](int k, const DmaTile& d) __attribute__((always_inline)) {
-        if (k < HD / 64)
-            lds_dma16_s(min(krow_off[k], d.kclamp) + kchunk_off[k], d.k, d.lds_k + 1024u * k);
-        else
-            lds_dma16_s(dof.v[k - HD / 64], d.v, d.lds_v + 1024u * (k - HD / 64));
-    };
-    auto issue = [&](int t) __attribute__((always_inline)) {
-        const DmaTile d = dma_tile(t);
-#pragma unroll
-        for (int k = 0; k < PER; k++) dma_part(k, d);
-    };
-#pragma unroll
-    for (int p = 0; p <= D; p++) issue(p);
-
-    // q after the first tiles' DMAs, so that the two latencies overlap (the wait for q, in issue
-    // order, also covers those tiles). q stays in AGPRs: the score MFMA reads its B operand from
-    // there, and the VGPRs hold the output accumulators (this file is compiled with MFMA
-    // accumulators in VGPRs, so that their rescale is plain VALU).
-    f16x8 qop[NQ];
-    {
-        const uint16_t* qr = ent.q + ((uint64_t)tok_c * NQH + kvh * G + head) * HD + 8 * half;
-#pragma unroll
-        for (int s = 0; s < NQ; s++) qop[s] = ldg<f16x8>(qr + 16 * s);
-#pragma unroll
-        for (int s = 0; s < NQ; s++) asm volatile("" : "+a"(qop[s]));
-    }
-
-    float m_run = -INFINITY, l_run = 0.0f;
-    f32x16 acc[8];
-#pragma unroll
-    for (int b = 0; b < 8; b++) acc[b] = f32x16{};
-    // LDS operand addresses inside a stage: K chunk c = 2s + half of row krow; V^T chunk 2s + half of row 32b + col.
-    const unsigned krow = key_of_row((unsigned)col);
-    const unsigned kx = swz_k(krow), vx = swz_v((unsigned)col);
-    unsigned koff[8];  // chunk 2s + half of the key row lies at koff[s % 8] + 256 (s / 8)
-#pragma unroll
-    for (int b = 0; b < 8; b++) koff[b] = krow * (2u * HD) + ((((unsigned)(2 * b + half)) ^ kx) << 4);
-    unsigned voff[2];
-#pragma unroll
-    for (int s = 0; s < 2; s++) voff[s] = (unsigned)col * 64u + ((((unsigned)(2 * s + half)) ^ vx) << 4);
-
-    // Software pipeline over tiles: the score MFMAs of tile it + 1 are issued in the same basic
-    // block as the softmax of tile it (independent work: the VALU runs while the matrix core
-    // works), then tile it's output MFMAs. Masking is branch-free for that reason: key in [lo, hi]
-    // is (key - lo) < span (unsigned), with span 0 for rows past the chunk.
-    const unsigned span = dead ? 0u : hi - lo + 1u;
-    auto scores = [&](int stage) __attribute__((always_inline)) {
-        const unsigned char* kbuf = sm.k[stage];
-        f32x16 sc = f32x16{};
-#pragma unroll
-        for (int s = 0; s < NQ; s++) {
-            const f16x8 k0 = *reinterpret_cast<const f16x8*>(kbuf + koff[s & 7] + 256u * (s >> 3));
-            sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(k0, qop[s], sc, 0, 0, 0);
-        }
-        return sc;
-    };
-    // Probabilities of one tile's raw scores (register r: key kt0 + 16 (r / 8) + 8 half + r % 8),
-    // with the lazy update of the row's reference max; returns whether any row moved it.
-    auto softmax = [&](f32x16 sc, unsigned kt0, f16x8 (&pop)[2], float& alpha) __attribute__((always_inline)) {
-        const unsigned rel = kt0 + 8u * (unsigned)half - lo;
-#pragma unroll
-        for (int r = 0; r < 16; r++)
-            sc[r] = rel + (unsigned)(16 * (r >> 3) + (r & 7)) < span ? sc[r] : -INFINITY;
-        float smax = sc[0];
-#pragma unroll
-        for (int r = 1; r < 16; r++) smax = fmaxf(smax, sc[r]);
-        float tmax = smax * qs;  // the scale is positive
-        {
-            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(tmax), __float_as_uint(tmax), false, false);
-            tmax = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));  // max over both halves of the row
-        }
-        const bool move = tmax > m_run + kPfLazy;
-        const float m_new = move ? tmax : m_run;
-        alpha = move ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;  // 0 from -inf (acc, l are 0)
-        l_run *= alpha;
-        m_run = m_new;
-        const float nmu = m_run == -INFINITY ? 0.0f : -m_run;
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], qs, nmu));
-            l_run += p;
-            pop[r >> 3][r & 7] = (f16)p;
-        }
-        return __any(move);
-    };
-    auto output = [&](int stage, const f16x8 (&pop)[2]) __attribute__((always_inline)) {
-        const unsigned char* vbuf = sm.vt[stage];
-#pragma unroll
-        for (int b = 0; b < 8; b++) {
-#pragma unroll
-            for (int s = 0; s < 2; s++) {
-                const f16x8 vop = *reinterpret_cast<const f16x8*>(vbuf + voff[s] + 2048u * b);
-                acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vop, pop[s], acc[b], 0, 0, 0);
-            }
-        }
-    };
-
-    // One steady iteration in issue order: NQ steps, each one score MFMA of the next tile and, every
-    // NQ/16 steps, one output MFMA of the previous tile; the LDS operand reads R steps ahead, one DMA
-    // instruction of tile it + 1 + D every two steps, and after every MFMA one slot of this tile's
-    // softmax (slots 0-7: masking and running max of two scores; 8-9: the row's reference max and
-    // alpha; 10-25: one exponential each, every second one packing the f16 pair and adding it to
-    // the row sum with a dot product). A wave issues in order and an MFMA waits for the previous
-    // one, so VALU work placed after each MFMA runs in that MFMA's shadow; sched_barrier(0) keeps
-    // the order. `mask` is false for tiles whose keys lie inside the window of every row of the
-    // wave. The row sum adds the f16-rounded probabilities the output MFMAs use.
-    auto steady = [&](bool mask, int ks, int vs, const DmaTile& tdma, unsigned kt0, f32x16& sc, const f16x8 (&pin)[2],
-                      f16x8 (&pout)[2], f32x16& nxt, float& alpha) __attribute__((always_inline)) {
-        constexpr int R = 3, OSTEP = NQ / 16;
-        const unsigned char* kbuf = sm.k[ks];
-        const unsigned char* vbuf = sm.vt[vs];
-        f16x8 kr[NQ], vr[16];
-        auto kread = [&](int s) __attribute__((always_inline)) {
-            kr[s] = *reinterpret_cast<const f16x8*>(kbuf + koff[s & 7] + 256u * (s >> 3));
-        };
-        auto vread = [&](int o) __attribute__((always_inline)) {
-            vr[o] = *reinterpret_cast<const f16x8*>(vbuf + voff[o & 1] + 2048u * (o >> 1));
-        };
-#pragma unroll
-        for (int i = 0; i < R; i++) {
-            vread(i);
-            kread(i);
-        }
-        const unsigned rel = kt0 + 8u * (unsigned)half - lo;
-        float mx = -INFINITY, tmax = 0.0f, nmu = 0.0f;
-        float p[16];
-        bool moved = false;
-        auto slot = [&](int q) __attribute__((always_inline)) {
-            if (q < 8) {
-                const int r = 2 * q;
-                if (mask) {
-                    sc[r] = rel + (unsigned)(16 * (r >> 3) + (r & 7)) < span ? sc[r] : -INFINITY;
-                    sc[r + 1] = rel + (unsigned)(16 * ((r + 1) >> 3) + ((r + 1) & 7)) < span ? sc[r + 1] : -INFINITY;
-                }
-                mx = fmaxf(mx, fmaxf(sc[r], sc[r + 1]));
-            } else if (q == 8) {
-                tmax = mx * qs;  // the scale is positive
-                const auto sw =
-                    __builtin_amdgcn_permlane32_swap(__float_as_uint(tmax), __float_as_uint(tmax), false, false);
-                tmax = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));  // max over both halves of the row
-            } else if (q == 9) {
-                const bool move = tmax > m_run + kPfLazy;
-                const float m_new = move ? tmax : m_run;
-                alpha = move ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;  // 0 from -inf (acc, l are 0)
-                l_run *= alpha;
-                m_run = m_new;
-                nmu = m_run == -INFINITY ? 0.0f : -m_run;
-                moved = __any(move);
-            } else if (q < 26) {
-                const int r = q - 10;
-                p[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], qs, nmu));
-                if (r & 1) {
-                    const f16x2 h = f16x2{(f16)p[r - 1], (f16)p[r]};
-                    pout[r >> 3][(r - 1) & 7] = h[0];
-                    pout[r >> 3][r & 7] = h[1];
-                    l_run = __builtin_amdgcn_fdot2(h, f16x2{(f16)1.0f, (f16)1.0f}, l_run, false);
-                }
-            }
-        };
-        nxt = f32x16{};
-        int q = 0;  // MFMAs issued so far
-#pragma unroll
-        for (int j = 0; j < NQ; j++) {
-            if (j % OSTEP == 0) {
-                const int o = j / OSTEP;
-                acc[o >> 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vr[o], pin[o & 1], acc[o >> 1], 0, 0, 0);
-                if (o + R < 16) vread(o + R);
-                slot(q++);
-                __builtin_amdgcn_sched_barrier(0);
-            }
-            nxt = __builtin_amdgcn_mfma_f32_32x32x16_f16(kr[j], qop[j], nxt, 0, 0, 0);
-            if (j + R < NQ) kread(j + R);
-            if (j % 2 == 0 && j / 2 < PER) dma_part(j / 2, tdma);  // one instruction per two steps
-            slot(q++);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        asm volatile("" : "+v"(pout[0]), "+v"(pout[1]), "+v"(l_run));  // formed before the rescale branch
-        return moved;
-    };
-
-    // Iteration it issues tile it + 1 + D, computes the scores of tile it + 1, the output of
-    // tile it - 1 and the probabilities of tile it: one basic block of independent MFMA and VALU
-    // work, then the rare rescale of the accumulators (after tile it - 1's output).
-    auto rescale = [&](float alpha) __attribute__((always_inline)) {
-#pragma unroll
-        for (int b = 0; b < 8; b++) acc[b] *= alpha;
-    };
-    // Tiles [t_in0, t_in1) of the range lie inside every row's window of this wave (no masking).
-    int t_in0, t_in1;
-    {
-        int a0 = dead ? 0x7fffffff : (lo > kb ? (int)((lo - kb + kPfKeys - 1) / kPfKeys) : 0);
-        int a1 = dead || hi + 1 < kb ? 0 : (int)((hi + 1 - kb) / kPfKeys);
-#pragma unroll
-        for (int m = 32; m >= 1; m >>= 1) {
-            a0 = max(a0, __shfl_xor(a0, m));
-            a1 = min(a1, __shfl_xor(a1, m));
-        }
-        t_in0 = __builtin_amdgcn_readfirstlane(a0);
-        t_in1 = __builtin_amdgcn_readfirstlane(a1);
-    }
-    auto step = [&](bool mask, int it, f32x16& sc, const f16x8 (&pin)[2], f16x8 (&pout)[2], f32x16& nxt) __attribute__((always_inline)) {
-        it = __builtin_amdgcn_readfirstlane(it);  // tile and stage arithmetic on the scalar unit
-        dma_wait_barrier<PER>(D - 1);  // tile it + 1 is in LDS; tile it + 1 + D goes to the stages of K(it), V^T(it - 2)
-        float alpha;
-        const DmaTile d = dma_tile(it + 1 + D);
-        if (steady(mask, (it + 1) % NK, (it - 1) % NV, d, kb + (unsigned)it * kPfKeys, sc, pin, pout, nxt, alpha))
-            rescale(alpha);
-    };
-    f16x8 pa[2], pb[2];
-    f32x16 sa, sb;
-    // Steady iteration it with masking, tile it's scores in sb and tile it - 1's probabilities in pa
-    // before and after.
-    auto step_masked = [&](int it) __attribute__((always_inline)) {
-        step(true, it, sb, pa, pb, sa);
-        sb = sa;
-        pa[0] = pb[0];
-        pa[1] = pb[1];
-    };
-    float alpha;
-    dma_wait_barrier<PER>(D);  // tile 0 is in LDS
-    sa = scores(0);
-    if (n_tiles == 1) {
-        softmax(sa, kb, pa, alpha);  // the accumulators are still zero: no rescale
-        output(0, pa);
-    } else {
-        dma_wait_barrier<PER>(D - 1);  // tile 1 is in LDS; every wave is past scores(0)
-        issue(D + 1);
-        sb = scores(1 % NK);
-        softmax(sa, kb, pa, alpha);
-        // Masked iterations before the tiles that lie inside every row's window, those tiles
-        // unmasked, two per pass (the score and probability registers alternate in place), then the
-        // masked rest (head_dim 512: every iteration masked, one form for the register budget).
-        int it = 1;
-        if constexpr (HD == 256) {
-            for (; it + 1 < n_tiles && it < t_in0; it++) step_masked(it);
-            for (; it + 2 < n_tiles && it + 1 < t_in1; it += 2) {
-                step(false, it, sb, pa, pb, sa);      // scores of tile it + 1 into sa, probabilities of tile it into pb
-                step(false, it + 1, sa, pb, pa, sb);  // scores of tile it + 2 into sb, probabilities of tile it + 1 into pa
-            }
-        }
-        for (; it + 1 < n_tiles; it++) step_masked(it);
-        output((it - 1) % NV, pa);
-        if (softmax(sb, kb + (unsigned)it * kPfKeys, pb, alpha)) rescale(alpha);
-        output(it % NV, pb);
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no LDS write of this workgroup outlives it
-
-    const float L = l_run + __shfl_xor(l_run, 32);
-    if (dead) return;
-    const uint64_t qrow = (uint64_t)tok * NQH + kvh * G + head;
-    if (wk.n_parts == 1) {
-        float* dst = ent.out + qrow * HD + 256u * dh + 4 * half;
-        const float inv = 1.0f / L;
-#pragma unroll
-        for (int b = 0; b < 8; b++)
-#pragma unroll
-            for (int g = 0; g < 4; g++)
-                stg<f32x4>(dst + 32 * b + 8 * g, f32x4{acc[b][4 * g] * inv, acc[b][4 * g + 1] * inv,
-                                                      acc[b][4 * g + 2] * inv, acc[b][4 * g + 3] * inv});
-        return;
-    }
-    const unsigned tile_tok0 = (unsigned)wk.tile * kPfRows / G;
-    const uint64_t slot = (uint64_t)wk.split_base + (uint64_t)(tok - tile_tok0) * wk.n_parts + wk.part;
-    const uint64_t rec = (slot * NKH + kvh) * G + head;
-    float* po = a.part_o + rec * HD + 256u * dh + 4 * half;
-#pragma unroll
-    for (int b = 0; b < 8; b++)
-#pragma unroll
-        for (int g = 0; g < 4; g++)
-            stg<f32x4>(po + 32 * b + 8 * g, f32x4{acc[b][4 * g], acc[b][4 * g + 1], acc[b][4 * g + 2], acc[b][4 * g + 3]});
-    if (half == 0 && dh == 0) stg<f32x2>(a.part_ml + rec * 2, f32x2{m_run, L});  // both halves hold the same
-}
-
 // ---- two waves per SIMD: score waves and output waves (head_dim 256) -------
 //
-// The same tiles, rings, DMA schedule and per-tile arithmetic as k_prefill_dma,
-// with the work of one 32-row wave split over two waves that share a SIMD:
+// Each group of 32 q-rows is served by two waves that share a SIMD:
 // waves 0..3 ("score waves") compute the scores and the online softmax of
 // their 32 q-rows, waves 4..7 ("output waves") accumulate O^T of the same rows
 // over the full head dimension and issue the tile DMAs. Wave w and w + 4 are
@@ -1513,11 +939,6 @@ constexpr uint32_t kPrefillMagic = 0x67345046u;
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-int pf_env(const char* name, int dflt) {
-    const char* s = getenv(name);
-    return s && *s ? atoi(s) : dflt;
-}
-
 struct PrefillPlanRep {
     char* ws;
     uint32_t n_entries;
@@ -1527,10 +948,10 @@ struct PrefillPlanRep {
     uint16_t num_q_heads;
     uint16_t num_kv_heads;
     uint16_t head_dim;     // 256 or 512
-    uint16_t dma;          // 1: the pipelined forms (V read as V^T blocks); 0: the register-staged form
+    uint16_t pad;
     uint32_t magic;
     uint32_t off_work, off_merge, off_ml, off_o;  // workspace byte offsets (workspaces stay under 4 GiB)
-    uint32_t off_vtc;      // V^T cache table (pipelined form)
+    uint32_t off_vtc;      // V^T cache table
     uint32_t n_vtc;        // caches to transpose (none when every entry brings its V^T cache)
     uint32_t vt_blocks;    // their 32-key blocks, in total
 };
@@ -1560,25 +981,13 @@ struct VtPlan {
     uint32_t total_blocks = 0;
 };
 
-bool prefill_dma_enabled() {
-    static const int env = pf_env("G4_PREFILL_DMA", 1);
-    return env != 0;
-}
-
-// The pipelined form's kernels: score and output waves sharing the scores (k_prefill_pp at head_dim
-// 256, k_prefill_pp512 at 512), or with G4_PREFILL_PP=0 one wave per SIMD (k_prefill_dma).
-bool prefill_pp_enabled() {
-    static const int env = pf_env("G4_PREFILL_PP", 1);
-    return env != 0;
-}
-
 // Work list, merge list and workspace layout for a set of entries.
-int build(const g4_prefill_entry* ents, uint32_t n, uint32_t nqh, uint32_t nkh, uint32_t hd, uint32_t part_keys, bool dma,
+int build(const g4_prefill_entry* ents, uint32_t n, uint32_t nqh, uint32_t nkh, uint32_t hd,
           std::vector<PrefillEntryDev>* tab, std::vector<PrefillWorkDev>* work, std::vector<DecodeEntryDev>* merge,
           uint32_t* max_parts, Layout* L, VtPlan* vp) {
     const uint32_t G = nqh / nkh;
     *vp = VtPlan{};
-    if (dma) {
+    {
         vp->of.assign(n, ~0u);
         for (uint32_t i = 0; i < n; i++) {
             const g4_prefill_entry& e = ents[i];
@@ -1612,7 +1021,8 @@ int build(const g4_prefill_entry* ents, uint32_t n, uint32_t nqh, uint32_t nkh, 
         uint32_t keys;
     };
     std::vector<Item> items;
-    if (part_keys == 0) {
+    uint32_t part_keys = 0;
+    {
         // Parts about 1.15x the keys per CU of the whole call (one workgroup per CU): long query
         // tiles split so that the longest item stays near a CU's share, short ones stay whole
         // (every extra part costs a record write and its merge). prefill4k: 3008 keys; measured
@@ -1624,7 +1034,7 @@ int build(const g4_prefill_entry* ents, uint32_t n, uint32_t nqh, uint32_t nkh, 
             for (uint32_t t = 0; t < tiles; t++) {
                 uint32_t kb, ke;
                 tile_keys(e, G, t, &kb, &ke);
-                w += ke - (dma ? kb & ~(uint32_t)(kPfKeys - 1) : kb);
+                w += ke - (kb & ~(uint32_t)(kPfKeys - 1));
             }
         }
         const uint64_t share = w * nkh * (hd / 256) * 115 / (100 * (uint64_t)device_cus());  // head_dim 512: two halves
@@ -1633,14 +1043,14 @@ int build(const g4_prefill_entry* ents, uint32_t n, uint32_t nqh, uint32_t nkh, 
     }
     for (uint32_t i = 0; i < n; i++) {
         const g4_prefill_entry& e = ents[i];
-        const uint32_t vt_blocks = !dma ? 0u : e.vt_cache ? (e.vt_rows + kPfKeys - 1) / kPfKeys : vp->blocks[vp->of[i]];
-        (*tab)[i] = PrefillEntryDev{e.q, e.k_cache, e.v_cache, e.out, e.n_tokens, e.start, e.sliding_window,
-                                    e.scale * kLog2e, dma ? e.vt_cache : nullptr, vt_blocks, 0u};
+        const uint32_t vt_blocks = e.vt_cache ? (e.vt_rows + kPfKeys - 1) / kPfKeys : vp->blocks[vp->of[i]];
+        (*tab)[i] = PrefillEntryDev{e.q, e.k_cache, e.out, e.n_tokens, e.start, e.sliding_window,
+                                    e.scale * kLog2e, e.vt_cache, vt_blocks, 0u};
         const uint32_t tiles = (uint32_t)(((uint64_t)e.n_tokens * G + kPfRows - 1) / kPfRows);
         for (uint32_t t = 0; t < tiles; t++) {
             uint32_t kb, ke;
             tile_keys(e, G, t, &kb, &ke);
-            if (dma) kb &= ~(uint32_t)(kPfKeys - 1);  // the pipelined form reads 32-aligned tiles
+            kb &= ~(uint32_t)(kPfKeys - 1);  // tiles are 32-aligned
             const uint32_t nk = ke - kb;
             const uint32_t parts = (nk + part_keys - 1) / part_keys;
             const uint32_t tok0 = t * (uint32_t)kPfRows / G;
@@ -1686,8 +1096,7 @@ int build(const g4_prefill_entry* ents, uint32_t n, uint32_t nqh, uint32_t nkh, 
 
 int check(const g4_prefill_entry* ents, uint32_t n, uint32_t nqh, uint32_t nkh, uint32_t hd) {
     if (!ents || n == 0) return fail(G4_EINVAL, "attnPrefill: no entries");
-    if (hd != 256 && !(hd == 512 && prefill_dma_enabled()))
-        return fail(G4_EINVAL, "attnPrefill: head_dim %u unsupported (256, or 512 in the pipelined form)", hd);
+    if (hd != 256 && hd != 512) return fail(G4_EINVAL, "attnPrefill: head_dim %u unsupported (256 or 512)", hd);
     if (nkh == 0 || nqh % nkh || nqh / nkh > (uint32_t)kMaxGroup || 32 % (nqh / nkh))
         return fail(G4_EINVAL, "attnPrefill: %u query heads over %u kv heads unsupported", nqh, nkh);
     for (uint32_t i = 0; i < n; i++) {
@@ -1700,16 +1109,8 @@ int check(const g4_prefill_entry* ents, uint32_t n, uint32_t nqh, uint32_t nkh, 
         if (e.vt_cache && (uint64_t)e.start + e.n_tokens > e.vt_rows)
             return fail(G4_EINVAL, "attnPrefill: entry %u attends rows up to %u past its V^T cache's %u rows", i,
                         e.start + e.n_tokens - 1, e.vt_rows);
-        if (e.vt_cache && !prefill_dma_enabled())
-            return fail(G4_EINVAL, "attnPrefill: entry %u: a V^T cache needs the pipelined form", i);
     }
     return G4_OK;
-}
-
-// Keys per part: G4_PREFILL_PART_KEYS, or 0 for the per-call share computed in build().
-uint32_t part_keys_default() {
-    static const int env = pf_env("G4_PREFILL_PART_KEYS", 0);
-    return env > 0 ? (uint32_t)((env + kPfKeys - 1) / kPfKeys * kPfKeys) : 0u;
 }
 
 }  // namespace
@@ -1727,9 +1128,7 @@ int g4_attn_prefill_workspace_size(const g4_prefill_entry* entries, uint32_t n_e
     uint32_t mp;
     Layout L;
     VtPlan vp;
-    rc = build(entries, n_entries, num_q_heads, num_kv_heads, head_dim, part_keys_default(), prefill_dma_enabled(), &tab,
-               &work,
-               &merge, &mp, &L, &vp);
+    rc = build(entries, n_entries, num_q_heads, num_kv_heads, head_dim, &tab, &work, &merge, &mp, &L, &vp);
     if (rc) return rc;
     *bytes = L.total;
     return G4_OK;
@@ -1747,9 +1146,7 @@ int g4_attn_prefill_prepare(const g4_prefill_entry* entries, uint32_t n_entries,
     uint32_t max_parts;
     Layout L;
     VtPlan vp;
-    const bool dma = prefill_dma_enabled();
-    rc = build(entries, n_entries, num_q_heads, num_kv_heads, head_dim, part_keys_default(), dma, &tab, &work, &merge,
-               &max_parts, &L, &vp);
+    rc = build(entries, n_entries, num_q_heads, num_kv_heads, head_dim, &tab, &work, &merge, &max_parts, &L, &vp);
     if (rc) return rc;
     if (max_parts > 8192) return fail(G4_EINVAL, "attnPrefill: %u key parts per tile (max 8192)", max_parts);
     if (!workspace || workspace_bytes < L.total)
@@ -1761,9 +1158,8 @@ int g4_attn_prefill_prepare(const g4_prefill_entry* entries, uint32_t n_entries,
     for (size_t c = 0; c < vp.v.size(); c++)
         vtc[c] = VtCacheDev{vp.v[c], reinterpret_cast<uint16_t*>(ws + L.vt + vp.off[c]), vp.rows[c], vp.blocks[c],
                             vp.block0[c], 0u};
-    if (dma)
-        for (uint32_t i = 0; i < n_entries; i++)
-            if (!entries[i].vt_cache) tab[i].vt = vtc[vp.of[i]].vt;
+    for (uint32_t i = 0; i < n_entries; i++)
+        if (!entries[i].vt_cache) tab[i].vt = vtc[vp.of[i]].vt;
     std::vector<char> blob(L.vtc - L.table + vtc.size() * sizeof(VtCacheDev));
     memcpy(blob.data(), tab.data(), tab.size() * sizeof(PrefillEntryDev));
     memcpy(blob.data() + (L.work - L.table), work.data(), work.size() * sizeof(PrefillWorkDev));
@@ -1786,9 +1182,8 @@ int g4_attn_prefill_prepare(const g4_prefill_entry* entries, uint32_t n_entries,
     r.off_ml = (uint32_t)L.ml;
     r.off_o = (uint32_t)L.o;
     r.off_vtc = (uint32_t)L.vtc;
-    r.n_vtc = dma ? (uint32_t)vp.v.size() : 0u;
+    r.n_vtc = (uint32_t)vp.v.size();
     r.vt_blocks = vp.total_blocks;
-    r.dma = dma ? 1u : 0u;
     memset(plan, 0, sizeof *plan);
     memcpy(plan, &r, sizeof r);
     return G4_OK;
@@ -1809,7 +1204,7 @@ static int prefill_run(const g4_decode_plan* plan, void* stream, hipEvent_t star
     a.part_o = reinterpret_cast<float*>(r.ws + r.off_o);
     hipStream_t st = as_stream(stream);
     const bool hd512 = r.head_dim == 512;
-    if (r.n_vtc) {  // V^T blocks for the pipelined form
+    if (r.n_vtc) {  // V^T blocks of the caches without their own
         const VtCacheDev* vtc = reinterpret_cast<const VtCacheDev*>(r.ws + r.off_vtc);
         const dim3 vgrid(r.vt_blocks, r.num_kv_heads);
         if (hd512)
@@ -1819,31 +1214,15 @@ static int prefill_run(const g4_decode_plan* plan, void* stream, hipEvent_t star
         G4_CHECK_LAUNCH("attnPrefill (V^T blocks)");
     }
     const dim3 grid(r.n_work, r.num_kv_heads, r.head_dim / 256);
-    if (r.dma) {
-        if (hd512 && prefill_pp_enabled()) {  // grid z: the row half of each work item's query tile
-            if (start_ev || stop_ev)
-                hipExtLaunchKernelGGL(k_prefill_pp512, grid, dim3(6 * 64), 0, st, start_ev, stop_ev, 0, a);
-            else
-                G4_LAUNCH(k_prefill_pp512, grid, dim3(6 * 64), 0, st, a);
-        } else if (hd512) {  // grid z: the output half of the head dimension
-            if (start_ev || stop_ev)
-                hipExtLaunchKernelGGL(k_prefill_dma<512>, grid, dim3(kPfThreads), 0, st, start_ev, stop_ev, 0, a);
-            else
-                G4_LAUNCH(k_prefill_dma<512>, grid, dim3(kPfThreads), 0, st, a);
-        } else if (prefill_pp_enabled()) {
-            if (start_ev || stop_ev)
-                hipExtLaunchKernelGGL(k_prefill_pp, grid, dim3(2 * kPfThreads), 0, st, start_ev, stop_ev, 0, a);
-            else
-                G4_LAUNCH(k_prefill_pp, grid, dim3(2 * kPfThreads), 0, st, a);
-        } else if (start_ev || stop_ev) {
-            hipExtLaunchKernelGGL(k_prefill_dma<256>, grid, dim3(kPfThreads), 0, st, start_ev, stop_ev, 0, a);
-        } else {
-            G4_LAUNCH(k_prefill_dma<256>, grid, dim3(kPfThreads), 0, st, a);
-        }
+    if (hd512) {  // grid z: the row half of each work item's query tile
+        if (start_ev || stop_ev)
+            hipExtLaunchKernelGGL(k_prefill_pp512, grid, dim3(6 * 64), 0, st, start_ev, stop_ev, 0, a);
+        else
+            G4_LAUNCH(k_prefill_pp512, grid, dim3(6 * 64), 0, st, a);
     } else if (start_ev || stop_ev) {
-        hipExtLaunchKernelGGL(k_prefill, grid, dim3(kPfThreads), 0, st, start_ev, stop_ev, 0, a);
+        hipExtLaunchKernelGGL(k_prefill_pp, grid, dim3(2 * kPfThreads), 0, st, start_ev, stop_ev, 0, a);
     } else {
-        G4_LAUNCH(k_prefill, grid, dim3(kPfThreads), 0, st, a);
+        G4_LAUNCH(k_prefill_pp, grid, dim3(2 * kPfThreads), 0, st, a);
     }
     G4_CHECK_LAUNCH("attnPrefill");
     if (!r.n_merge) return G4_OK;

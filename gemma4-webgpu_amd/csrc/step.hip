@@ -295,11 +295,6 @@ namespace {
 
 constexpr uint32_t kStepMagic = 0x67345354u;
 
-int step_env(const char* name, int dflt) {
-    const char* s = getenv(name);
-    return s && *s ? atoi(s) : dflt;
-}
-
 struct StepPlanRep {
     char* tables;   // the plan's tables region (work items | merge table | entry table | RoPE factors)
     char* part_ml;  // its partial records: (m, l) pairs, then the o rows at step_part_o_offset()
@@ -343,18 +338,6 @@ int g4_attn_step_workspace_size(uint32_t n_entries, uint32_t num_q_heads, uint32
     return G4_OK;
 }
 
-// G4_STEP_WAVES (4 or 8), G4_STEP_WGS_PER_CU and G4_STEP_MAX_WGS override the grid choice.
-static const StepTuning& step_tuning() {
-    static const StepTuning tune = [] {
-        StepTuning t;
-        t.waves = step_env("G4_STEP_WAVES", 0);
-        t.wgs_per_cu = step_env("G4_STEP_WGS_PER_CU", 0);
-        t.max_wgs = step_env("G4_STEP_MAX_WGS", 0);
-        return t;
-    }();
-    return tune;
-}
-
 static void write_plan(g4_decode_plan* plan, char* tables, char* part_ml, const g4_step_entry* entries,
                        uint32_t n_entries, uint32_t num_kv_heads, uint32_t G, uint32_t head_dim,
                        const StepPlanHost& ph) {
@@ -395,7 +378,7 @@ int g4_attn_step_prepare(const g4_step_entry* entries, uint32_t n_entries, uint3
     char* ws = static_cast<char*>(workspace);
     static thread_local StepPlanHost ph;  // the planner's storage, kept between the thread's prepares
     char err[256];
-    rc = plan_step(entries, n_entries, num_q_heads, num_kv_heads, head_dim, device_cus(), step_tuning(),
+    rc = plan_step(entries, n_entries, num_q_heads, num_kv_heads, head_dim, device_cus(), StepTuning{},
                    ws + L.tables, &ph, err, sizeof err);
     if (rc) return fail(rc, "%s", err);
     rc = stage_upload(ws + L.tables, ph.blob.data(), ph.blob.size(), as_stream(stream));  // the tables in one copy
@@ -442,7 +425,7 @@ int g4_attn_step_prepare_layers(const g4_step_entry* entries, uint32_t n_layers,
     char err[256];
     for (uint32_t i = 0; i < n_layers; i++) {
         char* const tables = ws + blob.size();
-        rc = plan_step(entries + (size_t)i * E, E, num_q_heads, num_kv_heads, head_dim, device_cus(), step_tuning(),
+        rc = plan_step(entries + (size_t)i * E, E, num_q_heads, num_kv_heads, head_dim, device_cus(), StepTuning{},
                        tables, &ph, err, sizeof err, &share);
         if (rc) {  // no plan of this call is usable: their tables were never uploaded
             for (uint32_t j = 0; j < i; j++) memset(&plans[j], 0, sizeof plans[j]);

@@ -87,7 +87,8 @@ inline uint64_t pick_tiles_per_wg(const std::vector<uint32_t>& tiles, uint64_t t
     return lo;
 }
 
-// Overrides of the grid choice (0 = the default rule).
+// Overrides of the grid choice (0 = the default rule; the library passes the
+// defaults, the planner's checks and experiments others).
 struct StepTuning {
     int waves = 0;       // 4 or 8 waves per workgroup (head_dim 256)
     int wgs_per_cu = 0;  // workgroups per CU
