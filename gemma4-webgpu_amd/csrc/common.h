@@ -55,8 +55,10 @@ bool pass_events(hipEvent_t* start, hipEvent_t* stop);
 // staging memory from a per-thread ring of slots, copied by a kernel on `st`
 // (16-byte aligned dst; otherwise by the copy engine). A slot is reused only once
 // the copy that last read it has completed; when every slot is still in flight
-// the ring grows (up to kStageMaxSlots slots, past which the oldest slot is
-// waited for), so enqueueing never waits on the GPU in practice.
+// the ring grows (up to kStageMaxSlots slots and 64 MiB of pinned memory, past
+// which the oldest slot is waited for), so enqueueing rarely waits on the GPU.
+// Buffers a slot outgrew, and the rings of threads that have ended, go to a
+// process-wide pool that every thread's ring takes from first.
 constexpr int kStageMaxSlots = 4096;
 int stage_upload(void* dst, const void* src, size_t bytes, hipStream_t st);
 // Slots currently held by the calling thread's ring (for tests).

@@ -33,23 +33,107 @@ namespace {
 struct StageSlot {
     void* buf = nullptr;
     size_t cap = 0;
-    hipEvent_t done = nullptr;  // recorded after the copy that last read buf
+    hipEvent_t done = nullptr;  // recorded after the copy that last read buf (nullptr: no copy pending)
 };
 
-// The calling thread's ring. Slots and their pinned buffers live until the
-// thread ends (they are not returned to the runtime, which may already be torn
-// down when thread-local storage is destroyed at process exit). A slot that
-// outgrows its buffer takes a new one of at least twice the size; the old
-// buffer, which kernels have read, is kept rather than freed.
+// Whether a slot's last copy has completed (hipEventQuery does not wait).
+int slot_free(const StageSlot& s, bool* is_free) {
+    *is_free = true;
+    if (!s.done) return G4_OK;
+    const hipError_t q = hipEventQuery(s.done);
+    if (q == hipErrorNotReady) *is_free = false;
+    else if (q != hipSuccess) return hip_fail(q, "stage_upload: hipEventQuery");
+    return G4_OK;
+}
+
+// Process-wide spares: the buffers a slot outgrew (their copies had
+// completed) and the slots of rings whose thread has ended, for any thread's
+// ring to take. Past kStagePoolBytes the smallest free spares are returned to
+// the runtime. Never destroyed, so rings ending at process exit can still
+// hand their slots over (they make no HIP call then: the runtime may already
+// be torn down).
+constexpr size_t kStagePoolBytes = 64ull << 20;
+struct StagePool {
+    std::mutex mu;
+    std::vector<StageSlot> spare;
+    size_t bytes = 0;
+};
+
+StagePool& pool() {
+    static StagePool* p = new StagePool();
+    return *p;
+}
+
+// The calling thread's ring. A slot that outgrows its buffer takes a spare
+// or a new one of at least twice the size and gives the old one to the pool.
+// Past kStageRingBytes of pinned memory the ring stops growing and waits for
+// its oldest copy instead, so a thread that queues far ahead of the GPU holds
+// a bounded amount.
+constexpr size_t kStageRingBytes = 64ull << 20;
 struct StageRing {
     std::vector<StageSlot> slots;
-    std::vector<void*> retired;
     size_t next = 0;
+    size_t bytes = 0;  // pinned bytes held by the slots
+    ~StageRing() {
+        StagePool& p = pool();
+        std::lock_guard<std::mutex> lock(p.mu);
+        for (const StageSlot& s : slots) {
+            p.spare.push_back(s);
+            p.bytes += s.cap;
+        }
+    }
 };
 
 StageRing& ring() {
-    static thread_local StageRing* r = new StageRing();
-    return *r;
+    static thread_local StageRing r;
+    return r;
+}
+
+// A spare slot whose copy has completed and whose buffer holds `bytes` (any
+// size when bytes is 0), removed from the pool; false when there is none.
+int take_spare(size_t bytes, StageSlot* out, bool* found) {
+    *found = false;
+    StagePool& p = pool();
+    std::lock_guard<std::mutex> lock(p.mu);
+    size_t best = p.spare.size();
+    for (size_t i = 0; i < p.spare.size(); i++) {
+        const StageSlot& c = p.spare[i];
+        if (c.cap < bytes || (best < p.spare.size() && c.cap >= p.spare[best].cap)) continue;
+        bool fr = false;
+        if (int rc = slot_free(c, &fr)) return rc;
+        if (fr) best = i;
+    }
+    if (best == p.spare.size()) return G4_OK;
+    *out = p.spare[best];
+    p.spare.erase(p.spare.begin() + best);
+    p.bytes -= out->cap;
+    *found = true;
+    return G4_OK;
+}
+
+// A buffer whose copies have completed goes to the pool; the pool then
+// returns its smallest free buffers to the runtime while it holds more than
+// kStagePoolBytes.
+int give_spare(void* buf, size_t cap) {
+    StagePool& p = pool();
+    std::lock_guard<std::mutex> lock(p.mu);
+    p.spare.push_back(StageSlot{buf, cap, nullptr});
+    p.bytes += cap;
+    while (p.bytes > kStagePoolBytes) {
+        size_t pick = p.spare.size();
+        for (size_t i = 0; i < p.spare.size(); i++) {
+            bool fr = false;
+            if (int rc = slot_free(p.spare[i], &fr)) return rc;
+            if (fr && (pick == p.spare.size() || p.spare[i].cap < p.spare[pick].cap)) pick = i;
+        }
+        if (pick == p.spare.size()) break;  // every spare is still read by a queued copy
+        StageSlot v = p.spare[pick];
+        p.spare.erase(p.spare.begin() + pick);
+        p.bytes -= v.cap;
+        if (v.done) G4_CHECK_HIP(hipEventDestroy(v.done));
+        G4_CHECK_HIP(hipHostFree(v.buf));
+    }
+    return G4_OK;
 }
 
 // The upload itself: the GPU reads the pinned slot (mapped into its address
@@ -71,44 +155,59 @@ __global__ __launch_bounds__(256) void k_stage_copy(const u32x4* __restrict__ sr
 int stage_upload(void* dst, const void* src, size_t bytes, hipStream_t st) {
     if (bytes == 0) return G4_OK;
     StageRing& R = ring();
-    // A free slot: never used, or its last copy has completed (hipEventQuery
-    // does not wait). Slots are tried from the oldest use on.
+    // A free slot: its last copy has completed. Slots are tried from the oldest use on.
     StageSlot* s = nullptr;
     const size_t n = R.slots.size();
     for (size_t i = 0; i < n && !s; i++) {
         StageSlot& c = R.slots[(R.next + i) % n];
-        const hipError_t q = hipEventQuery(c.done);
-        if (q == hipSuccess) {
+        bool fr = false;
+        if (int rc = slot_free(c, &fr)) return rc;
+        if (fr) {
             s = &c;
             R.next = (R.next + i + 1) % n;
-        } else if (q != hipErrorNotReady) {
-            return hip_fail(q, "stage_upload: hipEventQuery");
         }
     }
-    if (!s && n < (size_t)kStageMaxSlots) {
+    if (!s && n < (size_t)kStageMaxSlots && R.bytes < kStageRingBytes) {
         StageSlot fresh;
-        // The host only learns from the event that the copy has read the slot: no timing, and no
-        // system-scope release (an L2 write-back) behind the copy.
-        G4_CHECK_HIP(hipEventCreateWithFlags(&fresh.done, hipEventDisableTiming | hipEventDisableSystemFence));
+        bool found = false;
+        if (int rc = take_spare(0, &fresh, &found)) return rc;
+        if (found) R.bytes += fresh.cap;
+        if (!fresh.done) {
+            // The host only learns from the event that the copy has read the slot: no timing, and no
+            // system-scope release (an L2 write-back) behind the copy.
+            G4_CHECK_HIP(hipEventCreateWithFlags(&fresh.done, hipEventDisableTiming | hipEventDisableSystemFence));
+        }
         R.slots.insert(R.slots.begin() + R.next, fresh);  // the newest use sits just before `next`
         s = &R.slots[R.next];
         R.next = (R.next + 1) % R.slots.size();
     }
-    if (!s) {  // kStageMaxSlots copies in flight: wait for the oldest
+    if (!s) {  // every slot in flight and the ring at its limit: wait for the oldest
         s = &R.slots[R.next];
         R.next = (R.next + 1) % n;
         G4_CHECK_HIP(hipEventSynchronize(s->done));
     }
     if (s->cap < bytes) {
-        // Coherent: the copy kernel's loads reach host memory, not lines the GPU cached from an
-        // earlier use of the slot.
-        size_t cap = bytes < 4096 ? 4096 : bytes;
-        if (cap < 2 * s->cap) cap = 2 * s->cap;
-        void* buf = nullptr;
-        G4_CHECK_HIP(hipHostMalloc(&buf, cap, hipHostMallocCoherent));
-        if (s->buf) R.retired.push_back(s->buf);
+        // A spare that holds the table, or a new buffer. Coherent: the copy kernel's loads reach
+        // host memory, not lines the GPU cached from an earlier use of the buffer.
+        StageSlot sp;
+        bool found = false;
+        if (int rc = take_spare(bytes, &sp, &found)) return rc;
+        void* buf = sp.buf;
+        size_t cap = sp.cap;
+        if (found) {
+            if (sp.done) G4_CHECK_HIP(hipEventDestroy(sp.done));  // completed: the slot's own event stays
+        } else {
+            cap = bytes < 4096 ? 4096 : bytes;
+            if (cap < 2 * s->cap) cap = 2 * s->cap;
+            G4_CHECK_HIP(hipHostMalloc(&buf, cap, hipHostMallocCoherent));
+        }
+        void* old = s->buf;
+        const size_t old_cap = s->cap;
         s->buf = buf;
         s->cap = cap;
+        R.bytes += cap - old_cap;
+        if (old)  // its last copy has completed (the slot was free)
+            if (int rc = give_spare(old, old_cap)) return rc;
     }
     memcpy(s->buf, src, bytes);
     if (reinterpret_cast<uintptr_t>(dst) & 15 || bytes / 16 > 0xffffffffull) {
@@ -276,9 +375,22 @@ int g4_readback_finish(g4_readback* handle, void* host_dst) {
 // kernels' own start and end, with nothing launched between them). Markers
 // release to agent scope only (no system-scope cache write-back: a timestamp
 // orders nothing for the host). The events live as long as the set.
+//
+// The set itself records its open pass (at most one, on the thread that
+// opened it) and the slot ranges being resolved, under its mutex, so that
+// calls from different threads see each other: a resolve refuses slots of
+// the open pass, and a pass or marker refuses slots being resolved.
 struct g4_query_set {
     std::vector<hipEvent_t> ev;
     std::vector<uint8_t> written;
+    std::mutex mu;
+    int64_t open_slot = -1;                                 // first slot of the open pass, or -1
+    std::vector<std::pair<uint32_t, uint32_t>> resolving;  // [first, end) ranges being resolved
+    bool busy(uint32_t b, uint32_t e) const {              // [b, e) meets a range being resolved
+        for (const auto& r : resolving)
+            if (b < r.second && r.first < e) return true;
+        return false;
+    }
 };
 
 namespace {
@@ -298,7 +410,10 @@ bool g4::pass_events(hipEvent_t* start, hipEvent_t* stop) {
     if (!p.set) return false;
     *start = p.started ? nullptr : p.set->ev[p.slot];
     *stop = p.set->ev[p.slot + 1];
-    p.set->written[p.slot] = p.set->written[p.slot + 1] = 1;
+    {
+        std::lock_guard<std::mutex> lock(p.set->mu);
+        p.set->written[p.slot] = p.set->written[p.slot + 1] = 1;
+    }
     p.started = true;
     return true;
 }
@@ -331,6 +446,8 @@ int g4_query_write(g4_query_set* set, uint32_t slot, void* stream) {
     if (!set) return fail(G4_EINVAL, "g4_query_write: set is NULL");
     if (slot >= set->ev.size())
         return fail(G4_EINVAL, "g4_query_write: slot %u outside a set of %zu", slot, set->ev.size());
+    std::lock_guard<std::mutex> lock(set->mu);
+    if (set->busy(slot, slot + 1)) return fail(G4_EINVAL, "g4_query_write: slot %u is being resolved", slot);
     G4_CHECK_HIP(hipEventRecord(set->ev[slot], as_stream(stream)));
     set->written[slot] = 1;
     return G4_OK;
@@ -342,6 +459,13 @@ int g4_query_begin_pass(g4_query_set* set, uint32_t slot) {
         return fail(G4_EINVAL, "g4_query_begin_pass: slots %u, %u outside a set of %zu", slot, slot + 1,
                     set->ev.size());
     if (t_pass.set) return fail(G4_EINVAL, "g4_query_begin_pass: a pass is already open on this thread");
+    {
+        std::lock_guard<std::mutex> lock(set->mu);
+        if (set->open_slot >= 0) return fail(G4_EINVAL, "g4_query_begin_pass: a pass of this set is open on another thread");
+        if (set->busy(slot, slot + 2))
+            return fail(G4_EINVAL, "g4_query_begin_pass: slots %u, %u are being resolved", slot, slot + 1);
+        set->open_slot = slot;
+    }
     t_pass.set = set;
     t_pass.slot = slot;
     t_pass.started = false;
@@ -350,6 +474,10 @@ int g4_query_begin_pass(g4_query_set* set, uint32_t slot) {
 
 int g4_query_end_pass(void) {
     if (!t_pass.set) return fail(G4_EINVAL, "g4_query_end_pass: no pass open on this thread");
+    {
+        std::lock_guard<std::mutex> lock(t_pass.set->mu);
+        t_pass.set->open_slot = -1;
+    }
     t_pass = OpenPass();
     return G4_OK;
 }
@@ -360,23 +488,49 @@ int g4_query_resolve(g4_query_set* set, uint32_t first, uint32_t n_pairs, double
     if ((uint64_t)first + 2ull * n_pairs > set->ev.size())
         return fail(G4_EINVAL, "g4_query_resolve: %u pairs from slot %u outside a set of %zu", n_pairs, first,
                     set->ev.size());
-    if (t_pass.set == set) return fail(G4_EINVAL, "g4_query_resolve: a pass of this set is still open");
-    for (uint32_t i = 0; i < n_pairs; ++i) {
-        const uint32_t b = first + 2 * i, e = b + 1;
+    const uint32_t end = first + 2 * n_pairs;
+    std::vector<uint8_t> w;
+    {
+        std::lock_guard<std::mutex> lock(set->mu);
+        if (set->open_slot >= 0 && (uint64_t)set->open_slot < end && first < (uint64_t)set->open_slot + 2)
+            return fail(G4_EINVAL, "g4_query_resolve: a pass of this set on slots %lld, %lld is still open",
+                        (long long)set->open_slot, (long long)set->open_slot + 1);
+        if (set->busy(first, end)) return fail(G4_EINVAL, "g4_query_resolve: slots already being resolved");
+        set->resolving.emplace_back(first, end);
+        w.assign(set->written.begin() + first, set->written.begin() + end);
+    }
+    hipError_t err = hipSuccess;
+    for (uint32_t i = 0; i < n_pairs; ++i) {  // outside the lock: passes on other slots go on meanwhile
+        const uint32_t b = 2 * i, e = b + 1;
         ns_out[i] = NAN;
-        if (!set->written[b] || !set->written[e]) continue;
-        G4_CHECK_HIP(hipEventSynchronize(set->ev[e]));
+        if (!w[b] || !w[e] || err != hipSuccess) continue;
         float ms = 0.f;
-        G4_CHECK_HIP(hipEventElapsedTime(&ms, set->ev[b], set->ev[e]));
+        if ((err = hipEventSynchronize(set->ev[first + e])) != hipSuccess ||
+            (err = hipEventElapsedTime(&ms, set->ev[first + b], set->ev[first + e])) != hipSuccess)
+            continue;
         ns_out[i] = (double)ms * 1e6;
     }
-    for (uint32_t i = 0; i < 2 * n_pairs; ++i) set->written[first + i] = 0;
+    {
+        std::lock_guard<std::mutex> lock(set->mu);
+        for (uint32_t i = first; i < end; ++i) set->written[i] = 0;
+        for (size_t r = 0; r < set->resolving.size(); ++r)
+            if (set->resolving[r].first == first && set->resolving[r].second == end) {
+                set->resolving.erase(set->resolving.begin() + r);
+                break;
+            }
+    }
+    if (err != hipSuccess) return hip_fail(err, "g4_query_resolve");
     return G4_OK;
 }
 
 int g4_query_set_destroy(g4_query_set* set) {
     if (!set) return fail(G4_EINVAL, "g4_query_set_destroy: set is NULL");
-    if (t_pass.set == set) t_pass = OpenPass();
+    if (t_pass.set == set) t_pass = OpenPass();  // this thread's own pass: closed with the set
+    else {
+        std::lock_guard<std::mutex> lock(set->mu);
+        if (set->open_slot >= 0) return fail(G4_EINVAL, "g4_query_set_destroy: a pass of this set is open on another thread");
+        if (!set->resolving.empty()) return fail(G4_EINVAL, "g4_query_set_destroy: slots of this set are being resolved");
+    }
     hipError_t first_err = hipSuccess;
     for (hipEvent_t e : set->ev) {
         const hipError_t r = hipEventDestroy(e);

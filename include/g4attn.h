@@ -92,7 +92,10 @@ int g4_readback_finish(g4_readback* handle, void* host_dst);
  * and writes ns_out[i] = the time from slot first+2i to slot first+2i+1 in
  * nanoseconds, or NaN where either slot was not written since the last resolve
  * of it (a pass that launched nothing); the resolved slots may then be written
- * again. */
+ * again. A set has at most one open pass, on any thread. Each call sees the
+ * others, whatever their threads: resolve refuses the slots of the open pass,
+ * begin_pass and write refuse slots being resolved, and destroy refuses a set
+ * with a pass open on another thread or a resolve under way (G4_EINVAL). */
 typedef struct g4_query_set g4_query_set;
 int g4_query_set_create(uint32_t count, g4_query_set** out);
 int g4_query_begin_pass(g4_query_set* set, uint32_t slot);

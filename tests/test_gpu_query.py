@@ -80,3 +80,51 @@ def test_pass_pairs_time_their_kernels(dev):
         assert st == abi.G4_EINVAL and "outside" in lib.g4_last_error().decode()
     finally:
         q.close()
+
+
+def test_open_pass_seen_from_other_threads(dev):
+    """A pass opened on one thread is seen by calls from another: a resolve of its slots, a second pass
+    on the set and the set's destroy are refused there, while a resolve of other slots goes on."""
+    import threading
+
+    announce("timestamp queries: a pass open on another thread")
+    q = ops.QuerySet(8)
+    lib = abi.load()
+    opened, release, done = threading.Event(), threading.Event(), threading.Event()
+    errors = []
+
+    def holder():
+        try:
+            q.begin_pass(2)
+            opened.set()
+            release.wait(30)
+            q.end_pass()
+        except Exception as e:  # reported by the main thread
+            errors.append(e)
+        finally:
+            opened.set()
+            done.set()
+
+    t = threading.Thread(target=holder)
+    t.start()
+    try:
+        assert opened.wait(30) and not errors, errors
+        out = (C.c_double * 4)()
+        st = lib.g4_query_resolve(q.handle, 2, 1, out)
+        assert st == abi.G4_EINVAL and "still open" in lib.g4_last_error().decode()
+        st = lib.g4_query_resolve(q.handle, 0, 2, out)  # slots 0..3 meet the pass's 2, 3
+        assert st == abi.G4_EINVAL and "still open" in lib.g4_last_error().decode()
+        assert math.isnan(q.resolve(4, 2)[0])  # other slots: nothing written, NaN
+        st = lib.g4_query_begin_pass(q.handle, 6)
+        assert st == abi.G4_EINVAL and "another thread" in lib.g4_last_error().decode()
+        st = lib.g4_query_set_destroy(q.handle)
+        assert st == abi.G4_EINVAL and "another thread" in lib.g4_last_error().decode()
+    finally:
+        release.set()
+        done.wait(30)
+        t.join(30)
+    assert not errors, errors
+    assert math.isnan(q.resolve(2, 1)[0])  # closed, and it launched nothing
+    q.begin_pass(6)  # free again
+    q.end_pass()
+    q.close()
