@@ -223,6 +223,26 @@ export interface QkvPrep {
   eps?: number;
 }
 
+// captureHidden's per-layer capture points (src/engine.ts:2749-2815; the kinds of src/types.ts:341-348):
+// after the q/k/v projection, after the per-head norms and RoPE, after the attention.
+export type AttnCapturePoint = 'preRopeQ' | 'preRopeK' | 'preRopeV' | 'postRopeQ' | 'postRopeK' | 'attnOut';
+
+// One layer's attention block for one token, as captureAttention runs it.
+export interface AttnCaptureLayer {
+  input: DeviceBuffer;        // the attention-normed hidden state f32 [n]
+  n: number;
+  segments: QkvSegment[];     // f16 weights: q, then k and v on KV-producer layers (outs: the layer's q/k/v)
+  prep: QkvPrep;              // norms, RoPE and (producer layers) the cache row at `slot` = seqLen - 1
+  kCache: DeviceBuffer;       // the caches the layer attends (its producer's on a consumer layer)
+  vCache: DeviceBuffer;
+  seqLen: number;
+  slidingWindow?: number;
+  scale?: number;
+  out: DeviceBuffer;          // attnOut f32 [NQH][HD]
+  prepWorkspace: DeviceBuffer;  // linearQkvPrepWorkspaceSize bytes, cleared once
+  stepWorkspace: DeviceBuffer;  // attnStepWorkspaceSize(1) bytes
+}
+
 // The fused sampling head: lm head over an f16 [vocab][hidden] weight, softcap (0 = none), argmax.
 export interface LmHeadShape {
   vocab: number;
@@ -749,6 +769,53 @@ export class HipAttention {
     } finally {
       this.endPass(slot);
     }
+  }
+
+  // captureHidden for the attention block of one layer (src/engine.ts:2749-2815 with the stop points of
+  // :2053-2095) on the fused kernels: runs the block for one token up to `stopAt` and returns the F32 contents
+  // of the work buffer there. preRope*: attn.linearQKV alone (the raw projection). postRope*: linearQkvPrep,
+  // whose epilogue leaves q and k post-norm, post-RoPE in place as fusedPerHeadNormRope leaves the engine's q
+  // and k buffers (it also stores the producer's K/V row, which the engine does next in kvCacheStore).
+  // attnOut: linearQkvPrep, then attnStep on the ready q with the row read from the cache. preRopeK,
+  // preRopeV and postRopeK exist on KV-producer layers only, as in the engine.
+  captureAttention(layer: AttnCaptureLayer, shape: StepShape, stopAt: AttnCapturePoint): Promise<Float32Array> {
+    const producer = layer.segments.length === 3;
+    if (!producer && (stopAt === 'preRopeK' || stopAt === 'preRopeV' || stopAt === 'postRopeK')) {
+      return Promise.reject(new Error('captureAttention: ' + stopAt + ' exists on KV-producer layers only'));
+    }
+    const HD = shape.headDim;
+    let src: DeviceBuffer;
+    let count: number;
+    try {
+      if (stopAt === 'preRopeQ' || stopAt === 'preRopeK' || stopAt === 'preRopeV') {
+        this.linear(layer.input, layer.n, layer.segments.map(function (g) {
+          return { weight: g.weight, out: g.out, rows: g.rows };
+        }));
+        const i = stopAt === 'preRopeQ' ? 0 : stopAt === 'preRopeK' ? 1 : 2;
+        src = layer.segments[i].out;
+        count = (i === 0 ? shape.numQHeads : shape.numKvHeads) * HD;
+      } else {
+        this.linearQkvPrep(layer.input, layer.n, 'f16', layer.segments, layer.prep, shape, layer.prepWorkspace);
+        if (stopAt === 'attnOut') {
+          this.attnStep([{
+            q: layer.segments[0].out, qWeight: layer.prep.qWeight, ropeFreqs: layer.prep.ropeFreqs,
+            kCache: layer.kCache, vCache: layer.vCache, out: layer.out, seqLen: layer.seqLen,
+            position: layer.prep.position, slidingWindow: layer.slidingWindow || 0, storeKv: false,
+            theta: layer.prep.theta, applyDivisor: layer.prep.applyDivisor || 0, scale: layer.scale,
+            eps: layer.prep.eps, qReady: true,
+          }], shape, layer.stepWorkspace);
+          src = layer.out;
+          count = shape.numQHeads * HD;
+        } else {
+          src = layer.segments[stopAt === 'postRopeQ' ? 0 : 1].out;
+          count = (stopAt === 'postRopeQ' ? shape.numQHeads : shape.numKvHeads) * HD;
+        }
+      }
+    } catch (e) {
+      return Promise.reject(e);
+    }
+    const out = new Float32Array(count);
+    return this.readBufferAsync(src, 0, out).then(function () { return out; });
   }
 
   // The same with the engine's quantized weights: each row bit-identical to a matmulQ8 / matmulQ4K dispatch.

@@ -19,6 +19,8 @@
 //   node host/run.js readback <dir> f32 values from <dir>/case.bin: logitSoftcap in place, then two
 //                                   readBufferAsync calls around a clearBuffer; both results (the
 //                                   softcapped values, then zeros) go to <dir>/out.bin.
+//   node host/run.js capture <dir>  captureAttention at each per-layer capture point of a producer and a
+//                                   consumer layer from <dir>/case.json + case.bin; results to <dir>/out.bin.
 //   node host/run.js linear <dir>   the projections from <dir>/case.json + case.bin: one matmulQuant
 //                                   dispatch per weight matrix (attn.linearQKV, src/engine.ts:2045-2051),
 //                                   then one linear call over all of them; results go to <dir>/out.bin.
@@ -616,6 +618,78 @@ function qkvPrep(dir: string): string[] {
   return ['linearQkvPrep: 1 call', 'attnStep (qReady): 1 call', 'results written'];
 }
 
+// captureAttention at every per-layer capture point of a KV-producer layer, then postRopeQ and attnOut of a
+// consumer layer reading the producer's caches (case.json as qkvPrep's, with `cw0`: the consumer's q
+// weight, `cqw`: its q norm); out.bin = the producer's preRopeQ, preRopeK, preRopeV, postRopeQ, postRopeK,
+// attnOut, then the consumer's postRopeQ and attnOut (f32), then both caches.
+async function capture(dir: string): Promise<string[]> {
+  const spec = JSON.parse(fs.readFileSync(path.join(dir, 'case.json'), 'utf8')) as QkvPrepSpec;
+  const bin: Uint8Array = fs.readFileSync(path.join(dir, 'case.bin'));
+  const att = new HipAttention(loadAddon(), 0);
+  const bufs: DeviceBuffer[] = [];
+  function alloc(bytes: number): DeviceBuffer {
+    const b = att.createBuffer(bytes);
+    att.clearBuffer(b);
+    bufs.push(b);
+    return b;
+  }
+  function upload(name: string): DeviceBuffer {
+    const r = spec.arrays[name];
+    const b = alloc(r[1]);
+    att.writeBuffer(b, 0, bin.subarray(r[0], r[0] + r[1]));
+    return b;
+  }
+  const shape = { numQHeads: spec.nqh, numKvHeads: spec.nkh, headDim: spec.hd };
+  const rows = [spec.nqh * spec.hd, spec.nkh * spec.hd, spec.nkh * spec.hd];
+  const kc = upload('kc'), vc = upload('vc'), x = upload('x'), rf = upload('rf');
+  const qw = upload('qw'), kw = upload('kw'), cqw = upload('cqw');
+  const prepWs = alloc(att.linearQkvPrepWorkspaceSize(shape));
+  const stepWs = alloc(att.attnStepWorkspaceSize(1, shape));
+  const prep = { ropeFreqs: rf, position: spec.position, slot: spec.slot, maxSeqLen: spec.rows, theta: spec.theta,
+    applyDivisor: spec.div };
+  const producer = {
+    input: x, n: spec.n,
+    segments: rows.map(function (r, i) { return { weight: upload('w' + i), out: alloc(r * 4), rows: r }; }),
+    prep: Object.assign({ qWeight: qw, kWeight: kw, kCache: kc, vCache: vc }, prep),
+    kCache: kc, vCache: vc, seqLen: spec.seq, out: alloc(spec.nqh * spec.hd * 4),
+    prepWorkspace: prepWs, stepWorkspace: stepWs,
+  };
+  const consumer = {
+    input: x, n: spec.n, segments: [{ weight: upload('cw0'), out: alloc(rows[0] * 4), rows: rows[0] }],
+    prep: Object.assign({ qWeight: cqw }, prep),
+    kCache: kc, vCache: vc, seqLen: spec.seq, out: alloc(spec.nqh * spec.hd * 4),
+    prepWorkspace: prepWs, stepWorkspace: stepWs,
+  };
+  const got: Float32Array[] = [];
+  for (const k of ['preRopeQ', 'preRopeK', 'preRopeV', 'postRopeQ', 'postRopeK', 'attnOut'] as const) {
+    got.push(await att.captureAttention(producer, shape, k));
+  }
+  got.push(await att.captureAttention(consumer, shape, 'postRopeQ'));
+  got.push(await att.captureAttention(consumer, shape, 'attnOut'));
+  let refused = '';
+  try {
+    await att.captureAttention(consumer, shape, 'postRopeK');
+  } catch (e) {
+    refused = String(e);
+  }
+  if (refused.indexOf('KV-producer layers only') < 0) fail('postRopeK of a consumer layer not refused: ' + refused);
+  let total = kc.size + vc.size;
+  for (const g of got) total += g.byteLength;
+  const res = new Uint8Array(total);
+  let off = 0;
+  for (const g of got) {
+    res.set(new Uint8Array(g.buffer, g.byteOffset, g.byteLength), off);
+    off += g.byteLength;
+  }
+  att.readBuffer(kc, 0, res.subarray(off, off + kc.size));
+  att.readBuffer(vc, 0, res.subarray(off + kc.size, off + kc.size + vc.size));
+  fs.writeFileSync(path.join(dir, 'out.bin'), res);
+  for (const b of bufs) att.destroyBuffer(b);
+  att.dispose();
+  return ['captureAttention: 6 points of a producer layer, 2 of a consumer', 'postRopeK of a consumer refused',
+    'results written'];
+}
+
 // Promise readback: each copy is ordered where it was issued on the stream, whatever enqueues follow it.
 function readback(dir: string): Promise<string[]> {
   const bin: Uint8Array = fs.readFileSync(path.join(dir, 'case.bin'));
@@ -707,8 +781,9 @@ async function profile(dir: string): Promise<string[]> {
 
 export function main(argv: string[]): void {
   const mode = argv[0];
-  if (mode === 'readback' || mode === 'profile' || mode === 'batch') {
-    (mode === 'readback' ? readback(argv[1]) : mode === 'profile' ? profile(argv[1]) : batch(argv[1])).then(function (done) {
+  if (mode === 'readback' || mode === 'profile' || mode === 'batch' || mode === 'capture') {
+    (mode === 'readback' ? readback(argv[1]) : mode === 'profile' ? profile(argv[1])
+      : mode === 'capture' ? capture(argv[1]) : batch(argv[1])).then(function (done) {
       process.stdout.write(JSON.stringify({ ok: true, checks: done }) + '\n');
     }, function (e) {
       process.stderr.write(String(e && e.stack ? e.stack : e) + '\n');
@@ -724,6 +799,6 @@ export function main(argv: string[]): void {
   else if (mode === 'promptprep') done = promptPrep(argv[1]);
   else if (mode === 'linear') done = linear(argv[1]);
   else if (mode === 'qkvprep') done = qkvPrep(argv[1]);
-  else fail(`usage: run.js cpu | layer <dir> | prefill <dir> | promptprep <dir> | head <dir> | linear <dir> | qkvprep <dir> | batch <dir> | readback <dir> | profile`);
+  else fail(`usage: run.js cpu | layer <dir> | prefill <dir> | promptprep <dir> | head <dir> | linear <dir> | qkvprep <dir> | capture <dir> | batch <dir> | readback <dir> | profile`);
   process.stdout.write(JSON.stringify({ ok: true, checks: done }) + '\n');
 }

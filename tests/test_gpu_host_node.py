@@ -493,3 +493,63 @@ def test_linear_qkv_prep_through_ts_host(tmp_path):
     want = orc.attention_chain(want_q, orc.f16_bits_to_f32(gkc).reshape(-1), orc.f16_bits_to_f32(gvc).reshape(-1),
                                NQH, NKH, hd, seq, 1.0, 0)
     assert max_abs(out, want) <= 2e-3
+
+
+@pytest.mark.skipif(NODE is None, reason="node is not installed")
+def test_capture_points_through_ts_host(tmp_path):
+    """HipAttention.captureAttention (captureHidden's per-layer stop points, src/engine.ts:2053-2095,
+    2749-2815) on the fused kernels: for a KV-producer layer preRopeQ/K/V are the oracle's matmulQuant rows,
+    postRopeQ/K its fused_per_head_norm_rope over them (bit-identical), attnOut within 2e-3 of its chain; a
+    consumer layer's postRopeQ and attnOut over the producer's caches likewise, its postRopeK refused."""
+    announce("TS host captureAttention")
+    n, hd, theta, div, seq = 1536, 256, 1e4, 0, 700
+    pos = seq - 1
+    rng = np.random.default_rng(71)
+    x = rng.standard_normal(n, dtype=np.float32)
+    w = [(rng.standard_normal((r, n), dtype=np.float32) * 0.05).astype(np.float16).view(np.uint16)
+         for r in (NQH * hd, NKH * hd, NKH * hd)]
+    cw = (rng.standard_normal((NQH * hd, n), dtype=np.float32) * 0.05).astype(np.float16).view(np.uint16)
+    qw, kw, cqw = f16_weight_bits(72, hd), f16_weight_bits(73, hd), f16_weight_bits(74, hd)
+    kc = np.zeros((seq, NKH * hd), np.uint16)
+    vc = np.zeros((seq, NKH * hd), np.uint16)
+    kc[:pos] = cache_f16(75, pos, NKH, hd).reshape(pos, -1)
+    vc[:pos] = cache_f16(76, pos, NKH, hd).reshape(pos, -1)
+    arrs = {"x": x, "w0": w[0], "w1": w[1], "w2": w[2], "cw0": cw, "qw": qw, "kw": kw, "cqw": cqw, "rf": ROPE,
+            "kc": kc, "vc": vc}
+    blob, index = bytearray(), {}
+    for name, a in arrs.items():
+        b = np.ascontiguousarray(a).tobytes()
+        index[name] = [len(blob), len(b)]
+        blob += b
+    (tmp_path / "case.bin").write_bytes(bytes(blob))
+    (tmp_path / "case.json").write_text(json.dumps(dict(n=n, nqh=NQH, nkh=NKH, hd=hd, position=pos, slot=pos, rows=seq,
+                                                        theta=theta, div=div, seq=seq, arrays=index)))
+    r = subprocess.run([NODE, str(RUN), "capture", str(tmp_path)], cwd=ROOT, capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 0, r.stderr
+    assert '"ok":true' in r.stdout
+    raw = (tmp_path / "out.bin").read_bytes()
+    qn, kn = NQH * hd, NKH * hd
+    sizes = [qn * 4, kn * 4, kn * 4, qn * 4, kn * 4, qn * 4, qn * 4, qn * 4, seq * kn * 2, seq * kn * 2]
+    parts, off = [], 0
+    for sz in sizes:
+        parts.append(raw[off:off + sz])
+        off += sz
+    f = [np.frombuffer(p_, np.float32) for p_ in parts[:8]]
+    gkc, gvc = (np.frombuffer(p_, np.uint16).reshape(seq, -1) for p_ in parts[8:])
+    pre = [orc.matmul_quant(x, w[i], rr, n) for i, rr in enumerate((qn, kn, kn))]
+    for i, name in enumerate(("preRopeQ", "preRopeK", "preRopeV")):
+        np.testing.assert_array_equal(f[i].view(np.uint32), pre[i].view(np.uint32), err_msg=name)
+    want_q = orc.fused_per_head_norm_rope(pre[0], qw, ROPE, NQH, hd, EPS, pos, theta, div)
+    want_k = orc.fused_per_head_norm_rope(pre[1], kw, ROPE, NKH, hd, EPS, pos, theta, div)
+    want_v = orc.per_head_rms_norm_no_weight(pre[2], NKH, hd, EPS)
+    np.testing.assert_array_equal(f[3].view(np.uint32), want_q.view(np.uint32), err_msg="postRopeQ")
+    np.testing.assert_array_equal(f[4].view(np.uint32), want_k.view(np.uint32), err_msg="postRopeK")
+    np.testing.assert_array_equal(gkc[pos], orc.f32_to_f16_bits(want_k))
+    np.testing.assert_array_equal(gvc[pos], orc.f32_to_f16_bits(want_v))
+    kb, vb = orc.f16_bits_to_f32(gkc).reshape(-1), orc.f16_bits_to_f32(gvc).reshape(-1)
+    assert max_abs(f[5], orc.attention_chain(want_q, kb, vb, NQH, NKH, hd, seq, 1.0, 0)) <= 2e-3
+    cq = orc.fused_per_head_norm_rope(orc.matmul_quant(x, cw, qn, n), cqw, ROPE, NQH, hd, EPS, pos, theta, div)
+    np.testing.assert_array_equal(f[6].view(np.uint32), cq.view(np.uint32), err_msg="consumer postRopeQ")
+    assert max_abs(f[7], orc.attention_chain(cq, kb, vb, NQH, NKH, hd, seq, 1.0, 0)) <= 2e-3
+    print(r.stdout.strip())
