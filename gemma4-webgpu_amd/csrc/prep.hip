@@ -153,8 +153,21 @@ __global__ __launch_bounds__(kWG) void k_prompt_prep(const float* __restrict__ q
     const unsigned wave = threadIdx.x >> 6;
     const unsigned S = p.num_q_heads + (p.store_kv ? 2 * p.num_kv_heads : 0);
     const unsigned vt_blocks = (p.max_seq_len + 31) / 32;
-    for (unsigned w = wave; w < nt * S; w += kWG / 64) {  // uniform per wave
-        const unsigned tt = w / S, slot = w % S;
+    uint32_t wq[J], wk[J];  // the norm weights, loaded once per wave
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+        wq[j] = q_weight[lane + 64 * j];
+        wk[j] = p.store_kv ? k_weight[lane + 64 * j] : 0u;
+    }
+    // The wave's slots w = wave, wave + 4, ... of the nt * S (token, head slot) pairs, as (tt, slot)
+    // stepped without a division.
+    if (S == 0) return;  // (the host refuses it) every step below takes slot down by S
+    unsigned tt = 0, slot = wave;
+    while (slot >= S && tt < nt) {  // uniform
+        slot -= S;
+        tt++;
+    }
+    for (; tt < nt;) {  // uniform per wave
         const unsigned t = t0 + tt, pos = p.start + t;
         const bool is_q = slot < p.num_q_heads;
         const unsigned r = slot - p.num_q_heads;
@@ -168,7 +181,7 @@ __global__ __launch_bounds__(kWG) void k_prompt_prep(const float* __restrict__ q
 #pragma unroll
         for (int j = 0; j < J; j++) {
             x[j] = src[lane + 64 * j];
-            wb[j] = rope ? (is_q ? q_weight : k_weight)[lane + 64 * j] : 0u;
+            wb[j] = is_q ? wq[j] : wk[j];  // v: not used (weightless)
         }
         RopeLane<PJ> rl;
 #pragma unroll
@@ -185,6 +198,11 @@ __global__ __launch_bounds__(kWG) void k_prompt_prep(const float* __restrict__ q
             uint16_t* vt = vt_cache + ((uint64_t)h * vt_blocks + pos / 32) * (HD * 32) + pos % 32;
 #pragma unroll
             for (int j = 0; j < J; j++) vt[(lane + 64 * j) * 32] = f2h(x[j]);
+        }
+        slot += kWG / 64;
+        while (slot >= S) {  // uniform
+            slot -= S;
+            tt++;
         }
     }
 }

@@ -262,6 +262,21 @@ __device__ __forceinline__ float wave_tree_sum(float c) {
 // tree with strides 128, 64 (in the lane) and 32..1 (across lanes), so every
 // value is bit-identical to fused_per_head_norm_rope.wgsl /
 // per_head_rms_norm_no_weight.wgsl.
+// a / b, correctly rounded, for many dividends over one divisor b whose
+// correctly rounded reciprocal y = 1.0f / b is computed once: q0 = a y is
+// within an ulp of a / b, the residual a - q0 b is exact in one FMA, and
+// q0 + (a - q0 b) y rounds to the correctly rounded quotient (Markstein's
+// theorem; Muller et al., Handbook of Floating-Point Arithmetic, 2nd ed.,
+// ch. 4). Tiny, zero or non-finite dividends and divisors of 2^32 or more,
+// where an intermediate could leave the normal range, take the IEEE
+// division. Checked bit for bit against a / b over 10^9 operand pairs
+// (tests/div_check.c).
+__device__ __forceinline__ float div_shared(float a, float b, float y) {
+    if (!(fabsf(a) >= 0x1p-64f) || !(b < 0x1p32f)) return a / b;
+    const float q0 = a * y;
+    return __builtin_fmaf(__builtin_fmaf(-q0, b, a), y, q0);
+}
+
 template <int J>
 __device__ __forceinline__ void wave_norm_rope(float (&x)[J], const uint32_t (&wbits)[J], bool weighted, bool rope,
                                                const RopeLane<J / 2>& r, float eps) {
@@ -278,8 +293,9 @@ __device__ __forceinline__ void wave_norm_rope(float (&x)[J], const uint32_t (&w
     const float b = part[1] + part[3];  // t = lane + 64 : s[t] + s[t + 128]
     const float total = wave_tree_sum(a + b);  // stride 64, then 32 .. 1
     const float rms = sqrtf(total / (float)HD + eps);
+    const float inv = 1.0f / rms;  // correctly rounded: the divisor's reciprocal for div_shared
 #pragma unroll
-    for (int j = 0; j < J; j++) x[j] = weighted ? x[j] * h2f((uint16_t)wbits[j]) / rms : x[j] / rms;
+    for (int j = 0; j < J; j++) x[j] = div_shared(weighted ? x[j] * h2f((uint16_t)wbits[j]) : x[j], rms, inv);
     if (!rope) return;
 #pragma unroll
     for (int p = 0; p < PJ; p++) {
