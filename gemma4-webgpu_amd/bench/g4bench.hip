@@ -180,7 +180,7 @@ static int run_lmhead(const std::string& mode, int iters) {
 // rotated so the bytes read per cycle exceed twice the 256 MB MALL.
 //   --mode q8 | q4k: the same with the engine's quantized weights (g4_linear_quant), and
 //   q8chain | q4kchain: one matmulQ8 / matmulQ4K dispatch per matrix.
-static int run_proj(const std::string& wl, const std::string& mode, int iters) {
+static int run_proj(const std::string& wl, const std::string& mode, int iters, int sets_arg) {
     const uint32_t H = 1536, hd = wl == "proj512" ? 512 : 256, NQ = NQH * hd, NK = NKH * hd;
     const int fmt = mode.rfind("q8", 0) == 0 ? 1 : mode.rfind("q4k", 0) == 0 ? 2 : 0;
     const bool qchain = fmt && mode.find("chain") != std::string::npos;
@@ -189,7 +189,8 @@ static int run_proj(const std::string& wl, const std::string& mode, int iters) {
     const uint64_t welems = (uint64_t)(NQ + 2 * NK) * H + (uint64_t)H * NQ;
     const uint64_t wbytes = (uint64_t)(welems * bpe);
     const uint64_t bytes = wbytes + (H + NQ) * 4 + (uint64_t)(NQ + 2 * NK + H) * 4;
-    const int sets = (int)((512ull << 20) / wbytes) + 1;
+    // --sets N: N weight sets instead (1: the same weights every iteration, served from the MALL)
+    const int sets = sets_arg > 0 ? sets_arg : (int)((512ull << 20) / wbytes) + 1;
     printf("workload %s: head_dim %u, %.2f MB of weights per layer, %d weight sets\n", wl.c_str(), hd, wbytes / 1e6,
            sets);
     printf("bytes_per_step: %llu\n", (unsigned long long)bytes);
@@ -410,7 +411,7 @@ int main(int argc, char** argv) {
     if (wl == "copy") return run_copy(iters);
     if (wl == "prefill4k" || wl == "prefill4k512") return run_prefill(wl, mode, iters);
     if (wl == "lmhead") return run_lmhead(mode, iters);
-    if (wl == "proj256" || wl == "proj512") return run_proj(wl, mode, iters);
+    if (wl == "proj256" || wl == "proj512") return run_proj(wl, mode, iters, sets);
     std::vector<Layer> L = workload(wl);
     const bool uniform_pos = wl.rfind("stack", 0) == 0 || L.size() == 1;
     uint64_t step_bytes = 0, total_rows = 0;

@@ -181,3 +181,60 @@ def test_prep_then_step_equals_raw_step(dev, hd, window, theta, div, seq):
     want = orc.attention_chain(q_, orc.f16_bits_to_f32(kb[lo:]).reshape(-1), orc.f16_bits_to_f32(vb[lo:]).reshape(-1),
                                nqh, nkh, hd, seq - lo, 1.0, 0)
     assert max_abs(a, want) <= 2e-3
+
+
+@pytest.mark.parametrize("hd,window,theta,div,seq0", [(256, 512, 1e4, 0, 500), (512, 0, 1e6, 1, 990)])
+def test_fused_layer_tokens_with_advanced_plan(dev, hd, window, theta, div, seq0):
+    """The fully fused engine order over consecutive tokens: per token a new hidden state, g4_linear_qkv_prep
+    (projection, norms, RoPE, the K/V row stored at the token's slot), then the attention of a q_ready plan
+    prepared at the first token and advanced on the host every token after (g4_attn_step_advance), across the
+    window edge (local layer) and a 32-row tile boundary. Each token: q, k, v and the stored row bit-identical
+    to the oracle's matmulQuant followed by the reference prep, attnOut within 2e-3 of the oracle's chain over
+    the cache as that token leaves it."""
+    from helpers import cache_f16_torch, max_abs
+    n, nqh, nkh, T = 1536, 8, 1, 40
+    announce(f"linearQkvPrep -> attnStep(q_ready, advanced) over {T} tokens, hd={hd} seq0={seq0}")
+    rows = seq0 + T
+    L = Layer(dev, 5000 + hd, "f16", n, nqh, nkh, hd, True, rows=rows)
+    L.kc.copy_(torch.zeros_like(L.kc))
+    L.vc.copy_(torch.zeros_like(L.vc))
+    L.kc[: (seq0 - 1) * hd] = cache_f16_torch(5100 + hd, seq0 - 1, nkh, hd, dev).view(torch.int16).reshape(-1)
+    L.vc[: (seq0 - 1) * hd] = cache_f16_torch(5200 + hd, seq0 - 1, nkh, hd, dev).view(torch.int16).reshape(-1)
+    out = torch.full((nqh * hd,), float("nan"), device=dev)
+    pws = torch.zeros(ops.qkv_prep_workspace_bytes(nqh, nkh), dtype=torch.uint8, device=dev)
+    sws = torch.empty(ops.step_workspace_bytes(1, nqh, nkh, hd), dtype=torch.uint8, device=dev)
+    inv_dev = ops.rope_inv_freq(theta, hd, div, L.drf)
+    inv_host = ops.rope_inv_freq_host(theta, hd, div, ROPE)
+    plan = None
+    rng = np.random.default_rng(5300 + hd)
+    for t in range(T):
+        seq = seq0 + t
+        pos = seq - 1
+        L.x = rng.standard_normal(n, dtype=np.float32)
+        L.dx.copy_(torch.from_numpy(L.x))
+        ops.linear_qkv_prep(L.dx, n, "f16", L.dev_segs, L.dqw, nqh, nkh, hd, pos, theta, div, pws, k_weight=L.dkw,
+                            rope_freqs=L.drf, rope_inv_freq=inv_dev, k_cache=L.kc, v_cache=L.vc, slot=pos,
+                            max_seq_len=rows)
+        if plan is None:
+            e = dict(q=L.outs[0], k=None, v=None, q_weight=L.dqw, k_weight=None, rope_freqs=L.drf,
+                     rope_inv_freq_host=inv_host, k_cache=L.kc, v_cache=L.vc, out=out, seq_len=seq, position=pos,
+                     sliding_window=window, store_kv=False, theta=theta, apply_divisor=div, q_ready=True)
+            plan = ops.attn_step_prepare(ops.make_step_entries([e], nqh, nkh, hd), nqh, nkh, hd, sws)
+        else:
+            ops.attn_step_advance(plan, 1)
+        ops.attn_step_run(plan)
+        torch.cuda.synchronize()
+        q = orc.fused_per_head_norm_rope(L.raw(0), L.qw, ROPE, nqh, hd, EPS, pos, theta, div)
+        k = orc.fused_per_head_norm_rope(L.raw(1), L.kw, ROPE, nkh, hd, EPS, pos, theta, div)
+        v = orc.per_head_rms_norm_no_weight(L.raw(2), nkh, hd, EPS)
+        np.testing.assert_array_equal(L.outs[0].cpu().numpy().view(np.uint32), q.view(np.uint32),
+                                      err_msg=f"token {t} q")
+        kc = L.kc.cpu().numpy().view(np.uint16).reshape(rows, -1)
+        vc = L.vc.cpu().numpy().view(np.uint16).reshape(rows, -1)
+        np.testing.assert_array_equal(kc[pos], orc.f32_to_f16_bits(k), err_msg=f"token {t} stored k")
+        np.testing.assert_array_equal(vc[pos], orc.f32_to_f16_bits(v), err_msg=f"token {t} stored v")
+        lo = seq - window if window and seq > window else 0
+        want = orc.attention_chain(q, orc.f16_bits_to_f32(kc[lo:seq]).reshape(-1),
+                                   orc.f16_bits_to_f32(vc[lo:seq]).reshape(-1), nqh, nkh, hd, seq - lo, 1.0, 0)
+        err = max_abs(out.cpu().numpy(), want)
+        assert err <= 2e-3, f"token {t}: attnOut max-abs {err}"
