@@ -25,6 +25,11 @@
         readings), next to rocprofv3's own MfmaUtil, and the f16 MFMA flops issued
         (512 per MOP).
 
+    profile_summary.py counters --dir D [--dir D2 ...] --kernel REGEX --command "..."
+        Every counter found for the kernel matching REGEX in the given `--pmc` passes, as a mean
+        per dispatch (the rows of one dispatch summed), and each SQ_INSTS_* counter per wave
+        when SQ_WAVES is among them.
+
 Counter values are KiB per dispatch. The summary prints `hbm_bytes_per_launch:`,
 which bench.py reads as the roofline's `traffic`.
 """
@@ -178,6 +183,32 @@ def cmd_mfma(a) -> None:
         print(f"issued_over_algorithmic: {flops / a.algorithmic_flops:.4f}")
 
 
+def cmd_counters(a) -> None:
+    rx = re.compile(a.kernel)
+    names: list[str] = []
+    for d in a.dir:
+        for f in _csvs(d, "counter_collection.csv"):
+            for row in csv.DictReader(f.open()):
+                if rx.search(row["Kernel_Name"]) and row["Counter_Name"] not in names:
+                    names.append(row["Counter_Name"])
+    print(f"command: {a.command}")
+    vals: dict[str, float] = {}
+    for name in names:
+        for d in a.dir:
+            try:
+                v, n = counter_per_dispatch(d, name, a.kernel)
+            except SystemExit:
+                continue
+            vals[name] = v
+            print(f"{name}: {v:.0f} per dispatch ({n} dispatches)")
+            break
+    waves = vals.get("SQ_WAVES")
+    if waves:
+        for name, v in vals.items():
+            if name.startswith("SQ_INSTS_"):
+                print(f"{name.lower()}_per_wave: {v / waves:.1f}")
+
+
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     sub = ap.add_subparsers(dest="mode", required=True)
@@ -204,8 +235,12 @@ def main() -> None:
     m.add_argument("--simds", type=int, default=1024)
     m.add_argument("--xcds", type=int, default=8)
     m.add_argument("--algorithmic-flops", type=float, default=0.0)
+    c = sub.add_parser("counters")
+    c.add_argument("--dir", required=True, action="append")
+    c.add_argument("--kernel", required=True)
+    c.add_argument("--command", required=True)
     a = ap.parse_args()
-    {"trace": cmd_trace, "gaps": cmd_gaps, "traffic": cmd_traffic, "mfma": cmd_mfma}[a.mode](a)
+    {"trace": cmd_trace, "gaps": cmd_gaps, "traffic": cmd_traffic, "mfma": cmd_mfma, "counters": cmd_counters}[a.mode](a)
 
 
 if __name__ == "__main__":
