@@ -525,12 +525,13 @@ int g4_query_resolve(g4_query_set* set, uint32_t first, uint32_t n_pairs, double
 
 int g4_query_set_destroy(g4_query_set* set) {
     if (!set) return fail(G4_EINVAL, "g4_query_set_destroy: set is NULL");
-    if (t_pass.set == set) t_pass = OpenPass();  // this thread's own pass: closed with the set
-    else {
+    {
         std::lock_guard<std::mutex> lock(set->mu);
-        if (set->open_slot >= 0) return fail(G4_EINVAL, "g4_query_set_destroy: a pass of this set is open on another thread");
+        if (set->open_slot >= 0 && t_pass.set != set)
+            return fail(G4_EINVAL, "g4_query_set_destroy: a pass of this set is open on another thread");
         if (!set->resolving.empty()) return fail(G4_EINVAL, "g4_query_set_destroy: slots of this set are being resolved");
     }
+    if (t_pass.set == set) t_pass = OpenPass();  // this thread's own pass: closed with the set
     hipError_t first_err = hipSuccess;
     for (hipEvent_t e : set->ev) {
         const hipError_t r = hipEventDestroy(e);
