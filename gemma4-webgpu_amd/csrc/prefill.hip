@@ -29,6 +29,13 @@
 // A part that covers a tile's whole key range writes attnOut rows directly;
 // otherwise it writes a partial record (m, l, unnormalised o) per q-row and
 // the fixed-order log-sum-exp merge of decode.hip combines the parts.
+//
+// Work items (a tile's part) are spread on the host over one list per CU,
+// longest first to the least loaded list, and each workgroup runs its list's
+// items in a loop: a workgroup's end waits for its result stores, which cost
+// ~5 us per item when every item was a workgroup of its own (prefill4k: 100 us
+// with the stores skipped against 116), while in the loop they drain under the
+// next item's first tiles.
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
@@ -36,6 +43,7 @@
 #include <hip/hip_ext.h>
 
 #include <algorithm>
+#include <queue>
 #include <vector>
 
 #include "decode_core.h"
@@ -86,6 +94,7 @@ struct PrefillWorkDev {
 struct PrefillArgs {
     const PrefillEntryDev* table;
     const PrefillWorkDev* work;
+    const uint32_t* lists;  // [n_lists + 1]: list l is work[lists[l] .. lists[l + 1])
     uint32_t num_q_heads;
     uint32_t num_kv_heads;
     uint32_t group;
@@ -187,13 +196,12 @@ __device__ __forceinline__ void lds_dma16_m0(uint32_t voff, const void* sbase, u
 }
 #pragma clang diagnostic pop
 
-__global__ __launch_bounds__(512, 1) void k_prefill_pp(PrefillArgs a) {
+// One work item: the body of k_prefill_pp's loop.
+__device__ __forceinline__ void prefill_pp_item(const PrefillArgs& a, const PrefillWorkDev wk, PrefillPpSmem& sm) {
     constexpr int HD = 256;
     constexpr unsigned SM = kPpStages - 1;                       // stage of tile t: t & SM
     constexpr int NQ = HD / 16, KPER = HD / 64, PER = KPER + 4;  // score steps; K and all DMAs per tile and score wave
     constexpr int R = 3;                                         // LDS operand reads ahead of their MFMA
-    __shared__ PrefillPpSmem sm;
-    const PrefillWorkDev wk = a.work[wg_x()];
     const PrefillEntryDev& ent = a.table[wk.entry];
     const unsigned kvh = wg_y();
     const unsigned G = a.group, NQH = a.num_q_heads, NKH = a.num_kv_heads;
@@ -539,6 +547,18 @@ __global__ __launch_bounds__(512, 1) void k_prefill_pp(PrefillArgs a) {
     if (half == 0) stg<f32x2>(a.part_ml + rec * 2, f32x2{m_fin, L});
 }
 
+// A workgroup runs the work items of its list (lists[l] .. lists[l + 1] of the
+// work array, built on the host longest first to the least loaded list) one
+// after the other: the output waves' stores of an item drain while the score
+// waves load the next item's q and first tiles, and no workgroup is launched
+// per item. Grid: the lists x kv heads.
+__global__ __launch_bounds__(512, 1) void k_prefill_pp(PrefillArgs a) {
+    __shared__ PrefillPpSmem sm;
+    const unsigned l = wg_x();
+    const unsigned i1 = a.lists[l + 1];
+    for (unsigned i = a.lists[l]; i < i1; i++) prefill_pp_item(a, a.work[i], sm);
+}
+
 // ---- head_dim 512: shared scores, six waves -----------------------------------
 //
 // The head_dim 512 form of k_prefill_pp. A workgroup takes one 64-row half of a
@@ -572,13 +592,12 @@ __device__ __forceinline__ void vm_barrier() {
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-__global__ __launch_bounds__(384, 1) void k_prefill_pp512(PrefillArgs a) {
+// One work item's row half zh: the body of k_prefill_pp512's loop.
+__device__ __forceinline__ void prefill_pp512_item(const PrefillArgs& a, const PrefillWorkDev wk, unsigned zh,
+                                                   PrefillPp512Smem& sm) {
     constexpr int HD = 512;
     constexpr int NQ = HD / 16;  // score steps
     constexpr int R = 3;         // LDS operand reads ahead of their MFMA
-    __shared__ PrefillPp512Smem sm;
-    const unsigned zh = wg_z();  // row half of the work item's query tile
-    const PrefillWorkDev wk = a.work[wg_x()];
     const PrefillEntryDev& ent = a.table[wk.entry];
     const unsigned kvh = wg_y();
     const unsigned G = a.group, NQH = a.num_q_heads, NKH = a.num_kv_heads;
@@ -888,6 +907,18 @@ __global__ __launch_bounds__(384, 1) void k_prefill_pp512(PrefillArgs a) {
     if (half == 0 && dh == 0) stg<f32x2>(a.part_ml + rec * 2, f32x2{m_fin, L});
 }
 
+// A workgroup runs the work items of its list (lists[l] .. lists[l + 1] of the
+// work array, built on the host longest first to the least loaded list) one
+// after the other, so that an item's result stores drain while the next item's
+// q and first tiles load, and no workgroup is launched per item. Grid: the
+// lists x kv heads x the two row halves.
+__global__ __launch_bounds__(384, 1) void k_prefill_pp512(PrefillArgs a) {
+    __shared__ PrefillPp512Smem sm;
+    const unsigned l = wg_x(), zh = wg_z();
+    const unsigned i1 = a.lists[l + 1];
+    for (unsigned i = a.lists[l]; i < i1; i++) prefill_pp512_item(a, a.work[i], zh, sm);
+}
+
 // V of one cache in 32-key blocks [kv head][block][HD][32] (f16): block j holds
 // rows 32 j .. 32 j + 31 (rows past the cache's end repeat its last row).
 struct VtCacheDev {
@@ -948,7 +979,7 @@ struct PrefillPlanRep {
     uint16_t num_q_heads;
     uint16_t num_kv_heads;
     uint16_t head_dim;     // 256 or 512
-    uint16_t pad;
+    uint16_t n_lists;      // workgroup lists (at most one per CU)
     uint32_t magic;
     uint32_t off_work, off_merge, off_ml, off_o;  // workspace byte offsets (workspaces stay under 4 GiB)
     uint32_t off_vtc;      // V^T cache table
@@ -967,8 +998,12 @@ void tile_keys(const g4_prefill_entry& e, uint32_t G, uint32_t tile, uint32_t* k
 }
 
 struct Layout {
-    size_t table, work, merge, ml, o, vtc, vt, total;
+    size_t table, work, lists, merge, ml, o, vtc, vt, total;
 };
+
+// The fixed cost of a work item (its first tiles' latency, the result
+// stores), in tiles, when items are spread over the workgroups' lists.
+constexpr uint64_t kPfItemCost = 10;
 
 // The caches whose V the pipelined form transposes: one per distinct v_cache
 // of the entries without a V^T cache of their own, long enough for every
@@ -983,8 +1018,8 @@ struct VtPlan {
 
 // Work list, merge list and workspace layout for a set of entries.
 int build(const g4_prefill_entry* ents, uint32_t n, uint32_t nqh, uint32_t nkh, uint32_t hd,
-          std::vector<PrefillEntryDev>* tab, std::vector<PrefillWorkDev>* work, std::vector<DecodeEntryDev>* merge,
-          uint32_t* max_parts, Layout* L, VtPlan* vp) {
+          std::vector<PrefillEntryDev>* tab, std::vector<PrefillWorkDev>* work, std::vector<uint32_t>* lists,
+          std::vector<DecodeEntryDev>* merge, uint32_t* max_parts, Layout* L, VtPlan* vp) {
     const uint32_t G = nqh / nkh;
     *vp = VtPlan{};
     {
@@ -1070,16 +1105,39 @@ int build(const g4_prefill_entry* ents, uint32_t n, uint32_t nqh, uint32_t nkh, 
             }
         }
     }
-    // Longest items first: the dispatcher starts workgroups in index order.
+    // One list per workgroup running at once (one per CU; an item takes num_kv_heads workgroups,
+    // twice that at head_dim 512): the items, longest first, each to the least loaded list (its
+    // tiles plus the fixed cost of an item). A list's items lie together in the work array.
     std::stable_sort(items.begin(), items.end(), [](const Item& x, const Item& y) { return x.keys > y.keys; });
+    const uint32_t wgs_per_item = nkh * (hd / 256);
+    const uint32_t n_lists = (uint32_t)std::min<uint64_t>(std::max(1u, (uint32_t)device_cus() / wgs_per_item),
+                                                          std::max<size_t>(items.size(), 1));
+    std::vector<std::vector<uint32_t>> member(n_lists);
+    {
+        using Load = std::pair<uint64_t, uint32_t>;  // (load, list): the smallest load first, then the lowest list
+        std::priority_queue<Load, std::vector<Load>, std::greater<Load>> heap;
+        for (uint32_t l = 0; l < n_lists; l++) heap.push({0, l});
+        for (uint32_t i = 0; i < items.size(); i++) {
+            const Load top = heap.top();
+            heap.pop();
+            member[top.second].push_back(i);
+            heap.push({top.first + (items[i].keys + kPfKeys - 1) / kPfKeys + kPfItemCost, top.second});
+        }
+    }
     work->clear();
-    for (auto& it : items) work->push_back(it.w);
+    lists->assign(1, 0u);
+    for (const auto& m : member) {
+        for (uint32_t i : m) work->push_back(items[i].w);
+        lists->push_back((uint32_t)work->size());
+    }
     if (work->size() > 0x7fffffffu || slots > 0x7fffffffu) return fail(G4_EINVAL, "attnPrefill: too much work");
     size_t off = 0;
     L->table = off;
     off += align256(n * sizeof(PrefillEntryDev));
     L->work = off;
     off += align256(work->size() * sizeof(PrefillWorkDev));
+    L->lists = off;
+    off += align256(lists->size() * sizeof(uint32_t));
     L->merge = off;
     off += align256(merge->size() * sizeof(DecodeEntryDev));
     L->vtc = off;  // the four tables are contiguous: prepare uploads them in one copy
@@ -1124,11 +1182,12 @@ int g4_attn_prefill_workspace_size(const g4_prefill_entry* entries, uint32_t n_e
     if (rc) return rc;
     std::vector<PrefillEntryDev> tab;
     std::vector<PrefillWorkDev> work;
+    std::vector<uint32_t> lists;
     std::vector<DecodeEntryDev> merge;
     uint32_t mp;
     Layout L;
     VtPlan vp;
-    rc = build(entries, n_entries, num_q_heads, num_kv_heads, head_dim, &tab, &work, &merge, &mp, &L, &vp);
+    rc = build(entries, n_entries, num_q_heads, num_kv_heads, head_dim, &tab, &work, &lists, &merge, &mp, &L, &vp);
     if (rc) return rc;
     *bytes = L.total;
     return G4_OK;
@@ -1142,11 +1201,12 @@ int g4_attn_prefill_prepare(const g4_prefill_entry* entries, uint32_t n_entries,
     if (!plan) return fail(G4_EINVAL, "attnPrefill: plan is NULL");
     std::vector<PrefillEntryDev> tab;
     std::vector<PrefillWorkDev> work;
+    std::vector<uint32_t> lists;
     std::vector<DecodeEntryDev> merge;
     uint32_t max_parts;
     Layout L;
     VtPlan vp;
-    rc = build(entries, n_entries, num_q_heads, num_kv_heads, head_dim, &tab, &work, &merge, &max_parts, &L, &vp);
+    rc = build(entries, n_entries, num_q_heads, num_kv_heads, head_dim, &tab, &work, &lists, &merge, &max_parts, &L, &vp);
     if (rc) return rc;
     if (max_parts > 8192) return fail(G4_EINVAL, "attnPrefill: %u key parts per tile (max 8192)", max_parts);
     if (!workspace || workspace_bytes < L.total)
@@ -1163,6 +1223,7 @@ int g4_attn_prefill_prepare(const g4_prefill_entry* entries, uint32_t n_entries,
     std::vector<char> blob(L.vtc - L.table + vtc.size() * sizeof(VtCacheDev));
     memcpy(blob.data(), tab.data(), tab.size() * sizeof(PrefillEntryDev));
     memcpy(blob.data() + (L.work - L.table), work.data(), work.size() * sizeof(PrefillWorkDev));
+    memcpy(blob.data() + (L.lists - L.table), lists.data(), lists.size() * sizeof(uint32_t));
     if (!merge.empty()) memcpy(blob.data() + (L.merge - L.table), merge.data(), merge.size() * sizeof(DecodeEntryDev));
     if (!vtc.empty()) memcpy(blob.data() + (L.vtc - L.table), vtc.data(), vtc.size() * sizeof(VtCacheDev));
     rc = stage_upload(ws + L.table, blob.data(), blob.size(), st);  // the four tables in one copy
@@ -1178,6 +1239,7 @@ int g4_attn_prefill_prepare(const g4_prefill_entry* entries, uint32_t n_entries,
     r.head_dim = (uint16_t)head_dim;
     r.magic = kPrefillMagic;
     r.off_work = (uint32_t)L.work;
+    r.n_lists = (uint16_t)(lists.size() - 1);
     r.off_merge = (uint32_t)L.merge;
     r.off_ml = (uint32_t)L.ml;
     r.off_o = (uint32_t)L.o;
@@ -1197,6 +1259,7 @@ static int prefill_run(const g4_decode_plan* plan, void* stream, hipEvent_t star
     PrefillArgs a = {};
     a.table = reinterpret_cast<const PrefillEntryDev*>(r.ws);
     a.work = reinterpret_cast<const PrefillWorkDev*>(r.ws + r.off_work);
+    a.lists = reinterpret_cast<const uint32_t*>(r.ws + r.off_work + align256((size_t)r.n_work * sizeof(PrefillWorkDev)));
     a.num_q_heads = r.num_q_heads;
     a.num_kv_heads = r.num_kv_heads;
     a.group = r.num_q_heads / r.num_kv_heads;
@@ -1213,7 +1276,7 @@ static int prefill_run(const g4_decode_plan* plan, void* stream, hipEvent_t star
             G4_LAUNCH(k_vt_blocks<256>, vgrid, dim3(256), 0, st, vtc, r.n_vtc, (uint32_t)r.num_kv_heads);
         G4_CHECK_LAUNCH("attnPrefill (V^T blocks)");
     }
-    const dim3 grid(r.n_work, r.num_kv_heads, r.head_dim / 256);
+    const dim3 grid(r.n_lists, r.num_kv_heads, r.head_dim / 256);
     if (hd512) {  // grid z: the row half of each work item's query tile
         if (start_ev || stop_ev)
             hipExtLaunchKernelGGL(k_prefill_pp512, grid, dim3(6 * 64), 0, st, start_ev, stop_ev, 0, a);
