@@ -91,10 +91,12 @@ struct PrefillWorkDev {
     uint32_t pad;
 };
 
+// The kernels' scalars and record pointers. The plan's tables (entries, work
+// items, lists: list l is work[lists[l] .. lists[l + 1])) come as kernel
+// arguments of their own, declared __restrict__: nothing the kernel stores
+// aliases them, so their loads stay scalar loads after an item's stores (a
+// vector load's wait would also wait for those stores).
 struct PrefillArgs {
-    const PrefillEntryDev* table;
-    const PrefillWorkDev* work;
-    const uint32_t* lists;  // [n_lists + 1]: list l is work[lists[l] .. lists[l + 1])
     uint32_t num_q_heads;
     uint32_t num_kv_heads;
     uint32_t group;
@@ -186,6 +188,47 @@ __device__ __forceinline__ void vm_wait_barrier() {
     asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
+// An output wave's 32 q-rows of 256 f32 columns to global memory, 512
+// contiguous bytes per row and store instruction. Accumulator block b of lane
+// (col, half) holds columns 32 b + 8 g + 4 half + 0..3 of q-row col in
+// acc[b][4 g .. 4 g + 3]; stored in that layout, an instruction writes 32-byte
+// pieces of 32 rows, and issuing an item's stores took ~7 us under the other
+// CUs' tile traffic (~5 us this way). The columns go through 16 KiB of LDS in
+// two rounds of 128 (blocks 4k .. 4k + 3, whose registers are then free; row
+// r's 16-byte chunk C at r * 512 + 16 (C ^ (r % 16)): sixteen rows per sixteen
+// lanes when written, sixteen chunks of one row when read, distinct banks both
+// ways); each store instruction then writes rows r (lanes 0-31) and r + 16
+// (lanes 32-63). Rows r < n_live go to row_ptr(r); `scale` multiplies every
+// value.
+template <typename RowPtr>
+__device__ __forceinline__ void store_rows(const f32x16 (&acc)[8], float scale, unsigned char* lds, int lane,
+                                           unsigned n_live, RowPtr row_ptr) {
+    const unsigned col = (unsigned)lane & 31u, half = (unsigned)lane >> 5;
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+#pragma unroll
+        for (int b = 0; b < 4; b++)
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const f32x16& x = acc[4 * k + b];
+                const unsigned c = 8u * b + 2u * g + half;
+                *reinterpret_cast<f32x4*>(lds + col * 512u + ((c ^ (col & 15u)) << 4)) =
+                    f32x4{x[4 * g] * scale, x[4 * g + 1] * scale, x[4 * g + 2] * scale, x[4 * g + 3] * scale};
+            }
+#pragma unroll 1
+        for (unsigned r0 = 0; r0 < 16; r0 += 4) {  // four row pairs at a time (bounds the registers in flight)
+            f32x4 v[4];
+#pragma unroll
+            for (unsigned r = r0; r < r0 + 4; r++)
+                v[r - r0] = *reinterpret_cast<const f32x4*>(lds + (r + 16 * half) * 512u + ((col ^ r) << 4));
+#pragma unroll
+            for (unsigned r = r0; r < r0 + 4; r++)
+                if (r + 16 * half < n_live) stg<f32x4>(row_ptr(r + 16 * half) + 128 * k + 4 * col, v[r - r0]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+}
+
 // lds_dma16_s for a kernel in which the compiler itself never uses M0 (checked
 // in the assembly of k_prefill_pp: its only M0 writes are these): M0 is set
 // and left, two scalar instructions fewer per DMA than saving and restoring it.
@@ -197,12 +240,13 @@ __device__ __forceinline__ void lds_dma16_m0(uint32_t voff, const void* sbase, u
 #pragma clang diagnostic pop
 
 // One work item: the body of k_prefill_pp's loop.
-__device__ __forceinline__ void prefill_pp_item(const PrefillArgs& a, const PrefillWorkDev wk, PrefillPpSmem& sm) {
+__device__ __forceinline__ void prefill_pp_item(const PrefillArgs& a, const PrefillEntryDev* __restrict__ table,
+                                                const PrefillWorkDev wk, PrefillPpSmem& sm) {
     constexpr int HD = 256;
     constexpr unsigned SM = kPpStages - 1;                       // stage of tile t: t & SM
     constexpr int NQ = HD / 16, KPER = HD / 64, PER = KPER + 4;  // score steps; K and all DMAs per tile and score wave
     constexpr int R = 3;                                         // LDS operand reads ahead of their MFMA
-    const PrefillEntryDev& ent = a.table[wk.entry];
+    const PrefillEntryDev& ent = table[wk.entry];
     const unsigned kvh = wg_y();
     const unsigned G = a.group, NQH = a.num_q_heads, NKH = a.num_kv_heads;
     const int lane = tid_x() & 63;
@@ -519,32 +563,34 @@ __device__ __forceinline__ void prefill_pp_item(const PrefillArgs& a, const Pref
         lds_barrier();
         output(it);
     }
-    lds_barrier();  // (m, l) of every row are in LDS
+    // (m, l) of every row are in LDS, and every read of this item's tiles is done. Until the next
+    // item's barrier 2, its DMAs write only K stages 0-2 and V^T stage 0: the output waves pass
+    // their rows through K stage 3 and V^T stages 1-3.
+    lds_barrier();
     const float m_fin = sm.ml[pair][0][lane];
     const float L = sm.ml[pair][1][lane];
-    if (!row_live) return;
-    const uint64_t qrow = (uint64_t)tok * NQH + kvh * G + head;
+    const unsigned rho0 = (unsigned)wk.tile * kPfRows + (unsigned)pair * 32u;  // the wave's first q-row
+    const int live = (int)(ent.n_tokens * G) - (int)rho0;
+    const unsigned n_live = live <= 0 ? 0u : live >= 32 ? 32u : (unsigned)live;
+    const unsigned gs = (unsigned)__builtin_ctz(G);  // G divides 32: row r is head r % G of token tok0 + r / G
+    const unsigned tok0 = rho0 >> gs;
+    unsigned char* lds = pair == 0 ? sm.k[kPpStages - 1] : sm.vt[pair];
     if (wk.n_parts == 1) {
-        float* dst = ent.out + qrow * HD + 4 * half;
-        const float inv = 1.0f / L;
-#pragma unroll
-        for (int b = 0; b < 8; b++)
-#pragma unroll
-            for (int g = 0; g < 4; g++)
-                stg<f32x4>(dst + 32 * b + 8 * g, f32x4{acc[b][4 * g] * inv, acc[b][4 * g + 1] * inv,
-                                                      acc[b][4 * g + 2] * inv, acc[b][4 * g + 3] * inv});
+        float* out = ent.out + (uint64_t)kvh * G * HD;
+        store_rows(acc, 1.0f / L, lds, lane, n_live, [&](unsigned r) __attribute__((always_inline)) {
+            return out + ((uint64_t)(tok0 + (r >> gs)) * NQH + (r & (G - 1))) * HD;
+        });
         return;
     }
     const unsigned tile_tok0 = (unsigned)wk.tile * kPfRows / G;
-    const uint64_t slot = (uint64_t)wk.split_base + (uint64_t)(tok - tile_tok0) * wk.n_parts + wk.part;
-    const uint64_t rec = (slot * NKH + kvh) * G + head;
-    float* po = a.part_o + rec * HD + 4 * half;
-#pragma unroll
-    for (int b = 0; b < 8; b++)
-#pragma unroll
-        for (int g = 0; g < 4; g++)
-            stg<f32x4>(po + 32 * b + 8 * g, f32x4{acc[b][4 * g], acc[b][4 * g + 1], acc[b][4 * g + 2], acc[b][4 * g + 3]});
-    if (half == 0) stg<f32x2>(a.part_ml + rec * 2, f32x2{m_fin, L});
+    const uint64_t slot0 = (uint64_t)wk.split_base + (uint64_t)(tok0 - tile_tok0) * wk.n_parts + wk.part;
+    store_rows(acc, 1.0f, lds, lane, n_live, [&](unsigned r) __attribute__((always_inline)) {
+        return a.part_o + (((slot0 + (uint64_t)(r >> gs) * wk.n_parts) * NKH + kvh) * G + (r & (G - 1))) * HD;
+    });
+    if (row_live && half == 0) {
+        const uint64_t slot = (uint64_t)wk.split_base + (uint64_t)(tok - tile_tok0) * wk.n_parts + wk.part;
+        stg<f32x2>(a.part_ml + ((slot * NKH + kvh) * G + head) * 2, f32x2{m_fin, L});
+    }
 }
 
 // A workgroup runs the work items of its list (lists[l] .. lists[l + 1] of the
@@ -552,11 +598,14 @@ __device__ __forceinline__ void prefill_pp_item(const PrefillArgs& a, const Pref
 // after the other: the output waves' stores of an item drain while the score
 // waves load the next item's q and first tiles, and no workgroup is launched
 // per item. Grid: the lists x kv heads.
-__global__ __launch_bounds__(512, 1) void k_prefill_pp(PrefillArgs a) {
+__global__ __launch_bounds__(512, 1) void k_prefill_pp(PrefillArgs a, const PrefillEntryDev* __restrict__ table,
+                                                      const PrefillWorkDev* __restrict__ work,
+                                                      const uint32_t* __restrict__ lists) {
     __shared__ PrefillPpSmem sm;
     const unsigned l = wg_x();
-    const unsigned i1 = a.lists[l + 1];
-    for (unsigned i = a.lists[l]; i < i1; i++) prefill_pp_item(a, a.work[i], sm);
+    const unsigned i1 = lists[l + 1];
+    for (unsigned i = lists[l]; i < i1; i++)  // i is uniform; the item's early exits hide that
+        prefill_pp_item(a, table, work[__builtin_amdgcn_readfirstlane(i)], sm);
 }
 
 // ---- head_dim 512: shared scores, six waves -----------------------------------
@@ -593,12 +642,12 @@ __device__ __forceinline__ void vm_barrier() {
 }
 
 // One work item's row half zh: the body of k_prefill_pp512's loop.
-__device__ __forceinline__ void prefill_pp512_item(const PrefillArgs& a, const PrefillWorkDev wk, unsigned zh,
-                                                   PrefillPp512Smem& sm) {
+__device__ __forceinline__ void prefill_pp512_item(const PrefillArgs& a, const PrefillEntryDev* __restrict__ table,
+                                                   const PrefillWorkDev wk, unsigned zh, PrefillPp512Smem& sm) {
     constexpr int HD = 512;
     constexpr int NQ = HD / 16;  // score steps
     constexpr int R = 3;         // LDS operand reads ahead of their MFMA
-    const PrefillEntryDev& ent = a.table[wk.entry];
+    const PrefillEntryDev& ent = table[wk.entry];
     const unsigned kvh = wg_y();
     const unsigned G = a.group, NQH = a.num_q_heads, NKH = a.num_kv_heads;
     const int lane = tid_x() & 63;
@@ -879,32 +928,35 @@ __device__ __forceinline__ void prefill_pp512_item(const PrefillArgs& a, const P
         vm_barrier();
         output(it);
     }
-    lds_barrier();  // (m, l) of every row are in LDS
+    // (m, l) of every row are in LDS, and every read of this item's tiles is done. Until the next
+    // item's barrier 1, its DMAs write only K stage 0: the output waves pass their rows through
+    // K stage 1 (half 0) and V^T stage 1 (half 1), 16 KiB per wave.
+    lds_barrier();
     const float m_fin = sm.ml[sw][0][lane];
     const float L = sm.ml[sw][1][lane];
-    if (!row_live) return;
-    const uint64_t qrow = (uint64_t)tok * NQH + kvh * G + head;
+    const unsigned rho0 = (unsigned)wk.tile * kPfRows + 64u * zh + (unsigned)sw * 32u;  // the wave's first q-row
+    const int live = (int)(ent.n_tokens * G) - (int)rho0;
+    const unsigned n_live = live <= 0 ? 0u : live >= 32 ? 32u : (unsigned)live;
+    const unsigned gs = (unsigned)__builtin_ctz(G);  // G divides 32: row r is head r % G of token tok0 + r / G
+    const unsigned tok0 = rho0 >> gs;
+    unsigned char* lds = (dh == 0 ? sm.k[1] : sm.vt[1]) + 16384u * (unsigned)sw;
     if (wk.n_parts == 1) {
-        float* dst = ent.out + qrow * HD + 256u * dh + 4 * half;
-        const float inv = 1.0f / L;
-#pragma unroll
-        for (int b = 0; b < 8; b++)
-#pragma unroll
-            for (int g = 0; g < 4; g++)
-                stg<f32x4>(dst + 32 * b + 8 * g, f32x4{acc[b][4 * g] * inv, acc[b][4 * g + 1] * inv,
-                                                      acc[b][4 * g + 2] * inv, acc[b][4 * g + 3] * inv});
+        float* out = ent.out + (uint64_t)kvh * G * HD + 256u * dh;
+        store_rows(acc, 1.0f / L, lds, lane, n_live, [&](unsigned r) __attribute__((always_inline)) {
+            return out + ((uint64_t)(tok0 + (r >> gs)) * NQH + (r & (G - 1))) * HD;
+        });
         return;
     }
     const unsigned tile_tok0 = (unsigned)wk.tile * kPfRows / G;
-    const uint64_t slot = (uint64_t)wk.split_base + (uint64_t)(tok - tile_tok0) * wk.n_parts + wk.part;
-    const uint64_t rec = (slot * NKH + kvh) * G + head;
-    float* po = a.part_o + rec * HD + 256u * dh + 4 * half;
-#pragma unroll
-    for (int b = 0; b < 8; b++)
-#pragma unroll
-        for (int g = 0; g < 4; g++)
-            stg<f32x4>(po + 32 * b + 8 * g, f32x4{acc[b][4 * g], acc[b][4 * g + 1], acc[b][4 * g + 2], acc[b][4 * g + 3]});
-    if (half == 0 && dh == 0) stg<f32x2>(a.part_ml + rec * 2, f32x2{m_fin, L});
+    const uint64_t slot0 = (uint64_t)wk.split_base + (uint64_t)(tok0 - tile_tok0) * wk.n_parts + wk.part;
+    store_rows(acc, 1.0f, lds, lane, n_live, [&](unsigned r) __attribute__((always_inline)) {
+        return a.part_o + (((slot0 + (uint64_t)(r >> gs) * wk.n_parts) * NKH + kvh) * G + (r & (G - 1))) * HD +
+               256u * dh;
+    });
+    if (row_live && half == 0 && dh == 0) {
+        const uint64_t slot = (uint64_t)wk.split_base + (uint64_t)(tok - tile_tok0) * wk.n_parts + wk.part;
+        stg<f32x2>(a.part_ml + ((slot * NKH + kvh) * G + head) * 2, f32x2{m_fin, L});
+    }
 }
 
 // A workgroup runs the work items of its list (lists[l] .. lists[l + 1] of the
@@ -912,11 +964,14 @@ __device__ __forceinline__ void prefill_pp512_item(const PrefillArgs& a, const P
 // after the other, so that an item's result stores drain while the next item's
 // q and first tiles load, and no workgroup is launched per item. Grid: the
 // lists x kv heads x the two row halves.
-__global__ __launch_bounds__(384, 1) void k_prefill_pp512(PrefillArgs a) {
+__global__ __launch_bounds__(384, 1) void k_prefill_pp512(PrefillArgs a, const PrefillEntryDev* __restrict__ table,
+                                                         const PrefillWorkDev* __restrict__ work,
+                                                         const uint32_t* __restrict__ lists) {
     __shared__ PrefillPp512Smem sm;
     const unsigned l = wg_x(), zh = wg_z();
-    const unsigned i1 = a.lists[l + 1];
-    for (unsigned i = a.lists[l]; i < i1; i++) prefill_pp512_item(a, a.work[i], zh, sm);
+    const unsigned i1 = lists[l + 1];
+    for (unsigned i = lists[l]; i < i1; i++)  // i is uniform; the item's early exits hide that
+        prefill_pp512_item(a, table, work[__builtin_amdgcn_readfirstlane(i)], zh, sm);
 }
 
 // V of one cache in 32-key blocks [kv head][block][HD][32] (f16): block j holds
@@ -1257,9 +1312,10 @@ static int prefill_run(const g4_decode_plan* plan, void* stream, hipEvent_t star
     memcpy(&r, plan, sizeof r);
     if (r.magic != kPrefillMagic) return fail(G4_EINVAL, "attnPrefill: plan was not prepared by g4_attn_prefill_prepare");
     PrefillArgs a = {};
-    a.table = reinterpret_cast<const PrefillEntryDev*>(r.ws);
-    a.work = reinterpret_cast<const PrefillWorkDev*>(r.ws + r.off_work);
-    a.lists = reinterpret_cast<const uint32_t*>(r.ws + r.off_work + align256((size_t)r.n_work * sizeof(PrefillWorkDev)));
+    const PrefillEntryDev* table = reinterpret_cast<const PrefillEntryDev*>(r.ws);
+    const PrefillWorkDev* work = reinterpret_cast<const PrefillWorkDev*>(r.ws + r.off_work);
+    const uint32_t* lists =
+        reinterpret_cast<const uint32_t*>(r.ws + r.off_work + align256((size_t)r.n_work * sizeof(PrefillWorkDev)));
     a.num_q_heads = r.num_q_heads;
     a.num_kv_heads = r.num_kv_heads;
     a.group = r.num_q_heads / r.num_kv_heads;
@@ -1279,13 +1335,15 @@ static int prefill_run(const g4_decode_plan* plan, void* stream, hipEvent_t star
     const dim3 grid(r.n_lists, r.num_kv_heads, r.head_dim / 256);
     if (hd512) {  // grid z: the row half of each work item's query tile
         if (start_ev || stop_ev)
-            hipExtLaunchKernelGGL(k_prefill_pp512, grid, dim3(6 * 64), 0, st, start_ev, stop_ev, 0, a);
+            hipExtLaunchKernelGGL(k_prefill_pp512, grid, dim3(6 * 64), 0, st, start_ev, stop_ev, 0, a, table, work,
+                                  lists);
         else
-            G4_LAUNCH(k_prefill_pp512, grid, dim3(6 * 64), 0, st, a);
+            G4_LAUNCH(k_prefill_pp512, grid, dim3(6 * 64), 0, st, a, table, work, lists);
     } else if (start_ev || stop_ev) {
-        hipExtLaunchKernelGGL(k_prefill_pp, grid, dim3(2 * kPfThreads), 0, st, start_ev, stop_ev, 0, a);
+        hipExtLaunchKernelGGL(k_prefill_pp, grid, dim3(2 * kPfThreads), 0, st, start_ev, stop_ev, 0, a, table, work,
+                              lists);
     } else {
-        G4_LAUNCH(k_prefill_pp, grid, dim3(2 * kPfThreads), 0, st, a);
+        G4_LAUNCH(k_prefill_pp, grid, dim3(2 * kPfThreads), 0, st, a, table, work, lists);
     }
     G4_CHECK_LAUNCH("attnPrefill");
     if (!r.n_merge) return G4_OK;
