@@ -1057,8 +1057,11 @@ struct Layout {
 };
 
 // The fixed cost of a work item (its first tiles' latency, the result
-// stores), in tiles, when items are spread over the workgroups' lists.
-constexpr uint64_t kPfItemCost = 10;
+// stores), in tiles, when items are spread over the workgroups' lists. A
+// later item of a list waits ~5 us for its first tiles and the previous
+// item's stores, the first one ~4 us; a tile takes ~1 us. Measured on
+// prefill4k: 6 -> 109-110 us, 8 -> 110-113, 10 -> 111-113, 13 -> 112-114.
+constexpr uint64_t kPfItemCost = 6;
 
 // The caches whose V the pipelined form transposes: one per distinct v_cache
 // of the entries without a V^T cache of their own, long enough for every
