@@ -150,7 +150,7 @@ __global__ __launch_bounds__(kWG) void k_prompt_prep(const float* __restrict__ q
     }
     __syncthreads();
     const unsigned lane = threadIdx.x & 63;
-    const unsigned wave = threadIdx.x >> 6;
+    const unsigned wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // slot stepping stays scalar
     const unsigned S = p.num_q_heads + (p.store_kv ? 2 * p.num_kv_heads : 0);
     const unsigned vt_blocks = (p.max_seq_len + 31) / 32;
     uint32_t wq[J], wk[J];  // the norm weights, loaded once per wave
@@ -167,22 +167,45 @@ __global__ __launch_bounds__(kWG) void k_prompt_prep(const float* __restrict__ q
         slot -= S;
         tt++;
     }
-    for (; tt < nt;) {  // uniform per wave
+    // Each row is requested one slot ahead, before the previous row's stores: a wait for a load
+    // also waits for every older vector memory operation, so a row requested after those stores
+    // would wait for them.
+    auto row_src = [&](unsigned tt_, unsigned slot_) __attribute__((always_inline)) {
+        const unsigned t_ = t0 + tt_;
+        const unsigned r_ = slot_ - p.num_q_heads;
+        return slot_ < p.num_q_heads ? q + ((uint64_t)t_ * p.num_q_heads + slot_) * HD
+                                     : (r_ < p.num_kv_heads ? k + ((uint64_t)t_ * p.num_kv_heads + r_) * HD
+                                                            : v + ((uint64_t)t_ * p.num_kv_heads + r_ - p.num_kv_heads) * HD);
+    };
+    if (tt >= nt) return;
+    float x[J];
+    {
+        const float* src = row_src(tt, slot);
+#pragma unroll
+        for (int j = 0; j < J; j++) x[j] = src[lane + 64 * j];
+    }
+    for (;;) {  // uniform per wave
+        unsigned tn = tt, sn = slot + kWG / 64;  // the wave's next slot
+        while (sn >= S) {  // uniform
+            sn -= S;
+            tn++;
+        }
+        const bool more = tn < nt;
+        float xn[J];
+        {  // unconditional (the last slot re-reads its own row), so the waits below count exactly
+            const float* src = more ? row_src(tn, sn) : row_src(tt, slot);
+#pragma unroll
+            for (int j = 0; j < J; j++) xn[j] = src[lane + 64 * j];
+        }
         const unsigned t = t0 + tt, pos = p.start + t;
         const bool is_q = slot < p.num_q_heads;
         const unsigned r = slot - p.num_q_heads;
         const bool is_k = !is_q && r < p.num_kv_heads;
         const bool rope = is_q || is_k;  // v: weightless norm only
         const unsigned h = is_q ? slot : (is_k ? r : r - p.num_kv_heads);
-        const float* src = is_q ? q + ((uint64_t)t * p.num_q_heads + h) * HD
-                                : (is_k ? k : v) + ((uint64_t)t * p.num_kv_heads + h) * HD;
-        float x[J];
         uint32_t wb[J];
 #pragma unroll
-        for (int j = 0; j < J; j++) {
-            x[j] = src[lane + 64 * j];
-            wb[j] = is_q ? wq[j] : wk[j];  // v: not used (weightless)
-        }
+        for (int j = 0; j < J; j++) wb[j] = is_q ? wq[j] : wk[j];  // v: not used (weightless)
         RopeLane<PJ> rl;
 #pragma unroll
         for (int pp = 0; pp < PJ; pp++) {
@@ -199,11 +222,11 @@ __global__ __launch_bounds__(kWG) void k_prompt_prep(const float* __restrict__ q
 #pragma unroll
             for (int j = 0; j < J; j++) vt[(lane + 64 * j) * 32] = f2h(x[j]);
         }
-        slot += kWG / 64;
-        while (slot >= S) {  // uniform
-            slot -= S;
-            tt++;
-        }
+        if (!more) break;
+        tt = tn;
+        slot = sn;
+#pragma unroll
+        for (int j = 0; j < J; j++) x[j] = xn[j];
     }
 }
 
