@@ -196,3 +196,40 @@ def test_prefill4k_bench_plan(dev, vt):
             assert err <= TOL, f"window {w} token {t}: max-abs {err}"
             worst = max(worst, err)
         print(f"prefill4k window={w}: {len(tokens)} tokens checked, worst err {worst:.2e}", flush=True)
+
+
+@pytest.mark.timeout(900)
+def test_prefill4k512_plan(dev):
+    """The head_dim 512 launch g4bench --workload prefill4k512 times: the global layer of the 4096-token
+    prompt alone (eight 512-token chunks, one launch), V from the V^T cache the prompt prep wrote. Its
+    256 work items (query tiles of 16 to 4096 keys, none split) fill the 128 workgroup lists of a
+    head_dim-512 launch (two workgroups per item) two each, so the lists' item loop and the rows passed
+    through LDS between items run at 512. Checked against the oracle's decode chain at the first 64
+    tokens, every 16th token, and the last 128 tokens."""
+    from g4attn import workloads
+
+    H5 = 512
+    announce("attnPrefill prefill4k global layer at head_dim 512 (8 entries, one launch)")
+    layers, entries, _ = workloads.prefill4k(dev, 8, 1, H5, windows=(0,))
+    arr = ops.make_prefill_entries(entries, 8, 1, H5)
+    ws = torch.empty(ops.prefill_workspace_bytes(arr, 8, 1, H5), dtype=torch.uint8, device=dev)
+    for _, _, _, out, _ in layers:
+        out.fill_(float("nan"))
+    plan = ops.attn_prefill_prepare(arr, 8, 1, H5, ws)
+    ops.attn_prefill_run(plan)
+    torch.cuda.synchronize()
+    T = workloads.PREFILL_T
+    tokens = sorted(set(range(64)) | set(range(T - 128, T)) | set(range(64, T - 128, 16)))
+    q, kc, vc, out, w = layers[0]
+    got = out.cpu().numpy().reshape(T, 8 * H5)
+    assert np.isfinite(got).all(), "non-finite output"
+    qf = orc.f16_bits_to_f32(q.cpu().numpy().view(np.uint16)).reshape(T, 8 * H5)
+    kf = orc.f16_bits_to_f32(kc.cpu().numpy().view(np.uint16)).reshape(T, H5)
+    vf = orc.f16_bits_to_f32(vc.cpu().numpy().view(np.uint16)).reshape(T, H5)
+    worst = 0.0
+    for t in tokens:
+        want = orc.attention_chain(qf[t], kf[:t + 1].reshape(-1), vf[:t + 1].reshape(-1), 8, 1, H5, t + 1, 1.0, 0)
+        err = max_abs(got[t], want)
+        assert err <= TOL, f"token {t}: max-abs {err}"
+        worst = max(worst, err)
+    print(f"prefill4k hd=512: {len(tokens)} tokens checked, worst err {worst:.2e}", flush=True)
