@@ -443,9 +443,11 @@ int g4_attn_step_prepare_layers(const g4_step_entry* entries, uint32_t n_layers,
  * at that position (attn_score.wgsl -> softmax.wgsl -> attn_output.wgsl)
  * within f32/f16 rounding. q is the post norm + RoPE query in f16; the
  * caches already hold the chunk's own K/V rows. Several entries (chunks,
- * layers, sequences) go in one launch. head_dim 256 or 512 (one per call;
- * 512 needs the default pipelined form), 32 % (num_q_heads / num_kv_heads)
- * == 0. */
+ * layers, sequences) go in one launch. head_dim 256 or 512 (one per call),
+ * 32 % (num_q_heads / num_kv_heads) == 0. The prepare splits long query tiles'
+ * key ranges into parts and spreads the work over one workgroup per CU;
+ * parts of a tile are merged by a second launch. A plan runs as often as
+ * wanted; runs on one workspace must not overlap. */
 typedef struct g4_prefill_entry {
     const uint16_t* q;        /* f16 [n_tokens][num_q_heads][head_dim] */
     const uint16_t* k_cache;  /* f16 [rows][num_kv_heads][head_dim], rows >= start + n_tokens */
