@@ -147,7 +147,7 @@ class CacheSet:
     """One complete set of per-entry buffers (caches, raw q/k/v projections, outputs) and the
     prepared one-launch steps over the entries (one per head_dim)."""
 
-    def __init__(self, spec, set_idx, dev, torch, ops, synth, e2b, extra_rows=0):
+    def __init__(self, spec, set_idx, dev, torch, ops, synth, e2b, extra_rows=0, pair=True):
         import numpy as np
 
         seed0 = spec["seed"] + 7919 * set_idx
@@ -193,9 +193,21 @@ class CacheSet:
             ws = torch.empty(ops.step_workspace_bytes(len(idx), NQH, NKH, hd), dtype=torch.uint8, device=dev)
             # [head_dim, entry indexes, ctypes entries, workspace, plan, tokens advanced since its prepare]
             self.groups.append([hd, idx, arr, ws, ops.attn_step_prepare(arr, NQH, NKH, hd, ws), 0])
+        # Two head_dims (E2B): both attention passes in one launch (g4_attn_step_run_pair), then each merge.
+        self.paired = pair and [g[0] for g in self.groups] == [256, 512]
+        self.launches = 1 if self.paired else len(self.groups)
         self.layer_plans = None
 
     def run(self, ops, ev=None):
+        if self.paired:
+            p256, p512 = self.groups[0][4], self.groups[1][4]
+            if ev is None:
+                ops.attn_step_run_pair(p512, p256)
+            else:
+                ops.attn_step_run_attention_pair_timed(p512, p256, ev[0][0], ev[0][1])
+                ops.attn_step_run_merge(p512)
+                ops.attn_step_run_merge(p256)
+            return
         for gi, (hd, idx, arr, ws, plan, _) in enumerate(self.groups):
             if ev is None:
                 ops.attn_step_run(plan)
@@ -325,12 +337,13 @@ def run_gpu(spec, args, decode_loop=False):
     loop_tokens = 2 * (args.warmup + args.steps) if decode_loop else 0  # two loops append rows
     log(f"workload {spec['name']}: {len(spec['layers'])} entries, {per_step / 1e6:.1f} MB/step, {sets} cache sets")
     t0 = time.time()
-    csets = [CacheSet(spec, s, dev, torch, ops, synth, e2b, extra_rows=loop_tokens) for s in range(sets)]
+    csets = [CacheSet(spec, s, dev, torch, ops, synth, e2b, extra_rows=loop_tokens, pair=args.pair)
+             for s in range(sets)]
     torch.cuda.synchronize()
     log(f"inputs ready in {time.time() - t0:.1f}s")
 
     stream = torch.cuda.current_stream()
-    n_groups = len(csets[0].groups)
+    n_groups = csets[0].launches
 
     def step(i, ev=None):
         csets[i % sets].run(ops, ev)
@@ -840,6 +853,8 @@ def main():
                     help="also time the layer-after-layer issue order (HIP graph)")
     ap.add_argument("--decode-loop", action=argparse.BooleanOptionalAction, default=True,
                     help="also time a position-advancing decode loop (prepare + run per token)")
+    ap.add_argument("--pair", action=argparse.BooleanOptionalAction, default=True,
+                    help="run a two-head_dim token's attention passes as one launch (E2B workloads)")
     ap.add_argument("--also", default=None,
                     help="a second decode workload reported nested in the same line (default: stack8k when the "
                          "workload is the default)")

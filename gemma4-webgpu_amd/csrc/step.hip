@@ -90,16 +90,14 @@ struct StepSmem {
 // factors are evaluated here from the inverse frequencies of the entry's set,
 // in f64 rounded to f32 as the host evaluates the prepared position's.
 template <int W, int HD>
-__global__ __launch_bounds__(64 * W, HD == 256 ? 8 / W : 1) void k_attn_step(
-    const StepWorkDev* __restrict__ work, float* part_ml, float* part_o, uint32_t num_kv_heads, uint32_t group,
-    uint32_t adv) {
+__device__ __forceinline__ void attn_step_body(const StepWorkDev* __restrict__ work, float* part_ml, float* part_o,
+                                               uint32_t num_kv_heads, uint32_t group, uint32_t adv, unsigned wg,
+                                               unsigned kvh, StepSmem<W, HD>& sm) {
     const StepArgs a{work, num_kv_heads, group, part_ml, part_o};
     using D = DecodeDims<HD>;
     constexpr int J = HD / 64;                          // elements of a head per lane
     constexpr int PJ = J / 2;                           // RoPE pairs per lane
     constexpr int kQPerWave = (kMaxGroup + W - 1) / W;  // query heads per wave
-    __shared__ StepSmem<W, HD> sm;
-    const unsigned kvh = blockIdx.y;
     const unsigned NKH = a.num_kv_heads;
     const unsigned G = a.group;
     const int lane = threadIdx.x & 63;
@@ -108,7 +106,7 @@ __global__ __launch_bounds__(64 * W, HD == 256 ? 8 / W : 1) void k_attn_step(
     const int g = lane >> 4;
     const bool lo_col = n >= 8;
 
-    const StepWorkDev wk = work[blockIdx.x];
+    const StepWorkDev wk = work[wg];
     const StepEntryDev& ent = wk.ent;
     const unsigned key_end = ent.key_end + adv;
     const unsigned position = ent.position + adv;
@@ -285,6 +283,36 @@ __global__ __launch_bounds__(64 * W, HD == 256 ? 8 / W : 1) void k_attn_step(
     }
     const uint64_t rec = ((uint64_t)wk.part * NKH + kvh) * G;
     wg_combine_write<HD>(sm.dec, G, false, nullptr, a.part_o + rec * HD, a.part_ml + rec * 2, em, ev);
+}
+
+template <int W, int HD>
+__global__ __launch_bounds__(64 * W, HD == 256 ? 8 / W : 1) void k_attn_step(
+    const StepWorkDev* __restrict__ work, float* part_ml, float* part_o, uint32_t num_kv_heads, uint32_t group,
+    uint32_t adv) {
+    __shared__ StepSmem<W, HD> sm;
+    attn_step_body<W, HD>(work, part_ml, part_o, num_kv_heads, group, adv, blockIdx.x, blockIdx.y, sm);
+}
+
+// Two plans of one token in one launch (E2B's two head_dim groups): the
+// head_dim-512 plan's workgroups first, one per CU, then the head_dim-256
+// plan's, in 4-wave workgroups of the same size, which take the CUs the first
+// ones leave as they finish. Grid: (wgs_a + wgs_b) x the larger kv-head count.
+union StepPairSmem {
+    StepSmem<4, 512> a;
+    StepSmem<4, 256> b;
+};
+
+__global__ __launch_bounds__(256, 1) void k_attn_step_pair(
+    const StepWorkDev* __restrict__ work_a, float* ml_a, float* o_a, uint32_t nkh_a, uint32_t group_a, uint32_t adv_a,
+    uint32_t wgs_a, const StepWorkDev* __restrict__ work_b, float* ml_b, float* o_b, uint32_t nkh_b, uint32_t group_b,
+    uint32_t adv_b) {
+    __shared__ StepPairSmem sm;
+    const unsigned x = blockIdx.x, y = blockIdx.y;
+    if (x < wgs_a) {  // uniform
+        if (y < nkh_a) attn_step_body<4, 512>(work_a, ml_a, o_a, nkh_a, group_a, adv_a, x, y, sm.a);
+    } else if (y < nkh_b) {
+        attn_step_body<4, 256>(work_b, ml_b, o_b, nkh_b, group_b, adv_b, x - wgs_a, y, sm.b);
+    }
 }
 
 }  // namespace g4
@@ -492,6 +520,59 @@ static int launch_attention(const g4_decode_plan* plan, void* stream, hipEvent_t
     }
     G4_CHECK_LAUNCH("attnStep");
     return G4_OK;
+}
+
+// The head_dim-512 and head_dim-256 plans of one token as one launch (k_attn_step_pair).
+static int launch_attention_pair(const g4_decode_plan* plan_1, const g4_decode_plan* plan_2, void* stream,
+                                 hipEvent_t start, hipEvent_t stop) {
+    StepPlanRep r1, r2;
+    int rc = step_plan(plan_1, &r1);
+    if (rc) return rc;
+    rc = step_plan(plan_2, &r2);
+    if (rc) return rc;
+    const StepPlanRep& a = r1.head_dim == 512 ? r1 : r2;
+    const StepPlanRep& b = r1.head_dim == 512 ? r2 : r1;
+    if (a.head_dim != 512 || b.head_dim != 256)
+        return fail(G4_EINVAL, "attnStepPair: needs one plan of head_dim 512 and one of 256 (got %u and %u)",
+                    r1.head_dim, r2.head_dim);
+    if (a.tables == b.tables) return fail(G4_EINVAL, "attnStepPair: the two plans share their tables");
+    auto ml = [](const StepPlanRep& r) { return reinterpret_cast<float*>(r.part_ml); };
+    auto po = [](const StepPlanRep& r) {
+        return reinterpret_cast<float*>(r.part_ml + step_part_o_offset(r.num_kv_heads, r.group));
+    };
+    const dim3 grid((uint32_t)a.n_wgs + b.n_wgs, std::max(a.num_kv_heads, b.num_kv_heads));
+    const StepWorkDev* wa = reinterpret_cast<const StepWorkDev*>(a.tables);
+    const StepWorkDev* wb = reinterpret_cast<const StepWorkDev*>(b.tables);
+    hipStream_t st = as_stream(stream);
+    if (start || stop)
+        hipExtLaunchKernelGGL(k_attn_step_pair, grid, dim3(256), 0, st, start, stop, 0, wa, ml(a), po(a),
+                              (uint32_t)a.num_kv_heads, (uint32_t)a.group, a.adv, (uint32_t)a.n_wgs, wb, ml(b), po(b),
+                              (uint32_t)b.num_kv_heads, (uint32_t)b.group, b.adv);
+    else
+        G4_LAUNCH(k_attn_step_pair, grid, dim3(256), 0, st, wa, ml(a), po(a), (uint32_t)a.num_kv_heads,
+                  (uint32_t)a.group, a.adv, (uint32_t)a.n_wgs, wb, ml(b), po(b), (uint32_t)b.num_kv_heads,
+                  (uint32_t)b.group, b.adv);
+    G4_CHECK_LAUNCH("attnStepPair");
+    return G4_OK;
+}
+
+int g4_attn_step_run_attention_pair(const g4_decode_plan* plan_1, const g4_decode_plan* plan_2, void* stream) {
+    return launch_attention_pair(plan_1, plan_2, stream, nullptr, nullptr);
+}
+
+int g4_attn_step_run_attention_pair_timed(const g4_decode_plan* plan_1, const g4_decode_plan* plan_2, void* stream,
+                                          void* start_event, void* stop_event) {
+    if (!start_event || !stop_event) return fail(G4_EINVAL, "attnStepPair: timing events are NULL");
+    return launch_attention_pair(plan_1, plan_2, stream, static_cast<hipEvent_t>(start_event),
+                                 static_cast<hipEvent_t>(stop_event));
+}
+
+int g4_attn_step_run_pair(const g4_decode_plan* plan_1, const g4_decode_plan* plan_2, void* stream) {
+    int rc = launch_attention_pair(plan_1, plan_2, stream, nullptr, nullptr);
+    if (rc) return rc;
+    rc = g4_attn_step_run_merge(plan_1, stream);
+    if (rc) return rc;
+    return g4_attn_step_run_merge(plan_2, stream);
 }
 
 int g4_attn_step_advance(g4_decode_plan* plan, uint32_t tokens) {

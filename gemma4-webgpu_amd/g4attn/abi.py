@@ -187,6 +187,9 @@ SIGNATURES: dict[str, list] = {
     "g4_attn_step_run_merge": [C.POINTER(DecodePlan), _P],
     "g4_attn_step_run_out": [C.POINTER(DecodePlan), C.POINTER(LinearSeg), _U32, _P],
     "g4_attn_step_run_attention_timed": [C.POINTER(DecodePlan), _P, _P, _P],
+    "g4_attn_step_run_attention_pair": [C.POINTER(DecodePlan), C.POINTER(DecodePlan), _P],
+    "g4_attn_step_run_attention_pair_timed": [C.POINTER(DecodePlan), C.POINTER(DecodePlan), _P, _P, _P],
+    "g4_attn_step_run_pair": [C.POINTER(DecodePlan), C.POINTER(DecodePlan), _P],
     "g4_attn_step": [C.POINTER(StepEntry), _U32, _U32, _U32, _U32, _P, _SZ, _P],
     "g4_attn_prefill_workspace_size": [C.POINTER(PrefillEntry), _U32, _U32, _U32, _U32, C.POINTER(C.c_size_t)],
     "g4_attn_prefill_prepare": [C.POINTER(PrefillEntry), _U32, _U32, _U32, _U32, _P, _SZ, C.POINTER(DecodePlan),

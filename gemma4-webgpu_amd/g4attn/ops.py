@@ -349,6 +349,25 @@ def attn_step_run_merge(plan: DecodePlan, stream=None):
     abi.call("g4_attn_step_run_merge", C.byref(plan), _stream(stream))
 
 
+def attn_step_run_pair(plan_1: DecodePlan, plan_2: DecodePlan, stream=None):
+    """A token's head_dim-512 and head_dim-256 plans (either order): both attention passes in one launch, then
+    each plan's merge."""
+    abi.call("g4_attn_step_run_pair", C.byref(plan_1), C.byref(plan_2), _stream(stream))
+
+
+def attn_step_run_attention_pair(plan_1: DecodePlan, plan_2: DecodePlan, stream=None):
+    abi.call("g4_attn_step_run_attention_pair", C.byref(plan_1), C.byref(plan_2), _stream(stream))
+
+
+def attn_step_run_attention_pair_timed(plan_1: DecodePlan, plan_2: DecodePlan, start, stop, stream=None):
+    """attn_step_run_attention_pair with torch.cuda.Events (timing enabled) around the one launch."""
+    for e, name in ((start, "start"), (stop, "stop")):
+        if not getattr(e, "cuda_event", 0):
+            raise ValueError(f"{name} event has no HIP event yet (record it once first)")
+    abi.call("g4_attn_step_run_attention_pair_timed", C.byref(plan_1), C.byref(plan_2), _stream(stream),
+             C.c_void_p(start.cuda_event), C.c_void_p(stop.cuda_event))
+
+
 def attn_step_run_out(plan: DecodePlan, n, segments, stream=None):
     """attn.linearOut after g4_attn_step_run_attention, with the step's merge folded in: one
     (weight f16 [rows][n], out f32 [rows], rows) segment per entry of the plan, n = num_q_heads * head_dim.

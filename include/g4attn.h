@@ -407,6 +407,22 @@ int g4_attn_step_run_merge(const g4_decode_plan* plan, void* stream);
  * g4_attn_step_run_attention with two hipEvent_t (created with timing enabled)
  * that record the kernel's own start and end. */
 int g4_attn_step_run_attention_timed(const g4_decode_plan* plan, void* stream, void* start_event, void* stop_event);
+/* A token of a model with two head_dims (E2B: 512 on the global layers, 256
+ * on the local ones) has one plan per head_dim. These run both plans' attention
+ * passes as one launch: the head_dim-512 plan's workgroups first, then the
+ * head_dim-256 plan's, which take the CUs the first ones leave (one launch and
+ * its start-up instead of two, and the short local layers in the long global
+ * ones' tail). The plans (either order) come from separate prepares with
+ * separate workspaces. Each plan's merge then runs as usual
+ * (g4_attn_step_run_merge); g4_attn_step_run_pair does all three. The
+ * head_dim-256 entries are computed by 4-wave workgroups whatever the plan's
+ * own form, so their results agree with g4_attn_step_run's to rounding, not
+ * bit for bit, when that plan took 8-wave workgroups. No counterpart in the
+ * reference (one dispatch per kernel per layer, src/engine.ts:2056-2095). */
+int g4_attn_step_run_attention_pair(const g4_decode_plan* plan_1, const g4_decode_plan* plan_2, void* stream);
+int g4_attn_step_run_attention_pair_timed(const g4_decode_plan* plan_1, const g4_decode_plan* plan_2, void* stream,
+                                          void* start_event, void* stop_event);
+int g4_attn_step_run_pair(const g4_decode_plan* plan_1, const g4_decode_plan* plan_2, void* stream);
 /* prepare + run. */
 int g4_attn_step(const g4_step_entry* entries, uint32_t n_entries, uint32_t num_q_heads, uint32_t num_kv_heads,
                  uint32_t head_dim, void* workspace, size_t workspace_bytes, void* stream);

@@ -16,7 +16,8 @@ import torch
 from conftest import announce
 from g4attn import e2b
 from helpers import max_abs
-from test_gpu_step import TOL, Layer, check, run_step
+from g4attn import ops
+from test_gpu_step import NKH, NQH, TOL, Layer, check, run_step
 
 pytestmark = pytest.mark.gpu
 
@@ -72,6 +73,54 @@ def test_e2b_token_two_launches(dev, seq):
             assert err <= TOL, f"consumer layer {il}: max-abs {err}"
             worst = max(worst, err)
     print(f"E2B stack seq={seq}: 35 layers checked, worst err {worst:.2e}", flush=True)
+
+
+@pytest.mark.timeout(900)
+@pytest.mark.parametrize("seq", [2049, 32769])
+def test_e2b_token_one_pair_launch(dev, seq):
+    """The same token with both head_dims' attention passes in one launch (g4_attn_step_run_pair): every
+    layer against the oracle as above, and three replays with the same bits."""
+    announce(f"E2B stack one token seq={seq}: both head_dims in one launch")
+    cfg, pmap, layers = build_stack(dev, seq, 41000 + seq)
+    plans = {}
+    for hd in (256, 512):
+        ents = entries_for(layers, pmap, hd, cfg)
+        arr = ops.make_step_entries(ents, NQH, NKH, hd)
+        ws = torch.empty(ops.step_workspace_bytes(len(ents), NQH, NKH, hd), dtype=torch.uint8, device=dev)
+        plans[hd] = (arr, ws, ops.attn_step_prepare(arr, NQH, NKH, hd, ws))
+    outs = []
+    for rep in range(3):
+        for L in layers:
+            L.out.fill_(float("nan"))
+        ops.attn_step_run_pair(plans[512][2], plans[256][2])
+        torch.cuda.synchronize()
+        outs.append(np.concatenate([L.out.cpu().numpy() for L in layers]).view(np.uint32))
+    np.testing.assert_array_equal(outs[0], outs[1])
+    np.testing.assert_array_equal(outs[0], outs[2])
+    worst = 0.0
+    for il, L in enumerate(layers):
+        if pmap[il] == il:
+            want, kb, vb = L.expected()
+            worst = max(worst, check(L, want, kb, vb, f"producer layer {il}"))
+        else:
+            want, _, _ = L.expected(kv_from=layers[pmap[il]])
+            got = L.out.cpu().numpy()
+            assert np.isfinite(got).all(), f"consumer layer {il}: non-finite output"
+            err = max_abs(got, want)
+            assert err <= TOL, f"consumer layer {il}: max-abs {err}"
+            worst = max(worst, err)
+    print(f"E2B stack seq={seq} (one launch): 35 layers checked, worst err {worst:.2e}", flush=True)
+
+
+def test_e2b_step_pair_refuses_bad_plans(dev):
+    """Two plans of one head_dim, or one plan twice, are refused before anything is enqueued."""
+    cfg, pmap, layers = build_stack(dev, 600, 42000)
+    ents = entries_for(layers, pmap, 256, cfg)
+    arr = ops.make_step_entries(ents, NQH, NKH, 256)
+    ws = torch.empty(ops.step_workspace_bytes(len(ents), NQH, NKH, 256), dtype=torch.uint8, device=dev)
+    p256 = ops.attn_step_prepare(arr, NQH, NKH, 256, ws)
+    with pytest.raises(RuntimeError, match="head_dim 512 and one of 256"):
+        ops.attn_step_run_pair(p256, p256)
 
 
 def test_e2b_token_engine_order(dev):
