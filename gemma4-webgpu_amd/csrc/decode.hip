@@ -133,8 +133,8 @@ constexpr unsigned kMaxMergeChunks = 16;
 // passed by value when there is no table.
 
 __device__ __forceinline__ DecodeEntryDev merge_entry(const DecodeEntryDev* table, float* one_out,
-                                                      uint32_t one_split_base, uint32_t one_splits) {
-    if (table) return table[blockIdx.x];
+                                                      uint32_t one_split_base, uint32_t one_splits, unsigned bx) {
+    if (table) return table[bx];
     DecodeEntryDev e{};
     e.out = one_out;
     e.split_base = one_split_base;
@@ -142,14 +142,15 @@ __device__ __forceinline__ DecodeEntryDev merge_entry(const DecodeEntryDev* tabl
     return e;
 }
 
+// One workgroup (entry bx, query head by of its kv head, column chunk bz) of k_decode_merge.
 template <int HD>
-__global__ __launch_bounds__(kMergeThreads) void k_decode_merge(const DecodeEntryDev* __restrict__ table, float* one_out,
-                                                                uint32_t one_split_base, uint32_t one_splits,
-                                                                float* part_ml, float* part_o, uint32_t num_kv_heads,
-                                                                uint32_t group, uint32_t n_chunks) {
+__device__ __forceinline__ void merge_body(const DecodeEntryDev* __restrict__ table, float* one_out,
+                                           uint32_t one_split_base, uint32_t one_splits, float* part_ml,
+                                           float* part_o, uint32_t num_kv_heads, uint32_t group, uint32_t n_chunks,
+                                           unsigned bx, unsigned by, unsigned bz) {
     __shared__ f32x4 part[kMergeThreads];
     __shared__ float gm[kMergeThreads], gl[kMergeThreads];  // per group: running max, rescaled l
-    const DecodeEntryDev ent = merge_entry(table, one_out, one_split_base, one_splits);
+    const DecodeEntryDev ent = merge_entry(table, one_out, one_split_base, one_splits, bx);
     DecodeArgs a{};
     a.num_kv_heads = num_kv_heads;
     a.group = group;
@@ -158,11 +159,11 @@ __global__ __launch_bounds__(kMergeThreads) void k_decode_merge(const DecodeEntr
     const unsigned ns = ent.n_splits;
     if (ns <= 1) return;
     const unsigned G = a.group;
-    const unsigned kvh = blockIdx.y / G, h = blockIdx.y % G;
+    const unsigned kvh = by / G, h = by % G;
     const unsigned t = threadIdx.x;
     const unsigned dc = HD / n_chunks, R = dc / 4, P = kMergeThreads / R;
     const unsigned grp = t / R, q = t % R;
-    const unsigned d = blockIdx.z * dc + q * 4;
+    const unsigned d = bz * dc + q * 4;
     const uint64_t rec_stride = (uint64_t)a.num_kv_heads * G;  // partial records per split
     const uint64_t rec0 = ((uint64_t)ent.split_base * a.num_kv_heads + kvh) * G + h;
     const float* o = a.part_o + rec0 * HD + d;
@@ -219,6 +220,15 @@ __global__ __launch_bounds__(kMergeThreads) void k_decode_merge(const DecodeEntr
     }
 }
 
+template <int HD>
+__global__ __launch_bounds__(kMergeThreads) void k_decode_merge(const DecodeEntryDev* __restrict__ table, float* one_out,
+                                                                uint32_t one_split_base, uint32_t one_splits,
+                                                                float* part_ml, float* part_o, uint32_t num_kv_heads,
+                                                                uint32_t group, uint32_t n_chunks) {
+    merge_body<HD>(table, one_out, one_split_base, one_splits, part_ml, part_o, num_kv_heads, group, n_chunks,
+                   blockIdx.x, blockIdx.y, blockIdx.z);
+}
+
 // The same merge for entries of at most kSmallMergeSplits records: one
 // workgroup per (entry, kv head) covers all G query heads (256 / G threads per
 // head, COLS = G * HD / 256 columns per thread), so a merge of many entries
@@ -272,16 +282,15 @@ __device__ __forceinline__ void merge_small_fold(const f32x4 (&v)[NS][COLS / 4],
 // NS: the launch's largest split count rounded up to 2, 4 or 8 (records past an entry's own count
 // are not loaded).
 template <int HD, int COLS, int NS>
-__global__ __launch_bounds__(kMergeThreads) void k_decode_merge_small(const DecodeEntryDev* __restrict__ table,
-                                                                      float* one_out, uint32_t one_split_base,
-                                                                      uint32_t one_splits, float* part_ml,
-                                                                      float* part_o, uint32_t num_kv_heads,
-                                                                      uint32_t group) {
+__device__ __forceinline__ void merge_small_body(const DecodeEntryDev* __restrict__ table, float* one_out,
+                                                 uint32_t one_split_base, uint32_t one_splits, float* part_ml,
+                                                 float* part_o, uint32_t num_kv_heads, uint32_t group, unsigned bx,
+                                                 unsigned by) {
     constexpr unsigned TPH = HD / COLS;  // threads per query head
-    const DecodeEntryDev ent = merge_entry(table, one_out, one_split_base, one_splits);
+    const DecodeEntryDev ent = merge_entry(table, one_out, one_split_base, one_splits, bx);
     const unsigned ns = ent.n_splits;
     if (ns <= 1) return;
-    const unsigned G = group, kvh = blockIdx.y;
+    const unsigned G = group, kvh = by;
     const unsigned h = threadIdx.x / TPH, d = (threadIdx.x % TPH) * COLS;
     if (h >= G) return;
     const uint64_t rec_stride = (uint64_t)num_kv_heads * G;  // partial records per split
@@ -294,6 +303,38 @@ __global__ __launch_bounds__(kMergeThreads) void k_decode_merge_small(const Deco
     float* out = ent.out + ((uint64_t)kvh * G + h) * HD + d;
 #pragma unroll
     for (int c = 0; c < COLS / 4; c++) stg<f32x4>(out + 4 * c, res[c]);
+}
+
+template <int HD, int COLS, int NS>
+__global__ __launch_bounds__(kMergeThreads) void k_decode_merge_small(const DecodeEntryDev* __restrict__ table,
+                                                                      float* one_out, uint32_t one_split_base,
+                                                                      uint32_t one_splits, float* part_ml,
+                                                                      float* part_o, uint32_t num_kv_heads,
+                                                                      uint32_t group) {
+    merge_small_body<HD, COLS, NS>(table, one_out, one_split_base, one_splits, part_ml, part_o, num_kv_heads, group,
+                                   blockIdx.x, blockIdx.y);
+}
+
+// The merges of two step plans of one token in one launch (E2B's head_dim-512
+// plan with many parts per entry, then its head_dim-256 plan with at most
+// kSmallMergeSplits): workgroups 0 .. n_a - 1 are k_decode_merge<512>'s
+// (entry, query head, chunk), the rest k_decode_merge_small<256, COLS, NS>'s
+// (entry, kv head); the same arithmetic, so the same bits as the two launches.
+template <int COLS, int NS>
+__global__ __launch_bounds__(kMergeThreads) void k_decode_merge_pair(
+    const DecodeEntryDev* __restrict__ table_a, float* ml_a, float* o_a, uint32_t nkh_a, uint32_t group_a,
+    uint32_t ents_a, uint32_t chunks_a, const DecodeEntryDev* __restrict__ table_b, float* ml_b, float* o_b,
+    uint32_t nkh_b, uint32_t group_b, uint32_t ents_b) {
+    const unsigned heads_a = nkh_a * group_a, n_a = ents_a * heads_a * chunks_a;
+    unsigned x = blockIdx.x;
+    if (x < n_a) {  // uniform
+        const unsigned e = x % ents_a;
+        x /= ents_a;
+        merge_body<512>(table_a, nullptr, 0, 0, ml_a, o_a, nkh_a, group_a, chunks_a, e, x % heads_a, x / heads_a);
+    } else {
+        x -= n_a;
+        merge_small_body<256, COLS, NS>(table_b, nullptr, 0, 0, ml_b, o_b, nkh_b, group_b, x % ents_b, x / ents_b);
+    }
 }
 
 #define MERGE_KARGS                                                                                               \
@@ -337,6 +378,38 @@ int launch_decode_merge_hd(const DecodeArgs& a, unsigned n_entries, unsigned max
 }
 
 #undef MERGE_KARGS
+
+int launch_decode_merge_pair(const DecodeArgs& a, unsigned n_a, unsigned max_a, const DecodeArgs& b, unsigned n_b,
+                             unsigned max_b, hipStream_t st) {
+    if (!n_a || max_a <= kSmallMergeSplits || max_a > (unsigned)kMaxMergeSplits) return 1;
+    if (!n_b || max_b <= 1 || max_b > kSmallMergeSplits || (b.group != 8 && b.group != 4)) return 1;
+    constexpr unsigned kRecsPerChunk = kMergeBatch * 4 * kMergeThreads / 512;  // as launch_decode_merge_hd<512>
+    unsigned chunks = 1;
+    while (chunks < kMaxMergeChunks && max_a > kRecsPerChunk * chunks) chunks *= 2;
+    const uint64_t wgs = (uint64_t)n_a * a.num_kv_heads * a.group * chunks + (uint64_t)n_b * b.num_kv_heads;
+    if (wgs > 0x7fffffffu) return 1;
+    const dim3 grid((uint32_t)wgs), block(kMergeThreads);
+#define PAIR_KARGS a.table, a.part_ml, a.part_o, a.num_kv_heads, a.group, n_a, chunks, b.table, b.part_ml, b.part_o, \
+                   b.num_kv_heads, b.group, n_b
+    if (b.group == 8) {
+        if (max_b <= 2)
+            G4_LAUNCH((k_decode_merge_pair<8, 2>), grid, block, 0, st, PAIR_KARGS);
+        else if (max_b <= 4)
+            G4_LAUNCH((k_decode_merge_pair<8, 4>), grid, block, 0, st, PAIR_KARGS);
+        else
+            G4_LAUNCH((k_decode_merge_pair<8, 8>), grid, block, 0, st, PAIR_KARGS);
+    } else {
+        if (max_b <= 2)
+            G4_LAUNCH((k_decode_merge_pair<4, 2>), grid, block, 0, st, PAIR_KARGS);
+        else if (max_b <= 4)
+            G4_LAUNCH((k_decode_merge_pair<4, 4>), grid, block, 0, st, PAIR_KARGS);
+        else
+            G4_LAUNCH((k_decode_merge_pair<4, 8>), grid, block, 0, st, PAIR_KARGS);
+    }
+#undef PAIR_KARGS
+    G4_CHECK_LAUNCH("attnStepPair merge");
+    return G4_OK;
+}
 
 int launch_decode_merge(const DecodeArgs& a, unsigned n_entries, unsigned max_splits, hipStream_t st,
                         unsigned head_dim) {

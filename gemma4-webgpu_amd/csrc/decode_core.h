@@ -111,6 +111,12 @@ struct DecodeArgs {
 // head_dim: 256 or 512.
 int launch_decode_merge(const DecodeArgs& a, unsigned n_entries, unsigned max_splits, hipStream_t st,
                         unsigned head_dim = 256);
+// The merges of a token's head_dim-512 step plan (a: more than 8 parts per
+// entry) and head_dim-256 plan (b: at most 8, group 4 or 8) in one launch, with
+// the bits of the two separate merges. Returns 1, launching nothing, when the
+// plans are not of those kinds.
+int launch_decode_merge_pair(const DecodeArgs& a, unsigned n_a, unsigned max_a, const DecodeArgs& b, unsigned n_b,
+                             unsigned max_b, hipStream_t st);
 
 // attn.linearOut over the entries of a decode step, with the step's merge
 // folded in (decode.hip): workgroup (x, e) merges entry e's partial records

@@ -567,9 +567,30 @@ int g4_attn_step_run_attention_pair_timed(const g4_decode_plan* plan_1, const g4
                                  static_cast<hipEvent_t>(stop_event));
 }
 
+static DecodeArgs merge_args(const StepPlanRep& r) {
+    DecodeArgs m = {};
+    m.table = reinterpret_cast<const DecodeEntryDev*>(r.tables + r.off_merge);
+    m.n_entries = r.n_merge;
+    m.num_kv_heads = r.num_kv_heads;
+    m.group = r.group;
+    m.part_ml = reinterpret_cast<float*>(r.part_ml);
+    m.part_o = reinterpret_cast<float*>(r.part_ml + step_part_o_offset(r.num_kv_heads, r.group));
+    return m;
+}
+
 int g4_attn_step_run_pair(const g4_decode_plan* plan_1, const g4_decode_plan* plan_2, void* stream) {
     int rc = launch_attention_pair(plan_1, plan_2, stream, nullptr, nullptr);
     if (rc) return rc;
+    // Both merges in one launch when the plans' merges are of the two kinds it takes (checked above:
+    // one plan per head_dim); otherwise one after the other.
+    StepPlanRep r1, r2;
+    memcpy(&r1, plan_1, sizeof r1);
+    memcpy(&r2, plan_2, sizeof r2);
+    const StepPlanRep& a = r1.head_dim == 512 ? r1 : r2;
+    const StepPlanRep& b = r1.head_dim == 512 ? r2 : r1;
+    rc = launch_decode_merge_pair(merge_args(a), a.n_merge, a.max_parts, merge_args(b), b.n_merge, b.max_parts,
+                                  as_stream(stream));
+    if (rc <= 0) return rc;
     rc = g4_attn_step_run_merge(plan_1, stream);
     if (rc) return rc;
     return g4_attn_step_run_merge(plan_2, stream);

@@ -78,8 +78,9 @@ def test_e2b_token_two_launches(dev, seq):
 @pytest.mark.timeout(900)
 @pytest.mark.parametrize("seq", [2049, 32769])
 def test_e2b_token_one_pair_launch(dev, seq):
-    """The same token with both head_dims' attention passes in one launch (g4_attn_step_run_pair): every
-    layer against the oracle as above, and three replays with the same bits."""
+    """The same token with both head_dims' attention passes in one launch and both merges in one
+    (g4_attn_step_run_pair): every layer against the oracle as above, three replays with the same bits, and
+    the same bits through the two plans' own merge launches."""
     announce(f"E2B stack one token seq={seq}: both head_dims in one launch")
     cfg, pmap, layers = build_stack(dev, seq, 41000 + seq)
     plans = {}
@@ -97,6 +98,14 @@ def test_e2b_token_one_pair_launch(dev, seq):
         outs.append(np.concatenate([L.out.cpu().numpy() for L in layers]).view(np.uint32))
     np.testing.assert_array_equal(outs[0], outs[1])
     np.testing.assert_array_equal(outs[0], outs[2])
+    # the one merge launch gives the bits of the two plans' own merges
+    for L in layers:
+        L.out.fill_(float("nan"))
+    ops.attn_step_run_attention_pair(plans[512][2], plans[256][2])
+    ops.attn_step_run_merge(plans[512][2])
+    ops.attn_step_run_merge(plans[256][2])
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(np.concatenate([L.out.cpu().numpy() for L in layers]).view(np.uint32), outs[0])
     worst = 0.0
     for il, L in enumerate(layers):
         if pmap[il] == il:
