@@ -1073,6 +1073,28 @@ napi_value AttnStepRun(napi_env env, napi_callback_info info) {
     return undefined(env);
 }
 
+// attnStepRunPair(plan1, plan2, stream): a token's head_dim-512 and head_dim-256 plans (either order) as one
+// attention launch and one merge launch (g4_attn_step_run_pair).
+napi_value AttnStepRunPair(napi_env env, napi_callback_info info) {
+    Args a(env, info, 3);  // plan1, plan2, stream
+    void* d1 = nullptr;
+    void* d2 = nullptr;
+    size_t n1 = 0, n2 = 0;
+    a.bytes(0, &d1, &n1);
+    a.bytes(1, &d2, &n2);
+    void* s = a.ptr(2);
+    if (!a.ok) return nullptr;
+    if (n1 != sizeof(g4_decode_plan) || n2 != sizeof(g4_decode_plan)) {
+        napi_throw_type_error(env, nullptr, "attnStepRunPair: not plans from attnStepPrepare");
+        return nullptr;
+    }
+    g4_decode_plan p1, p2;
+    memcpy(&p1, d1, sizeof p1);
+    memcpy(&p2, d2, sizeof p2);
+    CALL(env, g4_attn_step_run_pair(&p1, &p2, s));
+    return undefined(env);
+}
+
 // attnStepAdvance(plan, tokens): the prepared plan moves `tokens` decode steps ahead, in place (the
 // 64-byte array from attnStepPrepare / attnStepPrepareLayers); host only, nothing is enqueued.
 napi_value AttnStepAdvance(napi_env env, napi_callback_info info) {
@@ -1360,6 +1382,7 @@ napi_value Init(napi_env env, napi_value exports) {
         {"attnStepLayersWorkspaceSize", AttnStepLayersWorkspaceSize},
         {"attnStepPrepareLayers", AttnStepPrepareLayers},
         {"attnStepRun", AttnStepRun},
+        {"attnStepRunPair", AttnStepRunPair},
         {"attnStepAdvance", AttnStepAdvance},
         {"attnStepRunAttention", AttnStepRunAttention},
         {"attnStepRunOut", AttnStepRunOut},

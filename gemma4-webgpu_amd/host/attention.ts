@@ -323,6 +323,7 @@ export interface Addon {
   attnStepPrepareLayers(entries: any[], perLayer: number, nqh: number, nkh: number, hd: number, ws: bigint,
     wsBytes: number, s: bigint): Uint8Array[];
   attnStepRun(plan: Uint8Array, s: bigint): void;
+  attnStepRunPair(plan1: Uint8Array, plan2: Uint8Array, s: bigint): void;
   attnStepAdvance(plan: Uint8Array, tokens: number): void;
   attnStepRunAttention(plan: Uint8Array, s: bigint): void;
   attnStepRunOut(plan: Uint8Array, segs: { weight: bigint; out: bigint; rows: number }[], s: bigint): void;
@@ -587,6 +588,18 @@ export class HipAttention {
     const slot = this.beginPass(PASS_LABELS.attnStep);
     try {
       this.g4.attnStepRun(plan, this.stream);
+    } finally {
+      this.endPass(slot);
+    }
+  }
+
+  // A token of a model with two head_dims (E2B: 512 on the global layers, 256 on the local ones), one plan
+  // per head_dim (either order): both attention passes in one launch, the head_dim-256 workgroups in the
+  // tail of the head_dim-512 ones, then both merges in one launch.
+  attnStepRunPair(plan1: Uint8Array, plan2: Uint8Array): void {
+    const slot = this.beginPass(PASS_LABELS.attnStep);
+    try {
+      this.g4.attnStepRunPair(plan1, plan2, this.stream);
     } finally {
       this.endPass(slot);
     }

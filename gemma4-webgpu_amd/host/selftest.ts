@@ -124,6 +124,9 @@ export function cpuChecks(): string[] {
   done.push('slot table');
   if (typeof g4.version() !== 'string') fail('version');
   done.push('addon loaded: ' + g4.version());
+  // attnStepRunPair takes two 64-byte plans; anything else is refused before the library is called
+  throws(() => g4.attnStepRunPair(new Uint8Array(3), new Uint8Array(64), BigInt(0)), 'attnStepRunPair: short plan');
+  done.push('step pair arguments');
   return done;
 }
 
