@@ -109,7 +109,8 @@ def workload_spec(name: str) -> dict:
                         producer=None if pmap[il] == il else pmap[il]) for il in range(35)]
         return dict(name=name, layers=layers, seed=BASE_SEED + (6 if name == "e2b8k" else 7),
                     desc=f"Gemma-4-E2B attention stack, bs1, position {pos}: head_dim 512 on the 7 global layers, "
-                         "layers 15..34 reading layer 13's / 14's cache, one launch per head_dim")
+                         "layers 15..34 reading layer 13's / 14's cache, one plan per head_dim, both run as one attention "
+                         "launch and one merge launch")
     if name == "long128k":
         pos = 131071
         return dict(name=name, layers=[layer(window=0, theta=1e6, divisor=1, seq=pos + 1, pos=pos)],
