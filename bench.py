@@ -380,7 +380,8 @@ def run_gpu(spec, args, decode_loop=False):
     log(f"k_attn_step: avg {att_avg * 1e3:.2f} us, median {att_ms[len(att_ms) // 2] * 1e3:.2f} us (events, "
         f"{n_groups} launch(es) per step)")
     result = dict(wall_s=wall, steps=args.steps, attn_avg_ms=att_avg, attn_median_ms=att_ms[len(att_ms) // 2],
-                  sets=sets, bytes=per_step, launches=n_groups)
+                  sets=sets, bytes=per_step, launches=n_groups,
+                  kernel="k_attn_step_pair" if csets[0].paired else "k_attn_step")
 
     if decode_loop:
         # Position-advancing decode loops, all inside the timed region: every token every entry is one
@@ -794,8 +795,9 @@ def decode_line(name, args, decode_loop):
                    "bytes_per_step": r["bytes"], "cache_sets_rotated": r["sets"],
                    "issue": "per head_dim, all entries of the step in one attention launch (q/k RMSNorm+RoPE, "
                             "v-norm, KV store, split-K attention) plus the log-sum-exp merge launch when the plan "
-                            "has split entries"},
-        "roofline": {"bound": "hbm", "kernel": "k_attn_step", "launches_per_step": r["launches"],
+                            "has split entries; two head_dims: both plans' attention passes in one launch and "
+                            "their merges in one"},
+        "roofline": {"bound": "hbm", "kernel": r["kernel"], "launches_per_step": r["launches"],
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "avg_us": round(r["attn_avg_ms"] * 1e3, 2),
