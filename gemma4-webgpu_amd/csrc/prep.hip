@@ -85,6 +85,7 @@ constexpr unsigned kPrepTokens = 2;  // measured: 1, 2, 4, 8 tokens -> 43.0, 40.
 // Workgroups per 32-row block (kPrepTokens tokens each), and the XCDs whose
 // workgroups a launch interleaves (workgroup b runs on XCD b % kXcds).
 constexpr unsigned kPrepPerBlock = 32 / kPrepTokens;
+constexpr unsigned kPromptPrepMany = 8;  // entries of one g4_attn_prompt_prep_many launch
 constexpr unsigned kXcds = 8;
 
 // The chunk's positions [start, start + n) in whole 32-row blocks from
@@ -109,22 +110,21 @@ __device__ __forceinline__ unsigned prep_first_pos(unsigned b, unsigned base) {
 // whole blocks multiplies finite values by the zero probabilities of keys it
 // does not attend (the next chunk's prep overwrites them).
 template <int HD>
-__global__ __launch_bounds__(kWG) void k_prompt_prep(const float* __restrict__ q, const float* __restrict__ k,
-                                                     const float* __restrict__ v,
-                                                     const uint16_t* __restrict__ q_weight,
-                                                     const uint16_t* __restrict__ k_weight,
-                                                     const uint16_t* __restrict__ rope_freqs,
-                                                     const float* __restrict__ inv_table,
-                                                     uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_cache,
-                                                     uint16_t* __restrict__ v_cache, uint16_t* __restrict__ vt_cache,
-                                                     g4_prompt_prep_params p) {
+__device__ __forceinline__ void prompt_prep_body(const float* __restrict__ q, const float* __restrict__ k,
+                                                 const float* __restrict__ v, const uint16_t* __restrict__ q_weight,
+                                                 const uint16_t* __restrict__ k_weight,
+                                                 const uint16_t* __restrict__ rope_freqs,
+                                                 const float* __restrict__ inv_table, uint16_t* __restrict__ q_out,
+                                                 uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache,
+                                                 uint16_t* __restrict__ vt_cache, const g4_prompt_prep_params& p,
+                                                 unsigned wg) {
     constexpr int J = HD / 64, PJ = J / 2;
     constexpr unsigned NP = HD / 2;  // RoPE pairs
     static_assert(NP <= kWG, "one thread per RoPE pair");
     __shared__ float inv[NP];
     __shared__ float rc[kPrepTokens][NP], rs[kPrepTokens][NP];
     const unsigned base = p.start & ~31u, end = p.start + p.n_tokens;
-    const unsigned pos0 = prep_first_pos(blockIdx.x, base);
+    const unsigned pos0 = prep_first_pos(wg, base);
     if (pos0 >= end) return;  // uniform: past the chunk's last block (or a block's pair past its end)
     const unsigned lo = max(pos0, p.start);  // this workgroup's positions [lo, hi)
     const unsigned hi = min(pos0 + kPrepTokens, end);
@@ -230,6 +230,39 @@ __global__ __launch_bounds__(kWG) void k_prompt_prep(const float* __restrict__ q
     }
 }
 
+template <int HD>
+__global__ __launch_bounds__(kWG) void k_prompt_prep(const float* __restrict__ q, const float* __restrict__ k,
+                                                     const float* __restrict__ v,
+                                                     const uint16_t* __restrict__ q_weight,
+                                                     const uint16_t* __restrict__ k_weight,
+                                                     const uint16_t* __restrict__ rope_freqs,
+                                                     const float* __restrict__ inv_table,
+                                                     uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_cache,
+                                                     uint16_t* __restrict__ v_cache, uint16_t* __restrict__ vt_cache,
+                                                     g4_prompt_prep_params p) {
+    prompt_prep_body<HD>(q, k, v, q_weight, k_weight, rope_freqs, inv_table, q_out, k_cache, v_cache, vt_cache, p,
+                         blockIdx.x);
+}
+
+// Several chunks' preps in one launch (layers or sequences of one head_dim): entry i takes workgroups
+// [first[i], first[i + 1]) of the grid, each a multiple of the XCD count (so a workgroup's XCD is the one
+// its index within the entry names). The entries come by value in the kernel arguments.
+struct PromptPrepMany {
+    g4_prompt_prep_entry e[kPromptPrepMany];
+    uint32_t first[kPromptPrepMany + 1];
+    uint32_t n;
+};
+
+template <int HD>
+__global__ __launch_bounds__(kWG) void k_prompt_prep_many(const PromptPrepMany m) {
+    const unsigned g = blockIdx.x;
+    unsigned i = 0;
+    while (i + 1 < m.n && g >= m.first[i + 1]) i++;  // uniform
+    const g4_prompt_prep_entry& e = m.e[i];
+    prompt_prep_body<HD>(e.q, e.k, e.v, e.q_weight, e.k_weight, e.rope_freqs, e.rope_inv_freq, e.q_out, e.k_cache,
+                         e.v_cache, e.vt_cache, e.p, g - m.first[i]);
+}
+
 }  // namespace g4
 
 using namespace g4;
@@ -267,9 +300,12 @@ extern "C" int g4_attn_prep(float* q, float* k, float* v, const uint16_t* q_weig
     return G4_OK;
 }
 
-static int prompt_prep(const float* q, const float* k, const float* v, const uint16_t* q_weight, const uint16_t* k_weight,
-                       const uint16_t* rope_freqs, const float* rope_inv_freq, uint16_t* q_out, uint16_t* k_cache,
-                       uint16_t* v_cache, uint16_t* vt_cache, const g4_prompt_prep_params& p, void* stream) {
+// Checks one chunk's prep and gives its workgroup count (0: nothing to do).
+static int prompt_prep_check(const float* q, const float* k, const float* v, const uint16_t* q_weight,
+                             const uint16_t* k_weight, const uint16_t* rope_freqs, const float* rope_inv_freq,
+                             uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache, uint16_t* vt_cache,
+                             const g4_prompt_prep_params& p, uint32_t* wgs_out) {
+    *wgs_out = 0;
     if (p.head_dim != 256 && p.head_dim != 512)
         return fail(G4_EINVAL, "attnPromptPrep: head_dim %u unsupported (256 or 512)", p.head_dim);
     if (p.num_q_heads == 0 || p.num_kv_heads == 0) return fail(G4_EINVAL, "attnPromptPrep: no heads");
@@ -285,12 +321,24 @@ static int prompt_prep(const float* q, const float* k, const float* v, const uin
     }
     if (vt_cache && !p.store_kv) return fail(G4_EINVAL, "attnPromptPrep: vt_cache needs store_kv (a KV producer)");
     if ((uint64_t)p.start + p.n_tokens + 31 > 0xffffffffull) return fail(G4_EINVAL, "attnPromptPrep: position range");
+    (void)rope_inv_freq;
     if (p.n_tokens == 0) return G4_OK;
-    hipStream_t st = as_stream(stream);
     const uint64_t blocks = ((uint64_t)p.start + p.n_tokens - (p.start & ~31u) + 31) / 32;
     const uint64_t wgs = (blocks + kXcds - 1) / kXcds * kXcds * kPrepPerBlock;
     if (wgs > 0x7fffffffu) return fail(G4_EINVAL, "attnPromptPrep: too many tokens");
-    const dim3 grid((uint32_t)wgs);
+    *wgs_out = (uint32_t)wgs;
+    return G4_OK;
+}
+
+static int prompt_prep(const float* q, const float* k, const float* v, const uint16_t* q_weight, const uint16_t* k_weight,
+                       const uint16_t* rope_freqs, const float* rope_inv_freq, uint16_t* q_out, uint16_t* k_cache,
+                       uint16_t* v_cache, uint16_t* vt_cache, const g4_prompt_prep_params& p, void* stream) {
+    uint32_t wgs = 0;
+    const int rc = prompt_prep_check(q, k, v, q_weight, k_weight, rope_freqs, rope_inv_freq, q_out, k_cache, v_cache,
+                                     vt_cache, p, &wgs);
+    if (rc || !wgs) return rc;
+    hipStream_t st = as_stream(stream);
+    const dim3 grid(wgs);
     if (p.head_dim == 512)
         G4_LAUNCH(k_prompt_prep<512>, grid, dim3(kWG), 0, st, q, k, v, q_weight, k_weight, rope_freqs,
                            rope_inv_freq, q_out, k_cache, v_cache, vt_cache, p);
@@ -298,6 +346,38 @@ static int prompt_prep(const float* q, const float* k, const float* v, const uin
         G4_LAUNCH(k_prompt_prep<256>, grid, dim3(kWG), 0, st, q, k, v, q_weight, k_weight, rope_freqs,
                            rope_inv_freq, q_out, k_cache, v_cache, vt_cache, p);
     G4_CHECK_LAUNCH("attnPromptPrep");
+    return G4_OK;
+}
+
+extern "C" int g4_attn_prompt_prep_many(const g4_prompt_prep_entry* entries, uint32_t n_entries, void* stream) {
+    if (!entries || n_entries == 0) return fail(G4_EINVAL, "attnPromptPrepMany: no entries");
+    if (n_entries > kPromptPrepMany)
+        return fail(G4_EINVAL, "attnPromptPrepMany: %u entries (max %u)", n_entries, kPromptPrepMany);
+    PromptPrepMany m = {};
+    uint64_t total = 0;
+    for (uint32_t i = 0; i < n_entries; i++) {
+        const g4_prompt_prep_entry& e = entries[i];
+        if (e.p.head_dim != entries[0].p.head_dim)
+            return fail(G4_EINVAL, "attnPromptPrepMany: entry %u has head_dim %u, entry 0 %u", i, e.p.head_dim,
+                        entries[0].p.head_dim);
+        uint32_t wgs = 0;
+        const int rc = prompt_prep_check(e.q, e.k, e.v, e.q_weight, e.k_weight, e.rope_freqs, e.rope_inv_freq,
+                                         e.q_out, e.k_cache, e.v_cache, e.vt_cache, e.p, &wgs);
+        if (rc) return rc;
+        m.e[i] = e;
+        m.first[i] = (uint32_t)total;
+        total += wgs;  // a multiple of kXcds
+    }
+    if (total == 0) return G4_OK;
+    if (total > 0x7fffffffu) return fail(G4_EINVAL, "attnPromptPrepMany: too many tokens");
+    m.first[n_entries] = (uint32_t)total;
+    m.n = n_entries;
+    hipStream_t st = as_stream(stream);
+    if (entries[0].p.head_dim == 512)
+        G4_LAUNCH(k_prompt_prep_many<512>, dim3((uint32_t)total), dim3(kWG), 0, st, m);
+    else
+        G4_LAUNCH(k_prompt_prep_many<256>, dim3((uint32_t)total), dim3(kWG), 0, st, m);
+    G4_CHECK_LAUNCH("attnPromptPrepMany");
     return G4_OK;
 }
 

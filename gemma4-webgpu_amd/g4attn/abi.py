@@ -104,6 +104,13 @@ class PromptPrepParams(C.Structure):
                 ("apply_divisor", C.c_uint32), ("store_kv", C.c_uint32), ("max_seq_len", C.c_uint32)]
 
 
+class PromptPrepEntry(C.Structure):
+    _fields_ = [("q", C.c_void_p), ("k", C.c_void_p), ("v", C.c_void_p), ("q_weight", C.c_void_p),
+                ("k_weight", C.c_void_p), ("rope_freqs", C.c_void_p), ("rope_inv_freq", C.c_void_p),
+                ("q_out", C.c_void_p), ("k_cache", C.c_void_p), ("v_cache", C.c_void_p), ("vt_cache", C.c_void_p),
+                ("p", PromptPrepParams)]
+
+
 class MatmulParams(C.Structure):  # matmul_quant.wgsl:12
     _fields_ = [("M", C.c_uint32), ("N", C.c_uint32)]
 
@@ -199,6 +206,7 @@ SIGNATURES: dict[str, list] = {
     "g4_attn_prefill": [C.POINTER(PrefillEntry), _U32, _U32, _U32, _U32, _P, _SZ, _P],
     "g4_attn_prompt_prep": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, PromptPrepParams, _P],
     "g4_attn_prompt_prep_vt": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, PromptPrepParams, _P],
+    "g4_attn_prompt_prep_many": [C.POINTER(PromptPrepEntry), C.c_uint32, _P],
     "g4_matmul_quant_f16": [_P, _P, _P, MatmulParams, _P],
     "g4_linear_f16": [_P, _U32, C.POINTER(LinearSeg), _U32, _P],
     "g4_read_ceiling": [_P, _SZ, _P, _P, _P, _P],

@@ -443,6 +443,41 @@ def vt_cache_elems(max_seq_len, num_kv_heads, head_dim) -> int:
     return (max_seq_len + 31) // 32 * 32 * num_kv_heads * head_dim
 
 
+def _prompt_prep_args(q, q_weight, q_out, n_tokens, start, num_q_heads, num_kv_heads, head_dim, theta, apply_divisor,
+                      rope_freqs=None, k=None, v=None, k_weight=None, k_cache=None, v_cache=None, max_seq_len=0,
+                      eps=1e-6, rope_inv_freq=None, vt_cache=None):
+    """The checked device pointers and params of one chunk's prompt prep (attn_prompt_prep's arguments)."""
+    store = k is not None
+    nq = n_tokens * num_q_heads * head_dim
+    nk = n_tokens * num_kv_heads * head_dim
+    p = PromptPrepParams(num_q_heads, num_kv_heads, head_dim, n_tokens, start, eps, theta, 1 if apply_divisor else 0,
+                         1 if store else 0, max_seq_len)
+    rows = max_seq_len * num_kv_heads * head_dim
+    args = [_f32(q, "q", nq), _f32(k, "k", nk) if store else None,
+            _f32(v, "v", nk) if store else None, _f16(q_weight, "q_weight", head_dim),
+            _f16(k_weight, "k_weight", head_dim) if store else None,
+            _f16(rope_freqs, "rope_freqs", head_dim // 2) if rope_freqs is not None else None,
+            _f32(rope_inv_freq, "rope_inv_freq", head_dim // 2) if rope_inv_freq is not None else None,
+            _f16(q_out, "q_out", nq), _f16(k_cache, "k_cache", rows) if store else None,
+            _f16(v_cache, "v_cache", rows) if store else None]
+    vt = _f16(vt_cache, "vt_cache", vt_cache_elems(max_seq_len, num_kv_heads, head_dim)) \
+        if vt_cache is not None else None
+    return args, vt, p
+
+
+def attn_prompt_prep_many(chunks, stream=None):
+    """Several chunks' prompt preps (dicts of attn_prompt_prep's keyword arguments, one head_dim) in one launch
+    (g4_attn_prompt_prep_many), each giving the bits of its own attn_prompt_prep call."""
+    from .abi import PromptPrepEntry
+
+    chunks = list(chunks)
+    arr = (PromptPrepEntry * len(chunks))()
+    for i, kw in enumerate(chunks):
+        args, vt, p = _prompt_prep_args(**kw)
+        arr[i] = PromptPrepEntry(*args, vt, p)
+    abi.call("g4_attn_prompt_prep_many", arr, len(chunks), _stream(stream))
+
+
 def attn_prompt_prep(q, q_weight, q_out, n_tokens, start, num_q_heads, num_kv_heads, head_dim, theta, apply_divisor,
                      rope_freqs=None, k=None, v=None, k_weight=None, k_cache=None, v_cache=None, max_seq_len=0,
                      eps=1e-6, rope_inv_freq=None, vt_cache=None, stream=None):

@@ -29,7 +29,7 @@ def prefill4k(dev, nqh=8, nkh=1, hd=256, T=PREFILL_T, chunk=PREFILL_CHUNK, windo
     the engine's rope_freqs table; the chunked prompt prep (q/k RMSNorm + RoPE at every position, v
     weightless norm, f16 K/V rows stored) fills the f16 query and the caches. Returns the per-layer
     device tensors (q f16, k_cache, v_cache, out, window), the prefill entries (every chunk of every
-    layer, layer order then chunk order) and `prep()`, which re-runs the two layers' prep launches.
+    layer, layer order then chunk order) and `prep()`, which re-runs the two layers' preps (one launch).
     vt: the prep also writes V^T blocks beside each cache and the entries read V from them (False: the
     prefill transposes the attended rows itself at every call)."""
     import numpy as np
@@ -61,9 +61,8 @@ def prefill4k(dev, nqh=8, nkh=1, hd=256, T=PREFILL_T, chunk=PREFILL_CHUNK, windo
                                 n_tokens=min(chunk, T - c0), start=c0, sliding_window=w, scale=1.0,
                                 vt_cache=vtc, vt_rows=T))
 
-    def prep():
-        for kw in preps:
-            ops.attn_prompt_prep(**kw)
+    def prep():  # both layers' chunks in one launch
+        ops.attn_prompt_prep_many(preps)
 
     prep()
     return layers, entries, prep

@@ -539,6 +539,28 @@ int g4_attn_prompt_prep_vt(const float* q, const float* k, const float* v, const
                            const uint16_t* k_weight, const uint16_t* rope_freqs, const float* rope_inv_freq,
                            uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache, uint16_t* vt_cache,
                            g4_prompt_prep_params p, void* stream);
+/* Several chunks' preps in one launch: chunks of several sequences in a
+ * batched prefill (or several layers whose inputs are all ready), one
+ * head_dim for all. Entry i is exactly the call g4_attn_prompt_prep (vt_cache
+ * NULL) or g4_attn_prompt_prep_vt (vt_cache set) with its arguments, and gives
+ * the same bits; the entries' outputs must not overlap. At most 8 entries.
+ * No counterpart in the reference (one token per dispatch, src/engine.ts:
+ * 2460-2479). */
+typedef struct g4_prompt_prep_entry {
+    const float* q;
+    const float* k;
+    const float* v;
+    const uint16_t* q_weight;
+    const uint16_t* k_weight;
+    const uint16_t* rope_freqs;
+    const float* rope_inv_freq;
+    uint16_t* q_out;
+    uint16_t* k_cache;
+    uint16_t* v_cache;
+    uint16_t* vt_cache;
+    g4_prompt_prep_params p;
+} g4_prompt_prep_entry;
+int g4_attn_prompt_prep_many(const g4_prompt_prep_entry* entries, uint32_t n_entries, void* stream);
 
 /* ---- the f16 projections either side of the block ------------------------
  * attn.linearQKV (src/engine.ts:2045-2051) and attn.linearOut (:2096):

@@ -49,14 +49,18 @@ class Chunk:
                              device=dev) if vt else None
         self.dqw, self.dkw, self.drf = t16(self.qw, dev), t16(self.kw, dev), t16(ROPE, dev)
 
-    def run(self, inv_table=False):
-        """inv_table: pass the layer's inverse-frequency table from g4_rope_inv_freq instead of letting each
-        workgroup evaluate it."""
+    def kwargs(self, inv_table=False):
+        """attn_prompt_prep's arguments for this chunk. inv_table: pass the layer's inverse-frequency table from
+        g4_rope_inv_freq instead of letting each workgroup evaluate it."""
         kw = dict(k=self.dk, v=self.dv, k_weight=self.dkw, k_cache=self.kc, v_cache=self.vc,
                   max_seq_len=self.rows, vt_cache=self.vt) if self.store else {}
         inv = ops.rope_inv_freq(self.theta, self.hd, self.div, self.drf) if inv_table else None
-        ops.attn_prompt_prep(self.dq, self.dqw, self.q_out, self.T, self.start, self.nqh, self.nkh, self.hd,
-                             self.theta, self.div, rope_freqs=self.drf, eps=EPS, rope_inv_freq=inv, **kw)
+        return dict(q=self.dq, q_weight=self.dqw, q_out=self.q_out, n_tokens=self.T, start=self.start,
+                    num_q_heads=self.nqh, num_kv_heads=self.nkh, head_dim=self.hd, theta=self.theta,
+                    apply_divisor=self.div, rope_freqs=self.drf, eps=EPS, rope_inv_freq=inv, **kw)
+
+    def run(self, inv_table=False):
+        ops.attn_prompt_prep(**self.kwargs(inv_table))
         torch.cuda.synchronize()
 
     def expected(self):
@@ -122,6 +126,33 @@ def test_prompt_prep_bit_exact(dev, start, T, hd, theta, div, inv_table, vt):
     c = Chunk(dev, 500 + start + hd, start, T, hd, theta, div, vt=vt)
     c.run(inv_table)
     c.check()
+
+
+@pytest.mark.parametrize("hd", [256, 512])
+def test_prompt_prep_many_in_one_launch(dev, hd):
+    """g4_attn_prompt_prep_many: chunks of different starts and lengths, producers with and without V^T blocks,
+    a consumer, local and global layers and a 4:1 group over two kv heads, in one launch; every chunk bit for
+    bit as its own call gives it (the oracle's bits)."""
+    announce(f"attnPromptPrepMany hd={hd}")
+    chunks = [Chunk(dev, 800 + hd, 0, 512, hd, 1e4, 0, vt=True),
+              Chunk(dev, 801 + hd, 4096 + 19, 301, hd, 1e6, 1, vt=True),
+              Chunk(dev, 802 + hd, 77, 5, hd, 1e4, 0),
+              Chunk(dev, 803 + hd, 300, 64, hd, 1e4, 0, store=False),
+              Chunk(dev, 804 + hd, 33, 90, hd, 1e6, 1, nqh=8, nkh=2, vt=True),
+              Chunk(dev, 805 + hd, 131071 - 300, 300, hd, 1e6, 1)]
+    ops.attn_prompt_prep_many([c.kwargs(inv_table=(i % 2 == 0)) for i, c in enumerate(chunks)])
+    torch.cuda.synchronize()
+    for c in chunks:
+        c.check()
+
+
+def test_prompt_prep_many_refuses(dev):
+    """Mixed head_dims and more than eight entries are refused before anything is enqueued."""
+    a, b = Chunk(dev, 900, 0, 8, 256, 1e4, 0), Chunk(dev, 901, 0, 8, 512, 1e4, 0)
+    with pytest.raises(RuntimeError, match="head_dim"):
+        ops.attn_prompt_prep_many([a.kwargs(), b.kwargs()])
+    with pytest.raises(RuntimeError, match="max 8"):
+        ops.attn_prompt_prep_many([a.kwargs()] * 9)
 
 
 def test_prompt_prep_consumer_and_gqa(dev):
