@@ -1334,6 +1334,30 @@ napi_value AttnPromptPrepVt(napi_env env, napi_callback_info info) {
     return undefined(env);
 }
 
+// attnPromptPrepMany(entries (n g4_prompt_prep_entry records as bytes), n, stream): several chunks' preps
+// in one launch (g4_attn_prompt_prep_many).
+napi_value AttnPromptPrepMany(napi_env env, napi_callback_info info) {
+    Args a(env, info, 3);
+    void* d = nullptr;
+    size_t bytes = 0;
+    a.bytes(0, &d, &bytes);
+    const uint32_t n = a.u32(1);
+    void* s = a.ptr(2);
+    if (!a.ok) return nullptr;
+    if (n == 0 || bytes != (size_t)n * sizeof(g4_prompt_prep_entry)) {
+        napi_throw_type_error(env, nullptr, "attnPromptPrepMany: entries must hold n g4_prompt_prep_entry records");
+        return nullptr;
+    }
+    std::vector<g4_prompt_prep_entry> ents(n);
+    memcpy(ents.data(), d, bytes);
+    CALL(env, g4_attn_prompt_prep_many(ents.data(), n, s));
+    return undefined(env);
+}
+
+napi_value SizeofPromptPrepEntry(napi_env env, napi_callback_info) {
+    return number(env, (double)sizeof(g4_prompt_prep_entry));
+}
+
 napi_value Init(napi_env env, napi_value exports) {
     struct {
         const char* name;
@@ -1390,6 +1414,8 @@ napi_value Init(napi_env env, napi_value exports) {
         {"attnPrefillPrepare", AttnPrefillPrepare},
         {"attnPrefillRun", AttnPrefillRun},
         {"attnPromptPrep", AttnPromptPrep},
+        {"attnPromptPrepMany", AttnPromptPrepMany},
+        {"sizeofPromptPrepEntry", SizeofPromptPrepEntry},
         {"attnPromptPrepVt", AttnPromptPrepVt},
     };
     for (auto& f : fns) {

@@ -335,6 +335,7 @@ export interface Addon {
     inv: bigint | null, qOut: bigint, kc: bigint | null, vc: bigint | null, p: Uint8Array, s: bigint): void;
   attnPromptPrepVt(q: bigint, k: bigint, v: bigint, qw: bigint, kw: bigint, rf: bigint | null,
     inv: bigint | null, qOut: bigint, kc: bigint, vc: bigint, vt: bigint, p: Uint8Array, s: bigint): void;
+  attnPromptPrepMany(entries: Uint8Array, n: number, s: bigint): void;
   [key: string]: any;
 }
 
@@ -706,6 +707,38 @@ export class HipAttention {
         this.g4.attnPromptPrep(p.q.ptr, ptr(p.k), ptr(p.v), p.qWeight.ptr, ptr(p.kWeight), ptr(p.ropeFreqs),
           ptr(p.ropeInvFreq), p.qOut.ptr, ptr(p.kCache), ptr(p.vCache), params.bytes, this.stream);
       }
+    } finally {
+      this.endPass(slot);
+    }
+  }
+
+  // Several chunks' preps in one launch (chunks of several sequences in a batched prefill, or several layers
+  // whose inputs are all ready); one head_dim for all, each chunk as attnPromptPrep would give it.
+  attnPromptPrepMany(chunks: PromptPrep[], shape: StepShape): void {
+    const REC = 128;  // g4_prompt_prep_entry: eleven pointers, then the ten 4-byte params fields
+    const bytes = new Uint8Array(REC * chunks.length);
+    const dv = new DataView(bytes.buffer);
+    chunks.forEach(function (p, i) {
+      const store = p.k !== undefined;
+      if (store && (!p.v || !p.kWeight || !p.kCache || !p.vCache || p.maxSeqLen === undefined)) {
+        throw new Error('attnPromptPrepMany: a producer layer needs k, v, kWeight, kCache, vCache and maxSeqLen');
+      }
+      if (p.vtCache && !store) throw new Error('attnPromptPrepMany: vtCache on a layer that stores no rows');
+      const ptrs = [p.q, p.k, p.v, p.qWeight, p.kWeight, p.ropeFreqs, p.ropeInvFreq, p.qOut, p.kCache, p.vCache,
+        p.vtCache];
+      const o = i * REC;
+      ptrs.forEach(function (b, j) { dv.setBigUint64(o + 8 * j, b ? b.ptr : BigInt(0), true); });
+      const u = [shape.numQHeads, shape.numKvHeads, shape.headDim, p.nTokens, p.start];
+      u.forEach(function (x, j) { dv.setUint32(o + 88 + 4 * j, x, true); });
+      dv.setFloat32(o + 108, p.eps === undefined ? 1e-6 : p.eps, true);
+      dv.setFloat32(o + 112, p.theta, true);
+      dv.setUint32(o + 116, p.applyDivisor, true);
+      dv.setUint32(o + 120, store ? 1 : 0, true);
+      dv.setUint32(o + 124, p.maxSeqLen || 0, true);
+    });
+    const slot = this.beginPass(PASS_LABELS.attnPromptPrep);
+    try {
+      this.g4.attnPromptPrepMany(bytes, chunks.length, this.stream);
     } finally {
       this.endPass(slot);
     }

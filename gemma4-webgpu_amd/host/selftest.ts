@@ -127,6 +127,9 @@ export function cpuChecks(): string[] {
   // attnStepRunPair takes two 64-byte plans; anything else is refused before the library is called
   throws(() => g4.attnStepRunPair(new Uint8Array(3), new Uint8Array(64), BigInt(0)), 'attnStepRunPair: short plan');
   done.push('step pair arguments');
+  if (g4.sizeofPromptPrepEntry() !== 128) fail(`g4_prompt_prep_entry is ${g4.sizeofPromptPrepEntry()} B, the host writes 128`);
+  throws(() => g4.attnPromptPrepMany(new Uint8Array(100), 1, BigInt(0)), 'attnPromptPrepMany: short record');
+  done.push('prompt prep records');
   return done;
 }
 
@@ -336,6 +339,22 @@ function promptPrep(dir: string): string[] {
     ropeFreqs: rf, ropeInvFreq: inv, qOut: qOut, kCache: kc, vCache: vc, nTokens: spec.nTokens, start: spec.start,
     theta: spec.theta, applyDivisor: spec.div, maxSeqLen: spec.rows, vtCache: vt,
   }, shape);
+  // the same chunk through attnPromptPrepMany (one entry) into fresh buffers: the same bits
+  const qOut2 = alloc(qOut.size), kc2 = alloc(kc.size), vc2 = alloc(vc.size);
+  const vt2 = vt ? alloc(vt.size) : undefined;
+  att.attnPromptPrepMany([{
+    q: upload(A.q), k: upload(A.k), v: upload(A.v), qWeight: upload(A.qw), kWeight: upload(A.kw),
+    ropeFreqs: rf, ropeInvFreq: inv, qOut: qOut2, kCache: kc2, vCache: vc2, nTokens: spec.nTokens, start: spec.start,
+    theta: spec.theta, applyDivisor: spec.div, maxSeqLen: spec.rows, vtCache: vt2,
+  }], shape);
+  const pairs: DeviceBuffer[][] = [[qOut, qOut2], [kc, kc2], [vc, vc2]];
+  if (vt && vt2) pairs.push([vt, vt2]);
+  for (const [x, y] of pairs) {
+    const bx = new Uint8Array(x.size), by = new Uint8Array(y.size);
+    att.readBuffer(x, 0, bx);
+    att.readBuffer(y, 0, by);
+    for (let i = 0; i < bx.length; i++) if (bx[i] !== by[i]) fail(`attnPromptPrepMany differs at byte ${i}`);
+  }
   const parts: DeviceBuffer[] = [qOut, kc, vc];
   if (vt) {
     const out = alloc(spec.nTokens * spec.nqh * spec.hd * 4);
@@ -357,7 +376,7 @@ function promptPrep(dir: string): string[] {
   for (const b of bufs) att.destroyBuffer(b);
   att.dispose();
   return ['attnPromptPrep: ' + spec.nTokens + ' tokens' + (vt ? ', V^T blocks, attnPrefill through them' : ''),
-    'results written'];
+    'attnPromptPrepMany: same bits', 'results written'];
 }
 
 interface HeadSpec {
