@@ -487,23 +487,12 @@ def attn_prompt_prep(q, q_weight, q_out, n_tokens, start, num_q_heads, num_kv_he
     device table from rope_inv_freq() for this layer's theta/divisor (else each workgroup evaluates it).
     vt_cache (KV producers): the V rows also go there as V^T blocks (g4_attn_prompt_prep_vt), of
     vt_cache_elems(max_seq_len, ...) f16 elements."""
-    store = k is not None
-    nq = n_tokens * num_q_heads * head_dim
-    nk = n_tokens * num_kv_heads * head_dim
-    p = PromptPrepParams(num_q_heads, num_kv_heads, head_dim, n_tokens, start, eps, theta, 1 if apply_divisor else 0,
-                         1 if store else 0, max_seq_len)
-    rows = max_seq_len * num_kv_heads * head_dim
-    args = [_f32(q, "q", nq), _f32(k, "k", nk) if store else None,
-            _f32(v, "v", nk) if store else None, _f16(q_weight, "q_weight", head_dim),
-            _f16(k_weight, "k_weight", head_dim) if store else None,
-            _f16(rope_freqs, "rope_freqs", head_dim // 2) if rope_freqs is not None else None,
-            _f32(rope_inv_freq, "rope_inv_freq", head_dim // 2) if rope_inv_freq is not None else None,
-            _f16(q_out, "q_out", nq), _f16(k_cache, "k_cache", rows) if store else None,
-            _f16(v_cache, "v_cache", rows) if store else None]
-    if vt_cache is None:
+    args, vt, p = _prompt_prep_args(q, q_weight, q_out, n_tokens, start, num_q_heads, num_kv_heads, head_dim, theta,
+                                    apply_divisor, rope_freqs, k, v, k_weight, k_cache, v_cache, max_seq_len, eps,
+                                    rope_inv_freq, vt_cache)
+    if vt is None:
         abi.call("g4_attn_prompt_prep", *args, p, _stream(stream))
     else:
-        vt = _f16(vt_cache, "vt_cache", vt_cache_elems(max_seq_len, num_kv_heads, head_dim))
         abi.call("g4_attn_prompt_prep_vt", *args, vt, p, _stream(stream))
 
 
