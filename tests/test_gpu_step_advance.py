@@ -130,6 +130,42 @@ def test_advance_bit_identical_to_fresh_prepare(dev):
         del fws
 
 
+def test_advance_pair_bit_identical_to_fresh_prepare(dev):
+    """A token of two head_dims run as one pair launch (g4_attn_step_run_pair): both plans advanced every
+    token give the bits of both plans prepared fresh every token, run as a pair too (12 tokens)."""
+    announce("attnStep advance: head_dim 256 and 512 plans as one pair launch, against fresh prepares")
+    T = 12
+    groups = {hd: [Stream(dev, 300 + 10 * i + hd, seq0, T, w, th, dv, tab, hd=hd)
+                   for i, (_, seq0, w, th, dv, tab) in enumerate(SAME_PARTS)] for hd in (256, 512)}
+    fresh = {hd: [(s.kc.clone(), s.vc.clone(), torch.full_like(s.out, float("nan"))) for s in ss]
+             for hd, ss in groups.items()}
+    plans = {}
+    for t in range(T):
+        for ss in groups.values():
+            for s in ss:
+                s.load_raw(t)
+        for hd, ss in groups.items():
+            if t == 0:
+                plans[hd] = prepare(dev, [s.entry(0) for s in ss], hd)
+            else:
+                ops.attn_step_advance(plans[hd][0], 1)
+        ops.attn_step_run_pair(plans[512][0], plans[256][0])
+        fp = {hd: prepare(dev, [s.entry(t, o, k, v) for s, (k, v, o) in zip(ss, fresh[hd])], hd)
+              for hd, ss in groups.items()}
+        ops.attn_step_run_pair(fp[256][0], fp[512][0])
+        torch.cuda.synchronize()
+        for hd, ss in groups.items():
+            for i, s in enumerate(ss):
+                k, v, o = fresh[hd][i]
+                row = s.seq0 + t - 1
+                a_, b_ = s.out.cpu().numpy(), o.cpu().numpy()
+                assert np.isfinite(a_).all(), (t, hd, i)
+                np.testing.assert_array_equal(a_.view(np.uint32), b_.view(np.uint32), err_msg=f"t {t} hd {hd} {i}")
+                np.testing.assert_array_equal(s.kc[row].cpu().numpy(), k[row].cpu().numpy(), err_msg=f"K {t} {hd} {i}")
+                np.testing.assert_array_equal(s.vc[row].cpu().numpy(), v[row].cpu().numpy(), err_msg=f"V {t} {hd} {i}")
+        del fp
+
+
 # (seed, first seq_len, window, theta, divisor, host table): tile boundaries crossed, windows filling up
 CROSSING = [(21, 60, 0, 1e6, 1, True), (22, 40, 64, 1e4, 0, True), (23, 500, 512, 1e4, 0, True),
             (24, 1, 0, 1e4, 0, False), (25, 200, 96, 1e6, 1, True)]
