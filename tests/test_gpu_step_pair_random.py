@@ -19,25 +19,33 @@ from test_gpu_step import TOL, Layer
 pytestmark = pytest.mark.gpu
 
 
-def draw_group(rng, hd):
+def draw_group(rng, hd, large=False):
+    """large: 6-8 entries of 24000-40000 rows with no window or a wide one (at least 144000 attended rows,
+    above the 131072 up to which a head_dim-256 step is cut for one 8-wave workgroup per CU), so the
+    head_dim-256 plan takes its 4-wave form."""
     nkh = int(rng.choice([1, 1, 2]))
     group = int(rng.choice([8, 4]))
     specs = []
-    for _ in range(int(rng.integers(1, 7))):
+    for _ in range(int(rng.integers(6, 9)) if large else int(rng.integers(1, 7))):
         r = rng.random()
-        seq = int(rng.integers(1, 40)) if r < 0.25 else int(rng.integers(40, 3000)) if r < 0.7 else \
-            int(rng.integers(3000, 16001))
-        w = int(rng.choice([0, 0, 512, int(rng.integers(1, 33)), int(rng.integers(33, 2000))]))
+        if large:
+            seq = int(rng.integers(24000, 40001))
+            w = int(rng.choice([0, 0, int(rng.integers(24000, 40001))]))
+        else:
+            seq = int(rng.integers(1, 40)) if r < 0.25 else int(rng.integers(40, 3000)) if r < 0.7 else \
+                int(rng.integers(3000, 16001))
+            w = int(rng.choice([0, 0, 512, int(rng.integers(1, 33)), int(rng.integers(33, 2000))]))
         glob = w == 0
         specs.append(dict(seq=seq, window=w, theta=1e6 if glob else 1e4, div=1 if glob else 0,
                           host=bool(rng.random() < 0.5)))
     return dict(hd=hd, nkh=nkh, group=group, specs=specs)
 
 
-@pytest.mark.parametrize("seed", range(10))
+@pytest.mark.parametrize("seed", range(13))
 def test_random_pairs_match_the_oracle(dev, seed):
+    """Seeds 10-12 draw a large head_dim-256 plan (its 4-wave form); the others draw small ones."""
     rng = np.random.default_rng(9100 + seed)
-    groups = [draw_group(rng, 512), draw_group(rng, 256)]
+    groups = [draw_group(rng, 512), draw_group(rng, 256, large=seed >= 10)]
     swap = bool(seed % 2)
     announce(f"attnStep pair random case {seed}: swap={swap} " + " | ".join(
         f"hd={g['hd']} nkh={g['nkh']} group={g['group']} {[(s['seq'], s['window']) for s in g['specs']]}"
