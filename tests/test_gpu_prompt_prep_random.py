@@ -10,8 +10,10 @@ oracle's fused_per_head_norm_rope / per_head_rms_norm_no_weight bit for bit, and
 """
 import numpy as np
 import pytest
+import torch
 
 from conftest import announce
+from g4attn import ops
 from test_gpu_prompt_prep import Chunk
 
 pytestmark = pytest.mark.gpu
@@ -19,9 +21,9 @@ pytestmark = pytest.mark.gpu
 CASES = 12
 
 
-def draw(seed):
+def draw(seed, hd=None):
     r = np.random.default_rng(seed)
-    hd = int(r.choice([256, 512]))
+    hd = int(r.choice([256, 512])) if hd is None else hd
     nkh = int(r.choice([1, 1, 2, 4]))
     group = int(r.choice([1, 2, 4, 8]))
     glob = bool(r.integers(2))
@@ -43,3 +45,22 @@ def test_random_prompt_prep_launches_match_the_oracle(dev, case):
               store=p["store"], vt=p["vt"])
     c.run(p["inv_table"])
     c.check()
+
+
+@pytest.mark.parametrize("case", range(6))
+def test_random_prompt_prep_many_launches_match_the_oracle(dev, case):
+    """g4_attn_prompt_prep_many over 1-8 chunks of one head_dim, each drawn as above (its own kv heads,
+    group, layer class, start, length, producer or consumer, V^T cache and inverse-frequency table): every
+    chunk to the same bars, in one launch."""
+    hd = 512 if case % 3 == 2 else 256
+    n = int(np.random.default_rng(7300 + case).integers(1, 9))
+    ps = [draw(7400 + 11 * case + i, hd) for i in range(n)]
+    announce(f"attnPromptPrepMany random case {case}: hd={hd} "
+             f"{[(p['start'], p['T'], p['nkh'], p['nqh'], p['store'], p['vt']) for p in ps]}")
+    chunks = [Chunk(dev, 9500 + 17 * case + 3 * i, p["start"], p["T"], hd, p["theta"], p["div"], nqh=p["nqh"],
+                    nkh=p["nkh"], store=p["store"], vt=p["vt"]) for i, p in enumerate(ps)]
+    ops.attn_prompt_prep_many([c.kwargs(p["inv_table"]) for c, p in zip(chunks, ps)])
+    torch.cuda.synchronize()
+    for i, c in enumerate(chunks):
+        announce(f"  chunk {i}")
+        c.check()
